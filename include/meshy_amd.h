@@ -1,0 +1,326 @@
+/*
+ * meshy_amd.h -- C ABI of libmeshy_amd.so, the MI355X (gfx950) implementation
+ * of Meshy's ragged-batch path between rollout and trainer.
+ *
+ * Every entry point takes plain pointers and sizes.  Device pointers are HIP
+ * device addresses; every device entry point is asynchronous on the stream it
+ * is given and allocates nothing: scratch space comes in through a caller-owned
+ * workspace whose size the matching *_workspace_size call reports.
+ *
+ * Return convention (all entry points):
+ *     0   success
+ *    <0   invalid argument (a MESHY_E* code); meshy_last_error() has the text
+ *    >0   a hipError_t raised by a launch; meshy_last_error() has the text
+ *
+ * Reference paths below are relative to the OpenBMB/Meshy source tree.
+ */
+#ifndef MESHY_AMD_H
+#define MESHY_AMD_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+#define MESHY_OK 0
+#define MESHY_EINVAL (-1)     /* bad argument value or shape            */
+#define MESHY_ENULL (-2)      /* required pointer was NULL              */
+#define MESHY_EALIGN (-3)     /* pointer or stride misaligned           */
+#define MESHY_ESPACE (-4)     /* workspace too small                    */
+#define MESHY_ENOTDIV (-5)    /* batch size not divisible by DP size    */
+#define MESHY_EEMPTY (-6)     /* empty batch                            */
+
+/* Text of the last error raised on the calling thread ("" when none). */
+const char* meshy_last_error(void);
+/* ABI version: bumped on any signature change. */
+int meshy_abi_version(void);
+
+/* ------------------------------------------------------------------------
+ * Token-budget planner (host).
+ * Replaces build_plan (meshy/backend/titan/plan.py:211-288), including
+ * _snake (plan.py:145-155), _pack_micros (plan.py:158-203) and filler_micro
+ * (plan.py:206-208).  PlannerConfig's own validation (plan.py:60-81) stays
+ * in the Python dataclass; this call re-checks what it relies on.
+ * ---------------------------------------------------------------------- */
+#define MESHY_LAYOUT_PADDED 0
+#define MESHY_LAYOUT_PACKED 1
+
+typedef struct meshy_planner_cfg {
+    int32_t layout;               /* MESHY_LAYOUT_*                          */
+    int32_t reserved;
+    int64_t mini_batch_size;
+    int64_t seq_len;
+    int64_t align;
+    int64_t max_tokens_per_micro; /* <= 0 means None                         */
+    int64_t micro_batch_size;     /* <= 0 means None                         */
+} meshy_planner_cfg;
+
+/*
+ * Caller-allocated plan tables.  With n samples, dp ranks,
+ * n_local = n / dp and n_mini = ceil(n_local / mini_batch_size):
+ *   local_indices        [dp * n_local]       Plan.local_indices
+ *   mini_n_micro         [n_mini]             micros per mini (equal on all ranks)
+ *   mini_n_docs_global   [n_mini]             MiniPlan.n_docs_global
+ *   mini_n_tokens_global [n_mini]             MiniPlan.n_tokens_global
+ *   mini_tokens_per_rank [n_mini * dp]        MiniPlan.tokens_per_rank
+ *   micro_seq_len        [dp * n_local]       MicroPlan.seq_len, rank-major
+ *   micro_doc_start      [dp * (n_local + 1)] CSR row pointer of each rank's micros
+ *   doc_sample           [dp * n_local]       MicroPlan.sample_idx, flattened
+ *   doc_len              [dp * n_local]       MicroPlan.doc_lens, flattened
+ * Rank r's k-th micro (minis in order, fillers last within a mini) is
+ * micro_seq_len[r*n_local + k] with documents
+ * doc_*[r*n_local + micro_doc_start[r*(n_local+1) + k] ...
+ *        r*n_local + micro_doc_start[r*(n_local+1) + k + 1]).
+ * n_micro_total receives the micro count per rank (<= n_local).
+ */
+typedef struct meshy_plan_out {
+    int32_t* local_indices;
+    int32_t* mini_n_micro;
+    int64_t* mini_n_docs_global;
+    int64_t* mini_n_tokens_global;
+    int64_t* mini_tokens_per_rank;
+    int64_t* micro_seq_len;
+    int32_t* micro_doc_start;
+    int32_t* doc_sample;
+    int64_t* doc_len;
+    int32_t n_micro_total;
+    int32_t reserved;
+} meshy_plan_out;
+
+int meshy_plan_build(const int64_t* lengths, const int64_t* loss_tokens, int64_t n,
+                     int64_t dp_size, const meshy_planner_cfg* cfg, meshy_plan_out* out);
+
+/* ------------------------------------------------------------------------
+ * Micro-batch materialisation (device).
+ * Replaces build_micro_batch (meshy/backend/titan/batch.py:96-230): per-doc
+ * shift-by-one (batch.py:91-93), doc_ids with the padding slot, per-doc
+ * positions, cu_seqlens (batch.py:154-178, make_varlen_metadata 233-243).
+ * One launch materialises any number of micros of one rank.
+ * ---------------------------------------------------------------------- */
+typedef struct meshy_pack_args {
+    /* rank-local samples, concatenated (device) */
+    const void* tokens;            /* [total] int32 or int64                  */
+    int32_t tokens_elem_bytes;     /* 4 or 8                                  */
+    int32_t layout;                /* MESHY_LAYOUT_*                          */
+    const float* mask;             /* [total] mask_assistant                  */
+    const float* logprobs;         /* [total] rollout logprobs, nullable      */
+    const float* adv_tokens;       /* [total] per-token advantages (already on
+                                      the next-token grid), nullable         */
+    const float* adv_samples;      /* [n_samples] per-sample advantage
+                                      (sample["advantage"]), nullable        */
+    const int64_t* sample_offsets; /* [n_samples + 1]                         */
+    int64_t n_samples;
+    /* the micros to build (device) */
+    int64_t n_micro;
+    const int64_t* micro_seq_len;  /* [n_micro]                               */
+    const int64_t* micro_out_off;  /* [n_micro + 1] element offset of each
+                                      micro in the flat outputs (rows*seq_len
+                                      elements per micro)                    */
+    const int32_t* micro_doc_start;/* [n_micro + 1]                           */
+    const int32_t* doc_sample;     /* [n_docs_total] rank-local sample index  */
+    const int64_t* doc_len;        /* [n_docs_total] tokens entering forward  */
+    int64_t max_micro_elems;       /* max over micros of rows*seq_len         */
+    int64_t max_docs_per_micro;    /* max over micros of n_docs               */
+    /* flat outputs (device) */
+    int64_t* input_ids;
+    int64_t* labels;
+    int32_t* positions;
+    float* mask_out;
+    int64_t* doc_ids;
+    float* rollout_lp;             /* nullable (need_rollout_lp=False)        */
+    float* adv_tok;                /* nullable.  With adv_tokens: the sample's
+                                      per-token advantages, unshifted
+                                      (batch.py:166-170).  Otherwise, with
+                                      adv_samples: the per-document advantage
+                                      broadcast over the micro, 0 on the
+                                      padding slot (trainer.py:753-756)      */
+    float* adv_doc;                /* [n_docs_total] per-document advantage
+                                      (batch.py:110-116), nullable; needs
+                                      adv_samples                            */
+    int32_t* doc_len_out;          /* [n_docs_total] Batch.lengths, nullable  */
+    int32_t* cu_seqlens;           /* packed only, required there: micro k
+                                      writes n_docs_k + 1 (+1 with a pad doc)
+                                      values at micro_doc_start[k] + 2*k     */
+} meshy_pack_args;
+
+int meshy_pack_micro_batches(const meshy_pack_args* args, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * GRPO group-normalised advantages (device).
+ * Replaces grpo_advantage (meshy/worker/rollout.py:88-97) for all groups of a
+ * batch at once: a size-1 group keeps its reward, otherwise
+ * (r - mean) / clamp(unbiased std, min=1e-8).
+ * ---------------------------------------------------------------------- */
+int meshy_grpo_advantage(const float* rewards, const int64_t* group_offsets,
+                         int64_t n_groups, float* advantages, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Fused packed log_softmax + gather + entropy (device), bf16 logits.
+ * Replaces the chunk loop of TitanTrainer._forward_logprobs
+ * (meshy/backend/titan/trainer.py:451-527) with its bodies _chunk_logprobs
+ * (trainer.py:414-428: -cross_entropy(logits.float(), labels)) and
+ * _chunk_entropy (trainer.py:430-449: logsumexp - sum softmax * z).
+ *
+ * logits element (b, t, v) lives at logits[b*stride_b + t*stride_t + v]
+ * (strides in elements; stride_b, stride_t multiples of 8 and logits 16-byte
+ * aligned take the vector path, anything else the unaligned path).
+ * labels is contiguous [rows * T]; a label of -100 (cross_entropy's default
+ * ignore_index) gives logp = 0; a label outside [0, V) gives NaN.
+ * Outputs are contiguous [rows * T] fp32; each may be NULL.  lse is what the
+ * backward consumes.
+ * ---------------------------------------------------------------------- */
+int meshy_logprob_entropy_fwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
+                              int64_t stride_b, int64_t stride_t, const int64_t* labels,
+                              float* logp, float* entropy, float* lse, hipStream_t stream);
+
+/*
+ * Backward of logp with respect to the logits:
+ *   grad_logits[r, v] = grad_logp[r] * (onehot(label_r)[v] - exp(z[r, v] - lse[r]))
+ * written as bf16 into a contiguous [rows * T, V] buffer.  Ignored labels
+ * (-100) give a zero row.  This is the gradient torch autograd produces for
+ * the reference's checkpointed -cross_entropy chunk (trainer.py:504-517).
+ */
+int meshy_logprob_bwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
+                      int64_t stride_b, int64_t stride_t, const int64_t* labels,
+                      const float* lse, const float* grad_logp, uint16_t* grad_logits,
+                      hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Token-level clipped PPO loss with its diagnostics (device).
+ * Replaces TitanTrainer._ppo_clip_loss (meshy/backend/titan/trainer.py:705-848)
+ * and the per-mini sums _reduce_mini_metrics reads (trainer.py:1020-1047).
+ *
+ * Documents are contiguous token ranges: slot d covers tokens
+ * [seg_offsets[d], seg_offsets[d+1]) of the flattened [rows, S] grid, for
+ * d in [0, n_docs]; slot n_docs is the padding slot.  This is the segment
+ * structure of doc_ids in both batch layouts (batch.py:123, 150-162).
+ * ---------------------------------------------------------------------- */
+enum meshy_ppo_out {
+    MESHY_PPO_LOSS = 0,            /* pg loss (trainer.py:793-799)            */
+    MESHY_PPO_TOTAL_LOSS,          /* loss + coef * positive_lm_loss          */
+    MESHY_PPO_POSITIVE_LM_LOSS,
+    MESHY_PPO_TIS_RATIO_SUM,
+    MESHY_PPO_RATIO_SUM,
+    MESHY_PPO_CLIP_SUM,
+    MESHY_PPO_TIS_MASKED_SUM,
+    MESHY_PPO_TOKEN_COUNT,
+    MESHY_PPO_KL_SUM,
+    MESHY_PPO_LOG_RATIO_ABS_SUM,
+    MESHY_PPO_ESS_SUM,
+    MESHY_PPO_DOC_COUNT,
+    MESHY_PPO_TRAIN_ROLLOUT_KL_SUM,
+    MESHY_PPO_TRAIN_ROLLOUT_LOGDIFF_ABS_SUM,
+    MESHY_PPO_ENTROPY_SUM,
+    MESHY_PPO_NOUT
+};
+
+typedef struct meshy_ppo_args {
+    const float* new_lp;           /* [n_tokens]                              */
+    const float* old_lp;           /* [n_tokens]                              */
+    const float* mask;             /* [n_tokens]                              */
+    const float* rollout_lp;       /* [n_tokens] nullable                     */
+    const float* entropy;          /* [n_tokens] nullable                     */
+    const float* adv;              /* [n_docs] or [n_tokens]                  */
+    const float* positive_lm_weights; /* [n_docs], nullable                   */
+    const int64_t* seg_offsets;    /* [n_docs + 2]                            */
+    int64_t n_tokens;
+    int64_t n_docs;
+    int64_t n_docs_global;         /* MiniPlan.n_docs_global                  */
+    int64_t n_tokens_global;       /* MiniPlan.n_tokens_global                */
+    float clip_low;                /* ppo_clip_eps_low                        */
+    float clip_high;               /* ppo_clip_eps_high                       */
+    float tis_min;
+    float tis_max;
+    float positive_lm_coef;
+    int32_t adv_per_token;
+    int32_t use_tis;
+    int32_t use_icepop;
+    int32_t per_token_loss;        /* calculate_per_token_loss                */
+    int32_t train_lp_is_old;       /* old_logprobs_source == "train"          */
+    int32_t cp_degree;
+    int32_t reserved;
+    void* workspace;
+    size_t workspace_bytes;
+} meshy_ppo_args;
+
+/* Segment structure of a doc_ids tensor whose flattened values are
+ * non-decreasing (both batch layouts, batch.py:123, 150-162):
+ * seg_offsets[d] = number of tokens with id < d, for d in [0, n_slots].
+ * unsorted (nullable, device int32) is set to 1 when some doc_ids[i] >
+ * doc_ids[i+1]; the caller clears it beforehand. */
+int meshy_segment_offsets(const int64_t* doc_ids, int64_t n_tokens, int64_t n_slots,
+                          int64_t* seg_offsets, int32_t* unsorted, hipStream_t stream);
+
+size_t meshy_ppo_workspace_size(int64_t n_tokens, int64_t n_docs);
+/* out: [MESHY_PPO_NOUT] fp32 (device).  seg_cnt: [n_docs + 1] fp32 (device),
+ * the per-document masked token counts the backward needs. */
+int meshy_ppo_loss_fwd(const meshy_ppo_args* args, float* out, float* seg_cnt,
+                       hipStream_t stream);
+/* grad_new[i] = d(total loss)/d new_lp[i] * grad_loss[0]  (grad_loss is a
+ * device scalar), matching torch autograd through trainer.py:751-809. */
+int meshy_ppo_loss_bwd(const meshy_ppo_args* args, const float* seg_cnt,
+                       const float* grad_loss, float* grad_new, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Segment-aware GAE and returns as a reverse affine scan (device).
+ * Replaces compute_vapo_gae (meshy/backend/titan/critic/gae.py:208-293) and
+ * compute_returns (gae.py:183-205), whose definition is the sequential loop
+ * _reverse_scan_reference (gae.py:162-180) with the continuation rule of
+ * _continuation_mask (gae.py:77-93) and the lambda rule of _lambda_per_doc
+ * (gae.py:70-74).
+ *
+ * Inputs are [rows, S] row-major.  doc_ids in [0, n_docs] (n_docs = padding
+ * slot).  values are fp32 (values_bf16 = 0) or bf16 (values_bf16 = 1).
+ * lengths ([n_docs] fp32) may be NULL: each document's masked count is used.
+ * Outputs: adv [rows*S] (nullable), returns [rows*S] (nullable, decay gamma),
+ * lam_doc [n_docs] (nullable).
+ * ---------------------------------------------------------------------- */
+typedef struct meshy_gae_args {
+    const float* rewards;
+    const void* values;            /* nullable when adv is NULL               */
+    const float* mask;
+    const int64_t* doc_ids;
+    const float* lengths;
+    int64_t rows;
+    int64_t S;
+    int64_t n_docs;
+    float gamma;
+    float alpha;
+    float epsilon;
+    int32_t values_bf16;
+    float* adv;
+    float* returns;
+    float* lam_doc;
+    void* workspace;
+    size_t workspace_bytes;
+} meshy_gae_args;
+
+size_t meshy_gae_workspace_size(int64_t rows, int64_t S, int64_t n_docs);
+int meshy_gae(const meshy_gae_args* args, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Masked global whitening of per-token advantages (device).
+ * Replaces the arithmetic of whiten_advantages (meshy/backend/titan/vapo.py:6-32):
+ * fp64 sum / sum of squares / count over tokens with mask != 0, unbiased
+ * variance (count >= 2), x <- (x - mean) * rsqrt(var + 1e-8) on the mask and
+ * 0 elsewhere.  stats (device, [3] fp64) receives (sum, sumsq, count) before
+ * the apply; `replication` divides them as the reference does before its
+ * all-reduce.  Two phases so a caller can all-reduce `stats` in between:
+ * meshy_whiten_stats then meshy_whiten_apply.
+ * ---------------------------------------------------------------------- */
+size_t meshy_whiten_workspace_size(int64_t n);
+int meshy_whiten_stats(const float* adv, const float* mask, int64_t n, double replication,
+                       double* stats, void* workspace, size_t workspace_bytes,
+                       hipStream_t stream);
+int meshy_whiten_apply(float* adv, const float* mask, int64_t n, const double* stats,
+                       hipStream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* MESHY_AMD_H */

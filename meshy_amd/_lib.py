@@ -1,0 +1,246 @@
+"""ctypes binding of libmeshy_amd.so (declared in include/meshy_amd.h).
+
+The library is the only compute path of this package: every public function
+routes through it, and loading fails loudly when the shared object has not
+been built (``python -c "import __graft_entry__ as g; g.build()"``).
+"""
+
+from __future__ import annotations
+
+import ctypes
+import os
+from ctypes import POINTER, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+
+LIB_NAME = "libmeshy_amd.so"
+LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
+
+MESHY_LAYOUT_PADDED = 0
+MESHY_LAYOUT_PACKED = 1
+
+# enum meshy_ppo_out
+PPO_OUT_NAMES = (
+    "loss",
+    "total_loss",
+    "positive_lm_loss",
+    "tis_ratio_sum",
+    "ratio_sum",
+    "clip_sum",
+    "tis_masked_sum",
+    "token_count",
+    "ppo_kl_sum",
+    "log_ratio_abs_sum",
+    "ess_sum",
+    "doc_count",
+    "train_rollout_kl_sum",
+    "train_rollout_logdiff_abs_sum",
+    "entropy_sum",
+)
+PPO_NOUT = len(PPO_OUT_NAMES)
+
+
+class PlannerCfg(ctypes.Structure):
+    _fields_ = [
+        ("layout", c_int32),
+        ("reserved", c_int32),
+        ("mini_batch_size", c_int64),
+        ("seq_len", c_int64),
+        ("align", c_int64),
+        ("max_tokens_per_micro", c_int64),
+        ("micro_batch_size", c_int64),
+    ]
+
+
+class PlanOut(ctypes.Structure):
+    _fields_ = [
+        ("local_indices", POINTER(c_int32)),
+        ("mini_n_micro", POINTER(c_int32)),
+        ("mini_n_docs_global", POINTER(c_int64)),
+        ("mini_n_tokens_global", POINTER(c_int64)),
+        ("mini_tokens_per_rank", POINTER(c_int64)),
+        ("micro_seq_len", POINTER(c_int64)),
+        ("micro_doc_start", POINTER(c_int32)),
+        ("doc_sample", POINTER(c_int32)),
+        ("doc_len", POINTER(c_int64)),
+        ("n_micro_total", c_int32),
+        ("reserved", c_int32),
+    ]
+
+
+class PackArgs(ctypes.Structure):
+    _fields_ = [
+        ("tokens", c_void_p),
+        ("tokens_elem_bytes", c_int32),
+        ("layout", c_int32),
+        ("mask", c_void_p),
+        ("logprobs", c_void_p),
+        ("adv_tokens", c_void_p),
+        ("adv_samples", c_void_p),
+        ("sample_offsets", c_void_p),
+        ("n_samples", c_int64),
+        ("n_micro", c_int64),
+        ("micro_seq_len", c_void_p),
+        ("micro_out_off", c_void_p),
+        ("micro_doc_start", c_void_p),
+        ("doc_sample", c_void_p),
+        ("doc_len", c_void_p),
+        ("max_micro_elems", c_int64),
+        ("max_docs_per_micro", c_int64),
+        ("input_ids", c_void_p),
+        ("labels", c_void_p),
+        ("positions", c_void_p),
+        ("mask_out", c_void_p),
+        ("doc_ids", c_void_p),
+        ("rollout_lp", c_void_p),
+        ("adv_tok", c_void_p),
+        ("adv_doc", c_void_p),
+        ("doc_len_out", c_void_p),
+        ("cu_seqlens", c_void_p),
+    ]
+
+
+class PpoArgs(ctypes.Structure):
+    _fields_ = [
+        ("new_lp", c_void_p),
+        ("old_lp", c_void_p),
+        ("mask", c_void_p),
+        ("rollout_lp", c_void_p),
+        ("entropy", c_void_p),
+        ("adv", c_void_p),
+        ("positive_lm_weights", c_void_p),
+        ("seg_offsets", c_void_p),
+        ("n_tokens", c_int64),
+        ("n_docs", c_int64),
+        ("n_docs_global", c_int64),
+        ("n_tokens_global", c_int64),
+        ("clip_low", c_float),
+        ("clip_high", c_float),
+        ("tis_min", c_float),
+        ("tis_max", c_float),
+        ("positive_lm_coef", c_float),
+        ("adv_per_token", c_int32),
+        ("use_tis", c_int32),
+        ("use_icepop", c_int32),
+        ("per_token_loss", c_int32),
+        ("train_lp_is_old", c_int32),
+        ("cp_degree", c_int32),
+        ("reserved", c_int32),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
+    ]
+
+
+class GaeArgs(ctypes.Structure):
+    _fields_ = [
+        ("rewards", c_void_p),
+        ("values", c_void_p),
+        ("mask", c_void_p),
+        ("doc_ids", c_void_p),
+        ("lengths", c_void_p),
+        ("rows", c_int64),
+        ("S", c_int64),
+        ("n_docs", c_int64),
+        ("gamma", c_float),
+        ("alpha", c_float),
+        ("epsilon", c_float),
+        ("values_bf16", c_int32),
+        ("adv", c_void_p),
+        ("returns", c_void_p),
+        ("lam_doc", c_void_p),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
+    ]
+
+
+# name -> (restype, argtypes); every symbol include/meshy_amd.h declares.
+SIGNATURES = {
+    "meshy_last_error": (ctypes.c_char_p, []),
+    "meshy_abi_version": (c_int, []),
+    "meshy_plan_build": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int64, POINTER(PlannerCfg), POINTER(PlanOut)],
+    ),
+    "meshy_pack_micro_batches": (c_int, [POINTER(PackArgs), c_void_p]),
+    "meshy_grpo_advantage": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "meshy_logprob_entropy_fwd": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p],
+    ),
+    "meshy_logprob_bwd": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p],
+    ),
+    "meshy_segment_offsets": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
+    "meshy_ppo_workspace_size": (c_size_t, [c_int64, c_int64]),
+    "meshy_ppo_loss_fwd": (c_int, [POINTER(PpoArgs), c_void_p, c_void_p, c_void_p]),
+    "meshy_ppo_loss_bwd": (c_int, [POINTER(PpoArgs), c_void_p, c_void_p, c_void_p, c_void_p]),
+    "meshy_gae_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
+    "meshy_gae": (c_int, [POINTER(GaeArgs), c_void_p]),
+    "meshy_whiten_workspace_size": (c_size_t, [c_int64]),
+    "meshy_whiten_stats": (
+        c_int, [c_void_p, c_void_p, c_int64, c_double, c_void_p, c_void_p, c_size_t, c_void_p]
+    ),
+    "meshy_whiten_apply": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+}
+
+ABI_VERSION = 1
+
+_LIB: ctypes.CDLL | None = None
+
+
+class MeshyError(RuntimeError):
+    """A HIP error raised by a launch inside libmeshy_amd."""
+
+
+def load() -> ctypes.CDLL:
+    """Load libmeshy_amd.so once; raise if it is missing or stale."""
+    global _LIB
+    if _LIB is not None:
+        return _LIB
+    if not os.path.exists(LIB_PATH):
+        raise ImportError(
+            f"{LIB_PATH} is not built; run __graft_entry__.build() (hipcc --offload-arch=gfx950)"
+        )
+    lib = ctypes.CDLL(LIB_PATH)
+    for name, (res, args) in SIGNATURES.items():
+        fn = getattr(lib, name)
+        fn.restype = res
+        fn.argtypes = args
+    if lib.meshy_abi_version() != ABI_VERSION:
+        raise ImportError(f"{LIB_PATH} has ABI {lib.meshy_abi_version()}, expected {ABI_VERSION}")
+    _LIB = lib
+    return lib
+
+
+def check(rc: int, what: str) -> None:
+    """Raise the Python error matching a C-ABI return code."""
+    if rc == 0:
+        return
+    msg = load().meshy_last_error().decode(errors="replace") or what
+    if rc < 0:
+        raise ValueError(msg)
+    raise MeshyError(f"{what}: {msg} (hip error {rc})")
+
+
+def ptr(t) -> int | None:
+    """Device (or host) address of a tensor, or None."""
+    if t is None:
+        return None
+    return t.data_ptr()
+
+
+def stream_of(device) -> int:
+    """The current HIP stream of `device` as an integer handle."""
+    import torch
+
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def require_gpu(*tensors) -> None:
+    """Every kernel entry point runs on a HIP device; CPU tensors are an error."""
+    for t in tensors:
+        if t is not None and not t.is_cuda:
+            raise ValueError(
+                "meshy_amd kernels run on the GPU; got a CPU tensor (move inputs to a HIP device)"
+            )

@@ -1,0 +1,37 @@
+// Error reporting and version entry points of libmeshy_amd.
+#include <stdarg.h>
+#include <stdio.h>
+
+#include <hip/hip_runtime.h>
+
+#include "common.h"
+
+namespace meshy {
+
+namespace {
+thread_local char g_last_error[512] = {0};
+}
+
+int set_error(int code, const char* fmt, ...) {
+    va_list ap;
+    va_start(ap, fmt);
+    vsnprintf(g_last_error, sizeof(g_last_error), fmt, ap);
+    va_end(ap);
+    return code;
+}
+
+void clear_error() { g_last_error[0] = 0; }
+
+int check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) {
+        return set_error(static_cast<int>(e), "%s: %s", what, hipGetErrorString(e));
+    }
+    return MESHY_OK;
+}
+
+}  // namespace meshy
+
+extern "C" const char* meshy_last_error(void) { return meshy::g_last_error; }
+
+extern "C" int meshy_abi_version(void) { return 1; }

@@ -1,0 +1,409 @@
+// Segment-aware GAE / returns as a reverse affine scan, and masked whitening,
+// for gfx950.
+//
+// The recursion of _reverse_scan_reference (meshy/backend/titan/critic/gae.py:162-180)
+//     A_t = x_t + decay_t * cont_t * A_{t+1},   A = 0 outside valid
+// is a composition of affine maps f_t(A) = a_t * A + b_t with a_t = decay_t *
+// cont_t and b_t = x_t (zero outside valid).  cont_t (gae.py:77-93) is 0 at
+// the end of each row, at a document change and at a mask hole, so the whole
+// [rows, S] grid is one flattened sequence and no segment bookkeeping is
+// needed beyond a_t = 0.  Maps compose as (p1, q1) o (p2, q2) = (p1 p2, q1 + p1 q2):
+//   k_gae_count  masked token count per document (index_add, gae.py:264-269),
+//                only when lengths are not given;
+//   k_gae_chunks each workgroup folds a chunk of kChunk tokens into one map
+//                per scan (advantages and returns);
+//   k_gae_carry  one workgroup scans the chunk maps from the right and emits
+//                each chunk's carry-in, plus lambda per document (gae.py:70-74);
+//   k_gae_apply  each workgroup re-folds its chunk, scans its threads from the
+//                right seeded with the carry, and writes A_t and G_t.
+// Everything is fp32, like the reference's sequential fallback.
+#include <algorithm>
+
+#include "common.h"
+
+namespace meshy {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kItems = 16;
+constexpr int64_t kChunk = static_cast<int64_t>(kThreads) * kItems;
+constexpr int kCarryThreads = 1024;
+constexpr int kCountThreads = 256;
+constexpr int kCountItems = 16;
+
+struct Aff {
+    float p, q;  // A_before = p * A_after + q
+};
+
+// left covers earlier positions than right.
+__device__ __forceinline__ Aff compose(Aff left, Aff right) {
+    return Aff{left.p * right.p, fmaf(left.p, right.q, left.q)};
+}
+
+struct Pair {
+    Aff adv, ret;
+};
+__device__ __forceinline__ Pair compose(const Pair& l, const Pair& r) {
+    return Pair{compose(l.adv, r.adv), compose(l.ret, r.ret)};
+}
+__device__ __forceinline__ Pair identity_pair() { return Pair{Aff{1.f, 0.f}, Aff{1.f, 0.f}}; }
+
+__device__ __forceinline__ Pair shfl_down_pair(const Pair& v, int off) {
+    return Pair{Aff{__shfl_down(v.adv.p, off, kWave), __shfl_down(v.adv.q, off, kWave)},
+                Aff{__shfl_down(v.ret.p, off, kWave), __shfl_down(v.ret.q, off, kWave)}};
+}
+
+struct Workspace {
+    float* cnt;     // [n_docs + 1]
+    Pair* chunk;    // [n_chunks]
+    float* carry;   // [n_chunks][2]: A and G right after the chunk
+};
+
+int64_t n_chunks_of(int64_t n) { return (n + kChunk - 1) / kChunk; }
+
+size_t ws_bytes(int64_t n, int64_t n_docs) {
+    const int64_t nc = n_chunks_of(n);
+    return align_up(sizeof(float) * (n_docs + 1), 256) + align_up(sizeof(Pair) * nc, 256) +
+           align_up(sizeof(float) * 2 * nc, 256);
+}
+
+Workspace ws_of(void* base, int64_t n, int64_t n_docs) {
+    const int64_t nc = n_chunks_of(n);
+    char* p = static_cast<char*>(base);
+    Workspace w;
+    w.cnt = reinterpret_cast<float*>(p);
+    p += align_up(sizeof(float) * (n_docs + 1), 256);
+    w.chunk = reinterpret_cast<Pair*>(p);
+    p += align_up(sizeof(Pair) * nc, 256);
+    w.carry = reinterpret_cast<float*>(p);
+    return w;
+}
+
+__device__ __forceinline__ float lambda_of(float L, float alpha, float epsilon) {
+    // _lambda_per_doc: clamp(1 - 1/(alpha * max(L, 1)), 0, 1 - epsilon)
+    const float lam = 1.f - 1.f / (alpha * fmaxf(L, 1.f));
+    return fminf(fmaxf(lam, 0.f), 1.f - epsilon);
+}
+
+__device__ __forceinline__ float doc_length(const meshy_gae_args& g, const float* cnt, int64_t d) {
+    return g.lengths ? g.lengths[d] : cnt[d];
+}
+
+__device__ __forceinline__ float value_at(const meshy_gae_args& g, int64_t t) {
+    if (!g.values) return 0.f;
+    if (g.values_bf16) return bf16_to_f32(static_cast<const uint16_t*>(g.values)[t]);
+    return static_cast<const float*>(g.values)[t];
+}
+
+// The two affine maps of position t.
+__device__ __forceinline__ Pair token_maps(const meshy_gae_args& g, const float* cnt, int64_t t) {
+    const int64_t row = t / g.S;
+    const int64_t s = t - row * g.S;
+    const float mk = g.mask[t];
+    const bool valid = mk > 0.f;
+    const int64_t d = g.doc_ids[t];
+    bool cont = false;
+    float vn = 0.f;
+    if (s + 1 < g.S) {
+        cont = valid && g.doc_ids[t + 1] == d && g.mask[t + 1] > 0.f;
+        vn = value_at(g, t + 1);
+    }
+    const float contf = cont ? 1.f : 0.f;
+    const float validf = valid ? 1.f : 0.f;
+    const float r = g.rewards[t];
+    // lambda of the document; the padding slot (and any id outside [0, n_docs)) gets 0.
+    const float lam = (d >= 0 && d < g.n_docs) ? lambda_of(doc_length(g, cnt, d), g.alpha, g.epsilon) : 0.f;
+    const float v = value_at(g, t);
+    const float delta = (r + g.gamma * vn * contf - v) * validf;
+    Pair m;
+    m.adv = Aff{(g.gamma * lam) * contf, valid ? delta : 0.f};
+    m.ret = Aff{g.gamma * contf, valid ? r : 0.f};
+    return m;
+}
+
+// Suffix composition across the block: returns, for each thread, the map of
+// all items of the threads after it (exclusive), and the block total.
+__device__ __forceinline__ Pair block_suffix_exclusive(Pair mine, Pair* s_wave, Pair& total) {
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+    constexpr int kW = kThreads / kWave;
+    Pair incl = mine;  // becomes compose(mine, ..., last lane of the wave)
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const Pair other = shfl_down_pair(incl, off);
+        if (lane + off < kWave) incl = compose(incl, other);
+    }
+    if (lane == 0) s_wave[wid] = incl;  // whole-wave map
+    __syncthreads();
+    Pair after_wave = identity_pair();
+    for (int w = kW - 1; w > wid; --w) after_wave = compose(s_wave[w], after_wave);
+    total = identity_pair();
+    for (int w = kW - 1; w >= 0; --w) total = compose(s_wave[w], total);
+    __syncthreads();
+    // exclusive within the wave = inclusive of the next lane.
+    Pair next = shfl_down_pair(incl, 1);
+    Pair excl = (lane + 1 < kWave) ? compose(next, after_wave) : after_wave;
+    return excl;
+}
+
+__global__ __launch_bounds__(kThreads) void k_gae_zero(float* p, int64_t n) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i < n) p[i] = 0.f;
+}
+
+__global__ __launch_bounds__(kCountThreads) void k_gae_count(meshy_gae_args g, float* cnt, int64_t n) {
+    const int64_t t0 = (static_cast<int64_t>(blockIdx.x) * kCountThreads + threadIdx.x) * kCountItems;
+    if (t0 >= n) return;
+    const int64_t t1 = min(t0 + kCountItems, n);
+    int64_t cur = g.doc_ids[t0];
+    float acc = 0.f;
+    for (int64_t t = t0; t < t1; ++t) {
+        const int64_t d = g.doc_ids[t];
+        if (d != cur) {
+            if (cur >= 0 && cur <= g.n_docs && acc != 0.f) atomicAdd(cnt + cur, acc);
+            cur = d;
+            acc = 0.f;
+        }
+        acc += g.mask[t];
+    }
+    if (cur >= 0 && cur <= g.n_docs && acc != 0.f) atomicAdd(cnt + cur, acc);
+}
+
+// Loads the thread's items (contiguous) and folds them right to left.
+__device__ __forceinline__ Pair load_items(const meshy_gae_args& g, const float* cnt, int64_t t0, int64_t n,
+                                           Pair (&items)[kItems]) {
+    Pair agg = identity_pair();
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+        const int64_t t = t0 + k;
+        items[k] = (t < n) ? token_maps(g, cnt, t) : identity_pair();
+    }
+#pragma unroll
+    for (int k = kItems - 1; k >= 0; --k) agg = compose(items[k], agg);
+    return agg;
+}
+
+__global__ __launch_bounds__(kThreads) void k_gae_chunks(meshy_gae_args g, Workspace ws, int64_t n) {
+    __shared__ Pair s_wave[kThreads / kWave];
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kChunk + static_cast<int64_t>(threadIdx.x) * kItems;
+    Pair items[kItems];
+    const Pair mine = load_items(g, ws.cnt, t0, n, items);
+    Pair total;
+    (void)block_suffix_exclusive(mine, s_wave, total);
+    if (threadIdx.x == 0) ws.chunk[blockIdx.x] = total;
+}
+
+__global__ __launch_bounds__(kCarryThreads) void k_gae_carry(meshy_gae_args g, Workspace ws, int64_t n_chunks) {
+    __shared__ Pair s_wave[kCarryThreads / kWave];
+    // Lambda per document (gae.py:271-275), reported to the caller.
+    if (g.lam_doc) {
+        for (int64_t d = threadIdx.x; d < g.n_docs; d += kCarryThreads)
+            g.lam_doc[d] = lambda_of(doc_length(g, ws.cnt, d), g.alpha, g.epsilon);
+    }
+    // Each thread owns a contiguous run of chunks.
+    const int64_t per = (n_chunks + kCarryThreads - 1) / kCarryThreads;
+    const int64_t c0 = static_cast<int64_t>(threadIdx.x) * per;
+    const int64_t c1 = min(c0 + per, n_chunks);
+    Pair mine = identity_pair();
+    for (int64_t c = c1 - 1; c >= c0; --c) mine = compose(ws.chunk[c], mine);
+    // Block-wide suffix scan over the threads' runs (1024 threads = 16 waves).
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+    constexpr int kW = kCarryThreads / kWave;
+    Pair incl = mine;
+#pragma unroll
+    for (int off = 1; off < kWave; off <<= 1) {
+        const Pair other = shfl_down_pair(incl, off);
+        if (lane + off < kWave) incl = compose(incl, other);
+    }
+    if (lane == 0) s_wave[wid] = incl;
+    __syncthreads();
+    Pair after_wave = identity_pair();
+    for (int w = kW - 1; w > wid; --w) after_wave = compose(s_wave[w], after_wave);
+    const Pair next = shfl_down_pair(incl, 1);
+    const Pair excl = (lane + 1 < kWave) ? compose(next, after_wave) : after_wave;
+    // The sequence ends with A = G = 0, so the carry after this run is excl applied to 0.
+    float a = excl.adv.q;
+    float r = excl.ret.q;
+    for (int64_t c = c1 - 1; c >= c0; --c) {
+        ws.carry[2 * c] = a;
+        ws.carry[2 * c + 1] = r;
+        const Pair m = ws.chunk[c];
+        a = fmaf(m.adv.p, a, m.adv.q);
+        r = fmaf(m.ret.p, r, m.ret.q);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Workspace ws, int64_t n) {
+    __shared__ Pair s_wave[kThreads / kWave];
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kChunk + static_cast<int64_t>(threadIdx.x) * kItems;
+    Pair items[kItems];
+    const Pair mine = load_items(g, ws.cnt, t0, n, items);
+    Pair total;
+    const Pair excl = block_suffix_exclusive(mine, s_wave, total);
+    const float ca = ws.carry[2 * blockIdx.x];
+    const float cr = ws.carry[2 * blockIdx.x + 1];
+    float A = fmaf(excl.adv.p, ca, excl.adv.q);
+    float G = fmaf(excl.ret.p, cr, excl.ret.q);
+#pragma unroll
+    for (int k = kItems - 1; k >= 0; --k) {
+        const int64_t t = t0 + k;
+        A = fmaf(items[k].adv.p, A, items[k].adv.q);
+        G = fmaf(items[k].ret.p, G, items[k].ret.q);
+        if (t < n) {
+            if (g.adv) g.adv[t] = A;
+            if (g.returns) g.returns[t] = G;
+        }
+    }
+}
+
+// ---------------------------------------------------------------- whitening
+constexpr int kWhitenThreads = 256;
+constexpr int kWhitenBlocks = 1024;
+
+struct Stats3 {
+    double s, q, c;
+};
+
+__global__ __launch_bounds__(kWhitenThreads) void k_whiten_partial(const float* __restrict__ adv,
+                                                                   const float* __restrict__ mask, int64_t n,
+                                                                   double* __restrict__ partial) {
+    __shared__ double scratch[kWhitenThreads / kWave];
+    double s = 0.0, q = 0.0, c = 0.0;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kWhitenThreads + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kWhitenThreads) {
+        if (mask[i] != 0.f) {
+            const double x = adv[i];
+            s += x;
+            q += x * x;
+            c += 1.0;
+        }
+    }
+    s = block_sum<kWhitenThreads>(s, scratch);
+    q = block_sum<kWhitenThreads>(q, scratch);
+    c = block_sum<kWhitenThreads>(c, scratch);
+    if (threadIdx.x == 0) {
+        partial[3 * blockIdx.x + 0] = s;
+        partial[3 * blockIdx.x + 1] = q;
+        partial[3 * blockIdx.x + 2] = c;
+    }
+}
+
+__global__ __launch_bounds__(kWhitenThreads) void k_whiten_final(const double* __restrict__ partial, int nb,
+                                                                 double replication, double* __restrict__ stats) {
+    __shared__ double scratch[kWhitenThreads / kWave];
+    double v[3] = {0.0, 0.0, 0.0};
+    for (int b = threadIdx.x; b < nb; b += kWhitenThreads) {
+        v[0] += partial[3 * b + 0];
+        v[1] += partial[3 * b + 1];
+        v[2] += partial[3 * b + 2];
+    }
+#pragma unroll
+    for (int k = 0; k < 3; ++k) v[k] = block_sum<kWhitenThreads>(v[k], scratch);
+    if (threadIdx.x == 0) {
+        stats[0] = v[0] / replication;
+        stats[1] = v[1] / replication;
+        stats[2] = v[2] / replication;
+    }
+}
+
+__global__ __launch_bounds__(kWhitenThreads) void k_whiten_apply(float* __restrict__ adv,
+                                                                 const float* __restrict__ mask, int64_t n,
+                                                                 const double* __restrict__ stats) {
+    // vapo.py:25-32: mean, clamped variance, Bessel factor when count >= 2.
+    const double total = stats[0], squares = stats[1], count = stats[2];
+    const double cnt = fmax(count, 1.0);
+    const double mean = total / cnt;
+    double var = fmax(squares / cnt - mean * mean, 0.0);
+    if (count >= 2.0) var *= count / (count - 1.0);
+    const float mean_f = static_cast<float>(mean);
+    const float scale = rsqrtf(static_cast<float>(var) + 1e-8f);
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kWhitenThreads + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kWhitenThreads) {
+        adv[i] = (mask[i] != 0.f) ? (adv[i] - mean_f) * scale : 0.f;
+    }
+}
+
+}  // namespace
+}  // namespace meshy
+
+extern "C" size_t meshy_gae_workspace_size(int64_t rows, int64_t S, int64_t n_docs) {
+    if (rows < 0 || S < 0 || n_docs < 0) return 0;
+    return meshy::ws_bytes(rows * S, n_docs);
+}
+
+extern "C" int meshy_gae(const meshy_gae_args* args, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    if (!args) return set_error(MESHY_ENULL, "meshy_gae: args is NULL");
+    const meshy_gae_args& g = *args;
+    if (g.rows < 0 || g.S < 0 || g.n_docs < 0) return set_error(MESHY_EINVAL, "meshy_gae: negative sizes");
+    const int64_t n = g.rows * g.S;
+    if (!g.rewards || !g.mask || !g.doc_ids) return set_error(MESHY_ENULL, "meshy_gae: rewards, mask and doc_ids are required");
+    if (g.adv && !g.values) return set_error(MESHY_ENULL, "meshy_gae: advantages need values");
+    if (!(g.alpha > 0.f)) return set_error(MESHY_EINVAL, "meshy_gae: alpha must be positive");
+    if (!g.workspace || g.workspace_bytes < ws_bytes(n, g.n_docs))
+        return set_error(MESHY_ESPACE, "meshy_gae: workspace needs %zu bytes", ws_bytes(n, g.n_docs));
+    const int64_t nc = n_chunks_of(n);
+    if (nc > INT32_MAX) return set_error(MESHY_EINVAL, "meshy_gae: too many tokens");
+    const Workspace ws = ws_of(g.workspace, n, g.n_docs);
+    int rc;
+    if (!g.lengths) {
+        const int64_t nz = g.n_docs + 1;
+        hipLaunchKernelGGL(k_gae_zero, dim3(static_cast<unsigned>(ceil_div(nz, kThreads))), dim3(kThreads), 0, stream,
+                           ws.cnt, nz);
+        if ((rc = check_launch("meshy_gae(zero)"))) return rc;
+        if (n > 0) {
+            const int64_t per = static_cast<int64_t>(kCountThreads) * kCountItems;
+            hipLaunchKernelGGL(k_gae_count, dim3(static_cast<unsigned>(ceil_div(n, per))), dim3(kCountThreads), 0,
+                               stream, g, ws.cnt, n);
+            if ((rc = check_launch("meshy_gae(count)"))) return rc;
+        }
+    }
+    if (nc > 0) {
+        hipLaunchKernelGGL(k_gae_chunks, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n);
+        if ((rc = check_launch("meshy_gae(chunks)"))) return rc;
+    }
+    hipLaunchKernelGGL(k_gae_carry, dim3(1), dim3(kCarryThreads), 0, stream, g, ws, nc);
+    if ((rc = check_launch("meshy_gae(carry)"))) return rc;
+    if (nc > 0 && (g.adv || g.returns)) {
+        hipLaunchKernelGGL(k_gae_apply, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n);
+        if ((rc = check_launch("meshy_gae(apply)"))) return rc;
+    }
+    return MESHY_OK;
+}
+
+extern "C" size_t meshy_whiten_workspace_size(int64_t n) {
+    (void)n;
+    return sizeof(double) * 3 * meshy::kWhitenBlocks;
+}
+
+extern "C" int meshy_whiten_stats(const float* adv, const float* mask, int64_t n, double replication, double* stats,
+                                  void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    if (n < 0) return set_error(MESHY_EINVAL, "meshy_whiten_stats: negative size");
+    if (!stats || !workspace || (n > 0 && (!adv || !mask)))
+        return set_error(MESHY_ENULL, "meshy_whiten_stats: NULL pointer");
+    if (workspace_bytes < meshy_whiten_workspace_size(n))
+        return set_error(MESHY_ESPACE, "meshy_whiten_stats: workspace needs %zu bytes", meshy_whiten_workspace_size(n));
+    if (!(replication > 0.0)) return set_error(MESHY_EINVAL, "meshy_whiten_stats: replication must be positive");
+    const int nb = static_cast<int>(std::min<int64_t>(kWhitenBlocks, std::max<int64_t>(1, ceil_div(n, kWhitenThreads))));
+    double* partial = static_cast<double*>(workspace);
+    hipLaunchKernelGGL(k_whiten_partial, dim3(nb), dim3(kWhitenThreads), 0, stream, adv, mask, n, partial);
+    int rc = check_launch("meshy_whiten_stats(partial)");
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_whiten_final, dim3(1), dim3(kWhitenThreads), 0, stream, partial, nb, replication, stats);
+    return check_launch("meshy_whiten_stats(final)");
+}
+
+extern "C" int meshy_whiten_apply(float* adv, const float* mask, int64_t n, const double* stats, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    if (n < 0) return set_error(MESHY_EINVAL, "meshy_whiten_apply: negative size");
+    if (n == 0) return MESHY_OK;
+    if (!adv || !mask || !stats) return set_error(MESHY_ENULL, "meshy_whiten_apply: NULL pointer");
+    const int nb = static_cast<int>(std::min<int64_t>(kWhitenBlocks, ceil_div(n, kWhitenThreads)));
+    hipLaunchKernelGGL(k_whiten_apply, dim3(nb), dim3(kWhitenThreads), 0, stream, adv, mask, n, stats);
+    return check_launch("meshy_whiten_apply");
+}

@@ -1,0 +1,420 @@
+// Fused packed log_softmax + gather + entropy over bf16 logits, and its
+// backward, for gfx950.
+//
+// Forward (replaces the chunk loop of TitanTrainer._forward_logprobs,
+// meshy/backend/titan/trainer.py:451-527, i.e. -cross_entropy(z.float(), y)
+// at trainer.py:414-428 and logsumexp(z) - sum(softmax(z) * z) at
+// trainer.py:430-449): one workgroup streams one row of V logits from HBM
+// exactly once with 16-byte loads and keeps, per lane, an online triple
+//     m = running max of z,
+//     s = sum exp(z - m),
+//     t = sum exp(z - m) * (z - m) * log2(e)
+// updated once per register tile (tile max first, then one exp2 per element).
+// Lanes and waves merge their triples; thread 0 writes
+//     lse = m + ln s,  logp = z_y - lse,  H = ln 2 * (log2 s - t / s).
+// The row never leaves registers: no fp32 copy of the logits is made.
+//
+// Backward: grad[r, v] = g[r] * (onehot(y_r)[v] - exp(z[r, v] - lse[r])), bf16.
+#include <hip/hip_bf16.h>
+
+#include "common.h"
+
+namespace meshy {
+namespace {
+
+// Native 4 x u32 vector: what the nontemporal load/store builtins accept.
+typedef unsigned int v4u __attribute__((ext_vector_type(4)));
+
+constexpr float kLog2e = 1.4426950408889634f;
+constexpr float kLn2 = 0.69314718055994531f;
+constexpr float kInit = -1e30f;  // finite "minus infinity": keeps 0 * d finite
+constexpr int64_t kIgnoreIndex = -100;
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Merges (m2, s2, t2) into (m, s, t).
+__device__ __forceinline__ void merge(float& m, float& s, float& t, float m2, float s2, float t2) {
+    const float mn = fmaxf(m, m2);
+    const float d1 = (m - mn) * kLog2e;
+    const float d2 = (m2 - mn) * kLog2e;
+    const float a1 = fast_exp2(d1);
+    const float a2 = fast_exp2(d2);
+    t = a1 * fmaf(d1, s, t) + a2 * fmaf(d2, s2, t2);
+    s = a1 * s + a2 * s2;
+    m = mn;
+}
+
+// Moves the running max to at least `tm`, rescaling s and t.
+__device__ __forceinline__ void raise_max(float& m, float& s, float& t, float tm) {
+    const float mn = fmaxf(m, tm);
+    const float d = (m - mn) * kLog2e;
+    const float a = fast_exp2(d);
+    t = a * fmaf(d, s, t);
+    s = a * s;
+    m = mn;
+}
+
+template <int N>
+__device__ __forceinline__ void unpack(const v4u (&v)[N], float (&z)[N * 8]) {
+#pragma unroll
+    for (int u = 0; u < N; ++u) {
+        z[8 * u + 0] = bf16_lo(v[u].x);
+        z[8 * u + 1] = bf16_hi(v[u].x);
+        z[8 * u + 2] = bf16_lo(v[u].y);
+        z[8 * u + 3] = bf16_hi(v[u].y);
+        z[8 * u + 4] = bf16_lo(v[u].z);
+        z[8 * u + 5] = bf16_hi(v[u].z);
+        z[8 * u + 6] = bf16_lo(v[u].w);
+        z[8 * u + 7] = bf16_hi(v[u].w);
+    }
+}
+
+// Accumulates a full register tile (every element valid).
+template <int K>
+__device__ __forceinline__ void accumulate(const float (&z)[K], float& m, float& s, float& t) {
+    float tm = z[0];
+#pragma unroll
+    for (int i = 1; i < K; ++i) tm = fmaxf(tm, z[i]);
+    raise_max(m, s, t, tm);
+    const float nm = -m * kLog2e;
+    float s0 = 0.f, s1 = 0.f, t0 = 0.f, t1 = 0.f;
+#pragma unroll
+    for (int i = 0; i < K; i += 2) {
+        const float x0 = fmaf(z[i], kLog2e, nm);
+        const float x1 = fmaf(z[i + 1], kLog2e, nm);
+        const float e0 = fast_exp2(x0);
+        const float e1 = fast_exp2(x1);
+        s0 += e0;
+        s1 += e1;
+        t0 = fmaf(e0, x0, t0);
+        t1 = fmaf(e1, x1, t1);
+    }
+    s += s0 + s1;
+    t += t0 + t1;
+}
+
+// Accumulates one element that may be absent.
+__device__ __forceinline__ void accumulate_one(float z, bool ok, float& m, float& s, float& t) {
+    if (!ok) return;
+    raise_max(m, s, t, z);
+    const float x = (z - m) * kLog2e;
+    const float e = fast_exp2(x);
+    s += e;
+    t = fmaf(e, x, t);
+}
+
+// Block-wide merge of the per-lane triples; the result lands in thread 0.
+template <int NT>
+__device__ __forceinline__ void block_merge(float& m, float& s, float& t) {
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float m2 = __shfl_xor(m, off, kWave);
+        const float s2 = __shfl_xor(s, off, kWave);
+        const float t2 = __shfl_xor(t, off, kWave);
+        merge(m, s, t, m2, s2, t2);
+    }
+    if constexpr (NT > kWave) {
+        constexpr int kWaves = NT / kWave;
+        __shared__ float sm[kWaves], ss[kWaves], st[kWaves];
+        const int lane = threadIdx.x % kWave;
+        const int wid = threadIdx.x / kWave;
+        if (lane == 0) {
+            sm[wid] = m;
+            ss[wid] = s;
+            st[wid] = t;
+        }
+        __syncthreads();
+        if (threadIdx.x == 0) {
+#pragma unroll
+            for (int w = 1; w < kWaves; ++w) merge(m, s, t, sm[w], ss[w], st[w]);
+        }
+    }
+}
+
+__device__ __forceinline__ void write_row(int64_t r, float m, float s, float t, float zy, int64_t y,
+                                          int64_t V, bool has_label, float* logp, float* ent,
+                                          float* lse_out) {
+    const float l2s = __log2f(s);
+    const float lse = fmaf(l2s, kLn2, m);
+    if (lse_out) lse_out[r] = lse;
+    if (ent) ent[r] = kLn2 * (l2s - t / s);
+    if (logp) {
+        float v;
+        if (!has_label || y == kIgnoreIndex) v = 0.f;
+        else if (y < 0 || y >= V) v = __builtin_nanf("");
+        else v = zy - lse;
+        logp[r] = v;
+    }
+}
+
+// Vector path: row base 16-byte aligned.  NT threads per row, U 16-byte loads
+// in flight per thread per tile.
+template <int NT, int U>
+__global__ __launch_bounds__(NT) void k_lpe_fwd_vec(const uint16_t* __restrict__ logits, int64_t T,
+                                                    int64_t V, int64_t stride_b, int64_t stride_t,
+                                                    const int64_t* __restrict__ labels,
+                                                    float* __restrict__ logp,
+                                                    float* __restrict__ ent,
+                                                    float* __restrict__ lse_out) {
+    const int64_t r = blockIdx.x;
+    const int64_t b = r / T;
+    const uint16_t* row = logits + b * stride_b + (r - b * T) * stride_t;
+    const v4u* row4 = reinterpret_cast<const v4u*>(row);
+    const int tid = threadIdx.x;
+
+    int64_t y = 0;
+    float zy = 0.f;
+    if (tid == 0 && labels) {
+        y = labels[r];
+        if (y >= 0 && y < V) zy = bf16_to_f32(row[y]);
+    }
+
+    float m = kInit, s = 0.f, t = 0.f;
+    const int64_t n8 = V >> 3;
+    constexpr int64_t kTile = static_cast<int64_t>(NT) * U;
+    const int64_t n_full = n8 / kTile;
+    const v4u* p = row4 + tid;
+    for (int64_t it = 0; it < n_full; ++it, p += kTile) {
+        v4u v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(p + u * NT);
+        float z[U * 8];
+        unpack(v, z);
+        accumulate(z, m, s, t);
+    }
+    // Remaining 16-byte chunks, one at a time.
+    for (int64_t c = n_full * kTile + tid; c < n8; c += NT) {
+        v4u v1[1] = {__builtin_nontemporal_load(row4 + c)};
+        float z[8];
+        unpack(v1, z);
+        accumulate(z, m, s, t);
+    }
+    // Tail elements when V is not a multiple of 8.
+    {
+        const int64_t e = (n8 << 3) + tid;
+        const bool ok = e < V;
+        accumulate_one(ok ? bf16_to_f32(row[e]) : 0.f, ok, m, s, t);
+    }
+
+    block_merge<NT>(m, s, t);
+    if (tid == 0) write_row(r, m, s, t, zy, y, V, labels != nullptr, logp, ent, lse_out);
+}
+
+// Generic path: any alignment and stride, 2-byte coalesced loads.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_lpe_fwd_any(const uint16_t* __restrict__ logits, int64_t T,
+                                                    int64_t V, int64_t stride_b, int64_t stride_t,
+                                                    const int64_t* __restrict__ labels,
+                                                    float* __restrict__ logp,
+                                                    float* __restrict__ ent,
+                                                    float* __restrict__ lse_out) {
+    const int64_t r = blockIdx.x;
+    const int64_t b = r / T;
+    const uint16_t* row = logits + b * stride_b + (r - b * T) * stride_t;
+    const int tid = threadIdx.x;
+    int64_t y = 0;
+    float zy = 0.f;
+    if (tid == 0 && labels) {
+        y = labels[r];
+        if (y >= 0 && y < V) zy = bf16_to_f32(row[y]);
+    }
+    float m = kInit, s = 0.f, t = 0.f;
+    int64_t e = tid;
+    for (; e + 7 * NT < V; e += 8 * NT) {
+        float z[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) z[u] = bf16_to_f32(row[e + u * NT]);
+        accumulate(z, m, s, t);
+    }
+    for (; e < V; e += NT) accumulate_one(bf16_to_f32(row[e]), true, m, s, t);
+    block_merge<NT>(m, s, t);
+    if (tid == 0) write_row(r, m, s, t, zy, y, V, labels != nullptr, logp, ent, lse_out);
+}
+
+__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
+    const __hip_bfloat16 a = __float2bfloat16(lo);
+    const __hip_bfloat16 b = __float2bfloat16(hi);
+    return static_cast<uint32_t>(__bfloat16_as_ushort(a)) |
+           (static_cast<uint32_t>(__bfloat16_as_ushort(b)) << 16);
+}
+
+// Backward, vector path: 16-byte loads of z and 16-byte stores of the gradient.
+template <int NT, int U>
+__global__ __launch_bounds__(NT) void k_lp_bwd_vec(const uint16_t* __restrict__ logits, int64_t T,
+                                                   int64_t V, int64_t stride_b, int64_t stride_t,
+                                                   const int64_t* __restrict__ labels,
+                                                   const float* __restrict__ lse,
+                                                   const float* __restrict__ grad_logp,
+                                                   uint16_t* __restrict__ grad) {
+    const int64_t r = blockIdx.x;
+    const int64_t b = r / T;
+    const uint16_t* row = logits + b * stride_b + (r - b * T) * stride_t;
+    uint16_t* grow = grad + r * V;
+    const v4u* row4 = reinterpret_cast<const v4u*>(row);
+    v4u* grow4 = reinterpret_cast<v4u*>(grow);
+    const int tid = threadIdx.x;
+    const int64_t y = labels[r];
+    const int64_t n8 = V >> 3;
+
+    if (y == kIgnoreIndex || !(y >= 0 && y < V)) {
+        const uint16_t fill = (y == kIgnoreIndex) ? 0 : 0x7fc0;  // 0 or NaN
+        const uint32_t f2 = static_cast<uint32_t>(fill) * 0x10001u;
+        const v4u fv = v4u{f2, f2, f2, f2};
+        for (int64_t c = tid; c < n8; c += NT) grow4[c] = fv;
+        for (int64_t e = (n8 << 3) + tid; e < V; e += NT) grow[e] = fill;
+        return;
+    }
+    const float g = grad_logp[r];
+    const float ng = -g;
+    const float nl = -lse[r] * kLog2e;
+    constexpr int64_t kTile = static_cast<int64_t>(NT) * U;
+    const int64_t n_full = n8 / kTile;
+    for (int64_t it = 0; it < n_full; ++it) {
+        v4u v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(row4 + it * kTile + u * NT + tid);
+        float z[U * 8];
+        unpack(v, z);
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            const int64_t c = it * kTile + u * NT + tid;
+            float q[8];
+#pragma unroll
+            for (int k = 0; k < 8; ++k) q[k] = ng * fast_exp2(fmaf(z[8 * u + k], kLog2e, nl));
+            const uint64_t off = static_cast<uint64_t>(y - (c << 3));
+            if (off < 8) {
+#pragma unroll
+                for (int k = 0; k < 8; ++k)
+                    if (static_cast<uint64_t>(k) == off) q[k] += g;
+            }
+            v4u o;
+            o.x = pack_bf16x2(q[0], q[1]);
+            o.y = pack_bf16x2(q[2], q[3]);
+            o.z = pack_bf16x2(q[4], q[5]);
+            o.w = pack_bf16x2(q[6], q[7]);
+            __builtin_nontemporal_store(o, grow4 + c);
+        }
+    }
+    for (int64_t c = n_full * kTile + tid; c < n8; c += NT) {
+        v4u v1[1] = {__builtin_nontemporal_load(row4 + c)};
+        float z[8];
+        unpack(v1, z);
+        float q[8];
+#pragma unroll
+        for (int k = 0; k < 8; ++k) q[k] = ng * fast_exp2(fmaf(z[k], kLog2e, nl));
+        const uint64_t off = static_cast<uint64_t>(y - (c << 3));
+        if (off < 8) {
+#pragma unroll
+            for (int k = 0; k < 8; ++k)
+                if (static_cast<uint64_t>(k) == off) q[k] += g;
+        }
+        v4u o;
+        o.x = pack_bf16x2(q[0], q[1]);
+        o.y = pack_bf16x2(q[2], q[3]);
+        o.z = pack_bf16x2(q[4], q[5]);
+        o.w = pack_bf16x2(q[6], q[7]);
+        __builtin_nontemporal_store(o, grow4 + c);
+    }
+    for (int64_t e = (n8 << 3) + tid; e < V; e += NT) {
+        float q = ng * fast_exp2(fmaf(bf16_to_f32(row[e]), kLog2e, nl));
+        if (e == y) q += g;
+        grow[e] = __bfloat16_as_ushort(__float2bfloat16(q));
+    }
+}
+
+// Backward, generic path.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_lp_bwd_any(const uint16_t* __restrict__ logits, int64_t T,
+                                                   int64_t V, int64_t stride_b, int64_t stride_t,
+                                                   const int64_t* __restrict__ labels,
+                                                   const float* __restrict__ lse,
+                                                   const float* __restrict__ grad_logp,
+                                                   uint16_t* __restrict__ grad) {
+    const int64_t r = blockIdx.x;
+    const int64_t b = r / T;
+    const uint16_t* row = logits + b * stride_b + (r - b * T) * stride_t;
+    uint16_t* grow = grad + r * V;
+    const int64_t y = labels[r];
+    if (y == kIgnoreIndex || !(y >= 0 && y < V)) {
+        const uint16_t fill = (y == kIgnoreIndex) ? 0 : 0x7fc0;
+        for (int64_t e = threadIdx.x; e < V; e += NT) grow[e] = fill;
+        return;
+    }
+    const float g = grad_logp[r];
+    const float nl = -lse[r] * kLog2e;
+    for (int64_t e = threadIdx.x; e < V; e += NT) {
+        float q = -g * fast_exp2(fmaf(bf16_to_f32(row[e]), kLog2e, nl));
+        if (e == y) q += g;
+        grow[e] = __bfloat16_as_ushort(__float2bfloat16(q));
+    }
+}
+
+constexpr int kFwdThreads = 256;
+constexpr int kFwdUnroll = 4;
+constexpr int kBwdThreads = 256;
+constexpr int kBwdUnroll = 2;
+
+int check_common(const void* logits, int64_t rows, int64_t T, int64_t V, int64_t stride_b,
+                 int64_t stride_t, const char* who) {
+    if (!logits) return set_error(MESHY_ENULL, "%s: logits is NULL", who);
+    if (rows < 0 || T < 0 || V <= 0)
+        return set_error(MESHY_EINVAL, "%s: bad shape rows=%lld T=%lld V=%lld", who,
+                         static_cast<long long>(rows), static_cast<long long>(T),
+                         static_cast<long long>(V));
+    if (stride_b < 0 || stride_t < 0) return set_error(MESHY_EINVAL, "%s: negative stride", who);
+    if (rows * T > INT32_MAX) return set_error(MESHY_EINVAL, "%s: too many rows", who);
+    return MESHY_OK;
+}
+
+bool vector_ok(const void* logits, int64_t stride_b, int64_t stride_t) {
+    return (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (stride_b % 8 == 0) && (stride_t % 8 == 0);
+}
+
+}  // namespace
+}  // namespace meshy
+
+extern "C" int meshy_logprob_entropy_fwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
+                                         int64_t stride_b, int64_t stride_t, const int64_t* labels,
+                                         float* logp, float* entropy, float* lse,
+                                         hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    int rc = check_common(logits, rows, T, V, stride_b, stride_t, "meshy_logprob_entropy_fwd");
+    if (rc) return rc;
+    if (logp && !labels) return set_error(MESHY_ENULL, "meshy_logprob_entropy_fwd: logp needs labels");
+    const int64_t n = rows * T;
+    if (n == 0) return MESHY_OK;
+    const dim3 grid(static_cast<unsigned>(n));
+    if (vector_ok(logits, stride_b, stride_t)) {
+        hipLaunchKernelGGL((k_lpe_fwd_vec<kFwdThreads, kFwdUnroll>), grid, dim3(kFwdThreads), 0, stream,
+                           logits, T, V, stride_b, stride_t, labels, logp, entropy, lse);
+    } else {
+        hipLaunchKernelGGL((k_lpe_fwd_any<kFwdThreads>), grid, dim3(kFwdThreads), 0, stream, logits, T,
+                           V, stride_b, stride_t, labels, logp, entropy, lse);
+    }
+    return check_launch("meshy_logprob_entropy_fwd");
+}
+
+extern "C" int meshy_logprob_bwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
+                                 int64_t stride_b, int64_t stride_t, const int64_t* labels,
+                                 const float* lse, const float* grad_logp, uint16_t* grad_logits,
+                                 hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    int rc = check_common(logits, rows, T, V, stride_b, stride_t, "meshy_logprob_bwd");
+    if (rc) return rc;
+    if (!labels || !lse || !grad_logp || !grad_logits)
+        return set_error(MESHY_ENULL, "meshy_logprob_bwd: labels, lse, grad_logp and grad_logits are required");
+    const int64_t n = rows * T;
+    if (n == 0) return MESHY_OK;
+    const dim3 grid(static_cast<unsigned>(n));
+    if (vector_ok(logits, stride_b, stride_t) && reinterpret_cast<uintptr_t>(grad_logits) % 16 == 0 &&
+        V % 8 == 0) {
+        hipLaunchKernelGGL((k_lp_bwd_vec<kBwdThreads, kBwdUnroll>), grid, dim3(kBwdThreads), 0, stream,
+                           logits, T, V, stride_b, stride_t, labels, lse, grad_logp, grad_logits);
+    } else {
+        hipLaunchKernelGGL((k_lp_bwd_any<kBwdThreads>), grid, dim3(kBwdThreads), 0, stream, logits, T, V,
+                           stride_b, stride_t, labels, lse, grad_logp, grad_logits);
+    }
+    return check_launch("meshy_logprob_bwd");
+}

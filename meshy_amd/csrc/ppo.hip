@@ -1,0 +1,439 @@
+// Token-level clipped PPO loss, its diagnostics and its gradient, for gfx950.
+//
+// Restates TitanTrainer._ppo_clip_loss (meshy/backend/titan/trainer.py:705-848):
+//   r   = exp(new - old)
+//   pg  = -min(r*A, clamp(r, 1-eps_lo, 1+eps_hi)*A)                  (760-764)
+//   IcePop: w = exp(old - rollout); pg = where(lo<=w<=hi, pg, 0) * w    (766-772)
+//   TIS:    pg = where(lo<=r<=hi, pg, 0)                                (773-776)
+//   pg *= mask; positive = -new * w_doc * mask                          (777-785)
+//   per-document sums, token-mean or sequence-mean reduction            (787-809)
+//   diagnostic sums (ratio, clip, KL, ESS, k3, entropy)                 (813-847)
+//
+// Layout: documents are contiguous token ranges given by seg_offsets.  The
+// token axis is cut into tiles of kTile tokens.  A (tile, document) pair with
+// a non-empty overlap is handled by one wavefront; because both tiles and
+// documents are ordered, the overlapping pairs form a monotone staircase and
+// `tile + document` indexes them without collision.
+//   k_ppo_tiles  per pair: 5 per-document partial sums -> workspace[tile+doc];
+//                per tile: 10 token-level partial sums.
+//   k_ppo_final  one workgroup: per-document totals in tile order, then the
+//                loss, ESS and every diagnostic, in a fixed order (no
+//                atomics, so results are bitwise reproducible).
+//   k_ppo_bwd    per token: d(total loss)/d new_lp, as torch autograd gives it
+//                (min splits ties 1/2-1/2, clamp passes on [lo, hi]).
+#include <math.h>
+
+#include <algorithm>
+
+#include "common.h"
+
+namespace meshy {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int64_t kTile = 2048;
+constexpr int kTokSums = 10;  // token-level sums
+constexpr int kSegSums = 5;   // per-document sums: pg, cnt, w, w2, positive
+constexpr int kFinalThreads = 1024;
+
+enum TokSum { TS_TIS = 0, TS_RATIO, TS_CLIP, TS_TIS_MASKED, TS_COUNT, TS_KL, TS_LR_ABS, TS_K3, TS_LOGDIFF, TS_ENT };
+
+struct Workspace {
+    float* tok;  // [n_tiles][kTokSums]
+    float* seg;  // [n_tiles + n_slots][kSegSums]
+};
+
+__host__ __device__ inline int64_t n_tiles_of(int64_t n) { return (n + kTile - 1) / kTile; }
+
+size_t ws_bytes(int64_t n_tokens, int64_t n_docs) {
+    const int64_t nt = n_tiles_of(n_tokens);
+    return align_up(sizeof(float) * nt * kTokSums, 256) + align_up(sizeof(float) * (nt + n_docs + 1) * kSegSums, 256);
+}
+
+Workspace ws_of(void* base, int64_t n_tokens) {
+    const int64_t nt = n_tiles_of(n_tokens);
+    char* p = static_cast<char*>(base);
+    Workspace w;
+    w.tok = reinterpret_cast<float*>(p);
+    w.seg = reinterpret_cast<float*>(p + align_up(sizeof(float) * nt * kTokSums, 256));
+    return w;
+}
+
+// torch semantics: NaN propagates through min and clamp.
+__device__ __forceinline__ float t_min(float a, float b) {
+    if (isnan(a) || isnan(b)) return __builtin_nanf("");
+    return a < b ? a : b;
+}
+__device__ __forceinline__ float t_clamp(float x, float lo, float hi) {
+    if (isnan(x)) return x;
+    return x < lo ? lo : (x > hi ? hi : x);
+}
+__device__ __forceinline__ float nan_to_num(float x) {
+    if (isnan(x)) return 0.f;
+    if (isinf(x)) return x > 0 ? 3.40282347e38f : -3.40282347e38f;
+    return x;
+}
+
+// Largest d in [0, n_slots] with off[d] <= i (off has n_slots + 1 entries).
+__device__ __forceinline__ int64_t doc_of(const int64_t* off, int64_t n_slots, int64_t i) {
+    int64_t lo = 0, hi = n_slots;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (off[mid] <= i) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
+struct TokenTerms {
+    float pg;       // pg_per_token after TIS/IcePop and mask
+    float ratio;
+    float tis_ratio;
+    bool tis_mask;
+};
+
+__device__ __forceinline__ TokenTerms token_terms(const meshy_ppo_args& a, int64_t i, float A, float nw,
+                                                  float ol, float mk, float& log_ratio) {
+    TokenTerms r;
+    log_ratio = nw - ol;
+    const float ratio = expf(log_ratio);
+    const float u = ratio * A;
+    const float c = t_clamp(ratio, 1.f - a.clip_low, 1.f + a.clip_high) * A;
+    float pg = -t_min(u, c);
+    float tis = ratio;
+    bool tm = true;
+    if (a.use_icepop) {
+        tis = expf(ol - a.rollout_lp[i]);
+        tm = (tis >= a.tis_min) && (tis <= a.tis_max);
+        const float weight = tm ? tis : 0.f;
+        pg = (tm ? pg : 0.f) * weight;
+    } else if (a.use_tis) {
+        tm = (ratio >= a.tis_min) && (ratio <= a.tis_max);
+        pg = tm ? pg : 0.f;
+    }
+    r.pg = pg * mk;
+    r.ratio = ratio;
+    r.tis_ratio = tis;
+    r.tis_mask = tm;
+    return r;
+}
+
+__global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Workspace ws) {
+    __shared__ int64_t s_range[2];
+    __shared__ float s_tok[kWaves][kTokSums];
+    const int64_t b = blockIdx.x;
+    const int64_t t0 = b * kTile;
+    const int64_t t1 = min(t0 + kTile, a.n_tokens);
+    const int64_t n_slots = a.n_docs + 1;
+    if (threadIdx.x == 0) {
+        s_range[0] = doc_of(a.seg_offsets, n_slots, t0);
+        s_range[1] = doc_of(a.seg_offsets, n_slots, t1 - 1);
+    }
+    __syncthreads();
+    const int64_t d_first = s_range[0];
+    const int64_t d_last = s_range[1];
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+
+    float acc[kTokSums];
+#pragma unroll
+    for (int k = 0; k < kTokSums; ++k) acc[k] = 0.f;
+
+    for (int64_t d = d_first + wid; d <= d_last; d += kWaves) {
+        const int64_t lo = max(a.seg_offsets[d], t0);
+        const int64_t hi = min(a.seg_offsets[d + 1], t1);
+        if (lo >= hi) continue;
+        const bool real = d < a.n_docs;
+        const float A_doc = (!a.adv_per_token && real) ? a.adv[d] : 0.f;
+        const float w_doc = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
+        float sg[kSegSums] = {0.f, 0.f, 0.f, 0.f, 0.f};
+        for (int64_t i = lo + lane; i < hi; i += kWave) {
+            const float nw = a.new_lp[i];
+            const float ol = a.old_lp[i];
+            const float mk = a.mask[i];
+            const float A = a.adv_per_token ? a.adv[i] : A_doc;
+            float lr;
+            const TokenTerms tt = token_terms(a, i, A, nw, ol, mk, lr);
+            sg[0] += tt.pg;
+            sg[1] += mk;
+            sg[2] += tt.ratio * mk;
+            sg[3] += tt.ratio * tt.ratio * mk;
+            if (a.positive_lm_coef != 0.f) sg[4] += -nw * w_doc * mk;
+            acc[TS_TIS] += tt.tis_ratio * mk;
+            acc[TS_RATIO] += tt.ratio * mk;
+            acc[TS_CLIP] += ((tt.ratio < 1.f - a.clip_low) || (tt.ratio > 1.f + a.clip_high)) ? mk : 0.f * mk;
+            acc[TS_TIS_MASKED] += tt.tis_mask ? 0.f * mk : mk;
+            acc[TS_COUNT] += mk;
+            acc[TS_KL] += -lr * mk;
+            acc[TS_LR_ABS] += fabsf(lr) * mk;
+            if (a.rollout_lp) {
+                const float train_lp = a.train_lp_is_old ? ol : nw;
+                const float diff = a.rollout_lp[i] - train_lp;
+                const float lrt = t_clamp(diff, -10.f, 10.f);
+                const float k3 = expf(lrt) - lrt - 1.f;
+                acc[TS_K3] += nan_to_num(k3) * mk;
+                acc[TS_LOGDIFF] += nan_to_num(fabsf(diff)) * mk;
+            }
+            if (a.entropy) acc[TS_ENT] += a.entropy[i] * mk;
+        }
+#pragma unroll
+        for (int k = 0; k < kSegSums; ++k) sg[k] = wave_sum(sg[k]);
+        if (lane == 0) {
+            float* dst = ws.seg + (b + d) * kSegSums;
+#pragma unroll
+            for (int k = 0; k < kSegSums; ++k) dst[k] = sg[k];
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < kTokSums; ++k) acc[k] = wave_sum(acc[k]);
+    if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < kTokSums; ++k) s_tok[wid][k] = acc[k];
+    }
+    __syncthreads();
+    if (threadIdx.x < kTokSums) {
+        float v = 0.f;
+#pragma unroll
+        for (int w = 0; w < kWaves; ++w) v += s_tok[w][threadIdx.x];
+        ws.tok[b * kTokSums + threadIdx.x] = v;
+    }
+}
+
+__global__ __launch_bounds__(kFinalThreads) void k_ppo_final(meshy_ppo_args a, Workspace ws,
+                                                             float* __restrict__ out,
+                                                             float* __restrict__ seg_cnt_out) {
+    __shared__ double scratch[kFinalThreads / kWave];
+    const int64_t n_slots = a.n_docs + 1;
+    const int64_t n_tiles = n_tiles_of(a.n_tokens);
+    // Per-document totals (tile order) and their contributions.
+    double loss_c = 0.0, pos_c = 0.0, ess_c = 0.0, doc_c = 0.0;
+    for (int64_t d = threadIdx.x; d < n_slots; d += kFinalThreads) {
+        const int64_t lo = a.seg_offsets[d];
+        const int64_t hi = a.seg_offsets[d + 1];
+        float sg[kSegSums] = {0.f, 0.f, 0.f, 0.f, 0.f};
+        if (hi > lo) {
+            const int64_t b0 = lo / kTile;
+            const int64_t b1 = (hi - 1) / kTile;
+            for (int64_t b = b0; b <= b1; ++b) {
+                const float* src = ws.seg + (b + d) * kSegSums;
+#pragma unroll
+                for (int k = 0; k < kSegSums; ++k) sg[k] += src[k];
+            }
+        }
+        if (seg_cnt_out) seg_cnt_out[d] = sg[1];
+        if (d < a.n_docs) {
+            if (a.per_token_loss) {
+                loss_c += sg[0];
+                pos_c += sg[4];
+            } else {
+                const float c = fmaxf(sg[1], 1.f);
+                loss_c += sg[0] / c;
+                pos_c += sg[4] / c;
+            }
+            if (sg[1] > 0.f) {
+                ess_c += (sg[2] * sg[2]) / (fmaxf(sg[1], 1.f) * fmaxf(sg[3], 1e-8f));
+                doc_c += 1.0;
+            }
+        }
+    }
+    loss_c = block_sum<kFinalThreads>(loss_c, scratch);
+    pos_c = block_sum<kFinalThreads>(pos_c, scratch);
+    ess_c = block_sum<kFinalThreads>(ess_c, scratch);
+    doc_c = block_sum<kFinalThreads>(doc_c, scratch);
+    double tok[kTokSums];
+#pragma unroll
+    for (int k = 0; k < kTokSums; ++k) {
+        double v = 0.0;
+        for (int64_t b = threadIdx.x; b < n_tiles; b += kFinalThreads) v += ws.tok[b * kTokSums + k];
+        tok[k] = block_sum<kFinalThreads>(v, scratch);
+    }
+    if (threadIdx.x == 0) {
+        const double den = a.per_token_loss ? static_cast<double>(max<int64_t>(1, a.n_tokens_global))
+                                            : static_cast<double>(max<int64_t>(1, a.n_docs_global));
+        const float loss = static_cast<float>(loss_c / den);
+        const float pos = static_cast<float>(pos_c / den);
+        const float cp = static_cast<float>(max(1, a.cp_degree));
+        out[MESHY_PPO_LOSS] = loss;
+        out[MESHY_PPO_TOTAL_LOSS] = loss + a.positive_lm_coef * pos;
+        out[MESHY_PPO_POSITIVE_LM_LOSS] = pos;
+        out[MESHY_PPO_TIS_RATIO_SUM] = static_cast<float>(tok[TS_TIS]);
+        out[MESHY_PPO_RATIO_SUM] = static_cast<float>(tok[TS_RATIO]);
+        out[MESHY_PPO_CLIP_SUM] = static_cast<float>(tok[TS_CLIP]);
+        out[MESHY_PPO_TIS_MASKED_SUM] = static_cast<float>(tok[TS_TIS_MASKED]);
+        out[MESHY_PPO_TOKEN_COUNT] = static_cast<float>(tok[TS_COUNT]);
+        out[MESHY_PPO_KL_SUM] = static_cast<float>(tok[TS_KL]);
+        out[MESHY_PPO_LOG_RATIO_ABS_SUM] = static_cast<float>(tok[TS_LR_ABS]);
+        out[MESHY_PPO_ESS_SUM] = static_cast<float>(ess_c) / cp;
+        out[MESHY_PPO_DOC_COUNT] = static_cast<float>(doc_c) / cp;
+        out[MESHY_PPO_TRAIN_ROLLOUT_KL_SUM] = static_cast<float>(tok[TS_K3]);
+        out[MESHY_PPO_TRAIN_ROLLOUT_LOGDIFF_ABS_SUM] = static_cast<float>(tok[TS_LOGDIFF]);
+        out[MESHY_PPO_ENTROPY_SUM] = static_cast<float>(tok[TS_ENT]);
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_ppo_bwd(meshy_ppo_args a, const float* __restrict__ seg_cnt,
+                                                      const float* __restrict__ grad_loss,
+                                                      float* __restrict__ grad_new) {
+    __shared__ int64_t s_range[2];
+    const int64_t b = blockIdx.x;
+    const int64_t t0 = b * kTile;
+    const int64_t t1 = min(t0 + kTile, a.n_tokens);
+    const int64_t n_slots = a.n_docs + 1;
+    if (threadIdx.x == 0) {
+        s_range[0] = doc_of(a.seg_offsets, n_slots, t0);
+        s_range[1] = doc_of(a.seg_offsets, n_slots, t1 - 1);
+    }
+    __syncthreads();
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+    const float G = grad_loss[0];
+    const float lo_c = 1.f - a.clip_low;
+    const float hi_c = 1.f + a.clip_high;
+    for (int64_t d = s_range[0] + wid; d <= s_range[1]; d += kWaves) {
+        const int64_t lo = max(a.seg_offsets[d], t0);
+        const int64_t hi = min(a.seg_offsets[d + 1], t1);
+        if (lo >= hi) continue;
+        const bool real = d < a.n_docs;
+        // d loss / d (per-token pg) for this document.
+        float D = 0.f;
+        if (real) {
+            D = a.per_token_loss ? 1.f / static_cast<float>(max<int64_t>(1, a.n_tokens_global))
+                                 : 1.f / (fmaxf(seg_cnt[d], 1.f) * static_cast<float>(max<int64_t>(1, a.n_docs_global)));
+        }
+        const float gD = G * D;
+        const float A_doc = (!a.adv_per_token && real) ? a.adv[d] : 0.f;
+        const float w_doc = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
+        for (int64_t i = lo + lane; i < hi; i += kWave) {
+            const float nw = a.new_lp[i];
+            const float ol = a.old_lp[i];
+            const float mk = a.mask[i];
+            const float A = a.adv_per_token ? a.adv[i] : A_doc;
+            const float ratio = expf(nw - ol);
+            const float u = ratio * A;
+            const float c = t_clamp(ratio, lo_c, hi_c) * A;
+            // grad of pg_per_token (before masking) w.r.t. pg = -min(u, c)
+            float g = gD * mk;
+            if (a.use_icepop) {
+                const float tis = expf(ol - a.rollout_lp[i]);
+                const bool tm = (tis >= a.tis_min) && (tis <= a.tis_max);
+                g = tm ? g * (tm ? tis : 0.f) : 0.f;
+            } else if (a.use_tis) {
+                const bool tm = (ratio >= a.tis_min) && (ratio <= a.tis_max);
+                g = tm ? g : 0.f;
+            }
+            const float gm = -g;  // through the negation
+            float gu, gc;
+            if (u == c) {
+                gu = 0.5f * gm;
+                gc = 0.5f * gm;
+            } else {
+                gu = (u > c) ? 0.f : gm;
+                gc = (u < c) ? 0.f : gm;
+            }
+            const float in_range = (ratio >= lo_c && ratio <= hi_c) ? 1.f : 0.f;
+            const float g_ratio = gu * A + (gc * A) * in_range;
+            float gn = g_ratio * ratio;
+            if (a.positive_lm_coef != 0.f) gn += (G * D * a.positive_lm_coef) * (-(w_doc * mk));
+            grad_new[i] = gn;
+        }
+    }
+}
+
+int validate(const meshy_ppo_args& a, const char* who) {
+    if (a.n_tokens < 0 || a.n_docs < 0) return set_error(MESHY_EINVAL, "%s: negative sizes", who);
+    if (!a.new_lp || !a.old_lp || !a.mask || !a.seg_offsets || (a.n_docs > 0 && !a.adv && !a.adv_per_token) ||
+        (a.adv_per_token && !a.adv))
+        return set_error(MESHY_ENULL, "%s: new_lp, old_lp, mask, adv and seg_offsets are required", who);
+    if (a.use_icepop && !a.rollout_lp) return set_error(MESHY_EINVAL, "%s: IcePop requires rollout log-probabilities", who);
+    if (a.positive_lm_coef != 0.f && !a.positive_lm_weights && a.n_docs > 0)
+        return set_error(MESHY_EINVAL, "%s: Positive LM loss requires group weights", who);
+    if (a.n_tokens > INT32_MAX) return set_error(MESHY_EINVAL, "%s: too many tokens", who);
+    return MESHY_OK;
+}
+
+}  // namespace
+}  // namespace meshy
+
+extern "C" size_t meshy_ppo_workspace_size(int64_t n_tokens, int64_t n_docs) {
+    if (n_tokens < 0 || n_docs < 0) return 0;
+    return meshy::ws_bytes(n_tokens, n_docs);
+}
+
+extern "C" int meshy_ppo_loss_fwd(const meshy_ppo_args* args, float* out, float* seg_cnt, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    if (!args || !out) return set_error(MESHY_ENULL, "meshy_ppo_loss_fwd: args and out are required");
+    const meshy_ppo_args& a = *args;
+    int rc = validate(a, "meshy_ppo_loss_fwd");
+    if (rc) return rc;
+    if (!a.workspace || a.workspace_bytes < ws_bytes(a.n_tokens, a.n_docs))
+        return set_error(MESHY_ESPACE, "meshy_ppo_loss_fwd: workspace needs %zu bytes",
+                         ws_bytes(a.n_tokens, a.n_docs));
+    const Workspace ws = ws_of(a.workspace, a.n_tokens);
+    const int64_t nt = n_tiles_of(a.n_tokens);
+    if (nt > 0) {
+        hipLaunchKernelGGL(k_ppo_tiles, dim3(static_cast<unsigned>(nt)), dim3(kThreads), 0, stream, a, ws);
+        rc = check_launch("meshy_ppo_loss_fwd(tiles)");
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(k_ppo_final, dim3(1), dim3(kFinalThreads), 0, stream, a, ws, out, seg_cnt);
+    return check_launch("meshy_ppo_loss_fwd(final)");
+}
+
+extern "C" int meshy_ppo_loss_bwd(const meshy_ppo_args* args, const float* seg_cnt, const float* grad_loss,
+                                  float* grad_new, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    if (!args || !seg_cnt || !grad_loss || !grad_new)
+        return set_error(MESHY_ENULL, "meshy_ppo_loss_bwd: args, seg_cnt, grad_loss and grad_new are required");
+    const meshy_ppo_args& a = *args;
+    int rc = validate(a, "meshy_ppo_loss_bwd");
+    if (rc) return rc;
+    const int64_t nt = n_tiles_of(a.n_tokens);
+    if (nt == 0) return MESHY_OK;
+    hipLaunchKernelGGL(k_ppo_bwd, dim3(static_cast<unsigned>(nt)), dim3(kThreads), 0, stream, a, seg_cnt,
+                       grad_loss, grad_new);
+    return check_launch("meshy_ppo_loss_bwd");
+}
+
+namespace meshy {
+namespace {
+
+__global__ __launch_bounds__(kThreads) void k_segment_offsets(const int64_t* __restrict__ ids, int64_t n,
+                                                              int64_t n_slots, int64_t* __restrict__ off,
+                                                              int32_t* __restrict__ unsorted) {
+    const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (gid <= n_slots) {
+        // lower_bound(ids, gid)
+        int64_t lo = 0, hi = n;
+        while (lo < hi) {
+            const int64_t mid = (lo + hi) >> 1;
+            if (ids[mid] < gid) lo = mid + 1;
+            else hi = mid;
+        }
+        off[gid] = lo;
+    }
+    if (unsorted) {
+        for (int64_t i = gid; i + 1 < n; i += static_cast<int64_t>(gridDim.x) * kThreads)
+            if (ids[i] > ids[i + 1]) unsorted[0] = 1;
+    }
+}
+
+}  // namespace
+}  // namespace meshy
+
+extern "C" int meshy_segment_offsets(const int64_t* doc_ids, int64_t n_tokens, int64_t n_slots,
+                                     int64_t* seg_offsets, int32_t* unsorted, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    if (n_tokens < 0 || n_slots < 0) return set_error(MESHY_EINVAL, "meshy_segment_offsets: negative sizes");
+    if (!seg_offsets || (n_tokens > 0 && !doc_ids))
+        return set_error(MESHY_ENULL, "meshy_segment_offsets: NULL pointer");
+    const int64_t need = n_slots + 1;
+    int64_t blocks = ceil_div(need, kThreads);
+    if (unsorted) blocks = std::max<int64_t>(blocks, std::min<int64_t>(1024, ceil_div(n_tokens, kThreads)));
+    hipLaunchKernelGGL(k_segment_offsets, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream,
+                       doc_ids, n_tokens, n_slots, seg_offsets, unsorted);
+    return check_launch("meshy_segment_offsets");
+}

@@ -1,0 +1,142 @@
+"""Fused logprob + entropy kernel against the oracle (the reference's fp32 torch path).
+
+Tolerance: 1e-3 absolute on fp32 logp and entropy (the bar for this path).
+"""
+
+import math
+
+import pytest
+import torch
+
+from oracle import logprob as olp
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _logits(rows, T, V, seed, scale=2.0):
+    g = torch.Generator().manual_seed(seed)
+    z = (torch.randn(rows, T, V, generator=g) * scale).to(torch.bfloat16)
+    y = torch.randint(0, V, (rows, T), generator=g)
+    return z, y
+
+
+def _check(z, y, dev, with_entropy=True):
+    from meshy_amd import logprob
+
+    lp, ent = logprob.logprobs_and_entropy(z.to(dev), y.to(dev), with_entropy=True)
+    ref_lp = olp.chunk_logprobs(z, y)
+    ref_ent = olp.chunk_entropy(z)
+    assert lp.dtype == torch.float32 and lp.shape == y.shape
+    assert (lp.cpu() - ref_lp).abs().max().item() <= TOL
+    assert (ent.cpu() - ref_ent).abs().max().item() <= TOL
+
+
+@pytest.mark.parametrize("V", [151936, 131072, 50, 8, 7, 1001, 4096 * 4 + 3])
+def test_matches_oracle_across_vocab_sizes(dev, V):
+    z, y = _logits(2, 33, V, seed=V)
+    _check(z, y, dev)
+
+
+def test_strided_chunk_view(dev):
+    # logits[:, s:e, :] views as the reference's chunk loop makes them.
+    z, y = _logits(2, 40, 1024, seed=3)
+    zd = z.to(dev)
+    from meshy_amd import logprob
+
+    lp = logprob.chunk_logprobs(zd[:, 8:30, :], y[:, 8:30].to(dev))
+    assert (lp.cpu() - olp.chunk_logprobs(z[:, 8:30, :], y[:, 8:30])).abs().max() <= TOL
+
+
+def test_unaligned_rows_take_generic_path(dev):
+    # V odd: row starts are not 16-byte aligned.
+    z, y = _logits(1, 17, 999, seed=5)
+    _check(z, y, dev)
+
+
+def test_ignore_index_and_out_of_range_labels(dev):
+    from meshy_amd import logprob
+
+    z, y = _logits(1, 6, 300, seed=7)
+    y[0, 1] = -100
+    y[0, 2] = 300  # out of range -> NaN (torch would raise)
+    lp = logprob.chunk_logprobs(z.to(dev), y.to(dev)).cpu()
+    assert lp[0, 1].item() == 0.0
+    assert math.isnan(lp[0, 2].item())
+    ok = torch.tensor([0, 3, 4, 5])
+    ref = olp.chunk_logprobs(z[:, ok], y[:, ok])
+    assert (lp[:, ok] - ref).abs().max() <= TOL
+
+
+def test_closed_forms(dev):
+    from meshy_amd import logprob
+
+    V = 151936
+    # Uniform logits: logp = -ln V, H = ln V.
+    z = torch.full((1, 4, V), 3.0).to(torch.bfloat16)
+    y = torch.tensor([[0, 5, V - 1, 77]])
+    lp, ent = logprob.logprobs_and_entropy(z.to(dev), y.to(dev), with_entropy=True)
+    assert torch.allclose(lp.cpu(), torch.full((1, 4), -math.log(V)), atol=1e-4)
+    assert torch.allclose(ent.cpu(), torch.full((1, 4), math.log(V)), atol=1e-4)
+    # One dominant logit: p -> 1 on it, H -> 0.
+    z = torch.zeros(1, 1, V)
+    z[0, 0, 123] = 200.0
+    lp, ent = logprob.logprobs_and_entropy(z.to(torch.bfloat16).to(dev), torch.tensor([[123]]).to(dev),
+                                           with_entropy=True)
+    assert abs(lp.item()) < 1e-4 and abs(ent.item()) < 1e-4
+
+
+def test_large_dynamic_range(dev):
+    # Logits far from zero exercise the online max rescaling.
+    z, y = _logits(2, 9, 5000, seed=11, scale=40.0)
+    z = (z.float() + 500.0).to(torch.bfloat16)
+    _check(z, y, dev)
+
+
+def test_deterministic(dev):
+    from meshy_amd import logprob
+
+    z, y = _logits(3, 16, 151936, seed=13)
+    zd, yd = z.to(dev), y.to(dev)
+    a = logprob.logprobs_and_entropy(zd, yd, with_entropy=True)
+    b = logprob.logprobs_and_entropy(zd, yd, with_entropy=True)
+    assert torch.equal(a[0], b[0]) and torch.equal(a[1], b[1])
+
+
+def test_backward_matches_autograd(dev):
+    from meshy_amd import logprob
+
+    z, y = _logits(2, 12, 3000, seed=17)
+    y[1, 3] = -100
+    g = torch.randn(2, 12, generator=torch.Generator().manual_seed(1))
+    zd = z.to(dev).requires_grad_(True)
+    lp = logprob.logprobs_and_entropy(zd, y.to(dev))
+    (lp * g.to(dev)).sum().backward()
+    ref = olp.logprob_grad(z, y, g)
+    got = zd.grad.float().cpu()
+    # bf16 gradient: relative rounding 2^-8 on |grad| <= |g|.
+    assert (got - ref).abs().max().item() <= 4e-3 * g.abs().max().item()
+    assert got[1, 3].abs().max().item() == 0.0
+
+
+def test_full_size_rows_subset(dev):
+    """T=16384, V=151936 (the headline shape): a row subset against the oracle,
+    and size-independent properties on every row."""
+    from meshy_amd import logprob
+
+    T, V = 16384, 151936
+    gen = torch.Generator(device=dev).manual_seed(1)
+    z = (torch.randn(1, T, V, generator=gen, device=dev, dtype=torch.bfloat16) * 2.0)
+    y = torch.randint(0, V, (1, T), generator=gen, device=dev)
+    lp, ent = logprob.logprobs_and_entropy(z, y, with_entropy=True)
+    # properties: logp <= 0, 0 <= H <= ln V, finite
+    assert torch.isfinite(lp).all() and torch.isfinite(ent).all()
+    assert (lp <= 1e-6).all()
+    assert (ent >= -1e-6).all() and (ent <= math.log(V) + 1e-4).all()
+    rows = torch.tensor([0, 1, 4095, 8191, 12000, T - 2, T - 1])
+    zs = z[:, rows.to(dev)].cpu()
+    ref_lp = olp.chunk_logprobs(zs, y[:, rows.to(dev)].cpu())
+    ref_ent = olp.chunk_entropy(zs)
+    assert (lp[:, rows.to(dev)].cpu() - ref_lp).abs().max() <= TOL
+    assert (ent[:, rows.to(dev)].cpu() - ref_ent).abs().max() <= TOL
