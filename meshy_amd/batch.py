@@ -1,0 +1,336 @@
+"""Micro-batch materialisation with the call surface of meshy/backend/titan/batch.py.
+
+``build_micro_batch`` (batch.py:96-230) builds one micro; ``build_micro_batches``
+builds any number of micros of one rank in one go.  Either way the samples'
+tokens, masks, rollout logprobs and per-token advantages are gathered into one
+pinned staging buffer next to the plan tables, copied to the device in ONE
+host-to-device transfer, and laid out by the ``meshy_pack_micro_batches``
+kernel: per-document shift-by-one, doc ids with the padding slot, per-document
+positions and ``cu_seqlens`` (a device prefix scan).  ``Batch`` keeps the
+reference's fields (batch.py:52-74) so the forward and the loss read it as is.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, NamedTuple, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from .plan import Layout, MicroPlan
+
+#: Per-token advantage column (batch.py:81): already on the next-token grid,
+#: laid out like rollout logprobs but not shifted again.
+ADVANTAGE_TOKENS = "advantage_tokens"
+
+
+class VarlenMetadata(NamedTuple):
+    """Document boundaries for variable-length attention.
+
+    Same fields as torchtitan's ``VarlenMetadata`` (cu_seq_q, cu_seq_k, max_q,
+    max_k), which batch.py:233-243 constructs.
+    """
+
+    cu_seq_q: torch.Tensor
+    cu_seq_k: torch.Tensor
+    max_q: int
+    max_k: int
+
+
+@dataclass
+class Batch:
+    """One micro-batch, next-token aligned (batch.py:52-74)."""
+
+    input_ids: torch.Tensor
+    labels: torch.Tensor
+    positions: torch.Tensor
+    mask: torch.Tensor
+    doc_ids: torch.Tensor
+    advantages: torch.Tensor
+    rollout_logprobs: torch.Tensor | None
+    lengths: torch.Tensor
+    n_docs: int
+    attention_masks: Any = None
+    positive_lm_weights: torch.Tensor | None = None
+
+    @property
+    def n_slots(self) -> int:
+        """Segment-buffer size: one slot per sample plus one for padding."""
+        return self.n_docs + 1
+
+
+def make_varlen_metadata(cu_seqlens, max_len: int, device) -> VarlenMetadata:
+    """VarlenMetadata from explicit document boundaries (batch.py:233-243)."""
+    cu = cu_seqlens if isinstance(cu_seqlens, torch.Tensor) else torch.tensor(
+        list(cu_seqlens), dtype=torch.int32)
+    cu = cu.to(device=device, dtype=torch.int32)
+    return VarlenMetadata(cu_seq_q=cu, cu_seq_k=cu, max_q=int(max_len), max_k=int(max_len))
+
+
+class _Staging:
+    """A grow-only pinned host buffer, reused once its last copy has landed."""
+
+    def __init__(self) -> None:
+        self.buf: torch.Tensor | None = None
+        self.event = None
+
+    def get(self, nbytes: int) -> torch.Tensor:
+        if self.event is not None:
+            self.event.synchronize()
+        if self.buf is None or self.buf.numel() < nbytes:
+            self.buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, pin_memory=True)
+        return self.buf
+
+    def mark(self, stream) -> None:
+        self.event = torch.cuda.Event()
+        self.event.record(stream)
+
+
+_STAGING: dict[int, _Staging] = {}
+
+
+class _Layout:
+    """Byte layout of the staging buffer: 256-byte aligned regions."""
+
+    def __init__(self) -> None:
+        self.size = 0
+        self.regions: dict[str, tuple[int, int, torch.dtype]] = {}
+
+    def add(self, name: str, n: int, dtype: torch.dtype) -> None:
+        esize = torch.empty((), dtype=dtype).element_size()
+        self.regions[name] = (self.size, n, dtype)
+        self.size += (n * esize + 255) // 256 * 256
+
+    def view(self, buf: torch.Tensor, name: str) -> torch.Tensor:
+        off, n, dtype = self.regions[name]
+        esize = torch.empty((), dtype=dtype).element_size()
+        return buf[off:off + n * esize].view(dtype)
+
+
+def _scalar(td, key: str, default: float = 0.0) -> float:
+    v = td.get(key, default) if hasattr(td, "get") else default
+    if isinstance(v, torch.Tensor):
+        return float(v.reshape(-1)[0].item()) if v.numel() else default
+    return float(v)
+
+
+def build_micro_batches(
+    samples: Sequence[Any],
+    micros: Sequence[MicroPlan],
+    *,
+    layout: Layout,
+    device,
+    sharder=None,
+    need_rollout_lp: bool,
+) -> list[Batch]:
+    """Materialise ``micros`` from the rank-local ``samples`` in one transfer and one launch."""
+    if layout not in ("padded", "packed"):
+        raise ValueError(f"unknown layout {layout!r}")
+    device = torch.device(device)
+    if device.type != "cuda":
+        raise ValueError("meshy_amd builds micro-batches on a HIP device; pass a cuda device")
+    lib = _lib.load()
+
+    # Samples used by these micros, remapped to a compact list.
+    remap: dict[int, int] = {}
+    used: list[int] = []
+    need_len: list[int] = []
+    for m in micros:
+        if layout == "packed" and m.n_tokens > m.seq_len:
+            raise AssertionError(f"micro seq_len {m.seq_len} smaller than its tokens {m.n_tokens}")
+        for idx, L in zip(m.sample_idx, m.doc_lens):
+            if idx not in remap:
+                remap[idx] = len(used)
+                used.append(idx)
+                need_len.append(int(L))
+            else:
+                need_len[remap[idx]] = max(need_len[remap[idx]], int(L))
+    n_s = len(used)
+    for j, idx in enumerate(used):
+        if int(len(samples[idx]["tokens"])) < need_len[j]:
+            raise ValueError(f"sample {idx} has {len(samples[idx]['tokens'])} tokens, micro wants {need_len[j]}")
+    per_token_adv = any(ADVANTAGE_TOKENS in samples[m.sample_idx[0]] for m in micros if m.sample_idx)
+    s_off = np.zeros(n_s + 1, np.int64)
+    np.cumsum(need_len, out=s_off[1:])
+    total = int(s_off[-1])
+
+    # Plan tables.
+    n_micro = len(micros)
+    seq = np.array([m.seq_len for m in micros], np.int64)
+    rows = np.array([1 if layout == "packed" else m.n_rows for m in micros], np.int64)
+    elems = seq * rows
+    out_off = np.zeros(n_micro + 1, np.int64)
+    np.cumsum(elems, out=out_off[1:])
+    n_docs = np.array([len(m.sample_idx) for m in micros], np.int64)
+    doc_start = np.zeros(n_micro + 1, np.int32)
+    np.cumsum(n_docs, out=doc_start[1:])
+    n_docs_total = int(doc_start[-1])
+    doc_sample = np.array([remap[i] for m in micros for i in m.sample_idx], np.int32)
+    doc_len = np.array([L for m in micros for L in m.doc_lens], np.int64)
+    adv_samples = np.array([_scalar(samples[i], "advantage") for i in used], np.float32)
+    pos_w = np.array([
+        _scalar(samples[i], "positive_lm_weight") if _scalar(samples[i], "reward") > 0.5 else 0.0
+        for m in micros for i in m.sample_idx], np.float32)
+
+    # Token ids travel as int32 (any vocabulary fits) and come out int64 like the reference's.
+    tok_dtype = torch.int32
+
+    lay = _Layout()
+    lay.add("tokens", total, tok_dtype)
+    lay.add("mask", total, torch.float32)
+    if need_rollout_lp:
+        lay.add("logprobs", total, torch.float32)
+    if per_token_adv:
+        lay.add("adv_tokens", total, torch.float32)
+    lay.add("adv_samples", max(n_s, 1), torch.float32)
+    lay.add("s_off", n_s + 1, torch.int64)
+    lay.add("seq", n_micro, torch.int64)
+    lay.add("out_off", n_micro + 1, torch.int64)
+    lay.add("doc_len", max(n_docs_total, 1), torch.int64)
+    lay.add("doc_start", n_micro + 1, torch.int32)
+    lay.add("doc_sample", max(n_docs_total, 1), torch.int32)
+    lay.add("pos_w", max(n_docs_total, 1), torch.float32)
+
+    stage = _STAGING.setdefault(device.index or 0, _Staging())
+    host = stage.get(lay.size)
+    if n_s:
+        srcs = [samples[i] for i in used]
+        torch.cat([s["tokens"][:L].to(tok_dtype) for s, L in zip(srcs, need_len)],
+                  out=lay.view(host, "tokens"))
+        torch.cat([s["mask_assistant"][:L].to(torch.float32) for s, L in zip(srcs, need_len)],
+                  out=lay.view(host, "mask"))
+        if need_rollout_lp:
+            torch.cat([s["logprobs"][:L].to(torch.float32) for s, L in zip(srcs, need_len)],
+                      out=lay.view(host, "logprobs"))
+        if per_token_adv:
+            parts = []
+            for s, L in zip(srcs, need_len):
+                a = s[ADVANTAGE_TOKENS][:L].to(device="cpu", dtype=torch.float32)
+                if a.numel() < L:
+                    a = torch.cat([a, a.new_zeros(L - a.numel())])
+                parts.append(a)
+            torch.cat(parts, out=lay.view(host, "adv_tokens"))
+    lay.view(host, "adv_samples")[:n_s] = torch.from_numpy(adv_samples)
+    lay.view(host, "s_off").copy_(torch.from_numpy(s_off))
+    lay.view(host, "seq").copy_(torch.from_numpy(seq))
+    lay.view(host, "out_off").copy_(torch.from_numpy(out_off))
+    lay.view(host, "doc_start").copy_(torch.from_numpy(doc_start))
+    if n_docs_total:
+        lay.view(host, "doc_len")[:n_docs_total] = torch.from_numpy(doc_len)
+        lay.view(host, "doc_sample")[:n_docs_total] = torch.from_numpy(doc_sample)
+        lay.view(host, "pos_w")[:n_docs_total] = torch.from_numpy(pos_w)
+
+    stream = torch.cuda.current_stream(device)
+    dbuf = torch.empty(lay.size, dtype=torch.uint8, device=device)
+    dbuf.copy_(host[:lay.size], non_blocking=True)
+    stage.mark(stream)
+
+    n_out = int(out_off[-1])
+    input_ids = torch.empty(n_out, dtype=torch.int64, device=device)
+    labels = torch.empty(n_out, dtype=torch.int64, device=device)
+    positions = torch.empty(n_out, dtype=torch.int32, device=device)
+    mask = torch.empty(n_out, dtype=torch.float32, device=device)
+    doc_ids = torch.empty(n_out, dtype=torch.int64, device=device)
+    rollout_lp = torch.empty(n_out, dtype=torch.float32, device=device) if need_rollout_lp else None
+    adv_tok = torch.empty(n_out, dtype=torch.float32, device=device) if per_token_adv else None
+    adv_doc = torch.empty(max(n_docs_total, 1), dtype=torch.float32, device=device)
+    lengths = torch.empty(max(n_docs_total, 1), dtype=torch.int32, device=device)
+    cu = torch.empty(n_docs_total + 2 * n_micro, dtype=torch.int32, device=device)
+
+    a = _lib.PackArgs()
+    a.tokens = lay.view(dbuf, "tokens").data_ptr()
+    a.tokens_elem_bytes = 4 if tok_dtype == torch.int32 else 8
+    a.layout = _lib.MESHY_LAYOUT_PACKED if layout == "packed" else _lib.MESHY_LAYOUT_PADDED
+    a.mask = lay.view(dbuf, "mask").data_ptr()
+    a.logprobs = lay.view(dbuf, "logprobs").data_ptr() if need_rollout_lp else None
+    a.adv_tokens = lay.view(dbuf, "adv_tokens").data_ptr() if per_token_adv else None
+    a.adv_samples = lay.view(dbuf, "adv_samples").data_ptr()
+    a.sample_offsets = lay.view(dbuf, "s_off").data_ptr()
+    a.n_samples = n_s
+    a.n_micro = n_micro
+    a.micro_seq_len = lay.view(dbuf, "seq").data_ptr()
+    a.micro_out_off = lay.view(dbuf, "out_off").data_ptr()
+    a.micro_doc_start = lay.view(dbuf, "doc_start").data_ptr()
+    a.doc_sample = lay.view(dbuf, "doc_sample").data_ptr()
+    a.doc_len = lay.view(dbuf, "doc_len").data_ptr()
+    a.max_micro_elems = int(elems.max()) if n_micro else 0
+    a.max_docs_per_micro = int(n_docs.max()) if n_micro else 0
+    a.input_ids = input_ids.data_ptr()
+    a.labels = labels.data_ptr()
+    a.positions = positions.data_ptr()
+    a.mask_out = mask.data_ptr()
+    a.doc_ids = doc_ids.data_ptr()
+    a.rollout_lp = _lib.ptr(rollout_lp)
+    a.adv_tok = _lib.ptr(adv_tok)
+    a.adv_doc = adv_doc.data_ptr()
+    a.doc_len_out = lengths.data_ptr()
+    a.cu_seqlens = cu.data_ptr()
+    rc = lib.meshy_pack_micro_batches(_lib.ctypes.byref(a), stream.cuda_stream)
+    _lib.check(rc, "meshy_pack_micro_batches")
+    pos_w_dev = lay.view(dbuf, "pos_w")
+
+    out: list[Batch] = []
+    for k, m in enumerate(micros):
+        o0, o1 = int(out_off[k]), int(out_off[k + 1])
+        R, S = int(rows[k]), int(seq[k])
+        d0, d1 = int(doc_start[k]), int(doc_start[k + 1])
+        nd = d1 - d0
+
+        def v(t):
+            return None if t is None else t[o0:o1].view(R, S)
+
+        ii, lb, ps, mk, di, rl, at = (v(input_ids), v(labels), v(positions), v(mask), v(doc_ids),
+                                      v(rollout_lp), v(adv_tok))
+        attn = None
+        if layout == "packed":
+            pad = S - m.n_tokens
+            n_cu = nd + 1 + (1 if pad > 0 else 0)
+            c0 = d0 + 2 * k
+            max_len = max(list(m.doc_lens) + ([pad] if pad > 0 else []))
+            attn = make_varlen_metadata(cu[c0:c0 + n_cu], max_len, device)
+        else:
+            # One CP shard call for every per-token tensor (batch.py:195-207);
+            # the identity on one GPU.
+            if sharder is not None:
+                optional = [t for t in (rl, at) if t is not None]
+                sharded = sharder.shard_seq(ii, lb, ps, mk, di, *optional)
+                ii, lb, ps, mk, di = sharded[:5]
+                rest = list(sharded[5:])
+                if rl is not None:
+                    rl = rest.pop(0)
+                if at is not None:
+                    at = rest.pop(0)
+        out.append(Batch(
+            input_ids=ii,
+            labels=lb,
+            positions=ps,
+            mask=mk,
+            doc_ids=di,
+            advantages=at if at is not None else adv_doc[d0:d1],
+            rollout_logprobs=rl,
+            lengths=lengths[d0:d1],
+            n_docs=nd,
+            attention_masks=attn,
+            positive_lm_weights=pos_w_dev[d0:d1],
+        ))
+    return out
+
+
+def build_micro_batch(
+    samples: Sequence[Any],
+    micro: MicroPlan,
+    *,
+    layout: Layout,
+    device,
+    sharder=None,
+    need_rollout_lp: bool,
+) -> Batch:
+    """Materialise one ``micro`` from the rank-local ``samples`` (batch.py:96-230)."""
+    return build_micro_batches(samples, [micro], layout=layout, device=device, sharder=sharder,
+                               need_rollout_lp=need_rollout_lp)[0]
+
+
+__all__ = ["ADVANTAGE_TOKENS", "Batch", "VarlenMetadata", "build_micro_batch",
+           "build_micro_batches", "make_varlen_metadata"]

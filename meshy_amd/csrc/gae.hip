@@ -348,7 +348,8 @@ extern "C" int meshy_gae(const meshy_gae_args* args, hipStream_t stream) {
     if (nc > INT32_MAX) return set_error(MESHY_EINVAL, "meshy_gae: too many tokens");
     const Workspace ws = ws_of(g.workspace, n, g.n_docs);
     int rc;
-    if (!g.lengths) {
+    // Document lengths only matter for lambda (advantages / lam_doc), not for returns.
+    if (!g.lengths && (g.adv || g.lam_doc)) {
         const int64_t nz = g.n_docs + 1;
         hipLaunchKernelGGL(k_gae_zero, dim3(static_cast<unsigned>(ceil_div(nz, kThreads))), dim3(kThreads), 0, stream,
                            ws.cnt, nz);

@@ -404,7 +404,11 @@ __global__ __launch_bounds__(kThreads) void k_segment_offsets(const int64_t* __r
                                                               int64_t n_slots, int64_t* __restrict__ off,
                                                               int32_t* __restrict__ unsorted) {
     const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (gid <= n_slots) {
+    if (gid == n_slots) {
+        // The last offset is the token count, so every token lies in some slot
+        // (ids beyond the padding slot, which the Batch contract excludes, fold into it).
+        off[gid] = n;
+    } else if (gid < n_slots) {
         // lower_bound(ids, gid)
         int64_t lo = 0, hi = n;
         while (lo < hi) {

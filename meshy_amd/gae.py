@@ -1,0 +1,114 @@
+"""Segment-aware GAE and returns with the call surface of
+meshy/backend/titan/critic/gae.py.
+
+``compute_vapo_gae`` (gae.py:208-293) and ``compute_returns`` (gae.py:183-205)
+run the ``meshy_gae`` kernels: the recursion ``A_t = x_t + decay_t * cont_t *
+A_{t+1}`` as a reverse scan of affine maps over the flattened ``[rows, S]``
+grid, in fp32, with no closed form and therefore no underflow fallback
+(gae.py:149-150).  ``gae_and_returns`` produces both in one pass.
+"""
+
+from __future__ import annotations
+
+import torch
+
+from . import _lib
+
+
+def _run(rewards, values, mask, doc_ids, n_docs, *, lengths, gamma, alpha, epsilon, want_adv,
+         want_returns, want_lam):
+    if rewards.dim() != 2:
+        raise ValueError(f"expected [rows, S] tensors, got {tuple(rewards.shape)}")
+    rows, S = rewards.shape
+    for name, t in (("values", values), ("mask", mask), ("doc_ids", doc_ids)):
+        if t is not None and tuple(t.shape) != (rows, S):
+            raise ValueError(f"{name} {tuple(t.shape)} does not match rewards {(rows, S)}")
+    _lib.require_gpu(rewards, values, mask, doc_ids, lengths)
+    dev = rewards.device
+    r = rewards.to(torch.float32).contiguous()
+    m = mask.to(torch.float32).contiguous()
+    ids = doc_ids.to(torch.int64).contiguous()
+    v = None
+    bf16 = 0
+    if values is not None:
+        if values.dtype == torch.bfloat16:
+            v, bf16 = values.contiguous(), 1
+        else:
+            v = values.to(torch.float32).contiguous()
+    lens = None if lengths is None else lengths.reshape(-1).to(device=dev, dtype=torch.float32).contiguous()
+    if lens is not None and lens.numel() < n_docs:
+        raise ValueError(f"lengths has {lens.numel()} entries for {n_docs} documents")
+    adv = torch.empty(rows, S, dtype=torch.float32, device=dev) if want_adv else None
+    ret = torch.empty(rows, S, dtype=torch.float32, device=dev) if want_returns else None
+    lam = torch.empty(max(n_docs, 1), dtype=torch.float32, device=dev) if want_lam else None
+    lib = _lib.load()
+    ws = torch.empty(max(int(lib.meshy_gae_workspace_size(rows, S, n_docs)), 1), dtype=torch.uint8,
+                     device=dev)
+    g = _lib.GaeArgs()
+    g.rewards = r.data_ptr()
+    g.values = _lib.ptr(v)
+    g.mask = m.data_ptr()
+    g.doc_ids = ids.data_ptr()
+    g.lengths = _lib.ptr(lens)
+    g.rows, g.S, g.n_docs = rows, S, int(n_docs)
+    g.gamma, g.alpha, g.epsilon = float(gamma), float(alpha), float(epsilon)
+    g.values_bf16 = bf16
+    g.adv = _lib.ptr(adv)
+    g.returns = _lib.ptr(ret)
+    g.lam_doc = _lib.ptr(lam)
+    g.workspace = ws.data_ptr()
+    g.workspace_bytes = ws.numel()
+    rc = lib.meshy_gae(_lib.ctypes.byref(g), _lib.stream_of(dev))
+    _lib.check(rc, "meshy_gae")
+    return adv, ret, (lam[:n_docs] if lam is not None else None)
+
+
+def compute_vapo_gae(
+    rewards: torch.Tensor,
+    values: torch.Tensor,
+    mask: torch.Tensor,
+    doc_ids: torch.Tensor,
+    n_docs: int,
+    *,
+    lengths: torch.Tensor | None = None,
+    gamma: float = 1.0,
+    alpha: float = 1.5,
+    epsilon: float = 1e-6,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """VAPO GAE with per-document lambda = 1 - 1/(alpha * L) (gae.py:208-293)."""
+    adv, _, lam = _run(rewards, values, mask, doc_ids, n_docs, lengths=lengths, gamma=gamma,
+                       alpha=alpha, epsilon=epsilon, want_adv=True, want_returns=False, want_lam=True)
+    return adv, lam
+
+
+def compute_returns(
+    rewards: torch.Tensor,
+    mask: torch.Tensor,
+    doc_ids: torch.Tensor,
+    *,
+    gamma: float = 1.0,
+) -> torch.Tensor:
+    """Discounted return-to-go G_t = r_t + gamma * cont_t * G_{t+1} (gae.py:183-205)."""
+    _, ret, _ = _run(rewards, None, mask, doc_ids, 0, lengths=None, gamma=gamma, alpha=1.0,
+                     epsilon=1e-6, want_adv=False, want_returns=True, want_lam=False)
+    return ret
+
+
+def gae_and_returns(
+    rewards: torch.Tensor,
+    values: torch.Tensor,
+    mask: torch.Tensor,
+    doc_ids: torch.Tensor,
+    n_docs: int,
+    *,
+    lengths: torch.Tensor | None = None,
+    gamma: float = 1.0,
+    alpha: float = 1.5,
+    epsilon: float = 1e-6,
+) -> tuple[torch.Tensor, torch.Tensor, torch.Tensor]:
+    """Advantages, returns and lambda per document from one pass over the inputs."""
+    return _run(rewards, values, mask, doc_ids, n_docs, lengths=lengths, gamma=gamma, alpha=alpha,
+                epsilon=epsilon, want_adv=True, want_returns=True, want_lam=True)
+
+
+__all__ = ["compute_returns", "compute_vapo_gae", "gae_and_returns"]

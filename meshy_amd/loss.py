@@ -1,0 +1,199 @@
+"""Clipped PPO loss with the call surface of TitanTrainer._ppo_clip_loss.
+
+``ppo_clip_loss(self, new_lp, old_lp, mb, mini, entropy=None)`` reads only the
+attributes the reference reads (trainer.py:705-848): ``ppo_clip_eps_low/high``,
+``use_tis``, ``use_icepop``, ``tis_ratio_min/max``, ``calculate_per_token_loss``,
+``positive_lm_loss_coef``, ``old_logprobs_source``, ``sharder`` and
+``parallel_dims.cp``; it can be called unbound on a ``SimpleNamespace`` like the
+reference's tests do.  The forward is ``meshy_ppo_loss_fwd`` (one tiled pass over
+the tokens plus one combine), the gradient with respect to ``new_lp`` is
+``meshy_ppo_loss_bwd``; both are wrapped in an autograd Function so
+``loss.backward()`` works as before.  ``reduce_mini_metrics`` is
+_reduce_mini_metrics (trainer.py:1020-1047).
+"""
+
+from __future__ import annotations
+
+from typing import Any
+
+import torch
+import torch.distributed as dist
+
+from . import _lib
+
+
+def segment_offsets(doc_ids: torch.Tensor, n_slots: int, check_sorted: bool = False) -> torch.Tensor:
+    """Token offsets of each document slot of a non-decreasing ``doc_ids`` tensor."""
+    ids = doc_ids.reshape(-1).to(torch.int64).contiguous()
+    off = torch.empty(n_slots + 1, dtype=torch.int64, device=ids.device)
+    flag = torch.zeros(1, dtype=torch.int32, device=ids.device) if check_sorted else None
+    rc = _lib.load().meshy_segment_offsets(ids.data_ptr(), ids.numel(), n_slots, off.data_ptr(),
+                                           _lib.ptr(flag), _lib.stream_of(ids.device))
+    _lib.check(rc, "meshy_segment_offsets")
+    if check_sorted and int(flag.item()):
+        raise ValueError("doc_ids must be non-decreasing over the flattened micro-batch")
+    return off
+
+
+class _Inputs:
+    """Everything the two kernels read besides new_lp, kept alive for the backward."""
+
+    def __init__(self, stub, new_lp, old_lp, mb, mini, entropy) -> None:
+        dev = new_lp.device
+        self.n_tokens = new_lp.numel()
+        self.old = old_lp.detach().reshape(-1).to(torch.float32).contiguous()
+        self.mask = mb.mask.reshape(-1).to(torch.float32).contiguous()
+        self.rollout = (None if mb.rollout_logprobs is None else
+                        mb.rollout_logprobs.detach().reshape(-1).to(torch.float32).contiguous())
+        self.entropy = None if entropy is None else entropy.detach().reshape(-1).to(torch.float32).contiguous()
+        adv = mb.advantages
+        self.adv_per_token = adv.dim() != 1
+        self.adv = adv.detach().reshape(-1).to(torch.float32).contiguous()
+        self.n_docs = int(mb.n_docs)
+        self.use_icepop = bool(getattr(stub, "use_icepop", False))
+        self.use_tis = bool(stub.use_tis) and not self.use_icepop
+        self.coef = float(getattr(stub, "positive_lm_loss_coef", 0.0) or 0.0)
+        if self.use_icepop and self.rollout is None:
+            raise ValueError("IcePop requires rollout log-probabilities")
+        self.pos_w = None
+        if self.coef:
+            if mb.positive_lm_weights is None:
+                raise ValueError("Positive LM loss requires group weights")
+            self.pos_w = mb.positive_lm_weights.reshape(-1).to(torch.float32).contiguous()
+        _lib.require_gpu(new_lp, self.old, self.mask, self.adv, mb.doc_ids, self.rollout, self.entropy,
+                         self.pos_w)
+        self.seg_off = segment_offsets(mb.doc_ids, self.n_docs + 1)
+        ws = _lib.load().meshy_ppo_workspace_size(self.n_tokens, self.n_docs)
+        self.workspace = torch.empty(max(int(ws), 1), dtype=torch.uint8, device=dev)
+        self.clip_low = float(stub.ppo_clip_eps_low)
+        self.clip_high = float(stub.ppo_clip_eps_high)
+        self.tis_min = float(getattr(stub, "tis_ratio_min", 0.5))
+        self.tis_max = float(getattr(stub, "tis_ratio_max", 5.0))
+        self.per_token = bool(stub.calculate_per_token_loss)
+        self.train_is_old = getattr(stub, "old_logprobs_source", "rollout") == "train"
+        self.cp = max(1, int(getattr(getattr(stub, "parallel_dims", None), "cp", 1) or 1))
+        self.n_docs_global = int(mini.n_docs_global)
+        self.n_tokens_global = int(mini.n_tokens_global)
+
+    def args(self, new_flat: torch.Tensor) -> _lib.PpoArgs:
+        a = _lib.PpoArgs()
+        a.new_lp = new_flat.data_ptr()
+        a.old_lp = self.old.data_ptr()
+        a.mask = self.mask.data_ptr()
+        a.rollout_lp = _lib.ptr(self.rollout)
+        a.entropy = _lib.ptr(self.entropy)
+        a.adv = self.adv.data_ptr()
+        a.positive_lm_weights = _lib.ptr(self.pos_w)
+        a.seg_offsets = self.seg_off.data_ptr()
+        a.n_tokens = self.n_tokens
+        a.n_docs = self.n_docs
+        a.n_docs_global = self.n_docs_global
+        a.n_tokens_global = self.n_tokens_global
+        a.clip_low = self.clip_low
+        a.clip_high = self.clip_high
+        a.tis_min = self.tis_min
+        a.tis_max = self.tis_max
+        a.positive_lm_coef = self.coef
+        a.adv_per_token = int(self.adv_per_token)
+        a.use_tis = int(self.use_tis)
+        a.use_icepop = int(self.use_icepop)
+        a.per_token_loss = int(self.per_token)
+        a.train_lp_is_old = int(self.train_is_old)
+        a.cp_degree = self.cp
+        a.workspace = self.workspace.data_ptr()
+        a.workspace_bytes = self.workspace.numel()
+        return a
+
+
+class _PPOLoss(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, new_flat, inputs: _Inputs):
+        dev = new_flat.device
+        out = torch.empty(_lib.PPO_NOUT, dtype=torch.float32, device=dev)
+        seg_cnt = torch.empty(inputs.n_docs + 1, dtype=torch.float32, device=dev)
+        a = inputs.args(new_flat)
+        rc = _lib.load().meshy_ppo_loss_fwd(_lib.ctypes.byref(a), out.data_ptr(), seg_cnt.data_ptr(),
+                                            _lib.stream_of(dev))
+        _lib.check(rc, "meshy_ppo_loss_fwd")
+        ctx.inputs = inputs
+        ctx.save_for_backward(new_flat, seg_cnt)
+        loss = out[1].clone()
+        ctx.mark_non_differentiable(out)
+        return loss, out
+
+    @staticmethod
+    def backward(ctx, grad_loss, grad_out):
+        new_flat, seg_cnt = ctx.saved_tensors
+        inputs: _Inputs = ctx.inputs
+        g = grad_loss.reshape(1).to(torch.float32).contiguous()
+        grad = torch.empty_like(new_flat)
+        a = inputs.args(new_flat)
+        rc = _lib.load().meshy_ppo_loss_bwd(_lib.ctypes.byref(a), seg_cnt.data_ptr(), g.data_ptr(),
+                                            grad.data_ptr(), _lib.stream_of(new_flat.device))
+        _lib.check(rc, "meshy_ppo_loss_bwd")
+        return grad, None
+
+
+def ppo_clip_loss(
+    self: Any,
+    new_lp: torch.Tensor,
+    old_lp: torch.Tensor,
+    mb: Any,
+    mini: Any,
+    entropy: torch.Tensor | None = None,
+) -> tuple[torch.Tensor, dict[str, torch.Tensor]]:
+    """Drop-in for ``TitanTrainer._ppo_clip_loss`` (trainer.py:705-848)."""
+    sharder = getattr(self, "sharder", None)
+    if sharder is not None and getattr(sharder, "enabled", False):
+        raise NotImplementedError(
+            "context-parallel PPO loss needs the per-document all-reduce between the two "
+            "kernel phases; this build runs one GPU")
+    inputs = _Inputs(self, new_lp, old_lp, mb, mini, entropy)
+    new_flat = new_lp.reshape(-1)
+    if new_flat.dtype != torch.float32:
+        new_flat = new_flat.float()
+    if not new_flat.is_contiguous():
+        new_flat = new_flat.contiguous()
+    loss, out = _PPOLoss.apply(new_flat, inputs)
+    names = _lib.PPO_OUT_NAMES
+    sums = {names[k]: out[k] for k in range(12)}
+    if inputs.rollout is not None:
+        sums["train_rollout_kl_sum"] = out[12]
+        sums["train_rollout_logdiff_abs_sum"] = out[13]
+    if inputs.entropy is not None:
+        sums["entropy_sum"] = out[14]
+    return loss, sums
+
+
+def reduce_mini_metrics(self: Any, sums: dict[str, torch.Tensor]) -> dict[str, float]:
+    """Per-rank sums -> mini-batch metrics (trainer.py:1020-1047)."""
+    keys = list(sums)
+    stacked = torch.stack([sums[k].float().reshape(()) for k in keys])
+    pd = getattr(self, "parallel_dims", None)
+    loss_mesh = pd.get_optional_mesh("loss") if pd is not None and hasattr(pd, "get_optional_mesh") else None
+    if loss_mesh is not None:
+        dist.all_reduce(stacked, op=dist.ReduceOp.SUM, group=loss_mesh.get_group())
+    values = dict(zip(keys, stacked.tolist()))
+    tokens = max(values["token_count"], 1.0)
+    out = {
+        "pg_loss": values["loss"],
+        "ratio_mean": values["ratio_sum"] / tokens,
+        "clip_frac": values["clip_sum"] / tokens,
+        "tis_masked_frac": values["tis_masked_sum"] / tokens,
+        "ppo_kl": values["ppo_kl_sum"] / tokens,
+        "log_ratio_abs_mean": values["log_ratio_abs_sum"] / tokens,
+        "ess_ratio": values["ess_sum"] / max(values.get("doc_count", 0.0), 1.0),
+    }
+    if "train_rollout_kl_sum" in values:
+        out["train_rollout_kl"] = values["train_rollout_kl_sum"] / tokens
+        out["train_rollout_logdiff_abs"] = values["train_rollout_logdiff_abs_sum"] / tokens
+    if "entropy_sum" in values:
+        out["entropy"] = values["entropy_sum"] / tokens
+    if "tis_ratio_sum" in values:
+        out["tis_ratio_mean"] = values["tis_ratio_sum"] / tokens
+        out["positive_lm_loss"] = values["positive_lm_loss"]
+        out["total_loss"] = values["total_loss"]
+    return out
+
+
+__all__ = ["ppo_clip_loss", "reduce_mini_metrics", "segment_offsets"]

@@ -1,0 +1,177 @@
+"""Segment-aware GAE, returns and whitening on the GPU against the oracle (the
+reference's sequential recursion, critic/gae.py:162-180, and vapo.py:6-32).
+Tolerance: 1e-3 absolute on fp32 advantages and returns."""
+
+from __future__ import annotations
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import gae as ogae
+from oracle import vapo as ovapo
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+def _random_grid(rows, S, n_docs_per_row, seed, hole_p=0.05):
+    g = torch.Generator().manual_seed(seed)
+    doc_ids = torch.zeros(rows, S, dtype=torch.long)
+    mask = torch.zeros(rows, S)
+    next_id = 0
+    for r in range(rows):
+        cuts = sorted(torch.randint(1, S, (n_docs_per_row - 1,), generator=g).tolist())
+        bounds = [0] + cuts + [S]
+        for a, b in zip(bounds[:-1], bounds[1:]):
+            doc_ids[r, a:b] = next_id
+            p = int(torch.randint(0, max(1, (b - a) // 3 + 1), (1,), generator=g))
+            mask[r, a + p:b] = 1.0
+            next_id += 1
+    holes = torch.rand(rows, S, generator=g) < hole_p
+    mask[holes] = 0.0
+    values = torch.randn(rows, S, generator=g)
+    rewards = torch.zeros(rows, S)
+    rewards[torch.rand(rows, S, generator=g) < 0.02] = 1.0
+    return rewards, values, mask, doc_ids, next_id
+
+
+@pytest.mark.parametrize("gamma,alpha,const_lam", [(1.0, 1.5, None), (0.99, 0.5, None), (1.0, 1.0, 0.95),
+                                                   (0.9, 1.0, 0.0)])
+def test_matches_sequential_oracle(dev, gamma, alpha, const_lam):
+    from meshy_amd.gae import compute_returns, compute_vapo_gae, gae_and_returns
+
+    rewards, values, mask, doc_ids, n_docs = _random_grid(5, 3000, 4, seed=int(gamma * 100))
+    n_docs_total = n_docs
+    lengths = None
+    if const_lam is not None:
+        lengths = torch.full((n_docs_total,), 1.0 / max(1e-9, 1.0 - const_lam))
+    ref_adv, ref_lam = ogae.compute_vapo_gae(rewards, values, mask, doc_ids, n_docs_total, lengths=lengths,
+                                             gamma=gamma, alpha=alpha)
+    ref_ret = ogae.compute_returns(rewards, mask, doc_ids, gamma=gamma)
+    d = [t.to(dev) for t in (rewards, values, mask, doc_ids)]
+    adv, lam = compute_vapo_gae(*d, n_docs_total, lengths=None if lengths is None else lengths.to(dev),
+                                gamma=gamma, alpha=alpha)
+    ret = compute_returns(d[0], d[2], d[3], gamma=gamma)
+    assert (adv.cpu() - ref_adv).abs().max().item() <= TOL
+    assert (ret.cpu() - ref_ret).abs().max().item() <= TOL
+    assert (lam.cpu() - ref_lam).abs().max().item() <= 1e-6
+    a2, r2, l2 = gae_and_returns(*d, n_docs_total, lengths=None if lengths is None else lengths.to(dev),
+                                 gamma=gamma, alpha=alpha)
+    assert torch.equal(a2, adv) and torch.equal(r2, ret) and torch.equal(l2, lam)
+
+
+def test_packed_with_padding_slot_and_bf16_values(dev):
+    from meshy_amd.gae import compute_vapo_gae
+
+    g = torch.Generator().manual_seed(2)
+    lens = [5, 1, 300, 77, 4096 * 2 + 5]
+    pad = 40
+    T = sum(lens) + pad
+    doc_ids = torch.cat([torch.full((L,), j) for j, L in enumerate(lens)] + [torch.full((pad,), len(lens))])
+    mask = torch.ones(T)
+    mask[doc_ids == len(lens)] = 0
+    mask[torch.rand(T, generator=g) < 0.01] = 0
+    values = torch.randn(T, generator=g).to(torch.bfloat16)
+    rewards = torch.randn(T, generator=g)
+    args = [x.reshape(1, -1) for x in (rewards, values, mask, doc_ids)]
+    ref_adv, ref_lam = ogae.compute_vapo_gae(*args, len(lens), gamma=1.0, alpha=1.5)
+    adv, lam = compute_vapo_gae(*[a.to(dev) for a in args], len(lens), gamma=1.0, alpha=1.5)
+    assert (adv.cpu() - ref_adv).abs().max().item() <= TOL
+    assert (lam.cpu() - ref_lam).abs().max().item() <= 1e-6
+
+
+def test_closed_form_terminal_reward(dev):
+    """V = 0, one terminal reward R, constant lambda, gamma = 1: A_t = lambda^(T-1-t) R,
+    returns = R on the whole run (gae.py:196-199)."""
+    from meshy_amd.gae import compute_returns, compute_vapo_gae
+
+    S, R, lam = 5000, 0.75, 0.95
+    mask = torch.ones(1, S)
+    rewards = torch.zeros(1, S)
+    rewards[0, -1] = R
+    values = torch.zeros(1, S)
+    doc_ids = torch.zeros(1, S, dtype=torch.long)
+    lengths = torch.full((1,), 1.0 / (1.0 - lam))
+    adv, _ = compute_vapo_gae(rewards.to(dev), values.to(dev), mask.to(dev), doc_ids.to(dev), 1,
+                              lengths=lengths.to(dev), gamma=1.0, alpha=1.0)
+    lam_f = float(1.0 - 1.0 / (1.0 * float(lengths[0])))
+    expect = torch.tensor([lam_f ** (S - 1 - t) * R for t in range(S)], dtype=torch.float64)
+    assert (adv[0].cpu().double() - expect).abs().max().item() <= 1e-5
+    ret = compute_returns(rewards.to(dev), mask.to(dev), doc_ids.to(dev), gamma=1.0)
+    assert torch.allclose(ret.cpu(), torch.full((1, S), R))
+
+
+def test_config4_full_size(dev):
+    """Config 4: 1024 docs (~5.9M tokens), values bf16, gamma 1, lambda 0.95 (lengths trick),
+    packed [1, T] on the GPU against the sequential loop on padded [1024, S_max] rows."""
+    from meshy_amd import workloads
+    from meshy_amd.gae import gae_and_returns
+
+    batch, values, terminal = workloads.config4(4)
+    n = len(batch.lengths)
+    L = batch.lengths
+    S_max = int(L.max())
+    doc_ids_flat = np.repeat(np.arange(n), L)
+    pos = np.arange(batch.total) - np.repeat(batch.offsets[:-1], L)
+    mask_flat = batch.mask
+    rewards_flat = np.zeros(batch.total, np.float32)
+    last = batch.offsets[1:] - 1
+    rewards_flat[last] = terminal
+    v_bf16 = torch.from_numpy(values).to(torch.bfloat16)
+    lengths = torch.full((n,), 1.0 / (1.0 - 0.95))
+    adv, ret, lam = gae_and_returns(
+        torch.from_numpy(rewards_flat).reshape(1, -1).to(dev), v_bf16.reshape(1, -1).to(dev),
+        torch.from_numpy(mask_flat).reshape(1, -1).to(dev),
+        torch.from_numpy(doc_ids_flat).reshape(1, -1).to(dev), n, lengths=lengths.to(dev), gamma=1.0, alpha=1.0)
+    # the same data as padded rows for the sequential oracle
+    R = torch.zeros(n, S_max)
+    Vp = torch.zeros(n, S_max)
+    M = torch.zeros(n, S_max)
+    R[doc_ids_flat, pos] = torch.from_numpy(rewards_flat)
+    Vp[doc_ids_flat, pos] = v_bf16.float()
+    M[doc_ids_flat, pos] = torch.from_numpy(mask_flat)
+    ids = torch.arange(n).unsqueeze(1).expand(n, S_max).contiguous()
+    ref_adv, _ = ogae.compute_vapo_gae(R, Vp, M, ids, n, lengths=lengths, gamma=1.0, alpha=1.0)
+    ref_ret = ogae.compute_returns(R, M, ids, gamma=1.0)
+    got_adv = torch.zeros(n, S_max)
+    got_ret = torch.zeros(n, S_max)
+    got_adv[doc_ids_flat, pos] = adv.reshape(-1).cpu()
+    got_ret[doc_ids_flat, pos] = ret.reshape(-1).cpu()
+    assert (got_adv - ref_adv).abs().max().item() <= TOL
+    assert (got_ret - ref_ret).abs().max().item() <= TOL
+
+
+def test_whitening_known_answers(dev):
+    # test_vapo_alignment.py:39-46
+    from meshy_amd.batch import ADVANTAGE_TOKENS
+    from meshy_amd.vapo import whiten_advantages
+
+    def row(vals):
+        return {ADVANTAGE_TOKENS: torch.tensor(vals, dtype=torch.float32),
+                "mask_assistant": torch.tensor([0] + [1] * (len(vals) - 1))}
+
+    s = row([2., 4., 1000.])
+    whiten_advantages([s], 3, dev)
+    torch.testing.assert_close(s[ADVANTAGE_TOKENS], torch.tensor([-2 ** -.5, 2 ** -.5, 0.]))
+    s = row([2., 2., 1000.])
+    whiten_advantages([s], 3, dev)
+    assert s[ADVANTAGE_TOKENS].abs().sum() == 0
+    whiten_advantages([], 3, dev)
+
+
+def test_whitening_matches_oracle(dev):
+    from meshy_amd.batch import ADVANTAGE_TOKENS
+    from meshy_amd.vapo import whiten_advantages
+
+    g = torch.Generator().manual_seed(0)
+    mk = []
+    for j in range(20):
+        n = int(torch.randint(1, 400, (1,), generator=g))
+        mk.append({ADVANTAGE_TOKENS: torch.randn(n, generator=g) * 3 + 1,
+                   "mask_assistant": (torch.rand(n, generator=g) > 0.3).float()})
+    ref = [{k: v.clone() for k, v in s.items()} for s in mk]
+    whiten_advantages(mk, 300, dev)
+    ovapo.whiten_advantages(ref, 300)
+    for a, b in zip(mk, ref):
+        assert (a[ADVANTAGE_TOKENS] - b[ADVANTAGE_TOKENS]).abs().max().item() <= 1e-4

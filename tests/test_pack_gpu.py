@@ -1,0 +1,271 @@
+"""Micro-batch packing and GRPO on the GPU against the oracle and the
+reference's known answers (tests/test_dynamic_batching.py:240-316,
+tests/test_rollout_advantage.py:13-18).  Indices and copies are bit-exact."""
+
+from __future__ import annotations
+
+from types import SimpleNamespace
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import batch as obatch
+from oracle import grpo as ogrpo
+
+pytestmark = pytest.mark.gpu
+
+
+class _NoCp:
+    enabled = False
+
+    def shard_seq(self, *tensors):
+        return tensors
+
+
+def _sample(length, prompt=3, adv=1.0, seed=0):
+    g = torch.Generator().manual_seed(seed)
+    mask = torch.ones(length)
+    mask[:prompt] = 0
+    return {
+        "tokens": torch.randint(1, 1000, (length,), generator=g),
+        "logprobs": torch.randn(length, generator=g),
+        "mask_assistant": mask,
+        "advantage": torch.tensor(adv),
+    }
+
+
+def _shift(x):
+    return torch.cat([x[1:], x.new_zeros(1)])
+
+
+def _assert_same(mb, ref, layout):
+    for k in ("input_ids", "labels", "positions", "mask", "doc_ids"):
+        got = getattr(mb, k).cpu()
+        assert got.dtype == ref[k].dtype, k
+        assert torch.equal(got, ref[k]), k
+    if ref["rollout_logprobs"] is None:
+        assert mb.rollout_logprobs is None
+    else:
+        assert torch.equal(mb.rollout_logprobs.cpu(), ref["rollout_logprobs"])
+    assert torch.equal(mb.advantages.cpu(), ref["advantages"])
+    assert torch.equal(mb.lengths.cpu(), ref["lengths"])
+    assert mb.n_docs == ref["n_docs"]
+    assert torch.equal(mb.positive_lm_weights.cpu(), ref["positive_lm_weights"])
+    if layout == "packed":
+        assert torch.equal(mb.attention_masks.cu_seq_q.cpu(), ref["cu_seqlens"])
+        assert mb.attention_masks.max_q == ref["max_seqlen"] == mb.attention_masks.max_k
+    else:
+        assert mb.attention_masks is None
+
+
+def test_packed_layout_and_metadata(dev):
+    # test_dynamic_batching.py:259-285
+    from meshy_amd.batch import build_micro_batch
+    from meshy_amd.plan import MicroPlan
+
+    samples = [_sample(10, seed=1), _sample(6, seed=2, adv=2.0)]
+    mb = build_micro_batch(samples, MicroPlan((0, 1), 32, (10, 6)), layout="packed", device=dev,
+                           sharder=_NoCp(), need_rollout_lp=True)
+    assert mb.input_ids.shape == (1, 32)
+    row = mb.input_ids[0].cpu()
+    assert torch.equal(row[:10], samples[0]["tokens"]) and torch.equal(row[10:16], samples[1]["tokens"])
+    assert (row[16:] == 0).all()
+    assert torch.equal(mb.labels[0, :10].cpu(), _shift(samples[0]["tokens"]))
+    assert mb.mask[0, 9] == 0 and mb.mask[0, 15] == 0
+    assert torch.equal(mb.rollout_logprobs[0, 10:16].cpu(), _shift(samples[1]["logprobs"]))
+    assert torch.equal(mb.positions[0, 16:].cpu(), torch.arange(16, dtype=torch.int32))
+    assert (mb.doc_ids[0, 16:] == 2).all()
+    assert torch.equal(mb.attention_masks.cu_seq_q.cpu(), torch.tensor([0, 10, 16, 32], dtype=torch.int32))
+    assert mb.attention_masks.max_q == 16
+    assert torch.allclose(mb.advantages.cpu(), torch.tensor([1.0, 2.0]))
+    ref = obatch.build_micro_batch(samples, (0, 1), 32, (10, 6), layout="packed", need_rollout_lp=True)
+    _assert_same(mb, ref, "packed")
+
+
+def test_packed_without_padding_has_no_pad_doc(dev):
+    from meshy_amd.batch import build_micro_batch
+    from meshy_amd.plan import MicroPlan
+
+    mb = build_micro_batch([_sample(8, seed=3)], MicroPlan((0,), 8, (8,)), layout="packed", device=dev,
+                           sharder=_NoCp(), need_rollout_lp=False)
+    assert torch.equal(mb.attention_masks.cu_seq_q.cpu(), torch.tensor([0, 8], dtype=torch.int32))
+    assert mb.rollout_logprobs is None
+
+
+@pytest.mark.parametrize("layout", ["padded", "packed"])
+def test_filler_micro_is_all_padding(dev, layout):
+    from meshy_amd.batch import build_micro_batch
+    from meshy_amd.plan import MicroPlan
+
+    mb = build_micro_batch([], MicroPlan((), 64, ()), layout=layout, device=dev, sharder=_NoCp(),
+                           need_rollout_lp=True)
+    assert mb.n_docs == 0 and mb.input_ids.shape == (1, 64)
+    assert (mb.mask == 0).all() and (mb.doc_ids == 0).all() and mb.advantages.numel() == 0
+    ref = obatch.build_micro_batch([], (), 64, (), layout=layout, need_rollout_lp=True)
+    _assert_same(mb, ref, layout)
+
+
+def test_padded_matches_per_sample_shift(dev):
+    # test_dynamic_batching.py:240-256
+    from meshy_amd.batch import build_micro_batch
+    from meshy_amd.plan import MicroPlan
+
+    samples = [_sample(10, seed=1), _sample(6, seed=2, adv=-0.5)]
+    mb = build_micro_batch(samples, MicroPlan((0, 1), 16, (10, 6)), layout="padded", device=dev,
+                           sharder=_NoCp(), need_rollout_lp=True)
+    assert mb.input_ids.shape == (2, 16) and mb.n_slots == 3
+    ref = obatch.build_micro_batch(samples, (0, 1), 16, (10, 6), layout="padded", need_rollout_lp=True)
+    _assert_same(mb, ref, "padded")
+    assert torch.allclose(mb.advantages.cpu(), torch.tensor([1.0, -0.5]))
+
+
+def test_truncation_in_micro(dev):
+    # test_dynamic_batching.py:309-316
+    from meshy_amd.batch import build_micro_batch
+    from meshy_amd.plan import MicroPlan
+
+    samples = [_sample(20, seed=4)]
+    mb = build_micro_batch(samples, MicroPlan((0,), 16, (12,)), layout="padded", device=dev,
+                           sharder=_NoCp(), need_rollout_lp=False)
+    assert torch.equal(mb.input_ids[0, :12].cpu(), samples[0]["tokens"][:12])
+    assert mb.labels[0, 11] == 0 and mb.mask[0, 11] == 0 and int(mb.lengths[0]) == 12
+
+
+def test_per_token_advantages_and_positive_weights(dev):
+    from meshy_amd.batch import ADVANTAGE_TOKENS, build_micro_batches
+    from meshy_amd.plan import MicroPlan
+
+    samples = [_sample(9, seed=5), _sample(7, seed=6), _sample(12, seed=7)]
+    for j, s in enumerate(samples):
+        s[ADVANTAGE_TOKENS] = torch.randn(len(s["tokens"]), generator=torch.Generator().manual_seed(j))
+        s["reward"] = torch.tensor([1.0, 0.0, 0.9][j])
+        s["positive_lm_weight"] = torch.tensor(0.25 * (j + 1))
+    micros = [MicroPlan((2, 0), 32, (12, 9)), MicroPlan((1,), 8, (7,))]
+    for layout in ("packed", "padded"):
+        mbs = build_micro_batches(samples, micros, layout=layout, device=dev, sharder=_NoCp(),
+                                  need_rollout_lp=True)
+        for mb, m in zip(mbs, micros):
+            ref = obatch.build_micro_batch(samples, m.sample_idx, m.seq_len, m.doc_lens, layout=layout,
+                                           need_rollout_lp=True)
+            _assert_same(mb, ref, layout)
+
+
+@pytest.mark.parametrize("layout,align", [("packed", 2048), ("packed", 1), ("packed", 64), ("padded", 64)])
+def test_config0_full_plan_bit_exact(dev, layout, align):
+    """Config 0 (256 samples, budget 8192): every micro of the plan against the oracle."""
+    from meshy_amd import workloads
+    from meshy_amd.batch import build_micro_batches
+    from meshy_amd.plan import PlannerConfig, build_plan
+
+    batch, rewards, _ = workloads.config0(0)
+    adv = np.linspace(-1, 1, len(rewards)).astype(np.float32)
+    samples = batch.sample_dicts(rewards=rewards, advantages=adv)
+    budget = 8192 if layout == "packed" else 16384
+    cfg = PlannerConfig(layout=layout, mini_batch_size=256, seq_len=8192, align=align,
+                        max_tokens_per_micro=budget)
+    lt = batch.loss_tokens(8192)
+    plan = build_plan(batch.lengths.tolist(), lt.tolist(), 1, cfg)
+    local = plan.local_samples(samples, 0)
+    micros = [m for mini in plan.per_rank[0] for m in mini.micros]
+    mbs = build_micro_batches(local, micros, layout=layout, device=dev, sharder=_NoCp(),
+                              need_rollout_lp=True)
+    assert len(mbs) == len(micros)
+    for mb, m in zip(mbs, micros):
+        ref = obatch.build_micro_batch(local, m.sample_idx, m.seq_len, m.doc_lens, layout=layout,
+                                       need_rollout_lp=True)
+        _assert_same(mb, ref, layout)
+
+
+def test_config3_long_context_micros(dev):
+    """Config 3 planner edge cases materialised: exact-budget fits and a full 131072 micro."""
+    from meshy_amd import workloads
+    from meshy_amd.batch import build_micro_batches
+    from meshy_amd.plan import PlannerConfig, build_plan
+
+    rng = np.random.default_rng(3)
+    for lengths in ([131072], [65536, 65536], [131071, 1], [100000, 31073]):
+        prompt = np.full(len(lengths), 16)
+        batch = workloads.RaggedBatch(prompt, np.array(lengths) - 16, rng)
+        samples = batch.sample_dicts()
+        cfg = PlannerConfig(layout="packed", mini_batch_size=len(lengths), seq_len=131072, align=2048,
+                            max_tokens_per_micro=131072)
+        plan = build_plan(lengths, lengths, 1, cfg)
+        micros = [m for mini in plan.per_rank[0] for m in mini.micros]
+        mbs = build_micro_batches(samples, micros, layout="packed", device=dev, sharder=_NoCp(),
+                                  need_rollout_lp=False)
+        for mb, m in zip(mbs, micros):
+            assert m.seq_len <= 131072
+            ref = obatch.build_micro_batch(samples, m.sample_idx, m.seq_len, m.doc_lens, layout="packed",
+                                           need_rollout_lp=False)
+            _assert_same(mb, ref, "packed")
+
+
+def test_deterministic_and_repeatable(dev):
+    from meshy_amd import workloads
+    from meshy_amd.batch import build_micro_batches
+    from meshy_amd.plan import PlannerConfig, build_plan
+
+    batch, rewards, _ = workloads.config0(1)
+    samples = batch.sample_dicts(rewards=rewards, advantages=rewards)
+    cfg = PlannerConfig(layout="packed", mini_batch_size=256, seq_len=8192, align=2048,
+                        max_tokens_per_micro=8192)
+    plan = build_plan(batch.lengths.tolist(), batch.loss_tokens(8192).tolist(), 1, cfg)
+    samples = plan.local_samples(samples, 0)
+    micros = [m for mini in plan.per_rank[0] for m in mini.micros]
+    a = build_micro_batches(samples, micros, layout="packed", device=dev, need_rollout_lp=True)
+    b = build_micro_batches(samples, micros, layout="packed", device=dev, need_rollout_lp=True)
+    for x, y in zip(a, b):
+        assert torch.equal(x.input_ids, y.input_ids) and torch.equal(x.mask, y.mask)
+        assert torch.equal(x.attention_masks.cu_seq_q, y.attention_masks.cu_seq_q)
+
+
+def test_cpu_device_is_rejected():
+    from meshy_amd.batch import build_micro_batch
+    from meshy_amd.plan import MicroPlan
+
+    with pytest.raises(ValueError):
+        build_micro_batch([_sample(4)], MicroPlan((0,), 4, (4,)), layout="packed",
+                          device=torch.device("cpu"), sharder=_NoCp(), need_rollout_lp=False)
+
+
+# ---------------------------------------------------------------------- GRPO
+
+def test_grpo_known_answer(dev):
+    # test_rollout_advantage.py:13-18 (pins the unbiased std)
+    from meshy_amd.advantage import grpo_advantage
+
+    samples = [SimpleNamespace(reward=r, advantage=None) for r in (1.0, 2.0, 3.0)]
+    grpo_advantage(samples, device=dev)
+    assert [s.advantage for s in samples] == pytest.approx([-1.0, 0.0, 1.0], abs=1e-6)
+
+
+def test_grpo_special_cases(dev):
+    from meshy_amd.advantage import grpo_advantage, grpo_advantages
+
+    one = [SimpleNamespace(reward=0.7, advantage=None)]
+    grpo_advantage(one, device=dev)
+    assert one[0].advantage == 0.7
+    r = torch.tensor([1.0, 1.0, 1.0, 0.0, 0.0, 0.5], device=dev)
+    off = torch.tensor([0, 3, 5, 6], device=dev)
+    adv = grpo_advantages(r, off).cpu()
+    assert adv[:5].abs().max() == 0.0  # all-equal groups -> 0
+    assert adv[5].item() == 0.5         # size-1 group keeps its reward
+
+
+def test_grpo_config0_matches_oracle(dev):
+    from meshy_amd import workloads
+    from meshy_amd.advantage import grpo_advantages
+
+    _, rewards, group_offsets = workloads.config0(0)
+    r = torch.from_numpy(rewards)
+    off = torch.from_numpy(group_offsets)
+    got = grpo_advantages(r.to(dev), off.to(dev)).cpu()
+    ref = ogrpo.grpo_batched(r, off)
+    assert (got - ref).abs().max().item() <= 1e-5
+    # ragged groups with random float rewards
+    g = torch.Generator().manual_seed(0)
+    r = torch.rand(100, generator=g)
+    off = torch.tensor([0, 1, 9, 10, 40, 41, 100])
+    got = grpo_advantages(r.to(dev), off.to(dev)).cpu()
+    assert (got - ogrpo.grpo_batched(r, off)).abs().max().item() <= 1e-4

@@ -1,0 +1,255 @@
+"""Clipped PPO loss on the GPU: the reference's known answers
+(tests/test_ppo_diagnostics.py:58-95, tests/test_vapo_alignment.py:116-149)
+and the oracle (the reference's torch restatement, autograd for gradients).
+Tolerance: 1e-3 absolute on loss, diagnostics and gradients."""
+
+from __future__ import annotations
+
+import math
+from types import SimpleNamespace as NS
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import ppo as oppo
+
+pytestmark = pytest.mark.gpu
+TOL = 1e-3
+
+
+class _NoCp:
+    enabled = False
+
+    def all_reduce_sum(self, value):
+        return value
+
+
+def _stub(**kw):
+    base = dict(ppo_clip_eps_low=0.2, ppo_clip_eps_high=0.28, use_tis=True, tis_ratio_min=0.5,
+                tis_ratio_max=5.0, calculate_per_token_loss=True, old_logprobs_source="rollout",
+                sharder=_NoCp(), parallel_dims=NS(cp=1))
+    base.update(kw)
+    return NS(**base)
+
+
+def _batch(dev, rows=2, S=8):
+    from meshy_amd.batch import Batch
+
+    mask = torch.ones(rows, S)
+    mask[:, -1] = 0
+    doc_ids = torch.arange(rows).unsqueeze(1).expand(rows, S).clone()
+    return Batch(
+        input_ids=torch.zeros(rows, S, dtype=torch.long, device=dev),
+        labels=torch.zeros(rows, S, dtype=torch.long, device=dev),
+        positions=torch.zeros(rows, S, dtype=torch.int32, device=dev),
+        mask=mask.to(dev), doc_ids=doc_ids.to(dev), advantages=torch.tensor([1.0, -1.0], device=dev),
+        rollout_logprobs=None, lengths=torch.tensor([S, S], dtype=torch.int32, device=dev), n_docs=rows,
+    )
+
+
+def test_reports_kl_and_ess(dev):
+    # test_ppo_diagnostics.py:58-80
+    from meshy_amd.loss import ppo_clip_loss, reduce_mini_metrics
+    from meshy_amd.plan import MiniPlan
+
+    mb = _batch(dev)
+    mini = MiniPlan(micros=(), n_docs_global=2, n_tokens_global=int(mb.mask.sum()), tokens_per_rank=(16,))
+    old = -torch.ones(2, 8, device=dev)
+    new = (old + 0.1).requires_grad_()
+    mb.rollout_logprobs = old.clone()
+    loss, sums = ppo_clip_loss(_stub(), new, old, mb, mini, entropy=torch.full((2, 8), 2.0, device=dev))
+    red = reduce_mini_metrics(NS(parallel_dims=NS(get_optional_mesh=lambda name: None)), sums)
+    assert red["ppo_kl"] == pytest.approx(-0.1, abs=1e-6)
+    assert red["log_ratio_abs_mean"] == pytest.approx(0.1, abs=1e-6)
+    assert red["ratio_mean"] == pytest.approx(math.exp(0.1), rel=1e-6)
+    assert red["ess_ratio"] == pytest.approx(1.0, rel=1e-6)
+    assert red["entropy"] == pytest.approx(2.0, rel=1e-6)
+    assert red["train_rollout_kl"] == pytest.approx(math.exp(-0.1) + 0.1 - 1, rel=1e-4)
+    assert red["train_rollout_logdiff_abs"] == pytest.approx(0.1, rel=1e-5)
+    assert sums["token_count"].item() == float(mb.mask.sum())
+    loss.backward()
+
+
+def test_ess_drops_with_uneven_weights(dev):
+    # test_ppo_diagnostics.py:83-95
+    from meshy_amd.loss import ppo_clip_loss, reduce_mini_metrics
+    from meshy_amd.plan import MiniPlan
+
+    mb = _batch(dev)
+    mini = MiniPlan(micros=(), n_docs_global=2, n_tokens_global=int(mb.mask.sum()), tokens_per_rank=(16,))
+    old = torch.zeros(2, 8, device=dev)
+    new = torch.zeros(2, 8, device=dev)
+    new[:, 0] = 1.5
+    _, sums = ppo_clip_loss(_stub(), new, old, mb, mini)
+    red = reduce_mini_metrics(NS(parallel_dims=NS(get_optional_mesh=lambda name: None)), sums)
+    assert 0.0 < red["ess_ratio"] < 1.0
+    assert "train_rollout_kl" not in red
+
+
+def test_icepop_and_positive_lm_gradient(dev):
+    # test_vapo_alignment.py:116-149
+    from meshy_amd.batch import Batch
+    from meshy_amd.loss import ppo_clip_loss
+    from meshy_amd.plan import MiniPlan
+
+    stub = NS(ppo_clip_eps_low=.2, ppo_clip_eps_high=.28, use_tis=True, use_icepop=True, tis_ratio_min=.5,
+              tis_ratio_max=5., calculate_per_token_loss=True, positive_lm_loss_coef=.1,
+              old_logprobs_source="train", sharder=NS(all_reduce_sum=lambda x: x), parallel_dims=NS(cp=1))
+    old = torch.full((1, 3), -2., device=dev)
+    new = old.clone().requires_grad_()
+    z = torch.zeros(1, 3, dtype=torch.long, device=dev)
+    batch = Batch(z, z, z.int(), torch.ones(1, 3, device=dev), z.clone(), torch.ones(1, device=dev),
+                  old - torch.tensor([[2., 6., .25]], device=dev).log(), torch.tensor([3], device=dev), 1,
+                  positive_lm_weights=torch.tensor([.5], device=dev))
+    mini = MiniPlan(micros=(), n_docs_global=1, n_tokens_global=3, tokens_per_rank=(3,))
+    loss, sums = ppo_clip_loss(stub, new, old, batch, mini)
+    assert float(loss.detach()) == pytest.approx(-2 / 3 + .1, abs=1e-6)
+    assert float(sums["tis_masked_sum"]) == 2.
+    assert float(sums["ratio_sum"]) == 3.
+    loss.backward()
+    torch.testing.assert_close(new.grad.cpu(), torch.tensor([[-2.05 / 3, -.05 / 3, -.05 / 3]]))
+    stub.calculate_per_token_loss = False
+    batch.rollout_logprobs = old - torch.tensor([[.5, 5., 1.]], device=dev).log()
+    loss, sums = ppo_clip_loss(stub, old.clone().requires_grad_(), old, batch, mini)
+    assert float(sums["tis_masked_sum"]) == 0.
+    assert float(loss.detach()) == pytest.approx(-6.5 / 3 + .1, abs=1e-6)
+    stub.use_icepop = False
+    stub.positive_lm_loss_coef = 0.
+    loss, sums = ppo_clip_loss(stub, old, old, batch, mini)
+    assert float(loss) == pytest.approx(-1., abs=1e-6)
+
+
+def _compare(dev, new, old, mask, doc_ids, adv, n_docs, *, rollout=None, entropy=None, pos_w=None, **cfg):
+    """Kernel vs oracle: loss, every sum, and d loss / d new."""
+    from meshy_amd.batch import Batch
+    from meshy_amd.loss import ppo_clip_loss
+    from meshy_amd.plan import MiniPlan
+
+    n_docs_global = cfg.pop("n_docs_global", n_docs)
+    n_tokens_global = cfg.pop("n_tokens_global", int(mask.sum()))
+    stub = NS(ppo_clip_eps_low=cfg.get("clip_low", 0.2), ppo_clip_eps_high=cfg.get("clip_high", 0.28),
+              use_tis=cfg.get("use_tis", False), use_icepop=cfg.get("use_icepop", False),
+              tis_ratio_min=cfg.get("tis_min", 0.5), tis_ratio_max=cfg.get("tis_max", 5.0),
+              calculate_per_token_loss=cfg.get("per_token_loss", True),
+              positive_lm_loss_coef=cfg.get("positive_lm_coef", 0.0),
+              old_logprobs_source="train" if cfg.get("train_lp_is_old") else "rollout",
+              sharder=_NoCp(), parallel_dims=NS(cp=1))
+    rows, S = new.shape
+    z = torch.zeros(rows, S, dtype=torch.long, device=dev)
+    mb = Batch(z, z, z.int(), mask.to(dev), doc_ids.to(dev), adv.to(dev),
+               None if rollout is None else rollout.to(dev), torch.zeros(max(n_docs, 1), device=dev), n_docs,
+               positive_lm_weights=None if pos_w is None else pos_w.to(dev))
+    mini = MiniPlan(micros=(), n_docs_global=n_docs_global, n_tokens_global=n_tokens_global, tokens_per_rank=())
+    nd = new.to(dev).requires_grad_(True)
+    loss, sums = ppo_clip_loss(stub, nd, old.to(dev), mb, mini, entropy=None if entropy is None else entropy.to(dev))
+    loss.backward()
+    nr = new.clone().requires_grad_(True)
+    ref_loss, ref_sums = oppo.ppo_clip_loss(
+        nr, old, mask, doc_ids, adv, n_docs, n_docs_global=n_docs_global, n_tokens_global=n_tokens_global,
+        clip_low=stub.ppo_clip_eps_low, clip_high=stub.ppo_clip_eps_high, use_tis=stub.use_tis,
+        use_icepop=stub.use_icepop, tis_min=stub.tis_ratio_min, tis_max=stub.tis_ratio_max,
+        per_token_loss=stub.calculate_per_token_loss, positive_lm_coef=stub.positive_lm_loss_coef,
+        positive_lm_weights=pos_w, rollout_lp=rollout, train_lp_is_old=cfg.get("train_lp_is_old", False),
+        entropy=entropy)
+    ref_loss.backward()
+    assert set(sums) == set(ref_sums)
+    assert abs(loss.item() - ref_loss.item()) <= TOL
+    for k in ref_sums:
+        # 1e-3 absolute for O(1) values, 1e-3 relative for token sums over many tokens.
+        a, b = float(sums[k]), float(ref_sums[k])
+        assert abs(a - b) <= TOL * max(1.0, abs(b)), k
+    g = nd.grad.cpu()
+    assert (g - nr.grad).abs().max().item() <= TOL * max(1e-6, nr.grad.abs().max().item())
+    return loss, sums
+
+
+def _random_packed(n_docs, seed, max_len=300, pad=17):
+    g = torch.Generator().manual_seed(seed)
+    lens = torch.randint(1, max_len, (n_docs,), generator=g).tolist()
+    T = sum(lens) + pad
+    doc_ids = torch.cat([torch.full((L,), j) for j, L in enumerate(lens)] + [torch.full((pad,), n_docs)])
+    mask = (torch.rand(T, generator=g) > 0.3).float()
+    mask[doc_ids == n_docs] = 0
+    old = -torch.rand(T, generator=g) * 8
+    new = old + torch.randn(T, generator=g) * 0.3
+    roll = old + torch.randn(T, generator=g) * 0.2
+    ent = torch.rand(T, generator=g) * 5
+    adv = torch.randn(n_docs, generator=g)
+    posw = torch.rand(n_docs, generator=g)
+    return [x.reshape(1, -1) if x.numel() == T else x for x in (new, old, mask, doc_ids)] + [adv, roll.reshape(1, -1),
+                                                                                            ent.reshape(1, -1), posw]
+
+
+@pytest.mark.parametrize("variant", [
+    dict(),
+    dict(per_token_loss=False),
+    dict(use_tis=True),
+    dict(use_icepop=True, train_lp_is_old=True),
+    dict(use_icepop=True, positive_lm_coef=0.1, per_token_loss=False),
+    dict(positive_lm_coef=0.3),
+])
+def test_matches_oracle_packed(dev, variant):
+    new, old, mask, doc_ids, adv, roll, ent, posw = _random_packed(37, seed=len(str(variant)))
+    _compare(dev, new, old, mask, doc_ids, adv, 37, rollout=roll, entropy=ent, pos_w=posw, **variant)
+
+
+def test_per_token_advantages_padded_rows(dev):
+    g = torch.Generator().manual_seed(5)
+    rows, S = 6, 700
+    doc_ids = torch.arange(rows).unsqueeze(1).expand(rows, S).clone()
+    mask = (torch.rand(rows, S, generator=g) > 0.2).float()
+    old = -torch.rand(rows, S, generator=g) * 3
+    new = old + torch.randn(rows, S, generator=g) * 0.5
+    adv = torch.randn(rows, S, generator=g)
+    _compare(dev, new, old, mask, doc_ids, adv, rows, per_token_loss=False)
+
+
+def test_many_tiny_documents_and_empty_pad(dev):
+    # 3000 one- and two-token documents: many (tile, document) pairs per tile.
+    g = torch.Generator().manual_seed(9)
+    lens = (torch.randint(1, 3, (3000,), generator=g)).tolist()
+    doc_ids = torch.cat([torch.full((L,), j) for j, L in enumerate(lens)]).reshape(1, -1)
+    T = doc_ids.numel()
+    mask = torch.ones(1, T)
+    old = -torch.rand(1, T, generator=g)
+    new = old + torch.randn(1, T, generator=g) * 0.4
+    adv = torch.randn(3000, generator=g)
+    _compare(dev, new, old, mask, doc_ids, adv, 3000, per_token_loss=False)
+
+
+def test_config2_full_size(dev):
+    """Config 2: ~2M packed tokens, 512 docs, token-mean, eps 0.2/0.28, TIS off."""
+    from meshy_amd import workloads
+
+    batch, old, new, rewards, group_offsets = workloads.config2(2)
+    from oracle.grpo import grpo_batched
+
+    adv = grpo_batched(torch.from_numpy(rewards), torch.from_numpy(group_offsets))
+    n = len(batch.lengths)
+    doc_ids = torch.from_numpy(np.repeat(np.arange(n), batch.lengths)).reshape(1, -1)
+    mask = torch.from_numpy(batch.mask).reshape(1, -1)
+    loss, sums = _compare(dev, torch.from_numpy(new).reshape(1, -1), torch.from_numpy(old).reshape(1, -1),
+                          mask, doc_ids, adv, n, clip_low=0.2, clip_high=0.28, per_token_loss=True)
+    assert 0.0 <= float(sums["clip_sum"]) / float(sums["token_count"]) <= 1.0
+
+
+def test_deterministic(dev):
+    from meshy_amd.batch import Batch
+    from meshy_amd.loss import ppo_clip_loss
+    from meshy_amd.plan import MiniPlan
+
+    new, old, mask, doc_ids, adv, roll, ent, posw = _random_packed(200, seed=3, max_len=5000)
+    rows, S = new.shape
+    z = torch.zeros(rows, S, dtype=torch.long, device=dev)
+    mb = Batch(z, z, z.int(), mask.to(dev), doc_ids.to(dev), adv.to(dev), roll.to(dev),
+               torch.zeros(200, device=dev), 200)
+    mini = MiniPlan((), 200, int(mask.sum()), ())
+    outs = []
+    for _ in range(2):
+        nd = new.to(dev).requires_grad_(True)
+        loss, sums = ppo_clip_loss(_stub(use_tis=False), nd, old.to(dev), mb, mini)
+        loss.backward()
+        outs.append((loss.item(), torch.stack(list(sums.values())).cpu(), nd.grad.cpu()))
+    assert outs[0][0] == outs[1][0]
+    assert torch.equal(outs[0][1], outs[1][1]) and torch.equal(outs[0][2], outs[1][2])
