@@ -1,18 +1,23 @@
 """Benchmark of the ragged-batch hot path on one MI355X.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--cpu-rows R] [--no-cpu]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--quick] [--no-cpu]
 
 A step is one pass of the fused packed logprob + entropy kernel over one
 micro-batch of bf16 logits [T=16384, V=151936] (Qwen3-1.7B vocabulary),
-already resident in HBM.  Prints ONE JSON line:
+already resident in HBM.  Prints ONE JSON line with
 
-* value            packed tokens/s of the logprob + entropy pass
-* roofline         algorithmic bytes per launch / average launch time vs 8 TB/s
-* cpu_baseline     the reference's chunk loop (-cross_entropy on 1024-row fp32
-                   upcasts + 512-row entropy slices) restated on CPU torch, on a
-                   bounded row sample, on this host's cores
-* pack_latency_us  config-0 pack (host plan + one H2D + device pack + GRPO)
-* kernels          per-kernel µs and GB/s of the other hot-path kernels
+* value / ms_per_step  packed tokens/s of that pass (the headline metric)
+* roofline             algorithmic bytes per launch / average launch time
+                       (HIP events over the timed region) against 8 TB/s
+* cpu_baseline         the reference's chunk loop (fp32 upcast, 1024-row
+                       -cross_entropy, 512-row entropy slices) restated on CPU
+                       torch on a bounded row sample, on this host's cores
+* pack_latency_us      config 0: 256 samples -> native plan -> one host-to-
+                       device copy -> GRPO + pack kernels, wall clock
+* kernels              per-kernel device time, algorithmic GB/s and the
+                       restated CPU path for configs 0, 2, 3 and 4
+* end_to_end           pack -> logprob+entropy -> GRPO -> PPO fwd+bwd at
+                       T = 16384, GPU wall against the CPU restatement
 """
 
 from __future__ import annotations
@@ -29,32 +34,60 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 T_TOK, VOCAB = 16384, 151936
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "traffic.json")
 
 
-def _sync_all():
+def _sync():
     import torch
 
     torch.cuda.synchronize()
 
 
-def _time_launches(fn, steps: int, warmup: int) -> float:
-    """Average ms per call of `fn` over `steps` calls, HIP events on the current stream."""
+def _gpu_ms(fn, steps: int, warmup: int) -> float:
+    """Average ms per call of `fn` (HIP events on the current stream)."""
     import torch
 
     for _ in range(warmup):
         fn()
-    _sync_all()
+    _sync()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
     start.record()
     for _ in range(steps):
         fn()
     stop.record()
-    _sync_all()
+    _sync()
     return start.elapsed_time(stop) / steps
 
 
-def bench_logprob(steps: int, warmup: int):
+def _wall_ms(fn, runs: int, warmup: int = 1, gpu: bool = True) -> float:
+    """Median wall ms of `fn` (synchronized when `gpu`)."""
+    times = []
+    for i in range(warmup + runs):
+        if gpu:
+            _sync()
+        t0 = time.perf_counter()
+        fn()
+        if gpu:
+            _sync()
+        if i >= warmup:
+            times.append((time.perf_counter() - t0) * 1e3)
+    return statistics.median(times)
+
+
+def _entry(us: float, nbytes: float, cpu_ms: float | None = None, **extra):
+    gbs = nbytes / (us * 1e-6) / 1e9
+    e = {"us": round(us, 2), "bytes": int(nbytes), "GBps": round(gbs, 1), "frac_hbm": round(gbs / HBM_PEAK_GBS, 4)}
+    if cpu_ms is not None:
+        e["cpu_ms"] = round(cpu_ms, 3)
+        e["speedup_vs_cpu"] = round(cpu_ms * 1e3 / us, 1)
+    e.update(extra)
+    return e
+
+
+# ---------------------------------------------------------------- config 1
+
+def bench_logprob(steps, warmup):
     import torch
 
     from meshy_amd import logprob
@@ -68,38 +101,326 @@ def bench_logprob(steps: int, warmup: int):
     def step():
         out["r"] = logprob.logprobs_and_entropy(logits, labels, with_entropy=True)
 
-    ms = _time_launches(step, steps, warmup)
-    bytes_per_launch = T_TOK * VOCAB * 2 + T_TOK * 8 + T_TOK * 8
+    ms = _gpu_ms(step, steps, warmup)
     lp, ent = out["r"]
     assert torch.isfinite(lp).all() and torch.isfinite(ent).all()
-    return ms, bytes_per_launch, logits, labels
+    nbytes = T_TOK * VOCAB * 2 + T_TOK * 8 + T_TOK * 8
+    return ms, nbytes, logits, labels
 
 
-def cpu_baseline_logprob(logits_gpu, labels_gpu, rows: int):
-    """The reference chunk loop restated (oracle) on `rows` rows, on this host's cores."""
+def cpu_logprob_tokens_per_s(logits_gpu, labels_gpu, rows: int, runs: int = 5):
     import torch
 
     from oracle import logprob as olp
 
-    torch.set_num_threads(os.cpu_count() or 1)
     z = logits_gpu[:, :rows].cpu()
     y = labels_gpu[:, :rows].cpu()
-    times = []
-    for i in range(6):
-        t0 = time.perf_counter()
-        olp.forward_logprobs(z, y, chunk=1024, with_entropy=True, entropy_chunk_size=512)
-        dt = time.perf_counter() - t0
-        if i > 0:
-            times.append(dt)
-    med = statistics.median(times)
-    return {
-        "value": rows / med,
-        "unit": "tokens/s",
-        "cores": torch.get_num_threads(),
-        "kind": "port",
-        "sample": f"{rows} rows of the same [16384, 151936] bf16 logits, median of 5 after 1 warm-up "
-                  f"({med:.3f} s per pass)",
+    ms = _wall_ms(lambda: olp.forward_logprobs(z, y, chunk=1024, with_entropy=True, entropy_chunk_size=512),
+                  runs, gpu=False)
+    return rows / (ms * 1e-3), ms
+
+
+# ---------------------------------------------------------------- config 0
+
+def bench_pack(runs, no_cpu):
+    import torch
+
+    from meshy_amd import workloads
+    from meshy_amd.pipeline import RaggedSamples, pack_step
+    from meshy_amd.plan import PlannerConfig
+
+    dev = torch.device("cuda:0")
+    batch, rewards, group_offsets = workloads.config0(0)
+    ragged = RaggedSamples.from_arrays(batch.tokens, batch.mask, batch.logprobs, batch.offsets, rewards,
+                                       group_offsets)
+    cfg = PlannerConfig(layout="packed", mini_batch_size=256, seq_len=8192, align=2048,
+                        max_tokens_per_micro=8192)
+    res = {}
+
+    def full():
+        res["r"] = pack_step(ragged, cfg, dev)
+
+    wall = _wall_ms(full, runs, warmup=3)
+    lite = _wall_ms(lambda: pack_step(ragged, cfg, dev, with_plan_objects=False), runs, warmup=2)
+
+    def host_plan():
+        lengths, loss = ragged.sample_lengths(8192)
+        from meshy_amd.plan import plan_tables
+
+        plan_tables(lengths, loss, 1, cfg)
+
+    plan_ms = _wall_ms(host_plan, runs, gpu=False)
+    r = res["r"]
+    n_out = sum(mb.input_ids.numel() for mb in r.batches)
+    real = int(sum(m.n_tokens for m in (mm for mini in r.plan.per_rank[0] for mm in mini.micros)))
+    out = {
+        "pack_latency_us": round(wall * 1e3, 1),
+        "pack_latency_no_dataclasses_us": round(lite * 1e3, 1),
+        "host_plan_us": round(plan_ms * 1e3, 1),
+        "n_micro": len(r.batches),
+        "tokens": real,
+        "out_tokens": n_out,
+        # reads: token 4 + mask 4 + logprob 4 per real token; writes: ids, labels,
+        # doc_ids 8 each, positions 4, mask 4, rollout lp 4, adv_tok 4 per output token
+        "bytes": real * 12 + n_out * 40,
     }
+    if not no_cpu:
+        from oracle import batch as obatch
+        from oracle import grpo as ogrpo
+        from oracle import plan as oplan
+
+        samples = batch.sample_dicts(rewards=rewards)
+
+        def cpu():
+            lengths, loss = oplan.sample_lengths(samples, 8192)
+            local, per_rank = oplan.build_plan(lengths, loss, 1, layout="packed", mini_batch_size=256,
+                                               seq_len=8192, align=2048, max_tokens_per_micro=8192)
+            adv = [0.0] * len(samples)
+            for g in range(len(group_offsets) - 1):
+                a, b = int(group_offsets[g]), int(group_offsets[g + 1])
+                adv[a:b] = ogrpo.grpo_group([float(s["reward"]) for s in samples[a:b]])
+            loc = [dict(samples[i], advantage=adv[i]) for i in local[0]]
+            for micros, *_ in per_rank[0]:
+                for idx, seq_len, doc_lens in micros:
+                    obatch.build_micro_batch(loc, idx, seq_len, doc_lens, layout="packed", need_rollout_lp=True)
+
+        out["cpu_ms"] = round(_wall_ms(cpu, 5, gpu=False), 2)
+        out["speedup_vs_cpu"] = round(out["cpu_ms"] / wall, 1)
+    return out, ragged, cfg
+
+
+# ---------------------------------------------------------------- config 2
+
+def bench_ppo(steps, warmup, no_cpu):
+    from types import SimpleNamespace as NS
+
+    import numpy as np
+    import torch
+
+    from meshy_amd import workloads
+    from meshy_amd.advantage import grpo_advantages
+    from meshy_amd.batch import Batch
+    from meshy_amd.loss import ppo_clip_loss
+    from meshy_amd.plan import MiniPlan
+
+    dev = torch.device("cuda:0")
+    batch, old, new, rewards, group_offsets = workloads.config2(2)
+    n = len(batch.lengths)
+    T = batch.total
+    adv = grpo_advantages(torch.from_numpy(rewards).to(dev), torch.from_numpy(group_offsets).to(dev))
+    doc_ids = torch.from_numpy(np.repeat(np.arange(n), batch.lengths)).reshape(1, -1).to(dev)
+    mask = torch.from_numpy(batch.mask).reshape(1, -1).to(dev)
+    z = torch.zeros(1, 1, dtype=torch.long, device=dev)
+    mb = Batch(z, z, z.int(), mask, doc_ids, adv, None, torch.zeros(n, device=dev), n)
+    mini = MiniPlan((), n, int(mask.sum().item()), ())
+    stub = NS(ppo_clip_eps_low=0.2, ppo_clip_eps_high=0.28, use_tis=False, use_icepop=False,
+              calculate_per_token_loss=True, old_logprobs_source="rollout", sharder=None, parallel_dims=NS(cp=1))
+    old_d = torch.from_numpy(old).reshape(1, -1).to(dev)
+    new_d = torch.from_numpy(new).reshape(1, -1).to(dev).requires_grad_(True)
+
+    def fwd():
+        with torch.no_grad():
+            ppo_clip_loss(stub, new_d, old_d, mb, mini)
+
+    def fwd_bwd():
+        new_d.grad = None
+        loss, _ = ppo_clip_loss(stub, new_d, old_d, mb, mini)
+        loss.backward()
+
+    fwd_ms = _gpu_ms(fwd, steps, warmup)
+    fb_ms = _gpu_ms(fwd_bwd, steps, warmup)
+    cpu_ms = None
+    if not no_cpu:
+        from oracle import ppo as oppo
+
+        old_c = torch.from_numpy(old).reshape(1, -1)
+        adv_c = adv.cpu()
+        ids_c = doc_ids.cpu()
+        mask_c = mask.cpu()
+
+        def cpu():
+            nr = torch.from_numpy(new).reshape(1, -1).requires_grad_(True)
+            loss, sums = oppo.ppo_clip_loss(nr, old_c, mask_c, ids_c, adv_c, n, n_docs_global=n,
+                                            n_tokens_global=mini.n_tokens_global, clip_low=0.2, clip_high=0.28,
+                                            per_token_loss=True)
+            loss.backward()
+            oppo.reduce_mini_metrics(sums)
+
+        cpu_ms = _wall_ms(cpu, 5, gpu=False)
+    fwd_bytes = T * 12
+    return {
+        "ppo_loss_fwd": _entry(fwd_ms * 1e3, fwd_bytes, tokens=T),
+        "ppo_loss_fwd_bwd": _entry(fb_ms * 1e3, fwd_bytes + T * 16, cpu_ms, tokens=T),
+    }
+
+
+# ---------------------------------------------------------------- config 3
+
+def bench_long_context(steps, warmup, no_cpu):
+    import torch
+
+    from meshy_amd import logprob, workloads
+    from meshy_amd.plan import PlannerConfig, build_plan
+
+    dev = torch.device("cuda:0")
+    lengths = workloads.config3_lengths(3).tolist()
+    cfg = PlannerConfig(layout="packed", mini_batch_size=16, seq_len=131072, align=2048,
+                        max_tokens_per_micro=131072)
+    plan = build_plan(lengths, lengths, 1, cfg)
+    T = max(m.seq_len for mini in plan.per_rank[0] for m in mini.micros)
+    V = 131072
+    gen = torch.Generator(device=dev).manual_seed(3)
+    logits = torch.randn(1, T, V, generator=gen, device=dev, dtype=torch.bfloat16) * 2.0
+    labels = torch.randint(0, V, (1, T), generator=gen, device=dev)
+    ms = _gpu_ms(lambda: logprob.logprobs_and_entropy(logits, labels, with_entropy=True), steps, warmup)
+    cpu_ms = None
+    rows = 8192
+    if not no_cpu:
+        tps, cms = cpu_logprob_tokens_per_s(logits, labels, rows, runs=3)
+        cpu_ms = cms * T / rows  # scaled to the full micro
+    del logits
+    torch.cuda.empty_cache()
+    nbytes = T * V * 2 + 16 * T
+    return _entry(ms * 1e3, nbytes, cpu_ms, T=T, V=V, tokens_per_s=round(T / (ms * 1e-3)),
+                  cpu_sample=f"{rows} rows, scaled to T")
+
+
+# ---------------------------------------------------------------- config 4
+
+def bench_gae(steps, warmup, no_cpu):
+    import numpy as np
+    import torch
+
+    from meshy_amd import workloads
+    from meshy_amd.gae import gae_and_returns
+
+    dev = torch.device("cuda:0")
+    batch, values, terminal = workloads.config4(4)
+    n = len(batch.lengths)
+    T = batch.total
+    rewards = np.zeros(T, np.float32)
+    rewards[batch.offsets[1:] - 1] = terminal
+    doc_ids = torch.from_numpy(np.repeat(np.arange(n), batch.lengths)).reshape(1, -1).to(dev)
+    r = torch.from_numpy(rewards).reshape(1, -1).to(dev)
+    v = torch.from_numpy(values).to(torch.bfloat16).reshape(1, -1).to(dev)
+    m = torch.from_numpy(batch.mask).reshape(1, -1).to(dev)
+    lengths = torch.full((n,), 1.0 / (1.0 - 0.95), device=dev)
+    ms = _gpu_ms(lambda: gae_and_returns(r, v, m, doc_ids, n, lengths=lengths, gamma=1.0, alpha=1.0), steps, warmup)
+    cpu_ms = None
+    if not no_cpu:
+        from oracle import gae as ogae
+
+        L = batch.lengths
+        S = int(L.max())
+        pos = np.arange(T) - np.repeat(batch.offsets[:-1], L)
+        ids = np.repeat(np.arange(n), L)
+        R = torch.zeros(n, S)
+        Vp = torch.zeros(n, S)
+        M = torch.zeros(n, S)
+        R[ids, pos] = torch.from_numpy(rewards)
+        Vp[ids, pos] = v.reshape(-1).float().cpu()
+        M[ids, pos] = torch.from_numpy(batch.mask)
+        rid = torch.arange(n).unsqueeze(1).expand(n, S).contiguous()
+        lc = lengths.cpu()
+
+        def cpu():
+            ogae.compute_vapo_gae(R, Vp, M, rid, n, lengths=lc, gamma=1.0, alpha=1.0)
+            ogae.compute_returns(R, M, rid, gamma=1.0)
+
+        cpu_ms = _wall_ms(cpu, 3, gpu=False)
+    # reads rewards 4 + values 2 + mask 4 + doc id 8, writes adv 4 + returns 4
+    return _entry(ms * 1e3, T * 26, cpu_ms, tokens=T, docs=n, cpu_sample="sequential loop on padded [1024, S_max]")
+
+
+# ---------------------------------------------------------------- end to end
+
+def bench_end_to_end(runs, no_cpu):
+    """Config-0 samples truncated to the micros that fill T=16384 -> pack ->
+    logprob+entropy on [16384, 151936] logits -> GRPO -> PPO fwd+bwd."""
+    from types import SimpleNamespace as NS
+
+    import numpy as np
+    import torch
+
+    from meshy_amd import logprob, workloads
+    from meshy_amd.loss import ppo_clip_loss
+    from meshy_amd.pipeline import RaggedSamples, pack_step
+    from meshy_amd.plan import PlannerConfig
+
+    dev = torch.device("cuda:0")
+    batch, rewards, group_offsets = workloads.config0(0)
+    # the first groups whose samples make two full 8192-token micros
+    keep = 0
+    tot = 0
+    while keep < len(batch.lengths) and tot + int(batch.lengths[keep:keep + 8].sum()) <= 2 * 8192 - 2048:
+        tot += int(batch.lengths[keep:keep + 8].sum())
+        keep += 8
+    o = batch.offsets[keep]
+    ragged = RaggedSamples.from_arrays(batch.tokens[:o], batch.mask[:o], batch.logprobs[:o],
+                                       batch.offsets[:keep + 1], rewards[:keep], group_offsets[:keep // 8 + 1])
+    cfg = PlannerConfig(layout="packed", mini_batch_size=keep, seq_len=8192, align=2048,
+                        max_tokens_per_micro=8192)
+    gen = torch.Generator(device=dev).manual_seed(5)
+    logits = torch.randn(1, T_TOK, VOCAB, generator=gen, device=dev, dtype=torch.bfloat16) * 2.0
+    stub = NS(ppo_clip_eps_low=0.2, ppo_clip_eps_high=0.28, use_tis=False, use_icepop=False,
+              calculate_per_token_loss=True, old_logprobs_source="rollout", sharder=None, parallel_dims=NS(cp=1))
+    info = {}
+
+    def gpu_step():
+        res = pack_step(ragged, cfg, dev)
+        mini = res.plan.per_rank[0][0]
+        off = 0
+        for mb in res.batches:
+            T = mb.input_ids.shape[1]
+            z = logits[:, off:off + T] if off + T <= T_TOK else logits[:, :T]
+            off += T
+            lp, ent = logprob.logprobs_and_entropy(z, mb.labels, with_entropy=True)
+            new = lp.detach().requires_grad_(True)
+            loss, sums = ppo_clip_loss(stub, new, mb.rollout_logprobs, mb, mini, entropy=ent)
+            loss.backward()
+        info["tokens"] = sum(mb.input_ids.shape[1] for mb in res.batches)
+        info["micros"] = len(res.batches)
+
+    gpu_ms = _wall_ms(gpu_step, runs, warmup=2)
+    out = {"gpu_ms": round(gpu_ms, 3), "tokens": info["tokens"], "micros": info["micros"], "V": VOCAB}
+    if not no_cpu:
+        from oracle import batch as obatch
+        from oracle import grpo as ogrpo
+        from oracle import logprob as olp
+        from oracle import plan as oplan
+        from oracle import ppo as oppo
+
+        samples = batch.sample_dicts(rewards=rewards)[:keep]
+        zc = logits.cpu()
+
+        def cpu_step():
+            lengths, loss_t = oplan.sample_lengths(samples, 8192)
+            local, per_rank = oplan.build_plan(lengths, loss_t, 1, layout="packed", mini_batch_size=keep,
+                                               seq_len=8192, align=2048, max_tokens_per_micro=8192)
+            adv = []
+            for g in range(keep // 8):
+                adv += ogrpo.grpo_group([float(s["reward"]) for s in samples[8 * g:8 * g + 8]])
+            loc = [dict(samples[i], advantage=adv[i]) for i in local[0]]
+            micros, n_docs_g, n_tok_g, _ = per_rank[0][0]
+            off = 0
+            for idx, seq_len, doc_lens in micros:
+                mbc = obatch.build_micro_batch(loc, idx, seq_len, doc_lens, layout="packed", need_rollout_lp=True)
+                z = zc[:, off:off + seq_len] if off + seq_len <= T_TOK else zc[:, :seq_len]
+                off += seq_len
+                lp, ent = olp.forward_logprobs(z, mbc["labels"], with_entropy=True)
+                nr = lp.detach().requires_grad_(True)
+                loss, _ = oppo.ppo_clip_loss(nr, mbc["rollout_logprobs"], mbc["mask"], mbc["doc_ids"],
+                                             mbc["advantages"], mbc["n_docs"], n_docs_global=n_docs_g,
+                                             n_tokens_global=n_tok_g, clip_low=0.2, clip_high=0.28,
+                                             per_token_loss=True, entropy=ent)
+                loss.backward()
+
+        cpu_ms = _wall_ms(cpu_step, 3, gpu=False)
+        out["cpu_ms"] = round(cpu_ms, 1)
+        out["speedup_vs_cpu"] = round(cpu_ms / gpu_ms, 1)
+    del logits
+    torch.cuda.empty_cache()
+    return out
 
 
 def main() -> int:
@@ -108,11 +429,12 @@ def main() -> int:
     ap.add_argument("--steps", type=int, default=50)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--cpu-rows", type=int, default=1024)
-    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--no-cpu", action="store_true", help="skip every CPU reference timing")
+    ap.add_argument("--quick", action="store_true", help="headline kernel only")
     args = ap.parse_args()
     if args.gpus != 1:
-        print("bench.py measures one GPU: this path's kernels run per GPU and a multi-GPU "
-              "figure is not produced here (run with --gpus 1)", file=sys.stderr)
+        print("bench.py measures one GPU: the hot path's kernels run per GPU and no multi-GPU figure "
+              "is produced (run with --gpus 1)", file=sys.stderr)
         return 2
 
     import torch
@@ -120,10 +442,14 @@ def main() -> int:
     if not torch.cuda.is_available():
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
+    torch.set_num_threads(os.cpu_count() or 1)
 
-    _sync_all()
     ms, nbytes, logits, labels = bench_logprob(args.steps, args.warmup)
     achieved = nbytes / (ms * 1e-3) / 1e9
+    traffic = None
+    if os.path.exists(TRAFFIC_FILE):
+        with open(TRAFFIC_FILE) as f:
+            traffic = json.load(f).get("k_lpe_fwd_vec", {}).get("hbm_bytes_per_launch")
     result = {
         "metric": "packed tokens/sec for logprob+entropy (V=151936) + % of HBM peak; pack latency",
         "value": T_TOK / (ms * 1e-3),
@@ -137,15 +463,50 @@ def main() -> int:
         "vs_baseline": None,
         "dtype": "bf16",
         "data": "synthetic: logits N(0, 2^2) bf16 from a seeded generator, labels uniform in [0, V)",
-        "config": {"workload": "fused packed logprob+entropy, one micro-batch", "T": T_TOK,
+        "config": {"workload": "fused packed logprob+entropy over one micro-batch of logits", "T": T_TOK,
                    "V": VOCAB, "global_batch": T_TOK, "seq_len": T_TOK, "parallelism": "none (1 GPU)"},
-        "roofline": {"bound": "hbm", "achieved": achieved, "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": achieved / HBM_PEAK_GBS, "traffic": None},
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
     }
     if not args.no_cpu:
-        result["cpu_baseline"] = cpu_baseline_logprob(logits, labels, args.cpu_rows)
+        tps, cms = cpu_logprob_tokens_per_s(logits, labels, args.cpu_rows)
+        result["cpu_baseline"] = {
+            "value": round(tps, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
+            "sample": f"first {args.cpu_rows} rows of the same [16384, 151936] bf16 logits, median of 5 "
+                      f"after 1 warm-up ({cms:.1f} ms per pass)"}
+    del logits, labels
+    torch.cuda.empty_cache()
+    if not args.quick:
+        kernels = {"logprob_entropy_fwd_T16384_V151936": _entry(ms * 1e3, nbytes,
+                                                                 result.get("cpu_baseline") and
+                                                                 T_TOK / result["cpu_baseline"]["value"] * 1e3)}
+        pack, _, _ = bench_pack(20, args.no_cpu)
+        result["pack_latency_us"] = pack["pack_latency_us"]
+        kernels["pack_grpo_config0"] = pack
+        kernels.update(bench_ppo(args.steps, args.warmup, args.no_cpu))
+        kernels["gae_returns_config4"] = bench_gae(args.steps, args.warmup, args.no_cpu)
+        kernels["logprob_entropy_config3"] = bench_long_context(max(3, args.steps // 10), 2, args.no_cpu)
+        result["kernels"] = kernels
+        result["end_to_end"] = bench_end_to_end(5, args.no_cpu)
+        if result.get("cpu_baseline"):
+            result["cpu_baseline"]["host"] = _host_info()
     print(json.dumps(result), flush=True)
     return 0
+
+
+def _host_info():
+    import platform
+
+    model = platform.processor()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"cpu_model": model, "os_cpu_count": os.cpu_count()}
 
 
 if __name__ == "__main__":

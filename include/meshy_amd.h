@@ -94,6 +94,14 @@ typedef struct meshy_plan_out {
 int meshy_plan_build(const int64_t* lengths, const int64_t* loss_tokens, int64_t n,
                      int64_t dp_size, const meshy_planner_cfg* cfg, meshy_plan_out* out);
 
+/* Per-sample planner inputs from a flat host mask (host).
+ * Replaces TitanTrainer._sample_lengths (meshy/backend/titan/trainer.py:577-588):
+ * sample i covers mask[offsets[i] .. offsets[i+1]); lengths[i] is its token
+ * count and loss_tokens[i] = #(mask[1:L] > 0) with L = min(length, seq_len),
+ * 0 when L <= 1. */
+int meshy_sample_loss_tokens(const float* mask, const int64_t* offsets, int64_t n,
+                             int64_t seq_len, int64_t* lengths, int64_t* loss_tokens);
+
 /* ------------------------------------------------------------------------
  * Micro-batch materialisation (device).
  * Replaces build_micro_batch (meshy/backend/titan/batch.py:96-230): per-doc

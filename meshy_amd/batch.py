@@ -54,6 +54,10 @@ class Batch:
     n_docs: int
     attention_masks: Any = None
     positive_lm_weights: torch.Tensor | None = None
+    #: Per-document advantages broadcast over the micro's tokens (padding slot
+    #: 0), i.e. the ``adv_tok`` the loss derives (trainer.py:753-756); only
+    #: filled when the pack is asked for it.
+    advantage_tokens: torch.Tensor | None = None
 
     @property
     def n_slots(self) -> int:
@@ -116,22 +120,46 @@ def _scalar(td, key: str, default: float = 0.0) -> float:
     return float(v)
 
 
-def build_micro_batches(
+@dataclass
+class PackJob:
+    """Device-resident inputs of one pack launch (see ``stage_micro_batches``)."""
+
+    micros: tuple
+    layout: str
+    device: torch.device
+    dbuf: torch.Tensor
+    lay: Any
+    need_rollout_lp: bool
+    per_token_adv: bool
+    n_samples: int
+    seq: np.ndarray
+    rows: np.ndarray
+    out_off: np.ndarray
+    doc_start: np.ndarray
+    max_elems: int
+    max_docs: int
+    #: Device per-sample advantages indexed like ``doc_sample`` (overrides the
+    #: staged ``sample["advantage"]`` values).
+    adv_samples: torch.Tensor | None = None
+    #: Also write ``Batch.advantage_tokens`` (per-document advantage per token).
+    broadcast_advantages: bool = False
+
+
+def stage_micro_batches(
     samples: Sequence[Any],
     micros: Sequence[MicroPlan],
     *,
     layout: Layout,
     device,
-    sharder=None,
     need_rollout_lp: bool,
-) -> list[Batch]:
-    """Materialise ``micros`` from the rank-local ``samples`` in one transfer and one launch."""
+) -> PackJob:
+    """Gather what ``micros`` read from ``samples`` into one pinned buffer and copy it
+    to the device in one transfer (asynchronous on the current stream)."""
     if layout not in ("padded", "packed"):
         raise ValueError(f"unknown layout {layout!r}")
     device = torch.device(device)
     if device.type != "cuda":
         raise ValueError("meshy_amd builds micro-batches on a HIP device; pass a cuda device")
-    lib = _lib.load()
 
     # Samples used by these micros, remapped to a compact list.
     remap: dict[int, int] = {}
@@ -226,37 +254,52 @@ def build_micro_batches(
     dbuf = torch.empty(lay.size, dtype=torch.uint8, device=device)
     dbuf.copy_(host[:lay.size], non_blocking=True)
     stage.mark(stream)
+    return PackJob(
+        micros=tuple(micros), layout=layout, device=device, dbuf=dbuf, lay=lay,
+        need_rollout_lp=need_rollout_lp, per_token_adv=per_token_adv, n_samples=n_s, seq=seq, rows=rows,
+        out_off=out_off, doc_start=doc_start, max_elems=int(elems.max()) if n_micro else 0,
+        max_docs=int(n_docs.max()) if n_micro else 0,
+    )
 
-    n_out = int(out_off[-1])
+
+def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
+    """Run the pack kernels over a staged job and return one ``Batch`` per micro."""
+    lib = _lib.load()
+    device, lay, dbuf, layout = job.device, job.lay, job.dbuf, job.layout
+    n_micro = len(job.micros)
+    n_docs_total = int(job.doc_start[-1])
+    n_out = int(job.out_off[-1])
     input_ids = torch.empty(n_out, dtype=torch.int64, device=device)
     labels = torch.empty(n_out, dtype=torch.int64, device=device)
     positions = torch.empty(n_out, dtype=torch.int32, device=device)
     mask = torch.empty(n_out, dtype=torch.float32, device=device)
     doc_ids = torch.empty(n_out, dtype=torch.int64, device=device)
-    rollout_lp = torch.empty(n_out, dtype=torch.float32, device=device) if need_rollout_lp else None
-    adv_tok = torch.empty(n_out, dtype=torch.float32, device=device) if per_token_adv else None
+    rollout_lp = torch.empty(n_out, dtype=torch.float32, device=device) if job.need_rollout_lp else None
+    want_tok = job.per_token_adv or job.broadcast_advantages
+    adv_tok = torch.empty(n_out, dtype=torch.float32, device=device) if want_tok else None
     adv_doc = torch.empty(max(n_docs_total, 1), dtype=torch.float32, device=device)
     lengths = torch.empty(max(n_docs_total, 1), dtype=torch.int32, device=device)
     cu = torch.empty(n_docs_total + 2 * n_micro, dtype=torch.int32, device=device)
 
     a = _lib.PackArgs()
     a.tokens = lay.view(dbuf, "tokens").data_ptr()
-    a.tokens_elem_bytes = 4 if tok_dtype == torch.int32 else 8
+    a.tokens_elem_bytes = 4
     a.layout = _lib.MESHY_LAYOUT_PACKED if layout == "packed" else _lib.MESHY_LAYOUT_PADDED
     a.mask = lay.view(dbuf, "mask").data_ptr()
-    a.logprobs = lay.view(dbuf, "logprobs").data_ptr() if need_rollout_lp else None
-    a.adv_tokens = lay.view(dbuf, "adv_tokens").data_ptr() if per_token_adv else None
-    a.adv_samples = lay.view(dbuf, "adv_samples").data_ptr()
+    a.logprobs = lay.view(dbuf, "logprobs").data_ptr() if job.need_rollout_lp else None
+    a.adv_tokens = lay.view(dbuf, "adv_tokens").data_ptr() if job.per_token_adv else None
+    a.adv_samples = (job.adv_samples.data_ptr() if job.adv_samples is not None
+                     else lay.view(dbuf, "adv_samples").data_ptr())
     a.sample_offsets = lay.view(dbuf, "s_off").data_ptr()
-    a.n_samples = n_s
+    a.n_samples = job.n_samples
     a.n_micro = n_micro
     a.micro_seq_len = lay.view(dbuf, "seq").data_ptr()
     a.micro_out_off = lay.view(dbuf, "out_off").data_ptr()
     a.micro_doc_start = lay.view(dbuf, "doc_start").data_ptr()
     a.doc_sample = lay.view(dbuf, "doc_sample").data_ptr()
     a.doc_len = lay.view(dbuf, "doc_len").data_ptr()
-    a.max_micro_elems = int(elems.max()) if n_micro else 0
-    a.max_docs_per_micro = int(n_docs.max()) if n_micro else 0
+    a.max_micro_elems = job.max_elems
+    a.max_docs_per_micro = job.max_docs
     a.input_ids = input_ids.data_ptr()
     a.labels = labels.data_ptr()
     a.positions = positions.data_ptr()
@@ -267,15 +310,15 @@ def build_micro_batches(
     a.adv_doc = adv_doc.data_ptr()
     a.doc_len_out = lengths.data_ptr()
     a.cu_seqlens = cu.data_ptr()
-    rc = lib.meshy_pack_micro_batches(_lib.ctypes.byref(a), stream.cuda_stream)
+    rc = lib.meshy_pack_micro_batches(_lib.ctypes.byref(a), torch.cuda.current_stream(device).cuda_stream)
     _lib.check(rc, "meshy_pack_micro_batches")
     pos_w_dev = lay.view(dbuf, "pos_w")
 
     out: list[Batch] = []
-    for k, m in enumerate(micros):
-        o0, o1 = int(out_off[k]), int(out_off[k + 1])
-        R, S = int(rows[k]), int(seq[k])
-        d0, d1 = int(doc_start[k]), int(doc_start[k + 1])
+    for k, m in enumerate(job.micros):
+        o0, o1 = int(job.out_off[k]), int(job.out_off[k + 1])
+        R, S = int(job.rows[k]), int(job.seq[k])
+        d0, d1 = int(job.doc_start[k]), int(job.doc_start[k + 1])
         nd = d1 - d0
 
         def v(t):
@@ -290,32 +333,47 @@ def build_micro_batches(
             c0 = d0 + 2 * k
             max_len = max(list(m.doc_lens) + ([pad] if pad > 0 else []))
             attn = make_varlen_metadata(cu[c0:c0 + n_cu], max_len, device)
-        else:
+        elif sharder is not None:
             # One CP shard call for every per-token tensor (batch.py:195-207);
             # the identity on one GPU.
-            if sharder is not None:
-                optional = [t for t in (rl, at) if t is not None]
-                sharded = sharder.shard_seq(ii, lb, ps, mk, di, *optional)
-                ii, lb, ps, mk, di = sharded[:5]
-                rest = list(sharded[5:])
-                if rl is not None:
-                    rl = rest.pop(0)
-                if at is not None:
-                    at = rest.pop(0)
+            optional = [t for t in (rl, at) if t is not None]
+            sharded = sharder.shard_seq(ii, lb, ps, mk, di, *optional)
+            ii, lb, ps, mk, di = sharded[:5]
+            rest = list(sharded[5:])
+            if rl is not None:
+                rl = rest.pop(0)
+            if at is not None:
+                at = rest.pop(0)
+        per_token = at if job.per_token_adv else None
         out.append(Batch(
             input_ids=ii,
             labels=lb,
             positions=ps,
             mask=mk,
             doc_ids=di,
-            advantages=at if at is not None else adv_doc[d0:d1],
+            advantages=per_token if per_token is not None else adv_doc[d0:d1],
             rollout_logprobs=rl,
             lengths=lengths[d0:d1],
             n_docs=nd,
             attention_masks=attn,
             positive_lm_weights=pos_w_dev[d0:d1],
+            advantage_tokens=at if job.broadcast_advantages and not job.per_token_adv else None,
         ))
     return out
+
+
+def build_micro_batches(
+    samples: Sequence[Any],
+    micros: Sequence[MicroPlan],
+    *,
+    layout: Layout,
+    device,
+    sharder=None,
+    need_rollout_lp: bool,
+) -> list[Batch]:
+    """Materialise ``micros`` from the rank-local ``samples`` in one transfer and one launch."""
+    job = stage_micro_batches(samples, micros, layout=layout, device=device, need_rollout_lp=need_rollout_lp)
+    return launch_pack(job, sharder)
 
 
 def build_micro_batch(
@@ -332,5 +390,5 @@ def build_micro_batch(
                                need_rollout_lp=need_rollout_lp)[0]
 
 
-__all__ = ["ADVANTAGE_TOKENS", "Batch", "VarlenMetadata", "build_micro_batch",
-           "build_micro_batches", "make_varlen_metadata"]
+__all__ = ["ADVANTAGE_TOKENS", "Batch", "PackJob", "VarlenMetadata", "build_micro_batch",
+           "build_micro_batches", "launch_pack", "make_varlen_metadata", "stage_micro_batches"]

@@ -95,30 +95,112 @@ __device__ __forceinline__ float value_at(const meshy_gae_args& g, int64_t t) {
     return static_cast<const float*>(g.values)[t];
 }
 
-// The two affine maps of position t.
-__device__ __forceinline__ Pair token_maps(const meshy_gae_args& g, const float* cnt, int64_t t) {
-    const int64_t row = t / g.S;
-    const int64_t s = t - row * g.S;
-    const float mk = g.mask[t];
-    const bool valid = mk > 0.f;
-    const int64_t d = g.doc_ids[t];
-    bool cont = false;
-    float vn = 0.f;
-    if (s + 1 < g.S) {
-        cont = valid && g.doc_ids[t + 1] == d && g.mask[t + 1] > 0.f;
-        vn = value_at(g, t + 1);
+// The inputs of a thread's kItems positions plus the next one (its neighbour
+// in time), loaded with 16-byte vector loads when the run is whole and aligned.
+struct ThreadInputs {
+    float mk[kItems + 1];
+    int64_t d[kItems + 1];
+    float v[kItems + 1];
+    float r[kItems];
+};
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef long long i64x2 __attribute__((ext_vector_type(2)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+__device__ __forceinline__ void load_inputs(const meshy_gae_args& g, int64_t t0, int64_t n, bool vec,
+                                            ThreadInputs& in) {
+    const bool whole = vec && t0 + kItems <= n;
+    if (whole) {
+#pragma unroll
+        for (int q = 0; q < kItems / 4; ++q) {
+            const f32x4 m4 = *reinterpret_cast<const f32x4*>(g.mask + t0 + 4 * q);
+            const f32x4 r4 = *reinterpret_cast<const f32x4*>(g.rewards + t0 + 4 * q);
+            in.mk[4 * q + 0] = m4.x; in.mk[4 * q + 1] = m4.y; in.mk[4 * q + 2] = m4.z; in.mk[4 * q + 3] = m4.w;
+            in.r[4 * q + 0] = r4.x; in.r[4 * q + 1] = r4.y; in.r[4 * q + 2] = r4.z; in.r[4 * q + 3] = r4.w;
+        }
+#pragma unroll
+        for (int q = 0; q < kItems / 2; ++q) {
+            const i64x2 d2 = *reinterpret_cast<const i64x2*>(g.doc_ids + t0 + 2 * q);
+            in.d[2 * q] = d2.x;
+            in.d[2 * q + 1] = d2.y;
+        }
+        if (g.values) {
+            if (g.values_bf16) {
+                const uint16_t* vb = static_cast<const uint16_t*>(g.values) + t0;
+#pragma unroll
+                for (int q = 0; q < kItems / 8; ++q) {
+                    const u32x4 w = *reinterpret_cast<const u32x4*>(vb + 8 * q);
+                    in.v[8 * q + 0] = bf16_lo(w.x); in.v[8 * q + 1] = bf16_hi(w.x);
+                    in.v[8 * q + 2] = bf16_lo(w.y); in.v[8 * q + 3] = bf16_hi(w.y);
+                    in.v[8 * q + 4] = bf16_lo(w.z); in.v[8 * q + 5] = bf16_hi(w.z);
+                    in.v[8 * q + 6] = bf16_lo(w.w); in.v[8 * q + 7] = bf16_hi(w.w);
+                }
+            } else {
+                const float* vf = static_cast<const float*>(g.values) + t0;
+#pragma unroll
+                for (int q = 0; q < kItems / 4; ++q) {
+                    const f32x4 v4 = *reinterpret_cast<const f32x4*>(vf + 4 * q);
+                    in.v[4 * q + 0] = v4.x; in.v[4 * q + 1] = v4.y; in.v[4 * q + 2] = v4.z; in.v[4 * q + 3] = v4.w;
+                }
+            }
+        } else {
+#pragma unroll
+            for (int k = 0; k < kItems; ++k) in.v[k] = 0.f;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kItems; ++k) {
+            const int64_t t = t0 + k;
+            const bool ok = t < n;
+            in.mk[k] = ok ? g.mask[t] : 0.f;
+            in.r[k] = ok ? g.rewards[t] : 0.f;
+            in.d[k] = ok ? g.doc_ids[t] : -1;
+            in.v[k] = ok ? value_at(g, t) : 0.f;
+        }
     }
-    const float contf = cont ? 1.f : 0.f;
-    const float validf = valid ? 1.f : 0.f;
-    const float r = g.rewards[t];
-    // lambda of the document; the padding slot (and any id outside [0, n_docs)) gets 0.
-    const float lam = (d >= 0 && d < g.n_docs) ? lambda_of(doc_length(g, cnt, d), g.alpha, g.epsilon) : 0.f;
-    const float v = value_at(g, t);
-    const float delta = (r + g.gamma * vn * contf - v) * validf;
-    Pair m;
-    m.adv = Aff{(g.gamma * lam) * contf, valid ? delta : 0.f};
-    m.ret = Aff{g.gamma * contf, valid ? r : 0.f};
-    return m;
+    const int64_t tn = t0 + kItems;
+    const bool okn = tn < n;
+    in.mk[kItems] = okn ? g.mask[tn] : 0.f;
+    in.d[kItems] = okn ? g.doc_ids[tn] : -1;
+    in.v[kItems] = okn ? value_at(g, tn) : 0.f;
+}
+
+// The affine maps of a thread's positions t0 .. t0 + kItems - 1 (identity past n).
+// Row ends come from a column counter started with one division; lambda is
+// recomputed only when the document changes.
+__device__ __forceinline__ void thread_maps(const meshy_gae_args& g, const float* cnt, int64_t t0, int64_t n,
+                                            bool vec, Pair (&items)[kItems]) {
+    ThreadInputs in;
+    load_inputs(g, t0, n, vec, in);
+    int64_t s = t0 % g.S;
+    int64_t cur_d = -2;
+    float cur_lam = 0.f;
+#pragma unroll
+    for (int k = 0; k < kItems; ++k) {
+        if (t0 + k >= n) {
+            items[k] = identity_pair();
+            continue;
+        }
+        const bool row_end = (s == g.S - 1);
+        s = row_end ? 0 : s + 1;
+        const float mk = in.mk[k];
+        const bool valid = mk > 0.f;
+        const int64_t d = in.d[k];
+        const bool cont = valid && !row_end && in.d[k + 1] == d && in.mk[k + 1] > 0.f;
+        const float vn = row_end ? 0.f : in.v[k + 1];
+        if (d != cur_d) {
+            cur_d = d;
+            // The padding slot (and any id outside [0, n_docs)) gets lambda 0.
+            cur_lam = (d >= 0 && d < g.n_docs) ? lambda_of(doc_length(g, cnt, d), g.alpha, g.epsilon) : 0.f;
+        }
+        const float contf = cont ? 1.f : 0.f;
+        const float validf = valid ? 1.f : 0.f;
+        const float r = in.r[k];
+        const float delta = (r + g.gamma * vn * contf - in.v[k]) * validf;
+        items[k].adv = Aff{(g.gamma * cur_lam) * contf, valid ? delta : 0.f};
+        items[k].ret = Aff{g.gamma * contf, valid ? r : 0.f};
+    }
 }
 
 // Suffix composition across the block: returns, for each thread, the map of
@@ -169,25 +251,21 @@ __global__ __launch_bounds__(kCountThreads) void k_gae_count(meshy_gae_args g, f
     if (cur >= 0 && cur <= g.n_docs && acc != 0.f) atomicAdd(cnt + cur, acc);
 }
 
-// Loads the thread's items (contiguous) and folds them right to left.
+// Builds the thread's maps (contiguous positions) and folds them right to left.
 __device__ __forceinline__ Pair load_items(const meshy_gae_args& g, const float* cnt, int64_t t0, int64_t n,
-                                           Pair (&items)[kItems]) {
+                                           bool vec, Pair (&items)[kItems]) {
+    thread_maps(g, cnt, t0, n, vec, items);
     Pair agg = identity_pair();
-#pragma unroll
-    for (int k = 0; k < kItems; ++k) {
-        const int64_t t = t0 + k;
-        items[k] = (t < n) ? token_maps(g, cnt, t) : identity_pair();
-    }
 #pragma unroll
     for (int k = kItems - 1; k >= 0; --k) agg = compose(items[k], agg);
     return agg;
 }
 
-__global__ __launch_bounds__(kThreads) void k_gae_chunks(meshy_gae_args g, Workspace ws, int64_t n) {
+__global__ __launch_bounds__(kThreads) void k_gae_chunks(meshy_gae_args g, Workspace ws, int64_t n, bool vec) {
     __shared__ Pair s_wave[kThreads / kWave];
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kChunk + static_cast<int64_t>(threadIdx.x) * kItems;
     Pair items[kItems];
-    const Pair mine = load_items(g, ws.cnt, t0, n, items);
+    const Pair mine = load_items(g, ws.cnt, t0, n, vec, items);
     Pair total;
     (void)block_suffix_exclusive(mine, s_wave, total);
     if (threadIdx.x == 0) ws.chunk[blockIdx.x] = total;
@@ -234,25 +312,42 @@ __global__ __launch_bounds__(kCarryThreads) void k_gae_carry(meshy_gae_args g, W
     }
 }
 
-__global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Workspace ws, int64_t n) {
+__global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Workspace ws, int64_t n, bool vec) {
     __shared__ Pair s_wave[kThreads / kWave];
     const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kChunk + static_cast<int64_t>(threadIdx.x) * kItems;
     Pair items[kItems];
-    const Pair mine = load_items(g, ws.cnt, t0, n, items);
+    const Pair mine = load_items(g, ws.cnt, t0, n, vec, items);
     Pair total;
     const Pair excl = block_suffix_exclusive(mine, s_wave, total);
     const float ca = ws.carry[2 * blockIdx.x];
     const float cr = ws.carry[2 * blockIdx.x + 1];
     float A = fmaf(excl.adv.p, ca, excl.adv.q);
     float G = fmaf(excl.ret.p, cr, excl.ret.q);
+    float outA[kItems], outG[kItems];
 #pragma unroll
     for (int k = kItems - 1; k >= 0; --k) {
-        const int64_t t = t0 + k;
         A = fmaf(items[k].adv.p, A, items[k].adv.q);
         G = fmaf(items[k].ret.p, G, items[k].ret.q);
-        if (t < n) {
-            if (g.adv) g.adv[t] = A;
-            if (g.returns) g.returns[t] = G;
+        outA[k] = A;
+        outG[k] = G;
+    }
+    if (vec && t0 + kItems <= n) {
+#pragma unroll
+        for (int q = 0; q < kItems / 4; ++q) {
+            if (g.adv)
+                *reinterpret_cast<f32x4*>(g.adv + t0 + 4 * q) =
+                    f32x4{outA[4 * q], outA[4 * q + 1], outA[4 * q + 2], outA[4 * q + 3]};
+            if (g.returns)
+                *reinterpret_cast<f32x4*>(g.returns + t0 + 4 * q) =
+                    f32x4{outG[4 * q], outG[4 * q + 1], outG[4 * q + 2], outG[4 * q + 3]};
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kItems; ++k) {
+            if (t0 + k < n) {
+                if (g.adv) g.adv[t0 + k] = outA[k];
+                if (g.returns) g.returns[t0 + k] = outG[k];
+            }
         }
     }
 }
@@ -361,14 +456,19 @@ extern "C" int meshy_gae(const meshy_gae_args* args, hipStream_t stream) {
             if ((rc = check_launch("meshy_gae(count)"))) return rc;
         }
     }
+    // 16-byte vector loads and stores need every per-token array 16-byte aligned
+    // (each thread's first position is a multiple of kItems).
+    auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool vec = al16(g.rewards) && al16(g.mask) && al16(g.doc_ids) && (!g.values || al16(g.values)) &&
+                     (!g.adv || al16(g.adv)) && (!g.returns || al16(g.returns));
     if (nc > 0) {
-        hipLaunchKernelGGL(k_gae_chunks, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n);
+        hipLaunchKernelGGL(k_gae_chunks, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, vec);
         if ((rc = check_launch("meshy_gae(chunks)"))) return rc;
     }
     hipLaunchKernelGGL(k_gae_carry, dim3(1), dim3(kCarryThreads), 0, stream, g, ws, nc);
     if ((rc = check_launch("meshy_gae(carry)"))) return rc;
     if (nc > 0 && (g.adv || g.returns)) {
-        hipLaunchKernelGGL(k_gae_apply, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n);
+        hipLaunchKernelGGL(k_gae_apply, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, vec);
         if ((rc = check_launch("meshy_gae(apply)"))) return rc;
     }
     return MESHY_OK;

@@ -19,7 +19,7 @@ namespace {
 
 constexpr int kScanThreads = 256;
 constexpr int kFillThreads = 256;
-constexpr int kFillItems = 4;  // tokens per thread
+constexpr int kFillItems = 1;  // tokens per thread
 
 // Inclusive block scan of one int64 per thread.
 __device__ __forceinline__ int64_t block_inclusive_scan(int64_t v, int64_t* wave_tot) {
@@ -65,19 +65,47 @@ __global__ __launch_bounds__(kScanThreads) void k_pack_scan(const int64_t* __res
     }
 }
 
+// Packed micros with at most kLdsDocs documents scan their offsets in LDS
+// inside k_pack_fill; larger ones use k_pack_scan's global table.
+constexpr int kLdsDocs = 1024;
+
 template <typename Tok>
 __global__ __launch_bounds__(kFillThreads) void k_pack_fill(meshy_pack_args a) {
+    __shared__ int32_t s_cu[kLdsDocs + 2];
+    __shared__ int64_t wave_tot[kFillThreads / kWave];
     const int k = blockIdx.y;
     const int64_t out0 = a.micro_out_off[k];
     const int64_t n_elems = a.micro_out_off[k + 1] - out0;
     const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * (kFillThreads * kFillItems);
-    if (tile0 >= n_elems) return;
+    if (tile0 >= n_elems) return;  // uniform over the workgroup
     const int64_t S = a.micro_seq_len[k];
     const int32_t d0 = a.micro_doc_start[k];
     const int32_t nd = a.micro_doc_start[k + 1] - d0;
-    const int32_t* cu = a.cu_seqlens + d0 + 2 * k;
     const Tok* tokens = static_cast<const Tok*>(a.tokens);
     const bool packed = a.layout == MESHY_LAYOUT_PACKED;
+    int32_t* cu_out = a.cu_seqlens ? a.cu_seqlens + d0 + 2 * k : nullptr;
+    const int32_t* cu = cu_out;
+    if (packed && nd <= kLdsDocs) {
+        // Exclusive prefix of the document lengths: cu_seqlens (batch.py:154-177).
+        int64_t carry = 0;
+        for (int32_t base = 0; base < nd; base += kFillThreads) {
+            const int32_t j = base + threadIdx.x;
+            const int64_t len = (j < nd) ? a.doc_len[d0 + j] : 0;
+            const int64_t incl = block_inclusive_scan(len, wave_tot);
+            if (j < nd) s_cu[j + 1] = static_cast<int32_t>(carry + incl);
+            int64_t tot = 0;
+            for (int w = 0; w < kFillThreads / kWave; ++w) tot += wave_tot[w];
+            __syncthreads();
+            carry += tot;
+        }
+        if (threadIdx.x == 0) s_cu[0] = 0;
+        __syncthreads();
+        cu = s_cu;
+        if (blockIdx.x == 0) {
+            for (int32_t j = threadIdx.x; j <= nd; j += kFillThreads) cu_out[j] = s_cu[j];
+            if (threadIdx.x == 0 && S > carry) cu_out[nd + 1] = static_cast<int32_t>(S);
+        }
+    }
 
     if (blockIdx.x == 0) {
         for (int32_t j = threadIdx.x; j < nd; j += kFillThreads) {
@@ -194,7 +222,9 @@ extern "C" int meshy_pack_micro_batches(const meshy_pack_args* args, hipStream_t
                          static_cast<long long>(a.max_micro_elems));
     if (a.n_micro > 65535) return set_error(MESHY_EINVAL, "meshy_pack_micro_batches: too many micros");
 
-    if (a.layout == MESHY_LAYOUT_PACKED) {
+    // max_docs_per_micro must bound every micro's document count: micros with
+    // more than kLdsDocs documents read the table this launch writes.
+    if (a.layout == MESHY_LAYOUT_PACKED && a.max_docs_per_micro > kLdsDocs) {
         hipLaunchKernelGGL(k_pack_scan, dim3(static_cast<unsigned>(a.n_micro)), dim3(kScanThreads), 0, stream,
                            a.micro_seq_len, a.micro_doc_start, a.doc_len, a.cu_seqlens);
         int rc = check_launch("meshy_pack_micro_batches(scan)");

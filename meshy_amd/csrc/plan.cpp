@@ -205,6 +205,26 @@ int plan_impl(const int64_t* lengths, const int64_t* loss_tokens, int64_t n, int
 
 }  // namespace
 
+extern "C" int meshy_sample_loss_tokens(const float* mask, const int64_t* offsets, int64_t n,
+                                        int64_t seq_len, int64_t* lengths, int64_t* loss_tokens) {
+    meshy::clear_error();
+    if (n < 0 || seq_len <= 0) return set_error(MESHY_EINVAL, "meshy_sample_loss_tokens: bad sizes");
+    if (n > 0 && (!offsets || !lengths || !loss_tokens || (!mask && offsets[n] > offsets[0])))
+        return set_error(MESHY_ENULL, "meshy_sample_loss_tokens: NULL pointer");
+    for (int64_t i = 0; i < n; ++i) {
+        const int64_t a = offsets[i];
+        const int64_t len = offsets[i + 1] - a;
+        if (len < 0) return set_error(MESHY_EINVAL, "meshy_sample_loss_tokens: offsets decrease at %lld",
+                                      static_cast<long long>(i));
+        lengths[i] = len;
+        const int64_t L = std::min(len, seq_len);
+        int64_t c = 0;
+        for (int64_t t = 1; t < L; ++t) c += mask[a + t] > 0.f ? 1 : 0;
+        loss_tokens[i] = L > 1 ? c : 0;
+    }
+    return MESHY_OK;
+}
+
 extern "C" int meshy_plan_build(const int64_t* lengths, const int64_t* loss_tokens, int64_t n,
                                 int64_t dp_size, const meshy_planner_cfg* cfg, meshy_plan_out* out) {
     meshy::clear_error();

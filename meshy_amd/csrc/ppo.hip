@@ -10,16 +10,19 @@
 //   diagnostic sums (ratio, clip, KL, ESS, k3, entropy)                 (813-847)
 //
 // Layout: documents are contiguous token ranges given by seg_offsets.  The
-// token axis is cut into tiles of kTile tokens.  A (tile, document) pair with
-// a non-empty overlap is handled by one wavefront; because both tiles and
-// documents are ordered, the overlapping pairs form a monotone staircase and
-// `tile + document` indexes them without collision.
-//   k_ppo_tiles  per pair: 5 per-document partial sums -> workspace[tile+doc];
-//                per tile: 10 token-level partial sums.
+// token axis is cut into tiles of kTile tokens, one workgroup each.  A tile
+// usually overlaps one to three documents: then every thread strides the whole
+// tile (coalesced) and accumulates into up to kFastDocs per-document slots,
+// reduced once per workgroup.  A tile crossing more documents falls back to one
+// wavefront per (tile, document) pair.  Both tiles and documents are ordered,
+// so the overlapping pairs form a monotone staircase and `tile + document`
+// indexes them without collision.
+//   k_ppo_tiles  5 per-document partial sums per pair -> workspace[tile+doc],
+//                10 token-level partial sums per tile;
 //   k_ppo_final  one workgroup: per-document totals in tile order, then the
-//                loss, ESS and every diagnostic, in a fixed order (no
-//                atomics, so results are bitwise reproducible).
-//   k_ppo_bwd    per token: d(total loss)/d new_lp, as torch autograd gives it
+//                loss, ESS and every diagnostic in one fused block reduction
+//                (fixed order, no atomics: bitwise reproducible);
+//   k_ppo_bwd    per token: d(total loss)/d new_lp as torch autograd gives it
 //                (min splits ties 1/2-1/2, clamp passes on [lo, hi]).
 #include <math.h>
 
@@ -33,9 +36,11 @@ namespace {
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int64_t kTile = 2048;
+constexpr int kFastDocs = 4;  // documents per tile handled by the whole workgroup
 constexpr int kTokSums = 10;  // token-level sums
 constexpr int kSegSums = 5;   // per-document sums: pg, cnt, w, w2, positive
 constexpr int kFinalThreads = 1024;
+constexpr int kFinalVals = 4 + kTokSums;
 
 enum TokSum { TS_TIS = 0, TS_RATIO, TS_CLIP, TS_TIS_MASKED, TS_COUNT, TS_KL, TS_LR_ABS, TS_K3, TS_LOGDIFF, TS_ENT };
 
@@ -86,21 +91,22 @@ __device__ __forceinline__ int64_t doc_of(const int64_t* off, int64_t n_slots, i
     return lo;
 }
 
-struct TokenTerms {
-    float pg;       // pg_per_token after TIS/IcePop and mask
-    float ratio;
-    float tis_ratio;
-    bool tis_mask;
+// Per-token forward terms and every per-token sum contribution.
+struct Contrib {
+    float seg[kSegSums];
+    float tok[kTokSums];
 };
 
-__device__ __forceinline__ TokenTerms token_terms(const meshy_ppo_args& a, int64_t i, float A, float nw,
-                                                  float ol, float mk, float& log_ratio) {
-    TokenTerms r;
-    log_ratio = nw - ol;
-    const float ratio = expf(log_ratio);
+__device__ __forceinline__ void token_contrib(const meshy_ppo_args& a, int64_t i, float A, float w_doc,
+                                              Contrib& c) {
+    const float nw = a.new_lp[i];
+    const float ol = a.old_lp[i];
+    const float mk = a.mask[i];
+    const float lr = nw - ol;
+    const float ratio = expf(lr);
     const float u = ratio * A;
-    const float c = t_clamp(ratio, 1.f - a.clip_low, 1.f + a.clip_high) * A;
-    float pg = -t_min(u, c);
+    const float cl = t_clamp(ratio, 1.f - a.clip_low, 1.f + a.clip_high) * A;
+    float pg = -t_min(u, cl);
     float tis = ratio;
     bool tm = true;
     if (a.use_icepop) {
@@ -112,16 +118,35 @@ __device__ __forceinline__ TokenTerms token_terms(const meshy_ppo_args& a, int64
         tm = (ratio >= a.tis_min) && (ratio <= a.tis_max);
         pg = tm ? pg : 0.f;
     }
-    r.pg = pg * mk;
-    r.ratio = ratio;
-    r.tis_ratio = tis;
-    r.tis_mask = tm;
-    return r;
+    c.seg[0] = pg * mk;
+    c.seg[1] = mk;
+    c.seg[2] = ratio * mk;
+    c.seg[3] = ratio * ratio * mk;
+    c.seg[4] = (a.positive_lm_coef != 0.f) ? -nw * w_doc * mk : 0.f;
+    c.tok[TS_TIS] = tis * mk;
+    c.tok[TS_RATIO] = ratio * mk;
+    c.tok[TS_CLIP] = ((ratio < 1.f - a.clip_low) || (ratio > 1.f + a.clip_high)) ? mk : 0.f * mk;
+    c.tok[TS_TIS_MASKED] = tm ? 0.f * mk : mk;
+    c.tok[TS_COUNT] = mk;
+    c.tok[TS_KL] = -lr * mk;
+    c.tok[TS_LR_ABS] = fabsf(lr) * mk;
+    c.tok[TS_K3] = 0.f;
+    c.tok[TS_LOGDIFF] = 0.f;
+    if (a.rollout_lp) {
+        const float train_lp = a.train_lp_is_old ? ol : nw;
+        const float diff = a.rollout_lp[i] - train_lp;
+        const float lrt = t_clamp(diff, -10.f, 10.f);
+        const float k3 = expf(lrt) - lrt - 1.f;
+        c.tok[TS_K3] = nan_to_num(k3) * mk;
+        c.tok[TS_LOGDIFF] = nan_to_num(fabsf(diff)) * mk;
+    }
+    c.tok[TS_ENT] = a.entropy ? a.entropy[i] * mk : 0.f;
 }
 
 __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Workspace ws) {
+    __shared__ int64_t s_off[kFastDocs + 1];
     __shared__ int64_t s_range[2];
-    __shared__ float s_tok[kWaves][kTokSums];
+    __shared__ float s_red[kWaves][kTokSums + kFastDocs * kSegSums];
     const int64_t b = blockIdx.x;
     const int64_t t0 = b * kTile;
     const int64_t t1 = min(t0 + kTile, a.n_tokens);
@@ -132,15 +157,85 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
     }
     __syncthreads();
     const int64_t d_first = s_range[0];
-    const int64_t d_last = s_range[1];
+    const int64_t nd = s_range[1] - d_first + 1;
     const int lane = threadIdx.x % kWave;
     const int wid = threadIdx.x / kWave;
-
     float acc[kTokSums];
 #pragma unroll
     for (int k = 0; k < kTokSums; ++k) acc[k] = 0.f;
 
-    for (int64_t d = d_first + wid; d <= d_last; d += kWaves) {
+    if (nd <= kFastDocs) {
+        if (threadIdx.x <= nd) s_off[threadIdx.x] = a.seg_offsets[d_first + threadIdx.x];
+        __syncthreads();
+        float A_d[kFastDocs], W_d[kFastDocs];
+#pragma unroll
+        for (int r = 0; r < kFastDocs; ++r) {
+            const int64_t d = d_first + r;
+            const bool real = r < nd && d < a.n_docs;
+            A_d[r] = (!a.adv_per_token && real) ? a.adv[d] : 0.f;
+            W_d[r] = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
+        }
+        float sg[kFastDocs][kSegSums];
+#pragma unroll
+        for (int r = 0; r < kFastDocs; ++r)
+#pragma unroll
+            for (int k = 0; k < kSegSums; ++k) sg[r][k] = 0.f;
+        for (int64_t i = t0 + threadIdx.x; i < t1; i += kThreads) {
+            int slot = 0;
+#pragma unroll
+            for (int j = 1; j < kFastDocs; ++j) slot += (j < nd && i >= s_off[j]) ? 1 : 0;
+            float A = 0.f, W = 0.f;
+#pragma unroll
+            for (int r = 0; r < kFastDocs; ++r) {
+                A = (slot == r) ? A_d[r] : A;
+                W = (slot == r) ? W_d[r] : W;
+            }
+            if (a.adv_per_token) A = a.adv[i];
+            Contrib c;
+            token_contrib(a, i, A, W, c);
+#pragma unroll
+            for (int k = 0; k < kTokSums; ++k) acc[k] += c.tok[k];
+#pragma unroll
+            for (int r = 0; r < kFastDocs; ++r)
+#pragma unroll
+                for (int k = 0; k < kSegSums; ++k) sg[r][k] += (slot == r) ? c.seg[k] : 0.f;
+        }
+        // One block reduction of the 10 token sums and the 4 x 5 document sums.
+#pragma unroll
+        for (int k = 0; k < kTokSums; ++k) acc[k] = wave_sum(acc[k]);
+#pragma unroll
+        for (int r = 0; r < kFastDocs; ++r)
+#pragma unroll
+            for (int k = 0; k < kSegSums; ++k) sg[r][k] = wave_sum(sg[r][k]);
+        if (lane == 0) {
+#pragma unroll
+            for (int k = 0; k < kTokSums; ++k) s_red[wid][k] = acc[k];
+#pragma unroll
+            for (int r = 0; r < kFastDocs; ++r)
+#pragma unroll
+                for (int k = 0; k < kSegSums; ++k) s_red[wid][kTokSums + r * kSegSums + k] = sg[r][k];
+        }
+        __syncthreads();
+        const int j = threadIdx.x;
+        if (j < kTokSums + kFastDocs * kSegSums) {
+            float v = 0.f;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) v += s_red[w][j];
+            if (j < kTokSums) {
+                ws.tok[b * kTokSums + j] = v;
+            } else {
+                const int r = (j - kTokSums) / kSegSums;
+                const int k = (j - kTokSums) % kSegSums;
+                const int64_t lo = max(s_off[r], t0);
+                const int64_t hi = r < nd ? min(s_off[r + 1], t1) : lo;
+                if (lo < hi) ws.seg[(b + d_first + r) * kSegSums + k] = v;
+            }
+        }
+        return;
+    }
+
+    // Many documents in this tile: one wavefront per (tile, document) pair.
+    for (int64_t d = d_first + wid; d < d_first + nd; d += kWaves) {
         const int64_t lo = max(a.seg_offsets[d], t0);
         const int64_t hi = min(a.seg_offsets[d + 1], t1);
         if (lo >= hi) continue;
@@ -149,33 +244,12 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
         const float w_doc = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
         float sg[kSegSums] = {0.f, 0.f, 0.f, 0.f, 0.f};
         for (int64_t i = lo + lane; i < hi; i += kWave) {
-            const float nw = a.new_lp[i];
-            const float ol = a.old_lp[i];
-            const float mk = a.mask[i];
-            const float A = a.adv_per_token ? a.adv[i] : A_doc;
-            float lr;
-            const TokenTerms tt = token_terms(a, i, A, nw, ol, mk, lr);
-            sg[0] += tt.pg;
-            sg[1] += mk;
-            sg[2] += tt.ratio * mk;
-            sg[3] += tt.ratio * tt.ratio * mk;
-            if (a.positive_lm_coef != 0.f) sg[4] += -nw * w_doc * mk;
-            acc[TS_TIS] += tt.tis_ratio * mk;
-            acc[TS_RATIO] += tt.ratio * mk;
-            acc[TS_CLIP] += ((tt.ratio < 1.f - a.clip_low) || (tt.ratio > 1.f + a.clip_high)) ? mk : 0.f * mk;
-            acc[TS_TIS_MASKED] += tt.tis_mask ? 0.f * mk : mk;
-            acc[TS_COUNT] += mk;
-            acc[TS_KL] += -lr * mk;
-            acc[TS_LR_ABS] += fabsf(lr) * mk;
-            if (a.rollout_lp) {
-                const float train_lp = a.train_lp_is_old ? ol : nw;
-                const float diff = a.rollout_lp[i] - train_lp;
-                const float lrt = t_clamp(diff, -10.f, 10.f);
-                const float k3 = expf(lrt) - lrt - 1.f;
-                acc[TS_K3] += nan_to_num(k3) * mk;
-                acc[TS_LOGDIFF] += nan_to_num(fabsf(diff)) * mk;
-            }
-            if (a.entropy) acc[TS_ENT] += a.entropy[i] * mk;
+            Contrib c;
+            token_contrib(a, i, a.adv_per_token ? a.adv[i] : A_doc, w_doc, c);
+#pragma unroll
+            for (int k = 0; k < kSegSums; ++k) sg[k] += c.seg[k];
+#pragma unroll
+            for (int k = 0; k < kTokSums; ++k) acc[k] += c.tok[k];
         }
 #pragma unroll
         for (int k = 0; k < kSegSums; ++k) sg[k] = wave_sum(sg[k]);
@@ -189,13 +263,13 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
     for (int k = 0; k < kTokSums; ++k) acc[k] = wave_sum(acc[k]);
     if (lane == 0) {
 #pragma unroll
-        for (int k = 0; k < kTokSums; ++k) s_tok[wid][k] = acc[k];
+        for (int k = 0; k < kTokSums; ++k) s_red[wid][k] = acc[k];
     }
     __syncthreads();
     if (threadIdx.x < kTokSums) {
         float v = 0.f;
 #pragma unroll
-        for (int w = 0; w < kWaves; ++w) v += s_tok[w][threadIdx.x];
+        for (int w = 0; w < kWaves; ++w) v += s_red[w][threadIdx.x];
         ws.tok[b * kTokSums + threadIdx.x] = v;
     }
 }
@@ -203,11 +277,14 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
 __global__ __launch_bounds__(kFinalThreads) void k_ppo_final(meshy_ppo_args a, Workspace ws,
                                                              float* __restrict__ out,
                                                              float* __restrict__ seg_cnt_out) {
-    __shared__ double scratch[kFinalThreads / kWave];
+    __shared__ double s_red[kFinalThreads / kWave][kFinalVals];
     const int64_t n_slots = a.n_docs + 1;
     const int64_t n_tiles = n_tiles_of(a.n_tokens);
-    // Per-document totals (tile order) and their contributions.
-    double loss_c = 0.0, pos_c = 0.0, ess_c = 0.0, doc_c = 0.0;
+    double v[kFinalVals];
+#pragma unroll
+    for (int k = 0; k < kFinalVals; ++k) v[k] = 0.0;
+    // Per-document totals (tile order) and their contributions: v[0..3] =
+    // loss terms, positive-LM terms, ESS terms, documents with tokens.
     for (int64_t d = threadIdx.x; d < n_slots; d += kFinalThreads) {
         const int64_t lo = a.seg_offsets[d];
         const int64_t hi = a.seg_offsets[d + 1];
@@ -224,36 +301,47 @@ __global__ __launch_bounds__(kFinalThreads) void k_ppo_final(meshy_ppo_args a, W
         if (seg_cnt_out) seg_cnt_out[d] = sg[1];
         if (d < a.n_docs) {
             if (a.per_token_loss) {
-                loss_c += sg[0];
-                pos_c += sg[4];
+                v[0] += sg[0];
+                v[1] += sg[4];
             } else {
                 const float c = fmaxf(sg[1], 1.f);
-                loss_c += sg[0] / c;
-                pos_c += sg[4] / c;
+                v[0] += sg[0] / c;
+                v[1] += sg[4] / c;
             }
             if (sg[1] > 0.f) {
-                ess_c += (sg[2] * sg[2]) / (fmaxf(sg[1], 1.f) * fmaxf(sg[3], 1e-8f));
-                doc_c += 1.0;
+                v[2] += (sg[2] * sg[2]) / (fmaxf(sg[1], 1.f) * fmaxf(sg[3], 1e-8f));
+                v[3] += 1.0;
             }
         }
     }
-    loss_c = block_sum<kFinalThreads>(loss_c, scratch);
-    pos_c = block_sum<kFinalThreads>(pos_c, scratch);
-    ess_c = block_sum<kFinalThreads>(ess_c, scratch);
-    doc_c = block_sum<kFinalThreads>(doc_c, scratch);
-    double tok[kTokSums];
+    // Token-level sums of every tile: v[4..13].
+    for (int64_t b = threadIdx.x; b < n_tiles; b += kFinalThreads) {
+        const float* src = ws.tok + b * kTokSums;
 #pragma unroll
-    for (int k = 0; k < kTokSums; ++k) {
-        double v = 0.0;
-        for (int64_t b = threadIdx.x; b < n_tiles; b += kFinalThreads) v += ws.tok[b * kTokSums + k];
-        tok[k] = block_sum<kFinalThreads>(v, scratch);
+        for (int k = 0; k < kTokSums; ++k) v[4 + k] += src[k];
     }
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+#pragma unroll
+    for (int k = 0; k < kFinalVals; ++k) v[k] = wave_sum(v[k]);
+    if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < kFinalVals; ++k) s_red[wid][k] = v[k];
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
+        double t[kFinalVals];
+#pragma unroll
+        for (int k = 0; k < kFinalVals; ++k) {
+            t[k] = 0.0;
+            for (int w = 0; w < kFinalThreads / kWave; ++w) t[k] += s_red[w][k];
+        }
         const double den = a.per_token_loss ? static_cast<double>(max<int64_t>(1, a.n_tokens_global))
                                             : static_cast<double>(max<int64_t>(1, a.n_docs_global));
-        const float loss = static_cast<float>(loss_c / den);
-        const float pos = static_cast<float>(pos_c / den);
+        const float loss = static_cast<float>(t[0] / den);
+        const float pos = static_cast<float>(t[1] / den);
         const float cp = static_cast<float>(max(1, a.cp_degree));
+        const double* tok = t + 4;
         out[MESHY_PPO_LOSS] = loss;
         out[MESHY_PPO_TOTAL_LOSS] = loss + a.positive_lm_coef * pos;
         out[MESHY_PPO_POSITIVE_LM_LOSS] = pos;
@@ -264,17 +352,60 @@ __global__ __launch_bounds__(kFinalThreads) void k_ppo_final(meshy_ppo_args a, W
         out[MESHY_PPO_TOKEN_COUNT] = static_cast<float>(tok[TS_COUNT]);
         out[MESHY_PPO_KL_SUM] = static_cast<float>(tok[TS_KL]);
         out[MESHY_PPO_LOG_RATIO_ABS_SUM] = static_cast<float>(tok[TS_LR_ABS]);
-        out[MESHY_PPO_ESS_SUM] = static_cast<float>(ess_c) / cp;
-        out[MESHY_PPO_DOC_COUNT] = static_cast<float>(doc_c) / cp;
+        out[MESHY_PPO_ESS_SUM] = static_cast<float>(t[2]) / cp;
+        out[MESHY_PPO_DOC_COUNT] = static_cast<float>(t[3]) / cp;
         out[MESHY_PPO_TRAIN_ROLLOUT_KL_SUM] = static_cast<float>(tok[TS_K3]);
         out[MESHY_PPO_TRAIN_ROLLOUT_LOGDIFF_ABS_SUM] = static_cast<float>(tok[TS_LOGDIFF]);
         out[MESHY_PPO_ENTROPY_SUM] = static_cast<float>(tok[TS_ENT]);
     }
 }
 
+// d(total loss)/d new_lp of token i in document d (gD = grad_loss * D_d).
+__device__ __forceinline__ float token_grad(const meshy_ppo_args& a, int64_t i, float A, float w_doc, float gD) {
+    const float lo_c = 1.f - a.clip_low;
+    const float hi_c = 1.f + a.clip_high;
+    const float nw = a.new_lp[i];
+    const float ol = a.old_lp[i];
+    const float mk = a.mask[i];
+    const float ratio = expf(nw - ol);
+    const float u = ratio * A;
+    const float c = t_clamp(ratio, lo_c, hi_c) * A;
+    // grad of pg_per_token (before masking) w.r.t. pg = -min(u, c)
+    float g = gD * mk;
+    if (a.use_icepop) {
+        const float tis = expf(ol - a.rollout_lp[i]);
+        const bool tm = (tis >= a.tis_min) && (tis <= a.tis_max);
+        g = tm ? g * tis : 0.f;
+    } else if (a.use_tis) {
+        const bool tm = (ratio >= a.tis_min) && (ratio <= a.tis_max);
+        g = tm ? g : 0.f;
+    }
+    const float gm = -g;  // through the negation
+    float gu, gc;
+    if (u == c) {
+        gu = 0.5f * gm;
+        gc = 0.5f * gm;
+    } else {
+        gu = (u > c) ? 0.f : gm;
+        gc = (u < c) ? 0.f : gm;
+    }
+    const float in_range = (ratio >= lo_c && ratio <= hi_c) ? 1.f : 0.f;
+    const float g_ratio = gu * A + (gc * A) * in_range;
+    float gn = g_ratio * ratio;
+    if (a.positive_lm_coef != 0.f) gn += (gD * a.positive_lm_coef) * (-(w_doc * mk));
+    return gn;
+}
+
+__device__ __forceinline__ float doc_scale(const meshy_ppo_args& a, const float* seg_cnt, int64_t d) {
+    if (d >= a.n_docs) return 0.f;  // the padding slot is not in the loss
+    return a.per_token_loss ? 1.f / static_cast<float>(max<int64_t>(1, a.n_tokens_global))
+                            : 1.f / (fmaxf(seg_cnt[d], 1.f) * static_cast<float>(max<int64_t>(1, a.n_docs_global)));
+}
+
 __global__ __launch_bounds__(kThreads) void k_ppo_bwd(meshy_ppo_args a, const float* __restrict__ seg_cnt,
                                                       const float* __restrict__ grad_loss,
                                                       float* __restrict__ grad_new) {
+    __shared__ int64_t s_off[kFastDocs + 1];
     __shared__ int64_t s_range[2];
     const int64_t b = blockIdx.x;
     const int64_t t0 = b * kTile;
@@ -285,59 +416,61 @@ __global__ __launch_bounds__(kThreads) void k_ppo_bwd(meshy_ppo_args a, const fl
         s_range[1] = doc_of(a.seg_offsets, n_slots, t1 - 1);
     }
     __syncthreads();
-    const int lane = threadIdx.x % kWave;
-    const int wid = threadIdx.x / kWave;
+    const int64_t d_first = s_range[0];
+    const int64_t nd = s_range[1] - d_first + 1;
     const float G = grad_loss[0];
-    const float lo_c = 1.f - a.clip_low;
-    const float hi_c = 1.f + a.clip_high;
-    for (int64_t d = s_range[0] + wid; d <= s_range[1]; d += kWaves) {
-        const int64_t lo = max(a.seg_offsets[d], t0);
-        const int64_t hi = min(a.seg_offsets[d + 1], t1);
-        if (lo >= hi) continue;
-        const bool real = d < a.n_docs;
-        // d loss / d (per-token pg) for this document.
-        float D = 0.f;
-        if (real) {
-            D = a.per_token_loss ? 1.f / static_cast<float>(max<int64_t>(1, a.n_tokens_global))
-                                 : 1.f / (fmaxf(seg_cnt[d], 1.f) * static_cast<float>(max<int64_t>(1, a.n_docs_global)));
+    if (nd <= kFastDocs) {
+        if (threadIdx.x <= nd) s_off[threadIdx.x] = a.seg_offsets[d_first + threadIdx.x];
+        __syncthreads();
+        float A_d[kFastDocs], W_d[kFastDocs], gD_d[kFastDocs];
+#pragma unroll
+        for (int r = 0; r < kFastDocs; ++r) {
+            const int64_t d = d_first + r;
+            const bool real = r < nd && d < a.n_docs;
+            A_d[r] = (!a.adv_per_token && real) ? a.adv[d] : 0.f;
+            W_d[r] = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
+            gD_d[r] = real ? G * doc_scale(a, seg_cnt, d) : 0.f;
         }
-        const float gD = G * D;
-        const float A_doc = (!a.adv_per_token && real) ? a.adv[d] : 0.f;
-        const float w_doc = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
-        for (int64_t i = lo + lane; i < hi; i += kWave) {
-            const float nw = a.new_lp[i];
-            const float ol = a.old_lp[i];
-            const float mk = a.mask[i];
-            const float A = a.adv_per_token ? a.adv[i] : A_doc;
-            const float ratio = expf(nw - ol);
-            const float u = ratio * A;
-            const float c = t_clamp(ratio, lo_c, hi_c) * A;
-            // grad of pg_per_token (before masking) w.r.t. pg = -min(u, c)
-            float g = gD * mk;
-            if (a.use_icepop) {
-                const float tis = expf(ol - a.rollout_lp[i]);
-                const bool tm = (tis >= a.tis_min) && (tis <= a.tis_max);
-                g = tm ? g * (tm ? tis : 0.f) : 0.f;
-            } else if (a.use_tis) {
-                const bool tm = (ratio >= a.tis_min) && (ratio <= a.tis_max);
-                g = tm ? g : 0.f;
+        for (int64_t i = t0 + threadIdx.x; i < t1; i += kThreads) {
+            int slot = 0;
+#pragma unroll
+            for (int j = 1; j < kFastDocs; ++j) slot += (j < nd && i >= s_off[j]) ? 1 : 0;
+            float A = 0.f, W = 0.f, gD = 0.f;
+#pragma unroll
+            for (int r = 0; r < kFastDocs; ++r) {
+                A = (slot == r) ? A_d[r] : A;
+                W = (slot == r) ? W_d[r] : W;
+                gD = (slot == r) ? gD_d[r] : gD;
             }
-            const float gm = -g;  // through the negation
-            float gu, gc;
-            if (u == c) {
-                gu = 0.5f * gm;
-                gc = 0.5f * gm;
-            } else {
-                gu = (u > c) ? 0.f : gm;
-                gc = (u < c) ? 0.f : gm;
-            }
-            const float in_range = (ratio >= lo_c && ratio <= hi_c) ? 1.f : 0.f;
-            const float g_ratio = gu * A + (gc * A) * in_range;
-            float gn = g_ratio * ratio;
-            if (a.positive_lm_coef != 0.f) gn += (G * D * a.positive_lm_coef) * (-(w_doc * mk));
-            grad_new[i] = gn;
+            if (a.adv_per_token) A = a.adv[i];
+            grad_new[i] = token_grad(a, i, A, W, gD);
         }
+        return;
     }
+    for (int64_t i = t0 + threadIdx.x; i < t1; i += kThreads) {
+        const int64_t d = doc_of(a.seg_offsets, n_slots, i);
+        const bool real = d < a.n_docs;
+        const float A = a.adv_per_token ? a.adv[i] : (real ? a.adv[d] : 0.f);
+        const float W = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
+        grad_new[i] = token_grad(a, i, A, W, G * doc_scale(a, seg_cnt, d));
+    }
+}
+
+// seg_offsets[d] = first token with id >= d, for sorted ids: token i writes
+// every d in (ids[i-1], ids[i]]; the slots after the last id get n.
+__global__ __launch_bounds__(kThreads) void k_segment_offsets(const int64_t* __restrict__ ids, int64_t n,
+                                                              int64_t n_slots, int64_t* __restrict__ off,
+                                                              int32_t* __restrict__ unsorted) {
+    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
+    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i <= n; i += stride) {
+        const int64_t prev = (i == 0) ? -1 : ids[i - 1];
+        const int64_t cur = (i == n) ? n_slots : ids[i];
+        if (unsorted && i > 0 && i < n && prev > cur) unsorted[0] = 1;
+        const int64_t lo = max<int64_t>(prev + 1, 0);
+        const int64_t hi = min<int64_t>(cur, n_slots - 1);
+        for (int64_t d = lo; d <= hi; ++d) off[d] = i;
+    }
+    if (blockIdx.x == 0 && threadIdx.x == 0) off[n_slots] = n;
 }
 
 int validate(const meshy_ppo_args& a, const char* who) {
@@ -397,46 +530,14 @@ extern "C" int meshy_ppo_loss_bwd(const meshy_ppo_args* args, const float* seg_c
     return check_launch("meshy_ppo_loss_bwd");
 }
 
-namespace meshy {
-namespace {
-
-__global__ __launch_bounds__(kThreads) void k_segment_offsets(const int64_t* __restrict__ ids, int64_t n,
-                                                              int64_t n_slots, int64_t* __restrict__ off,
-                                                              int32_t* __restrict__ unsorted) {
-    const int64_t gid = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (gid == n_slots) {
-        // The last offset is the token count, so every token lies in some slot
-        // (ids beyond the padding slot, which the Batch contract excludes, fold into it).
-        off[gid] = n;
-    } else if (gid < n_slots) {
-        // lower_bound(ids, gid)
-        int64_t lo = 0, hi = n;
-        while (lo < hi) {
-            const int64_t mid = (lo + hi) >> 1;
-            if (ids[mid] < gid) lo = mid + 1;
-            else hi = mid;
-        }
-        off[gid] = lo;
-    }
-    if (unsorted) {
-        for (int64_t i = gid; i + 1 < n; i += static_cast<int64_t>(gridDim.x) * kThreads)
-            if (ids[i] > ids[i + 1]) unsorted[0] = 1;
-    }
-}
-
-}  // namespace
-}  // namespace meshy
-
 extern "C" int meshy_segment_offsets(const int64_t* doc_ids, int64_t n_tokens, int64_t n_slots,
                                      int64_t* seg_offsets, int32_t* unsorted, hipStream_t stream) {
     using namespace meshy;
     clear_error();
-    if (n_tokens < 0 || n_slots < 0) return set_error(MESHY_EINVAL, "meshy_segment_offsets: negative sizes");
+    if (n_tokens < 0 || n_slots < 1) return set_error(MESHY_EINVAL, "meshy_segment_offsets: bad sizes");
     if (!seg_offsets || (n_tokens > 0 && !doc_ids))
         return set_error(MESHY_ENULL, "meshy_segment_offsets: NULL pointer");
-    const int64_t need = n_slots + 1;
-    int64_t blocks = ceil_div(need, kThreads);
-    if (unsorted) blocks = std::max<int64_t>(blocks, std::min<int64_t>(1024, ceil_div(n_tokens, kThreads)));
+    const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(2048, ceil_div(n_tokens + 1, kThreads)));
     hipLaunchKernelGGL(k_segment_offsets, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream,
                        doc_ids, n_tokens, n_slots, seg_offsets, unsorted);
     return check_launch("meshy_segment_offsets");

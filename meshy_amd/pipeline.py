@@ -1,0 +1,185 @@
+"""The packed step between rollout and trainer, end to end, with one host-to-device copy.
+
+``RaggedSamples`` holds one step's samples as flat pinned host arrays (tokens,
+assistant mask, rollout logprobs, per-sample rewards and group offsets) plus
+room for the plan tables: the jagged layout the rollout's columns already use.
+``pack_step`` then
+
+1. counts tokens and loss tokens per sample on the host (``meshy_sample_loss_tokens``,
+   trainer.py:577-588) and plans the batch (``meshy_plan_build``, plan.py:211-288);
+2. writes the rank's micro tables into the same pinned buffer and copies it to
+   the device in ONE transfer;
+3. normalises rewards per group (``meshy_grpo_advantage``, rollout.py:88-97) and
+   materialises every micro of the rank (``meshy_pack_micro_batches``,
+   batch.py:96-230).  Documents index the samples' global positions, so no gather
+   is needed between the two kernels.
+"""
+
+from __future__ import annotations
+
+from typing import Any, Sequence
+
+import numpy as np
+import torch
+
+from . import _lib
+from .batch import Batch, PackJob, _Layout, launch_pack
+from .plan import Plan, PlannerConfig, plan_tables, tables_to_plan
+
+
+class RaggedSamples:
+    """One step's samples as flat pinned host arrays, in global sample order."""
+
+    def __init__(self, lengths: np.ndarray, n_groups: int, need_rollout_lp: bool) -> None:
+        n = len(lengths)
+        self.n = n
+        self.lengths = np.asarray(lengths, np.int64)
+        self.offsets = np.zeros(n + 1, np.int64)
+        np.cumsum(self.lengths, out=self.offsets[1:])
+        self.total = int(self.offsets[-1])
+        self.need_rollout_lp = need_rollout_lp
+        lay = _Layout()
+        lay.add("tokens", self.total, torch.int32)
+        lay.add("mask", self.total, torch.float32)
+        if need_rollout_lp:
+            lay.add("logprobs", self.total, torch.float32)
+        lay.add("s_off", n + 1, torch.int64)
+        lay.add("rewards", max(n, 1), torch.float32)
+        lay.add("group_off", n_groups + 1, torch.int64)
+        # plan tables of one rank: at most n micros and n documents
+        lay.add("seq", max(n, 1), torch.int64)
+        lay.add("out_off", n + 1, torch.int64)
+        lay.add("doc_len", max(n, 1), torch.int64)
+        lay.add("doc_start", n + 1, torch.int32)
+        lay.add("doc_sample", max(n, 1), torch.int32)
+        lay.add("pos_w", max(n, 1), torch.float32)
+        lay.add("adv_samples", max(n, 1), torch.float32)
+        self.lay = lay
+        self.n_groups = n_groups
+        # Pinned when a device is present, so the one copy to it is a DMA.
+        self.buf = torch.empty(lay.size, dtype=torch.uint8, pin_memory=torch.cuda.is_available())
+        self.copied = None  # event of the last host-to-device copy out of buf
+        self.view("s_off").copy_(torch.from_numpy(self.offsets))
+        self.view("pos_w").zero_()
+
+    def view(self, name: str) -> torch.Tensor:
+        return self.lay.view(self.buf, name)
+
+    @classmethod
+    def from_arrays(cls, tokens, mask, logprobs, offsets, rewards, group_offsets) -> "RaggedSamples":
+        """From flat numpy arrays (sample i = [offsets[i], offsets[i+1]))."""
+        offsets = np.asarray(offsets, np.int64)
+        r = cls(np.diff(offsets), len(group_offsets) - 1, logprobs is not None)
+        r.view("tokens").copy_(torch.from_numpy(np.ascontiguousarray(tokens, np.int32)))
+        r.view("mask").copy_(torch.from_numpy(np.ascontiguousarray(mask, np.float32)))
+        if logprobs is not None:
+            r.view("logprobs").copy_(torch.from_numpy(np.ascontiguousarray(logprobs, np.float32)))
+        r.view("rewards")[:r.n] = torch.from_numpy(np.ascontiguousarray(rewards, np.float32))
+        r.view("group_off").copy_(torch.from_numpy(np.asarray(group_offsets, np.int64)))
+        return r
+
+    @classmethod
+    def from_samples(cls, samples: Sequence[Any], group_offsets, need_rollout_lp: bool = True) -> "RaggedSamples":
+        """From TensorDict-like samples (``tokens``, ``mask_assistant``, ``logprobs``, ``reward``)."""
+        lengths = np.array([len(s["tokens"]) for s in samples], np.int64)
+        r = cls(lengths, len(group_offsets) - 1, need_rollout_lp)
+        torch.cat([s["tokens"].to(torch.int32) for s in samples], out=r.view("tokens"))
+        torch.cat([s["mask_assistant"].to(torch.float32) for s in samples], out=r.view("mask"))
+        if need_rollout_lp:
+            torch.cat([s["logprobs"].to(torch.float32) for s in samples], out=r.view("logprobs"))
+        r.view("rewards")[:r.n] = torch.tensor([float(s["reward"]) for s in samples], dtype=torch.float32)
+        r.view("group_off").copy_(torch.as_tensor(np.asarray(group_offsets, np.int64)))
+        return r
+
+    def sample_lengths(self, seq_len: int) -> tuple[np.ndarray, np.ndarray]:
+        """(token count, loss tokens) per sample, natively (trainer.py:577-588)."""
+        lengths = np.empty(self.n, np.int64)
+        loss = np.empty(self.n, np.int64)
+        rc = _lib.load().meshy_sample_loss_tokens(
+            self.view("mask").data_ptr(), self.offsets.ctypes.data, self.n, seq_len,
+            lengths.ctypes.data, loss.ctypes.data)
+        _lib.check(rc, "meshy_sample_loss_tokens")
+        return lengths, loss
+
+
+class PackResult:
+    def __init__(self, plan: Plan | None, tables, batches: list[Batch], advantages: torch.Tensor) -> None:
+        self.plan = plan
+        self.tables = tables
+        self.batches = batches
+        self.advantages = advantages
+
+
+def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int = 1, rank: int = 0,
+              with_plan_objects: bool = True, broadcast_advantages: bool = True) -> PackResult:
+    """Plan, copy once, normalise rewards and build every micro of ``rank``."""
+    device = torch.device(device)
+    lengths, loss = ragged.sample_lengths(cfg.seq_len)
+    t = plan_tables(lengths, loss, dp_size, cfg)
+    if ragged.copied is not None:
+        ragged.copied.synchronize()  # the tables below reuse the pinned buffer
+    n_local = t.n_local
+    nm = t.n_micro_total
+    seq = t.micro_seq_len[rank * n_local: rank * n_local + nm]
+    start = t.micro_doc_start[rank * (n_local + 1): rank * (n_local + 1) + nm + 1]
+    local = t.local_indices[rank * n_local:(rank + 1) * n_local]
+    dsample = local[t.doc_sample[rank * n_local:(rank + 1) * n_local]]  # global sample index
+    dlen = t.doc_len[rank * n_local:(rank + 1) * n_local]
+    n_docs = np.diff(start)
+    packed = cfg.layout == "packed"
+    rows = np.ones(nm, np.int64) if packed else np.maximum(n_docs, 1)
+    elems = seq * rows
+    out_off = np.zeros(nm + 1, np.int64)
+    np.cumsum(elems, out=out_off[1:])
+    ragged.view("seq")[:nm] = torch.from_numpy(seq)
+    ragged.view("out_off")[:nm + 1] = torch.from_numpy(out_off)
+    ragged.view("doc_start")[:nm + 1] = torch.from_numpy(start)
+    nd_total = int(start[-1])
+    ragged.view("doc_sample")[:nd_total] = torch.from_numpy(dsample[:nd_total].astype(np.int32))
+    ragged.view("doc_len")[:nd_total] = torch.from_numpy(dlen[:nd_total])
+
+    stream = torch.cuda.current_stream(device)
+    dbuf = torch.empty(ragged.lay.size, dtype=torch.uint8, device=device)
+    dbuf.copy_(ragged.buf, non_blocking=True)
+    ragged.copied = torch.cuda.Event()
+    ragged.copied.record(stream)
+    lay = ragged.lay
+
+    adv = lay.view(dbuf, "adv_samples")[:ragged.n]
+    rc = _lib.load().meshy_grpo_advantage(lay.view(dbuf, "rewards").data_ptr(), lay.view(dbuf, "group_off").data_ptr(),
+                                          ragged.n_groups, adv.data_ptr(), stream.cuda_stream)
+    _lib.check(rc, "meshy_grpo_advantage")
+
+    plan = tables_to_plan(t) if with_plan_objects else None
+    if plan is not None:
+        micros = tuple(m for mini in plan.per_rank[rank] for m in mini.micros)
+    else:
+        micros = tuple(_LiteMicro(int(seq[k]), int(n_docs[k]), int(dlen[start[k]:start[k + 1]].sum()),
+                                  tuple(int(x) for x in dlen[start[k]:start[k + 1]])) for k in range(nm))
+    job = PackJob(
+        micros=micros, layout=cfg.layout, device=device, dbuf=dbuf, lay=lay,
+        need_rollout_lp=ragged.need_rollout_lp, per_token_adv=False, n_samples=ragged.n, seq=seq,
+        rows=rows, out_off=out_off, doc_start=start, max_elems=int(elems.max()) if nm else 0,
+        max_docs=int(n_docs.max()) if nm else 0, adv_samples=adv, broadcast_advantages=broadcast_advantages,
+    )
+    batches = launch_pack(job)
+    return PackResult(plan, t, batches, adv)
+
+
+class _LiteMicro:
+    """What ``launch_pack`` reads of a MicroPlan, without building the dataclasses."""
+
+    __slots__ = ("seq_len", "n_docs", "n_tokens", "doc_lens")
+
+    def __init__(self, seq_len: int, n_docs: int, n_tokens: int, doc_lens: tuple) -> None:
+        self.seq_len = seq_len
+        self.n_docs = n_docs
+        self.n_tokens = n_tokens
+        self.doc_lens = doc_lens
+
+    @property
+    def n_rows(self) -> int:
+        return max(1, self.n_docs)
+
+
+__all__ = ["PackResult", "RaggedSamples", "pack_step"]

@@ -220,6 +220,24 @@ def test_deterministic_and_repeatable(dev):
         assert torch.equal(x.attention_masks.cu_seq_q, y.attention_masks.cu_seq_q)
 
 
+def test_packed_micro_with_many_documents(dev):
+    """1500 short documents in one packed micro: more than the in-LDS offset table holds."""
+    from meshy_amd.batch import build_micro_batches
+    from meshy_amd.plan import MicroPlan
+
+    g = torch.Generator().manual_seed(11)
+    lens = torch.randint(2, 5, (1500,), generator=g).tolist()
+    samples = [_sample(L, prompt=1, seed=j) for j, L in enumerate(lens)]
+    small = MicroPlan((0, 1), 16, (lens[0], lens[1]))
+    big = MicroPlan(tuple(range(1500)), sum(lens) + 100, tuple(lens))
+    mbs = build_micro_batches(samples, [small, big], layout="packed", device=dev, sharder=_NoCp(),
+                              need_rollout_lp=True)
+    for mb, m in zip(mbs, [small, big]):
+        ref = obatch.build_micro_batch(samples, m.sample_idx, m.seq_len, m.doc_lens, layout="packed",
+                                       need_rollout_lp=True)
+        _assert_same(mb, ref, "packed")
+
+
 def test_cpu_device_is_rejected():
     from meshy_amd.batch import build_micro_batch
     from meshy_amd.plan import MicroPlan
@@ -269,3 +287,43 @@ def test_grpo_config0_matches_oracle(dev):
     off = torch.tensor([0, 1, 9, 10, 40, 41, 100])
     got = grpo_advantages(r.to(dev), off.to(dev)).cpu()
     assert (got - ogrpo.grpo_batched(r, off)).abs().max().item() <= 1e-4
+
+
+# ------------------------------------------------------------ pack_step (config 0)
+
+def test_pack_step_config0_matches_oracle(dev):
+    """Plan + one H2D + GRPO + pack: micro map, cu_seqlens, positions bit-exact;
+    advantages (per document and broadcast per token) within 1e-5."""
+    from meshy_amd import workloads
+    from meshy_amd.pipeline import RaggedSamples, pack_step
+    from meshy_amd.plan import PlannerConfig
+    from oracle import plan as oplan
+
+    batch, rewards, group_offsets = workloads.config0(0)
+    ragged = RaggedSamples.from_arrays(batch.tokens, batch.mask, batch.logprobs, batch.offsets, rewards,
+                                       group_offsets)
+    cfg = PlannerConfig(layout="packed", mini_batch_size=256, seq_len=8192, align=2048,
+                        max_tokens_per_micro=8192)
+    res = pack_step(ragged, cfg, dev)
+    samples = batch.sample_dicts(rewards=rewards)
+    lengths, loss = oplan.sample_lengths(samples, 8192)
+    local, per_rank = oplan.build_plan(lengths, loss, 1, layout="packed", mini_batch_size=256, seq_len=8192,
+                                       align=2048, max_tokens_per_micro=8192)
+    ref_adv = ogrpo.grpo_batched(torch.from_numpy(rewards), torch.from_numpy(group_offsets))
+    assert (res.advantages.cpu() - ref_adv).abs().max().item() <= 1e-5
+    assert tuple(res.plan.local_indices[0]) == tuple(local[0])
+    for s, a in zip(samples, ref_adv):
+        s["advantage"] = a
+    local_samples = [samples[i] for i in local[0]]
+    micros = [m for mini in per_rank[0] for m in mini[0]]
+    assert len(res.batches) == len(micros)
+    for mb, (idx, seq_len, doc_lens) in zip(res.batches, micros):
+        ref = obatch.build_micro_batch(local_samples, idx, seq_len, doc_lens, layout="packed",
+                                       need_rollout_lp=True)
+        for k in ("input_ids", "labels", "positions", "mask", "doc_ids"):
+            assert torch.equal(getattr(mb, k).cpu(), ref[k]), k
+        assert torch.equal(mb.rollout_logprobs.cpu(), ref["rollout_logprobs"])
+        assert torch.equal(mb.attention_masks.cu_seq_q.cpu(), ref["cu_seqlens"])
+        assert (mb.advantages.cpu() - ref["advantages"]).abs().max().item() <= 1e-5
+        bcast = torch.cat([ref["advantages"], torch.zeros(1)])[ref["doc_ids"]]
+        assert (mb.advantage_tokens.cpu() - bcast).abs().max().item() <= 1e-5
