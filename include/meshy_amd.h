@@ -311,6 +311,46 @@ size_t meshy_gae_workspace_size(int64_t rows, int64_t S, int64_t n_docs);
 int meshy_gae(const meshy_gae_args* args, hipStream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Per-token GAE advantages for a batch of samples (device).
+ * Replaces TitanTrainer._attach_gae_advantages (meshy/backend/titan/trainer.py:603-699).
+ * Samples are ragged: sample j covers [offsets[j], offsets[j+1]) of the flat
+ * inputs, already cut to its width min(len, seq_len).  On the next-token grid
+ * (trainer.py:656-667): mask[t] = mask_assistant[t+1] (0 at the sample's last
+ * position), values as given, and the sample's reward at last - 1 where last
+ * is its last position with mask_assistant > 0 (no reward when there is none
+ * or last == 0).  lambda < 0 selects VAPO (lambda from each sample's masked
+ * length with alpha); lambda in [0, 1] the constant-lambda rule with alpha = 1
+ * and lengths 1 / max(1e-9, 1 - lambda) (trainer.py:669-683).
+ * Outputs: adv [total] (zero outside the mask), grid_mask [total] (the
+ * shifted mask, nullable), lam_doc [n] (nullable) and metrics [5] =
+ * critic/value_mean, advantage_mean, advantage_abs_mean, advantage_seq_mean,
+ * lambda_mean (trainer.py:688-699).
+ * ---------------------------------------------------------------------- */
+typedef struct meshy_gae_attach_args {
+    const float* mask_assistant;   /* [total]                                 */
+    const void* values;            /* [total] fp32 or bf16                    */
+    const float* reward;           /* [n]                                     */
+    const int64_t* offsets;        /* [n + 1]                                 */
+    int64_t n;
+    int64_t total;
+    float gamma;
+    float alpha;
+    float lambda;                  /* < 0: VAPO                               */
+    float epsilon;
+    int32_t values_bf16;
+    int32_t reserved;
+    float* adv;                    /* [total]                                 */
+    float* grid_mask;              /* [total], nullable                       */
+    float* lam_doc;                /* [n], nullable                           */
+    float* metrics;                /* [5], nullable                           */
+    void* workspace;
+    size_t workspace_bytes;
+} meshy_gae_attach_args;
+
+size_t meshy_gae_attach_workspace_size(int64_t n, int64_t total);
+int meshy_gae_attach(const meshy_gae_attach_args* args, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
  * Masked global whitening of per-token advantages (device).
  * Replaces the arithmetic of whiten_advantages (meshy/backend/titan/vapo.py:6-32):
  * fp64 sum / sum of squares / count over tokens with mask != 0, unbiased

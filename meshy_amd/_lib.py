@@ -151,6 +151,29 @@ class GaeArgs(ctypes.Structure):
     ]
 
 
+class GaeAttachArgs(ctypes.Structure):
+    _fields_ = [
+        ("mask_assistant", c_void_p),
+        ("values", c_void_p),
+        ("reward", c_void_p),
+        ("offsets", c_void_p),
+        ("n", c_int64),
+        ("total", c_int64),
+        ("gamma", c_float),
+        ("alpha", c_float),
+        ("lambda_", c_float),
+        ("epsilon", c_float),
+        ("values_bf16", c_int32),
+        ("reserved", c_int32),
+        ("adv", c_void_p),
+        ("grid_mask", c_void_p),
+        ("lam_doc", c_void_p),
+        ("metrics", c_void_p),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
+    ]
+
+
 # name -> (restype, argtypes); every symbol include/meshy_amd.h declares.
 SIGNATURES = {
     "meshy_last_error": (ctypes.c_char_p, []),
@@ -178,6 +201,8 @@ SIGNATURES = {
     "meshy_ppo_loss_bwd": (c_int, [POINTER(PpoArgs), c_void_p, c_void_p, c_void_p, c_void_p]),
     "meshy_gae_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
     "meshy_gae": (c_int, [POINTER(GaeArgs), c_void_p]),
+    "meshy_gae_attach_workspace_size": (c_size_t, [c_int64, c_int64]),
+    "meshy_gae_attach": (c_int, [POINTER(GaeAttachArgs), c_void_p]),
     "meshy_whiten_workspace_size": (c_size_t, [c_int64]),
     "meshy_whiten_stats": (
         c_int, [c_void_p, c_void_p, c_int64, c_double, c_void_p, c_void_p, c_size_t, c_void_p]

@@ -143,6 +143,8 @@ class PackJob:
     adv_samples: torch.Tensor | None = None
     #: Also write ``Batch.advantage_tokens`` (per-document advantage per token).
     broadcast_advantages: bool = False
+    #: Per-token advantages gathered on the device (indexed like the staged tokens).
+    adv_tokens_dev: torch.Tensor | None = None
 
 
 def stage_micro_batches(
@@ -205,12 +207,24 @@ def stage_micro_batches(
     # Token ids travel as int32 (any vocabulary fits) and come out int64 like the reference's.
     tok_dtype = torch.int32
 
+    # Per-token advantages already on the device (attach_gae_advantages leaves
+    # them there) are gathered on the device; host ones travel with the rest.
+    adv_dev = None
+    if per_token_adv and n_s and all(samples[i][ADVANTAGE_TOKENS].is_cuda for i in used):
+        parts = []
+        for i, L in zip(used, need_len):
+            a = samples[i][ADVANTAGE_TOKENS][:L].to(device=device, dtype=torch.float32)
+            if a.numel() < L:
+                a = torch.cat([a, a.new_zeros(L - a.numel())])
+            parts.append(a)
+        adv_dev = torch.cat(parts)
+
     lay = _Layout()
     lay.add("tokens", total, tok_dtype)
     lay.add("mask", total, torch.float32)
     if need_rollout_lp:
         lay.add("logprobs", total, torch.float32)
-    if per_token_adv:
+    if per_token_adv and adv_dev is None:
         lay.add("adv_tokens", total, torch.float32)
     lay.add("adv_samples", max(n_s, 1), torch.float32)
     lay.add("s_off", n_s + 1, torch.int64)
@@ -232,7 +246,7 @@ def stage_micro_batches(
         if need_rollout_lp:
             torch.cat([s["logprobs"][:L].to(torch.float32) for s, L in zip(srcs, need_len)],
                       out=lay.view(host, "logprobs"))
-        if per_token_adv:
+        if per_token_adv and adv_dev is None:
             parts = []
             for s, L in zip(srcs, need_len):
                 a = s[ADVANTAGE_TOKENS][:L].to(device="cpu", dtype=torch.float32)
@@ -258,7 +272,7 @@ def stage_micro_batches(
         micros=tuple(micros), layout=layout, device=device, dbuf=dbuf, lay=lay,
         need_rollout_lp=need_rollout_lp, per_token_adv=per_token_adv, n_samples=n_s, seq=seq, rows=rows,
         out_off=out_off, doc_start=doc_start, max_elems=int(elems.max()) if n_micro else 0,
-        max_docs=int(n_docs.max()) if n_micro else 0,
+        max_docs=int(n_docs.max()) if n_micro else 0, adv_tokens_dev=adv_dev,
     )
 
 
@@ -287,7 +301,10 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
     a.layout = _lib.MESHY_LAYOUT_PACKED if layout == "packed" else _lib.MESHY_LAYOUT_PADDED
     a.mask = lay.view(dbuf, "mask").data_ptr()
     a.logprobs = lay.view(dbuf, "logprobs").data_ptr() if job.need_rollout_lp else None
-    a.adv_tokens = lay.view(dbuf, "adv_tokens").data_ptr() if job.per_token_adv else None
+    if job.adv_tokens_dev is not None:
+        a.adv_tokens = job.adv_tokens_dev.data_ptr()
+    else:
+        a.adv_tokens = lay.view(dbuf, "adv_tokens").data_ptr() if job.per_token_adv else None
     a.adv_samples = (job.adv_samples.data_ptr() if job.adv_samples is not None
                      else lay.view(dbuf, "adv_samples").data_ptr())
     a.sample_offsets = lay.view(dbuf, "s_off").data_ptr()

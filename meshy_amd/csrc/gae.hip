@@ -427,11 +427,10 @@ extern "C" size_t meshy_gae_workspace_size(int64_t rows, int64_t S, int64_t n_do
     return meshy::ws_bytes(rows * S, n_docs);
 }
 
-extern "C" int meshy_gae(const meshy_gae_args* args, hipStream_t stream) {
-    using namespace meshy;
-    clear_error();
-    if (!args) return set_error(MESHY_ENULL, "meshy_gae: args is NULL");
-    const meshy_gae_args& g = *args;
+namespace meshy {
+namespace {
+
+int gae_launch(const meshy_gae_args& g, hipStream_t stream) {
     if (g.rows < 0 || g.S < 0 || g.n_docs < 0) return set_error(MESHY_EINVAL, "meshy_gae: negative sizes");
     const int64_t n = g.rows * g.S;
     if (!g.rewards || !g.mask || !g.doc_ids) return set_error(MESHY_ENULL, "meshy_gae: rewards, mask and doc_ids are required");
@@ -470,6 +469,213 @@ extern "C" int meshy_gae(const meshy_gae_args* args, hipStream_t stream) {
     if (nc > 0 && (g.adv || g.returns)) {
         hipLaunchKernelGGL(k_gae_apply, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, vec);
         if ((rc = check_launch("meshy_gae(apply)"))) return rc;
+    }
+    return MESHY_OK;
+}
+
+}  // namespace
+}  // namespace meshy
+
+extern "C" int meshy_gae(const meshy_gae_args* args, hipStream_t stream) {
+    meshy::clear_error();
+    if (!args) return meshy::set_error(MESHY_ENULL, "meshy_gae: args is NULL");
+    return meshy::gae_launch(*args, stream);
+}
+
+// ------------------------------------------------- _attach_gae_advantages
+namespace meshy {
+namespace {
+
+constexpr int kAttachThreads = 256;
+
+struct AttachWs {
+    float* grid_mask;  // [total] (when the caller passes none)
+    float* rewards;    // [total]
+    int64_t* doc_ids;  // [total]
+    float* lengths;    // [n]
+    float* lam;        // [n] (when the caller passes none)
+    float* sums;       // [n][4]: sum v*m, sum a*m, sum |a|*m, sum m
+    void* gae_ws;
+    size_t gae_ws_bytes;
+};
+
+size_t attach_ws_bytes(int64_t n, int64_t total) {
+    return 3 * align_up(sizeof(float) * total, 256) + align_up(sizeof(int64_t) * total, 256) +
+           2 * align_up(sizeof(float) * std::max<int64_t>(n, 1), 256) +
+           align_up(sizeof(float) * 4 * std::max<int64_t>(n, 1), 256) + ws_bytes(total, n);
+}
+
+AttachWs attach_ws_of(void* base, int64_t n, int64_t total) {
+    char* p = static_cast<char*>(base);
+    AttachWs w;
+    w.grid_mask = reinterpret_cast<float*>(p);
+    p += align_up(sizeof(float) * total, 256);
+    w.rewards = reinterpret_cast<float*>(p);
+    p += align_up(sizeof(float) * total, 256);
+    p += align_up(sizeof(float) * total, 256);  // reserved
+    w.doc_ids = reinterpret_cast<int64_t*>(p);
+    p += align_up(sizeof(int64_t) * total, 256);
+    w.lengths = reinterpret_cast<float*>(p);
+    p += align_up(sizeof(float) * std::max<int64_t>(n, 1), 256);
+    w.lam = reinterpret_cast<float*>(p);
+    p += align_up(sizeof(float) * std::max<int64_t>(n, 1), 256);
+    w.sums = reinterpret_cast<float*>(p);
+    p += align_up(sizeof(float) * 4 * std::max<int64_t>(n, 1), 256);
+    w.gae_ws = p;
+    w.gae_ws_bytes = ws_bytes(total, n);
+    return w;
+}
+
+// One workgroup per sample: the next-token grid of trainer.py:656-667.
+__global__ __launch_bounds__(kAttachThreads) void k_attach_prep(meshy_gae_attach_args g, AttachWs ws,
+                                                                float* grid_mask, float length_const) {
+    __shared__ int64_t s_last[kAttachThreads / kWave];
+    const int64_t j = blockIdx.x;
+    const int64_t o = g.offsets[j];
+    const int64_t L = g.offsets[j + 1] - o;
+    const float* m = g.mask_assistant + o;
+    int64_t last = -1;
+    for (int64_t p = threadIdx.x; p < L; p += kAttachThreads)
+        if (m[p] > 0.f) last = max(last, p);
+    last = wave_max(last);
+    if (threadIdx.x % kWave == 0) s_last[threadIdx.x / kWave] = last;
+    __syncthreads();
+    last = s_last[0];
+#pragma unroll
+    for (int w = 1; w < kAttachThreads / kWave; ++w) last = max(last, s_last[w]);
+    const float r = g.reward[j];
+    for (int64_t p = threadIdx.x; p < L; p += kAttachThreads) {
+        grid_mask[o + p] = (p + 1 < L) ? m[p + 1] : 0.f;
+        ws.rewards[o + p] = (last > 0 && p == last - 1) ? r : 0.f;
+        ws.doc_ids[o + p] = j;
+    }
+    if (threadIdx.x == 0) ws.lengths[j] = length_const;
+}
+
+// One workgroup per sample: the four sums behind the critic/* metrics.
+__global__ __launch_bounds__(kAttachThreads) void k_attach_sums(meshy_gae_attach_args g, AttachWs ws,
+                                                                const float* grid_mask) {
+    __shared__ float scratch[kAttachThreads / kWave];
+    const int64_t j = blockIdx.x;
+    const int64_t o = g.offsets[j];
+    const int64_t L = g.offsets[j + 1] - o;
+    float vm = 0.f, am = 0.f, aam = 0.f, mm = 0.f;
+    for (int64_t p = threadIdx.x; p < L; p += kAttachThreads) {
+        const float mk = grid_mask[o + p];
+        const float v = g.values_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(g.values)[o + p])
+                                      : static_cast<const float*>(g.values)[o + p];
+        const float a = g.adv[o + p];
+        vm += v * mk;
+        am += a * mk;
+        aam += fabsf(a) * mk;
+        mm += mk;
+    }
+    vm = block_sum<kAttachThreads>(vm, scratch);
+    am = block_sum<kAttachThreads>(am, scratch);
+    aam = block_sum<kAttachThreads>(aam, scratch);
+    mm = block_sum<kAttachThreads>(mm, scratch);
+    if (threadIdx.x == 0) {
+        ws.sums[4 * j + 0] = vm;
+        ws.sums[4 * j + 1] = am;
+        ws.sums[4 * j + 2] = aam;
+        ws.sums[4 * j + 3] = mm;
+    }
+}
+
+__global__ __launch_bounds__(1024) void k_attach_final(meshy_gae_attach_args g, AttachWs ws, const float* lam) {
+    __shared__ double s_red[1024 / kWave][6];
+    double v[6] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0};  // vm, am, aam, m, per-sequence mean, lambda
+    for (int64_t j = threadIdx.x; j < g.n; j += 1024) {
+        const float* s = ws.sums + 4 * j;
+        v[0] += s[0];
+        v[1] += s[1];
+        v[2] += s[2];
+        v[3] += s[3];
+        v[4] += s[1] / fmaxf(s[3], 1.f);
+        v[5] += lam[j];
+    }
+#pragma unroll
+    for (int k = 0; k < 6; ++k) v[k] = wave_sum(v[k]);
+    if (threadIdx.x % kWave == 0) {
+#pragma unroll
+        for (int k = 0; k < 6; ++k) s_red[threadIdx.x / kWave][k] = v[k];
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t[6] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0};
+        for (int w = 0; w < 1024 / kWave; ++w)
+#pragma unroll
+            for (int k = 0; k < 6; ++k) t[k] += s_red[w][k];
+        const double n_tok = fmax(1.0, t[3]);
+        const double rows = fmax(1.0, static_cast<double>(g.n));
+        g.metrics[0] = static_cast<float>(t[0] / n_tok);
+        g.metrics[1] = static_cast<float>(t[1] / n_tok);
+        g.metrics[2] = static_cast<float>(t[2] / n_tok);
+        g.metrics[3] = static_cast<float>(t[4] / rows);
+        g.metrics[4] = static_cast<float>(t[5] / rows);
+    }
+}
+
+}  // namespace
+}  // namespace meshy
+
+extern "C" size_t meshy_gae_attach_workspace_size(int64_t n, int64_t total) {
+    if (n < 0 || total < 0) return 0;
+    return meshy::attach_ws_bytes(n, total);
+}
+
+extern "C" int meshy_gae_attach(const meshy_gae_attach_args* args, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    if (!args) return set_error(MESHY_ENULL, "meshy_gae_attach: args is NULL");
+    const meshy_gae_attach_args& g = *args;
+    if (g.n < 0 || g.total < 0) return set_error(MESHY_EINVAL, "meshy_gae_attach: negative sizes");
+    if (g.n == 0) return MESHY_OK;
+    if (!g.mask_assistant || !g.values || !g.reward || !g.offsets || !g.adv)
+        return set_error(MESHY_ENULL, "meshy_gae_attach: mask_assistant, values, reward, offsets and adv are required");
+    if (!(g.alpha > 0.f)) return set_error(MESHY_EINVAL, "meshy_gae_attach: alpha must be positive");
+    if (g.lambda > 1.f) return set_error(MESHY_EINVAL, "meshy_gae_attach: lambda must be within [0, 1]");
+    if (!g.workspace || g.workspace_bytes < attach_ws_bytes(g.n, g.total))
+        return set_error(MESHY_ESPACE, "meshy_gae_attach: workspace needs %zu bytes", attach_ws_bytes(g.n, g.total));
+    if (g.n > INT32_MAX) return set_error(MESHY_EINVAL, "meshy_gae_attach: too many samples");
+    const AttachWs ws = attach_ws_of(g.workspace, g.n, g.total);
+    float* grid_mask = g.grid_mask ? g.grid_mask : ws.grid_mask;
+    float* lam = g.lam_doc ? g.lam_doc : ws.lam;
+    const bool vapo = g.lambda < 0.f;
+    // The constant-lambda rule (trainer.py:676-679): lengths chosen so that
+    // 1 - 1/(1 * L) == lambda.
+    const float length_const =
+        vapo ? 0.f : static_cast<float>(1.0 / std::max(1e-9, 1.0 - static_cast<double>(g.lambda)));
+    hipLaunchKernelGGL(k_attach_prep, dim3(static_cast<unsigned>(g.n)), dim3(kAttachThreads), 0, stream, g, ws,
+                       grid_mask, length_const);
+    int rc = check_launch("meshy_gae_attach(prep)");
+    if (rc) return rc;
+    meshy_gae_args a{};
+    a.rewards = ws.rewards;
+    a.values = g.values;
+    a.mask = grid_mask;
+    a.doc_ids = ws.doc_ids;
+    a.lengths = vapo ? nullptr : ws.lengths;
+    a.rows = 1;
+    a.S = g.total;
+    a.n_docs = g.n;
+    a.gamma = g.gamma;
+    a.alpha = vapo ? g.alpha : 1.f;
+    a.epsilon = g.epsilon;
+    a.values_bf16 = g.values_bf16;
+    a.adv = g.adv;
+    a.returns = nullptr;
+    a.lam_doc = lam;
+    a.workspace = ws.gae_ws;
+    a.workspace_bytes = ws.gae_ws_bytes;
+    rc = gae_launch(a, stream);
+    if (rc) return rc;
+    if (g.metrics) {
+        hipLaunchKernelGGL(k_attach_sums, dim3(static_cast<unsigned>(g.n)), dim3(kAttachThreads), 0, stream, g, ws,
+                           grid_mask);
+        if ((rc = check_launch("meshy_gae_attach(sums)"))) return rc;
+        hipLaunchKernelGGL(k_attach_final, dim3(1), dim3(1024), 0, stream, g, ws, lam);
+        if ((rc = check_launch("meshy_gae_attach(final)"))) return rc;
     }
     return MESHY_OK;
 }

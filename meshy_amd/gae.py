@@ -10,6 +10,9 @@ grid, in fp32, with no closed form and therefore no underflow fallback
 
 from __future__ import annotations
 
+from typing import Any, Sequence
+
+import numpy as np
 import torch
 
 from . import _lib
@@ -111,4 +114,93 @@ def gae_and_returns(
                 epsilon=epsilon, want_adv=True, want_returns=True, want_lam=True)
 
 
-__all__ = ["compute_returns", "compute_vapo_gae", "gae_and_returns"]
+CRITIC_METRICS = (
+    "critic/value_mean",
+    "critic/advantage_mean",
+    "critic/advantage_abs_mean",
+    "critic/advantage_seq_mean",
+    "critic/lambda_mean",
+)
+
+
+def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]:
+    """Drop-in for ``TitanTrainer._attach_gae_advantages`` (trainer.py:603-699).
+
+    Reads ``self.seq_len``, ``self.gae_gamma``, ``self.gae_alpha``,
+    ``self.gae_lambda`` and ``self.device``.  The samples' masks, values and
+    rewards travel to the device in one copy; ``meshy_gae_attach`` shifts them
+    onto the next-token grid, places each reward, runs the reverse scan over the
+    samples laid end to end (one document per sample, so no padding rows) and
+    reduces the critic metrics.  Each sample gets ``ADVANTAGE_TOKENS``, a device
+    view of its advantages, of length ``min(len(tokens), seq_len)``.
+    """
+    from .batch import ADVANTAGE_TOKENS, _Layout
+
+    if not samples:
+        return {}
+    seq_len = int(self.seq_len)
+    dev = torch.device(getattr(self, "device", None) or "cuda")
+    if dev.type != "cuda":
+        raise ValueError("meshy_amd runs GAE on a HIP device; self.device must be a cuda device")
+    n = len(samples)
+    widths = [min(int(len(td["tokens"])), seq_len) for td in samples]
+    for j, td in enumerate(samples):
+        if int(td["values"][:widths[j]].shape[0]) != widths[j]:
+            raise ValueError(
+                f"row {j}: critic published {tuple(td['values'].shape)} values "
+                f"for {widths[j]} tokens; the critic and the trainer disagree about "
+                f"the sequence"
+            )
+    offsets = np.zeros(n + 1, np.int64)
+    np.cumsum(widths, out=offsets[1:])
+    total = int(offsets[-1])
+    bf16 = all(td["values"].dtype == torch.bfloat16 for td in samples)
+    vdt = torch.bfloat16 if bf16 else torch.float32
+    lay = _Layout()
+    lay.add("mask", total, torch.float32)
+    lay.add("values", total, vdt)
+    lay.add("reward", n, torch.float32)
+    lay.add("offsets", n + 1, torch.int64)
+    host = torch.empty(lay.size, dtype=torch.uint8, pin_memory=True)
+    torch.cat([td["mask_assistant"][:L].to(device="cpu", dtype=torch.float32) for td, L in zip(samples, widths)],
+              out=lay.view(host, "mask"))
+    torch.cat([td["values"][:L].to(device="cpu", dtype=vdt) for td, L in zip(samples, widths)],
+              out=lay.view(host, "values"))
+    lay.view(host, "reward").copy_(torch.tensor(
+        [float(td["reward"].reshape(-1)[0].item()) if isinstance(td["reward"], torch.Tensor) else float(td["reward"])
+         for td in samples], dtype=torch.float32))
+    lay.view(host, "offsets").copy_(torch.from_numpy(offsets))
+    dbuf = torch.empty(lay.size, dtype=torch.uint8, device=dev)
+    dbuf.copy_(host, non_blocking=True)
+
+    lib = _lib.load()
+    adv = torch.empty(max(total, 1), dtype=torch.float32, device=dev)
+    lam = torch.empty(n, dtype=torch.float32, device=dev)
+    metrics = torch.empty(len(CRITIC_METRICS), dtype=torch.float32, device=dev)
+    ws = torch.empty(int(lib.meshy_gae_attach_workspace_size(n, total)), dtype=torch.uint8, device=dev)
+    g = _lib.GaeAttachArgs()
+    g.mask_assistant = lay.view(dbuf, "mask").data_ptr()
+    g.values = lay.view(dbuf, "values").data_ptr()
+    g.reward = lay.view(dbuf, "reward").data_ptr()
+    g.offsets = lay.view(dbuf, "offsets").data_ptr()
+    g.n, g.total = n, total
+    g.gamma = float(self.gae_gamma)
+    g.alpha = float(self.gae_alpha)
+    lam_const = getattr(self, "gae_lambda", None)
+    g.lambda_ = -1.0 if lam_const is None else float(lam_const)
+    g.epsilon = 1e-6
+    g.values_bf16 = int(bf16)
+    g.adv = adv.data_ptr()
+    g.grid_mask = None
+    g.lam_doc = lam.data_ptr()
+    g.metrics = metrics.data_ptr()
+    g.workspace = ws.data_ptr()
+    g.workspace_bytes = ws.numel()
+    rc = lib.meshy_gae_attach(_lib.ctypes.byref(g), _lib.stream_of(dev))
+    _lib.check(rc, "meshy_gae_attach")
+    for j, td in enumerate(samples):
+        td[ADVANTAGE_TOKENS] = adv[int(offsets[j]):int(offsets[j + 1])]
+    return dict(zip(CRITIC_METRICS, metrics.tolist()))
+
+
+__all__ = ["CRITIC_METRICS", "attach_gae_advantages", "compute_returns", "compute_vapo_gae", "gae_and_returns"]

@@ -58,14 +58,32 @@ def whiten_advantages(samples, seq_len, device, mesh=None, replication=1) -> Non
         stats_only = torch.zeros(0, dtype=torch.float32, device=device)
         whiten_flat(stats_only, stats_only, mesh, replication)
         return
-    flat = torch.cat([a.to(device=device, dtype=torch.float32) for a in advs])
     flat_mask = torch.cat(masks).to(device, non_blocking=True)
+    base = _tiled_view(advs)
+    if base is not None:
+        whiten_flat(base, flat_mask, mesh, replication)
+        return
+    flat = torch.cat([a.to(device=device, dtype=torch.float32) for a in advs])
     whiten_flat(flat, flat_mask, mesh, replication)
     o = 0
     for a in advs:
         n = len(a)
         a.copy_(flat[o:o + n])
         o += n
+
+
+def _tiled_view(tensors) -> torch.Tensor | None:
+    """The flat device view the tensors tile, in order, if they do (else None)."""
+    t0 = tensors[0]
+    if not all(t.is_cuda and t.dtype == torch.float32 and t.dim() == 1 and t.is_contiguous() for t in tensors):
+        return None
+    ptr = t0.untyped_storage().data_ptr()
+    off = t0.storage_offset()
+    for t in tensors:
+        if t.untyped_storage().data_ptr() != ptr or t.storage_offset() != off:
+            return None
+        off += t.numel()
+    return t0.as_strided((off - t0.storage_offset(),), (1,), t0.storage_offset())
 
 
 __all__ = ["whiten_advantages", "whiten_flat"]

@@ -69,6 +69,54 @@ def compute_vapo_gae(rewards, values, mask, doc_ids, n_docs, *, lengths=None, ga
     return adv, lam_doc[:n_docs]
 
 
+def attach_gae_advantages(samples, *, seq_len, gamma=1.0, alpha=1.5, gae_lambda=None):
+    """TitanTrainer._attach_gae_advantages (trainer.py:603-699): padded [rows, S]
+    block on the next-token grid, one document per row.  Returns (per-sample
+    advantages, metrics dict)."""
+    if not samples:
+        return [], {}
+    rows = len(samples)
+    widths = [min(int(len(td["tokens"])), seq_len) for td in samples]
+    S = max(widths)
+    mask = torch.zeros(rows, S)
+    values = torch.zeros(rows, S)
+    rewards = torch.zeros(rows, S)
+    doc_ids = torch.arange(rows, dtype=torch.long).unsqueeze(1).expand(rows, S).contiguous()
+    for j, td in enumerate(samples):
+        L = widths[j]
+        m = td["mask_assistant"][:L].to(torch.float32)
+        v = td["values"][:L].to(torch.float32)
+        if v.shape[0] != L:
+            raise ValueError("critic and trainer disagree about the sequence")
+        mask[j, :L - 1] = m[1:L]
+        values[j, :L] = v
+        response = (m > 0).nonzero()
+        if response.numel() == 0:
+            continue
+        last = int(response[-1].item())
+        if last == 0:
+            continue
+        rewards[j, last - 1] = float(td["reward"].reshape(-1)[0].item())
+    if gae_lambda is None:
+        lengths = None
+    else:
+        alpha = 1.0
+        lengths = torch.full((rows,), 1.0 / max(1e-9, 1.0 - gae_lambda), dtype=torch.float32)
+    adv, lam = compute_vapo_gae(rewards, values, mask, doc_ids, rows, gamma=gamma, alpha=alpha, lengths=lengths)
+    per_sample = [adv[j, :widths[j]].clone() for j in range(rows)]
+    counts = mask.sum(dim=1).clamp(min=1)
+    per_seq = (adv * mask).sum(dim=1) / counts
+    n_tokens = float(mask.sum())
+    metrics = {
+        "critic/value_mean": float((values * mask).sum() / max(1.0, n_tokens)),
+        "critic/advantage_mean": float((adv * mask).sum() / max(1.0, n_tokens)),
+        "critic/advantage_abs_mean": float((adv.abs() * mask).sum() / max(1.0, n_tokens)),
+        "critic/advantage_seq_mean": float(per_seq.mean()),
+        "critic/lambda_mean": float(lam.mean()),
+    }
+    return per_sample, metrics
+
+
 def gae_brute_force(rewards, values, mask, doc_ids, lam_doc, gamma):
     """Independent O(S^2) evaluation of the GAE sum, for tiny inputs:
     A_t = sum_k (prod_{j<k} gamma*lam*cont_{t+j}) * delta_{t+k}, computed per

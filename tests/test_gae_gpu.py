@@ -142,6 +142,80 @@ def test_config4_full_size(dev):
     assert (got_ret - ref_ret).abs().max().item() <= TOL
 
 
+def _critic_samples(n, seed, max_len=700, bf16=False):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for j in range(n):
+        L = int(torch.randint(1, max_len, (1,), generator=g))
+        prompt = int(torch.randint(0, max(1, L // 2), (1,), generator=g))
+        mask = torch.zeros(L)
+        mask[prompt:] = 1.0
+        if j % 7 == 3:
+            mask[:] = 0.0  # a sample without response tokens
+        v = torch.randn(L, generator=g)
+        out.append({"tokens": torch.arange(L), "mask_assistant": mask,
+                    "values": v.to(torch.bfloat16) if bf16 else v,
+                    "reward": torch.tensor(float(torch.rand(1, generator=g) < 0.5))})
+    return out
+
+
+@pytest.mark.parametrize("gae_lambda,alpha,gamma,seq_len,bf16", [
+    (None, 1.5, 1.0, 10 ** 6, False),
+    (0.95, 1.5, 1.0, 10 ** 6, True),
+    (None, 0.3, 0.97, 300, False),
+    (0.0, 1.0, 1.0, 500, False),
+])
+def test_attach_gae_advantages_matches_oracle(dev, gae_lambda, alpha, gamma, seq_len, bf16):
+    from types import SimpleNamespace as NS
+
+    from meshy_amd.batch import ADVANTAGE_TOKENS
+    from meshy_amd.gae import attach_gae_advantages
+
+    samples = _critic_samples(40, seed=hash((gae_lambda, alpha)) % 1000, bf16=bf16)
+    ref_adv, ref_m = ogae.attach_gae_advantages(
+        [{k: (v.float() if k == "values" else v) for k, v in s.items()} for s in samples],
+        seq_len=seq_len, gamma=gamma, alpha=alpha, gae_lambda=gae_lambda)
+    trainer = NS(seq_len=seq_len, gae_gamma=gamma, gae_alpha=alpha, gae_lambda=gae_lambda, device=dev)
+    metrics = attach_gae_advantages(trainer, samples)
+    for s, r in zip(samples, ref_adv):
+        got = s[ADVANTAGE_TOKENS]
+        assert got.is_cuda and got.shape == r.shape
+        assert (got.cpu() - r).abs().max().item() <= TOL
+    assert set(metrics) == set(ref_m)
+    for k in ref_m:
+        assert abs(metrics[k] - ref_m[k]) <= TOL, k
+
+
+def test_attach_then_whiten_and_pack(dev):
+    """GAE advantages left on the device feed whitening (in place, one buffer)
+    and the pack (per-token advantages gathered on the device)."""
+    from types import SimpleNamespace as NS
+
+    from meshy_amd.batch import ADVANTAGE_TOKENS, build_micro_batches
+    from meshy_amd.gae import attach_gae_advantages
+    from meshy_amd.plan import MicroPlan
+    from meshy_amd.vapo import whiten_advantages
+    from oracle import batch as obatch
+
+    samples = _critic_samples(12, seed=5, max_len=300)
+    trainer = NS(seq_len=256, gae_gamma=1.0, gae_alpha=1.5, gae_lambda=None, device=dev)
+    attach_gae_advantages(trainer, samples)
+    ref = [{**s, ADVANTAGE_TOKENS: s[ADVANTAGE_TOKENS].cpu().clone()} for s in samples]
+    whiten_advantages(samples, 256, dev)
+    ovapo.whiten_advantages(ref, 256)
+    for s, r in zip(samples, ref):
+        assert (s[ADVANTAGE_TOKENS].cpu() - r[ADVANTAGE_TOKENS]).abs().max().item() <= 1e-4
+    for s, r in zip(samples, ref):
+        s["logprobs"] = r["logprobs"] = torch.zeros(len(s["tokens"]))
+    widths = [min(len(s["tokens"]), 256) for s in samples]
+    micro = MicroPlan(tuple(range(4)), sum(widths[:4]) + 9, tuple(widths[:4]))
+    mb = build_micro_batches(samples, [micro], layout="packed", device=dev, need_rollout_lp=True)[0]
+    ref_mb = obatch.build_micro_batch(ref, micro.sample_idx, micro.seq_len, micro.doc_lens, layout="packed",
+                                      need_rollout_lp=True)
+    assert (mb.advantages.cpu() - ref_mb["advantages"]).abs().max().item() <= 1e-4
+    assert torch.equal(mb.mask.cpu(), ref_mb["mask"])
+
+
 def test_whitening_known_answers(dev):
     # test_vapo_alignment.py:39-46
     from meshy_amd.batch import ADVANTAGE_TOKENS

@@ -187,6 +187,31 @@ def test_gae_oracle_matches_brute_force_with_holes_and_docs():
         == [[0, 0, 1, 0]]
 
 
+def test_attach_gae_oracle_grid_shift_and_reward_placement():
+    # prompt of 3 (mask 0) + response of 5; on the next-token grid the loss
+    # mask is positions 2..6 and the reward sits at last - 1 = 6.
+    lam, R = 0.9, 0.5
+    s = {"tokens": torch.arange(8), "mask_assistant": torch.tensor([0, 0, 0, 1, 1, 1, 1, 1.]),
+         "values": torch.zeros(8), "reward": torch.tensor(R)}
+    empty = {"tokens": torch.arange(4), "mask_assistant": torch.zeros(4), "values": torch.ones(4),
+             "reward": torch.tensor(1.0)}
+    first_only = {"tokens": torch.arange(3), "mask_assistant": torch.tensor([1., 0, 0]), "values": torch.zeros(3),
+                  "reward": torch.tensor(1.0)}
+    adv, metrics = ogae.attach_gae_advantages([s, empty, first_only], seq_len=100, gae_lambda=lam)
+    lam_f = float(1.0 - 1.0 / float(torch.tensor(1.0 / (1.0 - lam), dtype=torch.float32)))
+    expect = torch.tensor([0, 0, lam_f ** 4 * R, lam_f ** 3 * R, lam_f ** 2 * R, lam_f * R, R, 0], dtype=torch.float64)
+    assert torch.allclose(adv[0].double(), expect, atol=1e-6)
+    assert adv[1].abs().sum() == 0 and adv[2].abs().sum() == 0  # no response / response at 0: no reward
+    # 'empty' has values 1 but no loss tokens; first_only has none either: 5 loss tokens in all
+    assert metrics["critic/value_mean"] == 0.0
+    assert metrics["critic/advantage_mean"] == pytest.approx(float(expect.sum()) / 5, rel=1e-5)
+    assert metrics["critic/advantage_seq_mean"] == pytest.approx(float(expect.sum()) / 5 / 3, rel=1e-5)
+    assert metrics["critic/lambda_mean"] == pytest.approx(lam, abs=1e-6)
+    # truncation to seq_len: the sample is cut to 6 tokens, its last response token is 5
+    adv_t, _ = ogae.attach_gae_advantages([s], seq_len=6, gae_lambda=lam)
+    assert adv_t[0].shape == (6,) and adv_t[0][4] == R
+
+
 # ------------------------------------------------------------------ whitening
 
 
