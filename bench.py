@@ -108,6 +108,47 @@ def bench_logprob(steps, warmup):
     return ms, nbytes, logits, labels
 
 
+def bench_read_ceiling(logits, steps, warmup):
+    """GB/s of a plain streaming read with K1's access pattern over the same logits."""
+    import torch
+
+    from meshy_amd import _lib
+
+    lib = _lib.load()
+    out = torch.zeros(1, dtype=torch.int32, device=logits.device)
+    rows = logits.shape[0] * logits.shape[1]
+    row_bytes = logits.shape[2] * 2
+
+    def step():
+        _lib.check(lib.meshy_stream_read(logits.data_ptr(), rows, row_bytes, out.data_ptr(),
+                                         _lib.stream_of(logits.device)), "meshy_stream_read")
+
+    ms = _gpu_ms(step, steps, warmup)
+    return rows * row_bytes / (ms * 1e-3) / 1e9
+
+
+def bench_logprob_bwd(logits, labels, steps, warmup):
+    """K1b: d logp / d logits written as bf16, one read of z and one write of dz."""
+    import torch
+
+    from meshy_amd import _lib, logprob
+
+    lse = logprob.logsumexp_rows(logits)
+    g = torch.ones_like(lse)
+    grad = torch.empty_like(logits)
+    rows, T, V = logits.shape
+    lib = _lib.load()
+
+    def step():
+        _lib.check(lib.meshy_logprob_bwd(logits.data_ptr(), rows, T, V, logits.stride(0), logits.stride(1),
+                                         labels.data_ptr(), lse.data_ptr(), g.data_ptr(), grad.data_ptr(),
+                                         _lib.stream_of(logits.device)), "meshy_logprob_bwd")
+
+    ms = _gpu_ms(step, steps, warmup)
+    del grad
+    return ms, rows * T * V * 4 + rows * T * 16
+
+
 def cpu_logprob_tokens_per_s(logits_gpu, labels_gpu, rows: int, runs: int = 5):
     import torch
 
@@ -446,6 +487,7 @@ def main() -> int:
 
     ms, nbytes, logits, labels = bench_logprob(args.steps, args.warmup)
     achieved = nbytes / (ms * 1e-3) / 1e9
+    read_ceiling = bench_read_ceiling(logits, args.steps, args.warmup)
     traffic = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
@@ -466,7 +508,9 @@ def main() -> int:
         "config": {"workload": "fused packed logprob+entropy over one micro-batch of logits", "T": T_TOK,
                    "V": VOCAB, "global_batch": T_TOK, "seq_len": T_TOK, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic},
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "read_ceiling": round(read_ceiling, 1),
+                     "frac_of_read_ceiling": round(achieved / read_ceiling, 4)},
     }
     if not args.no_cpu:
         tps, cms = cpu_logprob_tokens_per_s(logits, labels, args.cpu_rows)
@@ -474,12 +518,17 @@ def main() -> int:
             "value": round(tps, 1), "unit": "tokens/s", "cores": torch.get_num_threads(), "kind": "port",
             "sample": f"first {args.cpu_rows} rows of the same [16384, 151936] bf16 logits, median of 5 "
                       f"after 1 warm-up ({cms:.1f} ms per pass)"}
+    kernels = {"logprob_entropy_fwd_T16384_V151936": _entry(ms * 1e3, nbytes,
+                                                             result.get("cpu_baseline") and
+                                                             T_TOK / result["cpu_baseline"]["value"] * 1e3),
+               "stream_read_ceiling_T16384_V151936": {"GBps": round(read_ceiling, 1),
+                                                      "frac_hbm": round(read_ceiling / HBM_PEAK_GBS, 4)}}
+    if not args.quick:
+        bms, bbytes = bench_logprob_bwd(logits, labels, max(5, args.steps // 2), 2)
+        kernels["logprob_bwd_T16384_V151936"] = _entry(bms * 1e3, bbytes)
     del logits, labels
     torch.cuda.empty_cache()
     if not args.quick:
-        kernels = {"logprob_entropy_fwd_T16384_V151936": _entry(ms * 1e3, nbytes,
-                                                                 result.get("cpu_baseline") and
-                                                                 T_TOK / result["cpu_baseline"]["value"] * 1e3)}
         pack, _, _ = bench_pack(20, args.no_cpu)
         result["pack_latency_us"] = pack["pack_latency_us"]
         kernels["pack_grpo_config0"] = pack

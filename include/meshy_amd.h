@@ -367,6 +367,17 @@ int meshy_whiten_stats(const float* adv, const float* mask, int64_t n, double re
 int meshy_whiten_apply(float* adv, const float* mask, int64_t n, const double* stats,
                        hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Measurement helper; no counterpart in the reference.  Streams rows x
+ * row_bytes bytes from src (one workgroup per row, 16-byte nontemporal loads,
+ * 8 in flight per thread, the access pattern of meshy_logprob_entropy_fwd)
+ * and folds them into out[0], so a benchmark can report the read bandwidth
+ * this device reaches on that pattern next to the kernels' figures.
+ * row_bytes must be a multiple of 16 and src 16-byte aligned.
+ * ---------------------------------------------------------------------- */
+int meshy_stream_read(const void* src, int64_t rows, int64_t row_bytes, uint32_t* out,
+                      hipStream_t stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -208,6 +208,7 @@ SIGNATURES = {
         c_int, [c_void_p, c_void_p, c_int64, c_double, c_void_p, c_void_p, c_size_t, c_void_p]
     ),
     "meshy_whiten_apply": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "meshy_stream_read": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
 }
 
 ABI_VERSION = 1

@@ -331,25 +331,49 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
     _lib.check(rc, "meshy_pack_micro_batches")
     pos_w_dev = lay.view(dbuf, "pos_w")
 
+    # Per-micro views, one torch.split per output (the per-micro slicing of
+    # seven tensors is what the host time of a pack is otherwise made of).
+    sizes = np.diff(job.out_off).tolist()
+    rows_l = job.rows.tolist()
+    seq_l = job.seq.tolist()
+    if layout == "packed":
+        def views(t):
+            return None if t is None else torch.split(t.view(1, -1), sizes, dim=1)
+    else:
+        def views(t):
+            if t is None:
+                return None
+            return [p.view(R, S) for p, R, S in zip(torch.split(t, sizes), rows_l, seq_l)]
+    f_ids, f_lab, f_pos, f_mask, f_doc = (views(input_ids), views(labels), views(positions), views(mask),
+                                          views(doc_ids))
+    f_rl, f_at = views(rollout_lp), views(adv_tok)
+    nd_l = np.diff(job.doc_start).tolist()
+    f_adv = torch.split(adv_doc[:n_docs_total], nd_l)
+    f_len = torch.split(lengths[:n_docs_total], nd_l)
+    f_pw = torch.split(pos_w_dev[:n_docs_total], nd_l)
+    f_cu = None
+    pads = []
+    if layout == "packed":
+        # micro k's cu_seqlens: n_docs + 1 (+1 with a pad doc) slots out of n_docs + 2
+        cu_sizes = []
+        for k, m in enumerate(job.micros):
+            pad = seq_l[k] - m.n_tokens
+            pads.append(pad)
+            n_cu = nd_l[k] + 1 + (1 if pad > 0 else 0)
+            cu_sizes += [n_cu, nd_l[k] + 2 - n_cu]
+        f_cu = torch.split(cu, cu_sizes)[0::2]
+
     out: list[Batch] = []
     for k, m in enumerate(job.micros):
-        o0, o1 = int(job.out_off[k]), int(job.out_off[k + 1])
-        R, S = int(job.rows[k]), int(job.seq[k])
-        d0, d1 = int(job.doc_start[k]), int(job.doc_start[k + 1])
-        nd = d1 - d0
-
-        def v(t):
-            return None if t is None else t[o0:o1].view(R, S)
-
-        ii, lb, ps, mk, di, rl, at = (v(input_ids), v(labels), v(positions), v(mask), v(doc_ids),
-                                      v(rollout_lp), v(adv_tok))
+        nd = nd_l[k]
+        ii, lb, ps, mk, di = f_ids[k], f_lab[k], f_pos[k], f_mask[k], f_doc[k]
+        rl = f_rl[k] if f_rl is not None else None
+        at = f_at[k] if f_at is not None else None
         attn = None
         if layout == "packed":
-            pad = S - m.n_tokens
-            n_cu = nd + 1 + (1 if pad > 0 else 0)
-            c0 = d0 + 2 * k
-            max_len = max(list(m.doc_lens) + ([pad] if pad > 0 else []))
-            attn = make_varlen_metadata(cu[c0:c0 + n_cu], max_len, device)
+            pad = pads[k]
+            max_len = max(max(m.doc_lens, default=0), pad if pad > 0 else 0)
+            attn = VarlenMetadata(cu_seq_q=f_cu[k], cu_seq_k=f_cu[k], max_q=int(max_len), max_k=int(max_len))
         elif sharder is not None:
             # One CP shard call for every per-token tensor (batch.py:195-207);
             # the identity on one GPU.
@@ -368,12 +392,12 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
             positions=ps,
             mask=mk,
             doc_ids=di,
-            advantages=per_token if per_token is not None else adv_doc[d0:d1],
+            advantages=per_token if per_token is not None else f_adv[k],
             rollout_logprobs=rl,
-            lengths=lengths[d0:d1],
+            lengths=f_len[k],
             n_docs=nd,
             attention_masks=attn,
-            positive_lm_weights=pos_w_dev[d0:d1],
+            positive_lm_weights=f_pw[k],
             advantage_tokens=at if job.broadcast_advantages and not job.per_token_adv else None,
         ))
     return out

@@ -349,8 +349,10 @@ __global__ __launch_bounds__(NT) void k_lp_bwd_any(const uint16_t* __restrict__ 
     }
 }
 
+// 256 threads x 8 16-byte loads in flight per tile: the fastest shape of a
+// sweep over {64..1024} threads x {2, 4, 8} loads on MI355X.
 constexpr int kFwdThreads = 256;
-constexpr int kFwdUnroll = 4;
+constexpr int kFwdUnroll = 8;
 constexpr int kBwdThreads = 256;
 constexpr int kBwdUnroll = 2;
 
@@ -393,6 +395,49 @@ extern "C" int meshy_logprob_entropy_fwd(const uint16_t* logits, int64_t rows, i
                            V, stride_b, stride_t, labels, logp, entropy, lse);
     }
     return check_launch("meshy_logprob_entropy_fwd");
+}
+
+namespace meshy {
+namespace {
+
+// Bandwidth probe with K1's access pattern and no arithmetic.
+template <int NT, int U>
+__global__ __launch_bounds__(NT) void k_stream_read(const v4u* __restrict__ src, int64_t n16_per_row,
+                                                    uint32_t* __restrict__ out) {
+    const v4u* row = src + static_cast<int64_t>(blockIdx.x) * n16_per_row;
+    uint32_t acc = 0;
+    constexpr int64_t kTile = static_cast<int64_t>(NT) * U;
+    int64_t c = threadIdx.x;
+    for (; c + (U - 1) * NT < n16_per_row; c += kTile) {
+        v4u v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(row + c + u * NT);
+#pragma unroll
+        for (int u = 0; u < U; ++u) acc ^= v[u].x ^ v[u].y ^ v[u].z ^ v[u].w;
+    }
+    for (; c < n16_per_row; c += NT) {
+        const v4u v = __builtin_nontemporal_load(row + c);
+        acc ^= v.x ^ v.y ^ v.z ^ v.w;
+    }
+    acc = wave_sum(acc);
+    if (threadIdx.x == 0 && acc == 0x9e3779b9u) out[0] = acc;  // keeps the loads live
+}
+
+}  // namespace
+}  // namespace meshy
+
+extern "C" int meshy_stream_read(const void* src, int64_t rows, int64_t row_bytes, uint32_t* out,
+                                 hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    if (!src || !out) return set_error(MESHY_ENULL, "meshy_stream_read: NULL pointer");
+    if (rows < 0 || row_bytes < 0 || row_bytes % 16 != 0 || rows > INT32_MAX)
+        return set_error(MESHY_EINVAL, "meshy_stream_read: bad shape");
+    if (reinterpret_cast<uintptr_t>(src) % 16 != 0) return set_error(MESHY_EALIGN, "meshy_stream_read: src misaligned");
+    if (rows == 0) return MESHY_OK;
+    hipLaunchKernelGGL((k_stream_read<256, 8>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream,
+                       static_cast<const v4u*>(src), row_bytes / 16, out);
+    return check_launch("meshy_stream_read");
 }
 
 extern "C" int meshy_logprob_bwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,

@@ -97,11 +97,27 @@ struct Contrib {
     float tok[kTokSums];
 };
 
-__device__ __forceinline__ void token_contrib(const meshy_ppo_args& a, int64_t i, float A, float w_doc,
-                                              Contrib& c) {
-    const float nw = a.new_lp[i];
-    const float ol = a.old_lp[i];
-    const float mk = a.mask[i];
+// The per-token inputs, loaded ahead of the arithmetic.
+struct TokIn {
+    float nw, ol, mk, ro, en, ad;
+};
+
+__device__ __forceinline__ TokIn load_tok(const meshy_ppo_args& a, int64_t i, bool ok) {
+    TokIn x;
+    x.nw = ok ? a.new_lp[i] : 0.f;
+    x.ol = ok ? a.old_lp[i] : 0.f;
+    x.mk = ok ? a.mask[i] : 0.f;
+    x.ro = (ok && a.rollout_lp) ? a.rollout_lp[i] : 0.f;
+    x.en = (ok && a.entropy) ? a.entropy[i] : 0.f;
+    x.ad = (ok && a.adv_per_token) ? a.adv[i] : 0.f;
+    return x;
+}
+
+__device__ __forceinline__ void token_contrib_v(const meshy_ppo_args& a, const TokIn& x, float A, float w_doc,
+                                                Contrib& c) {
+    const float nw = x.nw;
+    const float ol = x.ol;
+    const float mk = x.mk;
     const float lr = nw - ol;
     const float ratio = expf(lr);
     const float u = ratio * A;
@@ -110,7 +126,7 @@ __device__ __forceinline__ void token_contrib(const meshy_ppo_args& a, int64_t i
     float tis = ratio;
     bool tm = true;
     if (a.use_icepop) {
-        tis = expf(ol - a.rollout_lp[i]);
+        tis = expf(ol - x.ro);
         tm = (tis >= a.tis_min) && (tis <= a.tis_max);
         const float weight = tm ? tis : 0.f;
         pg = (tm ? pg : 0.f) * weight;
@@ -134,13 +150,13 @@ __device__ __forceinline__ void token_contrib(const meshy_ppo_args& a, int64_t i
     c.tok[TS_LOGDIFF] = 0.f;
     if (a.rollout_lp) {
         const float train_lp = a.train_lp_is_old ? ol : nw;
-        const float diff = a.rollout_lp[i] - train_lp;
+        const float diff = x.ro - train_lp;
         const float lrt = t_clamp(diff, -10.f, 10.f);
         const float k3 = expf(lrt) - lrt - 1.f;
         c.tok[TS_K3] = nan_to_num(k3) * mk;
         c.tok[TS_LOGDIFF] = nan_to_num(fabsf(diff)) * mk;
     }
-    c.tok[TS_ENT] = a.entropy ? a.entropy[i] * mk : 0.f;
+    c.tok[TS_ENT] = a.entropy ? x.en * mk : 0.f;
 }
 
 __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Workspace ws) {
@@ -180,7 +196,18 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
         for (int r = 0; r < kFastDocs; ++r)
 #pragma unroll
             for (int k = 0; k < kSegSums; ++k) sg[r][k] = 0.f;
-        for (int64_t i = t0 + threadIdx.x; i < t1; i += kThreads) {
+        // Every load of the thread's kPer tokens first, then the arithmetic.
+        constexpr int kPer = static_cast<int>(kTile / kThreads);
+        TokIn in[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int64_t i = t0 + q * kThreads + threadIdx.x;
+            in[q] = load_tok(a, i, i < t1);
+        }
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int64_t i = t0 + q * kThreads + threadIdx.x;
+            if (i >= t1) break;
             int slot = 0;
 #pragma unroll
             for (int j = 1; j < kFastDocs; ++j) slot += (j < nd && i >= s_off[j]) ? 1 : 0;
@@ -190,9 +217,9 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
                 A = (slot == r) ? A_d[r] : A;
                 W = (slot == r) ? W_d[r] : W;
             }
-            if (a.adv_per_token) A = a.adv[i];
+            if (a.adv_per_token) A = in[q].ad;
             Contrib c;
-            token_contrib(a, i, A, W, c);
+            token_contrib_v(a, in[q], A, W, c);
 #pragma unroll
             for (int k = 0; k < kTokSums; ++k) acc[k] += c.tok[k];
 #pragma unroll
@@ -245,7 +272,8 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
         float sg[kSegSums] = {0.f, 0.f, 0.f, 0.f, 0.f};
         for (int64_t i = lo + lane; i < hi; i += kWave) {
             Contrib c;
-            token_contrib(a, i, a.adv_per_token ? a.adv[i] : A_doc, w_doc, c);
+            const TokIn x = load_tok(a, i, true);
+            token_contrib_v(a, x, a.adv_per_token ? x.ad : A_doc, w_doc, c);
 #pragma unroll
             for (int k = 0; k < kSegSums; ++k) sg[k] += c.seg[k];
 #pragma unroll
@@ -360,20 +388,21 @@ __global__ __launch_bounds__(kFinalThreads) void k_ppo_final(meshy_ppo_args a, W
     }
 }
 
-// d(total loss)/d new_lp of token i in document d (gD = grad_loss * D_d).
-__device__ __forceinline__ float token_grad(const meshy_ppo_args& a, int64_t i, float A, float w_doc, float gD) {
+// d(total loss)/d new_lp of one token (gD = grad_loss * D_d).
+__device__ __forceinline__ float token_grad_v(const meshy_ppo_args& a, const TokIn& x, float A, float w_doc,
+                                              float gD) {
     const float lo_c = 1.f - a.clip_low;
     const float hi_c = 1.f + a.clip_high;
-    const float nw = a.new_lp[i];
-    const float ol = a.old_lp[i];
-    const float mk = a.mask[i];
+    const float nw = x.nw;
+    const float ol = x.ol;
+    const float mk = x.mk;
     const float ratio = expf(nw - ol);
     const float u = ratio * A;
     const float c = t_clamp(ratio, lo_c, hi_c) * A;
     // grad of pg_per_token (before masking) w.r.t. pg = -min(u, c)
     float g = gD * mk;
     if (a.use_icepop) {
-        const float tis = expf(ol - a.rollout_lp[i]);
+        const float tis = expf(ol - x.ro);
         const bool tm = (tis >= a.tis_min) && (tis <= a.tis_max);
         g = tm ? g * tis : 0.f;
     } else if (a.use_tis) {
@@ -431,7 +460,17 @@ __global__ __launch_bounds__(kThreads) void k_ppo_bwd(meshy_ppo_args a, const fl
             W_d[r] = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
             gD_d[r] = real ? G * doc_scale(a, seg_cnt, d) : 0.f;
         }
-        for (int64_t i = t0 + threadIdx.x; i < t1; i += kThreads) {
+        constexpr int kPer = static_cast<int>(kTile / kThreads);
+        TokIn in[kPer];
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int64_t i = t0 + q * kThreads + threadIdx.x;
+            in[q] = load_tok(a, i, i < t1);
+        }
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int64_t i = t0 + q * kThreads + threadIdx.x;
+            if (i >= t1) break;
             int slot = 0;
 #pragma unroll
             for (int j = 1; j < kFastDocs; ++j) slot += (j < nd && i >= s_off[j]) ? 1 : 0;
@@ -442,17 +481,18 @@ __global__ __launch_bounds__(kThreads) void k_ppo_bwd(meshy_ppo_args a, const fl
                 W = (slot == r) ? W_d[r] : W;
                 gD = (slot == r) ? gD_d[r] : gD;
             }
-            if (a.adv_per_token) A = a.adv[i];
-            grad_new[i] = token_grad(a, i, A, W, gD);
+            if (a.adv_per_token) A = in[q].ad;
+            grad_new[i] = token_grad_v(a, in[q], A, W, gD);
         }
         return;
     }
     for (int64_t i = t0 + threadIdx.x; i < t1; i += kThreads) {
         const int64_t d = doc_of(a.seg_offsets, n_slots, i);
         const bool real = d < a.n_docs;
-        const float A = a.adv_per_token ? a.adv[i] : (real ? a.adv[d] : 0.f);
+        const TokIn x = load_tok(a, i, true);
+        const float A = a.adv_per_token ? x.ad : (real ? a.adv[d] : 0.f);
         const float W = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
-        grad_new[i] = token_grad(a, i, A, W, G * doc_scale(a, seg_cnt, d));
+        grad_new[i] = token_grad_v(a, x, A, W, G * doc_scale(a, seg_cnt, d));
     }
 }
 
