@@ -138,11 +138,13 @@ def bench_logprob_bwd(logits, labels, steps, warmup):
     grad = torch.empty_like(logits)
     rows, T, V = logits.shape
     lib = _lib.load()
+    ws = logprob.bwd_workspace(rows * T, logits.device)
 
     def step():
         _lib.check(lib.meshy_logprob_bwd(logits.data_ptr(), rows, T, V, logits.stride(0), logits.stride(1),
                                          labels.data_ptr(), lse.data_ptr(), g.data_ptr(), grad.data_ptr(),
-                                         _lib.stream_of(logits.device)), "meshy_logprob_bwd")
+                                         ws.data_ptr(), ws.numel(), _lib.stream_of(logits.device)),
+                   "meshy_logprob_bwd")
 
     ms = _gpu_ms(step, steps, warmup)
     del grad
@@ -159,6 +161,79 @@ def cpu_logprob_tokens_per_s(logits_gpu, labels_gpu, rows: int, runs: int = 5):
     ms = _wall_ms(lambda: olp.forward_logprobs(z, y, chunk=1024, with_entropy=True, entropy_chunk_size=512),
                   runs, gpu=False)
     return rows / (ms * 1e-3), ms
+
+
+# ---------------------------------------------------------------- OPD on config-1 logits
+
+def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
+    """Student Top-K OPD on the [16384, 151936] logits: Teacher Top-K (K = 8), the
+    gather of K + 1 ids (Teacher's K plus the label) forward and backward, and the
+    distillation loss forward + backward over the 16384 tokens."""
+    from types import SimpleNamespace as NS
+
+    import torch
+
+    from meshy_amd import _lib, logprob, opd, topk
+    from meshy_amd.batch import Batch
+    from meshy_amd.plan import MiniPlan
+
+    dev = logits.device
+    rows, T, V = logits.shape
+    K = 8
+    out = {}
+    res = {}
+    ms = _gpu_ms(lambda: res.__setitem__("t", topk.teacher_topk(logits, K)), steps, warmup)
+    t_ids, t_lps = res["t"]
+    cpu_ms = None
+    if not no_cpu:
+        from oracle import topk as otopk
+
+        zc = logits[:, :cpu_rows].cpu()
+        cms = _wall_ms(lambda: otopk.teacher_topk_reference_loop(zc, K), 3, gpu=False)
+        cpu_ms = cms * T / cpu_rows
+    out["teacher_topk_K8_T16384_V151936"] = _entry(ms * 1e3, T * V * 2 + T * K * 12, cpu_ms,
+                                                   cpu_sample=f"{cpu_rows} rows, scaled to T" if cpu_ms else None)
+    ids = torch.cat([t_ids, labels.unsqueeze(-1)], -1).contiguous()
+    ms = _gpu_ms(lambda: topk.gather_logprobs(logits, ids), steps, warmup)
+    out["gather_logprobs_K9_fwd"] = _entry(ms * 1e3, T * V * 2 + T * (K + 1) * 12)
+    lse = logprob.logsumexp_rows(logits)
+    g = torch.randn(rows, T, K + 1, device=dev)
+    grad = torch.empty_like(logits)
+    ws = logprob.bwd_workspace(rows * T, dev)
+    lib = _lib.load()
+
+    def bwd():
+        _lib.check(lib.meshy_gather_logprobs_bwd(logits.data_ptr(), rows, T, V, logits.stride(0), logits.stride(1),
+                                                 ids.data_ptr(), K + 1, lse.data_ptr(), g.data_ptr(),
+                                                 grad.data_ptr(), ws.data_ptr(), ws.numel(),
+                                                 _lib.stream_of(dev)), "meshy_gather_logprobs_bwd")
+
+    ms = _gpu_ms(bwd, max(5, steps // 2), 2)
+    out["gather_logprobs_K9_bwd"] = _entry(ms * 1e3, T * V * 4 + T * (K + 1) * 12)
+    del grad
+    # distillation loss over the T tokens: 12 documents, gathered log-probs from the kernel above
+    gathered = topk.gather_logprobs(logits, ids)
+    n_docs = 12
+    doc_ids = (torch.arange(T, device=dev) * n_docs // T).reshape(1, T)
+    mask = torch.ones(1, T, device=dev)
+    z = torch.zeros(1, 1, dtype=torch.long, device=dev)
+    mb = opd.TopKBatch(z, labels, z.int(), mask, doc_ids, torch.zeros(n_docs, device=dev),
+                       torch.full((1, T), -1.0, device=dev), torch.zeros(n_docs, device=dev), n_docs,
+                       teacher_topk_ids=t_ids, teacher_topk_logprobs=t_lps)
+    mini = MiniPlan((), n_docs, T, ())
+    stub = NS(calculate_per_token_loss=False, log_prob_min_clamp=-10.0, loss_max_clamp=10.0, sharder=None)
+    gd = gathered.detach().requires_grad_(True)
+
+    def loss_fb():
+        gd.grad = None
+        loss, _ = opd.distill_from_gathered(stub, gd, mb, mini)
+        loss.backward()
+
+    ms = _gpu_ms(loss_fb, steps, warmup)
+    # fwd reads student (K+1)*4 + teacher K*4 + mask 4 + rollout 4; bwd reads the same, writes (K+1)*4
+    per_tok = (K + 1) * 4 + K * 4 + 8
+    out["distill_loss_fwd_bwd_K8_T16384"] = _entry(ms * 1e3, T * (2 * per_tok + (K + 1) * 4), tokens=T)
+    return out
 
 
 # ---------------------------------------------------------------- config 0
@@ -526,6 +601,7 @@ def main() -> int:
     if not args.quick:
         bms, bbytes = bench_logprob_bwd(logits, labels, max(5, args.steps // 2), 2)
         kernels["logprob_bwd_T16384_V151936"] = _entry(bms * 1e3, bbytes)
+        kernels["opd"] = bench_opd(logits, labels, args.steps, args.warmup, args.no_cpu)
     del logits, labels
     torch.cuda.empty_cache()
     if not args.quick:

@@ -153,6 +153,15 @@ typedef struct meshy_pack_args {
     int32_t* cu_seqlens;           /* packed only, required there: micro k
                                       writes n_docs_k + 1 (+1 with a pad doc)
                                       values at micro_doc_start[k] + 2*k     */
+    /* Optional Teacher Top-K columns of on-policy distillation (replaces
+       layout_teacher_topk, meshy/backend/titan/opd.py:58-89): rows indexed
+       by logits position, NOT shifted; zero outside the documents.  Off
+       when teacher_k == 0. */
+    int64_t teacher_k;
+    const int32_t* teacher_ids;    /* [total, teacher_k], like tokens         */
+    const float* teacher_lps;      /* [total, teacher_k]                      */
+    int64_t* teacher_ids_out;      /* [n_out, teacher_k]                      */
+    float* teacher_lps_out;        /* [n_out, teacher_k]                      */
 } meshy_pack_args;
 
 int meshy_pack_micro_batches(const meshy_pack_args* args, hipStream_t stream);
@@ -189,13 +198,119 @@ int meshy_logprob_entropy_fwd(const uint16_t* logits, int64_t rows, int64_t T, i
  * Backward of logp with respect to the logits:
  *   grad_logits[r, v] = grad_logp[r] * (onehot(label_r)[v] - exp(z[r, v] - lse[r]))
  * written as bf16 into a contiguous [rows * T, V] buffer.  Ignored labels
- * (-100) give a zero row.  This is the gradient torch autograd produces for
- * the reference's checkpointed -cross_entropy chunk (trainer.py:504-517).
+ * (-100) give a zero row, labels outside [0, V) a NaN row.  This is the
+ * gradient torch autograd produces for the reference's checkpointed
+ * -cross_entropy chunk (trainer.py:504-517).  The workspace holds two floats
+ * per row (meshy_logprob_bwd_workspace_size(rows * T) bytes).
  */
+size_t meshy_logprob_bwd_workspace_size(int64_t n_rows);
 int meshy_logprob_bwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
                       int64_t stride_b, int64_t stride_t, const int64_t* labels,
                       const float* lse, const float* grad_logp, uint16_t* grad_logits,
-                      hipStream_t stream);
+                      void* workspace, size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * log_softmax(logits).gather(ids) over bf16 logits, and its backward (device).
+ * Replaces gather_logprobs (meshy/backend/titan/topk_loss.py:40-57) and its
+ * chunk body _chunk_gather_logprobs (topk_loss.py:35-37), with the
+ * checkpointed recompute of the chunk in backward.
+ *
+ * ids is contiguous [rows * T, n_ids] int64 (1 <= n_ids <= 256); out the
+ * same shape in fp32: out[r, k] = z[r, ids[r, k]] - lse[r].  An id of -100
+ * gives 0, an id outside [0, V) NaN.  lse ([rows * T], nullable) receives
+ * the per-row log-sum-exp the backward consumes.  Same logits layout rules
+ * as meshy_logprob_entropy_fwd.
+ *
+ * Backward: grad_logits[r, v] = sum_k grad_out[r, k] onehot(ids[r, k])[v]
+ *                               - (sum_k grad_out[r, k]) exp(z[r, v] - lse[r]),
+ * ids of -100 contributing nothing, as bf16 into a contiguous [rows * T, V]
+ * buffer; workspace as meshy_logprob_bwd.
+ * ---------------------------------------------------------------------- */
+int meshy_gather_logprobs_fwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
+                              int64_t stride_b, int64_t stride_t, const int64_t* ids,
+                              int64_t n_ids, float* out, float* lse, hipStream_t stream);
+int meshy_gather_logprobs_bwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
+                              int64_t stride_b, int64_t stride_t, const int64_t* ids,
+                              int64_t n_ids, const float* lse, const float* grad_out,
+                              uint16_t* grad_logits, void* workspace, size_t workspace_bytes,
+                              hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Teacher Top-K with log-probabilities (device), bf16 logits.
+ * Replaces teacher_topk (meshy/backend/titan/topk_loss.py:20-32):
+ *   ids[r, :]      the k columns of the k largest logits of row r, by value
+ *                  descending, equal values by ascending column;
+ *   logprobs[r, :] those logits minus the row's logsumexp (fp32);
+ *   lse[r]         the row's logsumexp (nullable).
+ * Outputs are contiguous [rows * T, k]; 1 <= k <= min(64, V).  Same logits
+ * layout rules as meshy_logprob_entropy_fwd.  NaN logits are never selected.
+ * ---------------------------------------------------------------------- */
+int meshy_topk_logprobs(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
+                        int64_t stride_b, int64_t stride_t, int64_t k, int64_t* ids,
+                        float* logprobs, float* lse, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Student Top-K distillation loss with its sums (device).
+ * Replaces StudentTopKTrainer._distill_loss after the gather
+ * (meshy/backend/titan/opd.py:164-197) and forward_kl_topk
+ * (meshy/backend/titan/topk_loss.py:60-80).  Documents are contiguous token
+ * ranges given by seg_offsets, as for the PPO loss.
+ * ---------------------------------------------------------------------- */
+enum meshy_distill_out {
+    MESHY_DISTILL_LOSS = 0,                     /* opd.py:178-181          */
+    MESHY_DISTILL_TOKEN_COUNT,
+    MESHY_DISTILL_STUDENT_MASS_SUM,
+    MESHY_DISTILL_TEACHER_MASS_SUM,
+    MESHY_DISTILL_TRAIN_ROLLOUT_KL_SUM,          /* with rollout_lp only    */
+    MESHY_DISTILL_TRAIN_ROLLOUT_LOGDIFF_ABS_SUM, /* with rollout_lp only    */
+    MESHY_DISTILL_NOUT
+};
+
+typedef struct meshy_distill_args {
+    const float* student;          /* [n_tokens, k + 1]: log-probs of the k
+                                      Teacher ids then of the sampled label  */
+    const float* teacher;          /* [n_tokens, k] Teacher log-probs         */
+    const float* mask;             /* [n_tokens]                              */
+    const float* rollout_lp;       /* [n_tokens], nullable                    */
+    const int64_t* seg_offsets;    /* [n_docs + 2]                            */
+    int64_t n_tokens;
+    int64_t n_docs;
+    int64_t k;                     /* 1 <= k <= 256                           */
+    int64_t n_docs_global;         /* MiniPlan.n_docs_global                  */
+    int64_t n_tokens_global;       /* MiniPlan.n_tokens_global                */
+    float lp_min_clamp;            /* log_prob_min_clamp (has_lp_clamp)       */
+    float loss_max_clamp;          /* loss_max_clamp (has_loss_clamp)         */
+    int32_t has_lp_clamp;
+    int32_t has_loss_clamp;
+    int32_t per_token_loss;        /* calculate_per_token_loss                */
+    int32_t reserved;
+    void* workspace;
+    size_t workspace_bytes;
+} meshy_distill_args;
+
+size_t meshy_distill_workspace_size(int64_t n_tokens, int64_t n_docs);
+/* out: [MESHY_DISTILL_NOUT] fp32 (device).  seg_cnt: [n_docs + 1] fp32
+ * (device, nullable), the per-document mask counts the backward needs. */
+int meshy_distill_loss_fwd(const meshy_distill_args* args, float* out, float* seg_cnt,
+                           hipStream_t stream);
+/* grad_student [n_tokens, k + 1]: d loss / d student * grad_loss[0] (device
+ * scalar); column k (the sampled token, detached in the reference) is 0. */
+int meshy_distill_loss_bwd(const meshy_distill_args* args, const float* seg_cnt,
+                           const float* grad_loss, float* grad_student, hipStream_t stream);
+
+/* forward_kl_topk alone (meshy/backend/titan/topk_loss.py:60-80), per
+ * position i of n: kl[i] = sum_k exp(t) (t - s) over the k log-probs
+ * student[i, :] and teacher[i, :] (contiguous [n, k]), both clamped from
+ * below by lp_min_clamp when has_lp_clamp, the sum clamped to
+ * [-loss_max_clamp, loss_max_clamp] when has_loss_clamp.  The backward
+ * writes grad_student [n, k] = d kl / d student * grad_kl. */
+int meshy_forward_kl_topk(const float* student, const float* teacher, int64_t n, int64_t k,
+                          int32_t has_lp_clamp, float lp_min_clamp, int32_t has_loss_clamp,
+                          float loss_max_clamp, float* kl, hipStream_t stream);
+int meshy_forward_kl_topk_bwd(const float* student, const float* teacher, int64_t n, int64_t k,
+                              int32_t has_lp_clamp, float lp_min_clamp, int32_t has_loss_clamp,
+                              float loss_max_clamp, const float* grad_kl, float* grad_student,
+                              hipStream_t stream);
 
 /* ------------------------------------------------------------------------
  * Token-level clipped PPO loss with its diagnostics (device).

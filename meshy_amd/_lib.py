@@ -95,6 +95,46 @@ class PackArgs(ctypes.Structure):
         ("adv_doc", c_void_p),
         ("doc_len_out", c_void_p),
         ("cu_seqlens", c_void_p),
+        ("teacher_k", c_int64),
+        ("teacher_ids", c_void_p),
+        ("teacher_lps", c_void_p),
+        ("teacher_ids_out", c_void_p),
+        ("teacher_lps_out", c_void_p),
+    ]
+
+
+# enum meshy_distill_out
+DISTILL_OUT_NAMES = (
+    "loss",
+    "token_count",
+    "student_mass_sum",
+    "teacher_mass_sum",
+    "train_rollout_kl_sum",
+    "train_rollout_logdiff_abs_sum",
+)
+DISTILL_NOUT = len(DISTILL_OUT_NAMES)
+
+
+class DistillArgs(ctypes.Structure):
+    _fields_ = [
+        ("student", c_void_p),
+        ("teacher", c_void_p),
+        ("mask", c_void_p),
+        ("rollout_lp", c_void_p),
+        ("seg_offsets", c_void_p),
+        ("n_tokens", c_int64),
+        ("n_docs", c_int64),
+        ("k", c_int64),
+        ("n_docs_global", c_int64),
+        ("n_tokens_global", c_int64),
+        ("lp_min_clamp", c_float),
+        ("loss_max_clamp", c_float),
+        ("has_lp_clamp", c_int32),
+        ("has_loss_clamp", c_int32),
+        ("per_token_loss", c_int32),
+        ("reserved", c_int32),
+        ("workspace", c_void_p),
+        ("workspace_bytes", c_size_t),
     ]
 
 
@@ -190,11 +230,40 @@ SIGNATURES = {
         [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
          c_void_p, c_void_p],
     ),
+    "meshy_logprob_bwd_workspace_size": (c_size_t, [c_int64]),
     "meshy_logprob_bwd": (
         c_int,
         [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p, c_size_t, c_void_p],
+    ),
+    "meshy_gather_logprobs_fwd": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
          c_void_p, c_void_p],
     ),
+    "meshy_gather_logprobs_bwd": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,
+         c_void_p, c_void_p, c_void_p, c_size_t, c_void_p],
+    ),
+    "meshy_topk_logprobs": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p,
+         c_void_p, c_void_p],
+    ),
+    "meshy_forward_kl_topk": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int64, c_int32, c_float, c_int32, c_float, c_void_p,
+         c_void_p],
+    ),
+    "meshy_forward_kl_topk_bwd": (
+        c_int,
+        [c_void_p, c_void_p, c_int64, c_int64, c_int32, c_float, c_int32, c_float, c_void_p,
+         c_void_p, c_void_p],
+    ),
+    "meshy_distill_workspace_size": (c_size_t, [c_int64, c_int64]),
+    "meshy_distill_loss_fwd": (c_int, [POINTER(DistillArgs), c_void_p, c_void_p, c_void_p]),
+    "meshy_distill_loss_bwd": (c_int, [POINTER(DistillArgs), c_void_p, c_void_p, c_void_p, c_void_p]),
     "meshy_segment_offsets": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p]),
     "meshy_ppo_workspace_size": (c_size_t, [c_int64, c_int64]),
     "meshy_ppo_loss_fwd": (c_int, [POINTER(PpoArgs), c_void_p, c_void_p, c_void_p]),
@@ -211,7 +280,7 @@ SIGNATURES = {
     "meshy_stream_read": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
 }
 
-ABI_VERSION = 1
+ABI_VERSION = 2
 
 _LIB: ctypes.CDLL | None = None
 

@@ -25,6 +25,9 @@ from .plan import Layout, MicroPlan
 #: laid out like rollout logprobs but not shifted again.
 ADVANTAGE_TOKENS = "advantage_tokens"
 
+#: OPD Teacher columns of a sample (meshy/config.py:506), ``[L, K]`` each.
+TEACHER_FIELDS = ("teacher_topk_ids", "teacher_topk_logprobs")
+
 
 class VarlenMetadata(NamedTuple):
     """Document boundaries for variable-length attention.
@@ -145,6 +148,11 @@ class PackJob:
     broadcast_advantages: bool = False
     #: Per-token advantages gathered on the device (indexed like the staged tokens).
     adv_tokens_dev: torch.Tensor | None = None
+    #: Teacher Top-K width staged with the samples (0: no Teacher columns).
+    teacher_k: int = 0
+    #: Per micro (ids, logprobs) Teacher columns in the micro's layout, filled by
+    #: ``launch_pack`` when ``teacher_k`` > 0.
+    teacher_views: list | None = None
 
 
 def stage_micro_batches(
@@ -154,9 +162,14 @@ def stage_micro_batches(
     layout: Layout,
     device,
     need_rollout_lp: bool,
+    teacher: bool = False,
 ) -> PackJob:
     """Gather what ``micros`` read from ``samples`` into one pinned buffer and copy it
-    to the device in one transfer (asynchronous on the current stream)."""
+    to the device in one transfer (asynchronous on the current stream).
+
+    With ``teacher`` the samples' OPD Teacher columns (``teacher_topk_ids``,
+    ``teacher_topk_logprobs``, ``[L, K]`` each) travel too and the pack lays them
+    out like ``layout_teacher_topk`` (opd.py:58-89)."""
     if layout not in ("padded", "packed"):
         raise ValueError(f"unknown layout {layout!r}")
     device = torch.device(device)
@@ -185,6 +198,7 @@ def stage_micro_batches(
     s_off = np.zeros(n_s + 1, np.int64)
     np.cumsum(need_len, out=s_off[1:])
     total = int(s_off[-1])
+    teacher_k = _teacher_width(samples, used, need_len) if teacher else 0
 
     # Plan tables.
     n_micro = len(micros)
@@ -234,6 +248,9 @@ def stage_micro_batches(
     lay.add("doc_start", n_micro + 1, torch.int32)
     lay.add("doc_sample", max(n_docs_total, 1), torch.int32)
     lay.add("pos_w", max(n_docs_total, 1), torch.float32)
+    if teacher_k:
+        lay.add("teacher_ids", total * teacher_k, torch.int32)
+        lay.add("teacher_lps", total * teacher_k, torch.float32)
 
     stage = _STAGING.setdefault(device.index or 0, _Staging())
     host = stage.get(lay.size)
@@ -246,6 +263,11 @@ def stage_micro_batches(
         if need_rollout_lp:
             torch.cat([s["logprobs"][:L].to(torch.float32) for s, L in zip(srcs, need_len)],
                       out=lay.view(host, "logprobs"))
+        if teacher_k:
+            torch.cat([s[TEACHER_FIELDS[0]][:L].to(torch.int32).reshape(-1) for s, L in zip(srcs, need_len)],
+                      out=lay.view(host, "teacher_ids"))
+            torch.cat([s[TEACHER_FIELDS[1]][:L].to(torch.float32).reshape(-1) for s, L in zip(srcs, need_len)],
+                      out=lay.view(host, "teacher_lps"))
         if per_token_adv and adv_dev is None:
             parts = []
             for s, L in zip(srcs, need_len):
@@ -272,8 +294,27 @@ def stage_micro_batches(
         micros=tuple(micros), layout=layout, device=device, dbuf=dbuf, lay=lay,
         need_rollout_lp=need_rollout_lp, per_token_adv=per_token_adv, n_samples=n_s, seq=seq, rows=rows,
         out_off=out_off, doc_start=doc_start, max_elems=int(elems.max()) if n_micro else 0,
-        max_docs=int(n_docs.max()) if n_micro else 0, adv_tokens_dev=adv_dev,
+        max_docs=int(n_docs.max()) if n_micro else 0, adv_tokens_dev=adv_dev, teacher_k=teacher_k,
     )
+
+
+def _teacher_width(samples, used, need_len) -> int:
+    """Top-K width of the used samples' Teacher columns; checks they cover the micros
+    (opd.py:39-55)."""
+    k = 0
+    for i, L in zip(used, need_len):
+        td = samples[i]
+        ids, lps = td[TEACHER_FIELDS[0]], td[TEACHER_FIELDS[1]]
+        if ids.shape[0] < L or lps.shape[0] < L:
+            raise ValueError(
+                f"teacher columns cover {int(min(ids.shape[0], lps.shape[0]))} positions but the student "
+                f"micro-batch needs {L}; the Teacher seq_len must be >= the Student's"
+            )
+        width = int(ids.shape[-1])
+        if k and width != k:
+            raise ValueError(f"Teacher Top-K widths differ across samples ({k} vs {width})")
+        k = width
+    return k
 
 
 def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
@@ -327,6 +368,16 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
     a.adv_doc = adv_doc.data_ptr()
     a.doc_len_out = lengths.data_ptr()
     a.cu_seqlens = cu.data_ptr()
+    t_ids = t_lps = None
+    if job.teacher_k:
+        K = job.teacher_k
+        t_ids = torch.empty(n_out * K, dtype=torch.int64, device=device)
+        t_lps = torch.empty(n_out * K, dtype=torch.float32, device=device)
+        a.teacher_k = K
+        a.teacher_ids = lay.view(dbuf, "teacher_ids").data_ptr()
+        a.teacher_lps = lay.view(dbuf, "teacher_lps").data_ptr()
+        a.teacher_ids_out = t_ids.data_ptr()
+        a.teacher_lps_out = t_lps.data_ptr()
     rc = lib.meshy_pack_micro_batches(_lib.ctypes.byref(a), torch.cuda.current_stream(device).cuda_stream)
     _lib.check(rc, "meshy_pack_micro_batches")
     pos_w_dev = lay.view(dbuf, "pos_w")
@@ -362,6 +413,22 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
             n_cu = nd_l[k] + 1 + (1 if pad > 0 else 0)
             cu_sizes += [n_cu, nd_l[k] + 2 - n_cu]
         f_cu = torch.split(cu, cu_sizes)[0::2]
+
+    if job.teacher_k:
+        K = job.teacher_k
+        sizes_k = [n * K for n in sizes]
+        tv = []
+        for part_i, part_l, R, S, m in zip(torch.split(t_ids, sizes_k), torch.split(t_lps, sizes_k), rows_l, seq_l,
+                                           job.micros):
+            if m.is_filler:
+                # infer_top_k of no samples is 1 (opd.py:39-44)
+                tv.append((torch.zeros(R, S, 1, dtype=torch.int64, device=device),
+                           torch.zeros(R, S, 1, dtype=torch.float32, device=device)))
+            else:
+                tv.append((part_i.view(R, S, K), part_l.view(R, S, K)))
+        if layout == "padded" and sharder is not None:
+            tv = [tuple(sharder.shard_seq(i, l)) for i, l in tv]
+        job.teacher_views = tv
 
     out: list[Batch] = []
     for k, m in enumerate(job.micros):
@@ -431,5 +498,5 @@ def build_micro_batch(
                                need_rollout_lp=need_rollout_lp)[0]
 
 
-__all__ = ["ADVANTAGE_TOKENS", "Batch", "PackJob", "VarlenMetadata", "build_micro_batch",
+__all__ = ["ADVANTAGE_TOKENS", "TEACHER_FIELDS", "Batch", "PackJob", "VarlenMetadata", "build_micro_batch",
            "build_micro_batches", "launch_pack", "make_varlen_metadata", "stage_micro_batches"]

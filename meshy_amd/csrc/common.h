@@ -66,6 +66,18 @@ __device__ __forceinline__ T block_sum(T v, T* scratch) {
     }
 }
 
+// Largest d in [0, n_slots] with off[d] <= i (off has n_slots + 1 entries,
+// non-decreasing): the document slot owning token i.
+__device__ __forceinline__ int64_t doc_of(const int64_t* off, int64_t n_slots, int64_t i) {
+    int64_t lo = 0, hi = n_slots;
+    while (lo < hi) {
+        const int64_t mid = (lo + hi + 1) >> 1;
+        if (off[mid] <= i) lo = mid;
+        else hi = mid - 1;
+    }
+    return lo;
+}
+
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }

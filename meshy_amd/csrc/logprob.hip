@@ -4,146 +4,63 @@
 // Forward (replaces the chunk loop of TitanTrainer._forward_logprobs,
 // meshy/backend/titan/trainer.py:451-527, i.e. -cross_entropy(z.float(), y)
 // at trainer.py:414-428 and logsumexp(z) - sum(softmax(z) * z) at
-// trainer.py:430-449): one workgroup streams one row of V logits from HBM
-// exactly once with 16-byte loads and keeps, per lane, an online triple
-//     m = running max of z,
-//     s = sum exp(z - m),
-//     t = sum exp(z - m) * (z - m) * log2(e)
-// updated once per register tile (tile max first, then one exp2 per element).
-// Lanes and waves merge their triples; thread 0 writes
-//     lse = m + ln s,  logp = z_y - lse,  H = ln 2 * (log2 s - t / s).
-// The row never leaves registers: no fp32 copy of the logits is made.
+// trainer.py:430-449, and the chunked gather of gather_logprobs,
+// meshy/backend/titan/topk_loss.py:35-57): one workgroup streams one row of
+// V logits from HBM exactly once with 16-byte loads and keeps, per lane, the
+// online (m, s, t) state of rowstream.h, updated once per register tile.
+// Lanes and waves merge their triples; then
+//     lse = m + ln s,  logp_k = z_{y_k} - lse,  H = ln 2 * (log2 s - t / s)
+// for the row's n_ids gather ids y_k.  No fp32 copy of the logits is made.
 //
-// Backward: grad[r, v] = g[r] * (onehot(y_r)[v] - exp(z[r, v] - lse[r])), bf16.
-#include <hip/hip_bf16.h>
+// Backward: grad[r, v] = sum_k g[r,k] onehot(y_k)[v] - G_r exp(z[r, v] - lse[r]),
+// G_r = sum_k g[r,k], written as bf16 in three launches: a per-row prep
+// (-G_r and -lse_r log2 e into the workspace), the streaming pass of the
+// softmax term, and a fixup of the n_ids one-hot positions.  The streaming
+// pass walks the flattened [rows * V] grid with a grid-stride loop when the
+// logits are contiguous: on MI355X that order writes 8 % faster than one
+// workgroup per row.
+#include <algorithm>
 
-#include "common.h"
+#include "rowstream.h"
 
 namespace meshy {
 namespace {
 
-// Native 4 x u32 vector: what the nontemporal load/store builtins accept.
-typedef unsigned int v4u __attribute__((ext_vector_type(4)));
-
-constexpr float kLog2e = 1.4426950408889634f;
-constexpr float kLn2 = 0.69314718055994531f;
-constexpr float kInit = -1e30f;  // finite "minus infinity": keeps 0 * d finite
-constexpr int64_t kIgnoreIndex = -100;
-
-__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
-
-// Merges (m2, s2, t2) into (m, s, t).
-__device__ __forceinline__ void merge(float& m, float& s, float& t, float m2, float s2, float t2) {
-    const float mn = fmaxf(m, m2);
-    const float d1 = (m - mn) * kLog2e;
-    const float d2 = (m2 - mn) * kLog2e;
-    const float a1 = fast_exp2(d1);
-    const float a2 = fast_exp2(d2);
-    t = a1 * fmaf(d1, s, t) + a2 * fmaf(d2, s2, t2);
-    s = a1 * s + a2 * s2;
-    m = mn;
+// thread 0: lse, entropy, and (with one id) the log-prob.
+__device__ __forceinline__ float id_logp(int64_t y, float zy, float lse, int64_t V) {
+    if (y == kIgnoreIndex) return 0.f;
+    if (y < 0 || y >= V) return __builtin_nanf("");
+    return zy - lse;
 }
 
-// Moves the running max to at least `tm`, rescaling s and t.
-__device__ __forceinline__ void raise_max(float& m, float& s, float& t, float tm) {
-    const float mn = fmaxf(m, tm);
-    const float d = (m - mn) * kLog2e;
-    const float a = fast_exp2(d);
-    t = a * fmaf(d, s, t);
-    s = a * s;
-    m = mn;
-}
-
-template <int N>
-__device__ __forceinline__ void unpack(const v4u (&v)[N], float (&z)[N * 8]) {
-#pragma unroll
-    for (int u = 0; u < N; ++u) {
-        z[8 * u + 0] = bf16_lo(v[u].x);
-        z[8 * u + 1] = bf16_hi(v[u].x);
-        z[8 * u + 2] = bf16_lo(v[u].y);
-        z[8 * u + 3] = bf16_hi(v[u].y);
-        z[8 * u + 4] = bf16_lo(v[u].z);
-        z[8 * u + 5] = bf16_hi(v[u].z);
-        z[8 * u + 6] = bf16_lo(v[u].w);
-        z[8 * u + 7] = bf16_hi(v[u].w);
+// Loads the row's gather id for thread `tid` (< n_ids) and its logit.
+__device__ __forceinline__ void load_id(const uint16_t* row, const int64_t* ids, int64_t r, int n_ids,
+                                        int64_t V, int64_t& y, float& zy) {
+    y = 0;
+    zy = 0.f;
+    const int tid = threadIdx.x;
+    if (ids && tid < n_ids) {
+        y = ids[r * n_ids + tid];
+        if (y >= 0 && y < V) zy = bf16_to_f32(row[y]);
     }
 }
 
-// Accumulates a full register tile (every element valid).
-template <int K>
-__device__ __forceinline__ void accumulate(const float (&z)[K], float& m, float& s, float& t) {
-    float tm = z[0];
-#pragma unroll
-    for (int i = 1; i < K; ++i) tm = fmaxf(tm, z[i]);
-    raise_max(m, s, t, tm);
-    const float nm = -m * kLog2e;
-    float s0 = 0.f, s1 = 0.f, t0 = 0.f, t1 = 0.f;
-#pragma unroll
-    for (int i = 0; i < K; i += 2) {
-        const float x0 = fmaf(z[i], kLog2e, nm);
-        const float x1 = fmaf(z[i + 1], kLog2e, nm);
-        const float e0 = fast_exp2(x0);
-        const float e1 = fast_exp2(x1);
-        s0 += e0;
-        s1 += e1;
-        t0 = fmaf(e0, x0, t0);
-        t1 = fmaf(e1, x1, t1);
-    }
-    s += s0 + s1;
-    t += t0 + t1;
-}
-
-// Accumulates one element that may be absent.
-__device__ __forceinline__ void accumulate_one(float z, bool ok, float& m, float& s, float& t) {
-    if (!ok) return;
-    raise_max(m, s, t, z);
-    const float x = (z - m) * kLog2e;
-    const float e = fast_exp2(x);
-    s += e;
-    t = fmaf(e, x, t);
-}
-
-// Block-wide merge of the per-lane triples; the result lands in thread 0.
+// Writes the row's outputs once block_merge has left (m, s, t) in thread 0.
 template <int NT>
-__device__ __forceinline__ void block_merge(float& m, float& s, float& t) {
-#pragma unroll
-    for (int off = kWave / 2; off > 0; off >>= 1) {
-        const float m2 = __shfl_xor(m, off, kWave);
-        const float s2 = __shfl_xor(s, off, kWave);
-        const float t2 = __shfl_xor(t, off, kWave);
-        merge(m, s, t, m2, s2, t2);
+__device__ __forceinline__ void finish_row(int64_t r, float m, float s, float t, int64_t y, float zy,
+                                           int64_t V, int n_ids, float* logp, float* ent, float* lse_out) {
+    __shared__ float s_lse;
+    if (threadIdx.x == 0) {
+        const float l2s = __log2f(s);
+        const float lse = fmaf(l2s, kLn2, m);
+        if (lse_out) lse_out[r] = lse;
+        if (ent) ent[r] = kLn2 * (l2s - t / s);
+        if (n_ids == 1 && logp) logp[r] = id_logp(y, zy, lse, V);
+        s_lse = lse;
     }
-    if constexpr (NT > kWave) {
-        constexpr int kWaves = NT / kWave;
-        __shared__ float sm[kWaves], ss[kWaves], st[kWaves];
-        const int lane = threadIdx.x % kWave;
-        const int wid = threadIdx.x / kWave;
-        if (lane == 0) {
-            sm[wid] = m;
-            ss[wid] = s;
-            st[wid] = t;
-        }
+    if (n_ids > 1 && logp) {
         __syncthreads();
-        if (threadIdx.x == 0) {
-#pragma unroll
-            for (int w = 1; w < kWaves; ++w) merge(m, s, t, sm[w], ss[w], st[w]);
-        }
-    }
-}
-
-__device__ __forceinline__ void write_row(int64_t r, float m, float s, float t, float zy, int64_t y,
-                                          int64_t V, bool has_label, float* logp, float* ent,
-                                          float* lse_out) {
-    const float l2s = __log2f(s);
-    const float lse = fmaf(l2s, kLn2, m);
-    if (lse_out) lse_out[r] = lse;
-    if (ent) ent[r] = kLn2 * (l2s - t / s);
-    if (logp) {
-        float v;
-        if (!has_label || y == kIgnoreIndex) v = 0.f;
-        else if (y < 0 || y >= V) v = __builtin_nanf("");
-        else v = zy - lse;
-        logp[r] = v;
+        if (threadIdx.x < n_ids) logp[r * n_ids + threadIdx.x] = id_logp(y, zy, s_lse, V);
     }
 }
 
@@ -152,22 +69,17 @@ __device__ __forceinline__ void write_row(int64_t r, float m, float s, float t, 
 template <int NT, int U>
 __global__ __launch_bounds__(NT) void k_lpe_fwd_vec(const uint16_t* __restrict__ logits, int64_t T,
                                                     int64_t V, int64_t stride_b, int64_t stride_t,
-                                                    const int64_t* __restrict__ labels,
+                                                    const int64_t* __restrict__ ids, int n_ids,
                                                     float* __restrict__ logp,
                                                     float* __restrict__ ent,
                                                     float* __restrict__ lse_out) {
     const int64_t r = blockIdx.x;
-    const int64_t b = r / T;
-    const uint16_t* row = logits + b * stride_b + (r - b * T) * stride_t;
+    const uint16_t* row = row_ptr(logits, r, T, stride_b, stride_t);
     const v4u* row4 = reinterpret_cast<const v4u*>(row);
     const int tid = threadIdx.x;
-
-    int64_t y = 0;
-    float zy = 0.f;
-    if (tid == 0 && labels) {
-        y = labels[r];
-        if (y >= 0 && y < V) zy = bf16_to_f32(row[y]);
-    }
+    int64_t y;
+    float zy;
+    load_id(row, ids, r, n_ids, V, y, zy);
 
     float m = kInit, s = 0.f, t = 0.f;
     const int64_t n8 = V >> 3;
@@ -197,27 +109,23 @@ __global__ __launch_bounds__(NT) void k_lpe_fwd_vec(const uint16_t* __restrict__
     }
 
     block_merge<NT>(m, s, t);
-    if (tid == 0) write_row(r, m, s, t, zy, y, V, labels != nullptr, logp, ent, lse_out);
+    finish_row<NT>(r, m, s, t, y, zy, V, n_ids, logp, ent, lse_out);
 }
 
 // Generic path: any alignment and stride, 2-byte coalesced loads.
 template <int NT>
 __global__ __launch_bounds__(NT) void k_lpe_fwd_any(const uint16_t* __restrict__ logits, int64_t T,
                                                     int64_t V, int64_t stride_b, int64_t stride_t,
-                                                    const int64_t* __restrict__ labels,
+                                                    const int64_t* __restrict__ ids, int n_ids,
                                                     float* __restrict__ logp,
                                                     float* __restrict__ ent,
                                                     float* __restrict__ lse_out) {
     const int64_t r = blockIdx.x;
-    const int64_t b = r / T;
-    const uint16_t* row = logits + b * stride_b + (r - b * T) * stride_t;
+    const uint16_t* row = row_ptr(logits, r, T, stride_b, stride_t);
     const int tid = threadIdx.x;
-    int64_t y = 0;
-    float zy = 0.f;
-    if (tid == 0 && labels) {
-        y = labels[r];
-        if (y >= 0 && y < V) zy = bf16_to_f32(row[y]);
-    }
+    int64_t y;
+    float zy;
+    load_id(row, ids, r, n_ids, V, y, zy);
     float m = kInit, s = 0.f, t = 0.f;
     int64_t e = tid;
     for (; e + 7 * NT < V; e += 8 * NT) {
@@ -228,133 +136,157 @@ __global__ __launch_bounds__(NT) void k_lpe_fwd_any(const uint16_t* __restrict__
     }
     for (; e < V; e += NT) accumulate_one(bf16_to_f32(row[e]), true, m, s, t);
     block_merge<NT>(m, s, t);
-    if (tid == 0) write_row(r, m, s, t, zy, y, V, labels != nullptr, logp, ent, lse_out);
+    finish_row<NT>(r, m, s, t, y, zy, V, n_ids, logp, ent, lse_out);
 }
 
-__device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-    const __hip_bfloat16 a = __float2bfloat16(lo);
-    const __hip_bfloat16 b = __float2bfloat16(hi);
-    return static_cast<uint32_t>(__bfloat16_as_ushort(a)) |
-           (static_cast<uint32_t>(__bfloat16_as_ushort(b)) << 16);
-}
+// ---------------------------------------------------------------- backward
 
-// Backward, vector path: 16-byte loads of z and 16-byte stores of the gradient.
-template <int NT, int U>
-__global__ __launch_bounds__(NT) void k_lp_bwd_vec(const uint16_t* __restrict__ logits, int64_t T,
-                                                   int64_t V, int64_t stride_b, int64_t stride_t,
-                                                   const int64_t* __restrict__ labels,
-                                                   const float* __restrict__ lse,
-                                                   const float* __restrict__ grad_logp,
-                                                   uint16_t* __restrict__ grad) {
-    const int64_t r = blockIdx.x;
-    const int64_t b = r / T;
-    const uint16_t* row = logits + b * stride_b + (r - b * T) * stride_t;
-    uint16_t* grow = grad + r * V;
-    const v4u* row4 = reinterpret_cast<const v4u*>(row);
-    v4u* grow4 = reinterpret_cast<v4u*>(grow);
-    const int tid = threadIdx.x;
-    const int64_t y = labels[r];
-    const int64_t n8 = V >> 3;
-
-    if (y == kIgnoreIndex || !(y >= 0 && y < V)) {
-        const uint16_t fill = (y == kIgnoreIndex) ? 0 : 0x7fc0;  // 0 or NaN
-        const uint32_t f2 = static_cast<uint32_t>(fill) * 0x10001u;
-        const v4u fv = v4u{f2, f2, f2, f2};
-        for (int64_t c = tid; c < n8; c += NT) grow4[c] = fv;
-        for (int64_t e = (n8 << 3) + tid; e < V; e += NT) grow[e] = fill;
-        return;
+// Per row: ng = -G (NaN when an id is neither -100 nor in [0, V)) and
+// nl = -lse * log2 e.
+__global__ __launch_bounds__(256) void k_lp_bwd_prep(const int64_t* __restrict__ ids, int n_ids,
+                                                     const float* __restrict__ lse,
+                                                     const float* __restrict__ grad, int64_t n_rows,
+                                                     int64_t V, float* __restrict__ ng,
+                                                     float* __restrict__ nl) {
+    const int64_t r = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (r >= n_rows) return;
+    float G = 0.f;
+    bool bad = false;
+    for (int k = 0; k < n_ids; ++k) {
+        const int64_t y = ids[r * n_ids + k];
+        if (y == kIgnoreIndex) continue;
+        if (y < 0 || y >= V) bad = true;
+        G += grad[r * n_ids + k];
     }
-    const float g = grad_logp[r];
-    const float ng = -g;
-    const float nl = -lse[r] * kLog2e;
-    constexpr int64_t kTile = static_cast<int64_t>(NT) * U;
-    const int64_t n_full = n8 / kTile;
-    for (int64_t it = 0; it < n_full; ++it) {
+    ng[r] = bad ? __builtin_nanf("") : -G;
+    nl[r] = -lse[r] * kLog2e;
+}
+
+__device__ __forceinline__ v4u softmax_term8(v4u v, float ng, float nl) {
+    float z[8];
+    const v4u vv[1] = {v};
+    unpack(vv, z);
+    float q[8];
+#pragma unroll
+    for (int k = 0; k < 8; ++k) q[k] = ng * fast_exp2(fmaf(z[k], kLog2e, nl));
+    v4u o;
+    o.x = pack_bf16x2(q[0], q[1]);
+    o.y = pack_bf16x2(q[2], q[3]);
+    o.z = pack_bf16x2(q[4], q[5]);
+    o.w = pack_bf16x2(q[6], q[7]);
+    return o;
+}
+
+// Row index of 16-byte chunk c of a contiguous [rows, V] grid (n8 chunks per
+// row): a double-precision estimate corrected by one step.
+__device__ __forceinline__ uint32_t row_of_chunk(uint32_t c, uint32_t n8, double inv_n8) {
+    uint32_t r = static_cast<uint32_t>(static_cast<double>(c) * inv_n8);
+    if (r * n8 > c) --r;
+    else if ((r + 1) * n8 <= c) ++r;
+    return r;
+}
+
+// Streaming pass over contiguous logits [rows, V], V % 8 == 0: grid-stride
+// over the n_chunks 16-byte chunks, U loads in flight per thread.
+template <int NT, int U>
+__global__ __launch_bounds__(NT) void k_lp_bwd_flat(const v4u* __restrict__ z4, uint32_t n8,
+                                                    uint32_t n_chunks, double inv_n8,
+                                                    const float* __restrict__ ng,
+                                                    const float* __restrict__ nl,
+                                                    v4u* __restrict__ g4) {
+    uint32_t i = blockIdx.x * (NT * U) + threadIdx.x;
+    const uint32_t stride = gridDim.x * (NT * U);
+    for (; i + (U - 1) * NT < n_chunks; i += stride) {
         v4u v[U];
 #pragma unroll
-        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(row4 + it * kTile + u * NT + tid);
-        float z[U * 8];
-        unpack(v, z);
+        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(z4 + i + u * NT);
 #pragma unroll
         for (int u = 0; u < U; ++u) {
-            const int64_t c = it * kTile + u * NT + tid;
-            float q[8];
-#pragma unroll
-            for (int k = 0; k < 8; ++k) q[k] = ng * fast_exp2(fmaf(z[8 * u + k], kLog2e, nl));
-            const uint64_t off = static_cast<uint64_t>(y - (c << 3));
-            if (off < 8) {
-#pragma unroll
-                for (int k = 0; k < 8; ++k)
-                    if (static_cast<uint64_t>(k) == off) q[k] += g;
-            }
-            v4u o;
-            o.x = pack_bf16x2(q[0], q[1]);
-            o.y = pack_bf16x2(q[2], q[3]);
-            o.z = pack_bf16x2(q[4], q[5]);
-            o.w = pack_bf16x2(q[6], q[7]);
-            __builtin_nontemporal_store(o, grow4 + c);
+            const uint32_t c = i + u * NT;
+            const uint32_t r = row_of_chunk(c, n8, inv_n8);
+            __builtin_nontemporal_store(softmax_term8(v[u], ng[r], nl[r]), g4 + c);
         }
     }
-    for (int64_t c = n_full * kTile + tid; c < n8; c += NT) {
-        v4u v1[1] = {__builtin_nontemporal_load(row4 + c)};
-        float z[8];
-        unpack(v1, z);
-        float q[8];
-#pragma unroll
-        for (int k = 0; k < 8; ++k) q[k] = ng * fast_exp2(fmaf(z[k], kLog2e, nl));
-        const uint64_t off = static_cast<uint64_t>(y - (c << 3));
-        if (off < 8) {
-#pragma unroll
-            for (int k = 0; k < 8; ++k)
-                if (static_cast<uint64_t>(k) == off) q[k] += g;
-        }
-        v4u o;
-        o.x = pack_bf16x2(q[0], q[1]);
-        o.y = pack_bf16x2(q[2], q[3]);
-        o.z = pack_bf16x2(q[4], q[5]);
-        o.w = pack_bf16x2(q[6], q[7]);
-        __builtin_nontemporal_store(o, grow4 + c);
-    }
-    for (int64_t e = (n8 << 3) + tid; e < V; e += NT) {
-        float q = ng * fast_exp2(fmaf(bf16_to_f32(row[e]), kLog2e, nl));
-        if (e == y) q += g;
-        grow[e] = __bfloat16_as_ushort(__float2bfloat16(q));
+    for (; i < n_chunks; i += NT) {
+        const uint32_t r = row_of_chunk(i, n8, inv_n8);
+        __builtin_nontemporal_store(softmax_term8(__builtin_nontemporal_load(z4 + i), ng[r], nl[r]), g4 + i);
     }
 }
 
-// Backward, generic path.
+// Streaming pass, one workgroup per row: strided logits with 16-byte aligned
+// rows and V % 8 == 0.
+template <int NT, int U>
+__global__ __launch_bounds__(NT) void k_lp_bwd_rows(const uint16_t* __restrict__ logits, int64_t T,
+                                                    int64_t V, int64_t stride_b, int64_t stride_t,
+                                                    const float* __restrict__ ng,
+                                                    const float* __restrict__ nl,
+                                                    uint16_t* __restrict__ grad) {
+    const int64_t r = blockIdx.x;
+    const v4u* row4 = reinterpret_cast<const v4u*>(row_ptr(logits, r, T, stride_b, stride_t));
+    v4u* grow4 = reinterpret_cast<v4u*>(grad + r * V);
+    const float g = ng[r], l = nl[r];
+    const int64_t n8 = V >> 3;
+    int64_t c = threadIdx.x;
+    for (; c + (U - 1) * NT < n8; c += NT * U) {
+        v4u v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(row4 + c + u * NT);
+#pragma unroll
+        for (int u = 0; u < U; ++u) __builtin_nontemporal_store(softmax_term8(v[u], g, l), grow4 + c + u * NT);
+    }
+    for (; c < n8; c += NT) __builtin_nontemporal_store(softmax_term8(__builtin_nontemporal_load(row4 + c), g, l), grow4 + c);
+}
+
+// Streaming pass, generic: any alignment, stride and V.
 template <int NT>
 __global__ __launch_bounds__(NT) void k_lp_bwd_any(const uint16_t* __restrict__ logits, int64_t T,
                                                    int64_t V, int64_t stride_b, int64_t stride_t,
-                                                   const int64_t* __restrict__ labels,
-                                                   const float* __restrict__ lse,
-                                                   const float* __restrict__ grad_logp,
+                                                   const float* __restrict__ ng,
+                                                   const float* __restrict__ nl,
                                                    uint16_t* __restrict__ grad) {
     const int64_t r = blockIdx.x;
-    const int64_t b = r / T;
-    const uint16_t* row = logits + b * stride_b + (r - b * T) * stride_t;
+    const uint16_t* row = row_ptr(logits, r, T, stride_b, stride_t);
     uint16_t* grow = grad + r * V;
-    const int64_t y = labels[r];
-    if (y == kIgnoreIndex || !(y >= 0 && y < V)) {
-        const uint16_t fill = (y == kIgnoreIndex) ? 0 : 0x7fc0;
-        for (int64_t e = threadIdx.x; e < V; e += NT) grow[e] = fill;
-        return;
-    }
-    const float g = grad_logp[r];
-    const float nl = -lse[r] * kLog2e;
-    for (int64_t e = threadIdx.x; e < V; e += NT) {
-        float q = -g * fast_exp2(fmaf(bf16_to_f32(row[e]), kLog2e, nl));
-        if (e == y) q += g;
-        grow[e] = __bfloat16_as_ushort(__float2bfloat16(q));
-    }
+    const float g = ng[r], l = nl[r];
+    for (int64_t e = threadIdx.x; e < V; e += NT)
+        grow[e] = __bfloat16_as_ushort(__float2bfloat16(g * fast_exp2(fmaf(bf16_to_f32(row[e]), kLog2e, l))));
 }
 
-// 256 threads x 8 16-byte loads in flight per tile: the fastest shape of a
-// sweep over {64..1024} threads x {2, 4, 8} loads on MI355X.
+// One thread per (row, id): the final value at the id's position, i.e. the
+// softmax term recomputed exactly as the streaming pass computed it, plus the
+// gradients of every id of the row equal to this one.  Threads of duplicate
+// ids store the same value.
+__global__ __launch_bounds__(256) void k_lp_bwd_fix(const uint16_t* __restrict__ logits, int64_t T, int64_t V,
+                                                    int64_t stride_b, int64_t stride_t,
+                                                    const int64_t* __restrict__ ids, int n_ids,
+                                                    const float* __restrict__ grad,
+                                                    const float* __restrict__ ng,
+                                                    const float* __restrict__ nl, int64_t n_rows,
+                                                    uint16_t* __restrict__ out) {
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * 256 + threadIdx.x;
+    if (j >= n_rows * n_ids) return;
+    const int64_t r = j / n_ids;
+    const int64_t y = ids[j];
+    if (y < 0 || y >= V) return;  // ignored id, or a NaN row already written
+    const float g = ng[r];
+    if (isnan(g)) return;
+    const uint16_t* row = row_ptr(logits, r, T, stride_b, stride_t);
+    float q = g * fast_exp2(fmaf(bf16_to_f32(row[y]), kLog2e, nl[r]));
+    for (int k = 0; k < n_ids; ++k)
+        if (ids[r * n_ids + k] == y) q += grad[r * n_ids + k];
+    out[r * V + y] = __bfloat16_as_ushort(__float2bfloat16(q));
+}
+
+// 256 threads x 8 16-byte loads in flight per tile: the fastest forward shape
+// of a sweep over {64..1024} threads x {2, 4, 8} loads on MI355X.  The flat
+// backward: 256 threads x 4 loads, 65536 workgroups (sweep over 16384..65536
+// workgroups, 2..8 loads).
 constexpr int kFwdThreads = 256;
 constexpr int kFwdUnroll = 8;
 constexpr int kBwdThreads = 256;
-constexpr int kBwdUnroll = 2;
+constexpr int kBwdUnroll = 4;
+constexpr uint32_t kBwdFlatBlocks = 65536;
+constexpr int kMaxIds = 256;  // gather ids per row (one thread each)
 
 int check_common(const void* logits, int64_t rows, int64_t T, int64_t V, int64_t stride_b,
                  int64_t stride_t, const char* who) {
@@ -372,6 +304,66 @@ bool vector_ok(const void* logits, int64_t stride_b, int64_t stride_t) {
     return (reinterpret_cast<uintptr_t>(logits) % 16 == 0) && (stride_b % 8 == 0) && (stride_t % 8 == 0);
 }
 
+int launch_fwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V, int64_t stride_b,
+               int64_t stride_t, const int64_t* ids, int n_ids, float* out, float* entropy, float* lse,
+               hipStream_t stream, const char* who) {
+    const int64_t n = rows * T;
+    if (n == 0) return MESHY_OK;
+    const dim3 grid(static_cast<unsigned>(n));
+    if (vector_ok(logits, stride_b, stride_t)) {
+        hipLaunchKernelGGL((k_lpe_fwd_vec<kFwdThreads, kFwdUnroll>), grid, dim3(kFwdThreads), 0, stream,
+                           logits, T, V, stride_b, stride_t, ids, n_ids, out, entropy, lse);
+    } else {
+        hipLaunchKernelGGL((k_lpe_fwd_any<kFwdThreads>), grid, dim3(kFwdThreads), 0, stream, logits, T,
+                           V, stride_b, stride_t, ids, n_ids, out, entropy, lse);
+    }
+    return check_launch(who);
+}
+
+size_t bwd_ws_bytes(int64_t n_rows) { return 2 * align_up(sizeof(float) * static_cast<size_t>(n_rows), 256); }
+
+int launch_bwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V, int64_t stride_b,
+               int64_t stride_t, const int64_t* ids, int n_ids, const float* lse, const float* grad_out,
+               uint16_t* grad_logits, void* workspace, size_t workspace_bytes, hipStream_t stream,
+               const char* who) {
+    const int64_t n = rows * T;
+    if (n == 0) return MESHY_OK;
+    if (!workspace || workspace_bytes < bwd_ws_bytes(n))
+        return set_error(MESHY_ESPACE, "%s: workspace needs %zu bytes", who, bwd_ws_bytes(n));
+    float* ng = static_cast<float*>(workspace);
+    float* nl = reinterpret_cast<float*>(static_cast<char*>(workspace) + bwd_ws_bytes(n) / 2);
+    const unsigned row_blocks = static_cast<unsigned>(ceil_div(n, 256));
+    hipLaunchKernelGGL(k_lp_bwd_prep, dim3(row_blocks), dim3(256), 0, stream, ids, n_ids, lse, grad_out, n, V, ng,
+                       nl);
+    int rc = check_launch(who);
+    if (rc) return rc;
+    const bool vec = vector_ok(logits, stride_b, stride_t) && reinterpret_cast<uintptr_t>(grad_logits) % 16 == 0 &&
+                     V % 8 == 0;
+    const bool contiguous = stride_t == V && (rows == 1 || stride_b == T * V);
+    const int64_t n_chunks = n * (V / 8);
+    // The grid-stride index stays below 2^32: n_chunks plus one grid stride.
+    if (vec && contiguous && n_chunks <= (int64_t{1} << 32) - (int64_t{1} << 28)) {
+        const int64_t need = ceil_div(n_chunks, kBwdThreads * kBwdUnroll);
+        const unsigned blocks = static_cast<unsigned>(std::min<int64_t>(need, kBwdFlatBlocks));
+        hipLaunchKernelGGL((k_lp_bwd_flat<kBwdThreads, kBwdUnroll>), dim3(blocks), dim3(kBwdThreads), 0, stream,
+                           reinterpret_cast<const v4u*>(logits), static_cast<uint32_t>(V / 8),
+                           static_cast<uint32_t>(n_chunks), 1.0 / static_cast<double>(V / 8), ng, nl,
+                           reinterpret_cast<v4u*>(grad_logits));
+    } else if (vec) {
+        hipLaunchKernelGGL((k_lp_bwd_rows<kBwdThreads, kBwdUnroll>), dim3(static_cast<unsigned>(n)),
+                           dim3(kBwdThreads), 0, stream, logits, T, V, stride_b, stride_t, ng, nl, grad_logits);
+    } else {
+        hipLaunchKernelGGL((k_lp_bwd_any<kBwdThreads>), dim3(static_cast<unsigned>(n)), dim3(kBwdThreads), 0,
+                           stream, logits, T, V, stride_b, stride_t, ng, nl, grad_logits);
+    }
+    rc = check_launch(who);
+    if (rc) return rc;
+    const unsigned fix_blocks = static_cast<unsigned>(ceil_div(n * n_ids, 256));
+    hipLaunchKernelGGL(k_lp_bwd_fix, dim3(fix_blocks), dim3(256), 0, stream, logits, T, V, stride_b, stride_t, ids,
+                       n_ids, grad_out, ng, nl, n, grad_logits);
+    return check_launch(who);
+}
+
 }  // namespace
 }  // namespace meshy
 
@@ -381,20 +373,66 @@ extern "C" int meshy_logprob_entropy_fwd(const uint16_t* logits, int64_t rows, i
                                          hipStream_t stream) {
     using namespace meshy;
     clear_error();
-    int rc = check_common(logits, rows, T, V, stride_b, stride_t, "meshy_logprob_entropy_fwd");
+    const char* who = "meshy_logprob_entropy_fwd";
+    int rc = check_common(logits, rows, T, V, stride_b, stride_t, who);
     if (rc) return rc;
-    if (logp && !labels) return set_error(MESHY_ENULL, "meshy_logprob_entropy_fwd: logp needs labels");
-    const int64_t n = rows * T;
-    if (n == 0) return MESHY_OK;
-    const dim3 grid(static_cast<unsigned>(n));
-    if (vector_ok(logits, stride_b, stride_t)) {
-        hipLaunchKernelGGL((k_lpe_fwd_vec<kFwdThreads, kFwdUnroll>), grid, dim3(kFwdThreads), 0, stream,
-                           logits, T, V, stride_b, stride_t, labels, logp, entropy, lse);
-    } else {
-        hipLaunchKernelGGL((k_lpe_fwd_any<kFwdThreads>), grid, dim3(kFwdThreads), 0, stream, logits, T,
-                           V, stride_b, stride_t, labels, logp, entropy, lse);
-    }
-    return check_launch("meshy_logprob_entropy_fwd");
+    if (logp && !labels) return set_error(MESHY_ENULL, "%s: logp needs labels", who);
+    return launch_fwd(logits, rows, T, V, stride_b, stride_t, logp ? labels : nullptr, logp ? 1 : 0, logp,
+                      entropy, lse, stream, who);
+}
+
+extern "C" int meshy_gather_logprobs_fwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
+                                         int64_t stride_b, int64_t stride_t, const int64_t* ids,
+                                         int64_t n_ids, float* out, float* lse, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    const char* who = "meshy_gather_logprobs_fwd";
+    int rc = check_common(logits, rows, T, V, stride_b, stride_t, who);
+    if (rc) return rc;
+    if (n_ids < 1 || n_ids > kMaxIds)
+        return set_error(MESHY_EINVAL, "%s: n_ids must be in [1, %d], got %lld", who, kMaxIds,
+                         static_cast<long long>(n_ids));
+    if (!ids || !out) return set_error(MESHY_ENULL, "%s: ids and out are required", who);
+    return launch_fwd(logits, rows, T, V, stride_b, stride_t, ids, static_cast<int>(n_ids), out, nullptr, lse,
+                      stream, who);
+}
+
+extern "C" size_t meshy_logprob_bwd_workspace_size(int64_t n_rows) {
+    return n_rows < 0 ? 0 : meshy::bwd_ws_bytes(n_rows);
+}
+
+extern "C" int meshy_logprob_bwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
+                                 int64_t stride_b, int64_t stride_t, const int64_t* labels,
+                                 const float* lse, const float* grad_logp, uint16_t* grad_logits,
+                                 void* workspace, size_t workspace_bytes, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    const char* who = "meshy_logprob_bwd";
+    int rc = check_common(logits, rows, T, V, stride_b, stride_t, who);
+    if (rc) return rc;
+    if (!labels || !lse || !grad_logp || !grad_logits)
+        return set_error(MESHY_ENULL, "%s: labels, lse, grad_logp and grad_logits are required", who);
+    return launch_bwd(logits, rows, T, V, stride_b, stride_t, labels, 1, lse, grad_logp, grad_logits, workspace,
+                      workspace_bytes, stream, who);
+}
+
+extern "C" int meshy_gather_logprobs_bwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
+                                         int64_t stride_b, int64_t stride_t, const int64_t* ids,
+                                         int64_t n_ids, const float* lse, const float* grad_out,
+                                         uint16_t* grad_logits, void* workspace, size_t workspace_bytes,
+                                         hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    const char* who = "meshy_gather_logprobs_bwd";
+    int rc = check_common(logits, rows, T, V, stride_b, stride_t, who);
+    if (rc) return rc;
+    if (n_ids < 1 || n_ids > kMaxIds)
+        return set_error(MESHY_EINVAL, "%s: n_ids must be in [1, %d], got %lld", who, kMaxIds,
+                         static_cast<long long>(n_ids));
+    if (!ids || !lse || !grad_out || !grad_logits)
+        return set_error(MESHY_ENULL, "%s: ids, lse, grad_out and grad_logits are required", who);
+    return launch_bwd(logits, rows, T, V, stride_b, stride_t, ids, static_cast<int>(n_ids), lse, grad_out,
+                      grad_logits, workspace, workspace_bytes, stream, who);
 }
 
 namespace meshy {
@@ -438,28 +476,4 @@ extern "C" int meshy_stream_read(const void* src, int64_t rows, int64_t row_byte
     hipLaunchKernelGGL((k_stream_read<256, 8>), dim3(static_cast<unsigned>(rows)), dim3(256), 0, stream,
                        static_cast<const v4u*>(src), row_bytes / 16, out);
     return check_launch("meshy_stream_read");
-}
-
-extern "C" int meshy_logprob_bwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
-                                 int64_t stride_b, int64_t stride_t, const int64_t* labels,
-                                 const float* lse, const float* grad_logp, uint16_t* grad_logits,
-                                 hipStream_t stream) {
-    using namespace meshy;
-    clear_error();
-    int rc = check_common(logits, rows, T, V, stride_b, stride_t, "meshy_logprob_bwd");
-    if (rc) return rc;
-    if (!labels || !lse || !grad_logp || !grad_logits)
-        return set_error(MESHY_ENULL, "meshy_logprob_bwd: labels, lse, grad_logp and grad_logits are required");
-    const int64_t n = rows * T;
-    if (n == 0) return MESHY_OK;
-    const dim3 grid(static_cast<unsigned>(n));
-    if (vector_ok(logits, stride_b, stride_t) && reinterpret_cast<uintptr_t>(grad_logits) % 16 == 0 &&
-        V % 8 == 0) {
-        hipLaunchKernelGGL((k_lp_bwd_vec<kBwdThreads, kBwdUnroll>), grid, dim3(kBwdThreads), 0, stream,
-                           logits, T, V, stride_b, stride_t, labels, lse, grad_logp, grad_logits);
-    } else {
-        hipLaunchKernelGGL((k_lp_bwd_any<kBwdThreads>), grid, dim3(kBwdThreads), 0, stream, logits, T, V,
-                           stride_b, stride_t, labels, lse, grad_logp, grad_logits);
-    }
-    return check_launch("meshy_logprob_bwd");
 }

@@ -139,10 +139,11 @@ __global__ __launch_bounds__(kFillThreads) void k_pack_fill(meshy_pack_args a) {
         int64_t in_id = 0, lab = 0;
         float mk = 0.f, lp = 0.f, adv = 0.f;
         const bool real = d < nd && p < a.doc_len[d0 + d];
+        int64_t src = -1;
         if (real) {
             const int32_t smp = a.doc_sample[d0 + d];
             const int64_t L = a.doc_len[d0 + d];
-            const int64_t src = a.sample_offsets[smp] + p;
+            src = a.sample_offsets[smp] + p;
             in_id = static_cast<int64_t>(tokens[src]);
             if (p + 1 < L) {
                 lab = static_cast<int64_t>(tokens[src + 1]);
@@ -161,6 +162,16 @@ __global__ __launch_bounds__(kFillThreads) void k_pack_fill(meshy_pack_args a) {
         // single row is padding slot 0 (batch.py:123, 137-139).
         a.doc_ids[o] = packed ? static_cast<int64_t>(d) : (nd == 0 ? 0 : static_cast<int64_t>(d));
         a.positions[o] = static_cast<int32_t>(p);
+        if (a.teacher_k > 0) {
+            // Teacher rows are indexed by logits position: no shift (opd.py:58-89).
+            const int64_t K = a.teacher_k;
+            int64_t* ids_o = a.teacher_ids_out + o * K;
+            float* lps_o = a.teacher_lps_out + o * K;
+            for (int64_t j = 0; j < K; ++j) {
+                ids_o[j] = src >= 0 ? static_cast<int64_t>(a.teacher_ids[src * K + j]) : 0;
+                lps_o[j] = src >= 0 ? a.teacher_lps[src * K + j] : 0.f;
+            }
+        }
     }
 }
 
@@ -221,6 +232,10 @@ extern "C" int meshy_pack_micro_batches(const meshy_pack_args* args, hipStream_t
         return set_error(MESHY_EINVAL, "meshy_pack_micro_batches: bad max_micro_elems %lld",
                          static_cast<long long>(a.max_micro_elems));
     if (a.n_micro > 65535) return set_error(MESHY_EINVAL, "meshy_pack_micro_batches: too many micros");
+    if (a.teacher_k < 0) return set_error(MESHY_EINVAL, "meshy_pack_micro_batches: negative teacher_k");
+    if (a.teacher_k > 0 && (!a.teacher_ids_out || !a.teacher_lps_out ||
+                            (a.max_docs_per_micro > 0 && (!a.teacher_ids || !a.teacher_lps))))
+        return set_error(MESHY_ENULL, "meshy_pack_micro_batches: teacher columns need inputs and outputs");
 
     // max_docs_per_micro must bound every micro's document count: micros with
     // more than kLdsDocs documents read the table this launch writes.

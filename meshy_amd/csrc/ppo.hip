@@ -80,17 +80,6 @@ __device__ __forceinline__ float nan_to_num(float x) {
     return x;
 }
 
-// Largest d in [0, n_slots] with off[d] <= i (off has n_slots + 1 entries).
-__device__ __forceinline__ int64_t doc_of(const int64_t* off, int64_t n_slots, int64_t i) {
-    int64_t lo = 0, hi = n_slots;
-    while (lo < hi) {
-        const int64_t mid = (lo + hi + 1) >> 1;
-        if (off[mid] <= i) lo = mid;
-        else hi = mid - 1;
-    }
-    return lo;
-}
-
 // Per-token forward terms and every per-token sum contribution.
 struct Contrib {
     float seg[kSegSums];

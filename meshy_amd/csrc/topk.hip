@@ -1,0 +1,248 @@
+// Teacher Top-K of bf16 logits with their log-probabilities, for gfx950.
+//
+// Replaces teacher_topk (meshy/backend/titan/topk_loss.py:20-32): per row,
+// the K largest logits (indices and values - logsumexp) of the fp32-upcast
+// logits, sorted by value, in one streaming pass over the row instead of an
+// fp32 copy, a topk and a logsumexp per chunk.
+//
+// One workgroup per row.  Every lane streams its 16-byte register tiles once
+// and updates the online log-sum-exp (rowstream.h).  Each wavefront also keeps
+// a running sorted list of its best entries spread over its 64 lanes (lane j
+// holds rank j).  The rank K-1 value is the wavefront's threshold: a tile whose
+// lane maxima all fall below it costs one compare, otherwise every element at
+// or above the threshold is offered to the list one at a time (a ballot, then
+// a shift of the lanes below the insertion point).  After a few tiles the
+// threshold sits near the row's top values and offers are rare.  The waves'
+// lists are then merged by wave 0.
+//
+// Order: larger value first, equal values by smaller index (a stable sort of
+// the row in descending order).  NaN logits are never selected.  Every list
+// update runs with all 64 lanes active: loops are wave-uniform and absent
+// elements carry NaN.
+#include <algorithm>
+
+#include "rowstream.h"
+
+namespace meshy {
+namespace {
+
+constexpr int kTopkThreads = 256;
+constexpr int kTopkWaves = kTopkThreads / kWave;
+constexpr int kTopkUnroll = 4;
+constexpr int kMaxTopK = kWave;
+constexpr int32_t kNoIndex = INT32_MAX;
+
+// (a, ia) ranks before (b, ib).
+__device__ __forceinline__ bool ranks_before(float a, int32_t ia, float b, int32_t ib) {
+    return a > b || (a == b && ia < ib);
+}
+
+__device__ __forceinline__ float read_lane(float x, int l) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(x), l));
+}
+__device__ __forceinline__ int32_t read_lane(int32_t x, int l) { return __builtin_amdgcn_readlane(x, l); }
+
+// A wavefront's sorted list; (tv, ti) is the entry of rank K-1 (the threshold).
+struct WaveTop {
+    float v = -__builtin_inff();
+    int32_t i = kNoIndex;
+    float tv = -__builtin_inff();
+    int32_t ti = kNoIndex;
+};
+
+// Inserts the wave-uniform candidate (cv, ci); the entries ranked before it
+// form a prefix of the lanes.
+__device__ __forceinline__ void top_insert(WaveTop& w, float cv, int32_t ci, int k) {
+    const int lane = threadIdx.x % kWave;
+    const int pos = __popcll(__ballot(ranks_before(w.v, w.i, cv, ci)));
+    const float uv = __shfl_up(w.v, 1, kWave);
+    const int32_t ui = __shfl_up(w.i, 1, kWave);
+    if (lane == pos) {
+        w.v = cv;
+        w.i = ci;
+    } else if (lane > pos) {
+        w.v = uv;
+        w.i = ui;
+    }
+    w.tv = read_lane(w.v, k - 1);
+    w.ti = read_lane(w.i, k - 1);
+}
+
+// Offers one element per lane (z, NaN when absent); col(l) is lane l's column.
+template <class ColF>
+__device__ __forceinline__ void top_offer(WaveTop& w, float z, int k, ColF col) {
+    uint64_t b = __ballot(z >= w.tv);
+    while (b) {
+        const int l = __builtin_ctzll(b);
+        b &= b - 1;
+        const float cv = read_lane(z, l);
+        const int32_t ci = col(l);
+        if (ranks_before(cv, ci, w.tv, w.ti)) top_insert(w, cv, ci, k);
+    }
+}
+
+// Merges the waves' lists into wave 0's (call from every thread).
+__device__ __forceinline__ void merge_waves(WaveTop& w, int k) {
+    __shared__ float s_v[kTopkWaves][kMaxTopK];
+    __shared__ int32_t s_i[kTopkWaves][kMaxTopK];
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+    if (lane < k) {
+        s_v[wid][lane] = w.v;
+        s_i[wid][lane] = w.i;
+    }
+    __syncthreads();
+    if (wid == 0) {
+        for (int ww = 1; ww < kTopkWaves; ++ww) {
+            for (int j = 0; j < k; ++j) {
+                const float cv = s_v[ww][j];
+                const int32_t ci = s_i[ww][j];
+                // Each list is sorted: once an entry misses, the rest miss too.
+                if (!ranks_before(cv, ci, w.tv, w.ti)) break;
+                top_insert(w, cv, ci, k);
+            }
+        }
+    }
+}
+
+// Writes wave 0's list with lse = m + ln s (thread 0 holds the merged m, s).
+__device__ __forceinline__ void write_top(const WaveTop& w, float m, float s, int64_t r, int k,
+                                          int64_t* __restrict__ ids, float* __restrict__ lps,
+                                          float* __restrict__ lse_out) {
+    if (threadIdx.x >= kWave) return;
+    const float lse0 = fmaf(__log2f(s), kLn2, m);
+    const float lse = read_lane(lse0, 0);
+    const int lane = threadIdx.x;
+    if (lane == 0 && lse_out) lse_out[r] = lse;
+    if (lane < k) {
+        ids[r * k + lane] = w.i;
+        lps[r * k + lane] = w.v - lse;
+    }
+}
+
+template <int NT, int U>
+__global__ __launch_bounds__(NT) void k_topk_vec(const uint16_t* __restrict__ logits, int64_t T, int64_t V,
+                                                 int64_t stride_b, int64_t stride_t, int k,
+                                                 int64_t* __restrict__ ids, float* __restrict__ lps,
+                                                 float* __restrict__ lse_out) {
+    const int64_t r = blockIdx.x;
+    const uint16_t* row = row_ptr(logits, r, T, stride_b, stride_t);
+    const v4u* row4 = reinterpret_cast<const v4u*>(row);
+    const int tid = threadIdx.x;
+    const int wave0 = __builtin_amdgcn_readfirstlane(tid - tid % kWave);  // first thread of this wavefront
+    float m = kInit, s = 0.f, t = 0.f;
+    WaveTop w;
+    const int64_t n8 = V >> 3;
+    constexpr int64_t kTile = static_cast<int64_t>(NT) * U;
+    const int64_t n_full = n8 / kTile;
+    for (int64_t it = 0; it < n_full; ++it) {
+        const int64_t c0 = it * kTile;
+        v4u v[U];
+#pragma unroll
+        for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(row4 + c0 + u * NT + tid);
+        float z[U * 8];
+        unpack(v, z);
+        const float tm = tile_max(z);
+        accumulate<false>(z, tm, m, s, t);
+        if (__ballot(tm >= w.tv)) {
+#pragma unroll
+            for (int j = 0; j < U * 8; ++j) {
+                top_offer(w, z[j], k, [&](int l) {
+                    return static_cast<int32_t>(8 * (c0 + (j / 8) * NT + wave0 + l) + (j % 8));
+                });
+            }
+        }
+    }
+    // Remaining 16-byte chunks: wave-uniform loop, absent chunks are NaN.
+    for (int64_t c0 = n_full * kTile; c0 < n8; c0 += NT) {
+        const int64_t c = c0 + tid;
+        const bool ok = c < n8;
+        float z[8];
+        if (ok) {
+            v4u v1[1] = {__builtin_nontemporal_load(row4 + c)};
+            unpack(v1, z);
+            accumulate<false>(z, m, s, t);
+        } else {
+#pragma unroll
+            for (int j = 0; j < 8; ++j) z[j] = __builtin_nanf("");
+        }
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+            top_offer(w, z[j], k, [&](int l) { return static_cast<int32_t>(8 * (c0 + wave0 + l) + j); });
+        }
+    }
+    // Tail elements when V is not a multiple of 8 (fewer than 8 < NT).
+    if (V & 7) {
+        const int64_t e = (n8 << 3) + tid;
+        const bool ok = e < V;
+        const float z = ok ? bf16_to_f32(row[e]) : __builtin_nanf("");
+        accumulate_one(z, ok, m, s, t);
+        top_offer(w, z, k, [&](int l) { return static_cast<int32_t>((n8 << 3) + wave0 + l); });
+    }
+    merge_waves(w, k);
+    block_merge<NT>(m, s, t);
+    write_top(w, m, s, r, k, ids, lps, lse_out);
+}
+
+// Generic path: any alignment and stride, 2-byte loads, 8 per thread per step.
+template <int NT>
+__global__ __launch_bounds__(NT) void k_topk_any(const uint16_t* __restrict__ logits, int64_t T, int64_t V,
+                                                 int64_t stride_b, int64_t stride_t, int k,
+                                                 int64_t* __restrict__ ids, float* __restrict__ lps,
+                                                 float* __restrict__ lse_out) {
+    const int64_t r = blockIdx.x;
+    const uint16_t* row = row_ptr(logits, r, T, stride_b, stride_t);
+    const int tid = threadIdx.x;
+    const int wave0 = __builtin_amdgcn_readfirstlane(tid - tid % kWave);
+    float m = kInit, s = 0.f, t = 0.f;
+    WaveTop w;
+    for (int64_t e0 = 0; e0 < V; e0 += 8 * NT) {
+        float z[8];
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            const int64_t e = e0 + u * NT + tid;
+            const bool ok = e < V;
+            z[u] = ok ? bf16_to_f32(row[e]) : __builtin_nanf("");
+            accumulate_one(z[u], ok, m, s, t);
+        }
+#pragma unroll
+        for (int u = 0; u < 8; ++u) {
+            top_offer(w, z[u], k, [&](int l) { return static_cast<int32_t>(e0 + u * NT + wave0 + l); });
+        }
+    }
+    merge_waves(w, k);
+    block_merge<NT>(m, s, t);
+    write_top(w, m, s, r, k, ids, lps, lse_out);
+}
+
+}  // namespace
+}  // namespace meshy
+
+extern "C" int meshy_topk_logprobs(const uint16_t* logits, int64_t rows, int64_t T, int64_t V, int64_t stride_b,
+                                   int64_t stride_t, int64_t k, int64_t* ids, float* logprobs, float* lse,
+                                   hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    const char* who = "meshy_topk_logprobs";
+    if (!logits || !ids || !logprobs) return set_error(MESHY_ENULL, "%s: logits, ids and logprobs are required", who);
+    if (rows < 0 || T < 0 || V <= 0 || stride_b < 0 || stride_t < 0)
+        return set_error(MESHY_EINVAL, "%s: bad shape rows=%lld T=%lld V=%lld", who, static_cast<long long>(rows),
+                         static_cast<long long>(T), static_cast<long long>(V));
+    if (V > INT32_MAX) return set_error(MESHY_EINVAL, "%s: V must fit in int32", who);
+    if (k < 1 || k > kMaxTopK || k > V)
+        return set_error(MESHY_EINVAL, "%s: k must be in [1, min(%d, V)], got %lld", who, kMaxTopK,
+                         static_cast<long long>(k));
+    if (rows * T > INT32_MAX) return set_error(MESHY_EINVAL, "%s: too many rows", who);
+    const int64_t n = rows * T;
+    if (n == 0) return MESHY_OK;
+    const dim3 grid(static_cast<unsigned>(n));
+    const bool vec = reinterpret_cast<uintptr_t>(logits) % 16 == 0 && stride_b % 8 == 0 && stride_t % 8 == 0;
+    if (vec) {
+        hipLaunchKernelGGL((k_topk_vec<kTopkThreads, kTopkUnroll>), grid, dim3(kTopkThreads), 0, stream, logits, T,
+                           V, stride_b, stride_t, static_cast<int>(k), ids, logprobs, lse);
+    } else {
+        hipLaunchKernelGGL((k_topk_any<kTopkThreads>), grid, dim3(kTopkThreads), 0, stream, logits, T, V, stride_b,
+                           stride_t, static_cast<int>(k), ids, logprobs, lse);
+    }
+    return check_launch(who);
+}

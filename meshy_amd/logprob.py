@@ -55,6 +55,12 @@ def _fwd(logits, labels, *, want_logp: bool, want_entropy: bool, want_lse: bool)
     return logp, ent, lse
 
 
+def bwd_workspace(n_rows: int, device) -> torch.Tensor:
+    """Scratch of the logprob / gather backward: two floats per row."""
+    nbytes = int(_lib.load().meshy_logprob_bwd_workspace_size(n_rows))
+    return torch.empty(max(nbytes, 1), dtype=torch.uint8, device=device)
+
+
 class _FusedLogprob(torch.autograd.Function):
     """logp = log_softmax(logits.float()).gather(labels) with a fused backward."""
 
@@ -73,9 +79,12 @@ class _FusedLogprob(torch.autograd.Function):
         rows, T, V = logits.shape
         grad = torch.empty(rows, T, V, dtype=logits.dtype, device=logits.device)
         g = grad_logp.float().contiguous()
-        rc = _lib.load().meshy_logprob_bwd(
+        lib = _lib.load()
+        ws = bwd_workspace(rows * T, logits.device)
+        rc = lib.meshy_logprob_bwd(
             logits.data_ptr(), rows, T, V, logits.stride(0), logits.stride(1), labels.data_ptr(),
-            lse.data_ptr(), g.data_ptr(), grad.data_ptr(), _lib.stream_of(logits.device),
+            lse.data_ptr(), g.data_ptr(), grad.data_ptr(), ws.data_ptr(), ws.numel(),
+            _lib.stream_of(logits.device),
         )
         _lib.check(rc, "meshy_logprob_bwd")
         return grad, None, None
@@ -120,5 +129,5 @@ def logsumexp_rows(logits: torch.Tensor) -> torch.Tensor:
     return lse
 
 
-__all__ = ["IGNORE_INDEX", "chunk_entropy", "chunk_logprobs", "logprobs_and_entropy",
+__all__ = ["IGNORE_INDEX", "bwd_workspace", "chunk_entropy", "chunk_logprobs", "logprobs_and_entropy",
            "logsumexp_rows"]

@@ -1,0 +1,252 @@
+"""Student Top-K on-policy distillation with the call surface of
+meshy/backend/titan/opd.py: the Teacher columns in the micro-batch layout and
+the distillation loss with its metrics.
+
+* ``layout_teacher_topk`` / ``build_topk_micro_batches``  the Teacher's
+  ``[L, K]`` columns laid out like the micro (opd.py:58-89), written by the
+  pack kernel in the same launch as the rest of the micro-batch;
+* ``split_teacher_topk``, ``infer_top_k``, ``TopKBatch``  as in opd.py;
+* ``distill_loss``  drop-in for ``StudentTopKTrainer._distill_loss``
+  (opd.py:153-197): the model forward, one fused gather of the K Teacher ids
+  plus the sampled label (``meshy_gather_logprobs_fwd``), then
+  ``meshy_distill_loss_fwd`` for the loss and every sum; ``loss.backward()``
+  runs ``meshy_distill_loss_bwd`` and ``meshy_gather_logprobs_bwd``;
+* ``reduce_distill_metrics``  ``StudentTopKTrainer._reduce_mini_metrics``
+  (opd.py:234-251).
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+from typing import Any, Sequence
+
+import torch
+import torch.distributed as dist
+
+from . import _lib
+from .batch import TEACHER_FIELDS, Batch, launch_pack, stage_micro_batches
+from .loss import segment_offsets
+from .plan import Layout, MicroPlan
+from .topk import gather_logprobs
+
+OPD_TEACHER_FIELDS = list(TEACHER_FIELDS)
+
+
+def infer_top_k(samples: Sequence[Any], default: int = 1) -> int:
+    """Top-K width of the first sample carrying Teacher columns (opd.py:39-44)."""
+    for td in samples:
+        value = td.get(OPD_TEACHER_FIELDS[0], None)
+        if value is not None:
+            return int(value.shape[-1])
+    return default
+
+
+@dataclass
+class TopKBatch(Batch):
+    """A :class:`Batch` plus the Teacher's Top-K columns in the same layout (opd.py:115-120)."""
+
+    teacher_topk_ids: torch.Tensor | None = None       # [rows, S_local, K] long
+    teacher_topk_logprobs: torch.Tensor | None = None  # [rows, S_local, K] float
+
+
+def build_topk_micro_batches(
+    samples: Sequence[Any],
+    micros: Sequence[MicroPlan],
+    *,
+    layout: Layout,
+    device,
+    sharder=None,
+    need_rollout_lp: bool,
+) -> list[TopKBatch]:
+    """``build_micro_batch`` plus ``layout_teacher_topk`` for every micro, in one
+    transfer and one pack launch (what ``StudentTopKTrainer._build_micro`` does per
+    micro, opd.py:141-148)."""
+    job = stage_micro_batches(samples, micros, layout=layout, device=device, need_rollout_lp=need_rollout_lp,
+                              teacher=any(m.sample_idx for m in micros))
+    batches = launch_pack(job, sharder)
+    out = []
+    for k, mb in enumerate(batches):
+        if job.teacher_views is not None:
+            ids, lps = job.teacher_views[k]
+        else:  # only fillers: infer_top_k of no samples is 1
+            m = job.micros[k]
+            shape = (m.n_rows, m.seq_len, 1) if layout == "padded" else (1, m.seq_len, 1)
+            ids = torch.zeros(shape, dtype=torch.int64, device=job.device)
+            lps = torch.zeros(shape, dtype=torch.float32, device=job.device)
+        out.append(TopKBatch(**vars(mb), teacher_topk_ids=ids, teacher_topk_logprobs=lps))
+    return out
+
+
+def layout_teacher_topk(
+    samples: Sequence[Any],
+    micro: MicroPlan,
+    *,
+    layout: Layout,
+    device,
+) -> tuple[torch.Tensor, torch.Tensor]:
+    """``[rows, S, K]`` Teacher ids / log-probs in the micro-batch's layout (opd.py:58-89)."""
+    if layout not in ("padded", "packed"):
+        raise ValueError(f"unknown layout {layout!r}")
+    mb = build_topk_micro_batches(samples, [micro], layout=layout, device=device, need_rollout_lp=False)[0]
+    return mb.teacher_topk_ids, mb.teacher_topk_logprobs
+
+
+def split_teacher_topk(values: torch.Tensor, micro: MicroPlan, *, layout: Layout) -> list[torch.Tensor]:
+    """Inverse of :func:`layout_teacher_topk` for one ``[rows, S, K]`` tensor
+    (opd.py:92-110): one ``[L_j, K]`` view per ``micro.sample_idx[j]``."""
+    out: list[torch.Tensor] = []
+    if layout == "padded":
+        for j, L in enumerate(micro.doc_lens):
+            out.append(values[j, :L])
+    elif layout == "packed":
+        off = 0
+        for L in micro.doc_lens:
+            out.append(values[0, off:off + L])
+            off += L
+    else:
+        raise ValueError(f"unknown layout {layout!r}")
+    return out
+
+
+class _Inputs:
+    """Everything the distillation kernels read besides the student log-probs."""
+
+    def __init__(self, stub, mb, mini, k: int, n_tokens: int, device) -> None:
+        self.k = k
+        self.n_tokens = n_tokens
+        self.n_docs = int(mb.n_docs)
+        self.teacher = mb.teacher_topk_logprobs.detach().reshape(-1, k).to(torch.float32).contiguous()
+        self.mask = mb.mask.reshape(-1).to(torch.float32).contiguous()
+        self.rollout = (None if mb.rollout_logprobs is None else
+                        mb.rollout_logprobs.detach().reshape(-1).to(torch.float32).contiguous())
+        _lib.require_gpu(self.teacher, self.mask, mb.doc_ids, self.rollout)
+        self.seg_off = segment_offsets(mb.doc_ids, self.n_docs + 1)
+        ws = _lib.load().meshy_distill_workspace_size(n_tokens, self.n_docs)
+        self.workspace = torch.empty(max(int(ws), 1), dtype=torch.uint8, device=device)
+        self.lp_min = getattr(stub, "log_prob_min_clamp", None)
+        self.loss_max = getattr(stub, "loss_max_clamp", None)
+        self.per_token = bool(stub.calculate_per_token_loss)
+        self.n_docs_global = int(mini.n_docs_global)
+        self.n_tokens_global = int(mini.n_tokens_global)
+
+    def args(self, student: torch.Tensor) -> _lib.DistillArgs:
+        a = _lib.DistillArgs()
+        a.student = student.data_ptr()
+        a.teacher = self.teacher.data_ptr()
+        a.mask = self.mask.data_ptr()
+        a.rollout_lp = _lib.ptr(self.rollout)
+        a.seg_offsets = self.seg_off.data_ptr()
+        a.n_tokens = self.n_tokens
+        a.n_docs = self.n_docs
+        a.k = self.k
+        a.n_docs_global = self.n_docs_global
+        a.n_tokens_global = self.n_tokens_global
+        a.has_lp_clamp = int(self.lp_min is not None)
+        a.lp_min_clamp = float(self.lp_min) if self.lp_min is not None else 0.0
+        a.has_loss_clamp = int(self.loss_max is not None)
+        a.loss_max_clamp = float(self.loss_max) if self.loss_max is not None else 0.0
+        a.per_token_loss = int(self.per_token)
+        a.workspace = self.workspace.data_ptr()
+        a.workspace_bytes = self.workspace.numel()
+        return a
+
+
+class _DistillLoss(torch.autograd.Function):
+    @staticmethod
+    def forward(ctx, student, inputs: _Inputs):
+        dev = student.device
+        out = torch.empty(_lib.DISTILL_NOUT, dtype=torch.float32, device=dev)
+        seg_cnt = torch.empty(inputs.n_docs + 1, dtype=torch.float32, device=dev)
+        a = inputs.args(student)
+        rc = _lib.load().meshy_distill_loss_fwd(_lib.ctypes.byref(a), out.data_ptr(), seg_cnt.data_ptr(),
+                                                _lib.stream_of(dev))
+        _lib.check(rc, "meshy_distill_loss_fwd")
+        ctx.inputs = inputs
+        ctx.save_for_backward(student, seg_cnt)
+        loss = out[0].clone()
+        ctx.mark_non_differentiable(out)
+        return loss, out
+
+    @staticmethod
+    def backward(ctx, grad_loss, grad_out):
+        student, seg_cnt = ctx.saved_tensors
+        inputs: _Inputs = ctx.inputs
+        g = grad_loss.reshape(1).to(torch.float32).contiguous()
+        grad = torch.empty_like(student)
+        a = inputs.args(student)
+        rc = _lib.load().meshy_distill_loss_bwd(_lib.ctypes.byref(a), seg_cnt.data_ptr(), g.data_ptr(),
+                                                grad.data_ptr(), _lib.stream_of(student.device))
+        _lib.check(rc, "meshy_distill_loss_bwd")
+        return grad, None
+
+
+def distill_from_gathered(self: Any, gathered: torch.Tensor, mb: Any, mini: Any):
+    """The loss and sums of ``_distill_loss`` from the ``[rows, S, K + 1]`` gather
+    (K Teacher ids then the sampled label), opd.py:161-197."""
+    sharder = getattr(self, "sharder", None)
+    if sharder is not None and getattr(sharder, "enabled", False):
+        raise NotImplementedError(
+            "context-parallel distillation needs the per-document count all-reduce between the two "
+            "kernel phases; this build runs one GPU")
+    k = gathered.shape[-1] - 1
+    student = gathered.reshape(-1, k + 1)
+    if student.dtype != torch.float32:
+        student = student.float()
+    if not student.is_contiguous():
+        student = student.contiguous()
+    inputs = _Inputs(self, mb, mini, k, student.shape[0], student.device)
+    loss, out = _DistillLoss.apply(student, inputs)
+    names = _lib.DISTILL_OUT_NAMES
+    sums = {names[j]: out[j] for j in range(4)}
+    if inputs.rollout is not None:
+        sums["train_rollout_kl_sum"] = out[4]
+        sums["train_rollout_logdiff_abs_sum"] = out[5]
+    return loss, sums
+
+
+def distill_loss(self: Any, mb: TopKBatch, mini: Any) -> tuple[torch.Tensor, dict[str, torch.Tensor]]:
+    """Drop-in for ``StudentTopKTrainer._distill_loss`` (opd.py:153-197).
+
+    Reads what the reference reads: ``model_parts``, ``_LOGPROB_CHUNK``,
+    ``log_prob_min_clamp``, ``loss_max_clamp``, ``calculate_per_token_loss`` and
+    ``sharder``."""
+    logits = self.model_parts[0](mb.input_ids, positions=mb.positions, attention_masks=mb.attention_masks)
+    # One gather for the Teacher's K candidates plus the sampled token (opd.py:156-159).
+    ids = torch.cat([mb.teacher_topk_ids, mb.labels.unsqueeze(-1)], dim=-1)
+    gathered = gather_logprobs(logits, ids, chunk=getattr(self, "_LOGPROB_CHUNK", 1024))
+    del logits
+    return distill_from_gathered(self, gathered, mb, mini)
+
+
+def reduce_distill_metrics(self: Any, sums: dict[str, torch.Tensor]) -> dict[str, float]:
+    """Per-rank sums -> distillation metrics (opd.py:234-251)."""
+    keys = list(sums)
+    stacked = torch.stack([sums[k].float().reshape(()) for k in keys])
+    pd = getattr(self, "parallel_dims", None)
+    loss_mesh = pd.get_optional_mesh("loss") if pd is not None and hasattr(pd, "get_optional_mesh") else None
+    if loss_mesh is not None:
+        dist.all_reduce(stacked, op=dist.ReduceOp.SUM, group=loss_mesh.get_group())
+    values = dict(zip(keys, stacked.tolist()))
+    tokens = max(values["token_count"], 1.0)
+    out = {
+        "train/distill_loss": values["loss"],
+        "train/student_topk_mass": values["student_mass_sum"] / tokens,
+        "train/teacher_topk_mass": values["teacher_mass_sum"] / tokens,
+    }
+    if "train_rollout_kl_sum" in values:
+        out["train_rollout_kl"] = values["train_rollout_kl_sum"] / tokens
+        out["train_rollout_logdiff_abs"] = values["train_rollout_logdiff_abs_sum"] / tokens
+    return out
+
+
+__all__ = [
+    "OPD_TEACHER_FIELDS",
+    "TopKBatch",
+    "build_topk_micro_batches",
+    "distill_from_gathered",
+    "distill_loss",
+    "infer_top_k",
+    "layout_teacher_topk",
+    "reduce_distill_metrics",
+    "split_teacher_topk",
+]

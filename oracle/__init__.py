@@ -29,4 +29,9 @@ Modules and what pins each one (the checks live in ``tests/test_oracle_*.py``):
                                                       delta; returns -> R broadcast),
                                                       brute force on tiny inputs
     vapo     whiten_advantages (vapo.py:6-32)         test_vapo_alignment.py:24-46
+    topk     teacher_topk, gather_logprobs,           test_opd_loss.py:13-49, brute-force
+             forward_kl_topk (topk_loss.py:20-80)     (value, index) sort, closed-form KL
+    opd      layout_teacher_topk, split_teacher_topk, test_opd_batch.py:42-75, closed
+             _distill_loss, _reduce_mini_metrics      forms (equal distributions -> 0,
+             (opd.py:39-251)                          ln 2 per token), torch autograd
 """

@@ -1,0 +1,364 @@
+"""Student Top-K OPD kernels against the oracle (the reference's torch path on CPU).
+
+Bars: Top-K ids bit-exact (ties by ascending index), teacher columns bit-exact,
+1e-3 absolute on fp32 log-probs, KL, loss and sums (relative 1e-5 on token
+sums), bf16 gradients within their rounding (4e-3 x |g|), fp32 gradients 1e-6.
+"""
+
+import math
+from types import SimpleNamespace as NS
+
+import pytest
+import torch
+
+from oracle import logprob as olp
+from oracle import opd as oopd
+from oracle import topk as otopk
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def _bf16_logits(rows, T, V, seed, scale=2.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(rows, T, V, generator=g) * scale).to(torch.bfloat16)
+
+
+# ------------------------------------------------------------------ teacher_topk
+
+
+@pytest.mark.parametrize("V,k", [(151936, 8), (50, 5), (8, 8), (1001, 7), (16387, 64), (4096, 1), (20000, 33)])
+def test_topk_matches_oracle(dev, V, k):
+    from meshy_amd import topk
+
+    z = _bf16_logits(2, 19, V, seed=V + k)
+    ids, lps = topk.teacher_topk(z.to(dev), k)
+    rids, rlps = otopk.teacher_topk(z, k)
+    assert ids.dtype == torch.int64 and lps.dtype == torch.float32 and ids.shape == (2, 19, k)
+    assert torch.equal(ids.cpu(), rids)
+    assert (lps.cpu() - rlps).abs().max().item() <= TOL
+
+
+def test_topk_many_ties_and_strided_view(dev):
+    from meshy_amd import topk
+
+    g = torch.Generator().manual_seed(2)
+    # Integer-valued logits: long runs of equal values around the K-th rank.
+    z = torch.randint(-3, 4, (2, 40, 3000), generator=g).float().to(torch.bfloat16)
+    zd = z.to(dev)
+    ids, lps = topk.teacher_topk(zd[:, 5:33, :], 16)
+    rids, rlps = otopk.teacher_topk(z[:, 5:33, :], 16)
+    assert torch.equal(ids.cpu(), rids)
+    assert (lps.cpu() - rlps).abs().max().item() <= TOL
+    # values agree with torch.topk's (whose tie order is unspecified)
+    tv = torch.log_softmax(z[:, 5:33].float(), -1).topk(16, dim=-1).values
+    assert (lps.cpu() - tv).abs().max().item() <= TOL
+
+
+def test_topk_nan_and_inf(dev):
+    from meshy_amd import topk
+
+    z = _bf16_logits(1, 3, 500, seed=9).float()
+    z[0, 0, 7] = float("nan")      # never selected
+    z[0, 1, :] = float("-inf")
+    z[0, 1, 10] = 1.0              # one finite logit, the rest -inf: ties by index
+    z = z.to(torch.bfloat16)
+    ids, lps = topk.teacher_topk(z.to(dev), 4)
+    ids, lps = ids.cpu(), lps.cpu()
+    assert 7 not in ids[0, 0].tolist()
+    assert ids[0, 1].tolist() == [10, 0, 1, 2]
+    assert lps[0, 1, 0].item() == 0.0 and math.isinf(lps[0, 1, 1].item())
+    rids, rlps = otopk.teacher_topk(z[:, 2:], 4)
+    assert torch.equal(ids[:, 2:], rids)
+
+
+def test_topk_full_size_rows_subset(dev):
+    """[16384, 151936] bf16 (config-1 shape), K = 8: a row subset against the
+    oracle, size-independent properties on every row."""
+    from meshy_amd import topk
+
+    T, V, K = 16384, 151936, 8
+    gen = torch.Generator(device=dev).manual_seed(1)
+    z = torch.randn(1, T, V, generator=gen, device=dev, dtype=torch.bfloat16) * 2.0
+    ids, lps = topk.teacher_topk(z, K)
+    assert ((ids >= 0) & (ids < V)).all()
+    assert (lps <= 1e-6).all() and torch.isfinite(lps).all()
+    assert (lps[..., :-1] >= lps[..., 1:]).all()  # sorted by value
+    srt = ids.sort(dim=-1).values
+    assert (srt[..., 1:] != srt[..., :-1]).all()  # distinct
+    # the selected logits, in order
+    top_vals = torch.gather(z, -1, ids).float()
+    assert (top_vals[..., :-1] >= top_vals[..., 1:]).all()
+    rows = torch.tensor([0, 1, 777, 8191, 12345, T - 1])
+    zs = z[:, rows.to(dev)].cpu()
+    rids, rlps = otopk.teacher_topk(zs, K)
+    assert torch.equal(ids[:, rows.to(dev)].cpu(), rids)
+    assert (lps[:, rows.to(dev)].cpu() - rlps).abs().max().item() <= TOL
+
+
+def test_topk_rejects_bad_k(dev):
+    from meshy_amd import topk
+
+    z = _bf16_logits(1, 2, 100, seed=0).to(dev)
+    with pytest.raises(ValueError):
+        topk.teacher_topk(z, 65)
+    with pytest.raises(ValueError):
+        topk.teacher_topk(z, 0)
+
+
+# ------------------------------------------------------------------ gather_logprobs
+
+
+@pytest.mark.parametrize("V", [151936, 1001, 64])
+def test_gather_fwd_bwd_matches_oracle(dev, V):
+    from meshy_amd import topk
+
+    z = _bf16_logits(2, 11, V, seed=V)
+    g = torch.Generator().manual_seed(4)
+    ids = torch.randint(0, V, (2, 11, 9), generator=g)
+    ids[0, 0, 3] = ids[0, 0, 1]  # duplicate ids add their gradients
+    ids[1, 2, :] = ids[1, 2, 0]
+    zd = z.to(dev).requires_grad_(True)
+    out = topk.gather_logprobs(zd, ids.to(dev))
+    ref = otopk.gather_logprobs(z, ids)
+    assert out.shape == (2, 11, 9) and (out.detach().cpu() - ref).abs().max().item() <= TOL
+    w = torch.randn(2, 11, 9, generator=g)
+    (out * w.to(dev)).sum().backward()
+    zr = z.float().requires_grad_(True)
+    (otopk.gather_logprobs(zr, ids) * w).sum().backward()
+    got = zd.grad.float().cpu()
+    bound = 4e-3 * w.abs().sum(-1).max().item()
+    assert (got - zr.grad).abs().max().item() <= bound
+
+
+def test_gather_no_grad_and_strided(dev):
+    from meshy_amd import topk
+
+    z = _bf16_logits(1, 30, 2048, seed=8)
+    ids = torch.randint(0, 2048, (1, 10, 5), generator=torch.Generator().manual_seed(0))
+    with torch.no_grad():
+        out = topk.gather_logprobs(z.to(dev)[:, 10:20], ids.to(dev))
+    assert (out.cpu() - otopk.gather_logprobs(z[:, 10:20], ids)).abs().max().item() <= TOL
+
+
+# ------------------------------------------------------------------ backward paths of K1b
+
+
+@pytest.mark.parametrize("case", ["flat", "rows", "any"])
+def test_logprob_backward_paths(dev, case):
+    """The flat grid-stride pass (contiguous), the per-row pass (strided view) and
+    the generic pass (odd V) against autograd of the reference's fp32 path."""
+    from meshy_amd import logprob
+
+    V = 999 if case == "any" else 4096
+    z = _bf16_logits(2, 24, V, seed=21)
+    y = torch.randint(0, V, (2, 24), generator=torch.Generator().manual_seed(2))
+    y[0, 5] = -100
+    g = torch.randn(2, 24, generator=torch.Generator().manual_seed(3))
+    if case == "rows":
+        # every other row of an interleaved copy: a view equal to z with stride_t = 2 V
+        base = torch.stack([z, z], dim=2).reshape(2, 48, V).to(dev).requires_grad_(True)
+        zd = base[:, ::2]
+        assert zd.stride(1) == 2 * V and torch.equal(zd.detach().cpu(), z)
+    else:
+        base = zd = z.to(dev).requires_grad_(True)
+    lp = logprob.logprobs_and_entropy(zd, y.to(dev))
+    (lp * g.to(dev)).sum().backward()
+    ref = olp.logprob_grad(z, y, g)
+    got = (base.grad[:, ::2] if case == "rows" else base.grad).float().cpu()
+    assert (got - ref).abs().max().item() <= 4e-3 * g.abs().max().item()
+    assert got[0, 5].abs().max().item() == 0.0
+
+
+def test_logprob_backward_flat_equals_rows_bitwise(dev):
+    from meshy_amd import _lib, logprob
+
+    V = 4096
+    z = _bf16_logits(1, 64, V, seed=31).to(dev)
+    y = torch.randint(0, V, (1, 64), generator=torch.Generator().manual_seed(1)).to(dev)
+    lse = logprob.logsumexp_rows(z)
+    g = torch.randn(1, 64, generator=torch.Generator().manual_seed(2)).to(dev)
+    lib = _lib.load()
+    outs = []
+    strided = torch.stack([z, z], dim=2).reshape(1, 128, V)[:, ::2]
+    assert torch.equal(strided, z) and strided.stride(1) == 2 * V
+    for zz in (z, strided):
+        grad = torch.empty(1, 64, V, dtype=torch.bfloat16, device=dev)
+        ws = logprob.bwd_workspace(64, dev)
+        rc = lib.meshy_logprob_bwd(zz.data_ptr(), 1, 64, V, zz.stride(0), zz.stride(1), y.data_ptr(),
+                                   lse.data_ptr(), g.data_ptr(), grad.data_ptr(), ws.data_ptr(), ws.numel(),
+                                   _lib.stream_of(dev))
+        _lib.check(rc, "meshy_logprob_bwd")
+        outs.append(grad)
+    assert torch.equal(outs[0], outs[1])
+
+
+# ------------------------------------------------------------------ forward_kl_topk
+
+
+@pytest.mark.parametrize("clamps", [(None, None), (-10.0, 10.0), (-3.0, 0.5)])
+def test_forward_kl_matches_oracle(dev, clamps):
+    from meshy_amd import topk
+
+    g = torch.Generator().manual_seed(6)
+    s = torch.log_softmax(torch.randn(3, 17, 8, generator=g) * 3, -1)
+    t = torch.log_softmax(torch.randn(3, 17, 8, generator=g) * 3, -1)
+    s[0, 0, 0] = -40.0  # below the clamp
+    kw = dict(log_prob_min_clamp=clamps[0], loss_max_clamp=clamps[1])
+    sd = s.to(dev).requires_grad_(True)
+    kl = topk.forward_kl_topk(sd, t.to(dev), **kw)
+    sr = s.clone().requires_grad_(True)
+    rk = otopk.forward_kl_topk(sr, t, **kw)
+    assert kl.shape == (3, 17) and (kl.detach().cpu() - rk).abs().max().item() <= TOL
+    w = torch.randn(3, 17, generator=g)
+    (kl * w.to(dev)).sum().backward()
+    (rk * w).sum().backward()
+    assert (sd.grad.cpu() - sr.grad).abs().max().item() <= 1e-5
+
+
+# ------------------------------------------------------------------ Teacher columns in the pack
+
+
+def _opd_sample(L, K, seed, V=1000):
+    g = torch.Generator().manual_seed(seed)
+    tokens = torch.randint(0, V, (L,), generator=g)
+    mask = torch.ones(L)
+    mask[: max(1, L // 4)] = 0
+    return {
+        "tokens": tokens,
+        "logprobs": -torch.rand(L, generator=g),
+        "mask_assistant": mask,
+        "advantage": torch.tensor(0.0),
+        "teacher_topk_ids": torch.randint(0, V, (L, K), generator=g),
+        "teacher_topk_logprobs": -torch.rand(L, K, generator=g) * 5,
+    }
+
+
+@pytest.mark.parametrize("layout", ["padded", "packed"])
+def test_teacher_layout_matches_oracle(dev, layout):
+    from meshy_amd import opd
+    from meshy_amd.plan import MicroPlan
+
+    K = 8
+    samples = [_opd_sample(L, K, i) for i, L in enumerate([37, 64, 5, 120, 90])]
+    micros = [MicroPlan((1, 0, 2), 128 if layout == "packed" else 64, (64, 37, 5)),
+              MicroPlan((3, 4), 256 if layout == "packed" else 120, (120, 60)),  # sample 4 truncated
+              MicroPlan((), 64, ())]  # filler
+    mbs = opd.build_topk_micro_batches(samples, micros, layout=layout, device=dev, need_rollout_lp=True)
+    for mb, m in zip(mbs, micros):
+        rids, rlps = oopd.layout_teacher_topk(samples, m.sample_idx, m.seq_len, m.doc_lens, layout=layout)
+        assert torch.equal(mb.teacher_topk_ids.cpu(), rids)
+        assert torch.equal(mb.teacher_topk_logprobs.cpu(), rlps)
+    ids, lps = opd.layout_teacher_topk(samples, micros[0], layout=layout, device=dev)
+    back = opd.split_teacher_topk(ids, micros[0], layout=layout)
+    for j, i in enumerate(micros[0].sample_idx):
+        assert torch.equal(back[j].cpu(), samples[i]["teacher_topk_ids"][:micros[0].doc_lens[j]])
+
+
+def test_teacher_layout_short_rows_raise(dev):
+    from meshy_amd import opd
+    from meshy_amd.plan import MicroPlan
+
+    s = _opd_sample(6, 3, 1)
+    s["teacher_topk_ids"] = s["teacher_topk_ids"][:2]
+    with pytest.raises(ValueError, match="Teacher seq_len"):
+        opd.layout_teacher_topk([s], MicroPlan((0,), 4, (4,)), layout="padded", device=dev)
+    assert opd.infer_top_k([_opd_sample(2, 3, 0)]) == 3
+
+
+# ------------------------------------------------------------------ the distillation loss
+
+
+def _stub(per_token, lp_min=-10.0, loss_max=10.0, model=None):
+    return NS(calculate_per_token_loss=per_token, log_prob_min_clamp=lp_min, loss_max_clamp=loss_max,
+              sharder=None, parallel_dims=NS(cp=1), model_parts=[model], _LOGPROB_CHUNK=1024)
+
+
+@pytest.mark.parametrize("per_token", [True, False])
+@pytest.mark.parametrize("clamps", [(-10.0, 10.0), (None, None), (-2.0, 1.0)])
+@pytest.mark.parametrize("rollout", [True, False])
+def test_distill_from_gathered_matches_oracle(dev, per_token, clamps, rollout):
+    from meshy_amd import opd
+    from meshy_amd.plan import MicroPlan, MiniPlan
+
+    K = 8
+    samples = [_opd_sample(L, K, 10 + i) for i, L in enumerate([300, 41, 700, 2, 129])]
+    micro = MicroPlan((0, 1, 2, 3, 4), 1280, (300, 41, 700, 2, 129))
+    mb = opd.build_topk_micro_batches(samples, [micro], layout="packed", device=dev,
+                                      need_rollout_lp=rollout)[0]
+    g = torch.Generator().manual_seed(7)
+    S = micro.seq_len
+    gathered = torch.log_softmax(torch.randn(1, S, K + 1, generator=g) * 4, -1)
+    gathered[0, 10, :3] = -30.0  # below the lp clamp
+    mini = MiniPlan((micro,), 6, int(mb.mask.sum().item()) + 3, (0,))
+    stub = _stub(per_token, *clamps)
+    gd = gathered.to(dev).requires_grad_(True)
+    loss, sums = opd.distill_from_gathered(stub, gd, mb, mini)
+    gr = gathered.clone().requires_grad_(True)
+    rl, rs = oopd.distill_loss(gr, mb.teacher_topk_logprobs.cpu(), mb.mask.cpu(), mb.doc_ids.cpu(), mb.n_docs,
+                               rollout_lp=mb.rollout_logprobs.cpu() if rollout else None,
+                               n_docs_global=mini.n_docs_global, n_tokens_global=mini.n_tokens_global,
+                               per_token_loss=per_token, log_prob_min_clamp=clamps[0], loss_max_clamp=clamps[1])
+    assert abs(float(loss) - float(rl)) <= TOL
+    assert set(sums) == set(rs)
+    for key in rs:
+        want = float(rs[key])
+        assert abs(float(sums[key]) - want) <= TOL + 1e-5 * abs(want), key
+    loss.backward()
+    rl.backward()
+    assert (gd.grad.cpu() - gr.grad).abs().max().item() <= 1e-6
+    m = opd.reduce_distill_metrics(stub, sums)
+    rm = oopd.reduce_distill_metrics(rs)
+    for key in rm:
+        assert m[key] == pytest.approx(rm[key], abs=TOL), key
+
+
+def test_distill_loss_drop_in_end_to_end(dev):
+    """_distill_loss with a stub model: bf16 logits -> gather of K + 1 ids -> fused
+    loss; loss, sums and d loss / d logits against the reference chain on CPU."""
+    from meshy_amd import opd
+    from meshy_amd.plan import MicroPlan, MiniPlan
+
+    K, V = 8, 5000
+    samples = [_opd_sample(L, K, 20 + i, V=V) for i, L in enumerate([200, 77, 33])]
+    micro = MicroPlan((0, 1, 2), 320, (200, 77, 33))
+    mb = opd.build_topk_micro_batches(samples, [micro], layout="packed", device=dev, need_rollout_lp=True)[0]
+    z = _bf16_logits(1, 320, V, seed=3)
+    zd = z.to(dev).requires_grad_(True)
+    model = lambda ids, positions=None, attention_masks=None: zd  # noqa: E731
+    mini = MiniPlan((micro,), 3, int(mb.mask.sum().item()), (0,))
+    for per_token in (True, False):
+        zd.grad = None
+        stub = _stub(per_token, model=model)
+        loss, sums = opd.distill_loss(stub, mb, mini)
+        loss.backward()
+        zr = z.float().requires_grad_(True)
+        ids = torch.cat([mb.teacher_topk_ids.cpu(), mb.labels.cpu().unsqueeze(-1)], -1)
+        gathered = otopk.gather_logprobs(zr, ids)
+        rl, rs = oopd.distill_loss(gathered, mb.teacher_topk_logprobs.cpu(), mb.mask.cpu(), mb.doc_ids.cpu(),
+                                   mb.n_docs, rollout_lp=mb.rollout_logprobs.cpu(), n_docs_global=3,
+                                   n_tokens_global=mini.n_tokens_global, per_token_loss=per_token)
+        rl.backward()
+        assert abs(float(loss) - float(rl)) <= TOL
+        for key in rs:
+            want = float(rs[key])
+            assert abs(float(sums[key]) - want) <= TOL + 1e-5 * abs(want), key
+        gmax = zr.grad.abs().max().item()
+        assert (zd.grad.float().cpu() - zr.grad).abs().max().item() <= 4e-3 * max(gmax, 1e-6) + 1e-7
+
+
+def test_distill_deterministic(dev):
+    from meshy_amd import opd
+    from meshy_amd.plan import MicroPlan, MiniPlan
+
+    K = 4
+    samples = [_opd_sample(L, K, 40 + i) for i, L in enumerate([1000, 1, 333, 4000])]
+    micro = MicroPlan((0, 1, 2, 3), 5376, (1000, 1, 333, 4000))
+    mb = opd.build_topk_micro_batches(samples, [micro], layout="packed", device=dev, need_rollout_lp=True)[0]
+    gathered = torch.log_softmax(torch.randn(1, micro.seq_len, K + 1, generator=torch.Generator().manual_seed(1)),
+                                 -1).to(dev)
+    mini = MiniPlan((micro,), 4, 4000, (0,))
+    a = opd.distill_from_gathered(_stub(False), gathered, mb, mini)
+    b = opd.distill_from_gathered(_stub(False), gathered, mb, mini)
+    assert torch.equal(a[0], b[0]) and all(torch.equal(a[1][k], b[1][k]) for k in a[1])
