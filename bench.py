@@ -448,6 +448,120 @@ def bench_gae(steps, warmup, no_cpu):
     return _entry(ms * 1e3, T * 26, cpu_ms, tokens=T, docs=n, cpu_sample="sequential loop on padded [1024, S_max]")
 
 
+# ---------------------------------------------------------------- critic reductions and rollout metrics
+
+def bench_critic(steps, warmup, no_cpu):
+    """Config 4's shapes: per-sequence mean and clipped value error over the 6.35 M
+    packed tokens, the Accumulator over the padded [1024, S_max] critic grid."""
+    import numpy as np
+    import torch
+
+    from meshy_amd import critic, workloads
+
+    dev = torch.device("cuda:0")
+    batch, values, _ = workloads.config4(4)
+    n = len(batch.lengths)
+    T = batch.total
+    g = torch.Generator(device=dev).manual_seed(4)
+    doc_ids = torch.from_numpy(np.repeat(np.arange(n), batch.lengths)).reshape(1, -1).to(dev)
+    mask = torch.from_numpy(batch.mask).reshape(1, -1).to(dev)
+    adv = torch.randn(1, T, generator=g, device=dev)
+    out = {}
+    ms = _gpu_ms(lambda: critic.advantages_to_per_sequence(adv, mask, doc_ids, n), steps, warmup)
+    cpu_ms = None
+    if not no_cpu:
+        from oracle import critic as ocritic
+
+        a_c, m_c, d_c = adv.cpu(), mask.cpu(), doc_ids.cpu()
+        cpu_ms = _wall_ms(lambda: ocritic.advantages_to_per_sequence(a_c * m_c, m_c, d_c, n), 5, gpu=False)
+    # reads adv 4 + mask 4 per token (seg offsets from doc ids: 8 more)
+    out["per_sequence_mean_config4"] = _entry(ms * 1e3, T * 16, cpu_ms, tokens=T, docs=n)
+    v = torch.randn(T, generator=g, device=dev).requires_grad_(True)
+    t = torch.randn(T, generator=g, device=dev)
+    o = (v.detach() + 0.1 * torch.randn(T, generator=g, device=dev))
+
+    def cve():
+        v.grad = None
+        critic.clipped_value_error(v, t, o, 0.2).sum().backward()
+
+    ms = _gpu_ms(cve, steps, warmup)
+    cpu_ms = None
+    if not no_cpu:
+        from oracle import critic as ocritic
+
+        vc, tc, oc = v.detach().cpu().requires_grad_(True), t.cpu(), o.cpu()
+
+        def cpu():
+            vc.grad = None
+            ocritic.clipped_value_error(vc, tc, oc, 0.2).sum().backward()
+
+        cpu_ms = _wall_ms(cpu, 5, gpu=False)
+    # fwd: v, t, o read + out written; bwd: v, t, o, grad read + grad written
+    out["clipped_value_error_fwd_bwd_config4"] = _entry(ms * 1e3, T * 36, cpu_ms, tokens=T)
+    S = int(batch.lengths.max())
+    rows = n
+    pos = np.arange(T) - np.repeat(batch.offsets[:-1], batch.lengths)
+    ids = np.repeat(np.arange(n), batch.lengths)
+    flat = torch.from_numpy(ids * S + pos).to(dev)
+    vals = torch.zeros(rows * S, device=dev, dtype=torch.bfloat16)
+    vals[flat] = torch.from_numpy(values).to(dev).to(torch.bfloat16)
+    rets = torch.zeros(rows * S, device=dev)
+    rets[flat] = torch.randn(T, generator=g, device=dev)
+    msk = torch.zeros(rows * S, device=dev)
+    msk[flat] = mask.reshape(-1)
+    vals, rets, msk = vals.view(rows, S), rets.view(rows, S), msk.view(rows, S)
+    rew = torch.rand(rows, device=dev)
+    grp = torch.arange(rows, device=dev) // 8
+
+    def acc():
+        a = critic.Accumulator()
+        a.update(vals, rets, msk, rew, grp)
+        return a.state
+
+    ms = _wall_ms(acc, steps // 5 + 3, warmup=2)
+    cpu_ms = None
+    if not no_cpu:
+        from oracle import critic as ocritic
+
+        vc, rc, mc, rwc, gc = vals.cpu(), rets.cpu(), msk.cpu(), rew.cpu(), grp.cpu()
+
+        def cpu_acc():
+            a = ocritic.Accumulator()
+            a.update(vc, rc, mc, rwc, gc)
+
+        cpu_ms = _wall_ms(cpu_acc, 3, gpu=False)
+    # reads values 2 + returns 4 + mask 4 per grid element
+    out["accumulator_update_config4_padded"] = _entry(ms * 1e3, rows * S * 10, cpu_ms, rows=rows, S=S,
+                                                      note="wall time including the state's host read")
+    return out
+
+
+def bench_rollout_metrics(runs, no_cpu):
+    """Config 0's 256 samples: _rollout_metrics from the sample list and from the
+    wire columns, wall time including every host read of the result."""
+    import torch
+
+    from meshy_amd import wire, workloads
+    from meshy_amd.rollout_metrics import rollout_metrics
+
+    batch, rewards, _ = workloads.config0(0)
+    samples = batch.sample_dicts(rewards=rewards)
+    for i, s in enumerate(samples):
+        s.update(weight_version=torch.tensor(3 - i % 2), truncated=torch.tensor(i % 9 == 0),
+                 repetition=torch.tensor(0), mixed_version=torch.tensor(0), advantage=torch.tensor(0.5))
+    fields = list(samples[0])
+    cols = wire.samples_to_columns(samples, fields)
+    out = {"samples": len(samples), "tokens": int(batch.total)}
+    out["gpu_from_samples_ms"] = round(_wall_ms(lambda: rollout_metrics(samples, 8192, 4), runs, warmup=2), 3)
+    out["gpu_from_columns_ms"] = round(_wall_ms(lambda: rollout_metrics(cols, 8192, 4), runs, warmup=2), 3)
+    if not no_cpu:
+        from oracle import rollout_metrics as orm
+
+        out["cpu_ms"] = round(_wall_ms(lambda: orm.rollout_metrics(samples, 8192, 4), 3, gpu=False), 3)
+        out["speedup_vs_cpu"] = round(out["cpu_ms"] / out["gpu_from_columns_ms"], 1)
+    return out
+
+
 # ---------------------------------------------------------------- end to end
 
 def bench_end_to_end(runs, no_cpu):
@@ -611,6 +725,8 @@ def main() -> int:
         kernels.update(bench_ppo(args.steps, args.warmup, args.no_cpu))
         kernels["gae_returns_config4"] = bench_gae(args.steps, args.warmup, args.no_cpu)
         kernels["logprob_entropy_config3"] = bench_long_context(max(3, args.steps // 10), 2, args.no_cpu)
+        kernels["critic"] = bench_critic(args.steps, args.warmup, args.no_cpu)
+        kernels["rollout_metrics_config0"] = bench_rollout_metrics(10, args.no_cpu)
         result["kernels"] = kernels
         result["end_to_end"] = bench_end_to_end(5, args.no_cpu)
         if result.get("cpu_baseline"):

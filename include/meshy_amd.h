@@ -483,6 +483,60 @@ int meshy_whiten_apply(float* adv, const float* mask, int64_t n, const double* s
                        hipStream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Critic-side reductions (device).
+ *
+ * meshy_per_sequence_mean replaces advantages_to_per_sequence
+ * (meshy/backend/titan/critic/gae.py:296-312): for each document d < n_docs,
+ * out[d] = sum x[i] mask[i] / max(sum mask[i], 1) over its token range
+ * [seg_offsets[d], seg_offsets[d+1]) (seg_offsets as for the PPO loss).
+ *
+ * meshy_critic_accumulate replaces Accumulator.update
+ * (meshy/backend/titan/critic/metrics.py:238-275) on one [rows, S] row-major
+ * micro-batch: with m = (mask > 0), v = values m (fp32 or bf16 values),
+ * r = returns m, d = v - r, sums[0..4] (fp64, device) receive the sums of
+ * m, r, r^2, d, d^2 and row_value[row] = sum_S v / max(sum_S m, 1).  The
+ * workspace holds 5 doubles per row.
+ *
+ * meshy_clipped_value_error replaces clipped_value_error
+ * (meshy/backend/titan/vapo.py:35-41): out = (v - t)^2, or with has_clip
+ * max((v - t)^2, (o + clamp(v - o, -clip, clip) - t)^2); the backward gives
+ * d out / d v * grad_out (maximum splits ties, clamp passes on its range).
+ * ---------------------------------------------------------------------- */
+int meshy_per_sequence_mean(const float* x, const float* mask, const int64_t* seg_offsets,
+                            int64_t n_docs, float* out, hipStream_t stream);
+size_t meshy_critic_accumulate_workspace_size(int64_t rows);
+int meshy_critic_accumulate(const void* values, int32_t values_bf16, const float* returns,
+                            const float* mask, int64_t rows, int64_t S, double* sums,
+                            float* row_value, void* workspace, size_t workspace_bytes,
+                            hipStream_t stream);
+int meshy_clipped_value_error(const float* values, const float* targets, const float* old_values,
+                              int32_t has_clip, float clip, int64_t n, float* out,
+                              hipStream_t stream);
+int meshy_clipped_value_error_bwd(const float* values, const float* targets,
+                                  const float* old_values, int32_t has_clip, float clip, int64_t n,
+                                  const float* grad_out, float* grad_values, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Token-level rollout statistics over jagged sample columns (device).
+ * Replaces the per-token loops of TitanTrainer._rollout_metrics
+ * (meshy/backend/titan/metrics.py:197-212).  Sample s covers
+ * mask[offsets[s] .. offsets[s+1]) and logprobs[lp_offsets[s] ..
+ * lp_offsets[s+1]) (the values() / offsets() of jagged nested columns).
+ *   resp_len[s]  #(mask > 0)
+ *   lp_sum[s]    sum of the kept log-probs (fp64): those with mask > 0 when
+ *                the sample's log-prob column is as long as its mask, else all
+ *   out_off      [n + 1] exclusive scan of the kept counts (required)
+ *   kept_lp      the kept log-probs in sample order (nullable; room for every
+ *                log-prob is enough)
+ * logprobs may be NULL (no log-prob column).  Workspace: one int64 per sample.
+ * ---------------------------------------------------------------------- */
+size_t meshy_ragged_token_stats_workspace_size(int64_t n);
+int meshy_ragged_token_stats(const float* mask, const float* logprobs, const int64_t* offsets,
+                             const int64_t* lp_offsets, int64_t n, int64_t* resp_len,
+                             double* lp_sum, int64_t* out_off, float* kept_lp, void* workspace,
+                             size_t workspace_bytes, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
  * Measurement helper; no counterpart in the reference.  Streams rows x
  * row_bytes bytes from src (one workgroup per row, 16-byte nontemporal loads,
  * 8 in flight per thread, the access pattern of meshy_logprob_entropy_fwd)

@@ -278,6 +278,23 @@ SIGNATURES = {
     ),
     "meshy_whiten_apply": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "meshy_stream_read": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "meshy_per_sequence_mean": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
+    "meshy_critic_accumulate_workspace_size": (c_size_t, [c_int64]),
+    "meshy_critic_accumulate": (
+        c_int, [c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+                c_size_t, c_void_p]
+    ),
+    "meshy_clipped_value_error": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_float, c_int64, c_void_p, c_void_p]
+    ),
+    "meshy_clipped_value_error_bwd": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_float, c_int64, c_void_p, c_void_p, c_void_p]
+    ),
+    "meshy_ragged_token_stats_workspace_size": (c_size_t, [c_int64]),
+    "meshy_ragged_token_stats": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p, c_void_p, c_void_p,
+                c_void_p, c_size_t, c_void_p]
+    ),
 }
 
 ABI_VERSION = 2

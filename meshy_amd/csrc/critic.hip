@@ -1,0 +1,237 @@
+// Critic-side reductions of the PPO critic path, for gfx950.
+//
+//   meshy_per_sequence_mean     advantages_to_per_sequence
+//                               (meshy/backend/titan/critic/gae.py:296-312):
+//                               out[d] = sum_{i in d} x_i m_i / max(sum m_i, 1);
+//   meshy_critic_accumulate     Accumulator.update
+//                               (meshy/backend/titan/critic/metrics.py:238-275):
+//                               with m = (mask > 0), v = values m, r = returns m,
+//                               d = v - r, the window sums of m, r, r^2, d, d^2
+//                               (fp64) and each row's v-sum / max(m-sum, 1);
+//   meshy_clipped_value_error   clipped_value_error (meshy/backend/titan/vapo.py:35-41)
+//   (+ _bwd)                    max((v - t)^2, (o + clamp(v - o, -c, c) - t)^2)
+//                               and its gradient as torch autograd gives it
+//                               (maximum splits ties 1/2-1/2, clamp passes on
+//                               its closed range).
+//
+// One workgroup per document (per row for the accumulator) strides its tokens
+// with coalesced loads and reduces in a fixed order, so results are bitwise
+// reproducible; the window sums take a second one-workgroup pass over the rows.
+#include <math.h>
+
+#include "common.h"
+
+namespace meshy {
+namespace {
+
+constexpr int kThreads = 256;
+constexpr int kWaves = kThreads / kWave;
+constexpr int kAccSums = 5;  // m, r, r^2, d, d^2
+
+template <typename T>
+__device__ __forceinline__ T block_sum_to0(T v, T* scratch) {
+    v = wave_sum(v);
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+    if (lane == 0) scratch[wid] = v;
+    __syncthreads();
+    T r = 0;
+    if (threadIdx.x == 0) {
+        for (int w = 0; w < kWaves; ++w) r += scratch[w];
+    }
+    __syncthreads();
+    return r;
+}
+
+__global__ __launch_bounds__(kThreads) void k_seq_mean(const float* __restrict__ x, const float* __restrict__ mask,
+                                                       const int64_t* __restrict__ seg_off,
+                                                       float* __restrict__ out) {
+    __shared__ float s_a[kWaves], s_b[kWaves];
+    const int64_t d = blockIdx.x;
+    const int64_t lo = seg_off[d], hi = seg_off[d + 1];
+    float sx = 0.f, sm = 0.f;
+    for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads) {
+        const float m = mask[i];
+        sx = fmaf(x[i], m, sx);
+        sm += m;
+    }
+    sx = block_sum_to0(sx, s_a);
+    sm = block_sum_to0(sm, s_b);
+    if (threadIdx.x == 0) out[d] = sx / fmaxf(sm, 1.f);
+}
+
+__device__ __forceinline__ float load_value(const void* v, int bf16, int64_t i) {
+    return bf16 ? bf16_to_f32(static_cast<const uint16_t*>(v)[i]) : static_cast<const float*>(v)[i];
+}
+
+// One workgroup per row: row sums into part[row][5] (fp64) and row_value[row].
+__global__ __launch_bounds__(kThreads) void k_acc_rows(const void* __restrict__ values, int values_bf16,
+                                                       const float* __restrict__ returns,
+                                                       const float* __restrict__ mask, int64_t S,
+                                                       double* __restrict__ part, float* __restrict__ row_value) {
+    __shared__ double s_red[kAccSums + 1][kWaves];
+    const int64_t row = blockIdx.x;
+    const int64_t base = row * S;
+    double acc[kAccSums + 1] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0};  // m, r, r2, d, d2, v
+    for (int64_t j = threadIdx.x; j < S; j += kThreads) {
+        const int64_t i = base + j;
+        const float m = mask[i] > 0.f ? 1.f : 0.f;
+        const float v = load_value(values, values_bf16, i) * m;
+        const float r = returns[i] * m;
+        const float dv = v - r;
+        acc[0] += m;
+        acc[1] += r;
+        acc[2] += static_cast<double>(r) * r;
+        acc[3] += dv;
+        acc[4] += static_cast<double>(dv) * dv;
+        acc[5] += v;
+    }
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+#pragma unroll
+    for (int k = 0; k <= kAccSums; ++k) {
+        const double w = wave_sum(acc[k]);
+        if (lane == 0) s_red[k][wid] = w;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t[kAccSums + 1];
+#pragma unroll
+        for (int k = 0; k <= kAccSums; ++k) {
+            t[k] = 0.0;
+            for (int w = 0; w < kWaves; ++w) t[k] += s_red[k][w];
+        }
+#pragma unroll
+        for (int k = 0; k < kAccSums; ++k) part[row * kAccSums + k] = t[k];
+        // _response_mean: v-sum over max(m-sum, 1)
+        row_value[row] = static_cast<float>(t[kAccSums] / fmax(t[0], 1.0));
+    }
+}
+
+// One workgroup: the window sums over rows in row order.
+__global__ __launch_bounds__(kThreads) void k_acc_final(const double* __restrict__ part, int64_t rows,
+                                                        double* __restrict__ sums) {
+    __shared__ double s_red[kWaves];
+    for (int k = 0; k < kAccSums; ++k) {
+        double v = 0.0;
+        for (int64_t r = threadIdx.x; r < rows; r += kThreads) v += part[r * kAccSums + k];
+        v = block_sum_to0(v, s_red);
+        if (threadIdx.x == 0) sums[k] = v;
+    }
+}
+
+__device__ __forceinline__ float clamp_c(float x, float c) { return isnan(x) ? x : (x < -c ? -c : (x > c ? c : x)); }
+
+__global__ __launch_bounds__(kThreads) void k_cve_fwd(const float* __restrict__ v, const float* __restrict__ t,
+                                                      const float* __restrict__ o, float clip, int has_clip,
+                                                      int64_t n, float* __restrict__ out) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const float e = v[i] - t[i];
+    float err = e * e;
+    if (has_clip) {
+        const float c = (o[i] + clamp_c(v[i] - o[i], clip)) - t[i];
+        err = fmaxf(err, c * c);
+        if (isnan(e) || isnan(c)) err = __builtin_nanf("");
+    }
+    out[i] = err;
+}
+
+__global__ __launch_bounds__(kThreads) void k_cve_bwd(const float* __restrict__ v, const float* __restrict__ t,
+                                                      const float* __restrict__ o, float clip, int has_clip,
+                                                      int64_t n, const float* __restrict__ g,
+                                                      float* __restrict__ gv) {
+    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
+    if (i >= n) return;
+    const float e = v[i] - t[i];
+    const float gi = g[i];
+    if (!has_clip) {
+        gv[i] = gi * (2.f * e);
+        return;
+    }
+    const float dlt = v[i] - o[i];
+    const float c = (o[i] + clamp_c(dlt, clip)) - t[i];
+    const float err = e * e, cerr = c * c;
+    float ga = 0.f, gc = 0.f;  // shares of the gradient through each branch of maximum
+    if (err > cerr) ga = gi;
+    else if (err < cerr) gc = gi;
+    else {
+        ga = 0.5f * gi;
+        gc = 0.5f * gi;
+    }
+    const float pass = (dlt >= -clip && dlt <= clip) ? 1.f : 0.f;
+    gv[i] = ga * (2.f * e) + (gc * (2.f * c)) * pass;
+}
+
+}  // namespace
+}  // namespace meshy
+
+extern "C" int meshy_per_sequence_mean(const float* x, const float* mask, const int64_t* seg_offsets,
+                                       int64_t n_docs, float* out, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    const char* who = "meshy_per_sequence_mean";
+    if (n_docs < 0 || n_docs > INT32_MAX) return set_error(MESHY_EINVAL, "%s: bad n_docs", who);
+    if (n_docs == 0) return MESHY_OK;
+    if (!x || !mask || !seg_offsets || !out) return set_error(MESHY_ENULL, "%s: NULL pointer", who);
+    hipLaunchKernelGGL(k_seq_mean, dim3(static_cast<unsigned>(n_docs)), dim3(kThreads), 0, stream, x, mask,
+                       seg_offsets, out);
+    return check_launch(who);
+}
+
+extern "C" size_t meshy_critic_accumulate_workspace_size(int64_t rows) {
+    return rows < 0 ? 0 : meshy::align_up(sizeof(double) * meshy::kAccSums * static_cast<size_t>(rows), 256);
+}
+
+extern "C" int meshy_critic_accumulate(const void* values, int32_t values_bf16, const float* returns,
+                                       const float* mask, int64_t rows, int64_t S, double* sums,
+                                       float* row_value, void* workspace, size_t workspace_bytes,
+                                       hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    const char* who = "meshy_critic_accumulate";
+    if (rows < 0 || S < 0 || rows > INT32_MAX) return set_error(MESHY_EINVAL, "%s: bad shape", who);
+    if (!sums || (rows > 0 && (!values || !returns || !mask || !row_value)))
+        return set_error(MESHY_ENULL, "%s: NULL pointer", who);
+    if (workspace_bytes < meshy_critic_accumulate_workspace_size(rows) || (rows > 0 && !workspace))
+        return set_error(MESHY_ESPACE, "%s: workspace needs %zu bytes", who,
+                         meshy_critic_accumulate_workspace_size(rows));
+    double* part = static_cast<double*>(workspace);
+    if (rows > 0) {
+        hipLaunchKernelGGL(k_acc_rows, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, stream, values,
+                           values_bf16, returns, mask, S, part, row_value);
+        int rc = check_launch(who);
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(k_acc_final, dim3(1), dim3(kThreads), 0, stream, part, rows, sums);
+    return check_launch(who);
+}
+
+extern "C" int meshy_clipped_value_error(const float* values, const float* targets, const float* old_values,
+                                         int32_t has_clip, float clip, int64_t n, float* out, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    const char* who = "meshy_clipped_value_error";
+    if (n < 0) return set_error(MESHY_EINVAL, "%s: negative size", who);
+    if (n == 0) return MESHY_OK;
+    if (!values || !targets || !out || (has_clip && !old_values))
+        return set_error(MESHY_ENULL, "%s: NULL pointer", who);
+    hipLaunchKernelGGL(k_cve_fwd, dim3(static_cast<unsigned>(ceil_div(n, kThreads))), dim3(kThreads), 0, stream,
+                       values, targets, old_values, clip, has_clip, n, out);
+    return check_launch(who);
+}
+
+extern "C" int meshy_clipped_value_error_bwd(const float* values, const float* targets, const float* old_values,
+                                             int32_t has_clip, float clip, int64_t n, const float* grad_out,
+                                             float* grad_values, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    const char* who = "meshy_clipped_value_error_bwd";
+    if (n < 0) return set_error(MESHY_EINVAL, "%s: negative size", who);
+    if (n == 0) return MESHY_OK;
+    if (!values || !targets || !grad_out || !grad_values || (has_clip && !old_values))
+        return set_error(MESHY_ENULL, "%s: NULL pointer", who);
+    hipLaunchKernelGGL(k_cve_bwd, dim3(static_cast<unsigned>(ceil_div(n, kThreads))), dim3(kThreads), 0, stream,
+                       values, targets, old_values, clip, has_clip, n, grad_out, grad_values);
+    return check_launch(who);
+}

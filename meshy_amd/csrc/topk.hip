@@ -9,11 +9,14 @@
 // and updates the online log-sum-exp (rowstream.h).  Each wavefront also keeps
 // a running sorted list of its best entries spread over its 64 lanes (lane j
 // holds rank j).  The rank K-1 value is the wavefront's threshold: a tile whose
-// lane maxima all fall below it costs one compare, otherwise every element at
-// or above the threshold is offered to the list one at a time (a ballot, then
-// a shift of the lanes below the insertion point).  After a few tiles the
-// threshold sits near the row's top values and offers are rare.  The waves'
-// lists are then merged by wave 0.
+// lane maxima all fall below it costs one compare, otherwise each 16-byte
+// chunk whose maximum reaches it offers its elements at or above it to the
+// list one at a time (a ballot, then a shift of the lanes below the insertion
+// point).  The first tile sets a floor: the K-th largest of the 64 lanes' tile
+// maxima (a 64-lane bitonic sort), which K of the wavefront's elements reach,
+// so nothing below it is ever offered.  The threshold then climbs towards the
+// row's top values and offers become rare.  The waves' lists are merged by
+// wave 0.
 //
 // Order: larger value first, equal values by smaller index (a stable sort of
 // the row in descending order).  NaN logits are never selected.  Every list
@@ -28,7 +31,11 @@ namespace {
 
 constexpr int kTopkThreads = 256;
 constexpr int kTopkWaves = kTopkThreads / kWave;
-constexpr int kTopkUnroll = 4;
+// 8 loads in flight per thread for K <= 16 (764 us on [16384, 151936] at K = 8
+// against 820 us with 4); 4 above, where the larger list dominates.
+constexpr int kTopkUnrollSmallK = 8;
+constexpr int kTopkUnrollLargeK = 4;
+constexpr int kSmallK = 16;
 constexpr int kMaxTopK = kWave;
 constexpr int32_t kNoIndex = INT32_MAX;
 
@@ -42,13 +49,43 @@ __device__ __forceinline__ float read_lane(float x, int l) {
 }
 __device__ __forceinline__ int32_t read_lane(int32_t x, int l) { return __builtin_amdgcn_readlane(x, l); }
 
-// A wavefront's sorted list; (tv, ti) is the entry of rank K-1 (the threshold).
+// A wavefront's sorted list.  (tv, ti) is the threshold a candidate must rank
+// before: the entry of rank K-1, or (floor, kNoIndex) while that entry is below
+// the floor, a value at least K of the wavefront's elements reach.
 struct WaveTop {
     float v = -__builtin_inff();
     int32_t i = kNoIndex;
     float tv = -__builtin_inff();
     int32_t ti = kNoIndex;
+    float floor = -__builtin_inff();
 };
+
+__device__ __forceinline__ void refresh_threshold(WaveTop& w, int k) {
+    w.tv = read_lane(w.v, k - 1);
+    w.ti = read_lane(w.i, k - 1);
+    if (w.tv < w.floor) {
+        w.tv = w.floor;
+        w.ti = kNoIndex;
+    }
+}
+
+// The k-th largest of the 64 lanes' x (NaN counts as -inf): a 64-lane
+// bitonic sort, descending, then lane k-1.
+__device__ __forceinline__ float kth_largest_lane(float x, int k) {
+    const int lane = threadIdx.x % kWave;
+    float v = isnan(x) ? -__builtin_inff() : x;
+#pragma unroll
+    for (int size = 2; size <= kWave; size <<= 1) {
+#pragma unroll
+        for (int stride = size / 2; stride > 0; stride >>= 1) {
+            const float o = __shfl_xor(v, stride, kWave);
+            const bool desc = (lane & size) == 0 || size == kWave;
+            const bool lower = (lane & stride) == 0;
+            v = (desc == lower) ? fmaxf(v, o) : fminf(v, o);
+        }
+    }
+    return read_lane(v, k - 1);
+}
 
 // Inserts the wave-uniform candidate (cv, ci); the entries ranked before it
 // form a prefix of the lanes.
@@ -64,8 +101,7 @@ __device__ __forceinline__ void top_insert(WaveTop& w, float cv, int32_t ci, int
         w.v = uv;
         w.i = ui;
     }
-    w.tv = read_lane(w.v, k - 1);
-    w.ti = read_lane(w.i, k - 1);
+    refresh_threshold(w, k);
 }
 
 // Offers one element per lane (z, NaN when absent); col(l) is lane l's column.
@@ -142,14 +178,33 @@ __global__ __launch_bounds__(NT) void k_topk_vec(const uint16_t* __restrict__ lo
         for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(row4 + c0 + u * NT + tid);
         float z[U * 8];
         unpack(v, z);
-        const float tm = tile_max(z);
+        float cm[U];  // per 16-byte chunk maxima
+#pragma unroll
+        for (int u = 0; u < U; ++u) {
+            cm[u] = z[8 * u];
+#pragma unroll
+            for (int j = 1; j < 8; ++j) cm[u] = fmaxf(cm[u], z[8 * u + j]);
+        }
+        float tm = cm[0];
+#pragma unroll
+        for (int u = 1; u < U; ++u) tm = fmaxf(tm, cm[u]);
         accumulate<false>(z, tm, m, s, t);
+        if (it == 0) {
+            // k lanes hold an element >= the k-th largest lane maximum.
+            w.floor = kth_largest_lane(tm, k);
+            refresh_threshold(w, k);
+        }
         if (__ballot(tm >= w.tv)) {
 #pragma unroll
-            for (int j = 0; j < U * 8; ++j) {
-                top_offer(w, z[j], k, [&](int l) {
-                    return static_cast<int32_t>(8 * (c0 + (j / 8) * NT + wave0 + l) + (j % 8));
-                });
+            for (int u = 0; u < U; ++u) {
+                if (__ballot(cm[u] >= w.tv)) {
+#pragma unroll
+                    for (int j = 0; j < 8; ++j) {
+                        top_offer(w, z[8 * u + j], k, [&](int l) {
+                            return static_cast<int32_t>(8 * (c0 + u * NT + wave0 + l) + j);
+                        });
+                    }
+                }
             }
         }
     }
@@ -237,9 +292,12 @@ extern "C" int meshy_topk_logprobs(const uint16_t* logits, int64_t rows, int64_t
     if (n == 0) return MESHY_OK;
     const dim3 grid(static_cast<unsigned>(n));
     const bool vec = reinterpret_cast<uintptr_t>(logits) % 16 == 0 && stride_b % 8 == 0 && stride_t % 8 == 0;
-    if (vec) {
-        hipLaunchKernelGGL((k_topk_vec<kTopkThreads, kTopkUnroll>), grid, dim3(kTopkThreads), 0, stream, logits, T,
-                           V, stride_b, stride_t, static_cast<int>(k), ids, logprobs, lse);
+    if (vec && k <= kSmallK) {
+        hipLaunchKernelGGL((k_topk_vec<kTopkThreads, kTopkUnrollSmallK>), grid, dim3(kTopkThreads), 0, stream,
+                           logits, T, V, stride_b, stride_t, static_cast<int>(k), ids, logprobs, lse);
+    } else if (vec) {
+        hipLaunchKernelGGL((k_topk_vec<kTopkThreads, kTopkUnrollLargeK>), grid, dim3(kTopkThreads), 0, stream,
+                           logits, T, V, stride_b, stride_t, static_cast<int>(k), ids, logprobs, lse);
     } else {
         hipLaunchKernelGGL((k_topk_any<kTopkThreads>), grid, dim3(kTopkThreads), 0, stream, logits, T, V, stride_b,
                            stride_t, static_cast<int>(k), ids, logprobs, lse);

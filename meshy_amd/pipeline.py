@@ -25,6 +25,7 @@ import torch
 from . import _lib
 from .batch import Batch, PackJob, _Layout, launch_pack
 from .plan import Plan, PlannerConfig, plan_tables, tables_to_plan
+from .wire import jagged_parts
 
 
 class RaggedSamples:
@@ -88,6 +89,24 @@ class RaggedSamples:
         if need_rollout_lp:
             torch.cat([s["logprobs"].to(torch.float32) for s in samples], out=r.view("logprobs"))
         r.view("rewards")[:r.n] = torch.tensor([float(s["reward"]) for s in samples], dtype=torch.float32)
+        r.view("group_off").copy_(torch.as_tensor(np.asarray(group_offsets, np.int64)))
+        return r
+
+    @classmethod
+    def from_columns(cls, columns, group_offsets, need_rollout_lp: bool = True) -> "RaggedSamples":
+        """From a batch of wire columns (``meshy_amd.wire``, adapter.py:39-132): the
+        jagged ``tokens`` / ``mask_assistant`` / ``logprobs`` columns are copied from
+        their flat ``values()`` in one pass each, ``reward`` from its ``[B, 1]`` column."""
+        tok, off = jagged_parts(columns["tokens"])
+        r = cls(torch.diff(off).numpy(), len(group_offsets) - 1, need_rollout_lp)
+        r.view("tokens").copy_(tok.reshape(-1).to(torch.int32))
+        names = ["mask_assistant"] + (["logprobs"] if need_rollout_lp else [])
+        for name, region in zip(names, ["mask", "logprobs"]):
+            flat, o = jagged_parts(columns[name])
+            if not torch.equal(o.cpu(), off.cpu()):
+                raise ValueError(f"column {name!r} is not as long as 'tokens' in every sample")
+            r.view(region).copy_(flat.reshape(-1).to(torch.float32))
+        r.view("rewards")[:r.n] = torch.as_tensor(columns["reward"]).reshape(-1).to(torch.float32)
         r.view("group_off").copy_(torch.as_tensor(np.asarray(group_offsets, np.int64)))
         return r
 

@@ -1,0 +1,249 @@
+"""Batch-level rollout statistics with the call surface of
+``TitanTrainer._rollout_metrics`` (meshy/backend/titan/metrics.py:171-322).
+
+The per-token work -- response lengths, the sampled tokens' behaviour-policy
+log-probs and their mean -- runs on the device over the jagged columns
+(``meshy_ragged_token_stats``); the per-sample scalars (rewards, advantages,
+weight versions, quality stamps, percentiles of the per-sample lengths) are
+sample-level host arithmetic, as in the reference.  The histogram of sampled
+log-probs is returned as a device tensor rather than a Python list.
+
+``samples`` may be a list of mappings (the reference's input) or a batch of
+wire columns (``meshy_amd.wire``): the jagged ``tokens`` / ``mask_assistant`` /
+``logprobs`` columns are then read in place.
+"""
+
+from __future__ import annotations
+
+import math
+from typing import Any
+
+import torch
+
+from . import _lib
+from .wire import jagged_parts
+
+
+def _percentile(values: list[float], q: float) -> float:
+    """Linear-interpolated percentile of a sorted copy (metrics.py:123-131)."""
+    if not values:
+        return 0.0
+    values = sorted(values)
+    pos = (len(values) - 1) * q
+    lo, hi = math.floor(pos), math.ceil(pos)
+    if lo == hi:
+        return values[lo]
+    return values[lo] + (values[hi] - values[lo]) * (pos - lo)
+
+
+def _mean(values: list[float]) -> float:
+    return sum(values) / len(values) if values else 0.0
+
+
+def _get(sample: Any, f: str) -> Any:
+    return sample.get(f, None) if hasattr(sample, "get") else getattr(sample, f, None)
+
+
+def _scalars(samples, columns, f: str) -> list[float]:
+    """Per-sample values of a scalar column (the samples that carry one)."""
+    if columns is not None:
+        v = columns.get(f)
+        if v is None:
+            return []
+        return [float(x) for x in (v.reshape(-1).tolist() if isinstance(v, torch.Tensor) else v)]
+    out = []
+    for s in samples:
+        v = _get(s, f)
+        if v is None:
+            continue
+        for x in (v.detach().cpu().reshape(-1).tolist() if torch.is_tensor(v) else
+                  (list(v) if hasattr(v, "__iter__") else [v])):
+            try:
+                out.append(float(x))
+            except (TypeError, ValueError):
+                pass
+    return out
+
+
+def _flags(samples, columns, n: int, f: str) -> list[float] | None:
+    values = _scalars(samples, columns, f)
+    if len(values) != n:
+        return None
+    return [1.0 if v > 0.5 else 0.0 for v in values]
+
+
+def _token_stats(samples, columns, device):
+    """Per-sample total and response lengths and the kept log-probs (device),
+    with the reference's presence rules (metrics.py:197-212): a length per sample
+    with tokens, a response length per sample with a mask, log-probs kept where
+    the mask is on when the sample's mask is as long as its log-probs."""
+    if columns is not None:
+        tok = columns.get("tokens")
+        mask_col = columns.get("mask_assistant", columns.get("masks"))
+        lp_col = columns.get("logprobs")
+        lengths = [] if tok is None else [float(x) for x in torch.diff(jagged_parts(tok)[1]).tolist() if x > 0]
+        has_mask = None if mask_col is None else [True] * (jagged_parts(mask_col)[1].numel() - 1)
+    else:
+        lengths = []
+        for smp in samples:
+            t = _get(smp, "tokens")
+            if t is not None and len(t) > 0:
+                lengths.append(float(len(t)))
+        masks = []
+        for smp in samples:
+            mk = _get(smp, "mask_assistant")
+            masks.append(_get(smp, "masks") if mk is None else mk)
+        has_mask = [mk is not None for mk in masks]
+        mask_col = None if not any(has_mask) else [torch.zeros(0) if mk is None else _as_float(mk) for mk in masks]
+        lps = [_get(smp, "logprobs") for smp in samples]
+        lp_col = None if all(v is None for v in lps) else [torch.zeros(0) if v is None else _as_float(v) for v in lps]
+    if mask_col is None and lp_col is None:
+        return lengths, [], None
+    if mask_col is not None:
+        mflat, moff = jagged_parts(mask_col)
+    else:
+        mflat, moff = torch.zeros(0), torch.zeros(len(samples) + 1, dtype=torch.int64)
+    nsamp = moff.numel() - 1
+    mflat = mflat.to(device=device, dtype=torch.float32).contiguous()
+    moff_d = moff.to(device)
+    lflat = loff_d = None
+    if lp_col is not None:
+        lflat, loff = jagged_parts(lp_col)
+        lflat = lflat.to(device=device, dtype=torch.float32).contiguous()
+        loff_d = loff.to(device)
+    resp = torch.empty(max(nsamp, 1), dtype=torch.int64, device=device)
+    lp_sum = torch.empty(max(nsamp, 1), dtype=torch.float64, device=device)
+    out_off = torch.empty(nsamp + 1, dtype=torch.int64, device=device)
+    kept = torch.empty(max(lflat.numel() if lflat is not None else 0, 1), dtype=torch.float32, device=device)
+    lib = _lib.load()
+    ws = torch.empty(max(int(lib.meshy_ragged_token_stats_workspace_size(nsamp)), 1), dtype=torch.uint8,
+                     device=device)
+    rc = lib.meshy_ragged_token_stats(mflat.data_ptr(), _lib.ptr(lflat), moff_d.data_ptr(), _lib.ptr(loff_d),
+                                      nsamp, resp.data_ptr(), lp_sum.data_ptr(), out_off.data_ptr(),
+                                      _lib.ptr(kept if lflat is not None else None), ws.data_ptr(), ws.numel(),
+                                      _lib.stream_of(device))
+    _lib.check(rc, "meshy_ragged_token_stats")
+    response_lengths = []
+    if has_mask is not None:
+        response_lengths = [float(x) for x, h in zip(resp[:nsamp].tolist(), has_mask) if h]
+    logprobs = None
+    if lflat is not None:
+        n_kept = int(out_off[-1].item())
+        logprobs = (kept[:n_kept], float(lp_sum[:nsamp].sum().item()))
+    return lengths, response_lengths, logprobs
+
+
+def _as_float(v: Any) -> torch.Tensor:
+    t = v if torch.is_tensor(v) else torch.as_tensor(v)
+    return t.reshape(-1).to(torch.float32)
+
+
+def rollout_metrics(samples: Any, seq_len: int, current_version: int | None = None, *,
+                    device=None) -> tuple[dict[str, float], dict[str, Any]]:
+    """Drop-in for ``TitanTrainer._rollout_metrics`` (metrics.py:171-322)."""
+    columns = samples if isinstance(samples, dict) else None
+    if columns is not None:
+        first = next(iter(columns.values()))
+        n = first.size(0) if isinstance(first, torch.Tensor) else len(first)
+    else:
+        n = len(samples)
+    if device is None:
+        device = torch.device("cuda", torch.cuda.current_device())
+    rewards = _scalars(samples, columns, "reward")
+    raw = _scalars(samples, columns, "raw_reward")
+    raw_rewards = raw or rewards
+    shaped = bool(raw)
+    advantages = _scalars(samples, columns, "advantage")
+    weight_versions = _scalars(samples, columns, "weight_version")
+    lengths, response_lengths, lp = _token_stats(samples, columns, torch.device(device))
+
+    m: dict[str, float] = {}
+    if response_lengths:
+        m.update({
+            "rollout/response_len/max": max(response_lengths),
+            "rollout/response_len/mean": _mean(response_lengths),
+            "rollout/response_len/median": _percentile(response_lengths, 0.5),
+            "rollout/response_len/min": min(response_lengths),
+            "rollout/response_len/p0": _percentile(response_lengths, 0.0),
+            "rollout/response_len/p25": _percentile(response_lengths, 0.25),
+            "rollout/response_len/p50": _percentile(response_lengths, 0.5),
+            "rollout/response_len/p75": _percentile(response_lengths, 0.75),
+            "rollout/response_len/p90": _percentile(response_lengths, 0.9),
+            "rollout/response_len/p95": _percentile(response_lengths, 0.95),
+            "rollout/response_len/p99": _percentile(response_lengths, 0.99),
+            "rollout/response_lengths": _mean(response_lengths),
+        })
+    if lengths:
+        m["rollout/total_lengths"] = _mean(lengths)
+        m["rollout/seq_len_truncated_ratio"] = sum(v >= seq_len for v in lengths) / len(lengths)
+    truncated = _flags(samples, columns, n, "truncated")
+    if truncated is not None:
+        m["rollout/truncated_ratio"] = _mean(truncated)
+        m["rollout/truncated"] = m["rollout/truncated_ratio"]
+    repetition = _flags(samples, columns, n, "repetition")
+    if repetition is not None:
+        m["rollout/repetition_frac"] = _mean(repetition)
+    if advantages:
+        nonzero = [v for v in advantages if abs(v) > 1e-8]
+        m.update({
+            "grpo_metrics/effective_count": float(len(nonzero)),
+            "grpo_metrics/effective_ratio": len(nonzero) / len(advantages),
+            "grpo_metrics/zero_advantage_ratio": 1.0 - len(nonzero) / len(advantages),
+            "rollout/advantages": _mean(advantages),
+            "rollout/advantages_abs_mean": _mean([abs(v) for v in advantages]),
+        })
+    if rewards:
+        solved = [v > 0.5 for v in raw_rewards]
+        m.update({
+            "grpo_metrics/solve_all": float(all(solved)),
+            "grpo_metrics/solve_none": float(not any(solved)),
+            "rollout/raw_reward_mean": _mean(raw_rewards),
+            "rollout/raw_reward": _mean(raw_rewards),
+            "rollout/rewards": _mean(rewards),
+            "rollout/reward_max": max(rewards),
+            "rollout/reward_min": min(rewards),
+            "rollout/pass_rate": _mean([1.0 if s else 0.0 for s in solved]),
+        })
+        if shaped:
+            deltas = [r - w for r, w in zip(rewards, raw_rewards)]
+            m.update({
+                "rollout/shaped_reward_mean": _mean(rewards),
+                "rollout/reward_shaping_delta_mean": _mean(deltas),
+                "rollout/reward_penalised_ratio": _mean([1.0 if abs(d) > 1e-8 else 0.0 for d in deltas]),
+            })
+    kept = None
+    if lp is not None and lp[0].numel():
+        kept, total = lp
+        mean_lp = total / kept.numel()
+        m.update({"rollout/log_probs": mean_lp, "rollout/rollout_log_probs": mean_lp})
+    if weight_versions:
+        newest = max(weight_versions)
+        m.update({
+            "rollout/weight_version/mean": _mean(weight_versions),
+            "rollout/weight_version/min": min(weight_versions),
+            "rollout/weight_version/max": newest,
+            "rollout/weight_version/median": _percentile(weight_versions, 0.5),
+            "rollout/weight_version/stale_ratio": _mean([1.0 if v < newest else 0.0 for v in weight_versions]),
+            "rollout/weight_version/num_versions": float(len(set(weight_versions))),
+        })
+        if current_version is not None:
+            staleness = [float(current_version) - v for v in weight_versions]
+            m["rollout/weight_version/staleness_mean"] = _mean(staleness)
+            m["rollout/weight_version/staleness_max"] = max(staleness)
+    mixed = _flags(samples, columns, n, "mixed_version")
+    if mixed is not None:
+        m["rollout/weight_version/mixed_version_ratio"] = _mean(mixed)
+
+    hist: dict[str, Any] = {"rollout/response_lengths": response_lengths, "rollout/total_lengths": lengths}
+    if rewards:
+        hist["rollout/rewards"] = rewards
+    if shaped:
+        hist["rollout/raw_rewards"] = raw_rewards
+    if advantages:
+        hist["rollout/advantages"] = advantages
+    if kept is not None:
+        hist["rollout/log_probs"] = kept
+    return m, hist
+
+
+__all__ = ["rollout_metrics"]

@@ -34,4 +34,9 @@ Modules and what pins each one (the checks live in ``tests/test_oracle_*.py``):
     opd      layout_teacher_topk, split_teacher_topk, test_opd_batch.py:42-75, closed
              _distill_loss, _reduce_mini_metrics      forms (equal distributions -> 0,
              (opd.py:39-251)                          ln 2 per token), torch autograd
+    critic   advantages_to_per_sequence,              closed forms, torch autograd for
+             Accumulator.update, clipped_value_error  the clipped value error
+             (critic/gae.py:296-312, critic/metrics.py:238-275, vapo.py:35-41)
+    rollout_metrics  _rollout_metrics                 test_rollout_metrics.py:51-106
+             (metrics.py:72-322)
 """

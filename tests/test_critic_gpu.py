@@ -1,0 +1,175 @@
+"""Critic-side reductions, rollout statistics and the wire-format ingest against
+the oracle.
+
+Bars: per-sequence means, row values and the clipped value error within 1e-5
+(fp32), window sums within 1e-6 relative, gradients 1e-6; rollout metrics within
+1e-6 relative (sample-level values exact); packs built from wire columns equal
+packs built from samples bit for bit.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import critic as ocritic
+from oracle import rollout_metrics as orm
+
+pytestmark = pytest.mark.gpu
+
+
+def _critic_batch(rows, S, seed, lo=3):
+    g = torch.Generator().manual_seed(seed)
+    lengths = torch.randint(lo, S + 1, (rows,), generator=g)
+    mask = torch.zeros(rows, S)
+    for j, L in enumerate(lengths.tolist()):
+        p = int(torch.randint(1, max(2, L // 2), (1,), generator=g))
+        mask[j, p:L] = 1.0
+    values = torch.randn(rows, S, generator=g)
+    returns = torch.randn(rows, S, generator=g)
+    doc = torch.arange(rows).unsqueeze(1).expand(rows, S).contiguous()
+    return values, returns, mask, doc
+
+
+@pytest.mark.parametrize("rows,S", [(7, 300), (64, 4096), (1, 1)])
+def test_per_sequence_mean_padded(dev, rows, S):
+    from meshy_amd import critic
+
+    adv, _, mask, doc = _critic_batch(rows, S, seed=rows + S, lo=1)
+    mask[0] = 0.0  # a document without masked tokens -> 0
+    out = critic.advantages_to_per_sequence((adv * mask).to(dev), mask.to(dev), doc.to(dev), rows)
+    ref = ocritic.advantages_to_per_sequence(adv * mask, mask, doc, rows)
+    assert out.shape == (rows,) and (out.cpu() - ref).abs().max().item() <= 1e-5
+
+
+def test_per_sequence_mean_packed_with_padding_slot(dev):
+    from meshy_amd import critic
+
+    g = torch.Generator().manual_seed(3)
+    lens = [5, 1, 300, 77, 0, 2048]
+    ids = torch.cat([torch.full((L,), d) for d, L in enumerate(lens)] + [torch.full((40,), len(lens))])
+    n = ids.numel()
+    adv = torch.randn(1, n, generator=g)
+    mask = (torch.rand(1, n, generator=g) > 0.3).float()
+    out = critic.advantages_to_per_sequence(adv.to(dev), mask.to(dev), ids.view(1, -1).to(dev), len(lens))
+    ref = ocritic.advantages_to_per_sequence(adv, mask, ids.view(1, -1), len(lens))
+    assert (out.cpu() - ref).abs().max().item() <= 1e-5
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_accumulator_matches_oracle(dev, bf16):
+    from meshy_amd import critic
+
+    acc, ref = critic.Accumulator(), ocritic.Accumulator()
+    for k, (rows, S) in enumerate([(6, 500), (3, 4096), (1, 17)]):
+        v, r, m, _ = _critic_batch(rows, S, seed=10 + k)
+        v = v.to(torch.bfloat16) if bf16 else v
+        rewards = torch.rand(rows)
+        groups = torch.arange(rows) // 2 + 100 * k
+        acc.update(v.to(dev), r.to(dev), m.to(dev), rewards.to(dev), groups.to(dev))
+        ref.update(v, r, m, rewards, groups)
+    st, rs = acc.state, ref.state
+    for key in ("n_tokens", "sum_r", "sum_r2", "sum_d", "sum_d2"):
+        want = rs[key]
+        assert abs(getattr(st, key) - want) <= 1e-6 * max(1.0, abs(want)) + 1e-4, key
+    assert np.allclose(st.row_value, rs["row_value"], atol=1e-5)
+    assert st.row_reward == pytest.approx(rs["row_reward"]) and st.row_group == rs["row_group"]
+
+
+@pytest.mark.parametrize("clip", [None, 0.2])
+def test_clipped_value_error_fwd_bwd(dev, clip):
+    from meshy_amd import critic
+
+    g = torch.Generator().manual_seed(5)
+    v = torch.randn(4, 1000, generator=g)
+    t = torch.randn(4, 1000, generator=g)
+    o = v + torch.randn(4, 1000, generator=g) * 0.3
+    o[0, :10] = v[0, :10]          # v == old: both branches equal -> ties
+    o[1, :10] = v[1, :10] - 0.2     # |v - old| on the clamp boundary
+    w = torch.randn(4, 1000, generator=g)
+    vd = v.to(dev).requires_grad_(True)
+    out = critic.clipped_value_error(vd, t.to(dev), o.to(dev), clip)
+    vr = v.clone().requires_grad_(True)
+    ref = ocritic.clipped_value_error(vr, t, o, clip)
+    assert (out.detach().cpu() - ref).abs().max().item() <= 1e-5
+    (out * w.to(dev)).sum().backward()
+    (ref * w).sum().backward()
+    assert (vd.grad.cpu() - vr.grad).abs().max().item() <= 1e-5
+
+
+def _rollout_samples(n, seed, *, stamps=True):
+    g = torch.Generator().manual_seed(seed)
+    out = []
+    for i in range(n):
+        L = int(torch.randint(2, 3000, (1,), generator=g))
+        p = int(torch.randint(1, L, (1,), generator=g))
+        mask = torch.zeros(L)
+        mask[p:] = 1.0
+        lp = -torch.rand(L, generator=g) * 3
+        lp[:p] = 0.0
+        s = {"tokens": torch.randint(0, 151936, (L,), generator=g), "logprobs": lp, "mask_assistant": mask,
+             "advantage": torch.tensor(float(torch.randn(1, generator=g)) if i % 3 else 0.0),
+             "reward": torch.tensor(float(i % 2)), "weight_version": torch.tensor(5 - i % 3)}
+        if stamps:
+            s.update(truncated=torch.tensor(i % 4 == 0, dtype=torch.int64),
+                     repetition=torch.tensor(i % 5 == 0, dtype=torch.int64),
+                     mixed_version=torch.tensor(i % 7 == 0, dtype=torch.int64),
+                     raw_reward=torch.tensor(float(i % 2) + (0.25 if i % 3 == 0 else 0.0)))
+        out.append(s)
+    return out
+
+
+def _compare(m, hist, rm, rh):
+    assert set(m) == set(rm)
+    for k, want in rm.items():
+        assert m[k] == pytest.approx(want, rel=1e-6, abs=1e-9), k
+    assert set(hist) == set(rh)
+    for k, want in rh.items():
+        got = hist[k]
+        got = got.cpu().tolist() if torch.is_tensor(got) else got
+        assert np.allclose(got, want, atol=1e-7), k
+
+
+@pytest.mark.parametrize("stamps", [True, False])
+def test_rollout_metrics_match_oracle(dev, stamps):
+    from meshy_amd.rollout_metrics import rollout_metrics
+
+    samples = _rollout_samples(40, seed=1, stamps=stamps)
+    samples[3]["logprobs"] = samples[3]["logprobs"][:-5]  # shorter than its mask: every log-prob is kept
+    del samples[4]["mask_assistant"]                        # no mask: no response length
+    m, hist = rollout_metrics(samples, seq_len=2048, current_version=6)
+    rm, rh = orm.rollout_metrics(samples, seq_len=2048, current_version=6)
+    _compare(m, hist, rm, rh)
+
+
+def test_rollout_metrics_from_wire_columns(dev):
+    from meshy_amd import wire
+    from meshy_amd.rollout_metrics import rollout_metrics
+
+    samples = _rollout_samples(25, seed=2)
+    fields = ["tokens", "logprobs", "mask_assistant", "advantage", "reward", "raw_reward", "weight_version",
+              "truncated", "repetition", "mixed_version"]
+    cols = wire.samples_to_columns(samples, fields)
+    m, hist = rollout_metrics(cols, seq_len=1024, current_version=9)
+    rm, rh = orm.rollout_metrics(samples, seq_len=1024, current_version=9)
+    _compare(m, hist, rm, rh)
+
+
+@pytest.mark.parametrize("layout", ["packed", "padded"])
+def test_pack_from_wire_columns_equals_pack_from_samples(dev, layout):
+    from meshy_amd import wire, workloads
+    from meshy_amd.pipeline import RaggedSamples, pack_step
+    from meshy_amd.plan import PlannerConfig
+
+    batch, rewards, group_offsets = workloads.config0(0)
+    samples = batch.sample_dicts(rewards=rewards)
+    cols = wire.samples_to_columns(samples, ["tokens", "mask_assistant", "logprobs", "reward"])
+    cfg = PlannerConfig(layout=layout, mini_batch_size=256, seq_len=8192, align=2048,
+                        max_tokens_per_micro=8192 if layout == "packed" else None,
+                        micro_batch_size=None if layout == "packed" else 4)
+    a = pack_step(RaggedSamples.from_samples(samples, group_offsets), cfg, dev)
+    b = pack_step(RaggedSamples.from_columns(cols, group_offsets), cfg, dev)
+    assert a.plan == b.plan
+    assert torch.equal(a.advantages, b.advantages)
+    for x, y in zip(a.batches, b.batches):
+        for f in ("input_ids", "labels", "positions", "mask", "doc_ids", "rollout_logprobs", "advantages"):
+            assert torch.equal(getattr(x, f), getattr(y, f)), f
