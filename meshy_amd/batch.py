@@ -106,14 +106,13 @@ class _Layout:
         self.regions: dict[str, tuple[int, int, torch.dtype]] = {}
 
     def add(self, name: str, n: int, dtype: torch.dtype) -> None:
-        esize = torch.empty((), dtype=dtype).element_size()
-        self.regions[name] = (self.size, n, dtype)
-        self.size += (n * esize + 255) // 256 * 256
+        nbytes = n * dtype.itemsize
+        self.regions[name] = (self.size, self.size + nbytes, dtype)
+        self.size += (nbytes + 255) // 256 * 256
 
     def view(self, buf: torch.Tensor, name: str) -> torch.Tensor:
-        off, n, dtype = self.regions[name]
-        esize = torch.empty((), dtype=dtype).element_size()
-        return buf[off:off + n * esize].view(dtype)
+        lo, hi, dtype = self.regions[name]
+        return buf[lo:hi].view(dtype)
 
 
 def _scalar(td, key: str, default: float = 0.0) -> float:

@@ -218,8 +218,10 @@ extern "C" int meshy_sample_loss_tokens(const float* mask, const int64_t* offset
                                       static_cast<long long>(i));
         lengths[i] = len;
         const int64_t L = std::min(len, seq_len);
-        int64_t c = 0;
-        for (int64_t t = 1; t < L; ++t) c += mask[a + t] > 0.f ? 1 : 0;
+        // Branch-free so the compiler vectorises the count.
+        int32_t c = 0;
+        const float* m = mask + a;
+        for (int64_t t = 1; t < L; ++t) c += static_cast<int32_t>(m[t] > 0.f);
         loss_tokens[i] = L > 1 ? c : 0;
     }
     return MESHY_OK;

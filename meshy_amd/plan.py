@@ -158,6 +158,13 @@ class PlanTables:
         return out
 
 
+def _as_int64(x: Sequence[int]) -> np.ndarray:
+    """A contiguous int64 copy of ``x`` (no Python loop when it is already an array)."""
+    if isinstance(x, np.ndarray) and x.dtype.kind in "iu":
+        return np.ascontiguousarray(x, dtype=np.int64)
+    return np.ascontiguousarray(np.asarray([int(v) for v in x], dtype=np.int64))
+
+
 def plan_tables(
     lengths: Sequence[int], loss_tokens: Sequence[int], dp_size: int, cfg: PlannerConfig
 ) -> PlanTables:
@@ -173,8 +180,8 @@ def plan_tables(
             "rollout.batch_size * group_size to a multiple of dp_replicate * dp_shard"
         )
     lib = _lib.load()
-    lens = np.ascontiguousarray(np.asarray([int(x) for x in lengths], dtype=np.int64))
-    loss = np.ascontiguousarray(np.asarray([int(x) for x in loss_tokens], dtype=np.int64))
+    lens = _as_int64(lengths)
+    loss = _as_int64(loss_tokens)
     c = _lib.PlannerCfg()
     c.layout = _lib.MESHY_LAYOUT_PACKED if cfg.layout == "packed" else _lib.MESHY_LAYOUT_PADDED
     c.mini_batch_size = cfg.mini_batch_size
