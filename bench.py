@@ -661,6 +661,9 @@ def main() -> int:
     ap.add_argument("--cpu-rows", type=int, default=1024)
     ap.add_argument("--no-cpu", action="store_true", help="skip every CPU reference timing")
     ap.add_argument("--quick", action="store_true", help="headline kernel only")
+    ap.add_argument("--pmc-kernels", action="store_true",
+                    help="for counter runs: Top-K (K = 8) x 3, logprob backward x 3 and a device copy x 3 over "
+                         "the [16384, 151936] logits, no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the hot path's kernels run per GPU and no multi-GPU figure "
@@ -673,6 +676,8 @@ def main() -> int:
         print("bench.py needs a HIP device", file=sys.stderr)
         return 2
     torch.set_num_threads(os.cpu_count() or 1)
+    if args.pmc_kernels:
+        return pmc_kernels()
 
     ms, nbytes, logits, labels = bench_logprob(args.steps, args.warmup)
     achieved = nbytes / (ms * 1e-3) / 1e9
@@ -732,6 +737,35 @@ def main() -> int:
         if result.get("cpu_baseline"):
             result["cpu_baseline"]["host"] = _host_info()
     print(json.dumps(result), flush=True)
+    return 0
+
+
+def pmc_kernels() -> int:
+    """The dispatches the HBM-traffic counter runs read: each big kernel three
+    times, then a device copy of known size (4,978,638,848 B) to calibrate."""
+    import torch
+
+    from meshy_amd import _lib, logprob, topk
+
+    dev = torch.device("cuda:0")
+    gen = torch.Generator(device=dev).manual_seed(1)
+    z = torch.randn(1, T_TOK, VOCAB, generator=gen, device=dev, dtype=torch.bfloat16) * 2.0
+    y = torch.randint(0, VOCAB, (1, T_TOK), generator=gen, device=dev)
+    for _ in range(3):
+        topk.teacher_topk(z, 8)
+    lse = logprob.logsumexp_rows(z)
+    gl = torch.ones(1, T_TOK, device=dev)
+    grad = torch.empty_like(z)
+    ws = logprob.bwd_workspace(T_TOK, dev)
+    lib = _lib.load()
+    for _ in range(3):
+        _lib.check(lib.meshy_logprob_bwd(z.data_ptr(), 1, T_TOK, VOCAB, z.stride(0), z.stride(1), y.data_ptr(),
+                                         lse.data_ptr(), gl.data_ptr(), grad.data_ptr(), ws.data_ptr(), ws.numel(),
+                                         _lib.stream_of(dev)), "meshy_logprob_bwd")
+    for _ in range(3):
+        grad.copy_(z)
+    torch.cuda.synchronize()
+    print("pmc kernels done", flush=True)
     return 0
 
 
