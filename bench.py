@@ -151,6 +151,25 @@ def bench_logprob_bwd(logits, labels, steps, warmup):
     return ms, rows * T * V * 4 + rows * T * 16
 
 
+def cpu_logprob_bwd_ms(logits_gpu, labels_gpu, rows: int) -> float:
+    """The reference's backward of a logprob chunk on CPU torch: the checkpointed
+    recompute of -cross_entropy(z.float(), y) plus autograd (trainer.py:504-517),
+    on a row sample, scaled to every row."""
+    import torch
+
+    from oracle import logprob as olp
+
+    z = logits_gpu[:, :rows].cpu()
+    y = labels_gpu[:, :rows].cpu()
+    g = torch.ones(z.shape[0], rows)
+
+    def cpu():
+        zr = z.detach().requires_grad_(True)
+        (olp.chunk_logprobs(zr, y) * g).sum().backward()
+
+    return _wall_ms(cpu, 3, gpu=False) * logits_gpu.shape[1] / rows
+
+
 def cpu_logprob_tokens_per_s(logits_gpu, labels_gpu, rows: int, runs: int = 5):
     import torch
 
@@ -195,7 +214,22 @@ def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
                                                    cpu_sample=f"{cpu_rows} rows, scaled to T" if cpu_ms else None)
     ids = torch.cat([t_ids, labels.unsqueeze(-1)], -1).contiguous()
     ms = _gpu_ms(lambda: topk.gather_logprobs(logits, ids), steps, warmup)
-    out["gather_logprobs_K9_fwd"] = _entry(ms * 1e3, T * V * 2 + T * (K + 1) * 12)
+    cpu_ms = cpu_bwd_ms = None
+    if not no_cpu:
+        from oracle import topk as otopk
+
+        zc = logits[:, :cpu_rows].cpu()
+        ic = ids[:, :cpu_rows].cpu()
+        cpu_ms = _wall_ms(lambda: otopk.gather_logprobs(zc, ic), 3, gpu=False) * T / cpu_rows
+        wc = torch.randn(rows, cpu_rows, K + 1)
+
+        def cpu_bwd():
+            zr = zc.detach().requires_grad_(True)  # bf16 leaf, as the model's logits
+            (otopk.gather_logprobs(zr, ic) * wc).sum().backward()
+
+        cpu_bwd_ms = _wall_ms(cpu_bwd, 3, gpu=False) * T / cpu_rows
+    out["gather_logprobs_K9_fwd"] = _entry(ms * 1e3, T * V * 2 + T * (K + 1) * 12, cpu_ms,
+                                           cpu_sample=f"{cpu_rows} rows, scaled to T" if cpu_ms else None)
     lse = logprob.logsumexp_rows(logits)
     g = torch.randn(rows, T, K + 1, device=dev)
     grad = torch.empty_like(logits)
@@ -209,7 +243,10 @@ def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
                                                  _lib.stream_of(dev)), "meshy_gather_logprobs_bwd")
 
     ms = _gpu_ms(bwd, max(5, steps // 2), 2)
-    out["gather_logprobs_K9_bwd"] = _entry(ms * 1e3, T * V * 4 + T * (K + 1) * 12)
+    out["gather_logprobs_K9_bwd"] = _entry(
+        ms * 1e3, T * V * 4 + T * (K + 1) * 12, cpu_bwd_ms,
+        cpu_sample=(f"{cpu_rows} rows, scaled to T; the reference's recompute of the chunk plus autograd"
+                    if cpu_bwd_ms else None))
     del grad
     # distillation loss over the T tokens: 12 documents, gathered log-probs from the kernel above
     gathered = topk.gather_logprobs(logits, ids)
@@ -225,14 +262,29 @@ def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
     gd = gathered.detach().requires_grad_(True)
 
     def loss_fb():
+        mb.__dict__.pop("_meshy_seg_offsets", None)  # a fresh micro-batch each call
         gd.grad = None
         loss, _ = opd.distill_from_gathered(stub, gd, mb, mini)
         loss.backward()
 
     ms = _gpu_ms(loss_fb, steps, warmup)
+    cpu_ms = None
+    if not no_cpu:
+        from oracle import opd as oopd
+
+        gc, tc, mc, dc, rc = (gathered.detach().cpu(), t_lps.cpu(), mask.cpu(), doc_ids.cpu(),
+                              mb.rollout_logprobs.cpu())
+
+        def cpu_loss():
+            g2 = gc.clone().requires_grad_(True)
+            loss, _ = oopd.distill_loss(g2, tc, mc, dc, n_docs, rollout_lp=rc, n_docs_global=n_docs,
+                                        n_tokens_global=T, per_token_loss=False)
+            loss.backward()
+
+        cpu_ms = _wall_ms(cpu_loss, 5, gpu=False)
     # fwd reads student (K+1)*4 + teacher K*4 + mask 4 + rollout 4; bwd reads the same, writes (K+1)*4
     per_tok = (K + 1) * 4 + K * 4 + 8
-    out["distill_loss_fwd_bwd_K8_T16384"] = _entry(ms * 1e3, T * (2 * per_tok + (K + 1) * 4), tokens=T)
+    out["distill_loss_fwd_bwd_K8_T16384"] = _entry(ms * 1e3, T * (2 * per_tok + (K + 1) * 4), cpu_ms, tokens=T)
     return out
 
 
@@ -334,11 +386,15 @@ def bench_ppo(steps, warmup, no_cpu):
     old_d = torch.from_numpy(old).reshape(1, -1).to(dev)
     new_d = torch.from_numpy(new).reshape(1, -1).to(dev).requires_grad_(True)
 
+    # Each call sees a fresh micro-batch: the document offsets a batch caches
+    # after its first loss call are dropped, so they are paid for every time.
     def fwd():
+        mb.__dict__.pop("_meshy_seg_offsets", None)
         with torch.no_grad():
             ppo_clip_loss(stub, new_d, old_d, mb, mini)
 
     def fwd_bwd():
+        mb.__dict__.pop("_meshy_seg_offsets", None)
         new_d.grad = None
         loss, _ = ppo_clip_loss(stub, new_d, old_d, mb, mini)
         loss.backward()
@@ -446,6 +502,102 @@ def bench_gae(steps, warmup, no_cpu):
         cpu_ms = _wall_ms(cpu, 3, gpu=False)
     # reads rewards 4 + values 2 + mask 4 + doc id 8, writes adv 4 + returns 4
     return _entry(ms * 1e3, T * 26, cpu_ms, tokens=T, docs=n, cpu_sample="sequential loop on padded [1024, S_max]")
+
+
+# ---------------------------------------------------------------- row 20 at config 4, pack at config 3
+
+def bench_attach_gae(runs, no_cpu):
+    """_attach_gae_advantages over config 4's 1024 samples (values bf16, terminal
+    rewards, constant lambda 0.95): GPU wall per call, samples staged from the host."""
+    from types import SimpleNamespace as NS
+
+    import numpy as np
+    import torch
+
+    from meshy_amd import workloads
+    from meshy_amd.gae import attach_gae_advantages
+
+    dev = torch.device("cuda:0")
+    batch, values, terminal = workloads.config4(4)
+    samples = []
+    for i in range(len(batch.lengths)):
+        a, b = int(batch.offsets[i]), int(batch.offsets[i + 1])
+        samples.append({"tokens": torch.zeros(b - a, dtype=torch.int64),
+                        "mask_assistant": torch.from_numpy(batch.mask[a:b].copy()),
+                        "values": torch.from_numpy(values[a:b].copy()).to(torch.bfloat16),
+                        "reward": torch.tensor(float(terminal[i]))})
+    trainer = NS(seq_len=32768 + 256, gae_gamma=1.0, gae_alpha=1.5, gae_lambda=0.95, device=dev)
+    ms = _wall_ms(lambda: attach_gae_advantages(trainer, samples), runs, warmup=2)
+    out = {"gpu_ms": round(ms, 3), "samples": len(samples), "tokens": int(batch.total)}
+    if not no_cpu:
+        from oracle import gae as ogae
+
+        fs = [{k: (v.float() if k == "values" else v) for k, v in smp.items()} for smp in samples]
+        cms = _wall_ms(lambda: ogae.attach_gae_advantages(fs, seq_len=trainer.seq_len, gamma=1.0, alpha=1.5,
+                                                          gae_lambda=0.95), 2, warmup=0, gpu=False)
+        out["cpu_ms"] = round(cms, 1)
+        out["speedup_vs_cpu"] = round(cms / ms, 1)
+        out["cpu_sample"] = "the reference's padded [1024, S_max] block and sequential scan"
+    return out
+
+
+def bench_pack_long_context(runs, no_cpu):
+    """Config 3: 16 samples U{8192..131072} under a 131072-token budget, align 2048."""
+    import numpy as np
+    import torch
+
+    from meshy_amd import workloads
+    from meshy_amd.pipeline import RaggedSamples, pack_step
+    from meshy_amd.plan import PlannerConfig
+
+    dev = torch.device("cuda:0")
+    rng = np.random.default_rng(3)
+    lengths = workloads.config3_lengths(3)
+    offsets = np.zeros(len(lengths) + 1, np.int64)
+    np.cumsum(lengths, out=offsets[1:])
+    total = int(offsets[-1])
+    tokens = rng.integers(0, 131072, total, dtype=np.int32)
+    pos = np.arange(total) - np.repeat(offsets[:-1], lengths)
+    prompt = np.repeat(rng.integers(64, 257, len(lengths)), lengths)
+    mask = (pos >= prompt).astype(np.float32)
+    lps = (-rng.uniform(0.0, 2.0, total)).astype(np.float32)
+    rewards = (rng.random(len(lengths)) < 0.4).astype(np.float32)
+    group_offsets = np.array([0, 8, 16], np.int64)
+    ragged = RaggedSamples.from_arrays(tokens, mask, lps, offsets, rewards, group_offsets)
+    cfg = PlannerConfig(layout="packed", mini_batch_size=16, seq_len=131072, align=2048,
+                        max_tokens_per_micro=131072)
+    res = {}
+    ms = _wall_ms(lambda: res.__setitem__("r", pack_step(ragged, cfg, dev)), runs, warmup=2)
+    r = res["r"]
+    n_out = sum(mb.input_ids.numel() for mb in r.batches)
+    out = {"pack_latency_us": round(ms * 1e3, 1), "n_micro": len(r.batches), "tokens": total, "out_tokens": n_out,
+           "bytes": total * 12 + n_out * 40}
+    out["GBps"] = round(out["bytes"] / (ms * 1e-3) / 1e9, 1)
+    if not no_cpu:
+        from oracle import batch as obatch
+        from oracle import grpo as ogrpo
+        from oracle import plan as oplan
+
+        samples = []
+        for i in range(len(lengths)):
+            a, b = int(offsets[i]), int(offsets[i + 1])
+            samples.append({"tokens": torch.from_numpy(tokens[a:b].astype(np.int64)),
+                            "mask_assistant": torch.from_numpy(mask[a:b].copy()),
+                            "logprobs": torch.from_numpy(lps[a:b].copy()), "reward": float(rewards[i])})
+
+        def cpu():
+            ln, loss = oplan.sample_lengths(samples, 131072)
+            local, per_rank = oplan.build_plan(ln, loss, 1, layout="packed", mini_batch_size=16, seq_len=131072,
+                                               align=2048, max_tokens_per_micro=131072)
+            adv = ogrpo.grpo_group([float(x) for x in rewards[:8]]) + ogrpo.grpo_group([float(x) for x in rewards[8:]])
+            loc = [dict(samples[i], advantage=adv[i]) for i in local[0]]
+            for micros, *_ in per_rank[0]:
+                for idx, seq_len, doc_lens in micros:
+                    obatch.build_micro_batch(loc, idx, seq_len, doc_lens, layout="packed", need_rollout_lp=True)
+
+        out["cpu_ms"] = round(_wall_ms(cpu, 3, gpu=False), 2)
+        out["speedup_vs_cpu"] = round(out["cpu_ms"] / ms, 1)
+    return out
 
 
 # ---------------------------------------------------------------- critic reductions and rollout metrics
@@ -719,7 +871,9 @@ def main() -> int:
                                                       "frac_hbm": round(read_ceiling / HBM_PEAK_GBS, 4)}}
     if not args.quick:
         bms, bbytes = bench_logprob_bwd(logits, labels, max(5, args.steps // 2), 2)
-        kernels["logprob_bwd_T16384_V151936"] = _entry(bms * 1e3, bbytes)
+        bcpu = None if args.no_cpu else cpu_logprob_bwd_ms(logits, labels, 512)
+        kernels["logprob_bwd_T16384_V151936"] = _entry(bms * 1e3, bbytes, bcpu,
+                                                       cpu_sample="512 rows, scaled to T" if bcpu else None)
         kernels["opd"] = bench_opd(logits, labels, args.steps, args.warmup, args.no_cpu)
     del logits, labels
     torch.cuda.empty_cache()
@@ -731,6 +885,8 @@ def main() -> int:
         kernels["gae_returns_config4"] = bench_gae(args.steps, args.warmup, args.no_cpu)
         kernels["logprob_entropy_config3"] = bench_long_context(max(3, args.steps // 10), 2, args.no_cpu)
         kernels["critic"] = bench_critic(args.steps, args.warmup, args.no_cpu)
+        kernels["attach_gae_config4"] = bench_attach_gae(5, args.no_cpu)
+        kernels["pack_grpo_config3"] = bench_pack_long_context(10, args.no_cpu)
         kernels["rollout_metrics_config0"] = bench_rollout_metrics(10, args.no_cpu)
         result["kernels"] = kernels
         result["end_to_end"] = bench_end_to_end(5, args.no_cpu)

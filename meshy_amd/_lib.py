@@ -344,10 +344,17 @@ def ptr(t) -> int | None:
 
 
 def stream_of(device) -> int:
-    """The current HIP stream of `device` as an integer handle."""
+    """The current HIP stream of `device` as an integer handle (the raw getter:
+    no Stream object is built on the hot path)."""
     import torch
 
-    return torch.cuda.current_stream(device).cuda_stream
+    if isinstance(device, int):
+        idx = device
+    else:
+        idx = device.index if isinstance(device, torch.device) else torch.device(device).index
+        if idx is None:
+            idx = torch.cuda.current_device()
+    return torch._C._cuda_getCurrentRawStream(idx)
 
 
 def require_gpu(*tensors) -> None:

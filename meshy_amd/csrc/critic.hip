@@ -49,15 +49,30 @@ __global__ __launch_bounds__(kThreads) void k_seq_mean(const float* __restrict__
     __shared__ float s_a[kWaves], s_b[kWaves];
     const int64_t d = blockIdx.x;
     const int64_t lo = seg_off[d], hi = seg_off[d + 1];
-    float sx = 0.f, sm = 0.f;
-    for (int64_t i = lo + threadIdx.x; i < hi; i += kThreads) {
-        const float m = mask[i];
-        sx = fmaf(x[i], m, sx);
-        sm += m;
+    // Four independent accumulator pairs keep four loads of each stream in flight.
+    float sx[4] = {0.f, 0.f, 0.f, 0.f}, sm[4] = {0.f, 0.f, 0.f, 0.f};
+    int64_t i = lo + threadIdx.x;
+    for (; i + 3 * kThreads < hi; i += 4 * kThreads) {
+        float m[4], v[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            m[u] = mask[i + u * kThreads];
+            v[u] = x[i + u * kThreads];
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            sx[u] = fmaf(v[u], m[u], sx[u]);
+            sm[u] += m[u];
+        }
     }
-    sx = block_sum_to0(sx, s_a);
-    sm = block_sum_to0(sm, s_b);
-    if (threadIdx.x == 0) out[d] = sx / fmaxf(sm, 1.f);
+    for (; i < hi; i += kThreads) {
+        const float m = mask[i];
+        sx[0] = fmaf(x[i], m, sx[0]);
+        sm[0] += m;
+    }
+    const float tx = block_sum_to0((sx[0] + sx[1]) + (sx[2] + sx[3]), s_a);
+    const float tm = block_sum_to0((sm[0] + sm[1]) + (sm[2] + sm[3]), s_b);
+    if (threadIdx.x == 0) out[d] = tx / fmaxf(tm, 1.f);
 }
 
 __device__ __forceinline__ float load_value(const void* v, int bf16, int64_t i) {
@@ -65,6 +80,22 @@ __device__ __forceinline__ float load_value(const void* v, int bf16, int64_t i) 
 }
 
 // One workgroup per row: row sums into part[row][5] (fp64) and row_value[row].
+// Each thread sums its ~S/256 elements in fp32 (two interleaved halves for
+// latency), the workgroup combines the threads in fp64.
+__device__ __forceinline__ void acc_elem(const void* values, int values_bf16, const float* returns,
+                                         const float* mask, int64_t i, float (&a)[kAccSums + 1]) {
+    const float m = mask[i] > 0.f ? 1.f : 0.f;
+    const float v = load_value(values, values_bf16, i) * m;
+    const float r = returns[i] * m;
+    const float dv = v - r;
+    a[0] += m;
+    a[1] += r;
+    a[2] = fmaf(r, r, a[2]);
+    a[3] += dv;
+    a[4] = fmaf(dv, dv, a[4]);
+    a[5] += v;
+}
+
 __global__ __launch_bounds__(kThreads) void k_acc_rows(const void* __restrict__ values, int values_bf16,
                                                        const float* __restrict__ returns,
                                                        const float* __restrict__ mask, int64_t S,
@@ -72,20 +103,17 @@ __global__ __launch_bounds__(kThreads) void k_acc_rows(const void* __restrict__ 
     __shared__ double s_red[kAccSums + 1][kWaves];
     const int64_t row = blockIdx.x;
     const int64_t base = row * S;
-    double acc[kAccSums + 1] = {0.0, 0.0, 0.0, 0.0, 0.0, 0.0};  // m, r, r2, d, d2, v
-    for (int64_t j = threadIdx.x; j < S; j += kThreads) {
-        const int64_t i = base + j;
-        const float m = mask[i] > 0.f ? 1.f : 0.f;
-        const float v = load_value(values, values_bf16, i) * m;
-        const float r = returns[i] * m;
-        const float dv = v - r;
-        acc[0] += m;
-        acc[1] += r;
-        acc[2] += static_cast<double>(r) * r;
-        acc[3] += dv;
-        acc[4] += static_cast<double>(dv) * dv;
-        acc[5] += v;
+    float a0[kAccSums + 1] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // m, r, r2, d, d2, v
+    float a1[kAccSums + 1] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
+    int64_t j = threadIdx.x;
+    for (; j + kThreads < S; j += 2 * kThreads) {
+        acc_elem(values, values_bf16, returns, mask, base + j, a0);
+        acc_elem(values, values_bf16, returns, mask, base + j + kThreads, a1);
     }
+    if (j < S) acc_elem(values, values_bf16, returns, mask, base + j, a0);
+    double acc[kAccSums + 1];
+#pragma unroll
+    for (int k = 0; k <= kAccSums; ++k) acc[k] = static_cast<double>(a0[k]) + static_cast<double>(a1[k]);
     const int lane = threadIdx.x % kWave;
     const int wid = threadIdx.x / kWave;
 #pragma unroll

@@ -156,15 +156,16 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
     const int64_t t0 = b * kTile;
     const int64_t t1 = min(t0 + kTile, a.n_tokens);
     const int64_t n_slots = a.n_docs + 1;
-    if (threadIdx.x == 0) {
-        s_range[0] = doc_of(a.seg_offsets, n_slots, t0);
-        s_range[1] = doc_of(a.seg_offsets, n_slots, t1 - 1);
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+    // The tile's first and last documents, searched by waves 0 and 1 at once.
+    if (wid < 2) {
+        const int64_t d = doc_of_wave(a.seg_offsets, n_slots, wid == 0 ? t0 : t1 - 1);
+        if (lane == 0) s_range[wid] = d;
     }
     __syncthreads();
     const int64_t d_first = s_range[0];
     const int64_t nd = s_range[1] - d_first + 1;
-    const int lane = threadIdx.x % kWave;
-    const int wid = threadIdx.x / kWave;
     float acc[kTokSums];
 #pragma unroll
     for (int k = 0; k < kTokSums; ++k) acc[k] = 0.f;
@@ -429,9 +430,10 @@ __global__ __launch_bounds__(kThreads) void k_ppo_bwd(meshy_ppo_args a, const fl
     const int64_t t0 = b * kTile;
     const int64_t t1 = min(t0 + kTile, a.n_tokens);
     const int64_t n_slots = a.n_docs + 1;
-    if (threadIdx.x == 0) {
-        s_range[0] = doc_of(a.seg_offsets, n_slots, t0);
-        s_range[1] = doc_of(a.seg_offsets, n_slots, t1 - 1);
+    const int wid = threadIdx.x / kWave;
+    if (wid < 2) {
+        const int64_t d = doc_of_wave(a.seg_offsets, n_slots, wid == 0 ? t0 : t1 - 1);
+        if (threadIdx.x % kWave == 0) s_range[wid] = d;
     }
     __syncthreads();
     const int64_t d_first = s_range[0];

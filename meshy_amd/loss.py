@@ -22,6 +22,24 @@ import torch.distributed as dist
 from . import _lib
 
 
+def batch_segment_offsets(mb: Any) -> torch.Tensor:
+    """``segment_offsets`` of a micro-batch's ``doc_ids`` over its ``n_docs + 1``
+    slots, cached on the batch object: the PPO and distillation losses of one
+    micro (forward, backward, later epochs) share it.  The cache key includes the
+    tensor's version counter, so an in-place change of ``doc_ids`` recomputes."""
+    ids = mb.doc_ids
+    key = (id(ids), ids._version, ids.data_ptr(), int(mb.n_docs))
+    hit = getattr(mb, "_meshy_seg_offsets", None)
+    if hit is not None and hit[0] == key:
+        return hit[1]
+    off = segment_offsets(ids, int(mb.n_docs) + 1)
+    try:
+        object.__setattr__(mb, "_meshy_seg_offsets", (key, off))
+    except (AttributeError, TypeError):
+        pass  # a batch type without an attribute dict: no cache
+    return off
+
+
 def segment_offsets(doc_ids: torch.Tensor, n_slots: int, check_sorted: bool = False) -> torch.Tensor:
     """Token offsets of each document slot of a non-decreasing ``doc_ids`` tensor."""
     ids = doc_ids.reshape(-1).to(torch.int64).contiguous()
@@ -62,7 +80,7 @@ class _Inputs:
             self.pos_w = mb.positive_lm_weights.reshape(-1).to(torch.float32).contiguous()
         _lib.require_gpu(new_lp, self.old, self.mask, self.adv, mb.doc_ids, self.rollout, self.entropy,
                          self.pos_w)
-        self.seg_off = segment_offsets(mb.doc_ids, self.n_docs + 1)
+        self.seg_off = batch_segment_offsets(mb)
         ws = _lib.load().meshy_ppo_workspace_size(self.n_tokens, self.n_docs)
         self.workspace = torch.empty(max(int(ws), 1), dtype=torch.uint8, device=dev)
         self.clip_low = float(stub.ppo_clip_eps_low)
@@ -155,13 +173,16 @@ def ppo_clip_loss(
     if not new_flat.is_contiguous():
         new_flat = new_flat.contiguous()
     loss, out = _PPOLoss.apply(new_flat, inputs)
+    # One unbind makes every 0-dim view at once (indexing one by one costs
+    # more host time than the kernels).
+    parts = out.unbind(0)
     names = _lib.PPO_OUT_NAMES
-    sums = {names[k]: out[k] for k in range(12)}
+    sums = dict(zip(names[:12], parts[:12]))
     if inputs.rollout is not None:
-        sums["train_rollout_kl_sum"] = out[12]
-        sums["train_rollout_logdiff_abs_sum"] = out[13]
+        sums["train_rollout_kl_sum"] = parts[12]
+        sums["train_rollout_logdiff_abs_sum"] = parts[13]
     if inputs.entropy is not None:
-        sums["entropy_sum"] = out[14]
+        sums["entropy_sum"] = parts[14]
     return loss, sums
 
 
@@ -196,4 +217,4 @@ def reduce_mini_metrics(self: Any, sums: dict[str, torch.Tensor]) -> dict[str, f
     return out
 
 
-__all__ = ["ppo_clip_loss", "reduce_mini_metrics", "segment_offsets"]
+__all__ = ["batch_segment_offsets", "ppo_clip_loss", "reduce_mini_metrics", "segment_offsets"]

@@ -25,7 +25,7 @@ import torch.distributed as dist
 
 from . import _lib
 from .batch import TEACHER_FIELDS, Batch, launch_pack, stage_micro_batches
-from .loss import segment_offsets
+from .loss import batch_segment_offsets
 from .plan import Layout, MicroPlan
 from .topk import gather_logprobs
 
@@ -120,7 +120,7 @@ class _Inputs:
         self.rollout = (None if mb.rollout_logprobs is None else
                         mb.rollout_logprobs.detach().reshape(-1).to(torch.float32).contiguous())
         _lib.require_gpu(self.teacher, self.mask, mb.doc_ids, self.rollout)
-        self.seg_off = segment_offsets(mb.doc_ids, self.n_docs + 1)
+        self.seg_off = batch_segment_offsets(mb)
         ws = _lib.load().meshy_distill_workspace_size(n_tokens, self.n_docs)
         self.workspace = torch.empty(max(int(ws), 1), dtype=torch.uint8, device=device)
         self.lp_min = getattr(stub, "log_prob_min_clamp", None)
@@ -196,11 +196,12 @@ def distill_from_gathered(self: Any, gathered: torch.Tensor, mb: Any, mini: Any)
         student = student.contiguous()
     inputs = _Inputs(self, mb, mini, k, student.shape[0], student.device)
     loss, out = _DistillLoss.apply(student, inputs)
+    parts = out.unbind(0)
     names = _lib.DISTILL_OUT_NAMES
-    sums = {names[j]: out[j] for j in range(4)}
+    sums = dict(zip(names[:4], parts[:4]))
     if inputs.rollout is not None:
-        sums["train_rollout_kl_sum"] = out[4]
-        sums["train_rollout_logdiff_abs_sum"] = out[5]
+        sums["train_rollout_kl_sum"] = parts[4]
+        sums["train_rollout_logdiff_abs_sum"] = parts[5]
     return loss, sums
 
 

@@ -253,3 +253,30 @@ def test_deterministic(dev):
         outs.append((loss.item(), torch.stack(list(sums.values())).cpu(), nd.grad.cpu()))
     assert outs[0][0] == outs[1][0]
     assert torch.equal(outs[0][1], outs[1][1]) and torch.equal(outs[0][2], outs[1][2])
+
+
+def test_segment_offsets_cache_follows_doc_ids(dev):
+    """A batch caches its document offsets after the first loss call; replacing
+    or editing doc_ids in place recomputes them."""
+    from meshy_amd.loss import batch_segment_offsets, ppo_clip_loss
+    from meshy_amd.plan import MiniPlan
+
+    mb = _batch(dev, rows=1, S=8)
+    mb.doc_ids = torch.tensor([[0, 0, 0, 0, 0, 1, 1, 1]], device=dev)
+    mb.advantages = torch.tensor([1.0], device=dev)
+    mb.n_docs = 1
+    a = batch_segment_offsets(mb)
+    assert a.tolist() == [0, 5, 8]
+    assert batch_segment_offsets(mb) is a  # cached
+    mb.doc_ids[0, 5:] = 0  # in place: every token now in document 0, padding slot empty
+    b = batch_segment_offsets(mb)
+    assert b is not a and b.tolist() == [0, 8, 8]
+    mini = MiniPlan(micros=(), n_docs_global=1, n_tokens_global=int(mb.mask.sum()), tokens_per_rank=(8,))
+    old = -torch.ones(1, 8, device=dev)
+    new = (old + 0.05).requires_grad_()
+    loss, _ = ppo_clip_loss(_stub(), new, old, mb, mini)
+    ref, _ = oppo.ppo_clip_loss(new.detach().cpu().requires_grad_(True), old.cpu(), mb.mask.cpu(),
+                                mb.doc_ids.cpu(), mb.advantages.cpu(), 1, n_docs_global=1,
+                                n_tokens_global=mini.n_tokens_global, clip_low=0.2, clip_high=0.28,
+                                per_token_loss=True, use_tis=True, tis_min=0.5, tis_max=5.0)
+    assert abs(float(loss) - float(ref)) <= TOL
