@@ -1,0 +1,105 @@
+"""Argument validation of the C ABI (CPU only): every device entry point rejects
+bad shapes, NULL pointers and short workspaces with a negative MESHY_E* code
+and a message, before anything reaches a device.  No call here passes its
+checks, so no kernel is launched."""
+
+from __future__ import annotations
+
+import ctypes
+
+import pytest
+
+from meshy_amd import _lib
+
+EINVAL, ENULL, EALIGN, ESPACE = -1, -2, -3, -4
+FAKE = 0x1000  # a non-NULL address never dereferenced: each call fails its checks first
+
+
+def _call(name, *args):
+    lib = _lib.load()
+    rc = getattr(lib, name)(*args)
+    msg = lib.meshy_last_error().decode()
+    return rc, msg
+
+
+@pytest.mark.parametrize("name,args,code,text", [
+    # logits, rows, T, V, stride_b, stride_t, labels, logp, entropy, lse, stream
+    ("meshy_logprob_entropy_fwd", (None, 1, 4, 8, 32, 8, FAKE, FAKE, None, None, None), ENULL, "logits is NULL"),
+    ("meshy_logprob_entropy_fwd", (FAKE, 1, 4, 0, 32, 8, FAKE, FAKE, None, None, None), EINVAL, "bad shape"),
+    ("meshy_logprob_entropy_fwd", (FAKE, 1, 4, 8, -1, 8, FAKE, FAKE, None, None, None), EINVAL, "negative stride"),
+    ("meshy_logprob_entropy_fwd", (FAKE, 1, 4, 8, 32, 8, None, FAKE, None, None, None), ENULL, "logp needs labels"),
+    ("meshy_logprob_entropy_fwd", (FAKE, 1 << 16, 1 << 16, 8, 8, 8, FAKE, FAKE, None, None, None), EINVAL,
+     "too many rows"),
+    ("meshy_gather_logprobs_fwd", (FAKE, 1, 4, 8, 32, 8, FAKE, 0, FAKE, None, None), EINVAL, "n_ids"),
+    ("meshy_gather_logprobs_fwd", (FAKE, 1, 4, 8, 32, 8, FAKE, 257, FAKE, None, None), EINVAL, "n_ids"),
+    ("meshy_gather_logprobs_fwd", (FAKE, 1, 4, 8, 32, 8, None, 3, FAKE, None, None), ENULL, "ids and out"),
+    # logits, rows, T, V, sb, st, labels, lse, grad_logp, grad, ws, ws_bytes, stream
+    ("meshy_logprob_bwd", (FAKE, 1, 4, 8, 32, 8, FAKE, FAKE, FAKE, None, FAKE, 4096, None), ENULL, "required"),
+    ("meshy_logprob_bwd", (FAKE, 1, 4, 8, 32, 8, FAKE, FAKE, FAKE, FAKE, FAKE, 8, None), ESPACE, "workspace"),
+    ("meshy_gather_logprobs_bwd", (FAKE, 1, 4, 8, 32, 8, FAKE, 300, FAKE, FAKE, FAKE, FAKE, 4096, None), EINVAL,
+     "n_ids"),
+    # logits, rows, T, V, sb, st, k, ids, logprobs, lse, stream
+    ("meshy_topk_logprobs", (FAKE, 1, 4, 100, 400, 100, 65, FAKE, FAKE, None, None), EINVAL, "k must be"),
+    ("meshy_topk_logprobs", (FAKE, 1, 4, 5, 20, 5, 8, FAKE, FAKE, None, None), EINVAL, "k must be"),
+    ("meshy_topk_logprobs", (FAKE, 1, 4, 100, 400, 100, 0, FAKE, FAKE, None, None), EINVAL, "k must be"),
+    ("meshy_topk_logprobs", (FAKE, 1, 4, 100, 400, 100, 8, None, FAKE, None, None), ENULL, "required"),
+    ("meshy_forward_kl_topk", (FAKE, FAKE, 4, 0, 0, 0.0, 0, 0.0, FAKE, None), EINVAL, "bad sizes"),
+    ("meshy_forward_kl_topk", (None, FAKE, 4, 3, 0, 0.0, 0, 0.0, FAKE, None), ENULL, "NULL"),
+    ("meshy_per_sequence_mean", (None, FAKE, FAKE, 3, FAKE, None), ENULL, "NULL"),
+    ("meshy_per_sequence_mean", (FAKE, FAKE, FAKE, -1, FAKE, None), EINVAL, "n_docs"),
+    ("meshy_clipped_value_error", (FAKE, FAKE, None, 1, 0.2, 10, FAKE, None), ENULL, "NULL"),
+    ("meshy_clipped_value_error", (FAKE, FAKE, None, 0, 0.2, -1, FAKE, None), EINVAL, "negative"),
+    ("meshy_critic_accumulate", (FAKE, 0, FAKE, FAKE, 4, 16, FAKE, FAKE, FAKE, 8, None), ESPACE, "workspace"),
+    ("meshy_critic_accumulate", (FAKE, 0, FAKE, FAKE, -4, 16, FAKE, FAKE, FAKE, 4096, None), EINVAL, "bad shape"),
+    ("meshy_ragged_token_stats", (FAKE, None, FAKE, None, 4, FAKE, FAKE, None, None, FAKE, 4096, None), ENULL,
+     "out_off"),
+    ("meshy_ragged_token_stats", (FAKE, FAKE, FAKE, None, 4, FAKE, FAKE, FAKE, None, FAKE, 4096, None), ENULL,
+     "lp_offsets"),
+    ("meshy_ragged_token_stats", (FAKE, None, FAKE, None, 4, FAKE, FAKE, FAKE, None, FAKE, 8, None), ESPACE,
+     "workspace"),
+    ("meshy_grpo_advantage", (FAKE, FAKE, -1, FAKE, None), EINVAL, "negative"),
+    ("meshy_grpo_advantage", (None, FAKE, 3, FAKE, None), ENULL, "NULL"),
+    ("meshy_segment_offsets", (FAKE, 10, 0, FAKE, None, None), EINVAL, "bad sizes"),
+    ("meshy_stream_read", (FAKE, 4, 17, FAKE, None), EINVAL, "bad shape"),
+    ("meshy_stream_read", (FAKE + 4, 4, 32, FAKE, None), EALIGN, "misaligned"),
+])
+def test_entry_point_rejects(name, args, code, text):
+    rc, msg = _call(name, *args)
+    assert rc == code, (rc, msg)
+    assert text in msg, msg
+
+
+def test_struct_entry_points_reject():
+    lib = _lib.load()
+    a = _lib.DistillArgs()
+    a.k = 0
+    assert lib.meshy_distill_loss_fwd(ctypes.byref(a), FAKE, None, None) == EINVAL
+    a.k = 8
+    a.n_tokens = 16
+    assert lib.meshy_distill_loss_fwd(ctypes.byref(a), FAKE, None, None) == ENULL  # student missing
+    a.student = a.teacher = a.mask = a.seg_offsets = FAKE
+    a.workspace, a.workspace_bytes = FAKE, 1
+    assert lib.meshy_distill_loss_fwd(ctypes.byref(a), FAKE, None, None) == ESPACE
+    assert b"workspace" in lib.meshy_last_error()
+    assert lib.meshy_distill_loss_bwd(ctypes.byref(a), None, FAKE, FAKE, None) == ENULL
+    p = _lib.PackArgs()
+    p.n_micro, p.layout, p.tokens_elem_bytes = 1, 7, 4
+    assert lib.meshy_pack_micro_batches(ctypes.byref(p), None) == EINVAL
+    p.layout, p.teacher_k = _lib.MESHY_LAYOUT_PACKED, -1
+    p.micro_seq_len = p.micro_out_off = p.micro_doc_start = FAKE
+    p.input_ids = p.labels = p.positions = p.mask_out = p.doc_ids = p.cu_seqlens = FAKE
+    p.max_micro_elems = 16
+    assert lib.meshy_pack_micro_batches(ctypes.byref(p), None) == EINVAL
+    assert b"teacher_k" in lib.meshy_last_error()
+    g = _lib.PpoArgs()
+    g.n_tokens = -1
+    assert lib.meshy_ppo_loss_fwd(ctypes.byref(g), FAKE, None, None) == EINVAL
+
+
+def test_workspace_sizes_are_consistent():
+    lib = _lib.load()
+    assert lib.meshy_logprob_bwd_workspace_size(1000) >= 8 * 1000
+    assert lib.meshy_logprob_bwd_workspace_size(-1) == 0
+    assert lib.meshy_distill_workspace_size(10_000, 12) >= 4 * 2 * (40 + 13)
+    assert lib.meshy_critic_accumulate_workspace_size(7) >= 7 * 5 * 8
+    assert lib.meshy_ragged_token_stats_workspace_size(9) >= 9 * 8

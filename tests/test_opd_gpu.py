@@ -300,7 +300,7 @@ def test_distill_from_gathered_matches_oracle(dev, per_token, clamps, rollout):
                                rollout_lp=mb.rollout_logprobs.cpu() if rollout else None,
                                n_docs_global=mini.n_docs_global, n_tokens_global=mini.n_tokens_global,
                                per_token_loss=per_token, log_prob_min_clamp=clamps[0], loss_max_clamp=clamps[1])
-    assert abs(float(loss) - float(rl)) <= TOL
+    assert abs(float(loss.detach()) - float(rl.detach())) <= TOL
     assert set(sums) == set(rs)
     for key in rs:
         want = float(rs[key])
@@ -340,7 +340,7 @@ def test_distill_loss_drop_in_end_to_end(dev):
                                    mb.n_docs, rollout_lp=mb.rollout_logprobs.cpu(), n_docs_global=3,
                                    n_tokens_global=mini.n_tokens_global, per_token_loss=per_token)
         rl.backward()
-        assert abs(float(loss) - float(rl)) <= TOL
+        assert abs(float(loss.detach()) - float(rl.detach())) <= TOL
         for key in rs:
             want = float(rs[key])
             assert abs(float(sums[key]) - want) <= TOL + 1e-5 * abs(want), key
@@ -362,3 +362,47 @@ def test_distill_deterministic(dev):
     a = opd.distill_from_gathered(_stub(False), gathered, mb, mini)
     b = opd.distill_from_gathered(_stub(False), gathered, mb, mini)
     assert torch.equal(a[0], b[0]) and all(torch.equal(a[1][k], b[1][k]) for k in a[1])
+
+
+# ------------------------------------------------------------------ randomised sweeps
+
+
+def _rand_case(seed):
+    g = torch.Generator().manual_seed(1000 + seed)
+    rows = int(torch.randint(1, 4, (1,), generator=g))
+    T = int(torch.randint(1, 24, (1,), generator=g))
+    V = int(torch.randint(1, 40000, (1,), generator=g))
+    scale = [0.01, 1.0, 8.0, 100.0][seed % 4]
+    z = torch.randn(rows, T, V, generator=g) * scale
+    if seed % 3 == 0:
+        z = torch.round(z * 2) / 2  # coarse values: many ties
+    return g, z.to(torch.bfloat16), V
+
+
+@pytest.mark.parametrize("seed", range(16))
+def test_topk_random_sweep(dev, seed):
+    from meshy_amd import topk
+
+    g, z, V = _rand_case(seed)
+    k = int(torch.randint(1, min(64, V) + 1, (1,), generator=g))
+    ids, lps = topk.teacher_topk(z.to(dev), k)
+    rids, rlps = otopk.teacher_topk(z, k)
+    assert torch.equal(ids.cpu(), rids), (z.shape, k)
+    assert (lps.cpu() - rlps).abs().max().item() <= TOL
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_gather_random_sweep(dev, seed):
+    from meshy_amd import topk
+
+    g, z, V = _rand_case(seed + 50)
+    rows, T, _ = z.shape
+    n = int(torch.randint(1, 20, (1,), generator=g))
+    ids = torch.randint(0, V, (rows, T, n), generator=g)
+    ids[..., -1] = ids[..., 0]  # a duplicate in every row
+    drop = torch.rand(rows, T, n, generator=g) < 0.1
+    ids = torch.where(drop, torch.full_like(ids, -100), ids)
+    out = topk.gather_logprobs(z.to(dev), ids.to(dev)).cpu()
+    ref = otopk.gather_logprobs(z, ids.clamp(min=0))
+    ref = torch.where(drop, torch.zeros_like(ref), ref)  # -100: 0, like cross_entropy's ignore_index
+    assert (out - ref).abs().max().item() <= TOL
