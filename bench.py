@@ -12,10 +12,11 @@ already resident in HBM.  Prints ONE JSON line with
 * cpu_baseline         the reference's chunk loop (fp32 upcast, 1024-row
                        -cross_entropy, 512-row entropy slices) restated on CPU
                        torch on a bounded row sample, on this host's cores
-* pack_latency_us      config 0: 256 samples -> native plan -> one host-to-
+* pack_latency_us      256 GRPO samples (budget 8192) -> native plan -> one host-to-
                        device copy -> GRPO + pack kernels, wall clock
 * kernels              per-kernel device time, algorithmic GB/s and the
-                       restated CPU path for configs 0, 2, 3 and 4
+                       restated CPU path for the 256-sample GRPO batch,
+                       the 512-doc PPO batch, 16 long sequences and 1024 GAE docs
 * end_to_end           pack -> logprob+entropy -> GRPO -> PPO fwd+bwd at
                        T = 16384, GPU wall against the CPU restatement
 """
@@ -85,7 +86,7 @@ def _entry(us: float, nbytes: float, cpu_ms: float | None = None, **extra):
     return e
 
 
-# ---------------------------------------------------------------- config 1
+# ---------------------------------------------------------------- logits [16384, 151936]
 
 def bench_logprob(steps, warmup):
     import torch
@@ -182,7 +183,7 @@ def cpu_logprob_tokens_per_s(logits_gpu, labels_gpu, rows: int, runs: int = 5):
     return rows / (ms * 1e-3), ms
 
 
-# ---------------------------------------------------------------- OPD on config-1 logits
+# ---------------------------------------------------------------- OPD on the [16384, 151936] logits
 
 def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
     """Student Top-K OPD on the [16384, 151936] logits: Teacher Top-K (K = 8), the
@@ -288,7 +289,7 @@ def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
     return out
 
 
-# ---------------------------------------------------------------- config 0
+# ---------------------------------------------------------------- 256 GRPO samples
 
 def bench_pack(runs, no_cpu):
     import torch
@@ -298,7 +299,7 @@ def bench_pack(runs, no_cpu):
     from meshy_amd.plan import PlannerConfig
 
     dev = torch.device("cuda:0")
-    batch, rewards, group_offsets = workloads.config0(0)
+    batch, rewards, group_offsets = workloads.grpo_256_samples(0)
     ragged = RaggedSamples.from_arrays(batch.tokens, batch.mask, batch.logprobs, batch.offsets, rewards,
                                        group_offsets)
     cfg = PlannerConfig(layout="packed", mini_batch_size=256, seq_len=8192, align=2048,
@@ -357,7 +358,7 @@ def bench_pack(runs, no_cpu):
     return out, ragged, cfg
 
 
-# ---------------------------------------------------------------- config 2
+# ---------------------------------------------------------------- PPO over 512 docs
 
 def bench_ppo(steps, warmup, no_cpu):
     from types import SimpleNamespace as NS
@@ -372,7 +373,7 @@ def bench_ppo(steps, warmup, no_cpu):
     from meshy_amd.plan import MiniPlan
 
     dev = torch.device("cuda:0")
-    batch, old, new, rewards, group_offsets = workloads.config2(2)
+    batch, old, new, rewards, group_offsets = workloads.ppo_512_docs(2)
     n = len(batch.lengths)
     T = batch.total
     adv = grpo_advantages(torch.from_numpy(rewards).to(dev), torch.from_numpy(group_offsets).to(dev))
@@ -426,7 +427,7 @@ def bench_ppo(steps, warmup, no_cpu):
     }
 
 
-# ---------------------------------------------------------------- config 3
+# ---------------------------------------------------------------- 16 long sequences
 
 def bench_long_context(steps, warmup, no_cpu):
     import torch
@@ -435,7 +436,7 @@ def bench_long_context(steps, warmup, no_cpu):
     from meshy_amd.plan import PlannerConfig, build_plan
 
     dev = torch.device("cuda:0")
-    lengths = workloads.config3_lengths(3).tolist()
+    lengths = workloads.long_context_16_lengths(3).tolist()
     cfg = PlannerConfig(layout="packed", mini_batch_size=16, seq_len=131072, align=2048,
                         max_tokens_per_micro=131072)
     plan = build_plan(lengths, lengths, 1, cfg)
@@ -457,7 +458,7 @@ def bench_long_context(steps, warmup, no_cpu):
                   cpu_sample=f"{rows} rows, scaled to T")
 
 
-# ---------------------------------------------------------------- config 4
+# ---------------------------------------------------------------- GAE over 1024 docs
 
 def bench_gae(steps, warmup, no_cpu):
     import numpy as np
@@ -467,7 +468,7 @@ def bench_gae(steps, warmup, no_cpu):
     from meshy_amd.gae import gae_and_returns
 
     dev = torch.device("cuda:0")
-    batch, values, terminal = workloads.config4(4)
+    batch, values, terminal = workloads.gae_1024_docs(4)
     n = len(batch.lengths)
     T = batch.total
     rewards = np.zeros(T, np.float32)
@@ -504,10 +505,10 @@ def bench_gae(steps, warmup, no_cpu):
     return _entry(ms * 1e3, T * 26, cpu_ms, tokens=T, docs=n, cpu_sample="sequential loop on padded [1024, S_max]")
 
 
-# ---------------------------------------------------------------- row 20 at config 4, pack at config 3
+# ---------------------------------------------------------------- GAE attach over 1024 docs, pack of 16 long sequences
 
 def bench_attach_gae(runs, no_cpu):
-    """_attach_gae_advantages over config 4's 1024 samples (values bf16, terminal
+    """_attach_gae_advantages over 1024 samples (values bf16, terminal
     rewards, constant lambda 0.95): GPU wall per call, samples staged from the host."""
     from types import SimpleNamespace as NS
 
@@ -518,7 +519,7 @@ def bench_attach_gae(runs, no_cpu):
     from meshy_amd.gae import attach_gae_advantages
 
     dev = torch.device("cuda:0")
-    batch, values, terminal = workloads.config4(4)
+    batch, values, terminal = workloads.gae_1024_docs(4)
     samples = []
     for i in range(len(batch.lengths)):
         a, b = int(batch.offsets[i]), int(batch.offsets[i + 1])
@@ -542,7 +543,7 @@ def bench_attach_gae(runs, no_cpu):
 
 
 def bench_pack_long_context(runs, no_cpu):
-    """Config 3: 16 samples U{8192..131072} under a 131072-token budget, align 2048."""
+    """16 samples U{8192..131072} under a 131072-token budget, align 2048."""
     import numpy as np
     import torch
 
@@ -552,7 +553,7 @@ def bench_pack_long_context(runs, no_cpu):
 
     dev = torch.device("cuda:0")
     rng = np.random.default_rng(3)
-    lengths = workloads.config3_lengths(3)
+    lengths = workloads.long_context_16_lengths(3)
     offsets = np.zeros(len(lengths) + 1, np.int64)
     np.cumsum(lengths, out=offsets[1:])
     total = int(offsets[-1])
@@ -603,7 +604,7 @@ def bench_pack_long_context(runs, no_cpu):
 # ---------------------------------------------------------------- critic reductions and rollout metrics
 
 def bench_critic(steps, warmup, no_cpu):
-    """Config 4's shapes: per-sequence mean and clipped value error over the 6.35 M
+    """1024 docs (lognormal(6000, 0.8) responses): per-sequence mean and clipped value error over the 6.35 M
     packed tokens, the Accumulator over the padded [1024, S_max] critic grid."""
     import numpy as np
     import torch
@@ -611,7 +612,7 @@ def bench_critic(steps, warmup, no_cpu):
     from meshy_amd import critic, workloads
 
     dev = torch.device("cuda:0")
-    batch, values, _ = workloads.config4(4)
+    batch, values, _ = workloads.gae_1024_docs(4)
     n = len(batch.lengths)
     T = batch.total
     g = torch.Generator(device=dev).manual_seed(4)
@@ -627,7 +628,7 @@ def bench_critic(steps, warmup, no_cpu):
         a_c, m_c, d_c = adv.cpu(), mask.cpu(), doc_ids.cpu()
         cpu_ms = _wall_ms(lambda: ocritic.advantages_to_per_sequence(a_c * m_c, m_c, d_c, n), 5, gpu=False)
     # reads adv 4 + mask 4 per token (seg offsets from doc ids: 8 more)
-    out["per_sequence_mean_config4"] = _entry(ms * 1e3, T * 16, cpu_ms, tokens=T, docs=n)
+    out["per_sequence_mean_1024_docs"] = _entry(ms * 1e3, T * 16, cpu_ms, tokens=T, docs=n)
     v = torch.randn(T, generator=g, device=dev).requires_grad_(True)
     t = torch.randn(T, generator=g, device=dev)
     o = (v.detach() + 0.1 * torch.randn(T, generator=g, device=dev))
@@ -649,7 +650,7 @@ def bench_critic(steps, warmup, no_cpu):
 
         cpu_ms = _wall_ms(cpu, 5, gpu=False)
     # fwd: v, t, o read + out written; bwd: v, t, o, grad read + grad written
-    out["clipped_value_error_fwd_bwd_config4"] = _entry(ms * 1e3, T * 36, cpu_ms, tokens=T)
+    out["clipped_value_error_fwd_bwd_1024_docs"] = _entry(ms * 1e3, T * 36, cpu_ms, tokens=T)
     S = int(batch.lengths.max())
     rows = n
     pos = np.arange(T) - np.repeat(batch.offsets[:-1], batch.lengths)
@@ -683,20 +684,20 @@ def bench_critic(steps, warmup, no_cpu):
 
         cpu_ms = _wall_ms(cpu_acc, 3, gpu=False)
     # reads values 2 + returns 4 + mask 4 per grid element
-    out["accumulator_update_config4_padded"] = _entry(ms * 1e3, rows * S * 10, cpu_ms, rows=rows, S=S,
+    out["accumulator_update_1024_docs_padded"] = _entry(ms * 1e3, rows * S * 10, cpu_ms, rows=rows, S=S,
                                                       note="wall time including the state's host read")
     return out
 
 
 def bench_rollout_metrics(runs, no_cpu):
-    """Config 0's 256 samples: _rollout_metrics from the sample list and from the
+    """The 256 GRPO samples: _rollout_metrics from the sample list and from the
     wire columns, wall time including every host read of the result."""
     import torch
 
     from meshy_amd import wire, workloads
     from meshy_amd.rollout_metrics import rollout_metrics
 
-    batch, rewards, _ = workloads.config0(0)
+    batch, rewards, _ = workloads.grpo_256_samples(0)
     samples = batch.sample_dicts(rewards=rewards)
     for i, s in enumerate(samples):
         s.update(weight_version=torch.tensor(3 - i % 2), truncated=torch.tensor(i % 9 == 0),
@@ -717,7 +718,7 @@ def bench_rollout_metrics(runs, no_cpu):
 # ---------------------------------------------------------------- end to end
 
 def bench_end_to_end(runs, no_cpu):
-    """Config-0 samples truncated to the micros that fill T=16384 -> pack ->
+    """The 256 GRPO samples truncated to the micros that fill T=16384 -> pack ->
     logprob+entropy on [16384, 151936] logits -> GRPO -> PPO fwd+bwd."""
     from types import SimpleNamespace as NS
 
@@ -730,7 +731,7 @@ def bench_end_to_end(runs, no_cpu):
     from meshy_amd.plan import PlannerConfig
 
     dev = torch.device("cuda:0")
-    batch, rewards, group_offsets = workloads.config0(0)
+    batch, rewards, group_offsets = workloads.grpo_256_samples(0)
     # the first groups whose samples make two full 8192-token micros
     keep = 0
     tot = 0
@@ -880,14 +881,14 @@ def main() -> int:
     if not args.quick:
         pack, _, _ = bench_pack(20, args.no_cpu)
         result["pack_latency_us"] = pack["pack_latency_us"]
-        kernels["pack_grpo_config0"] = pack
+        kernels["pack_grpo_256_samples"] = pack
         kernels.update(bench_ppo(args.steps, args.warmup, args.no_cpu))
-        kernels["gae_returns_config4"] = bench_gae(args.steps, args.warmup, args.no_cpu)
-        kernels["logprob_entropy_config3"] = bench_long_context(max(3, args.steps // 10), 2, args.no_cpu)
+        kernels["gae_returns_1024_docs"] = bench_gae(args.steps, args.warmup, args.no_cpu)
+        kernels["logprob_entropy_16_long_sequences"] = bench_long_context(max(3, args.steps // 10), 2, args.no_cpu)
         kernels["critic"] = bench_critic(args.steps, args.warmup, args.no_cpu)
-        kernels["attach_gae_config4"] = bench_attach_gae(5, args.no_cpu)
-        kernels["pack_grpo_config3"] = bench_pack_long_context(10, args.no_cpu)
-        kernels["rollout_metrics_config0"] = bench_rollout_metrics(10, args.no_cpu)
+        kernels["attach_gae_1024_docs"] = bench_attach_gae(5, args.no_cpu)
+        kernels["pack_16_long_sequences"] = bench_pack_long_context(10, args.no_cpu)
+        kernels["rollout_metrics_256_samples"] = bench_rollout_metrics(10, args.no_cpu)
         result["kernels"] = kernels
         result["end_to_end"] = bench_end_to_end(5, args.no_cpu)
         if result.get("cpu_baseline"):

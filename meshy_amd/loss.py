@@ -165,7 +165,7 @@ def ppo_clip_loss(
     if sharder is not None and getattr(sharder, "enabled", False):
         raise NotImplementedError(
             "context-parallel PPO loss needs the per-document all-reduce between the two "
-            "kernel phases; this build runs one GPU")
+            "kernel phases; this library drives one GPU")
     inputs = _Inputs(self, new_lp, old_lp, mb, mini, entropy)
     new_flat = new_lp.reshape(-1)
     if new_flat.dtype != torch.float32:

@@ -187,7 +187,7 @@ def distill_from_gathered(self: Any, gathered: torch.Tensor, mb: Any, mini: Any)
     if sharder is not None and getattr(sharder, "enabled", False):
         raise NotImplementedError(
             "context-parallel distillation needs the per-document count all-reduce between the two "
-            "kernel phases; this build runs one GPU")
+            "kernel phases; this library drives one GPU")
     k = gathered.shape[-1] - 1
     student = gathered.reshape(-1, k + 1)
     if student.dtype != torch.float32:

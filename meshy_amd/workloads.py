@@ -1,14 +1,14 @@
-"""Seeded synthetic workloads of the benchmark configurations (numpy, host side).
+"""Seeded synthetic workloads of the benchmarks and full-size tests (numpy, host side).
 
 Lognormal lengths with "mean m, sigma s" use mu = ln m - s^2 / 2, so the mean
 of the distribution is m; values are rounded to integers and clipped.  Every
 generator takes a seed and is reproducible on any host.
 
-    config 0  pack + GRPO: 256 samples in 32 groups of 8, prompt U{64..256},
-              response lognormal(600, 0.8) clipped [1, 2048], budget 8192
-    config 2  PPO loss: 512 docs, response lognormal(4000, 0.8) clipped [16, 8192]
-    config 3  long context: 16 sequences U{8192..131072}, budget 131072
-    config 4  GAE: 1024 docs, response lognormal(6000, 0.8) clipped [32, 32768]
+    grpo_256_samples         pack + GRPO: 256 samples in 32 groups of 8, prompt U{64..256},
+                             response lognormal(600, 0.8) clipped [1, 2048], budget 8192
+    ppo_512_docs             PPO loss: 512 docs, response lognormal(4000, 0.8) clipped [16, 8192]
+    long_context_16_lengths  long context: 16 sequences U{8192..131072}, budget 131072
+    gae_1024_docs            GAE: 1024 docs, response lognormal(6000, 0.8) clipped [32, 32768]
 """
 
 from __future__ import annotations
@@ -77,7 +77,7 @@ class RaggedBatch:
         return out
 
 
-def config0(seed: int = 0):
+def grpo_256_samples(seed: int = 0):
     rng = np.random.default_rng(seed)
     n_groups, group = 32, 8
     n = n_groups * group
@@ -89,7 +89,7 @@ def config0(seed: int = 0):
     return batch, rewards, group_offsets
 
 
-def config2(seed: int = 2):
+def ppo_512_docs(seed: int = 2):
     rng = np.random.default_rng(seed)
     n_docs, group = 512, 8
     prompt = rng.integers(64, 257, n_docs)
@@ -103,12 +103,12 @@ def config2(seed: int = 2):
     return batch, old, new, rewards, group_offsets
 
 
-def config3_lengths(seed: int = 3) -> np.ndarray:
+def long_context_16_lengths(seed: int = 3) -> np.ndarray:
     rng = np.random.default_rng(seed)
     return rng.integers(8192, 131072 + 1, 16).astype(np.int64)
 
 
-CONFIG3_EDGE_LISTS = (
+LONG_CONTEXT_EDGE_LISTS = (
     [131072],
     [65536, 65536],
     [131071, 1],
@@ -117,7 +117,7 @@ CONFIG3_EDGE_LISTS = (
 )
 
 
-def config4(seed: int = 4):
+def gae_1024_docs(seed: int = 4):
     rng = np.random.default_rng(seed)
     n_docs = 1024
     prompt = rng.integers(64, 257, n_docs)

@@ -3,7 +3,7 @@
 This package restates, on the CPU, the reference algorithms that the HIP
 kernels of ``meshy_amd`` replace.  It exists to check the product, never to
 be the product: only ``tests/``, ``__graft_entry__.smoke()`` and the
-``cpu_baseline`` leg of ``bench.py`` may import it, and only as the checker or
+``cpu_baseline`` leg of ``bench.py`` may import it, and only as the expected side of a comparison or
 as the timed CPU baseline.  Nothing in ``meshy_amd`` imports it.
 
 Modules and what pins each one (the checks live in ``tests/test_oracle_*.py``):

@@ -1,7 +1,7 @@
 """Oracle: the reference planner restated in plain Python (test infrastructure).
 
 Follows meshy/backend/titan/plan.py:141-288.  Returns plain tuples instead of
-the dataclasses so the checker shares no code with the product:
+the dataclasses so the oracle shares no code with the product:
 
     (local_indices, per_rank) where per_rank[r][i] =
         (micros, n_docs_global, n_tokens_global, tokens_per_rank) and

@@ -4,7 +4,7 @@ The reference's own tests pin groupings on hand-made cases but not the exact
 assignment (snake direction, first-fit order, filler placement) at the
 benchmark sizes, so this script loads the reference's stdlib-only
 meshy/backend/titan/plan.py by file path, in the build container only, and
-records its output for the seeded configuration-0/3 lengths, the long-context
+records its output for the seeded 256-sample GRPO and 16-sequence long-context lengths, the long-context
 edge lists and a sweep of layouts, DP sizes and budgets.  The vectors are data
 (inputs and the expected plan); no reference code is kept.
 
@@ -54,23 +54,23 @@ def plan_to_json(plan):
 
 
 def cases():
-    b0, _, _ = workloads.config0(0)
+    b0, _, _ = workloads.grpo_256_samples(0)
     lt0 = b0.loss_tokens(8192)
     base0 = dict(layout="packed", mini_batch_size=256, seq_len=8192, align=2048,
                  max_tokens_per_micro=8192, micro_batch_size=None)
-    yield "config0", b0.lengths.tolist(), lt0.tolist(), 1, base0
+    yield "grpo256", b0.lengths.tolist(), lt0.tolist(), 1, base0
     for align in (1, 64):
-        yield f"config0_align{align}", b0.lengths.tolist(), lt0.tolist(), 1, dict(base0, align=align)
-    yield "config0_mini64", b0.lengths.tolist(), lt0.tolist(), 1, dict(base0, mini_batch_size=64)
-    yield "config0_dp4", b0.lengths.tolist(), lt0.tolist(), 4, dict(base0, mini_batch_size=32)
-    yield "config0_padded", b0.lengths.tolist(), lt0.tolist(), 2, dict(
+        yield f"grpo256_align{align}", b0.lengths.tolist(), lt0.tolist(), 1, dict(base0, align=align)
+    yield "grpo256_mini64", b0.lengths.tolist(), lt0.tolist(), 1, dict(base0, mini_batch_size=64)
+    yield "grpo256_dp4", b0.lengths.tolist(), lt0.tolist(), 4, dict(base0, mini_batch_size=32)
+    yield "grpo256_padded", b0.lengths.tolist(), lt0.tolist(), 2, dict(
         base0, layout="padded", mini_batch_size=64)
-    l3 = workloads.config3_lengths(3).tolist()
+    l3 = workloads.long_context_16_lengths(3).tolist()
     base3 = dict(layout="packed", mini_batch_size=16, seq_len=131072, align=2048,
                  max_tokens_per_micro=131072, micro_batch_size=None)
-    yield "config3", l3, l3, 1, base3
-    for k, edge in enumerate(workloads.CONFIG3_EDGE_LISTS):
-        yield f"config3_edge{k}", list(edge), list(edge), 1, dict(base3, mini_batch_size=len(edge))
+    yield "long16", l3, l3, 1, base3
+    for k, edge in enumerate(workloads.LONG_CONTEXT_EDGE_LISTS):
+        yield f"long_edge{k}", list(edge), list(edge), 1, dict(base3, mini_batch_size=len(edge))
     rng = random.Random(1234)
     for k in range(24):
         layout = rng.choice(["padded", "packed"])

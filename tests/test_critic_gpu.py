@@ -160,7 +160,7 @@ def test_pack_from_wire_columns_equals_pack_from_samples(dev, layout):
     from meshy_amd.pipeline import RaggedSamples, pack_step
     from meshy_amd.plan import PlannerConfig
 
-    batch, rewards, group_offsets = workloads.config0(0)
+    batch, rewards, group_offsets = workloads.grpo_256_samples(0)
     samples = batch.sample_dicts(rewards=rewards)
     cols = wire.samples_to_columns(samples, ["tokens", "mask_assistant", "logprobs", "reward"])
     cfg = PlannerConfig(layout=layout, mini_batch_size=256, seq_len=8192, align=2048,

@@ -102,13 +102,13 @@ def test_closed_form_terminal_reward(dev):
     assert torch.allclose(ret.cpu(), torch.full((1, S), R))
 
 
-def test_config4_full_size(dev):
-    """Config 4: 1024 docs (~5.9M tokens), values bf16, gamma 1, lambda 0.95 (lengths trick),
+def test_gae_1024_docs_full_size(dev):
+    """1024 docs (~5.9M tokens), values bf16, gamma 1, lambda 0.95 (lengths trick),
     packed [1, T] on the GPU against the sequential loop on padded [1024, S_max] rows."""
     from meshy_amd import workloads
     from meshy_amd.gae import gae_and_returns
 
-    batch, values, terminal = workloads.config4(4)
+    batch, values, terminal = workloads.gae_1024_docs(4)
     n = len(batch.lengths)
     L = batch.lengths
     S_max = int(L.max())

@@ -74,7 +74,7 @@ def test_topk_nan_and_inf(dev):
 
 
 def test_topk_full_size_rows_subset(dev):
-    """[16384, 151936] bf16 (config-1 shape), K = 8: a row subset against the
+    """[16384, 151936] bf16, K = 8: a row subset against the
     oracle, size-independent properties on every row."""
     from meshy_amd import topk
 

@@ -112,7 +112,7 @@ def test_ppo_oracle_icepop_positive_lm_known_answers():
     ids = torch.zeros(1, 3, dtype=torch.long)
     loss, sums = oppo.ppo_clip_loss(new, old, torch.ones(1, 3), ids, torch.ones(1), 1, per_token_loss=True,
                                     rollout_lp=roll, **kw)
-    assert float(loss) == pytest.approx(-2 / 3 + .1, abs=1e-6)
+    assert float(loss.detach()) == pytest.approx(-2 / 3 + .1, abs=1e-6)
     assert float(sums["tis_masked_sum"]) == 2. and float(sums["ratio_sum"]) == 3.
     loss.backward()
     torch.testing.assert_close(new.grad, torch.tensor([[-2.05 / 3, -.05 / 3, -.05 / 3]]))

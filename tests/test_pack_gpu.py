@@ -152,13 +152,13 @@ def test_per_token_advantages_and_positive_weights(dev):
 
 
 @pytest.mark.parametrize("layout,align", [("packed", 2048), ("packed", 1), ("packed", 64), ("padded", 64)])
-def test_config0_full_plan_bit_exact(dev, layout, align):
-    """Config 0 (256 samples, budget 8192): every micro of the plan against the oracle."""
+def test_grpo_256_samples_full_plan_bit_exact(dev, layout, align):
+    """256 GRPO samples (budget 8192): every micro of the plan against the oracle."""
     from meshy_amd import workloads
     from meshy_amd.batch import build_micro_batches
     from meshy_amd.plan import PlannerConfig, build_plan
 
-    batch, rewards, _ = workloads.config0(0)
+    batch, rewards, _ = workloads.grpo_256_samples(0)
     adv = np.linspace(-1, 1, len(rewards)).astype(np.float32)
     samples = batch.sample_dicts(rewards=rewards, advantages=adv)
     budget = 8192 if layout == "packed" else 16384
@@ -177,8 +177,8 @@ def test_config0_full_plan_bit_exact(dev, layout, align):
         _assert_same(mb, ref, layout)
 
 
-def test_config3_long_context_micros(dev):
-    """Config 3 planner edge cases materialised: exact-budget fits and a full 131072 micro."""
+def test_16_long_sequences_micros(dev):
+    """Long-context planner edge cases materialised: exact-budget fits and a full 131072 micro."""
     from meshy_amd import workloads
     from meshy_amd.batch import build_micro_batches
     from meshy_amd.plan import PlannerConfig, build_plan
@@ -206,7 +206,7 @@ def test_deterministic_and_repeatable(dev):
     from meshy_amd.batch import build_micro_batches
     from meshy_amd.plan import PlannerConfig, build_plan
 
-    batch, rewards, _ = workloads.config0(1)
+    batch, rewards, _ = workloads.grpo_256_samples(1)
     samples = batch.sample_dicts(rewards=rewards, advantages=rewards)
     cfg = PlannerConfig(layout="packed", mini_batch_size=256, seq_len=8192, align=2048,
                         max_tokens_per_micro=8192)
@@ -271,11 +271,11 @@ def test_grpo_special_cases(dev):
     assert adv[5].item() == 0.5         # size-1 group keeps its reward
 
 
-def test_grpo_config0_matches_oracle(dev):
+def test_grpo_256_samples_matches_oracle(dev):
     from meshy_amd import workloads
     from meshy_amd.advantage import grpo_advantages
 
-    _, rewards, group_offsets = workloads.config0(0)
+    _, rewards, group_offsets = workloads.grpo_256_samples(0)
     r = torch.from_numpy(rewards)
     off = torch.from_numpy(group_offsets)
     got = grpo_advantages(r.to(dev), off.to(dev)).cpu()
@@ -289,9 +289,9 @@ def test_grpo_config0_matches_oracle(dev):
     assert (got - ogrpo.grpo_batched(r, off)).abs().max().item() <= 1e-4
 
 
-# ------------------------------------------------------------ pack_step (config 0)
+# ------------------------------------------------------------ pack_step (256 GRPO samples)
 
-def test_pack_step_config0_matches_oracle(dev):
+def test_pack_step_256_samples_matches_oracle(dev):
     """Plan + one H2D + GRPO + pack: micro map, cu_seqlens, positions bit-exact;
     advantages (per document and broadcast per token) within 1e-5."""
     from meshy_amd import workloads
@@ -299,7 +299,7 @@ def test_pack_step_config0_matches_oracle(dev):
     from meshy_amd.plan import PlannerConfig
     from oracle import plan as oplan
 
-    batch, rewards, group_offsets = workloads.config0(0)
+    batch, rewards, group_offsets = workloads.grpo_256_samples(0)
     ragged = RaggedSamples.from_arrays(batch.tokens, batch.mask, batch.logprobs, batch.offsets, rewards,
                                        group_offsets)
     cfg = PlannerConfig(layout="packed", mini_batch_size=256, seq_len=8192, align=2048,

@@ -321,7 +321,7 @@ def test_native_sample_lengths_match_oracle():
     from meshy_amd import workloads
     from meshy_amd.pipeline import RaggedSamples
 
-    batch, rewards, group_offsets = workloads.config0(0)
+    batch, rewards, group_offsets = workloads.grpo_256_samples(0)
     batch.mask[batch.offsets[3] + 1] = 0.0  # a hole inside a response
     ragged = RaggedSamples.from_arrays(batch.tokens, batch.mask, batch.logprobs, batch.offsets, rewards,
                                        group_offsets)

@@ -218,11 +218,11 @@ def test_many_tiny_documents_and_empty_pad(dev):
     _compare(dev, new, old, mask, doc_ids, adv, 3000, per_token_loss=False)
 
 
-def test_config2_full_size(dev):
-    """Config 2: ~2M packed tokens, 512 docs, token-mean, eps 0.2/0.28, TIS off."""
+def test_ppo_512_docs_full_size(dev):
+    """~2M packed tokens, 512 docs, token-mean, eps 0.2/0.28, TIS off."""
     from meshy_amd import workloads
 
-    batch, old, new, rewards, group_offsets = workloads.config2(2)
+    batch, old, new, rewards, group_offsets = workloads.ppo_512_docs(2)
     from oracle.grpo import grpo_batched
 
     adv = grpo_batched(torch.from_numpy(rewards), torch.from_numpy(group_offsets))
