@@ -12,10 +12,15 @@
 //                only when lengths are not given;
 //   k_gae_chunks each workgroup folds a chunk of kChunk tokens into one map
 //                per scan (advantages and returns);
-//   k_gae_carry  one workgroup scans the chunk maps from the right and emits
-//                each chunk's carry-in, plus lambda per document (gae.py:70-74);
-//   k_gae_apply  each workgroup re-folds its chunk, scans its threads from the
-//                right seeded with the carry, and writes A_t and G_t.
+//   k_gae_groups one wave per group of 64 chunks folds their maps into one,
+//                plus lambda per document (gae.py:70-74);
+//   k_gae_apply  each workgroup folds its carry-in from the maps of the chunks
+//                of its group to its right and of the groups to its right,
+//                re-folds its chunk, scans its threads from the right seeded
+//                with the carry, and writes A_t and G_t.
+// Every fold has a fixed order, so the results do not depend on timing.  The
+// apply pass visits each XCD's chunks from the highest down, so that it first
+// re-reads what the chunks pass read last (still in L2 or the Infinity Cache).
 // Everything is fp32, like the reference's sequential fallback.
 #include <algorithm>
 
@@ -25,9 +30,11 @@ namespace meshy {
 namespace {
 
 constexpr int kThreads = 256;
-constexpr int kItems = 16;
+constexpr int kItems = 8;
 constexpr int64_t kChunk = static_cast<int64_t>(kThreads) * kItems;
-constexpr int kCarryThreads = 1024;
+static_assert(kItems % 8 == 0 || kItems == 4, "bf16 values are loaded 8 (or 4) at a time");
+constexpr int64_t kGroup = kWave;  // chunks per group
+constexpr int64_t kXcds = 8;        // workgroups go round-robin over the XCDs
 constexpr int kCountThreads = 256;
 constexpr int kCountItems = 16;
 
@@ -56,15 +63,16 @@ __device__ __forceinline__ Pair shfl_down_pair(const Pair& v, int off) {
 struct Workspace {
     float* cnt;     // [n_docs + 1]
     Pair* chunk;    // [n_chunks]
-    float* carry;   // [n_chunks][2]: A and G right after the chunk
+    Pair* group;    // [n_groups]: fold of kGroup consecutive chunk maps
 };
 
 int64_t n_chunks_of(int64_t n) { return (n + kChunk - 1) / kChunk; }
+__host__ __device__ inline int64_t n_groups_of(int64_t nc) { return (nc + kGroup - 1) / kGroup; }
 
 size_t ws_bytes(int64_t n, int64_t n_docs) {
     const int64_t nc = n_chunks_of(n);
     return align_up(sizeof(float) * (n_docs + 1), 256) + align_up(sizeof(Pair) * nc, 256) +
-           align_up(sizeof(float) * 2 * nc, 256);
+           align_up(sizeof(Pair) * n_groups_of(nc), 256);
 }
 
 Workspace ws_of(void* base, int64_t n, int64_t n_docs) {
@@ -75,7 +83,7 @@ Workspace ws_of(void* base, int64_t n, int64_t n_docs) {
     p += align_up(sizeof(float) * (n_docs + 1), 256);
     w.chunk = reinterpret_cast<Pair*>(p);
     p += align_up(sizeof(Pair) * nc, 256);
-    w.carry = reinterpret_cast<float*>(p);
+    w.group = reinterpret_cast<Pair*>(p);
     return w;
 }
 
@@ -107,6 +115,7 @@ struct ThreadInputs {
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef long long i64x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
 __device__ __forceinline__ void load_inputs(const meshy_gae_args& g, int64_t t0, int64_t n, bool vec,
                                             ThreadInputs& in) {
@@ -128,13 +137,19 @@ __device__ __forceinline__ void load_inputs(const meshy_gae_args& g, int64_t t0,
         if (g.values) {
             if (g.values_bf16) {
                 const uint16_t* vb = static_cast<const uint16_t*>(g.values) + t0;
+                if constexpr (kItems % 8 == 0) {
 #pragma unroll
-                for (int q = 0; q < kItems / 8; ++q) {
-                    const u32x4 w = *reinterpret_cast<const u32x4*>(vb + 8 * q);
-                    in.v[8 * q + 0] = bf16_lo(w.x); in.v[8 * q + 1] = bf16_hi(w.x);
-                    in.v[8 * q + 2] = bf16_lo(w.y); in.v[8 * q + 3] = bf16_hi(w.y);
-                    in.v[8 * q + 4] = bf16_lo(w.z); in.v[8 * q + 5] = bf16_hi(w.z);
-                    in.v[8 * q + 6] = bf16_lo(w.w); in.v[8 * q + 7] = bf16_hi(w.w);
+                    for (int q = 0; q < kItems / 8; ++q) {
+                        const u32x4 w = *reinterpret_cast<const u32x4*>(vb + 8 * q);
+                        in.v[8 * q + 0] = bf16_lo(w.x); in.v[8 * q + 1] = bf16_hi(w.x);
+                        in.v[8 * q + 2] = bf16_lo(w.y); in.v[8 * q + 3] = bf16_hi(w.y);
+                        in.v[8 * q + 4] = bf16_lo(w.z); in.v[8 * q + 5] = bf16_hi(w.z);
+                        in.v[8 * q + 6] = bf16_lo(w.w); in.v[8 * q + 7] = bf16_hi(w.w);
+                    }
+                } else {
+                    const u32x2 w = *reinterpret_cast<const u32x2*>(vb);
+                    in.v[0] = bf16_lo(w.x); in.v[1] = bf16_hi(w.x);
+                    in.v[2] = bf16_lo(w.y); in.v[3] = bf16_hi(w.y);
                 }
             } else {
                 const float* vf = static_cast<const float*>(g.values) + t0;
@@ -271,58 +286,87 @@ __global__ __launch_bounds__(kThreads) void k_gae_chunks(meshy_gae_args g, Works
     if (threadIdx.x == 0) ws.chunk[blockIdx.x] = total;
 }
 
-__global__ __launch_bounds__(kCarryThreads) void k_gae_carry(meshy_gae_args g, Workspace ws, int64_t n_chunks) {
-    __shared__ Pair s_wave[kCarryThreads / kWave];
-    // Lambda per document (gae.py:271-275), reported to the caller.
-    if (g.lam_doc) {
-        for (int64_t d = threadIdx.x; d < g.n_docs; d += kCarryThreads)
-            g.lam_doc[d] = lambda_of(doc_length(g, ws.cnt, d), g.alpha, g.epsilon);
-    }
-    // Each thread owns a contiguous run of chunks.
-    const int64_t per = (n_chunks + kCarryThreads - 1) / kCarryThreads;
-    const int64_t c0 = static_cast<int64_t>(threadIdx.x) * per;
-    const int64_t c1 = min(c0 + per, n_chunks);
-    Pair mine = identity_pair();
-    for (int64_t c = c1 - 1; c >= c0; --c) mine = compose(ws.chunk[c], mine);
-    // Block-wide suffix scan over the threads' runs (1024 threads = 16 waves).
+// Composition of the 64 lanes' maps in lane order (lane 0 leftmost), in a
+// fixed tree; the result is in lane 0.
+__device__ __forceinline__ Pair wave_fold(Pair x) {
     const int lane = threadIdx.x % kWave;
-    const int wid = threadIdx.x / kWave;
-    constexpr int kW = kCarryThreads / kWave;
-    Pair incl = mine;
 #pragma unroll
     for (int off = 1; off < kWave; off <<= 1) {
-        const Pair other = shfl_down_pair(incl, off);
-        if (lane + off < kWave) incl = compose(incl, other);
+        const Pair other = shfl_down_pair(x, off);
+        if (lane + off < kWave) x = compose(x, other);
     }
-    if (lane == 0) s_wave[wid] = incl;
-    __syncthreads();
-    Pair after_wave = identity_pair();
-    for (int w = kW - 1; w > wid; --w) after_wave = compose(s_wave[w], after_wave);
-    const Pair next = shfl_down_pair(incl, 1);
-    const Pair excl = (lane + 1 < kWave) ? compose(next, after_wave) : after_wave;
-    // The sequence ends with A = G = 0, so the carry after this run is excl applied to 0.
-    float a = excl.adv.q;
-    float r = excl.ret.q;
-    for (int64_t c = c1 - 1; c >= c0; --c) {
-        ws.carry[2 * c] = a;
-        ws.carry[2 * c + 1] = r;
-        const Pair m = ws.chunk[c];
-        a = fmaf(m.adv.p, a, m.adv.q);
-        r = fmaf(m.ret.p, r, m.ret.q);
-    }
+    return x;
 }
 
-__global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Workspace ws, int64_t n, bool vec) {
+__device__ __forceinline__ void write_lambda(const meshy_gae_args& g, const float* cnt, int64_t first, int64_t step) {
+    // Lambda per document (gae.py:271-275), reported to the caller.
+    for (int64_t d = first; d < g.n_docs; d += step) g.lam_doc[d] = lambda_of(doc_length(g, cnt, d), g.alpha, g.epsilon);
+}
+
+__global__ __launch_bounds__(kWave) void k_gae_groups(meshy_gae_args g, Workspace ws, int64_t nc) {
+    const int lane = threadIdx.x;
+    if (g.lam_doc) write_lambda(g, ws.cnt, static_cast<int64_t>(blockIdx.x) * kWave + lane,
+                                static_cast<int64_t>(gridDim.x) * kWave);
+    const int64_t j = static_cast<int64_t>(blockIdx.x) * kGroup + lane;
+    const Pair x = wave_fold(j < nc ? ws.chunk[j] : identity_pair());
+    if (lane == 0) ws.group[blockIdx.x] = x;
+}
+
+__global__ __launch_bounds__(kThreads) void k_gae_lambda(meshy_gae_args g, const float* cnt) {
+    write_lambda(g, cnt, static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x,
+                 static_cast<int64_t>(gridDim.x) * kThreads);
+}
+
+// Workgroup b of the apply pass takes the chunks of its XCD (b mod kXcds) in
+// decreasing order: a bijection of [0, nc).
+__device__ __forceinline__ int64_t apply_chunk(int64_t b, int64_t nc) {
+    const int64_t x = b % kXcds;
+    const int64_t i = b / kXcds;
+    const int64_t m = (nc - x + kXcds - 1) / kXcds;  // chunks c < nc with c mod kXcds == x
+    return x + kXcds * (m - 1 - i);
+}
+
+__global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Workspace ws, int64_t n, int64_t nc,
+                                                        bool vec) {
     __shared__ Pair s_wave[kThreads / kWave];
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kChunk + static_cast<int64_t>(threadIdx.x) * kItems;
+    __shared__ float s_carry[2];
+    const int64_t c = apply_chunk(blockIdx.x, nc);
+    const int64_t t0 = c * kChunk + static_cast<int64_t>(threadIdx.x) * kItems;
+    const int lane = threadIdx.x % kWave;
+    const int64_t ng = n_groups_of(nc);
+    const int64_t grp = c / kGroup;
+    const int64_t g0 = grp * kGroup;
+    const int64_t g1 = min(g0 + kGroup, nc);
+    // Wave 0 loads the maps of the carry-in before the chunk's inputs: the chunks
+    // of this group to the right of c, and the first 64 groups to the right.
+    Pair right = identity_pair();
+    Pair after = identity_pair();
+    if (threadIdx.x < kWave) {
+        const int64_t j = g0 + lane;
+        if (j > c && j < g1) right = ws.chunk[j];
+        const int64_t k = grp + 1 + lane;
+        if (k < ng) after = ws.group[k];
+    }
     Pair items[kItems];
     const Pair mine = load_items(g, ws.cnt, t0, n, vec, items);
+    if (threadIdx.x < kWave) {
+        right = wave_fold(right);
+        after = wave_fold(after);
+        for (int64_t w0 = grp + 1 + kWave; w0 < ng; w0 += kWave) {
+            const int64_t k = w0 + lane;
+            after = compose(after, wave_fold(k < ng ? ws.group[k] : identity_pair()));
+        }
+        if (lane == 0) {
+            // The sequence ends with A = G = 0, so the carry is the map applied to 0.
+            const Pair m = compose(right, after);
+            s_carry[0] = m.adv.q;
+            s_carry[1] = m.ret.q;
+        }
+    }
     Pair total;
-    const Pair excl = block_suffix_exclusive(mine, s_wave, total);
-    const float ca = ws.carry[2 * blockIdx.x];
-    const float cr = ws.carry[2 * blockIdx.x + 1];
-    float A = fmaf(excl.adv.p, ca, excl.adv.q);
-    float G = fmaf(excl.ret.p, cr, excl.ret.q);
+    const Pair excl = block_suffix_exclusive(mine, s_wave, total);  // its barriers publish s_carry
+    float A = fmaf(excl.adv.p, s_carry[0], excl.adv.q);
+    float G = fmaf(excl.ret.p, s_carry[1], excl.ret.q);
     float outA[kItems], outG[kItems];
 #pragma unroll
     for (int k = kItems - 1; k >= 0; --k) {
@@ -460,15 +504,18 @@ int gae_launch(const meshy_gae_args& g, hipStream_t stream) {
     auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     const bool vec = al16(g.rewards) && al16(g.mask) && al16(g.doc_ids) && (!g.values || al16(g.values)) &&
                      (!g.adv || al16(g.adv)) && (!g.returns || al16(g.returns));
-    if (nc > 0) {
+    if (nc > 0 && (g.adv || g.returns)) {
         hipLaunchKernelGGL(k_gae_chunks, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, vec);
         if ((rc = check_launch("meshy_gae(chunks)"))) return rc;
-    }
-    hipLaunchKernelGGL(k_gae_carry, dim3(1), dim3(kCarryThreads), 0, stream, g, ws, nc);
-    if ((rc = check_launch("meshy_gae(carry)"))) return rc;
-    if (nc > 0 && (g.adv || g.returns)) {
-        hipLaunchKernelGGL(k_gae_apply, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, vec);
+        hipLaunchKernelGGL(k_gae_groups, dim3(static_cast<unsigned>(n_groups_of(nc))), dim3(kWave), 0, stream, g, ws,
+                           nc);
+        if ((rc = check_launch("meshy_gae(groups)"))) return rc;
+        hipLaunchKernelGGL(k_gae_apply, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, nc, vec);
         if ((rc = check_launch("meshy_gae(apply)"))) return rc;
+    } else if (g.lam_doc && g.n_docs > 0) {
+        const unsigned nb = static_cast<unsigned>(std::min<int64_t>(1024, ceil_div(g.n_docs, kThreads)));
+        hipLaunchKernelGGL(k_gae_lambda, dim3(nb), dim3(kThreads), 0, stream, g, ws.cnt);
+        if ((rc = check_launch("meshy_gae(lambda)"))) return rc;
     }
     return MESHY_OK;
 }

@@ -94,6 +94,16 @@ def test_struct_entry_points_reject():
     g = _lib.PpoArgs()
     g.n_tokens = -1
     assert lib.meshy_ppo_loss_fwd(ctypes.byref(g), FAKE, None, None) == EINVAL
+    e = _lib.GaeArgs()
+    e.rewards = e.mask = e.doc_ids = e.values = e.adv = FAKE
+    e.rows, e.S, e.n_docs, e.gamma, e.alpha = 1, 100, 1, 1.0, 0.0
+    assert lib.meshy_gae(ctypes.byref(e), None) == EINVAL
+    assert b"alpha" in lib.meshy_last_error()
+    e.alpha = 1.0
+    e.workspace, e.workspace_bytes = FAKE, lib.meshy_gae_workspace_size(1, 100, 1) - 1
+    assert lib.meshy_gae(ctypes.byref(e), None) == ESPACE
+    e.adv, e.values = FAKE, None
+    assert lib.meshy_gae(ctypes.byref(e), None) == ENULL
 
 
 def test_workspace_sizes_are_consistent():

@@ -142,6 +142,66 @@ def test_gae_1024_docs_full_size(dev):
     assert (got_ret - ref_ret).abs().max().item() <= TOL
 
 
+def _run_suffix_sums(r, valid, doc):
+    """Suffix sums of r over each maximal run of valid positions of one document."""
+    n = len(r)
+    cont = np.zeros(n, bool)
+    cont[:-1] = valid[:-1] & valid[1:] & (doc[:-1] == doc[1:])
+    rv = np.where(valid, r, 0).astype(np.int64)
+    run_end = np.zeros(n, np.int64)  # index of the last position of t's run
+    ends = np.flatnonzero(~cont)
+    run_end[:] = ends[np.searchsorted(ends, np.arange(n))]
+    suffix = np.concatenate([np.cumsum(rv[::-1])[::-1], [0]])
+    return suffix[np.arange(n)] - suffix[run_end + 1]
+
+
+@pytest.mark.parametrize("n", [4096 * 64, 4096 * 64 + 1, 4096 * 129 + 17, 4096 * 64 * 65 + 3])
+def test_exact_carry_across_chunks_and_groups(dev, n):
+    """gamma = lambda = 1 with integer rewards and values: G_t is the suffix sum of r
+    over t's run of valid tokens and A_t = G_t - V_t (the deltas telescope), all
+    exact in fp32, so every carry (between threads, workgroups and the carry
+    scan's runs) is checked bit for bit, on up to 17M tokens."""
+    from meshy_amd.gae import gae_and_returns
+
+    rng = np.random.default_rng(n)
+    n_docs = max(1, n // 300_000)
+    cuts = np.sort(rng.choice(np.arange(1, n), n_docs - 1, replace=False)) if n_docs > 1 else np.array([], int)
+    doc = np.zeros(n, np.int64)
+    doc[cuts] = 1
+    doc = np.cumsum(doc)
+    valid = rng.random(n) > 1e-4
+    r = (rng.random(n) < 0.05).astype(np.float32)
+    v = rng.integers(-8, 9, n).astype(np.float32)
+    G = _run_suffix_sums(r, valid, doc).astype(np.float32)
+    A = np.where(valid, G - v, 0).astype(np.float32)
+    lengths = torch.full((n_docs,), 1e30, device=dev)
+    adv, ret, lam = gae_and_returns(
+        torch.from_numpy(r).reshape(1, -1).to(dev), torch.from_numpy(v).to(torch.bfloat16).reshape(1, -1).to(dev),
+        torch.from_numpy(valid.astype(np.float32)).reshape(1, -1).to(dev),
+        torch.from_numpy(doc).reshape(1, -1).to(dev), n_docs, lengths=lengths, gamma=1.0, alpha=1.0, epsilon=0.0)
+    assert torch.equal(lam.cpu(), torch.ones(n_docs))
+    assert np.array_equal(ret.reshape(-1).cpu().numpy(), G)
+    assert np.array_equal(adv.reshape(-1).cpu().numpy(), A)
+
+
+def test_scan_is_deterministic(dev):
+    """Two calls on the same inputs give bitwise equal results: every fold has a
+    fixed order, whichever workgroup finishes first."""
+    from meshy_amd.gae import gae_and_returns
+
+    g = torch.Generator().manual_seed(11)
+    n = 4096 * 300 + 5
+    doc = torch.cumsum((torch.rand(n, generator=g) < 1e-4).long(), 0)
+    n_docs = int(doc[-1]) + 1
+    args = [torch.randn(n, generator=g), torch.randn(n, generator=g),
+            (torch.rand(n, generator=g) > 0.01).float(), doc]
+    d = [a.reshape(1, -1).to(dev) for a in args]
+    first = gae_and_returns(*d, n_docs, gamma=0.999, alpha=1.5)
+    for _ in range(3):
+        again = gae_and_returns(*d, n_docs, gamma=0.999, alpha=1.5)
+        assert all(torch.equal(a, b) for a, b in zip(first, again))
+
+
 def _critic_samples(n, seed, max_len=700, bf16=False):
     g = torch.Generator().manual_seed(seed)
     out = []
