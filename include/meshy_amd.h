@@ -500,7 +500,9 @@ int meshy_whiten_apply(float* adv, const float* mask, int64_t n, const double* s
  * meshy_clipped_value_error replaces clipped_value_error
  * (meshy/backend/titan/vapo.py:35-41): out = (v - t)^2, or with has_clip
  * max((v - t)^2, (o + clamp(v - o, -clip, clip) - t)^2); the backward gives
- * d out / d v * grad_out (maximum splits ties, clamp passes on its range).
+ * d out / d v * grad_out[i * grad_stride] (maximum splits ties, clamp passes
+ * on its range); grad_stride 0 broadcasts one value, as the gradient of a sum
+ * or a mean arrives, so it is never materialised.
  * ---------------------------------------------------------------------- */
 int meshy_per_sequence_mean(const float* x, const float* mask, const int64_t* seg_offsets,
                             int64_t n_docs, float* out, hipStream_t stream);
@@ -514,7 +516,8 @@ int meshy_clipped_value_error(const float* values, const float* targets, const f
                               hipStream_t stream);
 int meshy_clipped_value_error_bwd(const float* values, const float* targets,
                                   const float* old_values, int32_t has_clip, float clip, int64_t n,
-                                  const float* grad_out, float* grad_values, hipStream_t stream);
+                                  const float* grad_out, int64_t grad_stride, float* grad_values,
+                                  hipStream_t stream);
 
 /* ------------------------------------------------------------------------
  * Token-level rollout statistics over jagged sample columns (device).

@@ -288,7 +288,7 @@ SIGNATURES = {
         c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_float, c_int64, c_void_p, c_void_p]
     ),
     "meshy_clipped_value_error_bwd": (
-        c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_float, c_int64, c_void_p, c_void_p, c_void_p]
+        c_int, [c_void_p, c_void_p, c_void_p, c_int32, c_float, c_int64, c_void_p, c_int64, c_void_p, c_void_p]
     ),
     "meshy_ragged_token_stats_workspace_size": (c_size_t, [c_int64]),
     "meshy_ragged_token_stats": (
@@ -297,7 +297,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 _LIB: ctypes.CDLL | None = None
 

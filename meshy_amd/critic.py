@@ -128,10 +128,16 @@ class _ClippedValueError(torch.autograd.Function):
         clip = ctx.clip
         has = clip is not None
         gv = torch.empty_like(v)
-        gc = g.to(torch.float32).contiguous()
+        gc = g.to(torch.float32)
+        # The gradient of a sum or a mean is one value broadcast (stride 0):
+        # the kernel reads it as such instead of a materialised copy.
+        stride = 0 if gc.dim() == 1 and gc.stride(0) == 0 else 1
+        if stride:
+            gc = gc.contiguous()
         rc = _lib.load().meshy_clipped_value_error_bwd(v.data_ptr(), t.data_ptr(), o.data_ptr() if has else None,
                                                        int(has), float(clip) if has else 0.0, v.numel(),
-                                                       gc.data_ptr(), gv.data_ptr(), _lib.stream_of(v.device))
+                                                       gc.data_ptr(), stride, gv.data_ptr(),
+                                                       _lib.stream_of(v.device))
         _lib.check(rc, "meshy_clipped_value_error_bwd")
         return gv, None, None, None
 

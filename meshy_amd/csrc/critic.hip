@@ -150,35 +150,23 @@ __global__ __launch_bounds__(kThreads) void k_acc_final(const double* __restrict
 
 __device__ __forceinline__ float clamp_c(float x, float c) { return isnan(x) ? x : (x < -c ? -c : (x > c ? c : x)); }
 
-__global__ __launch_bounds__(kThreads) void k_cve_fwd(const float* __restrict__ v, const float* __restrict__ t,
-                                                      const float* __restrict__ o, float clip, int has_clip,
-                                                      int64_t n, float* __restrict__ out) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const float e = v[i] - t[i];
+__device__ __forceinline__ float cve_of(float v, float t, float o, float clip, int has_clip) {
+    const float e = v - t;
     float err = e * e;
     if (has_clip) {
-        const float c = (o[i] + clamp_c(v[i] - o[i], clip)) - t[i];
+        const float c = (o + clamp_c(v - o, clip)) - t;
         err = fmaxf(err, c * c);
         if (isnan(e) || isnan(c)) err = __builtin_nanf("");
     }
-    out[i] = err;
+    return err;
 }
 
-__global__ __launch_bounds__(kThreads) void k_cve_bwd(const float* __restrict__ v, const float* __restrict__ t,
-                                                      const float* __restrict__ o, float clip, int has_clip,
-                                                      int64_t n, const float* __restrict__ g,
-                                                      float* __restrict__ gv) {
-    const int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x;
-    if (i >= n) return;
-    const float e = v[i] - t[i];
-    const float gi = g[i];
-    if (!has_clip) {
-        gv[i] = gi * (2.f * e);
-        return;
-    }
-    const float dlt = v[i] - o[i];
-    const float c = (o[i] + clamp_c(dlt, clip)) - t[i];
+// d err / d v times gi: maximum splits ties 1/2-1/2, clamp passes on [-clip, clip].
+__device__ __forceinline__ float cve_grad(float v, float t, float o, float clip, int has_clip, float gi) {
+    const float e = v - t;
+    if (!has_clip) return gi * (2.f * e);
+    const float dlt = v - o;
+    const float c = (o + clamp_c(dlt, clip)) - t;
     const float err = e * e, cerr = c * c;
     float ga = 0.f, gc = 0.f;  // shares of the gradient through each branch of maximum
     if (err > cerr) ga = gi;
@@ -188,7 +176,58 @@ __global__ __launch_bounds__(kThreads) void k_cve_bwd(const float* __restrict__ 
         gc = 0.5f * gi;
     }
     const float pass = (dlt >= -clip && dlt <= clip) ? 1.f : 0.f;
-    gv[i] = ga * (2.f * e) + (gc * (2.f * c)) * pass;
+    return ga * (2.f * e) + (gc * (2.f * c)) * pass;
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
+inline bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+// Four consecutive elements per thread: 16-byte loads and stores when the
+// arrays are 16-byte aligned and the four are in range, scalar otherwise.
+__global__ __launch_bounds__(kThreads) void k_cve_fwd(const float* __restrict__ v, const float* __restrict__ t,
+                                                      const float* __restrict__ o, float clip, int has_clip,
+                                                      int64_t n, bool vec, float* __restrict__ out) {
+    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 4;
+    if (i0 >= n) return;
+    if (vec && i0 + 4 <= n) {
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(v + i0);
+        const f32x4 t4 = *reinterpret_cast<const f32x4*>(t + i0);
+        const f32x4 o4 = has_clip ? *reinterpret_cast<const f32x4*>(o + i0) : f32x4{0.f, 0.f, 0.f, 0.f};
+        f32x4 r;
+        r.x = cve_of(v4.x, t4.x, o4.x, clip, has_clip);
+        r.y = cve_of(v4.y, t4.y, o4.y, clip, has_clip);
+        r.z = cve_of(v4.z, t4.z, o4.z, clip, has_clip);
+        r.w = cve_of(v4.w, t4.w, o4.w, clip, has_clip);
+        *reinterpret_cast<f32x4*>(out + i0) = r;
+        return;
+    }
+    for (int64_t i = i0; i < min(i0 + 4, n); ++i) out[i] = cve_of(v[i], t[i], has_clip ? o[i] : 0.f, clip, has_clip);
+}
+
+// grad_out is read at i * gs: gs = 1 for a dense gradient, 0 for one value
+// broadcast to every element (the gradient of a sum or a mean).
+__global__ __launch_bounds__(kThreads) void k_cve_bwd(const float* __restrict__ v, const float* __restrict__ t,
+                                                      const float* __restrict__ o, float clip, int has_clip,
+                                                      int64_t n, bool vec, const float* __restrict__ g, int64_t gs,
+                                                      float* __restrict__ gv) {
+    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 4;
+    if (i0 >= n) return;
+    if (vec && i0 + 4 <= n) {
+        const f32x4 v4 = *reinterpret_cast<const f32x4*>(v + i0);
+        const f32x4 t4 = *reinterpret_cast<const f32x4*>(t + i0);
+        const f32x4 o4 = has_clip ? *reinterpret_cast<const f32x4*>(o + i0) : f32x4{0.f, 0.f, 0.f, 0.f};
+        const f32x4 g4 = gs ? *reinterpret_cast<const f32x4*>(g + i0) : f32x4{g[0], g[0], g[0], g[0]};
+        f32x4 r;
+        r.x = cve_grad(v4.x, t4.x, o4.x, clip, has_clip, g4.x);
+        r.y = cve_grad(v4.y, t4.y, o4.y, clip, has_clip, g4.y);
+        r.z = cve_grad(v4.z, t4.z, o4.z, clip, has_clip, g4.z);
+        r.w = cve_grad(v4.w, t4.w, o4.w, clip, has_clip, g4.w);
+        *reinterpret_cast<f32x4*>(gv + i0) = r;
+        return;
+    }
+    for (int64_t i = i0; i < min(i0 + 4, n); ++i)
+        gv[i] = cve_grad(v[i], t[i], has_clip ? o[i] : 0.f, clip, has_clip, g[i * gs]);
 }
 
 }  // namespace
@@ -244,22 +283,26 @@ extern "C" int meshy_clipped_value_error(const float* values, const float* targe
     if (n == 0) return MESHY_OK;
     if (!values || !targets || !out || (has_clip && !old_values))
         return set_error(MESHY_ENULL, "%s: NULL pointer", who);
-    hipLaunchKernelGGL(k_cve_fwd, dim3(static_cast<unsigned>(ceil_div(n, kThreads))), dim3(kThreads), 0, stream,
-                       values, targets, old_values, clip, has_clip, n, out);
+    const bool vec = al16(values) && al16(targets) && al16(out) && (!has_clip || al16(old_values));
+    hipLaunchKernelGGL(k_cve_fwd, dim3(static_cast<unsigned>(ceil_div(n, 4 * kThreads))), dim3(kThreads), 0, stream,
+                       values, targets, old_values, clip, has_clip, n, vec, out);
     return check_launch(who);
 }
 
 extern "C" int meshy_clipped_value_error_bwd(const float* values, const float* targets, const float* old_values,
                                              int32_t has_clip, float clip, int64_t n, const float* grad_out,
-                                             float* grad_values, hipStream_t stream) {
+                                             int64_t grad_stride, float* grad_values, hipStream_t stream) {
     using namespace meshy;
     clear_error();
     const char* who = "meshy_clipped_value_error_bwd";
     if (n < 0) return set_error(MESHY_EINVAL, "%s: negative size", who);
+    if (grad_stride != 0 && grad_stride != 1) return set_error(MESHY_EINVAL, "%s: grad_stride must be 0 or 1", who);
     if (n == 0) return MESHY_OK;
     if (!values || !targets || !grad_out || !grad_values || (has_clip && !old_values))
         return set_error(MESHY_ENULL, "%s: NULL pointer", who);
-    hipLaunchKernelGGL(k_cve_bwd, dim3(static_cast<unsigned>(ceil_div(n, kThreads))), dim3(kThreads), 0, stream,
-                       values, targets, old_values, clip, has_clip, n, grad_out, grad_values);
+    const bool vec = al16(values) && al16(targets) && al16(grad_values) && (!has_clip || al16(old_values)) &&
+                     (grad_stride == 0 || al16(grad_out));
+    hipLaunchKernelGGL(k_cve_bwd, dim3(static_cast<unsigned>(ceil_div(n, 4 * kThreads))), dim3(kThreads), 0, stream,
+                       values, targets, old_values, clip, has_clip, n, vec, grad_out, grad_stride, grad_values);
     return check_launch(who);
 }

@@ -49,6 +49,9 @@ def _call(name, *args):
     ("meshy_per_sequence_mean", (FAKE, FAKE, FAKE, -1, FAKE, None), EINVAL, "n_docs"),
     ("meshy_clipped_value_error", (FAKE, FAKE, None, 1, 0.2, 10, FAKE, None), ENULL, "NULL"),
     ("meshy_clipped_value_error", (FAKE, FAKE, None, 0, 0.2, -1, FAKE, None), EINVAL, "negative"),
+    # values, targets, old, has_clip, clip, n, grad_out, grad_stride, grad_values, stream
+    ("meshy_clipped_value_error_bwd", (FAKE, FAKE, None, 0, 0.2, 10, FAKE, 2, FAKE, None), EINVAL, "grad_stride"),
+    ("meshy_clipped_value_error_bwd", (FAKE, FAKE, None, 1, 0.2, 10, FAKE, 0, FAKE, None), ENULL, "NULL"),
     ("meshy_critic_accumulate", (FAKE, 0, FAKE, FAKE, 4, 16, FAKE, FAKE, FAKE, 8, None), ESPACE, "workspace"),
     ("meshy_critic_accumulate", (FAKE, 0, FAKE, FAKE, -4, 16, FAKE, FAKE, FAKE, 4096, None), EINVAL, "bad shape"),
     ("meshy_ragged_token_stats", (FAKE, None, FAKE, None, 4, FAKE, FAKE, None, None, FAKE, 4096, None), ENULL,

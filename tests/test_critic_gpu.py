@@ -96,6 +96,32 @@ def test_clipped_value_error_fwd_bwd(dev, clip):
     assert (vd.grad.cpu() - vr.grad).abs().max().item() <= 1e-5
 
 
+@pytest.mark.parametrize("clip", [None, 0.2])
+@pytest.mark.parametrize("reduce", ["sum", "mean"])
+@pytest.mark.parametrize("offset", [0, 1])
+def test_clipped_value_error_broadcast_grad_and_tails(dev, clip, reduce, offset):
+    """The gradient of a sum or a mean arrives as one broadcast value (read with
+    stride 0); 3003 elements leave a tail of 3 after the 4-wide vectors, and a
+    one-element offset makes every array misaligned (the scalar path)."""
+    from meshy_amd import critic
+
+    g = torch.Generator().manual_seed(9)
+    n = 3003
+    base = torch.randn(3, n + offset, generator=g)
+    v, t = base[0, offset:], base[1, offset:]
+    o = v + base[2, offset:] * 0.3
+    vd_base = base[0].to(dev).clone().requires_grad_(True)
+    vd = vd_base[offset:]
+    td, od = base[1].to(dev)[offset:], (base[0] + base[2] * 0.3).to(dev)[offset:]
+    out = critic.clipped_value_error(vd, td, od, clip)
+    vr = v.clone().requires_grad_(True)
+    ref = ocritic.clipped_value_error(vr, t, o, clip)
+    assert (out.detach().cpu() - ref).abs().max().item() <= 1e-5
+    getattr(out, reduce)().backward()
+    getattr(ref, reduce)().backward()
+    assert (vd_base.grad[offset:].cpu() - vr.grad).abs().max().item() <= 1e-6
+
+
 def _rollout_samples(n, seed, *, stamps=True):
     g = torch.Generator().manual_seed(seed)
     out = []
