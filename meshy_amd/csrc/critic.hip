@@ -82,11 +82,10 @@ __device__ __forceinline__ float load_value(const void* v, int bf16, int64_t i) 
 // One workgroup per row: row sums into part[row][5] (fp64) and row_value[row].
 // Each thread sums its ~S/256 elements in fp32 (two interleaved halves for
 // latency), the workgroup combines the threads in fp64.
-__device__ __forceinline__ void acc_elem(const void* values, int values_bf16, const float* returns,
-                                         const float* mask, int64_t i, float (&a)[kAccSums + 1]) {
-    const float m = mask[i] > 0.f ? 1.f : 0.f;
-    const float v = load_value(values, values_bf16, i) * m;
-    const float r = returns[i] * m;
+__device__ __forceinline__ void acc_one(float mk, float val, float ret, float (&a)[kAccSums + 1]) {
+    const float m = mk > 0.f ? 1.f : 0.f;
+    const float v = val * m;
+    const float r = ret * m;
     const float dv = v - r;
     a[0] += m;
     a[1] += r;
@@ -96,21 +95,77 @@ __device__ __forceinline__ void acc_elem(const void* values, int values_bf16, co
     a[5] += v;
 }
 
+__device__ __forceinline__ void acc_elem(const void* values, int values_bf16, const float* returns,
+                                         const float* mask, int64_t i, float (&a)[kAccSums + 1]) {
+    acc_one(mask[i], load_value(values, values_bf16, i), returns[i], a);
+}
+
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+inline bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
+// The 8 elements at i, a multiple of 8: with 16-byte aligned bases every load
+// is a 16-byte vector (values: one for bf16, two for fp32).
+struct Elems8 {
+    f32x4 m0, m1, r0, r1, v0, v1;
+};
+
+__device__ __forceinline__ Elems8 load8(const void* values, int values_bf16, const float* returns,
+                                        const float* mask, int64_t i) {
+    Elems8 e;
+    e.m0 = *reinterpret_cast<const f32x4*>(mask + i);
+    e.m1 = *reinterpret_cast<const f32x4*>(mask + i + 4);
+    e.r0 = *reinterpret_cast<const f32x4*>(returns + i);
+    e.r1 = *reinterpret_cast<const f32x4*>(returns + i + 4);
+    if (values_bf16) {
+        const u32x4 w = *reinterpret_cast<const u32x4*>(static_cast<const uint16_t*>(values) + i);
+        e.v0 = f32x4{bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)};
+        e.v1 = f32x4{bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w)};
+    } else {
+        e.v0 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(values) + i);
+        e.v1 = *reinterpret_cast<const f32x4*>(static_cast<const float*>(values) + i + 4);
+    }
+    return e;
+}
+
+__device__ __forceinline__ void acc8(const Elems8& e, float (&a)[kAccSums + 1]) {
+    acc_one(e.m0.x, e.v0.x, e.r0.x, a);
+    acc_one(e.m0.y, e.v0.y, e.r0.y, a);
+    acc_one(e.m0.z, e.v0.z, e.r0.z, a);
+    acc_one(e.m0.w, e.v0.w, e.r0.w, a);
+    acc_one(e.m1.x, e.v1.x, e.r1.x, a);
+    acc_one(e.m1.y, e.v1.y, e.r1.y, a);
+    acc_one(e.m1.z, e.v1.z, e.r1.z, a);
+    acc_one(e.m1.w, e.v1.w, e.r1.w, a);
+}
+
+// One workgroup per row.  The row's elements from the first multiple of 8 are
+// read 8 at a time (two groups of 8 per thread in flight); the head before it
+// and the tail after the last whole group of 8 element by element.
 __global__ __launch_bounds__(kThreads) void k_acc_rows(const void* __restrict__ values, int values_bf16,
                                                        const float* __restrict__ returns,
-                                                       const float* __restrict__ mask, int64_t S,
+                                                       const float* __restrict__ mask, int64_t S, bool vec,
                                                        double* __restrict__ part, float* __restrict__ row_value) {
     __shared__ double s_red[kAccSums + 1][kWaves];
     const int64_t row = blockIdx.x;
     const int64_t base = row * S;
+    const int64_t end = base + S;
+    const int64_t body0 = vec ? min((base + 7) / 8 * 8, end) : end;
+    const int64_t n8 = (end - body0) / 8;
+    const int64_t body1 = body0 + 8 * n8;
     float a0[kAccSums + 1] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};  // m, r, r2, d, d2, v
     float a1[kAccSums + 1] = {0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
-    int64_t j = threadIdx.x;
-    for (; j + kThreads < S; j += 2 * kThreads) {
-        acc_elem(values, values_bf16, returns, mask, base + j, a0);
-        acc_elem(values, values_bf16, returns, mask, base + j + kThreads, a1);
+    int64_t c = threadIdx.x;
+    for (; c + kThreads < n8; c += 2 * kThreads) {
+        const Elems8 e0 = load8(values, values_bf16, returns, mask, body0 + 8 * c);
+        const Elems8 e1 = load8(values, values_bf16, returns, mask, body0 + 8 * (c + kThreads));
+        acc8(e0, a0);
+        acc8(e1, a1);
     }
-    if (j < S) acc_elem(values, values_bf16, returns, mask, base + j, a0);
+    if (c < n8) acc8(load8(values, values_bf16, returns, mask, body0 + 8 * c), a0);
+    for (int64_t j = base + threadIdx.x; j < body0; j += kThreads) acc_elem(values, values_bf16, returns, mask, j, a1);
+    for (int64_t j = body1 + threadIdx.x; j < end; j += kThreads) acc_elem(values, values_bf16, returns, mask, j, a1);
     double acc[kAccSums + 1];
 #pragma unroll
     for (int k = 0; k <= kAccSums; ++k) acc[k] = static_cast<double>(a0[k]) + static_cast<double>(a1[k]);
@@ -179,9 +234,6 @@ __device__ __forceinline__ float cve_grad(float v, float t, float o, float clip,
     return ga * (2.f * e) + (gc * (2.f * c)) * pass;
 }
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-
-inline bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 // Four consecutive elements per thread: 16-byte loads and stores when the
 // arrays are 16-byte aligned and the four are in range, scalar otherwise.
@@ -265,8 +317,9 @@ extern "C" int meshy_critic_accumulate(const void* values, int32_t values_bf16, 
                          meshy_critic_accumulate_workspace_size(rows));
     double* part = static_cast<double*>(workspace);
     if (rows > 0) {
+        const bool vec = al16(values) && al16(returns) && al16(mask);
         hipLaunchKernelGGL(k_acc_rows, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, stream, values,
-                           values_bf16, returns, mask, S, part, row_value);
+                           values_bf16, returns, mask, S, vec, part, row_value);
         int rc = check_launch(who);
         if (rc) return rc;
     }

@@ -60,7 +60,9 @@ def test_accumulator_matches_oracle(dev, bf16):
     from meshy_amd import critic
 
     acc, ref = critic.Accumulator(), ocritic.Accumulator()
-    for k, (rows, S) in enumerate([(6, 500), (3, 4096), (1, 17)]):
+    # S = 500 and 5003 start odd rows off a multiple of 8 (head, body, tail); 4096
+    # rows run the two-groups-in-flight loop.
+    for k, (rows, S) in enumerate([(6, 500), (3, 4096), (1, 17), (4, 5003)]):
         v, r, m, _ = _critic_batch(rows, S, seed=10 + k)
         v = v.to(torch.bfloat16) if bf16 else v
         rewards = torch.rand(rows)
