@@ -86,6 +86,22 @@ def _entry(us: float, nbytes: float, cpu_ms: float | None = None, **extra):
     return e
 
 
+def _with_device(e: dict, device_us: float, nbytes: float) -> dict:
+    """Adds the device time of the kernels alone (their C-ABI calls in a loop,
+    without the Python wrapper or the autograd engine) to a drop-in call's entry."""
+    gbs = nbytes / (device_us * 1e-6) / 1e9
+    e["device_us"] = round(device_us, 2)
+    e["device_GBps"] = round(gbs, 1)
+    e["device_frac_hbm"] = round(gbs / HBM_PEAK_GBS, 4)
+    return e
+
+
+def _checked(rc: int, what: str) -> None:
+    from meshy_amd import _lib
+
+    _lib.check(rc, what)
+
+
 # ---------------------------------------------------------------- logits [16384, 151936]
 
 def bench_logprob(steps, warmup):
@@ -283,9 +299,36 @@ def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
             loss.backward()
 
         cpu_ms = _wall_ms(cpu_loss, 5, gpu=False)
-    # fwd reads student (K+1)*4 + teacher K*4 + mask 4 + rollout 4; bwd reads the same, writes (K+1)*4
-    per_tok = (K + 1) * 4 + K * 4 + 8
-    out["distill_loss_fwd_bwd_K8_T16384"] = _entry(ms * 1e3, T * (2 * per_tok + (K + 1) * 4), cpu_ms, tokens=T)
+    # The kernels alone, through the C ABI: document offsets, loss, gradient.
+    import ctypes
+
+    from meshy_amd import _lib
+
+    student = gd.detach().reshape(-1, K + 1)
+    inputs = opd._Inputs(stub, mb, mini, K, T, dev)
+    args = inputs.args(student)
+    pa = ctypes.byref(args)
+    lib, stream = _lib.load(), _lib.stream_of(dev)
+    out_t = torch.empty(_lib.DISTILL_NOUT, device=dev)
+    seg = torch.empty(n_docs + 1, device=dev)
+    one = torch.ones(1, device=dev)
+    grad = torch.empty_like(student)
+    ids, off = inputs.ids, inputs.seg_off
+
+    def dev_fb():
+        lib.meshy_segment_offsets(ids.data_ptr(), ids.numel(), n_docs + 1, off.data_ptr(), None, stream)
+        lib.meshy_distill_loss_fwd(pa, out_t.data_ptr(), seg.data_ptr(), stream)
+        lib.meshy_distill_loss_bwd(pa, seg.data_ptr(), one.data_ptr(), grad.data_ptr(), stream)
+
+    _checked(lib.meshy_distill_loss_fwd(pa, out_t.data_ptr(), seg.data_ptr(), stream), "meshy_distill_loss_fwd")
+    _checked(lib.meshy_distill_loss_bwd(pa, seg.data_ptr(), one.data_ptr(), grad.data_ptr(), stream),
+             "meshy_distill_loss_bwd")
+    dev_us = _gpu_ms(dev_fb, steps, warmup) * 1e3
+    # fwd reads student (K+1)*4 + teacher K*4 + mask 4 + rollout 4 + doc id 8 (+ 8 for the
+    # offsets); bwd reads the same and writes (K+1)*4
+    per_tok = (K + 1) * 4 + K * 4 + 16
+    nbytes = T * (2 * per_tok + 8 + (K + 1) * 4)
+    out["distill_loss_fwd_bwd_K8_T16384"] = _with_device(_entry(ms * 1e3, nbytes, cpu_ms, tokens=T), dev_us, nbytes)
     return out
 
 
@@ -420,10 +463,43 @@ def bench_ppo(steps, warmup, no_cpu):
             oppo.reduce_mini_metrics(sums)
 
         cpu_ms = _wall_ms(cpu, 5, gpu=False)
-    fwd_bytes = T * 12
+    # The kernels alone, through the C ABI: the document offsets (recomputed for
+    # a fresh micro-batch) and the loss, then its gradient.
+    import ctypes
+
+    from meshy_amd import _lib
+    from meshy_amd import loss as loss_mod
+
+    inputs = loss_mod._Inputs(stub, new_d, old_d, mb, mini, None)
+    new_flat = new_d.detach().reshape(-1)
+    args = inputs.args(new_flat)
+    pa = ctypes.byref(args)
+    lib, stream = _lib.load(), _lib.stream_of(dev)
+    out_t = torch.empty(_lib.PPO_NOUT, device=dev)
+    seg = torch.empty(n + 1, device=dev)
+    one = torch.ones(1, device=dev)
+    grad = torch.empty_like(new_flat)
+    ids, off = inputs.ids, inputs.seg_off
+
+    def dev_fwd():
+        lib.meshy_segment_offsets(ids.data_ptr(), ids.numel(), n + 1, off.data_ptr(), None, stream)
+        lib.meshy_ppo_loss_fwd(pa, out_t.data_ptr(), seg.data_ptr(), stream)
+
+    def dev_bwd():
+        lib.meshy_ppo_loss_bwd(pa, seg.data_ptr(), one.data_ptr(), grad.data_ptr(), stream)
+
+    _checked(lib.meshy_ppo_loss_fwd(pa, out_t.data_ptr(), seg.data_ptr(), stream), "meshy_ppo_loss_fwd")
+    _checked(lib.meshy_ppo_loss_bwd(pa, seg.data_ptr(), one.data_ptr(), grad.data_ptr(), stream), "meshy_ppo_loss_bwd")
+    fwd_dev = _gpu_ms(dev_fwd, steps, warmup) * 1e3
+    bwd_dev = _gpu_ms(dev_bwd, steps, warmup) * 1e3
+    # fwd: new, old, mask, doc id 20 B/token (+ the offsets' 8 B doc id read);
+    # bwd: new, old, mask, doc id read + grad written 24 B/token
+    fwd_bytes = T * 28
+    bwd_bytes = T * 24
     return {
-        "ppo_loss_fwd": _entry(fwd_ms * 1e3, fwd_bytes, tokens=T),
-        "ppo_loss_fwd_bwd": _entry(fb_ms * 1e3, fwd_bytes + T * 16, cpu_ms, tokens=T),
+        "ppo_loss_fwd": _with_device(_entry(fwd_ms * 1e3, fwd_bytes, tokens=T), fwd_dev, fwd_bytes),
+        "ppo_loss_fwd_bwd": _with_device(_entry(fb_ms * 1e3, fwd_bytes + bwd_bytes, cpu_ms, tokens=T),
+                                         fwd_dev + bwd_dev, fwd_bytes + bwd_bytes),
     }
 
 
@@ -649,9 +725,27 @@ def bench_critic(steps, warmup, no_cpu):
             ocritic.clipped_value_error(vc, tc, oc, 0.2).sum().backward()
 
         cpu_ms = _wall_ms(cpu, 5, gpu=False)
+    # The two kernels alone, through the C ABI (the gradient broadcast, stride 0).
+    from meshy_amd import _lib
+
+    lib, stream = _lib.load(), _lib.stream_of(dev)
+    vf, tf, of = v.detach().reshape(-1), t.reshape(-1), o.reshape(-1)
+    err = torch.empty_like(vf)
+    gv = torch.empty_like(vf)
+    one = torch.ones(1, device=dev)
+
+    def dev_fb():
+        lib.meshy_clipped_value_error(vf.data_ptr(), tf.data_ptr(), of.data_ptr(), 1, 0.2, T, err.data_ptr(), stream)
+        lib.meshy_clipped_value_error_bwd(vf.data_ptr(), tf.data_ptr(), of.data_ptr(), 1, 0.2, T, one.data_ptr(), 0,
+                                          gv.data_ptr(), stream)
+
+    _checked(lib.meshy_clipped_value_error(vf.data_ptr(), tf.data_ptr(), of.data_ptr(), 1, 0.2, T, err.data_ptr(),
+                                           stream), "meshy_clipped_value_error")
+    dev_us = _gpu_ms(dev_fb, steps, warmup) * 1e3
     # fwd: v, t, o read + out written; bwd (the sum's gradient is one broadcast
     # value): v, t, o read + grad written
-    out["clipped_value_error_fwd_bwd_1024_docs"] = _entry(ms * 1e3, T * 32, cpu_ms, tokens=T)
+    out["clipped_value_error_fwd_bwd_1024_docs"] = _with_device(_entry(ms * 1e3, T * 32, cpu_ms, tokens=T), dev_us,
+                                                                T * 32)
     S = int(batch.lengths.max())
     rows = n
     pos = np.arange(T) - np.repeat(batch.offsets[:-1], batch.lengths)

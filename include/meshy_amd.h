@@ -273,6 +273,7 @@ typedef struct meshy_distill_args {
     const float* mask;             /* [n_tokens]                              */
     const float* rollout_lp;       /* [n_tokens], nullable                    */
     const int64_t* seg_offsets;    /* [n_docs + 2]                            */
+    const int64_t* doc_ids;        /* [n_tokens], the ids seg_offsets is of   */
     int64_t n_tokens;
     int64_t n_docs;
     int64_t k;                     /* 1 <= k <= 256                           */
@@ -350,6 +351,7 @@ typedef struct meshy_ppo_args {
     const float* adv;              /* [n_docs] or [n_tokens]                  */
     const float* positive_lm_weights; /* [n_docs], nullable                   */
     const int64_t* seg_offsets;    /* [n_docs + 2]                            */
+    const int64_t* doc_ids;        /* [n_tokens], the ids seg_offsets is of   */
     int64_t n_tokens;
     int64_t n_docs;
     int64_t n_docs_global;         /* MiniPlan.n_docs_global                  */

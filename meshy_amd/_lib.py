@@ -122,6 +122,7 @@ class DistillArgs(ctypes.Structure):
         ("mask", c_void_p),
         ("rollout_lp", c_void_p),
         ("seg_offsets", c_void_p),
+        ("doc_ids", c_void_p),
         ("n_tokens", c_int64),
         ("n_docs", c_int64),
         ("k", c_int64),
@@ -148,6 +149,7 @@ class PpoArgs(ctypes.Structure):
         ("adv", c_void_p),
         ("positive_lm_weights", c_void_p),
         ("seg_offsets", c_void_p),
+        ("doc_ids", c_void_p),
         ("n_tokens", c_int64),
         ("n_docs", c_int64),
         ("n_docs_global", c_int64),

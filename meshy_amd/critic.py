@@ -101,10 +101,17 @@ class Accumulator:
         if self._state is None:
             st = AccumulatorState()
             if self._sums is not None:
-                st.n_tokens, st.sum_r, st.sum_r2, st.sum_d, st.sum_d2 = (float(x) for x in self._sums.tolist())
-            st.row_value = [float(x) for x in torch.cat(self._row_value).tolist()]
-            st.row_reward = [float(x) for x in torch.cat(self._row_reward).tolist()]
-            st.row_group = [int(x) for x in torch.cat(self._row_group).tolist()]
+                # One device-to-host copy: the fp64 sums, the per-row values and
+                # rewards as fp64, and the group ids bit-cast to fp64.
+                vals = torch.cat(self._row_value).to(torch.float64)
+                rews = torch.cat(self._row_reward).to(torch.float64)
+                grps = torch.cat(self._row_group).to(torch.int64).view(torch.float64)
+                host = torch.cat([self._sums, vals, rews, grps]).cpu()
+                n = vals.numel()
+                st.n_tokens, st.sum_r, st.sum_r2, st.sum_d, st.sum_d2 = host[:5].tolist()
+                st.row_value = host[5:5 + n].tolist()
+                st.row_reward = host[5 + n:5 + 2 * n].tolist()
+                st.row_group = host[5 + 2 * n:].view(torch.int64).tolist()
             self._state = st
         return self._state
 

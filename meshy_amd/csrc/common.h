@@ -66,48 +66,6 @@ __device__ __forceinline__ T block_sum(T v, T* scratch) {
     }
 }
 
-// Largest d in [0, n_slots] with off[d] <= i (off has n_slots + 1 entries,
-// non-decreasing): the document slot owning token i.
-__device__ __forceinline__ int64_t doc_of(const int64_t* off, int64_t n_slots, int64_t i) {
-    int64_t lo = 0, hi = n_slots;
-    while (lo < hi) {
-        const int64_t mid = (lo + hi + 1) >> 1;
-        if (off[mid] <= i) lo = mid;
-        else hi = mid - 1;
-    }
-    return lo;
-}
-
-// doc_of restricted to [lo, hi] (off[lo] <= i): a few steps when the range is
-// the handful of documents one tile touches.
-__device__ __forceinline__ int64_t doc_of_range(const int64_t* off, int64_t lo, int64_t hi, int64_t i) {
-    while (lo < hi) {
-        const int64_t mid = (lo + hi + 1) >> 1;
-        if (off[mid] <= i) lo = mid;
-        else hi = mid - 1;
-    }
-    return lo;
-}
-
-// doc_of by one whole wavefront (every lane calls it, the result is uniform):
-// a 64-ary search, each round probes 64 evenly spaced slots with one load per
-// lane and keeps the bracket of the last slot <= i, so 4096 slots take 2
-// dependent loads instead of 12.
-__device__ __forceinline__ int64_t doc_of_wave(const int64_t* off, int64_t n_slots, int64_t i) {
-    const int lane = threadIdx.x % kWave;
-    int64_t lo = 0, hi = n_slots;  // invariant: off[lo] <= i, answer in [lo, hi]
-    while (lo < hi) {
-        const int64_t span = hi - lo;
-        const int64_t p = lo + (span * lane + (kWave - 1)) / kWave;
-        const uint64_t b = __ballot(off[p] <= i);  // a prefix of the lanes, lane 0 included
-        const int L = kWave - 1 - __clzll(b);
-        const int64_t pl = lo + (span * L + (kWave - 1)) / kWave;
-        hi = (L == kWave - 1) ? hi : lo + (span * (L + 1) + (kWave - 1)) / kWave - 1;
-        lo = pl;
-    }
-    return lo;
-}
-
 inline int64_t ceil_div(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
 inline size_t align_up(size_t x, size_t a) { return (x + a - 1) / a * a; }

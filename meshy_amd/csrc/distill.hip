@@ -13,8 +13,9 @@
 // plus the sampled label, opd.py:156-162); column K is the sampled token's
 // log-prob and carries no gradient.
 //
-// Layout: documents are contiguous token ranges (seg_offsets).  Tiles of 256
-// tokens, one per thread:
+// Layout: documents are contiguous token ranges (seg_offsets), and doc_ids
+// (non-decreasing) names each token's document.  Tiles of 256 tokens, one per
+// thread:
 //   k_distill_tiles  per token terms; a wavefront segmented scan plus a
 //                    carry over the waves gives each (tile, document) pair's
 //                    partial sums, stored at workspace[tile + document]
@@ -101,37 +102,27 @@ __device__ __forceinline__ void kl_grad(const float* st, const float* te, int K,
     }
 }
 
-// The first and last documents of tile b, searched by waves 0 and 1 at once,
-// into s_range (synchronises the workgroup).
-__device__ __forceinline__ void tile_doc_range(const meshy_distill_args& a, int64_t b, int wid, int lane,
-                                               int64_t* s_range) {
-    if (wid < 2) {
-        const int64_t t0 = b * kTileTok;
-        const int64_t t1 = min(t0 + kTileTok, a.n_tokens);
-        const int64_t dd = doc_of_wave(a.seg_offsets, a.n_docs + 1, wid == 0 ? t0 : t1 - 1);
-        if (lane == 0) s_range[wid] = dd;
-    }
-    __syncthreads();
+// The document of token i, clamped to the slots so that malformed ids stay in bounds.
+__device__ __forceinline__ int64_t doc_at(const meshy_distill_args& a, int64_t i) {
+    return min(max(a.doc_ids[i], static_cast<int64_t>(0)), a.n_docs);
 }
 
 __global__ __launch_bounds__(kTileTok) void k_distill_tiles(meshy_distill_args a, Ws ws) {
     __shared__ float s_tok[kTileWaves][kTokSums];
     __shared__ float s_tail[kTileWaves][2];     // last lane's segmented partials
     __shared__ int64_t s_first[kTileWaves], s_last[kTileWaves];
-    __shared__ int64_t s_range[2];
     const int64_t b = blockIdx.x;
     const int64_t i = b * kTileTok + threadIdx.x;
     const int64_t n_slots = a.n_docs + 1;
     const int lane = threadIdx.x % kWave;
     const int wid = threadIdx.x / kWave;
     const bool ok = i < a.n_tokens;
-    tile_doc_range(a, b, wid, lane, s_range);
 
     float klm = 0.f, mk = 0.f;
     float tok[kTokSums] = {0.f, 0.f, 0.f, 0.f, 0.f};
     int64_t d = n_slots + 1;  // past every slot: never merges with a real token
     if (ok) {
-        d = doc_of_range(a.seg_offsets, s_range[0], s_range[1], i);
+        d = doc_at(a, i);
         mk = a.mask[i];
         float kl = kl_pre(a, i);
         if (a.has_loss_clamp) kl = clamp_rng(kl, -a.loss_max_clamp, a.loss_max_clamp);
@@ -258,11 +249,9 @@ __global__ __launch_bounds__(kFinalThreads) void k_distill_final(meshy_distill_a
 __global__ __launch_bounds__(kTileTok) void k_distill_bwd(meshy_distill_args a, const float* __restrict__ seg_cnt,
                                                           const float* __restrict__ grad_loss,
                                                           float* __restrict__ grad) {
-    __shared__ int64_t s_range[2];
     const int64_t i = static_cast<int64_t>(blockIdx.x) * kTileTok + threadIdx.x;
-    tile_doc_range(a, blockIdx.x, threadIdx.x / kWave, threadIdx.x % kWave, s_range);
     if (i >= a.n_tokens) return;
-    const int64_t d = doc_of_range(a.seg_offsets, s_range[0], s_range[1], i);
+    const int64_t d = doc_at(a, i);
     float D = 0.f;  // the padding slot is not in the loss
     if (d < a.n_docs)
         D = a.per_token_loss ? 1.f / static_cast<float>(max<int64_t>(1, a.n_tokens_global))
@@ -309,8 +298,8 @@ __global__ __launch_bounds__(kTileTok) void k_fkl_bwd(const float* __restrict__ 
 int validate(const meshy_distill_args& a, const char* who) {
     if (a.n_tokens < 0 || a.n_docs < 0) return set_error(MESHY_EINVAL, "%s: negative sizes", who);
     if (a.k < 1 || a.k > kMaxK) return set_error(MESHY_EINVAL, "%s: k must be in [1, %d]", who, kMaxK);
-    if (!a.student || !a.teacher || !a.mask || !a.seg_offsets)
-        return set_error(MESHY_ENULL, "%s: student, teacher, mask and seg_offsets are required", who);
+    if (!a.student || !a.teacher || !a.mask || !a.seg_offsets || !a.doc_ids)
+        return set_error(MESHY_ENULL, "%s: student, teacher, mask, seg_offsets and doc_ids are required", who);
     return MESHY_OK;
 }
 

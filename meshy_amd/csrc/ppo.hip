@@ -9,12 +9,14 @@
 //   per-document sums, token-mean or sequence-mean reduction            (787-809)
 //   diagnostic sums (ratio, clip, KL, ESS, k3, entropy)                 (813-847)
 //
-// Layout: documents are contiguous token ranges given by seg_offsets.  The
-// token axis is cut into tiles of kTile tokens, one workgroup each.  A tile
-// usually overlaps one to three documents: then every thread strides the whole
-// tile (coalesced) and accumulates into up to kFastDocs per-document slots,
-// reduced once per workgroup.  A tile crossing more documents falls back to one
-// wavefront per (tile, document) pair.  Both tiles and documents are ordered,
+// Layout: documents are contiguous token ranges given by seg_offsets, and
+// doc_ids (non-decreasing) names each token's document directly.  The token
+// axis is cut into tiles of kTile tokens, one workgroup each; doc_ids at the
+// tile's ends give its document range with the token loads, without a search.
+// A tile usually overlaps one to three documents: then every thread strides the
+// whole tile (coalesced) and accumulates into up to kFastDocs per-document
+// slots, reduced once per workgroup.  A tile crossing more documents falls back
+// to one wavefront per (tile, document) pair.  Both tiles and documents are ordered,
 // so the overlapping pairs form a monotone staircase and `tile + document`
 // indexes them without collision.
 //   k_ppo_tiles  5 per-document partial sums per pair -> workspace[tile+doc],
@@ -22,8 +24,9 @@
 //   k_ppo_final  one workgroup: per-document totals in tile order, then the
 //                loss, ESS and every diagnostic in one fused block reduction
 //                (fixed order, no atomics: bitwise reproducible);
-//   k_ppo_bwd    per token: d(total loss)/d new_lp as torch autograd gives it
-//                (min splits ties 1/2-1/2, clamp passes on [lo, hi]).
+//   k_ppo_bwd    per token (8 per thread): d(total loss)/d new_lp as torch
+//                autograd gives it (min splits ties 1/2-1/2, clamp passes on
+//                [lo, hi]), the document's factors gathered by doc_ids.
 #include <math.h>
 
 #include <algorithm>
@@ -148,31 +151,35 @@ __device__ __forceinline__ void token_contrib_v(const meshy_ppo_args& a, const T
     c.tok[TS_ENT] = a.entropy ? x.en * mk : 0.f;
 }
 
+// The document of token i, clamped to the slots so that malformed ids stay in bounds.
+__device__ __forceinline__ int64_t doc_at(const meshy_ppo_args& a, int64_t i) {
+    return min(max(a.doc_ids[i], static_cast<int64_t>(0)), a.n_docs);
+}
+
 __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Workspace ws) {
-    __shared__ int64_t s_off[kFastDocs + 1];
-    __shared__ int64_t s_range[2];
     __shared__ float s_red[kWaves][kTokSums + kFastDocs * kSegSums];
     const int64_t b = blockIdx.x;
     const int64_t t0 = b * kTile;
     const int64_t t1 = min(t0 + kTile, a.n_tokens);
-    const int64_t n_slots = a.n_docs + 1;
     const int lane = threadIdx.x % kWave;
     const int wid = threadIdx.x / kWave;
-    // The tile's first and last documents, searched by waves 0 and 1 at once.
-    if (wid < 2) {
-        const int64_t d = doc_of_wave(a.seg_offsets, n_slots, wid == 0 ? t0 : t1 - 1);
-        if (lane == 0) s_range[wid] = d;
+    // The tile's tokens and its document range, loaded together.
+    constexpr int kPer = static_cast<int>(kTile / kThreads);
+    TokIn in[kPer];
+    int64_t id[kPer];
+#pragma unroll
+    for (int q = 0; q < kPer; ++q) {
+        const int64_t i = t0 + q * kThreads + threadIdx.x;
+        in[q] = load_tok(a, i, i < t1);
+        id[q] = i < t1 ? a.doc_ids[i] : 0;
     }
-    __syncthreads();
-    const int64_t d_first = s_range[0];
-    const int64_t nd = s_range[1] - d_first + 1;
+    const int64_t d_first = doc_at(a, t0);
+    const int64_t nd = max(doc_at(a, t1 - 1), d_first) - d_first + 1;
     float acc[kTokSums];
 #pragma unroll
     for (int k = 0; k < kTokSums; ++k) acc[k] = 0.f;
 
     if (nd <= kFastDocs) {
-        if (threadIdx.x <= nd) s_off[threadIdx.x] = a.seg_offsets[d_first + threadIdx.x];
-        __syncthreads();
         float A_d[kFastDocs], W_d[kFastDocs];
 #pragma unroll
         for (int r = 0; r < kFastDocs; ++r) {
@@ -186,21 +193,12 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
         for (int r = 0; r < kFastDocs; ++r)
 #pragma unroll
             for (int k = 0; k < kSegSums; ++k) sg[r][k] = 0.f;
-        // Every load of the thread's kPer tokens first, then the arithmetic.
-        constexpr int kPer = static_cast<int>(kTile / kThreads);
-        TokIn in[kPer];
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            const int64_t i = t0 + q * kThreads + threadIdx.x;
-            in[q] = load_tok(a, i, i < t1);
-        }
 #pragma unroll
         for (int q = 0; q < kPer; ++q) {
             const int64_t i = t0 + q * kThreads + threadIdx.x;
             if (i >= t1) break;
-            int slot = 0;
-#pragma unroll
-            for (int j = 1; j < kFastDocs; ++j) slot += (j < nd && i >= s_off[j]) ? 1 : 0;
+            const int64_t rel = id[q] - d_first;
+            const int slot = static_cast<int>(min(max(rel, static_cast<int64_t>(0)), nd - 1));
             float A = 0.f, W = 0.f;
 #pragma unroll
             for (int r = 0; r < kFastDocs; ++r) {
@@ -233,8 +231,10 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
                 for (int k = 0; k < kSegSums; ++k) s_red[wid][kTokSums + r * kSegSums + k] = sg[r][k];
         }
         __syncthreads();
+        // Every document between the first and the last lies within the tile
+        // (or is empty, with zero sums), so its (tile, document) pair is its own.
         const int j = threadIdx.x;
-        if (j < kTokSums + kFastDocs * kSegSums) {
+        if (j < kTokSums + nd * kSegSums) {
             float v = 0.f;
 #pragma unroll
             for (int w = 0; w < kWaves; ++w) v += s_red[w][j];
@@ -243,9 +243,7 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
             } else {
                 const int r = (j - kTokSums) / kSegSums;
                 const int k = (j - kTokSums) % kSegSums;
-                const int64_t lo = max(s_off[r], t0);
-                const int64_t hi = r < nd ? min(s_off[r + 1], t1) : lo;
-                if (lo < hi) ws.seg[(b + d_first + r) * kSegSums + k] = v;
+                ws.seg[(b + d_first + r) * kSegSums + k] = v;
             }
         }
         return;
@@ -421,94 +419,78 @@ __device__ __forceinline__ float doc_scale(const meshy_ppo_args& a, const float*
                             : 1.f / (fmaxf(seg_cnt[d], 1.f) * static_cast<float>(max<int64_t>(1, a.n_docs_global)));
 }
 
+constexpr int kBwdItems = 8;  // tokens per thread of k_ppo_bwd, strided by the workgroup
+
 __global__ __launch_bounds__(kThreads) void k_ppo_bwd(meshy_ppo_args a, const float* __restrict__ seg_cnt,
                                                       const float* __restrict__ grad_loss,
                                                       float* __restrict__ grad_new) {
-    __shared__ int64_t s_off[kFastDocs + 1];
-    __shared__ int64_t s_range[2];
-    const int64_t b = blockIdx.x;
-    const int64_t t0 = b * kTile;
-    const int64_t t1 = min(t0 + kTile, a.n_tokens);
-    const int64_t n_slots = a.n_docs + 1;
-    const int wid = threadIdx.x / kWave;
-    if (wid < 2) {
-        const int64_t d = doc_of_wave(a.seg_offsets, n_slots, wid == 0 ? t0 : t1 - 1);
-        if (threadIdx.x % kWave == 0) s_range[wid] = d;
-    }
-    __syncthreads();
-    const int64_t d_first = s_range[0];
-    const int64_t nd = s_range[1] - d_first + 1;
+    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kThreads * kBwdItems + threadIdx.x;
     const float G = grad_loss[0];
-    if (nd <= kFastDocs) {
-        if (threadIdx.x <= nd) s_off[threadIdx.x] = a.seg_offsets[d_first + threadIdx.x];
-        __syncthreads();
-        float A_d[kFastDocs], W_d[kFastDocs], gD_d[kFastDocs];
+    TokIn in[kBwdItems];
+    int64_t d[kBwdItems];
 #pragma unroll
-        for (int r = 0; r < kFastDocs; ++r) {
-            const int64_t d = d_first + r;
-            const bool real = r < nd && d < a.n_docs;
-            A_d[r] = (!a.adv_per_token && real) ? a.adv[d] : 0.f;
-            W_d[r] = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
-            gD_d[r] = real ? G * doc_scale(a, seg_cnt, d) : 0.f;
-        }
-        constexpr int kPer = static_cast<int>(kTile / kThreads);
-        TokIn in[kPer];
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            const int64_t i = t0 + q * kThreads + threadIdx.x;
-            in[q] = load_tok(a, i, i < t1);
-        }
-#pragma unroll
-        for (int q = 0; q < kPer; ++q) {
-            const int64_t i = t0 + q * kThreads + threadIdx.x;
-            if (i >= t1) break;
-            int slot = 0;
-#pragma unroll
-            for (int j = 1; j < kFastDocs; ++j) slot += (j < nd && i >= s_off[j]) ? 1 : 0;
-            float A = 0.f, W = 0.f, gD = 0.f;
-#pragma unroll
-            for (int r = 0; r < kFastDocs; ++r) {
-                A = (slot == r) ? A_d[r] : A;
-                W = (slot == r) ? W_d[r] : W;
-                gD = (slot == r) ? gD_d[r] : gD;
-            }
-            if (a.adv_per_token) A = in[q].ad;
-            grad_new[i] = token_grad_v(a, in[q], A, W, gD);
-        }
-        return;
+    for (int q = 0; q < kBwdItems; ++q) {
+        const int64_t i = t0 + q * kThreads;
+        const bool ok = i < a.n_tokens;
+        in[q] = load_tok(a, i, ok);
+        d[q] = ok ? doc_at(a, i) : 0;
     }
-    for (int64_t i = t0 + threadIdx.x; i < t1; i += kThreads) {
-        const int64_t d = doc_of(a.seg_offsets, n_slots, i);
-        const bool real = d < a.n_docs;
-        const TokIn x = load_tok(a, i, true);
-        const float A = a.adv_per_token ? x.ad : (real ? a.adv[d] : 0.f);
-        const float W = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
-        grad_new[i] = token_grad_v(a, x, A, W, G * doc_scale(a, seg_cnt, d));
+#pragma unroll
+    for (int q = 0; q < kBwdItems; ++q) {
+        const int64_t i = t0 + q * kThreads;
+        if (i >= a.n_tokens) break;
+        const bool real = d[q] < a.n_docs;
+        const float A = a.adv_per_token ? in[q].ad : (real ? a.adv[d[q]] : 0.f);
+        const float W = (a.positive_lm_weights && real) ? a.positive_lm_weights[d[q]] : 0.f;
+        grad_new[i] = token_grad_v(a, in[q], A, W, G * doc_scale(a, seg_cnt, d[q]));
     }
 }
 
 // seg_offsets[d] = first token with id >= d, for sorted ids: token i writes
 // every d in (ids[i-1], ids[i]]; the slots after the last id get n.
+typedef long long i64x2 __attribute__((ext_vector_type(2)));
+constexpr int kSegItems = 8;  // doc ids per thread of k_segment_offsets
+
+// Thread t owns the boundaries before positions i0 .. i0 + 7 (i0 = 8 t) and,
+// for the last thread, the one at n: every document slot whose first token is
+// there (empty slots included) gets offset i.  16-byte loads when aligned.
 __global__ __launch_bounds__(kThreads) void k_segment_offsets(const int64_t* __restrict__ ids, int64_t n,
-                                                              int64_t n_slots, int64_t* __restrict__ off,
+                                                              int64_t n_slots, bool vec, int64_t* __restrict__ off,
                                                               int32_t* __restrict__ unsorted) {
-    const int64_t stride = static_cast<int64_t>(gridDim.x) * kThreads;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x; i <= n; i += stride) {
-        const int64_t prev = (i == 0) ? -1 : ids[i - 1];
-        const int64_t cur = (i == n) ? n_slots : ids[i];
+    const int64_t i0 = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * kSegItems;
+    if (i0 > n) return;
+    int64_t v[kSegItems + 1];  // v[0] = ids[i0 - 1], v[k + 1] = ids[i0 + k] (n_slots from n on)
+    v[0] = (i0 == 0) ? -1 : ids[i0 - 1];
+    if (vec && i0 + kSegItems <= n) {
+#pragma unroll
+        for (int q = 0; q < kSegItems / 2; ++q) {
+            const i64x2 w = *reinterpret_cast<const i64x2*>(ids + i0 + 2 * q);
+            v[2 * q + 1] = w.x;
+            v[2 * q + 2] = w.y;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kSegItems; ++k) v[k + 1] = (i0 + k < n) ? ids[i0 + k] : n_slots;
+    }
+#pragma unroll
+    for (int k = 0; k < kSegItems; ++k) {
+        const int64_t i = i0 + k;
+        if (i > n) break;
+        const int64_t prev = v[k];
+        const int64_t cur = v[k + 1];
         if (unsorted && i > 0 && i < n && prev > cur) unsorted[0] = 1;
         const int64_t lo = max<int64_t>(prev + 1, 0);
         const int64_t hi = min<int64_t>(cur, n_slots - 1);
         for (int64_t d = lo; d <= hi; ++d) off[d] = i;
     }
-    if (blockIdx.x == 0 && threadIdx.x == 0) off[n_slots] = n;
+    if (i0 == 0) off[n_slots] = n;
 }
 
 int validate(const meshy_ppo_args& a, const char* who) {
     if (a.n_tokens < 0 || a.n_docs < 0) return set_error(MESHY_EINVAL, "%s: negative sizes", who);
-    if (!a.new_lp || !a.old_lp || !a.mask || !a.seg_offsets || (a.n_docs > 0 && !a.adv && !a.adv_per_token) ||
-        (a.adv_per_token && !a.adv))
-        return set_error(MESHY_ENULL, "%s: new_lp, old_lp, mask, adv and seg_offsets are required", who);
+    if (!a.new_lp || !a.old_lp || !a.mask || !a.seg_offsets || !a.doc_ids ||
+        (a.n_docs > 0 && !a.adv && !a.adv_per_token) || (a.adv_per_token && !a.adv))
+        return set_error(MESHY_ENULL, "%s: new_lp, old_lp, mask, adv, seg_offsets and doc_ids are required", who);
     if (a.use_icepop && !a.rollout_lp) return set_error(MESHY_EINVAL, "%s: IcePop requires rollout log-probabilities", who);
     if (a.positive_lm_coef != 0.f && !a.positive_lm_weights && a.n_docs > 0)
         return set_error(MESHY_EINVAL, "%s: Positive LM loss requires group weights", who);
@@ -556,7 +538,8 @@ extern "C" int meshy_ppo_loss_bwd(const meshy_ppo_args* args, const float* seg_c
     if (rc) return rc;
     const int64_t nt = n_tiles_of(a.n_tokens);
     if (nt == 0) return MESHY_OK;
-    hipLaunchKernelGGL(k_ppo_bwd, dim3(static_cast<unsigned>(nt)), dim3(kThreads), 0, stream, a, seg_cnt,
+    const int64_t nb = ceil_div(a.n_tokens, static_cast<int64_t>(kThreads) * kBwdItems);
+    hipLaunchKernelGGL(k_ppo_bwd, dim3(static_cast<unsigned>(nb)), dim3(kThreads), 0, stream, a, seg_cnt,
                        grad_loss, grad_new);
     return check_launch("meshy_ppo_loss_bwd");
 }
@@ -568,8 +551,11 @@ extern "C" int meshy_segment_offsets(const int64_t* doc_ids, int64_t n_tokens, i
     if (n_tokens < 0 || n_slots < 1) return set_error(MESHY_EINVAL, "meshy_segment_offsets: bad sizes");
     if (!seg_offsets || (n_tokens > 0 && !doc_ids))
         return set_error(MESHY_ENULL, "meshy_segment_offsets: NULL pointer");
-    const int64_t blocks = std::max<int64_t>(1, std::min<int64_t>(2048, ceil_div(n_tokens + 1, kThreads)));
+    // n / 8 + 1 threads: the last one also owns the boundary at n.
+    const int64_t blocks = ceil_div(n_tokens / kSegItems + 1, kThreads);
+    if (blocks > INT32_MAX) return set_error(MESHY_EINVAL, "meshy_segment_offsets: too many tokens");
+    const bool vec = reinterpret_cast<uintptr_t>(doc_ids) % 16 == 0;
     hipLaunchKernelGGL(k_segment_offsets, dim3(static_cast<unsigned>(blocks)), dim3(kThreads), 0, stream,
-                       doc_ids, n_tokens, n_slots, seg_offsets, unsorted);
+                       doc_ids, n_tokens, n_slots, vec, seg_offsets, unsorted);
     return check_launch("meshy_segment_offsets");
 }

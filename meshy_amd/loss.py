@@ -80,6 +80,18 @@ class _Inputs:
             self.pos_w = mb.positive_lm_weights.reshape(-1).to(torch.float32).contiguous()
         _lib.require_gpu(new_lp, self.old, self.mask, self.adv, mb.doc_ids, self.rollout, self.entropy,
                          self.pos_w)
+        self.ids = mb.doc_ids.reshape(-1).to(torch.int64).contiguous()
+        # The kernels read every per-token array at each of the n_tokens positions.
+        per_token = [("old_lp", self.old), ("mask", self.mask), ("doc_ids", self.ids),
+                     ("rollout_logprobs", self.rollout), ("entropy", self.entropy)]
+        per_doc = [("positive_lm_weights", self.pos_w)]
+        (per_token if self.adv_per_token else per_doc).append(("advantages", self.adv))
+        for name, x in per_token:
+            if x is not None and x.numel() != self.n_tokens:
+                raise ValueError(f"new_lp has {self.n_tokens} tokens but {name} has {x.numel()}")
+        for name, x in per_doc:
+            if x is not None and x.numel() < self.n_docs:
+                raise ValueError(f"{name} has {x.numel()} entries for {self.n_docs} documents")
         self.seg_off = batch_segment_offsets(mb)
         ws = _lib.load().meshy_ppo_workspace_size(self.n_tokens, self.n_docs)
         self.workspace = torch.empty(max(int(ws), 1), dtype=torch.uint8, device=dev)
@@ -103,6 +115,7 @@ class _Inputs:
         a.adv = self.adv.data_ptr()
         a.positive_lm_weights = _lib.ptr(self.pos_w)
         a.seg_offsets = self.seg_off.data_ptr()
+        a.doc_ids = self.ids.data_ptr()
         a.n_tokens = self.n_tokens
         a.n_docs = self.n_docs
         a.n_docs_global = self.n_docs_global

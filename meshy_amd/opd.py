@@ -120,6 +120,12 @@ class _Inputs:
         self.rollout = (None if mb.rollout_logprobs is None else
                         mb.rollout_logprobs.detach().reshape(-1).to(torch.float32).contiguous())
         _lib.require_gpu(self.teacher, self.mask, mb.doc_ids, self.rollout)
+        self.ids = mb.doc_ids.reshape(-1).to(torch.int64).contiguous()
+        # The kernels read every per-token array at each of the n_tokens positions.
+        for name, x, width in (("teacher_topk_logprobs", self.teacher, k), ("mask", self.mask, 1),
+                               ("doc_ids", self.ids, 1), ("rollout_logprobs", self.rollout, 1)):
+            if x is not None and x.numel() != n_tokens * width:
+                raise ValueError(f"the student has {n_tokens} tokens but {name} has {x.numel() // width}")
         self.seg_off = batch_segment_offsets(mb)
         ws = _lib.load().meshy_distill_workspace_size(n_tokens, self.n_docs)
         self.workspace = torch.empty(max(int(ws), 1), dtype=torch.uint8, device=device)
@@ -136,6 +142,7 @@ class _Inputs:
         a.mask = self.mask.data_ptr()
         a.rollout_lp = _lib.ptr(self.rollout)
         a.seg_offsets = self.seg_off.data_ptr()
+        a.doc_ids = self.ids.data_ptr()
         a.n_tokens = self.n_tokens
         a.n_docs = self.n_docs
         a.k = self.k

@@ -80,7 +80,7 @@ def test_struct_entry_points_reject():
     a.k = 8
     a.n_tokens = 16
     assert lib.meshy_distill_loss_fwd(ctypes.byref(a), FAKE, None, None) == ENULL  # student missing
-    a.student = a.teacher = a.mask = a.seg_offsets = FAKE
+    a.student = a.teacher = a.mask = a.seg_offsets = a.doc_ids = FAKE
     a.workspace, a.workspace_bytes = FAKE, 1
     assert lib.meshy_distill_loss_fwd(ctypes.byref(a), FAKE, None, None) == ESPACE
     assert b"workspace" in lib.meshy_last_error()

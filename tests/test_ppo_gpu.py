@@ -218,6 +218,39 @@ def test_many_tiny_documents_and_empty_pad(dev):
     _compare(dev, new, old, mask, doc_ids, adv, 3000, per_token_loss=False)
 
 
+@pytest.mark.parametrize("per_token_loss", [True, False])
+def test_empty_document_slots_inside_tiles(dev, per_token_loss):
+    """Documents without tokens between the ids a tile holds (ids 0, 2, 3, 7 ...):
+    the tile's document range counts them, their sums stay zero and no other
+    (tile, document) pair is disturbed; documents cross 2048-token tiles."""
+    g = torch.Generator().manual_seed(21)
+    n_docs = 40
+    present = sorted(torch.randperm(n_docs, generator=g)[:18].tolist())
+    lens = torch.randint(50, 1500, (len(present),), generator=g).tolist()
+    doc_ids = torch.cat([torch.full((L,), d) for d, L in zip(present, lens)]).reshape(1, -1)
+    T = doc_ids.numel()
+    mask = (torch.rand(1, T, generator=g) > 0.2).float()
+    old = -torch.rand(1, T, generator=g) * 4
+    new = old + torch.randn(1, T, generator=g) * 0.3
+    adv = torch.randn(n_docs, generator=g)
+    _compare(dev, new, old, mask, doc_ids, adv, n_docs, per_token_loss=per_token_loss)
+
+
+def test_size_mismatch_raises(dev):
+    from meshy_amd.batch import Batch
+    from meshy_amd.loss import ppo_clip_loss
+    from meshy_amd.plan import MiniPlan
+
+    stub = NS(ppo_clip_eps_low=0.2, ppo_clip_eps_high=0.28, use_tis=False, calculate_per_token_loss=True,
+              sharder=_NoCp(), parallel_dims=NS(cp=1))
+    z = torch.zeros(1, 8, dtype=torch.long, device=dev)
+    mb = Batch(z, z, z.int(), torch.ones(1, 8, device=dev), torch.zeros(1, 7, dtype=torch.long, device=dev),
+               torch.ones(1, device=dev), None, torch.zeros(1, device=dev), 1)
+    new = torch.zeros(1, 8, device=dev)
+    with pytest.raises(ValueError, match="doc_ids"):
+        ppo_clip_loss(stub, new, new, mb, MiniPlan((), 1, 8, ()))
+
+
 def test_ppo_512_docs_full_size(dev):
     """~2M packed tokens, 512 docs, token-mean, eps 0.2/0.28, TIS off."""
     from meshy_amd import workloads
@@ -253,6 +286,36 @@ def test_deterministic(dev):
         outs.append((loss.item(), torch.stack(list(sums.values())).cpu(), nd.grad.cpu()))
     assert outs[0][0] == outs[1][0]
     assert torch.equal(outs[0][1], outs[1][1]) and torch.equal(outs[0][2], outs[1][2])
+
+
+@pytest.mark.parametrize("n,n_slots,offset", [(0, 3, 0), (1, 1, 0), (7, 5, 0), (8, 4, 0), (9, 20, 1),
+                                               (17, 3, 1), (100_003, 513, 0), (1_000_000, 4097, 1)])
+def test_segment_offsets_match_searchsorted(dev, n, n_slots, offset):
+    """off[d] = first position whose id is >= d (empty slots and slots past the
+    last id included), off[n_slots] = n; lengths off a multiple of 8 and a
+    misaligned view exercise the scalar path."""
+    from meshy_amd.loss import segment_offsets
+
+    rng = np.random.default_rng(n + n_slots)
+    ids = np.sort(rng.integers(0, n_slots, n)).astype(np.int64)
+    if n > 10:
+        ids[ids == ids[n // 2]] = ids[n // 2] - 1 if ids[n // 2] > 0 else 0  # leave an empty slot
+        ids.sort()
+    base = torch.zeros(n + offset, dtype=torch.int64)
+    base[offset:] = torch.from_numpy(ids)
+    got = segment_offsets(base.to(dev)[offset:], n_slots).cpu().numpy()
+    want = np.concatenate([np.searchsorted(ids, np.arange(n_slots), side="left"), [n]])
+    assert np.array_equal(got, want)
+
+
+def test_segment_offsets_detect_unsorted(dev):
+    from meshy_amd.loss import segment_offsets
+
+    ids = torch.arange(1000, dtype=torch.int64) // 10
+    assert segment_offsets(ids.to(dev), 100, check_sorted=True).shape == (101,)
+    ids[517] = 3
+    with pytest.raises(ValueError):
+        segment_offsets(ids.to(dev), 100, check_sorted=True)
 
 
 def test_segment_offsets_cache_follows_doc_ids(dev):
