@@ -143,18 +143,28 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
     if dev.type != "cuda":
         raise ValueError("meshy_amd runs GAE on a HIP device; self.device must be a cuda device")
     n = len(samples)
-    widths = [min(int(len(td["tokens"])), seq_len) for td in samples]
+    # One pass over the samples: widths, the mask / value slices and the rewards.
+    widths, masks, vals, rewards = [], [], [], []
     for j, td in enumerate(samples):
-        if int(td["values"][:widths[j]].shape[0]) != widths[j]:
+        tok = td["tokens"]
+        L = min(int(tok.shape[0]) if isinstance(tok, torch.Tensor) else len(tok), seq_len)
+        v = td["values"]
+        v = v if v.shape[0] == L else v[:L]  # a view only where a sample is cut
+        if int(v.shape[0]) != L:
             raise ValueError(
                 f"row {j}: critic published {tuple(td['values'].shape)} values "
-                f"for {widths[j]} tokens; the critic and the trainer disagree about "
+                f"for {L} tokens; the critic and the trainer disagree about "
                 f"the sequence"
             )
+        widths.append(L)
+        m = td["mask_assistant"]
+        masks.append(m if m.shape[0] == L else m[:L])
+        vals.append(v)
+        rewards.append(td["reward"])
     offsets = np.zeros(n + 1, np.int64)
     np.cumsum(widths, out=offsets[1:])
     total = int(offsets[-1])
-    bf16 = all(td["values"].dtype == torch.bfloat16 for td in samples)
+    bf16 = all(v.dtype == torch.bfloat16 for v in vals)
     vdt = torch.bfloat16 if bf16 else torch.float32
     lay = _Layout()
     lay.add("mask", total, torch.float32)
@@ -162,13 +172,14 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
     lay.add("reward", n, torch.float32)
     lay.add("offsets", n + 1, torch.int64)
     host = torch.empty(lay.size, dtype=torch.uint8, pin_memory=True)
-    torch.cat([td["mask_assistant"][:L].to(device="cpu", dtype=torch.float32) for td, L in zip(samples, widths)],
-              out=lay.view(host, "mask"))
-    torch.cat([td["values"][:L].to(device="cpu", dtype=vdt) for td, L in zip(samples, widths)],
-              out=lay.view(host, "values"))
-    lay.view(host, "reward").copy_(torch.tensor(
-        [float(td["reward"].reshape(-1)[0].item()) if isinstance(td["reward"], torch.Tensor) else float(td["reward"])
-         for td in samples], dtype=torch.float32))
+    torch.cat([m.to(device="cpu", dtype=torch.float32) for m in masks], out=lay.view(host, "mask"))
+    torch.cat([v.to(device="cpu", dtype=vdt) for v in vals], out=lay.view(host, "values"))
+    if all(isinstance(r, torch.Tensor) and r.numel() == 1 for r in rewards):
+        reward = torch.stack([r.reshape(()) for r in rewards]).to(device="cpu", dtype=torch.float32)
+    else:
+        reward = torch.tensor([float(r.reshape(-1)[0]) if isinstance(r, torch.Tensor) else float(r) for r in rewards],
+                              dtype=torch.float32)
+    lay.view(host, "reward").copy_(reward)
     lay.view(host, "offsets").copy_(torch.from_numpy(offsets))
     dbuf = torch.empty(lay.size, dtype=torch.uint8, device=dev)
     dbuf.copy_(host, non_blocking=True)
@@ -198,8 +209,8 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
     g.workspace_bytes = ws.numel()
     rc = lib.meshy_gae_attach(_lib.ctypes.byref(g), _lib.stream_of(dev))
     _lib.check(rc, "meshy_gae_attach")
-    for j, td in enumerate(samples):
-        td[ADVANTAGE_TOKENS] = adv[int(offsets[j]):int(offsets[j + 1])]
+    for td, view in zip(samples, torch.split(adv[:total], widths)):
+        td[ADVANTAGE_TOKENS] = view
     return dict(zip(CRITIC_METRICS, metrics.tolist()))
 
 
