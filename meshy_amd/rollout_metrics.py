@@ -51,11 +51,17 @@ def _scalars(samples, columns, f: str) -> list[float]:
         if v is None:
             return []
         return [float(x) for x in (v.reshape(-1).tolist() if isinstance(v, torch.Tensor) else v)]
+    present = [v for v in (_get(s, f) for s in samples) if v is not None]
+    if (present and all(torch.is_tensor(v) and v.dim() == 0 for v in present)
+            and len({(v.dtype, v.device) for v in present}) == 1):
+        # One stack and one host copy instead of one per sample (one dtype, so
+        # nothing is promoted or rounded).
+        try:
+            return [float(x) for x in torch.stack([v.detach() for v in present]).cpu().tolist()]
+        except RuntimeError:
+            pass  # mixed devices or dtypes torch cannot stack: the general path below
     out = []
-    for s in samples:
-        v = _get(s, f)
-        if v is None:
-            continue
+    for v in present:
         for x in (v.detach().cpu().reshape(-1).tolist() if torch.is_tensor(v) else
                   (list(v) if hasattr(v, "__iter__") else [v])):
             try:
