@@ -38,6 +38,56 @@ __device__ __forceinline__ T wave_sum(T v) {
     return v;
 }
 
+// fp32 and fp64 sums over the 64 lanes without the LDS crossbar: each 16-lane
+// row reduces with DPP rotations (row_ror 8, 4, 2, 1: full-rate adds, a
+// balanced tree), then the four row sums are read into scalars and added as
+// (r0 + r1) + (r2 + r3).  Every lane gets the total; all 64 lanes must be active.
+template <int kCtrl>
+__device__ __forceinline__ int dpp_i32(int v) {
+    return __builtin_amdgcn_update_dpp(0, v, kCtrl, 0xF, 0xF, false);
+}
+constexpr int kDppRowRor1 = 0x121, kDppRowRor2 = 0x122, kDppRowRor4 = 0x124, kDppRowRor8 = 0x128;
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_f32(float v) {
+    return __int_as_float(dpp_i32<kCtrl>(__float_as_int(v)));
+}
+
+template <int kCtrl>
+__device__ __forceinline__ double dpp_f64(double v) {
+    const long long b = __double_as_longlong(v);
+    const unsigned lo = static_cast<unsigned>(dpp_i32<kCtrl>(static_cast<int>(b & 0xffffffffll)));
+    const unsigned hi = static_cast<unsigned>(dpp_i32<kCtrl>(static_cast<int>(b >> 32)));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+__device__ __forceinline__ float lane_f32(float v, int lane) {
+    return __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), lane));
+}
+
+__device__ __forceinline__ double lane_f64(double v, int lane) {
+    const long long b = __double_as_longlong(v);
+    const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(b & 0xffffffffll), lane));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(b >> 32), lane));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+
+__device__ __forceinline__ float wave_sum(float v) {
+    v += dpp_f32<kDppRowRor8>(v);
+    v += dpp_f32<kDppRowRor4>(v);
+    v += dpp_f32<kDppRowRor2>(v);
+    v += dpp_f32<kDppRowRor1>(v);
+    return (lane_f32(v, 0) + lane_f32(v, 16)) + (lane_f32(v, 32) + lane_f32(v, 48));
+}
+
+__device__ __forceinline__ double wave_sum(double v) {
+    v += dpp_f64<kDppRowRor8>(v);
+    v += dpp_f64<kDppRowRor4>(v);
+    v += dpp_f64<kDppRowRor2>(v);
+    v += dpp_f64<kDppRowRor1>(v);
+    return (lane_f64(v, 0) + lane_f64(v, 16)) + (lane_f64(v, 32) + lane_f64(v, 48));
+}
+
 template <typename T>
 __device__ __forceinline__ T wave_max(T v) {
 #pragma unroll
