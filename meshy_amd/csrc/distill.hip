@@ -197,11 +197,18 @@ __global__ __launch_bounds__(kFinalThreads) void k_distill_final(meshy_distill_a
                                                                  float* __restrict__ seg_cnt_out) {
     constexpr int kVals = 1 + kTokSums;
     __shared__ double s_red[kFinalThreads / kWave][kVals];
+    __shared__ double s_tot[kVals];
     const int64_t n_slots = a.n_docs + 1;
     const int64_t nt = n_tiles(a.n_tokens);
     double v[kVals];
 #pragma unroll
     for (int k = 0; k < kVals; ++k) v[k] = 0.0;
+    // The first kFinalThreads tiles' token sums load first: they depend on
+    // nothing and arrive while the documents' chain runs.
+    float tok0[kTokSums];
+    const bool has_tile = threadIdx.x < nt;
+#pragma unroll
+    for (int k = 0; k < kTokSums; ++k) tok0[k] = has_tile ? ws.tok[threadIdx.x * kTokSums + k] : 0.f;
     for (int64_t d = threadIdx.x; d < n_slots; d += kFinalThreads) {
         const int64_t lo = a.seg_offsets[d];
         const int64_t hi = a.seg_offsets[d + 1];
@@ -215,7 +222,9 @@ __global__ __launch_bounds__(kFinalThreads) void k_distill_final(meshy_distill_a
         if (seg_cnt_out) seg_cnt_out[d] = cnt;
         if (d < a.n_docs) v[0] += a.per_token_loss ? sum : sum / fmaxf(cnt, 1.f);
     }
-    for (int64_t t = threadIdx.x; t < nt; t += kFinalThreads) {
+#pragma unroll
+    for (int k = 0; k < kTokSums; ++k) v[1 + k] += tok0[k];
+    for (int64_t t = threadIdx.x + kFinalThreads; t < nt; t += kFinalThreads) {
 #pragma unroll
         for (int k = 0; k < kTokSums; ++k) v[1 + k] += ws.tok[t * kTokSums + k];
     }
@@ -228,13 +237,14 @@ __global__ __launch_bounds__(kFinalThreads) void k_distill_final(meshy_distill_a
         for (int k = 0; k < kVals; ++k) s_red[wid][k] = v[k];
     }
     __syncthreads();
+    if (threadIdx.x < kVals) {
+        double s = 0.0;
+        for (int w = 0; w < kFinalThreads / kWave; ++w) s += s_red[w][threadIdx.x];
+        s_tot[threadIdx.x] = s;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        double t[kVals];
-#pragma unroll
-        for (int k = 0; k < kVals; ++k) {
-            t[k] = 0.0;
-            for (int w = 0; w < kFinalThreads / kWave; ++w) t[k] += s_red[w][k];
-        }
+        const double* t = s_tot;
         const double den = a.per_token_loss ? static_cast<double>(max<int64_t>(1, a.n_tokens_global))
                                             : static_cast<double>(max<int64_t>(1, a.n_docs_global));
         out[MESHY_DISTILL_LOSS] = static_cast<float>(t[0] / den);

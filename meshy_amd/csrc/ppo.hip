@@ -294,11 +294,19 @@ __global__ __launch_bounds__(kFinalThreads) void k_ppo_final(meshy_ppo_args a, W
                                                              float* __restrict__ out,
                                                              float* __restrict__ seg_cnt_out) {
     __shared__ double s_red[kFinalThreads / kWave][kFinalVals];
+    __shared__ double s_tot[kFinalVals];
     const int64_t n_slots = a.n_docs + 1;
     const int64_t n_tiles = n_tiles_of(a.n_tokens);
     double v[kFinalVals];
 #pragma unroll
     for (int k = 0; k < kFinalVals; ++k) v[k] = 0.0;
+    // The token-level sums of the first kFinalThreads tiles are loaded first:
+    // they depend on nothing, so they arrive while the documents' chain
+    // (offsets, then their tiles' partials) runs.
+    float tok0[kTokSums];
+    const bool has_tile = threadIdx.x < n_tiles;
+#pragma unroll
+    for (int k = 0; k < kTokSums; ++k) tok0[k] = has_tile ? ws.tok[threadIdx.x * kTokSums + k] : 0.f;
     // Per-document totals (tile order) and their contributions: v[0..3] =
     // loss terms, positive-LM terms, ESS terms, documents with tokens.
     for (int64_t d = threadIdx.x; d < n_slots; d += kFinalThreads) {
@@ -331,7 +339,9 @@ __global__ __launch_bounds__(kFinalThreads) void k_ppo_final(meshy_ppo_args a, W
         }
     }
     // Token-level sums of every tile: v[4..13].
-    for (int64_t b = threadIdx.x; b < n_tiles; b += kFinalThreads) {
+#pragma unroll
+    for (int k = 0; k < kTokSums; ++k) v[4 + k] += tok0[k];
+    for (int64_t b = threadIdx.x + kFinalThreads; b < n_tiles; b += kFinalThreads) {
         const float* src = ws.tok + b * kTokSums;
 #pragma unroll
         for (int k = 0; k < kTokSums; ++k) v[4 + k] += src[k];
@@ -345,13 +355,14 @@ __global__ __launch_bounds__(kFinalThreads) void k_ppo_final(meshy_ppo_args a, W
         for (int k = 0; k < kFinalVals; ++k) s_red[wid][k] = v[k];
     }
     __syncthreads();
+    if (threadIdx.x < kFinalVals) {
+        double s = 0.0;
+        for (int w = 0; w < kFinalThreads / kWave; ++w) s += s_red[w][threadIdx.x];
+        s_tot[threadIdx.x] = s;
+    }
+    __syncthreads();
     if (threadIdx.x == 0) {
-        double t[kFinalVals];
-#pragma unroll
-        for (int k = 0; k < kFinalVals; ++k) {
-            t[k] = 0.0;
-            for (int w = 0; w < kFinalThreads / kWave; ++w) t[k] += s_red[w][k];
-        }
+        const double* t = s_tot;
         const double den = a.per_token_loss ? static_cast<double>(max<int64_t>(1, a.n_tokens_global))
                                             : static_cast<double>(max<int64_t>(1, a.n_docs_global));
         const float loss = static_cast<float>(t[0] / den);
