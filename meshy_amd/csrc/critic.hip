@@ -28,6 +28,11 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kAccSums = 5;  // m, r, r^2, d, d^2
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+
+inline bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
+
 template <typename T>
 __device__ __forceinline__ T block_sum_to0(T v, T* scratch) {
     v = wave_sum(v);
@@ -43,35 +48,45 @@ __device__ __forceinline__ T block_sum_to0(T v, T* scratch) {
     return r;
 }
 
+// One workgroup per document.  Its tokens from the first multiple of 8 are
+// read 8 at a time (two 16-byte loads per stream, two groups of 8 per thread
+// in flight); the head before it and the tail after the last whole group of 8
+// one by one.
 __global__ __launch_bounds__(kThreads) void k_seq_mean(const float* __restrict__ x, const float* __restrict__ mask,
-                                                       const int64_t* __restrict__ seg_off,
+                                                       const int64_t* __restrict__ seg_off, bool vec,
                                                        float* __restrict__ out) {
     __shared__ float s_a[kWaves], s_b[kWaves];
     const int64_t d = blockIdx.x;
     const int64_t lo = seg_off[d], hi = seg_off[d + 1];
-    // Four independent accumulator pairs keep four loads of each stream in flight.
-    float sx[4] = {0.f, 0.f, 0.f, 0.f}, sm[4] = {0.f, 0.f, 0.f, 0.f};
-    int64_t i = lo + threadIdx.x;
-    for (; i + 3 * kThreads < hi; i += 4 * kThreads) {
-        float m[4], v[4];
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            m[u] = mask[i + u * kThreads];
-            v[u] = x[i + u * kThreads];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-            sx[u] = fmaf(v[u], m[u], sx[u]);
-            sm[u] += m[u];
-        }
+    const int64_t body0 = vec ? min((lo + 7) / 8 * 8, hi) : hi;
+    const int64_t n8 = (hi - body0) / 8;
+    const int64_t body1 = body0 + 8 * n8;
+    float sx[2] = {0.f, 0.f}, sm[2] = {0.f, 0.f};
+    auto acc8 = [&](int64_t i, int s) {
+        const f32x4 m0 = *reinterpret_cast<const f32x4*>(mask + i);
+        const f32x4 m1 = *reinterpret_cast<const f32x4*>(mask + i + 4);
+        const f32x4 v0 = *reinterpret_cast<const f32x4*>(x + i);
+        const f32x4 v1 = *reinterpret_cast<const f32x4*>(x + i + 4);
+        sx[s] = fmaf(v0.x, m0.x, fmaf(v0.y, m0.y, fmaf(v0.z, m0.z, fmaf(v0.w, m0.w, sx[s]))));
+        sx[s] = fmaf(v1.x, m1.x, fmaf(v1.y, m1.y, fmaf(v1.z, m1.z, fmaf(v1.w, m1.w, sx[s]))));
+        sm[s] += ((m0.x + m0.y) + (m0.z + m0.w)) + ((m1.x + m1.y) + (m1.z + m1.w));
+    };
+    int64_t c = threadIdx.x;
+    for (; c + kThreads < n8; c += 2 * kThreads) {
+        acc8(body0 + 8 * c, 0);
+        acc8(body0 + 8 * (c + kThreads), 1);
     }
-    for (; i < hi; i += kThreads) {
-        const float m = mask[i];
-        sx[0] = fmaf(x[i], m, sx[0]);
-        sm[0] += m;
+    if (c < n8) acc8(body0 + 8 * c, 0);
+    for (int64_t i = lo + threadIdx.x; i < body0; i += kThreads) {
+        sx[1] = fmaf(x[i], mask[i], sx[1]);
+        sm[1] += mask[i];
     }
-    const float tx = block_sum_to0((sx[0] + sx[1]) + (sx[2] + sx[3]), s_a);
-    const float tm = block_sum_to0((sm[0] + sm[1]) + (sm[2] + sm[3]), s_b);
+    for (int64_t i = body1 + threadIdx.x; i < hi; i += kThreads) {
+        sx[1] = fmaf(x[i], mask[i], sx[1]);
+        sm[1] += mask[i];
+    }
+    const float tx = block_sum_to0(sx[0] + sx[1], s_a);
+    const float tm = block_sum_to0(sm[0] + sm[1], s_b);
     if (threadIdx.x == 0) out[d] = tx / fmaxf(tm, 1.f);
 }
 
@@ -100,10 +115,6 @@ __device__ __forceinline__ void acc_elem(const void* values, int values_bf16, co
     acc_one(mask[i], load_value(values, values_bf16, i), returns[i], a);
 }
 
-typedef float f32x4 __attribute__((ext_vector_type(4)));
-typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
-
-inline bool al16(const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; }
 
 // The 8 elements at i, a multiple of 8: with 16-byte aligned bases every load
 // is a 16-byte vector (values: one for bf16, two for fp32).
@@ -293,8 +304,9 @@ extern "C" int meshy_per_sequence_mean(const float* x, const float* mask, const 
     if (n_docs < 0 || n_docs > INT32_MAX) return set_error(MESHY_EINVAL, "%s: bad n_docs", who);
     if (n_docs == 0) return MESHY_OK;
     if (!x || !mask || !seg_offsets || !out) return set_error(MESHY_ENULL, "%s: NULL pointer", who);
+    const bool vec = al16(x) && al16(mask);
     hipLaunchKernelGGL(k_seq_mean, dim3(static_cast<unsigned>(n_docs)), dim3(kThreads), 0, stream, x, mask,
-                       seg_offsets, out);
+                       seg_offsets, vec, out);
     return check_launch(who);
 }
 

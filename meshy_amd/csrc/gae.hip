@@ -534,6 +534,17 @@ namespace meshy {
 namespace {
 
 constexpr int kAttachThreads = 256;
+// Workgroups per sample in k_attach_prep: sample lengths spread over three
+// orders of magnitude, and one workgroup per sample leaves the longest one
+// bound by a single workgroup's share of a CU.
+constexpr int kPrepSplits = 8;
+
+// Token range of split s of a sample [lo, hi): consecutive, each a multiple of 8 long.
+__device__ __forceinline__ void split_range(int64_t lo, int64_t hi, int s, int64_t& a, int64_t& b) {
+    const int64_t per = ((hi - lo + kPrepSplits - 1) / kPrepSplits + 7) / 8 * 8;
+    a = min(lo + per * s, hi);
+    b = min(a + per, hi);
+}
 
 struct AttachWs {
     float* grid_mask;  // [total] (when the caller passes none)
@@ -574,53 +585,138 @@ AttachWs attach_ws_of(void* base, int64_t n, int64_t total) {
 }
 
 // One workgroup per sample: the next-token grid of trainer.py:656-667.
+// The last masked token is found from the sample's end backwards, kLastChunk
+// tokens per step (usually one step: the response ends the sample).  The grid
+// mask (the mask shifted by one), the reward column and the sample ids are then
+// written in wave tiles of 256 tokens; the head and tail one by one.
+constexpr int kLastChunk = 4 * kAttachThreads;
+constexpr int64_t kWaveTile = 4 * kWave;  // tokens per wave step of k_attach_prep
+
 __global__ __launch_bounds__(kAttachThreads) void k_attach_prep(meshy_gae_attach_args g, AttachWs ws,
-                                                                float* grid_mask, float length_const) {
+                                                                float* grid_mask, float length_const, bool vec) {
     __shared__ int64_t s_last[kAttachThreads / kWave];
     const int64_t j = blockIdx.x;
-    const int64_t o = g.offsets[j];
-    const int64_t L = g.offsets[j + 1] - o;
-    const float* m = g.mask_assistant + o;
-    int64_t last = -1;
-    for (int64_t p = threadIdx.x; p < L; p += kAttachThreads)
-        if (m[p] > 0.f) last = max(last, p);
-    last = wave_max(last);
-    if (threadIdx.x % kWave == 0) s_last[threadIdx.x / kWave] = last;
-    __syncthreads();
-    last = s_last[0];
+    const int64_t lo = g.offsets[j];
+    const int64_t hi = g.offsets[j + 1];
+    const float* m = g.mask_assistant;
+    // Every split finds the sample's last masked position (usually one step).
+    int64_t last = -1;  // last masked position, relative to lo
+    for (int64_t end = hi; end > lo; end -= kLastChunk) {
+        int64_t cand = -1;
 #pragma unroll
-    for (int w = 1; w < kAttachThreads / kWave; ++w) last = max(last, s_last[w]);
-    const float r = g.reward[j];
-    for (int64_t p = threadIdx.x; p < L; p += kAttachThreads) {
-        grid_mask[o + p] = (p + 1 < L) ? m[p + 1] : 0.f;
-        ws.rewards[o + p] = (last > 0 && p == last - 1) ? r : 0.f;
-        ws.doc_ids[o + p] = j;
+        for (int k = 0; k < 4; ++k) {
+            const int64_t q = end - 1 - threadIdx.x - static_cast<int64_t>(k) * kAttachThreads;
+            if (q >= lo && m[q] > 0.f) cand = max(cand, q);
+        }
+        cand = wave_max(cand);
+        if (threadIdx.x % kWave == 0) s_last[threadIdx.x / kWave] = cand;
+        __syncthreads();
+        cand = s_last[0];
+#pragma unroll
+        for (int w = 1; w < kAttachThreads / kWave; ++w) cand = max(cand, s_last[w]);
+        __syncthreads();
+        if (cand >= 0) {
+            last = cand - lo;
+            break;
+        }
     }
-    if (threadIdx.x == 0) ws.lengths[j] = length_const;
+    const float r = g.reward[j];
+    const int64_t rpos = (last > 0) ? lo + last - 1 : -1;  // where the reward goes
+    // Token i of the grid: mask[i + 1] inside the sample, 0 at its last token.
+    auto grid_at = [&](int64_t i) { return (i + 1 < hi) ? m[i + 1] : 0.f; };
+    int64_t a, b;  // this split's tokens
+    split_range(lo, hi, static_cast<int>(blockIdx.y), a, b);
+    // Wave tiles of 256 tokens from the first multiple of 4: lane l reads and
+    // writes tokens [base + 4l, base + 4l + 4) with 16-byte accesses that are
+    // contiguous across the wave (whole cache lines per instruction), the
+    // ids as two 1 KB halves of 2 tokens per lane.
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+    const int64_t body0 = vec ? min((a + 3) / 4 * 4, b) : b;
+    const int64_t n_tiles = (b - body0) / kWaveTile;
+    const int64_t body1 = body0 + kWaveTile * n_tiles;
+    for (int64_t tile = wid; tile < n_tiles; tile += kAttachThreads / kWave) {
+        const int64_t base = body0 + kWaveTile * tile;
+        const int64_t i = base + 4 * lane;
+        const f32x4 mk = *reinterpret_cast<const f32x4*>(m + i);
+        const float next_lane = __shfl_down(mk.x, 1, kWave);  // mask[i + 4] for lanes 0..62
+        const float nx = (lane == kWave - 1) ? grid_at(i + 3) : next_lane;
+        *reinterpret_cast<f32x4*>(grid_mask + i) = f32x4{mk.y, mk.z, mk.w, nx};
+        f32x4 rw{0.f, 0.f, 0.f, 0.f};
+        if (rpos >= i && rpos < i + 4) rw[static_cast<int>(rpos - i)] = r;
+        *reinterpret_cast<f32x4*>(ws.rewards + i) = rw;
+        *reinterpret_cast<i64x2*>(ws.doc_ids + base + 2 * lane) = i64x2{j, j};
+        *reinterpret_cast<i64x2*>(ws.doc_ids + base + kWaveTile / 2 + 2 * lane) = i64x2{j, j};
+    }
+    auto one = [&](int64_t i) {
+        grid_mask[i] = grid_at(i);
+        ws.rewards[i] = (i == rpos) ? r : 0.f;
+        ws.doc_ids[i] = j;
+    };
+    for (int64_t i = a + threadIdx.x; i < body0; i += kAttachThreads) one(i);
+    for (int64_t i = body1 + threadIdx.x; i < b; i += kAttachThreads) one(i);
+    if (threadIdx.x == 0 && blockIdx.y == 0) ws.lengths[j] = length_const;
 }
 
-// One workgroup per sample: the four sums behind the critic/* metrics.
-__global__ __launch_bounds__(kAttachThreads) void k_attach_sums(meshy_gae_attach_args g, AttachWs ws,
-                                                                const float* grid_mask) {
-    __shared__ float scratch[kAttachThreads / kWave];
-    const int64_t j = blockIdx.x;
-    const int64_t o = g.offsets[j];
-    const int64_t L = g.offsets[j + 1] - o;
+// One workgroup per sample: the four sums behind the critic/* metrics.  The
+// sample's tokens from the first multiple of 8 are read 8 at a time (16-byte
+// loads, four groups of 8 per thread in flight); the head and tail one by one.
+struct AttachSums {
     float vm = 0.f, am = 0.f, aam = 0.f, mm = 0.f;
-    for (int64_t p = threadIdx.x; p < L; p += kAttachThreads) {
-        const float mk = grid_mask[o + p];
-        const float v = g.values_bf16 ? bf16_to_f32(static_cast<const uint16_t*>(g.values)[o + p])
-                                      : static_cast<const float*>(g.values)[o + p];
-        const float a = g.adv[o + p];
-        vm += v * mk;
-        am += a * mk;
-        aam += fabsf(a) * mk;
+    __device__ void add(float mk, float v, float a) {
+        vm = fmaf(v, mk, vm);
+        am = fmaf(a, mk, am);
+        aam = fmaf(fabsf(a), mk, aam);
         mm += mk;
     }
-    vm = block_sum<kAttachThreads>(vm, scratch);
-    am = block_sum<kAttachThreads>(am, scratch);
-    aam = block_sum<kAttachThreads>(aam, scratch);
-    mm = block_sum<kAttachThreads>(mm, scratch);
+};
+
+__global__ __launch_bounds__(kAttachThreads) void k_attach_sums(meshy_gae_attach_args g, AttachWs ws,
+                                                                const float* grid_mask, bool vec) {
+    __shared__ float scratch[kAttachThreads / kWave];
+    const int64_t j = blockIdx.x;
+    const int64_t lo = g.offsets[j];
+    const int64_t hi = g.offsets[j + 1];
+    const int64_t body0 = vec ? min((lo + 7) / 8 * 8, hi) : hi;
+    const int64_t n8 = (hi - body0) / 8;
+    const int64_t body1 = body0 + 8 * n8;
+    const uint16_t* vb = static_cast<const uint16_t*>(g.values);
+    const float* vf = static_cast<const float*>(g.values);
+    AttachSums s[4];
+    auto acc8 = [&](int64_t i, AttachSums& a) {
+        const f32x4 m0 = *reinterpret_cast<const f32x4*>(grid_mask + i);
+        const f32x4 m1 = *reinterpret_cast<const f32x4*>(grid_mask + i + 4);
+        const f32x4 a0 = *reinterpret_cast<const f32x4*>(g.adv + i);
+        const f32x4 a1 = *reinterpret_cast<const f32x4*>(g.adv + i + 4);
+        f32x4 v0, v1;
+        if (g.values_bf16) {
+            const u32x4 w = *reinterpret_cast<const u32x4*>(vb + i);
+            v0 = f32x4{bf16_lo(w.x), bf16_hi(w.x), bf16_lo(w.y), bf16_hi(w.y)};
+            v1 = f32x4{bf16_lo(w.z), bf16_hi(w.z), bf16_lo(w.w), bf16_hi(w.w)};
+        } else {
+            v0 = *reinterpret_cast<const f32x4*>(vf + i);
+            v1 = *reinterpret_cast<const f32x4*>(vf + i + 4);
+        }
+        a.add(m0.x, v0.x, a0.x); a.add(m0.y, v0.y, a0.y); a.add(m0.z, v0.z, a0.z); a.add(m0.w, v0.w, a0.w);
+        a.add(m1.x, v1.x, a1.x); a.add(m1.y, v1.y, a1.y); a.add(m1.z, v1.z, a1.z); a.add(m1.w, v1.w, a1.w);
+    };
+    auto acc1 = [&](int64_t i) {
+        s[1].add(grid_mask[i], g.values_bf16 ? bf16_to_f32(vb[i]) : vf[i], g.adv[i]);
+    };
+    int64_t c = threadIdx.x;
+    for (; c + 3 * kAttachThreads < n8; c += 4 * kAttachThreads) {
+        acc8(body0 + 8 * c, s[0]);
+        acc8(body0 + 8 * (c + kAttachThreads), s[1]);
+        acc8(body0 + 8 * (c + 2 * kAttachThreads), s[2]);
+        acc8(body0 + 8 * (c + 3 * kAttachThreads), s[3]);
+    }
+    for (; c < n8; c += kAttachThreads) acc8(body0 + 8 * c, s[0]);
+    for (int64_t i = lo + threadIdx.x; i < body0; i += kAttachThreads) acc1(i);
+    for (int64_t i = body1 + threadIdx.x; i < hi; i += kAttachThreads) acc1(i);
+    const float vm = block_sum<kAttachThreads>((s[0].vm + s[1].vm) + (s[2].vm + s[3].vm), scratch);
+    const float am = block_sum<kAttachThreads>((s[0].am + s[1].am) + (s[2].am + s[3].am), scratch);
+    const float aam = block_sum<kAttachThreads>((s[0].aam + s[1].aam) + (s[2].aam + s[3].aam), scratch);
+    const float mm = block_sum<kAttachThreads>((s[0].mm + s[1].mm) + (s[2].mm + s[3].mm), scratch);
     if (threadIdx.x == 0) {
         ws.sums[4 * j + 0] = vm;
         ws.sums[4 * j + 1] = am;
@@ -693,8 +789,10 @@ extern "C" int meshy_gae_attach(const meshy_gae_attach_args* args, hipStream_t s
     // 1 - 1/(1 * L) == lambda.
     const float length_const =
         vapo ? 0.f : static_cast<float>(1.0 / std::max(1e-9, 1.0 - static_cast<double>(g.lambda)));
-    hipLaunchKernelGGL(k_attach_prep, dim3(static_cast<unsigned>(g.n)), dim3(kAttachThreads), 0, stream, g, ws,
-                       grid_mask, length_const);
+    auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+    const bool vec_prep = al16(g.mask_assistant) && al16(grid_mask) && al16(ws.rewards) && al16(ws.doc_ids);
+    hipLaunchKernelGGL(k_attach_prep, dim3(static_cast<unsigned>(g.n), kPrepSplits), dim3(kAttachThreads), 0,
+                       stream, g, ws, grid_mask, length_const, vec_prep);
     int rc = check_launch("meshy_gae_attach(prep)");
     if (rc) return rc;
     meshy_gae_args a{};
@@ -718,8 +816,10 @@ extern "C" int meshy_gae_attach(const meshy_gae_attach_args* args, hipStream_t s
     rc = gae_launch(a, stream);
     if (rc) return rc;
     if (g.metrics) {
+        auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+        const bool vec = al16(grid_mask) && al16(g.adv) && al16(g.values);
         hipLaunchKernelGGL(k_attach_sums, dim3(static_cast<unsigned>(g.n)), dim3(kAttachThreads), 0, stream, g, ws,
-                           grid_mask);
+                           grid_mask, vec);
         if ((rc = check_launch("meshy_gae_attach(sums)"))) return rc;
         hipLaunchKernelGGL(k_attach_final, dim3(1), dim3(1024), 0, stream, g, ws, lam);
         if ((rc = check_launch("meshy_gae_attach(final)"))) return rc;
