@@ -94,14 +94,17 @@ struct TokIn {
     float nw, ol, mk, ro, en, ad;
 };
 
+// kLean: no rollout log-probs, entropy or per-token advantages (the common
+// configuration), so only new, old and mask are read and held.
+template <bool kLean = false>
 __device__ __forceinline__ TokIn load_tok(const meshy_ppo_args& a, int64_t i, bool ok) {
     TokIn x;
     x.nw = ok ? a.new_lp[i] : 0.f;
     x.ol = ok ? a.old_lp[i] : 0.f;
     x.mk = ok ? a.mask[i] : 0.f;
-    x.ro = (ok && a.rollout_lp) ? a.rollout_lp[i] : 0.f;
-    x.en = (ok && a.entropy) ? a.entropy[i] : 0.f;
-    x.ad = (ok && a.adv_per_token) ? a.adv[i] : 0.f;
+    x.ro = (!kLean && ok && a.rollout_lp) ? a.rollout_lp[i] : 0.f;
+    x.en = (!kLean && ok && a.entropy) ? a.entropy[i] : 0.f;
+    x.ad = (!kLean && ok && a.adv_per_token) ? a.adv[i] : 0.f;
     return x;
 }
 
@@ -156,6 +159,10 @@ __device__ __forceinline__ int64_t doc_at(const meshy_ppo_args& a, int64_t i) {
     return min(max(a.doc_ids[i], static_cast<int64_t>(0)), a.n_docs);
 }
 
+// kLean: the configuration without IcePop, rollout log-probs, entropy or
+// per-token advantages, whose per-token registers are then not allocated (so
+// that four workgroups fit per CU).
+template <bool kLean>
 __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Workspace ws) {
     __shared__ float s_red[kWaves][kTokSums + kFastDocs * kSegSums];
     const int64_t b = blockIdx.x;
@@ -166,12 +173,12 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
     // The tile's tokens and its document range, loaded together.
     constexpr int kPer = static_cast<int>(kTile / kThreads);
     TokIn in[kPer];
-    int64_t id[kPer];
+    int id[kPer];  // the tokens' documents (n_docs < 2^31)
 #pragma unroll
     for (int q = 0; q < kPer; ++q) {
         const int64_t i = t0 + q * kThreads + threadIdx.x;
-        in[q] = load_tok(a, i, i < t1);
-        id[q] = i < t1 ? a.doc_ids[i] : 0;
+        in[q] = load_tok<kLean>(a, i, i < t1);
+        id[q] = i < t1 ? static_cast<int>(a.doc_ids[i]) : 0;
     }
     const int64_t d_first = doc_at(a, t0);
     const int64_t nd = max(doc_at(a, t1 - 1), d_first) - d_first + 1;
@@ -188,40 +195,101 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
             A_d[r] = (!a.adv_per_token && real) ? a.adv[d] : 0.f;
             W_d[r] = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
         }
+        // A thread's tokens (i = t0 + q * kThreads + tid) go through the tile's
+        // documents in order, so the document sums accumulate in one run that
+        // is flushed into its slot when the document changes (at most nd - 1
+        // times).  Token sums that equal sums of the slots (mask count, ratio,
+        // and the TIS ratio without IcePop) or that are zero with a feature off
+        // are not accumulated per token.
         float sg[kFastDocs][kSegSums];
 #pragma unroll
         for (int r = 0; r < kFastDocs; ++r)
 #pragma unroll
             for (int k = 0; k < kSegSums; ++k) sg[r][k] = 0.f;
+        float run[kSegSums] = {0.f, 0.f, 0.f, 0.f, 0.f};
+        auto flush = [&](int slot) {
+#pragma unroll
+            for (int r = 0; r < kFastDocs; ++r)
+#pragma unroll
+                for (int k = 0; k < kSegSums; ++k) sg[r][k] += (slot == r) ? run[k] : 0.f;
+#pragma unroll
+            for (int k = 0; k < kSegSums; ++k) run[k] = 0.f;
+        };
+        const bool pos_lm = a.positive_lm_coef != 0.f;
+        const float lo_c = 1.f - a.clip_low, hi_c = 1.f + a.clip_high;
+        int cur = 0;
+        float A = A_d[0], W = W_d[0];
 #pragma unroll
         for (int q = 0; q < kPer; ++q) {
             const int64_t i = t0 + q * kThreads + threadIdx.x;
             if (i >= t1) break;
-            const int64_t rel = id[q] - d_first;
-            const int slot = static_cast<int>(min(max(rel, static_cast<int64_t>(0)), nd - 1));
-            float A = 0.f, W = 0.f;
+            const int slot = min(max(id[q] - static_cast<int>(d_first), 0), static_cast<int>(nd) - 1);
+            if (slot != cur) {
+                flush(cur);
+                cur = slot;
 #pragma unroll
-            for (int r = 0; r < kFastDocs; ++r) {
-                A = (slot == r) ? A_d[r] : A;
-                W = (slot == r) ? W_d[r] : W;
+                for (int r = 0; r < kFastDocs; ++r) {
+                    A = (slot == r) ? A_d[r] : A;
+                    W = (slot == r) ? W_d[r] : W;
+                }
             }
-            if (a.adv_per_token) A = in[q].ad;
-            Contrib c;
-            token_contrib_v(a, in[q], A, W, c);
-#pragma unroll
-            for (int k = 0; k < kTokSums; ++k) acc[k] += c.tok[k];
-#pragma unroll
-            for (int r = 0; r < kFastDocs; ++r)
-#pragma unroll
-                for (int k = 0; k < kSegSums; ++k) sg[r][k] += (slot == r) ? c.seg[k] : 0.f;
+            const TokIn& x = in[q];
+            const float mk = x.mk;
+            const float lr = x.nw - x.ol;
+            const float ratio = expf(lr);
+            const float At = (!kLean && a.adv_per_token) ? x.ad : A;
+            float pg = -t_min(ratio * At, t_clamp(ratio, lo_c, hi_c) * At);
+            bool tm = true;
+            float tis = ratio;
+            if (!kLean && a.use_icepop) {
+                tis = expf(x.ol - x.ro);
+                tm = (tis >= a.tis_min) && (tis <= a.tis_max);
+                pg = (tm ? pg : 0.f) * (tm ? tis : 0.f);
+            } else if (a.use_tis) {
+                tm = (ratio >= a.tis_min) && (ratio <= a.tis_max);
+                pg = tm ? pg : 0.f;
+            }
+            const float rm = ratio * mk;
+            run[0] = fmaf(pg, mk, run[0]);
+            run[1] += mk;
+            run[2] += rm;
+            run[3] = fmaf(ratio, rm, run[3]);
+            if (pos_lm) run[4] = fmaf(-x.nw * W, mk, run[4]);
+            acc[TS_CLIP] += ((ratio < lo_c) || (ratio > hi_c)) ? mk : 0.f * mk;
+            acc[TS_KL] = fmaf(-lr, mk, acc[TS_KL]);
+            acc[TS_LR_ABS] = fmaf(fabsf(lr), mk, acc[TS_LR_ABS]);
+            if (!kLean && a.use_icepop) acc[TS_TIS] = fmaf(tis, mk, acc[TS_TIS]);
+            if (a.use_icepop || a.use_tis) acc[TS_TIS_MASKED] += tm ? 0.f * mk : mk;
+            if (!kLean && a.rollout_lp) {
+                const float diff = x.ro - (a.train_lp_is_old ? x.ol : x.nw);
+                const float lrt = t_clamp(diff, -10.f, 10.f);
+                acc[TS_K3] = fmaf(nan_to_num(expf(lrt) - lrt - 1.f), mk, acc[TS_K3]);
+                acc[TS_LOGDIFF] = fmaf(nan_to_num(fabsf(diff)), mk, acc[TS_LOGDIFF]);
+            }
+            if (!kLean && a.entropy) acc[TS_ENT] = fmaf(x.en, mk, acc[TS_ENT]);
         }
-        // One block reduction of the 10 token sums and the 4 x 5 document sums.
+        flush(cur);
+        // The token sums that are sums of the slots.
 #pragma unroll
-        for (int k = 0; k < kTokSums; ++k) acc[k] = wave_sum(acc[k]);
+        for (int r = 0; r < kFastDocs; ++r) {
+            acc[TS_COUNT] += sg[r][1];
+            acc[TS_RATIO] += sg[r][2];
+        }
+        if (!a.use_icepop) acc[TS_TIS] = acc[TS_RATIO];
+        // One block reduction of the token sums and the nd x 5 document sums
+        // (the sums that are zero with a feature off stay zero).
+        const bool need[kTokSums] = {true, true, true, a.use_icepop || a.use_tis, true, true, true,
+                                     a.rollout_lp != nullptr, a.rollout_lp != nullptr, a.entropy != nullptr};
 #pragma unroll
-        for (int r = 0; r < kFastDocs; ++r)
+        for (int k = 0; k < kTokSums; ++k)
+            if (need[k]) acc[k] = wave_sum(acc[k]);
 #pragma unroll
-            for (int k = 0; k < kSegSums; ++k) sg[r][k] = wave_sum(sg[r][k]);
+        for (int r = 0; r < kFastDocs; ++r) {
+            if (r < nd) {
+#pragma unroll
+                for (int k = 0; k < kSegSums; ++k) sg[r][k] = wave_sum(sg[r][k]);
+            }
+        }
         if (lane == 0) {
 #pragma unroll
             for (int k = 0; k < kTokSums; ++k) s_red[wid][k] = acc[k];
@@ -506,6 +574,7 @@ int validate(const meshy_ppo_args& a, const char* who) {
     if (a.positive_lm_coef != 0.f && !a.positive_lm_weights && a.n_docs > 0)
         return set_error(MESHY_EINVAL, "%s: Positive LM loss requires group weights", who);
     if (a.n_tokens > INT32_MAX) return set_error(MESHY_EINVAL, "%s: too many tokens", who);
+    if (a.n_docs >= INT32_MAX) return set_error(MESHY_EINVAL, "%s: too many documents", who);
     return MESHY_OK;
 }
 
@@ -530,7 +599,11 @@ extern "C" int meshy_ppo_loss_fwd(const meshy_ppo_args* args, float* out, float*
     const Workspace ws = ws_of(a.workspace, a.n_tokens);
     const int64_t nt = n_tiles_of(a.n_tokens);
     if (nt > 0) {
-        hipLaunchKernelGGL(k_ppo_tiles, dim3(static_cast<unsigned>(nt)), dim3(kThreads), 0, stream, a, ws);
+        const bool lean = !a.use_icepop && !a.rollout_lp && !a.entropy && !a.adv_per_token;
+        if (lean)
+            hipLaunchKernelGGL(k_ppo_tiles<true>, dim3(static_cast<unsigned>(nt)), dim3(kThreads), 0, stream, a, ws);
+        else
+            hipLaunchKernelGGL(k_ppo_tiles<false>, dim3(static_cast<unsigned>(nt)), dim3(kThreads), 0, stream, a, ws);
         rc = check_launch("meshy_ppo_loss_fwd(tiles)");
         if (rc) return rc;
     }

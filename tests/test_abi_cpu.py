@@ -97,6 +97,10 @@ def test_struct_entry_points_reject():
     g = _lib.PpoArgs()
     g.n_tokens = -1
     assert lib.meshy_ppo_loss_fwd(ctypes.byref(g), FAKE, None, None) == EINVAL
+    g.n_tokens, g.n_docs = 16, 1 << 31
+    g.new_lp = g.old_lp = g.mask = g.adv = g.seg_offsets = g.doc_ids = FAKE
+    assert lib.meshy_ppo_loss_fwd(ctypes.byref(g), FAKE, None, None) == EINVAL
+    assert b"too many documents" in lib.meshy_last_error()
     e = _lib.GaeArgs()
     e.rewards = e.mask = e.doc_ids = e.values = e.adv = FAKE
     e.rows, e.S, e.n_docs, e.gamma, e.alpha = 1, 100, 1, 1.0, 0.0
