@@ -170,9 +170,10 @@ int meshy_pack_micro_batches(const meshy_pack_args* args, hipStream_t stream);
  * GRPO group-normalised advantages (device).
  * Replaces grpo_advantage (meshy/worker/rollout.py:88-97) for all groups of a
  * batch at once: a size-1 group keeps its reward, otherwise
- * (r - mean) / clamp(unbiased std, min=1e-8).
+ * (r - mean) / clamp(unbiased std, min=1e-8).  Group g is rewards
+ * [group_offsets[g], group_offsets[g+1]), clamped to [0, n_rewards).
  * ---------------------------------------------------------------------- */
-int meshy_grpo_advantage(const float* rewards, const int64_t* group_offsets,
+int meshy_grpo_advantage(const float* rewards, int64_t n_rewards, const int64_t* group_offsets,
                          int64_t n_groups, float* advantages, hipStream_t stream);
 
 /* ------------------------------------------------------------------------

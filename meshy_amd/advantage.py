@@ -26,7 +26,7 @@ def grpo_advantages(rewards: torch.Tensor, group_offsets: torch.Tensor) -> torch
     if n_groups < 0:
         raise ValueError("group_offsets must hold at least one entry")
     adv = torch.empty_like(r)
-    rc = _lib.load().meshy_grpo_advantage(r.data_ptr(), off.data_ptr(), n_groups, adv.data_ptr(),
+    rc = _lib.load().meshy_grpo_advantage(r.data_ptr(), r.numel(), off.data_ptr(), n_groups, adv.data_ptr(),
                                           _lib.stream_of(r.device))
     _lib.check(rc, "meshy_grpo_advantage")
     return adv

@@ -175,12 +175,13 @@ __global__ __launch_bounds__(kFillThreads) void k_pack_fill(meshy_pack_args a) {
     }
 }
 
-__global__ __launch_bounds__(kWave) void k_grpo(const float* __restrict__ rewards,
+// Each group's range is clamped to [0, n_rewards): malformed offsets stay in bounds.
+__global__ __launch_bounds__(kWave) void k_grpo(const float* __restrict__ rewards, int64_t n_rewards,
                                                 const int64_t* __restrict__ group_off,
                                                 float* __restrict__ adv) {
     const int64_t g = blockIdx.x;
-    const int64_t b = group_off[g];
-    const int64_t n = group_off[g + 1] - b;
+    const int64_t b = min(max(group_off[g], static_cast<int64_t>(0)), n_rewards);
+    const int64_t n = min(max(group_off[g + 1], b), n_rewards) - b;
     const int lane = threadIdx.x;
     if (n <= 0) return;
     if (n == 1) {
@@ -256,16 +257,16 @@ extern "C" int meshy_pack_micro_batches(const meshy_pack_args* args, hipStream_t
     return check_launch("meshy_pack_micro_batches(fill)");
 }
 
-extern "C" int meshy_grpo_advantage(const float* rewards, const int64_t* group_offsets, int64_t n_groups,
-                                    float* advantages, hipStream_t stream) {
+extern "C" int meshy_grpo_advantage(const float* rewards, int64_t n_rewards, const int64_t* group_offsets,
+                                    int64_t n_groups, float* advantages, hipStream_t stream) {
     using namespace meshy;
     clear_error();
-    if (n_groups < 0) return set_error(MESHY_EINVAL, "meshy_grpo_advantage: negative group count");
-    if (n_groups == 0) return MESHY_OK;
+    if (n_groups < 0 || n_rewards < 0) return set_error(MESHY_EINVAL, "meshy_grpo_advantage: negative count");
+    if (n_groups == 0 || n_rewards == 0) return MESHY_OK;
     if (!rewards || !group_offsets || !advantages)
         return set_error(MESHY_ENULL, "meshy_grpo_advantage: NULL pointer");
     if (n_groups > INT32_MAX) return set_error(MESHY_EINVAL, "meshy_grpo_advantage: too many groups");
-    hipLaunchKernelGGL(k_grpo, dim3(static_cast<unsigned>(n_groups)), dim3(kWave), 0, stream, rewards,
+    hipLaunchKernelGGL(k_grpo, dim3(static_cast<unsigned>(n_groups)), dim3(kWave), 0, stream, rewards, n_rewards,
                        group_offsets, advantages);
     return check_launch("meshy_grpo_advantage");
 }

@@ -165,8 +165,9 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
     lay = ragged.lay
 
     adv = lay.view(dbuf, "adv_samples")[:ragged.n]
-    rc = _lib.load().meshy_grpo_advantage(lay.view(dbuf, "rewards").data_ptr(), lay.view(dbuf, "group_off").data_ptr(),
-                                          ragged.n_groups, adv.data_ptr(), stream.cuda_stream)
+    rc = _lib.load().meshy_grpo_advantage(lay.view(dbuf, "rewards").data_ptr(), ragged.n,
+                                          lay.view(dbuf, "group_off").data_ptr(), ragged.n_groups, adv.data_ptr(),
+                                          stream.cuda_stream)
     _lib.check(rc, "meshy_grpo_advantage")
 
     plan = tables_to_plan(t) if with_plan_objects else None

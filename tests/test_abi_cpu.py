@@ -60,8 +60,10 @@ def _call(name, *args):
      "lp_offsets"),
     ("meshy_ragged_token_stats", (FAKE, None, FAKE, None, 4, FAKE, FAKE, FAKE, None, FAKE, 8, None), ESPACE,
      "workspace"),
-    ("meshy_grpo_advantage", (FAKE, FAKE, -1, FAKE, None), EINVAL, "negative"),
-    ("meshy_grpo_advantage", (None, FAKE, 3, FAKE, None), ENULL, "NULL"),
+    # rewards, n_rewards, group_offsets, n_groups, adv, stream
+    ("meshy_grpo_advantage", (FAKE, 8, FAKE, -1, FAKE, None), EINVAL, "negative"),
+    ("meshy_grpo_advantage", (FAKE, -8, FAKE, 1, FAKE, None), EINVAL, "negative"),
+    ("meshy_grpo_advantage", (None, 8, FAKE, 3, FAKE, None), ENULL, "NULL"),
     ("meshy_segment_offsets", (FAKE, 10, 0, FAKE, None, None), EINVAL, "bad sizes"),
     ("meshy_stream_read", (FAKE, 4, 17, FAKE, None), EINVAL, "bad shape"),
     ("meshy_stream_read", (FAKE + 4, 4, 32, FAKE, None), EALIGN, "misaligned"),

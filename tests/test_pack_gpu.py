@@ -271,6 +271,18 @@ def test_grpo_special_cases(dev):
     assert adv[5].item() == 0.5         # size-1 group keeps its reward
 
 
+def test_grpo_offsets_clamped_to_the_rewards(dev):
+    """Offsets past the end of the rewards are clamped to them: the groups that
+    fit are normalised as usual and nothing outside the arrays is touched."""
+    from meshy_amd.advantage import grpo_advantages
+
+    rewards = torch.tensor([1.0, 0.0, 1.0, 1.0, 0.0, 0.0], device=dev)
+    off = torch.tensor([0, 3, 9], dtype=torch.int64, device=dev)  # the last group claims 6, holds 3
+    adv = grpo_advantages(rewards, off).cpu()
+    ref = torch.cat([ogrpo.grpo_group(rewards[:3].cpu()), ogrpo.grpo_group(rewards[3:].cpu())])
+    assert torch.allclose(adv, ref, atol=1e-6)
+
+
 def test_grpo_256_samples_matches_oracle(dev):
     from meshy_amd import workloads
     from meshy_amd.advantage import grpo_advantages
