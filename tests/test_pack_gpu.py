@@ -279,7 +279,8 @@ def test_grpo_offsets_clamped_to_the_rewards(dev):
     rewards = torch.tensor([1.0, 0.0, 1.0, 1.0, 0.0, 0.0], device=dev)
     off = torch.tensor([0, 3, 9], dtype=torch.int64, device=dev)  # the last group claims 6, holds 3
     adv = grpo_advantages(rewards, off).cpu()
-    ref = torch.cat([ogrpo.grpo_group(rewards[:3].cpu()), ogrpo.grpo_group(rewards[3:].cpu())])
+    r = rewards.cpu().tolist()
+    ref = torch.tensor(ogrpo.grpo_group(r[:3]) + ogrpo.grpo_group(r[3:]))
     assert torch.allclose(adv, ref, atol=1e-6)
 
 
