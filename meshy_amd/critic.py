@@ -36,6 +36,8 @@ def advantages_to_per_sequence(adv: torch.Tensor, mask: torch.Tensor, doc_ids: t
         return out
     x = adv.reshape(-1).to(torch.float32).contiguous()
     m = mask.reshape(-1).to(torch.float32).contiguous()
+    if m.numel() != x.numel() or doc_ids.numel() != x.numel():
+        raise ValueError(f"adv has {x.numel()} tokens but mask and doc_ids have {m.numel()} and {doc_ids.numel()}")
     off = segment_offsets(doc_ids, n_docs + 1)
     rc = _lib.load().meshy_per_sequence_mean(x.data_ptr(), m.data_ptr(), off.data_ptr(), n_docs, out.data_ptr(),
                                              _lib.stream_of(adv.device))
@@ -160,6 +162,9 @@ def clipped_value_error(values: torch.Tensor, targets: torch.Tensor, old_values:
     o = None
     if clip is not None:
         o = old_values.detach().to(torch.float32).reshape(-1).contiguous()
+    for name, x in (("targets", t), ("old_values", o)):
+        if x is not None and x.numel() != v.numel():
+            raise ValueError(f"values has {v.numel()} elements but {name} has {x.numel()}")
     return _ClippedValueError.apply(v, t, o, clip).reshape(shape)
 
 

@@ -24,6 +24,8 @@ def whiten_flat(adv: torch.Tensor, mask: torch.Tensor, mesh=None, replication: i
         raise ValueError("adv must be a contiguous float32 tensor")
     m = mask.to(torch.float32).contiguous()
     n = adv.numel()
+    if m.numel() != n:
+        raise ValueError(f"adv has {n} elements but mask has {m.numel()}")
     dev = adv.device
     lib = _lib.load()
     stats = torch.empty(3, dtype=torch.float64, device=dev)

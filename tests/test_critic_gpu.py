@@ -124,6 +124,21 @@ def test_clipped_value_error_broadcast_grad_and_tails(dev, clip, reduce, offset)
     assert (vd_base.grad[offset:].cpu() - vr.grad).abs().max().item() <= 1e-6
 
 
+def test_size_mismatches_raise(dev):
+    from meshy_amd import critic, vapo
+
+    v = torch.zeros(10, device=dev)
+    with pytest.raises(ValueError, match="targets"):
+        critic.clipped_value_error(v, torch.zeros(9, device=dev), None, None)
+    with pytest.raises(ValueError, match="old_values"):
+        critic.clipped_value_error(v, v, torch.zeros(11, device=dev), 0.2)
+    with pytest.raises(ValueError, match="mask and doc_ids"):
+        critic.advantages_to_per_sequence(v, torch.ones(9, device=dev), torch.zeros(10, dtype=torch.long,
+                                                                                   device=dev), 1)
+    with pytest.raises(ValueError, match="mask"):
+        vapo.whiten_flat(v, torch.ones(12, device=dev))
+
+
 def _rollout_samples(n, seed, *, stamps=True):
     g = torch.Generator().manual_seed(seed)
     out = []
