@@ -22,12 +22,12 @@ def _logits(rows, T, V, seed, scale=2.0):
     return z, y
 
 
-def _check(z, y, dev, with_entropy=True):
+def _check(z, y, dev, with_entropy=True, ref_dtype=torch.float32):
     from meshy_amd import logprob
 
     lp, ent = logprob.logprobs_and_entropy(z.to(dev), y.to(dev), with_entropy=True)
-    ref_lp = olp.chunk_logprobs(z, y)
-    ref_ent = olp.chunk_entropy(z)
+    ref_lp = olp.chunk_logprobs(z, y, dtype=ref_dtype).float()
+    ref_ent = olp.chunk_entropy(z, dtype=ref_dtype).float()
     assert lp.dtype == torch.float32 and lp.shape == y.shape
     assert (lp.cpu() - ref_lp).abs().max().item() <= TOL
     assert (ent.cpu() - ref_ent).abs().max().item() <= TOL
@@ -92,6 +92,30 @@ def test_large_dynamic_range(dev):
     z, y = _logits(2, 9, 5000, seed=11, scale=40.0)
     z = (z.float() + 500.0).to(torch.bfloat16)
     _check(z, y, dev)
+
+
+@pytest.mark.parametrize("pattern", ["ramp", "late_rise", "late_spikes"])
+def test_running_max_raised_in_later_tiles(dev, pattern):
+    """Rows whose later register tiles exceed what a thread saw first by more
+    than exp2 can hold relative to it (> 88): each such tile is redone with its
+    exact max.  The ramp does it on nearly every tile of every thread."""
+    V = 151936
+    g = torch.Generator().manual_seed(17)
+    z = torch.randn(3, 5, V, generator=g) * 2.0
+    y = torch.randint(0, V, (3, 5), generator=g)
+    if pattern == "ramp":
+        z += torch.linspace(-600.0, 600.0, V)
+        y[:, 0] = V - 1
+    elif pattern == "late_rise":
+        z[..., V // 2:] += 120.0
+    else:
+        z[..., V - 100] = 250.0
+        z[..., V - 7001] = 180.0
+        y[:, 1] = V - 100
+        y[:, 2] = V - 7001
+    # Broad rows at an offset of 120: the fp32 formula is itself ~1.3e-3 off
+    # in entropy there, so the expected values are the formula in fp64.
+    _check(z.to(torch.bfloat16), y, dev, ref_dtype=torch.float64)
 
 
 def test_deterministic(dev):
