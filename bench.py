@@ -781,7 +781,49 @@ def bench_critic(steps, warmup, no_cpu):
     # reads values 2 + returns 4 + mask 4 per grid element
     out["accumulator_update_1024_docs_padded"] = _entry(ms * 1e3, rows * S * 10, cpu_ms, rows=rows, S=S,
                                                       note="wall time including the state's host read")
+    out["whiten_1024_docs"] = bench_whiten(batch, dev, steps, warmup, no_cpu)
     return out
+
+
+def bench_whiten(batch, dev, steps, warmup, no_cpu):
+    """Masked whitening (vapo.py:6-32) of the 6.35 M per-token advantages of the
+    1024 documents, held in one flat device buffer as GAE leaves them."""
+    import torch
+
+    from meshy_amd import _lib, vapo
+
+    T = batch.total
+    g = torch.Generator(device=dev).manual_seed(21)
+    adv = torch.randn(T, generator=g, device=dev) * 3.0 + 1.0
+    mask = torch.from_numpy(batch.mask).to(dev)
+    ms = _gpu_ms(lambda: vapo.whiten_flat(adv, mask), steps, warmup)
+    lib, stream = _lib.load(), _lib.stream_of(dev)
+    stats = torch.empty(3, dtype=torch.float64, device=dev)
+    ws = torch.empty(int(lib.meshy_whiten_workspace_size(T)), dtype=torch.uint8, device=dev)
+
+    def dev_call():
+        lib.meshy_whiten_stats(adv.data_ptr(), mask.data_ptr(), T, 1.0, stats.data_ptr(), ws.data_ptr(), ws.numel(),
+                               stream)
+        lib.meshy_whiten_apply(adv.data_ptr(), mask.data_ptr(), T, stats.data_ptr(), stream)
+
+    _checked(lib.meshy_whiten_stats(adv.data_ptr(), mask.data_ptr(), T, 1.0, stats.data_ptr(), ws.data_ptr(),
+                                    ws.numel(), stream), "meshy_whiten_stats")
+    dev_us = _gpu_ms(dev_call, steps, warmup) * 1e3
+    cpu_ms = None
+    if not no_cpu:
+        from oracle import vapo as ovapo
+
+        a_c, m_c = adv.cpu(), torch.from_numpy(batch.mask)
+        samples = []
+        for i in range(len(batch.lengths)):
+            lo, hi = int(batch.offsets[i]), int(batch.offsets[i + 1])
+            # the sample's loss mask is mask_assistant shifted by one
+            ma = torch.zeros(hi - lo)
+            ma[1:] = m_c[lo:hi - 1]
+            samples.append({ovapo.ADVANTAGE_TOKENS: a_c[lo:hi].clone(), "mask_assistant": ma})
+        cpu_ms = _wall_ms(lambda: ovapo.whiten_advantages(samples, 1 << 20), 3, gpu=False)
+    # stats: adv + mask read (8 B per token); apply: both read, adv written (12 B)
+    return _with_device(_entry(ms * 1e3, T * 20, cpu_ms, tokens=T), dev_us, T * 20)
 
 
 def bench_rollout_metrics(runs, no_cpu):

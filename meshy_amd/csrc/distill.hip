@@ -206,9 +206,19 @@ __global__ __launch_bounds__(kFinalThreads) void k_distill_final(meshy_distill_a
     // The first kFinalThreads tiles' token sums load first: they depend on
     // nothing and arrive while the documents' chain runs.
     float tok0[kTokSums];
+    // Every lane loads (tile 0 when it has none, then discarded): a load under
+    // a per-lane condition compiles to a branch that waits for each load
+    // before the next is issued.
     const bool has_tile = threadIdx.x < nt;
+    const int64_t tb = has_tile ? threadIdx.x : 0;
 #pragma unroll
-    for (int k = 0; k < kTokSums; ++k) tok0[k] = has_tile ? ws.tok[threadIdx.x * kTokSums + k] : 0.f;
+    for (int k = 0; k < kTokSums; ++k) tok0[k] = 0.f;
+    if (nt > 0) {
+#pragma unroll
+        for (int k = 0; k < kTokSums; ++k) tok0[k] = ws.tok[tb * kTokSums + k];
+#pragma unroll
+        for (int k = 0; k < kTokSums; ++k) tok0[k] = has_tile ? tok0[k] : 0.f;
+    }
     for (int64_t d = threadIdx.x; d < n_slots; d += kFinalThreads) {
         const int64_t lo = a.seg_offsets[d];
         const int64_t hi = a.seg_offsets[d + 1];

@@ -337,21 +337,20 @@ __global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Worksp
     const int64_t grp = c / kGroup;
     const int64_t g0 = grp * kGroup;
     const int64_t g1 = min(g0 + kGroup, nc);
-    // Wave 0 loads the maps of the carry-in before the chunk's inputs: the chunks
-    // of this group to the right of c, and the first 64 groups to the right.
-    Pair right = identity_pair();
-    Pair after = identity_pair();
-    if (threadIdx.x < kWave) {
-        const int64_t j = g0 + lane;
-        if (j > c && j < g1) right = ws.chunk[j];
-        const int64_t k = grp + 1 + lane;
-        if (k < ng) after = ws.group[k];
-    }
+    // The maps of the carry-in load before the chunk's inputs: the chunks of this
+    // group to the right of c, and the first 64 groups to the right.  Every
+    // wave loads them (indices clamped into range) and wave 0 alone uses them:
+    // loads under a condition would compile to a branch that waits for them
+    // before the inputs are issued.
+    const int64_t j = g0 + lane;
+    const int64_t k1 = grp + 1 + lane;
+    const Pair rj = ws.chunk[min(j, nc - 1)];
+    const Pair ak = ws.group[min(k1, ng - 1)];
     Pair items[kItems];
     const Pair mine = load_items(g, ws.cnt, t0, n, vec, items);
     if (threadIdx.x < kWave) {
-        right = wave_fold(right);
-        after = wave_fold(after);
+        const Pair right = wave_fold((j > c && j < g1) ? rj : identity_pair());
+        Pair after = wave_fold(k1 < ng ? ak : identity_pair());
         for (int64_t w0 = grp + 1 + kWave; w0 < ng; w0 += kWave) {
             const int64_t k = w0 + lane;
             after = compose(after, wave_fold(k < ng ? ws.group[k] : identity_pair()));
@@ -397,45 +396,96 @@ __global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Worksp
 }
 
 // ---------------------------------------------------------------- whitening
+// Both passes stream adv and mask in groups of 8 elements (two 16-byte loads
+// per array when both are 16-byte aligned), kWhitenGroups groups per thread and
+// kWhitenBlockElems elements per workgroup per step.  Every load of a step is
+// issued before any is used: group indices past the end are clamped to the last
+// group and their elements dropped by a select.  Elements after the last whole
+// group (all of them when unaligned) go one per thread, grid-strided.
 constexpr int kWhitenThreads = 256;
-constexpr int kWhitenBlocks = 1024;
+constexpr int kWhitenGroups = 4;
+constexpr int64_t kWhitenBlockElems = static_cast<int64_t>(kWhitenThreads) * kWhitenGroups * 8;
+constexpr int64_t kWhitenMaxBlocks = 16384;
 
-struct Stats3 {
-    double s, q, c;
-};
+inline int whiten_blocks(int64_t n) {
+    return static_cast<int>(std::min<int64_t>(kWhitenMaxBlocks, std::max<int64_t>(1, ceil_div(n, kWhitenBlockElems))));
+}
 
+__device__ __forceinline__ void whiten_load8(const float* p, int64_t g, float (&v)[8]) {
+    const f32x4 a = *reinterpret_cast<const f32x4*>(p + 8 * g);
+    const f32x4 b = *reinterpret_cast<const f32x4*>(p + 8 * g + 4);
+    v[0] = a.x; v[1] = a.y; v[2] = a.z; v[3] = a.w;
+    v[4] = b.x; v[5] = b.y; v[6] = b.z; v[7] = b.w;
+}
+
+// Per workgroup: the fp64 sum, sum of squares and count over mask != 0
+// (vapo.py:22-24) -> partial[3 * block ...].
 __global__ __launch_bounds__(kWhitenThreads) void k_whiten_partial(const float* __restrict__ adv,
                                                                    const float* __restrict__ mask, int64_t n,
-                                                                   double* __restrict__ partial) {
+                                                                   bool vec, double* __restrict__ partial) {
     __shared__ double scratch[kWhitenThreads / kWave];
-    double s = 0.0, q = 0.0, c = 0.0;
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kWhitenThreads + threadIdx.x; i < n;
-         i += static_cast<int64_t>(gridDim.x) * kWhitenThreads) {
-        if (mask[i] != 0.f) {
-            const double x = adv[i];
-            s += x;
-            q += x * x;
-            c += 1.0;
+    double s = 0.0, q = 0.0;
+    int c = 0;
+    auto add = [&](float x, bool on) {
+        const double xd = on ? static_cast<double>(x) : 0.0;
+        s += xd;
+        q = fma(xd, xd, q);
+        c += on;
+    };
+    const int64_t n8 = vec ? n / 8 : 0;
+    for (int64_t g0 = static_cast<int64_t>(blockIdx.x) * kWhitenThreads * kWhitenGroups; g0 < n8;
+         g0 += static_cast<int64_t>(gridDim.x) * kWhitenThreads * kWhitenGroups) {
+        float x[kWhitenGroups][8], m[kWhitenGroups][8];
+#pragma unroll
+        for (int k = 0; k < kWhitenGroups; ++k) {
+            const int64_t g = min(g0 + k * kWhitenThreads + threadIdx.x, n8 - 1);
+            whiten_load8(adv, g, x[k]);
+            whiten_load8(mask, g, m[k]);
         }
+#pragma unroll
+        for (int k = 0; k < kWhitenGroups; ++k) {
+            const bool ok = g0 + k * kWhitenThreads + threadIdx.x < n8;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) add(x[k][e], ok && m[k][e] != 0.f);
+        }
+    }
+    for (int64_t i = 8 * n8 + static_cast<int64_t>(blockIdx.x) * kWhitenThreads + threadIdx.x; i < n;
+         i += static_cast<int64_t>(gridDim.x) * kWhitenThreads) {
+        const float x = adv[i];
+        const float mk = mask[i];
+        add(x, mk != 0.f);
     }
     s = block_sum<kWhitenThreads>(s, scratch);
     q = block_sum<kWhitenThreads>(q, scratch);
-    c = block_sum<kWhitenThreads>(c, scratch);
+    const double cd = block_sum<kWhitenThreads>(static_cast<double>(c), scratch);
     if (threadIdx.x == 0) {
         partial[3 * blockIdx.x + 0] = s;
         partial[3 * blockIdx.x + 1] = q;
-        partial[3 * blockIdx.x + 2] = c;
+        partial[3 * blockIdx.x + 2] = cd;
     }
 }
 
+// The partials folded in a fixed order (bitwise reproducible), divided by the
+// replication of the data across ranks (vapo.py:27-28).
 __global__ __launch_bounds__(kWhitenThreads) void k_whiten_final(const double* __restrict__ partial, int nb,
                                                                  double replication, double* __restrict__ stats) {
     __shared__ double scratch[kWhitenThreads / kWave];
+    constexpr int kIn = 4;  // partials per thread per step, loaded together
     double v[3] = {0.0, 0.0, 0.0};
-    for (int b = threadIdx.x; b < nb; b += kWhitenThreads) {
-        v[0] += partial[3 * b + 0];
-        v[1] += partial[3 * b + 1];
-        v[2] += partial[3 * b + 2];
+    for (int b0 = 0; b0 < nb; b0 += kIn * kWhitenThreads) {
+        double r[kIn][3];
+#pragma unroll
+        for (int u = 0; u < kIn; ++u) {
+            const int b = min(b0 + u * kWhitenThreads + static_cast<int>(threadIdx.x), nb - 1);
+#pragma unroll
+            for (int k = 0; k < 3; ++k) r[u][k] = partial[3 * b + k];
+        }
+#pragma unroll
+        for (int u = 0; u < kIn; ++u) {
+            const bool ok = b0 + u * kWhitenThreads + static_cast<int>(threadIdx.x) < nb;
+#pragma unroll
+            for (int k = 0; k < 3; ++k) v[k] += ok ? r[u][k] : 0.0;
+        }
     }
 #pragma unroll
     for (int k = 0; k < 3; ++k) v[k] = block_sum<kWhitenThreads>(v[k], scratch);
@@ -446,10 +496,11 @@ __global__ __launch_bounds__(kWhitenThreads) void k_whiten_final(const double* _
     }
 }
 
+// adv <- (adv - mean) * rsqrt(var + 1e-8) where mask != 0, else 0 (vapo.py:25-32):
+// the mean, the clamped variance and the Bessel factor when count >= 2.
 __global__ __launch_bounds__(kWhitenThreads) void k_whiten_apply(float* __restrict__ adv,
-                                                                 const float* __restrict__ mask, int64_t n,
+                                                                 const float* __restrict__ mask, int64_t n, bool vec,
                                                                  const double* __restrict__ stats) {
-    // vapo.py:25-32: mean, clamped variance, Bessel factor when count >= 2.
     const double total = stats[0], squares = stats[1], count = stats[2];
     const double cnt = fmax(count, 1.0);
     const double mean = total / cnt;
@@ -457,9 +508,33 @@ __global__ __launch_bounds__(kWhitenThreads) void k_whiten_apply(float* __restri
     if (count >= 2.0) var *= count / (count - 1.0);
     const float mean_f = static_cast<float>(mean);
     const float scale = rsqrtf(static_cast<float>(var) + 1e-8f);
-    for (int64_t i = static_cast<int64_t>(blockIdx.x) * kWhitenThreads + threadIdx.x; i < n;
+    auto w = [&](float x, float mk) { return (mk != 0.f) ? (x - mean_f) * scale : 0.f; };
+    const int64_t n8 = vec ? n / 8 : 0;
+    for (int64_t g0 = static_cast<int64_t>(blockIdx.x) * kWhitenThreads * kWhitenGroups; g0 < n8;
+         g0 += static_cast<int64_t>(gridDim.x) * kWhitenThreads * kWhitenGroups) {
+        float x[kWhitenGroups][8], m[kWhitenGroups][8];
+#pragma unroll
+        for (int k = 0; k < kWhitenGroups; ++k) {
+            const int64_t g = min(g0 + k * kWhitenThreads + threadIdx.x, n8 - 1);
+            whiten_load8(adv, g, x[k]);
+            whiten_load8(mask, g, m[k]);
+        }
+#pragma unroll
+        for (int k = 0; k < kWhitenGroups; ++k) {
+            const int64_t g = g0 + k * kWhitenThreads + threadIdx.x;
+            if (g < n8) {
+                *reinterpret_cast<f32x4*>(adv + 8 * g) =
+                    f32x4{w(x[k][0], m[k][0]), w(x[k][1], m[k][1]), w(x[k][2], m[k][2]), w(x[k][3], m[k][3])};
+                *reinterpret_cast<f32x4*>(adv + 8 * g + 4) =
+                    f32x4{w(x[k][4], m[k][4]), w(x[k][5], m[k][5]), w(x[k][6], m[k][6]), w(x[k][7], m[k][7])};
+            }
+        }
+    }
+    for (int64_t i = 8 * n8 + static_cast<int64_t>(blockIdx.x) * kWhitenThreads + threadIdx.x; i < n;
          i += static_cast<int64_t>(gridDim.x) * kWhitenThreads) {
-        adv[i] = (mask[i] != 0.f) ? (adv[i] - mean_f) * scale : 0.f;
+        const float x = adv[i];
+        const float mk = mask[i];
+        adv[i] = w(x, mk);
     }
 }
 
@@ -602,11 +677,17 @@ __global__ __launch_bounds__(kAttachThreads) void k_attach_prep(meshy_gae_attach
     // Every split finds the sample's last masked position (usually one step).
     int64_t last = -1;  // last masked position, relative to lo
     for (int64_t end = hi; end > lo; end -= kLastChunk) {
+        // The four loads take indices clamped into the sample (lo < end) and
+        // are all issued before the compares: a load under a per-lane
+        // condition compiles to a branch that waits for it.
+        float mv[4];
+#pragma unroll
+        for (int k = 0; k < 4; ++k) mv[k] = m[max(end - 1 - threadIdx.x - static_cast<int64_t>(k) * kAttachThreads, lo)];
         int64_t cand = -1;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
             const int64_t q = end - 1 - threadIdx.x - static_cast<int64_t>(k) * kAttachThreads;
-            if (q >= lo && m[q] > 0.f) cand = max(cand, q);
+            cand = (q >= lo && mv[k] > 0.f) ? max(cand, q) : cand;
         }
         cand = wave_max(cand);
         if (threadIdx.x % kWave == 0) s_last[threadIdx.x / kWave] = cand;
@@ -639,8 +720,11 @@ __global__ __launch_bounds__(kAttachThreads) void k_attach_prep(meshy_gae_attach
         const int64_t base = body0 + kWaveTile * tile;
         const int64_t i = base + 4 * lane;
         const f32x4 mk = *reinterpret_cast<const f32x4*>(m + i);
+        // mask[i + 4], which lane 63 needs, loaded by every lane with the tile
+        // (the other lanes' addresses fall in lines the tile reads anyway).
+        const float after = m[min(i + 4, hi - 1)];
         const float next_lane = __shfl_down(mk.x, 1, kWave);  // mask[i + 4] for lanes 0..62
-        const float nx = (lane == kWave - 1) ? grid_at(i + 3) : next_lane;
+        const float nx = (lane == kWave - 1) ? (i + 4 < hi ? after : 0.f) : next_lane;
         *reinterpret_cast<f32x4*>(grid_mask + i) = f32x4{mk.y, mk.z, mk.w, nx};
         f32x4 rw{0.f, 0.f, 0.f, 0.f};
         if (rpos >= i && rpos < i + 4) rw[static_cast<int>(rpos - i)] = r;
@@ -828,8 +912,8 @@ extern "C" int meshy_gae_attach(const meshy_gae_attach_args* args, hipStream_t s
 }
 
 extern "C" size_t meshy_whiten_workspace_size(int64_t n) {
-    (void)n;
-    return sizeof(double) * 3 * meshy::kWhitenBlocks;
+    if (n < 0) return 0;
+    return sizeof(double) * 3 * static_cast<size_t>(meshy::whiten_blocks(n));
 }
 
 extern "C" int meshy_whiten_stats(const float* adv, const float* mask, int64_t n, double replication, double* stats,
@@ -842,9 +926,11 @@ extern "C" int meshy_whiten_stats(const float* adv, const float* mask, int64_t n
     if (workspace_bytes < meshy_whiten_workspace_size(n))
         return set_error(MESHY_ESPACE, "meshy_whiten_stats: workspace needs %zu bytes", meshy_whiten_workspace_size(n));
     if (!(replication > 0.0)) return set_error(MESHY_EINVAL, "meshy_whiten_stats: replication must be positive");
-    const int nb = static_cast<int>(std::min<int64_t>(kWhitenBlocks, std::max<int64_t>(1, ceil_div(n, kWhitenThreads))));
+    const int nb = whiten_blocks(n);
+    auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+    const bool vec = al16(adv) && al16(mask);
     double* partial = static_cast<double*>(workspace);
-    hipLaunchKernelGGL(k_whiten_partial, dim3(nb), dim3(kWhitenThreads), 0, stream, adv, mask, n, partial);
+    hipLaunchKernelGGL(k_whiten_partial, dim3(nb), dim3(kWhitenThreads), 0, stream, adv, mask, n, vec, partial);
     int rc = check_launch("meshy_whiten_stats(partial)");
     if (rc) return rc;
     hipLaunchKernelGGL(k_whiten_final, dim3(1), dim3(kWhitenThreads), 0, stream, partial, nb, replication, stats);
@@ -857,7 +943,9 @@ extern "C" int meshy_whiten_apply(float* adv, const float* mask, int64_t n, cons
     if (n < 0) return set_error(MESHY_EINVAL, "meshy_whiten_apply: negative size");
     if (n == 0) return MESHY_OK;
     if (!adv || !mask || !stats) return set_error(MESHY_ENULL, "meshy_whiten_apply: NULL pointer");
-    const int nb = static_cast<int>(std::min<int64_t>(kWhitenBlocks, ceil_div(n, kWhitenThreads)));
-    hipLaunchKernelGGL(k_whiten_apply, dim3(nb), dim3(kWhitenThreads), 0, stream, adv, mask, n, stats);
+    auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
+    const bool vec = al16(adv) && al16(mask);
+    hipLaunchKernelGGL(k_whiten_apply, dim3(whiten_blocks(n)), dim3(kWhitenThreads), 0, stream, adv, mask, n, vec,
+                       stats);
     return check_launch("meshy_whiten_apply");
 }

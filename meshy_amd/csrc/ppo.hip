@@ -96,15 +96,20 @@ struct TokIn {
 
 // kLean: no rollout log-probs, entropy or per-token advantages (the common
 // configuration), so only new, old and mask are read and held.
+// A lane past the end (!ok) reads token 0 and zeroes the values: loads under a
+// per-lane condition compile to branches, and arithmetic on a loaded value
+// inside such a branch to a wait per load.  Callers run with n_tokens >= 1.
 template <bool kLean = false>
 __device__ __forceinline__ TokIn load_tok(const meshy_ppo_args& a, int64_t i, bool ok) {
+    const int64_t j = ok ? i : 0;
     TokIn x;
-    x.nw = ok ? a.new_lp[i] : 0.f;
-    x.ol = ok ? a.old_lp[i] : 0.f;
-    x.mk = ok ? a.mask[i] : 0.f;
-    x.ro = (!kLean && ok && a.rollout_lp) ? a.rollout_lp[i] : 0.f;
-    x.en = (!kLean && ok && a.entropy) ? a.entropy[i] : 0.f;
-    x.ad = (!kLean && ok && a.adv_per_token) ? a.adv[i] : 0.f;
+    x.nw = a.new_lp[j];
+    x.ol = a.old_lp[j];
+    x.mk = a.mask[j];
+    x.ro = (!kLean && a.rollout_lp) ? a.rollout_lp[j] : 0.f;
+    x.en = (!kLean && a.entropy) ? a.entropy[j] : 0.f;
+    x.ad = (!kLean && a.adv_per_token) ? a.adv[j] : 0.f;
+    if (!ok) x = TokIn{0.f, 0.f, 0.f, 0.f, 0.f, 0.f};
     return x;
 }
 
@@ -178,7 +183,7 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
     for (int q = 0; q < kPer; ++q) {
         const int64_t i = t0 + q * kThreads + threadIdx.x;
         in[q] = load_tok<kLean>(a, i, i < t1);
-        id[q] = i < t1 ? static_cast<int>(a.doc_ids[i]) : 0;
+        id[q] = static_cast<int>(a.doc_ids[i < t1 ? i : t0]);
     }
     const int64_t d_first = doc_at(a, t0);
     const int64_t nd = max(doc_at(a, t1 - 1), d_first) - d_first + 1;
@@ -372,9 +377,19 @@ __global__ __launch_bounds__(kFinalThreads) void k_ppo_final(meshy_ppo_args a, W
     // they depend on nothing, so they arrive while the documents' chain
     // (offsets, then their tiles' partials) runs.
     float tok0[kTokSums];
+    // Every lane loads (tile 0 when it has none, then discarded): a load under
+    // a per-lane condition compiles to a branch that waits for each load
+    // before the next is issued.
     const bool has_tile = threadIdx.x < n_tiles;
+    const int64_t tb = has_tile ? threadIdx.x : 0;
 #pragma unroll
-    for (int k = 0; k < kTokSums; ++k) tok0[k] = has_tile ? ws.tok[threadIdx.x * kTokSums + k] : 0.f;
+    for (int k = 0; k < kTokSums; ++k) tok0[k] = 0.f;
+    if (n_tiles > 0) {
+#pragma unroll
+        for (int k = 0; k < kTokSums; ++k) tok0[k] = ws.tok[tb * kTokSums + k];
+#pragma unroll
+        for (int k = 0; k < kTokSums; ++k) tok0[k] = has_tile ? tok0[k] : 0.f;
+    }
     // Per-document totals (tile order) and their contributions: v[0..3] =
     // loss terms, positive-LM terms, ESS terms, documents with tokens.
     for (int64_t d = threadIdx.x; d < n_slots; d += kFinalThreads) {
@@ -512,7 +527,7 @@ __global__ __launch_bounds__(kThreads) void k_ppo_bwd(meshy_ppo_args a, const fl
         const int64_t i = t0 + q * kThreads;
         const bool ok = i < a.n_tokens;
         in[q] = load_tok(a, i, ok);
-        d[q] = ok ? doc_at(a, i) : 0;
+        d[q] = doc_at(a, ok ? i : 0);
     }
 #pragma unroll
     for (int q = 0; q < kBwdItems; ++q) {

@@ -13,7 +13,7 @@
 //   k_rs_count    one workgroup per sample: counts and the fp64 log-prob sum;
 //   k_rs_scan     one workgroup: exclusive scan of the kept counts;
 //   k_rs_compact  one workgroup per sample: an ordered stream compaction
-//                 (block prefix scan of the keep flags, 256 tokens per step).
+//                 (block prefix scan of the keep flags, 1024 tokens per step).
 #include "common.h"
 
 namespace meshy {
@@ -23,9 +23,11 @@ constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int kScanThreads = 1024;
 
-__device__ __forceinline__ bool keep_lp(const float* mask, int64_t m0, int64_t j, bool masked) {
-    return !masked || mask[m0 + j] > 0.f;
-}
+// Each thread takes kUnroll tokens of a step of kStep (token base + u * kThreads
+// + tid): their loads are issued together, so a sample of up to kStep tokens
+// costs one memory round trip instead of one per strided iteration.
+constexpr int kUnroll = 4;
+constexpr int64_t kStep = static_cast<int64_t>(kThreads) * kUnroll;
 
 __global__ __launch_bounds__(kThreads) void k_rs_count(const float* __restrict__ mask,
                                                        const float* __restrict__ lp,
@@ -38,27 +40,57 @@ __global__ __launch_bounds__(kThreads) void k_rs_count(const float* __restrict__
     __shared__ double s_s[kWaves];
     const int64_t s = blockIdx.x;
     const int64_t m0 = off[s], mn = off[s + 1] - m0;
-    int64_t c = 0, k = 0;
+    const int64_t l0 = lp ? lp_off[s] : 0, ln = lp ? lp_off[s + 1] - l0 : 0;
+    // Log-probs are kept where the mask is on when both columns are equally
+    // long, else all of them.
+    const bool masked = lp && ln == mn;
+    int c = 0, k = 0;
     double sum = 0.0;
-    for (int64_t j = threadIdx.x; j < mn; j += kThreads) c += mask[m0 + j] > 0.f ? 1 : 0;
-    if (lp) {
-        const int64_t l0 = lp_off[s], ln = lp_off[s + 1] - l0;
-        const bool masked = ln == mn;
-        for (int64_t j = threadIdx.x; j < ln; j += kThreads) {
-            if (keep_lp(mask, m0, j, masked)) {
-                ++k;
-                sum += lp[l0 + j];
+    // Loads take a clamped index and every one is issued; the out-of-range
+    // ones are discarded by a select.  (A load under `j < mn ? ... : 0` becomes
+    // a branch that waits for each load before the next.)
+    if (masked) {
+        for (int64_t base = 0; base < mn; base += kStep) {
+            float mv[kUnroll], lv[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const int64_t j = min(base + u * kThreads + threadIdx.x, mn - 1);
+                mv[u] = mask[m0 + j];
+                lv[u] = lp[l0 + j];
+            }
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) {
+                const bool on = base + u * kThreads + threadIdx.x < mn && mv[u] > 0.f;
+                c += on;
+                k += on;
+                sum += on ? static_cast<double>(lv[u]) : 0.0;
             }
         }
+    } else {
+        for (int64_t base = 0; base < mn; base += kStep) {
+            float mv[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) mv[u] = mask[m0 + min(base + u * kThreads + threadIdx.x, mn - 1)];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) c += base + u * kThreads + threadIdx.x < mn && mv[u] > 0.f;
+        }
+        for (int64_t base = 0; base < ln; base += kStep) {
+            float lv[kUnroll];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u) lv[u] = lp[l0 + min(base + u * kThreads + threadIdx.x, ln - 1)];
+#pragma unroll
+            for (int u = 0; u < kUnroll; ++u)
+                sum += base + u * kThreads + threadIdx.x < ln ? static_cast<double>(lv[u]) : 0.0;
+        }
     }
-    c = wave_sum(c);
-    k = wave_sum(k);
+    const int64_t cw = wave_sum(static_cast<int64_t>(c));
+    const int64_t kw = wave_sum(static_cast<int64_t>(k));
     sum = wave_sum(sum);
     const int lane = threadIdx.x % kWave;
     const int wid = threadIdx.x / kWave;
     if (lane == 0) {
-        s_c[wid] = c;
-        s_k[wid] = k;
+        s_c[wid] = cw;
+        s_k[wid] = kw;
         s_s[wid] = sum;
     }
     __syncthreads();
@@ -71,7 +103,7 @@ __global__ __launch_bounds__(kThreads) void k_rs_count(const float* __restrict__
             ts += s_s[w];
         }
         resp_len[s] = tc;
-        kept[s] = tk;
+        kept[s] = masked ? tk : ln;  // ln is 0 without log-probs
         lp_sum[s] = ts;
     }
 }
@@ -105,35 +137,65 @@ __global__ __launch_bounds__(kScanThreads) void k_rs_scan(const int64_t* __restr
     if (threadIdx.x == 0) out_off[0] = 0;
 }
 
+// Ordered compaction of one sample's kept log-probs, kStep tokens per step:
+// the kUnroll sub-steps' keep flags are balloted per wave, their popcounts
+// exchanged through LDS with one barrier, and each kept value written at
+// (tokens kept before its sub-step) + (waves before it) + (lanes before it).
 __global__ __launch_bounds__(kThreads) void k_rs_compact(const float* __restrict__ mask,
                                                          const float* __restrict__ lp,
                                                          const int64_t* __restrict__ off,
                                                          const int64_t* __restrict__ lp_off,
                                                          const int64_t* __restrict__ out_off,
                                                          float* __restrict__ out) {
-    __shared__ int s_w[kWaves];
+    __shared__ int s_w[2][kUnroll][kWaves];
     const int64_t s = blockIdx.x;
     const int64_t m0 = off[s], mn = off[s + 1] - m0;
     const int64_t l0 = lp_off[s], ln = lp_off[s + 1] - l0;
     const bool masked = ln == mn;
+    // The keep flags' source: the mask, or (all kept) the log-probs themselves
+    // as a stand-in that is always in range, so the loop has no branch.
+    const float* keep_src = masked ? mask + m0 : lp + l0;
     const int lane = threadIdx.x % kWave;
     const int wid = threadIdx.x / kWave;
+    const uint64_t below = (uint64_t{1} << lane) - 1;
     int64_t dst = out_off[s];
-    for (int64_t base = 0; base < ln; base += kThreads) {
-        const int64_t j = base + threadIdx.x;
-        const bool f = j < ln && keep_lp(mask, m0, j, masked);
-        const uint64_t b = __ballot(f);
-        const int before_lane = __popcll(b & ((uint64_t{1} << lane) - 1));
-        if (lane == 0) s_w[wid] = __popcll(b);
-        __syncthreads();
-        int before_wave = 0, total = 0;
-        for (int w = 0; w < kWaves; ++w) {
-            if (w < wid) before_wave += s_w[w];
-            total += s_w[w];
+    int buf = 0;
+    for (int64_t base = 0; base < ln; base += kStep, buf ^= 1) {
+        bool f[kUnroll];
+        float lv[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            // Clamped indices: every load is issued before any is used.
+            const int64_t j = base + u * kThreads + threadIdx.x;
+            const int64_t jc = min(j, ln - 1);
+            lv[u] = lp[l0 + jc];
+            const float mk = keep_src[jc];
+            f[u] = (j < ln) & (!masked | (mk > 0.f));  // no short circuit: no branch
         }
-        if (f) out[dst + before_wave + before_lane] = lp[l0 + j];
-        dst += total;
+        int before_lane[kUnroll];
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            const uint64_t b = __ballot(f[u]);
+            before_lane[u] = __popcll(b & below);
+            if (lane == 0) s_w[buf][u][wid] = __popcll(b);
+        }
+        // Two LDS buffers alternate between steps, so one barrier per step
+        // keeps a fast wave from overwriting counts another still reads.
         __syncthreads();
+        int64_t at = dst;
+#pragma unroll
+        for (int u = 0; u < kUnroll; ++u) {
+            int before_wave = 0, total = 0;
+#pragma unroll
+            for (int w = 0; w < kWaves; ++w) {
+                const int cw = s_w[buf][u][w];
+                before_wave += w < wid ? cw : 0;
+                total += cw;
+            }
+            if (f[u]) out[at + before_wave + before_lane[u]] = lv[u];
+            at += total;
+        }
+        dst = at;
     }
 }
 

@@ -184,6 +184,23 @@ def test_rollout_metrics_match_oracle(dev, stamps):
     _compare(m, hist, rm, rh)
 
 
+def test_rollout_metrics_step_boundaries(dev):
+    """Samples around the token-stats kernels' 1024-token steps, several steps
+    long, empty, and with log-prob columns longer or shorter than the mask."""
+    from meshy_amd.rollout_metrics import rollout_metrics
+
+    g = torch.Generator().manual_seed(5)
+    samples = []
+    for i, L in enumerate([1, 1023, 1024, 1025, 2048, 4097, 9001, 0, 3000]):
+        mask = (torch.rand(L, generator=g) > 0.3).float()
+        lp = -torch.rand(L + (7 if i == 5 else 0) - (3 if i == 6 and L else 0), generator=g) * 2
+        samples.append({"tokens": torch.randint(0, 1000, (L,), generator=g), "logprobs": lp,
+                        "mask_assistant": mask, "reward": torch.tensor(float(i % 2))})
+    m, hist = rollout_metrics(samples, seq_len=4096)
+    rm, rh = orm.rollout_metrics(samples, seq_len=4096)
+    _compare(m, hist, rm, rh)
+
+
 def test_rollout_metrics_from_wire_columns(dev):
     from meshy_amd import wire
     from meshy_amd.rollout_metrics import rollout_metrics

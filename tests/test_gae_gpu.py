@@ -309,3 +309,44 @@ def test_whitening_matches_oracle(dev):
     ovapo.whiten_advantages(ref, 300)
     for a, b in zip(mk, ref):
         assert (a[ADVANTAGE_TOKENS] - b[ADVANTAGE_TOKENS]).abs().max().item() <= 1e-4
+
+
+@pytest.mark.parametrize("offset", [0, 1])
+@pytest.mark.parametrize("n", [1, 7, 8, 9, 8191, 8192, 8193, 300_001])
+def test_whiten_flat_sizes_and_alignment(dev, n, offset):
+    """Flat buffers around the kernels' 8-element groups and 8192-element
+    workgroup steps; offset 1 makes both pointers unaligned (the one-element path)."""
+    from meshy_amd.batch import ADVANTAGE_TOKENS
+    from meshy_amd.vapo import whiten_flat
+
+    g = torch.Generator().manual_seed(n + offset)
+    a = torch.randn(n + offset, generator=g) * 2 + 0.5
+    m = (torch.rand(n + offset, generator=g) > 0.25).float()
+    ad, md = a.to(dev), m.to(dev)
+    whiten_flat(ad[offset:], md[offset:])
+    # The oracle's sample form: its loss mask is mask_assistant shifted by one,
+    # and the appended last token is outside it.
+    s = {ADVANTAGE_TOKENS: torch.cat([a[offset:], torch.zeros(1)]),
+         "mask_assistant": torch.cat([torch.zeros(1), m[offset:]])}
+    ovapo.whiten_advantages([s], n + 1)
+    assert (ad[offset:].cpu() - s[ADVANTAGE_TOKENS][:n]).abs().max().item() <= 1e-4
+    assert torch.equal(ad[:offset].cpu(), a[:offset])
+
+
+def test_whiten_flat_more_elements_than_one_grid_pass(dev):
+    """134 M elements: more than the largest grid covers in one step.  Checked by
+    what whitening fixes: the masked values' mean is 0 and their unbiased
+    variance var / (var + 1e-8); the rest are 0."""
+    from meshy_amd.vapo import whiten_flat
+
+    n = 16384 * 8192 + 13
+    g = torch.Generator(device=dev).manual_seed(3)
+    a = torch.randn(n, generator=g, device=dev) * 2 + 0.5
+    m = (torch.rand(n, generator=g, device=dev) > 0.25).float()
+    sel = a[m != 0].double()
+    var = sel.var().item()
+    whiten_flat(a, m)
+    w = a[m != 0].double()
+    assert abs(w.mean().item()) <= 1e-5
+    assert abs(w.var().item() - var / (var + 1e-8)) <= 1e-4
+    assert a[m == 0].abs().max().item() == 0.0
