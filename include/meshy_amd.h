@@ -94,6 +94,17 @@ typedef struct meshy_plan_out {
 int meshy_plan_build(const int64_t* lengths, const int64_t* loss_tokens, int64_t n,
                      int64_t dp_size, const meshy_planner_cfg* cfg, meshy_plan_out* out);
 
+/* Concatenation of host byte ranges (host).
+ * Replaces the per-sample torch.cat that stages jagged sample columns before
+ * their host-to-device copy: the critic path's concatenation of masks and
+ * values (meshy/backend/titan/trainer.py:644-667) and the per-sample slicing of
+ * build_micro_batch (meshy/backend/titan/batch.py:126-178).  Piece i
+ * (nbytes[i] bytes at srcs[i]) lands right after piece i - 1 in dst.  Runs on
+ * up to max_threads threads of a persistent pool (<= 0: the pool's size, at
+ * most 16), split by bytes; small gathers run on the calling thread. */
+int meshy_host_gather(const void* const* srcs, const int64_t* nbytes, int64_t n, void* dst,
+                      int max_threads);
+
 /* Per-sample planner inputs from a flat host mask (host).
  * Replaces TitanTrainer._sample_lengths (meshy/backend/titan/trainer.py:577-588):
  * sample i covers mask[offsets[i] .. offsets[i+1]); lengths[i] is its token

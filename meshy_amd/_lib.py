@@ -225,6 +225,7 @@ SIGNATURES = {
         [c_void_p, c_void_p, c_int64, c_int64, POINTER(PlannerCfg), POINTER(PlanOut)],
     ),
     "meshy_sample_loss_tokens": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "meshy_host_gather": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int]),
     "meshy_pack_micro_batches": (c_int, [POINTER(PackArgs), c_void_p]),
     "meshy_grpo_advantage": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
     "meshy_logprob_entropy_fwd": (

@@ -19,6 +19,7 @@ import numpy as np
 import torch
 
 from . import _lib
+from .hostio import gather_into
 from .plan import Layout, MicroPlan
 
 #: Per-token advantage column (batch.py:81): already on the next-token grid,
@@ -255,18 +256,13 @@ def stage_micro_batches(
     host = stage.get(lay.size)
     if n_s:
         srcs = [samples[i] for i in used]
-        torch.cat([s["tokens"][:L].to(tok_dtype) for s, L in zip(srcs, need_len)],
-                  out=lay.view(host, "tokens"))
-        torch.cat([s["mask_assistant"][:L].to(torch.float32) for s, L in zip(srcs, need_len)],
-                  out=lay.view(host, "mask"))
+        gather_into([s["tokens"][:L] for s, L in zip(srcs, need_len)], lay.view(host, "tokens"))
+        gather_into([s["mask_assistant"][:L] for s, L in zip(srcs, need_len)], lay.view(host, "mask"))
         if need_rollout_lp:
-            torch.cat([s["logprobs"][:L].to(torch.float32) for s, L in zip(srcs, need_len)],
-                      out=lay.view(host, "logprobs"))
+            gather_into([s["logprobs"][:L] for s, L in zip(srcs, need_len)], lay.view(host, "logprobs"))
         if teacher_k:
-            torch.cat([s[TEACHER_FIELDS[0]][:L].to(torch.int32).reshape(-1) for s, L in zip(srcs, need_len)],
-                      out=lay.view(host, "teacher_ids"))
-            torch.cat([s[TEACHER_FIELDS[1]][:L].to(torch.float32).reshape(-1) for s, L in zip(srcs, need_len)],
-                      out=lay.view(host, "teacher_lps"))
+            gather_into([s[TEACHER_FIELDS[0]][:L] for s, L in zip(srcs, need_len)], lay.view(host, "teacher_ids"))
+            gather_into([s[TEACHER_FIELDS[1]][:L] for s, L in zip(srcs, need_len)], lay.view(host, "teacher_lps"))
         if per_token_adv and adv_dev is None:
             parts = []
             for s, L in zip(srcs, need_len):
@@ -274,7 +270,7 @@ def stage_micro_batches(
                 if a.numel() < L:
                     a = torch.cat([a, a.new_zeros(L - a.numel())])
                 parts.append(a)
-            torch.cat(parts, out=lay.view(host, "adv_tokens"))
+            gather_into(parts, lay.view(host, "adv_tokens"))
     lay.view(host, "adv_samples")[:n_s] = torch.from_numpy(adv_samples)
     lay.view(host, "s_off").copy_(torch.from_numpy(s_off))
     lay.view(host, "seq").copy_(torch.from_numpy(seq))

@@ -20,7 +20,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "libmeshy_amd.so")
 
-SOURCES = ("capi.cpp", "plan.cpp", "logprob.hip", "topk.hip", "distill.hip", "pack.hip", "ppo.hip", "gae.hip", "critic.hip", "ragged.hip")
+SOURCES = ("capi.cpp", "plan.cpp", "hostio.cpp", "logprob.hip", "topk.hip", "distill.hip", "pack.hip", "ppo.hip", "gae.hip", "critic.hip", "ragged.hip")
 
 ARCH = os.environ.get("MESHY_OFFLOAD_ARCH", "gfx950")
 
@@ -66,7 +66,7 @@ def build(verbose: bool = False) -> str:
     with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
         objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
     tmp = OUT + ".tmp"
-    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", *objs, "-o", tmp]
+    cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", *objs, "-o", tmp]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -1,0 +1,161 @@
+// Host-side staging of jagged sample columns.
+//
+// The reference builds its step inputs from per-sample tensors with Python
+// loops and torch.cat (trainer.py:644-667 for the critic path, batch.py:126-178
+// for the micro-batches, metrics.py:197-212 for the rollout statistics).  Here
+// every column is staged into one pinned buffer for a single host-to-device
+// copy; meshy_host_gather does that concatenation on a small persistent pool of
+// threads, split by bytes, instead of torch.cat's one thread.
+#include <unistd.h>
+
+#include <algorithm>
+#include <atomic>
+#include <condition_variable>
+#include <cstdint>
+#include <cstring>
+#include <mutex>
+#include <thread>
+#include <vector>
+
+#include "common.h"
+
+namespace meshy {
+namespace {
+
+// Below this many bytes per worker a gather runs on fewer threads.
+constexpr int64_t kBytesPerWorker = 512 * 1024;
+constexpr int kMaxWorkers = 16;
+
+// One gather: pieces [0, n) of sizes nbytes[i] land at dst + start[i]; worker w
+// copies output bytes [w * total / k, (w + 1) * total / k).
+struct Job {
+    const void* const* srcs = nullptr;
+    const int64_t* nbytes = nullptr;
+    const int64_t* start = nullptr;  // exclusive prefix of nbytes, n + 1 entries
+    int64_t n = 0;
+    char* dst = nullptr;
+    int64_t total = 0;
+    int workers = 0;
+};
+
+void copy_share(const Job& j, int w) {
+    const int64_t lo = j.total * w / j.workers;
+    const int64_t hi = j.total * (w + 1) / j.workers;
+    if (lo >= hi) return;
+    // First piece overlapping [lo, hi).
+    int64_t i = std::upper_bound(j.start, j.start + j.n + 1, lo) - j.start - 1;
+    for (; i < j.n && j.start[i] < hi; ++i) {
+        const int64_t a = std::max(lo, j.start[i]);
+        const int64_t b = std::min(hi, j.start[i] + j.nbytes[i]);
+        if (b > a) std::memcpy(j.dst + a, static_cast<const char*>(j.srcs[i]) + (a - j.start[i]), b - a);
+    }
+}
+
+// Workers sleep on a condition variable between jobs; the calling thread takes
+// share 0 of each job.  One job at a time (callers serialise on run_mu).
+class Pool {
+  public:
+    static Pool& get() {
+        // A child process after fork() has none of the parent's threads: it
+        // builds its own pool (the parent's object is left alone).
+        static std::mutex mu;
+        static Pool* pool = nullptr;
+        std::lock_guard<std::mutex> lk(mu);
+        if (!pool || pool->pid_ != getpid()) pool = new Pool();
+        return *pool;
+    }
+
+    void run(const Job& job) {
+        std::lock_guard<std::mutex> serial(run_mu_);
+        const int helpers = job.workers - 1;
+        {
+            std::lock_guard<std::mutex> lk(mu_);
+            job_ = &job;
+            pending_ = helpers;
+            next_ = 1;
+            ++generation_;
+        }
+        cv_.notify_all();
+        copy_share(job, 0);
+        std::unique_lock<std::mutex> lk(mu_);
+        done_cv_.wait(lk, [&] { return pending_ == 0; });
+        job_ = nullptr;
+    }
+
+    int size() const { return static_cast<int>(threads_.size()) + 1; }
+
+  private:
+    Pool() : pid_(getpid()) {
+        const unsigned hw = std::thread::hardware_concurrency();
+        const int n = std::max(0, std::min<int>(kMaxWorkers, hw ? static_cast<int>(hw) : 1) - 1);
+        for (int t = 0; t < n; ++t) threads_.emplace_back([this] { loop(); });
+        for (auto& th : threads_) th.detach();
+    }
+
+    void loop() {
+        uint64_t seen = 0;
+        std::unique_lock<std::mutex> lk(mu_);
+        for (;;) {
+            cv_.wait(lk, [&] { return generation_ != seen; });
+            seen = generation_;
+            // Take shares while the job has any left.
+            while (job_ && next_ < job_->workers) {
+                const int w = next_++;
+                const Job* j = job_;
+                lk.unlock();
+                copy_share(*j, w);
+                lk.lock();
+                if (--pending_ == 0) done_cv_.notify_one();
+            }
+        }
+    }
+
+    pid_t pid_;
+    std::vector<std::thread> threads_;
+    std::mutex run_mu_;
+    std::mutex mu_;
+    std::condition_variable cv_, done_cv_;
+    const Job* job_ = nullptr;
+    int pending_ = 0;
+    int next_ = 0;
+    uint64_t generation_ = 0;
+};
+
+}  // namespace
+}  // namespace meshy
+
+extern "C" int meshy_host_gather(const void* const* srcs, const int64_t* nbytes, int64_t n, void* dst,
+                                 int max_threads) {
+    using namespace meshy;
+    clear_error();
+    if (n < 0) return set_error(MESHY_EINVAL, "meshy_host_gather: negative count");
+    if (n == 0) return MESHY_OK;
+    if (!srcs || !nbytes || !dst) return set_error(MESHY_ENULL, "meshy_host_gather: NULL pointer");
+    std::vector<int64_t> start(static_cast<size_t>(n) + 1);
+    start[0] = 0;
+    for (int64_t i = 0; i < n; ++i) {
+        if (nbytes[i] < 0) return set_error(MESHY_EINVAL, "meshy_host_gather: piece %lld has a negative size",
+                                            static_cast<long long>(i));
+        if (nbytes[i] > 0 && !srcs[i])
+            return set_error(MESHY_ENULL, "meshy_host_gather: piece %lld is NULL", static_cast<long long>(i));
+        start[i + 1] = start[i] + nbytes[i];
+    }
+    Job job;
+    job.srcs = srcs;
+    job.nbytes = nbytes;
+    job.start = start.data();
+    job.n = n;
+    job.dst = static_cast<char*>(dst);
+    job.total = start[n];
+    Pool& pool = Pool::get();
+    const int64_t want = std::max<int64_t>(1, job.total / kBytesPerWorker);
+    const int cap = max_threads > 0 ? std::min(max_threads, pool.size()) : pool.size();
+    job.workers = static_cast<int>(std::min<int64_t>(want, cap));
+    if (job.workers <= 1) {
+        job.workers = 1;
+        copy_share(job, 0);
+        return MESHY_OK;
+    }
+    pool.run(job);
+    return MESHY_OK;
+}

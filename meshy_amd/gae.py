@@ -135,6 +135,7 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
     view of its advantages, of length ``min(len(tokens), seq_len)``.
     """
     from .batch import ADVANTAGE_TOKENS, _Layout
+    from .hostio import gather_into
 
     if not samples:
         return {}
@@ -172,10 +173,14 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
     lay.add("reward", n, torch.float32)
     lay.add("offsets", n + 1, torch.int64)
     host = torch.empty(lay.size, dtype=torch.uint8, pin_memory=True)
-    torch.cat([m.to(device="cpu", dtype=torch.float32) for m in masks], out=lay.view(host, "mask"))
-    torch.cat([v.to(device="cpu", dtype=vdt) for v in vals], out=lay.view(host, "values"))
+    gather_into(masks, lay.view(host, "mask"))
+    gather_into(vals, lay.view(host, "values"))
     if all(isinstance(r, torch.Tensor) and r.numel() == 1 for r in rewards):
-        reward = torch.stack([r.reshape(()) for r in rewards]).to(device="cpu", dtype=torch.float32)
+        try:  # one shape (the usual 0-d rewards): stacked as they are
+            reward = torch.stack(rewards)
+        except RuntimeError:
+            reward = torch.stack([r.reshape(()) for r in rewards])
+        reward = reward.reshape(-1).to(device="cpu", dtype=torch.float32)
     else:
         reward = torch.tensor([float(r.reshape(-1)[0]) if isinstance(r, torch.Tensor) else float(r) for r in rewards],
                               dtype=torch.float32)

@@ -24,6 +24,7 @@ import torch
 
 from . import _lib
 from .batch import Batch, PackJob, _Layout, launch_pack
+from .hostio import gather_into
 from .plan import Plan, PlannerConfig, plan_tables, tables_to_plan
 from .wire import jagged_parts
 
@@ -84,10 +85,10 @@ class RaggedSamples:
         """From TensorDict-like samples (``tokens``, ``mask_assistant``, ``logprobs``, ``reward``)."""
         lengths = np.array([len(s["tokens"]) for s in samples], np.int64)
         r = cls(lengths, len(group_offsets) - 1, need_rollout_lp)
-        torch.cat([s["tokens"].to(torch.int32) for s in samples], out=r.view("tokens"))
-        torch.cat([s["mask_assistant"].to(torch.float32) for s in samples], out=r.view("mask"))
+        gather_into([s["tokens"] for s in samples], r.view("tokens"))
+        gather_into([s["mask_assistant"] for s in samples], r.view("mask"))
         if need_rollout_lp:
-            torch.cat([s["logprobs"].to(torch.float32) for s in samples], out=r.view("logprobs"))
+            gather_into([s["logprobs"] for s in samples], r.view("logprobs"))
         r.view("rewards")[:r.n] = torch.tensor([float(s["reward"]) for s in samples], dtype=torch.float32)
         r.view("group_off").copy_(torch.as_tensor(np.asarray(group_offsets, np.int64)))
         return r

@@ -1,0 +1,125 @@
+"""The host gather (meshy_host_gather / meshy_amd.hostio.gather_into) against
+torch.cat on the CPU: dtype conversion, empty, strided and 0-d parts, gathers
+large enough for every pool thread, concurrent callers and a forked child."""
+
+from __future__ import annotations
+
+import ctypes
+import multiprocessing as mp
+import threading
+
+import pytest
+import torch
+
+from meshy_amd import _lib
+from meshy_amd.hostio import gather_into
+
+
+def _parts(seed, n, hi, dtype=torch.float32):
+    g = torch.Generator().manual_seed(seed)
+    sizes = torch.randint(0, hi, (n,), generator=g).tolist()
+    return [torch.randn(s, generator=g).to(dtype) for s in sizes]
+
+
+@pytest.mark.parametrize("n,hi", [(1, 10), (7, 3), (300, 5000), (1024, 12000), (20000, 40)])
+def test_matches_cat(n, hi):
+    parts = _parts(n, n, hi)
+    out = torch.empty(sum(p.numel() for p in parts))
+    gather_into(parts, out)
+    assert torch.equal(out, torch.cat(parts))
+
+
+def test_converts_dtype_and_layout():
+    g = torch.Generator().manual_seed(3)
+    ints = torch.randint(0, 151936, (50, 7), generator=g)
+    parts = [ints[:, 2],                                   # strided
+             torch.tensor(5),                              # 0-d
+             torch.arange(10, dtype=torch.int64),          # another dtype
+             torch.zeros(0, dtype=torch.int32),            # empty
+             torch.arange(6, dtype=torch.int32).reshape(2, 3),
+             [1, 2, 3]]                                    # not a tensor
+    out = torch.empty(50 + 1 + 10 + 0 + 6 + 3, dtype=torch.int32)
+    gather_into(parts, out)
+    ref = torch.cat([ints[:, 2].to(torch.int32), torch.tensor([5], dtype=torch.int32),
+                     torch.arange(10, dtype=torch.int32), torch.arange(6, dtype=torch.int32),
+                     torch.tensor([1, 2, 3], dtype=torch.int32)])
+    assert torch.equal(out, ref)
+    bf = [torch.randn(100, generator=g) for _ in range(3)]
+    out = torch.empty(300, dtype=torch.bfloat16)
+    gather_into(bf, out)
+    assert torch.equal(out, torch.cat(bf).to(torch.bfloat16))
+
+
+def test_large_gather_every_thread_count():
+    parts = _parts(11, 64, 300_000)
+    ref = torch.cat(parts)
+    lib = _lib.load()
+    ptrs = (ctypes.c_void_p * len(parts))(*[p.data_ptr() for p in parts])
+    sizes = (ctypes.c_int64 * len(parts))(*[p.numel() * 4 for p in parts])
+    for threads in (1, 2, 3, 16, 0):
+        out = torch.full_like(ref, float("nan"))
+        assert lib.meshy_host_gather(ptrs, sizes, len(parts), out.data_ptr(), threads) == 0
+        assert torch.equal(out, ref), threads
+
+
+def test_concurrent_callers():
+    jobs = [_parts(100 + k, 40, 200_000) for k in range(6)]
+    outs = [torch.empty(sum(p.numel() for p in ps)) for ps in jobs]
+    errors = []
+
+    def work(k):
+        try:
+            for _ in range(5):
+                gather_into(jobs[k], outs[k])
+        except Exception as e:  # noqa: BLE001 - reported below
+            errors.append(e)
+
+    threads = [threading.Thread(target=work, args=(k,)) for k in range(len(jobs))]
+    for t in threads:
+        t.start()
+    for t in threads:
+        t.join()
+    assert not errors
+    for ps, out in zip(jobs, outs):
+        assert torch.equal(out, torch.cat(ps))
+
+
+def _child(q):
+    # torch's OpenMP pool does not survive fork(): the child's own torch ops
+    # stay on one thread (the gather's pool is what is under test).
+    torch.set_num_threads(1)
+    parts = _parts(7, 32, 200_000)
+    out = torch.empty(sum(p.numel() for p in parts))
+    gather_into(parts, out)
+    q.put(bool(torch.equal(out, torch.cat(parts))))
+
+
+def test_forked_child_has_its_own_pool():
+    gather_into(_parts(1, 32, 200_000), torch.empty(sum(p.numel() for p in _parts(1, 32, 200_000))))
+    ctx = mp.get_context("fork")
+    q = ctx.Queue()
+    p = ctx.Process(target=_child, args=(q,), daemon=True)
+    p.start()
+    try:
+        ok = q.get(timeout=60)
+    finally:
+        p.join(timeout=10)
+        if p.is_alive():
+            p.kill()
+    assert ok and p.exitcode == 0
+
+
+def test_errors():
+    with pytest.raises(ValueError, match="elements"):
+        gather_into([torch.ones(3)], torch.empty(4))
+    lib = _lib.load()
+    sizes = (ctypes.c_int64 * 2)(4, -1)
+    ptrs = (ctypes.c_void_p * 2)(0x1000, 0x1000)
+    assert lib.meshy_host_gather(ptrs, sizes, 2, 0x1000, 0) == -1
+    assert "negative size" in lib.meshy_last_error().decode()
+    sizes = (ctypes.c_int64 * 2)(4, 4)
+    ptrs = (ctypes.c_void_p * 2)(0x1000, None)
+    assert lib.meshy_host_gather(ptrs, sizes, 2, 0x1000, 0) == -2
+    assert lib.meshy_host_gather(None, sizes, 2, 0x1000, 0) == -2
+    assert lib.meshy_host_gather(ptrs, sizes, -1, 0x1000, 0) == -1
+    assert lib.meshy_host_gather(None, None, 0, None, 0) == 0
