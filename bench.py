@@ -842,6 +842,18 @@ def bench_rollout_metrics(runs, no_cpu):
     fields = list(samples[0])
     cols = wire.samples_to_columns(samples, fields)
     out = {"samples": len(samples), "tokens": int(batch.total)}
+    # The rollout side of the same wire (rollout.py:611-615): Python-list
+    # samples to columns, one pass per column against a tensor per sample.
+    from types import SimpleNamespace as NS
+
+    rollout = [NS(tokens=batch.tokens[a:b].astype(int).tolist(), logprobs=batch.logprobs[a:b].tolist(),
+                  masks=batch.mask[a:b].astype(int).tolist(), reward=float(rewards[i]), advantage=0.5,
+                  truncated=i % 9 == 0, repetition=False, mixed_version=False)
+               for i, (a, b) in enumerate(zip(batch.offsets[:-1], batch.offsets[1:]))]
+    out["wire_group_to_columns_ms"] = round(
+        _wall_ms(lambda: wire.rollout_group_to_columns(rollout, 3), runs, warmup=1, gpu=False), 3)
+    out["wire_per_sample_ms"] = round(_wall_ms(lambda: wire.samples_to_columns(
+        [wire.sample_to_tensordict(s, 3) for s in rollout], wire.GRPO_TRAINER_FIELDS), runs, warmup=1, gpu=False), 3)
     out["gpu_from_samples_ms"] = round(_wall_ms(lambda: rollout_metrics(samples, 8192, 4), runs, warmup=2), 3)
     out["gpu_from_columns_ms"] = round(_wall_ms(lambda: rollout_metrics(cols, 8192, 4), runs, warmup=2), 3)
     if not no_cpu:

@@ -14,8 +14,10 @@ touched on the way into the pack.
 
 from __future__ import annotations
 
+import itertools
 from typing import Any, Iterable
 
+import numpy as np
 import torch
 
 # How each known column is materialised in a batch (adapter.py:39-71).
@@ -45,6 +47,21 @@ _SCALAR_DTYPE: dict[str, torch.dtype] = {
     "truncated": torch.int64,
     "repetition": torch.int64,
     "mixed_version": torch.int64,
+}
+
+
+# The columns a GRPO rollout writes (meshy/config.py:248-261) and the shaped
+# reward's companion column (rollout.py:35).
+GRPO_TRAINER_FIELDS: tuple[str, ...] = ("tokens", "logprobs", "mask_assistant", "advantage", "weight_version",
+                                        "reward", "truncated", "repetition", "mixed_version")
+RAW_REWARD_FIELD = "raw_reward"
+
+# Per-token columns of a rollout sample: the sample attribute and dtype they
+# come from (rollout.py:124-126).
+_SEQ_SOURCE: dict[str, tuple[str, torch.dtype]] = {
+    "tokens": ("tokens", torch.int64),
+    "logprobs": ("logprobs", torch.float32),
+    "mask_assistant": ("masks", torch.float32),
 }
 
 
@@ -87,6 +104,70 @@ def samples_to_columns(samples: list[Any], fields: Iterable[str]) -> dict[str, A
     return out
 
 
+def _stamp(sample: Any, f: str, weight_version: int) -> float | int:
+    """A rollout sample's scalar column (rollout.py:127-152): a missing advantage
+    is 0, a missing raw reward is the reward, the quality stamps are 0/1."""
+    if f == "advantage":
+        return 0.0 if sample.advantage is None else float(sample.advantage)
+    if f == "weight_version":
+        return int(weight_version)
+    if f == "reward":
+        return float(sample.reward)
+    if f == "positive_lm_weight":
+        return float(getattr(sample, "positive_lm_weight", 0.0))
+    if f == RAW_REWARD_FIELD:
+        raw = getattr(sample, "raw_reward", None)
+        return float(sample.reward if raw is None else raw)
+    if f in ("truncated", "repetition", "mixed_version"):
+        return int(bool(getattr(sample, f, False)))
+    raise KeyError(f)
+
+
+_ROLLOUT_SCALARS = ("advantage", "weight_version", "reward", "positive_lm_weight", RAW_REWARD_FIELD, "truncated",
+                    "repetition", "mixed_version")
+
+
+def sample_to_tensordict(sample: Any, weight_version: int) -> dict[str, torch.Tensor]:
+    """One rollout sample as its columns (rollout.py:118-153), a ``dict`` in place
+    of the ``TensorDict``: the token, log-prob and mask sequences as ``[L]``
+    tensors (int64, fp32, fp32) and every scalar stamp as a 0-dim tensor."""
+    out: dict[str, torch.Tensor] = {}
+    for f, (attr, dt) in _SEQ_SOURCE.items():
+        out[f] = torch.tensor(list(getattr(sample, attr)), dtype=dt)
+    for f in _ROLLOUT_SCALARS:
+        out[f] = torch.tensor(_stamp(sample, f, weight_version), dtype=_SCALAR_DTYPE[f])
+    return out
+
+
+def rollout_group_to_columns(group: list[Any], weight_version: int,
+                             fields: Iterable[str] = GRPO_TRAINER_FIELDS) -> dict[str, Any]:
+    """``samples_to_columns([sample_to_tensordict(s, v) for s in group], fields)``
+    (the write of rollout.py:611-615) without a tensor per sample: each
+    per-token column is converted from the samples' sequences in one pass into
+    flat values plus offsets and wrapped as a jagged nested tensor over them;
+    each scalar column is one ``[B, 1]`` tensor."""
+    fields = list(fields)
+    batch = len(group)
+    if batch == 0:
+        raise ValueError("samples_to_td received an empty sample list")
+    out: dict[str, Any] = {}
+    for f in fields:
+        if f in _SEQ_SOURCE:
+            attr, dt = _SEQ_SOURCE[f]
+            seqs = [getattr(s, attr) for s in group]
+            off = np.zeros(batch + 1, np.int64)
+            np.cumsum(np.fromiter((len(x) for x in seqs), np.int64, batch), out=off[1:])
+            npdt = np.int64 if dt == torch.int64 else np.float32
+            flat = np.fromiter(itertools.chain.from_iterable(seqs), npdt, int(off[-1]))
+            out[f] = torch.nested.nested_tensor_from_jagged(torch.from_numpy(flat), torch.from_numpy(off))
+        elif f in _ROLLOUT_SCALARS:
+            out[f] = torch.tensor([_stamp(s, f, weight_version) for s in group],
+                                  dtype=_SCALAR_DTYPE[f]).reshape(batch, 1)
+        else:
+            raise KeyError(f"a rollout sample has no column {f!r}")
+    return out
+
+
 def _explode(value: Any, f: str, batch: int) -> list[Any]:
     """One batched column -> ``batch`` independent values (adapter.py:135-159)."""
     if isinstance(value, list):
@@ -125,4 +206,5 @@ def jagged_parts(column: Any) -> tuple[torch.Tensor, torch.Tensor]:
     return flat, off
 
 
-__all__ = ["FIELD_KINDS", "columns_to_samples", "field_kind", "jagged_parts", "samples_to_columns"]
+__all__ = ["FIELD_KINDS", "GRPO_TRAINER_FIELDS", "RAW_REWARD_FIELD", "columns_to_samples", "field_kind",
+           "jagged_parts", "rollout_group_to_columns", "sample_to_tensordict", "samples_to_columns"]

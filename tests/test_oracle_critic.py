@@ -5,7 +5,9 @@ closed forms, and the samples <-> columns round trip of adapter.py."""
 from __future__ import annotations
 
 import math
+from types import SimpleNamespace as NS
 
+import numpy as np
 import pytest
 import torch
 
@@ -156,3 +158,85 @@ def test_wire_round_trip_and_validation():
         wire.samples_to_columns([], ["tokens"])
     assert wire.field_kind("unknown") == "object"
     assert math.isclose(float(cols["reward"][0]), 1.0)
+
+
+def _rollout_sample(seed, L, **kw):
+    g = torch.Generator().manual_seed(seed)
+    s = NS(tokens=torch.randint(0, 151936, (L,), generator=g).tolist(),
+           logprobs=(-torch.rand(L, generator=g) * 3).tolist(),
+           masks=[0] * min(3, L) + [1] * max(0, L - 3),
+           reward=float(seed % 2), advantage=float(seed) / 7.0, raw_reward=None,
+           truncated=seed % 3 == 0, repetition=seed % 4 == 0, mixed_version=seed % 5 == 0,
+           positive_lm_weight=0.5 * (seed % 2))
+    for k, v in kw.items():
+        setattr(s, k, v)
+    return s
+
+
+def test_sample_to_tensordict_known_answers():
+    """test_rollout_stamps.py:34-46 and test_vapo_alignment.py:96-104."""
+    from meshy_amd import wire
+
+    s = NS(tokens=[1, 2, 3], logprobs=[0.0, -0.5, -0.5], masks=[0, 1, 1], reward=1.0, advantage=0.25,
+           truncated=True, mixed_version=True, repetition=True)
+    td = wire.sample_to_tensordict(s, weight_version=7)
+    assert set(wire.GRPO_TRAINER_FIELDS) <= set(td)
+    assert td["reward"].item() == 1.0 and td["truncated"].item() == 1
+    assert td["mixed_version"].item() == 1 and td["repetition"].item() == 1
+    assert td["weight_version"].item() == 7 and td["raw_reward"].item() == 1.0
+    assert td["positive_lm_weight"].item() == 0.0  # absent: 0
+    back = wire.columns_to_samples(wire.samples_to_columns([td, td], wire.GRPO_TRAINER_FIELDS),
+                                   wire.GRPO_TRAINER_FIELDS)
+    assert back[0]["truncated"].dtype == torch.int64 and back[1]["reward"].item() == 1.0
+    group = [NS(tokens=[1, 2, 3], logprobs=[-1.0] * 3, masks=[0, 1, 1], reward=r, advantage=0.0,
+                raw_reward=raw, positive_lm_weight=w)
+             for r, raw, w in [(1.0, 1.0, 0.5), (0.4, 1.0, 0.5), (0.0, 0.0, 0.0), (0.0, 0.0, 0.0)]]
+    fields = ("tokens", "logprobs", "mask_assistant", "reward", "positive_lm_weight")
+    packed = wire.samples_to_columns([wire.sample_to_tensordict(x, 0) for x in reversed(group)], fields)
+    assert packed["positive_lm_weight"].dtype == torch.float32
+    assert packed["positive_lm_weight"].reshape(-1).tolist() == [0.0, 0.0, 0.5, 0.5]
+    none_adv = wire.sample_to_tensordict(NS(tokens=[], logprobs=[], masks=[], reward=0.0, advantage=None), 1)
+    assert none_adv["advantage"].item() == 0.0 and none_adv["tokens"].shape == (0,)
+
+
+def test_rollout_group_columns_equal_the_per_sample_path():
+    """The one-pass group conversion against samples_to_columns over
+    sample_to_tensordict: sequences given as lists, tuples and numpy arrays,
+    an empty sample, a missing advantage and raw reward, every column."""
+    from meshy_amd import wire
+
+    group = [_rollout_sample(k, L) for k, L in enumerate([5, 1, 0, 700, 33, 2048])]
+    group[1].tokens = tuple(group[1].tokens)
+    group[3].logprobs = np.asarray(group[3].logprobs, np.float64)
+    group[4].advantage = None
+    group[5].raw_reward = 0.75
+    del group[0].positive_lm_weight
+    fields = list(wire.GRPO_TRAINER_FIELDS) + ["positive_lm_weight", "raw_reward"]
+    fast = wire.rollout_group_to_columns(group, 11, fields)
+    ref = wire.samples_to_columns([wire.sample_to_tensordict(s, 11) for s in group], fields)
+    for f in fields:
+        if wire.field_kind(f) == "nested":
+            (fv, fo), (rv, ro) = wire.jagged_parts(fast[f]), wire.jagged_parts(ref[f])
+            assert fv.dtype == rv.dtype and torch.equal(fv, rv) and torch.equal(fo, ro), f
+            assert all(torch.equal(a, b) for a, b in zip(fast[f].unbind(), ref[f].unbind())), f
+        else:
+            assert fast[f].dtype == ref[f].dtype and torch.equal(fast[f], ref[f]), f
+    with pytest.raises(KeyError):
+        wire.rollout_group_to_columns(group, 0, ["values"])
+    with pytest.raises(ValueError, match="empty"):
+        wire.rollout_group_to_columns([], 0)
+
+
+def test_rollout_group_columns_feed_the_pack_buffers():
+    """RaggedSamples.from_columns over the group columns stages the same bytes
+    as from_samples over the per-sample tensors."""
+    from meshy_amd import wire
+    from meshy_amd.pipeline import RaggedSamples
+
+    group = [_rollout_sample(k, L) for k, L in enumerate([9, 400, 17, 1024, 3, 250, 600, 64])]
+    cols = wire.rollout_group_to_columns(group, 2)
+    tds = [wire.sample_to_tensordict(s, 2) for s in group]
+    a = RaggedSamples.from_columns(cols, [0, 4, 8])
+    b = RaggedSamples.from_samples(tds, [0, 4, 8])
+    for name in ("tokens", "mask", "logprobs", "rewards", "group_off", "s_off"):
+        assert torch.equal(a.view(name), b.view(name)), name
