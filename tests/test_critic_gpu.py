@@ -77,6 +77,64 @@ def test_accumulator_matches_oracle(dev, bf16):
     assert st.row_reward == pytest.approx(rs["row_reward"]) and st.row_group == rs["row_group"]
 
 
+def _gauge_window(rows=24, span=40, seed=0):
+    """The window of the reference's gauge tests (test_critic_batching.py:145-154)."""
+    g = torch.Generator().manual_seed(seed)
+    mask = torch.zeros(rows, span)
+    for j in range(rows):
+        mask[j, 3 + j % 5:] = 1.0
+    returns = torch.randn(rows, span, generator=g) * mask
+    values = (returns + 0.3 * torch.randn(rows, span, generator=g)) * mask
+    rewards = (torch.rand(rows, generator=g) > 0.5).float()
+    groups = torch.arange(rows) // 4
+    return values, returns, mask, rewards, groups
+
+
+def _sums(states):
+    return {k: sum(getattr(s, k) for s in states) for k in ("n_tokens", "sum_r", "sum_r2", "sum_d", "sum_d2")}
+
+
+def test_accumulator_streaming_split_and_filler_rows(dev):
+    """test_critic_batching.py:158-212 on the states the gauges are built from:
+    5-row micro-batches, an interleaved two-rank split and all-zero-mask filler
+    rows give the window's sums (and its rows, in the split's order)."""
+    from meshy_amd import critic
+
+    w = [x.to(dev) for x in _gauge_window(seed=1)]
+    whole = critic.Accumulator()
+    whole.update(*w)
+    want = _sums([whole.state])
+    assert want["n_tokens"] == float(w[2].sum().item())
+
+    def close(got):
+        for k, v in want.items():
+            assert got[k] == pytest.approx(v, rel=1e-5, abs=1e-6), k
+
+    stream = critic.Accumulator()
+    for lo in range(0, 24, 5):
+        stream.update(*(x[lo:lo + 5] for x in w))
+    close(_sums([stream.state]))
+    assert stream.state.row_value == pytest.approx(whole.state.row_value, abs=1e-6)
+    assert stream.state.row_group == whole.state.row_group
+
+    ranks = []
+    for rank in range(2):
+        sel = torch.arange(rank, 24, 2, device=dev)
+        acc = critic.Accumulator()
+        acc.update(*(x[sel] for x in w))
+        ranks.append(acc.state)
+    close(_sums(ranks))
+    assert sorted(x for s in ranks for x in s.row_group) == sorted(whole.state.row_group)
+    assert sorted(x for s in ranks for x in s.row_value) == pytest.approx(sorted(whole.state.row_value), abs=1e-6)
+
+    filled = critic.Accumulator()
+    filled.update(*w)
+    v, r, m, rw, gr = w
+    filled.update(torch.randn_like(v[:3]), torch.randn_like(r[:3]), torch.zeros_like(m[:3]), rw[:3], gr[:3])
+    close(_sums([filled.state]))
+    assert filled.state.row_value[24:] == [0.0, 0.0, 0.0]
+
+
 @pytest.mark.parametrize("clip", [None, 0.2])
 def test_clipped_value_error_fwd_bwd(dev, clip):
     from meshy_amd import critic
