@@ -48,19 +48,22 @@ class RaggedSamples:
         lay.add("s_off", n + 1, torch.int64)
         lay.add("rewards", max(n, 1), torch.float32)
         lay.add("group_off", n_groups + 1, torch.int64)
+        lay.add("pos_w", max(n, 1), torch.float32)
+        # Everything above is the samples' and goes to the device as soon as a
+        # pack starts; the plan tables below follow once they are computed.
+        self.tables_at = lay.size
         # plan tables of one rank: at most n micros and n documents
         lay.add("seq", max(n, 1), torch.int64)
         lay.add("out_off", n + 1, torch.int64)
         lay.add("doc_len", max(n, 1), torch.int64)
         lay.add("doc_start", n + 1, torch.int32)
         lay.add("doc_sample", max(n, 1), torch.int32)
-        lay.add("pos_w", max(n, 1), torch.float32)
-        lay.add("adv_samples", max(n, 1), torch.float32)
+        lay.add("adv_samples", max(n, 1), torch.float32)  # written on the device
         self.lay = lay
         self.n_groups = n_groups
         # Pinned when a device is present, so the one copy to it is a DMA.
         self.buf = torch.empty(lay.size, dtype=torch.uint8, pin_memory=torch.cuda.is_available())
-        self.copied = None  # event of the last host-to-device copy out of buf
+        self.copied = None  # event of the last copy of the plan tables out of buf
         self.view("s_off").copy_(torch.from_numpy(self.offsets))
         self.view("pos_w").zero_()
 
@@ -132,8 +135,17 @@ class PackResult:
 
 def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int = 1, rank: int = 0,
               with_plan_objects: bool = True, broadcast_advantages: bool = True) -> PackResult:
-    """Plan, copy once, normalise rewards and build every micro of ``rank``."""
+    """Plan, copy, normalise rewards and build every micro of ``rank``.
+
+    The samples' part of the staging buffer is copied to the device first, so
+    the transfer runs while the host plans; the plan tables follow in a second,
+    small copy."""
     device = torch.device(device)
+    stream = torch.cuda.current_stream(device)
+    lay = ragged.lay
+    dbuf = torch.empty(lay.size, dtype=torch.uint8, device=device)
+    cut = ragged.tables_at
+    dbuf[:cut].copy_(ragged.buf[:cut], non_blocking=True)
     lengths, loss = ragged.sample_lengths(cfg.seq_len)
     t = plan_tables(lengths, loss, dp_size, cfg)
     if ragged.copied is not None:
@@ -158,12 +170,9 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
     ragged.view("doc_sample")[:nd_total] = torch.from_numpy(dsample[:nd_total].astype(np.int32))
     ragged.view("doc_len")[:nd_total] = torch.from_numpy(dlen[:nd_total])
 
-    stream = torch.cuda.current_stream(device)
-    dbuf = torch.empty(ragged.lay.size, dtype=torch.uint8, device=device)
-    dbuf.copy_(ragged.buf, non_blocking=True)
+    dbuf[cut:].copy_(ragged.buf[cut:], non_blocking=True)
     ragged.copied = torch.cuda.Event()
     ragged.copied.record(stream)
-    lay = ragged.lay
 
     adv = lay.view(dbuf, "adv_samples")[:ragged.n]
     rc = _lib.load().meshy_grpo_advantage(lay.view(dbuf, "rewards").data_ptr(), ragged.n,
