@@ -184,8 +184,9 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
     if plan is not None:
         micros = tuple(m for mini in plan.per_rank[rank] for m in mini.micros)
     else:
-        micros = tuple(_LiteMicro(int(seq[k]), int(n_docs[k]), int(dlen[start[k]:start[k + 1]].sum()),
-                                  tuple(int(x) for x in dlen[start[k]:start[k + 1]])) for k in range(nm))
+        sq, st, dl = seq.tolist(), start.tolist(), dlen[:nd_total].tolist()
+        micros = tuple(_LiteMicro(sq[k], st[k + 1] - st[k], sum(dl[st[k]:st[k + 1]]), tuple(dl[st[k]:st[k + 1]]))
+                       for k in range(nm))
     job = PackJob(
         micros=micros, layout=cfg.layout, device=device, dbuf=dbuf, lay=lay,
         need_rollout_lp=ragged.need_rollout_lp, per_token_adv=False, n_samples=ragged.n, seq=seq,

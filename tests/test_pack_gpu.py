@@ -340,3 +340,28 @@ def test_pack_step_256_samples_matches_oracle(dev):
         assert (mb.advantages.cpu() - ref["advantages"]).abs().max().item() <= 1e-5
         bcast = torch.cat([ref["advantages"], torch.zeros(1)])[ref["doc_ids"]]
         assert (mb.advantage_tokens.cpu() - bcast).abs().max().item() <= 1e-5
+
+
+@pytest.mark.parametrize("layout", ["packed", "padded"])
+def test_pack_step_without_plan_objects_builds_the_same_batches(dev, layout):
+    """with_plan_objects=False skips the Plan dataclasses, not any output; two
+    calls in a row over one staging buffer (the tables region is rewritten)."""
+    from meshy_amd import workloads
+    from meshy_amd.pipeline import RaggedSamples, pack_step
+    from meshy_amd.plan import PlannerConfig
+
+    batch, rewards, group_offsets = workloads.grpo_256_samples(0)
+    ragged = RaggedSamples.from_arrays(batch.tokens, batch.mask, batch.logprobs, batch.offsets, rewards,
+                                       group_offsets)
+    cfg = PlannerConfig(layout=layout, mini_batch_size=64, seq_len=8192, align=2048, max_tokens_per_micro=8192)
+    full = pack_step(ragged, cfg, dev)
+    lite = pack_step(ragged, cfg, dev, with_plan_objects=False)
+    assert lite.plan is None and full.plan is not None
+    assert len(full.batches) == len(lite.batches) > 4
+    for a, b in zip(full.batches, lite.batches):
+        for k in ("input_ids", "labels", "positions", "mask", "doc_ids", "rollout_logprobs", "advantages",
+                  "advantage_tokens", "lengths"):
+            x, y = getattr(a, k), getattr(b, k)
+            assert x.shape == y.shape and torch.equal(x, y), k
+        assert a.n_docs == b.n_docs
+    assert torch.equal(full.advantages, lite.advantages)
