@@ -384,6 +384,19 @@ def bench_pack(runs, no_cpu):
         # doc_ids 8 each, positions 4, mask 4, rollout lp 4, adv_tok 4 per output token
         "bytes": real * 12 + n_out * 40,
     }
+    # The trainer's drop-in (batch.py:96 build_micro_batch, all micros of the
+    # mini-batch in one call): per-sample tensors staged by the host gather,
+    # given the plan and the advantages.
+    from meshy_amd.batch import build_micro_batches
+
+    samples_t = [dict(s, advantage=torch.tensor(0.5)) for s in batch.sample_dicts(rewards=rewards)]
+    local_t = r.plan.local_samples(samples_t, 0)
+    micros = [m for mini in r.plan.per_rank[0] for m in mini.micros]
+    held = {}
+    out["build_micro_batches_from_samples_us"] = round(1e3 * _wall_ms(
+        lambda: held.__setitem__("b", build_micro_batches(local_t, micros, layout="packed", device=dev,
+                                                          need_rollout_lp=True)),
+        runs, warmup=2, before=lambda: held.pop("b", None)), 1)
     if not no_cpu:
         from oracle import batch as obatch
         from oracle import grpo as ogrpo

@@ -116,11 +116,35 @@ class _Layout:
         return buf[lo:hi].view(dtype)
 
 
-def _scalar(td, key: str, default: float = 0.0) -> float:
-    v = td.get(key, default) if hasattr(td, "get") else default
+def _scalar_of(v, default: float) -> float:
+    if v is None:
+        return default
     if isinstance(v, torch.Tensor):
         return float(v.reshape(-1)[0].item()) if v.numel() else default
     return float(v)
+
+
+def _scalars(samples: Sequence[Any], idxs: Sequence[int], key: str, default: float = 0.0) -> np.ndarray:
+    """``_scalar`` of each listed sample (fp64): one stack when every value is a
+    one-element tensor (the usual 0-dim columns), else one by one."""
+    vals = [samples[i].get(key, None) if hasattr(samples[i], "get") else None for i in idxs]
+    if vals and all(isinstance(v, torch.Tensor) for v in vals):
+        try:
+            st = torch.stack(vals)
+        except RuntimeError:  # shapes, devices or dtypes torch cannot stack
+            st = None
+        if st is not None and st.numel() == len(vals):
+            return st.reshape(-1).to(device="cpu", dtype=torch.float64).numpy()
+    return np.array([_scalar_of(v, default) for v in vals], np.float64)
+
+
+def _n(x) -> int:
+    return int(x.shape[0]) if isinstance(x, torch.Tensor) else len(x)
+
+
+def _head(x, L: int):
+    """The first L entries of a per-token column (the column itself when it has L)."""
+    return x if _n(x) == L else x[:L]
 
 
 @dataclass
@@ -191,9 +215,21 @@ def stage_micro_batches(
             else:
                 need_len[remap[idx]] = max(need_len[remap[idx]], int(L))
     n_s = len(used)
-    for j, idx in enumerate(used):
-        if int(len(samples[idx]["tokens"])) < need_len[j]:
-            raise ValueError(f"sample {idx} has {len(samples[idx]['tokens'])} tokens, micro wants {need_len[j]}")
+    # The per-token columns each micro reads, in one pass over the samples.
+    # Token ids travel in the samples' own int64 (the reference's dtype) or as
+    # int32 (any vocabulary fits), and come out int64 either way.
+    tok_parts, mask_parts, lp_parts = [], [], []
+    tok64 = True
+    for idx, L in zip(used, need_len):
+        s = samples[idx]
+        tk = s["tokens"]
+        if _n(tk) < L:
+            raise ValueError(f"sample {idx} has {_n(tk)} tokens, micro wants {L}")
+        tok64 = tok64 and isinstance(tk, torch.Tensor) and tk.dtype == torch.int64
+        tok_parts.append(_head(tk, L))
+        mask_parts.append(_head(s["mask_assistant"], L))
+        if need_rollout_lp:
+            lp_parts.append(_head(s["logprobs"], L))
     per_token_adv = any(ADVANTAGE_TOKENS in samples[m.sample_idx[0]] for m in micros if m.sample_idx)
     s_off = np.zeros(n_s + 1, np.int64)
     np.cumsum(need_len, out=s_off[1:])
@@ -213,13 +249,12 @@ def stage_micro_batches(
     n_docs_total = int(doc_start[-1])
     doc_sample = np.array([remap[i] for m in micros for i in m.sample_idx], np.int32)
     doc_len = np.array([L for m in micros for L in m.doc_lens], np.int64)
-    adv_samples = np.array([_scalar(samples[i], "advantage") for i in used], np.float32)
-    pos_w = np.array([
-        _scalar(samples[i], "positive_lm_weight") if _scalar(samples[i], "reward") > 0.5 else 0.0
-        for m in micros for i in m.sample_idx], np.float32)
-
-    # Token ids travel as int32 (any vocabulary fits) and come out int64 like the reference's.
-    tok_dtype = torch.int32
+    adv_samples = _scalars(samples, used, "advantage").astype(np.float32)
+    # Positive-LM weights only for rewards above 0.5 (batch.py:225-229).
+    pos_used = np.where(_scalars(samples, used, "reward") > 0.5, _scalars(samples, used, "positive_lm_weight"),
+                        0.0).astype(np.float32)
+    pos_w = pos_used[doc_sample] if n_docs_total else np.zeros(0, np.float32)
+    tok_dtype = torch.int64 if tok64 else torch.int32
 
     # Per-token advantages already on the device (attach_gae_advantages leaves
     # them there) are gathered on the device; host ones travel with the rest.
@@ -256,10 +291,10 @@ def stage_micro_batches(
     host = stage.get(lay.size)
     if n_s:
         srcs = [samples[i] for i in used]
-        gather_into([s["tokens"][:L] for s, L in zip(srcs, need_len)], lay.view(host, "tokens"))
-        gather_into([s["mask_assistant"][:L] for s, L in zip(srcs, need_len)], lay.view(host, "mask"))
+        gather_into(tok_parts, lay.view(host, "tokens"))
+        gather_into(mask_parts, lay.view(host, "mask"))
         if need_rollout_lp:
-            gather_into([s["logprobs"][:L] for s, L in zip(srcs, need_len)], lay.view(host, "logprobs"))
+            gather_into(lp_parts, lay.view(host, "logprobs"))
         if teacher_k:
             gather_into([s[TEACHER_FIELDS[0]][:L] for s, L in zip(srcs, need_len)], lay.view(host, "teacher_ids"))
             gather_into([s[TEACHER_FIELDS[1]][:L] for s, L in zip(srcs, need_len)], lay.view(host, "teacher_lps"))
@@ -333,7 +368,7 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
 
     a = _lib.PackArgs()
     a.tokens = lay.view(dbuf, "tokens").data_ptr()
-    a.tokens_elem_bytes = 4
+    a.tokens_elem_bytes = lay.regions["tokens"][2].itemsize
     a.layout = _lib.MESHY_LAYOUT_PACKED if layout == "packed" else _lib.MESHY_LAYOUT_PADDED
     a.mask = lay.view(dbuf, "mask").data_ptr()
     a.logprobs = lay.view(dbuf, "logprobs").data_ptr() if job.need_rollout_lp else None
