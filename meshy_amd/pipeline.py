@@ -32,7 +32,8 @@ from .wire import jagged_parts
 class RaggedSamples:
     """One step's samples as flat pinned host arrays, in global sample order."""
 
-    def __init__(self, lengths: np.ndarray, n_groups: int, need_rollout_lp: bool) -> None:
+    def __init__(self, lengths: np.ndarray, n_groups: int, need_rollout_lp: bool,
+                 token_dtype: torch.dtype = torch.int32) -> None:
         n = len(lengths)
         self.n = n
         self.lengths = np.asarray(lengths, np.int64)
@@ -41,7 +42,9 @@ class RaggedSamples:
         self.total = int(self.offsets[-1])
         self.need_rollout_lp = need_rollout_lp
         lay = _Layout()
-        lay.add("tokens", self.total, torch.int32)
+        if token_dtype not in (torch.int32, torch.int64):
+            raise ValueError("token ids are staged as int32 or int64")
+        lay.add("tokens", self.total, token_dtype)
         lay.add("mask", self.total, torch.float32)
         if need_rollout_lp:
             lay.add("logprobs", self.total, torch.float32)
@@ -86,9 +89,12 @@ class RaggedSamples:
     @classmethod
     def from_samples(cls, samples: Sequence[Any], group_offsets, need_rollout_lp: bool = True) -> "RaggedSamples":
         """From TensorDict-like samples (``tokens``, ``mask_assistant``, ``logprobs``, ``reward``)."""
-        lengths = np.array([len(s["tokens"]) for s in samples], np.int64)
-        r = cls(lengths, len(group_offsets) - 1, need_rollout_lp)
-        gather_into([s["tokens"] for s in samples], r.view("tokens"))
+        toks = [s["tokens"] for s in samples]
+        lengths = np.array([t.shape[0] if isinstance(t, torch.Tensor) else len(t) for t in toks], np.int64)
+        # int64 ids (the reference's dtype) are staged as they are, others as int32.
+        tok64 = all(isinstance(t, torch.Tensor) and t.dtype == torch.int64 for t in toks)
+        r = cls(lengths, len(group_offsets) - 1, need_rollout_lp, torch.int64 if tok64 else torch.int32)
+        gather_into(toks, r.view("tokens"))
         gather_into([s["mask_assistant"] for s in samples], r.view("mask"))
         if need_rollout_lp:
             gather_into([s["logprobs"] for s in samples], r.view("logprobs"))

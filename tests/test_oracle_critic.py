@@ -238,5 +238,7 @@ def test_rollout_group_columns_feed_the_pack_buffers():
     tds = [wire.sample_to_tensordict(s, 2) for s in group]
     a = RaggedSamples.from_columns(cols, [0, 4, 8])
     b = RaggedSamples.from_samples(tds, [0, 4, 8])
-    for name in ("tokens", "mask", "logprobs", "rewards", "group_off", "s_off"):
+    assert a.view("tokens").dtype == torch.int32 and b.view("tokens").dtype == torch.int64
+    assert torch.equal(a.view("tokens").long(), b.view("tokens"))
+    for name in ("mask", "logprobs", "rewards", "group_off", "s_off"):
         assert torch.equal(a.view(name), b.view(name)), name
