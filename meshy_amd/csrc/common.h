@@ -47,6 +47,8 @@ __device__ __forceinline__ int dpp_i32(int v) {
     return __builtin_amdgcn_update_dpp(0, v, kCtrl, 0xF, 0xF, false);
 }
 constexpr int kDppRowRor1 = 0x121, kDppRowRor2 = 0x122, kDppRowRor4 = 0x124, kDppRowRor8 = 0x128;
+// Whole-wavefront shift: lane l takes lane l - 1's value, lane 0 gets 0.
+constexpr int kDppWaveShr1 = 0x138;
 
 template <int kCtrl>
 __device__ __forceinline__ float dpp_f32(float v) {

@@ -92,8 +92,10 @@ __device__ __forceinline__ float kth_largest_lane(float x, int k) {
 __device__ __forceinline__ void top_insert(WaveTop& w, float cv, int32_t ci, int k) {
     const int lane = threadIdx.x % kWave;
     const int pos = __popcll(__ballot(ranks_before(w.v, w.i, cv, ci)));
-    const float uv = __shfl_up(w.v, 1, kWave);
-    const int32_t ui = __shfl_up(w.i, 1, kWave);
+    // The entries below the insertion point move down one lane: a DPP
+    // wavefront shift (one VALU op each) rather than an LDS-crossbar shuffle.
+    const float uv = dpp_f32<kDppWaveShr1>(w.v);
+    const int32_t ui = dpp_i32<kDppWaveShr1>(w.i);
     if (lane == pos) {
         w.v = cv;
         w.i = ci;
