@@ -5,13 +5,9 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
-#include "../../include/meshy_amd.h"
+#include "host_common.h"
 
 namespace meshy {
-
-// Records `msg` (printf-style) as the calling thread's last error and returns code.
-int set_error(int code, const char* fmt, ...);
-void clear_error();
 
 // Checks the launch that was just enqueued; maps a HIP error to its positive code.
 int check_launch(const char* what);

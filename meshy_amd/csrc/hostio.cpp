@@ -17,7 +17,7 @@
 #include <thread>
 #include <vector>
 
-#include "common.h"
+#include "host_common.h"
 
 namespace meshy {
 namespace {

@@ -14,7 +14,7 @@
 #include <new>
 #include <vector>
 
-#include "common.h"
+#include "host_common.h"
 
 namespace {
 
