@@ -350,3 +350,43 @@ def test_whiten_flat_more_elements_than_one_grid_pass(dev):
     assert abs(w.mean().item()) <= 1e-5
     assert abs(w.var().item() - var / (var + 1e-8)) <= 1e-4
     assert a[m == 0].abs().max().item() == 0.0
+
+
+def _unaligned(x, dev):
+    """The same values in a device view that starts one element past a 16-byte boundary."""
+    buf = torch.empty(x.numel() + 1, dtype=x.dtype, device=dev)
+    buf[1:] = x.reshape(-1).to(dev)
+    return buf[1:].view(x.shape)
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_vector_and_scalar_loads_and_renamed_ids_give_bitwise_equal_results(dev, bf16):
+    """Aligned inputs (16-byte loads) and unaligned views (one element at a
+    time) build the same maps, so bitwise equal advantages and returns.  The
+    ids enter only through equality and the lambda lookup, so ids spread 40000
+    apart with the lengths moved along give the same results too."""
+    from meshy_amd.gae import gae_and_returns
+
+    rewards, values, mask, doc_ids, n_docs = _random_grid(3, 20000, 7, seed=5)
+    values = values.to(torch.bfloat16) if bf16 else values
+    g = torch.Generator().manual_seed(6)
+    lengths = torch.rand(n_docs, generator=g) * 500 + 1
+    kw = dict(gamma=0.99, alpha=1.5)
+    d = [t.to(dev) for t in (rewards, values, mask, doc_ids)]
+    a0, r0, _ = gae_and_returns(*d, n_docs, lengths=lengths.to(dev), **kw)
+    u = [_unaligned(t, dev) for t in (rewards, values, mask, doc_ids)]
+    assert all(t.data_ptr() % 16 for t in u)
+    a1, r1, _ = gae_and_returns(*u, n_docs, lengths=lengths.to(dev), **kw)
+    spread = 40000
+    far_lengths = torch.ones(n_docs * spread)
+    far_lengths[torch.arange(n_docs) * spread] = lengths
+    a2, r2, _ = gae_and_returns(d[0], d[1], d[2], d[3] * spread, n_docs * spread, lengths=far_lengths.to(dev), **kw)
+    for a, r in ((a1, r1), (a2, r2)):
+        assert torch.equal(a, a0) and torch.equal(r, r0)
+    ref_adv, _ = ogae.compute_vapo_gae(rewards, values.float(), mask, doc_ids, n_docs, lengths=lengths, **kw)
+    assert (a0.cpu() - ref_adv).abs().max().item() <= TOL
+    # Negative ids (lambda 0 there): the vector and scalar loads agree.
+    neg = d[3] - 3
+    a3, r3, _ = gae_and_returns(d[0], d[1], d[2], neg, n_docs, lengths=lengths.to(dev), **kw)
+    a4, r4, _ = gae_and_returns(*u[:3], _unaligned(neg, dev), n_docs, lengths=lengths.to(dev), **kw)
+    assert torch.equal(a3, a4) and torch.equal(r3, r4)
