@@ -397,6 +397,20 @@ def bench_pack(runs, no_cpu):
         lambda: held.__setitem__("b", build_micro_batches(local_t, micros, layout="packed", device=dev,
                                                           need_rollout_lp=True)),
         runs, warmup=2, before=lambda: held.pop("b", None)), 1)
+    # The OPD student's drop-in (opd.py:141-148): the same micros with the
+    # Teacher's K = 8 int64 ids and fp32 log-probs per position.
+    from meshy_amd.opd import build_topk_micro_batches
+
+    gen = torch.Generator().manual_seed(8)
+    for s in samples_t:
+        L = s["tokens"].shape[0]
+        s["teacher_topk_ids"] = torch.randint(0, 151936, (L, 8), generator=gen)
+        s["teacher_topk_logprobs"] = -torch.rand(L, 8, generator=gen)
+    out["build_topk_micro_batches_from_samples_us"] = round(1e3 * _wall_ms(
+        lambda: held.__setitem__("b", build_topk_micro_batches(local_t, micros, layout="packed", device=dev,
+                                                               need_rollout_lp=True)),
+        runs, warmup=2, before=lambda: held.pop("b", None)), 1)
+    held.clear()
     if not no_cpu:
         from oracle import batch as obatch
         from oracle import grpo as ogrpo

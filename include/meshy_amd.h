@@ -169,10 +169,12 @@ typedef struct meshy_pack_args {
        by logits position, NOT shifted; zero outside the documents.  Off
        when teacher_k == 0. */
     int64_t teacher_k;
-    const int32_t* teacher_ids;    /* [total, teacher_k], like tokens         */
+    const void* teacher_ids;       /* [total, teacher_k], int32 or int64      */
     const float* teacher_lps;      /* [total, teacher_k]                      */
     int64_t* teacher_ids_out;      /* [n_out, teacher_k]                      */
     float* teacher_lps_out;        /* [n_out, teacher_k]                      */
+    int32_t teacher_ids_elem_bytes; /* 4 or 8 (0 reads as 4)                  */
+    int32_t reserved_t;
 } meshy_pack_args;
 
 int meshy_pack_micro_batches(const meshy_pack_args* args, hipStream_t stream);

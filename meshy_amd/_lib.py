@@ -100,6 +100,8 @@ class PackArgs(ctypes.Structure):
         ("teacher_lps", c_void_p),
         ("teacher_ids_out", c_void_p),
         ("teacher_lps_out", c_void_p),
+        ("teacher_ids_elem_bytes", c_int32),
+        ("reserved_t", c_int32),
     ]
 
 
@@ -300,7 +302,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 3
+ABI_VERSION = 4
 
 _LIB: ctypes.CDLL | None = None
 

@@ -234,7 +234,7 @@ def stage_micro_batches(
     s_off = np.zeros(n_s + 1, np.int64)
     np.cumsum(need_len, out=s_off[1:])
     total = int(s_off[-1])
-    teacher_k = _teacher_width(samples, used, need_len) if teacher else 0
+    teacher_k, teacher_ids64 = _teacher_width(samples, used, need_len) if teacher else (0, False)
 
     # Plan tables.
     n_micro = len(micros)
@@ -284,7 +284,8 @@ def stage_micro_batches(
     lay.add("doc_sample", max(n_docs_total, 1), torch.int32)
     lay.add("pos_w", max(n_docs_total, 1), torch.float32)
     if teacher_k:
-        lay.add("teacher_ids", total * teacher_k, torch.int32)
+        # int64 ids (the Teacher's dtype) are staged as they are.
+        lay.add("teacher_ids", total * teacher_k, torch.int64 if teacher_ids64 else torch.int32)
         lay.add("teacher_lps", total * teacher_k, torch.float32)
 
     stage = _STAGING.setdefault(device.index or 0, _Staging())
@@ -296,8 +297,8 @@ def stage_micro_batches(
         if need_rollout_lp:
             gather_into(lp_parts, lay.view(host, "logprobs"))
         if teacher_k:
-            gather_into([s[TEACHER_FIELDS[0]][:L] for s, L in zip(srcs, need_len)], lay.view(host, "teacher_ids"))
-            gather_into([s[TEACHER_FIELDS[1]][:L] for s, L in zip(srcs, need_len)], lay.view(host, "teacher_lps"))
+            gather_into([_head(s[TEACHER_FIELDS[0]], L) for s, L in zip(srcs, need_len)], lay.view(host, "teacher_ids"))
+            gather_into([_head(s[TEACHER_FIELDS[1]], L) for s, L in zip(srcs, need_len)], lay.view(host, "teacher_lps"))
         if per_token_adv and adv_dev is None:
             parts = []
             for s, L in zip(srcs, need_len):
@@ -328,10 +329,11 @@ def stage_micro_batches(
     )
 
 
-def _teacher_width(samples, used, need_len) -> int:
-    """Top-K width of the used samples' Teacher columns; checks they cover the micros
-    (opd.py:39-55)."""
+def _teacher_width(samples, used, need_len) -> tuple[int, bool]:
+    """Top-K width of the used samples' Teacher columns, and whether all their ids
+    are int64; checks they cover the micros (opd.py:39-55)."""
     k = 0
+    ids64 = True
     for i, L in zip(used, need_len):
         td = samples[i]
         ids, lps = td[TEACHER_FIELDS[0]], td[TEACHER_FIELDS[1]]
@@ -344,7 +346,8 @@ def _teacher_width(samples, used, need_len) -> int:
         if k and width != k:
             raise ValueError(f"Teacher Top-K widths differ across samples ({k} vs {width})")
         k = width
-    return k
+        ids64 = ids64 and isinstance(ids, torch.Tensor) and ids.dtype == torch.int64
+    return k, ids64
 
 
 def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
@@ -405,6 +408,7 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
         t_lps = torch.empty(n_out * K, dtype=torch.float32, device=device)
         a.teacher_k = K
         a.teacher_ids = lay.view(dbuf, "teacher_ids").data_ptr()
+        a.teacher_ids_elem_bytes = lay.regions["teacher_ids"][2].itemsize
         a.teacher_lps = lay.view(dbuf, "teacher_lps").data_ptr()
         a.teacher_ids_out = t_ids.data_ptr()
         a.teacher_lps_out = t_lps.data_ptr()

@@ -167,8 +167,12 @@ __global__ __launch_bounds__(kFillThreads) void k_pack_fill(meshy_pack_args a) {
             const int64_t K = a.teacher_k;
             int64_t* ids_o = a.teacher_ids_out + o * K;
             float* lps_o = a.teacher_lps_out + o * K;
+            const bool ids64 = a.teacher_ids_elem_bytes == 8;  // uniform over the launch
             for (int64_t j = 0; j < K; ++j) {
-                ids_o[j] = src >= 0 ? static_cast<int64_t>(a.teacher_ids[src * K + j]) : 0;
+                const int64_t at = src * K + j;
+                ids_o[j] = src < 0 ? 0
+                           : ids64 ? static_cast<const int64_t*>(a.teacher_ids)[at]
+                                   : static_cast<int64_t>(static_cast<const int32_t*>(a.teacher_ids)[at]);
                 lps_o[j] = src >= 0 ? a.teacher_lps[src * K + j] : 0.f;
             }
         }
@@ -234,6 +238,8 @@ extern "C" int meshy_pack_micro_batches(const meshy_pack_args* args, hipStream_t
                          static_cast<long long>(a.max_micro_elems));
     if (a.n_micro > 65535) return set_error(MESHY_EINVAL, "meshy_pack_micro_batches: too many micros");
     if (a.teacher_k < 0) return set_error(MESHY_EINVAL, "meshy_pack_micro_batches: negative teacher_k");
+    if (a.teacher_ids_elem_bytes != 0 && a.teacher_ids_elem_bytes != 4 && a.teacher_ids_elem_bytes != 8)
+        return set_error(MESHY_EINVAL, "meshy_pack_micro_batches: teacher ids must be int32 or int64");
     if (a.teacher_k > 0 && (!a.teacher_ids_out || !a.teacher_lps_out ||
                             (a.max_docs_per_micro > 0 && (!a.teacher_ids || !a.teacher_lps))))
         return set_error(MESHY_ENULL, "meshy_pack_micro_batches: teacher columns need inputs and outputs");

@@ -96,6 +96,10 @@ def test_struct_entry_points_reject():
     p.max_micro_elems = 16
     assert lib.meshy_pack_micro_batches(ctypes.byref(p), None) == EINVAL
     assert b"teacher_k" in lib.meshy_last_error()
+    p.teacher_k, p.teacher_ids_elem_bytes = 0, 2
+    assert lib.meshy_pack_micro_batches(ctypes.byref(p), None) == EINVAL
+    assert b"int32 or int64" in lib.meshy_last_error()
+    p.teacher_ids_elem_bytes = 0
     g = _lib.PpoArgs()
     g.n_tokens = -1
     assert lib.meshy_ppo_loss_fwd(ctypes.byref(g), FAKE, None, None) == EINVAL

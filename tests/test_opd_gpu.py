@@ -235,13 +235,17 @@ def _opd_sample(L, K, seed, V=1000):
     }
 
 
+@pytest.mark.parametrize("ids_dtype", [torch.int64, torch.int32])
 @pytest.mark.parametrize("layout", ["padded", "packed"])
-def test_teacher_layout_matches_oracle(dev, layout):
+def test_teacher_layout_matches_oracle(dev, layout, ids_dtype):
+    """Teacher ids staged as they come (int64, the Teacher's dtype) or as int32."""
     from meshy_amd import opd
     from meshy_amd.plan import MicroPlan
 
     K = 8
     samples = [_opd_sample(L, K, i) for i, L in enumerate([37, 64, 5, 120, 90])]
+    for s in samples:
+        s["teacher_topk_ids"] = s["teacher_topk_ids"].to(ids_dtype)
     micros = [MicroPlan((1, 0, 2), 128 if layout == "packed" else 64, (64, 37, 5)),
               MicroPlan((3, 4), 256 if layout == "packed" else 120, (120, 60)),  # sample 4 truncated
               MicroPlan((), 64, ())]  # filler
@@ -253,7 +257,7 @@ def test_teacher_layout_matches_oracle(dev, layout):
     ids, lps = opd.layout_teacher_topk(samples, micros[0], layout=layout, device=dev)
     back = opd.split_teacher_topk(ids, micros[0], layout=layout)
     for j, i in enumerate(micros[0].sample_idx):
-        assert torch.equal(back[j].cpu(), samples[i]["teacher_topk_ids"][:micros[0].doc_lens[j]])
+        assert torch.equal(back[j].cpu(), samples[i]["teacher_topk_ids"][:micros[0].doc_lens[j]].long())
 
 
 def test_teacher_layout_short_rows_raise(dev):
