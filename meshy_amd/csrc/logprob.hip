@@ -60,7 +60,7 @@ __device__ __forceinline__ void finish_row(int64_t r, float m, float s, float t,
     }
     if (n_ids > 1 && logp) {
         __syncthreads();
-        if (threadIdx.x < n_ids) logp[r * n_ids + threadIdx.x] = id_logp(y, zy, s_lse, V);
+        if (static_cast<int>(threadIdx.x) < n_ids) logp[r * n_ids + threadIdx.x] = id_logp(y, zy, s_lse, V);
     }
 }
 
