@@ -120,7 +120,8 @@ def test_icepop_and_positive_lm_gradient(dev):
     assert float(loss) == pytest.approx(-1., abs=1e-6)
 
 
-def _compare(dev, new, old, mask, doc_ids, adv, n_docs, *, rollout=None, entropy=None, pos_w=None, **cfg):
+def _compare(dev, new, old, mask, doc_ids, adv, n_docs, *, rollout=None, entropy=None, pos_w=None,
+             nonfinite=False, **cfg):
     """Kernel vs oracle: loss, every sum, and d loss / d new."""
     from meshy_amd.batch import Batch
     from meshy_amd.loss import ppo_clip_loss
@@ -154,13 +155,28 @@ def _compare(dev, new, old, mask, doc_ids, adv, n_docs, *, rollout=None, entropy
         entropy=entropy)
     ref_loss.backward()
     assert set(sums) == set(ref_sums)
-    assert abs(loss.item() - ref_loss.item()) <= TOL
+
+    def same(a, b, scale):
+        # NaN where torch gives NaN, the same infinity where it gives one.
+        if math.isnan(b):
+            return math.isnan(a)
+        if math.isinf(b):
+            return a == b
+        return abs(a - b) <= TOL * scale
+
+    assert same(loss.item(), ref_loss.item(), 1.0), (loss.item(), ref_loss.item())
     for k in ref_sums:
         # 1e-3 absolute for O(1) values, 1e-3 relative for token sums over many tokens.
         a, b = float(sums[k]), float(ref_sums[k])
-        assert abs(a - b) <= TOL * max(1.0, abs(b)), k
-    g = nd.grad.cpu()
-    assert (g - nr.grad).abs().max().item() <= TOL * max(1e-6, nr.grad.abs().max().item())
+        assert same(a, b, max(1.0, abs(b)) if math.isfinite(b) else 1.0), (k, a, b)
+    g, rg = nd.grad.cpu(), nr.grad
+    finite = torch.isfinite(new) & torch.isfinite(old)  # gradients compared where the inputs are finite
+    if nonfinite:
+        g, rg = g[finite], rg[finite]
+        assert torch.equal(torch.isnan(g), torch.isnan(rg))
+        keep = ~torch.isnan(rg)
+        g, rg = g[keep], rg[keep]
+    assert (g - rg).abs().max().item() <= TOL * max(1e-6, rg.abs().max().item())
     return loss, sums
 
 
@@ -192,6 +208,30 @@ def _random_packed(n_docs, seed, max_len=300, pad=17):
 def test_matches_oracle_packed(dev, variant):
     new, old, mask, doc_ids, adv, roll, ent, posw = _random_packed(37, seed=len(str(variant)))
     _compare(dev, new, old, mask, doc_ids, adv, 37, rollout=roll, entropy=ent, pos_w=posw, **variant)
+
+
+@pytest.mark.parametrize("case", ["nan_new_masked", "inf_ratio_pos_adv", "inf_ratio_neg_adv", "neg_inf_new_masked"])
+@pytest.mark.parametrize("per_token_loss", [True, False])
+def test_non_finite_inputs_propagate_like_torch(dev, case, per_token_loss):
+    """IEEE semantics as torch has them: a NaN at a masked token still gives a
+    NaN loss (NaN * 0), an infinite ratio is clipped to a finite term for a
+    positive advantage and an infinite one for a negative advantage, and every
+    diagnostic follows (inf * 0 = NaN in the masked sums, inf / inf in ESS)."""
+    new, old, mask, doc_ids, adv, roll, ent, posw = _random_packed(9, seed=3)
+    ids = doc_ids.reshape(-1)
+    tok = int((ids == 4).nonzero()[3])
+    if case == "nan_new_masked":
+        mask[0, tok] = 0.0
+        new[0, tok] = float("nan")
+    elif case in ("inf_ratio_pos_adv", "inf_ratio_neg_adv"):
+        mask[0, tok] = 1.0
+        old[0, tok] = float("-inf")
+        adv[4] = 0.7 if case == "inf_ratio_pos_adv" else -0.7
+    else:
+        mask[0, tok] = 0.0
+        new[0, tok] = float("-inf")
+    _compare(dev, new, old, mask, doc_ids, adv, 9, rollout=roll, entropy=ent, nonfinite=True,
+             per_token_loss=per_token_loss)
 
 
 def test_per_token_advantages_padded_rows(dev):
@@ -342,4 +382,4 @@ def test_segment_offsets_cache_follows_doc_ids(dev):
                                 mb.doc_ids.cpu(), mb.advantages.cpu(), 1, n_docs_global=1,
                                 n_tokens_global=mini.n_tokens_global, clip_low=0.2, clip_high=0.28,
                                 per_token_loss=True, use_tis=True, tis_min=0.5, tis_max=5.0)
-    assert abs(float(loss) - float(ref)) <= TOL
+    assert abs(float(loss.detach()) - float(ref.detach())) <= TOL
