@@ -148,7 +148,9 @@ __device__ __forceinline__ void write_top(const WaveTop& w, float m, float s, in
                                           int64_t* __restrict__ ids, float* __restrict__ lps,
                                           float* __restrict__ lse_out) {
     if (threadIdx.x >= kWave) return;
-    const float lse0 = fmaf(__log2f(s), kLn2, m);
+    // torch.logsumexp of a row whose max is +inf is +inf (its candidates' log-probs
+    // are then NaN for the +inf logit and -inf for finite ones); s is NaN there.
+    const float lse0 = (m == __builtin_inff()) ? m : fmaf(__log2f(s), kLn2, m);
     const float lse = read_lane(lse0, 0);
     const int lane = threadIdx.x;
     if (lane == 0 && lse_out) lse_out[r] = lse;

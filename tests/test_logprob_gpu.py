@@ -118,6 +118,30 @@ def test_running_max_raised_in_later_tiles(dev, pattern):
     _check(z.to(torch.bfloat16), y, dev, ref_dtype=torch.float64)
 
 
+def test_non_finite_logits_propagate_like_torch(dev):
+    """cross_entropy's log_softmax and the entropy formula on rows with +inf
+    (label elsewhere and at the +inf), NaN, all -inf, and a -inf label:
+    NaN wherever torch gives NaN, the same infinities, the rest within TOL."""
+    from meshy_amd import logprob
+
+    g = torch.Generator().manual_seed(9)
+    z = torch.randn(1, 6, 1000, generator=g)
+    z[0, 0, 3] = float("inf")
+    z[0, 1, 3] = float("inf")
+    z[0, 2, 500] = float("nan")
+    z[0, 3, :] = float("-inf")
+    z[0, 4, 7] = float("-inf")
+    y = torch.tensor([[0, 3, 0, 0, 7, 1]])
+    zb = z.to(torch.bfloat16)
+    lp, ent = logprob.logprobs_and_entropy(zb.to(dev), y.to(dev), with_entropy=True)
+    for got, want in ((lp.cpu(), olp.chunk_logprobs(zb, y)), (ent.cpu(), olp.chunk_entropy(zb))):
+        assert torch.equal(torch.isnan(got), torch.isnan(want)), (got, want)
+        inf = torch.isinf(want)
+        assert torch.equal(got[inf], want[inf])
+        fin = torch.isfinite(want)
+        assert (got[fin] - want[fin]).abs().max().item() <= TOL
+
+
 def test_deterministic(dev):
     from meshy_amd import logprob
 

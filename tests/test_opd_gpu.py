@@ -73,6 +73,28 @@ def test_topk_nan_and_inf(dev):
     assert torch.equal(ids[:, 2:], rids)
 
 
+def test_topk_row_with_plus_inf_matches_logsumexp(dev):
+    """A row whose max is +inf: torch.logsumexp is +inf, so the reference's
+    candidates get NaN (the +inf logit) and -inf (finite ones)."""
+    from meshy_amd import topk
+
+    g = torch.Generator().manual_seed(4)
+    z = torch.randn(1, 3, 300, generator=g)
+    z[0, 0, 17] = float("inf")
+    z[0, 2, 250] = float("inf")
+    z[0, 2, 3] = float("inf")   # two: the smaller index ranks first
+    zb = z.to(torch.bfloat16)
+    ids, lps = topk.teacher_topk(zb.to(dev), k=4)
+    rids, rlps = otopk.teacher_topk(zb, 4)
+    assert torch.equal(ids.cpu(), rids)
+    got = lps.cpu()
+    assert torch.equal(torch.isnan(got), torch.isnan(rlps))
+    inf = torch.isinf(rlps)
+    assert inf[0, 0, 1:].all() and inf[0, 2, 2:].all() and torch.equal(got[inf], rlps[inf])
+    fin = torch.isfinite(rlps)
+    assert (got[fin] - rlps[fin]).abs().max().item() <= TOL
+
+
 def test_topk_full_size_rows_subset(dev):
     """[16384, 151936] bf16, K = 8: a row subset against the
     oracle, size-independent properties on every row."""
