@@ -71,10 +71,14 @@ class _FusedLogprob(torch.autograd.Function):
         ctx.save_for_backward(logits, labels, lse)
         if ent is not None:
             ctx.mark_non_differentiable(ent)
+        # The backward reads only logp's gradient: no zero tensor for the entropy's.
+        ctx.set_materialize_grads(False)
         return logp, ent
 
     @staticmethod
     def backward(ctx, grad_logp, grad_ent):
+        if grad_logp is None:
+            return None, None, None
         logits, labels, lse = ctx.saved_tensors
         rows, T, V = logits.shape
         grad = torch.empty(rows, T, V, dtype=logits.dtype, device=logits.device)

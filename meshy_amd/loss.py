@@ -150,10 +150,14 @@ class _PPOLoss(torch.autograd.Function):
         ctx.save_for_backward(new_flat, seg_cnt)
         loss = out[1].clone()
         ctx.mark_non_differentiable(out)
+        # The backward reads only the loss's gradient: no zero tensor for `out`'s.
+        ctx.set_materialize_grads(False)
         return loss, out
 
     @staticmethod
     def backward(ctx, grad_loss, grad_out):
+        if grad_loss is None:
+            return None, None
         new_flat, seg_cnt = ctx.saved_tensors
         inputs: _Inputs = ctx.inputs
         g = grad_loss.reshape(1).to(torch.float32).contiguous()

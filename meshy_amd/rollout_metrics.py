@@ -44,20 +44,41 @@ def _get(sample: Any, f: str) -> Any:
     return sample.get(f, None) if hasattr(sample, "get") else getattr(sample, f, None)
 
 
-def _scalars(samples, columns, f: str) -> list[float]:
-    """Per-sample values of a scalar column (the samples that carry one)."""
+# Every per-sample field the statistics read.
+_FIELDS = ("reward", "raw_reward", "advantage", "weight_version", "truncated", "repetition", "mixed_version",
+           "tokens", "mask_assistant", "masks", "logprobs")
+
+
+def _per_sample(samples) -> dict[str, list]:
+    """One list per field of the samples' values (None where a sample lacks the
+    field), read in a single pass over the samples."""
+    lists = tuple([] for _ in _FIELDS)
+    pairs = tuple(zip(_FIELDS, lists))
+    for s in samples:
+        if isinstance(s, dict):
+            for f, out in pairs:
+                out.append(s.get(f))
+        else:
+            for f, out in pairs:
+                out.append(_get(s, f))
+    return dict(pairs)
+
+
+def _scalars(per, columns, f: str) -> list[float]:
+    """Per-sample values of a scalar column (the samples that carry one);
+    ``per`` is ``_per_sample``'s lists when the input is a sample list."""
     if columns is not None:
         v = columns.get(f)
         if v is None:
             return []
         return [float(x) for x in (v.reshape(-1).tolist() if isinstance(v, torch.Tensor) else v)]
-    present = [v for v in (_get(s, f) for s in samples) if v is not None]
-    if (present and all(torch.is_tensor(v) and v.dim() == 0 for v in present)
-            and len({(v.dtype, v.device) for v in present}) == 1):
+    present = [v for v in per[f] if v is not None]
+    if present and all(torch.is_tensor(v) for v in present) and len({v.dtype for v in present}) == 1:
         # One stack and one host copy instead of one per sample (one dtype, so
-        # nothing is promoted or rounded).
+        # nothing is promoted or rounded; equal shapes flatten in sample order,
+        # as the per-sample path below does).  Mixed devices or shapes raise.
         try:
-            return [float(x) for x in torch.stack([v.detach() for v in present]).cpu().tolist()]
+            return [float(x) for x in torch.stack(present).detach().reshape(-1).cpu().tolist()]
         except RuntimeError:
             pass  # mixed devices or dtypes torch cannot stack: the general path below
     out = []
@@ -71,14 +92,35 @@ def _scalars(samples, columns, f: str) -> list[float]:
     return out
 
 
-def _flags(samples, columns, n: int, f: str) -> list[float] | None:
-    values = _scalars(samples, columns, f)
+def _flags(per, columns, n: int, f: str) -> list[float] | None:
+    values = _scalars(per, columns, f)
     if len(values) != n:
         return None
     return [1.0 if v > 0.5 else 0.0 for v in values]
 
 
-def _token_stats(samples, columns, device):
+def _flat(col) -> tuple[torch.Tensor, torch.Tensor]:
+    """(flat values, int64 offsets [B + 1]) of a jagged column, or of a list of
+    per-sample values where None is an empty sample."""
+    if isinstance(col, torch.Tensor):
+        return jagged_parts(col)
+    present = [v for v in col if v is not None]
+    if (present and all(torch.is_tensor(v) and v.dim() == 1 for v in present)
+            and len({v.dtype for v in present}) == 1):
+        # One concatenation in the samples' own dtype, converted once later.
+        try:
+            flat = torch.cat(present).detach()
+        except RuntimeError:
+            flat = None  # mixed devices: the per-sample path
+        if flat is not None:
+            lengths = torch.tensor([0 if v is None else v.shape[0] for v in col], dtype=torch.int64)
+            off = torch.zeros(len(col) + 1, dtype=torch.int64)
+            torch.cumsum(lengths, 0, out=off[1:])
+            return flat, off
+    return jagged_parts([torch.zeros(0) if v is None else _as_float(v) for v in col])
+
+
+def _token_stats(per, columns, device):
     """Per-sample total and response lengths and the kept log-probs (device),
     with the reference's presence rules (metrics.py:197-212): a length per sample
     with tokens, a response length per sample with a mask, log-probs kept where
@@ -90,31 +132,24 @@ def _token_stats(samples, columns, device):
         lengths = [] if tok is None else [float(x) for x in torch.diff(jagged_parts(tok)[1]).tolist() if x > 0]
         has_mask = None if mask_col is None else [True] * (jagged_parts(mask_col)[1].numel() - 1)
     else:
-        lengths = []
-        for smp in samples:
-            t = _get(smp, "tokens")
-            if t is not None and len(t) > 0:
-                lengths.append(float(len(t)))
-        masks = []
-        for smp in samples:
-            mk = _get(smp, "mask_assistant")
-            masks.append(_get(smp, "masks") if mk is None else mk)
+        lengths = [float(len(t)) for t in per["tokens"] if t is not None and len(t) > 0]
+        masks = [ms if mk is None else mk for mk, ms in zip(per["mask_assistant"], per["masks"])]
         has_mask = [mk is not None for mk in masks]
-        mask_col = None if not any(has_mask) else [torch.zeros(0) if mk is None else _as_float(mk) for mk in masks]
-        lps = [_get(smp, "logprobs") for smp in samples]
-        lp_col = None if all(v is None for v in lps) else [torch.zeros(0) if v is None else _as_float(v) for v in lps]
+        mask_col = masks if any(has_mask) else None
+        lps = per["logprobs"]
+        lp_col = None if all(v is None for v in lps) else lps
     if mask_col is None and lp_col is None:
         return lengths, [], None
     if mask_col is not None:
-        mflat, moff = jagged_parts(mask_col)
+        mflat, moff = _flat(mask_col)
     else:
-        mflat, moff = torch.zeros(0), torch.zeros(len(samples) + 1, dtype=torch.int64)
+        mflat, moff = torch.zeros(0), torch.zeros(len(per["tokens"]) + 1, dtype=torch.int64)
     nsamp = moff.numel() - 1
     mflat = mflat.to(device=device, dtype=torch.float32).contiguous()
     moff_d = moff.to(device)
     lflat = loff_d = None
     if lp_col is not None:
-        lflat, loff = jagged_parts(lp_col)
+        lflat, loff = _flat(lp_col)
         lflat = lflat.to(device=device, dtype=torch.float32).contiguous()
         loff_d = loff.to(device)
     resp = torch.empty(max(nsamp, 1), dtype=torch.int64, device=device)
@@ -155,13 +190,14 @@ def rollout_metrics(samples: Any, seq_len: int, current_version: int | None = No
         n = len(samples)
     if device is None:
         device = torch.device("cuda", torch.cuda.current_device())
-    rewards = _scalars(samples, columns, "reward")
-    raw = _scalars(samples, columns, "raw_reward")
+    per = None if columns is not None else _per_sample(samples)
+    rewards = _scalars(per, columns, "reward")
+    raw = _scalars(per, columns, "raw_reward")
     raw_rewards = raw or rewards
     shaped = bool(raw)
-    advantages = _scalars(samples, columns, "advantage")
-    weight_versions = _scalars(samples, columns, "weight_version")
-    lengths, response_lengths, lp = _token_stats(samples, columns, torch.device(device))
+    advantages = _scalars(per, columns, "advantage")
+    weight_versions = _scalars(per, columns, "weight_version")
+    lengths, response_lengths, lp = _token_stats(per, columns, torch.device(device))
 
     m: dict[str, float] = {}
     if response_lengths:
@@ -182,11 +218,11 @@ def rollout_metrics(samples: Any, seq_len: int, current_version: int | None = No
     if lengths:
         m["rollout/total_lengths"] = _mean(lengths)
         m["rollout/seq_len_truncated_ratio"] = sum(v >= seq_len for v in lengths) / len(lengths)
-    truncated = _flags(samples, columns, n, "truncated")
+    truncated = _flags(per, columns, n, "truncated")
     if truncated is not None:
         m["rollout/truncated_ratio"] = _mean(truncated)
         m["rollout/truncated"] = m["rollout/truncated_ratio"]
-    repetition = _flags(samples, columns, n, "repetition")
+    repetition = _flags(per, columns, n, "repetition")
     if repetition is not None:
         m["rollout/repetition_frac"] = _mean(repetition)
     if advantages:
@@ -236,7 +272,7 @@ def rollout_metrics(samples: Any, seq_len: int, current_version: int | None = No
             staleness = [float(current_version) - v for v in weight_versions]
             m["rollout/weight_version/staleness_mean"] = _mean(staleness)
             m["rollout/weight_version/staleness_max"] = max(staleness)
-    mixed = _flags(samples, columns, n, "mixed_version")
+    mixed = _flags(per, columns, n, "mixed_version")
     if mixed is not None:
         m["rollout/weight_version/mixed_version_ratio"] = _mean(mixed)
 
