@@ -507,14 +507,14 @@ __device__ __forceinline__ float token_grad_v(const meshy_ppo_args& a, const Tok
     return gn;
 }
 
-__device__ __forceinline__ float doc_scale(const meshy_ppo_args& a, const float* seg_cnt, int64_t d) {
-    if (d >= a.n_docs) return 0.f;  // the padding slot is not in the loss
-    return a.per_token_loss ? 1.f / static_cast<float>(max<int64_t>(1, a.n_tokens_global))
-                            : 1.f / (fmaxf(seg_cnt[d], 1.f) * static_cast<float>(max<int64_t>(1, a.n_docs_global)));
-}
+constexpr int kBwdItems = 4;  // tokens per thread of k_ppo_bwd, strided by the workgroup (fastest of 2, 4, 8, 16)
 
-constexpr int kBwdItems = 8;  // tokens per thread of k_ppo_bwd, strided by the workgroup
-
+// Three phases per thread: every token's inputs, then every token's document
+// factors, then the arithmetic and the stores.  All loads take indices that are
+// valid for every lane (token 0 past the end; the document clamped into the
+// per-document arrays, whose value is dropped for the padding slot), so none
+// sits behind a per-lane branch, which would wait for each load in turn.  The
+// entropy is not read: the gradient does not depend on it.
 __global__ __launch_bounds__(kThreads) void k_ppo_bwd(meshy_ppo_args a, const float* __restrict__ seg_cnt,
                                                       const float* __restrict__ grad_loss,
                                                       float* __restrict__ grad_new) {
@@ -525,18 +525,36 @@ __global__ __launch_bounds__(kThreads) void k_ppo_bwd(meshy_ppo_args a, const fl
 #pragma unroll
     for (int q = 0; q < kBwdItems; ++q) {
         const int64_t i = t0 + q * kThreads;
-        const bool ok = i < a.n_tokens;
-        in[q] = load_tok(a, i, ok);
-        d[q] = doc_at(a, ok ? i : 0);
+        const int64_t j = i < a.n_tokens ? i : 0;
+        in[q].nw = a.new_lp[j];
+        in[q].ol = a.old_lp[j];
+        in[q].mk = a.mask[j];
+        in[q].ro = a.use_icepop ? a.rollout_lp[j] : 0.f;
+        in[q].en = 0.f;
+        in[q].ad = a.adv_per_token ? a.adv[j] : 0.f;
+        d[q] = doc_at(a, j);
     }
+    const bool have_docs = a.n_docs > 0;
+    const int64_t last = have_docs ? a.n_docs - 1 : 0;
+    float A[kBwdItems], W[kBwdItems], C[kBwdItems];
+#pragma unroll
+    for (int q = 0; q < kBwdItems; ++q) {
+        const int64_t dc = min(d[q], last);
+        A[q] = (have_docs && !a.adv_per_token) ? a.adv[dc] : 0.f;
+        W[q] = (have_docs && a.positive_lm_weights) ? a.positive_lm_weights[dc] : 0.f;
+        C[q] = (have_docs && !a.per_token_loss) ? seg_cnt[dc] : 0.f;
+    }
+    const float tok_scale = 1.f / static_cast<float>(max<int64_t>(1, a.n_tokens_global));
+    const float docs_g = static_cast<float>(max<int64_t>(1, a.n_docs_global));
 #pragma unroll
     for (int q = 0; q < kBwdItems; ++q) {
         const int64_t i = t0 + q * kThreads;
-        if (i >= a.n_tokens) break;
-        const bool real = d[q] < a.n_docs;
-        const float A = a.adv_per_token ? in[q].ad : (real ? a.adv[d[q]] : 0.f);
-        const float W = (a.positive_lm_weights && real) ? a.positive_lm_weights[d[q]] : 0.f;
-        grad_new[i] = token_grad_v(a, in[q], A, W, G * doc_scale(a, seg_cnt, d[q]));
+        const bool real = d[q] < a.n_docs;  // the padding slot is not in the loss
+        const float Aq = a.adv_per_token ? in[q].ad : (real ? A[q] : 0.f);
+        const float Wq = real ? W[q] : 0.f;
+        const float scale = !real ? 0.f : (a.per_token_loss ? tok_scale : 1.f / (fmaxf(C[q], 1.f) * docs_g));
+        const float g = token_grad_v(a, in[q], Aq, Wq, G * scale);
+        if (i < a.n_tokens) grad_new[i] = g;
     }
 }
 
