@@ -234,6 +234,37 @@ def test_non_finite_inputs_propagate_like_torch(dev, case, per_token_loss):
              per_token_loss=per_token_loss)
 
 
+@pytest.mark.parametrize("T", [1, 2, 1023, 1024, 1025, 2047, 2048, 2049, 4097])
+@pytest.mark.parametrize("per_token_loss", [True, False])
+def test_token_counts_around_workgroup_boundaries(dev, T, per_token_loss):
+    """The backward takes 1024 tokens per workgroup and the forward 2048 per
+    tile: counts on either side of both, with the last lanes past the end."""
+    g = torch.Generator().manual_seed(T)
+    n_docs = max(1, min(5, T // 3))
+    cuts = sorted(torch.randperm(max(T - 1, 1), generator=g)[:n_docs - 1].add(1).tolist()) if T > 1 else []
+    doc_ids = torch.zeros(T, dtype=torch.long)
+    for c in cuts:
+        doc_ids[c:] += 1
+    mask = (torch.rand(T, generator=g) > 0.25).float()
+    old = -torch.rand(T, generator=g) * 4
+    new = old + torch.randn(T, generator=g) * 0.3
+    adv = torch.randn(n_docs, generator=g)
+    _compare(dev, new.reshape(1, -1), old.reshape(1, -1), mask.reshape(1, -1), doc_ids.reshape(1, -1), adv, n_docs,
+             per_token_loss=per_token_loss)
+
+
+@pytest.mark.parametrize("per_token_loss", [True, False])
+def test_no_documents_gives_zero_loss_and_gradient(dev, per_token_loss):
+    """Every token in the padding slot (n_docs = 0): loss, sums and gradient are 0."""
+    T = 1500
+    g = torch.Generator().manual_seed(2)
+    old = -torch.rand(1, T, generator=g)
+    new = old + torch.randn(1, T, generator=g) * 0.3
+    loss, sums = _compare(dev, new, old, torch.zeros(1, T), torch.zeros(1, T, dtype=torch.long), torch.zeros(0), 0,
+                          per_token_loss=per_token_loss, n_docs_global=0, n_tokens_global=0)
+    assert loss.item() == 0.0
+
+
 def test_per_token_advantages_padded_rows(dev):
     g = torch.Generator().manual_seed(5)
     rows, S = 6, 700
