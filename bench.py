@@ -1084,8 +1084,10 @@ def main() -> int:
 
 
 def pmc_kernels() -> int:
-    """The dispatches the HBM-traffic counter runs read: each big kernel three
-    times, then a device copy of known size (4,978,638,848 B) to calibrate."""
+    """The dispatches the counter runs read: each big kernel three times (the
+    fused log-prob + entropy, the plain streaming read over the same logits,
+    Top-K, the log-prob backward), then a device copy of known size
+    (4,978,638,848 B) to calibrate."""
     import torch
 
     from meshy_amd import _lib, logprob, topk
@@ -1095,12 +1097,18 @@ def pmc_kernels() -> int:
     z = torch.randn(1, T_TOK, VOCAB, generator=gen, device=dev, dtype=torch.bfloat16) * 2.0
     y = torch.randint(0, VOCAB, (1, T_TOK), generator=gen, device=dev)
     for _ in range(3):
+        logprob.logprobs_and_entropy(z, y, with_entropy=True)
+    lib = _lib.load()
+    sink = torch.zeros(1, dtype=torch.int32, device=dev)
+    for _ in range(3):
+        _lib.check(lib.meshy_stream_read(z.data_ptr(), T_TOK, VOCAB * 2, sink.data_ptr(), _lib.stream_of(dev)),
+                   "meshy_stream_read")
+    for _ in range(3):
         topk.teacher_topk(z, 8)
     lse = logprob.logsumexp_rows(z)
     gl = torch.ones(1, T_TOK, device=dev)
     grad = torch.empty_like(z)
     ws = logprob.bwd_workspace(T_TOK, dev)
-    lib = _lib.load()
     for _ in range(3):
         _lib.check(lib.meshy_logprob_bwd(z.data_ptr(), 1, T_TOK, VOCAB, z.stride(0), z.stride(1), y.data_ptr(),
                                          lse.data_ptr(), gl.data_ptr(), grad.data_ptr(), ws.data_ptr(), ws.numel(),

@@ -64,8 +64,38 @@ __device__ __forceinline__ void finish_row(int64_t r, float m, float s, float t,
     }
 }
 
+// The row's last rem (< NT * GMAX) 16-byte chunks as one tile of
+// G = ceil(rem / NT) loads per thread, all in flight together.
+template <int NT, int G, int GMAX>
+__device__ __forceinline__ void lpe_tail(const v4u* base, int64_t rem, int tid, float& m, float& s, float& t) {
+    if constexpr (G <= GMAX) {
+        if (rem > static_cast<int64_t>(G) * NT) {
+            lpe_tail<NT, G + 1, GMAX>(base, rem, tid, m, s, t);
+            return;
+        }
+        v4u v[G];
+        bool ok[G];
+        load_tail<NT, G>(base, rem, tid, v, ok);
+        float z[G * 8];
+        unpack(v, z);
+        accumulate_masked<true>(z, ok, m, s, t);
+    }
+}
+
+// The exact tile update (tile max, rescale, accumulate) out of line: the rare
+// fallback of accumulate_at, kept from sharing registers with the common path.
+template <int U>
+__device__ __forceinline__ void accumulate_exact(v4u (&v)[U], float& m, float& s, float& t) {
+    float z[U * 8];
+    unpack(v, z);
+    accumulate(z, m, s, t);
+}
+
 // Vector path: row base 16-byte aligned.  NT threads per row, U 16-byte loads
-// in flight per thread per tile.
+// in flight per thread per tile.  A lane's first tile sets its running max;
+// later tiles are accumulated against it (accumulate_at) and take the tile
+// max only when an element lies more than 44 above it.  The chunks left after
+// the full tiles form one predicated tile.
 template <int NT, int U>
 __global__ __launch_bounds__(NT) void k_lpe_fwd_vec(const uint16_t* __restrict__ logits, int64_t T,
                                                     int64_t V, int64_t stride_b, int64_t stride_t,
@@ -90,17 +120,16 @@ __global__ __launch_bounds__(NT) void k_lpe_fwd_vec(const uint16_t* __restrict__
         v4u v[U];
 #pragma unroll
         for (int u = 0; u < U; ++u) v[u] = __builtin_nontemporal_load(p + u * NT);
-        float z[U * 8];
-        unpack(v, z);
-        accumulate(z, m, s, t);
+        if (it == 0) {
+            float z[U * 8];
+            unpack(v, z);
+            accumulate(z, m, s, t);
+        } else if (!accumulate_at<true>(v, m, s, t)) {
+            accumulate_exact(v, m, s, t);
+        }
     }
-    // Remaining 16-byte chunks, one at a time.
-    for (int64_t c = n_full * kTile + tid; c < n8; c += NT) {
-        v4u v1[1] = {__builtin_nontemporal_load(row4 + c)};
-        float z[8];
-        unpack(v1, z);
-        accumulate(z, m, s, t);
-    }
+    const int64_t rem = n8 - n_full * kTile;
+    if (rem > 0) lpe_tail<NT, 1, U>(row4 + n_full * kTile, rem, tid, m, s, t);
     // Tail elements when V is not a multiple of 8.
     {
         const int64_t e = (n8 << 3) + tid;

@@ -100,6 +100,83 @@ __device__ __forceinline__ void accumulate(const float (&z)[K], float& m, float&
     accumulate<kEntropy>(z, tile_max(z), m, s, t);
 }
 
+// Accumulates a full tile against the running max m as it stands, without a
+// tile max.  Any reference point gives the same lse and entropy (s and t are
+// both relative to m), so this is exact as long as the sums stay finite: it
+// is taken only when the tile's sum is at most 2^64, i.e. no element exceeds
+// m by more than 64 / log2(e) = 44.4.  Otherwise (and for NaN or infinite
+// inputs) it returns false with (s, t) untouched, and the caller accumulates
+// the tile with its max.  Saves the tile max and the rescale of every tile
+// after a lane's first.
+template <bool kEntropy, int U>
+__device__ __forceinline__ bool accumulate_at(const v4u (&v)[U], float m, float& s, float& t) {
+    const float nm = -m * kLog2e;
+    float s0 = 0.f, s1 = 0.f, t0 = 0.f, t1 = 0.f;
+#pragma unroll
+    for (int u = 0; u < U; ++u) {
+        const uint32_t w[4] = {v[u].x, v[u].y, v[u].z, v[u].w};
+#pragma unroll
+        for (int k = 0; k < 4; ++k) {
+            const float x0 = fmaf(bf16_lo(w[k]), kLog2e, nm);
+            const float x1 = fmaf(bf16_hi(w[k]), kLog2e, nm);
+            const float e0 = fast_exp2(x0);
+            const float e1 = fast_exp2(x1);
+            s0 += e0;
+            s1 += e1;
+            if (kEntropy) {
+                t0 = fmaf(e0, x0, t0);
+                t1 = fmaf(e1, x1, t1);
+            }
+        }
+    }
+    // Both sums are formed before the test and kept or dropped by a select:
+    // a branch around the t update would keep every exp of the tile live.
+    const float st = s0 + s1;
+    const bool ok = st <= 0x1p64f;
+    s = ok ? s + st : s;
+    if (kEntropy) t = ok ? t + (t0 + t1) : t;
+    return ok;
+}
+
+// Accumulates a tile in which only the 8-element groups with ok[g] hold
+// data; the others are ignored whatever their contents.
+template <bool kEntropy, int G>
+__device__ __forceinline__ void accumulate_masked(float (&z)[G * 8], const bool (&ok)[G], float& m, float& s,
+                                                  float& t) {
+#pragma unroll
+    for (int g = 0; g < G; ++g)
+#pragma unroll
+        for (int k = 0; k < 8; ++k) z[8 * g + k] = ok[g] ? z[8 * g + k] : kInit;
+    raise_max(m, s, t, tile_max(z));
+    const float nm = -m * kLog2e;
+    float s0 = 0.f, t0 = 0.f;
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+#pragma unroll
+        for (int k = 0; k < 8; ++k) {
+            const float x = fmaf(z[8 * g + k], kLog2e, nm);
+            const float e = ok[g] ? fast_exp2(x) : 0.f;
+            s0 += e;
+            if (kEntropy) t0 = fmaf(e, x, t0);
+        }
+    }
+    s += s0;
+    if (kEntropy) t += t0;
+}
+
+// Loads the last rem (<= NT * G) 16-byte chunks of a row, starting at base,
+// G per thread, all issued before any is used: thread tid's chunk g is
+// tid + g * NT; past rem it reads chunk 0 instead and its ok flag is false.
+template <int NT, int G>
+__device__ __forceinline__ void load_tail(const v4u* base, int64_t rem, int tid, v4u (&v)[G], bool (&ok)[G]) {
+#pragma unroll
+    for (int g = 0; g < G; ++g) {
+        const int64_t c = tid + static_cast<int64_t>(g) * NT;
+        ok[g] = c < rem;
+        v[g] = __builtin_nontemporal_load(base + (ok[g] ? c : 0));
+    }
+}
+
 // Accumulates one element that may be absent.
 __device__ __forceinline__ void accumulate_one(float z, bool ok, float& m, float& s, float& t) {
     if (!ok) return;
