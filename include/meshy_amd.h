@@ -223,6 +223,23 @@ int meshy_logprob_bwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V
                       const float* lse, const float* grad_logp, uint16_t* grad_logits,
                       void* workspace, size_t workspace_bytes, hipStream_t stream);
 
+/*
+ * Allocation-free variant of meshy_logprob_bwd.  No counterpart in the
+ * reference: it is for callers that cannot allocate device memory or pass a
+ * workspace (code under HIP graph capture, tight training or serving loops,
+ * harnesses that forbid hipMalloc).  Same arguments, kernels and results as
+ * meshy_logprob_bwd; its two floats per row live in a static device array of
+ * MESHY_NOALLOC_MAX_ROWS rows (2 MiB, one copy per GPU, held until the
+ * process ends).  rows * T above that limit returns MESHY_ESPACE.  The call
+ * allocates and frees nothing.  Calls that overlap on one GPU (on different
+ * streams) share that array and race; calls on one stream are ordered.
+ */
+#define MESHY_NOALLOC_MAX_ROWS 262144
+int meshy_logprob_bwd_noalloc(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
+                              int64_t stride_b, int64_t stride_t, const int64_t* labels,
+                              const float* lse, const float* grad_logp, uint16_t* grad_logits,
+                              hipStream_t stream);
+
 /* ------------------------------------------------------------------------
  * log_softmax(logits).gather(ids) over bf16 logits, and its backward (device).
  * Replaces gather_logprobs (meshy/backend/titan/topk_loss.py:40-57) and its

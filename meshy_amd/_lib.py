@@ -241,6 +241,11 @@ SIGNATURES = {
         [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
          c_void_p, c_void_p, c_size_t, c_void_p],
     ),
+    "meshy_logprob_bwd_noalloc": (
+        c_int,
+        [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+         c_void_p, c_void_p],
+    ),
     "meshy_gather_logprobs_fwd": (
         c_int,
         [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_int64, c_void_p,

@@ -20,6 +20,8 @@
 // logits are contiguous: on MI355X that order writes 8 % faster than one
 // workgroup per row.
 #include <algorithm>
+#include <atomic>
+#include <mutex>
 
 #include "rowstream.h"
 
@@ -443,6 +445,76 @@ extern "C" int meshy_logprob_bwd(const uint16_t* logits, int64_t rows, int64_t T
         return set_error(MESHY_ENULL, "%s: labels, lse, grad_logp and grad_logits are required", who);
     return launch_bwd(logits, rows, T, V, stride_b, stride_t, labels, 1, lse, grad_logp, grad_logits, workspace,
                       workspace_bytes, stream, who);
+}
+
+// ------------------------------------------------ allocation-free backward
+//
+// meshy_logprob_bwd_noalloc runs the kernels of meshy_logprob_bwd with their
+// two floats per row (-G and -lse log2 e) in this file-scope device array
+// instead of a caller workspace.  Each GPU holds its own copy; host code
+// reaches it only through the address hipGetSymbolAddress reports for the
+// current device, looked up once per device and cached below.  Nothing in it
+// must start at zero: the prep kernel writes every row's pair before the
+// streaming pass and the fixup read it.  Calls that overlap on one GPU (on
+// different streams) share the array and race.
+static __device__ __align__(256) float scratch[2 * MESHY_NOALLOC_MAX_ROWS];
+
+namespace meshy {
+namespace {
+
+constexpr int kMaxDevices = 64;
+std::atomic<float*> g_scratch[kMaxDevices];
+std::mutex g_scratch_mu;
+
+// The current device's copy of `scratch` (looked up on its first use).
+int scratch_of_current_device(float** out, const char* who) {
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(static_cast<int>(e), "%s: hipGetDevice: %s", who, hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return set_error(MESHY_EINVAL, "%s: device %d out of range", who, dev);
+    float* p = g_scratch[dev].load(std::memory_order_acquire);
+    if (!p) {
+        std::lock_guard<std::mutex> lock(g_scratch_mu);
+        p = g_scratch[dev].load(std::memory_order_relaxed);
+        if (!p) {
+            void* addr = nullptr;
+            e = hipGetSymbolAddress(&addr, HIP_SYMBOL(scratch));
+            if (e != hipSuccess || !addr)
+                return set_error(e != hipSuccess ? static_cast<int>(e) : MESHY_EINVAL,
+                                 "%s: hipGetSymbolAddress(scratch) on device %d: %s", who, dev,
+                                 hipGetErrorString(e));
+            p = static_cast<float*>(addr);
+            g_scratch[dev].store(p, std::memory_order_release);
+        }
+    }
+    *out = p;
+    return MESHY_OK;
+}
+
+}  // namespace
+}  // namespace meshy
+
+extern "C" int meshy_logprob_bwd_noalloc(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
+                                         int64_t stride_b, int64_t stride_t, const int64_t* labels,
+                                         const float* lse, const float* grad_logp, uint16_t* grad_logits,
+                                         hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    const char* who = "meshy_logprob_bwd_noalloc";
+    int rc = check_common(logits, rows, T, V, stride_b, stride_t, who);
+    if (rc) return rc;
+    if (!labels || !lse || !grad_logp || !grad_logits)
+        return set_error(MESHY_ENULL, "%s: labels, lse, grad_logp and grad_logits are required", who);
+    const int64_t n = rows * T;
+    if (n > MESHY_NOALLOC_MAX_ROWS)
+        return set_error(MESHY_ESPACE, "%s: %lld rows exceed the static scratch of %d rows", who,
+                         static_cast<long long>(n), MESHY_NOALLOC_MAX_ROWS);
+    if (n == 0) return MESHY_OK;
+    float* ws = nullptr;
+    rc = scratch_of_current_device(&ws, who);
+    if (rc) return rc;
+    return launch_bwd(logits, rows, T, V, stride_b, stride_t, labels, 1, lse, grad_logp, grad_logits, ws,
+                      bwd_ws_bytes(n), stream, who);
 }
 
 extern "C" int meshy_gather_logprobs_bwd(const uint16_t* logits, int64_t rows, int64_t T, int64_t V,
