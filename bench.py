@@ -17,8 +17,10 @@ already resident in HBM.  Prints ONE JSON line with
 * kernels              per-kernel device time, algorithmic GB/s and the
                        restated CPU path for the 256-sample GRPO batch,
                        the 512-doc PPO batch, 16 long sequences and 1024 GAE docs
-* end_to_end           pack -> logprob+entropy -> GRPO -> PPO fwd+bwd at
-                       T = 16384, GPU wall against the CPU restatement
+* end_to_end           pack + GRPO -> logprob+entropy -> PPO fwd+bwd -> logits
+                       backward at T = 16384, GPU wall against the CPU
+                       restatement, with the largest difference between the
+                       two chains' losses, sums and gradients
 """
 
 from __future__ import annotations
@@ -904,11 +906,15 @@ def bench_rollout_metrics(runs, no_cpu):
 # ---------------------------------------------------------------- end to end
 
 def bench_end_to_end(runs, no_cpu):
-    """The 256 GRPO samples truncated to the micros that fill T=16384 -> pack ->
-    logprob+entropy on [16384, 151936] logits -> GRPO -> PPO fwd+bwd."""
+    """The composed path at T = 16384: the 256 GRPO samples planned and packed
+    (one host-to-device copy, GRPO, every micro), then over the first two
+    micros (8192 tokens each, rows [0, 16384) of one [16384, 151936] bf16
+    logits tensor): fused logprob + entropy, PPO loss forward and backward, and
+    the backward into the logits.  The CPU leg restates the same chain on the
+    oracle; the entry reports both walls and the largest differences between
+    the two chains' outputs."""
     from types import SimpleNamespace as NS
 
-    import numpy as np
     import torch
 
     from meshy_amd import logprob, workloads
@@ -917,18 +923,12 @@ def bench_end_to_end(runs, no_cpu):
     from meshy_amd.plan import PlannerConfig
 
     dev = torch.device("cuda:0")
+    micro = 8192
     batch, rewards, group_offsets = workloads.grpo_256_samples(0)
-    # the first groups whose samples make two full 8192-token micros
-    keep = 0
-    tot = 0
-    while keep < len(batch.lengths) and tot + int(batch.lengths[keep:keep + 8].sum()) <= 2 * 8192 - 2048:
-        tot += int(batch.lengths[keep:keep + 8].sum())
-        keep += 8
-    o = batch.offsets[keep]
-    ragged = RaggedSamples.from_arrays(batch.tokens[:o], batch.mask[:o], batch.logprobs[:o],
-                                       batch.offsets[:keep + 1], rewards[:keep], group_offsets[:keep // 8 + 1])
-    cfg = PlannerConfig(layout="packed", mini_batch_size=keep, seq_len=8192, align=2048,
-                        max_tokens_per_micro=8192)
+    n = len(batch.lengths)
+    ragged = RaggedSamples.from_arrays(batch.tokens, batch.mask, batch.logprobs, batch.offsets, rewards,
+                                       group_offsets)
+    cfg = PlannerConfig(layout="packed", mini_batch_size=n, seq_len=micro, align=2048, max_tokens_per_micro=micro)
     gen = torch.Generator(device=dev).manual_seed(5)
     logits = torch.randn(1, T_TOK, VOCAB, generator=gen, device=dev, dtype=torch.bfloat16) * 2.0
     stub = NS(ppo_clip_eps_low=0.2, ppo_clip_eps_high=0.28, use_tis=False, use_icepop=False,
@@ -938,20 +938,23 @@ def bench_end_to_end(runs, no_cpu):
     def gpu_step():
         res = pack_step(ragged, cfg, dev)
         mini = res.plan.per_rank[0][0]
-        off = 0
-        for mb in res.batches:
-            T = mb.input_ids.shape[1]
-            z = logits[:, off:off + T] if off + T <= T_TOK else logits[:, :T]
-            off += T
+        outs = []
+        for j, mb in enumerate(res.batches[:T_TOK // micro]):
+            if mb.input_ids.shape[1] != micro:
+                raise RuntimeError("the first micros of the 256 GRPO samples are expected to be full")
+            z = logits[:, j * micro:(j + 1) * micro].detach().requires_grad_(True)
             lp, ent = logprob.logprobs_and_entropy(z, mb.labels, with_entropy=True)
-            new = lp.detach().requires_grad_(True)
-            loss, sums = ppo_clip_loss(stub, new, mb.rollout_logprobs, mb, mini, entropy=ent)
+            lp.retain_grad()
+            loss, sums = ppo_clip_loss(stub, lp, mb.rollout_logprobs, mb, mini, entropy=ent)
             loss.backward()
-        info["tokens"] = sum(mb.input_ids.shape[1] for mb in res.batches)
+            outs.append((loss, sums, lp.grad, z.grad))
+        info["outs"] = outs
         info["micros"] = len(res.batches)
 
     gpu_ms = _wall_ms(gpu_step, runs, warmup=2)
-    out = {"gpu_ms": round(gpu_ms, 3), "tokens": info["tokens"], "micros": info["micros"], "V": VOCAB}
+    out = {"gpu_ms": round(gpu_ms, 3), "tokens": T_TOK, "V": VOCAB, "packed_micros": info["micros"],
+           "work": "pack 256 samples (all micros) + GRPO, then logprob+entropy, PPO fwd+bwd and the logits "
+                   "backward over the first two 8192-token micros"}
     if not no_cpu:
         from oracle import batch as obatch
         from oracle import grpo as ogrpo
@@ -959,35 +962,58 @@ def bench_end_to_end(runs, no_cpu):
         from oracle import plan as oplan
         from oracle import ppo as oppo
 
-        samples = batch.sample_dicts(rewards=rewards)[:keep]
-        zc = logits.cpu()
+        samples = batch.sample_dicts(rewards=rewards)
+        zc_all = logits.cpu()
+        cinfo = {}
 
         def cpu_step():
-            lengths, loss_t = oplan.sample_lengths(samples, 8192)
-            local, per_rank = oplan.build_plan(lengths, loss_t, 1, layout="packed", mini_batch_size=keep,
-                                               seq_len=8192, align=2048, max_tokens_per_micro=8192)
+            lengths, loss_t = oplan.sample_lengths(samples, micro)
+            local, per_rank = oplan.build_plan(lengths, loss_t, 1, layout="packed", mini_batch_size=n,
+                                               seq_len=micro, align=2048, max_tokens_per_micro=micro)
             adv = []
-            for g in range(keep // 8):
-                adv += ogrpo.grpo_group([float(s["reward"]) for s in samples[8 * g:8 * g + 8]])
+            for g in range(len(group_offsets) - 1):
+                adv += ogrpo.grpo_group([float(r) for r in rewards[group_offsets[g]:group_offsets[g + 1]]])
             loc = [dict(samples[i], advantage=adv[i]) for i in local[0]]
             micros, n_docs_g, n_tok_g, _ = per_rank[0][0]
-            off = 0
-            for idx, seq_len, doc_lens in micros:
-                mbc = obatch.build_micro_batch(loc, idx, seq_len, doc_lens, layout="packed", need_rollout_lp=True)
-                z = zc[:, off:off + seq_len] if off + seq_len <= T_TOK else zc[:, :seq_len]
-                off += seq_len
-                lp, ent = olp.forward_logprobs(z, mbc["labels"], with_entropy=True)
-                nr = lp.detach().requires_grad_(True)
-                loss, _ = oppo.ppo_clip_loss(nr, mbc["rollout_logprobs"], mbc["mask"], mbc["doc_ids"],
-                                             mbc["advantages"], mbc["n_docs"], n_docs_global=n_docs_g,
-                                             n_tokens_global=n_tok_g, clip_low=0.2, clip_high=0.28,
-                                             per_token_loss=True, entropy=ent)
+            mbcs = [obatch.build_micro_batch(loc, idx, seq_len, doc_lens, layout="packed", need_rollout_lp=True)
+                    for idx, seq_len, doc_lens in micros]
+            outs = []
+            for j in range(T_TOK // micro):
+                mbc = mbcs[j]
+                z = zc_all[:, j * micro:(j + 1) * micro].float().requires_grad_(True)
+                lp = olp.forward_logprobs(z, mbc["labels"])
+                with torch.no_grad():
+                    ent = olp.chunk_entropy(z.detach())
+                lp.retain_grad()
+                loss, sums = oppo.ppo_clip_loss(lp, mbc["rollout_logprobs"], mbc["mask"], mbc["doc_ids"],
+                                                mbc["advantages"], mbc["n_docs"], n_docs_global=n_docs_g,
+                                                n_tokens_global=n_tok_g, clip_low=0.2, clip_high=0.28,
+                                                per_token_loss=True, entropy=ent,
+                                                rollout_lp=mbc["rollout_logprobs"])
                 loss.backward()
+                outs.append((loss, sums, lp.grad, z.grad))
+            cinfo["outs"] = outs
 
-        cpu_ms = _wall_ms(cpu_step, 3, gpu=False)
+        cpu_ms = _wall_ms(cpu_step, 2, warmup=0, gpu=False)
         out["cpu_ms"] = round(cpu_ms, 1)
+        out["cpu_threads"] = torch.get_num_threads()
         out["speedup_vs_cpu"] = round(cpu_ms / gpu_ms, 1)
+        d_loss = d_sum = d_new = d_z = 0.0
+        for (gl, gs, gn, gz), (cl, cs, cn, cz) in zip(info["outs"], cinfo["outs"]):
+            d_loss = max(d_loss, abs(gl.item() - cl.item()))
+            for k, v in cs.items():
+                d_sum = max(d_sum, abs(float(gs[k]) - float(v)) / max(1.0, abs(float(v))))
+            cn = cn.reshape(-1)
+            d_new = max(d_new, (gn.reshape(-1).cpu() - cn).abs().max().item() / max(cn.abs().max().item(), 1e-30))
+            for a in range(0, micro, 1024):
+                diff = (gz[0, a:a + 1024].float().cpu() - cz[0, a:a + 1024]).abs()
+                d_z = max(d_z, (diff / (cn[a:a + 1024, None].abs() + 1e-30)).max().item())
+        out["max_abs_diff_loss"] = d_loss
+        out["max_diff_sums_abs_or_rel"] = d_sum
+        out["max_rel_diff_dloss_dnew_lp"] = d_new
+        out["max_diff_dloss_dlogits_over_row_grad"] = d_z
     del logits
+    info.clear()
     torch.cuda.empty_cache()
     return out
 

@@ -96,9 +96,10 @@ def test_large_dynamic_range(dev):
 
 @pytest.mark.parametrize("pattern", ["ramp", "late_rise", "late_spikes"])
 def test_running_max_raised_in_later_tiles(dev, pattern):
-    """Rows whose later register tiles exceed what a thread saw first by more
-    than exp2 can hold relative to it (> 88): each such tile is redone with its
-    exact max.  The ramp does it on nearly every tile of every thread."""
+    """Rows whose later register tiles exceed the running max a thread holds
+    by more than 44 (a tile sum above 2^64): each such tile takes the exact
+    update with its own max.  The ramp does it on nearly every tile of every
+    thread; the spikes on one tile of one thread."""
     V = 151936
     g = torch.Generator().manual_seed(17)
     z = torch.randn(3, 5, V, generator=g) * 2.0
@@ -168,9 +169,9 @@ def test_backward_matches_autograd(dev):
     assert got[1, 3].abs().max().item() == 0.0
 
 
-def test_full_size_rows_subset(dev):
-    """T=16384, V=151936 (the headline shape): a row subset against the oracle,
-    and size-independent properties on every row."""
+def test_full_size_every_row(dev):
+    """T=16384, V=151936 (the headline shape): every row against the oracle,
+    1024 rows at a time, plus size-independent properties."""
     from meshy_amd import logprob
 
     T, V = 16384, 151936
@@ -182,9 +183,11 @@ def test_full_size_rows_subset(dev):
     assert torch.isfinite(lp).all() and torch.isfinite(ent).all()
     assert (lp <= 1e-6).all()
     assert (ent >= -1e-6).all() and (ent <= math.log(V) + 1e-4).all()
-    rows = torch.tensor([0, 1, 4095, 8191, 12000, T - 2, T - 1])
-    zs = z[:, rows.to(dev)].cpu()
-    ref_lp = olp.chunk_logprobs(zs, y[:, rows.to(dev)].cpu())
-    ref_ent = olp.chunk_entropy(zs)
-    assert (lp[:, rows.to(dev)].cpu() - ref_lp).abs().max() <= TOL
-    assert (ent[:, rows.to(dev)].cpu() - ref_ent).abs().max() <= TOL
+    lp, ent, yc = lp.cpu(), ent.cpu(), y.cpu()
+    worst_lp = worst_ent = 0.0
+    for a in range(0, T, 1024):
+        zs = z[:, a:a + 1024].cpu()
+        worst_lp = max(worst_lp, (lp[:, a:a + 1024] - olp.chunk_logprobs(zs, yc[:, a:a + 1024])).abs().max().item())
+        worst_ent = max(worst_ent, (ent[:, a:a + 1024] - olp.chunk_entropy(zs)).abs().max().item())
+    print(f"[16384, 151936] every row: max|dlogp|={worst_lp:.2e} max|dH|={worst_ent:.2e}")
+    assert worst_lp <= TOL and worst_ent <= TOL

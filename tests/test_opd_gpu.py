@@ -95,9 +95,10 @@ def test_topk_row_with_plus_inf_matches_logsumexp(dev):
     assert (got[fin] - rlps[fin]).abs().max().item() <= TOL
 
 
-def test_topk_full_size_rows_subset(dev):
-    """[16384, 151936] bf16, K = 8: a row subset against the
-    oracle, size-independent properties on every row."""
+def test_topk_full_size_every_row(dev):
+    """[16384, 151936] bf16, K = 8: every row against the oracle (1024 rows at
+    a time, by the one-selection form of the stable sort), plus
+    size-independent properties."""
     from meshy_amd import topk
 
     T, V, K = 16384, 151936, 8
@@ -109,14 +110,14 @@ def test_topk_full_size_rows_subset(dev):
     assert (lps[..., :-1] >= lps[..., 1:]).all()  # sorted by value
     srt = ids.sort(dim=-1).values
     assert (srt[..., 1:] != srt[..., :-1]).all()  # distinct
-    # the selected logits, in order
-    top_vals = torch.gather(z, -1, ids).float()
-    assert (top_vals[..., :-1] >= top_vals[..., 1:]).all()
-    rows = torch.tensor([0, 1, 777, 8191, 12345, T - 1])
-    zs = z[:, rows.to(dev)].cpu()
-    rids, rlps = otopk.teacher_topk(zs, K)
-    assert torch.equal(ids[:, rows.to(dev)].cpu(), rids)
-    assert (lps[:, rows.to(dev)].cpu() - rlps).abs().max().item() <= TOL
+    ids, lps = ids.cpu(), lps.cpu()
+    worst = 0.0
+    for a in range(0, T, 1024):
+        rids, rlps = otopk.teacher_topk_by_threshold(z[:, a:a + 1024].cpu(), K)
+        assert torch.equal(ids[:, a:a + 1024], rids), a
+        worst = max(worst, (lps[:, a:a + 1024] - rlps).abs().max().item())
+    print(f"Top-K [16384, 151936] every row: ids equal, max|dlogp|={worst:.2e}")
+    assert worst <= TOL
 
 
 def test_topk_rejects_bad_k(dev):

@@ -46,6 +46,25 @@ def test_teacher_topk_tie_order_brute_force():
             assert lps[r, t].tolist() == pytest.approx([row[j] - lse for j in want], abs=1e-5)
 
 
+@pytest.mark.parametrize("k", [1, 7, 64])
+def test_teacher_topk_by_threshold_equals_the_stable_sort(k):
+    """The one-selection form used on 16384-row batches gives the stable
+    sort's ids and log-probs: ties at and above the k-th value (integer
+    logits), -0 beside +0, a row of equal values, a row of -inf."""
+    g = torch.Generator().manual_seed(k)
+    z = torch.randint(-3, 4, (2, 9, 300), generator=g).float()
+    z[0, 0, 5], z[0, 0, 6] = -0.0, 0.0
+    z[1, 3, :] = 2.0
+    z[1, 4, :] = float("-inf")
+    z = z.to(torch.bfloat16)
+    a_ids, a_lps = otopk.teacher_topk(z, k, chunk=4)
+    b_ids, b_lps = otopk.teacher_topk_by_threshold(z, k, chunk=4)
+    assert torch.equal(a_ids, b_ids)
+    assert torch.equal(a_lps.nan_to_num(), b_lps.nan_to_num())
+    w = (torch.randn(1, 40, 5000, generator=g) * 2.0).to(torch.bfloat16)
+    assert torch.equal(otopk.teacher_topk(w, k)[0], otopk.teacher_topk_by_threshold(w, k)[0])
+
+
 def test_gather_logprobs_matches_dense_and_propagates_grad():
     # test_opd_loss.py:23-33
     z = _logits().requires_grad_(True)
