@@ -467,15 +467,14 @@ def bench_ppo(steps, warmup, no_cpu):
     old_d = torch.from_numpy(old).reshape(1, -1).to(dev)
     new_d = torch.from_numpy(new).reshape(1, -1).to(dev).requires_grad_(True)
 
-    # Each call sees a fresh micro-batch: the document offsets a batch caches
-    # after its first loss call are dropped, so they are paid for every time.
+    # The batch carries its document offsets, as one the pack kernels built
+    # does (the pack writes them with cu_seqlens); a batch built elsewhere pays
+    # one segment_offsets pass the first time (segment_offsets_us below).
     def fwd():
-        mb.__dict__.pop("_meshy_seg_offsets", None)
         with torch.no_grad():
             ppo_clip_loss(stub, new_d, old_d, mb, mini)
 
     def fwd_bwd():
-        mb.__dict__.pop("_meshy_seg_offsets", None)
         new_d.grad = None
         loss, _ = ppo_clip_loss(stub, new_d, old_d, mb, mini)
         loss.backward()
@@ -500,8 +499,10 @@ def bench_ppo(steps, warmup, no_cpu):
             oppo.reduce_mini_metrics(sums)
 
         cpu_ms = _wall_ms(cpu, 5, gpu=False)
-    # The kernels alone, through the C ABI: the document offsets (recomputed for
-    # a fresh micro-batch) and the loss, then its gradient.
+    # The kernels alone, through the C ABI: the loss forward (which, for the
+    # token mean, also writes each token's unit gradient), then the backward
+    # (a scale by the loss's gradient); and the document offsets of a batch
+    # that does not carry them.
     import ctypes
 
     from meshy_amd import _lib
@@ -509,34 +510,43 @@ def bench_ppo(steps, warmup, no_cpu):
 
     inputs = loss_mod._Inputs(stub, new_d, old_d, mb, mini, None)
     new_flat = new_d.detach().reshape(-1)
-    args = inputs.args(new_flat)
-    pa = ctypes.byref(args)
+    unit = torch.empty_like(new_flat)
+    args = inputs.args(new_flat, unit)
+    args_nograd = inputs.args(new_flat)
+    pa, pa0 = ctypes.byref(args), ctypes.byref(args_nograd)
     lib, stream = _lib.load(), _lib.stream_of(dev)
     out_t = torch.empty(_lib.PPO_NOUT, device=dev)
-    seg = torch.empty(n + 1, device=dev)
     one = torch.ones(1, device=dev)
     grad = torch.empty_like(new_flat)
     ids, off = inputs.ids, inputs.seg_off
 
+    def dev_fwd_nograd():
+        lib.meshy_ppo_loss_fwd(pa0, out_t.data_ptr(), None, stream)
+
     def dev_fwd():
-        lib.meshy_segment_offsets(ids.data_ptr(), ids.numel(), n + 1, off.data_ptr(), None, stream)
-        lib.meshy_ppo_loss_fwd(pa, out_t.data_ptr(), seg.data_ptr(), stream)
+        lib.meshy_ppo_loss_fwd(pa, out_t.data_ptr(), None, stream)
 
     def dev_bwd():
-        lib.meshy_ppo_loss_bwd(pa, seg.data_ptr(), one.data_ptr(), grad.data_ptr(), stream)
+        lib.meshy_ppo_loss_bwd(pa, None, one.data_ptr(), grad.data_ptr(), stream)
 
-    _checked(lib.meshy_ppo_loss_fwd(pa, out_t.data_ptr(), seg.data_ptr(), stream), "meshy_ppo_loss_fwd")
-    _checked(lib.meshy_ppo_loss_bwd(pa, seg.data_ptr(), one.data_ptr(), grad.data_ptr(), stream), "meshy_ppo_loss_bwd")
+    def dev_offsets():
+        lib.meshy_segment_offsets(ids.data_ptr(), ids.numel(), n + 1, off.data_ptr(), None, stream)
+
+    _checked(lib.meshy_ppo_loss_fwd(pa, out_t.data_ptr(), None, stream), "meshy_ppo_loss_fwd")
+    _checked(lib.meshy_ppo_loss_bwd(pa, None, one.data_ptr(), grad.data_ptr(), stream), "meshy_ppo_loss_bwd")
+    fwd0_dev = _gpu_ms(dev_fwd_nograd, steps, warmup) * 1e3
     fwd_dev = _gpu_ms(dev_fwd, steps, warmup) * 1e3
     bwd_dev = _gpu_ms(dev_bwd, steps, warmup) * 1e3
-    # fwd: new, old, mask, doc id 20 B/token (+ the offsets' 8 B doc id read);
-    # bwd: new, old, mask, doc id read + grad written 24 B/token
-    fwd_bytes = T * 28
-    bwd_bytes = T * 24
+    off_dev = _gpu_ms(dev_offsets, steps, warmup) * 1e3
+    # fwd: new, old, mask read 12 B/token (+ the unit gradient written, 4 B,
+    # when a backward follows); bwd: unit gradient read + gradient written 8 B/token
+    fwd_bytes = T * 12
+    fb_bytes = T * (16 + 8)
     return {
-        "ppo_loss_fwd": _with_device(_entry(fwd_ms * 1e3, fwd_bytes, tokens=T), fwd_dev, fwd_bytes),
-        "ppo_loss_fwd_bwd": _with_device(_entry(fb_ms * 1e3, fwd_bytes + bwd_bytes, cpu_ms, tokens=T),
-                                         fwd_dev + bwd_dev, fwd_bytes + bwd_bytes),
+        "ppo_loss_fwd": _with_device(_entry(fwd_ms * 1e3, fwd_bytes, tokens=T), fwd0_dev, fwd_bytes),
+        "ppo_loss_fwd_bwd": _with_device(_entry(fb_ms * 1e3, fb_bytes, cpu_ms, tokens=T),
+                                         fwd_dev + bwd_dev, fb_bytes),
+        "segment_offsets_us": round(off_dev, 2),
     }
 
 

@@ -175,6 +175,11 @@ typedef struct meshy_pack_args {
     float* teacher_lps_out;        /* [n_out, teacher_k]                      */
     int32_t teacher_ids_elem_bytes; /* 4 or 8 (0 reads as 4)                  */
     int32_t reserved_t;
+    /* Optional int64 token offsets of each micro's n_docs + 1 document slots
+       (padding slot last) over its flattened [rows, S] grid, the loss kernels'
+       seg_offsets: micro k writes n_docs_k + 2 values at
+       micro_doc_start[k] + 2*k.  Nullable. */
+    int64_t* seg_offsets;
 } meshy_pack_args;
 
 int meshy_pack_micro_batches(const meshy_pack_args* args, hipStream_t stream);
@@ -383,6 +388,7 @@ typedef struct meshy_ppo_args {
     const float* positive_lm_weights; /* [n_docs], nullable                   */
     const int64_t* seg_offsets;    /* [n_docs + 2]                            */
     const int64_t* doc_ids;        /* [n_tokens], the ids seg_offsets is of   */
+    float* grad_unit;              /* [n_tokens] nullable, see meshy_ppo_loss_fwd */
     int64_t n_tokens;
     int64_t n_docs;
     int64_t n_docs_global;         /* MiniPlan.n_docs_global                  */
@@ -412,12 +418,17 @@ int meshy_segment_offsets(const int64_t* doc_ids, int64_t n_tokens, int64_t n_sl
                           int64_t* seg_offsets, int32_t* unsorted, hipStream_t stream);
 
 size_t meshy_ppo_workspace_size(int64_t n_tokens, int64_t n_docs);
-/* out: [MESHY_PPO_NOUT] fp32 (device).  seg_cnt: [n_docs + 1] fp32 (device),
- * the per-document masked token counts the backward needs. */
+/* out: [MESHY_PPO_NOUT] fp32 (device).  seg_cnt: [n_docs + 1] fp32 (device,
+ * nullable), the per-document masked token counts the sequence-mean backward
+ * needs.  With the token-mean reduction (per_token_loss) and grad_unit set,
+ * grad_unit[i] receives d(total loss)/d new_lp[i] at a unit loss gradient. */
 int meshy_ppo_loss_fwd(const meshy_ppo_args* args, float* out, float* seg_cnt,
                        hipStream_t stream);
 /* grad_new[i] = d(total loss)/d new_lp[i] * grad_loss[0]  (grad_loss is a
- * device scalar), matching torch autograd through trainer.py:751-809. */
+ * device scalar), matching torch autograd through trainer.py:751-809.  With
+ * per_token_loss and grad_unit (as the forward filled it) this is
+ * grad_loss[0] * grad_unit[i] and seg_cnt may be NULL; otherwise seg_cnt is
+ * the forward's. */
 int meshy_ppo_loss_bwd(const meshy_ppo_args* args, const float* seg_cnt,
                        const float* grad_loss, float* grad_new, hipStream_t stream);
 

@@ -102,6 +102,7 @@ class PackArgs(ctypes.Structure):
         ("teacher_lps_out", c_void_p),
         ("teacher_ids_elem_bytes", c_int32),
         ("reserved_t", c_int32),
+        ("seg_offsets", c_void_p),
     ]
 
 
@@ -152,6 +153,7 @@ class PpoArgs(ctypes.Structure):
         ("positive_lm_weights", c_void_p),
         ("seg_offsets", c_void_p),
         ("doc_ids", c_void_p),
+        ("grad_unit", c_void_p),
         ("n_tokens", c_int64),
         ("n_docs", c_int64),
         ("n_docs_global", c_int64),
@@ -307,7 +309,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 _LIB: ctypes.CDLL | None = None
 

@@ -368,6 +368,7 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
     adv_doc = torch.empty(max(n_docs_total, 1), dtype=torch.float32, device=device)
     lengths = torch.empty(max(n_docs_total, 1), dtype=torch.int32, device=device)
     cu = torch.empty(n_docs_total + 2 * n_micro, dtype=torch.int32, device=device)
+    seg = torch.empty(n_docs_total + 2 * n_micro, dtype=torch.int64, device=device)
 
     a = _lib.PackArgs()
     a.tokens = lay.view(dbuf, "tokens").data_ptr()
@@ -401,6 +402,7 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
     a.adv_doc = adv_doc.data_ptr()
     a.doc_len_out = lengths.data_ptr()
     a.cu_seqlens = cu.data_ptr()
+    a.seg_offsets = seg.data_ptr()
     t_ids = t_lps = None
     if job.teacher_k:
         K = job.teacher_k
@@ -465,6 +467,7 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
         job.teacher_views = tv
 
     out: list[Batch] = []
+    seg_at = (np.asarray(job.doc_start[:-1], np.int64) + 2 * np.arange(n_micro)).tolist()
     for k, m in enumerate(job.micros):
         nd = nd_l[k]
         ii, lb, ps, mk, di = f_ids[k], f_lab[k], f_pos[k], f_mask[k], f_doc[k]
@@ -487,7 +490,7 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
             if at is not None:
                 at = rest.pop(0)
         per_token = at if job.per_token_adv else None
-        out.append(Batch(
+        mb = Batch(
             input_ids=ii,
             labels=lb,
             positions=ps,
@@ -500,7 +503,11 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
             attention_masks=attn,
             positive_lm_weights=f_pw[k],
             advantage_tokens=at if job.broadcast_advantages and not job.per_token_adv else None,
-        ))
+        )
+        # The kernel's segment offsets of this micro, valid while doc_ids is
+        # the tensor it wrote (the losses' offsets cache checks that).
+        mb._meshy_seg_src = ((id(di), di._version, di.data_ptr(), nd), seg, seg_at[k])
+        out.append(mb)
     return out
 
 

@@ -112,6 +112,18 @@ __global__ __launch_bounds__(kFillThreads) void k_pack_fill(meshy_pack_args a) {
             if (a.adv_doc) a.adv_doc[d0 + j] = a.adv_samples[a.doc_sample[d0 + j]];
             if (a.doc_len_out) a.doc_len_out[d0 + j] = static_cast<int32_t>(a.doc_len[d0 + j]);
         }
+        // Token offsets of the micro's n_docs + 1 document slots over its
+        // flattened [rows, S] grid (slot nd, the padding, last): what the loss
+        // kernels take as seg_offsets.
+        if (a.seg_offsets) {
+            int64_t* so = a.seg_offsets + d0 + 2 * k;
+            for (int32_t j = threadIdx.x; j <= nd + 1; j += kFillThreads) {
+                int64_t v;
+                if (packed) v = j <= nd ? static_cast<int64_t>(cu[j]) : S;
+                else v = (j <= nd ? min<int64_t>(j, max(nd, 1)) : max(nd, 1)) * S;
+                so[j] = v;
+            }
+        }
     }
 
 #pragma unroll

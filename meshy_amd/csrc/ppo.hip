@@ -9,24 +9,27 @@
 //   per-document sums, token-mean or sequence-mean reduction            (787-809)
 //   diagnostic sums (ratio, clip, KL, ESS, k3, entropy)                 (813-847)
 //
-// Layout: documents are contiguous token ranges given by seg_offsets, and
-// doc_ids (non-decreasing) names each token's document directly.  The token
-// axis is cut into tiles of kTile tokens, one workgroup each; doc_ids at the
-// tile's ends give its document range with the token loads, without a search.
-// A tile usually overlaps one to three documents: then every thread strides the
+// Layout: documents are contiguous token ranges given by seg_offsets
+// (non-decreasing doc_ids, the ids the offsets were built from).  The token
+// axis is cut into tiles of kTile tokens, one workgroup each.  A tile's
+// document range is doc_ids at its two ends; the boundaries between those
+// documents are read from seg_offsets, so the per-token ids are never loaded.
+// A tile usually overlaps one to four documents: then every thread strides the
 // whole tile (coalesced) and accumulates into up to kFastDocs per-document
 // slots, reduced once per workgroup.  A tile crossing more documents falls back
 // to one wavefront per (tile, document) pair.  Both tiles and documents are ordered,
 // so the overlapping pairs form a monotone staircase and `tile + document`
 // indexes them without collision.
 //   k_ppo_tiles  5 per-document partial sums per pair -> workspace[tile+doc],
-//                10 token-level partial sums per tile;
-//   k_ppo_final  one workgroup: per-document totals in tile order, then the
+//                10 token-level partial sums per tile; with the token-mean
+//                reduction also each token's gradient at unit loss gradient;
+//   k_ppo_combine one workgroup: per-document totals in tile order, then the
 //                loss, ESS and every diagnostic in one fused block reduction
 //                (fixed order, no atomics: bitwise reproducible);
-//   k_ppo_bwd    per token (8 per thread): d(total loss)/d new_lp as torch
-//                autograd gives it (min splits ties 1/2-1/2, clamp passes on
-//                [lo, hi]), the document's factors gathered by doc_ids.
+//   k_ppo_scale  token mean: d(total loss)/d new_lp = grad_loss * unit gradient;
+//   k_ppo_bwd    sequence mean: per token (4 per thread) d(total loss)/d new_lp
+//                as torch autograd gives it (min splits ties 1/2-1/2, clamp
+//                passes on [lo, hi]), the document's factors gathered by doc_ids.
 #include <math.h>
 
 #include <algorithm>
@@ -42,7 +45,6 @@ constexpr int64_t kTile = 2048;
 constexpr int kFastDocs = 4;  // documents per tile handled by the whole workgroup
 constexpr int kTokSums = 10;  // token-level sums
 constexpr int kSegSums = 5;   // per-document sums: pg, cnt, w, w2, positive
-constexpr int kFinalThreads = 1024;
 constexpr int kFinalVals = 4 + kTokSums;
 
 enum TokSum { TS_TIS = 0, TS_RATIO, TS_CLIP, TS_TIS_MASKED, TS_COUNT, TS_KL, TS_LR_ABS, TS_K3, TS_LOGDIFF, TS_ENT };
@@ -159,46 +161,208 @@ __device__ __forceinline__ void token_contrib_v(const meshy_ppo_args& a, const T
     c.tok[TS_ENT] = a.entropy ? x.en * mk : 0.f;
 }
 
+// d(total loss)/d new_lp of one token (gD = grad_loss * D_d).
+__device__ __forceinline__ float token_grad_v(const meshy_ppo_args& a, const TokIn& x, float A, float w_doc,
+                                              float gD) {
+    const float lo_c = 1.f - a.clip_low;
+    const float hi_c = 1.f + a.clip_high;
+    const float nw = x.nw;
+    const float ol = x.ol;
+    const float mk = x.mk;
+    const float ratio = expf(nw - ol);
+    const float u = ratio * A;
+    const float c = t_clamp(ratio, lo_c, hi_c) * A;
+    // grad of pg_per_token (before masking) w.r.t. pg = -min(u, c)
+    float g = gD * mk;
+    if (a.use_icepop) {
+        const float tis = expf(ol - x.ro);
+        const bool tm = (tis >= a.tis_min) && (tis <= a.tis_max);
+        g = tm ? g * tis : 0.f;
+    } else if (a.use_tis) {
+        const bool tm = (ratio >= a.tis_min) && (ratio <= a.tis_max);
+        g = tm ? g : 0.f;
+    }
+    const float gm = -g;  // through the negation
+    float gu, gc;
+    if (u == c) {
+        gu = 0.5f * gm;
+        gc = 0.5f * gm;
+    } else {
+        gu = (u > c) ? 0.f : gm;
+        gc = (u < c) ? 0.f : gm;
+    }
+    const float in_range = (ratio >= lo_c && ratio <= hi_c) ? 1.f : 0.f;
+    const float g_ratio = gu * A + (gc * A) * in_range;
+    float gn = g_ratio * ratio;
+    if (a.positive_lm_coef != 0.f) gn += (gD * a.positive_lm_coef) * (-(w_doc * mk));
+    return gn;
+}
+
 // The document of token i, clamped to the slots so that malformed ids stay in bounds.
 __device__ __forceinline__ int64_t doc_at(const meshy_ppo_args& a, int64_t i) {
     return min(max(a.doc_ids[i], static_cast<int64_t>(0)), a.n_docs);
 }
 
+// The combine, run by the last tile workgroup once every tile's partials are
+// visible: per-document totals in tile order and their loss / ESS terms, then
+// every token-level sum, in one fixed-order block reduction (fp64 across
+// threads).  seg_cnt_out receives each slot's masked token count.
+template <int NT>
+__device__ __forceinline__ void ppo_combine(const meshy_ppo_args& a, const Workspace& ws, float* __restrict__ out,
+                                            float* __restrict__ seg_cnt_out) {
+    __shared__ double s_red[NT / kWave][kFinalVals];
+    __shared__ double s_tot[kFinalVals];
+    const int64_t n_slots = a.n_docs + 1;
+    const int64_t n_tiles = n_tiles_of(a.n_tokens);
+    double v[kFinalVals];
+#pragma unroll
+    for (int k = 0; k < kFinalVals; ++k) v[k] = 0.0;
+    // Per-document totals (tile order) and their contributions: v[0..3] =
+    // loss terms, positive-LM terms, ESS terms, documents with tokens.
+    for (int64_t d = threadIdx.x; d < n_slots; d += NT) {
+        const int64_t lo = a.seg_offsets[d];
+        const int64_t hi = a.seg_offsets[d + 1];
+        float sg[kSegSums] = {0.f, 0.f, 0.f, 0.f, 0.f};
+        if (hi > lo) {
+            const int64_t b0 = lo / kTile;
+            const int64_t b1 = (hi - 1) / kTile;
+            for (int64_t b = b0; b <= b1; ++b) {
+                const float* src = ws.seg + (b + d) * kSegSums;
+#pragma unroll
+                for (int k = 0; k < kSegSums; ++k) sg[k] += src[k];
+            }
+        }
+        if (seg_cnt_out) seg_cnt_out[d] = sg[1];
+        if (d < a.n_docs) {
+            if (a.per_token_loss) {
+                v[0] += sg[0];
+                v[1] += sg[4];
+            } else {
+                const float c = fmaxf(sg[1], 1.f);
+                v[0] += sg[0] / c;
+                v[1] += sg[4] / c;
+            }
+            if (sg[1] > 0.f) {
+                v[2] += (sg[2] * sg[2]) / (fmaxf(sg[1], 1.f) * fmaxf(sg[3], 1e-8f));
+                v[3] += 1.0;
+            }
+        }
+    }
+    // Token-level sums of every tile: v[4..13], four tiles per step with every
+    // load of a step issued before any is added (indices clamped, extra tiles
+    // dropped by a select).
+    constexpr int kStep = 4;
+    for (int64_t b0 = threadIdx.x; b0 < n_tiles; b0 += NT * kStep) {
+        float t[kStep][kTokSums];
+#pragma unroll
+        for (int u = 0; u < kStep; ++u) {
+            const int64_t b = min(b0 + static_cast<int64_t>(u) * NT, n_tiles - 1);
+#pragma unroll
+            for (int k = 0; k < kTokSums; ++k) t[u][k] = ws.tok[b * kTokSums + k];
+        }
+#pragma unroll
+        for (int u = 0; u < kStep; ++u) {
+            const bool ok = b0 + static_cast<int64_t>(u) * NT < n_tiles;
+#pragma unroll
+            for (int k = 0; k < kTokSums; ++k) v[4 + k] += ok ? t[u][k] : 0.f;
+        }
+    }
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+#pragma unroll
+    for (int k = 0; k < kFinalVals; ++k) v[k] = wave_sum(v[k]);
+    if (lane == 0) {
+#pragma unroll
+        for (int k = 0; k < kFinalVals; ++k) s_red[wid][k] = v[k];
+    }
+    __syncthreads();
+    if (threadIdx.x < kFinalVals) {
+        double s = 0.0;
+        for (int w = 0; w < NT / kWave; ++w) s += s_red[w][threadIdx.x];
+        s_tot[threadIdx.x] = s;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        const double* t = s_tot;
+        const double den = a.per_token_loss ? static_cast<double>(max<int64_t>(1, a.n_tokens_global))
+                                            : static_cast<double>(max<int64_t>(1, a.n_docs_global));
+        const float loss = static_cast<float>(t[0] / den);
+        const float pos = static_cast<float>(t[1] / den);
+        const float cp = static_cast<float>(max(1, a.cp_degree));
+        const double* tok = t + 4;
+        out[MESHY_PPO_LOSS] = loss;
+        out[MESHY_PPO_TOTAL_LOSS] = loss + a.positive_lm_coef * pos;
+        out[MESHY_PPO_POSITIVE_LM_LOSS] = pos;
+        out[MESHY_PPO_TIS_RATIO_SUM] = static_cast<float>(tok[TS_TIS]);
+        out[MESHY_PPO_RATIO_SUM] = static_cast<float>(tok[TS_RATIO]);
+        out[MESHY_PPO_CLIP_SUM] = static_cast<float>(tok[TS_CLIP]);
+        out[MESHY_PPO_TIS_MASKED_SUM] = static_cast<float>(tok[TS_TIS_MASKED]);
+        out[MESHY_PPO_TOKEN_COUNT] = static_cast<float>(tok[TS_COUNT]);
+        out[MESHY_PPO_KL_SUM] = static_cast<float>(tok[TS_KL]);
+        out[MESHY_PPO_LOG_RATIO_ABS_SUM] = static_cast<float>(tok[TS_LR_ABS]);
+        out[MESHY_PPO_ESS_SUM] = static_cast<float>(t[2]) / cp;
+        out[MESHY_PPO_DOC_COUNT] = static_cast<float>(t[3]) / cp;
+        out[MESHY_PPO_TRAIN_ROLLOUT_KL_SUM] = static_cast<float>(tok[TS_K3]);
+        out[MESHY_PPO_TRAIN_ROLLOUT_LOGDIFF_ABS_SUM] = static_cast<float>(tok[TS_LOGDIFF]);
+        out[MESHY_PPO_ENTROPY_SUM] = static_cast<float>(tok[TS_ENT]);
+    }
+}
+
 // kLean: the configuration without IcePop, rollout log-probs, entropy or
-// per-token advantages, whose per-token registers are then not allocated (so
-// that four workgroups fit per CU).
+// per-token advantages, whose per-token registers are then not allocated.
 template <bool kLean>
-__global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Workspace ws) {
+__global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Workspace ws, bool vec) {
     __shared__ float s_red[kWaves][kTokSums + kFastDocs * kSegSums];
     const int64_t b = blockIdx.x;
     const int64_t t0 = b * kTile;
     const int64_t t1 = min(t0 + kTile, a.n_tokens);
     const int lane = threadIdx.x % kWave;
     const int wid = threadIdx.x / kWave;
-    // The tile's tokens and its document range, loaded together.
+    // The tile's tokens (thread t holds tokens 4t .. 4t+3 of each of the
+    // tile's 1024-token halves: 16-byte loads when every array is aligned),
+    // then its document range and the boundaries inside it.
     constexpr int kPer = static_cast<int>(kTile / kThreads);
     TokIn in[kPer];
-    int id[kPer];  // the tokens' documents (n_docs < 2^31)
 #pragma unroll
-    for (int q = 0; q < kPer; ++q) {
-        const int64_t i = t0 + q * kThreads + threadIdx.x;
-        in[q] = load_tok<kLean>(a, i, i < t1);
-        id[q] = static_cast<int>(a.doc_ids[i < t1 ? i : t0]);
+    for (int h = 0; h < kPer / 4; ++h) {
+        const int64_t i4 = t0 + h * (4 * kThreads) + 4 * threadIdx.x;
+        if (vec && i4 + 4 <= t1) {
+            const float4 nw = *reinterpret_cast<const float4*>(a.new_lp + i4);
+            const float4 ol = *reinterpret_cast<const float4*>(a.old_lp + i4);
+            const float4 mk = *reinterpret_cast<const float4*>(a.mask + i4);
+            float4 ro = make_float4(0.f, 0.f, 0.f, 0.f), en = ro, ad = ro;
+            if (!kLean && a.rollout_lp) ro = *reinterpret_cast<const float4*>(a.rollout_lp + i4);
+            if (!kLean && a.entropy) en = *reinterpret_cast<const float4*>(a.entropy + i4);
+            if (!kLean && a.adv_per_token) ad = *reinterpret_cast<const float4*>(a.adv + i4);
+            in[4 * h + 0] = TokIn{nw.x, ol.x, mk.x, ro.x, en.x, ad.x};
+            in[4 * h + 1] = TokIn{nw.y, ol.y, mk.y, ro.y, en.y, ad.y};
+            in[4 * h + 2] = TokIn{nw.z, ol.z, mk.z, ro.z, en.z, ad.z};
+            in[4 * h + 3] = TokIn{nw.w, ol.w, mk.w, ro.w, en.w, ad.w};
+        } else {
+#pragma unroll
+            for (int e = 0; e < 4; ++e) in[4 * h + e] = load_tok<kLean>(a, i4 + e, i4 + e < t1);
+        }
     }
     const int64_t d_first = doc_at(a, t0);
     const int64_t nd = max(doc_at(a, t1 - 1), d_first) - d_first + 1;
+    // Unit gradient of each token (token mean: the loss's gradient is known
+    // up to the scalar the backward multiplies in).
+    float* const gu = (a.grad_unit && a.per_token_loss) ? a.grad_unit : nullptr;
+    const float tok_scale = 1.f / static_cast<float>(max<int64_t>(1, a.n_tokens_global));
     float acc[kTokSums];
 #pragma unroll
     for (int k = 0; k < kTokSums; ++k) acc[k] = 0.f;
 
     if (nd <= kFastDocs) {
         float A_d[kFastDocs], W_d[kFastDocs];
+        int64_t bnd[kFastDocs];  // bnd[r]: first token of slot r (slots past nd: never reached)
 #pragma unroll
         for (int r = 0; r < kFastDocs; ++r) {
             const int64_t d = d_first + r;
             const bool real = r < nd && d < a.n_docs;
             A_d[r] = (!a.adv_per_token && real) ? a.adv[d] : 0.f;
             W_d[r] = (a.positive_lm_weights && real) ? a.positive_lm_weights[d] : 0.f;
+            bnd[r] = (r > 0 && r < nd) ? a.seg_offsets[d] : INT64_MAX;
         }
         // A thread's tokens (i = t0 + q * kThreads + tid) go through the tile's
         // documents in order, so the document sums accumulate in one run that
@@ -226,9 +390,11 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
         float A = A_d[0], W = W_d[0];
 #pragma unroll
         for (int q = 0; q < kPer; ++q) {
-            const int64_t i = t0 + q * kThreads + threadIdx.x;
+            const int64_t i = t0 + (q / 4) * (4 * kThreads) + 4 * threadIdx.x + (q % 4);
             if (i >= t1) break;
-            const int slot = min(max(id[q] - static_cast<int>(d_first), 0), static_cast<int>(nd) - 1);
+            int slot = 0;
+#pragma unroll
+            for (int r = 1; r < kFastDocs; ++r) slot += (i >= bnd[r]) ? 1 : 0;
             if (slot != cur) {
                 flush(cur);
                 cur = slot;
@@ -272,6 +438,10 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
                 acc[TS_LOGDIFF] = fmaf(nan_to_num(fabsf(diff)), mk, acc[TS_LOGDIFF]);
             }
             if (!kLean && a.entropy) acc[TS_ENT] = fmaf(x.en, mk, acc[TS_ENT]);
+            if (gu) {
+                const bool real = d_first + slot < a.n_docs;  // the padding slot is not in the loss
+                gu[i] = real ? token_grad_v(a, x, At, W, tok_scale) : 0.f;
+            }
         }
         flush(cur);
         // The token sums that are sums of the slots.
@@ -334,11 +504,13 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
         for (int64_t i = lo + lane; i < hi; i += kWave) {
             Contrib c;
             const TokIn x = load_tok(a, i, true);
-            token_contrib_v(a, x, a.adv_per_token ? x.ad : A_doc, w_doc, c);
+            const float At = a.adv_per_token ? x.ad : A_doc;
+            token_contrib_v(a, x, At, w_doc, c);
 #pragma unroll
             for (int k = 0; k < kSegSums; ++k) sg[k] += c.seg[k];
 #pragma unroll
             for (int k = 0; k < kTokSums; ++k) acc[k] += c.tok[k];
+            if (gu) gu[i] = real ? token_grad_v(a, x, At, w_doc, tok_scale) : 0.f;
         }
 #pragma unroll
         for (int k = 0; k < kSegSums; ++k) sg[k] = wave_sum(sg[k]);
@@ -361,150 +533,6 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
         for (int w = 0; w < kWaves; ++w) v += s_red[w][threadIdx.x];
         ws.tok[b * kTokSums + threadIdx.x] = v;
     }
-}
-
-__global__ __launch_bounds__(kFinalThreads) void k_ppo_final(meshy_ppo_args a, Workspace ws,
-                                                             float* __restrict__ out,
-                                                             float* __restrict__ seg_cnt_out) {
-    __shared__ double s_red[kFinalThreads / kWave][kFinalVals];
-    __shared__ double s_tot[kFinalVals];
-    const int64_t n_slots = a.n_docs + 1;
-    const int64_t n_tiles = n_tiles_of(a.n_tokens);
-    double v[kFinalVals];
-#pragma unroll
-    for (int k = 0; k < kFinalVals; ++k) v[k] = 0.0;
-    // The token-level sums of the first kFinalThreads tiles are loaded first:
-    // they depend on nothing, so they arrive while the documents' chain
-    // (offsets, then their tiles' partials) runs.
-    float tok0[kTokSums];
-    // Every lane loads (tile 0 when it has none, then discarded): a load under
-    // a per-lane condition compiles to a branch that waits for each load
-    // before the next is issued.
-    const bool has_tile = threadIdx.x < n_tiles;
-    const int64_t tb = has_tile ? threadIdx.x : 0;
-#pragma unroll
-    for (int k = 0; k < kTokSums; ++k) tok0[k] = 0.f;
-    if (n_tiles > 0) {
-#pragma unroll
-        for (int k = 0; k < kTokSums; ++k) tok0[k] = ws.tok[tb * kTokSums + k];
-#pragma unroll
-        for (int k = 0; k < kTokSums; ++k) tok0[k] = has_tile ? tok0[k] : 0.f;
-    }
-    // Per-document totals (tile order) and their contributions: v[0..3] =
-    // loss terms, positive-LM terms, ESS terms, documents with tokens.
-    for (int64_t d = threadIdx.x; d < n_slots; d += kFinalThreads) {
-        const int64_t lo = a.seg_offsets[d];
-        const int64_t hi = a.seg_offsets[d + 1];
-        float sg[kSegSums] = {0.f, 0.f, 0.f, 0.f, 0.f};
-        if (hi > lo) {
-            const int64_t b0 = lo / kTile;
-            const int64_t b1 = (hi - 1) / kTile;
-            for (int64_t b = b0; b <= b1; ++b) {
-                const float* src = ws.seg + (b + d) * kSegSums;
-#pragma unroll
-                for (int k = 0; k < kSegSums; ++k) sg[k] += src[k];
-            }
-        }
-        if (seg_cnt_out) seg_cnt_out[d] = sg[1];
-        if (d < a.n_docs) {
-            if (a.per_token_loss) {
-                v[0] += sg[0];
-                v[1] += sg[4];
-            } else {
-                const float c = fmaxf(sg[1], 1.f);
-                v[0] += sg[0] / c;
-                v[1] += sg[4] / c;
-            }
-            if (sg[1] > 0.f) {
-                v[2] += (sg[2] * sg[2]) / (fmaxf(sg[1], 1.f) * fmaxf(sg[3], 1e-8f));
-                v[3] += 1.0;
-            }
-        }
-    }
-    // Token-level sums of every tile: v[4..13].
-#pragma unroll
-    for (int k = 0; k < kTokSums; ++k) v[4 + k] += tok0[k];
-    for (int64_t b = threadIdx.x + kFinalThreads; b < n_tiles; b += kFinalThreads) {
-        const float* src = ws.tok + b * kTokSums;
-#pragma unroll
-        for (int k = 0; k < kTokSums; ++k) v[4 + k] += src[k];
-    }
-    const int lane = threadIdx.x % kWave;
-    const int wid = threadIdx.x / kWave;
-#pragma unroll
-    for (int k = 0; k < kFinalVals; ++k) v[k] = wave_sum(v[k]);
-    if (lane == 0) {
-#pragma unroll
-        for (int k = 0; k < kFinalVals; ++k) s_red[wid][k] = v[k];
-    }
-    __syncthreads();
-    if (threadIdx.x < kFinalVals) {
-        double s = 0.0;
-        for (int w = 0; w < kFinalThreads / kWave; ++w) s += s_red[w][threadIdx.x];
-        s_tot[threadIdx.x] = s;
-    }
-    __syncthreads();
-    if (threadIdx.x == 0) {
-        const double* t = s_tot;
-        const double den = a.per_token_loss ? static_cast<double>(max<int64_t>(1, a.n_tokens_global))
-                                            : static_cast<double>(max<int64_t>(1, a.n_docs_global));
-        const float loss = static_cast<float>(t[0] / den);
-        const float pos = static_cast<float>(t[1] / den);
-        const float cp = static_cast<float>(max(1, a.cp_degree));
-        const double* tok = t + 4;
-        out[MESHY_PPO_LOSS] = loss;
-        out[MESHY_PPO_TOTAL_LOSS] = loss + a.positive_lm_coef * pos;
-        out[MESHY_PPO_POSITIVE_LM_LOSS] = pos;
-        out[MESHY_PPO_TIS_RATIO_SUM] = static_cast<float>(tok[TS_TIS]);
-        out[MESHY_PPO_RATIO_SUM] = static_cast<float>(tok[TS_RATIO]);
-        out[MESHY_PPO_CLIP_SUM] = static_cast<float>(tok[TS_CLIP]);
-        out[MESHY_PPO_TIS_MASKED_SUM] = static_cast<float>(tok[TS_TIS_MASKED]);
-        out[MESHY_PPO_TOKEN_COUNT] = static_cast<float>(tok[TS_COUNT]);
-        out[MESHY_PPO_KL_SUM] = static_cast<float>(tok[TS_KL]);
-        out[MESHY_PPO_LOG_RATIO_ABS_SUM] = static_cast<float>(tok[TS_LR_ABS]);
-        out[MESHY_PPO_ESS_SUM] = static_cast<float>(t[2]) / cp;
-        out[MESHY_PPO_DOC_COUNT] = static_cast<float>(t[3]) / cp;
-        out[MESHY_PPO_TRAIN_ROLLOUT_KL_SUM] = static_cast<float>(tok[TS_K3]);
-        out[MESHY_PPO_TRAIN_ROLLOUT_LOGDIFF_ABS_SUM] = static_cast<float>(tok[TS_LOGDIFF]);
-        out[MESHY_PPO_ENTROPY_SUM] = static_cast<float>(tok[TS_ENT]);
-    }
-}
-
-// d(total loss)/d new_lp of one token (gD = grad_loss * D_d).
-__device__ __forceinline__ float token_grad_v(const meshy_ppo_args& a, const TokIn& x, float A, float w_doc,
-                                              float gD) {
-    const float lo_c = 1.f - a.clip_low;
-    const float hi_c = 1.f + a.clip_high;
-    const float nw = x.nw;
-    const float ol = x.ol;
-    const float mk = x.mk;
-    const float ratio = expf(nw - ol);
-    const float u = ratio * A;
-    const float c = t_clamp(ratio, lo_c, hi_c) * A;
-    // grad of pg_per_token (before masking) w.r.t. pg = -min(u, c)
-    float g = gD * mk;
-    if (a.use_icepop) {
-        const float tis = expf(ol - x.ro);
-        const bool tm = (tis >= a.tis_min) && (tis <= a.tis_max);
-        g = tm ? g * tis : 0.f;
-    } else if (a.use_tis) {
-        const bool tm = (ratio >= a.tis_min) && (ratio <= a.tis_max);
-        g = tm ? g : 0.f;
-    }
-    const float gm = -g;  // through the negation
-    float gu, gc;
-    if (u == c) {
-        gu = 0.5f * gm;
-        gc = 0.5f * gm;
-    } else {
-        gu = (u > c) ? 0.f : gm;
-        gc = (u < c) ? 0.f : gm;
-    }
-    const float in_range = (ratio >= lo_c && ratio <= hi_c) ? 1.f : 0.f;
-    const float g_ratio = gu * A + (gc * A) * in_range;
-    float gn = g_ratio * ratio;
-    if (a.positive_lm_coef != 0.f) gn += (gD * a.positive_lm_coef) * (-(w_doc * mk));
-    return gn;
 }
 
 constexpr int kBwdItems = 4;  // tokens per thread of k_ppo_bwd, strided by the workgroup (fastest of 2, 4, 8, 16)
@@ -556,6 +584,38 @@ __global__ __launch_bounds__(kThreads) void k_ppo_bwd(meshy_ppo_args a, const fl
         const float g = token_grad_v(a, in[q], Aq, Wq, G * scale);
         if (i < a.n_tokens) grad_new[i] = g;
     }
+}
+
+// 256 threads: as fast as 1024 here (the combine is bound by its chains of
+// dependent loads), with a smaller register file to allocate.
+constexpr int kCombineThreads = 256;
+
+// One workgroup: the combine of every tile's partials.
+__global__ __launch_bounds__(kCombineThreads) void k_ppo_combine(meshy_ppo_args a, Workspace ws,
+                                                                 float* __restrict__ out,
+                                                                 float* __restrict__ seg_cnt_out) {
+    ppo_combine<kCombineThreads>(a, ws, out, seg_cnt_out);
+}
+
+// Token mean: grad_new = grad_loss * unit gradient, 4 tokens per thread
+// (16-byte accesses when both buffers are aligned).
+__global__ __launch_bounds__(kThreads) void k_ppo_scale(const float* __restrict__ gu,
+                                                        const float* __restrict__ grad_loss,
+                                                        float* __restrict__ grad_new, int64_t n, bool vec) {
+    const float G = grad_loss[0];
+    const int64_t i = (static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x) * 4;
+    if (vec && i + 4 <= n) {
+        float4 v = *reinterpret_cast<const float4*>(gu + i);
+        v.x *= G;
+        v.y *= G;
+        v.z *= G;
+        v.w *= G;
+        *reinterpret_cast<float4*>(grad_new + i) = v;
+        return;
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k)
+        if (i + k < n) grad_new[i + k] = G * gu[i + k];
 }
 
 // seg_offsets[d] = first token with id >= d, for sorted ids: token i writes
@@ -631,30 +691,43 @@ extern "C" int meshy_ppo_loss_fwd(const meshy_ppo_args* args, float* out, float*
                          ws_bytes(a.n_tokens, a.n_docs));
     const Workspace ws = ws_of(a.workspace, a.n_tokens);
     const int64_t nt = n_tiles_of(a.n_tokens);
-    if (nt > 0) {
-        const bool lean = !a.use_icepop && !a.rollout_lp && !a.entropy && !a.adv_per_token;
-        if (lean)
-            hipLaunchKernelGGL(k_ppo_tiles<true>, dim3(static_cast<unsigned>(nt)), dim3(kThreads), 0, stream, a, ws);
-        else
-            hipLaunchKernelGGL(k_ppo_tiles<false>, dim3(static_cast<unsigned>(nt)), dim3(kThreads), 0, stream, a, ws);
-        rc = check_launch("meshy_ppo_loss_fwd(tiles)");
-        if (rc) return rc;
+    if (nt == 0) {
+        hipLaunchKernelGGL(k_ppo_combine, dim3(1), dim3(kCombineThreads), 0, stream, a, ws, out, seg_cnt);
+        return check_launch("meshy_ppo_loss_fwd(combine)");
     }
-    hipLaunchKernelGGL(k_ppo_final, dim3(1), dim3(kFinalThreads), 0, stream, a, ws, out, seg_cnt);
-    return check_launch("meshy_ppo_loss_fwd(final)");
+    const bool lean = !a.use_icepop && !a.rollout_lp && !a.entropy && !a.adv_per_token;
+    auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
+    const bool vec = al16(a.new_lp) && al16(a.old_lp) && al16(a.mask) && al16(a.rollout_lp) && al16(a.entropy) &&
+                     (!a.adv_per_token || al16(a.adv));
+    if (lean)
+        hipLaunchKernelGGL(k_ppo_tiles<true>, dim3(static_cast<unsigned>(nt)), dim3(kThreads), 0, stream, a, ws, vec);
+    else
+        hipLaunchKernelGGL(k_ppo_tiles<false>, dim3(static_cast<unsigned>(nt)), dim3(kThreads), 0, stream, a, ws, vec);
+    rc = check_launch("meshy_ppo_loss_fwd(tiles)");
+    if (rc) return rc;
+    hipLaunchKernelGGL(k_ppo_combine, dim3(1), dim3(kCombineThreads), 0, stream, a, ws, out, seg_cnt);
+    return check_launch("meshy_ppo_loss_fwd(combine)");
 }
 
 extern "C" int meshy_ppo_loss_bwd(const meshy_ppo_args* args, const float* seg_cnt, const float* grad_loss,
                                   float* grad_new, hipStream_t stream) {
     using namespace meshy;
     clear_error();
-    if (!args || !seg_cnt || !grad_loss || !grad_new)
-        return set_error(MESHY_ENULL, "meshy_ppo_loss_bwd: args, seg_cnt, grad_loss and grad_new are required");
+    if (!args || !grad_loss || !grad_new)
+        return set_error(MESHY_ENULL, "meshy_ppo_loss_bwd: args, grad_loss and grad_new are required");
     const meshy_ppo_args& a = *args;
     int rc = validate(a, "meshy_ppo_loss_bwd");
     if (rc) return rc;
-    const int64_t nt = n_tiles_of(a.n_tokens);
-    if (nt == 0) return MESHY_OK;
+    if (a.n_tokens == 0) return MESHY_OK;
+    if (a.grad_unit && a.per_token_loss) {
+        const int64_t nb = ceil_div(ceil_div(a.n_tokens, 4), static_cast<int64_t>(kThreads));
+        const bool vec = reinterpret_cast<uintptr_t>(a.grad_unit) % 16 == 0 &&
+                         reinterpret_cast<uintptr_t>(grad_new) % 16 == 0;
+        hipLaunchKernelGGL(k_ppo_scale, dim3(static_cast<unsigned>(nb)), dim3(kThreads), 0, stream, a.grad_unit,
+                           grad_loss, grad_new, a.n_tokens, vec);
+        return check_launch("meshy_ppo_loss_bwd(scale)");
+    }
+    if (!seg_cnt) return set_error(MESHY_ENULL, "meshy_ppo_loss_bwd: seg_cnt is required without grad_unit");
     const int64_t nb = ceil_div(a.n_tokens, static_cast<int64_t>(kThreads) * kBwdItems);
     hipLaunchKernelGGL(k_ppo_bwd, dim3(static_cast<unsigned>(nb)), dim3(kThreads), 0, stream, a, seg_cnt,
                        grad_loss, grad_new);

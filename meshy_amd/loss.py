@@ -6,8 +6,9 @@ attributes the reference reads (trainer.py:705-848): ``ppo_clip_eps_low/high``,
 ``positive_lm_loss_coef``, ``old_logprobs_source``, ``sharder`` and
 ``parallel_dims.cp``; it can be called unbound on a ``SimpleNamespace`` like the
 reference's tests do.  The forward is ``meshy_ppo_loss_fwd`` (one tiled pass over
-the tokens plus one combine), the gradient with respect to ``new_lp`` is
-``meshy_ppo_loss_bwd``; both are wrapped in an autograd Function so
+the tokens plus one combine; with the token-mean reduction the pass also
+writes each token's unit gradient), the gradient with respect to
+``new_lp`` is ``meshy_ppo_loss_bwd``; both are wrapped in an autograd Function so
 ``loss.backward()`` works as before.  ``reduce_mini_metrics`` is
 _reduce_mini_metrics (trainer.py:1020-1047).
 """
@@ -25,19 +26,33 @@ from . import _lib
 def batch_segment_offsets(mb: Any) -> torch.Tensor:
     """``segment_offsets`` of a micro-batch's ``doc_ids`` over its ``n_docs + 1``
     slots, cached on the batch object: the PPO and distillation losses of one
-    micro (forward, backward, later epochs) share it.  The cache key includes the
-    tensor's version counter, so an in-place change of ``doc_ids`` recomputes."""
+    micro (forward, backward, later epochs) share it.  A batch from the pack
+    kernels carries the offsets the pack wrote.  The keys include the tensor's
+    version counter, so an in-place change of ``doc_ids`` recomputes."""
     ids = mb.doc_ids
     key = (id(ids), ids._version, ids.data_ptr(), int(mb.n_docs))
     hit = getattr(mb, "_meshy_seg_offsets", None)
     if hit is not None and hit[0] == key:
         return hit[1]
-    off = segment_offsets(ids, int(mb.n_docs) + 1)
+    src = getattr(mb, "_meshy_seg_src", None)
+    if src is not None and src[0] == key:
+        # Written by the pack kernel next to doc_ids: no pass over the ids.
+        off = src[1][src[2]:src[2] + key[3] + 2]
+    else:
+        off = segment_offsets(ids, int(mb.n_docs) + 1)
     try:
         object.__setattr__(mb, "_meshy_seg_offsets", (key, off))
     except (AttributeError, TypeError):
         pass  # a batch type without an attribute dict: no cache
     return off
+
+
+def _flat_f32(t: torch.Tensor) -> torch.Tensor:
+    """A detached, contiguous fp32 view of ``t`` (a copy only when needed)."""
+    t = t.detach()
+    if t.dtype == torch.float32 and t.is_contiguous():
+        return t.view(-1)
+    return t.reshape(-1).to(torch.float32).contiguous()
 
 
 def segment_offsets(doc_ids: torch.Tensor, n_slots: int, check_sorted: bool = False) -> torch.Tensor:
@@ -59,14 +74,13 @@ class _Inputs:
     def __init__(self, stub, new_lp, old_lp, mb, mini, entropy) -> None:
         dev = new_lp.device
         self.n_tokens = new_lp.numel()
-        self.old = old_lp.detach().reshape(-1).to(torch.float32).contiguous()
-        self.mask = mb.mask.reshape(-1).to(torch.float32).contiguous()
-        self.rollout = (None if mb.rollout_logprobs is None else
-                        mb.rollout_logprobs.detach().reshape(-1).to(torch.float32).contiguous())
-        self.entropy = None if entropy is None else entropy.detach().reshape(-1).to(torch.float32).contiguous()
+        self.old = _flat_f32(old_lp)
+        self.mask = _flat_f32(mb.mask)
+        self.rollout = None if mb.rollout_logprobs is None else _flat_f32(mb.rollout_logprobs)
+        self.entropy = None if entropy is None else _flat_f32(entropy)
         adv = mb.advantages
         self.adv_per_token = adv.dim() != 1
-        self.adv = adv.detach().reshape(-1).to(torch.float32).contiguous()
+        self.adv = _flat_f32(adv)
         self.n_docs = int(mb.n_docs)
         self.use_icepop = bool(getattr(stub, "use_icepop", False))
         self.use_tis = bool(stub.use_tis) and not self.use_icepop
@@ -105,8 +119,9 @@ class _Inputs:
         self.n_docs_global = int(mini.n_docs_global)
         self.n_tokens_global = int(mini.n_tokens_global)
 
-    def args(self, new_flat: torch.Tensor) -> _lib.PpoArgs:
+    def args(self, new_flat: torch.Tensor, grad_unit: torch.Tensor | None = None) -> _lib.PpoArgs:
         a = _lib.PpoArgs()
+        a.grad_unit = _lib.ptr(grad_unit)
         a.new_lp = new_flat.data_ptr()
         a.old_lp = self.old.data_ptr()
         a.mask = self.mask.data_ptr()
@@ -140,15 +155,27 @@ class _PPOLoss(torch.autograd.Function):
     @staticmethod
     def forward(ctx, new_flat, inputs: _Inputs):
         dev = new_flat.device
-        out = torch.empty(_lib.PPO_NOUT, dtype=torch.float32, device=dev)
-        seg_cnt = torch.empty(inputs.n_docs + 1, dtype=torch.float32, device=dev)
-        a = inputs.args(new_flat)
-        rc = _lib.load().meshy_ppo_loss_fwd(_lib.ctypes.byref(a), out.data_ptr(), seg_cnt.data_ptr(),
+        # out[:NOUT] receives the sums; the loss handed to autograd is a view of
+        # its total-loss entry (no copy launched).
+        buf = torch.empty(_lib.PPO_NOUT + 1, dtype=torch.float32, device=dev)
+        # Token mean: the forward also writes each token's gradient at a unit
+        # loss gradient, so the backward is one scale.  Sequence mean: the
+        # backward needs the per-document counts.
+        unit = None
+        seg_cnt = None
+        if inputs.want_grad and inputs.per_token:
+            unit = torch.empty_like(new_flat)
+        elif inputs.want_grad:
+            seg_cnt = torch.empty(inputs.n_docs + 1, dtype=torch.float32, device=dev)
+        a = inputs.args(new_flat, unit)
+        rc = _lib.load().meshy_ppo_loss_fwd(_lib.ctypes.byref(a), buf.data_ptr(), _lib.ptr(seg_cnt),
                                             _lib.stream_of(dev))
         _lib.check(rc, "meshy_ppo_loss_fwd")
         ctx.inputs = inputs
-        ctx.save_for_backward(new_flat, seg_cnt)
-        loss = out[1].clone()
+        ctx.args = a
+        ctx.save_for_backward(new_flat, seg_cnt if unit is None else unit)
+        out = buf[:_lib.PPO_NOUT]
+        loss = buf[1]
         ctx.mark_non_differentiable(out)
         # The backward reads only the loss's gradient: no zero tensor for `out`'s.
         ctx.set_materialize_grads(False)
@@ -158,12 +185,14 @@ class _PPOLoss(torch.autograd.Function):
     def backward(ctx, grad_loss, grad_out):
         if grad_loss is None:
             return None, None
-        new_flat, seg_cnt = ctx.saved_tensors
-        inputs: _Inputs = ctx.inputs
-        g = grad_loss.reshape(1).to(torch.float32).contiguous()
+        new_flat, saved = ctx.saved_tensors
+        g = grad_loss.reshape(1)
+        if g.dtype != torch.float32:
+            g = g.float()
         grad = torch.empty_like(new_flat)
-        a = inputs.args(new_flat)
-        rc = _lib.load().meshy_ppo_loss_bwd(_lib.ctypes.byref(a), seg_cnt.data_ptr(), g.data_ptr(),
+        a = ctx.args  # carries grad_unit when the forward wrote it
+        seg_cnt = None if a.grad_unit else saved
+        rc = _lib.load().meshy_ppo_loss_bwd(_lib.ctypes.byref(a), _lib.ptr(seg_cnt), g.data_ptr(),
                                             grad.data_ptr(), _lib.stream_of(new_flat.device))
         _lib.check(rc, "meshy_ppo_loss_bwd")
         return grad, None
@@ -184,6 +213,7 @@ def ppo_clip_loss(
             "context-parallel PPO loss needs the per-document all-reduce between the two "
             "kernel phases; this library drives one GPU")
     inputs = _Inputs(self, new_lp, old_lp, mb, mini, entropy)
+    inputs.want_grad = torch.is_grad_enabled() and new_lp.requires_grad
     new_flat = new_lp.reshape(-1)
     if new_flat.dtype != torch.float32:
         new_flat = new_flat.float()

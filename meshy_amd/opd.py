@@ -17,7 +17,7 @@ the distillation loss with its metrics.
 
 from __future__ import annotations
 
-from dataclasses import dataclass
+from dataclasses import dataclass, fields
 from typing import Any, Sequence
 
 import torch
@@ -28,6 +28,8 @@ from .batch import TEACHER_FIELDS, Batch, launch_pack, stage_micro_batches
 from .loss import batch_segment_offsets
 from .plan import Layout, MicroPlan
 from .topk import gather_logprobs
+
+_BATCH_FIELDS = tuple(f.name for f in fields(Batch))
 
 OPD_TEACHER_FIELDS = list(TEACHER_FIELDS)
 
@@ -73,7 +75,10 @@ def build_topk_micro_batches(
             shape = (m.n_rows, m.seq_len, 1) if layout == "padded" else (1, m.seq_len, 1)
             ids = torch.zeros(shape, dtype=torch.int64, device=job.device)
             lps = torch.zeros(shape, dtype=torch.float32, device=job.device)
-        out.append(TopKBatch(**vars(mb), teacher_topk_ids=ids, teacher_topk_logprobs=lps))
+        kw = {f: getattr(mb, f) for f in _BATCH_FIELDS}
+        tb = TopKBatch(**kw, teacher_topk_ids=ids, teacher_topk_logprobs=lps)
+        tb._meshy_seg_src = mb._meshy_seg_src  # the pack's document offsets (same doc_ids)
+        out.append(tb)
     return out
 
 

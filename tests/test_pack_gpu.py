@@ -177,6 +177,32 @@ def test_grpo_256_samples_full_plan_bit_exact(dev, layout, align):
         _assert_same(mb, ref, layout)
 
 
+@pytest.mark.parametrize("layout", ["packed", "padded"])
+def test_pack_writes_the_segment_offsets_of_every_micro(dev, layout):
+    """The offsets the pack writes next to cu_seqlens equal those computed from
+    doc_ids (searchsorted of the flattened ids), fillers and truncated
+    documents included, and the losses take them without another pass."""
+    from meshy_amd import workloads
+    from meshy_amd.batch import build_micro_batches
+    from meshy_amd.loss import batch_segment_offsets
+    from meshy_amd.plan import MicroPlan, PlannerConfig, build_plan
+
+    batch, rewards, _ = workloads.grpo_256_samples(0)
+    samples = batch.sample_dicts(rewards=rewards, advantages=rewards)
+    cfg = PlannerConfig(layout=layout, mini_batch_size=64, seq_len=4096, align=64,
+                        max_tokens_per_micro=8192 if layout == "packed" else 16384)
+    plan = build_plan(np.minimum(batch.lengths, 4096).tolist(), batch.loss_tokens(4096).tolist(), 1, cfg)
+    local = plan.local_samples(samples, 0)
+    micros = [m for mini in plan.per_rank[0] for m in mini.micros] + [MicroPlan((), 64, ())]
+    mbs = build_micro_batches(local, micros, layout=layout, device=dev, sharder=_NoCp(), need_rollout_lp=True)
+    for mb in mbs:
+        ids = mb.doc_ids.reshape(-1).cpu()
+        want = torch.searchsorted(ids, torch.arange(mb.n_docs + 2), right=False)
+        got = batch_segment_offsets(mb)
+        assert got.dtype == torch.int64 and torch.equal(got.cpu(), want), (mb.n_docs, got, want)
+        assert getattr(mb, "_meshy_seg_src")[1].data_ptr() == got.untyped_storage().data_ptr()
+
+
 def test_16_long_sequences_micros(dev):
     """Long-context planner edge cases materialised: exact-budget fits and a full 131072 micro."""
     from meshy_amd import workloads
