@@ -443,6 +443,12 @@ int meshy_ppo_loss_bwd(const meshy_ppo_args* args, const float* seg_cnt,
  * Inputs are [rows, S] row-major.  doc_ids in [0, n_docs] (n_docs = padding
  * slot).  values are fp32 (values_bf16 = 0) or bf16 (values_bf16 = 1).
  * lengths ([n_docs] fp32) may be NULL: each document's masked count is used.
+ * seg_offsets ([n_docs + 2], nullable) are the segment offsets of doc_ids
+ * (meshy_segment_offsets) when the flattened ids are non-decreasing, as in
+ * both batch layouts: without lengths the masked counts are then fixed-order
+ * sums (the same bits on every call, fractional masks included); without
+ * offsets they are fp32 atomic sums, exact for 0/1 masks and order-dependent
+ * in their last bits for fractional ones.
  * Outputs: adv [rows*S] (nullable), returns [rows*S] (nullable, decay gamma),
  * lam_doc [n_docs] (nullable).
  * ---------------------------------------------------------------------- */
@@ -464,6 +470,7 @@ typedef struct meshy_gae_args {
     float* lam_doc;
     void* workspace;
     size_t workspace_bytes;
+    const int64_t* seg_offsets;    /* nullable, see above                     */
 } meshy_gae_args;
 
 size_t meshy_gae_workspace_size(int64_t rows, int64_t S, int64_t n_docs);

@@ -194,6 +194,7 @@ class GaeArgs(ctypes.Structure):
         ("lam_doc", c_void_p),
         ("workspace", c_void_p),
         ("workspace_bytes", c_size_t),
+        ("seg_offsets", c_void_p),
     ]
 
 
@@ -309,7 +310,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 _LIB: ctypes.CDLL | None = None
 

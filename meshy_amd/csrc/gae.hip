@@ -8,8 +8,12 @@
 // the end of each row, at a document change and at a mask hole, so the whole
 // [rows, S] grid is one flattened sequence and no segment bookkeeping is
 // needed beyond a_t = 0.  Maps compose as (p1, q1) o (p2, q2) = (p1 p2, q1 + p1 q2):
-//   k_gae_count  masked token count per document (index_add, gae.py:264-269),
-//                only when lengths are not given;
+//   k_gae_doc_count / k_gae_count  masked token count per document
+//                (index_add, gae.py:264-269), only when lengths are not given:
+//                one workgroup per document over its segment offsets, a
+//                fixed-order sum (bitwise reproducible), when the caller
+//                passes the offsets of non-decreasing ids; otherwise fp32
+//                atomics (exact for 0/1 masks);
 //   k_gae_chunks each workgroup folds a chunk of kChunk tokens into one map
 //                per scan (advantages and returns);
 //   k_gae_groups one wave per group of 64 chunks folds their maps into one,
@@ -18,7 +22,8 @@
 //                of its group to its right and of the groups to its right,
 //                re-folds its chunk, scans its threads from the right seeded
 //                with the carry, and writes A_t and G_t.
-// Every fold has a fixed order, so the results do not depend on timing.  The
+// Every fold of the scan has a fixed order, so the results do not depend on
+// timing (the atomic count aside).  The
 // apply pass visits each XCD's chunks from the highest down, so that it first
 // re-reads what the chunks pass read last (still in L2 or the Infinity Cache).
 // Everything is fp32, like the reference's sequential fallback.
@@ -264,6 +269,28 @@ __global__ __launch_bounds__(kCountThreads) void k_gae_count(meshy_gae_args g, f
         acc += g.mask[t];
     }
     if (cur >= 0 && cur <= g.n_docs && acc != 0.f) atomicAdd(cnt + cur, acc);
+}
+
+// Masked token count of document blockIdx.x over its offsets range: every
+// thread sums a fixed set of positions (four loads in flight), then a
+// fixed-order block sum; the result does not depend on timing.
+__global__ __launch_bounds__(kCountThreads) void k_gae_doc_count(const float* __restrict__ mask,
+                                                                 const int64_t* __restrict__ off,
+                                                                 float* __restrict__ cnt) {
+    __shared__ float s_red[kCountThreads / kWave];
+    const int64_t d = blockIdx.x;
+    const int64_t lo = off[d];
+    const int64_t hi = off[d + 1];
+    float acc = 0.f;
+    int64_t t = lo + threadIdx.x;
+    for (; t + 3 * kCountThreads < hi; t += 4 * kCountThreads) {
+        const float a0 = mask[t], a1 = mask[t + kCountThreads], a2 = mask[t + 2 * kCountThreads],
+                    a3 = mask[t + 3 * kCountThreads];
+        acc += (a0 + a1) + (a2 + a3);
+    }
+    for (; t < hi; t += kCountThreads) acc += mask[t];
+    acc = block_sum<kCountThreads>(acc, s_red);
+    if (threadIdx.x == 0) cnt[d] = acc;
 }
 
 // Builds the thread's maps (contiguous positions) and folds them right to left.
@@ -559,10 +586,17 @@ int gae_launch(const meshy_gae_args& g, hipStream_t stream) {
         return set_error(MESHY_ESPACE, "meshy_gae: workspace needs %zu bytes", ws_bytes(n, g.n_docs));
     const int64_t nc = n_chunks_of(n);
     if (nc > INT32_MAX) return set_error(MESHY_EINVAL, "meshy_gae: too many tokens");
+    if (g.n_docs > INT32_MAX) return set_error(MESHY_EINVAL, "meshy_gae: too many documents");
     const Workspace ws = ws_of(g.workspace, n, g.n_docs);
     int rc;
     // Document lengths only matter for lambda (advantages / lam_doc), not for returns.
-    if (!g.lengths && (g.adv || g.lam_doc)) {
+    if (!g.lengths && (g.adv || g.lam_doc) && g.seg_offsets) {
+        if (g.n_docs > 0) {
+            hipLaunchKernelGGL(k_gae_doc_count, dim3(static_cast<unsigned>(g.n_docs)), dim3(kCountThreads), 0,
+                               stream, g.mask, g.seg_offsets, ws.cnt);
+            if ((rc = check_launch("meshy_gae(count)"))) return rc;
+        }
+    } else if (!g.lengths && (g.adv || g.lam_doc)) {
         const int64_t nz = g.n_docs + 1;
         hipLaunchKernelGGL(k_gae_zero, dim3(static_cast<unsigned>(ceil_div(nz, kThreads))), dim3(kThreads), 0, stream,
                            ws.cnt, nz);

@@ -5,7 +5,10 @@ meshy/backend/titan/critic/gae.py.
 run the ``meshy_gae`` kernels: the recursion ``A_t = x_t + decay_t * cont_t *
 A_{t+1}`` as a reverse scan of affine maps over the flattened ``[rows, S]``
 grid, in fp32, with no closed form and therefore no underflow fallback
-(gae.py:149-150).  ``gae_and_returns`` produces both in one pass.
+(gae.py:149-150).  ``gae_and_returns`` produces both in one pass.  When the
+flattened doc_ids are non-decreasing (both batch layouts) and no lengths are
+given, the kernels take their segment offsets: the masked document lengths
+are then fixed-order sums, bitwise reproducible for fractional masks too.
 """
 
 from __future__ import annotations
@@ -16,10 +19,34 @@ import numpy as np
 import torch
 
 from . import _lib
+from .loss import segment_offsets
+
+# Segment offsets of recently seen doc_ids tensors (each entry holds its
+# tensor, so the identity in the key stays unique while cached).
+_OFFSETS: dict[tuple, tuple[torch.Tensor, torch.Tensor | None]] = {}
+_OFFSETS_MAX = 8
+
+
+def _doc_offsets(doc_ids: torch.Tensor, ids: torch.Tensor, n_docs: int) -> torch.Tensor | None:
+    """The segment offsets of ``doc_ids`` over its ``n_docs + 1`` slots when its
+    flattened values are non-decreasing (checked once per tensor version, one
+    device sync), else None: the kernels then read every token's id."""
+    key = (id(doc_ids), doc_ids._version, doc_ids.data_ptr(), int(n_docs))
+    hit = _OFFSETS.get(key)
+    if hit is not None:
+        return hit[1]
+    try:
+        off = segment_offsets(ids, int(n_docs) + 1, check_sorted=True)
+    except ValueError:
+        off = None
+    if len(_OFFSETS) >= _OFFSETS_MAX:
+        _OFFSETS.pop(next(iter(_OFFSETS)))
+    _OFFSETS[key] = (doc_ids, off)
+    return off
 
 
 def _run(rewards, values, mask, doc_ids, n_docs, *, lengths, gamma, alpha, epsilon, want_adv,
-         want_returns, want_lam):
+         want_returns, want_lam, offsets=True):
     if rewards.dim() != 2:
         raise ValueError(f"expected [rows, S] tensors, got {tuple(rewards.shape)}")
     rows, S = rewards.shape
@@ -61,6 +88,10 @@ def _run(rewards, values, mask, doc_ids, n_docs, *, lengths, gamma, alpha, epsil
     g.lam_doc = _lib.ptr(lam)
     g.workspace = ws.data_ptr()
     g.workspace_bytes = ws.numel()
+    # The offsets serve the masked document lengths, needed without `lengths`.
+    need = lens is None and (want_adv or want_lam) and n_docs > 0 and rows * S > 0
+    off = _doc_offsets(doc_ids, ids, n_docs) if offsets and need else None
+    g.seg_offsets = _lib.ptr(off)
     rc = lib.meshy_gae(_lib.ctypes.byref(g), _lib.stream_of(dev))
     _lib.check(rc, "meshy_gae")
     return adv, ret, (lam[:n_docs] if lam is not None else None)
@@ -93,7 +124,7 @@ def compute_returns(
 ) -> torch.Tensor:
     """Discounted return-to-go G_t = r_t + gamma * cont_t * G_{t+1} (gae.py:183-205)."""
     _, ret, _ = _run(rewards, None, mask, doc_ids, 0, lengths=None, gamma=gamma, alpha=1.0,
-                     epsilon=1e-6, want_adv=False, want_returns=True, want_lam=False)
+                     epsilon=1e-6, want_adv=False, want_returns=True, want_lam=False, offsets=False)
     return ret
 
 

@@ -202,6 +202,47 @@ def test_scan_is_deterministic(dev):
         assert all(torch.equal(a, b) for a, b in zip(first, again))
 
 
+def test_fractional_mask_without_lengths_is_deterministic(dev):
+    """A fractional mask and no lengths: the masked document lengths (and so
+    lambda and the advantages) come from fixed-order sums over each
+    document's offsets range, the same bits on every call, and match the
+    oracle's index_add lengths (gae.py:264-269)."""
+    from meshy_amd.gae import gae_and_returns
+
+    rewards, values, mask, doc_ids, n_docs = _random_grid(4, 9000, 5, seed=21)
+    g = torch.Generator().manual_seed(22)
+    mask = mask * (torch.rand(mask.shape, generator=g) * 0.9 + 0.1)
+    d = [t.to(dev) for t in (rewards, values, mask, doc_ids)]
+    first = gae_and_returns(*d, n_docs, gamma=0.99, alpha=1.5)
+    for _ in range(4):
+        again = gae_and_returns(*d, n_docs, gamma=0.99, alpha=1.5)
+        assert all(torch.equal(a, b) for a, b in zip(first, again))
+    ref_adv, ref_lam = ogae.compute_vapo_gae(rewards, values, mask, doc_ids, n_docs, gamma=0.99, alpha=1.5)
+    assert (first[0].cpu() - ref_adv).abs().max().item() <= TOL
+    assert (first[2].cpu() - ref_lam).abs().max().item() <= 1e-6
+
+
+@pytest.mark.parametrize("docs_per_row", [3, 40, 700])
+def test_offsets_and_atomic_counts_agree(dev, docs_per_row):
+    """0/1 masks without lengths: the per-document counts from the segment
+    offsets (fixed order) and from the atomic path are the same integers, so
+    bitwise equal lambdas, advantages and returns; empty document slots
+    included."""
+    from meshy_amd import gae
+
+    rewards, values, mask, doc_ids, n_docs = _random_grid(3, 12000, docs_per_row, seed=docs_per_row)
+    doc_ids = doc_ids * 2  # every other slot empty
+    n_docs = 2 * n_docs
+    d = [t.to(dev) for t in (rewards, values, mask, doc_ids)]
+    kw = dict(lengths=None, gamma=0.98, alpha=1.5, epsilon=1e-6, want_adv=True, want_returns=True, want_lam=True)
+    a0, r0, l0 = gae._run(*d, n_docs, offsets=True, **kw)
+    a1, r1, l1 = gae._run(*d, n_docs, offsets=False, **kw)
+    assert torch.equal(a0, a1) and torch.equal(r0, r1) and torch.equal(l0, l1)
+    ref_adv, ref_lam = ogae.compute_vapo_gae(rewards, values, mask, doc_ids, n_docs, gamma=0.98, alpha=1.5)
+    assert (a0.cpu() - ref_adv).abs().max().item() <= TOL
+    assert (l0.cpu() - ref_lam).abs().max().item() <= 1e-6
+
+
 def _critic_samples(n, seed, max_len=700, bf16=False):
     g = torch.Generator().manual_seed(seed)
     out = []
