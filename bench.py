@@ -363,22 +363,41 @@ def bench_pack(runs, no_cpu):
     wall = _wall_ms(full, runs, warmup=3, before=drop)
     lite = _wall_ms(lambda: res.__setitem__("r", pack_step(ragged, cfg, dev, with_plan_objects=False)), runs,
                     warmup=2, before=drop)
+
+    fields = ("input_ids", "labels", "positions", "mask", "doc_ids", "advantages", "rollout_logprobs", "lengths",
+              "attention_masks", "positive_lm_weights", "advantage_tokens")
+
+    def full_views():
+        r = pack_step(ragged, cfg, dev)
+        for mb in r.batches:
+            for name in fields:
+                getattr(mb, name)
+        res["r"] = r
+
+    wall_views = _wall_ms(full_views, runs, warmup=2, before=drop)
     full()
 
-    def host_plan():
-        lengths, loss = ragged.sample_lengths(8192)
-        from meshy_amd.plan import plan_tables
+    from meshy_amd.plan import plan_tables, tables_to_plan
 
-        plan_tables(lengths, loss, 1, cfg)
-
-    plan_ms = _wall_ms(host_plan, runs, gpu=False)
+    lengths, loss = ragged.sample_lengths(8192)
+    tables = plan_tables(lengths, loss, 1, cfg)
+    count_ms = _wall_ms(lambda: ragged.sample_lengths(8192), runs, gpu=False)
+    plan_ms = _wall_ms(lambda: plan_tables(lengths, loss, 1, cfg), runs, gpu=False)
+    dc_ms = _wall_ms(lambda: tables_to_plan(tables), runs, gpu=False)
     r = res["r"]
     n_out = sum(mb.input_ids.numel() for mb in r.batches)
     real = int(sum(m.n_tokens for m in (mm for mini in r.plan.per_rank[0] for mm in mini.micros)))
     out = {
+        # plan + staging + the two host-to-device copies + GRPO + pack kernels,
+        # device-synchronized; each micro's Batch tensors are views made when
+        # the trainer first reads them (as it builds each micro when reaching it)
         "pack_latency_us": round(wall * 1e3, 1),
         "pack_latency_no_dataclasses_us": round(lite * 1e3, 1),
-        "host_plan_us": round(plan_ms * 1e3, 1),
+        # the same with every field of every micro's Batch read once (all views made)
+        "pack_latency_all_views_us": round(wall_views * 1e3, 1),
+        "host_phases_us": {"loss_token_count": round(count_ms * 1e3, 1), "planner": round(plan_ms * 1e3, 1),
+                           "plan_dataclasses": round(dc_ms * 1e3, 1)},
+        "host_plan_us": round((count_ms + plan_ms) * 1e3, 1),
         "n_micro": len(r.batches),
         "tokens": real,
         "out_tokens": n_out,

@@ -51,16 +51,17 @@ class PlannerCfg(ctypes.Structure):
 
 
 class PlanOut(ctypes.Structure):
+    # int32_t* / int64_t* tables, set from numpy addresses
     _fields_ = [
-        ("local_indices", POINTER(c_int32)),
-        ("mini_n_micro", POINTER(c_int32)),
-        ("mini_n_docs_global", POINTER(c_int64)),
-        ("mini_n_tokens_global", POINTER(c_int64)),
-        ("mini_tokens_per_rank", POINTER(c_int64)),
-        ("micro_seq_len", POINTER(c_int64)),
-        ("micro_doc_start", POINTER(c_int32)),
-        ("doc_sample", POINTER(c_int32)),
-        ("doc_len", POINTER(c_int64)),
+        ("local_indices", c_void_p),
+        ("mini_n_micro", c_void_p),
+        ("mini_n_docs_global", c_void_p),
+        ("mini_n_tokens_global", c_void_p),
+        ("mini_tokens_per_rank", c_void_p),
+        ("micro_seq_len", c_void_p),
+        ("micro_doc_start", c_void_p),
+        ("doc_sample", c_void_p),
+        ("doc_len", c_void_p),
         ("n_micro_total", c_int32),
         ("reserved", c_int32),
     ]

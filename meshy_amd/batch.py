@@ -115,6 +115,10 @@ class _Layout:
         lo, hi, dtype = self.regions[name]
         return buf[lo:hi].view(dtype)
 
+    def addr(self, base: int, name: str) -> int:
+        """Address of a region inside a buffer that starts at ``base``."""
+        return base + self.regions[name][0]
+
 
 def _scalar_of(v, default: float) -> float:
     if v is None:
@@ -371,25 +375,26 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
     seg = torch.empty(n_docs_total + 2 * n_micro, dtype=torch.int64, device=device)
 
     a = _lib.PackArgs()
-    a.tokens = lay.view(dbuf, "tokens").data_ptr()
+    base = dbuf.data_ptr()
+    a.tokens = lay.addr(base, "tokens")
     a.tokens_elem_bytes = lay.regions["tokens"][2].itemsize
     a.layout = _lib.MESHY_LAYOUT_PACKED if layout == "packed" else _lib.MESHY_LAYOUT_PADDED
-    a.mask = lay.view(dbuf, "mask").data_ptr()
-    a.logprobs = lay.view(dbuf, "logprobs").data_ptr() if job.need_rollout_lp else None
+    a.mask = lay.addr(base, "mask")
+    a.logprobs = lay.addr(base, "logprobs") if job.need_rollout_lp else None
     if job.adv_tokens_dev is not None:
         a.adv_tokens = job.adv_tokens_dev.data_ptr()
     else:
-        a.adv_tokens = lay.view(dbuf, "adv_tokens").data_ptr() if job.per_token_adv else None
+        a.adv_tokens = lay.addr(base, "adv_tokens") if job.per_token_adv else None
     a.adv_samples = (job.adv_samples.data_ptr() if job.adv_samples is not None
-                     else lay.view(dbuf, "adv_samples").data_ptr())
-    a.sample_offsets = lay.view(dbuf, "s_off").data_ptr()
+                     else lay.addr(base, "adv_samples"))
+    a.sample_offsets = lay.addr(base, "s_off")
     a.n_samples = job.n_samples
     a.n_micro = n_micro
-    a.micro_seq_len = lay.view(dbuf, "seq").data_ptr()
-    a.micro_out_off = lay.view(dbuf, "out_off").data_ptr()
-    a.micro_doc_start = lay.view(dbuf, "doc_start").data_ptr()
-    a.doc_sample = lay.view(dbuf, "doc_sample").data_ptr()
-    a.doc_len = lay.view(dbuf, "doc_len").data_ptr()
+    a.micro_seq_len = lay.addr(base, "seq")
+    a.micro_out_off = lay.addr(base, "out_off")
+    a.micro_doc_start = lay.addr(base, "doc_start")
+    a.doc_sample = lay.addr(base, "doc_sample")
+    a.doc_len = lay.addr(base, "doc_len")
     a.max_micro_elems = job.max_elems
     a.max_docs_per_micro = job.max_docs
     a.input_ids = input_ids.data_ptr()
@@ -409,53 +414,23 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
         t_ids = torch.empty(n_out * K, dtype=torch.int64, device=device)
         t_lps = torch.empty(n_out * K, dtype=torch.float32, device=device)
         a.teacher_k = K
-        a.teacher_ids = lay.view(dbuf, "teacher_ids").data_ptr()
+        a.teacher_ids = lay.addr(base, "teacher_ids")
         a.teacher_ids_elem_bytes = lay.regions["teacher_ids"][2].itemsize
-        a.teacher_lps = lay.view(dbuf, "teacher_lps").data_ptr()
+        a.teacher_lps = lay.addr(base, "teacher_lps")
         a.teacher_ids_out = t_ids.data_ptr()
         a.teacher_lps_out = t_lps.data_ptr()
     rc = lib.meshy_pack_micro_batches(_lib.ctypes.byref(a), torch.cuda.current_stream(device).cuda_stream)
     _lib.check(rc, "meshy_pack_micro_batches")
     pos_w_dev = lay.view(dbuf, "pos_w")
-
-    # Per-micro views, one torch.split per output (the per-micro slicing of
-    # seven tensors is what the host time of a pack is otherwise made of).
-    sizes = np.diff(job.out_off).tolist()
-    rows_l = job.rows.tolist()
-    seq_l = job.seq.tolist()
-    if layout == "packed":
-        def views(t):
-            return None if t is None else torch.split(t.view(1, -1), sizes, dim=1)
-    else:
-        def views(t):
-            if t is None:
-                return None
-            return [p.view(R, S) for p, R, S in zip(torch.split(t, sizes), rows_l, seq_l)]
-    f_ids, f_lab, f_pos, f_mask, f_doc = (views(input_ids), views(labels), views(positions), views(mask),
-                                          views(doc_ids))
-    f_rl, f_at = views(rollout_lp), views(adv_tok)
-    nd_l = np.diff(job.doc_start).tolist()
-    f_adv = torch.split(adv_doc[:n_docs_total], nd_l)
-    f_len = torch.split(lengths[:n_docs_total], nd_l)
-    f_pw = torch.split(pos_w_dev[:n_docs_total], nd_l)
-    f_cu = None
-    pads = []
-    if layout == "packed":
-        # micro k's cu_seqlens: n_docs + 1 (+1 with a pad doc) slots out of n_docs + 2
-        cu_sizes = []
-        for k, m in enumerate(job.micros):
-            pad = seq_l[k] - m.n_tokens
-            pads.append(pad)
-            n_cu = nd_l[k] + 1 + (1 if pad > 0 else 0)
-            cu_sizes += [n_cu, nd_l[k] + 2 - n_cu]
-        f_cu = torch.split(cu, cu_sizes)[0::2]
+    views = _PackViews(job, sharder, input_ids, labels, positions, mask, doc_ids, rollout_lp, adv_tok, adv_doc,
+                       lengths, pos_w_dev, cu, seg)
 
     if job.teacher_k:
         K = job.teacher_k
-        sizes_k = [n * K for n in sizes]
+        sizes_k = [n * K for n in views.sizes]
         tv = []
-        for part_i, part_l, R, S, m in zip(torch.split(t_ids, sizes_k), torch.split(t_lps, sizes_k), rows_l, seq_l,
-                                           job.micros):
+        for part_i, part_l, R, S, m in zip(torch.split(t_ids, sizes_k), torch.split(t_lps, sizes_k), views.rows,
+                                           views.seq, job.micros):
             if m.is_filler:
                 # infer_top_k of no samples is 1 (opd.py:39-44)
                 tv.append((torch.zeros(R, S, 1, dtype=torch.int64, device=device),
@@ -467,48 +442,147 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
         job.teacher_views = tv
 
     out: list[Batch] = []
-    seg_at = (np.asarray(job.doc_start[:-1], np.int64) + 2 * np.arange(n_micro)).tolist()
-    for k, m in enumerate(job.micros):
-        nd = nd_l[k]
-        ii, lb, ps, mk, di = f_ids[k], f_lab[k], f_pos[k], f_mask[k], f_doc[k]
-        rl = f_rl[k] if f_rl is not None else None
-        at = f_at[k] if f_at is not None else None
-        attn = None
-        if layout == "packed":
-            pad = pads[k]
-            max_len = max(max(m.doc_lens, default=0), pad if pad > 0 else 0)
-            attn = VarlenMetadata(cu_seq_q=f_cu[k], cu_seq_k=f_cu[k], max_q=int(max_len), max_k=int(max_len))
-        elif sharder is not None:
-            # One CP shard call for every per-token tensor (batch.py:195-207);
-            # the identity on one GPU.
-            optional = [t for t in (rl, at) if t is not None]
-            sharded = sharder.shard_seq(ii, lb, ps, mk, di, *optional)
-            ii, lb, ps, mk, di = sharded[:5]
-            rest = list(sharded[5:])
-            if rl is not None:
-                rl = rest.pop(0)
-            if at is not None:
-                at = rest.pop(0)
-        per_token = at if job.per_token_adv else None
-        mb = Batch(
-            input_ids=ii,
-            labels=lb,
-            positions=ps,
-            mask=mk,
-            doc_ids=di,
-            advantages=per_token if per_token is not None else f_adv[k],
-            rollout_logprobs=rl,
-            lengths=f_len[k],
-            n_docs=nd,
-            attention_masks=attn,
-            positive_lm_weights=f_pw[k],
-            advantage_tokens=at if job.broadcast_advantages and not job.per_token_adv else None,
-        )
-        # The kernel's segment offsets of this micro, valid while doc_ids is
-        # the tensor it wrote (the losses' offsets cache checks that).
-        mb._meshy_seg_src = ((id(di), di._version, di.data_ptr(), nd), seg, seg_at[k])
+    new = object.__new__
+    for k in range(n_micro):
+        mb = new(PackedBatch)
+        mb.__dict__.update(n_docs=views.nd[k], _src=views, _k=k)
         out.append(mb)
     return out
+
+
+class _PackViews:
+    """The flat outputs of one pack launch and where each micro lies in them.
+    A micro's tensors are views of these, made when its batch first needs them."""
+
+    def __init__(self, job: PackJob, sharder, input_ids, labels, positions, mask, doc_ids, rollout_lp, adv_tok,
+                 adv_doc, lengths, pos_w, cu, seg) -> None:
+        self.packed = job.layout == "packed"
+        self.sharder = sharder
+        self.per_token_adv = job.per_token_adv
+        self.broadcast_only = job.broadcast_advantages and not job.per_token_adv
+        self.tok = (input_ids, labels, positions, mask, doc_ids, rollout_lp, adv_tok)
+        self.docs = (adv_doc, lengths, pos_w)
+        self.cu, self.seg = cu, seg
+        self.out_off = job.out_off.tolist()
+        self.doc_start = job.doc_start.tolist()
+        self.sizes = np.diff(job.out_off).tolist()
+        self.rows = job.rows.tolist()
+        self.seq = job.seq.tolist()
+        self.nd = np.diff(job.doc_start).tolist()
+        self.micros = job.micros
+        self._tok = self._doc = self._cu = None
+
+    # Each group's views are made for every micro at once, the first time any
+    # micro needs them: one torch.split per tensor (a third of a microsecond
+    # per view) instead of a slice and a view per micro and field.
+
+    def _token_views(self) -> list:
+        if self._tok is None:
+            sizes = self.sizes
+            if self.packed:
+                cols = [None if t is None else torch.split(t.view(1, -1), sizes, dim=1) for t in self.tok]
+            else:
+                cols = [None if t is None else [p.view(R, S) for p, R, S in zip(torch.split(t, sizes), self.rows,
+                                                                                 self.seq)]
+                        for t in self.tok]
+            self._tok = [tuple(None if c is None else c[k] for c in cols) for k in range(len(sizes))]
+        return self._tok
+
+    def tokens(self, mb: "PackedBatch", f: dict) -> None:
+        """input_ids, labels, positions, mask, doc_ids, rollout_logprobs and the
+        advantage tokens of micro mb._k (one CP shard call in the padded layout,
+        batch.py:195-207; the identity on one GPU)."""
+        k = mb._k
+        ii, lb, ps, mk, di, rl, at = self._token_views()[k]
+        if not self.packed and self.sharder is not None:
+            optional = [t for t in (rl, at) if t is not None]
+            sharded = self.sharder.shard_seq(ii, lb, ps, mk, di, *optional)
+            ii, lb, ps, mk, sdi = sharded[:5]
+            rest = list(sharded[5:])
+            rl = rest.pop(0) if rl is not None else None
+            at = rest.pop(0) if at is not None else None
+        else:
+            sdi = di
+        f.update(input_ids=ii, labels=lb, positions=ps, mask=mk, doc_ids=sdi, rollout_logprobs=rl,
+                 advantage_tokens=at if self.broadcast_only else None)
+        if self.per_token_adv:
+            f["advantages"] = at
+        if sdi is di:  # not replaced by a context-parallel shard
+            d0 = self.doc_start[k]
+            mb.__dict__["_meshy_seg_src"] = ((id(di), di._version, di.data_ptr(), self.nd[k]), self.seg, d0 + 2 * k)
+
+    def doc_fields(self, mb: "PackedBatch", f: dict) -> None:
+        """Per-document advantages, lengths and positive-LM weights of micro mb._k."""
+        if self._doc is None:
+            n = self.doc_start[-1]
+            self._doc = [torch.split(t[:n], self.nd) for t in self.docs]
+        adv, lengths, pos_w = (c[mb._k] for c in self._doc)
+        if not self.per_token_adv:
+            f["advantages"] = adv
+        f["lengths"] = lengths
+        f["positive_lm_weights"] = pos_w
+
+    def attention(self, mb: "PackedBatch", f: dict) -> None:
+        """cu_seqlens (n_docs + 1 slots, + 1 with a padding document) and the
+        longest document of micro mb._k, as make_varlen_metadata builds them."""
+        if not self.packed:
+            f["attention_masks"] = None
+            return
+        if self._cu is None:
+            sizes, pads = [], []
+            for k, m in enumerate(self.micros):
+                pad = self.seq[k] - m.n_tokens
+                pads.append(pad)
+                n_cu = self.nd[k] + 1 + (1 if pad > 0 else 0)
+                sizes += [n_cu, self.nd[k] + 2 - n_cu]
+            self._cu = (torch.split(self.cu, sizes)[0::2], pads)
+        cus, pads = self._cu
+        k = mb._k
+        m, pad, cu = self.micros[k], pads[k], cus[k]
+        max_len = max(max(m.doc_lens, default=0), pad if pad > 0 else 0)
+        f["attention_masks"] = VarlenMetadata(cu_seq_q=cu, cu_seq_k=cu, max_q=int(max_len), max_k=int(max_len))
+
+
+class _Lazy:
+    """A field of PackedBatch that is not yet in the instance: made (with its
+    whole group) on first read.  A non-data descriptor, so once the instance
+    holds the value, reads and writes are plain attribute accesses."""
+
+    __slots__ = ("name", "group")
+
+    def __init__(self, name: str, group: str) -> None:
+        self.name, self.group = name, group
+
+    def __get__(self, obj, cls=None):
+        if obj is None:
+            return self
+        d = obj.__dict__
+        src = d.get("_src")
+        if src is not None:
+            getattr(src, self.group)(obj, d)
+            if self.name not in d:  # `advantages` is per token: the other group has it
+                getattr(src, "doc_fields" if self.group == "tokens" else "tokens")(obj, d)
+        try:
+            return d[self.name]
+        except KeyError:
+            raise AttributeError(self.name) from None
+
+
+class PackedBatch(Batch):
+    """A ``Batch`` over one micro of a pack launch.  All micros of the launch
+    live in flat device buffers; a micro's tensors are views of them, made on
+    first access (per group, for every micro of the launch at once: the
+    per-token tensors, the per-document tensors, the attention metadata), as
+    the reference's trainer builds each micro when it reaches it
+    (trainer.py:557-571).  Once made, fields are plain attributes."""
+
+
+for _name, _group in (("input_ids", "tokens"), ("labels", "tokens"), ("positions", "tokens"), ("mask", "tokens"),
+                      ("doc_ids", "tokens"), ("rollout_logprobs", "tokens"), ("advantage_tokens", "tokens"),
+                      ("advantages", "doc_fields"), ("lengths", "doc_fields"),
+                      ("positive_lm_weights", "doc_fields"), ("attention_masks", "attention")):
+    setattr(PackedBatch, _name, _Lazy(_name, _group))
+del _name, _group
 
 
 def build_micro_batches(
@@ -539,5 +613,5 @@ def build_micro_batch(
                                need_rollout_lp=need_rollout_lp)[0]
 
 
-__all__ = ["ADVANTAGE_TOKENS", "TEACHER_FIELDS", "Batch", "PackJob", "VarlenMetadata", "build_micro_batch",
+__all__ = ["ADVANTAGE_TOKENS", "TEACHER_FIELDS", "Batch", "PackJob", "PackedBatch", "VarlenMetadata", "build_micro_batch",
            "build_micro_batches", "launch_pack", "make_varlen_metadata", "stage_micro_batches"]

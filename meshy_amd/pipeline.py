@@ -29,6 +29,9 @@ from .plan import Plan, PlannerConfig, plan_tables, tables_to_plan
 from .wire import jagged_parts
 
 
+_NP_DTYPES = {torch.int32: np.int32, torch.int64: np.int64, torch.float32: np.float32}
+
+
 class RaggedSamples:
     """One step's samples as flat pinned host arrays, in global sample order."""
 
@@ -66,12 +69,23 @@ class RaggedSamples:
         self.n_groups = n_groups
         # Pinned when a device is present, so the one copy to it is a DMA.
         self.buf = torch.empty(lay.size, dtype=torch.uint8, pin_memory=torch.cuda.is_available())
+        self._np_buf = self.buf.numpy()
+        self._np: dict[str, np.ndarray] = {}
         self.copied = None  # event of the last copy of the plan tables out of buf
         self.view("s_off").copy_(torch.from_numpy(self.offsets))
         self.view("pos_w").zero_()
 
     def view(self, name: str) -> torch.Tensor:
         return self.lay.view(self.buf, name)
+
+    def np_view(self, name: str) -> np.ndarray:
+        """The region as a numpy array over the same pinned memory (cached)."""
+        v = self._np.get(name)
+        if v is None:
+            lo, hi, dtype = self.lay.regions[name]
+            v = self._np_buf[lo:hi].view(_NP_DTYPES[dtype])
+            self._np[name] = v
+        return v
 
     @classmethod
     def from_arrays(cls, tokens, mask, logprobs, offsets, rewards, group_offsets) -> "RaggedSamples":
@@ -169,12 +183,12 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
     elems = seq * rows
     out_off = np.zeros(nm + 1, np.int64)
     np.cumsum(elems, out=out_off[1:])
-    ragged.view("seq")[:nm] = torch.from_numpy(seq)
-    ragged.view("out_off")[:nm + 1] = torch.from_numpy(out_off)
-    ragged.view("doc_start")[:nm + 1] = torch.from_numpy(start)
+    ragged.np_view("seq")[:nm] = seq
+    ragged.np_view("out_off")[:nm + 1] = out_off
+    ragged.np_view("doc_start")[:nm + 1] = start
     nd_total = int(start[-1])
-    ragged.view("doc_sample")[:nd_total] = torch.from_numpy(dsample[:nd_total].astype(np.int32))
-    ragged.view("doc_len")[:nd_total] = torch.from_numpy(dlen[:nd_total])
+    ragged.np_view("doc_sample")[:nd_total] = dsample[:nd_total]
+    ragged.np_view("doc_len")[:nd_total] = dlen[:nd_total]
 
     dbuf[cut:].copy_(ragged.buf[cut:], non_blocking=True)
     ragged.copied = torch.cuda.Event()

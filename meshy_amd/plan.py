@@ -119,8 +119,17 @@ def filler_micro(cfg: PlannerConfig) -> MicroPlan:
     return MicroPlan((), cfg.align, ())
 
 
-def _np_ptr(a: np.ndarray):
-    return a.ctypes.data_as(_lib.c_void_p)
+def _np_ptr(a: np.ndarray) -> int:
+    return a.__array_interface__["data"][0]
+
+
+def _frozen(cls, **fields):
+    """An instance of the frozen dataclass ``cls`` with ``fields`` set directly:
+    the values come from the native planner, which already enforces what
+    ``__init__`` would (there is no validation hook on these types)."""
+    obj = object.__new__(cls)
+    obj.__dict__.update(fields)
+    return obj
 
 
 class PlanTables:
@@ -142,20 +151,10 @@ class PlanTables:
         self.n_micro_total = 0
 
     def c_struct(self) -> _lib.PlanOut:
-        out = _lib.PlanOut()
-        for name, ct in (
-            ("local_indices", _lib.c_int32),
-            ("mini_n_micro", _lib.c_int32),
-            ("mini_n_docs_global", _lib.c_int64),
-            ("mini_n_tokens_global", _lib.c_int64),
-            ("mini_tokens_per_rank", _lib.c_int64),
-            ("micro_seq_len", _lib.c_int64),
-            ("micro_doc_start", _lib.c_int32),
-            ("doc_sample", _lib.c_int32),
-            ("doc_len", _lib.c_int64),
-        ):
-            setattr(out, name, getattr(self, name).ctypes.data_as(_lib.POINTER(ct)))
-        return out
+        return _lib.PlanOut(_np_ptr(self.local_indices), _np_ptr(self.mini_n_micro),
+                            _np_ptr(self.mini_n_docs_global), _np_ptr(self.mini_n_tokens_global),
+                            _np_ptr(self.mini_tokens_per_rank), _np_ptr(self.micro_seq_len),
+                            _np_ptr(self.micro_doc_start), _np_ptr(self.doc_sample), _np_ptr(self.doc_len), 0, 0)
 
 
 def _as_int64(x: Sequence[int]) -> np.ndarray:
@@ -218,11 +217,13 @@ def tables_to_plan(t: PlanTables) -> Plan:
             micros = []
             for _ in range(n_micro[i]):
                 a, b = start[k], start[k + 1]
-                micros.append(MicroPlan(tuple(dsample[a:b]), seq[k], tuple(dlen[a:b])))
+                micros.append(_frozen(MicroPlan, sample_idx=tuple(dsample[a:b]), seq_len=seq[k],
+                                      doc_lens=tuple(dlen[a:b])))
                 k += 1
-            minis.append(MiniPlan(tuple(micros), docs_g[i], toks_g[i], tuple(tpr[i])))
+            minis.append(_frozen(MiniPlan, micros=tuple(micros), n_docs_global=docs_g[i],
+                                 n_tokens_global=toks_g[i], tokens_per_rank=tuple(tpr[i])))
         per_rank.append(tuple(minis))
-    return Plan(per_rank=tuple(per_rank), local_indices=tuple(tuple(x) for x in local))
+    return _frozen(Plan, per_rank=tuple(per_rank), local_indices=tuple(tuple(x) for x in local))
 
 
 def build_plan(
