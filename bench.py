@@ -1056,8 +1056,11 @@ def main() -> int:
     ap.add_argument("--no-cpu", action="store_true", help="skip every CPU reference timing")
     ap.add_argument("--quick", action="store_true", help="headline kernel only")
     ap.add_argument("--pmc-kernels", action="store_true",
-                    help="for counter runs: Top-K (K = 8) x 3, logprob backward x 3 and a device copy x 3 over "
-                         "the [16384, 151936] logits, no JSON line")
+                    help="for counter runs: logprob + entropy, the plain read, Top-K (K = 8) and the logprob "
+                         "backward x 3 each and a device copy x 3 over the [16384, 151936] logits, no JSON line")
+    ap.add_argument("--pmc-workloads", action="store_true",
+                    help="for counter runs: the pack, PPO, GAE, critic and whitening legs with a few steps each, "
+                         "then a 256 MiB device copy x 3 to calibrate, no JSON line")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the hot path's kernels run per GPU and no multi-GPU figure "
@@ -1072,14 +1075,19 @@ def main() -> int:
     torch.set_num_threads(os.cpu_count() or 1)
     if args.pmc_kernels:
         return pmc_kernels()
+    if args.pmc_workloads:
+        return pmc_workloads()
 
     ms, nbytes, logits, labels = bench_logprob(args.steps, args.warmup)
     achieved = nbytes / (ms * 1e-3) / 1e9
     read_ceiling = bench_read_ceiling(logits, args.steps, args.warmup)
-    traffic = None
+    traffic = traffic_src = None
     if os.path.exists(TRAFFIC_FILE):
         with open(TRAFFIC_FILE) as f:
-            traffic = json.load(f).get("k_lpe_fwd_vec", {}).get("hbm_bytes_per_launch")
+            stored = json.load(f).get("k_lpe_fwd_vec", {})
+        traffic = stored.get("hbm_bytes_per_launch")
+        traffic_src = ("stored, not measured in this run: FETCH_SIZE x 2 + WRITE_SIZE per launch from separate "
+                       f"rocprofv3 --pmc runs, {stored.get('source')}")
     result = {
         "metric": "packed tokens/sec for logprob+entropy (V=151936) + % of HBM peak; pack latency",
         "value": T_TOK / (ms * 1e-3),
@@ -1096,7 +1104,7 @@ def main() -> int:
         "config": {"workload": "fused packed logprob+entropy over one micro-batch of logits", "T": T_TOK,
                    "V": VOCAB, "global_batch": T_TOK, "seq_len": T_TOK, "parallelism": "none (1 GPU)"},
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
-                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic, "traffic_source": traffic_src,
                      "read_ceiling": round(read_ceiling, 1),
                      "frac_of_read_ceiling": round(achieved / read_ceiling, 4)},
     }
@@ -1172,6 +1180,40 @@ def pmc_kernels() -> int:
         grad.copy_(z)
     torch.cuda.synchronize()
     print("pmc kernels done", flush=True)
+    return 0
+
+
+def pmc_workloads() -> int:
+    """The dispatches of the per-workload traffic counter runs: the 256 GRPO
+    samples' pack, the 512-document PPO loss, GAE over 1024 documents (with and
+    without lengths), the critic reductions and whitening, a few times each;
+    then a device copy of exactly 268,435,456 B read and written, three times,
+    to calibrate the counters."""
+    import numpy as np
+    import torch
+
+    from meshy_amd import workloads
+    from meshy_amd.gae import gae_and_returns
+
+    bench_pack(3, True)
+    bench_ppo(3, 1, True)
+    bench_gae(3, 1, True)
+    dev = torch.device("cuda:0")
+    batch, values, terminal = workloads.gae_1024_docs(4)
+    n = len(batch.lengths)
+    doc_ids = torch.from_numpy(np.repeat(np.arange(n), batch.lengths)).reshape(1, -1).to(dev)
+    r = torch.zeros(1, batch.total, device=dev)
+    v = torch.from_numpy(values).to(torch.bfloat16).reshape(1, -1).to(dev)
+    m = torch.from_numpy(batch.mask).reshape(1, -1).to(dev)
+    for _ in range(3):
+        gae_and_returns(r, v, m, doc_ids, n, gamma=1.0, alpha=1.5)  # masked lengths counted (k_gae_doc_count)
+    bench_critic(3, 1, True)
+    src = torch.ones(64 * 1024 * 1024, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    print("pmc workloads done", flush=True)
     return 0
 
 
