@@ -195,6 +195,20 @@ int meshy_grpo_advantage(const float* rewards, int64_t n_rewards, const int64_t*
                          int64_t n_groups, float* advantages, hipStream_t stream);
 
 /* ------------------------------------------------------------------------
+ * Zero-variance group filter (device).
+ * Replaces is_zero_variance_group (meshy/worker/rollout.py:100-115) for all
+ * groups of a batch at once.  raw_rewards are the per-sample raw rewards in
+ * float64 (the reference compares Python floats): sample.raw_reward when set,
+ * else sample.reward.  flags[g] = 1 when max(raw) - min(raw) <= tolerance
+ * with Python's max()/min() over group g (a NaN first element makes the
+ * group 0, later NaNs are skipped), 1 for an empty group, else 0.  Group g is
+ * raw_rewards[group_offsets[g], group_offsets[g+1]), clamped to
+ * [0, n_rewards).  raw_rewards may be NULL when n_rewards is 0.
+ * ---------------------------------------------------------------------- */
+int meshy_zero_variance_groups(const double* raw_rewards, int64_t n_rewards, const int64_t* group_offsets,
+                               int64_t n_groups, double tolerance, uint8_t* flags, hipStream_t stream);
+
+/* ------------------------------------------------------------------------
  * Fused packed log_softmax + gather + entropy (device), bf16 logits.
  * Replaces the chunk loop of TitanTrainer._forward_logprobs
  * (meshy/backend/titan/trainer.py:451-527) with its bodies _chunk_logprobs

@@ -10,6 +10,8 @@
 //                buffers with the per-document shift-by-one of labels, mask and
 //                rollout logprobs (batch.py:91-93, 126-172), and the position
 //                is the offset inside the document.
+// meshy_zero_variance_groups flags the groups whose raw rewards are all equal
+// (within a tolerance), one wavefront per group.
 // meshy_grpo_advantage normalises rewards per group, one wavefront per group
 // (rollout.py:88-97).
 #include "common.h"
@@ -219,6 +221,35 @@ __global__ __launch_bounds__(kWave) void k_grpo(const float* __restrict__ reward
     for (int64_t i = lane; i < n; i += kWave) adv[b + i] = (rewards[b + i] - mean) / den;
 }
 
+// Python's max() and min() over a list start from the first element and take
+// a later one only when it compares greater (smaller).  A NaN first element
+// therefore stays, and a later NaN never wins.  So a group has zero variance
+// when its first raw reward is not NaN and the spread of its non-NaN rewards
+// is within the tolerance (inf - inf is NaN: not within).  Empty groups have
+// zero variance.  Ranges are clamped to [0, n_raw) as in k_grpo.
+__global__ __launch_bounds__(kWave) void k_zero_variance(const double* __restrict__ raw, int64_t n_raw,
+                                                         const int64_t* __restrict__ group_off, double tol,
+                                                         uint8_t* __restrict__ flags) {
+    const int64_t g = blockIdx.x;
+    const int64_t b = min(max(group_off[g], static_cast<int64_t>(0)), n_raw);
+    const int64_t n = min(max(group_off[g + 1], b), n_raw) - b;
+    const int lane = threadIdx.x;
+    double hi = -__builtin_inf(), lo = __builtin_inf();
+    for (int64_t i = lane; i < n; i += kWave) {
+        const double r = raw[b + i];
+        hi = r > hi ? r : hi;
+        lo = r < lo ? r : lo;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const double h = __shfl_xor(hi, off, kWave);
+        const double l = __shfl_xor(lo, off, kWave);
+        hi = h > hi ? h : hi;
+        lo = l < lo ? l : lo;
+    }
+    if (lane == 0) flags[g] = n <= 0 ? 1 : static_cast<uint8_t>(!isnan(raw[b]) && hi - lo <= tol);
+}
+
 }  // namespace
 }  // namespace meshy
 
@@ -287,4 +318,20 @@ extern "C" int meshy_grpo_advantage(const float* rewards, int64_t n_rewards, con
     hipLaunchKernelGGL(k_grpo, dim3(static_cast<unsigned>(n_groups)), dim3(kWave), 0, stream, rewards, n_rewards,
                        group_offsets, advantages);
     return check_launch("meshy_grpo_advantage");
+}
+
+extern "C" int meshy_zero_variance_groups(const double* raw_rewards, int64_t n_rewards,
+                                          const int64_t* group_offsets, int64_t n_groups, double tolerance,
+                                          uint8_t* flags, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    if (n_groups < 0 || n_rewards < 0)
+        return set_error(MESHY_EINVAL, "meshy_zero_variance_groups: negative count");
+    if (n_groups == 0) return MESHY_OK;
+    if ((!raw_rewards && n_rewards > 0) || !group_offsets || !flags)
+        return set_error(MESHY_ENULL, "meshy_zero_variance_groups: NULL pointer");
+    if (n_groups > INT32_MAX) return set_error(MESHY_EINVAL, "meshy_zero_variance_groups: too many groups");
+    hipLaunchKernelGGL(k_zero_variance, dim3(static_cast<unsigned>(n_groups)), dim3(kWave), 0, stream, raw_rewards,
+                       n_rewards, group_offsets, tolerance, flags);
+    return check_launch("meshy_zero_variance_groups");
 }

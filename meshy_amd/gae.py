@@ -19,30 +19,17 @@ import numpy as np
 import torch
 
 from . import _lib
-from .loss import segment_offsets
-
-# Segment offsets of recently seen doc_ids tensors (each entry holds its
-# tensor, so the identity in the key stays unique while cached).
-_OFFSETS: dict[tuple, tuple[torch.Tensor, torch.Tensor | None]] = {}
-_OFFSETS_MAX = 8
+from .loss import checked_segment_offsets
 
 
-def _doc_offsets(doc_ids: torch.Tensor, ids: torch.Tensor, n_docs: int) -> torch.Tensor | None:
+def _doc_offsets(doc_ids: torch.Tensor, n_docs: int) -> torch.Tensor | None:
     """The segment offsets of ``doc_ids`` over its ``n_docs + 1`` slots when its
     flattened values are non-decreasing (checked once per tensor version, one
-    device sync), else None: the kernels then read every token's id."""
-    key = (id(doc_ids), doc_ids._version, doc_ids.data_ptr(), int(n_docs))
-    hit = _OFFSETS.get(key)
-    if hit is not None:
-        return hit[1]
+    device sync), else None: the kernels then count lengths with atomics."""
     try:
-        off = segment_offsets(ids, int(n_docs) + 1, check_sorted=True)
+        return checked_segment_offsets(doc_ids, n_docs + 1)
     except ValueError:
-        off = None
-    if len(_OFFSETS) >= _OFFSETS_MAX:
-        _OFFSETS.pop(next(iter(_OFFSETS)))
-    _OFFSETS[key] = (doc_ids, off)
-    return off
+        return None
 
 
 def _run(rewards, values, mask, doc_ids, n_docs, *, lengths, gamma, alpha, epsilon, want_adv,
@@ -90,7 +77,7 @@ def _run(rewards, values, mask, doc_ids, n_docs, *, lengths, gamma, alpha, epsil
     g.workspace_bytes = ws.numel()
     # The offsets serve the masked document lengths, needed without `lengths`.
     need = lens is None and (want_adv or want_lam) and n_docs > 0 and rows * S > 0
-    off = _doc_offsets(doc_ids, ids, n_docs) if offsets and need else None
+    off = _doc_offsets(doc_ids, n_docs) if offsets and need else None
     g.seg_offsets = _lib.ptr(off)
     rc = lib.meshy_gae(_lib.ctypes.byref(g), _lib.stream_of(dev))
     _lib.check(rc, "meshy_gae")

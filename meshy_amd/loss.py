@@ -27,8 +27,10 @@ def batch_segment_offsets(mb: Any) -> torch.Tensor:
     """``segment_offsets`` of a micro-batch's ``doc_ids`` over its ``n_docs + 1``
     slots, cached on the batch object: the PPO and distillation losses of one
     micro (forward, backward, later epochs) share it.  A batch from the pack
-    kernels carries the offsets the pack wrote.  The keys include the tensor's
-    version counter, so an in-place change of ``doc_ids`` recomputes."""
+    kernels carries the offsets the pack wrote; for any other batch the order
+    of ``doc_ids`` is checked once (ValueError when it decreases).  The keys
+    include the tensor's version counter, so an in-place change of ``doc_ids``
+    recomputes."""
     ids = mb.doc_ids
     key = (id(ids), ids._version, ids.data_ptr(), int(mb.n_docs))
     hit = getattr(mb, "_meshy_seg_offsets", None)
@@ -39,11 +41,40 @@ def batch_segment_offsets(mb: Any) -> torch.Tensor:
         # Written by the pack kernel next to doc_ids: no pass over the ids.
         off = src[1][src[2]:src[2] + key[3] + 2]
     else:
-        off = segment_offsets(ids, int(mb.n_docs) + 1)
+        off = checked_segment_offsets(ids, int(mb.n_docs) + 1)
     try:
         object.__setattr__(mb, "_meshy_seg_offsets", (key, off))
     except (AttributeError, TypeError):
         pass  # a batch type without an attribute dict: no cache
+    return off
+
+
+# Segment offsets of recently seen doc_ids tensors whose order was checked,
+# None for a tensor found out of order (each entry holds its tensor, so the
+# identity in the key stays unique while cached).
+_CHECKED: dict[tuple, tuple[torch.Tensor, torch.Tensor | None]] = {}
+_CHECKED_MAX = 16
+
+
+def checked_segment_offsets(doc_ids: torch.Tensor, n_slots: int) -> torch.Tensor:
+    """``segment_offsets`` of ``doc_ids`` after checking, once per tensor and
+    version (one device sync), that its flattened values are non-decreasing;
+    raises ValueError otherwise.  The kernels that take these offsets rely on
+    that order, which both batch layouts have (batch.py:123, 150-162)."""
+    key = (id(doc_ids), doc_ids._version, doc_ids.data_ptr(), int(n_slots))
+    hit = _CHECKED.get(key)
+    if hit is not None:
+        off = hit[1]
+    else:
+        try:
+            off = segment_offsets(doc_ids, n_slots, check_sorted=True)
+        except ValueError:
+            off = None
+        if len(_CHECKED) >= _CHECKED_MAX:
+            _CHECKED.pop(next(iter(_CHECKED)))
+        _CHECKED[key] = (doc_ids, off)
+    if off is None:
+        raise ValueError("doc_ids must be non-decreasing over the flattened micro-batch")
     return off
 
 
@@ -264,4 +295,5 @@ def reduce_mini_metrics(self: Any, sums: dict[str, torch.Tensor]) -> dict[str, f
     return out
 
 
-__all__ = ["batch_segment_offsets", "ppo_clip_loss", "reduce_mini_metrics", "segment_offsets"]
+__all__ = ["batch_segment_offsets", "checked_segment_offsets", "ppo_clip_loss", "reduce_mini_metrics",
+           "segment_offsets"]

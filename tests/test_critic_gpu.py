@@ -55,6 +55,15 @@ def test_per_sequence_mean_packed_with_padding_slot(dev):
     assert (out.cpu() - ref).abs().max().item() <= 1e-5
 
 
+def test_per_sequence_mean_rejects_doc_ids_out_of_order(dev):
+    from meshy_amd import critic
+
+    ids = torch.tensor([[0, 0, 2, 1, 1]], device=dev)
+    ones = torch.ones(1, 5, device=dev)
+    with pytest.raises(ValueError, match="non-decreasing"):
+        critic.advantages_to_per_sequence(ones, ones, ids, 3)
+
+
 @pytest.mark.parametrize("bf16", [False, True])
 def test_accumulator_matches_oracle(dev, bf16):
     from meshy_amd import critic

@@ -7,6 +7,7 @@ from __future__ import annotations
 
 import math
 
+import numpy as np
 import pytest
 import torch
 
@@ -68,6 +69,39 @@ def test_grpo_oracle_known_answers():
     # one success in 8: mean 1/8, unbiased std sqrt(1/8) -> 0.875 / 0.35355
     adv = ogrpo.grpo_group([1.0] + [0.0] * 7)
     assert adv[0] == pytest.approx(0.875 / math.sqrt(1 / 8), rel=1e-6)
+
+
+def test_zero_variance_oracle_known_answers():
+    # test_rollout_advantage.py:90-93
+    assert ogrpo.zero_variance_group([0.0, 0.0, 0.0])
+    assert ogrpo.zero_variance_group([1.0, 1.0])
+    assert not ogrpo.zero_variance_group([0.0, 1.0])
+    assert ogrpo.zero_variance_group([])                        # rollout.py:109-110
+    # the comparison is in float64: a spread of 2e-8 at 1.0 is not within 1e-8
+    assert not ogrpo.zero_variance_group([1.0, 1.0 + 2e-8])
+    assert ogrpo.zero_variance_group([1.0, 1.0 + 5e-9])
+    assert not ogrpo.zero_variance_group([math.inf, math.inf])  # inf - inf is NaN
+
+
+def test_zero_variance_oracle_against_brute_force():
+    """For NaN-free groups the spread is the largest pairwise difference
+    (rounding is monotone, so the pair (max, min) attains it); with NaN the
+    builtins keep a NaN first element (never within) and skip later ones."""
+    rng = np.random.default_rng(5)
+    for _ in range(400):
+        n = int(rng.integers(1, 9))
+        base = float(rng.choice([0.0, 1.0, -3.5, 1e6]))
+        r = [base + float(rng.choice([0.0, 0.0, 4e-9, -6e-9, 1e-8, 0.3])) for _ in range(n)]
+        tol = float(rng.choice([1e-8, 0.0, 0.5]))
+        want = max(a - b for a in r for b in r) <= tol
+        assert ogrpo.zero_variance_group(r, tol) == want, (r, tol)
+        if n > 1 and rng.random() < 0.5:
+            k = int(rng.integers(0, n))
+            r2 = list(r)
+            r2[k] = math.nan
+            rest = [x for x in r2 if not math.isnan(x)]
+            want2 = k != 0 and max(a - b for a in rest for b in rest) <= tol
+            assert ogrpo.zero_variance_group(r2, tol) == want2, (r2, tol)
 
 
 # ------------------------------------------------------------------ PPO

@@ -4,6 +4,7 @@ tests/test_rollout_advantage.py:13-18).  Indices and copies are bit-exact."""
 
 from __future__ import annotations
 
+import math
 from types import SimpleNamespace
 
 import numpy as np
@@ -326,6 +327,60 @@ def test_grpo_256_samples_matches_oracle(dev):
     off = torch.tensor([0, 1, 9, 10, 40, 41, 100])
     got = grpo_advantages(r.to(dev), off.to(dev)).cpu()
     assert (got - ogrpo.grpo_batched(r, off)).abs().max().item() <= 1e-4
+
+
+def test_zero_variance_known_answers(dev):
+    # test_rollout_advantage.py:90-93; the raw reward wins over the shaped one
+    from meshy_amd.advantage import is_zero_variance_group
+
+    def group(*rewards, raw=None):
+        raw = raw or [None] * len(rewards)
+        return [SimpleNamespace(reward=r, raw_reward=w, advantage=None) for r, w in zip(rewards, raw)]
+
+    assert is_zero_variance_group(group(0.0, 0.0, 0.0), device=dev)
+    assert is_zero_variance_group(group(1.0, 1.0), device=dev)
+    assert not is_zero_variance_group(group(0.0, 1.0), device=dev)
+    assert is_zero_variance_group([], device=dev)
+    assert is_zero_variance_group(group(1.02, 0.97, 1.0, raw=[1.0, 1.0, 1.0]), device=dev)
+    assert not is_zero_variance_group(group(1.0, 1.0, raw=[1.0, 0.0]), device=dev)
+    assert not is_zero_variance_group(group(1.0, 1.0 + 2e-8), device=dev)  # float64, not float32
+    assert is_zero_variance_group(group(1, True), device=dev)               # ints and bools are floats
+
+
+def test_zero_variance_groups_match_oracle(dev):
+    """Ragged groups (empty, size 1, up to 200 samples) with spreads at the
+    tolerance, NaN first or later, +-inf, and offsets past the end (clamped):
+    every flag equals the oracle's."""
+    from meshy_amd.advantage import zero_variance_groups
+
+    rng = np.random.default_rng(11)
+    sizes = [0, 1, 2, 8, 8, 8, 200, 3, 0, 64, 65, 8]
+    vals, offs = [], [0]
+    for i, n in enumerate(sizes):
+        base = float(rng.choice([0.0, 1.0, -2.0, 1e6]))
+        g = [base] * n
+        kind = i % 6
+        if n and kind == 1:
+            g[int(rng.integers(0, n))] += 1e-8 * float(rng.choice([0.5, 1.0, 2.0]))
+        elif n and kind == 2:
+            g[int(rng.integers(0, n))] = math.nan
+        elif n and kind == 3:
+            g[0] = math.nan
+        elif n and kind == 4:
+            g[-1] = math.inf
+        elif n and kind == 5:
+            g = [float(x) for x in rng.random(n)]
+        vals += g
+        offs.append(len(vals))
+    offs.append(len(vals) + 5)  # a last group that claims five more samples than there are
+    for tol in (1e-8, 0.0, 2.0):
+        got = zero_variance_groups(torch.tensor(vals, dtype=torch.float64, device=dev),
+                                   torch.tensor(offs, device=dev), tol).cpu().tolist()
+        clamped = offs[:-1] + [len(vals)]
+        want = ogrpo.zero_variance_batched(vals, clamped, tol)
+        assert got == want, tol
+    assert zero_variance_groups(torch.zeros(0, dtype=torch.float64, device=dev),
+                                torch.zeros(3, dtype=torch.int64, device=dev)).cpu().tolist() == [True, True]
 
 
 # ------------------------------------------------------------ pack_step (256 GRPO samples)

@@ -389,6 +389,28 @@ def test_segment_offsets_detect_unsorted(dev):
         segment_offsets(ids.to(dev), 100, check_sorted=True)
 
 
+def test_loss_rejects_doc_ids_out_of_order(dev):
+    """A batch not built by the pack kernels has its doc_ids order checked once
+    (the offsets the kernels take assume it); decreasing ids raise ValueError,
+    again on the next call, and a fix in place is accepted."""
+    from meshy_amd.loss import ppo_clip_loss
+    from meshy_amd.plan import MiniPlan
+
+    mb = _batch(dev, rows=1, S=8)
+    mb.doc_ids = torch.tensor([[0, 0, 1, 1, 0, 1, 1, 1]], device=dev)
+    mb.advantages = torch.tensor([1.0, -1.0], device=dev)
+    mb.n_docs = 2
+    mini = MiniPlan(micros=(), n_docs_global=2, n_tokens_global=int(mb.mask.sum()), tokens_per_rank=(8,))
+    old = -torch.ones(1, 8, device=dev)
+    new = (old + 0.05).requires_grad_()
+    for _ in range(2):
+        with pytest.raises(ValueError, match="non-decreasing"):
+            ppo_clip_loss(_stub(), new, old, mb, mini)
+    mb.doc_ids[0, 4] = 1
+    loss, _ = ppo_clip_loss(_stub(), new, old, mb, mini)
+    assert torch.isfinite(loss)
+
+
 def test_segment_offsets_cache_follows_doc_ids(dev):
     """A batch caches its document offsets after the first loss call; replacing
     or editing doc_ids in place recomputes them."""
