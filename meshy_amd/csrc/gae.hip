@@ -22,6 +22,10 @@
 //                of its group to its right and of the groups to its right,
 //                re-folds its chunk, scans its threads from the right seeded
 //                with the carry, and writes A_t and G_t.
+// With the segment offsets of non-decreasing ids, a chunk holding at most
+// kMaxStarts document starts reads the ids only at its two ends and takes the
+// starts from the offsets (8 bytes per token less in each pass); other chunks
+// read every token's id.
 // Every fold of the scan has a fixed order, so the results do not depend on
 // timing (the atomic count aside).  The
 // apply pass visits each XCD's chunks from the highest down, so that it first
@@ -122,8 +126,57 @@ typedef long long i64x2 __attribute__((ext_vector_type(2)));
 typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
 typedef unsigned int u32x2 __attribute__((ext_vector_type(2)));
 
+// The documents of a chunk's window [c0, e), e = min(c0 + kChunk + 1, n) (the
+// chunk and the neighbour of its last position), from the ids at its two ends
+// and the offsets of the document starts between them, so that the per-token
+// ids are not read.  Used with offsets, both end ids in [0, n_docs] and at most
+// kMaxStarts starts inside; otherwise the chunk reads every token's id.
+constexpr int kMaxStarts = 4;
+
+struct ChunkDocs {
+    int64_t d0;                  // the id at c0
+    int64_t start[kMaxStarts];   // first position of documents d0 + 1, ... (INT64_MAX past the last)
+    bool use;
+};
+
+__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
+    const uint64_t u = static_cast<uint64_t>(v);
+    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
+    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
+    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+}
+
+__device__ __forceinline__ ChunkDocs chunk_docs(const meshy_gae_args& g, int64_t c0, int64_t n) {
+    ChunkDocs cd;
+    cd.use = false;
+    cd.d0 = 0;
+#pragma unroll
+    for (int r = 0; r < kMaxStarts; ++r) cd.start[r] = INT64_MAX;
+    if (!g.seg_offsets || c0 >= n) return cd;
+    const int64_t e = min(c0 + kChunk + 1, n);
+    const int64_t d0 = uniform_i64(g.doc_ids[c0]);
+    const int64_t d1 = uniform_i64(g.doc_ids[e - 1]);
+    if (d0 < 0 || d1 > g.n_docs || d1 < d0 || d1 - d0 > kMaxStarts) return cd;
+    cd.use = true;
+    cd.d0 = d0;
+#pragma unroll
+    for (int r = 0; r < kMaxStarts; ++r)
+        if (r < d1 - d0) cd.start[r] = uniform_i64(g.seg_offsets[d0 + 1 + r]);
+    return cd;
+}
+
+// The id at position t of the chunk's window (non-decreasing ids: the starts at
+// or before t, empty documents included, each add one).
+__device__ __forceinline__ int64_t id_in_chunk(const ChunkDocs& cd, int64_t t) {
+    int64_t d = cd.d0;
+#pragma unroll
+    for (int r = 0; r < kMaxStarts; ++r) d += (t >= cd.start[r]) ? 1 : 0;
+    return d;
+}
+
+template <bool kOff>
 __device__ __forceinline__ void load_inputs(const meshy_gae_args& g, int64_t t0, int64_t n, bool vec,
-                                            ThreadInputs& in) {
+                                            const ChunkDocs& cd, ThreadInputs& in) {
     const bool whole = vec && t0 + kItems <= n;
     if (whole) {
 #pragma unroll
@@ -133,11 +186,13 @@ __device__ __forceinline__ void load_inputs(const meshy_gae_args& g, int64_t t0,
             in.mk[4 * q + 0] = m4.x; in.mk[4 * q + 1] = m4.y; in.mk[4 * q + 2] = m4.z; in.mk[4 * q + 3] = m4.w;
             in.r[4 * q + 0] = r4.x; in.r[4 * q + 1] = r4.y; in.r[4 * q + 2] = r4.z; in.r[4 * q + 3] = r4.w;
         }
+        if constexpr (!kOff) {
 #pragma unroll
-        for (int q = 0; q < kItems / 2; ++q) {
-            const i64x2 d2 = *reinterpret_cast<const i64x2*>(g.doc_ids + t0 + 2 * q);
-            in.d[2 * q] = d2.x;
-            in.d[2 * q + 1] = d2.y;
+            for (int q = 0; q < kItems / 2; ++q) {
+                const i64x2 d2 = *reinterpret_cast<const i64x2*>(g.doc_ids + t0 + 2 * q);
+                in.d[2 * q] = d2.x;
+                in.d[2 * q + 1] = d2.y;
+            }
         }
         if (g.values) {
             if (g.values_bf16) {
@@ -175,24 +230,30 @@ __device__ __forceinline__ void load_inputs(const meshy_gae_args& g, int64_t t0,
             const bool ok = t < n;
             in.mk[k] = ok ? g.mask[t] : 0.f;
             in.r[k] = ok ? g.rewards[t] : 0.f;
-            in.d[k] = ok ? g.doc_ids[t] : -1;
+            if constexpr (!kOff) in.d[k] = ok ? g.doc_ids[t] : -1;
             in.v[k] = ok ? value_at(g, t) : 0.f;
         }
     }
     const int64_t tn = t0 + kItems;
     const bool okn = tn < n;
     in.mk[kItems] = okn ? g.mask[tn] : 0.f;
-    in.d[kItems] = okn ? g.doc_ids[tn] : -1;
     in.v[kItems] = okn ? value_at(g, tn) : 0.f;
+    if constexpr (kOff) {
+#pragma unroll
+        for (int k = 0; k <= kItems; ++k) in.d[k] = (t0 + k < n) ? id_in_chunk(cd, t0 + k) : -1;
+    } else {
+        in.d[kItems] = okn ? g.doc_ids[tn] : -1;
+    }
 }
 
 // The affine maps of a thread's positions t0 .. t0 + kItems - 1 (identity past n).
 // Row ends come from a column counter started with one division; lambda is
 // recomputed only when the document changes.
+template <bool kOff>
 __device__ __forceinline__ void thread_maps(const meshy_gae_args& g, const float* cnt, int64_t t0, int64_t n,
-                                            bool vec, Pair (&items)[kItems]) {
+                                            bool vec, const ChunkDocs& cd, Pair (&items)[kItems]) {
     ThreadInputs in;
-    load_inputs(g, t0, n, vec, in);
+    load_inputs<kOff>(g, t0, n, vec, cd, in);
     int64_t s = t0 % g.S;
     int64_t cur_d = -2;
     float cur_lam = 0.f;
@@ -294,9 +355,14 @@ __global__ __launch_bounds__(kCountThreads) void k_gae_doc_count(const float* __
 }
 
 // Builds the thread's maps (contiguous positions) and folds them right to left.
+// The branch on cd.use is uniform over the workgroup and holds each path's
+// loads and arithmetic whole.
 __device__ __forceinline__ Pair load_items(const meshy_gae_args& g, const float* cnt, int64_t t0, int64_t n,
-                                           bool vec, Pair (&items)[kItems]) {
-    thread_maps(g, cnt, t0, n, vec, items);
+                                           bool vec, const ChunkDocs& cd, Pair (&items)[kItems]) {
+    if (cd.use)
+        thread_maps<true>(g, cnt, t0, n, vec, cd, items);
+    else
+        thread_maps<false>(g, cnt, t0, n, vec, cd, items);
     Pair agg = identity_pair();
 #pragma unroll
     for (int k = kItems - 1; k >= 0; --k) agg = compose(items[k], agg);
@@ -305,9 +371,11 @@ __device__ __forceinline__ Pair load_items(const meshy_gae_args& g, const float*
 
 __global__ __launch_bounds__(kThreads) void k_gae_chunks(meshy_gae_args g, Workspace ws, int64_t n, bool vec) {
     __shared__ Pair s_wave[kThreads / kWave];
-    const int64_t t0 = static_cast<int64_t>(blockIdx.x) * kChunk + static_cast<int64_t>(threadIdx.x) * kItems;
+    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
+    const int64_t t0 = c0 + static_cast<int64_t>(threadIdx.x) * kItems;
+    const ChunkDocs cd = chunk_docs(g, c0, n);
     Pair items[kItems];
-    const Pair mine = load_items(g, ws.cnt, t0, n, vec, items);
+    const Pair mine = load_items(g, ws.cnt, t0, n, vec, cd, items);
     Pair total;
     (void)block_suffix_exclusive(mine, s_wave, total);
     if (threadIdx.x == 0) ws.chunk[blockIdx.x] = total;
@@ -373,8 +441,9 @@ __global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Worksp
     const int64_t k1 = grp + 1 + lane;
     const Pair rj = ws.chunk[min(j, nc - 1)];
     const Pair ak = ws.group[min(k1, ng - 1)];
+    const ChunkDocs cd = chunk_docs(g, c * kChunk, n);
     Pair items[kItems];
-    const Pair mine = load_items(g, ws.cnt, t0, n, vec, items);
+    const Pair mine = load_items(g, ws.cnt, t0, n, vec, cd, items);
     if (threadIdx.x < kWave) {
         const Pair right = wave_fold((j > c && j < g1) ? rj : identity_pair());
         Pair after = wave_fold(k1 < ng ? ak : identity_pair());
@@ -931,6 +1000,9 @@ extern "C" int meshy_gae_attach(const meshy_gae_attach_args* args, hipStream_t s
     a.lam_doc = lam;
     a.workspace = ws.gae_ws;
     a.workspace_bytes = ws.gae_ws_bytes;
+    // Sample j's ids fill [offsets[j], offsets[j+1]): the offsets are the
+    // segment offsets of the ids the prep writes.
+    a.seg_offsets = g.offsets;
     rc = gae_launch(a, stream);
     if (rc) return rc;
     if (g.metrics) {

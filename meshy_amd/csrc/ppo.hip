@@ -217,16 +217,54 @@ __device__ __forceinline__ void ppo_combine(const meshy_ppo_args& a, const Works
     double v[kFinalVals];
 #pragma unroll
     for (int k = 0; k < kFinalVals; ++k) v[k] = 0.0;
+    // Token-level sums of every tile: v[4..13], four tiles per step with every
+    // load of a step issued before any is added (indices clamped, extra tiles
+    // dropped by a select).  Issued first: they do not wait on the offsets.
+    constexpr int kStep = 4;
+    for (int64_t b0 = threadIdx.x; b0 < n_tiles; b0 += NT * kStep) {
+        float t[kStep][kTokSums];
+#pragma unroll
+        for (int u = 0; u < kStep; ++u) {
+            const int64_t b = min(b0 + static_cast<int64_t>(u) * NT, n_tiles - 1);
+#pragma unroll
+            for (int k = 0; k < kTokSums; ++k) t[u][k] = ws.tok[b * kTokSums + k];
+        }
+#pragma unroll
+        for (int u = 0; u < kStep; ++u) {
+            const bool ok = b0 + static_cast<int64_t>(u) * NT < n_tiles;
+#pragma unroll
+            for (int k = 0; k < kTokSums; ++k) v[4 + k] += ok ? t[u][k] : 0.f;
+        }
+    }
     // Per-document totals (tile order) and their contributions: v[0..3] =
-    // loss terms, positive-LM terms, ESS terms, documents with tokens.
+    // loss terms, positive-LM terms, ESS terms, documents with tokens.  The
+    // first kDocTiles tiles of a document are loaded together (indices clamped
+    // to its last tile, which is a written pair; an empty document's loads are
+    // dropped), so a document of up to kDocTiles tiles costs one round trip
+    // after its offsets.  Sums run in tile order either way.
+    constexpr int kDocTiles = 4;
     for (int64_t d = threadIdx.x; d < n_slots; d += NT) {
-        const int64_t lo = a.seg_offsets[d];
-        const int64_t hi = a.seg_offsets[d + 1];
+        // Clamped to the tokens, so that malformed offsets stay in bounds.
+        const int64_t lo = min(max(a.seg_offsets[d], static_cast<int64_t>(0)), a.n_tokens);
+        const int64_t hi = min(max(a.seg_offsets[d + 1], lo), a.n_tokens);
+        const int64_t b0 = lo / kTile;
+        const int64_t b1 = max(hi - 1, static_cast<int64_t>(0)) / kTile;
+        float t[kDocTiles][kSegSums];
+#pragma unroll
+        for (int u = 0; u < kDocTiles; ++u) {
+            const float* src = ws.seg + (min(b0 + u, b1) + d) * kSegSums;
+#pragma unroll
+            for (int k = 0; k < kSegSums; ++k) t[u][k] = src[k];
+        }
         float sg[kSegSums] = {0.f, 0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int u = 0; u < kDocTiles; ++u) {
+            const bool ok = hi > lo && b0 + u <= b1;
+#pragma unroll
+            for (int k = 0; k < kSegSums; ++k) sg[k] += ok ? t[u][k] : 0.f;
+        }
         if (hi > lo) {
-            const int64_t b0 = lo / kTile;
-            const int64_t b1 = (hi - 1) / kTile;
-            for (int64_t b = b0; b <= b1; ++b) {
+            for (int64_t b = b0 + kDocTiles; b <= b1; ++b) {
                 const float* src = ws.seg + (b + d) * kSegSums;
 #pragma unroll
                 for (int k = 0; k < kSegSums; ++k) sg[k] += src[k];
@@ -246,25 +284,6 @@ __device__ __forceinline__ void ppo_combine(const meshy_ppo_args& a, const Works
                 v[2] += (sg[2] * sg[2]) / (fmaxf(sg[1], 1.f) * fmaxf(sg[3], 1e-8f));
                 v[3] += 1.0;
             }
-        }
-    }
-    // Token-level sums of every tile: v[4..13], four tiles per step with every
-    // load of a step issued before any is added (indices clamped, extra tiles
-    // dropped by a select).
-    constexpr int kStep = 4;
-    for (int64_t b0 = threadIdx.x; b0 < n_tiles; b0 += NT * kStep) {
-        float t[kStep][kTokSums];
-#pragma unroll
-        for (int u = 0; u < kStep; ++u) {
-            const int64_t b = min(b0 + static_cast<int64_t>(u) * NT, n_tiles - 1);
-#pragma unroll
-            for (int k = 0; k < kTokSums; ++k) t[u][k] = ws.tok[b * kTokSums + k];
-        }
-#pragma unroll
-        for (int u = 0; u < kStep; ++u) {
-            const bool ok = b0 + static_cast<int64_t>(u) * NT < n_tiles;
-#pragma unroll
-            for (int k = 0; k < kTokSums; ++k) v[4 + k] += ok ? t[u][k] : 0.f;
         }
     }
     const int lane = threadIdx.x % kWave;
@@ -322,6 +341,10 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
     // tile's 1024-token halves: 16-byte loads when every array is aligned),
     // then its document range and the boundaries inside it.
     constexpr int kPer = static_cast<int>(kTile / kThreads);
+    // The document range is loaded first: the per-document loads that depend
+    // on it then issue while the token loads are still in flight.
+    const int64_t d_first = doc_at(a, t0);
+    const int64_t nd = max(doc_at(a, t1 - 1), d_first) - d_first + 1;
     TokIn in[kPer];
 #pragma unroll
     for (int h = 0; h < kPer / 4; ++h) {
@@ -343,8 +366,6 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
             for (int e = 0; e < 4; ++e) in[4 * h + e] = load_tok<kLean>(a, i4 + e, i4 + e < t1);
         }
     }
-    const int64_t d_first = doc_at(a, t0);
-    const int64_t nd = max(doc_at(a, t1 - 1), d_first) - d_first + 1;
     // Unit gradient of each token (token mean: the loss's gradient is known
     // up to the scalar the backward multiplies in).
     float* const gu = (a.grad_unit && a.per_token_loss) ? a.grad_unit : nullptr;

@@ -75,8 +75,9 @@ def _run(rewards, values, mask, doc_ids, n_docs, *, lengths, gamma, alpha, epsil
     g.lam_doc = _lib.ptr(lam)
     g.workspace = ws.data_ptr()
     g.workspace_bytes = ws.numel()
-    # The offsets serve the masked document lengths, needed without `lengths`.
-    need = lens is None and (want_adv or want_lam) and n_docs > 0 and rows * S > 0
+    # The offsets give the scan its document starts (the ids are then read at
+    # chunk ends only) and, without `lengths`, fixed-order masked lengths.
+    need = n_docs > 0 and rows * S > 0 and (want_adv or want_returns or want_lam)
     off = _doc_offsets(doc_ids, n_docs) if offsets and need else None
     g.seg_offsets = _lib.ptr(off)
     rc = lib.meshy_gae(_lib.ctypes.byref(g), _lib.stream_of(dev))

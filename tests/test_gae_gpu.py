@@ -243,6 +243,35 @@ def test_offsets_and_atomic_counts_agree(dev, docs_per_row):
     assert (l0.cpu() - ref_lam).abs().max().item() <= 1e-6
 
 
+@pytest.mark.parametrize("docs_per_row,rows,S", [(2, 4, 9000), (12, 3, 12000), (20, 2, 12000), (3, 1, 70000)])
+def test_scan_from_offsets_equals_scan_from_ids(dev, docs_per_row, rows, S):
+    """With offsets the scan reads the ids only at chunk ends and takes the
+    document starts between them from the offsets (chunks with up to four
+    starts) or reads every id (more): the same ids either way, so advantages,
+    returns and lambdas are bitwise equal to the per-token-id scan.  Doc sizes
+    put chunks on both sides of the four-start limit; a padding slot ends the
+    grid; bf16 and fp32 values; with and without lengths."""
+    from meshy_amd import gae
+
+    rewards, values, mask, doc_ids, n_docs = _random_grid(rows, S, docs_per_row, seed=S + docs_per_row)
+    doc_ids[-1, -37:] = n_docs  # the padding slot
+    mask[-1, -37:] = 0.0
+    lengths = torch.rand(n_docs, generator=torch.Generator().manual_seed(1)) * 900 + 1
+    for vals in (values, values.to(torch.bfloat16)):
+        d = [t.to(dev) for t in (rewards, vals, mask, doc_ids)]
+        for lens in (None, lengths.to(dev)):
+            kw = dict(lengths=lens, gamma=0.97, alpha=1.5, epsilon=1e-6, want_adv=True, want_returns=True,
+                      want_lam=True)
+            a0, r0, l0 = gae._run(*d, n_docs, offsets=True, **kw)
+            a1, r1, l1 = gae._run(*d, n_docs, offsets=False, **kw)
+            assert torch.equal(a0, a1) and torch.equal(r0, r1) and torch.equal(l0, l1)
+    ref_adv, _ = ogae.compute_vapo_gae(rewards, values, mask, doc_ids, n_docs, lengths=lengths, gamma=0.97,
+                                       alpha=1.5)
+    a, _, _ = gae._run(*[t.to(dev) for t in (rewards, values, mask, doc_ids)], n_docs, lengths=lengths.to(dev),
+                       gamma=0.97, alpha=1.5, epsilon=1e-6, want_adv=True, want_returns=False, want_lam=False)
+    assert (a.cpu() - ref_adv).abs().max().item() <= TOL
+
+
 def _critic_samples(n, seed, max_len=700, bf16=False):
     g = torch.Generator().manual_seed(seed)
     out = []
