@@ -856,6 +856,14 @@ def bench_critic(steps, warmup, no_cpu):
     # reads values 2 + returns 4 + mask 4 per grid element
     out["accumulator_update_1024_docs_padded"] = _entry(ms * 1e3, rows * S * 10, cpu_ms, rows=rows, S=S,
                                                       note="wall time including the state's host read")
+    # critic_diagnostics over the same window (groups of 8 rows): the token
+    # sums, the per-prompt AUC and Pearson, one host read
+    dms = _wall_ms(lambda: critic.critic_diagnostics(vals, rets, msk, rew, grp), steps // 5 + 3, warmup=2)
+    dcpu = None
+    if not no_cpu:
+        dcpu = _wall_ms(lambda: ocritic.critic_diagnostics(vc, rc, mc, rwc, gc), 3, gpu=False)
+    out["critic_diagnostics_1024_docs_padded"] = _entry(dms * 1e3, rows * S * 10, dcpu, rows=rows, S=S,
+                                                      note="wall time including the host read of the gauges")
     out["whiten_1024_docs"] = bench_whiten(batch, dev, steps, warmup, no_cpu)
     return out
 

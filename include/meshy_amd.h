@@ -579,6 +579,49 @@ int meshy_critic_accumulate(const void* values, int32_t values_bf16, const float
 int meshy_clipped_value_error(const float* values, const float* targets, const float* old_values,
                               int32_t has_clip, float clip, int64_t n, float* out,
                               hipStream_t stream);
+
+/* ------------------------------------------------------------------------
+ * Critic gauges of one window (device).
+ *
+ * meshy_critic_window_sums: the token-level part of critic_diagnostics
+ * (meshy/backend/titan/critic/metrics.py:189-217) over a [rows, S] row-major
+ * window, with the mask m as given (fractional values included).  With
+ * e = v - r (fp32), sel = (m > 0):
+ *   sums[MESHY_CW_SEL]    #sel                sums[MESHY_CW_M]    sum m
+ *   sums[MESHY_CW_R]      sum_sel r           sums[MESHY_CW_E2M]  sum e^2 m
+ *   sums[MESHY_CW_R2]     sum_sel r^2         sums[MESHY_CW_EM]   sum e m
+ *   sums[MESHY_CW_D]      sum_sel e           sums[MESHY_CW_RMIN] min_sel r
+ *   sums[MESHY_CW_D2]     sum_sel e^2         sums[MESHY_CW_RMAX] max_sel r
+ * (fp64, device; the sel sums select, as variance_reduction does, metrics.py:
+ * 120-138; the m sums multiply, as the loss and calibration_gap do), and
+ * row_value[row] = sum_S v m / max(sum_S m, 1) (_response_mean, 58-62).
+ * Workspace: MESHY_CW_VALS doubles per row.  Rows are reduced in a fixed
+ * order: the same bits on every call.
+ *
+ * meshy_group_gauges: within_prompt_auc (metrics.py:94-118) and prompt_pearson
+ * (64-91) over n rows in any order, grouped by group_ids.  A row is correct
+ * when row_reward >= correct_threshold.  out[0] = wins (pairs of a correct and
+ * an incorrect row of one group where the correct one's value is greater, ties
+ * counting 1/2), out[1] = such pairs, out[2] = groups, out[3] = Pearson r of
+ * the groups' mean value against their mean reward (NaN for fewer than two
+ * groups or a constant side).  The AUC is out[0] / out[1] (NaN without
+ * pairs).  O(n^2) pair checks (n is a window's row count); workspace 5
+ * doubles per row; fixed-order reductions.
+ * ---------------------------------------------------------------------- */
+enum {
+    MESHY_CW_SEL = 0, MESHY_CW_R, MESHY_CW_R2, MESHY_CW_D, MESHY_CW_D2,
+    MESHY_CW_M, MESHY_CW_E2M, MESHY_CW_EM, MESHY_CW_RMIN, MESHY_CW_RMAX,
+    MESHY_CW_VALS
+};
+size_t meshy_critic_window_workspace_size(int64_t rows);
+int meshy_critic_window_sums(const void* values, int32_t values_bf16, const float* returns,
+                             const float* mask, int64_t rows, int64_t S, double* sums,
+                             float* row_value, void* workspace, size_t workspace_bytes,
+                             hipStream_t stream);
+size_t meshy_group_gauges_workspace_size(int64_t n);
+int meshy_group_gauges(const float* row_value, const float* row_reward, const int64_t* group_ids,
+                       int64_t n, float correct_threshold, double* out, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
 int meshy_clipped_value_error_bwd(const float* values, const float* targets,
                                   const float* old_values, int32_t has_clip, float clip, int64_t n,
                                   const float* grad_out, int64_t grad_stride, float* grad_values,

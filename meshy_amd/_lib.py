@@ -37,6 +37,10 @@ PPO_OUT_NAMES = (
 )
 PPO_NOUT = len(PPO_OUT_NAMES)
 
+# meshy_critic_window_sums' value order (MESHY_CW_* in include/meshy_amd.h)
+CW_SEL, CW_R, CW_R2, CW_D, CW_D2, CW_M, CW_E2M, CW_EM, CW_RMIN, CW_RMAX = range(10)
+CW_VALS = 10
+
 
 class PlannerCfg(ctypes.Structure):
     _fields_ = [
@@ -295,6 +299,15 @@ SIGNATURES = {
     "meshy_stream_read": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "meshy_per_sequence_mean": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "meshy_critic_accumulate_workspace_size": (c_size_t, [c_int64]),
+    "meshy_critic_window_workspace_size": (c_size_t, [c_int64]),
+    "meshy_critic_window_sums": (
+        c_int, [c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
+                c_size_t, c_void_p]
+    ),
+    "meshy_group_gauges_workspace_size": (c_size_t, [c_int64]),
+    "meshy_group_gauges": (
+        c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_float, c_void_p, c_void_p, c_size_t, c_void_p]
+    ),
     "meshy_critic_accumulate": (
         c_int, [c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
                 c_size_t, c_void_p]

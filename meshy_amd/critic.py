@@ -9,13 +9,19 @@
 * ``clipped_value_error`` (meshy/backend/titan/vapo.py:35-41): an autograd
   Function over ``meshy_clipped_value_error`` and its backward.
 
+* ``critic_diagnostics`` / ``diagnostics_from_states`` / ``CriticDiagnostics``
+  and the gauges ``within_prompt_auc``, ``prompt_pearson``,
+  ``variance_reduction``, ``calibration_gap`` (metrics.py:58-217, 278-328):
+  ``meshy_critic_window_sums`` reduces the window's tokens and
+  ``meshy_group_gauges`` its rows; one host read per call.
+
 ``compute_returns`` on the critic path (engine/critic.py:348-350) is
 ``meshy_amd.gae.compute_returns``.
 """
 
 from __future__ import annotations
 
-from dataclasses import dataclass, field
+from dataclasses import asdict, dataclass, field
 
 import torch
 
@@ -119,6 +125,179 @@ class Accumulator:
         return self._state
 
 
+@dataclass(frozen=True)
+class CriticDiagnostics:
+    """The window's critic gauges (metrics.py:162-186): the same fields, dict
+    form and one-line text."""
+
+    value_loss: float
+    critic_auc: float
+    critic_var_ratio: float
+    critic_calibration_gap: float
+    prompt_pearson: float
+    n_rows: int
+    n_prompts: int
+    n_tokens: int
+
+    def as_dict(self) -> dict[str, float]:
+        return asdict(self)
+
+    def __str__(self) -> str:
+        return (
+            f"value_loss={self.value_loss:.4f}  "
+            f"within_prompt_auc={self.critic_auc:.4f}  "
+            f"var_reduction={self.critic_var_ratio:+.4f}  "
+            f"calib_gap={self.critic_calibration_gap:+.4f}  "
+            f"prompt_pearson={self.prompt_pearson:+.4f}  "
+            f"[{self.n_rows} rows / {self.n_prompts} prompts / {self.n_tokens} tokens]"
+        )
+
+
+def _window_sums(values: torch.Tensor, returns: torch.Tensor, mask: torch.Tensor):
+    """The token sums of ``meshy_critic_window_sums`` (fp64 [10], device) and
+    each row's masked mean value."""
+    if values.dim() != 2 or returns.shape != values.shape or mask.shape != values.shape:
+        raise ValueError("values, returns and mask must be [rows, S] of one shape")
+    _lib.require_gpu(values, returns, mask)
+    dev = values.device
+    rows, S = values.shape
+    bf16 = values.dtype == torch.bfloat16
+    v = values.contiguous() if bf16 else values.to(torch.float32).contiguous()
+    r = returns.to(torch.float32).contiguous()
+    m = mask.to(torch.float32).contiguous()
+    sums = torch.empty(_lib.CW_VALS, dtype=torch.float64, device=dev)
+    row_value = torch.empty(rows, dtype=torch.float32, device=dev)
+    lib = _lib.load()
+    ws = torch.empty(max(int(lib.meshy_critic_window_workspace_size(rows)), 1), dtype=torch.uint8, device=dev)
+    rc = lib.meshy_critic_window_sums(v.data_ptr(), int(bf16), r.data_ptr(), m.data_ptr(), rows, S, sums.data_ptr(),
+                                      row_value.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(dev))
+    _lib.check(rc, "meshy_critic_window_sums")
+    return sums, row_value
+
+
+def _group_gauges(row_value: torch.Tensor, row_reward: torch.Tensor, group_ids: torch.Tensor,
+                  correct_threshold: float, device: torch.device) -> torch.Tensor:
+    """``meshy_group_gauges`` on the device: fp64 [wins, pairs, groups, Pearson r]."""
+    v = row_value.detach().reshape(-1).to(device=device, dtype=torch.float32).contiguous()
+    r = row_reward.detach().reshape(-1).to(device=device, dtype=torch.float32).contiguous()
+    g = group_ids.detach().reshape(-1).to(device=device, dtype=torch.int64).contiguous()
+    n = v.numel()
+    if r.numel() != n or g.numel() != n:
+        raise ValueError(f"{n} row values but {r.numel()} rewards and {g.numel()} group ids")
+    out = torch.empty(4, dtype=torch.float64, device=device)
+    lib = _lib.load()
+    ws = torch.empty(max(int(lib.meshy_group_gauges_workspace_size(n)), 1), dtype=torch.uint8, device=device)
+    rc = lib.meshy_group_gauges(v.data_ptr(), r.data_ptr(), g.data_ptr(), n, float(correct_threshold),
+                                out.data_ptr(), ws.data_ptr(), ws.numel(), _lib.stream_of(device))
+    _lib.check(rc, "meshy_group_gauges")
+    return out
+
+
+def _gauge_device(*tensors: torch.Tensor) -> torch.device:
+    for t in tensors:
+        if t.is_cuda:
+            return t.device
+    if not torch.cuda.is_available():
+        raise RuntimeError("the critic gauges run on a HIP device and none is available")
+    return torch.device("cuda", torch.cuda.current_device())
+
+
+def _auc(gauges: list[float]) -> float:
+    return gauges[0] / gauges[1] if gauges[1] > 0 else float("nan")
+
+
+def within_prompt_auc(row_value: torch.Tensor, row_correct: torch.Tensor, group_ids: torch.Tensor) -> float:
+    """Pooled-pairs AUC of V ranking a prompt's correct rows above its
+    incorrect ones, ties 1/2; NaN when no prompt holds both (metrics.py:94-118)."""
+    dev = _gauge_device(row_value, row_correct, group_ids)
+    return _auc(_group_gauges(row_value, row_correct.float(), group_ids, 0.5, dev).tolist())
+
+
+def prompt_pearson(row_value: torch.Tensor, row_reward: torch.Tensor, group_ids: torch.Tensor) -> float:
+    """Pearson r between each prompt's mean V and its mean reward; NaN for
+    fewer than two prompts or a constant side (metrics.py:64-91)."""
+    dev = _gauge_device(row_value, row_reward, group_ids)
+    return float(_group_gauges(row_value, row_reward, group_ids, 0.5, dev)[3].item())
+
+
+def _var_ratio(c: list[float]) -> float:
+    n = c[_lib.CW_SEL]
+    if n < 2 or c[_lib.CW_RMIN] == c[_lib.CW_RMAX]:
+        return float("nan")  # too few tokens, or constant returns (zero variance)
+    var_r = c[_lib.CW_R2] / n - (c[_lib.CW_R] / n) ** 2
+    var_d = c[_lib.CW_D2] / n - (c[_lib.CW_D] / n) ** 2
+    return 1.0 - var_d / var_r
+
+
+def variance_reduction(values: torch.Tensor, returns: torch.Tensor, mask: torch.Tensor) -> float:
+    """``1 - Var(return - V) / Var(return)`` over the tokens with mask > 0
+    (metrics.py:120-138)."""
+    sums, _ = _window_sums(values, returns, mask)
+    return _var_ratio(sums.tolist())
+
+
+def calibration_gap(values: torch.Tensor, returns: torch.Tensor, mask: torch.Tensor) -> float:
+    """Mean signed error ``sum (V - return) m / max(sum m, 1)`` (metrics.py:141-160)."""
+    c = _window_sums(values, returns, mask)[0].tolist()
+    return c[_lib.CW_EM] / max(c[_lib.CW_M], 1.0)
+
+
+def critic_diagnostics(values: torch.Tensor, returns: torch.Tensor, mask: torch.Tensor, rewards: torch.Tensor,
+                       group_ids: torch.Tensor, *, correct_threshold: float = 0.5) -> CriticDiagnostics:
+    """The four gauges plus the masked value loss of a whole [rows, S] window
+    (metrics.py:189-217), from one pass over its tokens and one over its rows."""
+    sums, row_value = _window_sums(values, returns, mask)
+    if rewards.numel() != values.shape[0] or group_ids.numel() != values.shape[0]:
+        raise ValueError(f"{values.shape[0]} rows but {rewards.numel()} rewards and {group_ids.numel()} group ids")
+    gauges = _group_gauges(row_value, rewards.float(), group_ids, correct_threshold, values.device)
+    c = torch.cat([sums, gauges]).tolist()  # one host read
+    g = c[_lib.CW_VALS:]
+    n_tok = max(c[_lib.CW_M], 1.0)
+    return CriticDiagnostics(
+        value_loss=c[_lib.CW_E2M] / n_tok,
+        critic_auc=_auc(g),
+        critic_var_ratio=_var_ratio(c),
+        critic_calibration_gap=c[_lib.CW_EM] / n_tok,
+        prompt_pearson=g[3],
+        n_rows=int(values.shape[0]),
+        n_prompts=int(g[2]),
+        n_tokens=int(c[_lib.CW_M]),
+    )
+
+
+def diagnostics_from_states(states: list[AccumulatorState], *, correct_threshold: float = 0.5,
+                            device: torch.device | str | None = None) -> CriticDiagnostics:
+    """Merge per-rank partials into the verdict ``critic_diagnostics`` gives
+    (metrics.py:278-328): the token gauges from the five sums, the per-prompt
+    gauges from the rows (any order, any rank) on the device."""
+    n = sum(s.n_tokens for s in states)
+    if n <= 0:
+        raise ValueError("cannot build diagnostics from states with no masked tokens")
+    sum_r = sum(s.sum_r for s in states)
+    sum_r2 = sum(s.sum_r2 for s in states)
+    sum_d = sum(s.sum_d for s in states)
+    sum_d2 = sum(s.sum_d2 for s in states)
+    # Var(x) = E[x^2] - E[x]^2, the population form
+    var_r = sum_r2 / n - (sum_r / n) ** 2
+    var_d = sum_d2 / n - (sum_d / n) ** 2
+    var_ratio = float("nan") if var_r == 0.0 or n < 2 else 1.0 - var_d / var_r
+    dev = torch.device(device) if device is not None else _gauge_device()
+    row_value = torch.tensor([x for s in states for x in s.row_value], dtype=torch.float32)
+    row_reward = torch.tensor([x for s in states for x in s.row_reward], dtype=torch.float32)
+    group_ids = torch.tensor([x for s in states for x in s.row_group], dtype=torch.int64)
+    g = _group_gauges(row_value, row_reward, group_ids, correct_threshold, dev).tolist()
+    return CriticDiagnostics(
+        value_loss=sum_d2 / n,
+        critic_auc=_auc(g),
+        critic_var_ratio=var_ratio,
+        critic_calibration_gap=sum_d / n,
+        prompt_pearson=g[3],
+        n_rows=int(row_value.numel()),
+        n_prompts=int(g[2]),
+        n_tokens=int(n),
+    )
+
+
 class _ClippedValueError(torch.autograd.Function):
     @staticmethod
     def forward(ctx, v, t, o, clip):
@@ -169,5 +348,6 @@ def clipped_value_error(values: torch.Tensor, targets: torch.Tensor, old_values:
     return _ClippedValueError.apply(v, t, o, clip).reshape(shape)
 
 
-__all__ = ["Accumulator", "AccumulatorState", "advantages_to_per_sequence", "clipped_value_error",
-           "compute_returns"]
+__all__ = ["Accumulator", "AccumulatorState", "CriticDiagnostics", "advantages_to_per_sequence",
+           "calibration_gap", "clipped_value_error", "compute_returns", "critic_diagnostics",
+           "diagnostics_from_states", "prompt_pearson", "variance_reduction", "within_prompt_auc"]

@@ -8,6 +8,11 @@
 //                               with m = (mask > 0), v = values m, r = returns m,
 //                               d = v - r, the window sums of m, r, r^2, d, d^2
 //                               (fp64) and each row's v-sum / max(m-sum, 1);
+//   meshy_critic_window_sums    critic_diagnostics' token-level sums
+//                               (meshy/backend/titan/critic/metrics.py:189-217)
+//                               with the mask as given, and each row's mean V;
+//   meshy_group_gauges          within_prompt_auc and prompt_pearson
+//                               (metrics.py:64-118) over a window's rows;
 //   meshy_clipped_value_error   clipped_value_error (meshy/backend/titan/vapo.py:35-41)
 //   (+ _bwd)                    max((v - t)^2, (o + clamp(v - o, -c, c) - t)^2)
 //                               and its gradient as torch autograd gives it
@@ -293,6 +298,226 @@ __global__ __launch_bounds__(kThreads) void k_cve_bwd(const float* __restrict__ 
         gv[i] = cve_grad(v[i], t[i], has_clip ? o[i] : 0.f, clip, has_clip, g[i * gs]);
 }
 
+// ---------------------------------------------------------- window gauges
+// critic_diagnostics' token-level sums (meshy/backend/titan/critic/metrics.py:
+// 189-217) with the float mask as given: one workgroup per row, each thread
+// accumulating its strided elements in fp64 (this runs once per window, not
+// per step), then a fixed-order workgroup sum; the window takes a second
+// one-workgroup pass over the rows.
+constexpr int kCwSums = MESHY_CW_RMIN;  // the summed values; min and max follow
+
+__global__ __launch_bounds__(kThreads) void k_cw_rows(const void* __restrict__ values, int values_bf16,
+                                                      const float* __restrict__ returns,
+                                                      const float* __restrict__ mask, int64_t S,
+                                                      double* __restrict__ part, float* __restrict__ row_value) {
+    __shared__ double s_red[kCwSums + 1][kWaves];
+    __shared__ float s_min[kWaves], s_max[kWaves];
+    const int64_t row = blockIdx.x;
+    const int64_t base = row * S;
+    double a[kCwSums + 1];  // the sums, then sum v m of the row
+#pragma unroll
+    for (int k = 0; k <= kCwSums; ++k) a[k] = 0.0;
+    float rmin = __builtin_inff(), rmax = -__builtin_inff();
+    for (int64_t j = base + threadIdx.x; j < base + S; j += kThreads) {
+        const float m = mask[j];
+        const float v = load_value(values, values_bf16, j);
+        const float r = returns[j];
+        const float e = v - r;
+        const bool sel = m > 0.f;
+        // variance_reduction selects the masked tokens; the loss, the
+        // calibration gap and the row mean multiply by the mask.
+        a[MESHY_CW_SEL] += sel ? 1.0 : 0.0;
+        a[MESHY_CW_R] += sel ? static_cast<double>(r) : 0.0;
+        a[MESHY_CW_R2] += sel ? static_cast<double>(r) * r : 0.0;
+        a[MESHY_CW_D] += sel ? static_cast<double>(e) : 0.0;
+        a[MESHY_CW_D2] += sel ? static_cast<double>(e) * e : 0.0;
+        a[MESHY_CW_M] += m;
+        a[MESHY_CW_E2M] += static_cast<double>(e * e * m);
+        a[MESHY_CW_EM] += static_cast<double>(e * m);
+        a[kCwSums] += static_cast<double>(v * m);
+        rmin = (sel && r < rmin) ? r : rmin;
+        rmax = (sel && r > rmax) ? r : rmax;
+    }
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+#pragma unroll
+    for (int k = 0; k <= kCwSums; ++k) {
+        const double w = wave_sum(a[k]);
+        if (lane == 0) s_red[k][wid] = w;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const float lo = __shfl_xor(rmin, off, kWave);
+        const float hi = __shfl_xor(rmax, off, kWave);
+        rmin = lo < rmin ? lo : rmin;
+        rmax = hi > rmax ? hi : rmax;
+    }
+    if (lane == 0) {
+        s_min[wid] = rmin;
+        s_max[wid] = rmax;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        double t[kCwSums + 1];
+        float lo = __builtin_inff(), hi = -__builtin_inff();
+#pragma unroll
+        for (int k = 0; k <= kCwSums; ++k) {
+            t[k] = 0.0;
+            for (int w = 0; w < kWaves; ++w) t[k] += s_red[k][w];
+        }
+        for (int w = 0; w < kWaves; ++w) {
+            lo = s_min[w] < lo ? s_min[w] : lo;
+            hi = s_max[w] > hi ? s_max[w] : hi;
+        }
+        double* dst = part + row * MESHY_CW_VALS;
+#pragma unroll
+        for (int k = 0; k < kCwSums; ++k) dst[k] = t[k];
+        dst[MESHY_CW_RMIN] = lo;
+        dst[MESHY_CW_RMAX] = hi;
+        row_value[row] = static_cast<float>(t[kCwSums] / fmax(t[MESHY_CW_M], 1.0));
+    }
+}
+
+__global__ __launch_bounds__(kThreads) void k_cw_final(const double* __restrict__ part, int64_t rows,
+                                                       double* __restrict__ sums) {
+    __shared__ double s_red[kWaves];
+    for (int k = 0; k < kCwSums; ++k) {
+        double v = 0.0;
+        for (int64_t r = threadIdx.x; r < rows; r += kThreads) v += part[r * MESHY_CW_VALS + k];
+        v = block_sum_to0(v, s_red);
+        if (threadIdx.x == 0) sums[k] = v;
+    }
+    // min and max of r over the selected tokens (+inf / -inf when none)
+    double lo = __builtin_inf(), hi = -__builtin_inf();
+    for (int64_t r = threadIdx.x; r < rows; r += kThreads) {
+        const double a = part[r * MESHY_CW_VALS + MESHY_CW_RMIN];
+        const double b = part[r * MESHY_CW_VALS + MESHY_CW_RMAX];
+        lo = a < lo ? a : lo;
+        hi = b > hi ? b : hi;
+    }
+#pragma unroll
+    for (int off = kWave / 2; off > 0; off >>= 1) {
+        const double a = __shfl_xor(lo, off, kWave);
+        const double b = __shfl_xor(hi, off, kWave);
+        lo = a < lo ? a : lo;
+        hi = b > hi ? b : hi;
+    }
+    __shared__ double s_lo[kWaves], s_hi[kWaves];
+    if (threadIdx.x % kWave == 0) {
+        s_lo[threadIdx.x / kWave] = lo;
+        s_hi[threadIdx.x / kWave] = hi;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < kWaves; ++w) {
+            lo = s_lo[w] < lo ? s_lo[w] : lo;
+            hi = s_hi[w] > hi ? s_hi[w] : hi;
+        }
+        sums[MESHY_CW_RMIN] = lo;
+        sums[MESHY_CW_RMAX] = hi;
+    }
+}
+
+// ---------------------------------------------------------- group gauges
+// within_prompt_auc (metrics.py:94-118) and prompt_pearson (64-91): one
+// wavefront per row i scans every row j of the window (rows arrive in any
+// order and group ids are arbitrary), so row i learns its group's sums and
+// whether an earlier row shares its group, and, when it is correct, its wins
+// against the group's incorrect rows.  part[i] = {2 wins, pairs, first in
+// its group, group mean value, group mean reward}.
+constexpr int kGaugeVals = 5;
+
+__global__ __launch_bounds__(kWave) void k_group_rows(const float* __restrict__ value,
+                                                      const float* __restrict__ reward,
+                                                      const int64_t* __restrict__ gid, int64_t n, float thr,
+                                                      double* __restrict__ part) {
+    const int64_t i = blockIdx.x;
+    const int lane = threadIdx.x;
+    const int64_t gi = gid[i];
+    const float vi = value[i];
+    const bool ci = reward[i] >= thr;
+    double wins2 = 0.0, pairs = 0.0, sv = 0.0, sr = 0.0, cnt = 0.0;
+    bool earlier = false;
+    for (int64_t j = lane; j < n; j += kWave) {
+        const bool same = gid[j] == gi;
+        const float vj = value[j];
+        const float rj = reward[j];
+        const bool cj = rj >= thr;
+        cnt += same ? 1.0 : 0.0;
+        sv += same ? static_cast<double>(vj) : 0.0;
+        sr += same ? static_cast<double>(rj) : 0.0;
+        earlier = earlier || (same && j < i);
+        const bool pair = same && ci && !cj;
+        pairs += pair ? 1.0 : 0.0;
+        // NaN values compare neither greater nor equal: the pair counts, it never wins
+        wins2 += pair ? (vi > vj ? 2.0 : (vi == vj ? 1.0 : 0.0)) : 0.0;
+    }
+    wins2 = wave_sum(wins2);
+    pairs = wave_sum(pairs);
+    sv = wave_sum(sv);
+    sr = wave_sum(sr);
+    cnt = wave_sum(cnt);
+    const bool any_earlier = __ballot(earlier) != 0;
+    if (lane == 0) {
+        double* dst = part + i * kGaugeVals;
+        dst[0] = wins2;
+        dst[1] = pairs;
+        dst[2] = any_earlier ? 0.0 : 1.0;
+        dst[3] = sv / cnt;  // cnt >= 1: row i is in its own group
+        dst[4] = sr / cnt;
+    }
+}
+
+// One workgroup: the wins, pairs and groups in a fixed order, then Pearson r
+// over the groups' means, centred in a second pass as the reference does.
+__global__ __launch_bounds__(kThreads) void k_group_final(const double* __restrict__ part, int64_t n,
+                                                          double* __restrict__ out) {
+    __shared__ double s_red[kWaves];
+    double w = 0.0, p = 0.0, g = 0.0, mv = 0.0, mr = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += kThreads) {
+        const double* q = part + i * kGaugeVals;
+        const bool first = q[2] != 0.0;
+        w += q[0];
+        p += q[1];
+        g += q[2];
+        mv += first ? q[3] : 0.0;
+        mr += first ? q[4] : 0.0;
+    }
+    w = block_sum_to0(w, s_red);
+    p = block_sum_to0(p, s_red);
+    __shared__ double s_g, s_mv, s_mr;
+    g = block_sum_to0(g, s_red);
+    mv = block_sum_to0(mv, s_red);
+    mr = block_sum_to0(mr, s_red);
+    if (threadIdx.x == 0) {
+        s_g = g;
+        s_mv = g > 0.0 ? mv / g : 0.0;
+        s_mr = g > 0.0 ? mr / g : 0.0;
+    }
+    __syncthreads();
+    const double G = s_g, cv = s_mv, cr = s_mr;
+    double xy = 0.0, xx = 0.0, yy = 0.0;
+    for (int64_t i = threadIdx.x; i < n; i += kThreads) {
+        const double* q = part + i * kGaugeVals;
+        const bool first = q[2] != 0.0;
+        const double dv = first ? q[3] - cv : 0.0;
+        const double dr = first ? q[4] - cr : 0.0;
+        xy += dv * dr;
+        xx += dv * dv;
+        yy += dr * dr;
+    }
+    xy = block_sum_to0(xy, s_red);
+    xx = block_sum_to0(xx, s_red);
+    yy = block_sum_to0(yy, s_red);
+    if (threadIdx.x == 0) {
+        const double den = sqrt(xx) * sqrt(yy);
+        out[0] = 0.5 * w;
+        out[1] = p;
+        out[2] = G;
+        out[3] = (G < 2.0 || den == 0.0) ? __builtin_nan("") : xy / den;
+    }
+}
+
 }  // namespace
 }  // namespace meshy
 
@@ -369,5 +594,58 @@ extern "C" int meshy_clipped_value_error_bwd(const float* values, const float* t
                      (grad_stride == 0 || al16(grad_out));
     hipLaunchKernelGGL(k_cve_bwd, dim3(static_cast<unsigned>(ceil_div(n, 4 * kThreads))), dim3(kThreads), 0, stream,
                        values, targets, old_values, clip, has_clip, n, vec, grad_out, grad_stride, grad_values);
+    return check_launch(who);
+}
+
+extern "C" size_t meshy_critic_window_workspace_size(int64_t rows) {
+    return rows < 0 ? 0 : meshy::align_up(sizeof(double) * MESHY_CW_VALS * static_cast<size_t>(rows), 256);
+}
+
+extern "C" int meshy_critic_window_sums(const void* values, int32_t values_bf16, const float* returns,
+                                        const float* mask, int64_t rows, int64_t S, double* sums,
+                                        float* row_value, void* workspace, size_t workspace_bytes,
+                                        hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    const char* who = "meshy_critic_window_sums";
+    if (rows < 0 || S < 0 || rows > INT32_MAX) return set_error(MESHY_EINVAL, "%s: bad shape", who);
+    if (!sums || (rows > 0 && (!values || !returns || !mask || !row_value)))
+        return set_error(MESHY_ENULL, "%s: NULL pointer", who);
+    if (workspace_bytes < meshy_critic_window_workspace_size(rows) || (rows > 0 && !workspace))
+        return set_error(MESHY_ESPACE, "%s: workspace needs %zu bytes", who, meshy_critic_window_workspace_size(rows));
+    double* part = static_cast<double*>(workspace);
+    if (rows > 0) {
+        hipLaunchKernelGGL(k_cw_rows, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, stream, values,
+                           values_bf16, returns, mask, S, part, row_value);
+        int rc = check_launch(who);
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(k_cw_final, dim3(1), dim3(kThreads), 0, stream, part, rows, sums);
+    return check_launch(who);
+}
+
+extern "C" size_t meshy_group_gauges_workspace_size(int64_t n) {
+    return n < 0 ? 0 : meshy::align_up(sizeof(double) * meshy::kGaugeVals * static_cast<size_t>(n), 256);
+}
+
+extern "C" int meshy_group_gauges(const float* row_value, const float* row_reward, const int64_t* group_ids,
+                                  int64_t n, float correct_threshold, double* out, void* workspace,
+                                  size_t workspace_bytes, hipStream_t stream) {
+    using namespace meshy;
+    clear_error();
+    const char* who = "meshy_group_gauges";
+    if (n < 0 || n > INT32_MAX) return set_error(MESHY_EINVAL, "%s: bad size", who);
+    if (!out || (n > 0 && (!row_value || !row_reward || !group_ids)))
+        return set_error(MESHY_ENULL, "%s: NULL pointer", who);
+    if (workspace_bytes < meshy_group_gauges_workspace_size(n) || (n > 0 && !workspace))
+        return set_error(MESHY_ESPACE, "%s: workspace needs %zu bytes", who, meshy_group_gauges_workspace_size(n));
+    double* part = static_cast<double*>(workspace);
+    if (n > 0) {
+        hipLaunchKernelGGL(k_group_rows, dim3(static_cast<unsigned>(n)), dim3(kWave), 0, stream, row_value,
+                           row_reward, group_ids, n, correct_threshold, part);
+        int rc = check_launch(who);
+        if (rc) return rc;
+    }
+    hipLaunchKernelGGL(k_group_final, dim3(1), dim3(kThreads), 0, stream, part, n, out);
     return check_launch(who);
 }

@@ -64,6 +64,14 @@ def _call(name, *args):
     ("meshy_grpo_advantage", (FAKE, 8, FAKE, -1, FAKE, None), EINVAL, "negative"),
     ("meshy_grpo_advantage", (FAKE, -8, FAKE, 1, FAKE, None), EINVAL, "negative"),
     ("meshy_grpo_advantage", (None, 8, FAKE, 3, FAKE, None), ENULL, "NULL"),
+    # values, bf16, returns, mask, rows, S, sums, row_value, workspace, bytes, stream
+    ("meshy_critic_window_sums", (FAKE, 0, FAKE, FAKE, -1, 8, FAKE, FAKE, FAKE, 4096, None), EINVAL, "bad shape"),
+    ("meshy_critic_window_sums", (FAKE, 0, None, FAKE, 2, 8, FAKE, FAKE, FAKE, 4096, None), ENULL, "NULL"),
+    ("meshy_critic_window_sums", (FAKE, 0, FAKE, FAKE, 64, 8, FAKE, FAKE, FAKE, 8, None), ESPACE, "workspace"),
+    # row_value, row_reward, group_ids, n, threshold, out, workspace, bytes, stream
+    ("meshy_group_gauges", (FAKE, FAKE, FAKE, -3, 0.5, FAKE, FAKE, 4096, None), EINVAL, "bad size"),
+    ("meshy_group_gauges", (FAKE, None, FAKE, 3, 0.5, FAKE, FAKE, 4096, None), ENULL, "NULL"),
+    ("meshy_group_gauges", (FAKE, FAKE, FAKE, 300, 0.5, FAKE, FAKE, 8, None), ESPACE, "workspace"),
     # raw_rewards, n_rewards, group_offsets, n_groups, tolerance, flags, stream
     ("meshy_zero_variance_groups", (FAKE, 8, FAKE, -1, 1e-8, FAKE, None), EINVAL, "negative"),
     ("meshy_zero_variance_groups", (None, 8, FAKE, 2, 1e-8, FAKE, None), ENULL, "NULL"),

@@ -7,6 +7,8 @@ Bars: per-sequence means, row values and the clipped value error within 1e-5
 packs built from samples bit for bit.
 """
 
+import math
+
 import numpy as np
 import pytest
 import torch
@@ -97,6 +99,129 @@ def _gauge_window(rows=24, span=40, seed=0):
     rewards = (torch.rand(rows, generator=g) > 0.5).float()
     groups = torch.arange(rows) // 4
     return values, returns, mask, rewards, groups
+
+
+def _diag_dict(d):
+    return d.as_dict()
+
+
+def _odd_window(rows, S, seed, *, frac=False, bf16=False):
+    """Rows in shuffled group order with arbitrary ids, all-correct and
+    all-incorrect groups, tied row values, and (frac) a fractional mask."""
+    g = torch.Generator().manual_seed(seed)
+    mask = (torch.rand(rows, S, generator=g) > 0.3).float()
+    mask[:, : S // 5] = 0.0
+    if frac:
+        mask = mask * torch.rand(rows, S, generator=g)
+    mask[rows // 3] = 0.0  # a row with no token
+    returns = torch.randn(rows, S, generator=g)
+    values = returns + 0.5 * torch.randn(rows, S, generator=g)
+    values[rows // 2] = 0.25  # ties across rows
+    values[rows // 2 + 1] = 0.25
+    groups = torch.randint(0, max(1, rows // 4), (rows,), generator=g) * 13 - 40
+    rewards = (torch.rand(rows, generator=g) > 0.5).float()
+    rewards[groups == groups[0]] = 1.0  # an all-correct group
+    if bf16:
+        values = values.to(torch.bfloat16)
+    return values, returns, mask, rewards, groups
+
+
+@pytest.mark.parametrize("rows,S,frac,bf16", [(24, 40, False, False), (37, 300, True, False), (64, 1000, False, True),
+                                             (300, 129, True, True)])
+def test_critic_diagnostics_matches_oracle(dev, rows, S, frac, bf16):
+    from meshy_amd import critic
+
+    v, r, m, rew, grp = _odd_window(rows, S, seed=rows + S, frac=frac, bf16=bf16)
+    got = critic.critic_diagnostics(v.to(dev), r.to(dev), m.to(dev), rew.to(dev), grp.to(dev)).as_dict()
+    want = ocritic.critic_diagnostics(v.float(), r, m, rew, grp)
+    assert ocritic.same_gauges(got, want, rel=1e-4, abs_=1e-5), (got, want)
+    assert got["n_rows"] == want["n_rows"] and got["n_prompts"] == want["n_prompts"]
+    assert got["n_tokens"] == want["n_tokens"] or frac  # int() of a fractional sum may round apart
+
+
+def test_critic_diagnostics_degenerate_windows(dev):
+    """NaN where the reference gives NaN: one prompt (Pearson), no prompt with
+    both classes (AUC), constant returns (variance ratio)."""
+    from meshy_amd import critic
+
+    v, r, m, rew, _ = _odd_window(12, 64, seed=5)
+    one = torch.zeros(12, dtype=torch.long)
+    d = critic.critic_diagnostics(v.to(dev), r.to(dev), m.to(dev), rew.to(dev), one.to(dev))
+    assert math.isnan(d.prompt_pearson) and d.n_prompts == 1
+    d = critic.critic_diagnostics(v.to(dev), r.to(dev), m.to(dev), torch.ones(12, device=dev), one.to(dev))
+    assert math.isnan(d.critic_auc)
+    d = critic.critic_diagnostics(v.to(dev), torch.full_like(r, 0.5).to(dev), m.to(dev), rew.to(dev), one.to(dev))
+    assert math.isnan(d.critic_var_ratio)
+    want = ocritic.critic_diagnostics(v, torch.full_like(r, 0.5), m, rew, one)
+    assert math.isnan(want["critic_var_ratio"])
+    assert "within_prompt_auc=" in str(d) and "[12 rows / 1 prompts /" in str(d)
+
+
+def test_diagnostics_from_states_match_whole_window(dev):
+    """test_critic_batching.py:158-213 through this library: device
+    accumulators over 5-row micro-batches and an interleaved two-rank split give
+    the gauges of critic_diagnostics on the whole window (0/1 mask), and the
+    oracle's diagnostics_from_states on the same states."""
+    from meshy_amd import critic
+
+    for seed in (0, 1, 2):
+        w = _gauge_window(seed=seed)
+        want = critic.critic_diagnostics(*(x.to(dev) for x in w)).as_dict()
+        assert ocritic.same_gauges(want, ocritic.critic_diagnostics(*w), rel=1e-5, abs_=1e-6)
+        stream = critic.Accumulator()
+        for lo in range(0, 24, 5):
+            stream.update(*(x[lo:lo + 5].to(dev) for x in w))
+        got = critic.diagnostics_from_states([stream.state]).as_dict()
+        assert ocritic.same_gauges(got, want, rel=1e-5, abs_=1e-6), (got, want)
+        states = []
+        for rank in range(2):
+            sel = torch.arange(rank, 24, 2)
+            acc = critic.Accumulator()
+            acc.update(*(x[sel].to(dev) for x in w))
+            states.append(acc.state)
+        got = critic.diagnostics_from_states(states).as_dict()
+        assert ocritic.same_gauges(got, want, rel=1e-5, abs_=1e-6), (got, want)
+        assert got["n_rows"] == 24 and got["n_tokens"] == want["n_tokens"]
+    with pytest.raises(ValueError, match="no masked tokens"):
+        critic.diagnostics_from_states([critic.AccumulatorState()])
+
+
+@pytest.mark.parametrize("n", [1, 2, 65, 1000, 4097])
+def test_group_gauges_match_oracle(dev, n):
+    """AUC and Pearson over n rows with arbitrary, unsorted group ids, tied
+    values and NaN values (they pair but never win)."""
+    from meshy_amd import critic
+
+    g = torch.Generator().manual_seed(n)
+    vals = torch.round(torch.randn(n, generator=g) * 4) / 4
+    if n > 10:
+        vals[3] = float("nan")
+    rew = torch.rand(n, generator=g)
+    grp = torch.randint(-3, max(1, n // 6), (n,), generator=g) * 1000003
+    want_auc = ocritic.within_prompt_auc(vals, rew >= 0.5, grp)
+    want_r = ocritic.prompt_pearson(vals[~vals.isnan()], rew[~vals.isnan()], grp[~vals.isnan()])
+    got_auc = critic.within_prompt_auc(vals.to(dev), (rew >= 0.5).to(dev), grp.to(dev))
+    assert (math.isnan(want_auc) and math.isnan(got_auc)) or got_auc == pytest.approx(want_auc, abs=1e-12)
+    if n <= 10:
+        got_r = critic.prompt_pearson(vals.to(dev), rew.to(dev), grp.to(dev))
+        assert (math.isnan(want_r) and math.isnan(got_r)) or got_r == pytest.approx(want_r, abs=1e-5)
+    else:
+        # a NaN value makes its group's mean NaN, and so the correlation
+        assert math.isnan(critic.prompt_pearson(vals.to(dev), rew.to(dev), grp.to(dev)))
+        ok = ~vals.isnan()
+        got_r = critic.prompt_pearson(vals[ok].to(dev), rew[ok].to(dev), grp[ok].to(dev))
+        assert (math.isnan(want_r) and math.isnan(got_r)) or got_r == pytest.approx(want_r, abs=1e-5)
+
+
+def test_variance_reduction_and_calibration_gap(dev):
+    from meshy_amd import critic
+
+    v, r, m, _, _ = _odd_window(40, 200, seed=9, frac=True)
+    assert critic.variance_reduction(v.to(dev), r.to(dev), m.to(dev)) == pytest.approx(
+        ocritic.variance_reduction(v, r, m), rel=1e-5)
+    assert critic.calibration_gap(v.to(dev), r.to(dev), m.to(dev)) == pytest.approx(
+        ocritic.calibration_gap(v, r, m), rel=1e-5, abs=1e-7)
+    assert math.isnan(critic.variance_reduction(v.to(dev), r.to(dev), torch.zeros_like(m).to(dev)))
 
 
 def _sums(states):
