@@ -584,20 +584,27 @@ def bench_long_context(steps, warmup, no_cpu):
     plan = build_plan(lengths, lengths, 1, cfg)
     T = max(m.seq_len for mini in plan.per_rank[0] for m in mini.micros)
     V = 131072
-    gen = torch.Generator(device=dev).manual_seed(3)
-    logits = torch.randn(1, T, V, generator=gen, device=dev, dtype=torch.bfloat16) * 2.0
-    labels = torch.randint(0, V, (1, T), generator=gen, device=dev)
+    # logits from the counter-based generator (std 2), so the CPU leg
+    # regenerates its rows on the host instead of copying them
+    logits = workloads.synth_logits(T, V, seed=3, scale=2.0, device=dev).unsqueeze(0)
+    labels = torch.randint(0, V, (1, T), generator=torch.Generator(device=dev).manual_seed(3), device=dev)
     ms = _gpu_ms(lambda: logprob.logprobs_and_entropy(logits, labels, with_entropy=True), steps, warmup)
     cpu_ms = None
     rows = 8192
     if not no_cpu:
-        tps, cms = cpu_logprob_tokens_per_s(logits, labels, rows, runs=3)
+        from oracle import logprob as olp
+
+        z = workloads.synth_logit_rows(range(rows), V, seed=3, scale=2.0).unsqueeze(0)
+        y = labels[:, :rows].cpu()
+        cms = _wall_ms(lambda: olp.forward_logprobs(z, y, chunk=1024, with_entropy=True, entropy_chunk_size=512),
+                       3, gpu=False)
         cpu_ms = cms * T / rows  # scaled to the full micro
     del logits
     torch.cuda.empty_cache()
     nbytes = T * V * 2 + 16 * T
     return _entry(ms * 1e3, nbytes, cpu_ms, T=T, V=V, tokens_per_s=round(T / (ms * 1e-3)),
-                  cpu_sample=f"{rows} rows, scaled to T")
+                  cpu_sample=f"{rows} rows regenerated on the host, scaled to T",
+                  data="counter-based synthetic logits, std 2 (meshy_synth_bf16, seed 3)")
 
 
 # ---------------------------------------------------------------- GAE over 1024 docs

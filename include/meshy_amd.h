@@ -658,6 +658,25 @@ int meshy_ragged_token_stats(const float* mask, const float* logprobs, const int
 int meshy_stream_read(const void* src, int64_t rows, int64_t row_bytes, uint32_t* out,
                       hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Counter-based synthetic bf16 logits (device and host, the same bits).
+ * No reference counterpart: the synthetic inputs of the measured workloads,
+ * regenerated on the host for the rows a parity check reads, instead of
+ * copying a tensor of up to 34 GB.  Element k = row * cols + col is
+ *   h = mix(mix(seed) ^ k), mix = splitmix64's finaliser;
+ *   s = the sum of h's four 16-bit fields (Irwin-Hall of four uniforms);
+ *   x = (float(s) - 131070) * float(scale * sqrt(3) / 65536);
+ *   bf16(x) rounded to nearest even
+ * (mean 0, standard deviation scale, bounded at +-2 sqrt(3) scale).
+ * meshy_synth_bf16 fills out[row * row_stride + col] for a [rows, cols]
+ * block on the stream; meshy_synth_bf16_rows_host writes rows row_ids[i] of
+ * the same block to out[i * cols ...] on host threads.
+ * ---------------------------------------------------------------------- */
+int meshy_synth_bf16(uint16_t* out, int64_t rows, int64_t cols, int64_t row_stride, uint64_t seed, float scale,
+                     hipStream_t stream);
+int meshy_synth_bf16_rows_host(uint16_t* out, const int64_t* row_ids, int64_t n_rows, int64_t cols,
+                               uint64_t seed, float scale);
+
 #ifdef __cplusplus
 }
 #endif

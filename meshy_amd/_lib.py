@@ -9,7 +9,7 @@ from __future__ import annotations
 
 import ctypes
 import os
-from ctypes import POINTER, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_void_p
+from ctypes import POINTER, c_double, c_float, c_int, c_int32, c_int64, c_size_t, c_uint64, c_void_p
 
 LIB_NAME = "libmeshy_amd.so"
 LIB_PATH = os.path.join(os.path.dirname(os.path.abspath(__file__)), LIB_NAME)
@@ -299,6 +299,8 @@ SIGNATURES = {
     "meshy_stream_read": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "meshy_per_sequence_mean": (c_int, [c_void_p, c_void_p, c_void_p, c_int64, c_void_p, c_void_p]),
     "meshy_critic_accumulate_workspace_size": (c_size_t, [c_int64]),
+    "meshy_synth_bf16": (c_int, [c_void_p, c_int64, c_int64, c_int64, c_uint64, c_float, c_void_p]),
+    "meshy_synth_bf16_rows_host": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_uint64, c_float]),
     "meshy_critic_window_workspace_size": (c_size_t, [c_int64]),
     "meshy_critic_window_sums": (
         c_int, [c_void_p, c_int32, c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p,

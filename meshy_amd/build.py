@@ -20,7 +20,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "libmeshy_amd.so")
 
-SOURCES = ("capi.cpp", "plan.cpp", "hostio.cpp", "logprob.hip", "topk.hip", "distill.hip", "pack.hip", "ppo.hip", "gae.hip", "critic.hip", "ragged.hip")
+SOURCES = ("capi.cpp", "plan.cpp", "hostio.cpp", "logprob.hip", "topk.hip", "distill.hip", "pack.hip", "ppo.hip", "gae.hip", "critic.hip", "ragged.hip", "synth.hip")
 
 ARCH = os.environ.get("MESHY_OFFLOAD_ARCH", "gfx950")
 

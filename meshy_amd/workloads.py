@@ -9,6 +9,9 @@ generator takes a seed and is reproducible on any host.
     ppo_512_docs             PPO loss: 512 docs, response lognormal(4000, 0.8) clipped [16, 8192]
     long_context_16_lengths  long context: 16 sequences U{8192..131072}, budget 131072
     gae_1024_docs            GAE: 1024 docs, response lognormal(6000, 0.8) clipped [32, 32768]
+    synth_logits             bf16 logits from the counter-based generator (meshy_synth_bf16),
+                             filled on the device; synth_logit_rows regenerates any of their
+                             rows on the host, bit for bit
 """
 
 from __future__ import annotations
@@ -126,3 +129,34 @@ def gae_1024_docs(seed: int = 4):
     values = rng.standard_normal(batch.total).astype(np.float32)
     terminal = (rng.random(n_docs) < 0.5).astype(np.float32)
     return batch, values, terminal
+
+
+def synth_logits(rows: int, cols: int, seed: int, scale: float = 2.0, device=None):
+    """A [rows, cols] bf16 tensor of counter-based synthetic logits (mean 0,
+    standard deviation ``scale``), filled on the HIP device."""
+    import torch
+
+    from . import _lib
+
+    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
+    out = torch.empty(rows, cols, dtype=torch.bfloat16, device=dev)
+    _lib.require_gpu(out)
+    rc = _lib.load().meshy_synth_bf16(out.data_ptr(), rows, cols, cols, int(seed) & (2**64 - 1), float(scale),
+                                      _lib.stream_of(dev))
+    _lib.check(rc, "meshy_synth_bf16")
+    return out
+
+
+def synth_logit_rows(row_ids, cols: int, seed: int, scale: float = 2.0):
+    """Rows ``row_ids`` of ``synth_logits(*, cols, seed, scale)``, regenerated
+    on the host (CPU bf16 tensor [len(row_ids), cols])."""
+    import torch
+
+    from . import _lib
+
+    ids = torch.as_tensor(row_ids, dtype=torch.int64).reshape(-1).contiguous()
+    out = torch.empty(ids.numel(), cols, dtype=torch.bfloat16)
+    rc = _lib.load().meshy_synth_bf16_rows_host(out.data_ptr(), ids.data_ptr(), ids.numel(), cols,
+                                                int(seed) & (2**64 - 1), float(scale))
+    _lib.check(rc, "meshy_synth_bf16_rows_host")
+    return out

@@ -5,10 +5,13 @@ and its backward over the largest micro's bf16 logits [T, 131072].
 * every micro the GPU pack materialises is bit-exact against the oracle's
   build_micro_batch (batch.py:142-178) for the native plan (plan.py:211-288,
   itself pinned by the golden plans);
-* logp and entropy (trainer.py:414-449) on 8192 seeded rows of the largest
-  micro, labels being that micro's packed labels, within 1e-3 of the oracle;
-* the logits gradient of the whole micro (trainer.py:504-517) on 1024 seeded
-  rows within the bf16 rounding of the oracle's fp32 autograd gradient.
+* logp and entropy (trainer.py:414-449) on 8192 seeded rows of every micro
+  (all rows of a shorter one), labels being that micro's packed labels, within
+  1e-3 of the oracle.  The logits [T, 131072] come from the counter-based
+  generator on the device, and the host regenerates the checked rows instead
+  of copying them;
+* the logits gradient of the whole largest micro (trainer.py:504-517) on 1024
+  seeded rows within the bf16 rounding of the oracle's fp32 autograd gradient.
 """
 
 from __future__ import annotations
@@ -68,44 +71,65 @@ def test_every_long_micro_bit_exact(long_micros):
         assert mb.attention_masks.max_q == ref["max_seqlen"]
 
 
-def test_logprob_and_backward_on_the_largest_long_micro(dev, long_micros):
-    from meshy_amd import logprob
+N_MICROS = 7  # the plan of the 16 seeded lengths (asserted below)
+
+
+@pytest.mark.parametrize("j", range(N_MICROS))
+def test_logprob_on_every_long_micro(dev, long_micros, j):
+    """Logits of micro j come from the counter-based generator (seed 100 + j)
+    on the device; the host regenerates 8192 seeded rows (all rows of a shorter
+    micro) bit for bit and the oracle checks logp and entropy there."""
+    from meshy_amd import logprob, workloads
+
+    _, micros, mbs = long_micros
+    assert len(micros) == N_MICROS
+    labels = mbs[j].labels
+    T = labels.shape[1]
+    assert int(labels.max()) < V
+    z = workloads.synth_logits(T, V, seed=100 + j, device=dev).unsqueeze(0)
+    lp, ent = logprob.logprobs_and_entropy(z, labels, with_entropy=True)
+    assert torch.isfinite(lp).all() and torch.isfinite(ent).all()
+    n = min(T, 8192)
+    rows = np.sort(np.random.default_rng(7 + j).choice(T, n, replace=False))
+    zs = workloads.synth_logit_rows(rows, V, seed=100 + j)
+    probe = torch.from_numpy(rows[[0, n // 2, n - 1]]).to(dev)
+    assert torch.equal(z[0, probe].cpu(), zs[[0, n // 2, n - 1]])  # the host rows are the device's
+    rows_t = torch.from_numpy(rows).to(dev)
+    lp_s, ent_s, ys = lp[0, rows_t].cpu(), ent[0, rows_t].cpu(), labels[0, rows_t].cpu()
+    worst_lp = worst_ent = 0.0
+    for a in range(0, n, 1024):
+        zc = zs[a:a + 1024].unsqueeze(0)
+        worst_lp = max(worst_lp, (lp_s[a:a + 1024] - olp.chunk_logprobs(zc, ys[a:a + 1024].unsqueeze(0))[0])
+                       .abs().max().item())
+        worst_ent = max(worst_ent, (ent_s[a:a + 1024] - olp.chunk_entropy(zc)[0]).abs().max().item())
+    print(f"micro {j}: T={T} V={V}, {n} seeded rows: max|dlogp|={worst_lp:.2e} max|dH|={worst_ent:.2e}", flush=True)
+    assert worst_lp <= TOL and worst_ent <= TOL
+
+
+def test_backward_on_the_largest_long_micro(dev, long_micros):
+    """The logits gradient of the whole largest micro (trainer.py:504-517),
+    checked on 1024 seeded rows regenerated on the host, within the bf16
+    rounding of the oracle's fp32 autograd gradient."""
+    from meshy_amd import logprob, workloads
 
     _, micros, mbs = long_micros
     j = max(range(len(micros)), key=lambda i: micros[i].seq_len)
     labels = mbs[j].labels
     T = labels.shape[1]
     print(f"largest long micro: T={T} V={V} ({T * V * 2 / 1e9:.1f} GB of logits)", flush=True)
-    assert T >= 8192 and int(labels.max()) < V
-    gen = torch.Generator(device=dev).manual_seed(3)
-    z = torch.randn(1, T, V, generator=gen, device=dev, dtype=torch.bfloat16) * 2.0
-    lp, ent = logprob.logprobs_and_entropy(z, labels, with_entropy=True)
-    assert torch.isfinite(lp).all() and torch.isfinite(ent).all()
-
-    rows = torch.from_numpy(np.sort(np.random.default_rng(7).choice(T, 8192, replace=False))).to(dev)
-    zs, ys = z[0, rows], labels[0, rows]
-    lp_s, ent_s = lp[0, rows].cpu(), ent[0, rows].cpu()
-    worst_lp = worst_ent = 0.0
-    for a in range(0, 8192, 1024):
-        zc = zs[a:a + 1024].cpu().unsqueeze(0)
-        worst_lp = max(worst_lp, (lp_s[a:a + 1024] - olp.chunk_logprobs(zc, ys[a:a + 1024].cpu().unsqueeze(0))[0])
-                       .abs().max().item())
-        worst_ent = max(worst_ent, (ent_s[a:a + 1024] - olp.chunk_entropy(zc)[0]).abs().max().item())
-    print(f"8192 seeded rows: max|dlogp|={worst_lp:.2e} max|dH|={worst_ent:.2e}", flush=True)
-    assert worst_lp <= TOL and worst_ent <= TOL
-    del zs
-
-    # Backward over the whole micro, checked on 1024 seeded rows.
+    assert T >= 8192
+    z = workloads.synth_logits(T, V, seed=100 + j, device=dev).unsqueeze(0)
     g = torch.randn(1, T, generator=torch.Generator().manual_seed(8)).to(dev)
-    zg = z.detach().requires_grad_(True)
+    zg = z.requires_grad_(True)
     lpg = logprob.logprobs_and_entropy(zg, labels)
     (lpg * g).sum().backward()
     grad = zg.grad
     assert grad.shape == z.shape and grad.dtype == torch.bfloat16
-    rows = torch.from_numpy(np.sort(np.random.default_rng(9).choice(T, 1024, replace=False))).to(dev)
-    got = grad[0, rows].float().cpu()
-    ref = olp.logprob_grad(z[0, rows].cpu().unsqueeze(0), labels[0, rows].cpu().unsqueeze(0),
-                           g[0, rows].cpu().unsqueeze(0))[0]
-    gr = g[0, rows].cpu().abs()
+    rows = np.sort(np.random.default_rng(9).choice(T, 1024, replace=False))
+    rows_t = torch.from_numpy(rows).to(dev)
+    got = grad[0, rows_t].float().cpu()
+    ref = olp.logprob_grad(workloads.synth_logit_rows(rows, V, seed=100 + j).unsqueeze(0),
+                           labels[0, rows_t].cpu().unsqueeze(0), g[0, rows_t].cpu().unsqueeze(0))[0]
+    gr = g[0, rows_t].cpu().abs()
     assert torch.isfinite(got).all()
     assert ((got - ref).abs() <= 4e-3 * gr[:, None] + 1e-30).all()
