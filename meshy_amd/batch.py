@@ -12,6 +12,7 @@ reference's fields (batch.py:52-74) so the forward and the loss read it as is.
 
 from __future__ import annotations
 
+import weakref
 from dataclasses import dataclass
 from typing import Any, NamedTuple, Sequence
 
@@ -509,7 +510,8 @@ class _PackViews:
             f["advantages"] = at
         if sdi is di:  # not replaced by a context-parallel shard
             d0 = self.doc_start[k]
-            mb.__dict__["_meshy_seg_src"] = ((id(di), di._version, di.data_ptr(), self.nd[k]), self.seg, d0 + 2 * k)
+            mb.__dict__["_meshy_seg_src"] = ((id(di), di._version, di.data_ptr(), self.nd[k]), self.seg, d0 + 2 * k,
+                                             weakref.ref(di))
 
     def doc_fields(self, mb: "PackedBatch", f: dict) -> None:
         """Per-document advantages, lengths and positive-LM weights of micro mb._k."""

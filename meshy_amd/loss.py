@@ -15,6 +15,7 @@ _reduce_mini_metrics (trainer.py:1020-1047).
 
 from __future__ import annotations
 
+import weakref
 from typing import Any
 
 import torch
@@ -33,26 +34,29 @@ def batch_segment_offsets(mb: Any) -> torch.Tensor:
     recomputes."""
     ids = mb.doc_ids
     key = (id(ids), ids._version, ids.data_ptr(), int(mb.n_docs))
+    # Both caches name their doc_ids tensor by a weak reference as well as by
+    # its id: a replaced tensor may reuse the id and the address of a freed one.
     hit = getattr(mb, "_meshy_seg_offsets", None)
-    if hit is not None and hit[0] == key:
+    if hit is not None and hit[0] == key and hit[2]() is ids:
         return hit[1]
     src = getattr(mb, "_meshy_seg_src", None)
-    if src is not None and src[0] == key:
+    if src is not None and src[0] == key and src[3]() is ids:
         # Written by the pack kernel next to doc_ids: no pass over the ids.
         off = src[1][src[2]:src[2] + key[3] + 2]
     else:
         off = checked_segment_offsets(ids, int(mb.n_docs) + 1)
     try:
-        object.__setattr__(mb, "_meshy_seg_offsets", (key, off))
+        object.__setattr__(mb, "_meshy_seg_offsets", (key, off, weakref.ref(ids)))
     except (AttributeError, TypeError):
         pass  # a batch type without an attribute dict: no cache
     return off
 
 
 # Segment offsets of recently seen doc_ids tensors whose order was checked,
-# None for a tensor found out of order (each entry holds its tensor, so the
-# identity in the key stays unique while cached).
-_CHECKED: dict[tuple, tuple[torch.Tensor, torch.Tensor | None]] = {}
+# None for a tensor found out of order.  Entries hold a weak reference to
+# their tensor: a hit needs the same live object (its id and data pointer
+# may be reused once it is freed), and the cache never keeps a batch alive.
+_CHECKED: dict[tuple, tuple[weakref.ref, torch.Tensor | None]] = {}
 _CHECKED_MAX = 16
 
 
@@ -63,16 +67,17 @@ def checked_segment_offsets(doc_ids: torch.Tensor, n_slots: int) -> torch.Tensor
     that order, which both batch layouts have (batch.py:123, 150-162)."""
     key = (id(doc_ids), doc_ids._version, doc_ids.data_ptr(), int(n_slots))
     hit = _CHECKED.get(key)
-    if hit is not None:
+    if hit is not None and hit[0]() is doc_ids:
         off = hit[1]
     else:
         try:
             off = segment_offsets(doc_ids, n_slots, check_sorted=True)
         except ValueError:
             off = None
+        _CHECKED.pop(key, None)
         if len(_CHECKED) >= _CHECKED_MAX:
             _CHECKED.pop(next(iter(_CHECKED)))
-        _CHECKED[key] = (doc_ids, off)
+        _CHECKED[key] = (weakref.ref(doc_ids), off)
     if off is None:
         raise ValueError("doc_ids must be non-decreasing over the flattened micro-batch")
     return off

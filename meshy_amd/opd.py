@@ -77,7 +77,9 @@ def build_topk_micro_batches(
             lps = torch.zeros(shape, dtype=torch.float32, device=job.device)
         kw = {f: getattr(mb, f) for f in _BATCH_FIELDS}
         tb = TopKBatch(**kw, teacher_topk_ids=ids, teacher_topk_logprobs=lps)
-        tb._meshy_seg_src = mb._meshy_seg_src  # the pack's document offsets (same doc_ids)
+        src = getattr(mb, "_meshy_seg_src", None)  # the pack's document offsets (same doc_ids)
+        if src is not None:
+            tb._meshy_seg_src = src
         out.append(tb)
     return out
 
