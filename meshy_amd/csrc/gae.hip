@@ -64,11 +64,6 @@ __device__ __forceinline__ Pair compose(const Pair& l, const Pair& r) {
 }
 __device__ __forceinline__ Pair identity_pair() { return Pair{Aff{1.f, 0.f}, Aff{1.f, 0.f}}; }
 
-__device__ __forceinline__ Pair shfl_down_pair(const Pair& v, int off) {
-    return Pair{Aff{__shfl_down(v.adv.p, off, kWave), __shfl_down(v.adv.q, off, kWave)},
-                Aff{__shfl_down(v.ret.p, off, kWave), __shfl_down(v.ret.q, off, kWave)}};
-}
-
 struct Workspace {
     float* cnt;     // [n_docs + 1]
     Pair* chunk;    // [n_chunks]
@@ -139,11 +134,11 @@ struct ChunkDocs {
     bool use;
 };
 
-__device__ __forceinline__ int64_t uniform_i64(int64_t v) {
-    const uint64_t u = static_cast<uint64_t>(v);
-    const uint32_t lo = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u));
-    const uint32_t hi = __builtin_amdgcn_readfirstlane(static_cast<uint32_t>(u >> 32));
-    return static_cast<int64_t>((static_cast<uint64_t>(hi) << 32) | lo);
+// A load at a workgroup-uniform address of data the kernel does not write,
+// through the scalar unit: it waits on its own counter, not behind the
+// vector loads issued before it.
+__device__ __forceinline__ int64_t load_scalar(const int64_t* p) {
+    return *(const __attribute__((address_space(4))) int64_t*)(p);
 }
 
 __device__ __forceinline__ ChunkDocs chunk_docs(const meshy_gae_args& g, int64_t c0, int64_t n) {
@@ -154,14 +149,14 @@ __device__ __forceinline__ ChunkDocs chunk_docs(const meshy_gae_args& g, int64_t
     for (int r = 0; r < kMaxStarts; ++r) cd.start[r] = INT64_MAX;
     if (!g.seg_offsets || c0 >= n) return cd;
     const int64_t e = min(c0 + kChunk + 1, n);
-    const int64_t d0 = uniform_i64(g.doc_ids[c0]);
-    const int64_t d1 = uniform_i64(g.doc_ids[e - 1]);
+    const int64_t d0 = load_scalar(g.doc_ids + c0);
+    const int64_t d1 = load_scalar(g.doc_ids + e - 1);
     if (d0 < 0 || d1 > g.n_docs || d1 < d0 || d1 - d0 > kMaxStarts) return cd;
     cd.use = true;
     cd.d0 = d0;
 #pragma unroll
     for (int r = 0; r < kMaxStarts; ++r)
-        if (r < d1 - d0) cd.start[r] = uniform_i64(g.seg_offsets[d0 + 1 + r]);
+        if (r < d1 - d0) cd.start[r] = load_scalar(g.seg_offsets + d0 + 1 + r);
     return cd;
 }
 
@@ -174,9 +169,11 @@ __device__ __forceinline__ int64_t id_in_chunk(const ChunkDocs& cd, int64_t t) {
     return d;
 }
 
-template <bool kOff>
-__device__ __forceinline__ void load_inputs(const meshy_gae_args& g, int64_t t0, int64_t n, bool vec,
-                                            const ChunkDocs& cd, ThreadInputs& in) {
+// Mask, rewards and values of the thread's kItems positions and the next one
+// (its neighbour in time), with 16-byte vector loads when the run is whole
+// and aligned.
+__device__ __forceinline__ void load_tokens(const meshy_gae_args& g, int64_t t0, int64_t n, bool vec,
+                                            ThreadInputs& in) {
     const bool whole = vec && t0 + kItems <= n;
     if (whole) {
 #pragma unroll
@@ -185,14 +182,6 @@ __device__ __forceinline__ void load_inputs(const meshy_gae_args& g, int64_t t0,
             const f32x4 r4 = *reinterpret_cast<const f32x4*>(g.rewards + t0 + 4 * q);
             in.mk[4 * q + 0] = m4.x; in.mk[4 * q + 1] = m4.y; in.mk[4 * q + 2] = m4.z; in.mk[4 * q + 3] = m4.w;
             in.r[4 * q + 0] = r4.x; in.r[4 * q + 1] = r4.y; in.r[4 * q + 2] = r4.z; in.r[4 * q + 3] = r4.w;
-        }
-        if constexpr (!kOff) {
-#pragma unroll
-            for (int q = 0; q < kItems / 2; ++q) {
-                const i64x2 d2 = *reinterpret_cast<const i64x2*>(g.doc_ids + t0 + 2 * q);
-                in.d[2 * q] = d2.x;
-                in.d[2 * q + 1] = d2.y;
-            }
         }
         if (g.values) {
             if (g.values_bf16) {
@@ -230,7 +219,6 @@ __device__ __forceinline__ void load_inputs(const meshy_gae_args& g, int64_t t0,
             const bool ok = t < n;
             in.mk[k] = ok ? g.mask[t] : 0.f;
             in.r[k] = ok ? g.rewards[t] : 0.f;
-            if constexpr (!kOff) in.d[k] = ok ? g.doc_ids[t] : -1;
             in.v[k] = ok ? value_at(g, t) : 0.f;
         }
     }
@@ -238,22 +226,49 @@ __device__ __forceinline__ void load_inputs(const meshy_gae_args& g, int64_t t0,
     const bool okn = tn < n;
     in.mk[kItems] = okn ? g.mask[tn] : 0.f;
     in.v[kItems] = okn ? value_at(g, tn) : 0.f;
-    if constexpr (kOff) {
+}
+
+// Every position's id from doc_ids (-1 past n).
+__device__ __forceinline__ void load_ids(const meshy_gae_args& g, int64_t t0, int64_t n, bool vec,
+                                         ThreadInputs& in) {
+    if (vec && t0 + kItems <= n) {
+#pragma unroll
+        for (int q = 0; q < kItems / 2; ++q) {
+            const i64x2 d2 = *reinterpret_cast<const i64x2*>(g.doc_ids + t0 + 2 * q);
+            in.d[2 * q] = d2.x;
+            in.d[2 * q + 1] = d2.y;
+        }
+    } else {
+#pragma unroll
+        for (int k = 0; k < kItems; ++k) in.d[k] = (t0 + k < n) ? g.doc_ids[t0 + k] : -1;
+    }
+    const int64_t tn = t0 + kItems;
+    in.d[kItems] = tn < n ? g.doc_ids[tn] : -1;
+}
+
+// The thread's inputs: the token loads first, then the chunk's documents
+// (scalar loads, which do not wait behind them), then the ids, from the
+// chunk's starts when it has them, else from doc_ids.  The branch on cd.use is
+// uniform over the workgroup.
+__device__ __forceinline__ void load_inputs(const meshy_gae_args& g, int64_t c0, int64_t t0, int64_t n, bool vec,
+                                            ThreadInputs& in) {
+    load_tokens(g, t0, n, vec, in);
+    const ChunkDocs cd = chunk_docs(g, c0, n);
+    if (cd.use) {
 #pragma unroll
         for (int k = 0; k <= kItems; ++k) in.d[k] = (t0 + k < n) ? id_in_chunk(cd, t0 + k) : -1;
     } else {
-        in.d[kItems] = okn ? g.doc_ids[tn] : -1;
+        load_ids(g, t0, n, vec, in);
     }
 }
 
 // The affine maps of a thread's positions t0 .. t0 + kItems - 1 (identity past n).
 // Row ends come from a column counter started with one division; lambda is
 // recomputed only when the document changes.
-template <bool kOff>
-__device__ __forceinline__ void thread_maps(const meshy_gae_args& g, const float* cnt, int64_t t0, int64_t n,
-                                            bool vec, const ChunkDocs& cd, Pair (&items)[kItems]) {
+__device__ __forceinline__ void thread_maps(const meshy_gae_args& g, const float* cnt, int64_t c0, int64_t t0,
+                                            int64_t n, bool vec, Pair (&items)[kItems]) {
     ThreadInputs in;
-    load_inputs<kOff>(g, t0, n, vec, cd, in);
+    load_inputs(g, c0, t0, n, vec, in);
     int64_t s = t0 % g.S;
     int64_t cur_d = -2;
     float cur_lam = 0.f;
@@ -284,29 +299,85 @@ __device__ __forceinline__ void thread_maps(const meshy_gae_args& g, const float
     }
 }
 
-// Suffix composition across the block: returns, for each thread, the map of
-// all items of the threads after it (exclusive), and the block total.
+// DPP moves (checked on the device): row_shl:N, lane l reads lane l + N of its
+// 16-lane row; wave_shl:1, lane l reads lane l + 1 of the wave.  A lane whose
+// source lies past the row's (wave's) end keeps its own value.
+constexpr int kDppRowShl1 = 0x101, kDppRowShl2 = 0x102, kDppRowShl4 = 0x104, kDppRowShl8 = 0x108;
+constexpr int kDppWaveShl1 = 0x130;
+
+template <int kCtrl>
+__device__ __forceinline__ float dpp_mov(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(__float_as_int(v), __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+
+template <int kCtrl>
+__device__ __forceinline__ Pair dpp_pair(const Pair& v) {
+    return Pair{Aff{dpp_mov<kCtrl>(v.adv.p), dpp_mov<kCtrl>(v.adv.q)},
+                Aff{dpp_mov<kCtrl>(v.ret.p), dpp_mov<kCtrl>(v.ret.q)}};
+}
+
+__device__ __forceinline__ Pair lane_pair(const Pair& v, int l) {
+    return Pair{Aff{lane_f32(v.adv.p, l), lane_f32(v.adv.q, l)}, Aff{lane_f32(v.ret.p, l), lane_f32(v.ret.q, l)}};
+}
+
+// Composition of the 64 lanes' maps in lane order (lane 0 leftmost), as a
+// fixed tree: pairs, quads, eights and sixteens within each row through DPP
+// shifts (lanes 0, 16, 32, 48 then hold their row's fold), then
+// (row 0 o row 1) o (row 2 o row 3) from those lanes.  The result is in
+// every lane.  All 64 lanes must be active.
+__device__ __forceinline__ Pair wave_fold(Pair x) {
+    x = compose(x, dpp_pair<kDppRowShl1>(x));
+    x = compose(x, dpp_pair<kDppRowShl2>(x));
+    x = compose(x, dpp_pair<kDppRowShl4>(x));
+    x = compose(x, dpp_pair<kDppRowShl8>(x));
+    return compose(compose(lane_pair(x, 0), lane_pair(x, 16)), compose(lane_pair(x, 32), lane_pair(x, 48)));
+}
+
+// Suffix composition across the block (lane order, lane 0 leftmost): for each
+// thread the map of all items of the threads after it (exclusive), and the
+// block total.  Within each 16-lane row a scan through DPP row shifts (lane l
+// then holds its row's suffix from l); the rows' folds, read from lanes 0, 16,
+// 32 and 48, complete each lane's suffix to the wave's end; the waves meet in
+// LDS.  All 64 lanes of every wave must be active.
 __device__ __forceinline__ Pair block_suffix_exclusive(Pair mine, Pair* s_wave, Pair& total) {
     const int lane = threadIdx.x % kWave;
     const int wid = threadIdx.x / kWave;
+    const int rl = lane % 16;
     constexpr int kW = kThreads / kWave;
-    Pair incl = mine;  // becomes compose(mine, ..., last lane of the wave)
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const Pair other = shfl_down_pair(incl, off);
-        if (lane + off < kWave) incl = compose(incl, other);
+    Pair incl = mine;
+    {
+        const Pair o = dpp_pair<kDppRowShl1>(incl);
+        incl = rl + 1 < 16 ? compose(incl, o) : incl;
     }
-    if (lane == 0) s_wave[wid] = incl;  // whole-wave map
+    {
+        const Pair o = dpp_pair<kDppRowShl2>(incl);
+        incl = rl + 2 < 16 ? compose(incl, o) : incl;
+    }
+    {
+        const Pair o = dpp_pair<kDppRowShl4>(incl);
+        incl = rl + 4 < 16 ? compose(incl, o) : incl;
+    }
+    {
+        const Pair o = dpp_pair<kDppRowShl8>(incl);
+        incl = rl + 8 < 16 ? compose(incl, o) : incl;
+    }
+    const Pair r0 = lane_pair(incl, 0);
+    const Pair r3 = lane_pair(incl, 48);
+    const Pair a1 = compose(lane_pair(incl, 32), r3);  // rows 2, 3
+    const Pair a0 = compose(lane_pair(incl, 16), a1);  // rows 1, 2, 3
+    const int row = lane / 16;
+    const Pair after_row = row == 0 ? a0 : (row == 1 ? a1 : (row == 2 ? r3 : identity_pair()));
+    incl = compose(incl, after_row);  // lane l .. lane 63
+    if (lane == 0) s_wave[wid] = compose(r0, a0);  // whole-wave map
     __syncthreads();
     Pair after_wave = identity_pair();
     for (int w = kW - 1; w > wid; --w) after_wave = compose(s_wave[w], after_wave);
     total = identity_pair();
     for (int w = kW - 1; w >= 0; --w) total = compose(s_wave[w], total);
     __syncthreads();
-    // exclusive within the wave = inclusive of the next lane.
-    Pair next = shfl_down_pair(incl, 1);
-    Pair excl = (lane + 1 < kWave) ? compose(next, after_wave) : after_wave;
-    return excl;
+    // exclusive within the wave = inclusive of the next lane
+    const Pair next = dpp_pair<kDppWaveShl1>(incl);
+    return lane + 1 < kWave ? compose(next, after_wave) : after_wave;
 }
 
 __global__ __launch_bounds__(kThreads) void k_gae_zero(float* p, int64_t n) {
@@ -355,14 +426,9 @@ __global__ __launch_bounds__(kCountThreads) void k_gae_doc_count(const float* __
 }
 
 // Builds the thread's maps (contiguous positions) and folds them right to left.
-// The branch on cd.use is uniform over the workgroup and holds each path's
-// loads and arithmetic whole.
-__device__ __forceinline__ Pair load_items(const meshy_gae_args& g, const float* cnt, int64_t t0, int64_t n,
-                                           bool vec, const ChunkDocs& cd, Pair (&items)[kItems]) {
-    if (cd.use)
-        thread_maps<true>(g, cnt, t0, n, vec, cd, items);
-    else
-        thread_maps<false>(g, cnt, t0, n, vec, cd, items);
+__device__ __forceinline__ Pair load_items(const meshy_gae_args& g, const float* cnt, int64_t c0, int64_t t0,
+                                           int64_t n, bool vec, Pair (&items)[kItems]) {
+    thread_maps(g, cnt, c0, t0, n, vec, items);
     Pair agg = identity_pair();
 #pragma unroll
     for (int k = kItems - 1; k >= 0; --k) agg = compose(items[k], agg);
@@ -373,24 +439,17 @@ __global__ __launch_bounds__(kThreads) void k_gae_chunks(meshy_gae_args g, Works
     __shared__ Pair s_wave[kThreads / kWave];
     const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
     const int64_t t0 = c0 + static_cast<int64_t>(threadIdx.x) * kItems;
-    const ChunkDocs cd = chunk_docs(g, c0, n);
     Pair items[kItems];
-    const Pair mine = load_items(g, ws.cnt, t0, n, vec, cd, items);
-    Pair total;
-    (void)block_suffix_exclusive(mine, s_wave, total);
-    if (threadIdx.x == 0) ws.chunk[blockIdx.x] = total;
-}
-
-// Composition of the 64 lanes' maps in lane order (lane 0 leftmost), in a
-// fixed tree; the result is in lane 0.
-__device__ __forceinline__ Pair wave_fold(Pair x) {
-    const int lane = threadIdx.x % kWave;
-#pragma unroll
-    for (int off = 1; off < kWave; off <<= 1) {
-        const Pair other = shfl_down_pair(x, off);
-        if (lane + off < kWave) x = compose(x, other);
+    const Pair mine = load_items(g, ws.cnt, c0, t0, n, vec, items);
+    // The chunk's map: each wave's fold, then the waves in order.
+    const Pair wf = wave_fold(mine);
+    if (threadIdx.x % kWave == 0) s_wave[threadIdx.x / kWave] = wf;
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        Pair total = identity_pair();
+        for (int w = kThreads / kWave - 1; w >= 0; --w) total = compose(s_wave[w], total);
+        ws.chunk[blockIdx.x] = total;
     }
-    return x;
 }
 
 __device__ __forceinline__ void write_lambda(const meshy_gae_args& g, const float* cnt, int64_t first, int64_t step) {
@@ -441,9 +500,8 @@ __global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Worksp
     const int64_t k1 = grp + 1 + lane;
     const Pair rj = ws.chunk[min(j, nc - 1)];
     const Pair ak = ws.group[min(k1, ng - 1)];
-    const ChunkDocs cd = chunk_docs(g, c * kChunk, n);
     Pair items[kItems];
-    const Pair mine = load_items(g, ws.cnt, t0, n, vec, cd, items);
+    const Pair mine = load_items(g, ws.cnt, c * kChunk, t0, n, vec, items);
     if (threadIdx.x < kWave) {
         const Pair right = wave_fold((j > c && j < g1) ? rj : identity_pair());
         Pair after = wave_fold(k1 < ng ? ak : identity_pair());
