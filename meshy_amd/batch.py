@@ -504,10 +504,11 @@ class _PackViews:
             at = rest.pop(0) if at is not None else None
         else:
             sdi = di
-        f.update(input_ids=ii, labels=lb, positions=ps, mask=mk, doc_ids=sdi, rollout_logprobs=rl,
-                 advantage_tokens=at if self.broadcast_only else None)
+        made = dict(input_ids=ii, labels=lb, positions=ps, mask=mk, doc_ids=sdi, rollout_logprobs=rl,
+                    advantage_tokens=at if self.broadcast_only else None)
         if self.per_token_adv:
-            f["advantages"] = at
+            made["advantages"] = at
+        _keep_set_fields(f, made)
         if sdi is di:  # not replaced by a context-parallel shard
             d0 = self.doc_start[k]
             mb.__dict__["_meshy_seg_src"] = ((id(di), di._version, di.data_ptr(), self.nd[k]), self.seg, d0 + 2 * k,
@@ -519,16 +520,16 @@ class _PackViews:
             n = self.doc_start[-1]
             self._doc = [torch.split(t[:n], self.nd) for t in self.docs]
         adv, lengths, pos_w = (c[mb._k] for c in self._doc)
+        made = {"lengths": lengths, "positive_lm_weights": pos_w}
         if not self.per_token_adv:
-            f["advantages"] = adv
-        f["lengths"] = lengths
-        f["positive_lm_weights"] = pos_w
+            made["advantages"] = adv
+        _keep_set_fields(f, made)
 
     def attention(self, mb: "PackedBatch", f: dict) -> None:
         """cu_seqlens (n_docs + 1 slots, + 1 with a padding document) and the
         longest document of micro mb._k, as make_varlen_metadata builds them."""
         if not self.packed:
-            f["attention_masks"] = None
+            f.setdefault("attention_masks", None)
             return
         if self._cu is None:
             sizes, pads = [], []
@@ -542,7 +543,15 @@ class _PackViews:
         k = mb._k
         m, pad, cu = self.micros[k], pads[k], cus[k]
         max_len = max(max(m.doc_lens, default=0), pad if pad > 0 else 0)
-        f["attention_masks"] = VarlenMetadata(cu_seq_q=cu, cu_seq_k=cu, max_q=int(max_len), max_k=int(max_len))
+        f.setdefault("attention_masks",
+                     VarlenMetadata(cu_seq_q=cu, cu_seq_k=cu, max_q=int(max_len), max_k=int(max_len)))
+
+
+def _keep_set_fields(f: dict, made: dict) -> None:
+    """Adds the made views to a batch's attributes, keeping any field the
+    caller set before its first read."""
+    for k, v in made.items():
+        f.setdefault(k, v)
 
 
 class _Lazy:

@@ -385,6 +385,38 @@ def test_zero_variance_groups_match_oracle(dev):
 
 # ------------------------------------------------------------ pack_step (256 GRPO samples)
 
+def test_packed_batch_is_a_batch(dev):
+    """The pack's batches are Batch objects whose fields are views made on
+    first read: asdict and replace see the same tensors, a field set before
+    its first read stays as set, and micros of one launch read independently."""
+    import dataclasses
+
+    from meshy_amd import workloads
+    from meshy_amd.batch import Batch
+    from meshy_amd.pipeline import RaggedSamples, pack_step
+    from meshy_amd.plan import PlannerConfig
+
+    batch, rewards, group_offsets = workloads.grpo_256_samples(0)
+    ragged = RaggedSamples.from_arrays(batch.tokens, batch.mask, batch.logprobs, batch.offsets, rewards,
+                                       group_offsets)
+    cfg = PlannerConfig(layout="packed", mini_batch_size=256, seq_len=8192, align=2048, max_tokens_per_micro=8192)
+    res = pack_step(ragged, cfg, dev)
+    a, b = res.batches[0], res.batches[1]
+    assert isinstance(a, Batch)
+    d = dataclasses.asdict(b)
+    assert set(d) == {f.name for f in dataclasses.fields(Batch)}
+    assert torch.equal(d["input_ids"], b.input_ids) and torch.equal(d["doc_ids"], b.doc_ids)  # asdict copies
+    r = dataclasses.replace(b, n_docs=b.n_docs)
+    assert r.labels.data_ptr() == b.labels.data_ptr() and r.n_docs == b.n_docs
+    c = res.batches[2]  # no field of micro 2 read yet
+    c.mask = torch.ones(1, 5, device=dev)
+    assert c.input_ids.shape[1] == c.labels.shape[1] != 5  # reads the rest of the group
+    assert c.mask.shape == (1, 5)  # the field set before the first read stays as set
+    c.advantages = torch.zeros(3, device=dev)
+    assert c.lengths.numel() == c.n_docs and c.advantages.numel() == 3
+    assert a.input_ids.shape == (1, a.labels.shape[1])
+
+
 def test_pack_step_256_samples_matches_oracle(dev):
     """Plan + one H2D + GRPO + pack: micro map, cu_seqlens, positions bit-exact;
     advantages (per document and broadcast per token) within 1e-5."""
