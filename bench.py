@@ -46,12 +46,31 @@ def _sync():
     torch.cuda.synchronize()
 
 
-def _gpu_ms(fn, steps: int, warmup: int) -> float:
+# Host-bound calls (the drop-in wrappers, the pack, the autograd engine) run
+# 2-3x slower for the first few hundred calls of a fresh process, until the
+# host's clocks and caches settle: such legs keep warming for WARM_S seconds
+# before the clock starts.  The headline leg does exactly its W warm-up steps.
+WARM_S = 0.3
+
+
+def _warm(fn, warmup: int, warm_s: float, before=None, gpu: bool = False) -> None:
+    """At least `warmup` calls, and more until `warm_s` seconds have passed."""
+    t_end = time.perf_counter() + warm_s
+    i = 0
+    while i < warmup or time.perf_counter() < t_end:
+        if before is not None:
+            before()
+        fn()
+        if gpu:
+            _sync()
+        i += 1
+
+
+def _gpu_ms(fn, steps: int, warmup: int, warm_s: float = WARM_S) -> float:
     """Average ms per call of `fn` (HIP events on the current stream)."""
     import torch
 
-    for _ in range(warmup):
-        fn()
+    _warm(fn, warmup, warm_s)
     _sync()
     start = torch.cuda.Event(enable_timing=True)
     stop = torch.cuda.Event(enable_timing=True)
@@ -63,11 +82,12 @@ def _gpu_ms(fn, steps: int, warmup: int) -> float:
     return start.elapsed_time(stop) / steps
 
 
-def _wall_ms(fn, runs: int, warmup: int = 1, gpu: bool = True, before=None) -> float:
+def _wall_ms(fn, runs: int, warmup: int = 1, gpu: bool = True, before=None, warm_s: float = WARM_S) -> float:
     """Median wall ms of `fn` (synchronized when `gpu`); `before` runs untimed
     ahead of each call (e.g. releasing the previous call's result)."""
+    _warm(fn, warmup, warm_s, before=before, gpu=gpu)
     times = []
-    for i in range(warmup + runs):
+    for _ in range(runs):
         if before is not None:
             before()
         if gpu:
@@ -76,8 +96,7 @@ def _wall_ms(fn, runs: int, warmup: int = 1, gpu: bool = True, before=None) -> f
         fn()
         if gpu:
             _sync()
-        if i >= warmup:
-            times.append((time.perf_counter() - t0) * 1e3)
+        times.append((time.perf_counter() - t0) * 1e3)
     return statistics.median(times)
 
 
@@ -123,7 +142,7 @@ def bench_logprob(steps, warmup):
     def step():
         out["r"] = logprob.logprobs_and_entropy(logits, labels, with_entropy=True)
 
-    ms = _gpu_ms(step, steps, warmup)
+    ms = _gpu_ms(step, steps, warmup, warm_s=0.0)  # exactly W untimed warm-up steps
     lp, ent = out["r"]
     assert torch.isfinite(lp).all() and torch.isfinite(ent).all()
     nbytes = T_TOK * VOCAB * 2 + T_TOK * 8 + T_TOK * 8
@@ -145,7 +164,7 @@ def bench_read_ceiling(logits, steps, warmup):
         _lib.check(lib.meshy_stream_read(logits.data_ptr(), rows, row_bytes, out.data_ptr(),
                                          _lib.stream_of(logits.device)), "meshy_stream_read")
 
-    ms = _gpu_ms(step, steps, warmup)
+    ms = _gpu_ms(step, steps, warmup, warm_s=0.0)  # measured like the headline leg
     return rows * row_bytes / (ms * 1e-3) / 1e9
 
 
