@@ -72,6 +72,13 @@ def _call(name, *args):
     ("meshy_group_gauges", (FAKE, FAKE, FAKE, -3, 0.5, FAKE, FAKE, 4096, None), EINVAL, "bad size"),
     ("meshy_group_gauges", (FAKE, None, FAKE, 3, 0.5, FAKE, FAKE, 4096, None), ENULL, "NULL"),
     ("meshy_group_gauges", (FAKE, FAKE, FAKE, 300, 0.5, FAKE, FAKE, 8, None), ESPACE, "workspace"),
+    # out, rows, cols, row_stride, seed, scale, stream
+    ("meshy_synth_bf16", (FAKE, 4, 8, 7, 1, 2.0, None), EINVAL, "bad shape"),
+    ("meshy_synth_bf16", (FAKE, 4, 8, 8, 1, -1.0, None), EINVAL, "bad scale"),
+    ("meshy_synth_bf16", (None, 4, 8, 8, 1, 2.0, None), ENULL, "NULL"),
+    # out, row_ids, n_rows, cols, seed, scale (host)
+    ("meshy_synth_bf16_rows_host", (FAKE, None, 2, 8, 1, 2.0), ENULL, "NULL"),
+    ("meshy_synth_bf16_rows_host", (FAKE, FAKE, -2, 8, 1, 2.0), EINVAL, "bad shape"),
     # raw_rewards, n_rewards, group_offsets, n_groups, tolerance, flags, stream
     ("meshy_zero_variance_groups", (FAKE, 8, FAKE, -1, 1e-8, FAKE, None), EINVAL, "negative"),
     ("meshy_zero_variance_groups", (None, 8, FAKE, 2, 1e-8, FAKE, None), ENULL, "NULL"),
