@@ -20,7 +20,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .hostio import gather_into
+from .hostio import gather_heads_into, gather_into
 from .plan import Layout, MicroPlan
 
 #: Per-token advantage column (batch.py:81): already on the next-token grid,
@@ -143,15 +143,6 @@ def _scalars(samples: Sequence[Any], idxs: Sequence[int], key: str, default: flo
     return np.array([_scalar_of(v, default) for v in vals], np.float64)
 
 
-def _n(x) -> int:
-    return int(x.shape[0]) if isinstance(x, torch.Tensor) else len(x)
-
-
-def _head(x, L: int):
-    """The first L entries of a per-token column (the column itself when it has L)."""
-    return x if _n(x) == L else x[:L]
-
-
 @dataclass
 class PackJob:
     """Device-resident inputs of one pack launch (see ``stage_micro_batches``)."""
@@ -228,13 +219,14 @@ def stage_micro_batches(
     for idx, L in zip(used, need_len):
         s = samples[idx]
         tk = s["tokens"]
-        if _n(tk) < L:
-            raise ValueError(f"sample {idx} has {_n(tk)} tokens, micro wants {L}")
+        n_tk = tk.shape[0] if isinstance(tk, torch.Tensor) else len(tk)
+        if n_tk < L:
+            raise ValueError(f"sample {idx} has {n_tk} tokens, micro wants {L}")
         tok64 = tok64 and isinstance(tk, torch.Tensor) and tk.dtype == torch.int64
-        tok_parts.append(_head(tk, L))
-        mask_parts.append(_head(s["mask_assistant"], L))
+        tok_parts.append(tk)
+        mask_parts.append(s["mask_assistant"])
         if need_rollout_lp:
-            lp_parts.append(_head(s["logprobs"], L))
+            lp_parts.append(s["logprobs"])
     per_token_adv = any(ADVANTAGE_TOKENS in samples[m.sample_idx[0]] for m in micros if m.sample_idx)
     s_off = np.zeros(n_s + 1, np.int64)
     np.cumsum(need_len, out=s_off[1:])
@@ -297,13 +289,14 @@ def stage_micro_batches(
     host = stage.get(lay.size)
     if n_s:
         srcs = [samples[i] for i in used]
-        gather_into(tok_parts, lay.view(host, "tokens"))
-        gather_into(mask_parts, lay.view(host, "mask"))
+        # the first need_len[i] positions of each sample's columns
+        gather_heads_into(tok_parts, need_len, lay.view(host, "tokens"))
+        gather_heads_into(mask_parts, need_len, lay.view(host, "mask"))
         if need_rollout_lp:
-            gather_into(lp_parts, lay.view(host, "logprobs"))
+            gather_heads_into(lp_parts, need_len, lay.view(host, "logprobs"))
         if teacher_k:
-            gather_into([_head(s[TEACHER_FIELDS[0]], L) for s, L in zip(srcs, need_len)], lay.view(host, "teacher_ids"))
-            gather_into([_head(s[TEACHER_FIELDS[1]], L) for s, L in zip(srcs, need_len)], lay.view(host, "teacher_lps"))
+            gather_heads_into([s[TEACHER_FIELDS[0]] for s in srcs], need_len, lay.view(host, "teacher_ids"), teacher_k)
+            gather_heads_into([s[TEACHER_FIELDS[1]] for s in srcs], need_len, lay.view(host, "teacher_lps"), teacher_k)
         if per_token_adv and adv_dev is None:
             parts = []
             for s, L in zip(srcs, need_len):
