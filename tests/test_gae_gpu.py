@@ -272,6 +272,23 @@ def test_scan_from_offsets_equals_scan_from_ids(dev, docs_per_row, rows, S):
     assert (a.cpu() - ref_adv).abs().max().item() <= TOL
 
 
+def test_scan_from_offsets_with_ids_outside_the_slots(dev):
+    """Sorted ids that start below 0 and end past the padding slot: chunks whose
+    end ids leave [0, n_docs] read every id, so both scans still agree bit for
+    bit (ids outside the slots get lambda 0, as in the per-token scan)."""
+    from meshy_amd import gae
+
+    rewards, values, mask, doc_ids, n_docs = _random_grid(1, 20000, 12, seed=77)
+    doc_ids[0, :3000] = -1
+    doc_ids[0, -2500:] = n_docs + 3
+    d = [t.to(dev) for t in (rewards, values, mask, doc_ids)]
+    for lens in (None, torch.full((n_docs,), 20.0, device=dev)):
+        kw = dict(lengths=lens, gamma=0.99, alpha=1.5, epsilon=1e-6, want_adv=True, want_returns=True, want_lam=True)
+        a0, r0, l0 = gae._run(*d, n_docs, offsets=True, **kw)
+        a1, r1, l1 = gae._run(*d, n_docs, offsets=False, **kw)
+        assert torch.equal(a0, a1) and torch.equal(r0, r1) and torch.equal(l0, l1)
+
+
 def _critic_samples(n, seed, max_len=700, bf16=False):
     g = torch.Generator().manual_seed(seed)
     out = []
