@@ -289,6 +289,43 @@ def test_scan_from_offsets_with_ids_outside_the_slots(dev):
         assert torch.equal(a0, a1) and torch.equal(r0, r1) and torch.equal(l0, l1)
 
 
+def test_scan_from_offsets_random_grids(dev):
+    """40 seeded grids of random shape (1-4 rows of 1-9000 positions), document
+    sizes from 1 token to whole rows, empty document slots, mask holes and a
+    trailing padding slot: the offsets scan equals the per-token-id scan bit for
+    bit, and the sequential oracle within 1e-3 on the smaller ones."""
+    from meshy_amd import gae
+
+    rng = np.random.default_rng(2024)
+    for trial in range(40):
+        rows = int(rng.integers(1, 5))
+        S = int(rng.integers(1, 9001))
+        n = rows * S
+        # non-decreasing ids over the flattened grid with random run lengths
+        runs = []
+        while sum(runs) < n:
+            runs.append(int(rng.choice([1, 2, 7, 50, 700, 3000, 20000])))
+        ids = np.repeat(np.arange(len(runs)), runs)[:n]
+        ids = ids * int(rng.choice([1, 2]))  # every other slot empty
+        n_docs = int(ids.max()) + 1
+        if rng.random() < 0.5:
+            ids[-int(rng.integers(1, max(2, n // 10))):] = n_docs  # padding slot
+        mask = (rng.random(n) > float(rng.choice([0.0, 0.05, 0.3]))).astype(np.float32)
+        t = [torch.from_numpy(x.reshape(rows, S)) for x in
+             (rng.standard_normal(n).astype(np.float32) * (rng.random(n) < 0.05),
+              rng.standard_normal(n).astype(np.float32), mask, ids.astype(np.int64))]
+        lengths = None if rng.random() < 0.5 else torch.from_numpy(rng.random(n_docs).astype(np.float32) * 50 + 1)
+        d = [x.to(dev) for x in t]
+        kw = dict(lengths=None if lengths is None else lengths.to(dev), gamma=float(rng.choice([1.0, 0.97])),
+                  alpha=1.5, epsilon=1e-6, want_adv=True, want_returns=True, want_lam=True)
+        a0, r0, l0 = gae._run(*d, n_docs, offsets=True, **kw)
+        a1, r1, l1 = gae._run(*d, n_docs, offsets=False, **kw)
+        assert torch.equal(a0, a1) and torch.equal(r0, r1) and torch.equal(l0, l1), trial
+        if n <= 4000:
+            ref_adv, _ = ogae.compute_vapo_gae(*t, n_docs, lengths=lengths, gamma=kw["gamma"], alpha=1.5)
+            assert (a0.cpu() - ref_adv).abs().max().item() <= TOL, trial
+
+
 def _critic_samples(n, seed, max_len=700, bf16=False):
     g = torch.Generator().manual_seed(seed)
     out = []
