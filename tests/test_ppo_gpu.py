@@ -210,6 +210,37 @@ def test_matches_oracle_packed(dev, variant):
     _compare(dev, new, old, mask, doc_ids, adv, 37, rollout=roll, entropy=ent, pos_w=posw, **variant)
 
 
+def test_random_document_layouts(dev):
+    """30 seeded batches whose document sizes run from 1 token to several
+    2048-token tiles (tiles with one to many documents, both tile paths),
+    empty document slots, padded rows or a packed row, a padding slot, and every
+    variant of reduction, TIS, IcePop and positive-LM loss, against the oracle."""
+    rng = np.random.default_rng(31)
+    variants = [dict(), dict(per_token_loss=False), dict(use_tis=True), dict(use_icepop=True),
+                dict(positive_lm_coef=0.2, per_token_loss=False)]
+    for trial in range(30):
+        sizes = rng.choice([1, 2, 5, 60, 700, 2047, 2049, 5000], size=int(rng.integers(1, 40)))
+        ids = np.repeat(np.arange(len(sizes)), sizes) * int(rng.choice([1, 3]))
+        n_docs = int(ids.max()) + 1
+        pad = int(rng.integers(0, 50))
+        ids = np.concatenate([ids, np.full(pad, n_docs)])
+        n = len(ids)
+        rows = 1
+        for r in (2, 3, 4):
+            if n % r == 0 and rng.random() < 0.3:
+                rows = r
+        t = lambda x: torch.from_numpy(x).reshape(rows, -1)  # noqa: E731
+        old = -rng.random(n).astype(np.float32) * 8
+        new = (old + rng.standard_normal(n).astype(np.float32) * 0.3).astype(np.float32)
+        mask = (rng.random(n) > 0.2).astype(np.float32)
+        mask[ids == n_docs] = 0
+        roll = (old + rng.standard_normal(n).astype(np.float32) * 0.2).astype(np.float32)
+        adv = torch.from_numpy(rng.standard_normal(n_docs).astype(np.float32))
+        posw = torch.from_numpy(rng.random(n_docs).astype(np.float32))
+        _compare(dev, t(new), t(old), t(mask), t(ids.astype(np.int64)), adv, n_docs, rollout=t(roll), pos_w=posw,
+                 **variants[trial % len(variants)])
+
+
 @pytest.mark.parametrize("case", ["nan_new_masked", "inf_ratio_pos_adv", "inf_ratio_neg_adv", "neg_inf_new_masked"])
 @pytest.mark.parametrize("per_token_loss", [True, False])
 def test_non_finite_inputs_propagate_like_torch(dev, case, per_token_loss):
