@@ -356,6 +356,21 @@ def load() -> ctypes.CDLL:
     return lib
 
 
+_PYIO = None
+
+
+def pyio():
+    """The CPython helper module meshy_amd._pyio (built beside the library)."""
+    global _PYIO
+    if _PYIO is None:
+        try:
+            from . import _pyio as mod
+        except ImportError as e:
+            raise ImportError("meshy_amd._pyio is not built; run __graft_entry__.build()") from e
+        _PYIO = mod
+    return _PYIO
+
+
 def check(rc: int, what: str) -> None:
     """Raise the Python error matching a C-ABI return code."""
     if rc == 0:

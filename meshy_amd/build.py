@@ -3,7 +3,9 @@
     python -m meshy_amd.build
 
 Each source compiles to its own object under meshy_amd/_build/ (in parallel),
-then one link produces meshy_amd/libmeshy_amd.so next to this file.
+then one link produces meshy_amd/libmeshy_amd.so next to this file.  The
+CPython extension meshy_amd._pyio (host code over Python objects, no device
+code) is built beside it with the host compiler.
 """
 
 from __future__ import annotations
@@ -13,6 +15,7 @@ import os
 import shutil
 import subprocess
 import sys
+import sysconfig
 
 HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
@@ -21,6 +24,9 @@ BUILD_DIR = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "libmeshy_amd.so")
 
 SOURCES = ("capi.cpp", "plan.cpp", "hostio.cpp", "logprob.hip", "topk.hip", "distill.hip", "pack.hip", "ppo.hip", "gae.hip", "critic.hip", "ragged.hip", "synth.hip")
+
+PYIO_SRC = "pyio.cpp"
+PYIO_OUT = os.path.join(HERE, "_pyio" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 
 ARCH = os.environ.get("MESHY_OFFLOAD_ARCH", "gfx950")
 
@@ -60,11 +66,31 @@ def _compile(src: str, verbose: bool) -> str:
     return obj
 
 
+def build_pyio(verbose: bool = False) -> str:
+    """Compile the CPython extension meshy_amd._pyio; returns its path."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler found for meshy_amd._pyio")
+    tmp = PYIO_OUT + ".tmp"
+    cmd = [cxx, "-O3", "-std=c++17", "-shared", "-fPIC", "-pthread", "-Wall", f"-I{sysconfig.get_paths()['include']}",
+           os.path.join(CSRC, PYIO_SRC), "-o", tmp]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"{cxx} failed on {PYIO_SRC}:\n{res.stderr}")
+    os.replace(tmp, PYIO_OUT)
+    return PYIO_OUT
+
+
 def build(verbose: bool = False) -> str:
-    """Compile every source and link libmeshy_amd.so; returns its path."""
+    """Compile every source and link libmeshy_amd.so (and build meshy_amd._pyio);
+    returns the library's path."""
     os.makedirs(BUILD_DIR, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES), os.cpu_count() or 1)) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES) + 1, os.cpu_count() or 1)) as ex:
+        pyio = ex.submit(build_pyio, verbose)
         objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
+        pyio.result()
     tmp = OUT + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", *objs, "-o", tmp]
     if verbose:

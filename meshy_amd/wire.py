@@ -20,6 +20,8 @@ from typing import Any, Iterable
 import numpy as np
 import torch
 
+from . import _lib
+
 # How each known column is materialised in a batch (adapter.py:39-71).
 FIELD_KINDS: dict[str, str] = {
     "tokens": "nested",
@@ -104,23 +106,28 @@ def samples_to_columns(samples: list[Any], fields: Iterable[str]) -> dict[str, A
     return out
 
 
+def _stamp_raw_reward(sample: Any, weight_version: int) -> float:
+    raw = getattr(sample, "raw_reward", None)
+    return float(sample.reward if raw is None else raw)
+
+
+# A rollout sample's scalar columns (rollout.py:127-152): a missing advantage is
+# 0, a missing raw reward is the reward, the quality stamps are 0/1.
+_STAMPS: dict[str, Any] = {
+    "advantage": lambda s, v: 0.0 if s.advantage is None else float(s.advantage),
+    "weight_version": lambda s, v: int(v),
+    "reward": lambda s, v: float(s.reward),
+    "positive_lm_weight": lambda s, v: float(getattr(s, "positive_lm_weight", 0.0)),
+    RAW_REWARD_FIELD: _stamp_raw_reward,
+    "truncated": lambda s, v: int(bool(getattr(s, "truncated", False))),
+    "repetition": lambda s, v: int(bool(getattr(s, "repetition", False))),
+    "mixed_version": lambda s, v: int(bool(getattr(s, "mixed_version", False))),
+}
+
+
 def _stamp(sample: Any, f: str, weight_version: int) -> float | int:
-    """A rollout sample's scalar column (rollout.py:127-152): a missing advantage
-    is 0, a missing raw reward is the reward, the quality stamps are 0/1."""
-    if f == "advantage":
-        return 0.0 if sample.advantage is None else float(sample.advantage)
-    if f == "weight_version":
-        return int(weight_version)
-    if f == "reward":
-        return float(sample.reward)
-    if f == "positive_lm_weight":
-        return float(getattr(sample, "positive_lm_weight", 0.0))
-    if f == RAW_REWARD_FIELD:
-        raw = getattr(sample, "raw_reward", None)
-        return float(sample.reward if raw is None else raw)
-    if f in ("truncated", "repetition", "mixed_version"):
-        return int(bool(getattr(sample, f, False)))
-    raise KeyError(f)
+    """One scalar column's value for one rollout sample."""
+    return _STAMPS[f](sample, weight_version)
 
 
 _ROLLOUT_SCALARS = ("advantage", "weight_version", "reward", "positive_lm_weight", RAW_REWARD_FIELD, "truncated",
@@ -154,18 +161,37 @@ def rollout_group_to_columns(group: list[Any], weight_version: int,
     for f in fields:
         if f in _SEQ_SOURCE:
             attr, dt = _SEQ_SOURCE[f]
-            seqs = [getattr(s, attr) for s in group]
-            off = np.zeros(batch + 1, np.int64)
-            np.cumsum(np.fromiter((len(x) for x in seqs), np.int64, batch), out=off[1:])
-            npdt = np.int64 if dt == torch.int64 else np.float32
-            flat = np.fromiter(itertools.chain.from_iterable(seqs), npdt, int(off[-1]))
+            flat, off = flatten_sequences([getattr(s, attr) for s in group], dt)
             out[f] = torch.nested.nested_tensor_from_jagged(torch.from_numpy(flat), torch.from_numpy(off))
         elif f in _ROLLOUT_SCALARS:
-            out[f] = torch.tensor([_stamp(s, f, weight_version) for s in group],
+            stamp = _STAMPS[f]
+            out[f] = torch.tensor([stamp(s, weight_version) for s in group],
                                   dtype=_SCALAR_DTYPE[f]).reshape(batch, 1)
         else:
             raise KeyError(f"a rollout sample has no column {f!r}")
     return out
+
+
+def flatten_sequences(seqs: list[Any], dtype: torch.dtype) -> tuple[np.ndarray, np.ndarray]:
+    """(flat values, int64 offsets [len(seqs) + 1]) of a list of number
+    sequences, as int64 (``torch.int64``) or float32 (any other dtype).
+
+    Lists and tuples of Python ints, floats and bools go through
+    ``meshy_amd._pyio`` in one native pass; anything else (numpy arrays,
+    tensors, numpy scalars, ints beyond int64) through ``np.fromiter``, whose
+    conversions the native pass reproduces bit for bit."""
+    npdt = np.int64 if dtype == torch.int64 else np.float32
+    pyio = _lib.pyio()
+    off = np.empty(len(seqs) + 1, np.int64)
+    total = pyio.seq_offsets(seqs, off)
+    if total is not None:
+        flat = np.empty(total, npdt)
+        if pyio.flatten_into(seqs, flat, "q" if npdt is np.int64 else "f"):
+            return flat, off
+    else:
+        off[0] = 0
+        np.cumsum(np.fromiter((len(x) for x in seqs), np.int64, len(seqs)), out=off[1:])
+    return np.fromiter(itertools.chain.from_iterable(seqs), npdt, int(off[-1])), off
 
 
 def _explode(value: Any, f: str, batch: int) -> list[Any]:
@@ -207,4 +233,4 @@ def jagged_parts(column: Any) -> tuple[torch.Tensor, torch.Tensor]:
 
 
 __all__ = ["FIELD_KINDS", "GRPO_TRAINER_FIELDS", "RAW_REWARD_FIELD", "columns_to_samples", "field_kind",
-           "jagged_parts", "rollout_group_to_columns", "sample_to_tensordict", "samples_to_columns"]
+           "flatten_sequences", "jagged_parts", "rollout_group_to_columns", "sample_to_tensordict", "samples_to_columns"]
