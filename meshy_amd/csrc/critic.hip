@@ -53,6 +53,29 @@ __device__ __forceinline__ T block_sum_to0(T v, T* scratch) {
     return r;
 }
 
+// N block sums at once: thread 0's v[k] receives the sum of v[k] over the
+// block, in the order block_sum_to0 takes (the waves' sums in wave order).
+template <int N>
+__device__ __forceinline__ void block_sums_to0(double (&v)[N], double (&scratch)[N][kWaves]) {
+    const int lane = threadIdx.x % kWave;
+    const int wid = threadIdx.x / kWave;
+#pragma unroll
+    for (int k = 0; k < N; ++k) {
+        const double w = wave_sum(v[k]);
+        if (lane == 0) scratch[k][wid] = w;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int k = 0; k < N; ++k) {
+            double r = 0;
+            for (int w = 0; w < kWaves; ++w) r += scratch[k][w];
+            v[k] = r;
+        }
+    }
+    __syncthreads();
+}
+
 // One workgroup per document.  Its tokens from the first multiple of 8 are
 // read 8 at a time (two 16-byte loads per stream, two groups of 8 per thread
 // in flight); the head before it and the tail after the last whole group of 8
@@ -210,12 +233,18 @@ __global__ __launch_bounds__(kThreads) void k_acc_rows(const void* __restrict__ 
 // One workgroup: the window sums over rows in row order.
 __global__ __launch_bounds__(kThreads) void k_acc_final(const double* __restrict__ part, int64_t rows,
                                                         double* __restrict__ sums) {
-    __shared__ double s_red[kWaves];
-    for (int k = 0; k < kAccSums; ++k) {
-        double v = 0.0;
-        for (int64_t r = threadIdx.x; r < rows; r += kThreads) v += part[r * kAccSums + k];
-        v = block_sum_to0(v, s_red);
-        if (threadIdx.x == 0) sums[k] = v;
+    __shared__ double s_red[kAccSums][kWaves];
+    double v[kAccSums];
+#pragma unroll
+    for (int k = 0; k < kAccSums; ++k) v[k] = 0.0;
+    for (int64_t r = threadIdx.x; r < rows; r += kThreads) {
+#pragma unroll
+        for (int k = 0; k < kAccSums; ++k) v[k] += part[r * kAccSums + k];
+    }
+    block_sums_to0(v, s_red);
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int k = 0; k < kAccSums; ++k) sums[k] = v[k];
     }
 }
 
@@ -301,43 +330,78 @@ __global__ __launch_bounds__(kThreads) void k_cve_bwd(const float* __restrict__ 
 // ---------------------------------------------------------- window gauges
 // critic_diagnostics' token-level sums (meshy/backend/titan/critic/metrics.py:
 // 189-217) with the float mask as given: one workgroup per row, each thread
-// accumulating its strided elements in fp64 (this runs once per window, not
-// per step), then a fixed-order workgroup sum; the window takes a second
-// one-workgroup pass over the rows.
+// accumulating its elements in fp64, then a fixed-order workgroup sum; the
+// window takes a second one-workgroup pass over the rows.
 constexpr int kCwSums = MESHY_CW_RMIN;  // the summed values; min and max follow
 
+struct CwAcc {
+    double a[kCwSums + 1];  // the sums, then sum v m of the row
+    float rmin, rmax;       // of r over the selected tokens
+};
+
+__device__ __forceinline__ void cw_one(float m, float v, float r, CwAcc& c) {
+    const float e = v - r;
+    const bool sel = m > 0.f;
+    // variance_reduction selects the masked tokens; the loss, the calibration
+    // gap and the row mean multiply by the mask.
+    c.a[MESHY_CW_SEL] += sel ? 1.0 : 0.0;
+    c.a[MESHY_CW_R] += sel ? static_cast<double>(r) : 0.0;
+    c.a[MESHY_CW_R2] += sel ? static_cast<double>(r) * r : 0.0;
+    c.a[MESHY_CW_D] += sel ? static_cast<double>(e) : 0.0;
+    c.a[MESHY_CW_D2] += sel ? static_cast<double>(e) * e : 0.0;
+    c.a[MESHY_CW_M] += m;
+    c.a[MESHY_CW_E2M] += static_cast<double>(e * e * m);
+    c.a[MESHY_CW_EM] += static_cast<double>(e * m);
+    c.a[kCwSums] += static_cast<double>(v * m);
+    c.rmin = (sel && r < c.rmin) ? r : c.rmin;
+    c.rmax = (sel && r > c.rmax) ? r : c.rmax;
+}
+
+__device__ __forceinline__ void cw8(const Elems8& e, CwAcc& c) {
+    cw_one(e.m0.x, e.v0.x, e.r0.x, c);
+    cw_one(e.m0.y, e.v0.y, e.r0.y, c);
+    cw_one(e.m0.z, e.v0.z, e.r0.z, c);
+    cw_one(e.m0.w, e.v0.w, e.r0.w, c);
+    cw_one(e.m1.x, e.v1.x, e.r1.x, c);
+    cw_one(e.m1.y, e.v1.y, e.r1.y, c);
+    cw_one(e.m1.z, e.v1.z, e.r1.z, c);
+    cw_one(e.m1.w, e.v1.w, e.r1.w, c);
+}
+
+// The row's elements from the first multiple of 8 are read 8 at a time with
+// 16-byte loads (two groups of 8 per thread in flight, as in k_acc_rows); the
+// head before it and the tail after the last whole group element by element.
 __global__ __launch_bounds__(kThreads) void k_cw_rows(const void* __restrict__ values, int values_bf16,
                                                       const float* __restrict__ returns,
-                                                      const float* __restrict__ mask, int64_t S,
+                                                      const float* __restrict__ mask, int64_t S, bool vec,
                                                       double* __restrict__ part, float* __restrict__ row_value) {
     __shared__ double s_red[kCwSums + 1][kWaves];
     __shared__ float s_min[kWaves], s_max[kWaves];
     const int64_t row = blockIdx.x;
     const int64_t base = row * S;
-    double a[kCwSums + 1];  // the sums, then sum v m of the row
+    const int64_t end = base + S;
+    const int64_t body0 = vec ? min((base + 7) / 8 * 8, end) : end;
+    const int64_t n8 = (end - body0) / 8;
+    const int64_t body1 = body0 + 8 * n8;
+    CwAcc c;
 #pragma unroll
-    for (int k = 0; k <= kCwSums; ++k) a[k] = 0.0;
-    float rmin = __builtin_inff(), rmax = -__builtin_inff();
-    for (int64_t j = base + threadIdx.x; j < base + S; j += kThreads) {
-        const float m = mask[j];
-        const float v = load_value(values, values_bf16, j);
-        const float r = returns[j];
-        const float e = v - r;
-        const bool sel = m > 0.f;
-        // variance_reduction selects the masked tokens; the loss, the
-        // calibration gap and the row mean multiply by the mask.
-        a[MESHY_CW_SEL] += sel ? 1.0 : 0.0;
-        a[MESHY_CW_R] += sel ? static_cast<double>(r) : 0.0;
-        a[MESHY_CW_R2] += sel ? static_cast<double>(r) * r : 0.0;
-        a[MESHY_CW_D] += sel ? static_cast<double>(e) : 0.0;
-        a[MESHY_CW_D2] += sel ? static_cast<double>(e) * e : 0.0;
-        a[MESHY_CW_M] += m;
-        a[MESHY_CW_E2M] += static_cast<double>(e * e * m);
-        a[MESHY_CW_EM] += static_cast<double>(e * m);
-        a[kCwSums] += static_cast<double>(v * m);
-        rmin = (sel && r < rmin) ? r : rmin;
-        rmax = (sel && r > rmax) ? r : rmax;
+    for (int k = 0; k <= kCwSums; ++k) c.a[k] = 0.0;
+    c.rmin = __builtin_inff();
+    c.rmax = -__builtin_inff();
+    int64_t g = threadIdx.x;
+    for (; g + kThreads < n8; g += 2 * kThreads) {
+        const Elems8 e0 = load8(values, values_bf16, returns, mask, body0 + 8 * g);
+        const Elems8 e1 = load8(values, values_bf16, returns, mask, body0 + 8 * (g + kThreads));
+        cw8(e0, c);
+        cw8(e1, c);
     }
+    if (g < n8) cw8(load8(values, values_bf16, returns, mask, body0 + 8 * g), c);
+    for (int64_t j = base + threadIdx.x; j < body0; j += kThreads)
+        cw_one(mask[j], load_value(values, values_bf16, j), returns[j], c);
+    for (int64_t j = body1 + threadIdx.x; j < end; j += kThreads)
+        cw_one(mask[j], load_value(values, values_bf16, j), returns[j], c);
+    double (&a)[kCwSums + 1] = c.a;
+    float rmin = c.rmin, rmax = c.rmax;
     const int lane = threadIdx.x % kWave;
     const int wid = threadIdx.x / kWave;
 #pragma unroll
@@ -380,12 +444,18 @@ __global__ __launch_bounds__(kThreads) void k_cw_rows(const void* __restrict__ v
 
 __global__ __launch_bounds__(kThreads) void k_cw_final(const double* __restrict__ part, int64_t rows,
                                                        double* __restrict__ sums) {
-    __shared__ double s_red[kWaves];
-    for (int k = 0; k < kCwSums; ++k) {
-        double v = 0.0;
-        for (int64_t r = threadIdx.x; r < rows; r += kThreads) v += part[r * MESHY_CW_VALS + k];
-        v = block_sum_to0(v, s_red);
-        if (threadIdx.x == 0) sums[k] = v;
+    __shared__ double s_red[kCwSums][kWaves];
+    double v[kCwSums];
+#pragma unroll
+    for (int k = 0; k < kCwSums; ++k) v[k] = 0.0;
+    for (int64_t r = threadIdx.x; r < rows; r += kThreads) {
+#pragma unroll
+        for (int k = 0; k < kCwSums; ++k) v[k] += part[r * MESHY_CW_VALS + k];
+    }
+    block_sums_to0(v, s_red);
+    if (threadIdx.x == 0) {
+#pragma unroll
+        for (int k = 0; k < kCwSums; ++k) sums[k] = v[k];
     }
     // min and max of r over the selected tokens (+inf / -inf when none)
     double lo = __builtin_inf(), hi = -__builtin_inf();
@@ -615,8 +685,9 @@ extern "C" int meshy_critic_window_sums(const void* values, int32_t values_bf16,
         return set_error(MESHY_ESPACE, "%s: workspace needs %zu bytes", who, meshy_critic_window_workspace_size(rows));
     double* part = static_cast<double*>(workspace);
     if (rows > 0) {
+        const bool vec = al16(values) && al16(returns) && al16(mask);
         hipLaunchKernelGGL(k_cw_rows, dim3(static_cast<unsigned>(rows)), dim3(kThreads), 0, stream, values,
-                           values_bf16, returns, mask, S, part, row_value);
+                           values_bf16, returns, mask, S, vec, part, row_value);
         int rc = check_launch(who);
         if (rc) return rc;
     }

@@ -127,7 +127,7 @@ def _odd_window(rows, S, seed, *, frac=False, bf16=False):
 
 
 @pytest.mark.parametrize("rows,S,frac,bf16", [(24, 40, False, False), (37, 300, True, False), (64, 1000, False, True),
-                                             (300, 129, True, True)])
+                                             (300, 129, True, True), (5, 5003, True, True), (3, 8200, False, False)])
 def test_critic_diagnostics_matches_oracle(dev, rows, S, frac, bf16):
     from meshy_amd import critic
 
@@ -137,6 +137,31 @@ def test_critic_diagnostics_matches_oracle(dev, rows, S, frac, bf16):
     assert ocritic.same_gauges(got, want, rel=1e-4, abs_=1e-5), (got, want)
     assert got["n_rows"] == want["n_rows"] and got["n_prompts"] == want["n_prompts"]
     assert got["n_tokens"] == want["n_tokens"] or frac  # int() of a fractional sum may round apart
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_critic_window_sums_unaligned_storage(dev, bf16):
+    """Arrays one element off a 16-byte boundary take the element-by-element
+    path of the row pass: the same gauges as the aligned copies, and the
+    oracle's.  S = 5003 runs the aligned copies through the head, the loop of
+    two groups of 8 per thread in flight, the last single group and the tail."""
+    from meshy_amd import critic
+
+    rows, S = 4, 5003
+    v, r, m, rew, grp = _odd_window(rows, S, seed=77, frac=True, bf16=bf16)
+
+    def shifted(x):
+        buf = torch.empty(x.numel() + 1, dtype=x.dtype, device=dev)
+        buf[1:] = x.reshape(-1).to(dev)
+        out = buf[1:].view(rows, S)
+        assert out.data_ptr() % 16 != 0
+        return out
+
+    aligned = critic.critic_diagnostics(v.to(dev), r.to(dev), m.to(dev), rew.to(dev), grp.to(dev)).as_dict()
+    off = critic.critic_diagnostics(shifted(v), shifted(r), shifted(m), rew.to(dev), grp.to(dev)).as_dict()
+    want = ocritic.critic_diagnostics(v.float(), r, m, rew, grp)
+    assert ocritic.same_gauges(aligned, want, rel=1e-4, abs_=1e-5), (aligned, want)
+    assert ocritic.same_gauges(off, aligned, rel=1e-6, abs_=1e-9), (off, aligned)
 
 
 def test_critic_diagnostics_degenerate_windows(dev):
