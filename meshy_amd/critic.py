@@ -23,6 +23,7 @@ from __future__ import annotations
 
 from dataclasses import asdict, dataclass, field
 
+import numpy as np
 import torch
 
 from . import _lib
@@ -100,8 +101,8 @@ class Accumulator:
         _lib.check(rc, "meshy_critic_accumulate")
         self._sums = sums if self._sums is None else self._sums + sums
         self._row_value.append(row_value)
-        self._row_reward.append(rewards.detach().float().reshape(-1))
-        self._row_group.append(group_ids.detach().reshape(-1))
+        self._row_reward.append(rewards.detach().reshape(-1).to(device=dev, dtype=torch.float32).contiguous())
+        self._row_group.append(group_ids.detach().reshape(-1).to(device=dev, dtype=torch.int64).contiguous())
         self._state = None
 
     @property
@@ -110,17 +111,21 @@ class Accumulator:
         if self._state is None:
             st = AccumulatorState()
             if self._sums is not None:
-                # One device-to-host copy: the fp64 sums, the per-row values and
-                # rewards as fp64, and the group ids bit-cast to fp64.
-                vals = torch.cat(self._row_value).to(torch.float64)
-                rews = torch.cat(self._row_reward).to(torch.float64)
-                grps = torch.cat(self._row_group).to(torch.int64).view(torch.float64)
-                host = torch.cat([self._sums, vals, rews, grps]).cpu()
-                n = vals.numel()
-                st.n_tokens, st.sum_r, st.sum_r2, st.sum_d, st.sum_d2 = host[:5].tolist()
-                st.row_value = host[5:5 + n].tolist()
-                st.row_reward = host[5 + n:5 + 2 * n].tolist()
-                st.row_group = host[5 + 2 * n:].view(torch.int64).tolist()
+                # One concatenation of the bytes and one device-to-host copy:
+                # the fp64 sums, the fp32 row values and rewards, the int64
+                # group ids, each read back on the host with its own type.
+                parts = [self._sums, *self._row_value, *self._row_reward, *self._row_group]
+                host = torch.cat([t.view(torch.uint8) for t in parts]).cpu().numpy()
+                nv = sum(t.numel() for t in self._row_value)
+                nr = sum(t.numel() for t in self._row_reward)
+                ng = sum(t.numel() for t in self._row_group)
+                o_v = 5 * 8
+                o_r = o_v + 4 * nv
+                o_g = o_r + 4 * nr
+                st.n_tokens, st.sum_r, st.sum_r2, st.sum_d, st.sum_d2 = np.frombuffer(host, np.float64, 5).tolist()
+                st.row_value = np.frombuffer(host, np.float32, nv, o_v).tolist()
+                st.row_reward = np.frombuffer(host, np.float32, nr, o_r).tolist()
+                st.row_group = np.frombuffer(host, np.int64, ng, o_g).tolist()
             self._state = st
         return self._state
 

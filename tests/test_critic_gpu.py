@@ -78,7 +78,12 @@ def test_accumulator_matches_oracle(dev, bf16):
         v = v.to(torch.bfloat16) if bf16 else v
         rewards = torch.rand(rows)
         groups = torch.arange(rows) // 2 + 100 * k
-        acc.update(v.to(dev), r.to(dev), m.to(dev), rewards.to(dev), groups.to(dev))
+        if k % 2:
+            # rewards as a strided device view, fp64; group ids as int32 on the host
+            rw = torch.stack([rewards.double(), -rewards.double()], 1).to(dev)[:, 0]
+            acc.update(v.to(dev), r.to(dev), m.to(dev), rw, groups.to(torch.int32))
+        else:
+            acc.update(v.to(dev), r.to(dev), m.to(dev), rewards.to(dev), groups.to(dev))
         ref.update(v, r, m, rewards, groups)
     st, rs = acc.state, ref.state
     for key in ("n_tokens", "sum_r", "sum_r2", "sum_d", "sum_d2"):
