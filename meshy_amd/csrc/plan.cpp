@@ -10,7 +10,12 @@
 //   4. pad every mini-batch index to the same micro count with fillers and
 //      attach the global loss denominators (plan.py:259-283).
 // The output is a set of flat CSR tables (see meshy_plan_out in meshy_amd.h).
+// The sort of step 2 is a stable radix sort by length (its input is in index
+// order, so ties stay in index order), and the first fit of step 3 a descent
+// of a max-tree over the open micros' free capacities: O(n log m) where the
+// reference's scan of every open micro is O(n m).
 #include <algorithm>
+#include <climits>
 #include <new>
 #include <vector>
 
@@ -34,10 +39,52 @@ std::vector<std::vector<int64_t>> snake(const std::vector<int64_t>& order, int64
     return bins;
 }
 
-// Indices 0..n-1 ordered by (-len[i], i).
-std::vector<int64_t> by_length_desc(const std::vector<int64_t>& len) {
-    std::vector<int64_t> order(len.size());
-    for (size_t i = 0; i < order.size(); ++i) order[i] = static_cast<int64_t>(i);
+// Positions ordered by (-len[p], p), the reference's sort key (plan.py:164, 240).
+bool in_length_order(const std::vector<int64_t>& order, const std::vector<int64_t>& len) {
+    for (size_t k = 1; k < order.size(); ++k) {
+        const int64_t a = order[k - 1], b = order[k];
+        if (len[a] < len[b] || (len[a] == len[b] && a > b)) return false;
+    }
+    return true;
+}
+
+// Stable LSD radix sort of `order` by decreasing length, 11 bits of the
+// length's distance below the maximum per pass: ties keep their input order.
+void radix_by_length_desc(std::vector<int64_t>& order, const std::vector<int64_t>& len, int64_t hi,
+                          uint64_t range) {
+    constexpr int kBits = 11;
+    constexpr uint64_t kMask = (uint64_t{1} << kBits) - 1;
+    std::vector<int64_t> tmp(order.size());
+    std::vector<uint32_t> cnt(size_t{1} << kBits);
+    for (int shift = 0; shift == 0 || (shift < 64 && (range >> shift) != 0); shift += kBits) {
+        std::fill(cnt.begin(), cnt.end(), 0u);
+        for (int64_t p : order) ++cnt[(static_cast<uint64_t>(hi - len[p]) >> shift) & kMask];
+        uint32_t run = 0;
+        for (uint32_t& c : cnt) {
+            const uint32_t v = c;
+            c = run;
+            run += v;
+        }
+        for (int64_t p : order) tmp[cnt[(static_cast<uint64_t>(hi - len[p]) >> shift) & kMask]++] = p;
+        order.swap(tmp);
+    }
+}
+
+std::vector<int64_t> by_length_desc(const std::vector<int64_t>& idx, const std::vector<int64_t>& len,
+                                    bool ascending_input) {
+    std::vector<int64_t> order(idx);
+    if (order.size() < 2 || in_length_order(order, len)) return order;
+    int64_t lo = len[order[0]], hi = lo;
+    for (int64_t p : order) {
+        lo = std::min(lo, len[p]);
+        hi = std::max(hi, len[p]);
+    }
+    // hi - lo overflows only for lengths of opposite signs beyond 2^62.
+    const bool small_range = lo >= -(int64_t{1} << 62) && hi <= (int64_t{1} << 62);
+    if (ascending_input && small_range && order.size() >= 256) {
+        radix_by_length_desc(order, len, hi, static_cast<uint64_t>(hi - lo));
+        return order;
+    }
     std::sort(order.begin(), order.end(), [&](int64_t a, int64_t b) {
         if (len[a] != len[b]) return len[a] > len[b];
         return a < b;
@@ -45,67 +92,136 @@ std::vector<int64_t> by_length_desc(const std::vector<int64_t>& len) {
     return order;
 }
 
-struct Micro {
-    std::vector<int64_t> pos;   // rank-local sample positions
-    std::vector<int64_t> lens;  // truncated lengths
-    int64_t seq_len;
+// Indices 0..n-1 ordered by (-len[i], i).
+std::vector<int64_t> by_length_desc(const std::vector<int64_t>& len) {
+    std::vector<int64_t> idx(len.size());
+    for (size_t i = 0; i < idx.size(); ++i) idx[i] = static_cast<int64_t>(i);
+    return by_length_desc(idx, len, true);
+}
+
+// The micros of one mini-batch as flat tables: micro j holds the samples
+// pos[start[j] .. start[j + 1]) (rank-local positions, truncated lengths in
+// lens) and pads to seq_len[j].
+struct Micros {
+    std::vector<int64_t> seq_len;
+    std::vector<int64_t> start;
+    std::vector<int64_t> pos;
+    std::vector<int64_t> lens;
+    size_t size() const { return seq_len.size(); }
+};
+
+// The leftmost of the open micros (creation order) whose free capacity is at
+// least `need`, through a max-tree over the capacities: first-fit in O(log m)
+// per sample instead of a scan of every open micro.
+class FirstFit {
+   public:
+    int64_t find(int64_t need) const {
+        if (count_ == 0 || tree_[1] < need) return -1;
+        size_t node = 1;
+        // Branch-free descent: left child when it holds a fit, else right.
+        while (node < leaves_) node = 2 * node + static_cast<size_t>(tree_[2 * node] < need);
+        return static_cast<int64_t>(node - leaves_);
+    }
+    // Stops climbing where a node's maximum is unchanged.
+    void set(int64_t i, int64_t cap) {
+        size_t node = leaves_ + static_cast<size_t>(i);
+        tree_[node] = cap;
+        for (node >>= 1; node > 0; node >>= 1) {
+            const int64_t m = std::max(tree_[2 * node], tree_[2 * node + 1]);
+            if (tree_[node] == m) break;
+            tree_[node] = m;
+        }
+    }
+    int64_t push(int64_t cap) {
+        if (count_ == leaves_) grow();
+        set(static_cast<int64_t>(count_), cap);
+        return static_cast<int64_t>(count_++);
+    }
+
+   private:
+    static constexpr int64_t kNone = INT64_MIN;  // an unused leaf: never fits
+    void grow() {
+        const size_t nl = leaves_ ? 2 * leaves_ : 16;
+        std::vector<int64_t> t(2 * nl, kNone);
+        for (size_t i = 0; i < count_; ++i) t[nl + i] = tree_[leaves_ + i];
+        for (size_t node = nl - 1; node > 0; --node) t[node] = std::max(t[2 * node], t[2 * node + 1]);
+        tree_.swap(t);
+        leaves_ = nl;
+    }
+    std::vector<int64_t> tree_;
+    size_t leaves_ = 0;
+    size_t count_ = 0;
 };
 
 // First-fit-decreasing of `members` (rank-local positions) into micros
-// (plan.py:158-203).
-std::vector<Micro> pack_micros(const std::vector<int64_t>& members,
+// (plan.py:158-203).  A micro's admission test is a capacity against a need:
+//   packed:  round_up(total + L, align) <= budget  <=>  total + L <= floor(budget / align) * align,
+//            capacity floor(budget / align) * align - total, need L;
+//   padded:  (rows + 1) * row_len <= budget  <=>  rows + 1 <= floor(budget / row_len),
+//            or rows < micro_batch_size without a budget: capacity in rows, need 1.
+// Both forms keep the reference's choice, the first open micro that passes.
+Micros pack_micros(const std::vector<int64_t>& members,
                                const std::vector<int64_t>& local_len,
                                const meshy_planner_cfg& cfg) {
-    std::vector<int64_t> order(members);
-    std::sort(order.begin(), order.end(), [&](int64_t a, int64_t b) {
-        if (local_len[a] != local_len[b]) return local_len[a] > local_len[b];
-        return a < b;
-    });
+    // The members arrive in this order from the deal; the check keeps the
+    // sort for any other caller.
+    const std::vector<int64_t> order = by_length_desc(members, local_len, false);
     const bool padded = cfg.layout == MESHY_LAYOUT_PADDED;
     const bool has_budget = cfg.max_tokens_per_micro > 0;
     const int64_t budget = cfg.max_tokens_per_micro;
     // The row cap applies only without a token budget (plan.py:166-168).
-    const bool has_row_cap = !has_budget && cfg.micro_batch_size > 0;
     const int64_t max_rows = cfg.micro_batch_size;
+    const int64_t packed_cap = has_budget ? budget / cfg.align * cfg.align : 0;
 
-    struct Open {
-        std::vector<int64_t> pos;
-        std::vector<int64_t> lens;
-        int64_t acc;  // padded: row length fixed by the first sample; packed: token total
-    };
-    std::vector<Open> open;
-    for (int64_t p : order) {
-        const int64_t L = local_len[p];
-        bool placed = false;
-        for (Open& m : open) {
-            const int64_t rows = static_cast<int64_t>(m.pos.size());
-            if (has_row_cap && rows >= max_rows) continue;
-            if (has_budget) {
-                const int64_t cost = padded ? (rows + 1) * m.acc : round_up(m.acc + L, cfg.align);
-                if (cost > budget) continue;
+    std::vector<int64_t> acc;   // padded: row length fixed by the first sample; packed: token total
+    std::vector<int64_t> rows;  // samples in the micro
+    std::vector<int64_t> max_rows_of;  // padded: rows the micro admits
+    std::vector<int64_t> micro_of(order.size());
+    FirstFit fit;
+    for (size_t k = 0; k < order.size(); ++k) {
+        const int64_t L = local_len[order[k]];
+        const int64_t j = fit.find(padded ? 1 : L);
+        if (j >= 0) {
+            micro_of[k] = j;
+            ++rows[j];
+            if (padded) {
+                fit.set(j, max_rows_of[j] - rows[j]);
+            } else {
+                acc[j] += L;
+                fit.set(j, packed_cap - acc[j]);
             }
-            m.pos.push_back(p);
-            m.lens.push_back(L);
-            if (!padded) m.acc += L;
-            placed = true;
-            break;
-        }
-        if (!placed) {
-            Open m;
-            m.pos.push_back(p);
-            m.lens.push_back(L);
-            m.acc = padded ? round_up(L, cfg.align) : L;
-            open.push_back(std::move(m));
+        } else {
+            const int64_t a = padded ? round_up(L, cfg.align) : L;
+            int64_t cap;
+            if (padded) {
+                const int64_t mr = has_budget ? (a > 0 ? budget / a : INT64_MAX) : max_rows;
+                max_rows_of.push_back(mr);
+                cap = mr - 1;
+            } else {
+                max_rows_of.push_back(0);
+                cap = packed_cap - a;
+            }
+            micro_of[k] = fit.push(cap);
+            acc.push_back(a);
+            rows.push_back(1);
         }
     }
-    std::vector<Micro> out;
-    out.reserve(open.size());
-    for (Open& m : open) {
-        Micro mp;
-        mp.seq_len = padded ? m.acc : round_up(m.acc, cfg.align);
-        mp.pos = std::move(m.pos);
-        mp.lens = std::move(m.lens);
-        out.push_back(std::move(mp));
+    // Bucket the samples by micro, in placement order within each.
+    const size_t m = acc.size();
+    Micros out;
+    out.seq_len.resize(m);
+    out.start.assign(m + 1, 0);
+    for (size_t j = 0; j < m; ++j) {
+        out.seq_len[j] = padded ? acc[j] : round_up(acc[j], cfg.align);
+        out.start[j + 1] = out.start[j] + rows[j];
+    }
+    out.pos.resize(order.size());
+    out.lens.resize(order.size());
+    std::vector<int64_t> fill(out.start.begin(), out.start.end() - 1);
+    for (size_t k = 0; k < order.size(); ++k) {
+        const int64_t at = fill[static_cast<size_t>(micro_of[k])]++;
+        out.pos[at] = order[k];
+        out.lens[at] = local_len[order[k]];
     }
     return out;
 }
@@ -140,7 +256,7 @@ int plan_impl(const int64_t* lengths, const int64_t* loss_tokens, int64_t n, int
 
     // 2. Per rank: minis by snake, micros by first-fit-decreasing (plan.py:247-257).
     std::vector<std::vector<std::vector<int64_t>>> members(static_cast<size_t>(dp));
-    std::vector<std::vector<std::vector<Micro>>> minis(static_cast<size_t>(dp));
+    std::vector<std::vector<Micros>> minis(static_cast<size_t>(dp));
     for (int64_t r = 0; r < dp; ++r) {
         const std::vector<int64_t>& local = rank_samples[r];
         std::vector<int64_t> local_len(local.size());
@@ -182,15 +298,15 @@ int plan_impl(const int64_t* lengths, const int64_t* loss_tokens, int64_t n, int
         int32_t* dsample = out->doc_sample + r * n_local;
         int64_t* dlen = out->doc_len + r * n_local;
         for (int64_t i = 0; i < n_mini; ++i) {
-            const std::vector<Micro>& ms = minis[r][i];
+            const Micros& ms = minis[r][i];
             const int64_t n_micro = out->mini_n_micro[i];
             for (int64_t j = 0; j < n_micro; ++j, ++k) {
                 start[k] = cursor;
                 if (j < static_cast<int64_t>(ms.size())) {
-                    seq[k] = ms[j].seq_len;
-                    for (size_t d = 0; d < ms[j].pos.size(); ++d, ++cursor) {
-                        dsample[cursor] = static_cast<int32_t>(ms[j].pos[d]);
-                        dlen[cursor] = ms[j].lens[d];
+                    seq[k] = ms.seq_len[j];
+                    for (int64_t d = ms.start[j]; d < ms.start[j + 1]; ++d, ++cursor) {
+                        dsample[cursor] = static_cast<int32_t>(ms.pos[d]);
+                        dlen[cursor] = ms.lens[d];
                     }
                 } else {
                     seq[k] = cfg.align;  // filler micro (plan.py:206-208)

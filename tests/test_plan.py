@@ -308,6 +308,25 @@ def test_native_equals_oracle_random(lengths, dp, layout, align, budget, mbs, mi
         _check_invariants(native, lengths, PlannerConfig(**kw), dp)
 
 
+@pytest.mark.parametrize("layout,budget,micro_bs", [("packed", 8192, None), ("padded", 16384, None),
+                                                     ("padded", None, 5), ("packed", 3000, None)])
+@pytest.mark.parametrize("dp", [1, 4])
+def test_native_equals_oracle_large_batches(layout, budget, micro_bs, dp):
+    """Batches of 1536 samples, where the native planner sorts by radix and
+    finds each first fit through its capacity tree: the same plan as the
+    oracle's sorts and linear scans.  Lengths repeat (ties broken by index),
+    include 0 and lengths over seq_len (truncated), and span 2^11 and more."""
+    rng = random.Random(f"{layout}-{budget}-{micro_bs}-{dp}")
+    n = 1536
+    lengths = [rng.choice([0, 1, 7, 2048, 8192, 9000]) if rng.random() < 0.1 else rng.randint(1, 6000)
+               for _ in range(n)]
+    loss = [max(0, L - rng.randint(1, 50)) for L in lengths]
+    kw = dict(layout=layout, mini_batch_size=rng.choice([96, 384, 1536 // dp]), seq_len=8192, align=64,
+              max_tokens_per_micro=budget, micro_batch_size=micro_bs)
+    native = build_plan(lengths, loss, dp, PlannerConfig(**kw))
+    assert _plan_as_json(native) == _oracle_as_json(oplan.build_plan(lengths, loss, dp, **kw))
+
+
 def test_dataclass_contract():
     m = MicroPlan((), 64, ())
     assert m.is_filler and m.n_tokens == 0 and m.n_rows == 1
