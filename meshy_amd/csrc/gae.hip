@@ -16,12 +16,12 @@
 //                atomics (exact for 0/1 masks);
 //   k_gae_chunks each workgroup folds a chunk of kChunk tokens into one map
 //                per scan (advantages and returns);
-//   k_gae_groups one wave per group of 64 chunks folds their maps into one,
-//                plus lambda per document (gae.py:70-74);
 //   k_gae_apply  each workgroup folds its carry-in from the maps of the chunks
-//                of its group to its right and of the groups to its right,
+//                to its right, up to the first one that cuts both scans (both
+//                slopes exactly 0: nothing past it reaches the chunk),
 //                re-folds its chunk, scans its threads from the right seeded
-//                with the carry, and writes A_t and G_t.
+//                with the carry, and writes A_t and G_t; it also writes lambda
+//                per document (gae.py:70-74).
 // With the segment offsets of non-decreasing ids, a chunk holding at most
 // kMaxStarts document starts reads the ids only at its two ends and takes the
 // starts from the offsets (8 bytes per token less in each pass); other chunks
@@ -42,7 +42,6 @@ constexpr int kThreads = 256;
 constexpr int kItems = 8;
 constexpr int64_t kChunk = static_cast<int64_t>(kThreads) * kItems;
 static_assert(kItems % 8 == 0 || kItems == 4, "bf16 values are loaded 8 (or 4) at a time");
-constexpr int64_t kGroup = kWave;  // chunks per group
 constexpr int64_t kXcds = 8;        // workgroups go round-robin over the XCDs
 constexpr int kCountThreads = 256;
 constexpr int kCountItems = 16;
@@ -67,27 +66,21 @@ __device__ __forceinline__ Pair identity_pair() { return Pair{Aff{1.f, 0.f}, Aff
 struct Workspace {
     float* cnt;     // [n_docs + 1]
     Pair* chunk;    // [n_chunks]
-    Pair* group;    // [n_groups]: fold of kGroup consecutive chunk maps
 };
 
 int64_t n_chunks_of(int64_t n) { return (n + kChunk - 1) / kChunk; }
-__host__ __device__ inline int64_t n_groups_of(int64_t nc) { return (nc + kGroup - 1) / kGroup; }
 
 size_t ws_bytes(int64_t n, int64_t n_docs) {
     const int64_t nc = n_chunks_of(n);
-    return align_up(sizeof(float) * (n_docs + 1), 256) + align_up(sizeof(Pair) * nc, 256) +
-           align_up(sizeof(Pair) * n_groups_of(nc), 256);
+    return align_up(sizeof(float) * (n_docs + 1), 256) + align_up(sizeof(Pair) * nc, 256);
 }
 
 Workspace ws_of(void* base, int64_t n, int64_t n_docs) {
-    const int64_t nc = n_chunks_of(n);
     char* p = static_cast<char*>(base);
     Workspace w;
     w.cnt = reinterpret_cast<float*>(p);
     p += align_up(sizeof(float) * (n_docs + 1), 256);
     w.chunk = reinterpret_cast<Pair*>(p);
-    p += align_up(sizeof(Pair) * nc, 256);
-    w.group = reinterpret_cast<Pair*>(p);
     return w;
 }
 
@@ -457,15 +450,6 @@ __device__ __forceinline__ void write_lambda(const meshy_gae_args& g, const floa
     for (int64_t d = first; d < g.n_docs; d += step) g.lam_doc[d] = lambda_of(doc_length(g, cnt, d), g.alpha, g.epsilon);
 }
 
-__global__ __launch_bounds__(kWave) void k_gae_groups(meshy_gae_args g, Workspace ws, int64_t nc) {
-    const int lane = threadIdx.x;
-    if (g.lam_doc) write_lambda(g, ws.cnt, static_cast<int64_t>(blockIdx.x) * kWave + lane,
-                                static_cast<int64_t>(gridDim.x) * kWave);
-    const int64_t j = static_cast<int64_t>(blockIdx.x) * kGroup + lane;
-    const Pair x = wave_fold(j < nc ? ws.chunk[j] : identity_pair());
-    if (lane == 0) ws.group[blockIdx.x] = x;
-}
-
 __global__ __launch_bounds__(kThreads) void k_gae_lambda(meshy_gae_args g, const float* cnt) {
     write_lambda(g, cnt, static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x,
                  static_cast<int64_t>(gridDim.x) * kThreads);
@@ -487,33 +471,31 @@ __global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Worksp
     const int64_t c = apply_chunk(blockIdx.x, nc);
     const int64_t t0 = c * kChunk + static_cast<int64_t>(threadIdx.x) * kItems;
     const int lane = threadIdx.x % kWave;
-    const int64_t ng = n_groups_of(nc);
-    const int64_t grp = c / kGroup;
-    const int64_t g0 = grp * kGroup;
-    const int64_t g1 = min(g0 + kGroup, nc);
-    // The maps of the carry-in load before the chunk's inputs: the chunks of this
-    // group to the right of c, and the first 64 groups to the right.  Every
-    // wave loads them (indices clamped into range) and wave 0 alone uses them:
-    // loads under a condition would compile to a branch that waits for them
-    // before the inputs are issued.
-    const int64_t j = g0 + lane;
-    const int64_t k1 = grp + 1 + lane;
-    const Pair rj = ws.chunk[min(j, nc - 1)];
-    const Pair ak = ws.group[min(k1, ng - 1)];
+    // The carry-in: the chunks to the right of c in order, up to and including
+    // the first whose map cuts both scans (both slopes exactly 0: a document
+    // end, a row end or a mask hole lies in it), past which nothing reaches c.
+    // Their maps come 64 at a time; the first 64 load before the chunk's
+    // inputs, in every wave (indices clamped into range), and wave 0 alone
+    // folds them: loads under a condition would compile to a branch that
+    // waits for them before the inputs are issued.  A further 64 load only
+    // when a document runs on past them (more than 128 k tokens).
+    Pair r = ws.chunk[min(c + 1 + lane, nc - 1)];
     Pair items[kItems];
     const Pair mine = load_items(g, ws.cnt, c * kChunk, t0, n, vec, items);
     if (threadIdx.x < kWave) {
-        const Pair right = wave_fold((j > c && j < g1) ? rj : identity_pair());
-        Pair after = wave_fold(k1 < ng ? ak : identity_pair());
-        for (int64_t w0 = grp + 1 + kWave; w0 < ng; w0 += kWave) {
-            const int64_t k = w0 + lane;
-            after = compose(after, wave_fold(k < ng ? ws.group[k] : identity_pair()));
+        Pair carry = identity_pair();
+        for (int64_t j0 = c + 1; j0 < nc; j0 += kWave) {
+            const bool in = j0 + lane < nc;
+            const uint64_t cuts = __ballot(in && r.adv.p == 0.f && r.ret.p == 0.f);
+            const int first = cuts ? __builtin_ctzll(cuts) : kWave;
+            carry = compose(carry, wave_fold((in && lane <= first) ? r : identity_pair()));
+            if (cuts) break;
+            r = ws.chunk[min(j0 + kWave + lane, nc - 1)];
         }
         if (lane == 0) {
             // The sequence ends with A = G = 0, so the carry is the map applied to 0.
-            const Pair m = compose(right, after);
-            s_carry[0] = m.adv.q;
-            s_carry[1] = m.ret.q;
+            s_carry[0] = carry.adv.q;
+            s_carry[1] = carry.ret.q;
         }
     }
     Pair total;
@@ -547,6 +529,8 @@ __global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Worksp
             }
         }
     }
+    if (g.lam_doc) write_lambda(g, ws.cnt, static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x,
+                                static_cast<int64_t>(gridDim.x) * kThreads);
 }
 
 // ---------------------------------------------------------------- whitening
@@ -743,9 +727,6 @@ int gae_launch(const meshy_gae_args& g, hipStream_t stream) {
     if (nc > 0 && (g.adv || g.returns)) {
         hipLaunchKernelGGL(k_gae_chunks, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, vec);
         if ((rc = check_launch("meshy_gae(chunks)"))) return rc;
-        hipLaunchKernelGGL(k_gae_groups, dim3(static_cast<unsigned>(n_groups_of(nc))), dim3(kWave), 0, stream, g, ws,
-                           nc);
-        if ((rc = check_launch("meshy_gae(groups)"))) return rc;
         hipLaunchKernelGGL(k_gae_apply, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, nc, vec);
         if ((rc = check_launch("meshy_gae(apply)"))) return rc;
     } else if (g.lam_doc && g.n_docs > 0) {
