@@ -81,7 +81,7 @@ std::vector<int64_t> by_length_desc(const std::vector<int64_t>& idx, const std::
     }
     // hi - lo overflows only for lengths of opposite signs beyond 2^62.
     const bool small_range = lo >= -(int64_t{1} << 62) && hi <= (int64_t{1} << 62);
-    if (ascending_input && small_range && order.size() >= 256) {
+    if (ascending_input && small_range && order.size() >= 256 && order.size() < UINT32_MAX) {
         radix_by_length_desc(order, len, hi, static_cast<uint64_t>(hi - lo));
         return order;
     }

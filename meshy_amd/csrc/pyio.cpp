@@ -162,9 +162,17 @@ bool fill(PyObject** outer, Py_ssize_t n, T* dst, Py_ssize_t cap) {
     std::vector<char> ok(static_cast<size_t>(want), 0);
     std::vector<std::thread> pool;
     pool.reserve(static_cast<size_t>(want) - 1);
-    for (Py_ssize_t t = 1; t < want; ++t)
-        pool.emplace_back([&, t] { ok[t] = fill_range<T, Conv>(outer, cut[t], cut[t + 1], dst + start[cut[t]]); });
+    Py_ssize_t started = 1;  // runs [1, started) have a thread of their own
+    try {
+        for (; started < want; ++started) {
+            const Py_ssize_t t = started;
+            pool.emplace_back([&, t] { ok[t] = fill_range<T, Conv>(outer, cut[t], cut[t + 1], dst + start[cut[t]]); });
+        }
+    } catch (...) {
+        // No thread to be had: the calling thread converts the remaining runs.
+    }
     ok[0] = fill_range<T, Conv>(outer, cut[0], cut[1], dst);
+    for (Py_ssize_t t = started; t < want; ++t) ok[t] = fill_range<T, Conv>(outer, cut[t], cut[t + 1], dst + start[cut[t]]);
     for (std::thread& th : pool) th.join();
     return std::all_of(ok.begin(), ok.end(), [](char c) { return c != 0; });
 }
