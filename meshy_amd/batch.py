@@ -355,18 +355,29 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
     n_micro = len(job.micros)
     n_docs_total = int(job.doc_start[-1])
     n_out = int(job.out_off[-1])
-    input_ids = torch.empty(n_out, dtype=torch.int64, device=device)
-    labels = torch.empty(n_out, dtype=torch.int64, device=device)
-    positions = torch.empty(n_out, dtype=torch.int32, device=device)
-    mask = torch.empty(n_out, dtype=torch.float32, device=device)
-    doc_ids = torch.empty(n_out, dtype=torch.int64, device=device)
-    rollout_lp = torch.empty(n_out, dtype=torch.float32, device=device) if job.need_rollout_lp else None
-    want_tok = job.per_token_adv or job.broadcast_advantages
-    adv_tok = torch.empty(n_out, dtype=torch.float32, device=device) if want_tok else None
-    adv_doc = torch.empty(max(n_docs_total, 1), dtype=torch.float32, device=device)
-    lengths = torch.empty(max(n_docs_total, 1), dtype=torch.int32, device=device)
-    cu = torch.empty(n_docs_total + 2 * n_micro, dtype=torch.int32, device=device)
-    seg = torch.empty(n_docs_total + 2 * n_micro, dtype=torch.int64, device=device)
+    # Every output lives in one device allocation; the kernel gets addresses
+    # inside it, and the typed tensors are views made when a micro first needs
+    # them (_PackViews).
+    out_lay = _Layout()
+    for name, dtype in (("input_ids", torch.int64), ("labels", torch.int64), ("positions", torch.int32),
+                        ("mask", torch.float32), ("doc_ids", torch.int64)):
+        out_lay.add(name, n_out, dtype)
+    if job.need_rollout_lp:
+        out_lay.add("rollout_lp", n_out, torch.float32)
+    if job.per_token_adv or job.broadcast_advantages:
+        out_lay.add("adv_tok", n_out, torch.float32)
+    out_lay.add("adv_doc", max(n_docs_total, 1), torch.float32)
+    out_lay.add("lengths", max(n_docs_total, 1), torch.int32)
+    out_lay.add("cu", n_docs_total + 2 * n_micro, torch.int32)
+    out_lay.add("seg", n_docs_total + 2 * n_micro, torch.int64)
+    if job.teacher_k:
+        out_lay.add("teacher_ids", n_out * job.teacher_k, torch.int64)
+        out_lay.add("teacher_lps", n_out * job.teacher_k, torch.float32)
+    obuf = torch.empty(max(out_lay.size, 1), dtype=torch.uint8, device=device)
+    obase = obuf.data_ptr()
+
+    def out_addr(name: str) -> int | None:
+        return out_lay.addr(obase, name) if name in out_lay.regions else None
 
     a = _lib.PackArgs()
     base = dbuf.data_ptr()
@@ -391,36 +402,31 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
     a.doc_len = lay.addr(base, "doc_len")
     a.max_micro_elems = job.max_elems
     a.max_docs_per_micro = job.max_docs
-    a.input_ids = input_ids.data_ptr()
-    a.labels = labels.data_ptr()
-    a.positions = positions.data_ptr()
-    a.mask_out = mask.data_ptr()
-    a.doc_ids = doc_ids.data_ptr()
-    a.rollout_lp = _lib.ptr(rollout_lp)
-    a.adv_tok = _lib.ptr(adv_tok)
-    a.adv_doc = adv_doc.data_ptr()
-    a.doc_len_out = lengths.data_ptr()
-    a.cu_seqlens = cu.data_ptr()
-    a.seg_offsets = seg.data_ptr()
-    t_ids = t_lps = None
+    a.input_ids = out_addr("input_ids")
+    a.labels = out_addr("labels")
+    a.positions = out_addr("positions")
+    a.mask_out = out_addr("mask")
+    a.doc_ids = out_addr("doc_ids")
+    a.rollout_lp = out_addr("rollout_lp")
+    a.adv_tok = out_addr("adv_tok")
+    a.adv_doc = out_addr("adv_doc")
+    a.doc_len_out = out_addr("lengths")
+    a.cu_seqlens = out_addr("cu")
+    a.seg_offsets = out_addr("seg")
     if job.teacher_k:
-        K = job.teacher_k
-        t_ids = torch.empty(n_out * K, dtype=torch.int64, device=device)
-        t_lps = torch.empty(n_out * K, dtype=torch.float32, device=device)
-        a.teacher_k = K
+        a.teacher_k = job.teacher_k
         a.teacher_ids = lay.addr(base, "teacher_ids")
         a.teacher_ids_elem_bytes = lay.regions["teacher_ids"][2].itemsize
         a.teacher_lps = lay.addr(base, "teacher_lps")
-        a.teacher_ids_out = t_ids.data_ptr()
-        a.teacher_lps_out = t_lps.data_ptr()
+        a.teacher_ids_out = out_addr("teacher_ids")
+        a.teacher_lps_out = out_addr("teacher_lps")
     rc = lib.meshy_pack_micro_batches(_lib.ctypes.byref(a), torch.cuda.current_stream(device).cuda_stream)
     _lib.check(rc, "meshy_pack_micro_batches")
-    pos_w_dev = lay.view(dbuf, "pos_w")
-    views = _PackViews(job, sharder, input_ids, labels, positions, mask, doc_ids, rollout_lp, adv_tok, adv_doc,
-                       lengths, pos_w_dev, cu, seg)
+    views = _PackViews(job, sharder, obuf, out_lay, lay, dbuf)
 
     if job.teacher_k:
         K = job.teacher_k
+        t_ids, t_lps = out_lay.view(obuf, "teacher_ids"), out_lay.view(obuf, "teacher_lps")
         sizes_k = [n * K for n in views.sizes]
         tv = []
         for part_i, part_l, R, S, m in zip(torch.split(t_ids, sizes_k), torch.split(t_lps, sizes_k), views.rows,
@@ -448,15 +454,18 @@ class _PackViews:
     """The flat outputs of one pack launch and where each micro lies in them.
     A micro's tensors are views of these, made when its batch first needs them."""
 
-    def __init__(self, job: PackJob, sharder, input_ids, labels, positions, mask, doc_ids, rollout_lp, adv_tok,
-                 adv_doc, lengths, pos_w, cu, seg) -> None:
+    _TOK = ("input_ids", "labels", "positions", "mask", "doc_ids", "rollout_lp", "adv_tok")
+
+    def __init__(self, job: PackJob, sharder, obuf: torch.Tensor, out_lay: _Layout, lay: _Layout,
+                 dbuf: torch.Tensor) -> None:
         self.packed = job.layout == "packed"
         self.sharder = sharder
         self.per_token_adv = job.per_token_adv
         self.broadcast_only = job.broadcast_advantages and not job.per_token_adv
-        self.tok = (input_ids, labels, positions, mask, doc_ids, rollout_lp, adv_tok)
-        self.docs = (adv_doc, lengths, pos_w)
-        self.cu, self.seg = cu, seg
+        # The launch's one output buffer and its layout; the positive-LM
+        # weights stay in the staging buffer, where the host wrote them.
+        self.obuf, self.out_lay = obuf, out_lay
+        self.pos_w_src = (lay, dbuf)
         self.out_off = job.out_off.tolist()
         self.doc_start = job.doc_start.tolist()
         self.sizes = np.diff(job.out_off).tolist()
@@ -464,7 +473,19 @@ class _PackViews:
         self.seq = job.seq.tolist()
         self.nd = np.diff(job.doc_start).tolist()
         self.micros = job.micros
-        self._tok = self._doc = self._cu = None
+        self._tok = self._doc = self._cu = self._seg = None
+
+    def _flat(self, name: str) -> torch.Tensor | None:
+        """The whole-launch tensor of one output (None when not produced)."""
+        if name not in self.out_lay.regions:
+            return None
+        return self.out_lay.view(self.obuf, name)
+
+    @property
+    def seg(self) -> torch.Tensor:
+        if self._seg is None:
+            self._seg = self._flat("seg")
+        return self._seg
 
     # Each group's views are made for every micro at once, the first time any
     # micro needs them: one torch.split per tensor (a third of a microsecond
@@ -473,12 +494,13 @@ class _PackViews:
     def _token_views(self) -> list:
         if self._tok is None:
             sizes = self.sizes
+            tok = [self._flat(name) for name in self._TOK]
             if self.packed:
-                cols = [None if t is None else torch.split(t.view(1, -1), sizes, dim=1) for t in self.tok]
+                cols = [None if t is None else torch.split(t.view(1, -1), sizes, dim=1) for t in tok]
             else:
                 cols = [None if t is None else [p.view(R, S) for p, R, S in zip(torch.split(t, sizes), self.rows,
                                                                                  self.seq)]
-                        for t in self.tok]
+                        for t in tok]
             self._tok = [tuple(None if c is None else c[k] for c in cols) for k in range(len(sizes))]
         return self._tok
 
@@ -511,7 +533,9 @@ class _PackViews:
         """Per-document advantages, lengths and positive-LM weights of micro mb._k."""
         if self._doc is None:
             n = self.doc_start[-1]
-            self._doc = [torch.split(t[:n], self.nd) for t in self.docs]
+            lay, dbuf = self.pos_w_src
+            docs = (self._flat("adv_doc"), self._flat("lengths"), lay.view(dbuf, "pos_w"))
+            self._doc = [torch.split(t[:n], self.nd) for t in docs]
         adv, lengths, pos_w = (c[mb._k] for c in self._doc)
         made = {"lengths": lengths, "positive_lm_weights": pos_w}
         if not self.per_token_adv:
@@ -531,7 +555,7 @@ class _PackViews:
                 pads.append(pad)
                 n_cu = self.nd[k] + 1 + (1 if pad > 0 else 0)
                 sizes += [n_cu, self.nd[k] + 2 - n_cu]
-            self._cu = (torch.split(self.cu, sizes)[0::2], pads)
+            self._cu = (torch.split(self._flat("cu"), sizes)[0::2], pads)
         cus, pads = self._cu
         k = mb._k
         m, pad, cu = self.micros[k], pads[k], cus[k]

@@ -201,7 +201,9 @@ def test_pack_writes_the_segment_offsets_of_every_micro(dev, layout):
         want = torch.searchsorted(ids, torch.arange(mb.n_docs + 2), right=False)
         got = batch_segment_offsets(mb)
         assert got.dtype == torch.int64 and torch.equal(got.cpu(), want), (mb.n_docs, got, want)
-        assert getattr(mb, "_meshy_seg_src")[1].data_ptr() == got.untyped_storage().data_ptr()
+        # a view of the offsets the pack wrote, not a recomputation
+        seg = getattr(mb, "_meshy_seg_src")[1]
+        assert seg.data_ptr() <= got.data_ptr() < seg.data_ptr() + seg.numel() * seg.element_size()
 
 
 def test_16_long_sequences_micros(dev):
