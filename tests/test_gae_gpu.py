@@ -188,6 +188,30 @@ def test_exact_carry_across_chunks(dev, n, holes):
     assert np.array_equal(adv.reshape(-1).cpu().numpy(), A)
 
 
+def test_lambda_zero_is_not_a_cut_for_the_returns(dev):
+    """lambda = 0 zeroes the advantage scan's slope at every position while the
+    returns scan still carries (gamma = 1): a chunk with only the advantage
+    slope at 0 must not stop the returns' carry.  One 600 k-token document
+    without holes, integer rewards: G_t is the exact suffix sum and A_t the
+    exact one-step delta r_t + V_{t+1} - V_t (0 after the last token)."""
+    from meshy_amd.gae import gae_and_returns
+
+    n = 600_000
+    rng = np.random.default_rng(5)
+    r = (rng.random(n) < 0.05).astype(np.float32)
+    v = rng.integers(-8, 9, n).astype(np.float32)
+    G = np.cumsum(r[::-1])[::-1].astype(np.float32)
+    A = (r + np.append(v[1:], 0) - v).astype(np.float32)
+    lengths = torch.ones(1, device=dev)  # lambda = clamp(1 - 1 / (1 * 1), 0, .) = 0
+    adv, ret, lam = gae_and_returns(
+        torch.from_numpy(r).reshape(1, -1).to(dev), torch.from_numpy(v).to(torch.bfloat16).reshape(1, -1).to(dev),
+        torch.ones(1, n, device=dev), torch.zeros(1, n, dtype=torch.long, device=dev), 1, lengths=lengths,
+        gamma=1.0, alpha=1.0, epsilon=0.0)
+    assert lam.item() == 0.0
+    assert np.array_equal(ret.reshape(-1).cpu().numpy(), G)
+    assert np.array_equal(adv.reshape(-1).cpu().numpy(), A)
+
+
 def test_scan_is_deterministic(dev):
     """Two calls on the same inputs give bitwise equal results: every fold has a
     fixed order, whichever workgroup finishes first."""
