@@ -169,15 +169,20 @@ class _DistillLoss(torch.autograd.Function):
     @staticmethod
     def forward(ctx, student, inputs: _Inputs):
         dev = student.device
+        # The sums land in out; the loss handed to autograd is a view of its
+        # loss entry (no copy launched).
         out = torch.empty(_lib.DISTILL_NOUT, dtype=torch.float32, device=dev)
         seg_cnt = torch.empty(inputs.n_docs + 1, dtype=torch.float32, device=dev)
         a = inputs.args(student)
         rc = _lib.load().meshy_distill_loss_fwd(_lib.ctypes.byref(a), out.data_ptr(), seg_cnt.data_ptr(),
                                                 _lib.stream_of(dev))
         _lib.check(rc, "meshy_distill_loss_fwd")
+        # The backward reads the same arrays: the struct of their addresses, and
+        # the inputs that own them, kept alive until it runs.
         ctx.inputs = inputs
+        ctx.args = a
         ctx.save_for_backward(student, seg_cnt)
-        loss = out[0].clone()
+        loss = out[0]
         ctx.mark_non_differentiable(out)
         # The backward reads only the loss's gradient: no zero tensor for `out`'s.
         ctx.set_materialize_grads(False)
@@ -188,11 +193,11 @@ class _DistillLoss(torch.autograd.Function):
         if grad_loss is None:
             return None, None
         student, seg_cnt = ctx.saved_tensors
-        inputs: _Inputs = ctx.inputs
-        g = grad_loss.reshape(1).to(torch.float32).contiguous()
+        g = grad_loss.reshape(1)
+        if g.dtype != torch.float32:
+            g = g.float()
         grad = torch.empty_like(student)
-        a = inputs.args(student)
-        rc = _lib.load().meshy_distill_loss_bwd(_lib.ctypes.byref(a), seg_cnt.data_ptr(), g.data_ptr(),
+        rc = _lib.load().meshy_distill_loss_bwd(_lib.ctypes.byref(ctx.args), seg_cnt.data_ptr(), g.data_ptr(),
                                                 grad.data_ptr(), _lib.stream_of(student.device))
         _lib.check(rc, "meshy_distill_loss_bwd")
         return grad, None
