@@ -21,6 +21,7 @@ from typing import Any
 import torch
 
 from . import _lib
+from .hostio import gather_into
 from .wire import jagged_parts
 
 
@@ -51,7 +52,9 @@ _FIELDS = ("reward", "raw_reward", "advantage", "weight_version", "truncated", "
 
 def _per_sample(samples) -> dict[str, list]:
     """One list per field of the samples' values (None where a sample lacks the
-    field), read in a single pass over the samples."""
+    field): one comprehension per field over mappings, else one pass."""
+    if all(isinstance(s, dict) for s in samples):
+        return {f: [s.get(f) for s in samples] for f in _FIELDS}
     lists = tuple([] for _ in _FIELDS)
     pairs = tuple(zip(_FIELDS, lists))
     for s in samples:
@@ -73,7 +76,13 @@ def _scalars(per, columns, f: str) -> list[float]:
             return []
         return [float(x) for x in (v.reshape(-1).tolist() if isinstance(v, torch.Tensor) else v)]
     present = [v for v in per[f] if v is not None]
-    if present and all(torch.is_tensor(v) for v in present) and len({v.dtype for v in present}) == 1:
+    if present and all(isinstance(v, torch.Tensor) for v in present) and len({v.dtype for v in present}) == 1:
+        if not present[0].is_cuda:
+            # Host scalars: item() of each is cheaper than a stack and a copy.
+            try:
+                return [float(v.item()) for v in present]
+            except RuntimeError:
+                pass  # values of several elements: the stack below
         # One stack and one host copy instead of one per sample (one dtype, so
         # nothing is promoted or rounded; equal shapes flatten in sample order,
         # as the per-sample path below does).  Mixed devices or shapes raise.
@@ -105,18 +114,21 @@ def _flat(col) -> tuple[torch.Tensor, torch.Tensor]:
     if isinstance(col, torch.Tensor):
         return jagged_parts(col)
     present = [v for v in col if v is not None]
-    if (present and all(torch.is_tensor(v) and v.dim() == 1 for v in present)
+    if (present and all(isinstance(v, torch.Tensor) and v.dim() == 1 for v in present)
             and len({v.dtype for v in present}) == 1):
+        lengths = [0 if v is None else v.shape[0] for v in col]
+        off = torch.zeros(len(col) + 1, dtype=torch.int64)
+        torch.cumsum(torch.tensor(lengths, dtype=torch.int64), 0, out=off[1:])
+        if all(not v.is_cuda for v in present) and torch.cuda.is_available():
+            # Host tensors: one native multi-threaded gather into pinned
+            # memory, so the copy to the device is one DMA.
+            flat = torch.empty(int(off[-1]), dtype=present[0].dtype, pin_memory=True)
+            return gather_into(present, flat), off
         # One concatenation in the samples' own dtype, converted once later.
         try:
-            flat = torch.cat(present).detach()
+            return torch.cat(present).detach(), off
         except RuntimeError:
-            flat = None  # mixed devices: the per-sample path
-        if flat is not None:
-            lengths = torch.tensor([0 if v is None else v.shape[0] for v in col], dtype=torch.int64)
-            off = torch.zeros(len(col) + 1, dtype=torch.int64)
-            torch.cumsum(lengths, 0, out=off[1:])
-            return flat, off
+            pass  # mixed devices: the per-sample path
     return jagged_parts([torch.zeros(0) if v is None else _as_float(v) for v in col])
 
 
@@ -132,7 +144,8 @@ def _token_stats(per, columns, device):
         lengths = [] if tok is None else [float(x) for x in torch.diff(jagged_parts(tok)[1]).tolist() if x > 0]
         has_mask = None if mask_col is None else [True] * (jagged_parts(mask_col)[1].numel() - 1)
     else:
-        lengths = [float(len(t)) for t in per["tokens"] if t is not None and len(t) > 0]
+        lengths = [float(n) for n in (t.shape[0] if isinstance(t, torch.Tensor) else len(t)
+                                      for t in per["tokens"] if t is not None) if n > 0]
         masks = [ms if mk is None else mk for mk, ms in zip(per["mask_assistant"], per["masks"])]
         has_mask = [mk is not None for mk in masks]
         mask_col = masks if any(has_mask) else None
@@ -145,12 +158,12 @@ def _token_stats(per, columns, device):
     else:
         mflat, moff = torch.zeros(0), torch.zeros(len(per["tokens"]) + 1, dtype=torch.int64)
     nsamp = moff.numel() - 1
-    mflat = mflat.to(device=device, dtype=torch.float32).contiguous()
+    mflat = mflat.to(device=device, dtype=torch.float32, non_blocking=True).contiguous()
     moff_d = moff.to(device)
     lflat = loff_d = None
     if lp_col is not None:
         lflat, loff = _flat(lp_col)
-        lflat = lflat.to(device=device, dtype=torch.float32).contiguous()
+        lflat = lflat.to(device=device, dtype=torch.float32, non_blocking=True).contiguous()
         loff_d = loff.to(device)
     resp = torch.empty(max(nsamp, 1), dtype=torch.int64, device=device)
     lp_sum = torch.empty(max(nsamp, 1), dtype=torch.float64, device=device)
