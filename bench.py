@@ -678,12 +678,37 @@ def bench_gae(steps, warmup, no_cpu):
             ogae.compute_returns(R, M, rid, gamma=1.0)
 
         cpu_ms = _wall_ms(cpu, 3, gpu=False)
+    # The kernels alone: the same call through the C ABI in a loop (outputs,
+    # workspace and the cached offsets made once), without the wrapper's
+    # allocations and argument building.
+    import ctypes
+
+    from meshy_amd import _lib
+    from meshy_amd.loss import checked_segment_offsets
+
+    lib, stream = _lib.load(), _lib.stream_of(dev)
+    adv_o, ret_o, lam_o = torch.empty(T, device=dev), torch.empty(T, device=dev), torch.empty(n, device=dev)
+    ws = torch.empty(max(int(lib.meshy_gae_workspace_size(1, T, n)), 1), dtype=torch.uint8, device=dev)
+    off = checked_segment_offsets(doc_ids, n + 1)
+    ga = _lib.GaeArgs()
+    ga.rewards, ga.values, ga.mask, ga.doc_ids = r.data_ptr(), v.data_ptr(), m.data_ptr(), doc_ids.data_ptr()
+    ga.lengths = lengths.data_ptr()
+    ga.rows, ga.S, ga.n_docs = 1, T, n
+    ga.gamma, ga.alpha, ga.epsilon = 1.0, 1.0, 1e-6
+    ga.values_bf16 = 1
+    ga.adv, ga.returns, ga.lam_doc = adv_o.data_ptr(), ret_o.data_ptr(), lam_o.data_ptr()
+    ga.workspace, ga.workspace_bytes = ws.data_ptr(), ws.numel()
+    ga.seg_offsets = off.data_ptr()
+    pg = ctypes.byref(ga)
+    _checked(lib.meshy_gae(pg, stream), "meshy_gae")
+    dev_us = _gpu_ms(lambda: lib.meshy_gae(pg, stream), steps, warmup) * 1e3
     # reads rewards 4 + values 2 + mask 4, writes adv 4 + returns 4; document
     # starts come from the segment offsets of doc_ids (computed and
     # order-checked on the first call for the tensor, then reused), the ids
     # themselves are read at chunk ends
-    return _entry(ms * 1e3, T * 18, cpu_ms, tokens=T, docs=n, cpu_sample="sequential loop on padded [1024, S_max]",
-                  note="doc_ids offsets cached after the first call")
+    return _with_device(_entry(ms * 1e3, T * 18, cpu_ms, tokens=T, docs=n,
+                               cpu_sample="sequential loop on padded [1024, S_max]",
+                               note="doc_ids offsets cached after the first call"), dev_us, T * 18)
 
 
 # ---------------------------------------------------------------- GAE attach over 1024 docs, pack of 16 long sequences
