@@ -19,6 +19,8 @@ W warm-up steps start on a busy device.  Prints ONE JSON line with
 * kernels              per-kernel device time, algorithmic GB/s and the
                        restated CPU path for the 256-sample GRPO batch,
                        the 512-doc PPO batch, 16 long sequences and 1024 GAE docs
+                       (legs of sub-millisecond calls average over at least
+                       200 calls, whatever K is)
 * end_to_end           pack + GRPO -> logprob+entropy -> PPO fwd+bwd -> logits
                        backward at T = 16384, GPU wall against the CPU
                        restatement, with the largest difference between the
@@ -66,6 +68,16 @@ def _warm(fn, warmup: int, warm_s: float, before=None, gpu: bool = False) -> Non
         if gpu:
             _sync()
         i += 1
+
+
+# Legs whose calls take well under a millisecond average over at least this
+# many calls (a few milliseconds in all), whatever --steps is: with 20 calls the
+# first launches' queueing shows in the average.
+SMALL_STEPS = 200
+
+
+def _small(steps: int) -> int:
+    return max(steps, SMALL_STEPS)
 
 
 def _gpu_ms(fn, steps: int, warmup: int, warm_s: float = WARM_S) -> float:
@@ -317,7 +329,7 @@ def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
         loss, _ = opd.distill_from_gathered(stub, gd, mb, mini)
         loss.backward()
 
-    ms = _gpu_ms(loss_fb, steps, warmup)
+    ms = _gpu_ms(loss_fb, _small(steps), warmup)
     cpu_ms = None
     if not no_cpu:
         from oracle import opd as oopd
@@ -356,7 +368,7 @@ def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
     _checked(lib.meshy_distill_loss_fwd(pa, out_t.data_ptr(), seg.data_ptr(), stream), "meshy_distill_loss_fwd")
     _checked(lib.meshy_distill_loss_bwd(pa, seg.data_ptr(), one.data_ptr(), grad.data_ptr(), stream),
              "meshy_distill_loss_bwd")
-    dev_us = _gpu_ms(dev_fb, steps, warmup) * 1e3
+    dev_us = _gpu_ms(dev_fb, _small(steps), warmup) * 1e3
     # fwd reads student (K+1)*4 + teacher K*4 + mask 4 + rollout 4 + doc id 8 (+ 8 for the
     # offsets); bwd reads the same and writes (K+1)*4
     per_tok = (K + 1) * 4 + K * 4 + 16
@@ -526,8 +538,8 @@ def bench_ppo(steps, warmup, no_cpu):
         loss, _ = ppo_clip_loss(stub, new_d, old_d, mb, mini)
         loss.backward()
 
-    fwd_ms = _gpu_ms(fwd, steps, warmup)
-    fb_ms = _gpu_ms(fwd_bwd, steps, warmup)
+    fwd_ms = _gpu_ms(fwd, _small(steps), warmup)
+    fb_ms = _gpu_ms(fwd_bwd, _small(steps), warmup)
     cpu_ms = None
     if not no_cpu:
         from oracle import ppo as oppo
@@ -581,10 +593,10 @@ def bench_ppo(steps, warmup, no_cpu):
 
     _checked(lib.meshy_ppo_loss_fwd(pa, out_t.data_ptr(), None, stream), "meshy_ppo_loss_fwd")
     _checked(lib.meshy_ppo_loss_bwd(pa, None, one.data_ptr(), grad.data_ptr(), stream), "meshy_ppo_loss_bwd")
-    fwd0_dev = _gpu_ms(dev_fwd_nograd, steps, warmup) * 1e3
-    fwd_dev = _gpu_ms(dev_fwd, steps, warmup) * 1e3
-    bwd_dev = _gpu_ms(dev_bwd, steps, warmup) * 1e3
-    off_dev = _gpu_ms(dev_offsets, steps, warmup) * 1e3
+    fwd0_dev = _gpu_ms(dev_fwd_nograd, _small(steps), warmup) * 1e3
+    fwd_dev = _gpu_ms(dev_fwd, _small(steps), warmup) * 1e3
+    bwd_dev = _gpu_ms(dev_bwd, _small(steps), warmup) * 1e3
+    off_dev = _gpu_ms(dev_offsets, _small(steps), warmup) * 1e3
     # fwd: new, old, mask read 12 B/token (+ the unit gradient written, 4 B,
     # when a backward follows); bwd: unit gradient read + gradient written 8 B/token
     fwd_bytes = T * 12
@@ -655,7 +667,7 @@ def bench_gae(steps, warmup, no_cpu):
     v = torch.from_numpy(values).to(torch.bfloat16).reshape(1, -1).to(dev)
     m = torch.from_numpy(batch.mask).reshape(1, -1).to(dev)
     lengths = torch.full((n,), 1.0 / (1.0 - 0.95), device=dev)
-    ms = _gpu_ms(lambda: gae_and_returns(r, v, m, doc_ids, n, lengths=lengths, gamma=1.0, alpha=1.0), steps, warmup)
+    ms = _gpu_ms(lambda: gae_and_returns(r, v, m, doc_ids, n, lengths=lengths, gamma=1.0, alpha=1.0), _small(steps), warmup)
     cpu_ms = None
     if not no_cpu:
         from oracle import gae as ogae
@@ -701,7 +713,7 @@ def bench_gae(steps, warmup, no_cpu):
     ga.seg_offsets = off.data_ptr()
     pg = ctypes.byref(ga)
     _checked(lib.meshy_gae(pg, stream), "meshy_gae")
-    dev_us = _gpu_ms(lambda: lib.meshy_gae(pg, stream), steps, warmup) * 1e3
+    dev_us = _gpu_ms(lambda: lib.meshy_gae(pg, stream), _small(steps), warmup) * 1e3
     # reads rewards 4 + values 2 + mask 4, writes adv 4 + returns 4; document
     # starts come from the segment offsets of doc_ids (computed and
     # order-checked on the first call for the tensor, then reused), the ids
@@ -828,7 +840,7 @@ def bench_critic(steps, warmup, no_cpu):
     mask = torch.from_numpy(batch.mask).reshape(1, -1).to(dev)
     adv = torch.randn(1, T, generator=g, device=dev)
     out = {}
-    ms = _gpu_ms(lambda: critic.advantages_to_per_sequence(adv, mask, doc_ids, n), steps, warmup)
+    ms = _gpu_ms(lambda: critic.advantages_to_per_sequence(adv, mask, doc_ids, n), _small(steps), warmup)
     cpu_ms = None
     if not no_cpu:
         from oracle import critic as ocritic
@@ -848,7 +860,7 @@ def bench_critic(steps, warmup, no_cpu):
         v.grad = None
         critic.clipped_value_error(v, t, o, 0.2).sum().backward()
 
-    ms = _gpu_ms(cve, steps, warmup)
+    ms = _gpu_ms(cve, _small(steps), warmup)
     cpu_ms = None
     if not no_cpu:
         from oracle import critic as ocritic
@@ -876,7 +888,7 @@ def bench_critic(steps, warmup, no_cpu):
 
     _checked(lib.meshy_clipped_value_error(vf.data_ptr(), tf.data_ptr(), of.data_ptr(), 1, 0.2, T, err.data_ptr(),
                                            stream), "meshy_clipped_value_error")
-    dev_us = _gpu_ms(dev_fb, steps, warmup) * 1e3
+    dev_us = _gpu_ms(dev_fb, _small(steps), warmup) * 1e3
     # fwd: v, t, o read + out written; bwd (the sum's gradient is one broadcast
     # value): v, t, o read + grad written
     out["clipped_value_error_fwd_bwd_1024_docs"] = _with_device(_entry(ms * 1e3, T * 32, cpu_ms, tokens=T), dev_us,
@@ -939,7 +951,7 @@ def bench_whiten(batch, dev, steps, warmup, no_cpu):
     g = torch.Generator(device=dev).manual_seed(21)
     adv = torch.randn(T, generator=g, device=dev) * 3.0 + 1.0
     mask = torch.from_numpy(batch.mask).to(dev)
-    ms = _gpu_ms(lambda: vapo.whiten_flat(adv, mask), steps, warmup)
+    ms = _gpu_ms(lambda: vapo.whiten_flat(adv, mask), _small(steps), warmup)
     lib, stream = _lib.load(), _lib.stream_of(dev)
     stats = torch.empty(3, dtype=torch.float64, device=dev)
     ws = torch.empty(int(lib.meshy_whiten_workspace_size(T)), dtype=torch.uint8, device=dev)
@@ -951,7 +963,7 @@ def bench_whiten(batch, dev, steps, warmup, no_cpu):
 
     _checked(lib.meshy_whiten_stats(adv.data_ptr(), mask.data_ptr(), T, 1.0, stats.data_ptr(), ws.data_ptr(),
                                     ws.numel(), stream), "meshy_whiten_stats")
-    dev_us = _gpu_ms(dev_call, steps, warmup) * 1e3
+    dev_us = _gpu_ms(dev_call, _small(steps), warmup) * 1e3
     cpu_ms = None
     if not no_cpu:
         from oracle import vapo as ovapo
