@@ -16,6 +16,7 @@ import math
 import numpy as np
 import pytest
 import torch
+from hypothesis import given, settings, strategies as st
 
 from meshy_amd import _lib, wire
 
@@ -114,3 +115,55 @@ def test_group_columns_use_the_native_pass():
             assert fv.dtype == rv.dtype and torch.equal(fv, rv) and torch.equal(fo, ro), f
         else:
             assert fast[f].dtype == ref[f].dtype and torch.equal(fast[f], ref[f]), f
+
+
+@settings(max_examples=120, deadline=None)
+@given(
+    lengths=st.lists(st.integers(0, 40), min_size=0, max_size=30),
+    kind=st.sampled_from(["int", "float", "mixed"]),
+    dtype=st.sampled_from([torch.int64, torch.float32]),
+    seed=st.integers(0, 2**31 - 1),
+    use_tuples=st.booleans(),
+)
+def test_random_columns_match_numpy(lengths, kind, dtype, seed, use_tuples):
+    """Random jagged columns of ints, floats, bools and mixes: the native pass
+    (or its numpy fallback, for floats in an int64 column) equals numpy."""
+    rng = np.random.default_rng(seed)
+
+    def value():
+        pick = kind if kind != "mixed" else rng.choice(["int", "float", "bool"])
+        if pick == "int":
+            return int(rng.integers(-2**40, 2**40))
+        if pick == "float":
+            return float(rng.normal(0, 1e3))
+        return bool(rng.integers(0, 2))
+
+    seqs = [[value() for _ in range(L)] for L in lengths]
+    if use_tuples:
+        seqs = [tuple(s) for s in seqs]
+    npdt = np.int64 if dtype == torch.int64 else np.float32
+    try:
+        ref = _numpy_flat(seqs, npdt)
+    except (TypeError, ValueError, OverflowError) as e:
+        with pytest.raises(type(e)):
+            wire.flatten_sequences(seqs, dtype)
+        return
+    flat, off = wire.flatten_sequences(seqs, dtype)
+    assert flat.tobytes() == ref.tobytes()
+    assert off.tolist() == [0] + list(itertools.accumulate(lengths))
+
+
+def test_long_columns_split_over_threads_match_numpy():
+    """Columns of more than 64 k values are converted by several threads, cut
+    at sample boundaries by element count: lengths from 0 to 50 k, so that cuts
+    fall on long and empty samples alike."""
+    rng = np.random.default_rng(9)
+    lengths = [0, 50_000, 1, 0, 30_000, 7, 45_000, 0, 0, 12_345, 3, 60_000, 0, 20_000]
+    ints = [rng.integers(-2**62, 2**62, L).tolist() for L in lengths]
+    floats = [rng.normal(0, 5, L).tolist() for L in lengths]
+    _check(ints, torch.int64)
+    _check(floats, torch.float32)
+    # a declined value deep in a late run still sends the column to numpy
+    bad = [list(x) for x in ints]
+    bad[11][59_999] = np.int64(5)
+    _check(bad, torch.int64)
