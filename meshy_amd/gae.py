@@ -147,7 +147,8 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
 
     Reads ``self.seq_len``, ``self.gae_gamma``, ``self.gae_alpha``,
     ``self.gae_lambda`` and ``self.device``.  The samples' masks, values and
-    rewards travel to the device in one copy; ``meshy_gae_attach`` shifts them
+    rewards travel to the device in two copies (the masks' while the values
+    are gathered on the host); ``meshy_gae_attach`` shifts them
     onto the next-token grid, places each reward, runs the reverse scan over the
     samples laid end to end (one document per sample, so no padding rows) and
     reduces the critic metrics.  Each sample gets ``ADVANTAGE_TOKENS``, a device
@@ -192,7 +193,12 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
     lay.add("reward", n, torch.float32)
     lay.add("offsets", n + 1, torch.int64)
     host = torch.empty(lay.size, dtype=torch.uint8, pin_memory=True)
+    dbuf = torch.empty(lay.size, dtype=torch.uint8, device=dev)
     gather_into(masks, lay.view(host, "mask"))
+    # The masks travel to the device while the values are gathered (finer runs
+    # of samples, each copied once staged, measured no faster).
+    cut = lay.regions["values"][0]
+    dbuf[:cut].copy_(host[:cut], non_blocking=True)
     gather_into(vals, lay.view(host, "values"))
     if all(isinstance(r, torch.Tensor) and r.numel() == 1 for r in rewards):
         try:  # one shape (the usual 0-d rewards): stacked as they are
@@ -205,8 +211,7 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
                               dtype=torch.float32)
     lay.view(host, "reward").copy_(reward)
     lay.view(host, "offsets").copy_(torch.from_numpy(offsets))
-    dbuf = torch.empty(lay.size, dtype=torch.uint8, device=dev)
-    dbuf.copy_(host, non_blocking=True)
+    dbuf[cut:].copy_(host[cut:], non_blocking=True)
 
     lib = _lib.load()
     adv = torch.empty(max(total, 1), dtype=torch.float32, device=dev)
