@@ -617,7 +617,8 @@ extern "C" int meshy_critic_accumulate(const void* values, int32_t values_bf16, 
     clear_error();
     const char* who = "meshy_critic_accumulate";
     if (rows < 0 || S < 0 || rows > INT32_MAX) return set_error(MESHY_EINVAL, "%s: bad shape", who);
-    if (!sums || (rows > 0 && (!values || !returns || !mask || !row_value)))
+    // Rows of no tokens (S == 0) may come with NULL per-token arrays.
+    if (!sums || (rows > 0 && !row_value) || (rows * S > 0 && (!values || !returns || !mask)))
         return set_error(MESHY_ENULL, "%s: NULL pointer", who);
     if (workspace_bytes < meshy_critic_accumulate_workspace_size(rows) || (rows > 0 && !workspace))
         return set_error(MESHY_ESPACE, "%s: workspace needs %zu bytes", who,
@@ -679,7 +680,8 @@ extern "C" int meshy_critic_window_sums(const void* values, int32_t values_bf16,
     clear_error();
     const char* who = "meshy_critic_window_sums";
     if (rows < 0 || S < 0 || rows > INT32_MAX) return set_error(MESHY_EINVAL, "%s: bad shape", who);
-    if (!sums || (rows > 0 && (!values || !returns || !mask || !row_value)))
+    // Rows of no tokens (S == 0) may come with NULL per-token arrays.
+    if (!sums || (rows > 0 && !row_value) || (rows * S > 0 && (!values || !returns || !mask)))
         return set_error(MESHY_ENULL, "%s: NULL pointer", who);
     if (workspace_bytes < meshy_critic_window_workspace_size(rows) || (rows > 0 && !workspace))
         return set_error(MESHY_ESPACE, "%s: workspace needs %zu bytes", who, meshy_critic_window_workspace_size(rows));

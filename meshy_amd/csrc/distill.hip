@@ -318,7 +318,8 @@ __global__ __launch_bounds__(kTileTok) void k_fkl_bwd(const float* __restrict__ 
 int validate(const meshy_distill_args& a, const char* who) {
     if (a.n_tokens < 0 || a.n_docs < 0) return set_error(MESHY_EINVAL, "%s: negative sizes", who);
     if (a.k < 1 || a.k > kMaxK) return set_error(MESHY_EINVAL, "%s: k must be in [1, %d]", who, kMaxK);
-    if (!a.student || !a.teacher || !a.mask || !a.seg_offsets || !a.doc_ids)
+    // Without tokens the per-token arrays may be NULL (an empty tensor has no storage).
+    if ((a.n_tokens > 0 && (!a.student || !a.teacher || !a.mask || !a.doc_ids)) || !a.seg_offsets)
         return set_error(MESHY_ENULL, "%s: student, teacher, mask, seg_offsets and doc_ids are required", who);
     return MESHY_OK;
 }
@@ -358,13 +359,15 @@ extern "C" int meshy_distill_loss_bwd(const meshy_distill_args* args, const floa
     using namespace meshy;
     clear_error();
     const char* who = "meshy_distill_loss_bwd";
-    if (!args || !seg_cnt || !grad_loss || !grad_student)
+    if (!args || !seg_cnt || !grad_loss)
         return set_error(MESHY_ENULL, "%s: args, seg_cnt, grad_loss and grad_student are required", who);
     const meshy_distill_args& a = *args;
     int rc = validate(a, who);
     if (rc) return rc;
     const int64_t nt = n_tiles(a.n_tokens);
     if (nt == 0) return MESHY_OK;
+    if (!grad_student)
+        return set_error(MESHY_ENULL, "%s: args, seg_cnt, grad_loss and grad_student are required", who);
     hipLaunchKernelGGL(k_distill_bwd, dim3(static_cast<unsigned>(nt)), dim3(kTileTok), 0, stream, a, seg_cnt,
                        grad_loss, grad_student);
     return check_launch(who);

@@ -690,8 +690,11 @@ namespace {
 int gae_launch(const meshy_gae_args& g, hipStream_t stream) {
     if (g.rows < 0 || g.S < 0 || g.n_docs < 0) return set_error(MESHY_EINVAL, "meshy_gae: negative sizes");
     const int64_t n = g.rows * g.S;
-    if (!g.rewards || !g.mask || !g.doc_ids) return set_error(MESHY_ENULL, "meshy_gae: rewards, mask and doc_ids are required");
-    if (g.adv && !g.values) return set_error(MESHY_ENULL, "meshy_gae: advantages need values");
+    // Without tokens the per-token arrays may be NULL (an empty tensor has no
+    // storage); lambda per document is still written.
+    if (n > 0 && (!g.rewards || !g.mask || !g.doc_ids))
+        return set_error(MESHY_ENULL, "meshy_gae: rewards, mask and doc_ids are required");
+    if (n > 0 && g.adv && !g.values) return set_error(MESHY_ENULL, "meshy_gae: advantages need values");
     if (!(g.alpha > 0.f)) return set_error(MESHY_EINVAL, "meshy_gae: alpha must be positive");
     if (!g.workspace || g.workspace_bytes < ws_bytes(n, g.n_docs))
         return set_error(MESHY_ESPACE, "meshy_gae: workspace needs %zu bytes", ws_bytes(n, g.n_docs));

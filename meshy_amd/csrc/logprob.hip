@@ -319,15 +319,17 @@ constexpr int kBwdUnroll = 4;
 constexpr uint32_t kBwdFlatBlocks = 65536;
 constexpr int kMaxIds = 256;  // gather ids per row (one thread each)
 
+// Shape checks; an empty call (rows * T == 0) accepts NULL arrays, as an
+// empty tensor has no storage.
 int check_common(const void* logits, int64_t rows, int64_t T, int64_t V, int64_t stride_b,
                  int64_t stride_t, const char* who) {
-    if (!logits) return set_error(MESHY_ENULL, "%s: logits is NULL", who);
     if (rows < 0 || T < 0 || V <= 0)
         return set_error(MESHY_EINVAL, "%s: bad shape rows=%lld T=%lld V=%lld", who,
                          static_cast<long long>(rows), static_cast<long long>(T),
                          static_cast<long long>(V));
     if (stride_b < 0 || stride_t < 0) return set_error(MESHY_EINVAL, "%s: negative stride", who);
-    if (rows * T > INT32_MAX) return set_error(MESHY_EINVAL, "%s: too many rows", who);
+    if (T > 0 && rows > INT32_MAX / T) return set_error(MESHY_EINVAL, "%s: too many rows", who);
+    if (!logits && rows * T > 0) return set_error(MESHY_ENULL, "%s: logits is NULL", who);
     return MESHY_OK;
 }
 
@@ -407,6 +409,7 @@ extern "C" int meshy_logprob_entropy_fwd(const uint16_t* logits, int64_t rows, i
     const char* who = "meshy_logprob_entropy_fwd";
     int rc = check_common(logits, rows, T, V, stride_b, stride_t, who);
     if (rc) return rc;
+    if (rows * T == 0) return MESHY_OK;
     if (logp && !labels) return set_error(MESHY_ENULL, "%s: logp needs labels", who);
     return launch_fwd(logits, rows, T, V, stride_b, stride_t, logp ? labels : nullptr, logp ? 1 : 0, logp,
                       entropy, lse, stream, who);
@@ -423,6 +426,7 @@ extern "C" int meshy_gather_logprobs_fwd(const uint16_t* logits, int64_t rows, i
     if (n_ids < 1 || n_ids > kMaxIds)
         return set_error(MESHY_EINVAL, "%s: n_ids must be in [1, %d], got %lld", who, kMaxIds,
                          static_cast<long long>(n_ids));
+    if (rows * T == 0) return MESHY_OK;
     if (!ids || !out) return set_error(MESHY_ENULL, "%s: ids and out are required", who);
     return launch_fwd(logits, rows, T, V, stride_b, stride_t, ids, static_cast<int>(n_ids), out, nullptr, lse,
                       stream, who);
@@ -441,6 +445,7 @@ extern "C" int meshy_logprob_bwd(const uint16_t* logits, int64_t rows, int64_t T
     const char* who = "meshy_logprob_bwd";
     int rc = check_common(logits, rows, T, V, stride_b, stride_t, who);
     if (rc) return rc;
+    if (rows * T == 0) return MESHY_OK;
     if (!labels || !lse || !grad_logp || !grad_logits)
         return set_error(MESHY_ENULL, "%s: labels, lse, grad_logp and grad_logits are required", who);
     return launch_bwd(logits, rows, T, V, stride_b, stride_t, labels, 1, lse, grad_logp, grad_logits, workspace,
@@ -503,13 +508,13 @@ extern "C" int meshy_logprob_bwd_noalloc(const uint16_t* logits, int64_t rows, i
     const char* who = "meshy_logprob_bwd_noalloc";
     int rc = check_common(logits, rows, T, V, stride_b, stride_t, who);
     if (rc) return rc;
+    const int64_t n = rows * T;
+    if (n == 0) return MESHY_OK;
     if (!labels || !lse || !grad_logp || !grad_logits)
         return set_error(MESHY_ENULL, "%s: labels, lse, grad_logp and grad_logits are required", who);
-    const int64_t n = rows * T;
     if (n > MESHY_NOALLOC_MAX_ROWS)
         return set_error(MESHY_ESPACE, "%s: %lld rows exceed the static scratch of %d rows", who,
                          static_cast<long long>(n), MESHY_NOALLOC_MAX_ROWS);
-    if (n == 0) return MESHY_OK;
     float* ws = nullptr;
     rc = scratch_of_current_device(&ws, who);
     if (rc) return rc;
@@ -530,6 +535,7 @@ extern "C" int meshy_gather_logprobs_bwd(const uint16_t* logits, int64_t rows, i
     if (n_ids < 1 || n_ids > kMaxIds)
         return set_error(MESHY_EINVAL, "%s: n_ids must be in [1, %d], got %lld", who, kMaxIds,
                          static_cast<long long>(n_ids));
+    if (rows * T == 0) return MESHY_OK;
     if (!ids || !lse || !grad_out || !grad_logits)
         return set_error(MESHY_ENULL, "%s: ids, lse, grad_out and grad_logits are required", who);
     return launch_bwd(logits, rows, T, V, stride_b, stride_t, ids, static_cast<int>(n_ids), lse, grad_out,

@@ -681,8 +681,11 @@ __global__ __launch_bounds__(kThreads) void k_segment_offsets(const int64_t* __r
 
 int validate(const meshy_ppo_args& a, const char* who) {
     if (a.n_tokens < 0 || a.n_docs < 0) return set_error(MESHY_EINVAL, "%s: negative sizes", who);
-    if (!a.new_lp || !a.old_lp || !a.mask || !a.seg_offsets || !a.doc_ids ||
-        (a.n_docs > 0 && !a.adv && !a.adv_per_token) || (a.adv_per_token && !a.adv))
+    // Without tokens the per-token arrays may be NULL (an empty tensor has no
+    // storage); the document slots still get their sums.
+    const bool tok = a.n_tokens > 0;
+    if ((tok && (!a.new_lp || !a.old_lp || !a.mask || !a.doc_ids)) || !a.seg_offsets ||
+        (a.n_docs > 0 && !a.adv && !a.adv_per_token) || (tok && a.adv_per_token && !a.adv))
         return set_error(MESHY_ENULL, "%s: new_lp, old_lp, mask, adv, seg_offsets and doc_ids are required", who);
     if (a.use_icepop && !a.rollout_lp) return set_error(MESHY_EINVAL, "%s: IcePop requires rollout log-probabilities", who);
     if (a.positive_lm_coef != 0.f && !a.positive_lm_weights && a.n_docs > 0)
@@ -734,12 +737,13 @@ extern "C" int meshy_ppo_loss_bwd(const meshy_ppo_args* args, const float* seg_c
                                   float* grad_new, hipStream_t stream) {
     using namespace meshy;
     clear_error();
-    if (!args || !grad_loss || !grad_new)
+    if (!args || !grad_loss)
         return set_error(MESHY_ENULL, "meshy_ppo_loss_bwd: args, grad_loss and grad_new are required");
     const meshy_ppo_args& a = *args;
     int rc = validate(a, "meshy_ppo_loss_bwd");
     if (rc) return rc;
     if (a.n_tokens == 0) return MESHY_OK;
+    if (!grad_new) return set_error(MESHY_ENULL, "meshy_ppo_loss_bwd: args, grad_loss and grad_new are required");
     if (a.grad_unit && a.per_token_loss) {
         const int64_t nb = ceil_div(ceil_div(a.n_tokens, 4), static_cast<int64_t>(kThreads));
         const bool vec = reinterpret_cast<uintptr_t>(a.grad_unit) % 16 == 0 &&

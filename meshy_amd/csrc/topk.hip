@@ -283,7 +283,6 @@ extern "C" int meshy_topk_logprobs(const uint16_t* logits, int64_t rows, int64_t
     using namespace meshy;
     clear_error();
     const char* who = "meshy_topk_logprobs";
-    if (!logits || !ids || !logprobs) return set_error(MESHY_ENULL, "%s: logits, ids and logprobs are required", who);
     if (rows < 0 || T < 0 || V <= 0 || stride_b < 0 || stride_t < 0)
         return set_error(MESHY_EINVAL, "%s: bad shape rows=%lld T=%lld V=%lld", who, static_cast<long long>(rows),
                          static_cast<long long>(T), static_cast<long long>(V));
@@ -291,9 +290,10 @@ extern "C" int meshy_topk_logprobs(const uint16_t* logits, int64_t rows, int64_t
     if (k < 1 || k > kMaxTopK || k > V)
         return set_error(MESHY_EINVAL, "%s: k must be in [1, min(%d, V)], got %lld", who, kMaxTopK,
                          static_cast<long long>(k));
-    if (rows * T > INT32_MAX) return set_error(MESHY_EINVAL, "%s: too many rows", who);
+    if (T > 0 && rows > INT32_MAX / T) return set_error(MESHY_EINVAL, "%s: too many rows", who);
     const int64_t n = rows * T;
-    if (n == 0) return MESHY_OK;
+    if (n == 0) return MESHY_OK;  // an empty call: NULL arrays are accepted
+    if (!logits || !ids || !logprobs) return set_error(MESHY_ENULL, "%s: logits, ids and logprobs are required", who);
     const dim3 grid(static_cast<unsigned>(n));
     const bool vec = reinterpret_cast<uintptr_t>(logits) % 16 == 0 && stride_b % 8 == 0 && stride_t % 8 == 0;
     if (vec && k <= kSmallK) {

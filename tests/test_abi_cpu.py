@@ -93,6 +93,25 @@ def test_entry_point_rejects(name, args, code, text):
     assert text in msg, msg
 
 
+@pytest.mark.parametrize("name,args", [
+    # logits, rows, T, V, stride_b, stride_t, labels, logp, entropy, lse, stream
+    ("meshy_logprob_entropy_fwd", (None, 1, 0, 8, 0, 8, None, None, None, None, None)),
+    ("meshy_logprob_entropy_fwd", (None, 0, 5, 8, 40, 8, None, None, None, None, None)),
+    ("meshy_gather_logprobs_fwd", (None, 1, 0, 8, 0, 8, None, 3, None, None, None)),
+    ("meshy_logprob_bwd", (None, 1, 0, 8, 0, 8, None, None, None, None, None, 0, None)),
+    ("meshy_logprob_bwd_noalloc", (None, 1, 0, 8, 0, 8, None, None, None, None, None)),
+    ("meshy_gather_logprobs_bwd", (None, 1, 0, 8, 0, 8, None, 9, None, None, None, None, 0, None)),
+    ("meshy_topk_logprobs", (None, 1, 0, 100, 0, 100, 8, None, None, None, None)),
+    ("meshy_clipped_value_error", (None, None, None, 1, 0.2, 0, None, None)),
+    ("meshy_whiten_apply", (None, None, 0, None, None)),
+])
+def test_empty_calls_accept_null_arrays(name, args):
+    """An empty tensor has no storage: with nothing to read or write, every
+    entry point returns success for NULL arrays (before any device call)."""
+    rc, msg = _call(name, *args)
+    assert rc == 0, (rc, msg)
+
+
 def test_struct_entry_points_reject():
     lib = _lib.load()
     a = _lib.DistillArgs()
