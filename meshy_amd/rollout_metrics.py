@@ -172,6 +172,12 @@ def _token_stats(per, columns, device):
     lib = _lib.load()
     ws = torch.empty(max(int(lib.meshy_ragged_token_stats_workspace_size(nsamp)), 1), dtype=torch.uint8,
                      device=device)
+    # Columns of no tokens have no storage; a one-element stand-in is never
+    # read (every sample's range is empty) but keeps the column present.
+    if mflat.numel() == 0:
+        mflat = torch.zeros(1, dtype=torch.float32, device=device)
+    if lflat is not None and lflat.numel() == 0:
+        lflat = torch.zeros(1, dtype=torch.float32, device=device)
     rc = lib.meshy_ragged_token_stats(mflat.data_ptr(), _lib.ptr(lflat), moff_d.data_ptr(), _lib.ptr(loff_d),
                                       nsamp, resp.data_ptr(), lp_sum.data_ptr(), out_off.data_ptr(),
                                       _lib.ptr(kept if lflat is not None else None), ws.data_ptr(), ws.numel(),

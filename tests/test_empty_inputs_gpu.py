@@ -99,3 +99,19 @@ def test_ppo_loss_of_no_tokens(dev):
     loss.backward()
     assert loss.item() == 0.0 and new.grad.shape == (1, 0)
     assert all(v.item() == 0.0 for v in sums.values())
+
+
+def test_rollout_metrics_of_samples_without_tokens(dev):
+    """Samples whose token, mask and log-prob columns are all empty: the
+    oracle's statistics (zero response lengths, no kept log-probs)."""
+    from oracle import rollout_metrics as orm
+
+    from meshy_amd.rollout_metrics import rollout_metrics
+
+    samples = [{"tokens": torch.zeros(0, dtype=torch.long), "logprobs": torch.zeros(0),
+                "mask_assistant": torch.zeros(0), "reward": torch.tensor(float(i % 2))} for i in range(3)]
+    m, hist = rollout_metrics(samples, seq_len=64)
+    rm, rh = orm.rollout_metrics(samples, seq_len=64)
+    assert set(m) == set(rm) and set(hist) == set(rh)
+    for k, v in rm.items():
+        assert m[k] == pytest.approx(v, abs=1e-6), k
