@@ -79,7 +79,10 @@ __global__ __launch_bounds__(kFillThreads) void k_pack_fill(meshy_pack_args a) {
     const int64_t out0 = a.micro_out_off[k];
     const int64_t n_elems = a.micro_out_off[k + 1] - out0;
     const int64_t tile0 = static_cast<int64_t>(blockIdx.x) * (kFillThreads * kFillItems);
-    if (tile0 >= n_elems) return;  // uniform over the workgroup
+    // Uniform over the workgroup.  Workgroup 0 of every micro stays, even of
+    // one without output elements (all its documents empty): it writes the
+    // per-document tables.
+    if (tile0 >= n_elems && blockIdx.x > 0) return;
     const int64_t S = a.micro_seq_len[k];
     const int32_t d0 = a.micro_doc_start[k];
     const int32_t nd = a.micro_doc_start[k + 1] - d0;
@@ -276,7 +279,7 @@ extern "C" int meshy_pack_micro_batches(const meshy_pack_args* args, hipStream_t
         return set_error(MESHY_ENULL, "meshy_pack_micro_batches: adv_doc needs adv_samples");
     if (a.adv_tok && !a.adv_tokens && !a.adv_samples)
         return set_error(MESHY_ENULL, "meshy_pack_micro_batches: adv_tok needs adv_tokens or adv_samples");
-    if (a.max_micro_elems <= 0 || a.max_micro_elems > INT32_MAX)
+    if (a.max_micro_elems < 0 || a.max_micro_elems > INT32_MAX)
         return set_error(MESHY_EINVAL, "meshy_pack_micro_batches: bad max_micro_elems %lld",
                          static_cast<long long>(a.max_micro_elems));
     if (a.n_micro > 65535) return set_error(MESHY_EINVAL, "meshy_pack_micro_batches: too many micros");
@@ -296,7 +299,7 @@ extern "C" int meshy_pack_micro_batches(const meshy_pack_args* args, hipStream_t
         if (rc) return rc;
     }
     const int64_t per_block = static_cast<int64_t>(kFillThreads) * kFillItems;
-    const dim3 grid(static_cast<unsigned>(ceil_div(a.max_micro_elems, per_block)),
+    const dim3 grid(static_cast<unsigned>(std::max<int64_t>(1, ceil_div(a.max_micro_elems, per_block))),
                     static_cast<unsigned>(a.n_micro));
     if (a.tokens_elem_bytes == 4) {
         hipLaunchKernelGGL(k_pack_fill<int32_t>, grid, dim3(kFillThreads), 0, stream, a);

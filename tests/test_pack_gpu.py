@@ -480,3 +480,45 @@ def test_pack_step_without_plan_objects_builds_the_same_batches(dev, layout):
             assert x.shape == y.shape and torch.equal(x, y), k
         assert a.n_docs == b.n_docs
     assert torch.equal(full.advantages, lite.advantages)
+
+
+@pytest.mark.parametrize("layout", ["packed", "padded"])
+def test_empty_and_one_token_samples(dev, layout):
+    """Samples of 0, 1 and 2 tokens among longer ones, planned and packed:
+    every micro equals the oracle's (empty documents keep their cu_seqlens
+    slot, one-token documents have no label)."""
+    from meshy_amd.batch import build_micro_batches
+    from meshy_amd.plan import PlannerConfig, build_plan
+
+    lengths = [0, 1, 2, 0, 5, 300, 0, 1, 64, 3, 0, 2]
+    samples = [_sample(L, prompt=min(L, 1), adv=0.25 * j, seed=30 + j) for j, L in enumerate(lengths)]
+    cfg = PlannerConfig(layout=layout, mini_batch_size=len(lengths), seq_len=512, align=8,
+                        max_tokens_per_micro=512)
+    loss = [max(0, L - 1) for L in lengths]
+    plan = build_plan(lengths, loss, 1, cfg)
+    micros = [m for mini in plan.per_rank[0] for m in mini.micros]
+    local = plan.local_samples(samples, 0)
+    mbs = build_micro_batches(local, micros, layout=layout, device=dev, sharder=_NoCp(), need_rollout_lp=True)
+    for mb, m in zip(mbs, micros):
+        ref = obatch.build_micro_batch(local, m.sample_idx, m.seq_len, m.doc_lens, layout=layout,
+                                       need_rollout_lp=True)
+        _assert_same(mb, ref, layout)
+
+
+@pytest.mark.parametrize("layout", ["packed", "padded"])
+def test_micros_of_only_empty_samples(dev, layout):
+    """A batch whose samples are all empty: micros of no output elements that
+    still carry their documents' advantages, lengths and cu_seqlens."""
+    from meshy_amd.batch import build_micro_batches
+    from meshy_amd.plan import PlannerConfig, build_plan
+
+    samples = [_sample(0, prompt=0, adv=1.0 + j, seed=50 + j) for j in range(3)]
+    cfg = PlannerConfig(layout=layout, mini_batch_size=3, seq_len=64, align=8, max_tokens_per_micro=64)
+    plan = build_plan([0, 0, 0], [0, 0, 0], 1, cfg)
+    micros = [m for mini in plan.per_rank[0] for m in mini.micros]
+    local = plan.local_samples(samples, 0)
+    mbs = build_micro_batches(local, micros, layout=layout, device=dev, sharder=_NoCp(), need_rollout_lp=True)
+    for mb, m in zip(mbs, micros):
+        ref = obatch.build_micro_batch(local, m.sample_idx, m.seq_len, m.doc_lens, layout=layout,
+                                       need_rollout_lp=True)
+        _assert_same(mb, ref, layout)
