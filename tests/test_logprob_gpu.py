@@ -33,7 +33,7 @@ def _check(z, y, dev, with_entropy=True, ref_dtype=torch.float32):
     assert (ent.cpu() - ref_ent).abs().max().item() <= TOL
 
 
-@pytest.mark.parametrize("V", [151936, 131072, 50, 8, 7, 1001, 4096 * 4 + 3])
+@pytest.mark.parametrize("V", [151936, 131072, 50, 8, 7, 2, 1, 1001, 4096 * 4 + 3])
 def test_matches_oracle_across_vocab_sizes(dev, V):
     z, y = _logits(2, 33, V, seed=V)
     _check(z, y, dev)
