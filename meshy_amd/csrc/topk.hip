@@ -160,6 +160,45 @@ __device__ __forceinline__ void write_top(const WaveTop& w, float m, float s, in
     }
 }
 
+// The row's last rem (< NT * GMAX) 16-byte chunks, from chunk c0, as one tile
+// of G = ceil(rem / NT) loads per thread, all in flight together.  Thread
+// tid's group g is chunk c0 + tid + g * NT; groups are offered in order of g,
+// the order of one chunk per thread per step.
+template <int NT, int G, int GMAX>
+__device__ __forceinline__ void topk_tail(const v4u* row4, int64_t c0, int64_t rem, int tid, int wave0, int k,
+                                          WaveTop& w, float& m, float& s, float& t) {
+    if constexpr (G <= GMAX) {
+        if (rem > static_cast<int64_t>(G) * NT) {
+            topk_tail<NT, G + 1, GMAX>(row4, c0, rem, tid, wave0, k, w, m, s, t);
+            return;
+        }
+        v4u v[G];
+        bool ok[G];
+        load_tail<NT, G>(row4 + c0, rem, tid, v, ok);
+        float z[G * 8];
+        unpack(v, z);
+        float cm[G];  // per-group maxima, read only where ok
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            cm[g] = z[8 * g];
+#pragma unroll
+            for (int j = 1; j < 8; ++j) cm[g] = fmaxf(cm[g], z[8 * g + j]);
+        }
+        accumulate_masked<false>(z, ok, m, s, t);  // leaves the present groups' z as loaded
+#pragma unroll
+        for (int g = 0; g < G; ++g) {
+            if (__ballot(ok[g] && cm[g] >= w.tv)) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    top_offer(w, ok[g] ? z[8 * g + j] : __builtin_nanf(""), k, [&](int l) {
+                        return static_cast<int32_t>(8 * (c0 + static_cast<int64_t>(g) * NT + wave0 + l) + j);
+                    });
+                }
+            }
+        }
+    }
+}
+
 template <int NT, int U>
 __global__ __launch_bounds__(NT) void k_topk_vec(const uint16_t* __restrict__ logits, int64_t T, int64_t V,
                                                  int64_t stride_b, int64_t stride_t, int k,
@@ -212,24 +251,9 @@ __global__ __launch_bounds__(NT) void k_topk_vec(const uint16_t* __restrict__ lo
             }
         }
     }
-    // Remaining 16-byte chunks: wave-uniform loop, absent chunks are NaN.
-    for (int64_t c0 = n_full * kTile; c0 < n8; c0 += NT) {
-        const int64_t c = c0 + tid;
-        const bool ok = c < n8;
-        float z[8];
-        if (ok) {
-            v4u v1[1] = {__builtin_nontemporal_load(row4 + c)};
-            unpack(v1, z);
-            accumulate<false>(z, m, s, t);
-        } else {
-#pragma unroll
-            for (int j = 0; j < 8; ++j) z[j] = __builtin_nanf("");
-        }
-#pragma unroll
-        for (int j = 0; j < 8; ++j) {
-            top_offer(w, z[j], k, [&](int l) { return static_cast<int32_t>(8 * (c0 + wave0 + l) + j); });
-        }
-    }
+    // Remaining 16-byte chunks: one predicated tile.
+    const int64_t rem = n8 - n_full * kTile;
+    if (rem > 0) topk_tail<NT, 1, U>(row4, n_full * kTile, rem, tid, wave0, k, w, m, s, t);
     // Tail elements when V is not a multiple of 8 (fewer than 8 < NT).
     if (V & 7) {
         const int64_t e = (n8 << 3) + tid;
