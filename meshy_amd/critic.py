@@ -272,7 +272,7 @@ def critic_diagnostics(values: torch.Tensor, returns: torch.Tensor, mask: torch.
 
 def diagnostics_from_states(states: list[AccumulatorState], *, correct_threshold: float = 0.5,
                             device: torch.device | str | None = None) -> CriticDiagnostics:
-    """Merge per-rank partials into the verdict ``critic_diagnostics`` gives
+    """Merge per-rank partials into the gauges ``critic_diagnostics`` gives
     (metrics.py:278-328): the token gauges from the five sums, the per-prompt
     gauges from the rows (any order, any rank) on the device."""
     n = sum(s.n_tokens for s in states)
