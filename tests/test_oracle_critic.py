@@ -242,3 +242,23 @@ def test_rollout_group_columns_feed_the_pack_buffers():
     assert torch.equal(a.view("tokens").long(), b.view("tokens"))
     for name in ("mask", "logprobs", "rewards", "group_off", "s_off"):
         assert torch.equal(a.view(name), b.view(name)), name
+
+
+def test_weight_version_roundtrips_as_int64():
+    """test_tq_grpo_pipeline.py:74-81: the version column stays int64 through
+    the columns and back, for every sample of the batch."""
+    from meshy_amd import wire
+
+    samples = [wire.sample_to_tensordict(NS(tokens=[1, 2, 3][: i + 1], logprobs=[-0.5] * (i + 1),
+                                            masks=[1] * (i + 1), reward=float(i % 2), advantage=0.5), 41)
+               for i in range(3)]
+    cols = wire.samples_to_columns(samples, wire.GRPO_TRAINER_FIELDS)
+    assert cols["weight_version"].dtype == torch.int64
+    back = wire.columns_to_samples(cols, wire.GRPO_TRAINER_FIELDS)
+    assert len(back) == 3
+    for s in back:
+        assert s["weight_version"].dtype == torch.int64 and int(s["weight_version"]) == 41
+    # the one-pass group conversion gives the same column
+    grp = wire.rollout_group_to_columns([NS(tokens=[1, 2], logprobs=[-0.5, -0.5], masks=[1, 1], reward=1.0,
+                                            advantage=0.5)] * 2, 41, wire.GRPO_TRAINER_FIELDS)
+    assert grp["weight_version"].dtype == torch.int64 and grp["weight_version"].reshape(-1).tolist() == [41, 41]
