@@ -422,6 +422,24 @@ def test_topk_random_sweep(dev, seed):
     assert (lps.cpu() - rlps).abs().max().item() <= TOL
 
 
+# Vocabularies whose chunks of 8 left after the full tiles (2048 chunks per
+# tile for K <= 16, 1024 above) make the row's last tile 4 to 8 loads per
+# thread deep, with and without full tiles before it.
+@pytest.mark.parametrize("V,k", [(24384, 8), (8800, 5), (43968, 16), (13600, 1), (32760, 8), (16192, 40)])
+def test_topk_deep_row_tails(dev, V, k):
+    from meshy_amd import topk
+
+    g = torch.Generator().manual_seed(V)
+    z = torch.randn(1, 4, V, generator=g) * 3
+    z[0, 1] = torch.round(z[0, 1])  # many ties, broken by index
+    z[0, 2, -7:] = z[0, 2].max() + 1  # the row's best values in its last chunk
+    z = z.to(torch.bfloat16)
+    ids, lps = topk.teacher_topk(z.to(dev), k)
+    rids, rlps = otopk.teacher_topk(z, k)
+    assert torch.equal(ids.cpu(), rids), (V, k)
+    assert (lps.cpu() - rlps).abs().max().item() <= TOL
+
+
 @pytest.mark.parametrize("seed", range(12))
 def test_gather_random_sweep(dev, seed):
     from meshy_amd import topk
