@@ -39,6 +39,16 @@ def test_matches_oracle_across_vocab_sizes(dev, V):
     _check(z, y, dev)
 
 
+# Vocabularies whose chunks of 8 left after the full 2048-chunk tiles make
+# the row's last tile 4 to 8 loads per thread deep (with and without full
+# tiles before it); the last row holds its largest logits in the tail.
+@pytest.mark.parametrize("V", [24384, 8800, 43968, 13600, 32760])
+def test_matches_oracle_with_deep_row_tails(dev, V):
+    z, y = _logits(2, 5, V, seed=V)
+    z[1, 4, -9:] = 40.0  # far above the row's running max: the tail raises it
+    _check(z, y, dev)
+
+
 def test_strided_chunk_view(dev):
     # logits[:, s:e, :] views as the reference's chunk loop makes them.
     z, y = _logits(2, 40, 1024, seed=3)
