@@ -18,10 +18,13 @@
 // row's top values and offers become rare.  The waves' lists are merged by
 // wave 0.
 //
-// Order: larger value first, equal values by smaller index (a stable sort of
-// the row in descending order).  NaN logits are never selected.  Every list
-// update runs with all 64 lanes active: loops are wave-uniform and absent
-// elements carry NaN.
+// Order: torch.sort(descending=True, stable=True)'s, which torch.topk
+// follows: NaN ranks above every number (+inf included), larger values before
+// smaller, and equal values (NaNs among themselves, -0 and +0 alike) by
+// smaller index.  A wavefront that has met NaN or +inf (its running sum turns
+// NaN) checks its chunks for NaN explicitly from then on, since a chunk's
+// fmaxf maximum skips NaN.  Every list update runs with all 64 lanes active:
+// loops are wave-uniform and absent elements are masked by a flag.
 #include <algorithm>
 
 #include "rowstream.h"
@@ -39,9 +42,25 @@ constexpr int kSmallK = 16;
 constexpr int kMaxTopK = kWave;
 constexpr int32_t kNoIndex = INT32_MAX;
 
-// (a, ia) ranks before (b, ib).
+// (a, ia) ranks before (b, ib): NaN first, then by value descending, ties
+// (NaN with NaN included) by index ascending.
 __device__ __forceinline__ bool ranks_before(float a, int32_t ia, float b, int32_t ib) {
+    const bool na = isnan(a), nb = isnan(b);
+    if (na || nb) return na && (!nb || ia < ib);
     return a > b || (a == b && ia < ib);
+}
+
+// A candidate that may rank before the threshold value tv: NaN always may, a
+// number when it reaches tv.  One unordered compare: with tv NaN it also
+// passes numbers, which ranks_before then rejects.
+__device__ __forceinline__ bool may_enter(float z, float tv) { return !(z < tv); }
+
+// Whether any of the 8 elements of a 16-byte chunk is NaN.
+__device__ __forceinline__ bool chunk_has_nan(const float* z) {
+    bool nan = false;
+#pragma unroll
+    for (int j = 0; j < 8; ++j) nan |= isnan(z[j]);
+    return nan;
 }
 
 __device__ __forceinline__ float read_lane(float x, int l) {
@@ -106,10 +125,10 @@ __device__ __forceinline__ void top_insert(WaveTop& w, float cv, int32_t ci, int
     refresh_threshold(w, k);
 }
 
-// Offers one element per lane (z, NaN when absent); col(l) is lane l's column.
+// Offers one element per lane (z, where ok); col(l) is lane l's column.
 template <class ColF>
-__device__ __forceinline__ void top_offer(WaveTop& w, float z, int k, ColF col) {
-    uint64_t b = __ballot(z >= w.tv);
+__device__ __forceinline__ void top_offer(WaveTop& w, float z, bool ok, int k, ColF col) {
+    uint64_t b = __ballot(ok && may_enter(z, w.tv));
     while (b) {
         const int l = __builtin_ctzll(b);
         b &= b - 1;
@@ -148,9 +167,11 @@ __device__ __forceinline__ void write_top(const WaveTop& w, float m, float s, in
                                           int64_t* __restrict__ ids, float* __restrict__ lps,
                                           float* __restrict__ lse_out) {
     if (threadIdx.x >= kWave) return;
-    // torch.logsumexp of a row whose max is +inf is +inf (its candidates' log-probs
-    // are then NaN for the +inf logit and -inf for finite ones); s is NaN there.
-    const float lse0 = (m == __builtin_inff()) ? m : fmaf(__log2f(s), kLn2, m);
+    // torch.logsumexp: NaN for a row holding NaN, whose top entry is then NaN;
+    // otherwise +inf for a row whose max is +inf (its candidates' log-probs are
+    // then NaN for the +inf logit and -inf for finite ones), where s is NaN.
+    const float top = read_lane(w.v, 0);
+    const float lse0 = isnan(top) ? top : (m == __builtin_inff()) ? m : fmaf(__log2f(s), kLn2, m);
     const float lse = read_lane(lse0, 0);
     const int lane = threadIdx.x;
     if (lane == 0 && lse_out) lse_out[r] = lse;
@@ -178,19 +199,21 @@ __device__ __forceinline__ void topk_tail(const v4u* row4, int64_t c0, int64_t r
         float z[G * 8];
         unpack(v, z);
         float cm[G];  // per-group maxima, read only where ok
+        bool cn[G];   // per-group NaN flags
 #pragma unroll
         for (int g = 0; g < G; ++g) {
             cm[g] = z[8 * g];
 #pragma unroll
             for (int j = 1; j < 8; ++j) cm[g] = fmaxf(cm[g], z[8 * g + j]);
+            cn[g] = chunk_has_nan(z + 8 * g);
         }
         accumulate_masked<false>(z, ok, m, s, t);  // leaves the present groups' z as loaded
 #pragma unroll
         for (int g = 0; g < G; ++g) {
-            if (__ballot(ok[g] && cm[g] >= w.tv)) {
+            if (__ballot(ok[g] && (cn[g] || cm[g] >= w.tv))) {
 #pragma unroll
                 for (int j = 0; j < 8; ++j) {
-                    top_offer(w, ok[g] ? z[8 * g + j] : __builtin_nanf(""), k, [&](int l) {
+                    top_offer(w, z[8 * g + j], ok[g], k, [&](int l) {
                         return static_cast<int32_t>(8 * (c0 + static_cast<int64_t>(g) * NT + wave0 + l) + j);
                     });
                 }
@@ -243,10 +266,28 @@ __global__ __launch_bounds__(NT) void k_topk_vec(const uint16_t* __restrict__ lo
                 if (__ballot(cm[u] >= w.tv)) {
 #pragma unroll
                     for (int j = 0; j < 8; ++j) {
-                        top_offer(w, z[8 * u + j], k, [&](int l) {
+                        top_offer(w, z[8 * u + j], true, k, [&](int l) {
                             return static_cast<int32_t>(8 * (c0 + u * NT + wave0 + l) + j);
                         });
                     }
+                }
+            }
+        }
+    }
+    // A lane's running sum is NaN once it has met NaN or +inf.  The chunk
+    // maxima above skip NaN, so such a wavefront rebuilds its list from the
+    // full tiles with every chunk checked for NaN (rows of ordinary logits
+    // never take this).
+    if (__ballot(isnan(s))) {
+        w = WaveTop();
+        for (int64_t c = tid; c < n_full * kTile; c += NT) {
+            const v4u v1[1] = {row4[c]};
+            float z1[8];
+            unpack(v1, z1);
+            if (__ballot(chunk_has_nan(z1) || tile_max(z1) >= w.tv)) {
+#pragma unroll
+                for (int j = 0; j < 8; ++j) {
+                    top_offer(w, z1[j], true, k, [&](int l) { return static_cast<int32_t>(8 * (c - tid + wave0 + l) + j); });
                 }
             }
         }
@@ -258,9 +299,9 @@ __global__ __launch_bounds__(NT) void k_topk_vec(const uint16_t* __restrict__ lo
     if (V & 7) {
         const int64_t e = (n8 << 3) + tid;
         const bool ok = e < V;
-        const float z = ok ? bf16_to_f32(row[e]) : __builtin_nanf("");
+        const float z = ok ? bf16_to_f32(row[e]) : 0.f;
         accumulate_one(z, ok, m, s, t);
-        top_offer(w, z, k, [&](int l) { return static_cast<int32_t>((n8 << 3) + wave0 + l); });
+        top_offer(w, z, ok, k, [&](int l) { return static_cast<int32_t>((n8 << 3) + wave0 + l); });
     }
     merge_waves(w, k);
     block_merge<NT>(m, s, t);
@@ -281,16 +322,17 @@ __global__ __launch_bounds__(NT) void k_topk_any(const uint16_t* __restrict__ lo
     WaveTop w;
     for (int64_t e0 = 0; e0 < V; e0 += 8 * NT) {
         float z[8];
+        bool ok[8];
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
             const int64_t e = e0 + u * NT + tid;
-            const bool ok = e < V;
-            z[u] = ok ? bf16_to_f32(row[e]) : __builtin_nanf("");
-            accumulate_one(z[u], ok, m, s, t);
+            ok[u] = e < V;
+            z[u] = ok[u] ? bf16_to_f32(row[e]) : 0.f;
+            accumulate_one(z[u], ok[u], m, s, t);
         }
 #pragma unroll
         for (int u = 0; u < 8; ++u) {
-            top_offer(w, z[u], k, [&](int l) { return static_cast<int32_t>(e0 + u * NT + wave0 + l); });
+            top_offer(w, z[u], ok[u], k, [&](int l) { return static_cast<int32_t>(e0 + u * NT + wave0 + l); });
         }
     }
     merge_waves(w, k);

@@ -29,7 +29,8 @@ def _dense(logits: torch.Tensor) -> torch.Tensor:
 @torch.no_grad()
 def teacher_topk(logits: torch.Tensor, k: int, *, chunk: int = 1024) -> tuple[torch.Tensor, torch.Tensor]:
     """Top-K ids and their log-probs of ``logits`` ``[rows, S, V]`` -> ``[rows, S, K]``
-    (topk_loss.py:20-32).  Ties rank by ascending vocabulary index."""
+    (topk_loss.py:20-32).  NaN ranks above +inf and ties (NaNs among themselves) by ascending
+    vocabulary index, as a stable descending sort orders them."""
     logits, _ = _prep(_dense(logits), None)
     rows, S, V = logits.shape
     if not 1 <= int(k) <= V:

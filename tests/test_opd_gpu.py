@@ -5,7 +5,6 @@ Bars: Top-K ids bit-exact (ties by ascending index), teacher columns bit-exact,
 sums), bf16 gradients within their rounding (4e-3 x |g|), fp32 gradients 1e-6.
 """
 
-import math
 from types import SimpleNamespace as NS
 
 import pytest
@@ -56,25 +55,80 @@ def test_topk_many_ties_and_strided_view(dev):
     assert (lps.cpu() - tv).abs().max().item() <= TOL
 
 
-def test_topk_nan_and_inf(dev):
-    """NaN logits are never selected: a deliberate deviation from torch.topk,
-    which ranks NaN above +inf (topk([1, nan, 3, 2], 2) gives indices [1, 2]).
-    The NaN row's log-probs are NaN either way, so that row is asserted on the
-    kernel's own rule and left out of the oracle comparison."""
+def _special_rows(V, seed):
+    """Rows of [12, V] fp32 logits holding NaN, +inf and -inf in the places a
+    streaming selection treats differently: the first tile (which sets the
+    floor), the middle, the row's last chunks and elements, more NaNs than any
+    K, and rows made only of them."""
+    g = torch.Generator().manual_seed(seed)
+    z = torch.randn(12, V, generator=g) * 2.0
+    nan, inf = float("nan"), float("inf")
+    pick = lambda n: torch.randperm(V, generator=g)[:n]
+    z[0, pick(1)] = nan                                   # one NaN anywhere
+    z[1, [3, V // 2, V - 1]] = nan                        # first tile, middle, last element
+    z[2, pick(min(100, V // 2))] = nan                    # more NaNs than K: ties by index
+    z[3, [5, V - 2]] = inf
+    z[3, V // 3] = nan                                    # NaN ranks above +inf
+    z[4, :] = -inf
+    z[4, [1, V // 4, V - 3]] = torch.tensor([0.5, -1.0, 0.5])
+    z[4, V // 2] = nan                                    # -inf row with NaN and ties
+    z[5, :] = nan                                         # all NaN
+    z[6, 0:8] = nan                                       # a whole 16-byte chunk of NaN
+    z[6, V - 5] = inf
+    z[7, [V - 1, V - 2]] = inf                            # +inf only, in the row's tail
+    z[8, :] = -inf                                        # all -inf
+    z[9, :] = -inf
+    z[9, V - 1] = nan                                     # NaN as the very last element
+    z[10, pick(7)] = -inf                                 # a few -inf, no NaN
+    # row 11 stays an ordinary row
+    return z
+
+
+def _assert_topk_like_oracle(ids, lps, rids, rlps, what):
+    assert torch.equal(ids, rids), f"{what}: ids differ"
+    assert torch.equal(torch.isnan(lps), torch.isnan(rlps)), f"{what}: NaN pattern differs"
+    inf = torch.isinf(rlps)
+    assert torch.equal(lps[inf], rlps[inf]), f"{what}: infinities differ"
+    fin = torch.isfinite(rlps)
+    if fin.any():
+        assert (lps[fin] - rlps[fin]).abs().max().item() <= TOL, what
+
+
+@pytest.mark.parametrize("V", [500, 151936])
+@pytest.mark.parametrize("k", [1, 8, 64])
+def test_topk_nan_and_inf_rows_match_oracle(dev, V, k):
+    """torch.topk's order on rows with NaN and infinities: NaN ranks above
+    +inf, NaNs among themselves by index; the log-probs follow
+    torch.logsumexp (NaN for a row holding NaN, +inf for a row whose max is
+    +inf).  Aligned rows (vector path) and a misaligned view (generic path)."""
     from meshy_amd import topk
 
-    z = _bf16_logits(1, 3, 500, seed=9).float()
-    z[0, 0, 7] = float("nan")      # never selected
-    z[0, 1, :] = float("-inf")
-    z[0, 1, 10] = 1.0              # one finite logit, the rest -inf: ties by index
-    z = z.to(torch.bfloat16)
-    ids, lps = topk.teacher_topk(z.to(dev), 4)
-    ids, lps = ids.cpu(), lps.cpu()
-    assert 7 not in ids[0, 0].tolist()
-    assert ids[0, 1].tolist() == [10, 0, 1, 2]
-    assert lps[0, 1, 0].item() == 0.0 and math.isinf(lps[0, 1, 1].item())
-    rids, rlps = otopk.teacher_topk(z[:, 2:], 4)
-    assert torch.equal(ids[:, 2:], rids)
+    z = _special_rows(V, seed=V + k).to(torch.bfloat16).view(1, 12, V)
+    ids, lps = topk.teacher_topk(z.to(dev), k)
+    rids, rlps = otopk.teacher_topk(z, k)
+    _assert_topk_like_oracle(ids.cpu(), lps.cpu(), rids, rlps, f"vector V={V} k={k}")
+    # Known answers of the rules themselves.
+    if k == 8:
+        assert rids[0, 2, :8].tolist() == sorted(torch.nonzero(torch.isnan(z[0, 2].float())).flatten().tolist())[:8]
+        assert rids[0, 3, :3].tolist() == [V // 3, 5, V - 2]
+        assert rids[0, 5].tolist() == list(range(8))
+    # Misaligned rows: one element in, so the rows start 2 bytes off 16.
+    zp = torch.cat([torch.zeros(1, 12, 1, dtype=torch.bfloat16), z], dim=-1)
+    view = zp.to(dev)[:, :, 1:]
+    ids2, lps2 = topk.teacher_topk(view, k)
+    _assert_topk_like_oracle(ids2.cpu(), lps2.cpu(), rids, rlps, f"generic V={V} k={k}")
+
+
+def test_topk_matches_torch_topk_on_nan(dev):
+    """The reference's own call, z.topk(k), on the row of the known answer
+    [1, nan, 3, 2, nan, inf]: indices [1, 4, 5, 2]."""
+    from meshy_amd import topk
+
+    z = torch.tensor([[[1.0, float("nan"), 3.0, 2.0, float("nan"), float("inf"), 0.0, -1.0]]])
+    ids, lps = topk.teacher_topk(z.to(torch.bfloat16).to(dev), 4)
+    assert ids.cpu().flatten().tolist() == [1, 4, 5, 2]
+    assert torch.equal(ids.cpu(), z.topk(4, dim=-1).indices)
+    assert torch.isnan(lps.cpu()).all()  # logsumexp of a row holding NaN is NaN
 
 
 def test_topk_row_with_plus_inf_matches_logsumexp(dev):
