@@ -624,8 +624,8 @@ def bench_long_context(steps, warmup, no_cpu):
     plan = build_plan(lengths, lengths, 1, cfg)
     T = max(m.seq_len for mini in plan.per_rank[0] for m in mini.micros)
     V = 131072
-    # logits from the counter-based generator (std 2), so the CPU leg
-    # regenerates its rows on the host instead of copying them
+    # logits N(0, 2^2) from the counter-based Box-Muller generator, so the
+    # CPU leg regenerates its rows on the host instead of copying them
     logits = workloads.synth_logits(T, V, seed=3, scale=2.0, device=dev).unsqueeze(0)
     labels = torch.randint(0, V, (1, T), generator=torch.Generator(device=dev).manual_seed(3), device=dev)
     ms = _gpu_ms(lambda: logprob.logprobs_and_entropy(logits, labels, with_entropy=True), steps, warmup)
@@ -644,7 +644,7 @@ def bench_long_context(steps, warmup, no_cpu):
     nbytes = T * V * 2 + 16 * T
     return _entry(ms * 1e3, nbytes, cpu_ms, T=T, V=V, tokens_per_s=round(T / (ms * 1e-3)),
                   cpu_sample=f"{rows} rows regenerated on the host, scaled to T",
-                  data="counter-based synthetic logits, std 2 (meshy_synth_bf16, seed 3)")
+                  data="logits N(0, 2^2) bf16 from a counter-based Box-Muller generator (meshy_synth_bf16, seed 3)")
 
 
 # ---------------------------------------------------------------- GAE over 1024 docs

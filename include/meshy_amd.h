@@ -659,15 +659,18 @@ int meshy_stream_read(const void* src, int64_t rows, int64_t row_bytes, uint32_t
                       hipStream_t stream);
 
 /* ------------------------------------------------------------------------
- * Counter-based synthetic bf16 logits (device and host, the same bits).
- * No reference counterpart: the synthetic inputs of the measured workloads,
- * regenerated on the host for the rows a parity check reads, instead of
- * copying a tensor of up to 34 GB.  Element k = row * cols + col is
- *   h = mix(mix(seed) ^ k), mix = splitmix64's finaliser;
- *   s = the sum of h's four 16-bit fields (Irwin-Hall of four uniforms);
- *   x = (float(s) - 131070) * float(scale * sqrt(3) / 65536);
- *   bf16(x) rounded to nearest even
- * (mean 0, standard deviation scale, bounded at +-2 sqrt(3) scale).
+ * Counter-based synthetic bf16 logits drawn from N(0, scale^2) (device and
+ * host, the same bits).  No reference counterpart: the synthetic inputs of
+ * the measured workloads, regenerated on the host for the rows a parity
+ * check reads, instead of copying a tensor of up to 34 GB.  Elements 2p and
+ * 2p + 1 (element k = row * cols + col) are the Box-Muller pair of
+ *   h = mix(mix(seed) ^ p), mix = splitmix64's finaliser:
+ *   u1 = (lo32(h) + 1) / 2^32, theta = 2 pi hi32(h) / 2^32,
+ *   scale * sqrt(-2 ln u1) * (cos theta, sin theta),
+ * each rounded to bf16 (nearest even).  The fp32 log, square root, sine and
+ * cosine are the library's own, built from correctly rounded adds,
+ * multiplies and fused multiply-adds only, so both sides give the same bits;
+ * |value| <= 6.66 scale.
  * meshy_synth_bf16 fills out[row * row_stride + col] for a [rows, cols]
  * block on the stream; meshy_synth_bf16_rows_host writes rows row_ids[i] of
  * the same block to out[i * cols ...] on host threads.

@@ -50,10 +50,15 @@ def hipcc() -> str:
     return path
 
 
+# Per-source flags.  The synthetic-logit generator must give the same bits on
+# the host and the device, so no multiply and add may be fused implicitly.
+EXTRA_FLAGS = {"synth.hip": ["-ffp-contract=off"]}
+
+
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
     lang = ["-x", "hip"] if src.endswith(".hip") else []
-    cmd = [hipcc(), *COMMON_FLAGS, *lang, "-c", os.path.join(CSRC, src), "-o", obj]
+    cmd = [hipcc(), *COMMON_FLAGS, *EXTRA_FLAGS.get(src, []), *lang, "-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

@@ -9,9 +9,10 @@ generator takes a seed and is reproducible on any host.
     ppo_512_docs             PPO loss: 512 docs, response lognormal(4000, 0.8) clipped [16, 8192]
     long_context_16_lengths  long context: 16 sequences U{8192..131072}, budget 131072
     gae_1024_docs            GAE: 1024 docs, response lognormal(6000, 0.8) clipped [32, 32768]
-    synth_logits             bf16 logits from the counter-based generator (meshy_synth_bf16),
-                             filled on the device; synth_logit_rows regenerates any of their
-                             rows on the host, bit for bit
+    synth_logits             bf16 logits N(0, scale^2) from the counter-based Box-Muller
+                             generator (meshy_synth_bf16), filled on the device;
+                             synth_logit_rows regenerates any of their rows on the host, bit
+                             for bit
 """
 
 from __future__ import annotations
@@ -132,8 +133,8 @@ def gae_1024_docs(seed: int = 4):
 
 
 def synth_logits(rows: int, cols: int, seed: int, scale: float = 2.0, device=None):
-    """A [rows, cols] bf16 tensor of counter-based synthetic logits (mean 0,
-    standard deviation ``scale``), filled on the HIP device."""
+    """A [rows, cols] bf16 tensor of counter-based synthetic logits drawn from
+    N(0, scale^2) (a Box-Muller pair per hash), filled on the HIP device."""
     import torch
 
     from . import _lib

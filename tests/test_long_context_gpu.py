@@ -7,9 +7,9 @@ and its backward over the largest micro's bf16 logits [T, 131072].
   itself pinned by the golden plans);
 * logp and entropy (trainer.py:414-449) on 8192 seeded rows of every micro
   (all rows of a shorter one), labels being that micro's packed labels, within
-  1e-3 of the oracle.  The logits [T, 131072] come from the counter-based
-  generator on the device, and the host regenerates the checked rows instead
-  of copying them;
+  1e-3 of the oracle.  The logits [T, 131072] are N(0, 2^2) from the
+  counter-based Box-Muller generator on the device, and the host regenerates
+  the checked rows instead of copying them;
 * the logits gradient of the whole largest micro (trainer.py:504-517) on 1024
   seeded rows within the bf16 rounding of the oracle's fp32 autograd gradient.
 """
@@ -76,7 +76,7 @@ N_MICROS = 7  # the plan of the 16 seeded lengths (asserted below)
 
 @pytest.mark.parametrize("j", range(N_MICROS))
 def test_logprob_on_every_long_micro(dev, long_micros, j):
-    """Logits of micro j come from the counter-based generator (seed 100 + j)
+    """Logits of micro j are N(0, 2^2) from the counter-based generator (seed 100 + j)
     on the device; the host regenerates 8192 seeded rows (all rows of a shorter
     micro) bit for bit and the oracle checks logp and entropy there."""
     from meshy_amd import logprob, workloads
