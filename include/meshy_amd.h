@@ -426,8 +426,9 @@ typedef struct meshy_ppo_args {
 /* Segment structure of a doc_ids tensor whose flattened values are
  * non-decreasing (both batch layouts, batch.py:123, 150-162):
  * seg_offsets[d] = number of tokens with id < d, for d in [0, n_slots].
- * unsorted (nullable, device int32) is set to 1 when some doc_ids[i] >
- * doc_ids[i+1]; the caller clears it beforehand. */
+ * unsorted (nullable, device int32) gets bit 1 when some doc_ids[i] >
+ * doc_ids[i+1] and bit 2 when some id lies outside [0, n_slots - 1] (where
+ * the reference's index_add_ raises); the caller clears it beforehand. */
 int meshy_segment_offsets(const int64_t* doc_ids, int64_t n_tokens, int64_t n_slots,
                           int64_t* seg_offsets, int32_t* unsorted, hipStream_t stream);
 

@@ -671,7 +671,11 @@ __global__ __launch_bounds__(kThreads) void k_segment_offsets(const int64_t* __r
         if (i > n) break;
         const int64_t prev = v[k];
         const int64_t cur = v[k + 1];
-        if (unsorted && i > 0 && i < n && prev > cur) unsorted[0] = 1;
+        if (unsorted && i < n) {
+            // Rare error paths: an atomic keeps both reasons when both occur.
+            if (i > 0 && prev > cur) atomicOr(unsorted, 1);
+            if (cur < 0 || cur >= n_slots) atomicOr(unsorted, 2);
+        }
         const int64_t lo = max<int64_t>(prev + 1, 0);
         const int64_t hi = min<int64_t>(cur, n_slots - 1);
         for (int64_t d = lo; d <= hi; ++d) off[d] = i;

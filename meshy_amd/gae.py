@@ -19,15 +19,19 @@ import numpy as np
 import torch
 
 from . import _lib
-from .loss import checked_segment_offsets
+from .loss import DocIdRangeError, checked_segment_offsets
 
 
 def _doc_offsets(doc_ids: torch.Tensor, n_docs: int) -> torch.Tensor | None:
     """The segment offsets of ``doc_ids`` over its ``n_docs + 1`` slots when its
     flattened values are non-decreasing (checked once per tensor version, one
-    device sync), else None: the kernels then count lengths with atomics."""
+    device sync), else None: the kernels then count lengths with atomics.  An
+    id outside [0, n_docs] raises, as the reference's indexing does
+    (gae.py:266-276)."""
     try:
         return checked_segment_offsets(doc_ids, n_docs + 1)
+    except DocIdRangeError:
+        raise
     except ValueError:
         return None
 

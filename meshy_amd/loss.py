@@ -52,19 +52,26 @@ def batch_segment_offsets(mb: Any) -> torch.Tensor:
     return off
 
 
+class DocIdRangeError(ValueError):
+    """A doc id outside the document slots and the padding slot (the
+    reference's ``index_add_`` raises there)."""
+
+
 # Segment offsets of recently seen doc_ids tensors whose order was checked,
-# None for a tensor found out of order.  Entries hold a weak reference to
+# or the ValueError a rejected tensor raised.  Entries hold a weak reference to
 # their tensor: a hit needs the same live object (its id and data pointer
 # may be reused once it is freed), and the cache never keeps a batch alive.
-_CHECKED: dict[tuple, tuple[weakref.ref, torch.Tensor | None]] = {}
+_CHECKED: dict[tuple, tuple[weakref.ref, torch.Tensor | ValueError]] = {}
 _CHECKED_MAX = 16
 
 
 def checked_segment_offsets(doc_ids: torch.Tensor, n_slots: int) -> torch.Tensor:
     """``segment_offsets`` of ``doc_ids`` after checking, once per tensor and
-    version (one device sync), that its flattened values are non-decreasing;
-    raises ValueError otherwise.  The kernels that take these offsets rely on
-    that order, which both batch layouts have (batch.py:123, 150-162)."""
+    version (one device sync), that its flattened values are non-decreasing
+    and lie in ``[0, n_slots - 1]``; raises ValueError otherwise (the
+    reference's ``index_add_`` raises on an id out of range).  The kernels that
+    take these offsets rely on that order, which both batch layouts have
+    (batch.py:123, 150-162), and visit only tokens inside the slots' ranges."""
     key = (id(doc_ids), doc_ids._version, doc_ids.data_ptr(), int(n_slots))
     hit = _CHECKED.get(key)
     if hit is not None and hit[0]() is doc_ids:
@@ -72,14 +79,14 @@ def checked_segment_offsets(doc_ids: torch.Tensor, n_slots: int) -> torch.Tensor
     else:
         try:
             off = segment_offsets(doc_ids, n_slots, check_sorted=True)
-        except ValueError:
-            off = None
+        except ValueError as e:
+            off = e
         _CHECKED.pop(key, None)
         if len(_CHECKED) >= _CHECKED_MAX:
             _CHECKED.pop(next(iter(_CHECKED)))
         _CHECKED[key] = (weakref.ref(doc_ids), off)
-    if off is None:
-        raise ValueError("doc_ids must be non-decreasing over the flattened micro-batch")
+    if isinstance(off, ValueError):
+        raise type(off)(*off.args)
     return off
 
 
@@ -99,8 +106,12 @@ def segment_offsets(doc_ids: torch.Tensor, n_slots: int, check_sorted: bool = Fa
     rc = _lib.load().meshy_segment_offsets(ids.data_ptr(), ids.numel(), n_slots, off.data_ptr(),
                                            _lib.ptr(flag), _lib.stream_of(ids.device))
     _lib.check(rc, "meshy_segment_offsets")
-    if check_sorted and int(flag.item()):
-        raise ValueError("doc_ids must be non-decreasing over the flattened micro-batch")
+    if check_sorted:
+        bad = int(flag.item())
+        if bad & 2:
+            raise DocIdRangeError(f"doc_ids must lie in [0, {n_slots - 1}] (the document slots and the padding slot)")
+        if bad & 1:
+            raise ValueError("doc_ids must be non-decreasing over the flattened micro-batch")
     return off
 
 
@@ -300,5 +311,5 @@ def reduce_mini_metrics(self: Any, sums: dict[str, torch.Tensor]) -> dict[str, f
     return out
 
 
-__all__ = ["batch_segment_offsets", "checked_segment_offsets", "ppo_clip_loss", "reduce_mini_metrics",
+__all__ = ["DocIdRangeError", "batch_segment_offsets", "checked_segment_offsets", "ppo_clip_loss", "reduce_mini_metrics",
            "segment_offsets"]

@@ -36,6 +36,11 @@ def _call(name, *args):
     # logits, rows, T, V, sb, st, labels, lse, grad_logp, grad, ws, ws_bytes, stream
     ("meshy_logprob_bwd", (FAKE, 1, 4, 8, 32, 8, FAKE, FAKE, FAKE, None, FAKE, 4096, None), ENULL, "required"),
     ("meshy_logprob_bwd", (FAKE, 1, 4, 8, 32, 8, FAKE, FAKE, FAKE, FAKE, FAKE, 8, None), ESPACE, "workspace"),
+    # logits, rows, T, V, sb, st, labels, lse, grad_logp, grad, stream: one row past the static scratch's
+    # 262144 (refused before any HIP call)
+    ("meshy_logprob_bwd_noalloc", (FAKE, 1, 262145, 8, 262145 * 8, 8, FAKE, FAKE, FAKE, FAKE, None), ESPACE,
+     "static scratch"),
+    ("meshy_logprob_bwd_noalloc", (FAKE, 1, 4, 8, 32, 8, FAKE, FAKE, FAKE, None, None), ENULL, "required"),
     ("meshy_gather_logprobs_bwd", (FAKE, 1, 4, 8, 32, 8, FAKE, 300, FAKE, FAKE, FAKE, FAKE, 4096, None), EINVAL,
      "n_ids"),
     # logits, rows, T, V, sb, st, k, ids, logprobs, lse, stream

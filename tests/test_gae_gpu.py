@@ -300,16 +300,22 @@ def test_scan_from_offsets_equals_scan_from_ids(dev, docs_per_row, rows, S):
     assert (a.cpu() - ref_adv).abs().max().item() <= TOL
 
 
-def test_scan_from_offsets_with_ids_outside_the_slots(dev):
-    """Sorted ids that start below 0 and end past the padding slot: chunks whose
-    end ids leave [0, n_docs] read every id, so both scans still agree bit for
+def test_scan_from_offsets_with_ids_outside_the_slots(dev, monkeypatch):
+    """Sorted ids that start below 0 and end past the padding slot.  The
+    public call raises ValueError, as the reference's indexing does.  Handed
+    unchecked offsets through the C ABI, the kernels stay in bounds: chunks
+    whose end ids leave [0, n_docs] read every id, so both scans agree bit for
     bit (ids outside the slots get lambda 0, as in the per-token scan)."""
     from meshy_amd import gae
+    from meshy_amd.loss import segment_offsets
 
     rewards, values, mask, doc_ids, n_docs = _random_grid(1, 20000, 12, seed=77)
     doc_ids[0, :3000] = -1
     doc_ids[0, -2500:] = n_docs + 3
     d = [t.to(dev) for t in (rewards, values, mask, doc_ids)]
+    with pytest.raises(ValueError, match="doc_ids must lie"):
+        gae.compute_vapo_gae(d[0], d[1], d[2], d[3], n_docs)
+    monkeypatch.setattr(gae, "_doc_offsets", lambda ids, n: segment_offsets(ids, n + 1))
     for lens in (None, torch.full((n_docs,), 20.0, device=dev)):
         kw = dict(lengths=lens, gamma=0.99, alpha=1.5, epsilon=1e-6, want_adv=True, want_returns=True, want_lam=True)
         a0, r0, l0 = gae._run(*d, n_docs, offsets=True, **kw)
@@ -537,8 +543,15 @@ def test_vector_and_scalar_loads_and_renamed_ids_give_bitwise_equal_results(dev,
         assert torch.equal(a, a0) and torch.equal(r, r0)
     ref_adv, _ = ogae.compute_vapo_gae(rewards, values.float(), mask, doc_ids, n_docs, lengths=lengths, **kw)
     assert (a0.cpu() - ref_adv).abs().max().item() <= TOL
-    # Negative ids (lambda 0 there): the vector and scalar loads agree.
+    # Negative ids (lambda 0 there), given to the kernels without the range
+    # check of the public call: the vector and scalar loads agree.
+    from meshy_amd import gae
+
     neg = d[3] - 3
-    a3, r3, _ = gae_and_returns(d[0], d[1], d[2], neg, n_docs, lengths=lengths.to(dev), **kw)
-    a4, r4, _ = gae_and_returns(*u[:3], _unaligned(neg, dev), n_docs, lengths=lengths.to(dev), **kw)
+    kw2 = dict(lengths=lengths.to(dev), alpha=1.5, epsilon=1e-6, want_adv=True, want_returns=True,
+               want_lam=False, offsets=False, gamma=0.99)
+    a3, r3, _ = gae._run(d[0], d[1], d[2], neg, n_docs, **kw2)
+    a4, r4, _ = gae._run(*u[:3], _unaligned(neg, dev), n_docs, **kw2)
     assert torch.equal(a3, a4) and torch.equal(r3, r4)
+    with pytest.raises(ValueError, match="doc_ids must lie"):
+        gae_and_returns(d[0], d[1], d[2], neg, n_docs, lengths=lengths.to(dev), **kw)

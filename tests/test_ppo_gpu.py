@@ -442,6 +442,48 @@ def test_loss_rejects_doc_ids_out_of_order(dev):
     assert torch.isfinite(loss)
 
 
+@pytest.mark.parametrize("bad", [-1, 3, 7])
+def test_loss_rejects_doc_ids_out_of_range(dev, bad):
+    """Ids outside [0, n_docs] (n_docs = the padding slot) lie in no slot's
+    token range, so the tile kernels would never visit them: the order check
+    also rejects them, with ValueError, as the reference's index_add_ raises
+    (trainer.py:787-791).  Sorted or not, the range error is the one raised."""
+    from meshy_amd.loss import DocIdRangeError, ppo_clip_loss, segment_offsets
+    from meshy_amd.plan import MiniPlan
+
+    mb = _batch(dev, rows=1, S=8)
+    ids = [0, 0, 1, 1, 1, 2, 2, 2]
+    ids[0 if bad < 0 else 7] = bad
+    mb.doc_ids = torch.tensor([ids], device=dev)
+    mb.advantages = torch.tensor([1.0, -1.0], device=dev)
+    mb.n_docs = 2
+    mini = MiniPlan(micros=(), n_docs_global=2, n_tokens_global=int(mb.mask.sum()), tokens_per_rank=(8,))
+    old = -torch.ones(1, 8, device=dev)
+    new = (old + 0.05).requires_grad_()
+    for _ in range(2):  # the cached verdict raises the same error
+        with pytest.raises(DocIdRangeError, match=r"\[0, 2\]"):
+            ppo_clip_loss(_stub(), new, old, mb, mini)
+    with pytest.raises(DocIdRangeError):
+        segment_offsets(torch.tensor([2, 1, bad], device=dev), 3, check_sorted=True)
+
+
+def test_gae_rejects_doc_ids_out_of_range(dev):
+    """compute_vapo_gae indexes lambda by doc id (gae.py:266-276): an id past
+    the padding slot raises ValueError instead of falling back to the unsorted
+    path; compute_returns, which only compares ids (gae.py:77-93), accepts it."""
+    from meshy_amd import gae
+
+    rows, S = 2, 16
+    mask = torch.ones(rows, S, device=dev)
+    ids = torch.zeros(rows, S, dtype=torch.int64, device=dev)
+    ids[1] = 1
+    ids[1, -1] = 5
+    r = torch.zeros(rows, S, device=dev)
+    with pytest.raises(ValueError, match="doc_ids must lie"):
+        gae.compute_vapo_gae(r, torch.zeros(rows, S, device=dev), mask, ids, 2)
+    assert torch.isfinite(gae.compute_returns(r, mask, ids)).all()
+
+
 def test_segment_offsets_cache_follows_doc_ids(dev):
     """A batch caches its document offsets after the first loss call; replacing
     or editing doc_ids in place recomputes them."""

@@ -62,19 +62,3 @@ def test_no_alloc_matches_workspace_entry_point_on_two_calls(dev):
         assert torch.equal(a.view(torch.int16), b.view(torch.int16))
         assert torch.isfinite(a.float()).all()
         assert (a[0, 0].float() == 0).all()  # the ignored label's row
-
-
-def test_no_alloc_rejects_rows_beyond_its_scratch(dev):
-    from meshy_amd import _lib
-
-    lib = _lib.load()
-    rows = 1
-    T = 262144 + 1  # MESHY_NOALLOC_MAX_ROWS + 1: refused on the host, nothing launched
-    buf = torch.zeros(16, dtype=torch.bfloat16, device=dev)
-    out = torch.zeros(16, dtype=torch.bfloat16, device=dev)
-    ids = torch.zeros(16, dtype=torch.int64, device=dev)
-    f = torch.zeros(16, device=dev)
-    rc = lib.meshy_logprob_bwd_noalloc(buf.data_ptr(), rows, T, 8, T * 8, 8, ids.data_ptr(), f.data_ptr(),
-                                       f.data_ptr(), out.data_ptr(), _lib.stream_of(dev))
-    assert rc == -4, rc  # MESHY_ESPACE
-    assert b"static scratch" in lib.meshy_last_error()
