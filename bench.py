@@ -380,6 +380,7 @@ def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
 # ---------------------------------------------------------------- 256 GRPO samples
 
 def bench_pack(runs, no_cpu):
+    import numpy as np
     import torch
 
     from meshy_amd import workloads
@@ -401,8 +402,8 @@ def bench_pack(runs, no_cpu):
     # freeing a step's ~250 tensors is not part of packing the next one.
     drop = lambda: res.pop("r", None)  # noqa: E731
     wall = _wall_ms(full, runs, warmup=3, before=drop)
-    lite = _wall_ms(lambda: res.__setitem__("r", pack_step(ragged, cfg, dev, with_plan_objects=False)), runs,
-                    warmup=2, before=drop)
+    eager = _wall_ms(lambda: res.__setitem__("r", pack_step(ragged, cfg, dev, with_plan_objects=True)), runs,
+                     warmup=2, before=drop)
 
     fields = ("input_ids", "labels", "positions", "mask", "doc_ids", "advantages", "rollout_logprobs", "lengths",
               "attention_masks", "positive_lm_weights", "advantage_tokens")
@@ -432,7 +433,9 @@ def bench_pack(runs, no_cpu):
         # device-synchronized; each micro's Batch tensors are views made when
         # the trainer first reads them (as it builds each micro when reaching it)
         "pack_latency_us": round(wall * 1e3, 1),
-        "pack_latency_no_dataclasses_us": round(lite * 1e3, 1),
+        # the same with the Plan dataclasses built inside the call (they are
+        # otherwise built when PackResult.plan is first read)
+        "pack_latency_with_plan_dataclasses_us": round(eager * 1e3, 1),
         # the same with every field of every micro's Batch read once (all views made)
         "pack_latency_all_views_us": round(wall_views * 1e3, 1),
         "host_phases_us": {"loss_token_count": round(count_ms * 1e3, 1), "planner": round(plan_ms * 1e3, 1),
@@ -458,6 +461,24 @@ def bench_pack(runs, no_cpu):
         lambda: held.__setitem__("b", build_micro_batches(local_t, micros, layout="packed", device=dev,
                                                           need_rollout_lp=True)),
         runs, warmup=2, before=lambda: held.pop("b", None)), 1)
+    # The trainer's own call pattern: one build_micro_batch per micro as it
+    # reaches it (trainer.py:557-571), timed as the reference times it,
+    # "train/pack_batch" with a device sync (trainer.py:972).
+    from meshy_amd.batch import build_micro_batch
+
+    per_micro = []
+    for rep in range(max(3, runs // 20) + 2):
+        for m in micros:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            mb = build_micro_batch(local_t, m, layout="packed", device=dev, need_rollout_lp=True)
+            torch.cuda.synchronize()
+            if rep >= 2:  # the first two passes warm up
+                per_micro.append(time.perf_counter() - t0)
+            del mb
+    out["build_micro_batch_per_micro_us"] = {"median": round(float(np.median(per_micro)) * 1e6, 1),
+                                             "mean": round(float(np.mean(per_micro)) * 1e6, 1),
+                                             "micros": len(micros), "calls": len(per_micro)}
     # The OPD student's drop-in (opd.py:141-148): the same micros with the
     # Teacher's K = 8 int64 ids and fp32 log-probs per position.
     from meshy_amd.opd import build_topk_micro_batches
@@ -494,6 +515,19 @@ def bench_pack(runs, no_cpu):
 
         out["cpu_ms"] = round(_wall_ms(cpu, 5, gpu=False), 2)
         out["speedup_vs_cpu"] = round(out["cpu_ms"] / wall, 1)
+        # the reference's per-micro call restated on the CPU (batch.py:96-230,
+        # device = cpu, so no host-to-device copy), per micro
+        loc = [dict(s, advantage=0.5) for s in samples]
+        loc = [loc[i] for i in r.plan.local_indices[0]]
+        cpu_micro = []
+        for rep in range(3):
+            for m in micros:
+                t0 = time.perf_counter()
+                obatch.build_micro_batch(loc, m.sample_idx, m.seq_len, m.doc_lens, layout="packed",
+                                         need_rollout_lp=True)
+                if rep:
+                    cpu_micro.append(time.perf_counter() - t0)
+        out["cpu_build_micro_batch_per_micro_us"] = round(float(np.median(cpu_micro)) * 1e6, 1)
     return out, ragged, cfg
 
 
@@ -1190,6 +1224,21 @@ def bench_end_to_end(runs, no_cpu):
     return out
 
 
+# One workload leg each, for `--leg NAME` (the full run calls them in main).
+LEGS = {
+    "pack": lambda a: bench_pack(20, a.no_cpu)[0],
+    "ppo": lambda a: bench_ppo(a.steps, a.warmup, a.no_cpu),
+    "gae": lambda a: bench_gae(a.steps, a.warmup, a.no_cpu),
+    "critic": lambda a: bench_critic(a.steps, a.warmup, a.no_cpu),
+    "attach_gae": lambda a: bench_attach_gae(5, a.no_cpu),
+    "long_context": lambda a: bench_long_context(max(3, a.steps // 10), 2, a.no_cpu),
+    "pack_long_context": lambda a: bench_pack_long_context(10, a.no_cpu),
+    "rollout_metrics": lambda a: bench_rollout_metrics(10, a.no_cpu),
+    "group_plugins": lambda a: bench_group_plugins(10, a.no_cpu),
+    "end_to_end": lambda a: bench_end_to_end(5, a.no_cpu),
+}
+
+
 def main() -> int:
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -1204,6 +1253,7 @@ def main() -> int:
     ap.add_argument("--pmc-workloads", action="store_true",
                     help="for counter runs: the pack, PPO, GAE, critic and whitening legs with a few steps each, "
                          "then a 256 MiB device copy x 3 to calibrate, no JSON line")
+    ap.add_argument("--leg", choices=sorted(LEGS), help="run one workload leg and print its entry only")
     args = ap.parse_args()
     if args.gpus != 1:
         print("bench.py measures one GPU: the hot path's kernels run per GPU and no multi-GPU figure "
@@ -1220,6 +1270,9 @@ def main() -> int:
         return pmc_kernels()
     if args.pmc_workloads:
         return pmc_workloads()
+    if args.leg:
+        print(json.dumps({args.leg: LEGS[args.leg](args)}), flush=True)
+        return 0
 
     logits, labels = headline_inputs()
     bwd = None
@@ -1281,6 +1334,9 @@ def main() -> int:
     if not args.quick:
         pack, _, _ = bench_pack(20, args.no_cpu)
         result["pack_latency_us"] = pack["pack_latency_us"]
+        # the trainer's per-micro drop-in, the call the reference times as
+        # train/pack_batch (median over the 23 micros)
+        result["pack_latency_per_micro_us"] = pack["build_micro_batch_per_micro_us"]["median"]
         kernels["pack_grpo_256_samples"] = pack
         kernels.update(bench_ppo(args.steps, args.warmup, args.no_cpu))
         kernels["gae_returns_1024_docs"] = bench_gae(args.steps, args.warmup, args.no_cpu)

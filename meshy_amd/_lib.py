@@ -371,6 +371,21 @@ def pyio():
     return _PYIO
 
 
+_STAGE = None
+
+
+def stage():
+    """The CPython helper module meshy_amd._stage (built beside the library)."""
+    global _STAGE
+    if _STAGE is None:
+        try:
+            from . import _stage as mod
+        except ImportError as e:
+            raise ImportError("meshy_amd._stage is not built; run __graft_entry__.build()") from e
+        _STAGE = mod
+    return _STAGE
+
+
 def check(rc: int, what: str) -> None:
     """Raise the Python error matching a C-ABI return code."""
     if rc == 0:

@@ -20,7 +20,7 @@ import numpy as np
 import torch
 
 from . import _lib
-from .hostio import gather_heads_into, gather_into
+from .hostio import gather_into
 from .plan import Layout, MicroPlan
 
 #: Per-token advantage column (batch.py:81): already on the next-token grid,
@@ -83,6 +83,7 @@ class _Staging:
 
     def __init__(self) -> None:
         self.buf: torch.Tensor | None = None
+        self.np: np.ndarray | None = None  # the same pinned memory, as numpy
         self.event = None
 
     def get(self, nbytes: int) -> torch.Tensor:
@@ -90,6 +91,7 @@ class _Staging:
             self.event.synchronize()
         if self.buf is None or self.buf.numel() < nbytes:
             self.buf = torch.empty(max(nbytes, 1 << 20), dtype=torch.uint8, pin_memory=True)
+            self.np = self.buf.numpy()
         return self.buf
 
     def mark(self, stream) -> None:
@@ -120,27 +122,85 @@ class _Layout:
         """Address of a region inside a buffer that starts at ``base``."""
         return base + self.regions[name][0]
 
-
-def _scalar_of(v, default: float) -> float:
-    if v is None:
-        return default
-    if isinstance(v, torch.Tensor):
-        return float(v.reshape(-1)[0].item()) if v.numel() else default
-    return float(v)
+    def np_view(self, buf: np.ndarray, name: str) -> np.ndarray:
+        """The region of a uint8 numpy buffer as a numpy array of its dtype."""
+        lo, hi, dtype = self.regions[name]
+        return buf[lo:hi].view(_NP_DTYPE[dtype])
 
 
-def _scalars(samples: Sequence[Any], idxs: Sequence[int], key: str, default: float = 0.0) -> np.ndarray:
-    """``_scalar`` of each listed sample (fp64): one stack when every value is a
-    one-element tensor (the usual 0-dim columns), else one by one."""
-    vals = [samples[i].get(key, None) if hasattr(samples[i], "get") else None for i in idxs]
-    if vals and all(isinstance(v, torch.Tensor) for v in vals):
-        try:
-            st = torch.stack(vals)
-        except RuntimeError:  # shapes, devices or dtypes torch cannot stack
-            st = None
-        if st is not None and st.numel() == len(vals):
-            return st.reshape(-1).to(device="cpu", dtype=torch.float64).numpy()
-    return np.array([_scalar_of(v, default) for v in vals], np.float64)
+_NP_DTYPE = {torch.int32: np.int32, torch.int64: np.int64, torch.float32: np.float32}
+
+
+# Records of meshy_amd._stage.columns: one per used sample.
+_REC = np.dtype([("ptr", "<u8"), ("dim0", "<i8"), ("row", "<i8"), ("dtype", "<i4"), ("flags", "<i4")])
+# c10::ScalarType codes of the dtypes the staging writes.
+_SCALAR_TYPE = {torch.uint8: 0, torch.int8: 1, torch.int16: 2, torch.int32: 3, torch.int64: 4, torch.float16: 5,
+                torch.float32: 6, torch.float64: 7, torch.bool: 11, torch.bfloat16: 15}
+_CPU_CONTIGUOUS_TENSOR = 7  # record flags: a tensor, on the CPU, contiguous
+
+
+def _column(samples: Sequence[Any], used_b: bytes, key: str) -> np.ndarray:
+    return np.frombuffer(_lib.stage().columns(samples, used_b, key), _REC)
+
+
+_GATHER_FN: int | None = None
+
+
+def _gather_fn() -> int:
+    """Address of the library's meshy_host_gather, for meshy_amd._stage.gather."""
+    global _GATHER_FN
+    if _GATHER_FN is None:
+        _GATHER_FN = _lib.ctypes.cast(_lib.load().meshy_host_gather, _lib.ctypes.c_void_p).value
+    return _GATHER_FN
+
+
+def _gather_column(samples: Sequence[Any], used: np.ndarray, used_b: bytes, need: np.ndarray, key: str,
+                   out: torch.Tensor, row: int = 1, recs: np.ndarray | None = None) -> None:
+    """The first ``need[j]`` rows (``row`` elements each) of ``samples[used[j]][key]``
+    for every j, concatenated into the host tensor ``out``: columns that are CPU
+    contiguous tensors of ``out``'s dtype are read in place (one native call
+    when all are), any other is converted first."""
+    n = len(used)
+    if n == 0:
+        return
+    nbytes = int(need.sum()) * row * out.element_size()
+    if nbytes != out.numel() * out.element_size():
+        raise ValueError(f"column {key!r}: the samples hold {nbytes} bytes, the staging wants "
+                         f"{out.numel() * out.element_size()}")
+    if _lib.stage().gather(samples, used_b, need.tobytes(), key, out.data_ptr() if nbytes else 0,
+                           _SCALAR_TYPE[out.dtype], out.element_size(), row, _gather_fn()):
+        return
+    if recs is None:
+        recs = _column(samples, used_b, key)
+    short = np.flatnonzero((recs["flags"] & 1).astype(bool) & (recs["dim0"] < need))
+    if short.size:
+        j = int(short[0])
+        raise ValueError(f"column {key!r} of sample {int(used[j])} holds {int(recs['dim0'][j])} rows, "
+                         f"{int(need[j])} are needed")
+    ptrs = recs["ptr"].copy()
+    odd = np.flatnonzero((recs["flags"] != _CPU_CONTIGUOUS_TENSOR) | (recs["dtype"] != _SCALAR_TYPE[out.dtype])
+                         | (recs["row"] != row))
+    keep = []  # converted copies stay alive until the gather is done
+    for j in odd.tolist():
+        L = int(need[j])
+        c = torch.as_tensor(samples[int(used[j])][key])
+        if c.shape[0] < L:
+            raise ValueError(f"column {key!r} of sample {int(used[j])} holds {c.shape[0]} rows, {L} are needed")
+        c = c[:L].to(device="cpu", dtype=out.dtype).contiguous()
+        if c.numel() != L * row:
+            raise ValueError(f"column {key!r} of sample {int(used[j])} has rows of {c.numel() // max(L, 1)} "
+                             f"elements, {row} expected")
+        keep.append(c)
+        ptrs[j] = c.data_ptr() if L else 0
+    sizes = need * (row * out.element_size())
+    nbytes = int(sizes.sum())
+    if nbytes != out.numel() * out.element_size():
+        raise ValueError(f"column {key!r}: the samples hold {nbytes} bytes, the staging wants "
+                         f"{out.numel() * out.element_size()}")
+    if nbytes == 0:  # only empty samples (an empty view has no address)
+        return
+    rc = _lib.load().meshy_host_gather(ptrs.ctypes.data, sizes.ctypes.data, n, out.data_ptr(), 0)
+    _lib.check(rc, "meshy_host_gather")
 
 
 @dataclass
@@ -196,59 +256,57 @@ def stage_micro_batches(
     if device.type != "cuda":
         raise ValueError("meshy_amd builds micro-batches on a HIP device; pass a cuda device")
 
-    # Samples used by these micros, remapped to a compact list.
-    remap: dict[int, int] = {}
-    used: list[int] = []
-    need_len: list[int] = []
-    for m in micros:
-        if layout == "packed" and m.n_tokens > m.seq_len:
+    # Samples used by these micros, remapped to a compact list in order of
+    # first use, with the longest prefix any micro reads of each, and the
+    # per-document tables: one native pass over the micros.
+    micros = tuple(micros)
+    used_b, need_b, ds_b, dl_b, seq_b, nd_b, nt_b = _lib.stage().plan_tables(micros, len(samples))
+    used = np.frombuffer(used_b, np.int64)
+    need_len = np.frombuffer(need_b, np.int64)
+    seq = np.frombuffer(seq_b, np.int64)
+    n_docs = np.frombuffer(nd_b, np.int64)
+    if layout == "packed":
+        over = np.flatnonzero(np.frombuffer(nt_b, np.int64) > seq)
+        if over.size:
+            m = micros[int(over[0])]
             raise AssertionError(f"micro seq_len {m.seq_len} smaller than its tokens {m.n_tokens}")
-        for idx, L in zip(m.sample_idx, m.doc_lens):
-            if idx not in remap:
-                remap[idx] = len(used)
-                used.append(idx)
-                need_len.append(int(L))
-            else:
-                need_len[remap[idx]] = max(need_len[remap[idx]], int(L))
     n_s = len(used)
-    # The per-token columns each micro reads, in one pass over the samples.
     # Token ids travel in the samples' own int64 (the reference's dtype) or as
     # int32 (any vocabulary fits), and come out int64 either way.
-    tok_parts, mask_parts, lp_parts = [], [], []
-    tok64 = True
-    for idx, L in zip(used, need_len):
-        s = samples[idx]
-        tk = s["tokens"]
-        n_tk = tk.shape[0] if isinstance(tk, torch.Tensor) else len(tk)
-        if n_tk < L:
-            raise ValueError(f"sample {idx} has {n_tk} tokens, micro wants {L}")
-        tok64 = tok64 and isinstance(tk, torch.Tensor) and tk.dtype == torch.int64
-        tok_parts.append(tk)
-        mask_parts.append(s["mask_assistant"])
-        if need_rollout_lp:
-            lp_parts.append(s["logprobs"])
+    tok_recs = _column(samples, used_b, "tokens")
+    tok_tensor = (tok_recs["flags"] & 1).astype(bool)
+    n_tk = np.where(tok_tensor, tok_recs["dim0"], 0)
+    for j in np.flatnonzero(~tok_tensor).tolist():  # lists and arrays: their length
+        n_tk[j] = len(samples[int(used[j])]["tokens"])
+    short = np.flatnonzero(n_tk < need_len)
+    if short.size:
+        j = int(short[0])
+        raise ValueError(f"sample {int(used[j])} has {int(n_tk[j])} tokens, micro wants {int(need_len[j])}")
+    tok64 = bool(tok_tensor.all() and (tok_recs["dtype"] == _SCALAR_TYPE[torch.int64]).all())
     per_token_adv = any(ADVANTAGE_TOKENS in samples[m.sample_idx[0]] for m in micros if m.sample_idx)
     s_off = np.zeros(n_s + 1, np.int64)
     np.cumsum(need_len, out=s_off[1:])
     total = int(s_off[-1])
-    teacher_k, teacher_ids64 = _teacher_width(samples, used, need_len) if teacher else (0, False)
+    teacher_k, teacher_ids64, teacher_recs = (_teacher_width(samples, used, used_b, need_len) if teacher
+                                              else (0, False, (None, None)))
 
     # Plan tables.
     n_micro = len(micros)
-    seq = np.array([m.seq_len for m in micros], np.int64)
-    rows = np.array([1 if layout == "packed" else m.n_rows for m in micros], np.int64)
+    rows = (np.ones(n_micro, np.int64) if layout == "packed"
+            else np.array([m.n_rows for m in micros], np.int64))
     elems = seq * rows
     out_off = np.zeros(n_micro + 1, np.int64)
     np.cumsum(elems, out=out_off[1:])
-    n_docs = np.array([len(m.sample_idx) for m in micros], np.int64)
     doc_start = np.zeros(n_micro + 1, np.int32)
     np.cumsum(n_docs, out=doc_start[1:])
     n_docs_total = int(doc_start[-1])
-    doc_sample = np.array([remap[i] for m in micros for i in m.sample_idx], np.int32)
-    doc_len = np.array([L for m in micros for L in m.doc_lens], np.int64)
-    adv_samples = _scalars(samples, used, "advantage").astype(np.float32)
+    doc_sample = np.frombuffer(ds_b, np.int32)
+    doc_len = np.frombuffer(dl_b, np.int64)
+    st = _lib.stage()
+    adv_samples = np.frombuffer(st.scalars(samples, used_b, "advantage", 0.0), np.float64).astype(np.float32)
     # Positive-LM weights only for rewards above 0.5 (batch.py:225-229).
-    pos_used = np.where(_scalars(samples, used, "reward") > 0.5, _scalars(samples, used, "positive_lm_weight"),
+    pos_used = np.where(np.frombuffer(st.scalars(samples, used_b, "reward", 0.0), np.float64) > 0.5,
+                        np.frombuffer(st.scalars(samples, used_b, "positive_lm_weight", 0.0), np.float64),
                         0.0).astype(np.float32)
     pos_w = pos_used[doc_sample] if n_docs_total else np.zeros(0, np.float32)
     tok_dtype = torch.int64 if tok64 else torch.int32
@@ -256,9 +314,9 @@ def stage_micro_batches(
     # Per-token advantages already on the device (attach_gae_advantages leaves
     # them there) are gathered on the device; host ones travel with the rest.
     adv_dev = None
-    if per_token_adv and n_s and all(samples[i][ADVANTAGE_TOKENS].is_cuda for i in used):
+    if per_token_adv and n_s and all(samples[int(i)][ADVANTAGE_TOKENS].is_cuda for i in used):
         parts = []
-        for i, L in zip(used, need_len):
+        for i, L in zip(used.tolist(), need_len.tolist()):
             a = samples[i][ADVANTAGE_TOKENS][:L].to(device=device, dtype=torch.float32)
             if a.numel() < L:
                 a = torch.cat([a, a.new_zeros(L - a.numel())])
@@ -288,32 +346,34 @@ def stage_micro_batches(
     stage = _STAGING.setdefault(device.index or 0, _Staging())
     host = stage.get(lay.size)
     if n_s:
-        srcs = [samples[i] for i in used]
         # the first need_len[i] positions of each sample's columns
-        gather_heads_into(tok_parts, need_len, lay.view(host, "tokens"))
-        gather_heads_into(mask_parts, need_len, lay.view(host, "mask"))
+        _gather_column(samples, used, used_b, need_len, "tokens", lay.view(host, "tokens"), recs=tok_recs)
+        _gather_column(samples, used, used_b, need_len, "mask_assistant", lay.view(host, "mask"))
         if need_rollout_lp:
-            gather_heads_into(lp_parts, need_len, lay.view(host, "logprobs"))
+            _gather_column(samples, used, used_b, need_len, "logprobs", lay.view(host, "logprobs"))
         if teacher_k:
-            gather_heads_into([s[TEACHER_FIELDS[0]] for s in srcs], need_len, lay.view(host, "teacher_ids"), teacher_k)
-            gather_heads_into([s[TEACHER_FIELDS[1]] for s in srcs], need_len, lay.view(host, "teacher_lps"), teacher_k)
+            _gather_column(samples, used, used_b, need_len, TEACHER_FIELDS[0], lay.view(host, "teacher_ids"),
+                           row=teacher_k, recs=teacher_recs[0])
+            _gather_column(samples, used, used_b, need_len, TEACHER_FIELDS[1], lay.view(host, "teacher_lps"),
+                           row=teacher_k, recs=teacher_recs[1])
         if per_token_adv and adv_dev is None:
             parts = []
-            for s, L in zip(srcs, need_len):
-                a = s[ADVANTAGE_TOKENS][:L].to(device="cpu", dtype=torch.float32)
+            for i, L in zip(used.tolist(), need_len.tolist()):
+                a = samples[i][ADVANTAGE_TOKENS][:L].to(device="cpu", dtype=torch.float32)
                 if a.numel() < L:
                     a = torch.cat([a, a.new_zeros(L - a.numel())])
                 parts.append(a)
             gather_into(parts, lay.view(host, "adv_tokens"))
-    lay.view(host, "adv_samples")[:n_s] = torch.from_numpy(adv_samples)
-    lay.view(host, "s_off").copy_(torch.from_numpy(s_off))
-    lay.view(host, "seq").copy_(torch.from_numpy(seq))
-    lay.view(host, "out_off").copy_(torch.from_numpy(out_off))
-    lay.view(host, "doc_start").copy_(torch.from_numpy(doc_start))
+    hnp = stage.np
+    lay.np_view(hnp, "adv_samples")[:n_s] = adv_samples
+    lay.np_view(hnp, "s_off")[:] = s_off
+    lay.np_view(hnp, "seq")[:] = seq
+    lay.np_view(hnp, "out_off")[:] = out_off
+    lay.np_view(hnp, "doc_start")[:] = doc_start
     if n_docs_total:
-        lay.view(host, "doc_len")[:n_docs_total] = torch.from_numpy(doc_len)
-        lay.view(host, "doc_sample")[:n_docs_total] = torch.from_numpy(doc_sample)
-        lay.view(host, "pos_w")[:n_docs_total] = torch.from_numpy(pos_w)
+        lay.np_view(hnp, "doc_len")[:n_docs_total] = doc_len
+        lay.np_view(hnp, "doc_sample")[:n_docs_total] = doc_sample
+        lay.np_view(hnp, "pos_w")[:n_docs_total] = pos_w
 
     stream = torch.cuda.current_stream(device)
     dbuf = torch.empty(lay.size, dtype=torch.uint8, device=device)
@@ -327,25 +387,39 @@ def stage_micro_batches(
     )
 
 
-def _teacher_width(samples, used, need_len) -> tuple[int, bool]:
-    """Top-K width of the used samples' Teacher columns, and whether all their ids
-    are int64; checks they cover the micros (opd.py:39-55)."""
-    k = 0
-    ids64 = True
-    for i, L in zip(used, need_len):
-        td = samples[i]
-        ids, lps = td[TEACHER_FIELDS[0]], td[TEACHER_FIELDS[1]]
-        if ids.shape[0] < L or lps.shape[0] < L:
-            raise ValueError(
-                f"teacher columns cover {int(min(ids.shape[0], lps.shape[0]))} positions but the student "
-                f"micro-batch needs {L}; the Teacher seq_len must be >= the Student's"
-            )
-        width = int(ids.shape[-1])
-        if k and width != k:
-            raise ValueError(f"Teacher Top-K widths differ across samples ({k} vs {width})")
-        k = width
-        ids64 = ids64 and isinstance(ids, torch.Tensor) and ids.dtype == torch.int64
-    return k, ids64
+def _teacher_width(samples, used, used_b, need_len) -> tuple[int, bool, tuple]:
+    """Top-K width of the used samples' Teacher columns, whether all their ids
+    are int64, and the columns' records; checks they cover the micros
+    (opd.py:39-55)."""
+    recs = (_column(samples, used_b, TEACHER_FIELDS[0]), _column(samples, used_b, TEACHER_FIELDS[1]))
+    if not all((r["flags"] & 1).all() for r in recs):  # columns that are not tensors: one by one
+        k, ids64 = 0, True
+        for i, L in zip(used.tolist(), need_len.tolist()):
+            ids, lps = samples[i][TEACHER_FIELDS[0]], samples[i][TEACHER_FIELDS[1]]
+            if ids.shape[0] < L or lps.shape[0] < L:
+                raise ValueError(
+                    f"teacher columns cover {int(min(ids.shape[0], lps.shape[0]))} positions but the student "
+                    f"micro-batch needs {L}; the Teacher seq_len must be >= the Student's"
+                )
+            width = int(ids.shape[-1])
+            if k and width != k:
+                raise ValueError(f"Teacher Top-K widths differ across samples ({k} vs {width})")
+            k = width
+            ids64 = ids64 and isinstance(ids, torch.Tensor) and ids.dtype == torch.int64
+        return k, ids64, (None, None)
+    ids, lps = recs
+    cover = np.minimum(ids["dim0"], lps["dim0"])
+    short = np.flatnonzero(cover < need_len)
+    if short.size:
+        j = int(short[0])
+        raise ValueError(f"teacher columns cover {int(cover[j])} positions but the student micro-batch needs "
+                         f"{int(need_len[j])}; the Teacher seq_len must be >= the Student's")
+    widths = ids["row"]
+    if widths.size and (widths != widths[0]).any():
+        j = int(np.flatnonzero(widths != widths[0])[0])
+        raise ValueError(f"Teacher Top-K widths differ across samples ({int(widths[0])} vs {int(widths[j])})")
+    k = int(widths[0]) if widths.size else 0
+    return k, bool((ids["dtype"] == _SCALAR_TYPE[torch.int64]).all()), recs
 
 
 def launch_pack(job: PackJob, sharder=None) -> list[Batch]:

@@ -4,8 +4,9 @@
 
 Each source compiles to its own object under meshy_amd/_build/ (in parallel),
 then one link produces meshy_amd/libmeshy_amd.so next to this file.  The
-CPython extension meshy_amd._pyio (host code over Python objects, no device
-code) is built beside it with the host compiler.
+CPython extensions meshy_amd._pyio (host code over Python objects) and
+meshy_amd._stage (host code over libtorch's tensor type), no device code in
+either, are built beside it with the host compiler.
 """
 
 from __future__ import annotations
@@ -27,6 +28,8 @@ SOURCES = ("capi.cpp", "plan.cpp", "hostio.cpp", "logprob.hip", "topk.hip", "dis
 
 PYIO_SRC = "pyio.cpp"
 PYIO_OUT = os.path.join(HERE, "_pyio" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
+STAGE_SRC = "stage.cpp"
+STAGE_OUT = os.path.join(HERE, "_stage" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 
 ARCH = os.environ.get("MESHY_OFFLOAD_ARCH", "gfx950")
 
@@ -88,14 +91,42 @@ def build_pyio(verbose: bool = False) -> str:
     return PYIO_OUT
 
 
+def build_stage(verbose: bool = False) -> str:
+    """Compile the CPython extension meshy_amd._stage (host code over libtorch's
+    tensor type: reads each sample tensor's pointer, dtype and shape without a
+    Python attribute call); returns its path."""
+    import torch
+    from torch.utils import cpp_extension
+
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler found for meshy_amd._stage")
+    libdir = os.path.join(os.path.dirname(torch.__file__), "lib")
+    abi = int(bool(getattr(torch._C, "_GLIBCXX_USE_CXX11_ABI", True)))
+    tmp = STAGE_OUT + ".tmp"
+    cmd = [cxx, "-O2", "-std=c++17", "-shared", "-fPIC", "-Wall", f"-D_GLIBCXX_USE_CXX11_ABI={abi}",
+           *[f"-I{p}" for p in cpp_extension.include_paths()], f"-I{sysconfig.get_paths()['include']}",
+           os.path.join(CSRC, STAGE_SRC), "-o", tmp, f"-L{libdir}", "-ltorch_python", "-ltorch_cpu", "-lc10",
+           f"-Wl,-rpath,{libdir}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"{cxx} failed on {STAGE_SRC}:\n{res.stderr[-4000:]}")
+    os.replace(tmp, STAGE_OUT)
+    return STAGE_OUT
+
+
 def build(verbose: bool = False) -> str:
     """Compile every source and link libmeshy_amd.so (and build meshy_amd._pyio);
     returns the library's path."""
     os.makedirs(BUILD_DIR, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES) + 1, os.cpu_count() or 1)) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES) + 2, os.cpu_count() or 1)) as ex:
+        stage = ex.submit(build_stage, verbose)
         pyio = ex.submit(build_pyio, verbose)
         objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
         pyio.result()
+        stage.result()
     tmp = OUT + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", *objs, "-o", tmp]
     if verbose:

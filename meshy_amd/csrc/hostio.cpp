@@ -23,7 +23,7 @@ namespace meshy {
 namespace {
 
 // Below this many bytes per worker a gather runs on fewer threads.
-constexpr int64_t kBytesPerWorker = 512 * 1024;
+constexpr int64_t kBytesPerWorker = 128 * 1024;
 constexpr int kMaxWorkers = 16;
 
 // One gather: pieces [0, n) of sizes nbytes[i] land at dst + start[i]; worker w

@@ -1,0 +1,397 @@
+// meshy_amd._stage: the host side of staging per-sample tensors for the pack,
+// as a CPython extension over libtorch's tensor type (host code only).
+//
+// build_micro_batch (meshy/backend/titan/batch.py:96-230) reads, for every
+// sample of a micro, sample["tokens"], sample["mask_assistant"],
+// sample["logprobs"], sample.get("advantage"), ... one attribute at a time.
+// From Python each tensor attribute (data_ptr, dtype, shape, device,
+// contiguity) costs ~80 ns, ~1 us per column; these passes read them from the
+// at::Tensor behind each object in a few ns, so the staging of a step's 256
+// samples is one call per concern instead of ~3000 attribute reads.  Any
+// conversion of a column (a list, another dtype, a strided view) stays with
+// the caller.
+//
+//   plan_tables(micros, n_samples)
+//       -> (used, need_len, doc_sample, doc_len, seq_len, n_docs, n_tokens)
+//       The samples the micros read, compacted in order of first use
+//       (used[j] = sample index), the longest prefix any micro reads of each
+//       (need_len), and per document its compact sample and length; per micro
+//       its seq_len, document count and token count.  int64 (doc_sample
+//       int32) little-endian bytes.
+//   columns(samples, used, key)
+//       -> bytes of n_used records {u64 ptr; i64 dim0; i64 row; i32 dtype; i32 flags}
+//       sample[key] for each used sample (KeyError if absent): flags bit 0 a
+//       tensor, bit 1 on the CPU, bit 2 contiguous; ptr its data, dim0 its
+//       first dimension, row the elements per first-dimension index, dtype
+//       the c10::ScalarType (-1 when not a tensor).
+//   scalars(samples, used, key, default)
+//       -> bytes of n_used float64: sample.get(key), a number or the first
+//       element of a tensor, `default` when absent or None or empty.
+//   gather(samples, used, need, key, dst, dtype, elem_size, row, gather_fn)
+//       -> True after concatenating the first need[j] rows of each used
+//       sample's column at dst (through the library's threaded gather), or
+//       False, copying nothing, when some column is not a CPU contiguous
+//       tensor of that dtype and row width.
+#include <Python.h>
+
+#include <torch/csrc/autograd/python_variable.h>
+
+#include <cstdint>
+#include <cstring>
+#include <vector>
+
+namespace {
+
+struct Record {
+    uint64_t ptr;
+    int64_t dim0;
+    int64_t row;
+    int32_t dtype;
+    int32_t flags;
+};
+static_assert(sizeof(Record) == 32, "record layout");
+
+template <class T>
+PyObject* to_bytes(const std::vector<T>& v) {
+    return PyBytes_FromStringAndSize(reinterpret_cast<const char*>(v.data()),
+                                     static_cast<Py_ssize_t>(v.size() * sizeof(T)));
+}
+
+// A Python int as int64 (false with an exception set otherwise).
+bool as_i64(PyObject* o, int64_t& out) {
+    const long long v = PyLong_AsLongLong(o);
+    if (v == -1 && PyErr_Occurred()) return false;
+    out = v;
+    return true;
+}
+
+// The used sample indices from a bytes object of int64.
+bool used_of(PyObject* b, const int64_t*& p, Py_ssize_t& n) {
+    if (!PyBytes_Check(b)) {
+        PyErr_SetString(PyExc_TypeError, "used must be bytes of int64");
+        return false;
+    }
+    p = reinterpret_cast<const int64_t*>(PyBytes_AS_STRING(b));
+    n = PyBytes_GET_SIZE(b) / static_cast<Py_ssize_t>(sizeof(int64_t));
+    return true;
+}
+
+PyObject* plan_tables(PyObject*, PyObject* args) {
+    PyObject* micros;
+    long long n_samples;
+    if (!PyArg_ParseTuple(args, "OL", &micros, &n_samples)) return nullptr;
+    PyObject* seq = PySequence_Fast(micros, "micros must be a sequence");
+    if (!seq) return nullptr;
+    const Py_ssize_t n_micro = PySequence_Fast_GET_SIZE(seq);
+    std::vector<int64_t> remap(static_cast<size_t>(n_samples > 0 ? n_samples : 0), -1);
+    std::vector<int64_t> used, need, doc_len, seq_len, n_docs, n_tokens;
+    std::vector<int32_t> doc_sample;
+    seq_len.reserve(n_micro);
+    n_docs.reserve(n_micro);
+    n_tokens.reserve(n_micro);
+    bool ok = true;
+    for (Py_ssize_t k = 0; ok && k < n_micro; ++k) {
+        PyObject* m = PySequence_Fast_GET_ITEM(seq, k);
+        PyObject* sl = PyObject_GetAttrString(m, "seq_len");
+        PyObject* si = sl ? PyObject_GetAttrString(m, "sample_idx") : nullptr;
+        PyObject* dl = si ? PyObject_GetAttrString(m, "doc_lens") : nullptr;
+        PyObject* fsi = dl ? PySequence_Fast(si, "sample_idx must be a sequence") : nullptr;
+        PyObject* fdl = fsi ? PySequence_Fast(dl, "doc_lens must be a sequence") : nullptr;
+        int64_t s_len = 0;
+        ok = fdl && as_i64(sl, s_len);
+        if (ok && PySequence_Fast_GET_SIZE(fsi) != PySequence_Fast_GET_SIZE(fdl)) {
+            PyErr_SetString(PyExc_ValueError, "a micro's sample_idx and doc_lens differ in length");
+            ok = false;
+        }
+        int64_t tokens = 0;
+        const Py_ssize_t nd = ok ? PySequence_Fast_GET_SIZE(fsi) : 0;
+        for (Py_ssize_t j = 0; ok && j < nd; ++j) {
+            int64_t idx = 0, L = 0;
+            ok = as_i64(PySequence_Fast_GET_ITEM(fsi, j), idx) && as_i64(PySequence_Fast_GET_ITEM(fdl, j), L);
+            if (!ok) break;
+            if (idx < 0 || idx >= n_samples) {
+                PyErr_Format(PyExc_IndexError, "micro %zd reads sample %lld of %lld", k, static_cast<long long>(idx),
+                             n_samples);
+                ok = false;
+                break;
+            }
+            if (L < 0) {
+                PyErr_Format(PyExc_ValueError, "micro %zd has a negative document length", k);
+                ok = false;
+                break;
+            }
+            int64_t& c = remap[static_cast<size_t>(idx)];
+            if (c < 0) {
+                c = static_cast<int64_t>(used.size());
+                used.push_back(idx);
+                need.push_back(L);
+            } else if (L > need[static_cast<size_t>(c)]) {
+                need[static_cast<size_t>(c)] = L;
+            }
+            doc_sample.push_back(static_cast<int32_t>(c));
+            doc_len.push_back(L);
+            tokens += L;
+        }
+        if (ok) {
+            seq_len.push_back(s_len);
+            n_docs.push_back(nd);
+            n_tokens.push_back(tokens);
+        }
+        Py_XDECREF(fdl);
+        Py_XDECREF(fsi);
+        Py_XDECREF(dl);
+        Py_XDECREF(si);
+        Py_XDECREF(sl);
+    }
+    Py_DECREF(seq);
+    if (!ok) return nullptr;
+    return Py_BuildValue("(NNNNNNN)", to_bytes(used), to_bytes(need), to_bytes(doc_sample), to_bytes(doc_len),
+                         to_bytes(seq_len), to_bytes(n_docs), to_bytes(n_tokens));
+}
+
+PyObject* columns(PyObject*, PyObject* args) {
+    PyObject *samples, *used_b, *key;
+    if (!PyArg_ParseTuple(args, "OOO", &samples, &used_b, &key)) return nullptr;
+    const int64_t* used;
+    Py_ssize_t n;
+    if (!used_of(used_b, used, n)) return nullptr;
+    PyObject* seq = PySequence_Fast(samples, "samples must be a sequence");
+    if (!seq) return nullptr;
+    const Py_ssize_t n_samples = PySequence_Fast_GET_SIZE(seq);
+    std::vector<Record> out(static_cast<size_t>(n));
+    bool ok = true;
+    for (Py_ssize_t i = 0; ok && i < n; ++i) {
+        if (used[i] < 0 || used[i] >= n_samples) {
+            PyErr_SetString(PyExc_IndexError, "used sample index out of range");
+            ok = false;
+            break;
+        }
+        PyObject* s = PySequence_Fast_GET_ITEM(seq, used[i]);
+        PyObject* v;
+        if (PyDict_CheckExact(s)) {
+            v = PyDict_GetItemWithError(s, key);
+            if (!v) {
+                if (!PyErr_Occurred()) PyErr_SetObject(PyExc_KeyError, key);
+                ok = false;
+                break;
+            }
+            Py_INCREF(v);
+        } else {
+            v = PyObject_GetItem(s, key);
+            if (!v) {
+                ok = false;
+                break;
+            }
+        }
+        Record r{0, 0, 0, -1, 0};
+        if (THPVariable_Check(v)) {
+            const at::Tensor& t = THPVariable_Unpack(v);
+            r.flags = 1;
+            if (t.device().is_cpu()) r.flags |= 2;
+            if (t.is_contiguous()) r.flags |= 4;
+            r.dtype = static_cast<int32_t>(t.scalar_type());
+            if (t.dim() == 0) {
+                r.dim0 = 1;
+                r.row = 1;
+            } else {
+                r.dim0 = t.size(0);
+                r.row = r.dim0 ? t.numel() / r.dim0 : 1;
+                for (int64_t d = 1; d < t.dim() && !r.dim0; ++d) r.row *= t.size(d);
+            }
+            if ((r.flags & 6) == 6 && t.numel()) r.ptr = reinterpret_cast<uint64_t>(t.data_ptr());
+        }
+        Py_DECREF(v);
+        out[static_cast<size_t>(i)] = r;
+    }
+    Py_DECREF(seq);
+    if (!ok) return nullptr;
+    return to_bytes(out);
+}
+
+// The first element of a CPU contiguous tensor of a common numeric type, read
+// in place; anything else goes through item().
+bool first_element(const at::Tensor& t, double& out) {
+    if (!t.numel()) return false;
+    if (t.device().is_cpu() && t.is_contiguous()) {
+        const void* p = t.data_ptr();
+        switch (t.scalar_type()) {
+            case at::kFloat: out = *static_cast<const float*>(p); return true;
+            case at::kDouble: out = *static_cast<const double*>(p); return true;
+            case at::kLong: out = static_cast<double>(*static_cast<const int64_t*>(p)); return true;
+            case at::kInt: out = static_cast<double>(*static_cast<const int32_t*>(p)); return true;
+            case at::kBool: out = *static_cast<const bool*>(p) ? 1.0 : 0.0; return true;
+            default: break;
+        }
+    }
+    out = t.reshape(-1)[0].item<double>();
+    return true;
+}
+
+PyObject* scalars(PyObject*, PyObject* args) {
+    PyObject *samples, *used_b, *key;
+    double dflt;
+    if (!PyArg_ParseTuple(args, "OOOd", &samples, &used_b, &key, &dflt)) return nullptr;
+    const int64_t* used;
+    Py_ssize_t n;
+    if (!used_of(used_b, used, n)) return nullptr;
+    PyObject* seq = PySequence_Fast(samples, "samples must be a sequence");
+    if (!seq) return nullptr;
+    const Py_ssize_t n_samples = PySequence_Fast_GET_SIZE(seq);
+    std::vector<double> out(static_cast<size_t>(n), dflt);
+    bool ok = true;
+    try {
+        for (Py_ssize_t i = 0; ok && i < n; ++i) {
+            if (used[i] < 0 || used[i] >= n_samples) {
+                PyErr_SetString(PyExc_IndexError, "used sample index out of range");
+                ok = false;
+                break;
+            }
+            PyObject* s = PySequence_Fast_GET_ITEM(seq, used[i]);
+            PyObject* v = nullptr;
+            if (PyDict_CheckExact(s)) {
+                v = PyDict_GetItemWithError(s, key);
+                if (!v && PyErr_Occurred()) {
+                    ok = false;
+                    break;
+                }
+                Py_XINCREF(v);
+            } else if (PyObject_HasAttrString(s, "get")) {
+                v = PyObject_CallMethod(s, "get", "OO", key, Py_None);
+                if (!v) {
+                    ok = false;
+                    break;
+                }
+            }
+            if (!v || v == Py_None) {
+                Py_XDECREF(v);
+                continue;
+            }
+            double x = dflt;
+            if (THPVariable_Check(v)) {
+                if (!first_element(THPVariable_Unpack(v), x)) x = dflt;
+            } else {
+                x = PyFloat_AsDouble(v);
+                if (x == -1.0 && PyErr_Occurred()) ok = false;
+            }
+            Py_DECREF(v);
+            out[static_cast<size_t>(i)] = x;
+        }
+    } catch (const std::exception& e) {
+        PyErr_SetString(PyExc_RuntimeError, e.what());
+        ok = false;
+    }
+    Py_DECREF(seq);
+    if (!ok) return nullptr;
+    return to_bytes(out);
+}
+
+// The library's meshy_host_gather (passed in by address, so this module needs
+// no link to it).
+typedef int (*GatherFn)(const void* const*, const int64_t*, int64_t, void*, int);
+
+// gather(samples, used, need, key, dst, dtype, elem_size, row, gather_fn)
+//   Copies the first need[j] rows (row elements of elem_size bytes) of
+//   samples[used[j]][key] for every j, back to back, to the host address dst,
+//   when every column is a CPU contiguous tensor of c10::ScalarType dtype with
+//   rows of `row` elements; returns True.  Otherwise copies nothing and returns
+//   False (the caller converts).  A tensor column shorter than need[j] raises
+//   ValueError.
+PyObject* gather(PyObject*, PyObject* args) {
+    PyObject *samples, *used_b, *need_b, *key;
+    unsigned long long dst, fn;
+    int dtype;
+    long long elem_size, row;
+    if (!PyArg_ParseTuple(args, "OOOOKiLLK", &samples, &used_b, &need_b, &key, &dst, &dtype, &elem_size, &row,
+                          &fn))
+        return nullptr;
+    const int64_t *used, *need;
+    Py_ssize_t n, n_need;
+    if (!used_of(used_b, used, n) || !used_of(need_b, need, n_need)) return nullptr;
+    if (n_need != n) {
+        PyErr_SetString(PyExc_ValueError, "used and need differ in length");
+        return nullptr;
+    }
+    PyObject* seq = PySequence_Fast(samples, "samples must be a sequence");
+    if (!seq) return nullptr;
+    const Py_ssize_t n_samples = PySequence_Fast_GET_SIZE(seq);
+    std::vector<const void*> srcs(static_cast<size_t>(n));
+    std::vector<int64_t> nbytes(static_cast<size_t>(n));
+    bool ok = true, fast = true;
+    int64_t total = 0;
+    for (Py_ssize_t i = 0; ok && i < n; ++i) {
+        if (used[i] < 0 || used[i] >= n_samples) {
+            PyErr_SetString(PyExc_IndexError, "used sample index out of range");
+            ok = false;
+            break;
+        }
+        PyObject* s = PySequence_Fast_GET_ITEM(seq, used[i]);
+        PyObject* v;
+        if (PyDict_CheckExact(s)) {
+            v = PyDict_GetItemWithError(s, key);
+            if (!v) {
+                if (!PyErr_Occurred()) PyErr_SetObject(PyExc_KeyError, key);
+                ok = false;
+                break;
+            }
+            Py_INCREF(v);
+        } else {
+            v = PyObject_GetItem(s, key);
+            if (!v) {
+                ok = false;
+                break;
+            }
+        }
+        const int64_t L = need[i];
+        nbytes[static_cast<size_t>(i)] = L * row * elem_size;
+        total += nbytes[static_cast<size_t>(i)];
+        if (!THPVariable_Check(v)) {
+            fast = false;
+        } else {
+            const at::Tensor& t = THPVariable_Unpack(v);
+            const int64_t dim0 = t.dim() ? t.size(0) : 1;
+            if (dim0 < L) {
+                PyErr_Format(PyExc_ValueError, "column %R of sample %lld holds %lld rows, %lld are needed", key,
+                             static_cast<long long>(used[i]), static_cast<long long>(dim0),
+                             static_cast<long long>(L));
+                ok = false;
+            } else if (!t.device().is_cpu() || !t.is_contiguous() || static_cast<int>(t.scalar_type()) != dtype ||
+                       (dim0 && t.numel() / dim0 != row) || (!dim0 && L)) {
+                fast = false;
+            } else {
+                srcs[static_cast<size_t>(i)] = L ? t.data_ptr() : nullptr;
+            }
+        }
+        Py_DECREF(v);
+    }
+    Py_DECREF(seq);
+    if (!ok) return nullptr;
+    if (!fast) Py_RETURN_FALSE;
+    if (total > 0) {
+        if (!dst || !fn) {
+            PyErr_SetString(PyExc_ValueError, "gather: no destination or gather function");
+            return nullptr;
+        }
+        // The columns stay alive (the samples hold them) while the copy runs.
+        const int rc = reinterpret_cast<GatherFn>(fn)(srcs.data(), nbytes.data(), n, reinterpret_cast<void*>(dst), 0);
+        if (rc != 0) {
+            PyErr_Format(PyExc_RuntimeError, "meshy_host_gather failed (%d)", rc);
+            return nullptr;
+        }
+    }
+    Py_RETURN_TRUE;
+}
+
+PyMethodDef kMethods[] = {
+    {"gather", gather, METH_VARARGS, "Concatenate one column of the used samples into a host buffer."},
+    {"plan_tables", plan_tables, METH_VARARGS, "Compact sample map and document tables of a list of micros."},
+    {"columns", columns, METH_VARARGS, "Pointer, shape and dtype records of one column of the used samples."},
+    {"scalars", scalars, METH_VARARGS, "One scalar field of the used samples as float64."},
+    {nullptr, nullptr, 0, nullptr},
+};
+
+PyModuleDef kModule = {PyModuleDef_HEAD_INIT, "_stage", "Host staging passes over per-sample tensors.", -1,
+                       kMethods};
+
+}  // namespace
+
+PyMODINIT_FUNC PyInit__stage() { return PyModule_Create(&kModule); }

@@ -51,42 +51,4 @@ def gather_into(parts: Sequence, out: torch.Tensor) -> torch.Tensor:
     return out
 
 
-def gather_heads_into(cols: Sequence, lengths: Sequence[int], out: torch.Tensor, row: int = 1) -> torch.Tensor:
-    """``gather_into`` of the first ``lengths[i]`` rows (``row`` elements each)
-    of every column, without making a view per column: a contiguous host
-    column of ``out``'s dtype is read in place."""
-    if out.is_cuda or not out.is_contiguous():
-        raise ValueError("gather_heads_into writes a contiguous host tensor")
-    dt = out.dtype
-    es = out.element_size()
-    n = len(cols)
-    keep = []  # converted copies stay alive until the copy is done
-    ptrs = [0] * n
-    sizes = [0] * n
-    total = 0
-    for i, (c, L) in enumerate(zip(cols, lengths)):
-        L = int(L)
-        if type(c) is torch.Tensor and c.dtype is dt and not c.is_cuda and c.is_contiguous():
-            if c.shape[0] < L or c.numel() < L * row:
-                raise ValueError(f"column {i} holds {c.shape[0]} rows, {L} are needed")
-        else:
-            c = torch.as_tensor(c)
-            if c.shape[0] < L:
-                raise ValueError(f"column {i} holds {c.shape[0]} rows, {L} are needed")
-            c = c[:L].to(device="cpu", dtype=dt).contiguous()
-            keep.append(c)
-        ptrs[i] = c.data_ptr() if L else 0
-        sizes[i] = L * row * es
-        total += L * row
-    if total != out.numel():
-        raise ValueError(f"the columns hold {total} elements but out has {out.numel()}")
-    if n == 0 or total == 0:
-        return out
-    c_ptrs = (ctypes.c_void_p * n)(*ptrs)
-    c_sizes = (ctypes.c_int64 * n)(*sizes)
-    rc = _lib.load().meshy_host_gather(c_ptrs, c_sizes, n, out.data_ptr(), 0)
-    _lib.check(rc, "meshy_host_gather")
-    return out
-
-
-__all__ = ["gather_heads_into", "gather_into"]
+__all__ = ["gather_into"]

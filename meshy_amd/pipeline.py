@@ -146,20 +146,31 @@ class RaggedSamples:
 
 
 class PackResult:
+    """A packed step: the plan (the reference's dataclasses, built from the
+    flat tables the first time ``plan`` is read), the tables, one ``Batch`` per
+    micro of the rank and the per-sample advantages on the device."""
+
     def __init__(self, plan: Plan | None, tables, batches: list[Batch], advantages: torch.Tensor) -> None:
-        self.plan = plan
+        self._plan = plan
         self.tables = tables
         self.batches = batches
         self.advantages = advantages
 
+    @property
+    def plan(self) -> Plan:
+        if self._plan is None:
+            self._plan = tables_to_plan(self.tables)
+        return self._plan
+
 
 def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int = 1, rank: int = 0,
-              with_plan_objects: bool = True, broadcast_advantages: bool = True) -> PackResult:
+              with_plan_objects: bool = False, broadcast_advantages: bool = True) -> PackResult:
     """Plan, copy, normalise rewards and build every micro of ``rank``.
 
     The samples' part of the staging buffer is copied to the device first, so
     the transfer runs while the host plans; the plan tables follow in a second,
-    small copy."""
+    small copy.  The Plan dataclasses are built when ``PackResult.plan`` is
+    first read (``with_plan_objects`` builds them here)."""
     device = torch.device(device)
     stream = torch.cuda.current_stream(device)
     lay = ragged.lay
@@ -200,13 +211,9 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
                                           stream.cuda_stream)
     _lib.check(rc, "meshy_grpo_advantage")
 
-    plan = tables_to_plan(t) if with_plan_objects else None
-    if plan is not None:
-        micros = tuple(m for mini in plan.per_rank[rank] for m in mini.micros)
-    else:
-        sq, st, dl = seq.tolist(), start.tolist(), dlen[:nd_total].tolist()
-        micros = tuple(_LiteMicro(sq[k], st[k + 1] - st[k], sum(dl[st[k]:st[k + 1]]), tuple(dl[st[k]:st[k + 1]]))
-                       for k in range(nm))
+    sq, st, dl = seq.tolist(), start.tolist(), dlen[:nd_total].tolist()
+    micros = tuple(_LiteMicro(sq[k], st[k + 1] - st[k], sum(dl[st[k]:st[k + 1]]), tuple(dl[st[k]:st[k + 1]]))
+                   for k in range(nm))
     job = PackJob(
         micros=micros, layout=cfg.layout, device=device, dbuf=dbuf, lay=lay,
         need_rollout_lp=ragged.need_rollout_lp, per_token_adv=False, n_samples=ragged.n, seq=seq,
@@ -214,13 +221,14 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
         max_docs=int(n_docs.max()) if nm else 0, adv_samples=adv, broadcast_advantages=broadcast_advantages,
     )
     batches = launch_pack(job)
-    return PackResult(plan, t, batches, adv)
+    return PackResult(tables_to_plan(t) if with_plan_objects else None, t, batches, adv)
 
 
 class _LiteMicro:
     """What ``launch_pack`` reads of a MicroPlan, without building the dataclasses."""
 
     __slots__ = ("seq_len", "n_docs", "n_tokens", "doc_lens")
+    is_filler = property(lambda self: self.n_docs == 0)
 
     def __init__(self, seq_len: int, n_docs: int, n_tokens: int, doc_lens: tuple) -> None:
         self.seq_len = seq_len

@@ -459,8 +459,10 @@ def test_pack_step_256_samples_matches_oracle(dev):
 
 @pytest.mark.parametrize("layout", ["packed", "padded"])
 def test_pack_step_without_plan_objects_builds_the_same_batches(dev, layout):
-    """with_plan_objects=False skips the Plan dataclasses, not any output; two
-    calls in a row over one staging buffer (the tables region is rewritten)."""
+    """The Plan dataclasses are built when PackResult.plan is first read
+    (with_plan_objects=True builds them inside the call): the batches are the
+    same either way and so is the plan; two calls in a row over one staging
+    buffer (the tables region is rewritten)."""
     from meshy_amd import workloads
     from meshy_amd.pipeline import RaggedSamples, pack_step
     from meshy_amd.plan import PlannerConfig
@@ -469,9 +471,10 @@ def test_pack_step_without_plan_objects_builds_the_same_batches(dev, layout):
     ragged = RaggedSamples.from_arrays(batch.tokens, batch.mask, batch.logprobs, batch.offsets, rewards,
                                        group_offsets)
     cfg = PlannerConfig(layout=layout, mini_batch_size=64, seq_len=8192, align=2048, max_tokens_per_micro=8192)
-    full = pack_step(ragged, cfg, dev)
-    lite = pack_step(ragged, cfg, dev, with_plan_objects=False)
-    assert lite.plan is None and full.plan is not None
+    full = pack_step(ragged, cfg, dev, with_plan_objects=True)
+    lite = pack_step(ragged, cfg, dev)
+    assert lite._plan is None and full._plan is not None
+    assert lite.plan == full.plan  # built from the tables on first read
     assert len(full.batches) == len(lite.batches) > 4
     for a, b in zip(full.batches, lite.batches):
         for k in ("input_ids", "labels", "positions", "mask", "doc_ids", "rollout_logprobs", "advantages",
