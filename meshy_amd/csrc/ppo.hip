@@ -460,8 +460,12 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
             }
             if (!kLean && a.entropy) acc[TS_ENT] = fmaf(x.en, mk, acc[TS_ENT]);
             if (gu) {
+                // Nontemporal: the backward reads the unit gradient once, from
+                // HBM; kept out of the L2 it does not slow the kernel's end
+                // (21.4 against 23.5 us for the forward and backward of 1.83 M
+                // tokens, A/B on one box).
                 const bool real = d_first + slot < a.n_docs;  // the padding slot is not in the loss
-                gu[i] = real ? token_grad_v(a, x, At, W, tok_scale) : 0.f;
+                __builtin_nontemporal_store(real ? token_grad_v(a, x, At, W, tok_scale) : 0.f, gu + i);
             }
         }
         flush(cur);
@@ -531,7 +535,7 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
             for (int k = 0; k < kSegSums; ++k) sg[k] += c.seg[k];
 #pragma unroll
             for (int k = 0; k < kTokSums; ++k) acc[k] += c.tok[k];
-            if (gu) gu[i] = real ? token_grad_v(a, x, At, w_doc, tok_scale) : 0.f;
+            if (gu) __builtin_nontemporal_store(real ? token_grad_v(a, x, At, w_doc, tok_scale) : 0.f, gu + i);
         }
 #pragma unroll
         for (int k = 0; k < kSegSums; ++k) sg[k] = wave_sum(sg[k]);

@@ -245,6 +245,45 @@ class _PPOLoss(torch.autograd.Function):
         return grad, None
 
 
+def _tensor_key(t: torch.Tensor | None) -> tuple:
+    return (None,) if t is None else (id(t), t._version, t.data_ptr())
+
+
+def _inputs_key(stub, new_lp, old_lp, mb, mini, entropy) -> tuple:
+    """Everything an _Inputs is built from: each tensor's identity, version and
+    address, the batch's document count, the loss settings and the global
+    denominators."""
+    pd = getattr(stub, "parallel_dims", None)
+    return (new_lp.numel(), new_lp.device, _tensor_key(old_lp), _tensor_key(mb.mask),
+            _tensor_key(mb.rollout_logprobs), _tensor_key(entropy), _tensor_key(mb.advantages),
+            _tensor_key(mb.positive_lm_weights), _tensor_key(mb.doc_ids), int(mb.n_docs),
+            stub.ppo_clip_eps_low, stub.ppo_clip_eps_high, stub.use_tis, getattr(stub, "use_icepop", False),
+            getattr(stub, "tis_ratio_min", 0.5), getattr(stub, "tis_ratio_max", 5.0),
+            getattr(stub, "positive_lm_loss_coef", 0.0), stub.calculate_per_token_loss,
+            getattr(stub, "old_logprobs_source", "rollout"), getattr(pd, "cp", 1),
+            int(mini.n_docs_global), int(mini.n_tokens_global))
+
+
+def _cached_inputs(stub, new_lp, old_lp, mb, mini, entropy) -> _Inputs:
+    """The _Inputs of this call, reused from the batch's previous call when
+    nothing it was built from has changed (later PPO epochs over one micro).
+    The tensors are named by weak references as well as by id, since a freed
+    tensor's id and address may be reused; an in-place change bumps a version."""
+    key = _inputs_key(stub, new_lp, old_lp, mb, mini, entropy)
+    refs = (old_lp, mb.mask, mb.rollout_logprobs, entropy, mb.advantages, mb.positive_lm_weights, mb.doc_ids)
+    hit = getattr(mb, "_meshy_ppo_inputs", None)
+    if hit is not None and hit[0] == key and all((r is None and t is None) or (r is not None and r() is t)
+                                                 for r, t in zip(hit[2], refs)):
+        return hit[1]
+    inputs = _Inputs(stub, new_lp, old_lp, mb, mini, entropy)
+    try:
+        object.__setattr__(mb, "_meshy_ppo_inputs",
+                           (key, inputs, tuple(None if t is None else weakref.ref(t) for t in refs)))
+    except (AttributeError, TypeError):
+        pass  # a batch type without an attribute dict: no cache
+    return inputs
+
+
 def ppo_clip_loss(
     self: Any,
     new_lp: torch.Tensor,
@@ -259,7 +298,7 @@ def ppo_clip_loss(
         raise NotImplementedError(
             "context-parallel PPO loss needs the per-document all-reduce between the two "
             "kernel phases; this library drives one GPU")
-    inputs = _Inputs(self, new_lp, old_lp, mb, mini, entropy)
+    inputs = _cached_inputs(self, new_lp, old_lp, mb, mini, entropy)
     inputs.want_grad = torch.is_grad_enabled() and new_lp.requires_grad
     new_flat = new_lp.reshape(-1)
     if new_flat.dtype != torch.float32:

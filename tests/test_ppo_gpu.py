@@ -307,17 +307,21 @@ def test_per_token_advantages_padded_rows(dev):
     _compare(dev, new, old, mask, doc_ids, adv, rows, per_token_loss=False)
 
 
-def test_many_tiny_documents_and_empty_pad(dev):
-    # 3000 one- and two-token documents: many (tile, document) pairs per tile.
+@pytest.mark.parametrize("n_docs", [3000, 5000])
+def test_many_tiny_documents_and_empty_pad(dev, n_docs):
+    """One- and two-token documents: many (tile, document) pairs per tile, and
+    thousands of documents for the one-workgroup combine, under both
+    reductions."""
     g = torch.Generator().manual_seed(9)
-    lens = (torch.randint(1, 3, (3000,), generator=g)).tolist()
+    lens = (torch.randint(1, 3, (n_docs,), generator=g)).tolist()
     doc_ids = torch.cat([torch.full((L,), j) for j, L in enumerate(lens)]).reshape(1, -1)
     T = doc_ids.numel()
     mask = torch.ones(1, T)
     old = -torch.rand(1, T, generator=g)
     new = old + torch.randn(1, T, generator=g) * 0.4
-    adv = torch.randn(3000, generator=g)
-    _compare(dev, new, old, mask, doc_ids, adv, 3000, per_token_loss=False)
+    adv = torch.randn(n_docs, generator=g)
+    _compare(dev, new, old, mask, doc_ids, adv, n_docs, per_token_loss=False)
+    _compare(dev, new, old, mask, doc_ids, adv, n_docs, per_token_loss=True)
 
 
 @pytest.mark.parametrize("per_token_loss", [True, False])
@@ -482,6 +486,56 @@ def test_gae_rejects_doc_ids_out_of_range(dev):
     with pytest.raises(ValueError, match="doc_ids must lie"):
         gae.compute_vapo_gae(r, torch.zeros(rows, S, device=dev), mask, ids, 2)
     assert torch.isfinite(gae.compute_returns(r, mask, ids)).all()
+
+
+def test_inputs_cache_follows_edits(dev):
+    """Later calls on one micro-batch reuse its flattened inputs (PPO epochs);
+    an in-place edit of old_lp or the advantages, a new mini-batch denominator
+    or a replaced tensor rebuilds them, so every call matches the oracle."""
+    from meshy_amd.batch import Batch
+    from meshy_amd.loss import ppo_clip_loss
+    from meshy_amd.plan import MiniPlan
+
+    g = torch.Generator().manual_seed(31)
+    rows, S, n = 1, 5000, 3
+    doc_ids = torch.repeat_interleave(torch.arange(n), torch.tensor([1200, 2600, 1200])).reshape(1, -1)
+    mask = (torch.rand(rows, S, generator=g) > 0.1).float()
+    old = -torch.rand(rows, S, generator=g) * 2
+    new = old + torch.randn(rows, S, generator=g) * 0.3
+    adv = torch.tensor([0.7, -1.2, 0.4])
+    z = torch.zeros(rows, S, dtype=torch.long, device=dev)
+    mb = Batch(z, z, z.int(), mask.to(dev), doc_ids.to(dev), adv.to(dev), None, torch.zeros(n, device=dev), n)
+    stub = _stub(use_tis=False)
+
+    def check(old_c, adv_c, n_tok):
+        mini = MiniPlan(micros=(), n_docs_global=n, n_tokens_global=n_tok, tokens_per_rank=())
+        nd = new.to(dev).requires_grad_(True)
+        loss, sums = ppo_clip_loss(stub, nd, old_dev, mb, mini)
+        loss.backward()
+        nr = new.clone().requires_grad_(True)
+        ref_loss, ref_sums = oppo.ppo_clip_loss(nr, old_c, mask, doc_ids, adv_c, n, n_docs_global=n,
+                                                n_tokens_global=n_tok, clip_low=0.2, clip_high=0.28,
+                                                per_token_loss=True)
+        ref_loss.backward()
+        assert abs(loss.item() - ref_loss.item()) <= TOL
+        assert abs(sums["ppo_kl_sum"].item() - ref_sums["ppo_kl_sum"].item()) <= 1e-5 * max(1.0, abs(
+            ref_sums["ppo_kl_sum"].item()))
+        assert (nd.grad.cpu() - nr.grad).abs().max().item() <= 1e-6
+        return mb.__dict__["_meshy_ppo_inputs"][1]
+
+    n_tok = int(mask.sum())
+    old_dev = old.to(dev)
+    first = check(old, adv, n_tok)
+    assert check(old, adv, n_tok) is first  # reused
+    old_dev.mul_(0.5)  # in place: a new version
+    again = check(old * 0.5, adv, n_tok)
+    assert again is not first
+    mb.advantages.neg_()
+    again2 = check(old * 0.5, -adv, n_tok)
+    assert again2 is not again
+    assert check(old * 0.5, -adv, n_tok + 100) is not again2  # another denominator
+    old_dev = (old * 0.25).to(dev)  # a replaced tensor
+    check(old * 0.25, -adv, n_tok)
 
 
 def test_segment_offsets_cache_follows_doc_ids(dev):
