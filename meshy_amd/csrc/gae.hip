@@ -32,6 +32,7 @@
 // re-reads what the chunks pass read last (still in L2 or the Infinity Cache).
 // Everything is fp32, like the reference's sequential fallback.
 #include <algorithm>
+#include <atomic>
 
 #include "common.h"
 
@@ -50,16 +51,52 @@ struct Aff {
     float p, q;  // A_before = p * A_after + q
 };
 
-// left covers earlier positions than right.
+// A map with slope -0 is "hard": it ignores its input, as the recursion does at
+// a row end, where each row of the reference's [rows, S] grid starts afresh.
+// Every other slope is >= +0 (gamma >= 0), so a product of slopes is never -0
+// by itself.  A soft cut (a document end or a mask hole, slope +0) still passes
+// a NaN or infinite input on, since 0 * NaN and 0 * inf are NaN in the
+// reference's sequential loop; a hard one does not.
+__device__ __forceinline__ bool is_hard(float p) { return __float_as_uint(p) == 0x80000000u; }
+
+// left covers earlier positions than right.  kHard: hard if either is, and a
+// hard left map ignores the right one.  Without kHard, plain composition: the
+// same values whenever every input is finite (a row end's slope is a zero
+// either way), and cheaper; the kernels take it unless the call holds a
+// non-finite term.
+template <bool kHard>
 __device__ __forceinline__ Aff compose(Aff left, Aff right) {
-    return Aff{left.p * right.p, fmaf(left.p, right.q, left.q)};
+    if constexpr (kHard) {
+        const bool hl = is_hard(left.p);
+        const bool h = hl || is_hard(right.p);
+        return Aff{h ? -0.f : left.p * right.p, hl ? left.q : fmaf(left.p, right.q, left.q)};
+    } else {
+        return Aff{left.p * right.p, fmaf(left.p, right.q, left.q)};
+    }
 }
+
+// The map applied to a value: a hard map ignores it.
+template <bool kHard>
+__device__ __forceinline__ float apply_map(Aff f, float x) {
+    if constexpr (kHard) return is_hard(f.p) ? f.q : fmaf(f.p, x, f.q);
+    return fmaf(f.p, x, f.q);
+}
+
+// Set (atomic max) by the chunks pass to the call's epoch when some chunk holds
+// a non-finite term (a NaN or infinite advantage or return term at a valid
+// position).  The apply pass then composes with hardness and folds its carry
+// up to the row's end instead of stopping at the first cut, which a non-finite
+// value crosses in the reference.  Epochs grow per call, so no clearing is
+// needed and calls on other streams can only send a call down the slower,
+// exact path.
+__device__ unsigned long long g_gae_nonfinite_epoch = 0;
 
 struct Pair {
     Aff adv, ret;
 };
+template <bool kHard>
 __device__ __forceinline__ Pair compose(const Pair& l, const Pair& r) {
-    return Pair{compose(l.adv, r.adv), compose(l.ret, r.ret)};
+    return Pair{compose<kHard>(l.adv, r.adv), compose<kHard>(l.ret, r.ret)};
 }
 __device__ __forceinline__ Pair identity_pair() { return Pair{Aff{1.f, 0.f}, Aff{1.f, 0.f}}; }
 
@@ -259,12 +296,15 @@ __device__ __forceinline__ void load_inputs(const meshy_gae_args& g, int64_t c0,
 // Row ends come from a column counter started with one division; lambda is
 // recomputed only when the document changes.
 __device__ __forceinline__ void thread_maps(const meshy_gae_args& g, const float* cnt, int64_t c0, int64_t t0,
-                                            int64_t n, bool vec, Pair (&items)[kItems]) {
+                                            int64_t n, bool vec, Pair (&items)[kItems], uint32_t& valid_bits,
+                                            bool& has_row_end) {
     ThreadInputs in;
     load_inputs(g, c0, t0, n, vec, in);
     int64_t s = t0 % g.S;
     int64_t cur_d = -2;
     float cur_lam = 0.f;
+    valid_bits = 0;
+    has_row_end = false;
 #pragma unroll
     for (int k = 0; k < kItems; ++k) {
         if (t0 + k >= n) {
@@ -272,6 +312,7 @@ __device__ __forceinline__ void thread_maps(const meshy_gae_args& g, const float
             continue;
         }
         const bool row_end = (s == g.S - 1);
+        has_row_end |= row_end;
         s = row_end ? 0 : s + 1;
         const float mk = in.mk[k];
         const bool valid = mk > 0.f;
@@ -287,8 +328,9 @@ __device__ __forceinline__ void thread_maps(const meshy_gae_args& g, const float
         const float validf = valid ? 1.f : 0.f;
         const float r = in.r[k];
         const float delta = (r + g.gamma * vn * contf - in.v[k]) * validf;
-        items[k].adv = Aff{(g.gamma * cur_lam) * contf, valid ? delta : 0.f};
-        items[k].ret = Aff{g.gamma * contf, valid ? r : 0.f};
+        items[k].adv = Aff{row_end ? -0.f : (g.gamma * cur_lam) * contf, valid ? delta : 0.f};
+        items[k].ret = Aff{row_end ? -0.f : g.gamma * contf, valid ? r : 0.f};
+        valid_bits |= valid ? (1u << k) : 0u;
     }
 }
 
@@ -318,12 +360,14 @@ __device__ __forceinline__ Pair lane_pair(const Pair& v, int l) {
 // shifts (lanes 0, 16, 32, 48 then hold their row's fold), then
 // (row 0 o row 1) o (row 2 o row 3) from those lanes.  The result is in
 // every lane.  All 64 lanes must be active.
+template <bool kHard>
 __device__ __forceinline__ Pair wave_fold(Pair x) {
-    x = compose(x, dpp_pair<kDppRowShl1>(x));
-    x = compose(x, dpp_pair<kDppRowShl2>(x));
-    x = compose(x, dpp_pair<kDppRowShl4>(x));
-    x = compose(x, dpp_pair<kDppRowShl8>(x));
-    return compose(compose(lane_pair(x, 0), lane_pair(x, 16)), compose(lane_pair(x, 32), lane_pair(x, 48)));
+    x = compose<kHard>(x, dpp_pair<kDppRowShl1>(x));
+    x = compose<kHard>(x, dpp_pair<kDppRowShl2>(x));
+    x = compose<kHard>(x, dpp_pair<kDppRowShl4>(x));
+    x = compose<kHard>(x, dpp_pair<kDppRowShl8>(x));
+    return compose<kHard>(compose<kHard>(lane_pair(x, 0), lane_pair(x, 16)),
+                          compose<kHard>(lane_pair(x, 32), lane_pair(x, 48)));
 }
 
 // Suffix composition across the block (lane order, lane 0 leftmost): for each
@@ -332,6 +376,7 @@ __device__ __forceinline__ Pair wave_fold(Pair x) {
 // then holds its row's suffix from l); the rows' folds, read from lanes 0, 16,
 // 32 and 48, complete each lane's suffix to the wave's end; the waves meet in
 // LDS.  All 64 lanes of every wave must be active.
+template <bool kHard>
 __device__ __forceinline__ Pair block_suffix_exclusive(Pair mine, Pair* s_wave, Pair& total) {
     const int lane = threadIdx.x % kWave;
     const int wid = threadIdx.x / kWave;
@@ -340,37 +385,37 @@ __device__ __forceinline__ Pair block_suffix_exclusive(Pair mine, Pair* s_wave, 
     Pair incl = mine;
     {
         const Pair o = dpp_pair<kDppRowShl1>(incl);
-        incl = rl + 1 < 16 ? compose(incl, o) : incl;
+        incl = rl + 1 < 16 ? compose<kHard>(incl, o) : incl;
     }
     {
         const Pair o = dpp_pair<kDppRowShl2>(incl);
-        incl = rl + 2 < 16 ? compose(incl, o) : incl;
+        incl = rl + 2 < 16 ? compose<kHard>(incl, o) : incl;
     }
     {
         const Pair o = dpp_pair<kDppRowShl4>(incl);
-        incl = rl + 4 < 16 ? compose(incl, o) : incl;
+        incl = rl + 4 < 16 ? compose<kHard>(incl, o) : incl;
     }
     {
         const Pair o = dpp_pair<kDppRowShl8>(incl);
-        incl = rl + 8 < 16 ? compose(incl, o) : incl;
+        incl = rl + 8 < 16 ? compose<kHard>(incl, o) : incl;
     }
     const Pair r0 = lane_pair(incl, 0);
     const Pair r3 = lane_pair(incl, 48);
-    const Pair a1 = compose(lane_pair(incl, 32), r3);  // rows 2, 3
-    const Pair a0 = compose(lane_pair(incl, 16), a1);  // rows 1, 2, 3
+    const Pair a1 = compose<kHard>(lane_pair(incl, 32), r3);  // rows 2, 3
+    const Pair a0 = compose<kHard>(lane_pair(incl, 16), a1);  // rows 1, 2, 3
     const int row = lane / 16;
     const Pair after_row = row == 0 ? a0 : (row == 1 ? a1 : (row == 2 ? r3 : identity_pair()));
-    incl = compose(incl, after_row);  // lane l .. lane 63
-    if (lane == 0) s_wave[wid] = compose(r0, a0);  // whole-wave map
+    incl = compose<kHard>(incl, after_row);  // lane l .. lane 63
+    if (lane == 0) s_wave[wid] = compose<kHard>(r0, a0);  // whole-wave map
     __syncthreads();
     Pair after_wave = identity_pair();
-    for (int w = kW - 1; w > wid; --w) after_wave = compose(s_wave[w], after_wave);
+    for (int w = kW - 1; w > wid; --w) after_wave = compose<kHard>(s_wave[w], after_wave);
     total = identity_pair();
-    for (int w = kW - 1; w >= 0; --w) total = compose(s_wave[w], total);
+    for (int w = kW - 1; w >= 0; --w) total = compose<kHard>(s_wave[w], total);
     __syncthreads();
     // exclusive within the wave = inclusive of the next lane
     const Pair next = dpp_pair<kDppWaveShl1>(incl);
-    return lane + 1 < kWave ? compose(next, after_wave) : after_wave;
+    return lane + 1 < kWave ? compose<kHard>(next, after_wave) : after_wave;
 }
 
 __global__ __launch_bounds__(kThreads) void k_gae_zero(float* p, int64_t n) {
@@ -418,30 +463,60 @@ __global__ __launch_bounds__(kCountThreads) void k_gae_doc_count(const float* __
     if (threadIdx.x == 0) cnt[d] = acc;
 }
 
-// Builds the thread's maps (contiguous positions) and folds them right to left.
-__device__ __forceinline__ Pair load_items(const meshy_gae_args& g, const float* cnt, int64_t c0, int64_t t0,
-                                           int64_t n, bool vec, Pair (&items)[kItems]) {
-    thread_maps(g, cnt, c0, t0, n, vec, items);
+// The thread's maps (contiguous positions) folded right to left.
+template <bool kHard>
+__device__ __forceinline__ Pair fold_items(const Pair (&items)[kItems]) {
     Pair agg = identity_pair();
 #pragma unroll
-    for (int k = kItems - 1; k >= 0; --k) agg = compose(items[k], agg);
+    for (int k = kItems - 1; k >= 0; --k) agg = compose<kHard>(items[k], agg);
     return agg;
 }
 
-__global__ __launch_bounds__(kThreads) void k_gae_chunks(meshy_gae_args g, Workspace ws, int64_t n, bool vec) {
+// The chunk's map, composed in every wave (each wave folds the waves' maps from
+// LDS, so every thread holds the result).
+template <bool kHard>
+__device__ __forceinline__ Pair chunk_map(const Pair (&items)[kItems], Pair* s_wave) {
+    const Pair wf = wave_fold<kHard>(fold_items<kHard>(items));
+    if (threadIdx.x % kWave == 0) s_wave[threadIdx.x / kWave] = wf;
+    __syncthreads();
+    Pair total = identity_pair();
+    for (int w = kThreads / kWave - 1; w >= 0; --w) total = compose<kHard>(s_wave[w], total);
+    return total;
+}
+
+// A plain fold is NaN or infinite exactly when one of its terms is (0 * NaN,
+// 0 * inf and NaN + x are all NaN), so the plain chunk map tells whether the
+// chunk holds a non-finite term; only then is the map composed again with
+// hardness.  A plain map takes its hardness (a row end in the chunk) from the
+// positions.
+__global__ __launch_bounds__(kThreads) void k_gae_chunks(meshy_gae_args g, Workspace ws, int64_t n, bool vec,
+                                                         unsigned long long epoch) {
     __shared__ Pair s_wave[kThreads / kWave];
+    __shared__ Pair s_wave_hard[kThreads / kWave];
+    __shared__ int s_row_end[kThreads / kWave];
     const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
     const int64_t t0 = c0 + static_cast<int64_t>(threadIdx.x) * kItems;
     Pair items[kItems];
-    const Pair mine = load_items(g, ws.cnt, c0, t0, n, vec, items);
-    // The chunk's map: each wave's fold, then the waves in order.
-    const Pair wf = wave_fold(mine);
-    if (threadIdx.x % kWave == 0) s_wave[threadIdx.x / kWave] = wf;
-    __syncthreads();
+    uint32_t valid_bits;
+    bool has_row_end;
+    thread_maps(g, ws.cnt, c0, t0, n, vec, items, valid_bits, has_row_end);
+    const bool wave_row_end = __ballot(has_row_end) != 0;
+    if (threadIdx.x % kWave == 0) s_row_end[threadIdx.x / kWave] = wave_row_end;
+    Pair total = chunk_map<false>(items, s_wave);  // its barrier publishes s_row_end
+    const bool nonfinite = !isfinite(total.adv.q) || !isfinite(total.ret.q);  // the same in every thread
+    if (nonfinite) {
+        total = chunk_map<true>(items, s_wave_hard);
+    } else {
+        bool hard = false;
+        for (int w = 0; w < kThreads / kWave; ++w) hard |= s_row_end[w] != 0;
+        if (hard) {
+            total.adv.p = -0.f;
+            total.ret.p = -0.f;
+        }
+    }
     if (threadIdx.x == 0) {
-        Pair total = identity_pair();
-        for (int w = kThreads / kWave - 1; w >= 0; --w) total = compose(s_wave[w], total);
         ws.chunk[blockIdx.x] = total;
+        if (nonfinite) atomicMax(&g_gae_nonfinite_epoch, epoch);
     }
 }
 
@@ -464,31 +539,32 @@ __device__ __forceinline__ int64_t apply_chunk(int64_t b, int64_t nc) {
     return x + kXcds * (m - 1 - i);
 }
 
-__global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Workspace ws, int64_t n, int64_t nc,
-                                                        bool vec) {
-    __shared__ Pair s_wave[kThreads / kWave];
-    __shared__ float s_carry[2];
-    const int64_t c = apply_chunk(blockIdx.x, nc);
+// The apply pass of chunk c.  kHard (a non-finite term somewhere in the call):
+// compose with hardness and fold the carry up to the first chunk holding a row
+// end; otherwise plainly, up to the first chunk that cuts both scans.
+template <bool kHard>
+__device__ __forceinline__ void apply_chunk_pass(const meshy_gae_args& g, const Workspace& ws, int64_t n,
+                                                 int64_t nc, bool vec, int64_t c, Pair* s_wave, float* s_carry,
+                                                 Pair r, const Pair (&items)[kItems], uint32_t valid_bits) {
     const int64_t t0 = c * kChunk + static_cast<int64_t>(threadIdx.x) * kItems;
     const int lane = threadIdx.x % kWave;
     // The carry-in: the chunks to the right of c in order, up to and including
-    // the first whose map cuts both scans (both slopes exactly 0: a document
-    // end, a row end or a mask hole lies in it), past which nothing reaches c.
-    // Their maps come 64 at a time; the first 64 load before the chunk's
-    // inputs, in every wave (indices clamped into range), and wave 0 alone
-    // folds them: loads under a condition would compile to a branch that
-    // waits for them before the inputs are issued.  A further 64 load only
-    // when a document runs on past them (more than 128 k tokens).
-    Pair r = ws.chunk[min(c + 1 + lane, nc - 1)];
-    Pair items[kItems];
-    const Pair mine = load_items(g, ws.cnt, c * kChunk, t0, n, vec, items);
-    if (threadIdx.x < kWave) {
+    // the first whose map cuts both scans (both slopes zero: a document end, a
+    // row end or a mask hole lies in it; with kHard, a row end), past which
+    // nothing reaches c.  Their maps come 64 at a time; the first 64 load
+    // before the chunk's inputs, in every wave (indices clamped into range),
+    // and wave 0 alone folds them: loads under a condition would compile to a
+    // branch that waits for them before the inputs are issued.  A further 64
+    // load only when a document runs on past them (more than 128 k tokens).
+    const Pair mine = fold_items<kHard>(items);
+    if (threadIdx.x < kWave) {  // r is this wave's copy of the first 64 maps
         Pair carry = identity_pair();
         for (int64_t j0 = c + 1; j0 < nc; j0 += kWave) {
             const bool in = j0 + lane < nc;
-            const uint64_t cuts = __ballot(in && r.adv.p == 0.f && r.ret.p == 0.f);
+            const bool cut = kHard ? (is_hard(r.adv.p) && is_hard(r.ret.p)) : (r.adv.p == 0.f && r.ret.p == 0.f);
+            const uint64_t cuts = __ballot(in && cut);
             const int first = cuts ? __builtin_ctzll(cuts) : kWave;
-            carry = compose(carry, wave_fold((in && lane <= first) ? r : identity_pair()));
+            carry = compose<kHard>(carry, wave_fold<kHard>((in && lane <= first) ? r : identity_pair()));
             if (cuts) break;
             r = ws.chunk[min(j0 + kWave + lane, nc - 1)];
         }
@@ -499,16 +575,18 @@ __global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Worksp
         }
     }
     Pair total;
-    const Pair excl = block_suffix_exclusive(mine, s_wave, total);  // its barriers publish s_carry
-    float A = fmaf(excl.adv.p, s_carry[0], excl.adv.q);
-    float G = fmaf(excl.ret.p, s_carry[1], excl.ret.q);
+    const Pair excl = block_suffix_exclusive<kHard>(mine, s_wave, total);  // its barriers publish s_carry
+    float A = apply_map<kHard>(excl.adv, s_carry[0]);
+    float G = apply_map<kHard>(excl.ret, s_carry[1]);
     float outA[kItems], outG[kItems];
 #pragma unroll
     for (int k = kItems - 1; k >= 0; --k) {
-        A = fmaf(items[k].adv.p, A, items[k].adv.q);
-        G = fmaf(items[k].ret.p, G, items[k].ret.q);
-        outA[k] = A;
-        outG[k] = G;
+        A = apply_map<kHard>(items[k].adv, A);
+        G = apply_map<kHard>(items[k].ret, G);
+        // Zero outside valid (gae.py:180), whatever the recursion carries there.
+        const bool valid = (valid_bits >> k) & 1u;
+        outA[k] = valid ? A : 0.f;
+        outG[k] = valid ? G : 0.f;
     }
     if (vec && t0 + kItems <= n) {
 #pragma unroll
@@ -529,6 +607,25 @@ __global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Worksp
             }
         }
     }
+}
+
+__global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Workspace ws, int64_t n, int64_t nc,
+                                                        bool vec, unsigned long long epoch) {
+    __shared__ Pair s_wave[kThreads / kWave];
+    __shared__ float s_carry[2];
+    const int64_t c = apply_chunk(blockIdx.x, nc);
+    const bool hard_call = g_gae_nonfinite_epoch >= epoch;
+    // Every load of both paths is issued before the branch.
+    const Pair r = ws.chunk[min(c + 1 + static_cast<int64_t>(threadIdx.x % kWave), nc - 1)];
+    Pair items[kItems];
+    uint32_t valid_bits;
+    bool has_row_end;
+    thread_maps(g, ws.cnt, c * kChunk, c * kChunk + static_cast<int64_t>(threadIdx.x) * kItems, n, vec, items,
+                valid_bits, has_row_end);
+    if (hard_call)
+        apply_chunk_pass<true>(g, ws, n, nc, vec, c, s_wave, s_carry, r, items, valid_bits);
+    else
+        apply_chunk_pass<false>(g, ws, n, nc, vec, c, s_wave, s_carry, r, items, valid_bits);
     if (g.lam_doc) write_lambda(g, ws.cnt, static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x,
                                 static_cast<int64_t>(gridDim.x) * kThreads);
 }
@@ -687,8 +784,12 @@ extern "C" size_t meshy_gae_workspace_size(int64_t rows, int64_t S, int64_t n_do
 namespace meshy {
 namespace {
 
+// The calls' epochs for g_gae_nonfinite_epoch (process-wide; only growth matters).
+std::atomic<unsigned long long> g_gae_epoch{0};
+
 int gae_launch(const meshy_gae_args& g, hipStream_t stream) {
     if (g.rows < 0 || g.S < 0 || g.n_docs < 0) return set_error(MESHY_EINVAL, "meshy_gae: negative sizes");
+    if (!(g.gamma >= 0.f)) return set_error(MESHY_EINVAL, "meshy_gae: gamma must be non-negative");
     const int64_t n = g.rows * g.S;
     // Without tokens the per-token arrays may be NULL (an empty tensor has no
     // storage); lambda per document is still written.
@@ -728,9 +829,12 @@ int gae_launch(const meshy_gae_args& g, hipStream_t stream) {
     const bool vec = al16(g.rewards) && al16(g.mask) && al16(g.doc_ids) && (!g.values || al16(g.values)) &&
                      (!g.adv || al16(g.adv)) && (!g.returns || al16(g.returns));
     if (nc > 0 && (g.adv || g.returns)) {
-        hipLaunchKernelGGL(k_gae_chunks, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, vec);
+        const unsigned long long epoch = g_gae_epoch.fetch_add(1, std::memory_order_relaxed) + 1;
+        hipLaunchKernelGGL(k_gae_chunks, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, vec,
+                           epoch);
         if ((rc = check_launch("meshy_gae(chunks)"))) return rc;
-        hipLaunchKernelGGL(k_gae_apply, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, nc, vec);
+        hipLaunchKernelGGL(k_gae_apply, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, nc, vec,
+                           epoch);
         if ((rc = check_launch("meshy_gae(apply)"))) return rc;
     } else if (g.lam_doc && g.n_docs > 0) {
         const unsigned nb = static_cast<unsigned>(std::min<int64_t>(1024, ceil_div(g.n_docs, kThreads)));

@@ -555,3 +555,68 @@ def test_vector_and_scalar_loads_and_renamed_ids_give_bitwise_equal_results(dev,
     assert torch.equal(a3, a4) and torch.equal(r3, r4)
     with pytest.raises(ValueError, match="doc_ids must lie"):
         gae_and_returns(d[0], d[1], d[2], neg, n_docs, lengths=lengths.to(dev), **kw)
+
+
+def _assert_like_oracle(got, ref, what):
+    got = got.cpu()
+    assert torch.equal(torch.isnan(got), torch.isnan(ref)), f"{what}: NaN pattern"
+    inf = torch.isinf(ref)
+    assert torch.equal(got[inf], ref[inf]), f"{what}: infinities"
+    fin = torch.isfinite(ref)
+    assert (got[fin] - ref[fin]).abs().max().item() <= TOL, what
+
+
+@pytest.mark.parametrize("bf16", [False, True])
+def test_nonfinite_inputs_follow_the_sequential_loop(dev, bf16):
+    """NaN and infinite rewards or values, against the reference's sequential
+    recursion (gae.py:162-180), where 0 * NaN is NaN: a non-finite term at a
+    valid position reaches every valid position to its left in its row, across
+    document ends, mask holes and chunk boundaries, and stops at the row's start
+    (each row of the [rows, S] grid runs its own loop).  Rows of 5000 positions
+    (row ends inside 2048-token chunks), then one row of 20000 with the NaN near
+    its end (the carry folds across nine chunks), then a finite call again."""
+    from meshy_amd.gae import gae_and_returns
+
+    rewards, values, mask, doc_ids, n_docs = _random_grid(3, 5000, 4, seed=91)
+    mask[:, 2000:2100] = 0.0
+    mask[:, 3000:3100] = 1.0
+    rewards[0, 2050] = float("nan")   # invalid position: nothing changes
+    values[1, 3050] = float("nan")    # valid: row 1 up to 3050 (and 3049's delta) turns NaN
+    rewards[2, 3060] = float("inf")   # valid: inf within its run, NaN across the cuts before it
+    vals = values.to(torch.bfloat16) if bf16 else values
+    lengths = torch.full((n_docs,), 20.0)
+    ref_adv, _ = ogae.compute_vapo_gae(rewards, vals.float(), mask, doc_ids, n_docs, lengths=lengths, gamma=0.99,
+                                       alpha=1.5)
+    ref_ret = ogae.compute_returns(rewards, mask, doc_ids, gamma=0.99)
+    d = [t.to(dev) for t in (rewards, vals, mask, doc_ids)]
+    adv, ret, _ = gae_and_returns(*d, n_docs, lengths=lengths.to(dev), gamma=0.99, alpha=1.5)
+    _assert_like_oracle(adv, ref_adv, "advantages")
+    _assert_like_oracle(ret, ref_ret, "returns")
+    assert torch.isfinite(ref_adv[0]).all() and torch.isnan(ref_adv[1, :3000]).any()
+    assert torch.isfinite(ref_adv[1, 3100:]).all() and torch.isnan(ref_ret[2, :3000]).any()
+
+    # One row: the NaN near the end reaches back over every document and chunk.
+    r1, v1, m1, ids1, nd1 = _random_grid(1, 20000, 12, seed=92)
+    m1[0, 19990] = 1.0
+    r1[0, 19990] = float("nan")
+    ref_adv, _ = ogae.compute_vapo_gae(r1, v1, m1, ids1, nd1, gamma=1.0, alpha=1.5)
+    ref_ret = ogae.compute_returns(r1, m1, ids1, gamma=1.0)
+    adv, ret, _ = gae_and_returns(*[t.to(dev) for t in (r1, v1, m1, ids1)], nd1, gamma=1.0, alpha=1.5)
+    _assert_like_oracle(adv, ref_adv, "one row, advantages")
+    _assert_like_oracle(ret, ref_ret, "one row, returns")
+    assert torch.isnan(ref_ret[0, :19991][m1[0, :19991] > 0]).all()
+
+    # Finite inputs after a call with non-finite ones: the same results as ever.
+    r2, v2, m2, ids2, nd2 = _random_grid(2, 7000, 5, seed=93)
+    ref_adv, _ = ogae.compute_vapo_gae(r2, v2, m2, ids2, nd2, gamma=1.0, alpha=1.5)
+    adv, ret, _ = gae_and_returns(*[t.to(dev) for t in (r2, v2, m2, ids2)], nd2, gamma=1.0, alpha=1.5)
+    assert (adv.cpu() - ref_adv).abs().max().item() <= TOL
+    assert torch.isfinite(adv).all() and torch.isfinite(ret).all()
+
+
+def test_negative_gamma_is_refused(dev):
+    from meshy_amd.gae import compute_returns
+
+    z = torch.zeros(1, 8, device=dev)
+    with pytest.raises(ValueError, match="gamma"):
+        compute_returns(z, z + 1, torch.zeros(1, 8, dtype=torch.long, device=dev), gamma=-0.5)
