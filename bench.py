@@ -1055,31 +1055,22 @@ def bench_rollout_metrics(runs, no_cpu):
 
 # ---------------------------------------------------------------- end to end
 
-def bench_group_plugins(runs, no_cpu):
-    """The rollout worker's per-group plugins (rollout.py:88-115) on groups of 8
-    samples, next to the batched device forms over all 32 groups of the 256-sample
-    GRPO batch (one host-to-device copy, one launch, one copy back)."""
-    from types import SimpleNamespace
-
+def bench_group_advantages(runs, no_cpu):
+    """GRPO advantages and the zero-variance filter of a whole step (the 32
+    groups of 8 of the 256-sample GRPO batch) in one device call each (the
+    rewards' host-to-device copy, one launch, the copy back), next to the
+    reference's per-group host functions (rollout.py:88-115) called once per
+    group as its rollout worker does, summed over the 32 groups."""
     import numpy as np
     import torch
 
     from meshy_amd import workloads
-    from meshy_amd.advantage import grpo_advantage, grpo_advantages, is_zero_variance_group, zero_variance_groups
+    from meshy_amd.advantage import grpo_advantages, zero_variance_groups
 
     dev = torch.device("cuda:0")
     _, rewards, group_offsets = workloads.grpo_256_samples(0)
     n_groups = len(group_offsets) - 1
-    groups = [[SimpleNamespace(reward=float(r), raw_reward=None, advantage=None)
-               for r in rewards[group_offsets[g]:group_offsets[g + 1]]] for g in range(n_groups)]
-    assert all(len(g) == 8 for g in groups)
     reps = max(runs, 10)
-
-    def per_group(fn):
-        def run():
-            for g in groups:
-                fn(g)
-        return _wall_ms(run, reps, gpu=False) * 1e3 / n_groups
 
     def batched(fn, dtype):
         def run():
@@ -1089,25 +1080,24 @@ def bench_group_plugins(runs, no_cpu):
 
     out = {
         "group_size": 8, "n_groups": n_groups,
-        "grpo_advantage_plugin_us_per_group": round(per_group(lambda g: grpo_advantage(g, device=dev)), 1),
-        "grpo_advantages_batched_us_all_groups": round(batched(grpo_advantages, np.float32), 1),
-        "is_zero_variance_group_plugin_us_per_group": round(per_group(lambda g: is_zero_variance_group(g, device=dev)),
-                                                            1),
-        "zero_variance_groups_batched_us_all_groups": round(batched(zero_variance_groups, np.float64), 1),
+        "grpo_advantages_us_all_groups": round(batched(grpo_advantages, np.float32), 1),
+        "zero_variance_groups_us_all_groups": round(batched(zero_variance_groups, np.float64), 1),
     }
     if not no_cpu:
         from oracle import grpo as ogrpo
 
+        groups = [[float(r) for r in rewards[group_offsets[g]:group_offsets[g + 1]]] for g in range(n_groups)]
+
+        def per_group_total(fn):
+            def run():
+                for g in groups:
+                    fn(g)
+            return _wall_ms(run, reps, gpu=False) * 1e3
+
         # The reference's arithmetic on the host: CPU torch for the advantages,
         # Python builtins for the filter.
-        def ref_grpo(g):
-            adv = ogrpo.grpo_group([s.reward for s in g])
-            for s, a in zip(g, adv):
-                s.advantage = a
-
-        out["grpo_advantage_cpu_torch_us_per_group"] = round(per_group(ref_grpo), 1)
-        out["is_zero_variance_group_cpu_us_per_group"] = round(
-            per_group(lambda g: ogrpo.zero_variance_group([s.reward for s in g])), 2)
+        out["reference_grpo_advantage_us_all_groups"] = round(per_group_total(ogrpo.grpo_group), 1)
+        out["reference_is_zero_variance_group_us_all_groups"] = round(per_group_total(ogrpo.zero_variance_group), 1)
     return out
 
 
@@ -1234,7 +1224,7 @@ LEGS = {
     "long_context": lambda a: bench_long_context(max(3, a.steps // 10), 2, a.no_cpu),
     "pack_long_context": lambda a: bench_pack_long_context(10, a.no_cpu),
     "rollout_metrics": lambda a: bench_rollout_metrics(10, a.no_cpu),
-    "group_plugins": lambda a: bench_group_plugins(10, a.no_cpu),
+    "group_advantages": lambda a: bench_group_advantages(10, a.no_cpu),
     "end_to_end": lambda a: bench_end_to_end(5, a.no_cpu),
 }
 
@@ -1345,7 +1335,7 @@ def main() -> int:
         kernels["attach_gae_1024_docs"] = bench_attach_gae(5, args.no_cpu)
         kernels["pack_16_long_sequences"] = bench_pack_long_context(10, args.no_cpu)
         kernels["rollout_metrics_256_samples"] = bench_rollout_metrics(10, args.no_cpu)
-        kernels["group_plugins_32_groups_of_8"] = bench_group_plugins(10, args.no_cpu)
+        kernels["group_advantages_32_groups_of_8"] = bench_group_advantages(10, args.no_cpu)
         result["kernels"] = kernels
         result["end_to_end"] = bench_end_to_end(5, args.no_cpu)
         if result.get("cpu_baseline"):

@@ -1,24 +1,23 @@
 """GRPO group-normalised advantages (meshy/worker/rollout.py:88-97) and the
-zero-variance group filter (rollout.py:100-115).
+zero-variance group filter (rollout.py:100-115), for every group of a step at
+once.
 
-``grpo_advantage(samples)`` keeps the advantage-plugin contract of the
-rollout worker (called as ``fn(group, **kwargs)``, mutates
-``sample.advantage``, rollout.py:580-587).  ``grpo_advantages`` normalises
-every group of a batch in one launch on the device, which is what the packed
-pipeline uses: a size-1 group keeps its reward, any other group gets
-``(r - mean) / clamp(unbiased std, min=1e-8)``.
+``grpo_advantages(rewards, group_offsets)`` normalises all groups in one launch
+on the device: a size-1 group keeps its reward, any other group gets
+``(r - mean) / clamp(unbiased std, min=1e-8)``.  ``pack_step`` runs it on the
+rewards it uploads with the samples.  ``zero_variance_groups`` flags every
+group whose raw rewards are all equal within a tolerance, in one launch.
 
-``zero_variance_groups`` flags every group of a batch whose raw rewards are
-all equal within a tolerance, in one launch; ``is_zero_variance_group(samples)``
-keeps the reference's per-group signature.  The per-group forms cost a
-host-to-device copy, a launch and a synchronisation per group, more than the
-reference's host arithmetic over a handful of scalars: callers that hold a
-whole batch of groups use the batched forms.
+The reference calls its two functions once per completed group of the rollout
+worker (rollout.py:572, 580-587).  A device call per group of a few scalars
+costs a copy, a launch and a synchronisation, several times the reference's
+host arithmetic, so no per-group form is offered: the advantages are computed
+once per step over every group (the worker's ``advantage`` plugin is then left
+unset), and a filter that must decide as each group completes keeps the
+reference's host function.
 """
 
 from __future__ import annotations
-
-from typing import Any
 
 import torch
 
@@ -38,22 +37,6 @@ def grpo_advantages(rewards: torch.Tensor, group_offsets: torch.Tensor) -> torch
                                           _lib.stream_of(r.device))
     _lib.check(rc, "meshy_grpo_advantage")
     return adv
-
-
-def grpo_advantage(samples: list[Any], device: torch.device | str | None = None) -> None:
-    """Plugin form: one group, ``sample.advantage`` set to a Python float."""
-    if not samples:
-        return
-    if len(samples) == 1:
-        # A size-1 group keeps its reward object as is (rollout.py:91-93).
-        samples[0].advantage = samples[0].reward
-        return
-    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    rewards = torch.tensor([float(s.reward) for s in samples], dtype=torch.float32).to(dev)
-    off = torch.tensor([0, len(samples)], dtype=torch.int64).to(dev)
-    adv = grpo_advantages(rewards, off).tolist()
-    for s, a in zip(samples, adv):
-        s.advantage = float(a)
 
 
 def zero_variance_groups(raw_rewards: torch.Tensor, group_offsets: torch.Tensor,
@@ -76,19 +59,4 @@ def zero_variance_groups(raw_rewards: torch.Tensor, group_offsets: torch.Tensor,
     return flags.view(torch.bool)
 
 
-def is_zero_variance_group(samples: list[Any], *, tolerance: float = 1e-8,
-                           device: torch.device | str | None = None) -> bool:
-    """Plugin form (rollout.py:100-115): whether all raw rewards of a completed
-    group are equal.  The raw reward (``sample.raw_reward`` when set, else
-    ``sample.reward``) is used, so length shaping does not hide a group whose
-    outcomes were all the same."""
-    if not samples:
-        return True
-    dev = torch.device(device) if device is not None else torch.device("cuda", torch.cuda.current_device())
-    raw = [float(s.reward if getattr(s, "raw_reward", None) is None else s.raw_reward) for s in samples]
-    r = torch.tensor(raw, dtype=torch.float64).to(dev)
-    off = torch.tensor([0, len(raw)], dtype=torch.int64).to(dev)
-    return bool(zero_variance_groups(r, off, tolerance).item())
-
-
-__all__ = ["grpo_advantage", "grpo_advantages", "is_zero_variance_group", "zero_variance_groups"]
+__all__ = ["grpo_advantages", "zero_variance_groups"]

@@ -5,7 +5,6 @@ tests/test_rollout_advantage.py:13-18).  Indices and copies are bit-exact."""
 from __future__ import annotations
 
 import math
-from types import SimpleNamespace
 
 import numpy as np
 import pytest
@@ -280,24 +279,21 @@ def test_cpu_device_is_rejected():
 
 def test_grpo_known_answer(dev):
     # test_rollout_advantage.py:13-18 (pins the unbiased std)
-    from meshy_amd.advantage import grpo_advantage
+    from meshy_amd.advantage import grpo_advantages
 
-    samples = [SimpleNamespace(reward=r, advantage=None) for r in (1.0, 2.0, 3.0)]
-    grpo_advantage(samples, device=dev)
-    assert [s.advantage for s in samples] == pytest.approx([-1.0, 0.0, 1.0], abs=1e-6)
+    adv = grpo_advantages(torch.tensor([1.0, 2.0, 3.0], device=dev), torch.tensor([0, 3], device=dev))
+    assert adv.cpu().tolist() == pytest.approx([-1.0, 0.0, 1.0], abs=1e-6)
 
 
 def test_grpo_special_cases(dev):
-    from meshy_amd.advantage import grpo_advantage, grpo_advantages
+    from meshy_amd.advantage import grpo_advantages
 
-    one = [SimpleNamespace(reward=0.7, advantage=None)]
-    grpo_advantage(one, device=dev)
-    assert one[0].advantage == 0.7
-    r = torch.tensor([1.0, 1.0, 1.0, 0.0, 0.0, 0.5], device=dev)
-    off = torch.tensor([0, 3, 5, 6], device=dev)
+    r = torch.tensor([1.0, 1.0, 1.0, 0.0, 0.0, 0.5, 0.7], device=dev)
+    off = torch.tensor([0, 3, 5, 6, 7], device=dev)
     adv = grpo_advantages(r, off).cpu()
     assert adv[:5].abs().max() == 0.0  # all-equal groups -> 0
-    assert adv[5].item() == 0.5         # size-1 group keeps its reward
+    assert adv[5].item() == 0.5         # size-1 groups keep their reward
+    assert adv[6].item() == pytest.approx(0.7)
 
 
 def test_grpo_offsets_clamped_to_the_rewards(dev):
@@ -332,21 +328,15 @@ def test_grpo_256_samples_matches_oracle(dev):
 
 
 def test_zero_variance_known_answers(dev):
-    # test_rollout_advantage.py:90-93; the raw reward wins over the shaped one
-    from meshy_amd.advantage import is_zero_variance_group
+    # test_rollout_advantage.py:90-93, each group of the known answers in one call
+    from meshy_amd.advantage import zero_variance_groups
 
-    def group(*rewards, raw=None):
-        raw = raw or [None] * len(rewards)
-        return [SimpleNamespace(reward=r, raw_reward=w, advantage=None) for r, w in zip(rewards, raw)]
-
-    assert is_zero_variance_group(group(0.0, 0.0, 0.0), device=dev)
-    assert is_zero_variance_group(group(1.0, 1.0), device=dev)
-    assert not is_zero_variance_group(group(0.0, 1.0), device=dev)
-    assert is_zero_variance_group([], device=dev)
-    assert is_zero_variance_group(group(1.02, 0.97, 1.0, raw=[1.0, 1.0, 1.0]), device=dev)
-    assert not is_zero_variance_group(group(1.0, 1.0, raw=[1.0, 0.0]), device=dev)
-    assert not is_zero_variance_group(group(1.0, 1.0 + 2e-8), device=dev)  # float64, not float32
-    assert is_zero_variance_group(group(1, True), device=dev)               # ints and bools are floats
+    groups = [[0.0, 0.0, 0.0], [1.0, 1.0], [0.0, 1.0], [], [1.0, 1.0 + 2e-8], [1.0, 1.0]]
+    flat = torch.tensor([x for g in groups for x in g], dtype=torch.float64, device=dev)
+    off = torch.tensor(np.cumsum([0] + [len(g) for g in groups]), device=dev)
+    got = zero_variance_groups(flat, off).cpu().tolist()
+    # all equal, all equal, mixed, empty, a spread of 2e-8 (float64, not float32), all equal
+    assert got == [True, True, False, True, False, True]
 
 
 def test_zero_variance_groups_match_oracle(dev):
