@@ -134,6 +134,62 @@ def _with_device(e: dict, device_us: float, nbytes: float) -> dict:
     return e
 
 
+def _host_phases(call, runs: int = 200, warmup: int = 20) -> dict:
+    """Median host µs of each phase of one drop-in call.  ``call(mark)`` makes
+    the call, calling ``mark(name)`` at the end of each phase; the device is
+    synchronized after each call, never inside one, so a phase's figure is the
+    host time it takes to issue its work."""
+    samples: dict[str, list[float]] = {}
+
+    def run(record: bool) -> None:
+        stamps = [time.perf_counter()]
+        names = []
+
+        def mark(name: str) -> None:
+            stamps.append(time.perf_counter())
+            names.append(name)
+
+        call(mark)
+        if record:
+            for i, name in enumerate(names):
+                samples.setdefault(name, []).append((stamps[i + 1] - stamps[i]) * 1e6)
+
+    for _ in range(warmup):
+        run(False)
+        _sync()
+    for _ in range(runs):
+        run(True)
+        _sync()
+    out = {name: round(statistics.median(v), 1) for name, v in samples.items()}
+    out["total"] = round(sum(out.values()), 1)
+    return out
+
+
+def _autograd_floor_us(dev) -> float:
+    """Host µs of a custom autograd Function's forward and ``backward()`` that
+    allocate one tensor each and launch nothing: what any drop-in loss pays to
+    the autograd engine before its own work."""
+    import torch
+
+    class _Nothing(torch.autograd.Function):
+        @staticmethod
+        def forward(ctx, x):
+            return torch.empty((), device=x.device)
+
+        @staticmethod
+        def backward(ctx, g):
+            return torch.empty(1, device=g.device)
+
+    x = torch.empty(1, device=dev, requires_grad=True)
+
+    def call(mark):
+        x.grad = None
+        _Nothing.apply(x).backward()
+        mark("forward_and_backward")
+
+    return _host_phases(call)["forward_and_backward"]
+
+
 def _checked(rc: int, what: str) -> None:
     from meshy_amd import _lib
 
@@ -323,11 +379,30 @@ def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
     stub = NS(calculate_per_token_loss=False, log_prob_min_clamp=-10.0, loss_max_clamp=10.0, sharder=None)
     gd = gathered.detach().requires_grad_(True)
 
+    def fresh_micro():
+        # Each call sees a new micro-batch, as in the training loop (opd.py:207-214),
+        # which builds every micro once and takes one loss of it.
+        mb.__dict__.pop("_meshy_seg_offsets", None)
+        mb.__dict__.pop("_meshy_distill_inputs", None)
+
     def loss_fb():
-        mb.__dict__.pop("_meshy_seg_offsets", None)  # a fresh micro-batch each call
+        fresh_micro()
         gd.grad = None
         loss, _ = opd.distill_from_gathered(stub, gd, mb, mini)
         loss.backward()
+
+    def loss_phases(mark):
+        # the steps of distill_from_gathered, one mark after each
+        fresh_micro()
+        gd.grad = None
+        student = gd.reshape(-1, K + 1)
+        inputs = opd._cached_inputs(stub, mb, mini, K, student)
+        mark("inputs")
+        loss, parts = _lib.autograd().distill_loss(student, inputs.native)
+        dict(zip(_lib.DISTILL_OUT_NAMES, parts))
+        mark("forward")
+        loss.backward()
+        mark("backward")
 
     ms = _gpu_ms(loss_fb, _small(steps), warmup)
     cpu_ms = None
@@ -373,7 +448,9 @@ def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
     # offsets); bwd reads the same and writes (K+1)*4
     per_tok = (K + 1) * 4 + K * 4 + 16
     nbytes = T * (2 * per_tok + 8 + (K + 1) * 4)
-    out["distill_loss_fwd_bwd_K8_T16384"] = _with_device(_entry(ms * 1e3, nbytes, cpu_ms, tokens=T), dev_us, nbytes)
+    out["distill_loss_fwd_bwd_K8_T16384"] = _with_device(
+        _entry(ms * 1e3, nbytes, cpu_ms, tokens=T, host_phases_us=_host_phases(loss_phases),
+               note="a new micro-batch each call: its inputs are built every time"), dev_us, nbytes)
     return out
 
 
@@ -635,9 +712,29 @@ def bench_ppo(steps, warmup, no_cpu):
     # when a backward follows); bwd: unit gradient read + gradient written 8 B/token
     fwd_bytes = T * 12
     fb_bytes = T * (16 + 8)
+
+    def fb_phases(mark):
+        # the steps of ppo_clip_loss, one mark after each
+        new_d.grad = None
+        inputs = loss_mod._cached_inputs(stub, new_d, old_d, mb, mini, None)
+        flat = new_d.reshape(-1)
+        mark("inputs")
+        loss, parts = _lib.autograd().ppo_loss(flat, inputs.native)
+        dict(zip(_lib.PPO_OUT_NAMES[:12], parts[:12]))
+        mark("forward")
+        loss.backward()
+        mark("backward")
+
+    def inputs_uncached(mark):
+        loss_mod._Inputs(stub, new_d, old_d, mb, mini, None)
+        mark("inputs_uncached")
+
+    phases = _host_phases(fb_phases)
+    phases["inputs_uncached"] = _host_phases(inputs_uncached)["inputs_uncached"]
     return {
         "ppo_loss_fwd": _with_device(_entry(fwd_ms * 1e3, fwd_bytes, tokens=T), fwd0_dev, fwd_bytes),
-        "ppo_loss_fwd_bwd": _with_device(_entry(fb_ms * 1e3, fb_bytes, cpu_ms, tokens=T),
+        "ppo_loss_fwd_bwd": _with_device(_entry(fb_ms * 1e3, fb_bytes, cpu_ms, tokens=T, host_phases_us=phases,
+                                                autograd_floor_us=_autograd_floor_us(dev)),
                                          fwd_dev + bwd_dev, fb_bytes),
         "segment_offsets_us": round(off_dev, 2),
     }
@@ -925,8 +1022,18 @@ def bench_critic(steps, warmup, no_cpu):
     dev_us = _gpu_ms(dev_fb, _small(steps), warmup) * 1e3
     # fwd: v, t, o read + out written; bwd (the sum's gradient is one broadcast
     # value): v, t, o read + grad written
-    out["clipped_value_error_fwd_bwd_1024_docs"] = _with_device(_entry(ms * 1e3, T * 32, cpu_ms, tokens=T), dev_us,
-                                                                T * 32)
+    def cve_phases(mark):
+        v.grad = None
+        e = critic.clipped_value_error(v, t, o, 0.2)
+        mark("forward")
+        total = e.sum()
+        mark("reduce")
+        total.backward()
+        mark("backward")
+
+    out["clipped_value_error_fwd_bwd_1024_docs"] = _with_device(
+        _entry(ms * 1e3, T * 32, cpu_ms, tokens=T, host_phases_us=_host_phases(cve_phases),
+               note="us includes the .sum() whose gradient the backward reads"), dev_us, T * 32)
     S = int(batch.lengths.max())
     rows = n
     pos = np.arange(T) - np.repeat(batch.offsets[:-1], batch.lengths)
@@ -1217,6 +1324,7 @@ def bench_end_to_end(runs, no_cpu):
 # One workload leg each, for `--leg NAME` (the full run calls them in main).
 LEGS = {
     "pack": lambda a: bench_pack(20, a.no_cpu)[0],
+    "opd": lambda a: bench_opd(*headline_inputs(), a.steps, a.warmup, a.no_cpu),
     "ppo": lambda a: bench_ppo(a.steps, a.warmup, a.no_cpu),
     "gae": lambda a: bench_gae(a.steps, a.warmup, a.no_cpu),
     "critic": lambda a: bench_critic(a.steps, a.warmup, a.no_cpu),

@@ -386,6 +386,24 @@ def stage():
     return _STAGE
 
 
+_AUTOGRAD = None
+
+
+def autograd():
+    """The CPython extension meshy_amd._autograd (the loss drop-ins' autograd
+    nodes, built beside the library)."""
+    global _AUTOGRAD
+    if _AUTOGRAD is None:
+        load()  # the module links libmeshy_amd.so; load it (and its checks) first
+        try:
+            from . import _autograd as mod
+        except ImportError as e:
+            raise ImportError("meshy_amd._autograd is not built; run __graft_entry__.build()") from e
+        mod.set_error_type(MeshyError)
+        _AUTOGRAD = mod
+    return _AUTOGRAD
+
+
 def check(rc: int, what: str) -> None:
     """Raise the Python error matching a C-ABI return code."""
     if rc == 0:

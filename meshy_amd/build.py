@@ -30,6 +30,8 @@ PYIO_SRC = "pyio.cpp"
 PYIO_OUT = os.path.join(HERE, "_pyio" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 STAGE_SRC = "stage.cpp"
 STAGE_OUT = os.path.join(HERE, "_stage" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
+AUTOGRAD_SRC = "autograd.cpp"
+AUTOGRAD_OUT = os.path.join(HERE, "_autograd" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))
 
 ARCH = os.environ.get("MESHY_OFFLOAD_ARCH", "gfx950")
 
@@ -117,16 +119,70 @@ def build_stage(verbose: bool = False) -> str:
     return STAGE_OUT
 
 
+def _torch_host_flags() -> tuple[list[str], str]:
+    """g++ flags for host code over libtorch's headers, and torch's lib folder."""
+    import torch
+    from torch.utils import cpp_extension
+
+    abi = int(bool(getattr(torch._C, "_GLIBCXX_USE_CXX11_ABI", True)))
+    flags = [f"-D_GLIBCXX_USE_CXX11_ABI={abi}", *[f"-I{p}" for p in cpp_extension.include_paths()],
+             f"-I{sysconfig.get_paths()['include']}"]
+    return flags, os.path.join(os.path.dirname(torch.__file__), "lib")
+
+
+def _rocm_include() -> str:
+    """The ROCm include folder (beside hipcc's bin folder)."""
+    return os.path.join(os.path.dirname(os.path.dirname(os.path.realpath(hipcc()))), "include")
+
+
+def compile_autograd(verbose: bool = False) -> str:
+    """Compile csrc/autograd.cpp (the C++ autograd nodes of the loss drop-ins)
+    to an object file; returns its path."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    if cxx is None:
+        raise RuntimeError("no host C++ compiler found for meshy_amd._autograd")
+    flags, _ = _torch_host_flags()
+    obj = os.path.join(BUILD_DIR, "autograd.o")
+    # c10's HIP stream header reads the HIP runtime's declarations.
+    cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-Wall", "-c", "-D__HIP_PLATFORM_AMD__", *flags,
+           f"-I{_rocm_include()}", f"-I{os.path.join(ROOT, 'include')}", os.path.join(CSRC, AUTOGRAD_SRC), "-o", obj]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"{cxx} failed on {AUTOGRAD_SRC}:\n{res.stderr[-4000:]}")
+    return obj
+
+
+def link_autograd(obj: str, verbose: bool = False) -> str:
+    """Link meshy_amd._autograd against libmeshy_amd.so (found beside it at run
+    time) and libtorch; returns its path."""
+    cxx = shutil.which("g++") or shutil.which("c++")
+    _, libdir = _torch_host_flags()
+    tmp = AUTOGRAD_OUT + ".tmp"
+    cmd = [cxx, "-shared", obj, "-o", tmp, f"-L{HERE}", "-lmeshy_amd", f"-L{libdir}", "-ltorch_python",
+           "-ltorch_cpu", "-lc10_hip", "-lc10", "-Wl,-rpath,$ORIGIN", f"-Wl,-rpath,{libdir}"]
+    if verbose:
+        print(" ".join(cmd), flush=True)
+    res = subprocess.run(cmd, capture_output=True, text=True)
+    if res.returncode != 0:
+        raise RuntimeError(f"link of meshy_amd._autograd failed:\n{res.stderr[-4000:]}")
+    os.replace(tmp, AUTOGRAD_OUT)
+    return AUTOGRAD_OUT
+
+
 def build(verbose: bool = False) -> str:
     """Compile every source and link libmeshy_amd.so (and build meshy_amd._pyio);
     returns the library's path."""
     os.makedirs(BUILD_DIR, exist_ok=True)
-    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES) + 2, os.cpu_count() or 1)) as ex:
+    with cf.ThreadPoolExecutor(max_workers=min(len(SOURCES) + 3, os.cpu_count() or 1)) as ex:
         stage = ex.submit(build_stage, verbose)
         pyio = ex.submit(build_pyio, verbose)
+        autograd = ex.submit(compile_autograd, verbose)
         objs = list(ex.map(lambda s: _compile(s, verbose), SOURCES))
         pyio.result()
         stage.result()
+        autograd_obj = autograd.result()
     tmp = OUT + ".tmp"
     cmd = [hipcc(), f"--offload-arch={ARCH}", "-shared", "-fPIC", "-pthread", *objs, "-o", tmp]
     if verbose:
@@ -135,6 +191,7 @@ def build(verbose: bool = False) -> str:
     if res.returncode != 0:
         raise RuntimeError(f"link failed:\n{res.stderr}")
     os.replace(tmp, OUT)
+    link_autograd(autograd_obj, verbose)
     return OUT
 
 

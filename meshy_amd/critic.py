@@ -6,8 +6,8 @@
   220-275): ``meshy_critic_accumulate`` folds each ``[rows, S]`` micro-batch on
   the device; the window sums stay there until ``state`` is read, so a window
   of micro-batches costs one host synchronisation instead of five per update;
-* ``clipped_value_error`` (meshy/backend/titan/vapo.py:35-41): an autograd
-  Function over ``meshy_clipped_value_error`` and its backward.
+* ``clipped_value_error`` (meshy/backend/titan/vapo.py:35-41):
+  ``meshy_clipped_value_error`` with its backward as a C++ autograd node.
 
 * ``critic_diagnostics`` / ``diagnostics_from_states`` / ``CriticDiagnostics``
   and the gauges ``within_prompt_auc``, ``prompt_pearson``,
@@ -29,6 +29,14 @@ import torch
 from . import _lib
 from .gae import compute_returns
 from .loss import checked_segment_offsets
+
+
+def _flat_f32(t: torch.Tensor) -> torch.Tensor:
+    """``t`` as a flat contiguous fp32 tensor, a view when it already is one
+    (differentiable: ``values`` keeps its graph)."""
+    if t.dtype == torch.float32 and t.is_contiguous():
+        return t.view(-1)
+    return t.reshape(-1).to(torch.float32).contiguous()
 
 
 def advantages_to_per_sequence(adv: torch.Tensor, mask: torch.Tensor, doc_ids: torch.Tensor,
@@ -303,54 +311,20 @@ def diagnostics_from_states(states: list[AccumulatorState], *, correct_threshold
     )
 
 
-class _ClippedValueError(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, v, t, o, clip):
-        out = torch.empty_like(v)
-        has = clip is not None
-        rc = _lib.load().meshy_clipped_value_error(v.data_ptr(), t.data_ptr(), _lib.ptr(o), int(has),
-                                                   float(clip) if has else 0.0, v.numel(), out.data_ptr(),
-                                                   _lib.stream_of(v.device))
-        _lib.check(rc, "meshy_clipped_value_error")
-        ctx.save_for_backward(v, t, o if o is not None else v)
-        ctx.clip = clip
-        return out
-
-    @staticmethod
-    def backward(ctx, g):
-        v, t, o = ctx.saved_tensors
-        clip = ctx.clip
-        has = clip is not None
-        gv = torch.empty_like(v)
-        gc = g.to(torch.float32)
-        # The gradient of a sum or a mean is one value broadcast (stride 0):
-        # the kernel reads it as such instead of a materialised copy.
-        stride = 0 if gc.dim() == 1 and gc.stride(0) == 0 else 1
-        if stride:
-            gc = gc.contiguous()
-        rc = _lib.load().meshy_clipped_value_error_bwd(v.data_ptr(), t.data_ptr(), o.data_ptr() if has else None,
-                                                       int(has), float(clip) if has else 0.0, v.numel(),
-                                                       gc.data_ptr(), stride, gv.data_ptr(),
-                                                       _lib.stream_of(v.device))
-        _lib.check(rc, "meshy_clipped_value_error_bwd")
-        return gv, None, None, None
-
-
 def clipped_value_error(values: torch.Tensor, targets: torch.Tensor, old_values: torch.Tensor | None,
                         clip: float | None) -> torch.Tensor:
     """Per-token ``(v - t)^2``, or with ``clip`` the PPO-style clipped maximum
     (vapo.py:35-41); differentiable in ``values``."""
     _lib.require_gpu(values, targets, old_values if clip is not None else None)
     shape = values.shape
-    v = values.to(torch.float32).reshape(-1).contiguous()
-    t = targets.detach().to(torch.float32).reshape(-1).contiguous()
+    v = _flat_f32(values)
+    t = _flat_f32(targets.detach())
     o = None
     if clip is not None:
-        o = old_values.detach().to(torch.float32).reshape(-1).contiguous()
-    for name, x in (("targets", t), ("old_values", o)):
-        if x is not None and x.numel() != v.numel():
-            raise ValueError(f"values has {v.numel()} elements but {name} has {x.numel()}")
-    return _ClippedValueError.apply(v, t, o, clip).reshape(shape)
+        o = _flat_f32(old_values.detach())
+    # One native call (which checks the sizes); the output carries a C++
+    # backward node when values requires grad.
+    return _lib.autograd().clipped_value_error(v, t, o, None if clip is None else float(clip)).reshape(shape)
 
 
 __all__ = ["Accumulator", "AccumulatorState", "CriticDiagnostics", "advantages_to_per_sequence",

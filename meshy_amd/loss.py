@@ -8,8 +8,8 @@ attributes the reference reads (trainer.py:705-848): ``ppo_clip_eps_low/high``,
 reference's tests do.  The forward is ``meshy_ppo_loss_fwd`` (one tiled pass over
 the tokens plus one combine; with the token-mean reduction the pass also
 writes each token's unit gradient), the gradient with respect to
-``new_lp`` is ``meshy_ppo_loss_bwd``; both are wrapped in an autograd Function so
-``loss.backward()`` works as before.  ``reduce_mini_metrics`` is
+``new_lp`` is ``meshy_ppo_loss_bwd``, run by a C++ autograd node that the one
+native forward call hangs on the loss, so ``loss.backward()`` works as before.  ``reduce_mini_metrics`` is
 _reduce_mini_metrics (trainer.py:1020-1047).
 """
 
@@ -165,11 +165,17 @@ class _Inputs:
         self.cp = max(1, int(getattr(getattr(stub, "parallel_dims", None), "cp", 1) or 1))
         self.n_docs_global = int(mini.n_docs_global)
         self.n_tokens_global = int(mini.n_tokens_global)
+        # The argument struct (new_lp and grad_unit are filled per call) and
+        # the tensors it points into, held by each call's backward.
+        self.native = _lib.autograd().ppo_inputs(
+            bytes(self.args(None)),
+            (self.old, self.mask, self.rollout, self.entropy, self.adv, self.pos_w, self.ids, self.seg_off,
+             self.workspace))
 
-    def args(self, new_flat: torch.Tensor, grad_unit: torch.Tensor | None = None) -> _lib.PpoArgs:
+    def args(self, new_flat: torch.Tensor | None, grad_unit: torch.Tensor | None = None) -> _lib.PpoArgs:
         a = _lib.PpoArgs()
         a.grad_unit = _lib.ptr(grad_unit)
-        a.new_lp = new_flat.data_ptr()
+        a.new_lp = _lib.ptr(new_flat)
         a.old_lp = self.old.data_ptr()
         a.mask = self.mask.data_ptr()
         a.rollout_lp = _lib.ptr(self.rollout)
@@ -198,54 +204,7 @@ class _Inputs:
         return a
 
 
-class _PPOLoss(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, new_flat, inputs: _Inputs):
-        dev = new_flat.device
-        # out[:NOUT] receives the sums; the loss handed to autograd is a view of
-        # its total-loss entry (no copy launched).
-        buf = torch.empty(_lib.PPO_NOUT + 1, dtype=torch.float32, device=dev)
-        # Token mean: the forward also writes each token's gradient at a unit
-        # loss gradient, so the backward is one scale.  Sequence mean: the
-        # backward needs the per-document counts.
-        unit = None
-        seg_cnt = None
-        if inputs.want_grad and inputs.per_token:
-            unit = torch.empty_like(new_flat)
-        elif inputs.want_grad:
-            seg_cnt = torch.empty(inputs.n_docs + 1, dtype=torch.float32, device=dev)
-        a = inputs.args(new_flat, unit)
-        rc = _lib.load().meshy_ppo_loss_fwd(_lib.ctypes.byref(a), buf.data_ptr(), _lib.ptr(seg_cnt),
-                                            _lib.stream_of(dev))
-        _lib.check(rc, "meshy_ppo_loss_fwd")
-        ctx.inputs = inputs
-        ctx.args = a
-        ctx.save_for_backward(new_flat, seg_cnt if unit is None else unit)
-        out = buf[:_lib.PPO_NOUT]
-        loss = buf[1]
-        ctx.mark_non_differentiable(out)
-        # The backward reads only the loss's gradient: no zero tensor for `out`'s.
-        ctx.set_materialize_grads(False)
-        return loss, out
-
-    @staticmethod
-    def backward(ctx, grad_loss, grad_out):
-        if grad_loss is None:
-            return None, None
-        new_flat, saved = ctx.saved_tensors
-        g = grad_loss.reshape(1)
-        if g.dtype != torch.float32:
-            g = g.float()
-        grad = torch.empty_like(new_flat)
-        a = ctx.args  # carries grad_unit when the forward wrote it
-        seg_cnt = None if a.grad_unit else saved
-        rc = _lib.load().meshy_ppo_loss_bwd(_lib.ctypes.byref(a), _lib.ptr(seg_cnt), g.data_ptr(),
-                                            grad.data_ptr(), _lib.stream_of(new_flat.device))
-        _lib.check(rc, "meshy_ppo_loss_bwd")
-        return grad, None
-
-
-def _tensor_key(t: torch.Tensor | None) -> tuple:
+def tensor_key(t: torch.Tensor | None) -> tuple:
     return (None,) if t is None else (id(t), t._version, t.data_ptr())
 
 
@@ -254,9 +213,9 @@ def _inputs_key(stub, new_lp, old_lp, mb, mini, entropy) -> tuple:
     address, the batch's document count, the loss settings and the global
     denominators."""
     pd = getattr(stub, "parallel_dims", None)
-    return (new_lp.numel(), new_lp.device, _tensor_key(old_lp), _tensor_key(mb.mask),
-            _tensor_key(mb.rollout_logprobs), _tensor_key(entropy), _tensor_key(mb.advantages),
-            _tensor_key(mb.positive_lm_weights), _tensor_key(mb.doc_ids), int(mb.n_docs),
+    return (new_lp.numel(), new_lp.device, tensor_key(old_lp), tensor_key(mb.mask),
+            tensor_key(mb.rollout_logprobs), tensor_key(entropy), tensor_key(mb.advantages),
+            tensor_key(mb.positive_lm_weights), tensor_key(mb.doc_ids), int(mb.n_docs),
             stub.ppo_clip_eps_low, stub.ppo_clip_eps_high, stub.use_tis, getattr(stub, "use_icepop", False),
             getattr(stub, "tis_ratio_min", 0.5), getattr(stub, "tis_ratio_max", 5.0),
             getattr(stub, "positive_lm_loss_coef", 0.0), stub.calculate_per_token_loss,
@@ -264,24 +223,31 @@ def _inputs_key(stub, new_lp, old_lp, mb, mini, entropy) -> tuple:
             int(mini.n_docs_global), int(mini.n_tokens_global))
 
 
-def _cached_inputs(stub, new_lp, old_lp, mb, mini, entropy) -> _Inputs:
-    """The _Inputs of this call, reused from the batch's previous call when
-    nothing it was built from has changed (later PPO epochs over one micro).
-    The tensors are named by weak references as well as by id, since a freed
-    tensor's id and address may be reused; an in-place change bumps a version."""
-    key = _inputs_key(stub, new_lp, old_lp, mb, mini, entropy)
-    refs = (old_lp, mb.mask, mb.rollout_logprobs, entropy, mb.advantages, mb.positive_lm_weights, mb.doc_ids)
-    hit = getattr(mb, "_meshy_ppo_inputs", None)
+def batch_cached(mb: Any, attr: str, key: tuple, refs: tuple, build):
+    """``build()``'s value, kept on the batch object under ``attr`` and reused
+    while ``key`` and the tensors ``refs`` name are unchanged (later PPO epochs
+    over one micro).  The tensors are named by weak references as well as by
+    id, since a freed tensor's id and address may be reused; an in-place
+    change bumps a version, which ``key`` carries."""
+    hit = getattr(mb, attr, None)
     if hit is not None and hit[0] == key and all((r is None and t is None) or (r is not None and r() is t)
                                                  for r, t in zip(hit[2], refs)):
         return hit[1]
-    inputs = _Inputs(stub, new_lp, old_lp, mb, mini, entropy)
+    value = build()
     try:
-        object.__setattr__(mb, "_meshy_ppo_inputs",
-                           (key, inputs, tuple(None if t is None else weakref.ref(t) for t in refs)))
+        object.__setattr__(mb, attr, (key, value, tuple(None if t is None else weakref.ref(t) for t in refs)))
     except (AttributeError, TypeError):
         pass  # a batch type without an attribute dict: no cache
-    return inputs
+    return value
+
+
+def _cached_inputs(stub, new_lp, old_lp, mb, mini, entropy) -> _Inputs:
+    """The _Inputs of this call, reused from the batch's previous call when
+    nothing it was built from has changed."""
+    return batch_cached(mb, "_meshy_ppo_inputs", _inputs_key(stub, new_lp, old_lp, mb, mini, entropy),
+                        (old_lp, mb.mask, mb.rollout_logprobs, entropy, mb.advantages, mb.positive_lm_weights,
+                         mb.doc_ids),
+                        lambda: _Inputs(stub, new_lp, old_lp, mb, mini, entropy))
 
 
 def ppo_clip_loss(
@@ -299,16 +265,14 @@ def ppo_clip_loss(
             "context-parallel PPO loss needs the per-document all-reduce between the two "
             "kernel phases; this library drives one GPU")
     inputs = _cached_inputs(self, new_lp, old_lp, mb, mini, entropy)
-    inputs.want_grad = torch.is_grad_enabled() and new_lp.requires_grad
     new_flat = new_lp.reshape(-1)
     if new_flat.dtype != torch.float32:
         new_flat = new_flat.float()
     if not new_flat.is_contiguous():
         new_flat = new_flat.contiguous()
-    loss, out = _PPOLoss.apply(new_flat, inputs)
-    # One unbind makes every 0-dim view at once (indexing one by one costs
-    # more host time than the kernels).
-    parts = out.unbind(0)
+    # One native call: the forward kernels, the loss (carrying a C++ backward
+    # node when new_lp requires grad) and every sum as a 0-dim view.
+    loss, parts = _lib.autograd().ppo_loss(new_flat, inputs.native)
     names = _lib.PPO_OUT_NAMES
     sums = dict(zip(names[:12], parts[:12]))
     if inputs.rollout is not None:

@@ -25,7 +25,7 @@ import torch.distributed as dist
 
 from . import _lib
 from .batch import TEACHER_FIELDS, Batch, launch_pack, stage_micro_batches
-from .loss import batch_segment_offsets
+from .loss import batch_cached, batch_segment_offsets, tensor_key
 from .plan import Layout, MicroPlan
 from .topk import gather_logprobs
 
@@ -141,10 +141,14 @@ class _Inputs:
         self.per_token = bool(stub.calculate_per_token_loss)
         self.n_docs_global = int(mini.n_docs_global)
         self.n_tokens_global = int(mini.n_tokens_global)
+        # The argument struct (student filled per call) and the tensors it
+        # points into, held by each call's backward.
+        self.native = _lib.autograd().distill_inputs(
+            bytes(self.args(None)), (self.teacher, self.mask, self.rollout, self.ids, self.seg_off, self.workspace))
 
-    def args(self, student: torch.Tensor) -> _lib.DistillArgs:
+    def args(self, student: torch.Tensor | None) -> _lib.DistillArgs:
         a = _lib.DistillArgs()
-        a.student = student.data_ptr()
+        a.student = _lib.ptr(student)
         a.teacher = self.teacher.data_ptr()
         a.mask = self.mask.data_ptr()
         a.rollout_lp = _lib.ptr(self.rollout)
@@ -165,42 +169,16 @@ class _Inputs:
         return a
 
 
-class _DistillLoss(torch.autograd.Function):
-    @staticmethod
-    def forward(ctx, student, inputs: _Inputs):
-        dev = student.device
-        # The sums land in out; the loss handed to autograd is a view of its
-        # loss entry (no copy launched).
-        out = torch.empty(_lib.DISTILL_NOUT, dtype=torch.float32, device=dev)
-        seg_cnt = torch.empty(inputs.n_docs + 1, dtype=torch.float32, device=dev)
-        a = inputs.args(student)
-        rc = _lib.load().meshy_distill_loss_fwd(_lib.ctypes.byref(a), out.data_ptr(), seg_cnt.data_ptr(),
-                                                _lib.stream_of(dev))
-        _lib.check(rc, "meshy_distill_loss_fwd")
-        # The backward reads the same arrays: the struct of their addresses, and
-        # the inputs that own them, kept alive until it runs.
-        ctx.inputs = inputs
-        ctx.args = a
-        ctx.save_for_backward(student, seg_cnt)
-        loss = out[0]
-        ctx.mark_non_differentiable(out)
-        # The backward reads only the loss's gradient: no zero tensor for `out`'s.
-        ctx.set_materialize_grads(False)
-        return loss, out
-
-    @staticmethod
-    def backward(ctx, grad_loss, grad_out):
-        if grad_loss is None:
-            return None, None
-        student, seg_cnt = ctx.saved_tensors
-        g = grad_loss.reshape(1)
-        if g.dtype != torch.float32:
-            g = g.float()
-        grad = torch.empty_like(student)
-        rc = _lib.load().meshy_distill_loss_bwd(_lib.ctypes.byref(ctx.args), seg_cnt.data_ptr(), g.data_ptr(),
-                                                grad.data_ptr(), _lib.stream_of(student.device))
-        _lib.check(rc, "meshy_distill_loss_bwd")
-        return grad, None
+def _cached_inputs(stub, mb, mini, k: int, student: torch.Tensor) -> _Inputs:
+    """The _Inputs of this call, reused from the micro-batch's previous call
+    while nothing it was built from has changed."""
+    key = (k, student.shape[0], student.device, tensor_key(mb.teacher_topk_logprobs), tensor_key(mb.mask),
+           tensor_key(mb.rollout_logprobs), tensor_key(mb.doc_ids), int(mb.n_docs),
+           getattr(stub, "log_prob_min_clamp", None), getattr(stub, "loss_max_clamp", None),
+           bool(stub.calculate_per_token_loss), int(mini.n_docs_global), int(mini.n_tokens_global))
+    return batch_cached(mb, "_meshy_distill_inputs", key,
+                        (mb.teacher_topk_logprobs, mb.mask, mb.rollout_logprobs, mb.doc_ids),
+                        lambda: _Inputs(stub, mb, mini, k, student.shape[0], student.device))
 
 
 def distill_from_gathered(self: Any, gathered: torch.Tensor, mb: Any, mini: Any):
@@ -217,9 +195,10 @@ def distill_from_gathered(self: Any, gathered: torch.Tensor, mb: Any, mini: Any)
         student = student.float()
     if not student.is_contiguous():
         student = student.contiguous()
-    inputs = _Inputs(self, mb, mini, k, student.shape[0], student.device)
-    loss, out = _DistillLoss.apply(student, inputs)
-    parts = out.unbind(0)
+    inputs = _cached_inputs(self, mb, mini, k, student)
+    # One native call: the forward kernels, the loss (carrying a C++ backward
+    # node when the student requires grad) and every sum as a 0-dim view.
+    loss, parts = _lib.autograd().distill_loss(student, inputs.native)
     names = _lib.DISTILL_OUT_NAMES
     sums = dict(zip(names[:4], parts[:4]))
     if inputs.rollout is not None:

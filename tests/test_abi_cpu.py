@@ -169,3 +169,24 @@ def test_workspace_sizes_are_consistent():
     assert lib.meshy_distill_workspace_size(10_000, 12) >= 4 * 2 * (40 + 13)
     assert lib.meshy_critic_accumulate_workspace_size(7) >= 7 * 5 * 8
     assert lib.meshy_ragged_token_stats_workspace_size(9) >= 9 * 8
+
+
+def test_autograd_module_checks_its_arguments():
+    """The native autograd module loads beside the library and refuses, before
+    any device work, an argument struct of the wrong size and host tensors."""
+    import torch
+
+    ag = _lib.autograd()
+    with pytest.raises(ValueError, match="bytes"):
+        ag.ppo_inputs(b"\0" * (ctypes.sizeof(_lib.PpoArgs) - 8), ())
+    with pytest.raises(ValueError, match="bytes"):
+        ag.distill_inputs(b"\0" * (ctypes.sizeof(_lib.DistillArgs) + 8), ())
+    with pytest.raises(TypeError, match="tensors"):
+        ag.ppo_inputs(bytes(_lib.PpoArgs()), (1,))
+    cap = ag.ppo_inputs(bytes(_lib.PpoArgs()), (torch.zeros(3), None))
+    with pytest.raises(ValueError, match="device tensor"):
+        ag.ppo_loss(torch.zeros(3), cap)
+    with pytest.raises(TypeError, match="ppo_inputs capsule"):
+        ag.ppo_loss(torch.zeros(3), ag.distill_inputs(bytes(_lib.DistillArgs()), ()))
+    with pytest.raises(ValueError, match="device tensor"):
+        ag.clipped_value_error(torch.zeros(3), torch.zeros(3), None, None)

@@ -399,6 +399,51 @@ def test_distill_from_gathered_matches_oracle(dev, per_token, clamps, rollout):
         assert m[key] == pytest.approx(rm[key], abs=TOL), key
 
 
+def test_distill_inputs_cache_follows_edits(dev):
+    """A second loss over one micro-batch reuses its flattened inputs; an
+    in-place edit of the Teacher's log-probs or the mask, other clamps or a new
+    mini-batch denominator rebuilds them, so every call matches the oracle."""
+    from meshy_amd import opd
+    from meshy_amd.plan import MicroPlan, MiniPlan
+
+    K = 4
+    samples = [_opd_sample(L, K, 40 + i) for i, L in enumerate([90, 300, 17])]
+    micro = MicroPlan((0, 1, 2), 512, (90, 300, 17))
+    mb = opd.build_topk_micro_batches(samples, [micro], layout="packed", device=dev, need_rollout_lp=True)[0]
+    gathered = torch.log_softmax(torch.randn(1, 512, K + 1, generator=torch.Generator().manual_seed(5)) * 3, -1)
+
+    def check(stub, n_tok):
+        mini = MiniPlan((micro,), 3, n_tok, (0,))
+        gd = gathered.to(dev).requires_grad_(True)
+        loss, sums = opd.distill_from_gathered(stub, gd, mb, mini)
+        loss.backward()
+        gr = gathered.clone().requires_grad_(True)
+        rl, rs = oopd.distill_loss(gr, mb.teacher_topk_logprobs.cpu(), mb.mask.cpu(), mb.doc_ids.cpu(), mb.n_docs,
+                                   rollout_lp=mb.rollout_logprobs.cpu(), n_docs_global=3, n_tokens_global=n_tok,
+                                   per_token_loss=stub.calculate_per_token_loss,
+                                   log_prob_min_clamp=stub.log_prob_min_clamp, loss_max_clamp=stub.loss_max_clamp)
+        rl.backward()
+        assert abs(float(loss.detach()) - float(rl.detach())) <= TOL
+        for key in rs:
+            want = float(rs[key])
+            assert abs(float(sums[key]) - want) <= TOL + 1e-5 * abs(want), key
+        assert (gd.grad.cpu() - gr.grad).abs().max().item() <= 1e-6
+        return mb.__dict__["_meshy_distill_inputs"][1]
+
+    n_tok = int(mb.mask.sum().item())
+    stub = _stub(True)
+    first = check(stub, n_tok)
+    assert check(stub, n_tok) is first  # reused
+    mb.teacher_topk_logprobs.add_(-0.25)  # in place: a new version
+    second = check(stub, n_tok)
+    assert second is not first
+    mb.mask[0, 5:40] = 0.0
+    third = check(stub, int(mb.mask.sum().item()))
+    assert third is not second
+    assert check(_stub(True, -2.0, 1.0), int(mb.mask.sum().item())) is not third
+    assert check(_stub(False), 7 * int(mb.mask.sum().item())) is not third
+
+
 def test_distill_loss_drop_in_end_to_end(dev):
     """_distill_loss with a stub model: bf16 logits -> gather of K + 1 ids -> fused
     loss; loss, sums and d loss / d logits against the reference chain on CPU."""
