@@ -433,7 +433,7 @@ def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
     seg = torch.empty(n_docs + 1, device=dev)
     one = torch.ones(1, device=dev)
     grad = torch.empty_like(student)
-    ids, off = inputs.ids, inputs.seg_off
+    ids, off = mb.doc_ids.reshape(-1), inputs.seg_off
 
     def dev_fb():
         lib.meshy_segment_offsets(ids.data_ptr(), ids.numel(), n_docs + 1, off.data_ptr(), None, stream)
@@ -688,7 +688,7 @@ def bench_ppo(steps, warmup, no_cpu):
     out_t = torch.empty(_lib.PPO_NOUT, device=dev)
     one = torch.ones(1, device=dev)
     grad = torch.empty_like(new_flat)
-    ids, off = inputs.ids, inputs.seg_off
+    ids, off = mb.doc_ids.reshape(-1), inputs.seg_off
 
     def dev_fwd_nograd():
         lib.meshy_ppo_loss_fwd(pa0, out_t.data_ptr(), None, stream)

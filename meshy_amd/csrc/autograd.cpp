@@ -10,10 +10,12 @@
 // outputs, launches the forward on torch's current stream and hangs a C++
 // Node on the loss; the engine runs that Node's backward without Python.
 //
-//   ppo_inputs(args_bytes, keep) / distill_inputs(args_bytes, keep) -> capsule
-//       A meshy_ppo_args / meshy_distill_args (the bytes of the ctypes
-//       struct, checked against sizeof) and the tensors its pointers name,
-//       held for as long as any call's backward may read them.
+//   ppo_inputs(...) / distill_inputs(...) -> capsule
+//       The inputs of one micro-batch's loss, read once: a meshy_ppo_args /
+//       meshy_distill_args over the batch's tensors (each on the GPU, flat,
+//       converted only when its type or layout differs, sizes checked) with
+//       its workspace, and those tensors, held for as long as any call's
+//       backward may read them.  args_bytes(capsule) gives the struct.
 //   ppo_loss(new_lp, inputs) -> (loss, parts)
 //       meshy_ppo_loss_fwd over the flat fp32 new_lp (the struct's new_lp and
 //       grad_unit filled per call); loss is a 0-dim alias of the total-loss
@@ -47,6 +49,7 @@
 #include <cstdint>
 #include <cstring>
 #include <memory>
+#include <optional>
 #include <string>
 #include <utility>
 #include <vector>
@@ -129,42 +132,6 @@ const char* capsule_name<meshy_distill_args>() { return "meshy_amd.distill_input
 template <class Args>
 void capsule_free(PyObject* cap) {
     delete static_cast<std::shared_ptr<const Inputs<Args>>*>(PyCapsule_GetPointer(cap, capsule_name<Args>()));
-}
-
-template <class Args>
-PyObject* make_inputs(PyObject* args) {
-    HANDLE_TH_ERRORS
-    Py_buffer raw;
-    PyObject* keep;
-    if (!PyArg_ParseTuple(args, "y*O", &raw, &keep)) return nullptr;
-    if (static_cast<size_t>(raw.len) != sizeof(Args)) {
-        PyErr_Format(PyExc_ValueError, "argument struct has %zd bytes, the library's has %zu", raw.len,
-                     sizeof(Args));
-        PyBuffer_Release(&raw);
-        return nullptr;
-    }
-    auto in = std::make_shared<Inputs<Args>>();
-    std::memcpy(&in->args, raw.buf, sizeof(Args));
-    PyBuffer_Release(&raw);
-    PyObject* seq = PySequence_Fast(keep, "keep must be a sequence of tensors or None");
-    if (!seq) return nullptr;
-    const Py_ssize_t n = PySequence_Fast_GET_SIZE(seq);
-    for (Py_ssize_t i = 0; i < n; ++i) {
-        PyObject* item = PySequence_Fast_GET_ITEM(seq, i);
-        if (item == Py_None) continue;
-        if (!THPVariable_Check(item)) {
-            Py_DECREF(seq);
-            PyErr_SetString(PyExc_TypeError, "keep must hold tensors or None");
-            return nullptr;
-        }
-        in->keep.push_back(THPVariable_Unpack(item));
-    }
-    Py_DECREF(seq);
-    auto* holder = new std::shared_ptr<const Inputs<Args>>(std::move(in));
-    PyObject* cap = PyCapsule_New(holder, capsule_name<Args>(), capsule_free<Args>);
-    if (!cap) delete holder;
-    return cap;
-    END_HANDLE_TH_ERRORS
 }
 
 template <class Args>
@@ -433,13 +400,218 @@ PyObject* set_error_type(PyObject*, PyObject* cls) {
     Py_RETURN_NONE;
 }
 
-PyObject* ppo_inputs(PyObject*, PyObject* args) { return make_inputs<meshy_ppo_args>(args); }
-PyObject* distill_inputs(PyObject*, PyObject* args) { return make_inputs<meshy_distill_args>(args); }
+// ------------------------------------------------------------------ inputs
+
+// Reads the tensors of one loss's inputs as the kernels take them: each on
+// the GPU, flat, of one element type, a copy only when its type or layout
+// differs; every tensor read is held in `keep`.  Errors are Python
+// ValueErrors with the messages of the Python-side checks.
+class Reader {
+  public:
+    explicit Reader(std::vector<at::Tensor>& keep) : keep_(keep) {}
+
+    // The tensor behind `obj`, which must be a GPU tensor (nullopt for None;
+    // false with an exception set on error).
+    bool tensor(PyObject* obj, const char* what, at::Tensor& out) {
+        if (obj == Py_None) {
+            out = at::Tensor();
+            return true;
+        }
+        if (!unpack_tensor(obj, what, out)) return false;
+        if (!out.is_cuda()) {
+            PyErr_SetString(PyExc_ValueError,
+                            "meshy_amd kernels run on the GPU; got a CPU tensor (move inputs to a HIP device)");
+            return false;
+        }
+        if (device_ && out.device() != *device_) {
+            PyErr_Format(PyExc_ValueError, "%s is on another device than the other inputs", what);
+            return false;
+        }
+        if (!device_) device_ = out.device();
+        return true;
+    }
+
+    // A flat pointer of `dtype` over `t` (nullptr for an undefined tensor).
+    template <class T>
+    const T* flat(const at::Tensor& t, at::ScalarType dtype) {
+        if (!t.defined()) return nullptr;
+        at::Tensor x = t;
+        if (x.scalar_type() != dtype) x = x.to(dtype);
+        if (!x.is_contiguous()) x = x.contiguous();
+        keep_.push_back(x);
+        return x.data_ptr<T>();
+    }
+
+    // A uint8 workspace of `bytes` (at least one) on the inputs' device.
+    void* workspace(size_t bytes, size_t& size) {
+        size = bytes > 0 ? bytes : 1;
+        at::Tensor w = at::empty({static_cast<int64_t>(size)}, at::TensorOptions().dtype(at::kByte).device(*device_));
+        keep_.push_back(w);
+        return w.data_ptr();
+    }
+
+  private:
+    std::vector<at::Tensor>& keep_;
+    std::optional<at::Device> device_;
+};
+
+template <class Args>
+PyObject* wrap_inputs(std::shared_ptr<Inputs<Args>>&& in) {
+    auto* holder = new std::shared_ptr<const Inputs<Args>>(std::move(in));
+    PyObject* cap = PyCapsule_New(holder, capsule_name<Args>(), capsule_free<Args>);
+    if (!cap) delete holder;
+    return cap;
+}
+
+using Named = std::pair<const char*, const at::Tensor*>;
+
+bool bad_tokens(const char* fmt, const char* name, int64_t n_tokens, int64_t got) {
+    PyErr_Format(PyExc_ValueError, fmt, static_cast<long long>(n_tokens), name, static_cast<long long>(got));
+    return true;
+}
+
+// ppo_inputs(old_lp, mask, rollout_lp|None, entropy|None, advantages,
+//            positive_lm_weights|None, doc_ids, seg_offsets, n_tokens, n_docs,
+//            n_docs_global, n_tokens_global, clip_low, clip_high, tis_min,
+//            tis_max, positive_lm_coef, use_tis, use_icepop, per_token_loss,
+//            train_lp_is_old, cp_degree) -> capsule
+// Advantages of more than one dimension are per token, else per document.
+PyObject* ppo_inputs(PyObject*, PyObject* args) {
+    HANDLE_TH_ERRORS
+    PyObject *o_old, *o_mask, *o_roll, *o_ent, *o_adv, *o_pos, *o_ids, *o_off;
+    long long n_tokens, n_docs, n_docs_global, n_tokens_global;
+    double clip_low, clip_high, tis_min, tis_max, coef;
+    int use_tis, use_icepop, per_token, train_is_old, cp;
+    if (!PyArg_ParseTuple(args, "OOOOOOOOLLLLdddddppppi", &o_old, &o_mask, &o_roll, &o_ent, &o_adv, &o_pos, &o_ids,
+                          &o_off, &n_tokens, &n_docs, &n_docs_global, &n_tokens_global, &clip_low, &clip_high,
+                          &tis_min, &tis_max, &coef, &use_tis, &use_icepop, &per_token, &train_is_old, &cp))
+        return nullptr;
+    at::NoGradGuard no_grad;
+    auto in = std::make_shared<Inputs<meshy_ppo_args>>();
+    Reader rd(in->keep);
+    at::Tensor old, mask, roll, ent, adv, pos, ids, off;
+    if (!rd.tensor(o_old, "old_lp", old) || !rd.tensor(o_mask, "mask", mask) ||
+        !rd.tensor(o_adv, "advantages", adv) || !rd.tensor(o_ids, "doc_ids", ids) ||
+        !rd.tensor(o_roll, "rollout_logprobs", roll) || !rd.tensor(o_ent, "entropy", ent) ||
+        !rd.tensor(o_pos, "positive_lm_weights", pos) || !rd.tensor(o_off, "seg_offsets", off))
+        return nullptr;
+    const bool adv_per_token = adv.dim() != 1;
+    const char* tok_fmt = "new_lp has %lld tokens but %s has %lld";
+    for (auto [name, t] : {Named{"old_lp", &old}, Named{"mask", &mask}, Named{"doc_ids", &ids},
+                           Named{"rollout_logprobs", &roll}, Named{"entropy", &ent},
+                           Named{"advantages", adv_per_token ? &adv : nullptr}}) {
+        if (t && t->defined() && t->numel() != n_tokens && bad_tokens(tok_fmt, name, n_tokens, t->numel()))
+            return nullptr;
+    }
+    for (auto [name, t] : {Named{"positive_lm_weights", &pos}, Named{"advantages", adv_per_token ? nullptr : &adv}}) {
+        if (t && t->defined() && t->numel() < n_docs) {
+            PyErr_Format(PyExc_ValueError, "%s has %lld entries for %lld documents", name,
+                         static_cast<long long>(t->numel()), n_docs);
+            return nullptr;
+        }
+    }
+    if (off.scalar_type() != at::kLong || !off.is_contiguous() || off.numel() < n_docs + 2) {
+        PyErr_SetString(PyExc_ValueError, "seg_offsets must be n_docs + 2 contiguous int64 values");
+        return nullptr;
+    }
+    meshy_ppo_args& a = in->args;
+    a.old_lp = rd.flat<float>(old, at::kFloat);
+    a.mask = rd.flat<float>(mask, at::kFloat);
+    a.rollout_lp = rd.flat<float>(roll, at::kFloat);
+    a.entropy = rd.flat<float>(ent, at::kFloat);
+    a.adv = rd.flat<float>(adv, at::kFloat);
+    a.positive_lm_weights = rd.flat<float>(pos, at::kFloat);
+    a.doc_ids = rd.flat<int64_t>(ids, at::kLong);
+    a.seg_offsets = rd.flat<int64_t>(off, at::kLong);
+    a.n_tokens = n_tokens;
+    a.n_docs = n_docs;
+    a.n_docs_global = n_docs_global;
+    a.n_tokens_global = n_tokens_global;
+    a.clip_low = static_cast<float>(clip_low);
+    a.clip_high = static_cast<float>(clip_high);
+    a.tis_min = static_cast<float>(tis_min);
+    a.tis_max = static_cast<float>(tis_max);
+    a.positive_lm_coef = static_cast<float>(coef);
+    a.adv_per_token = adv_per_token;
+    a.use_tis = use_tis;
+    a.use_icepop = use_icepop;
+    a.per_token_loss = per_token;
+    a.train_lp_is_old = train_is_old;
+    a.cp_degree = cp;
+    a.workspace = rd.workspace(meshy_ppo_workspace_size(n_tokens, n_docs), a.workspace_bytes);
+    return wrap_inputs(std::move(in));
+    END_HANDLE_TH_ERRORS
+}
+
+// distill_inputs(teacher_lp, mask, rollout_lp|None, doc_ids, seg_offsets, k,
+//                n_tokens, n_docs, n_docs_global, n_tokens_global,
+//                lp_min_clamp|None, loss_max_clamp|None, per_token_loss) -> capsule
+PyObject* distill_inputs(PyObject*, PyObject* args) {
+    HANDLE_TH_ERRORS
+    PyObject *o_teacher, *o_mask, *o_roll, *o_ids, *o_off, *o_lp_min, *o_loss_max;
+    long long k, n_tokens, n_docs, n_docs_global, n_tokens_global;
+    int per_token;
+    if (!PyArg_ParseTuple(args, "OOOOOLLLLLOOp", &o_teacher, &o_mask, &o_roll, &o_ids, &o_off, &k, &n_tokens,
+                          &n_docs, &n_docs_global, &n_tokens_global, &o_lp_min, &o_loss_max, &per_token))
+        return nullptr;
+    at::NoGradGuard no_grad;
+    auto in = std::make_shared<Inputs<meshy_distill_args>>();
+    Reader rd(in->keep);
+    at::Tensor teacher, mask, roll, ids, off;
+    if (!rd.tensor(o_teacher, "teacher_topk_logprobs", teacher) || !rd.tensor(o_mask, "mask", mask) ||
+        !rd.tensor(o_ids, "doc_ids", ids) || !rd.tensor(o_roll, "rollout_logprobs", roll) ||
+        !rd.tensor(o_off, "seg_offsets", off))
+        return nullptr;
+    const char* tok_fmt = "the student has %lld tokens but %s has %lld";
+    if (teacher.numel() != n_tokens * k &&
+        bad_tokens(tok_fmt, "teacher_topk_logprobs", n_tokens, k > 0 ? teacher.numel() / k : teacher.numel()))
+        return nullptr;
+    for (auto [name, t] : {Named{"mask", &mask}, Named{"doc_ids", &ids}, Named{"rollout_logprobs", &roll}}) {
+        if (t->defined() && t->numel() != n_tokens && bad_tokens(tok_fmt, name, n_tokens, t->numel())) return nullptr;
+    }
+    if (off.scalar_type() != at::kLong || !off.is_contiguous() || off.numel() < n_docs + 2) {
+        PyErr_SetString(PyExc_ValueError, "seg_offsets must be n_docs + 2 contiguous int64 values");
+        return nullptr;
+    }
+    meshy_distill_args& a = in->args;
+    a.teacher = rd.flat<float>(teacher, at::kFloat);
+    a.mask = rd.flat<float>(mask, at::kFloat);
+    a.rollout_lp = rd.flat<float>(roll, at::kFloat);
+    a.doc_ids = rd.flat<int64_t>(ids, at::kLong);
+    a.seg_offsets = rd.flat<int64_t>(off, at::kLong);
+    a.n_tokens = n_tokens;
+    a.n_docs = n_docs;
+    a.k = k;
+    a.n_docs_global = n_docs_global;
+    a.n_tokens_global = n_tokens_global;
+    a.has_lp_clamp = o_lp_min != Py_None;
+    a.lp_min_clamp = a.has_lp_clamp ? static_cast<float>(PyFloat_AsDouble(o_lp_min)) : 0.f;
+    a.has_loss_clamp = o_loss_max != Py_None;
+    a.loss_max_clamp = a.has_loss_clamp ? static_cast<float>(PyFloat_AsDouble(o_loss_max)) : 0.f;
+    if (PyErr_Occurred()) return nullptr;
+    a.per_token_loss = per_token;
+    a.workspace = rd.workspace(meshy_distill_workspace_size(n_tokens, n_docs), a.workspace_bytes);
+    return wrap_inputs(std::move(in));
+    END_HANDLE_TH_ERRORS
+}
+
+// args_bytes(capsule) -> the bytes of its argument struct (for callers that
+// drive the C ABI themselves).
+PyObject* args_bytes(PyObject*, PyObject* cap) {
+    if (PyCapsule_IsValid(cap, capsule_name<meshy_ppo_args>())) {
+        const auto* in = unpack_inputs<meshy_ppo_args>(cap);
+        return PyBytes_FromStringAndSize(reinterpret_cast<const char*>(&(*in)->args), sizeof(meshy_ppo_args));
+    }
+    const auto* in = unpack_inputs<meshy_distill_args>(cap);
+    if (!in) return nullptr;
+    return PyBytes_FromStringAndSize(reinterpret_cast<const char*>(&(*in)->args), sizeof(meshy_distill_args));
+}
 
 PyMethodDef kMethods[] = {
-    {"ppo_inputs", ppo_inputs, METH_VARARGS, "Capsule of a meshy_ppo_args and the tensors it points into."},
+    {"ppo_inputs", ppo_inputs, METH_VARARGS, "Capsule of the PPO loss's inputs (argument struct and tensors)."},
     {"distill_inputs", distill_inputs, METH_VARARGS,
-     "Capsule of a meshy_distill_args and the tensors it points into."},
+     "Capsule of the distillation loss's inputs (argument struct and tensors)."},
+    {"args_bytes", args_bytes, METH_O, "The bytes of an inputs capsule's argument struct."},
     {"ppo_loss", ppo_loss, METH_VARARGS, "PPO clip loss forward; the loss carries its backward."},
     {"distill_loss", distill_loss, METH_VARARGS, "Top-K distillation loss forward; the loss carries its backward."},
     {"clipped_value_error", clipped_value_error, METH_VARARGS,

@@ -90,14 +90,6 @@ def checked_segment_offsets(doc_ids: torch.Tensor, n_slots: int) -> torch.Tensor
     return off
 
 
-def _flat_f32(t: torch.Tensor) -> torch.Tensor:
-    """A detached, contiguous fp32 view of ``t`` (a copy only when needed)."""
-    t = t.detach()
-    if t.dtype == torch.float32 and t.is_contiguous():
-        return t.view(-1)
-    return t.reshape(-1).to(torch.float32).contiguous()
-
-
 def segment_offsets(doc_ids: torch.Tensor, n_slots: int, check_sorted: bool = False) -> torch.Tensor:
     """Token offsets of each document slot of a non-decreasing ``doc_ids`` tensor."""
     ids = doc_ids.reshape(-1).to(torch.int64).contiguous()
@@ -116,91 +108,39 @@ def segment_offsets(doc_ids: torch.Tensor, n_slots: int, check_sorted: bool = Fa
 
 
 class _Inputs:
-    """Everything the two kernels read besides new_lp, kept alive for the backward."""
+    """Everything the two kernels read besides new_lp, read once per micro-batch
+    (``native``: the argument struct over the batch's tensors, which each
+    call's backward holds)."""
 
     def __init__(self, stub, new_lp, old_lp, mb, mini, entropy) -> None:
-        dev = new_lp.device
         self.n_tokens = new_lp.numel()
-        self.old = _flat_f32(old_lp)
-        self.mask = _flat_f32(mb.mask)
-        self.rollout = None if mb.rollout_logprobs is None else _flat_f32(mb.rollout_logprobs)
-        self.entropy = None if entropy is None else _flat_f32(entropy)
-        adv = mb.advantages
-        self.adv_per_token = adv.dim() != 1
-        self.adv = _flat_f32(adv)
-        self.n_docs = int(mb.n_docs)
-        self.use_icepop = bool(getattr(stub, "use_icepop", False))
-        self.use_tis = bool(stub.use_tis) and not self.use_icepop
-        self.coef = float(getattr(stub, "positive_lm_loss_coef", 0.0) or 0.0)
-        if self.use_icepop and self.rollout is None:
+        self.has_rollout = mb.rollout_logprobs is not None
+        self.has_entropy = entropy is not None
+        use_icepop = bool(getattr(stub, "use_icepop", False))
+        coef = float(getattr(stub, "positive_lm_loss_coef", 0.0) or 0.0)
+        if use_icepop and not self.has_rollout:
             raise ValueError("IcePop requires rollout log-probabilities")
-        self.pos_w = None
-        if self.coef:
-            if mb.positive_lm_weights is None:
-                raise ValueError("Positive LM loss requires group weights")
-            self.pos_w = mb.positive_lm_weights.reshape(-1).to(torch.float32).contiguous()
-        _lib.require_gpu(new_lp, self.old, self.mask, self.adv, mb.doc_ids, self.rollout, self.entropy,
-                         self.pos_w)
-        self.ids = mb.doc_ids.reshape(-1).to(torch.int64).contiguous()
-        # The kernels read every per-token array at each of the n_tokens positions.
-        per_token = [("old_lp", self.old), ("mask", self.mask), ("doc_ids", self.ids),
-                     ("rollout_logprobs", self.rollout), ("entropy", self.entropy)]
-        per_doc = [("positive_lm_weights", self.pos_w)]
-        (per_token if self.adv_per_token else per_doc).append(("advantages", self.adv))
-        for name, x in per_token:
-            if x is not None and x.numel() != self.n_tokens:
-                raise ValueError(f"new_lp has {self.n_tokens} tokens but {name} has {x.numel()}")
-        for name, x in per_doc:
-            if x is not None and x.numel() < self.n_docs:
-                raise ValueError(f"{name} has {x.numel()} entries for {self.n_docs} documents")
+        if coef and mb.positive_lm_weights is None:
+            raise ValueError("Positive LM loss requires group weights")
+        _lib.require_gpu(new_lp, mb.doc_ids)
         self.seg_off = batch_segment_offsets(mb)
-        ws = _lib.load().meshy_ppo_workspace_size(self.n_tokens, self.n_docs)
-        self.workspace = torch.empty(max(int(ws), 1), dtype=torch.uint8, device=dev)
-        self.clip_low = float(stub.ppo_clip_eps_low)
-        self.clip_high = float(stub.ppo_clip_eps_high)
-        self.tis_min = float(getattr(stub, "tis_ratio_min", 0.5))
-        self.tis_max = float(getattr(stub, "tis_ratio_max", 5.0))
-        self.per_token = bool(stub.calculate_per_token_loss)
-        self.train_is_old = getattr(stub, "old_logprobs_source", "rollout") == "train"
-        self.cp = max(1, int(getattr(getattr(stub, "parallel_dims", None), "cp", 1) or 1))
-        self.n_docs_global = int(mini.n_docs_global)
-        self.n_tokens_global = int(mini.n_tokens_global)
-        # The argument struct (new_lp and grad_unit are filled per call) and
-        # the tensors it points into, held by each call's backward.
+        # The native reader checks that every tensor is on the GPU and has the
+        # tokens (or documents) the kernels read, and flattens them.
         self.native = _lib.autograd().ppo_inputs(
-            bytes(self.args(None)),
-            (self.old, self.mask, self.rollout, self.entropy, self.adv, self.pos_w, self.ids, self.seg_off,
-             self.workspace))
+            old_lp, mb.mask, mb.rollout_logprobs, entropy, mb.advantages,
+            mb.positive_lm_weights if coef else None, mb.doc_ids, self.seg_off, self.n_tokens, int(mb.n_docs),
+            int(mini.n_docs_global), int(mini.n_tokens_global), float(stub.ppo_clip_eps_low),
+            float(stub.ppo_clip_eps_high), float(getattr(stub, "tis_ratio_min", 0.5)),
+            float(getattr(stub, "tis_ratio_max", 5.0)), coef, bool(stub.use_tis) and not use_icepop, use_icepop,
+            bool(stub.calculate_per_token_loss), getattr(stub, "old_logprobs_source", "rollout") == "train",
+            max(1, int(getattr(getattr(stub, "parallel_dims", None), "cp", 1) or 1)))
 
     def args(self, new_flat: torch.Tensor | None, grad_unit: torch.Tensor | None = None) -> _lib.PpoArgs:
-        a = _lib.PpoArgs()
-        a.grad_unit = _lib.ptr(grad_unit)
+        """The argument struct with new_lp and grad_unit set, for callers that
+        drive the C ABI themselves."""
+        a = _lib.PpoArgs.from_buffer_copy(_lib.autograd().args_bytes(self.native))
         a.new_lp = _lib.ptr(new_flat)
-        a.old_lp = self.old.data_ptr()
-        a.mask = self.mask.data_ptr()
-        a.rollout_lp = _lib.ptr(self.rollout)
-        a.entropy = _lib.ptr(self.entropy)
-        a.adv = self.adv.data_ptr()
-        a.positive_lm_weights = _lib.ptr(self.pos_w)
-        a.seg_offsets = self.seg_off.data_ptr()
-        a.doc_ids = self.ids.data_ptr()
-        a.n_tokens = self.n_tokens
-        a.n_docs = self.n_docs
-        a.n_docs_global = self.n_docs_global
-        a.n_tokens_global = self.n_tokens_global
-        a.clip_low = self.clip_low
-        a.clip_high = self.clip_high
-        a.tis_min = self.tis_min
-        a.tis_max = self.tis_max
-        a.positive_lm_coef = self.coef
-        a.adv_per_token = int(self.adv_per_token)
-        a.use_tis = int(self.use_tis)
-        a.use_icepop = int(self.use_icepop)
-        a.per_token_loss = int(self.per_token)
-        a.train_lp_is_old = int(self.train_is_old)
-        a.cp_degree = self.cp
-        a.workspace = self.workspace.data_ptr()
-        a.workspace_bytes = self.workspace.numel()
+        a.grad_unit = _lib.ptr(grad_unit)
         return a
 
 
@@ -275,10 +215,10 @@ def ppo_clip_loss(
     loss, parts = _lib.autograd().ppo_loss(new_flat, inputs.native)
     names = _lib.PPO_OUT_NAMES
     sums = dict(zip(names[:12], parts[:12]))
-    if inputs.rollout is not None:
+    if inputs.has_rollout:
         sums["train_rollout_kl_sum"] = parts[12]
         sums["train_rollout_logdiff_abs_sum"] = parts[13]
-    if inputs.entropy is not None:
+    if inputs.has_entropy:
         sums["entropy_sum"] = parts[14]
     return loss, sums
 

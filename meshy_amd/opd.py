@@ -116,56 +116,31 @@ def split_teacher_topk(values: torch.Tensor, micro: MicroPlan, *, layout: Layout
 
 
 class _Inputs:
-    """Everything the distillation kernels read besides the student log-probs."""
+    """Everything the distillation kernels read besides the student log-probs,
+    read once per micro-batch (``native``: the argument struct over the
+    batch's tensors, which each call's backward holds)."""
 
     def __init__(self, stub, mb, mini, k: int, n_tokens: int, device) -> None:
         self.k = k
         self.n_tokens = n_tokens
-        self.n_docs = int(mb.n_docs)
-        self.teacher = mb.teacher_topk_logprobs.detach().reshape(-1, k).to(torch.float32).contiguous()
-        self.mask = mb.mask.reshape(-1).to(torch.float32).contiguous()
-        self.rollout = (None if mb.rollout_logprobs is None else
-                        mb.rollout_logprobs.detach().reshape(-1).to(torch.float32).contiguous())
-        _lib.require_gpu(self.teacher, self.mask, mb.doc_ids, self.rollout)
-        self.ids = mb.doc_ids.reshape(-1).to(torch.int64).contiguous()
-        # The kernels read every per-token array at each of the n_tokens positions.
-        for name, x, width in (("teacher_topk_logprobs", self.teacher, k), ("mask", self.mask, 1),
-                               ("doc_ids", self.ids, 1), ("rollout_logprobs", self.rollout, 1)):
-            if x is not None and x.numel() != n_tokens * width:
-                raise ValueError(f"the student has {n_tokens} tokens but {name} has {x.numel() // width}")
+        self.has_rollout = mb.rollout_logprobs is not None
+        _lib.require_gpu(mb.doc_ids)
         self.seg_off = batch_segment_offsets(mb)
-        ws = _lib.load().meshy_distill_workspace_size(n_tokens, self.n_docs)
-        self.workspace = torch.empty(max(int(ws), 1), dtype=torch.uint8, device=device)
-        self.lp_min = getattr(stub, "log_prob_min_clamp", None)
-        self.loss_max = getattr(stub, "loss_max_clamp", None)
-        self.per_token = bool(stub.calculate_per_token_loss)
-        self.n_docs_global = int(mini.n_docs_global)
-        self.n_tokens_global = int(mini.n_tokens_global)
-        # The argument struct (student filled per call) and the tensors it
-        # points into, held by each call's backward.
+        # The native reader checks that every tensor is on the GPU and has the
+        # student's tokens, and flattens them.
+        lp_min = getattr(stub, "log_prob_min_clamp", None)
+        loss_max = getattr(stub, "loss_max_clamp", None)
         self.native = _lib.autograd().distill_inputs(
-            bytes(self.args(None)), (self.teacher, self.mask, self.rollout, self.ids, self.seg_off, self.workspace))
+            mb.teacher_topk_logprobs, mb.mask, mb.rollout_logprobs, mb.doc_ids, self.seg_off, k, n_tokens,
+            int(mb.n_docs), int(mini.n_docs_global), int(mini.n_tokens_global),
+            None if lp_min is None else float(lp_min), None if loss_max is None else float(loss_max),
+            bool(stub.calculate_per_token_loss))
 
     def args(self, student: torch.Tensor | None) -> _lib.DistillArgs:
-        a = _lib.DistillArgs()
+        """The argument struct with the student set, for callers that drive the
+        C ABI themselves."""
+        a = _lib.DistillArgs.from_buffer_copy(_lib.autograd().args_bytes(self.native))
         a.student = _lib.ptr(student)
-        a.teacher = self.teacher.data_ptr()
-        a.mask = self.mask.data_ptr()
-        a.rollout_lp = _lib.ptr(self.rollout)
-        a.seg_offsets = self.seg_off.data_ptr()
-        a.doc_ids = self.ids.data_ptr()
-        a.n_tokens = self.n_tokens
-        a.n_docs = self.n_docs
-        a.k = self.k
-        a.n_docs_global = self.n_docs_global
-        a.n_tokens_global = self.n_tokens_global
-        a.has_lp_clamp = int(self.lp_min is not None)
-        a.lp_min_clamp = float(self.lp_min) if self.lp_min is not None else 0.0
-        a.has_loss_clamp = int(self.loss_max is not None)
-        a.loss_max_clamp = float(self.loss_max) if self.loss_max is not None else 0.0
-        a.per_token_loss = int(self.per_token)
-        a.workspace = self.workspace.data_ptr()
-        a.workspace_bytes = self.workspace.numel()
         return a
 
 
@@ -201,7 +176,7 @@ def distill_from_gathered(self: Any, gathered: torch.Tensor, mb: Any, mini: Any)
     loss, parts = _lib.autograd().distill_loss(student, inputs.native)
     names = _lib.DISTILL_OUT_NAMES
     sums = dict(zip(names[:4], parts[:4]))
-    if inputs.rollout is not None:
+    if inputs.has_rollout:
         sums["train_rollout_kl_sum"] = parts[4]
         sums["train_rollout_logdiff_abs_sum"] = parts[5]
     return loss, sums

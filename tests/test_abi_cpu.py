@@ -173,20 +173,21 @@ def test_workspace_sizes_are_consistent():
 
 def test_autograd_module_checks_its_arguments():
     """The native autograd module loads beside the library and refuses, before
-    any device work, an argument struct of the wrong size and host tensors."""
+    any device work, host tensors and a capsule of the other loss."""
     import torch
 
     ag = _lib.autograd()
-    with pytest.raises(ValueError, match="bytes"):
-        ag.ppo_inputs(b"\0" * (ctypes.sizeof(_lib.PpoArgs) - 8), ())
-    with pytest.raises(ValueError, match="bytes"):
-        ag.distill_inputs(b"\0" * (ctypes.sizeof(_lib.DistillArgs) + 8), ())
-    with pytest.raises(TypeError, match="tensors"):
-        ag.ppo_inputs(bytes(_lib.PpoArgs()), (1,))
-    cap = ag.ppo_inputs(bytes(_lib.PpoArgs()), (torch.zeros(3), None))
-    with pytest.raises(ValueError, match="device tensor"):
-        ag.ppo_loss(torch.zeros(3), cap)
+    z = torch.zeros(3)
+    with pytest.raises(ValueError, match="run on the GPU"):
+        ag.ppo_inputs(z, z, None, None, z, None, z.long(), z.long(), 3, 1, 1, 3, 0.2, 0.28, 0.5, 5.0, 0.0,
+                      False, False, True, False, 1)
+    with pytest.raises(ValueError, match="run on the GPU"):
+        ag.distill_inputs(z, z, None, z.long(), z.long(), 1, 3, 1, 1, 3, None, None, True)
+    with pytest.raises(TypeError, match="must be a tensor"):
+        ag.distill_inputs([0.0], z, None, z.long(), z.long(), 1, 3, 1, 1, 3, None, None, True)
     with pytest.raises(TypeError, match="ppo_inputs capsule"):
-        ag.ppo_loss(torch.zeros(3), ag.distill_inputs(bytes(_lib.DistillArgs()), ()))
+        ag.ppo_loss(z, object())
+    with pytest.raises(TypeError, match="distill_inputs capsule"):
+        ag.args_bytes(object())
     with pytest.raises(ValueError, match="device tensor"):
-        ag.clipped_value_error(torch.zeros(3), torch.zeros(3), None, None)
+        ag.clipped_value_error(z, z, None, None)
