@@ -30,6 +30,7 @@ W warm-up steps start on a busy device.  Prints ONE JSON line with
 from __future__ import annotations
 
 import argparse
+import ctypes
 import json
 import os
 import statistics
@@ -854,6 +855,70 @@ def bench_gae(steps, warmup, no_cpu):
                                note="doc_ids offsets cached after the first call"), dev_us, T * 18)
 
 
+def bench_gae_cache(steps):
+    """Where GAE's second pass reads from: meshy_gae over the 1024 documents
+    back to back (the inputs stay in the 256 MB Infinity Cache between calls),
+    then each call after a 1 GiB read that evicts the L2s and the Infinity
+    Cache (the chunks pass then reads HBM, and the apply pass re-reads what
+    the chunks pass just brought in), then a 268,435,456 B device copy three
+    times (counter calibration).  Device us per call from HIP events around
+    the call alone."""
+    import numpy as np
+    import torch
+
+    from meshy_amd import _lib, workloads
+    from meshy_amd.loss import checked_segment_offsets
+
+    dev = torch.device("cuda:0")
+    batch, values, terminal = workloads.gae_1024_docs(4)
+    n, T = len(batch.lengths), int(batch.total)
+    rewards = np.zeros(T, np.float32)
+    rewards[batch.offsets[1:] - 1] = terminal
+    doc_ids = torch.from_numpy(np.repeat(np.arange(n), batch.lengths)).reshape(1, -1).to(dev)
+    r = torch.from_numpy(rewards).to(dev)
+    v = torch.from_numpy(values).to(torch.bfloat16).to(dev)
+    m = torch.from_numpy(batch.mask).to(dev)
+    lengths = torch.full((n,), 1.0 / (1.0 - 0.95), device=dev)
+    lib, stream = _lib.load(), _lib.stream_of(dev)
+    adv_o, ret_o, lam_o = torch.empty(T, device=dev), torch.empty(T, device=dev), torch.empty(n, device=dev)
+    ws = torch.empty(max(int(lib.meshy_gae_workspace_size(1, T, n)), 1), dtype=torch.uint8, device=dev)
+    off = checked_segment_offsets(doc_ids, n + 1)
+    ga = _lib.GaeArgs()
+    ga.rewards, ga.values, ga.mask, ga.doc_ids = r.data_ptr(), v.data_ptr(), m.data_ptr(), doc_ids.data_ptr()
+    ga.lengths, ga.seg_offsets = lengths.data_ptr(), off.data_ptr()
+    ga.rows, ga.S, ga.n_docs = 1, T, n
+    ga.gamma, ga.alpha, ga.epsilon, ga.values_bf16 = 1.0, 1.0, 1e-6, 1
+    ga.adv, ga.returns, ga.lam_doc = adv_o.data_ptr(), ret_o.data_ptr(), lam_o.data_ptr()
+    ga.workspace, ga.workspace_bytes = ws.data_ptr(), ws.numel()
+    pg = ctypes.byref(ga)
+    _checked(lib.meshy_gae(pg, stream), "meshy_gae")
+    big = torch.ones(256 * 1024 * 1024, device=dev)  # 1 GiB
+    sink = torch.empty((), device=dev)
+
+    def per_call(flush: bool) -> float:
+        times = []
+        for i in range(steps + 3):
+            if flush:
+                torch.sum(big, dim=0, out=sink)
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            a.record()
+            lib.meshy_gae(pg, stream)
+            b.record()
+            b.synchronize()
+            if i >= 3:
+                times.append(a.elapsed_time(b) * 1e3)
+        return round(statistics.median(times), 2)
+
+    out = {"back_to_back_us": per_call(False), "after_1GiB_read_us": per_call(True), "tokens": T, "docs": n,
+           "inputs_MB": round(T * 10 / 1e6, 1), "outputs_MB": round(T * 8 / 1e6, 1)}
+    src = torch.ones(64 * 1024 * 1024, device=dev)
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    return out
+
+
 # ---------------------------------------------------------------- GAE attach over 1024 docs, pack of 16 long sequences
 
 def bench_attach_gae(runs, no_cpu):
@@ -1327,6 +1392,7 @@ LEGS = {
     "opd": lambda a: bench_opd(*headline_inputs(), a.steps, a.warmup, a.no_cpu),
     "ppo": lambda a: bench_ppo(a.steps, a.warmup, a.no_cpu),
     "gae": lambda a: bench_gae(a.steps, a.warmup, a.no_cpu),
+    "gae_cache": lambda a: bench_gae_cache(a.steps),
     "critic": lambda a: bench_critic(a.steps, a.warmup, a.no_cpu),
     "attach_gae": lambda a: bench_attach_gae(5, a.no_cpu),
     "long_context": lambda a: bench_long_context(max(3, a.steps // 10), 2, a.no_cpu),
