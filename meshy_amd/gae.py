@@ -13,6 +13,7 @@ are then fixed-order sums, bitwise reproducible for fractional masks too.
 
 from __future__ import annotations
 
+import math
 from typing import Any, Sequence
 
 import numpy as np
@@ -158,8 +159,7 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
     reduces the critic metrics.  Each sample gets ``ADVANTAGE_TOKENS``, a device
     view of its advantages, of length ``min(len(tokens), seq_len)``.
     """
-    from .batch import ADVANTAGE_TOKENS, _Layout
-    from .hostio import gather_into
+    from .batch import _SCALAR_TYPE, ADVANTAGE_TOKENS, _column, _gather_column, _Layout
 
     if not samples:
         return {}
@@ -168,28 +168,29 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
     if dev.type != "cuda":
         raise ValueError("meshy_amd runs GAE on a HIP device; self.device must be a cuda device")
     n = len(samples)
-    # One pass over the samples: widths, the mask / value slices and the rewards.
-    widths, masks, vals, rewards = [], [], [], []
-    for j, td in enumerate(samples):
-        tok = td["tokens"]
-        L = min(int(tok.shape[0]) if isinstance(tok, torch.Tensor) else len(tok), seq_len)
-        v = td["values"]
-        v = v if v.shape[0] == L else v[:L]  # a view only where a sample is cut
-        if int(v.shape[0]) != L:
-            raise ValueError(
-                f"row {j}: critic published {tuple(td['values'].shape)} values "
-                f"for {L} tokens; the critic and the trainer disagree about "
-                f"the sequence"
-            )
-        widths.append(L)
-        m = td["mask_assistant"]
-        masks.append(m if m.shape[0] == L else m[:L])
-        vals.append(v)
-        rewards.append(td["reward"])
+    # The samples' columns are read by the native staging module: pointer,
+    # length and dtype records of every sample's tokens and values, then one
+    # threaded gather per column into the pinned staging buffer.
+    used = np.arange(n, dtype=np.int64)
+    used_b = used.tobytes()
+    trec = _column(samples, used_b, "tokens")
+    lens = trec["dim0"].copy()
+    for j in np.flatnonzero((trec["flags"] & 1) == 0).tolist():  # token lists
+        lens[j] = len(samples[j]["tokens"])
+    widths = np.minimum(lens, seq_len)
+    vrec = _column(samples, used_b, "values")
+    short = np.flatnonzero(((vrec["flags"] & 1) == 0) | (vrec["dim0"] < widths))
+    if short.size:
+        j = int(short[0])
+        raise ValueError(
+            f"row {j}: critic published {tuple(samples[j]['values'].shape)} values "
+            f"for {int(widths[j])} tokens; the critic and the trainer disagree about "
+            f"the sequence"
+        )
     offsets = np.zeros(n + 1, np.int64)
     np.cumsum(widths, out=offsets[1:])
     total = int(offsets[-1])
-    bf16 = all(v.dtype == torch.bfloat16 for v in vals)
+    bf16 = bool((vrec["dtype"] == _SCALAR_TYPE[torch.bfloat16]).all())
     vdt = torch.bfloat16 if bf16 else torch.float32
     lay = _Layout()
     lay.add("mask", total, torch.float32)
@@ -198,24 +199,24 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
     lay.add("offsets", n + 1, torch.int64)
     host = torch.empty(lay.size, dtype=torch.uint8, pin_memory=True)
     dbuf = torch.empty(lay.size, dtype=torch.uint8, device=dev)
-    gather_into(masks, lay.view(host, "mask"))
+    _gather_column(samples, used, used_b, widths, "mask_assistant", lay.view(host, "mask"))
     # The masks travel to the device while the values are gathered (finer runs
     # of samples, each copied once staged, measured no faster).
     cut = lay.regions["values"][0]
     dbuf[:cut].copy_(host[:cut], non_blocking=True)
-    gather_into(vals, lay.view(host, "values"))
-    if all(isinstance(r, torch.Tensor) and r.numel() == 1 for r in rewards):
-        try:  # one shape (the usual 0-d rewards): stacked as they are
-            reward = torch.stack(rewards)
-        except RuntimeError:
-            reward = torch.stack([r.reshape(()) for r in rewards])
-        reward = reward.reshape(-1).to(device="cpu", dtype=torch.float32)
+    _gather_column(samples, used, used_b, widths, "values", lay.view(host, "values"), recs=vrec)
+    r64 = np.frombuffer(_lib.stage().scalars(samples, used_b, "reward", math.nan), np.float64)
+    if np.isnan(r64).any():
+        # absent, None, empty or NaN somewhere: each sample's reward read as it is
+        rewards = [td["reward"] for td in samples]
+        reward = torch.tensor([float(r.reshape(-1)[0]) if isinstance(r, torch.Tensor) else float(r)
+                               for r in rewards], dtype=torch.float32)
     else:
-        reward = torch.tensor([float(r.reshape(-1)[0]) if isinstance(r, torch.Tensor) else float(r) for r in rewards],
-                              dtype=torch.float32)
+        reward = torch.from_numpy(r64.astype(np.float32))
     lay.view(host, "reward").copy_(reward)
     lay.view(host, "offsets").copy_(torch.from_numpy(offsets))
     dbuf[cut:].copy_(host[cut:], non_blocking=True)
+    widths = widths.tolist()
 
     lib = _lib.load()
     adv = torch.empty(max(total, 1), dtype=torch.float32, device=dev)

@@ -404,6 +404,45 @@ def test_attach_gae_advantages_matches_oracle(dev, gae_lambda, alpha, gamma, seq
         assert abs(metrics[k] - ref_m[k]) <= TOL, k
 
 
+def test_attach_reads_every_sample_form(dev):
+    """Token lists, bool or int masks, rewards as Python floats or 1-element
+    tensors, and values of mixed dtypes or non-contiguous take the converting
+    path of the staging and give the same advantages and metrics as plain
+    tensors; values shorter than the tokens are refused."""
+    from types import SimpleNamespace as NS
+
+    from meshy_amd.batch import ADVANTAGE_TOKENS
+    from meshy_amd.gae import attach_gae_advantages
+
+    base = _critic_samples(24, seed=9)
+    trainer = NS(seq_len=400, gae_gamma=1.0, gae_alpha=1.5, gae_lambda=None, device=dev)
+    plain = [dict(s) for s in base]
+    want_m = attach_gae_advantages(trainer, plain)
+    odd = []
+    for j, s in enumerate(base):
+        t = dict(s)
+        if j % 4 == 0:
+            t["tokens"] = t["tokens"].tolist()
+        if j % 4 == 1:
+            t["mask_assistant"] = t["mask_assistant"].bool()
+        if j % 4 == 2:
+            t["reward"] = float(t["reward"])
+        if j % 4 == 3:
+            t["reward"] = t["reward"].reshape(1)
+            t["values"] = torch.stack([t["values"], t["values"]], 1)[:, 0]  # non-contiguous
+        if j % 5 == 0:
+            t["mask_assistant"] = t["mask_assistant"].to(torch.int32)
+        odd.append(t)
+    got_m = attach_gae_advantages(trainer, odd)
+    for a, b in zip(plain, odd):
+        assert torch.equal(a[ADVANTAGE_TOKENS], b[ADVANTAGE_TOKENS])
+    assert got_m == want_m
+    short = [dict(s) for s in base[:3]]
+    short[1]["values"] = short[1]["values"][:-1]
+    with pytest.raises(ValueError, match="row 1: critic published"):
+        attach_gae_advantages(NS(seq_len=10 ** 6, gae_gamma=1.0, gae_alpha=1.5, gae_lambda=None, device=dev), short)
+
+
 def test_attach_then_whiten_and_pack(dev):
     """GAE advantages left on the device feed whitening (in place, one buffer)
     and the pack (per-token advantages gathered on the device)."""
