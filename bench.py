@@ -396,10 +396,9 @@ def bench_opd(logits, labels, steps, warmup, no_cpu, cpu_rows=512):
         # the steps of distill_from_gathered, one mark after each
         fresh_micro()
         gd.grad = None
-        student = gd.reshape(-1, K + 1)
-        inputs = opd._cached_inputs(stub, mb, mini, K, student)
+        inputs = opd._cached_inputs(stub, mb, mini, K, gd, T)
         mark("inputs")
-        loss, parts = _lib.autograd().distill_loss(student, inputs.native)
+        loss, parts = _lib.autograd().distill_loss(gd, inputs.native)
         dict(zip(_lib.DISTILL_OUT_NAMES, parts))
         mark("forward")
         loss.backward()
@@ -718,9 +717,8 @@ def bench_ppo(steps, warmup, no_cpu):
         # the steps of ppo_clip_loss, one mark after each
         new_d.grad = None
         inputs = loss_mod._cached_inputs(stub, new_d, old_d, mb, mini, None)
-        flat = new_d.reshape(-1)
         mark("inputs")
-        loss, parts = _lib.autograd().ppo_loss(flat, inputs.native)
+        loss, parts = _lib.autograd().ppo_loss(new_d, inputs.native)
         dict(zip(_lib.PPO_OUT_NAMES[:12], parts[:12]))
         mark("forward")
         loss.backward()

@@ -31,12 +31,12 @@ from .gae import compute_returns
 from .loss import checked_segment_offsets
 
 
-def _flat_f32(t: torch.Tensor) -> torch.Tensor:
-    """``t`` as a flat contiguous fp32 tensor, a view when it already is one
-    (differentiable: ``values`` keeps its graph)."""
+def _as_f32(t: torch.Tensor) -> torch.Tensor:
+    """``t`` as a contiguous fp32 tensor of its shape, ``t`` itself when it
+    already is one (differentiable: ``values`` keeps its graph)."""
     if t.dtype == torch.float32 and t.is_contiguous():
-        return t.view(-1)
-    return t.reshape(-1).to(torch.float32).contiguous()
+        return t
+    return t.to(torch.float32).contiguous()
 
 
 def advantages_to_per_sequence(adv: torch.Tensor, mask: torch.Tensor, doc_ids: torch.Tensor,
@@ -316,15 +316,16 @@ def clipped_value_error(values: torch.Tensor, targets: torch.Tensor, old_values:
     """Per-token ``(v - t)^2``, or with ``clip`` the PPO-style clipped maximum
     (vapo.py:35-41); differentiable in ``values``."""
     _lib.require_gpu(values, targets, old_values if clip is not None else None)
-    shape = values.shape
-    v = _flat_f32(values)
-    t = _flat_f32(targets.detach())
+    v = _as_f32(values)
+    t = _as_f32(targets.detach())
     o = None
     if clip is not None:
-        o = _flat_f32(old_values.detach())
-    # One native call (which checks the sizes); the output carries a C++
-    # backward node when values requires grad.
-    return _lib.autograd().clipped_value_error(v, t, o, None if clip is None else float(clip)).reshape(shape)
+        o = _as_f32(old_values.detach())
+    # One native call (which checks the sizes); the output has values' shape
+    # and carries a C++ backward node when values requires grad.  Contiguous
+    # fp32 inputs are passed as they are: no view node sits between the
+    # output's node and values' (each autograd node costs host time).
+    return _lib.autograd().clipped_value_error(v, t, o, None if clip is None else float(clip))
 
 
 __all__ = ["Accumulator", "AccumulatorState", "CriticDiagnostics", "advantages_to_per_sequence",

@@ -328,14 +328,12 @@ struct ClippedValueErrorBackward final : torch::autograd::Node {
         const float* op = has_clip ? o.get(node).data_ptr<float>() : nullptr;
         at::Tensor g = grads[0];
         if (g.scalar_type() != at::kFloat) g = g.to(at::kFloat);
-        // The gradient of a sum or a mean is one value broadcast (stride 0):
-        // the kernel reads it as such instead of a materialised copy.
-        int64_t stride = 1;
-        if (g.dim() == 1 && g.numel() > 0 && g.stride(0) == 0) {
-            stride = 0;
-        } else {
-            g = g.contiguous();
-        }
+        // The gradient of a sum or a mean is one value broadcast (every
+        // stride 0): the kernel reads it as such instead of a materialised copy.
+        bool broadcast = g.numel() > 0;
+        for (int64_t d = 0; d < g.dim() && broadcast; ++d) broadcast = g.size(d) <= 1 || g.stride(d) == 0;
+        const int64_t stride = broadcast ? 0 : 1;
+        if (!broadcast) g = g.contiguous();
         at::Tensor grad = at::empty_like(vv);
         int rc = meshy_clipped_value_error_bwd(vv.data_ptr<float>(), tt.data_ptr<float>(), op, has_clip, clip,
                                                vv.numel(), g.data_ptr<float>(), stride, grad.data_ptr<float>(),

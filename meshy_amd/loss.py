@@ -205,7 +205,10 @@ def ppo_clip_loss(
             "context-parallel PPO loss needs the per-document all-reduce between the two "
             "kernel phases; this library drives one GPU")
     inputs = _cached_inputs(self, new_lp, old_lp, mb, mini, entropy)
-    new_flat = new_lp.reshape(-1)
+    # The kernels read new_lp as one flat fp32 array; a contiguous fp32 tensor
+    # of any shape is passed as it is, so that no view node sits between the
+    # loss's node and new_lp's (each autograd node costs host time).
+    new_flat = new_lp
     if new_flat.dtype != torch.float32:
         new_flat = new_flat.float()
     if not new_flat.is_contiguous():

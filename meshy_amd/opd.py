@@ -144,16 +144,16 @@ class _Inputs:
         return a
 
 
-def _cached_inputs(stub, mb, mini, k: int, student: torch.Tensor) -> _Inputs:
+def _cached_inputs(stub, mb, mini, k: int, student: torch.Tensor, n_tokens: int) -> _Inputs:
     """The _Inputs of this call, reused from the micro-batch's previous call
     while nothing it was built from has changed."""
-    key = (k, student.shape[0], student.device, tensor_key(mb.teacher_topk_logprobs), tensor_key(mb.mask),
+    key = (k, n_tokens, student.device, tensor_key(mb.teacher_topk_logprobs), tensor_key(mb.mask),
            tensor_key(mb.rollout_logprobs), tensor_key(mb.doc_ids), int(mb.n_docs),
            getattr(stub, "log_prob_min_clamp", None), getattr(stub, "loss_max_clamp", None),
            bool(stub.calculate_per_token_loss), int(mini.n_docs_global), int(mini.n_tokens_global))
     return batch_cached(mb, "_meshy_distill_inputs", key,
                         (mb.teacher_topk_logprobs, mb.mask, mb.rollout_logprobs, mb.doc_ids),
-                        lambda: _Inputs(stub, mb, mini, k, student.shape[0], student.device))
+                        lambda: _Inputs(stub, mb, mini, k, n_tokens, student.device))
 
 
 def distill_from_gathered(self: Any, gathered: torch.Tensor, mb: Any, mini: Any):
@@ -165,12 +165,15 @@ def distill_from_gathered(self: Any, gathered: torch.Tensor, mb: Any, mini: Any)
             "context-parallel distillation needs the per-document count all-reduce between the two "
             "kernel phases; this library drives one GPU")
     k = gathered.shape[-1] - 1
-    student = gathered.reshape(-1, k + 1)
+    # The kernels read the gather as one [tokens, K + 1] fp32 array; a
+    # contiguous fp32 gather is passed as it is, so that no view node sits
+    # between the loss's node and the gather's.
+    student = gathered
     if student.dtype != torch.float32:
         student = student.float()
     if not student.is_contiguous():
         student = student.contiguous()
-    inputs = _cached_inputs(self, mb, mini, k, student)
+    inputs = _cached_inputs(self, mb, mini, k, student, student.numel() // (k + 1))
     # One native call: the forward kernels, the loss (carrying a C++ backward
     # node when the student requires grad) and every sum as a 0-dim view.
     loss, parts = _lib.autograd().distill_loss(student, inputs.native)

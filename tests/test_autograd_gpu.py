@@ -61,6 +61,8 @@ def test_ppo_node_gradients_and_graph_rules(dev, per_token):
     nd = new.to(dev).requires_grad_(True)
     loss, sums = ppo_clip_loss(stub, nd, old_d, mb, mini)
     assert loss.requires_grad and loss.grad_fn.name() == "MeshyPpoLossBackward"
+    # new_lp's own node follows directly: no view node in between
+    assert loss.grad_fn.next_functions[0][0].variable is nd
     assert abs(loss.item() - ref_loss.item()) <= TOL
     assert abs(sums["ppo_kl_sum"].item() - float(ref_sums["ppo_kl_sum"])) <= TOL
     (loss * 3.0).backward(retain_graph=True)
@@ -191,6 +193,15 @@ def test_clipped_value_error_node(dev, clip):
             tol = 1e-6 if dtype == torch.float32 else 1e-2 * max(want.abs().max().item(), 1e-6)
             assert vd.grad.dtype == dtype
             assert (vd.grad.float().cpu() - want).abs().max().item() <= tol, (dtype, reduce)
+    # a [rows, S] grid: the mean's gradient arrives broadcast over both dimensions
+    v2, t2, o2 = (x[:70_000].reshape(70, 1000) for x in (v, t, o))
+    vr = v2.clone().requires_grad_(True)
+    ocritic.clipped_value_error(vr, t2, o2, clip).mean().backward()
+    vd = v2.to(dev).requires_grad_(True)
+    e = critic.clipped_value_error(vd, t2.to(dev), o2.to(dev), clip)
+    assert e.shape == (70, 1000)
+    e.mean().backward()
+    assert vd.grad.shape == (70, 1000) and (vd.grad.cpu() - vr.grad).abs().max().item() <= 1e-6
     vd = v.to(dev).requires_grad_(True)
     s = critic.clipped_value_error(vd, td, od, clip).sum()
     s.backward()
