@@ -1227,10 +1227,12 @@ def bench_rollout_metrics(runs, no_cpu):
 
 def bench_group_advantages(runs, no_cpu):
     """GRPO advantages and the zero-variance filter of a whole step (the 32
-    groups of 8 of the 256-sample GRPO batch) in one device call each (the
-    rewards' host-to-device copy, one launch, the copy back), next to the
-    reference's per-group host functions (rollout.py:88-115) called once per
-    group as its rollout worker does, summed over the 32 groups."""
+    groups of 8 of the 256-sample GRPO batch): the advantages in one device
+    call (the rewards' host-to-device copy, one launch, the copy back), the
+    filter in one host call over the host rewards (and, for the record, in
+    one device call), next to the reference's per-group host functions
+    (rollout.py:88-115) called once per group as its rollout worker does,
+    summed over the 32 groups."""
     import numpy as np
     import torch
 
@@ -1248,10 +1250,15 @@ def bench_group_advantages(runs, no_cpu):
             fn(r, torch.from_numpy(group_offsets).to(dev)).tolist()
         return _wall_ms(run, reps, gpu=False) * 1e3
 
+    def host_filter():
+        # the rewards where the rollout worker holds them: on the host
+        zero_variance_groups(torch.from_numpy(rewards.astype(np.float64)), torch.from_numpy(group_offsets)).tolist()
+
     out = {
         "group_size": 8, "n_groups": n_groups,
         "grpo_advantages_us_all_groups": round(batched(grpo_advantages, np.float32), 1),
-        "zero_variance_groups_us_all_groups": round(batched(zero_variance_groups, np.float64), 1),
+        "zero_variance_groups_us_all_groups": round(_wall_ms(host_filter, reps, gpu=False) * 1e3, 1),
+        "zero_variance_groups_device_us_all_groups": round(batched(zero_variance_groups, np.float64), 1),
     }
     if not no_cpu:
         from oracle import grpo as ogrpo

@@ -207,6 +207,11 @@ int meshy_grpo_advantage(const float* rewards, int64_t n_rewards, const int64_t*
  * ---------------------------------------------------------------------- */
 int meshy_zero_variance_groups(const double* raw_rewards, int64_t n_rewards, const int64_t* group_offsets,
                                int64_t n_groups, double tolerance, uint8_t* flags, hipStream_t stream);
+/* The same filter over host arrays (raw_rewards, group_offsets and flags in
+ * host memory), for rewards that are still on the host as the rollout worker
+ * holds them (rollout.py:580-587): the same flags, no device round trip. */
+int meshy_zero_variance_groups_host(const double* raw_rewards, int64_t n_rewards, const int64_t* group_offsets,
+                                    int64_t n_groups, double tolerance, uint8_t* flags);
 
 /* ------------------------------------------------------------------------
  * Fused packed log_softmax + gather + entropy (device), bf16 logits.

@@ -239,6 +239,7 @@ SIGNATURES = {
     "meshy_pack_micro_batches": (c_int, [POINTER(PackArgs), c_void_p]),
     "meshy_grpo_advantage": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
     "meshy_zero_variance_groups": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_double, c_void_p, c_void_p]),
+    "meshy_zero_variance_groups_host": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_double, c_void_p]),
     "meshy_logprob_entropy_fwd": (
         c_int,
         [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,
@@ -327,7 +328,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 _LIB: ctypes.CDLL | None = None
 

@@ -13,8 +13,9 @@ worker (rollout.py:572, 580-587).  A device call per group of a few scalars
 costs a copy, a launch and a synchronisation, several times the reference's
 host arithmetic, so no per-group form is offered: the advantages are computed
 once per step over every group (the worker's ``advantage`` plugin is then left
-unset), and a filter that must decide as each group completes keeps the
-reference's host function.
+unset).  The filter takes the rewards where they are: on the host it runs in
+the library's host code, so a batch of groups costs less than the
+reference's per-group calls.
 """
 
 from __future__ import annotations
@@ -44,17 +45,28 @@ def zero_variance_groups(raw_rewards: torch.Tensor, group_offsets: torch.Tensor,
     """Bool ``[n_groups]``: group g's raw rewards span at most ``tolerance``
     (rollout.py:100-115), compared in float64 as the reference's Python floats
     are.  An empty group is True; a group whose first reward is NaN is False;
-    later NaNs are skipped, as Python's ``max``/``min`` skip them."""
-    _lib.require_gpu(raw_rewards, group_offsets)
+    later NaNs are skipped, as Python's ``max``/``min`` skip them.
+
+    Device tensors are filtered by ``meshy_zero_variance_groups``; host
+    tensors (the rewards as the rollout worker holds them) by
+    ``meshy_zero_variance_groups_host``, without a device round trip.  The
+    flags come back where the rewards are."""
+    if raw_rewards.is_cuda != group_offsets.is_cuda:
+        raise ValueError("raw_rewards and group_offsets must both be on the GPU or both on the host")
     r = raw_rewards.to(torch.float64).contiguous()
     off = group_offsets.to(torch.int64).contiguous()
     n_groups = off.numel() - 1
     if n_groups < 0:
         raise ValueError("group_offsets must hold at least one entry")
     flags = torch.empty(n_groups, dtype=torch.uint8, device=r.device)
-    rc = _lib.load().meshy_zero_variance_groups(_lib.ptr(r) if r.numel() else None, r.numel(), off.data_ptr(),
-                                                n_groups, float(tolerance), flags.data_ptr(),
-                                                _lib.stream_of(r.device))
+    lib = _lib.load()
+    rp = _lib.ptr(r) if r.numel() else None
+    if r.is_cuda:
+        rc = lib.meshy_zero_variance_groups(rp, r.numel(), off.data_ptr(), n_groups, float(tolerance),
+                                            flags.data_ptr(), _lib.stream_of(r.device))
+    else:
+        rc = lib.meshy_zero_variance_groups_host(rp, r.numel(), off.data_ptr(), n_groups, float(tolerance),
+                                                 flags.data_ptr())
     _lib.check(rc, "meshy_zero_variance_groups")
     return flags.view(torch.bool)
 

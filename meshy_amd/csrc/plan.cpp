@@ -343,6 +343,36 @@ extern "C" int meshy_sample_loss_tokens(const float* mask, const int64_t* offset
     return MESHY_OK;
 }
 
+// Python's max()/min() over the group (a NaN first element stays, later NaNs
+// lose every comparison), then the spread against the tolerance; offsets are
+// clamped to the rewards as the device filter clamps them.
+extern "C" int meshy_zero_variance_groups_host(const double* raw_rewards, int64_t n_rewards,
+                                               const int64_t* group_offsets, int64_t n_groups, double tolerance,
+                                               uint8_t* flags) {
+    meshy::clear_error();
+    if (n_groups < 0 || n_rewards < 0)
+        return set_error(MESHY_EINVAL, "meshy_zero_variance_groups_host: negative count");
+    if (n_groups == 0) return MESHY_OK;
+    if ((!raw_rewards && n_rewards > 0) || !group_offsets || !flags)
+        return set_error(MESHY_ENULL, "meshy_zero_variance_groups_host: NULL pointer");
+    for (int64_t g = 0; g < n_groups; ++g) {
+        const int64_t b = std::min(std::max(group_offsets[g], static_cast<int64_t>(0)), n_rewards);
+        const int64_t e = std::min(std::max(group_offsets[g + 1], b), n_rewards);
+        if (e <= b) {
+            flags[g] = 1;
+            continue;
+        }
+        double hi = raw_rewards[b], lo = raw_rewards[b];
+        for (int64_t i = b + 1; i < e; ++i) {
+            const double r = raw_rewards[i];
+            if (r > hi) hi = r;
+            if (r < lo) lo = r;
+        }
+        flags[g] = static_cast<uint8_t>(hi - lo <= tolerance);
+    }
+    return MESHY_OK;
+}
+
 extern "C" int meshy_plan_build(const int64_t* lengths, const int64_t* loss_tokens, int64_t n,
                                 int64_t dp_size, const meshy_planner_cfg* cfg, meshy_plan_out* out) {
     meshy::clear_error();

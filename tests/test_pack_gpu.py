@@ -373,6 +373,13 @@ def test_zero_variance_groups_match_oracle(dev):
         assert got == want, tol
     assert zero_variance_groups(torch.zeros(0, dtype=torch.float64, device=dev),
                                 torch.zeros(3, dtype=torch.int64, device=dev)).cpu().tolist() == [True, True]
+    # the host filter gives the device filter's flags; mixed placements are refused
+    host = zero_variance_groups(torch.tensor(vals, dtype=torch.float64), torch.tensor(offs)).tolist()
+    dev_flags = zero_variance_groups(torch.tensor(vals, dtype=torch.float64, device=dev),
+                                     torch.tensor(offs, device=dev)).cpu().tolist()
+    assert host == dev_flags
+    with pytest.raises(ValueError, match="on the GPU or both on the host"):
+        zero_variance_groups(torch.tensor(vals, dtype=torch.float64, device=dev), torch.tensor(offs))
 
 
 # ------------------------------------------------------------ pack_step (256 GRPO samples)
