@@ -1228,11 +1228,12 @@ def bench_rollout_metrics(runs, no_cpu):
 def bench_group_advantages(runs, no_cpu):
     """GRPO advantages and the zero-variance filter of a whole step (the 32
     groups of 8 of the 256-sample GRPO batch): the advantages in one device
-    call (the rewards' host-to-device copy, one launch, the copy back), the
-    filter in one host call over the host rewards (and, for the record, in
-    one device call), next to the reference's per-group host functions
-    (rollout.py:88-115) called once per group as its rollout worker does,
-    summed over the 32 groups."""
+    call (the rewards' host-to-device copy, one launch, the copy back) and
+    through the per-group plugin form (a host call per group), the filter in
+    one host call over the host rewards (and, for the record, in one device
+    call), next to the reference's per-group host functions (rollout.py:
+    88-115) called once per group as its rollout worker does, summed over the
+    32 groups."""
     import numpy as np
     import torch
 
@@ -1254,11 +1255,25 @@ def bench_group_advantages(runs, no_cpu):
         # the rewards where the rollout worker holds them: on the host
         zero_variance_groups(torch.from_numpy(rewards.astype(np.float64)), torch.from_numpy(group_offsets)).tolist()
 
+    # the per-group advantage plugin, called once per group on sample objects
+    # as the rollout worker calls its advantage_fn (rollout.py:580-587)
+    from types import SimpleNamespace as NS
+
+    from meshy_amd.advantage import grpo_advantage
+
+    group_samples = [[NS(reward=float(x), advantage=None) for x in rewards[group_offsets[g]:group_offsets[g + 1]]]
+                     for g in range(n_groups)]
+
+    def plugin_all():
+        for grp in group_samples:
+            grpo_advantage(grp)
+
     out = {
         "group_size": 8, "n_groups": n_groups,
         "grpo_advantages_us_all_groups": round(batched(grpo_advantages, np.float32), 1),
         "zero_variance_groups_us_all_groups": round(_wall_ms(host_filter, reps, gpu=False) * 1e3, 1),
         "zero_variance_groups_device_us_all_groups": round(batched(zero_variance_groups, np.float64), 1),
+        "grpo_advantage_plugin_us_all_groups": round(_wall_ms(plugin_all, reps, gpu=False) * 1e3, 1),
     }
     if not no_cpu:
         from oracle import grpo as ogrpo

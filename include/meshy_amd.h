@@ -193,6 +193,11 @@ int meshy_pack_micro_batches(const meshy_pack_args* args, hipStream_t stream);
  * ---------------------------------------------------------------------- */
 int meshy_grpo_advantage(const float* rewards, int64_t n_rewards, const int64_t* group_offsets,
                          int64_t n_groups, float* advantages, hipStream_t stream);
+/* The same over host arrays, for rewards the rollout worker holds on the host
+ * (its per-group advantage plugin, rollout.py:580-587): no device round trip.
+ * fp32 results, the mean and the variance summed in fp64. */
+int meshy_grpo_advantage_host(const float* rewards, int64_t n_rewards, const int64_t* group_offsets,
+                              int64_t n_groups, float* advantages);
 
 /* ------------------------------------------------------------------------
  * Zero-variance group filter (device).

@@ -240,6 +240,7 @@ SIGNATURES = {
     "meshy_grpo_advantage": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
     "meshy_zero_variance_groups": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_double, c_void_p, c_void_p]),
     "meshy_zero_variance_groups_host": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_double, c_void_p]),
+    "meshy_grpo_advantage_host": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p]),
     "meshy_logprob_entropy_fwd": (
         c_int,
         [c_void_p, c_int64, c_int64, c_int64, c_int64, c_int64, c_void_p, c_void_p, c_void_p,

@@ -16,6 +16,7 @@
 // reference's scan of every open micro is O(n m).
 #include <algorithm>
 #include <climits>
+#include <cmath>
 #include <new>
 #include <vector>
 
@@ -339,6 +340,41 @@ extern "C" int meshy_sample_loss_tokens(const float* mask, const int64_t* offset
         const float* m = mask + a;
         for (int64_t t = 1; t < L; ++t) c += static_cast<int32_t>(m[t] > 0.f);
         loss_tokens[i] = L > 1 ? c : 0;
+    }
+    return MESHY_OK;
+}
+
+// GRPO advantages of host rewards: per group (offsets clamped to the rewards
+// as the device kernel clamps them) a size-1 group keeps its reward, any other
+// gets (r - mean) / max(unbiased std, 1e-8), in fp32 like the reference's
+// torch arithmetic, with the two sums taken in fp64.
+extern "C" int meshy_grpo_advantage_host(const float* rewards, int64_t n_rewards, const int64_t* group_offsets,
+                                         int64_t n_groups, float* advantages) {
+    meshy::clear_error();
+    if (n_groups < 0 || n_rewards < 0) return set_error(MESHY_EINVAL, "meshy_grpo_advantage_host: negative count");
+    if (n_groups == 0) return MESHY_OK;
+    if ((!rewards && n_rewards > 0) || !group_offsets || (!advantages && n_rewards > 0))
+        return set_error(MESHY_ENULL, "meshy_grpo_advantage_host: NULL pointer");
+    for (int64_t g = 0; g < n_groups; ++g) {
+        const int64_t b = std::min(std::max(group_offsets[g], static_cast<int64_t>(0)), n_rewards);
+        const int64_t e = std::min(std::max(group_offsets[g + 1], b), n_rewards);
+        const int64_t n = e - b;
+        if (n <= 0) continue;
+        if (n == 1) {
+            advantages[b] = rewards[b];
+            continue;
+        }
+        double sum = 0.0;
+        for (int64_t i = b; i < e; ++i) sum += rewards[i];
+        const float mean = static_cast<float>(sum / static_cast<double>(n));
+        double sq = 0.0;
+        for (int64_t i = b; i < e; ++i) {
+            const double d = static_cast<double>(rewards[i] - mean);
+            sq += d * d;
+        }
+        const float sd = static_cast<float>(std::sqrt(sq / static_cast<double>(n - 1)));
+        const float den = std::max(sd, 1e-8f);
+        for (int64_t i = b; i < e; ++i) advantages[i] = (rewards[i] - mean) / den;
     }
     return MESHY_OK;
 }

@@ -89,6 +89,8 @@ def _call(name, *args):
     ("meshy_zero_variance_groups", (None, 8, FAKE, 2, 1e-8, FAKE, None), ENULL, "NULL"),
     ("meshy_zero_variance_groups", (FAKE, 8, FAKE, 2, 1e-8, None, None), ENULL, "NULL"),
     ("meshy_zero_variance_groups_host", (FAKE, -1, FAKE, 2, 1e-8, FAKE), EINVAL, "negative"),
+    ("meshy_grpo_advantage_host", (FAKE, 8, FAKE, -1, FAKE), EINVAL, "negative"),
+    ("meshy_grpo_advantage_host", (FAKE, 8, None, 2, FAKE), ENULL, "NULL"),
     ("meshy_zero_variance_groups_host", (FAKE, 8, None, 2, 1e-8, FAKE), ENULL, "NULL"),
     ("meshy_segment_offsets", (FAKE, 10, 0, FAKE, None, None), EINVAL, "bad sizes"),
     ("meshy_stream_read", (FAKE, 4, 17, FAKE, None), EINVAL, "bad shape"),
