@@ -39,6 +39,8 @@
 namespace meshy {
 namespace {
 
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+
 constexpr int kThreads = 256;
 constexpr int kWaves = kThreads / kWave;
 constexpr int64_t kTile = 2048;
@@ -407,6 +409,9 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
         };
         const bool pos_lm = a.positive_lm_coef != 0.f;
         const float lo_c = 1.f - a.clip_low, hi_c = 1.f + a.clip_high;
+        float gval[kPer];  // the unit gradient of the thread's tokens, stored after the loop
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) gval[q] = 0.f;
         int cur = 0;
         float A = A_d[0], W = W_d[0];
 #pragma unroll
@@ -460,15 +465,31 @@ __global__ __launch_bounds__(kThreads) void k_ppo_tiles(meshy_ppo_args a, Worksp
             }
             if (!kLean && a.entropy) acc[TS_ENT] = fmaf(x.en, mk, acc[TS_ENT]);
             if (gu) {
-                // Nontemporal: the backward reads the unit gradient once, from
-                // HBM; kept out of the L2 it does not slow the kernel's end
-                // (21.4 against 23.5 us for the forward and backward of 1.83 M
-                // tokens, A/B on one box).
                 const bool real = d_first + slot < a.n_docs;  // the padding slot is not in the loss
-                __builtin_nontemporal_store(real ? token_grad_v(a, x, At, W, tok_scale) : 0.f, gu + i);
+                gval[q] = real ? token_grad_v(a, x, At, W, tok_scale) : 0.f;
             }
         }
         flush(cur);
+        if (gu) {
+            // Nontemporal: the backward reads the unit gradient once, from
+            // HBM, and kept out of the L2 it does not slow the kernel's end
+            // (21.4 against 23.5 us for the forward and backward of 1.83 M
+            // tokens, A/B on one box).  One 16-byte store per thread and half:
+            // the wave writes whole lines (a 4-byte store per token wrote
+            // 16-byte-strided pieces that the counters saw as 3.8x the bytes).
+#pragma unroll
+            for (int h = 0; h < kPer / 4; ++h) {
+                const int64_t i4 = t0 + h * (4 * kThreads) + 4 * threadIdx.x;
+                if (vec && i4 + 4 <= t1) {
+                    const f32x4 g4 = {gval[4 * h], gval[4 * h + 1], gval[4 * h + 2], gval[4 * h + 3]};
+                    __builtin_nontemporal_store(g4, reinterpret_cast<f32x4*>(gu + i4));
+                } else {
+#pragma unroll
+                    for (int e = 0; e < 4; ++e)
+                        if (i4 + e < t1) __builtin_nontemporal_store(gval[4 * h + e], gu + i4 + e);
+                }
+            }
+        }
         // The token sums that are sums of the slots.
 #pragma unroll
         for (int r = 0; r < kFastDocs; ++r) {
@@ -730,7 +751,7 @@ extern "C" int meshy_ppo_loss_fwd(const meshy_ppo_args* args, float* out, float*
     const bool lean = !a.use_icepop && !a.rollout_lp && !a.entropy && !a.adv_per_token;
     auto al16 = [](const void* p) { return reinterpret_cast<uintptr_t>(p) % 16 == 0; };
     const bool vec = al16(a.new_lp) && al16(a.old_lp) && al16(a.mask) && al16(a.rollout_lp) && al16(a.entropy) &&
-                     (!a.adv_per_token || al16(a.adv));
+                     (!a.adv_per_token || al16(a.adv)) && al16(a.grad_unit);
     if (lean)
         hipLaunchKernelGGL(k_ppo_tiles<true>, dim3(static_cast<unsigned>(nt)), dim3(kThreads), 0, stream, a, ws, vec);
     else
