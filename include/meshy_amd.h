@@ -113,6 +113,42 @@ int meshy_host_gather(const void* const* srcs, const int64_t* nbytes, int64_t n,
 int meshy_sample_loss_tokens(const float* mask, const int64_t* offsets, int64_t n,
                              int64_t seq_len, int64_t* lengths, int64_t* loss_tokens);
 
+/* The host plan of one packing step in one call (host): what
+ * TitanTrainer.plan_batch does before it builds each micro
+ * (meshy/backend/titan/trainer.py:577-588, then plan.py:211-288):
+ * meshy_sample_loss_tokens over the flat mask (cfg.seq_len), meshy_plan_build
+ * into `plan`, then, for `rank`, the tables meshy_pack_micro_batches reads,
+ * written where the caller stages them:
+ *   micro_seq_len[k]     the rank's k-th micro's seq_len        [n_local]
+ *   micro_out_off[k]     its first output element (seq_len x rows, rows = 1
+ *                        packed, max(documents, 1) padded)    [n_local + 1]
+ *   micro_doc_start[k]   its first document                   [n_local + 1]
+ *   doc_sample[j]        document j's global sample index     [n_local]
+ *   doc_len[j]           document j's length                  [n_local]
+ * and the counts n_micro, n_docs, max_micro_elems, max_docs_per_micro.  The
+ * errors are those of the two calls it makes. */
+typedef struct meshy_step_plan_args {
+    const float* mask;             /* [offsets[n]] host                       */
+    const int64_t* offsets;        /* [n + 1]                                 */
+    int64_t n;
+    int64_t dp_size;
+    int64_t rank;
+    meshy_planner_cfg cfg;
+    meshy_plan_out plan;
+    int64_t* lengths;              /* [n] out: tokens per sample              */
+    int64_t* loss_tokens;          /* [n] out                                 */
+    int64_t* micro_seq_len;        /* the rank's pack tables, out             */
+    int64_t* micro_out_off;
+    int32_t* micro_doc_start;
+    int32_t* doc_sample;
+    int64_t* doc_len;
+    int64_t n_micro;               /* out                                     */
+    int64_t n_docs;                /* out                                     */
+    int64_t max_micro_elems;       /* out                                     */
+    int64_t max_docs_per_micro;    /* out                                     */
+} meshy_step_plan_args;
+int meshy_step_plan(meshy_step_plan_args* args);
+
 /* ------------------------------------------------------------------------
  * Micro-batch materialisation (device).
  * Replaces build_micro_batch (meshy/backend/titan/batch.py:96-230): per-doc

@@ -71,6 +71,29 @@ class PlanOut(ctypes.Structure):
     ]
 
 
+class StepPlanArgs(ctypes.Structure):
+    _fields_ = [
+        ("mask", c_void_p),
+        ("offsets", c_void_p),
+        ("n", c_int64),
+        ("dp_size", c_int64),
+        ("rank", c_int64),
+        ("cfg", PlannerCfg),
+        ("plan", PlanOut),
+        ("lengths", c_void_p),
+        ("loss_tokens", c_void_p),
+        ("micro_seq_len", c_void_p),
+        ("micro_out_off", c_void_p),
+        ("micro_doc_start", c_void_p),
+        ("doc_sample", c_void_p),
+        ("doc_len", c_void_p),
+        ("n_micro", c_int64),
+        ("n_docs", c_int64),
+        ("max_micro_elems", c_int64),
+        ("max_docs_per_micro", c_int64),
+    ]
+
+
 class PackArgs(ctypes.Structure):
     _fields_ = [
         ("tokens", c_void_p),
@@ -235,6 +258,7 @@ SIGNATURES = {
         [c_void_p, c_void_p, c_int64, c_int64, POINTER(PlannerCfg), POINTER(PlanOut)],
     ),
     "meshy_sample_loss_tokens": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "meshy_step_plan": (c_int, [POINTER(StepPlanArgs)]),
     "meshy_host_gather": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int]),
     "meshy_pack_micro_batches": (c_int, [POINTER(PackArgs), c_void_p]),
     "meshy_grpo_advantage": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),

@@ -230,6 +230,8 @@ class PackJob:
     adv_tokens_dev: torch.Tensor | None = None
     #: Teacher Top-K width staged with the samples (0: no Teacher columns).
     teacher_k: int = 0
+    #: The HIP stream handle to launch on (None: the device's current stream).
+    stream: int | None = None
     #: Per micro (ids, logprobs) Teacher columns in the micro's layout, filled by
     #: ``launch_pack`` when ``teacher_k`` > 0.
     teacher_views: list | None = None
@@ -494,7 +496,8 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
         a.teacher_lps = lay.addr(base, "teacher_lps")
         a.teacher_ids_out = out_addr("teacher_ids")
         a.teacher_lps_out = out_addr("teacher_lps")
-    rc = lib.meshy_pack_micro_batches(_lib.ctypes.byref(a), torch.cuda.current_stream(device).cuda_stream)
+    rc = lib.meshy_pack_micro_batches(_lib.ctypes.byref(a),
+                                      job.stream if job.stream is not None else _lib.stream_of(device))
     _lib.check(rc, "meshy_pack_micro_batches")
     views = _PackViews(job, sharder, obuf, out_lay, lay, dbuf)
 

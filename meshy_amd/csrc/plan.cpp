@@ -428,3 +428,51 @@ extern "C" int meshy_plan_build(const int64_t* lengths, const int64_t* loss_toke
         return set_error(MESHY_EINVAL, "meshy_plan_build: out of host memory");
     }
 }
+
+extern "C" int meshy_step_plan(meshy_step_plan_args* args) {
+    meshy::clear_error();
+    if (!args) return set_error(MESHY_ENULL, "meshy_step_plan: args is NULL");
+    meshy_step_plan_args& a = *args;
+    if (a.n <= 0) return set_error(MESHY_EEMPTY, "cannot plan an empty batch");
+    if (a.dp_size <= 0 || a.rank < 0 || a.rank >= a.dp_size)
+        return set_error(MESHY_EINVAL, "meshy_step_plan: rank %lld outside %lld ranks",
+                         static_cast<long long>(a.rank), static_cast<long long>(a.dp_size));
+    if (!a.micro_seq_len || !a.micro_out_off || !a.micro_doc_start || !a.doc_sample || !a.doc_len)
+        return set_error(MESHY_ENULL, "meshy_step_plan: every pack table is required");
+    int rc = meshy_sample_loss_tokens(a.mask, a.offsets, a.n, a.cfg.seq_len, a.lengths, a.loss_tokens);
+    if (rc) return rc;
+    rc = meshy_plan_build(a.lengths, a.loss_tokens, a.n, a.dp_size, &a.cfg, &a.plan);
+    if (rc) return rc;
+    // The rank's slice of the planner's tables, as the pack reads them.
+    const int64_t n_local = a.n / a.dp_size;
+    const int64_t nm = a.plan.n_micro_total;
+    const int64_t* seq = a.plan.micro_seq_len + a.rank * n_local;
+    const int32_t* start = a.plan.micro_doc_start + a.rank * (n_local + 1);
+    const int32_t* local = a.plan.local_indices + a.rank * n_local;
+    const int32_t* dsample = a.plan.doc_sample + a.rank * n_local;
+    const int64_t* dlen = a.plan.doc_len + a.rank * n_local;
+    const bool packed = a.cfg.layout == MESHY_LAYOUT_PACKED;
+    int64_t off = 0, max_elems = 0, max_docs = 0;
+    a.micro_out_off[0] = 0;
+    for (int64_t k = 0; k < nm; ++k) {
+        const int64_t docs = static_cast<int64_t>(start[k + 1]) - start[k];
+        const int64_t elems = seq[k] * (packed ? 1 : std::max<int64_t>(docs, 1));
+        a.micro_seq_len[k] = seq[k];
+        a.micro_doc_start[k] = start[k];
+        off += elems;
+        a.micro_out_off[k + 1] = off;
+        max_elems = std::max(max_elems, elems);
+        max_docs = std::max(max_docs, docs);
+    }
+    a.micro_doc_start[nm] = start[nm];
+    const int64_t nd = start[nm];
+    for (int64_t j = 0; j < nd; ++j) {
+        a.doc_sample[j] = local[dsample[j]];
+        a.doc_len[j] = dlen[j];
+    }
+    a.n_micro = nm;
+    a.n_docs = nd;
+    a.max_micro_elems = max_elems;
+    a.max_docs_per_micro = max_docs;
+    return MESHY_OK;
+}

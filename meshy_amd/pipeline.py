@@ -25,7 +25,7 @@ import torch
 from . import _lib
 from .batch import Batch, PackJob, _Layout, launch_pack
 from .hostio import gather_into
-from .plan import Plan, PlannerConfig, plan_tables, tables_to_plan
+from .plan import Plan, PlannerConfig, PlanTables, tables_to_plan
 from .wire import jagged_parts
 
 
@@ -72,11 +72,53 @@ class RaggedSamples:
         self._np_buf = self.buf.numpy()
         self._np: dict[str, np.ndarray] = {}
         self.copied = None  # event of the last copy of the plan tables out of buf
+        self._step_args = None  # meshy_step_plan's struct over this buffer
         self.view("s_off").copy_(torch.from_numpy(self.offsets))
         self.view("pos_w").zero_()
 
     def view(self, name: str) -> torch.Tensor:
         return self.lay.view(self.buf, name)
+
+    def step_plan_args(self, cfg: PlannerConfig, dp_size: int, rank: int, tables: PlanTables) -> "_lib.StepPlanArgs":
+        """The argument struct of ``meshy_step_plan`` for this step: the staged
+        mask and offsets, scratch for the counts, ``tables`` for the plan and
+        this buffer's pack-table regions (the pointers made once)."""
+        a = self._step_args
+        if a is None:
+            a = self._step_args = _lib.StepPlanArgs()
+            base = self.buf.data_ptr()
+            self._counts = np.empty((2, self.n), np.int64)
+            a.mask = self.lay.addr(base, "mask")
+            a.offsets = self.lay.addr(base, "s_off")
+            a.n = self.n
+            a.lengths = self._counts[0].ctypes.data
+            a.loss_tokens = self._counts[1].ctypes.data
+            for field, region in (("micro_seq_len", "seq"), ("micro_out_off", "out_off"),
+                                  ("micro_doc_start", "doc_start"), ("doc_sample", "doc_sample"),
+                                  ("doc_len", "doc_len")):
+                setattr(a, field, self.lay.addr(base, region))
+        a.dp_size, a.rank = dp_size, rank
+        c = a.cfg
+        c.layout = _lib.MESHY_LAYOUT_PACKED if cfg.layout == "packed" else _lib.MESHY_LAYOUT_PADDED
+        c.mini_batch_size = cfg.mini_batch_size
+        c.seq_len = cfg.seq_len
+        c.align = cfg.align
+        c.max_tokens_per_micro = cfg.max_tokens_per_micro or 0
+        c.micro_batch_size = cfg.micro_batch_size or 0
+        a.plan = tables.c_struct()
+        return a
+
+    def record_copy(self, device: torch.device) -> None:
+        """Marks the end of the copy just queued out of this buffer (on the
+        current stream of ``device``), which the next step waits for before it
+        rewrites the plan tables."""
+        ev = self.copied
+        if ev is None:
+            ev = self.copied = torch.cuda.Event()
+        if device.index is None or device.index == torch.cuda.current_device():
+            ev.record()
+        else:
+            ev.record(torch.cuda.current_stream(device))
 
     def np_view(self, name: str) -> np.ndarray:
         """The region as a numpy array over the same pinned memory (cached)."""
@@ -168,60 +210,82 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
     """Plan, copy, normalise rewards and build every micro of ``rank``.
 
     The samples' part of the staging buffer is copied to the device first, so
-    the transfer runs while the host plans; the plan tables follow in a second,
-    small copy.  The Plan dataclasses are built when ``PackResult.plan`` is
-    first read (``with_plan_objects`` builds them here)."""
+    the transfer runs while the host plans.  One native call
+    (``meshy_step_plan``) counts the loss tokens, plans and writes this rank's
+    pack tables into the staging buffer; they follow in a second, small copy.
+    The Plan dataclasses are built when ``PackResult.plan`` is first read
+    (``with_plan_objects`` builds them here)."""
     device = torch.device(device)
-    stream = torch.cuda.current_stream(device)
+    handle = _lib.stream_of(device)
     lay = ragged.lay
     dbuf = torch.empty(lay.size, dtype=torch.uint8, device=device)
     cut = ragged.tables_at
     dbuf[:cut].copy_(ragged.buf[:cut], non_blocking=True)
-    lengths, loss = ragged.sample_lengths(cfg.seq_len)
-    t = plan_tables(lengths, loss, dp_size, cfg)
     if ragged.copied is not None:
-        ragged.copied.synchronize()  # the tables below reuse the pinned buffer
-    n_local = t.n_local
-    nm = t.n_micro_total
-    seq = t.micro_seq_len[rank * n_local: rank * n_local + nm]
-    start = t.micro_doc_start[rank * (n_local + 1): rank * (n_local + 1) + nm + 1]
-    local = t.local_indices[rank * n_local:(rank + 1) * n_local]
-    dsample = local[t.doc_sample[rank * n_local:(rank + 1) * n_local]]  # global sample index
-    dlen = t.doc_len[rank * n_local:(rank + 1) * n_local]
-    n_docs = np.diff(start)
-    packed = cfg.layout == "packed"
-    rows = np.ones(nm, np.int64) if packed else np.maximum(n_docs, 1)
-    elems = seq * rows
-    out_off = np.zeros(nm + 1, np.int64)
-    np.cumsum(elems, out=out_off[1:])
-    ragged.np_view("seq")[:nm] = seq
-    ragged.np_view("out_off")[:nm + 1] = out_off
-    ragged.np_view("doc_start")[:nm + 1] = start
-    nd_total = int(start[-1])
-    ragged.np_view("doc_sample")[:nd_total] = dsample[:nd_total]
-    ragged.np_view("doc_len")[:nd_total] = dlen[:nd_total]
+        ragged.copied.synchronize()  # the tables below reuse the pinned buffer the last copy read
+    if dp_size <= 0 or ragged.n % dp_size != 0:
+        raise ValueError(
+            f"batch size {ragged.n} is not divisible by DP size {dp_size}; adjust "
+            "rollout.batch_size * group_size to a multiple of dp_replicate * dp_shard"
+        )
+    t = PlanTables(ragged.n, dp_size, cfg.mini_batch_size)
+    a = ragged.step_plan_args(cfg, dp_size, rank, t)
+    lib = _lib.load()
+    _lib.check(lib.meshy_step_plan(_lib.ctypes.byref(a)), "meshy_step_plan")
+    t.n_micro_total = int(a.plan.n_micro_total)
+    nm, nd_total = int(a.n_micro), int(a.n_docs)
 
     dbuf[cut:].copy_(ragged.buf[cut:], non_blocking=True)
-    ragged.copied = torch.cuda.Event()
-    ragged.copied.record(stream)
+    ragged.record_copy(device)
 
+    base = dbuf.data_ptr()
     adv = lay.view(dbuf, "adv_samples")[:ragged.n]
-    rc = _lib.load().meshy_grpo_advantage(lay.view(dbuf, "rewards").data_ptr(), ragged.n,
-                                          lay.view(dbuf, "group_off").data_ptr(), ragged.n_groups, adv.data_ptr(),
-                                          stream.cuda_stream)
+    rc = lib.meshy_grpo_advantage(lay.addr(base, "rewards"), ragged.n, lay.addr(base, "group_off"), ragged.n_groups,
+                                  adv.data_ptr(), handle)
     _lib.check(rc, "meshy_grpo_advantage")
 
-    sq, st, dl = seq.tolist(), start.tolist(), dlen[:nd_total].tolist()
-    micros = tuple(_LiteMicro(sq[k], st[k + 1] - st[k], sum(dl[st[k]:st[k + 1]]), tuple(dl[st[k]:st[k + 1]]))
-                   for k in range(nm))
+    seq = ragged.np_view("seq")[:nm]
+    start = ragged.np_view("doc_start")[:nm + 1]
+    out_off = ragged.np_view("out_off")[:nm + 1]
+    packed = cfg.layout == "packed"
     job = PackJob(
-        micros=micros, layout=cfg.layout, device=device, dbuf=dbuf, lay=lay,
+        micros=_LiteMicros(seq.tolist(), start.tolist(), ragged.np_view("doc_len")[:nd_total].tolist()),
+        layout=cfg.layout, device=device, dbuf=dbuf, lay=lay,
         need_rollout_lp=ragged.need_rollout_lp, per_token_adv=False, n_samples=ragged.n, seq=seq,
-        rows=rows, out_off=out_off, doc_start=start, max_elems=int(elems.max()) if nm else 0,
-        max_docs=int(n_docs.max()) if nm else 0, adv_samples=adv, broadcast_advantages=broadcast_advantages,
+        rows=np.ones(nm, np.int64) if packed else np.maximum(np.diff(start), 1), out_off=out_off, doc_start=start,
+        max_elems=int(a.max_micro_elems), max_docs=int(a.max_docs_per_micro), adv_samples=adv,
+        broadcast_advantages=broadcast_advantages, stream=handle,
     )
     batches = launch_pack(job)
     return PackResult(tables_to_plan(t) if with_plan_objects else None, t, batches, adv)
+
+
+class _LiteMicros:
+    """The micros of a step as ``launch_pack`` reads them, each made on first
+    use from the host lists of the plan (no dataclass per micro)."""
+
+    __slots__ = ("seq", "start", "dlen", "_made")
+
+    def __init__(self, seq: list, start: list, dlen: list) -> None:
+        self.seq, self.start, self.dlen = seq, start, dlen
+        self._made: dict = {}
+
+    def __len__(self) -> int:
+        return len(self.seq)
+
+    def __getitem__(self, k: int) -> "_LiteMicro":
+        m = self._made.get(k)
+        if m is None:
+            if not -len(self.seq) <= k < len(self.seq):
+                raise IndexError(k)
+            k %= len(self.seq)
+            a, b = self.start[k], self.start[k + 1]
+            dl = tuple(self.dlen[a:b])
+            m = self._made[k] = _LiteMicro(self.seq[k], b - a, sum(dl), dl)
+        return m
+
+    def __iter__(self):
+        return (self[k] for k in range(len(self.seq)))
 
 
 class _LiteMicro:

@@ -133,28 +133,33 @@ def _frozen(cls, **fields):
 
 
 class PlanTables:
-    """The flat CSR tables ``meshy_plan_build`` fills (see include/meshy_amd.h)."""
+    """The flat CSR tables ``meshy_plan_build`` fills (see include/meshy_amd.h),
+    as numpy views of one zeroed host buffer."""
 
     def __init__(self, n: int, dp: int, mini_batch_size: int) -> None:
         n_local = n // dp
         n_mini = -(-n_local // mini_batch_size)
         self.n, self.dp, self.n_local, self.n_mini = n, dp, n_local, n_mini
-        self.local_indices = np.zeros(dp * n_local, np.int32)
-        self.mini_n_micro = np.zeros(n_mini, np.int32)
-        self.mini_n_docs_global = np.zeros(n_mini, np.int64)
-        self.mini_n_tokens_global = np.zeros(n_mini, np.int64)
-        self.mini_tokens_per_rank = np.zeros(n_mini * dp, np.int64)
-        self.micro_seq_len = np.zeros(dp * n_local, np.int64)
-        self.micro_doc_start = np.zeros(dp * (n_local + 1), np.int32)
-        self.doc_sample = np.zeros(dp * n_local, np.int32)
-        self.doc_len = np.zeros(dp * n_local, np.int64)
+        counts = (dp * n_local, n_mini, n_mini, n_mini, n_mini * dp, dp * n_local, dp * (n_local + 1),
+                  dp * n_local, dp * n_local)
+        offs, total = [], 0
+        for (_, dtype), c in zip(self._FIELDS, counts):
+            offs.append(total)
+            total += -(-c * np.dtype(dtype).itemsize // 8) * 8
+        buf = np.zeros(max(total, 8), np.uint8)
+        self._base = buf.__array_interface__["data"][0]
+        self._offs = offs
+        for (name, dtype), o, c in zip(self._FIELDS, offs, counts):
+            setattr(self, name, buf[o:o + c * np.dtype(dtype).itemsize].view(dtype))
         self.n_micro_total = 0
 
+    _FIELDS = (("local_indices", np.int32), ("mini_n_micro", np.int32), ("mini_n_docs_global", np.int64),
+               ("mini_n_tokens_global", np.int64), ("mini_tokens_per_rank", np.int64), ("micro_seq_len", np.int64),
+               ("micro_doc_start", np.int32), ("doc_sample", np.int32), ("doc_len", np.int64))
+
     def c_struct(self) -> _lib.PlanOut:
-        return _lib.PlanOut(_np_ptr(self.local_indices), _np_ptr(self.mini_n_micro),
-                            _np_ptr(self.mini_n_docs_global), _np_ptr(self.mini_n_tokens_global),
-                            _np_ptr(self.mini_tokens_per_rank), _np_ptr(self.micro_seq_len),
-                            _np_ptr(self.micro_doc_start), _np_ptr(self.doc_sample), _np_ptr(self.doc_len), 0, 0)
+        b = self._base
+        return _lib.PlanOut(*[b + o for o in self._offs], 0, 0)
 
 
 def _as_int64(x: Sequence[int]) -> np.ndarray:
