@@ -520,9 +520,10 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
 
     out: list[Batch] = []
     new = object.__new__
+    nd = views.nd
     for k in range(n_micro):
         mb = new(PackedBatch)
-        mb.__dict__.update(n_docs=views.nd[k], _src=views, _k=k)
+        mb.__dict__ = {"n_docs": nd[k], "_src": views, "_k": k}
         out.append(mb)
     return out
 

@@ -73,6 +73,7 @@ class RaggedSamples:
         self._np: dict[str, np.ndarray] = {}
         self.copied = None  # event of the last copy of the plan tables out of buf
         self._step_args = None  # meshy_step_plan's struct over this buffer
+        self._stream = None  # (raw handle, torch Stream) of the last copy's stream
         self.view("s_off").copy_(torch.from_numpy(self.offsets))
         self.view("pos_w").zero_()
 
@@ -115,10 +116,12 @@ class RaggedSamples:
         ev = self.copied
         if ev is None:
             ev = self.copied = torch.cuda.Event()
-        if device.index is None or device.index == torch.cuda.current_device():
-            ev.record()
-        else:
-            ev.record(torch.cuda.current_stream(device))
+        # The stream object is kept while the device's current stream stays the
+        # same (building one per call costs more than the rest of the record).
+        handle = _lib.stream_of(device)
+        if self._stream is None or self._stream[0] != handle:
+            self._stream = (handle, torch.cuda.current_stream(device))
+        ev.record(self._stream[1])
 
     def np_view(self, name: str) -> np.ndarray:
         """The region as a numpy array over the same pinned memory (cached)."""

@@ -143,19 +143,21 @@ class PlanTables:
         counts = (dp * n_local, n_mini, n_mini, n_mini, n_mini * dp, dp * n_local, dp * (n_local + 1),
                   dp * n_local, dp * n_local)
         offs, total = [], 0
-        for (_, dtype), c in zip(self._FIELDS, counts):
+        for (_, _, size), c in zip(self._FIELDS, counts):
             offs.append(total)
-            total += -(-c * np.dtype(dtype).itemsize // 8) * 8
+            total += -(-c * size // 8) * 8
         buf = np.zeros(max(total, 8), np.uint8)
         self._base = buf.__array_interface__["data"][0]
         self._offs = offs
-        for (name, dtype), o, c in zip(self._FIELDS, offs, counts):
-            setattr(self, name, buf[o:o + c * np.dtype(dtype).itemsize].view(dtype))
+        d = self.__dict__
+        for (name, dtype, size), o, c in zip(self._FIELDS, offs, counts):
+            d[name] = buf[o:o + c * size].view(dtype)
         self.n_micro_total = 0
 
-    _FIELDS = (("local_indices", np.int32), ("mini_n_micro", np.int32), ("mini_n_docs_global", np.int64),
-               ("mini_n_tokens_global", np.int64), ("mini_tokens_per_rank", np.int64), ("micro_seq_len", np.int64),
-               ("micro_doc_start", np.int32), ("doc_sample", np.int32), ("doc_len", np.int64))
+    _FIELDS = (("local_indices", np.int32, 4), ("mini_n_micro", np.int32, 4), ("mini_n_docs_global", np.int64, 8),
+               ("mini_n_tokens_global", np.int64, 8), ("mini_tokens_per_rank", np.int64, 8),
+               ("micro_seq_len", np.int64, 8), ("micro_doc_start", np.int32, 4), ("doc_sample", np.int32, 4),
+               ("doc_len", np.int64, 8))
 
     def c_struct(self) -> _lib.PlanOut:
         b = self._base

@@ -76,7 +76,7 @@ def test_step_plan_equals_the_separate_calls(layout, dp, seed):
         assert lib.meshy_step_plan(ctypes.byref(a)) == 0, lib.meshy_last_error()
         t.n_micro_total = a.plan.n_micro_total
         assert np.array_equal(counts[0], ln) and np.array_equal(counts[1], lt)
-        for name, _ in PlanTables._FIELDS:
+        for name, _, _ in PlanTables._FIELDS:
             assert np.array_equal(getattr(t, name), getattr(want_t, name)), name
         w_seq, w_off, w_start, w_ds, w_dl, w_max_e, w_max_d = _derived(want_t, rank, layout == "packed")
         nm, nd = a.n_micro, a.n_docs
