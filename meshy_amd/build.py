@@ -62,7 +62,9 @@ EXTRA_FLAGS = {"synth.hip": ["-ffp-contract=off"]}
 
 def _compile(src: str, verbose: bool) -> str:
     obj = os.path.join(BUILD_DIR, os.path.basename(src) + ".o")
-    lang = ["-x", "hip"] if src.endswith(".hip") else []
+    # .hip sources are compiled for the device and the host; the .cpp sources
+    # are host code only (no device pass).
+    lang = ["-x", "hip"] if src.endswith(".hip") else ["--offload-host-only"]
     cmd = [hipcc(), *COMMON_FLAGS, *EXTRA_FLAGS.get(src, []), *lang, "-c", os.path.join(CSRC, src), "-o", obj]
     if verbose:
         print(" ".join(cmd), flush=True)

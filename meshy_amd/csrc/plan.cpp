@@ -322,6 +322,18 @@ int plan_impl(const int64_t* lengths, const int64_t* loss_tokens, int64_t n, int
 
 }  // namespace
 
+namespace {
+
+// #(m[t] > 0) over n floats; branch-free so it vectorises, with an AVX2 form
+// picked at load time where the CPU has it.
+__attribute__((target_clones("avx2", "default"))) int64_t count_positive(const float* m, int64_t n) {
+    int32_t c = 0;
+    for (int64_t t = 0; t < n; ++t) c += static_cast<int32_t>(m[t] > 0.f);
+    return c;
+}
+
+}  // namespace
+
 extern "C" int meshy_sample_loss_tokens(const float* mask, const int64_t* offsets, int64_t n,
                                         int64_t seq_len, int64_t* lengths, int64_t* loss_tokens) {
     meshy::clear_error();
@@ -335,11 +347,7 @@ extern "C" int meshy_sample_loss_tokens(const float* mask, const int64_t* offset
                                       static_cast<long long>(i));
         lengths[i] = len;
         const int64_t L = std::min(len, seq_len);
-        // Branch-free so the compiler vectorises the count.
-        int32_t c = 0;
-        const float* m = mask + a;
-        for (int64_t t = 1; t < L; ++t) c += static_cast<int32_t>(m[t] > 0.f);
-        loss_tokens[i] = L > 1 ? c : 0;
+        loss_tokens[i] = L > 1 ? count_positive(mask + a + 1, L - 1) : 0;
     }
     return MESHY_OK;
 }
