@@ -85,6 +85,7 @@ class _Staging:
         self.buf: torch.Tensor | None = None
         self.np: np.ndarray | None = None  # the same pinned memory, as numpy
         self.event = None
+        self._stream = None
 
     def get(self, nbytes: int) -> torch.Tensor:
         if self.event is not None:
@@ -94,9 +95,15 @@ class _Staging:
             self.np = self.buf.numpy()
         return self.buf
 
-    def mark(self, stream) -> None:
-        self.event = torch.cuda.Event()
-        self.event.record(stream)
+    def mark(self, device: torch.device, handle: int) -> None:
+        """Records the end of the copy just queued out of the buffer, on the
+        stream whose raw handle is ``handle`` (the stream object is kept while
+        the device's current stream stays the same)."""
+        if self.event is None:
+            self.event = torch.cuda.Event()
+        if self._stream is None or self._stream[0] != handle:
+            self._stream = (handle, torch.cuda.current_stream(device))
+        self.event.record(self._stream[1])
 
 
 _STAGING: dict[int, _Staging] = {}
@@ -377,15 +384,15 @@ def stage_micro_batches(
         lay.np_view(hnp, "doc_sample")[:n_docs_total] = doc_sample
         lay.np_view(hnp, "pos_w")[:n_docs_total] = pos_w
 
-    stream = torch.cuda.current_stream(device)
+    handle = _lib.stream_of(device)
     dbuf = torch.empty(lay.size, dtype=torch.uint8, device=device)
     dbuf.copy_(host[:lay.size], non_blocking=True)
-    stage.mark(stream)
+    stage.mark(device, handle)
     return PackJob(
         micros=tuple(micros), layout=layout, device=device, dbuf=dbuf, lay=lay,
         need_rollout_lp=need_rollout_lp, per_token_adv=per_token_adv, n_samples=n_s, seq=seq, rows=rows,
         out_off=out_off, doc_start=doc_start, max_elems=int(elems.max()) if n_micro else 0,
-        max_docs=int(n_docs.max()) if n_micro else 0, adv_tokens_dev=adv_dev, teacher_k=teacher_k,
+        max_docs=int(n_docs.max()) if n_micro else 0, adv_tokens_dev=adv_dev, teacher_k=teacher_k, stream=handle,
     )
 
 
