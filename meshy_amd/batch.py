@@ -265,10 +265,15 @@ def stage_micro_batches(
     if device.type != "cuda":
         raise ValueError("meshy_amd builds micro-batches on a HIP device; pass a cuda device")
 
+    micros = tuple(micros)
+    if not teacher:
+        job = _stage_common(samples, micros, layout, device, need_rollout_lp)
+        if job is not None:
+            return job
+
     # Samples used by these micros, remapped to a compact list in order of
     # first use, with the longest prefix any micro reads of each, and the
     # per-document tables: one native pass over the micros.
-    micros = tuple(micros)
     used_b, need_b, ds_b, dl_b, seq_b, nd_b, nt_b = _lib.stage().plan_tables(micros, len(samples))
     used = np.frombuffer(used_b, np.int64)
     need_len = np.frombuffer(need_b, np.int64)
@@ -393,6 +398,48 @@ def stage_micro_batches(
         need_rollout_lp=need_rollout_lp, per_token_adv=per_token_adv, n_samples=n_s, seq=seq, rows=rows,
         out_off=out_off, doc_start=doc_start, max_elems=int(elems.max()) if n_micro else 0,
         max_docs=int(n_docs.max()) if n_micro else 0, adv_tokens_dev=adv_dev, teacher_k=teacher_k, stream=handle,
+    )
+
+
+# Staging regions in the order stage_micro_batches lays them out without
+# per-token advantages or Teacher columns (the tokens' dtype is chosen per call).
+_COMMON_REGIONS = (("tokens", None), ("mask", torch.float32), ("logprobs", torch.float32),
+                   ("adv_samples", torch.float32), ("s_off", torch.int64), ("seq", torch.int64),
+                   ("out_off", torch.int64), ("doc_len", torch.int64), ("doc_start", torch.int32),
+                   ("doc_sample", torch.int32), ("pos_w", torch.float32))
+
+
+def _stage_common(samples, micros: tuple, layout: str, device: torch.device, need_rollout_lp: bool) -> PackJob | None:
+    """``stage_micro_batches`` in one native pass when every used sample's
+    tokens (all int64 or all int32), mask and log-probs are CPU contiguous
+    tensors and none has per-token advantages; None otherwise (nothing
+    staged), and the general path runs."""
+    stage = _STAGING.setdefault(device.index or 0, _Staging())
+    host = stage.get(0)  # waits for the buffer's previous copy
+    st = _lib.stage()
+    packed = layout == "packed"
+    res = st.stage_micros(samples, micros, packed, need_rollout_lp, host.data_ptr(), host.numel(), _gather_fn())
+    if isinstance(res, int):  # the buffer is too small: grow it and stage again
+        host = stage.get(res)
+        res = st.stage_micros(samples, micros, packed, need_rollout_lp, host.data_ptr(), host.numel(), _gather_fn())
+    if res is None:
+        return None
+    size, bounds_b, n_s, _total, tok64, _nd, max_elems, max_docs, seq_b, rows_b, out_off_b, doc_start_b = res
+    bounds = np.frombuffer(bounds_b, np.int64).tolist()
+    lay = _Layout()
+    lay.size = size
+    tok_dtype = torch.int64 if tok64 else torch.int32
+    lay.regions = {name: (bounds[2 * i], bounds[2 * i + 1], dtype or tok_dtype)
+                   for i, (name, dtype) in enumerate(_COMMON_REGIONS) if bounds[2 * i] >= 0}
+    handle = _lib.stream_of(device)
+    dbuf = torch.empty(size, dtype=torch.uint8, device=device)
+    dbuf.copy_(host[:size], non_blocking=True)
+    stage.mark(device, handle)
+    return PackJob(
+        micros=micros, layout=layout, device=device, dbuf=dbuf, lay=lay, need_rollout_lp=need_rollout_lp,
+        per_token_adv=False, n_samples=n_s, seq=np.frombuffer(seq_b, np.int64),
+        rows=np.frombuffer(rows_b, np.int64), out_off=np.frombuffer(out_off_b, np.int64),
+        doc_start=np.frombuffer(doc_start_b, np.int32), max_elems=max_elems, max_docs=max_docs, stream=handle,
     )
 
 

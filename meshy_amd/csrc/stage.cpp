@@ -32,12 +32,29 @@
 //       sample's column at dst (through the library's threaded gather), or
 //       False, copying nothing, when some column is not a CPU contiguous
 //       tensor of that dtype and row width.
+//   stage_micros(samples, micros, packed, need_rollout_lp, dst, capacity, gather_fn)
+//       The whole staging of build_micro_batches in one pass, for the common
+//       case: every used sample's tokens (all int64 or all int32), fp32 mask
+//       and (with need_rollout_lp) fp32 log-probs are CPU contiguous tensors
+//       long enough for the micros.  Lays the regions out as the Python
+//       staging does (256-byte aligned: tokens, mask, [logprobs],
+//       adv_samples, s_off, seq, out_off, doc_len, doc_start, doc_sample,
+//       pos_w), gathers the columns and writes every table at dst.  Returns
+//       None when a column is of another kind or a micro overflows its
+//       seq_len (the Python path handles and reports it), the byte size
+//       needed when capacity is smaller (nothing written), else
+//       (size, bounds, n_used, total, tokens_int64, n_docs_total, max_elems,
+//       max_docs, seq, rows, out_off, doc_start) with bounds the regions'
+//       [start, end) byte offsets in that order as int64 pairs (-1 for an
+//       absent region) and the four tables as bytes.
 #include <Python.h>
 
 #include <torch/csrc/autograd/python_variable.h>
 
+#include <algorithm>
 #include <cstdint>
 #include <cstring>
+#include <type_traits>
 #include <vector>
 
 namespace {
@@ -381,11 +398,257 @@ PyObject* gather(PyObject*, PyObject* args) {
     Py_RETURN_TRUE;
 }
 
+// sample[key] (a dict's item, or __getitem__), a new reference; nullptr with
+// an exception set when absent.
+PyObject* item_of(PyObject* s, PyObject* key) {
+    if (PyDict_CheckExact(s)) {
+        PyObject* v = PyDict_GetItemWithError(s, key);
+        if (!v) {
+            if (!PyErr_Occurred()) PyErr_SetObject(PyExc_KeyError, key);
+            return nullptr;
+        }
+        Py_INCREF(v);
+        return v;
+    }
+    return PyObject_GetItem(s, key);
+}
+
+// sample.get(key) as a float64 (the `scalars` rules): `dflt` when absent,
+// None or an empty tensor; false with an exception set on error.
+bool scalar_of(PyObject* s, PyObject* key, double dflt, double& out) {
+    out = dflt;
+    PyObject* v = nullptr;
+    if (PyDict_CheckExact(s)) {
+        v = PyDict_GetItemWithError(s, key);
+        if (!v) return !PyErr_Occurred();
+        Py_INCREF(v);
+    } else if (PyObject_HasAttrString(s, "get")) {
+        v = PyObject_CallMethod(s, "get", "OO", key, Py_None);
+        if (!v) return false;
+    } else {
+        return true;
+    }
+    bool ok = true;
+    if (v != Py_None) {
+        if (THPVariable_Check(v)) {
+            double x;
+            if (first_element(THPVariable_Unpack(v), x)) out = x;
+        } else {
+            const double x = PyFloat_AsDouble(v);
+            if (x == -1.0 && PyErr_Occurred()) ok = false;
+            else out = x;
+        }
+    }
+    Py_DECREF(v);
+    return ok;
+}
+
+// A CPU contiguous tensor column of `dtype` with one element per row and at
+// least `need` rows: its data pointer (nullptr for need == 0), else false.
+bool fast_column(PyObject* v, at::ScalarType dtype, int64_t need, const void*& ptr) {
+    if (!THPVariable_Check(v)) return false;
+    const at::Tensor& t = THPVariable_Unpack(v);
+    if (!t.device().is_cpu() || !t.is_contiguous() || t.scalar_type() != dtype || t.dim() != 1) return false;
+    if (t.size(0) < need) return false;
+    ptr = need ? t.data_ptr() : nullptr;
+    return true;
+}
+
+int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
+
+PyObject* stage_micros(PyObject*, PyObject* args) {
+    PyObject *samples, *micros;
+    int packed, need_lp;
+    unsigned long long dst, capacity, fn;
+    if (!PyArg_ParseTuple(args, "OOppKKK", &samples, &micros, &packed, &need_lp, &dst, &capacity, &fn))
+        return nullptr;
+    PyObject* seq_samples = PySequence_Fast(samples, "samples must be a sequence");
+    if (!seq_samples) return nullptr;
+    const Py_ssize_t n_samples = PySequence_Fast_GET_SIZE(seq_samples);
+    // The compact sample map and the document tables (as plan_tables).
+    PyObject* tables = Py_BuildValue("(On)", micros, n_samples);
+    PyObject* pt = tables ? plan_tables(nullptr, tables) : nullptr;
+    Py_XDECREF(tables);
+    if (!pt) {
+        Py_DECREF(seq_samples);
+        return nullptr;
+    }
+    auto vec_of = [&](int i, auto* type_tag) {
+        using T = std::remove_pointer_t<decltype(type_tag)>;
+        PyObject* b = PyTuple_GET_ITEM(pt, i);
+        const T* p = reinterpret_cast<const T*>(PyBytes_AS_STRING(b));
+        return std::vector<T>(p, p + PyBytes_GET_SIZE(b) / static_cast<Py_ssize_t>(sizeof(T)));
+    };
+    const std::vector<int64_t> used = vec_of(0, static_cast<int64_t*>(nullptr));
+    const std::vector<int64_t> need = vec_of(1, static_cast<int64_t*>(nullptr));
+    const std::vector<int32_t> doc_sample = vec_of(2, static_cast<int32_t*>(nullptr));
+    const std::vector<int64_t> doc_len = vec_of(3, static_cast<int64_t*>(nullptr));
+    const std::vector<int64_t> seq = vec_of(4, static_cast<int64_t*>(nullptr));
+    const std::vector<int64_t> n_docs = vec_of(5, static_cast<int64_t*>(nullptr));
+    const std::vector<int64_t> n_tok = vec_of(6, static_cast<int64_t*>(nullptr));
+    Py_DECREF(pt);
+    const int64_t n_s = static_cast<int64_t>(used.size());
+    const int64_t n_micro = static_cast<int64_t>(seq.size());
+    const int64_t nd_total = static_cast<int64_t>(doc_len.size());
+    bool fast = true;
+    for (int64_t k = 0; k < n_micro && fast; ++k) fast = !packed || n_tok[k] <= seq[k];
+    // The columns: all tensors of the staged dtypes, long enough.
+    std::vector<const void*> tok_p(n_s), mask_p(n_s), lp_p(need_lp ? n_s : 0);
+    std::vector<double> adv(n_s), reward(n_s), posw(n_s);
+    PyObject* k_tokens = PyUnicode_InternFromString("tokens");
+    PyObject* k_mask = PyUnicode_InternFromString("mask_assistant");
+    PyObject* k_lp = PyUnicode_InternFromString("logprobs");
+    PyObject* k_adv = PyUnicode_InternFromString("advantage");
+    PyObject* k_adv_tok = PyUnicode_InternFromString("advantage_tokens");
+    PyObject* k_reward = PyUnicode_InternFromString("reward");
+    PyObject* k_posw = PyUnicode_InternFromString("positive_lm_weight");
+    bool ok = k_tokens && k_mask && k_lp && k_adv && k_adv_tok && k_reward && k_posw;
+    int tok64 = -1;  // unknown until the first tensor
+    try {
+        for (int64_t j = 0; ok && fast && j < n_s; ++j) {
+            PyObject* s = PySequence_Fast_GET_ITEM(seq_samples, used[j]);
+            // Per-token advantages take the Python path.
+            // Any error (a missing column, an odd sample type) also leaves
+            // the micros to the Python staging, which reports it.
+            fast = PyDict_CheckExact(s) ? !PyDict_GetItemWithError(s, k_adv_tok) && !PyErr_Occurred()
+                                        : PySequence_Contains(s, k_adv_tok) == 0;
+            PyObject* t = fast ? item_of(s, k_tokens) : nullptr;
+            if (!t) {
+                fast = false;
+                break;
+            }
+            if (THPVariable_Check(t)) {
+                const at::ScalarType st = THPVariable_Unpack(t).scalar_type();
+                const int is64 = st == at::kLong ? 1 : (st == at::kInt ? 0 : -2);
+                if (is64 < 0 || (tok64 >= 0 && tok64 != is64)) fast = false;
+                else tok64 = is64;
+            } else {
+                fast = false;
+            }
+            fast = fast && fast_column(t, tok64 == 1 ? at::kLong : at::kInt, need[j], tok_p[j]);
+            Py_DECREF(t);
+            if (!fast) break;
+            PyObject* m = item_of(s, k_mask);
+            if (!m) {
+                fast = false;
+                break;
+            }
+            fast = fast_column(m, at::kFloat, need[j], mask_p[j]);
+            Py_DECREF(m);
+            if (fast && need_lp) {
+                PyObject* l = item_of(s, k_lp);
+                if (!l) {
+                    fast = false;
+                    break;
+                }
+                fast = fast_column(l, at::kFloat, need[j], lp_p[j]);
+                Py_DECREF(l);
+            }
+            fast = fast && scalar_of(s, k_adv, 0.0, adv[j]) && scalar_of(s, k_reward, 0.0, reward[j]) &&
+                   scalar_of(s, k_posw, 0.0, posw[j]);
+        }
+    } catch (const std::exception&) {
+        fast = false;
+    }
+    if (ok && !fast) PyErr_Clear();
+    Py_XDECREF(k_tokens);
+    Py_XDECREF(k_mask);
+    Py_XDECREF(k_lp);
+    Py_XDECREF(k_adv);
+    Py_XDECREF(k_adv_tok);
+    Py_XDECREF(k_reward);
+    Py_XDECREF(k_posw);
+    Py_DECREF(seq_samples);
+    if (!ok) return nullptr;
+    if (!fast) Py_RETURN_NONE;
+    if (tok64 < 0) tok64 = 1;  // no samples: an empty int64 region, as the Python staging
+    // The layout (the Python staging's region order).
+    int64_t total = 0;
+    for (int64_t L : need) total += L;
+    const int64_t tok_sz = tok64 ? 8 : 4;
+    const int64_t sizes[11] = {total * tok_sz,
+                               total * 4,
+                               need_lp ? total * 4 : -1,
+                               std::max<int64_t>(n_s, 1) * 4,
+                               (n_s + 1) * 8,
+                               n_micro * 8,
+                               (n_micro + 1) * 8,
+                               std::max<int64_t>(nd_total, 1) * 8,
+                               (n_micro + 1) * 4,
+                               std::max<int64_t>(nd_total, 1) * 4,
+                               std::max<int64_t>(nd_total, 1) * 4};
+    int64_t offs[11];
+    int64_t size = 0;
+    for (int r = 0; r < 11; ++r) {
+        offs[r] = size;
+        if (sizes[r] >= 0) size += align256(sizes[r]);
+    }
+    if (static_cast<unsigned long long>(size) > capacity) return PyLong_FromLongLong(size);
+    if (!dst || !fn) {
+        PyErr_SetString(PyExc_ValueError, "stage_micros: no destination or gather function");
+        return nullptr;
+    }
+    char* base = reinterpret_cast<char*>(dst);
+    // The columns, through the library's threaded gather.
+    std::vector<int64_t> nbytes(n_s);
+    auto gather_col = [&](const std::vector<const void*>& src, int64_t elem, int64_t off) -> bool {
+        for (int64_t j = 0; j < n_s; ++j) nbytes[j] = need[j] * elem;
+        if (total == 0) return true;
+        const int rc = reinterpret_cast<GatherFn>(fn)(src.data(), nbytes.data(), n_s, base + off, 0);
+        if (rc != 0) PyErr_Format(PyExc_RuntimeError, "meshy_host_gather failed (%d)", rc);
+        return rc == 0;
+    };
+    if (!gather_col(tok_p, tok_sz, offs[0]) || !gather_col(mask_p, 4, offs[1]) ||
+        (need_lp && !gather_col(lp_p, 4, offs[2])))
+        return nullptr;
+    // The tables.
+    float* adv_s = reinterpret_cast<float*>(base + offs[3]);
+    for (int64_t j = 0; j < n_s; ++j) adv_s[j] = static_cast<float>(adv[j]);
+    int64_t* s_off = reinterpret_cast<int64_t*>(base + offs[4]);
+    s_off[0] = 0;
+    for (int64_t j = 0; j < n_s; ++j) s_off[j + 1] = s_off[j] + need[j];
+    std::vector<int64_t> rows(n_micro), out_off(n_micro + 1);
+    std::vector<int32_t> doc_start(n_micro + 1);
+    int64_t max_elems = 0, max_docs = 0;
+    out_off[0] = 0;
+    doc_start[0] = 0;
+    for (int64_t k = 0; k < n_micro; ++k) {
+        rows[k] = packed ? 1 : std::max<int64_t>(n_docs[k], 1);
+        const int64_t elems = seq[k] * rows[k];
+        out_off[k + 1] = out_off[k] + elems;
+        doc_start[k + 1] = doc_start[k] + static_cast<int32_t>(n_docs[k]);
+        max_elems = std::max(max_elems, elems);
+        max_docs = std::max(max_docs, n_docs[k]);
+    }
+    std::memcpy(base + offs[5], seq.data(), n_micro * 8);
+    std::memcpy(base + offs[6], out_off.data(), (n_micro + 1) * 8);
+    std::memcpy(base + offs[7], doc_len.data(), nd_total * 8);
+    std::memcpy(base + offs[8], doc_start.data(), (n_micro + 1) * 4);
+    std::memcpy(base + offs[9], doc_sample.data(), nd_total * 4);
+    // Positive-LM weights only for rewards above 0.5 (batch.py:225-229).
+    float* pos_w = reinterpret_cast<float*>(base + offs[10]);
+    for (int64_t d = 0; d < nd_total; ++d) {
+        const int64_t j = doc_sample[d];
+        pos_w[d] = reward[j] > 0.5 ? static_cast<float>(posw[j]) : 0.f;
+    }
+    std::vector<int64_t> off_v(22, -1);  // [start, end) per region; -1 for no log-probs region
+    for (int r = 0; r < 11; ++r) {
+        if (sizes[r] < 0) continue;
+        off_v[2 * r] = offs[r];
+        off_v[2 * r + 1] = offs[r] + sizes[r];
+    }
+    return Py_BuildValue("(LNLLiLLLNNNN)", static_cast<long long>(size), to_bytes(off_v), static_cast<long long>(n_s),
+                         static_cast<long long>(total), tok64, static_cast<long long>(nd_total),
+                         static_cast<long long>(max_elems), static_cast<long long>(max_docs), to_bytes(seq),
+                         to_bytes(rows), to_bytes(out_off), to_bytes(doc_start));
+}
+
 PyMethodDef kMethods[] = {
     {"gather", gather, METH_VARARGS, "Concatenate one column of the used samples into a host buffer."},
     {"plan_tables", plan_tables, METH_VARARGS, "Compact sample map and document tables of a list of micros."},
     {"columns", columns, METH_VARARGS, "Pointer, shape and dtype records of one column of the used samples."},
     {"scalars", scalars, METH_VARARGS, "One scalar field of the used samples as float64."},
+    {"stage_micros", stage_micros, METH_VARARGS, "The whole staging of a list of micros, for the common case."},
     {nullptr, nullptr, 0, nullptr},
 };
 

@@ -522,3 +522,46 @@ def test_micros_of_only_empty_samples(dev, layout):
         ref = obatch.build_micro_batch(local, m.sample_idx, m.seq_len, m.doc_lens, layout=layout,
                                        need_rollout_lp=True)
         _assert_same(mb, ref, layout)
+
+
+@pytest.mark.parametrize("layout", ["packed", "padded"])
+@pytest.mark.parametrize("tok_dtype", [torch.int64, torch.int32])
+def test_one_pass_staging_equals_the_general_staging(dev, layout, tok_dtype, monkeypatch):
+    """The native one-pass staging stages the same bytes, and the pack makes the
+    same batches, as the general staging on the same samples and micros."""
+    from meshy_amd import batch as B
+    from meshy_amd.plan import MicroPlan
+
+    lengths = [11, 40, 3, 64, 25, 1, 70, 18]
+    samples = []
+    for i, L in enumerate(lengths):
+        s = _sample(L, prompt=2, adv=0.5 * i - 1.0, seed=10 + i)
+        s["tokens"] = s["tokens"].to(tok_dtype)
+        s["reward"] = 0.3 * (i % 4)
+        s["positive_lm_weight"] = 0.1 * (i + 1)
+        samples.append(s)
+    micros = [MicroPlan((0, 1, 2), 64, (11, 40, 3)), MicroPlan((3,), 64, (64,)), MicroPlan((), 64, ()),
+              MicroPlan((4, 5, 6), 96, (25, 1, 70)), MicroPlan((7, 1), 64, (18, 40))]
+    assert B._stage_common(samples, tuple(micros), layout, dev, True) is not None
+    fast = B.stage_micro_batches(samples, micros, layout=layout, device=dev, need_rollout_lp=True)
+    fast_mbs = B.launch_pack(fast, _NoCp())
+    torch.cuda.synchronize()
+    monkeypatch.setattr(B, "_stage_common", lambda *a: None)
+    slow = B.stage_micro_batches(samples, micros, layout=layout, device=dev, need_rollout_lp=True)
+    slow_mbs = B.launch_pack(slow, _NoCp())
+    torch.cuda.synchronize()
+
+    assert fast.lay.size == slow.lay.size and fast.lay.regions.keys() == slow.lay.regions.keys()
+    fbuf, sbuf = fast.dbuf.cpu(), slow.dbuf.cpu()
+    for name, (lo, hi, dtype) in slow.lay.regions.items():
+        assert fast.lay.regions[name] == (lo, hi, dtype), name
+        assert torch.equal(fbuf[lo:hi], sbuf[lo:hi]), name
+    for k in ("seq", "rows", "out_off", "doc_start"):
+        a, b = getattr(fast, k), getattr(slow, k)
+        assert a.dtype == b.dtype and np.array_equal(a, b), k
+    assert (fast.n_samples, fast.max_elems, fast.max_docs) == (slow.n_samples, slow.max_elems, slow.max_docs)
+    for mf, ms, m in zip(fast_mbs, slow_mbs, micros):
+        ref = obatch.build_micro_batch(samples, m.sample_idx, m.seq_len, m.doc_lens, layout=layout,
+                                       need_rollout_lp=True)
+        _assert_same(mf, ref, layout)
+        _assert_same(ms, ref, layout)
