@@ -537,6 +537,13 @@ typedef struct meshy_gae_args {
 size_t meshy_gae_workspace_size(int64_t rows, int64_t S, int64_t n_docs);
 int meshy_gae(const meshy_gae_args* args, hipStream_t stream);
 
+/* Test hook, no counterpart in the reference: the number of polls after which
+ * meshy_gae's one-pass kernel stops waiting for a neighbouring chunk's map
+ * and leaves the call to its exact fix-up pass (default 2000; a negative
+ * limit restores it).  Returns the previous limit.  Process-wide; it applies
+ * to calls launched after it (meshy_gae_attach included). */
+int meshy_gae_set_poll_limit(int limit);
+
 /* ------------------------------------------------------------------------
  * Per-token GAE advantages for a batch of samples (device).
  * Replaces TitanTrainer._attach_gae_advantages (meshy/backend/titan/trainer.py:603-699).

@@ -315,6 +315,7 @@ SIGNATURES = {
     "meshy_ppo_loss_bwd": (c_int, [POINTER(PpoArgs), c_void_p, c_void_p, c_void_p, c_void_p]),
     "meshy_gae_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
     "meshy_gae": (c_int, [POINTER(GaeArgs), c_void_p]),
+    "meshy_gae_set_poll_limit": (c_int, [c_int]),
     "meshy_gae_attach_workspace_size": (c_size_t, [c_int64, c_int64]),
     "meshy_gae_attach": (c_int, [POINTER(GaeAttachArgs), c_void_p]),
     "meshy_whiten_workspace_size": (c_size_t, [c_int64]),
@@ -353,7 +354,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 8
+ABI_VERSION = 9
 
 _LIB: ctypes.CDLL | None = None
 

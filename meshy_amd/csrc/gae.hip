@@ -14,22 +14,26 @@
 //                fixed-order sum (bitwise reproducible), when the caller
 //                passes the offsets of non-decreasing ids; otherwise fp32
 //                atomics (exact for 0/1 masks);
-//   k_gae_chunks each workgroup folds a chunk of kChunk tokens into one map
-//                per scan (advantages and returns);
-//   k_gae_apply  each workgroup folds its carry-in from the maps of the chunks
-//                to its right, up to the first one that cuts both scans (both
-//                slopes exactly 0: nothing past it reaches the chunk),
-//                re-folds its chunk, scans its threads from the right seeded
-//                with the carry, and writes A_t and G_t; it also writes lambda
-//                per document (gae.py:70-74).
+//   k_gae_scan   one pass, workgroup b on chunk nc - 1 - b (right to left):
+//                folds its chunk of kChunk tokens into one map per scan
+//                (advantages and returns) and publishes it in the chunk's
+//                slot, folds its carry-in from the slots of the chunks to its
+//                right up to the first one that cuts both scans (both slopes
+//                exactly 0: nothing past it reaches the chunk), waiting for
+//                slots not yet published, then scans its threads from the
+//                right seeded with the carry and writes A_t and G_t from the
+//                inputs it holds in registers; it also writes lambda per
+//                document (gae.py:70-74);
+//   k_gae_fix    returns at once unless the call held a non-finite term (or
+//                a wait was given up): then it redoes the outputs from the
+//                slots, composing with hardness, as the reference's loop
+//                carries a NaN across document ends.
 // With the segment offsets of non-decreasing ids, a chunk holding at most
 // kMaxStarts document starts reads the ids only at its two ends and takes the
-// starts from the offsets (8 bytes per token less in each pass); other chunks
-// read every token's id.
+// starts from the offsets (8 bytes per token less); other chunks read every
+// token's id.
 // Every fold of the scan has a fixed order, so the results do not depend on
-// timing (the atomic count aside).  The
-// apply pass visits each XCD's chunks from the highest down, so that it first
-// re-reads what the chunks pass read last (still in L2 or the Infinity Cache).
+// timing (the atomic count aside).
 // Everything is fp32, like the reference's sequential fallback.
 #include <algorithm>
 #include <atomic>
@@ -100,16 +104,27 @@ __device__ __forceinline__ Pair compose(const Pair& l, const Pair& r) {
 }
 __device__ __forceinline__ Pair identity_pair() { return Pair{Aff{1.f, 0.f}, Aff{1.f, 0.f}}; }
 
+// A chunk's published map: four 64-bit words (adv.p, adv.q, ret.p, ret.q),
+// each the float's bits in the low half and in the high half a tag drawn from
+// the call, the chunk and the word.  Each word is stored and loaded as one
+// single-copy atomic, so a reader takes a word as published exactly when its
+// tag is the call's: words left from an earlier call (or any other data the
+// workspace held) carry other tags, so nothing is cleared between calls.
+// A slot is accepted only when all four tags match.
+struct Slot {
+    unsigned long long w[4];
+};
+
 struct Workspace {
     float* cnt;     // [n_docs + 1]
-    Pair* chunk;    // [n_chunks]
+    Slot* slot;     // [n_chunks]
 };
 
 int64_t n_chunks_of(int64_t n) { return (n + kChunk - 1) / kChunk; }
 
 size_t ws_bytes(int64_t n, int64_t n_docs) {
     const int64_t nc = n_chunks_of(n);
-    return align_up(sizeof(float) * (n_docs + 1), 256) + align_up(sizeof(Pair) * nc, 256);
+    return align_up(sizeof(float) * (n_docs + 1), 256) + align_up(sizeof(Slot) * nc, 256);
 }
 
 Workspace ws_of(void* base, int64_t n, int64_t n_docs) {
@@ -117,8 +132,53 @@ Workspace ws_of(void* base, int64_t n, int64_t n_docs) {
     Workspace w;
     w.cnt = reinterpret_cast<float*>(p);
     p += align_up(sizeof(float) * (n_docs + 1), 256);
-    w.chunk = reinterpret_cast<Pair*>(p);
+    w.slot = reinterpret_cast<Slot*>(p);
     return w;
+}
+
+// The tag of word w of chunk c's slot in call `call` (a 64-bit mix).
+__device__ __forceinline__ uint32_t slot_tag(unsigned long long call, int64_t c, int w) {
+    unsigned long long x = call * 0x9E3779B97F4A7C15ull +
+                           (static_cast<unsigned long long>(c) * 4 + static_cast<unsigned>(w)) * 0xBF58476D1CE4E5B9ull;
+    x ^= x >> 31;
+    x *= 0x94D049BB133111EBull;
+    x ^= x >> 29;
+    return static_cast<uint32_t>(x >> 32);
+}
+
+__device__ __forceinline__ unsigned long long tagged(float v, unsigned long long call, int64_t c, int w) {
+    return (static_cast<unsigned long long>(slot_tag(call, c, w)) << 32) | __float_as_uint(v);
+}
+
+// Loads at device (agent) scope: they see stores other XCDs made during this
+// launch, whatever the loading XCD's L2 holds.
+__device__ __forceinline__ unsigned long long load_word(const unsigned long long* p) {
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+__device__ __forceinline__ float word_value(unsigned long long x) {
+    return __uint_as_float(static_cast<uint32_t>(x));
+}
+
+// Chunk k's map if all four words of its slot carry the call's tags.
+__device__ __forceinline__ bool read_slot(const Slot* slots, int64_t k, unsigned long long call, Pair& out) {
+    const unsigned long long a = load_word(&slots[k].w[0]);
+    const unsigned long long b = load_word(&slots[k].w[1]);
+    const unsigned long long c = load_word(&slots[k].w[2]);
+    const unsigned long long d = load_word(&slots[k].w[3]);
+    const bool ok = static_cast<uint32_t>(a >> 32) == slot_tag(call, k, 0) &&
+                    static_cast<uint32_t>(b >> 32) == slot_tag(call, k, 1) &&
+                    static_cast<uint32_t>(c >> 32) == slot_tag(call, k, 2) &&
+                    static_cast<uint32_t>(d >> 32) == slot_tag(call, k, 3);
+    out = Pair{Aff{word_value(a), word_value(b)}, Aff{word_value(c), word_value(d)}};
+    return ok;
+}
+
+// Chunk k's map after the launch that published it has ended (the tags are
+// not checked).
+__device__ __forceinline__ Pair slot_pair(const Slot* slots, int64_t k) {
+    const Slot s = slots[k];
+    return Pair{Aff{word_value(s.w[0]), word_value(s.w[1])}, Aff{word_value(s.w[2]), word_value(s.w[3])}};
 }
 
 __device__ __forceinline__ float lambda_of(float L, float alpha, float epsilon) {
@@ -484,40 +544,25 @@ __device__ __forceinline__ Pair chunk_map(const Pair (&items)[kItems], Pair* s_w
     return total;
 }
 
-// A plain fold is NaN or infinite exactly when one of its terms is (0 * NaN,
-// 0 * inf and NaN + x are all NaN), so the plain chunk map tells whether the
-// chunk holds a non-finite term; only then is the map composed again with
-// hardness.  A plain map takes its hardness (a row end in the chunk) from the
-// positions.
-__global__ __launch_bounds__(kThreads) void k_gae_chunks(meshy_gae_args g, Workspace ws, int64_t n, bool vec,
-                                                         unsigned long long epoch) {
-    __shared__ Pair s_wave[kThreads / kWave];
-    __shared__ Pair s_wave_hard[kThreads / kWave];
-    __shared__ int s_row_end[kThreads / kWave];
-    const int64_t c0 = static_cast<int64_t>(blockIdx.x) * kChunk;
-    const int64_t t0 = c0 + static_cast<int64_t>(threadIdx.x) * kItems;
-    Pair items[kItems];
-    uint32_t valid_bits;
-    bool has_row_end;
-    thread_maps(g, ws.cnt, c0, t0, n, vec, items, valid_bits, has_row_end);
+// The chunk's map for the slots.  A plain fold is NaN or infinite exactly
+// when one of its terms is (0 * NaN, 0 * inf and NaN + x are all NaN), so the
+// plain map tells whether the chunk holds a non-finite term; only then is the
+// map composed again with hardness.  A plain map takes its hardness (a row end
+// in the chunk) from the positions.  Every thread returns the same map.
+__device__ __forceinline__ Pair published_map(const Pair (&items)[kItems], bool has_row_end, Pair* s_wave,
+                                              Pair* s_wave_hard, int* s_row_end, bool& nonfinite) {
     const bool wave_row_end = __ballot(has_row_end) != 0;
     if (threadIdx.x % kWave == 0) s_row_end[threadIdx.x / kWave] = wave_row_end;
     Pair total = chunk_map<false>(items, s_wave);  // its barrier publishes s_row_end
-    const bool nonfinite = !isfinite(total.adv.q) || !isfinite(total.ret.q);  // the same in every thread
-    if (nonfinite) {
-        total = chunk_map<true>(items, s_wave_hard);
-    } else {
-        bool hard = false;
-        for (int w = 0; w < kThreads / kWave; ++w) hard |= s_row_end[w] != 0;
-        if (hard) {
-            total.adv.p = -0.f;
-            total.ret.p = -0.f;
-        }
+    nonfinite = !isfinite(total.adv.q) || !isfinite(total.ret.q);
+    if (nonfinite) return chunk_map<true>(items, s_wave_hard);
+    bool hard = false;
+    for (int w = 0; w < kThreads / kWave; ++w) hard |= s_row_end[w] != 0;
+    if (hard) {
+        total.adv.p = -0.f;
+        total.ret.p = -0.f;
     }
-    if (threadIdx.x == 0) {
-        ws.chunk[blockIdx.x] = total;
-        if (nonfinite) atomicMax(&g_gae_nonfinite_epoch, epoch);
-    }
+    return total;
 }
 
 __device__ __forceinline__ void write_lambda(const meshy_gae_args& g, const float* cnt, int64_t first, int64_t step) {
@@ -530,52 +575,17 @@ __global__ __launch_bounds__(kThreads) void k_gae_lambda(meshy_gae_args g, const
                  static_cast<int64_t>(gridDim.x) * kThreads);
 }
 
-// Workgroup b of the apply pass takes the chunks of its XCD (b mod kXcds) in
-// decreasing order: a bijection of [0, nc).
-__device__ __forceinline__ int64_t apply_chunk(int64_t b, int64_t nc) {
-    const int64_t x = b % kXcds;
-    const int64_t i = b / kXcds;
-    const int64_t m = (nc - x + kXcds - 1) / kXcds;  // chunks c < nc with c mod kXcds == x
-    return x + kXcds * (m - 1 - i);
-}
-
-// The apply pass of chunk c.  kHard (a non-finite term somewhere in the call):
-// compose with hardness and fold the carry up to the first chunk holding a row
-// end; otherwise plainly, up to the first chunk that cuts both scans.
+// The chunk's outputs from its carry-in (s_carry, written by wave 0 before
+// the call): scans the threads from the right seeded with the carry and
+// writes A_t and G_t.
 template <bool kHard>
-__device__ __forceinline__ void apply_chunk_pass(const meshy_gae_args& g, const Workspace& ws, int64_t n,
-                                                 int64_t nc, bool vec, int64_t c, Pair* s_wave, float* s_carry,
-                                                 Pair r, const Pair (&items)[kItems], uint32_t valid_bits) {
+__device__ __forceinline__ void scan_and_write(const meshy_gae_args& g, int64_t n, bool vec, int64_t c,
+                                               Pair* s_suffix, const float* s_carry, const Pair (&items)[kItems],
+                                               uint32_t valid_bits) {
     const int64_t t0 = c * kChunk + static_cast<int64_t>(threadIdx.x) * kItems;
-    const int lane = threadIdx.x % kWave;
-    // The carry-in: the chunks to the right of c in order, up to and including
-    // the first whose map cuts both scans (both slopes zero: a document end, a
-    // row end or a mask hole lies in it; with kHard, a row end), past which
-    // nothing reaches c.  Their maps come 64 at a time; the first 64 load
-    // before the chunk's inputs, in every wave (indices clamped into range),
-    // and wave 0 alone folds them: loads under a condition would compile to a
-    // branch that waits for them before the inputs are issued.  A further 64
-    // load only when a document runs on past them (more than 128 k tokens).
     const Pair mine = fold_items<kHard>(items);
-    if (threadIdx.x < kWave) {  // r is this wave's copy of the first 64 maps
-        Pair carry = identity_pair();
-        for (int64_t j0 = c + 1; j0 < nc; j0 += kWave) {
-            const bool in = j0 + lane < nc;
-            const bool cut = kHard ? (is_hard(r.adv.p) && is_hard(r.ret.p)) : (r.adv.p == 0.f && r.ret.p == 0.f);
-            const uint64_t cuts = __ballot(in && cut);
-            const int first = cuts ? __builtin_ctzll(cuts) : kWave;
-            carry = compose<kHard>(carry, wave_fold<kHard>((in && lane <= first) ? r : identity_pair()));
-            if (cuts) break;
-            r = ws.chunk[min(j0 + kWave + lane, nc - 1)];
-        }
-        if (lane == 0) {
-            // The sequence ends with A = G = 0, so the carry is the map applied to 0.
-            s_carry[0] = carry.adv.q;
-            s_carry[1] = carry.ret.q;
-        }
-    }
     Pair total;
-    const Pair excl = block_suffix_exclusive<kHard>(mine, s_wave, total);  // its barriers publish s_carry
+    const Pair excl = block_suffix_exclusive<kHard>(mine, s_suffix, total);  // its barriers publish s_carry
     float A = apply_map<kHard>(excl.adv, s_carry[0]);
     float G = apply_map<kHard>(excl.ret, s_carry[1]);
     float outA[kItems], outG[kItems];
@@ -609,25 +619,139 @@ __device__ __forceinline__ void apply_chunk_pass(const meshy_gae_args& g, const 
     }
 }
 
-__global__ __launch_bounds__(kThreads) void k_gae_apply(meshy_gae_args g, Workspace ws, int64_t n, int64_t nc,
-                                                        bool vec, unsigned long long epoch) {
+// Polls of one batch of slots before a wait is given up (each poll is a
+// round trip to memory and a short sleep: about 2-4 ms in all).  A chunk only
+// waits for chunks to its right, whose workgroups come earlier in the grid, so
+// every wait is expected to end; one given up leaves the call to k_gae_fix.
+constexpr int kMaxPolls = 2000;
+// Slots in a chunk's first batch: most chunks find a cut among their first
+// few neighbours, and polling 64 slots at once from every workgroup loads the
+// memory system (1024-document workload: 35.9 us per call with 64, 28.9 with
+// 4, 29.4 with 2); later batches take 64.
+constexpr int kFirstBatch = 4;
+
+// One pass: workgroup b takes chunk c = nc - 1 - b (the grid runs right to
+// left), folds it to its map and publishes it in the chunk's slot, then wave 0
+// folds the carry-in from the slots of the chunks to its right, in order, up
+// to and including the first whose map cuts both scans (both slopes exactly
+// 0: a document end, a row end or a mask hole lies in it).  With p = 0,
+// (p, q) o (p', q') = (0, q) for any finite q', so nothing past that chunk
+// reaches the carry; the maps come kFirstBatch, then 64 at a time (one
+// wave_fold per batch, composed in order), a ballot finds the first cut
+// and one DPP fold covers the lanes up to it, a fixed order whatever the
+// timing.  A slot not yet published is polled again.  Then the chunk rescans
+// itself from registers (each input is read once) and writes A and G; the grid
+// also writes lambda per document.
+// Everything composes plainly: the same values as composing with hardness
+// when every term is finite.  A chunk holding a non-finite term, or a wait
+// given up, records the call's epoch in g_gae_nonfinite_epoch and k_gae_fix
+// redoes the call's outputs.
+__global__ __launch_bounds__(kThreads) void k_gae_scan(meshy_gae_args g, Workspace ws, int64_t n, int64_t nc,
+                                                       bool vec, unsigned long long epoch, int max_polls) {
+    // The chunk map and the suffix scan use separate arrays: a wave may enter
+    // the scan while another still reads the map's array.
     __shared__ Pair s_wave[kThreads / kWave];
+    __shared__ Pair s_wave_hard[kThreads / kWave];
+    __shared__ Pair s_suffix[kThreads / kWave];
+    __shared__ int s_row_end[kThreads / kWave];
     __shared__ float s_carry[2];
-    const int64_t c = apply_chunk(blockIdx.x, nc);
-    const bool hard_call = g_gae_nonfinite_epoch >= epoch;
-    // Every load of both paths is issued before the branch.
-    const Pair r = ws.chunk[min(c + 1 + static_cast<int64_t>(threadIdx.x % kWave), nc - 1)];
+    const int64_t c = nc - 1 - static_cast<int64_t>(blockIdx.x);
+    const int lane = threadIdx.x % kWave;
     Pair items[kItems];
     uint32_t valid_bits;
     bool has_row_end;
     thread_maps(g, ws.cnt, c * kChunk, c * kChunk + static_cast<int64_t>(threadIdx.x) * kItems, n, vec, items,
                 valid_bits, has_row_end);
-    if (hard_call)
-        apply_chunk_pass<true>(g, ws, n, nc, vec, c, s_wave, s_carry, r, items, valid_bits);
-    else
-        apply_chunk_pass<false>(g, ws, n, nc, vec, c, s_wave, s_carry, r, items, valid_bits);
+    bool nonfinite;
+    const Pair total = published_map(items, has_row_end, s_wave, s_wave_hard, s_row_end, nonfinite);
+    if (threadIdx.x < 4) {
+        const float v = threadIdx.x == 0 ? total.adv.p
+                        : threadIdx.x == 1 ? total.adv.q
+                        : threadIdx.x == 2 ? total.ret.p
+                                           : total.ret.q;
+        if (nonfinite && threadIdx.x == 0) atomicMax(&g_gae_nonfinite_epoch, epoch);
+        __hip_atomic_store(&ws.slot[c].w[threadIdx.x], tagged(v, epoch, c, threadIdx.x), __ATOMIC_RELAXED,
+                           __HIP_MEMORY_SCOPE_AGENT);
+    }
+    if (threadIdx.x < kWave) {
+        Pair carry = identity_pair();
+        bool gave_up = false;
+        int width = kFirstBatch;
+        for (int64_t j0 = c + 1; j0 < nc; j0 += width, width = kWave) {
+            const int64_t k = j0 + lane;
+            const bool in = k < nc && lane < width;
+            Pair r = identity_pair();
+            bool ready = !in;
+            int first = kWave;
+            for (int poll = 0;; ++poll) {
+                if (!ready) ready = read_slot(ws.slot, k, epoch, r);
+                const bool cut = in && ready && r.adv.p == 0.f && r.ret.p == 0.f;
+                const uint64_t stop = __ballot(!ready || cut);
+                first = stop ? __builtin_ctzll(stop) : kWave;
+                // Settled when every lane up to the first cut is published.
+                const uint64_t unready = __ballot(!ready);
+                if (!(unready & ((first < kWave) ? ((2ull << first) - 1) : ~0ull))) break;
+                if (poll >= max_polls) {
+                    gave_up = true;
+                    break;
+                }
+                __builtin_amdgcn_s_sleep(2);
+            }
+            if (gave_up) break;
+            carry = compose<false>(carry, wave_fold<false>((in && lane <= first) ? r : identity_pair()));
+            if (first < kWave) break;
+        }
+        if (lane == 0) {
+            if (gave_up) atomicMax(&g_gae_nonfinite_epoch, epoch);
+            // The sequence ends with A = G = 0, so the carry is the map applied to 0.
+            s_carry[0] = carry.adv.q;
+            s_carry[1] = carry.ret.q;
+        }
+    }
+    scan_and_write<false>(g, n, vec, c, s_suffix, s_carry, items, valid_bits);
     if (g.lam_doc) write_lambda(g, ws.cnt, static_cast<int64_t>(blockIdx.x) * kThreads + threadIdx.x,
                                 static_cast<int64_t>(gridDim.x) * kThreads);
+}
+
+// Workgroups of k_gae_fix (each takes every gridDim.x-th chunk).
+constexpr int kFixBlocks = 512;
+
+// Redoes the outputs of a call whose epoch g_gae_nonfinite_epoch holds (a
+// non-finite term, or a wait k_gae_scan gave up), from the slots k_gae_scan
+// published: it composes with hardness and folds each chunk's carry from the
+// chunks to its right up to the first holding a row end (a non-finite value
+// crosses document ends and mask holes in the reference's sequential loop).
+// Every other call returns at once.
+__global__ __launch_bounds__(kThreads) void k_gae_fix(meshy_gae_args g, Workspace ws, int64_t n, int64_t nc,
+                                                      bool vec, unsigned long long epoch) {
+    if (g_gae_nonfinite_epoch < epoch) return;
+    __shared__ Pair s_wave[kThreads / kWave];
+    __shared__ float s_carry[2];
+    const int lane = threadIdx.x % kWave;
+    for (int64_t c = blockIdx.x; c < nc; c += gridDim.x) {
+        Pair items[kItems];
+        uint32_t valid_bits;
+        bool has_row_end;
+        thread_maps(g, ws.cnt, c * kChunk, c * kChunk + static_cast<int64_t>(threadIdx.x) * kItems, n, vec, items,
+                    valid_bits, has_row_end);
+        if (threadIdx.x < kWave) {
+            Pair carry = identity_pair();
+            for (int64_t j0 = c + 1; j0 < nc; j0 += kWave) {
+                const bool in = j0 + lane < nc;
+                const Pair r = in ? slot_pair(ws.slot, j0 + lane) : identity_pair();
+                const uint64_t cuts = __ballot(in && is_hard(r.adv.p) && is_hard(r.ret.p));
+                const int first = cuts ? __builtin_ctzll(cuts) : kWave;
+                carry = compose<true>(carry, wave_fold<true>((in && lane <= first) ? r : identity_pair()));
+                if (cuts) break;
+            }
+            if (lane == 0) {
+                s_carry[0] = carry.adv.q;
+                s_carry[1] = carry.ret.q;
+            }
+        }
+        scan_and_write<true>(g, n, vec, c, s_wave, s_carry, items, valid_bits);
+        __syncthreads();  // s_carry is read after the scan's last barrier
+    }
 }
 
 // ---------------------------------------------------------------- whitening
@@ -786,6 +910,8 @@ namespace {
 
 // The calls' epochs for g_gae_nonfinite_epoch (process-wide; only growth matters).
 std::atomic<unsigned long long> g_gae_epoch{0};
+// Polls before k_gae_scan gives a wait up (meshy_gae_set_poll_limit).
+std::atomic<int> g_gae_max_polls{kMaxPolls};
 
 int gae_launch(const meshy_gae_args& g, hipStream_t stream) {
     if (g.rows < 0 || g.S < 0 || g.n_docs < 0) return set_error(MESHY_EINVAL, "meshy_gae: negative sizes");
@@ -830,12 +956,12 @@ int gae_launch(const meshy_gae_args& g, hipStream_t stream) {
                      (!g.adv || al16(g.adv)) && (!g.returns || al16(g.returns));
     if (nc > 0 && (g.adv || g.returns)) {
         const unsigned long long epoch = g_gae_epoch.fetch_add(1, std::memory_order_relaxed) + 1;
-        hipLaunchKernelGGL(k_gae_chunks, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, vec,
-                           epoch);
-        if ((rc = check_launch("meshy_gae(chunks)"))) return rc;
-        hipLaunchKernelGGL(k_gae_apply, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, nc, vec,
-                           epoch);
-        if ((rc = check_launch("meshy_gae(apply)"))) return rc;
+        hipLaunchKernelGGL(k_gae_scan, dim3(static_cast<unsigned>(nc)), dim3(kThreads), 0, stream, g, ws, n, nc, vec,
+                           epoch, g_gae_max_polls.load(std::memory_order_relaxed));
+        if ((rc = check_launch("meshy_gae(scan)"))) return rc;
+        hipLaunchKernelGGL(k_gae_fix, dim3(static_cast<unsigned>(std::min<int64_t>(nc, kFixBlocks))), dim3(kThreads), 0,
+                           stream, g, ws, n, nc, vec, epoch);
+        if ((rc = check_launch("meshy_gae(fix)"))) return rc;
     } else if (g.lam_doc && g.n_docs > 0) {
         const unsigned nb = static_cast<unsigned>(std::min<int64_t>(1024, ceil_div(g.n_docs, kThreads)));
         hipLaunchKernelGGL(k_gae_lambda, dim3(nb), dim3(kThreads), 0, stream, g, ws.cnt);
@@ -851,6 +977,11 @@ extern "C" int meshy_gae(const meshy_gae_args* args, hipStream_t stream) {
     meshy::clear_error();
     if (!args) return meshy::set_error(MESHY_ENULL, "meshy_gae: args is NULL");
     return meshy::gae_launch(*args, stream);
+}
+
+extern "C" int meshy_gae_set_poll_limit(int limit) {
+    if (limit < 0) limit = meshy::kMaxPolls;
+    return meshy::g_gae_max_polls.exchange(limit);
 }
 
 // ------------------------------------------------- _attach_gae_advantages

@@ -188,6 +188,48 @@ def test_exact_carry_across_chunks(dev, n, holes):
     assert np.array_equal(adv.reshape(-1).cpu().numpy(), A)
 
 
+@pytest.mark.parametrize("holes", [True, False])
+def test_waits_given_up_leave_the_call_to_the_exact_fix_pass(dev, holes):
+    """With a poll limit of 0 the one-pass kernel gives up every wait for a
+    neighbouring chunk's map that is not published at its first poll, and the
+    fix-up pass redoes the call's outputs from the published maps: the same
+    exact values on the integer case above (documents of ~300 k tokens, so
+    carries fold several batches of maps), and the oracle's values within
+    the tolerance on a random grid."""
+    from meshy_amd import _lib
+    from meshy_amd.gae import compute_vapo_gae, gae_and_returns
+
+    n = 4096 * 129 + 17
+    rng = np.random.default_rng(3)
+    n_docs = 2
+    doc = np.zeros(n, np.int64)
+    doc[n // 3:] = 1
+    valid = rng.random(n) > 1e-4 if holes else np.ones(n, bool)
+    r = (rng.random(n) < 0.05).astype(np.float32)
+    v = rng.integers(-8, 9, n).astype(np.float32)
+    G = _run_suffix_sums(r, valid, doc).astype(np.float32)
+    A = np.where(valid, G - v, 0).astype(np.float32)
+    rewards, values, mask, doc_ids, n_grid = _random_grid(3, 60_000, 20, seed=9)
+    ref_adv, _ = ogae.compute_vapo_gae(rewards, values, mask, doc_ids, n_grid, gamma=0.99, alpha=1.5)
+    lib = _lib.load()
+    before = lib.meshy_gae_set_poll_limit(0)
+    try:
+        adv, ret, _ = gae_and_returns(
+            torch.from_numpy(r).reshape(1, -1).to(dev), torch.from_numpy(v).to(torch.bfloat16).reshape(1, -1).to(dev),
+            torch.from_numpy(valid.astype(np.float32)).reshape(1, -1).to(dev),
+            torch.from_numpy(doc).reshape(1, -1).to(dev), n_docs, lengths=torch.full((n_docs,), 1e30, device=dev),
+            gamma=1.0, alpha=1.0, epsilon=0.0)
+        got, _ = compute_vapo_gae(*[t.to(dev) for t in (rewards, values, mask, doc_ids)], n_grid, gamma=0.99,
+                                  alpha=1.5)
+        torch.cuda.synchronize()
+    finally:
+        assert lib.meshy_gae_set_poll_limit(-1) == 0
+    assert before == 2000
+    assert np.array_equal(ret.reshape(-1).cpu().numpy(), G)
+    assert np.array_equal(adv.reshape(-1).cpu().numpy(), A)
+    assert (got.cpu() - ref_adv).abs().max().item() <= TOL
+
+
 def test_lambda_zero_is_not_a_cut_for_the_returns(dev):
     """lambda = 0 zeroes the advantage scan's slope at every position while the
     returns scan still carries (gamma = 1): a chunk with only the advantage
