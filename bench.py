@@ -865,13 +865,12 @@ def bench_gae(steps, warmup, no_cpu):
 
 
 def bench_gae_cache(steps):
-    """Where GAE's second pass reads from: meshy_gae over the 1024 documents
-    back to back (the inputs stay in the 256 MB Infinity Cache between calls),
-    then each call after a 1 GiB read that evicts the L2s and the Infinity
-    Cache (the chunks pass then reads HBM, and the apply pass re-reads what
-    the chunks pass just brought in), then a 268,435,456 B device copy three
-    times (counter calibration).  Device us per call from HIP events around
-    the call alone."""
+    """Where GAE reads from: meshy_gae over the 1024 documents back to back
+    (the 114 MB of inputs and outputs can stay in the 256 MB Infinity Cache
+    between calls), then each call after a 1 GiB read that evicts the L2s and
+    the Infinity Cache (the scan then reads HBM), then a 268,435,456 B device
+    copy three times (counter calibration).  Device us per call from HIP
+    events around the call alone."""
     import numpy as np
     import torch
 
