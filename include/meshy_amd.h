@@ -105,6 +105,16 @@ int meshy_plan_build(const int64_t* lengths, const int64_t* loss_tokens, int64_t
 int meshy_host_gather(const void* const* srcs, const int64_t* nbytes, int64_t n, void* dst,
                       int max_threads);
 
+/* The same concatenation of fp32 mask pieces into bytes (host): piece i
+ * (counts[i] floats at srcs[i]) lands as counts[i] bytes right after piece
+ * i - 1 in dst, each byte the float's value.  *binary is set to 1 when every
+ * float was exactly +0.0 or 1.0 (bytes and floats then hold the same mask),
+ * else to 0 (dst then holds no mask: stage the floats instead).  For masks
+ * that are 0/1, as the reference's mask_assistant columns are, this quarters
+ * the bytes the critic path copies to the device (trainer.py:644-667). */
+int meshy_host_gather_mask_u8(const float* const* srcs, const int64_t* counts, int64_t n, uint8_t* dst,
+                              int max_threads, int32_t* binary);
+
 /* Per-sample planner inputs from a flat host mask (host).
  * Replaces TitanTrainer._sample_lengths (meshy/backend/titan/trainer.py:577-588):
  * sample i covers mask[offsets[i] .. offsets[i+1]); lengths[i] is its token
@@ -561,7 +571,7 @@ int meshy_gae_set_poll_limit(int limit);
  * lambda_mean (trainer.py:688-699).
  * ---------------------------------------------------------------------- */
 typedef struct meshy_gae_attach_args {
-    const float* mask_assistant;   /* [total]                                 */
+    const void* mask_assistant;    /* [total] fp32, or uint8 with mask_u8     */
     const void* values;            /* [total] fp32 or bf16                    */
     const float* reward;           /* [n]                                     */
     const int64_t* offsets;        /* [n + 1]                                 */
@@ -572,7 +582,8 @@ typedef struct meshy_gae_attach_args {
     float lambda;                  /* < 0: VAPO                               */
     float epsilon;
     int32_t values_bf16;
-    int32_t reserved;
+    int32_t mask_u8;               /* 1: mask_assistant holds bytes, each 0 or
+                                      1 (meshy_host_gather_mask_u8)            */
     float* adv;                    /* [total]                                 */
     float* grid_mask;              /* [total], nullable                       */
     float* lam_doc;                /* [n], nullable                           */

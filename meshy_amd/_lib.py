@@ -239,7 +239,7 @@ class GaeAttachArgs(ctypes.Structure):
         ("lambda_", c_float),
         ("epsilon", c_float),
         ("values_bf16", c_int32),
-        ("reserved", c_int32),
+        ("mask_u8", c_int32),
         ("adv", c_void_p),
         ("grid_mask", c_void_p),
         ("lam_doc", c_void_p),
@@ -260,6 +260,7 @@ SIGNATURES = {
     "meshy_sample_loss_tokens": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "meshy_step_plan": (c_int, [POINTER(StepPlanArgs)]),
     "meshy_host_gather": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int]),
+    "meshy_host_gather_mask_u8": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int, POINTER(c_int32)]),
     "meshy_pack_micro_batches": (c_int, [POINTER(PackArgs), c_void_p]),
     "meshy_grpo_advantage": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
     "meshy_zero_variance_groups": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_double, c_void_p, c_void_p]),
@@ -354,7 +355,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 _LIB: ctypes.CDLL | None = None
 

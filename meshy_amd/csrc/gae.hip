@@ -1047,13 +1047,26 @@ AttachWs attach_ws_of(void* base, int64_t n, int64_t total) {
 constexpr int kLastChunk = 4 * kAttachThreads;
 constexpr int64_t kWaveTile = 4 * kWave;  // tokens per wave step of k_attach_prep
 
+// mask_assistant as fp32, or as bytes holding 0 or 1 (mask_u8): the same
+// values either way.
+__device__ __forceinline__ float mask_at(const float* m, int64_t i) { return m[i]; }
+__device__ __forceinline__ float mask_at(const uint8_t* m, int64_t i) { return static_cast<float>(m[i]); }
+// Tokens i .. i + 3 (i a multiple of 4, the array 16-byte aligned for fp32, 4-byte for bytes).
+__device__ __forceinline__ f32x4 mask4(const float* m, int64_t i) { return *reinterpret_cast<const f32x4*>(m + i); }
+__device__ __forceinline__ f32x4 mask4(const uint8_t* m, int64_t i) {
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(m + i);
+    return f32x4{static_cast<float>(w & 0xffu), static_cast<float>((w >> 8) & 0xffu),
+                 static_cast<float>((w >> 16) & 0xffu), static_cast<float>(w >> 24)};
+}
+
+template <typename M>
 __global__ __launch_bounds__(kAttachThreads) void k_attach_prep(meshy_gae_attach_args g, AttachWs ws,
                                                                 float* grid_mask, float length_const, bool vec) {
     __shared__ int64_t s_last[kAttachThreads / kWave];
     const int64_t j = blockIdx.x;
     const int64_t lo = g.offsets[j];
     const int64_t hi = g.offsets[j + 1];
-    const float* m = g.mask_assistant;
+    const M* m = static_cast<const M*>(g.mask_assistant);
     // Every split finds the sample's last masked position (usually one step).
     int64_t last = -1;  // last masked position, relative to lo
     for (int64_t end = hi; end > lo; end -= kLastChunk) {
@@ -1062,7 +1075,8 @@ __global__ __launch_bounds__(kAttachThreads) void k_attach_prep(meshy_gae_attach
         // condition compiles to a branch that waits for it.
         float mv[4];
 #pragma unroll
-        for (int k = 0; k < 4; ++k) mv[k] = m[max(end - 1 - threadIdx.x - static_cast<int64_t>(k) * kAttachThreads, lo)];
+        for (int k = 0; k < 4; ++k)
+            mv[k] = mask_at(m, max(end - 1 - threadIdx.x - static_cast<int64_t>(k) * kAttachThreads, lo));
         int64_t cand = -1;
 #pragma unroll
         for (int k = 0; k < 4; ++k) {
@@ -1084,7 +1098,7 @@ __global__ __launch_bounds__(kAttachThreads) void k_attach_prep(meshy_gae_attach
     const float r = g.reward[j];
     const int64_t rpos = (last > 0) ? lo + last - 1 : -1;  // where the reward goes
     // Token i of the grid: mask[i + 1] inside the sample, 0 at its last token.
-    auto grid_at = [&](int64_t i) { return (i + 1 < hi) ? m[i + 1] : 0.f; };
+    auto grid_at = [&](int64_t i) { return (i + 1 < hi) ? mask_at(m, i + 1) : 0.f; };
     int64_t a, b;  // this split's tokens
     split_range(lo, hi, static_cast<int>(blockIdx.y), a, b);
     // Wave tiles of 256 tokens from the first multiple of 4: lane l reads and
@@ -1099,10 +1113,10 @@ __global__ __launch_bounds__(kAttachThreads) void k_attach_prep(meshy_gae_attach
     for (int64_t tile = wid; tile < n_tiles; tile += kAttachThreads / kWave) {
         const int64_t base = body0 + kWaveTile * tile;
         const int64_t i = base + 4 * lane;
-        const f32x4 mk = *reinterpret_cast<const f32x4*>(m + i);
+        const f32x4 mk = mask4(m, i);
         // mask[i + 4], which lane 63 needs, loaded by every lane with the tile
         // (the other lanes' addresses fall in lines the tile reads anyway).
-        const float after = m[min(i + 4, hi - 1)];
+        const float after = mask_at(m, min(i + 4, hi - 1));
         const float next_lane = __shfl_down(mk.x, 1, kWave);  // mask[i + 4] for lanes 0..62
         const float nx = (lane == kWave - 1) ? (i + 4 < hi ? after : 0.f) : next_lane;
         *reinterpret_cast<f32x4*>(grid_mask + i) = f32x4{mk.y, mk.z, mk.w, nx};
@@ -1254,9 +1268,15 @@ extern "C" int meshy_gae_attach(const meshy_gae_attach_args* args, hipStream_t s
     const float length_const =
         vapo ? 0.f : static_cast<float>(1.0 / std::max(1e-9, 1.0 - static_cast<double>(g.lambda)));
     auto al16 = [](const void* q) { return reinterpret_cast<uintptr_t>(q) % 16 == 0; };
-    const bool vec_prep = al16(g.mask_assistant) && al16(grid_mask) && al16(ws.rewards) && al16(ws.doc_ids);
-    hipLaunchKernelGGL(k_attach_prep, dim3(static_cast<unsigned>(g.n), kPrepSplits), dim3(kAttachThreads), 0,
-                       stream, g, ws, grid_mask, length_const, vec_prep);
+    // The wave tiles read the mask 4 tokens at a time: 16 bytes of fp32 or 4 bytes.
+    const bool mask_al = reinterpret_cast<uintptr_t>(g.mask_assistant) % (g.mask_u8 ? 4 : 16) == 0;
+    const bool vec_prep = mask_al && al16(grid_mask) && al16(ws.rewards) && al16(ws.doc_ids);
+    if (g.mask_u8)
+        hipLaunchKernelGGL(k_attach_prep<uint8_t>, dim3(static_cast<unsigned>(g.n), kPrepSplits), dim3(kAttachThreads),
+                           0, stream, g, ws, grid_mask, length_const, vec_prep);
+    else
+        hipLaunchKernelGGL(k_attach_prep<float>, dim3(static_cast<unsigned>(g.n), kPrepSplits), dim3(kAttachThreads),
+                           0, stream, g, ws, grid_mask, length_const, vec_prep);
     int rc = check_launch("meshy_gae_attach(prep)");
     if (rc) return rc;
     meshy_gae_args a{};

@@ -27,7 +27,8 @@ constexpr int64_t kBytesPerWorker = 128 * 1024;
 constexpr int kMaxWorkers = 16;
 
 // One gather: pieces [0, n) of sizes nbytes[i] land at dst + start[i]; worker w
-// copies output bytes [w * total / k, (w + 1) * total / k).
+// copies output bytes [w * total / k, (w + 1) * total / k).  With to_u8 the
+// pieces are fp32 masks of nbytes[i] floats, each written as one byte.
 struct Job {
     const void* const* srcs = nullptr;
     const int64_t* nbytes = nullptr;
@@ -36,7 +37,22 @@ struct Job {
     char* dst = nullptr;
     int64_t total = 0;
     int workers = 0;
+    bool to_u8 = false;
+    mutable std::atomic<bool> nonbinary{false};  // a float other than +0.0 and 1.0 was seen
 };
+
+// Floats to bytes; false when some float is not exactly +0.0 or 1.0.
+bool mask_to_u8(const float* src, int64_t count, uint8_t* dst) {
+    uint32_t bad = 0;
+    for (int64_t k = 0; k < count; ++k) {
+        uint32_t bits;
+        std::memcpy(&bits, src + k, 4);
+        const bool one = bits == 0x3f800000u;
+        bad |= static_cast<uint32_t>(!one && bits != 0u);
+        dst[k] = static_cast<uint8_t>(one);
+    }
+    return bad == 0;
+}
 
 void copy_share(const Job& j, int w) {
     const int64_t lo = j.total * w / j.workers;
@@ -44,11 +60,18 @@ void copy_share(const Job& j, int w) {
     if (lo >= hi) return;
     // First piece overlapping [lo, hi).
     int64_t i = std::upper_bound(j.start, j.start + j.n + 1, lo) - j.start - 1;
+    bool binary = true;
     for (; i < j.n && j.start[i] < hi; ++i) {
         const int64_t a = std::max(lo, j.start[i]);
         const int64_t b = std::min(hi, j.start[i] + j.nbytes[i]);
-        if (b > a) std::memcpy(j.dst + a, static_cast<const char*>(j.srcs[i]) + (a - j.start[i]), b - a);
+        if (b <= a) continue;
+        if (j.to_u8)
+            binary &= mask_to_u8(static_cast<const float*>(j.srcs[i]) + (a - j.start[i]), b - a,
+                                 reinterpret_cast<uint8_t*>(j.dst) + a);
+        else
+            std::memcpy(j.dst + a, static_cast<const char*>(j.srcs[i]) + (a - j.start[i]), b - a);
     }
+    if (!binary) j.nonbinary.store(true, std::memory_order_relaxed);
 }
 
 // Workers sleep on a condition variable between jobs; the calling thread takes
@@ -124,38 +147,66 @@ class Pool {
 }  // namespace
 }  // namespace meshy
 
-extern "C" int meshy_host_gather(const void* const* srcs, const int64_t* nbytes, int64_t n, void* dst,
-                                 int max_threads) {
-    using namespace meshy;
-    clear_error();
-    if (n < 0) return set_error(MESHY_EINVAL, "meshy_host_gather: negative count");
+namespace meshy {
+namespace {
+
+// Both gathers: sizes checked, then the job split over the pool.  `unit` is
+// the bytes read per output byte (1 for a copy, 4 for fp32 -> byte), which
+// sets how many workers the job is worth.
+int run_gather(const char* who, const void* const* srcs, const int64_t* sizes, int64_t n, void* dst,
+               int max_threads, bool to_u8, bool& binary) {
+    binary = true;
+    if (n < 0) return set_error(MESHY_EINVAL, "%s: negative count", who);
     if (n == 0) return MESHY_OK;
-    if (!srcs || !nbytes || !dst) return set_error(MESHY_ENULL, "meshy_host_gather: NULL pointer");
+    if (!srcs || !sizes || !dst) return set_error(MESHY_ENULL, "%s: NULL pointer", who);
     std::vector<int64_t> start(static_cast<size_t>(n) + 1);
     start[0] = 0;
     for (int64_t i = 0; i < n; ++i) {
-        if (nbytes[i] < 0) return set_error(MESHY_EINVAL, "meshy_host_gather: piece %lld has a negative size",
-                                            static_cast<long long>(i));
-        if (nbytes[i] > 0 && !srcs[i])
-            return set_error(MESHY_ENULL, "meshy_host_gather: piece %lld is NULL", static_cast<long long>(i));
-        start[i + 1] = start[i] + nbytes[i];
+        if (sizes[i] < 0)
+            return set_error(MESHY_EINVAL, "%s: piece %lld has a negative size", who, static_cast<long long>(i));
+        if (sizes[i] > 0 && !srcs[i])
+            return set_error(MESHY_ENULL, "%s: piece %lld is NULL", who, static_cast<long long>(i));
+        start[i + 1] = start[i] + sizes[i];
     }
     Job job;
     job.srcs = srcs;
-    job.nbytes = nbytes;
+    job.nbytes = sizes;
     job.start = start.data();
     job.n = n;
     job.dst = static_cast<char*>(dst);
     job.total = start[n];
+    job.to_u8 = to_u8;
     Pool& pool = Pool::get();
-    const int64_t want = std::max<int64_t>(1, job.total / kBytesPerWorker);
+    const int64_t want = std::max<int64_t>(1, job.total * (to_u8 ? 4 : 1) / kBytesPerWorker);
     const int cap = max_threads > 0 ? std::min(max_threads, pool.size()) : pool.size();
     job.workers = static_cast<int>(std::min<int64_t>(want, cap));
     if (job.workers <= 1) {
         job.workers = 1;
         copy_share(job, 0);
-        return MESHY_OK;
+    } else {
+        pool.run(job);
     }
-    pool.run(job);
+    binary = !job.nonbinary.load(std::memory_order_relaxed);
     return MESHY_OK;
+}
+
+}  // namespace
+}  // namespace meshy
+
+extern "C" int meshy_host_gather(const void* const* srcs, const int64_t* nbytes, int64_t n, void* dst,
+                                 int max_threads) {
+    meshy::clear_error();
+    bool binary;
+    return meshy::run_gather("meshy_host_gather", srcs, nbytes, n, dst, max_threads, false, binary);
+}
+
+extern "C" int meshy_host_gather_mask_u8(const float* const* srcs, const int64_t* counts, int64_t n, uint8_t* dst,
+                                         int max_threads, int32_t* binary) {
+    meshy::clear_error();
+    if (!binary) return meshy::set_error(MESHY_ENULL, "meshy_host_gather_mask_u8: binary is NULL");
+    bool ok;
+    const int rc = meshy::run_gather("meshy_host_gather_mask_u8", reinterpret_cast<const void* const*>(srcs), counts,
+                                     n, dst, max_threads, true, ok);
+    *binary = rc == MESHY_OK && ok ? 1 : 0;
+    return rc;
 }

@@ -147,19 +147,35 @@ CRITIC_METRICS = (
 )
 
 
+def _attach_layout(total: int, n: int, vdt: torch.dtype, mask_u8: bool, dev: torch.device):
+    """The attach's staging layout (masks as bytes or fp32, values, rewards,
+    offsets), a pinned host buffer and a device buffer of its size."""
+    from .batch import _Layout
+
+    lay = _Layout()
+    lay.add("mask", total, torch.uint8 if mask_u8 else torch.float32)
+    lay.add("values", total, vdt)
+    lay.add("reward", n, torch.float32)
+    lay.add("offsets", n + 1, torch.int64)
+    host = torch.empty(lay.size, dtype=torch.uint8, pin_memory=True)
+    dbuf = torch.empty(lay.size, dtype=torch.uint8, device=dev)
+    return lay, host, dbuf
+
+
 def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]:
     """Drop-in for ``TitanTrainer._attach_gae_advantages`` (trainer.py:603-699).
 
     Reads ``self.seq_len``, ``self.gae_gamma``, ``self.gae_alpha``,
     ``self.gae_lambda`` and ``self.device``.  The samples' masks, values and
     rewards travel to the device in two copies (the masks' while the values
-    are gathered on the host); ``meshy_gae_attach`` shifts them
+    are gathered on the host; masks of only 0 and 1 as one byte per token);
+    ``meshy_gae_attach`` shifts them
     onto the next-token grid, places each reward, runs the reverse scan over the
     samples laid end to end (one document per sample, so no padding rows) and
     reduces the critic metrics.  Each sample gets ``ADVANTAGE_TOKENS``, a device
     view of its advantages, of length ``min(len(tokens), seq_len)``.
     """
-    from .batch import _SCALAR_TYPE, ADVANTAGE_TOKENS, _column, _gather_column, _Layout
+    from .batch import _CPU_CONTIGUOUS_TENSOR, _SCALAR_TYPE, ADVANTAGE_TOKENS, _column, _gather_column
 
     if not samples:
         return {}
@@ -192,14 +208,24 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
     total = int(offsets[-1])
     bf16 = bool((vrec["dtype"] == _SCALAR_TYPE[torch.bfloat16]).all())
     vdt = torch.bfloat16 if bf16 else torch.float32
-    lay = _Layout()
-    lay.add("mask", total, torch.float32)
-    lay.add("values", total, vdt)
-    lay.add("reward", n, torch.float32)
-    lay.add("offsets", n + 1, torch.int64)
-    host = torch.empty(lay.size, dtype=torch.uint8, pin_memory=True)
-    dbuf = torch.empty(lay.size, dtype=torch.uint8, device=dev)
-    _gather_column(samples, used, used_b, widths, "mask_assistant", lay.view(host, "mask"))
+    # Masks that hold only 0 and 1 travel as bytes (a quarter of the copy, the
+    # same values); fractional ones, and columns that are not CPU fp32
+    # tensors, as fp32.
+    mrec = _column(samples, used_b, "mask_assistant")
+    lay, host, dbuf = _attach_layout(total, n, vdt, True, dev)
+    mask_u8 = bool(((mrec["flags"] == _CPU_CONTIGUOUS_TENSOR) & (mrec["dtype"] == _SCALAR_TYPE[torch.float32])
+                    & (mrec["row"] == 1) & (mrec["dim0"] >= widths)).all())
+    if mask_u8:
+        ptrs = np.ascontiguousarray(mrec["ptr"])
+        counts = np.ascontiguousarray(widths, dtype=np.int64)
+        binary = _lib.ctypes.c_int32(0)
+        _lib.check(_lib.load().meshy_host_gather_mask_u8(ptrs.ctypes.data, counts.ctypes.data, n,
+                                                         lay.addr(host.data_ptr(), "mask"), 0,
+                                                         _lib.ctypes.byref(binary)), "meshy_host_gather_mask_u8")
+        mask_u8 = bool(binary.value)
+    if not mask_u8:
+        lay, host, dbuf = _attach_layout(total, n, vdt, False, dev)
+        _gather_column(samples, used, used_b, widths, "mask_assistant", lay.view(host, "mask"), recs=mrec)
     # The masks travel to the device while the values are gathered (finer runs
     # of samples, each copied once staged, measured no faster).
     cut = lay.regions["values"][0]
@@ -235,6 +261,7 @@ def attach_gae_advantages(self: Any, samples: Sequence[Any]) -> dict[str, float]
     g.lambda_ = -1.0 if lam_const is None else float(lam_const)
     g.epsilon = 1e-6
     g.values_bf16 = int(bf16)
+    g.mask_u8 = int(mask_u8)
     g.adv = adv.data_ptr()
     g.grid_mask = None
     g.lam_doc = lam.data_ptr()

@@ -446,6 +446,41 @@ def test_attach_gae_advantages_matches_oracle(dev, gae_lambda, alpha, gamma, seq
         assert abs(metrics[k] - ref_m[k]) <= TOL, k
 
 
+def test_attach_stages_binary_masks_as_bytes_and_fractional_ones_as_fp32(dev):
+    """Masks of only 0 and 1 travel as bytes and give the same advantages and
+    metrics, bit for bit, as the same masks staged as fp32 (one sample's mask
+    as bool sends the whole batch down the fp32 path); a fractional mask
+    weight keeps fp32 and matches the oracle."""
+    from types import SimpleNamespace as NS
+
+    from meshy_amd.batch import ADVANTAGE_TOKENS
+    from meshy_amd.gae import attach_gae_advantages
+
+    trainer = NS(seq_len=500, gae_gamma=1.0, gae_alpha=1.5, gae_lambda=None, device=dev)
+    base = _critic_samples(30, seed=21)
+    as_bytes = [dict(s) for s in base]
+    as_fp32 = [dict(s) for s in base]
+    as_fp32[4]["mask_assistant"] = as_fp32[4]["mask_assistant"].bool()
+    m_bytes = attach_gae_advantages(trainer, as_bytes)
+    m_fp32 = attach_gae_advantages(trainer, as_fp32)
+    for a, b in zip(as_bytes, as_fp32):
+        assert torch.equal(a[ADVANTAGE_TOKENS], b[ADVANTAGE_TOKENS])
+    assert m_bytes == m_fp32
+    frac = [dict(s) for s in base]
+    g = torch.Generator().manual_seed(5)
+    for s in frac[::3]:
+        m = s["mask_assistant"].clone()
+        m[torch.rand(m.numel(), generator=g) < 0.2] *= 0.5
+        s["mask_assistant"] = m
+    ref_adv, ref_m = ogae.attach_gae_advantages([dict(s) for s in frac], seq_len=500, gamma=1.0, alpha=1.5,
+                                                gae_lambda=None)
+    metrics = attach_gae_advantages(trainer, frac)
+    for s, r in zip(frac, ref_adv):
+        assert (s[ADVANTAGE_TOKENS].cpu() - r).abs().max().item() <= TOL
+    for k in ref_m:
+        assert abs(metrics[k] - ref_m[k]) <= TOL, k
+
+
 def test_attach_reads_every_sample_form(dev):
     """Token lists, bool or int masks, rewards as Python floats or 1-element
     tensors, and values of mixed dtypes or non-contiguous take the converting

@@ -123,3 +123,50 @@ def test_errors():
     assert lib.meshy_host_gather(None, sizes, 2, 0x1000, 0) == -2
     assert lib.meshy_host_gather(ptrs, sizes, -1, 0x1000, 0) == -1
     assert lib.meshy_host_gather(None, None, 0, None, 0) == 0
+
+
+def _mask_u8(parts, threads=0):
+    lib = _lib.load()
+    ptrs = (ctypes.c_void_p * max(1, len(parts)))(*[p.data_ptr() for p in parts])
+    counts = (ctypes.c_int64 * max(1, len(parts)))(*[p.numel() for p in parts])
+    out = torch.full((sum(p.numel() for p in parts),), 7, dtype=torch.uint8)
+    binary = ctypes.c_int32(-1)
+    rc = lib.meshy_host_gather_mask_u8(ptrs, counts, len(parts), out.data_ptr(), threads, ctypes.byref(binary))
+    return rc, binary.value, out
+
+
+@pytest.mark.parametrize("n,hi", [(1, 10), (9, 3), (300, 5000), (64, 300_000)])
+def test_mask_u8_gather_of_binary_masks(n, hi):
+    """0/1 fp32 masks come out as the same values in bytes, on every thread count."""
+    g = torch.Generator().manual_seed(n)
+    parts = [(torch.rand(int(s), generator=g) > 0.4).float() for s in torch.randint(0, hi, (n,), generator=g)]
+    ref = torch.cat(parts).to(torch.uint8)
+    for threads in (1, 3, 0):
+        rc, binary, out = _mask_u8(parts, threads)
+        assert (rc, binary) == (0, 1)
+        assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("bad", [0.5, -0.0, 2.0, float("nan"), float("inf"), -1.0, 1e-45])
+def test_mask_u8_gather_reports_other_values(bad):
+    """Any float other than +0.0 and 1.0 (a fractional weight, -0.0, a
+    denormal, NaN) clears `binary`, wherever it lies."""
+    big = torch.ones(400_000)
+    for where in (0, 123_457, 399_999):
+        m = big.clone()
+        m[where] = bad
+        rc, binary, _ = _mask_u8([torch.zeros(5), m, torch.ones(3)])
+        assert (rc, binary) == (0, 0)
+
+
+def test_mask_u8_gather_errors():
+    lib = _lib.load()
+    binary = ctypes.c_int32(-1)
+    counts = (ctypes.c_int64 * 1)(-1)
+    ptrs = (ctypes.c_void_p * 1)(0x1000)
+    assert lib.meshy_host_gather_mask_u8(ptrs, counts, 1, 0x1000, 0, ctypes.byref(binary)) == -1
+    assert binary.value == 0
+    assert lib.meshy_host_gather_mask_u8(ptrs, counts, 1, 0x1000, 0, None) == -2
+    binary.value = -1
+    assert lib.meshy_host_gather_mask_u8(None, None, 0, None, 0, ctypes.byref(binary)) == 0
+    assert binary.value == 1
