@@ -547,6 +547,22 @@ typedef struct meshy_gae_args {
 size_t meshy_gae_workspace_size(int64_t rows, int64_t S, int64_t n_docs);
 int meshy_gae(const meshy_gae_args* args, hipStream_t stream);
 
+/* ------------------------------------------------------------------------
+ * Document order of unsorted doc_ids (device).
+ * The reference sums per document with index_add_ over doc_ids in any order
+ * (trainer.py:705-848 _ppo_clip_loss, opd.py:161-197 _distill_loss,
+ * critic/gae.py:296-312 advantages_to_per_sequence); the kernels here take
+ * each document as one run of tokens.  meshy_doc_order writes the stable sort
+ * of the n token positions by document: perm[k] is the position of the k-th
+ * token in document order (equal ids keep their order), sorted_ids[k] its id.
+ * Every id must lie in [0, n_slots) (meshy_segment_offsets' range flag checks
+ * it).  The workspace size comes from a query on the current device (0 when
+ * it fails).
+ * ---------------------------------------------------------------------- */
+size_t meshy_doc_order_workspace_size(int64_t n, int64_t n_slots);
+int meshy_doc_order(const int64_t* doc_ids, int64_t n, int64_t n_slots, int64_t* sorted_ids, int64_t* perm,
+                    void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* Test hook, no counterpart in the reference: the number of polls after which
  * meshy_gae's one-pass kernel stops waiting for a neighbouring chunk's map
  * and leaves the call to its exact fix-up pass (default 2000; a negative

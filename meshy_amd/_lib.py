@@ -317,6 +317,8 @@ SIGNATURES = {
     "meshy_gae_workspace_size": (c_size_t, [c_int64, c_int64, c_int64]),
     "meshy_gae": (c_int, [POINTER(GaeArgs), c_void_p]),
     "meshy_gae_set_poll_limit": (c_int, [c_int]),
+    "meshy_doc_order_workspace_size": (c_size_t, [c_int64, c_int64]),
+    "meshy_doc_order": (c_int, [c_void_p, c_int64, c_int64, c_void_p, c_void_p, c_void_p, c_size_t, c_void_p]),
     "meshy_gae_attach_workspace_size": (c_size_t, [c_int64, c_int64]),
     "meshy_gae_attach": (c_int, [POINTER(GaeAttachArgs), c_void_p]),
     "meshy_whiten_workspace_size": (c_size_t, [c_int64]),
@@ -355,7 +357,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 _LIB: ctypes.CDLL | None = None
 

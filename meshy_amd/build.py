@@ -24,7 +24,7 @@ CSRC = os.path.join(HERE, "csrc")
 BUILD_DIR = os.path.join(HERE, "_build")
 OUT = os.path.join(HERE, "libmeshy_amd.so")
 
-SOURCES = ("capi.cpp", "plan.cpp", "hostio.cpp", "logprob.hip", "topk.hip", "distill.hip", "pack.hip", "ppo.hip", "gae.hip", "critic.hip", "ragged.hip", "synth.hip")
+SOURCES = ("capi.cpp", "plan.cpp", "hostio.cpp", "logprob.hip", "topk.hip", "distill.hip", "pack.hip", "ppo.hip", "gae.hip", "critic.hip", "ragged.hip", "synth.hip", "order.hip")
 
 PYIO_SRC = "pyio.cpp"
 PYIO_OUT = os.path.join(HERE, "_pyio" + (sysconfig.get_config_var("EXT_SUFFIX") or ".so"))

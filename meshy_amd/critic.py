@@ -28,7 +28,7 @@ import torch
 
 from . import _lib
 from .gae import compute_returns
-from .loss import checked_segment_offsets
+from .loss import UnsortedDocIdsError, checked_segment_offsets, doc_order
 
 
 def _as_f32(t: torch.Tensor) -> torch.Tensor:
@@ -42,9 +42,9 @@ def _as_f32(t: torch.Tensor) -> torch.Tensor:
 def advantages_to_per_sequence(adv: torch.Tensor, mask: torch.Tensor, doc_ids: torch.Tensor,
                                n_docs: int) -> torch.Tensor:
     """Masked token-mean of per-token ``adv``, one fp32 scalar per document
-    (gae.py:296-312); the padding slot is ignored.  ``doc_ids`` must be
-    non-decreasing over the flattened micro-batch, as both batch layouts make
-    them (checked once per tensor: ValueError otherwise)."""
+    (gae.py:296-312); the padding slot is ignored.  ``doc_ids`` in any order
+    (non-decreasing, as both batch layouts make them, reads them as they
+    are; otherwise the tokens are taken in document order first)."""
     _lib.require_gpu(adv, mask, doc_ids)
     n_docs = int(n_docs)
     out = torch.empty(n_docs, dtype=torch.float32, device=adv.device)
@@ -54,7 +54,12 @@ def advantages_to_per_sequence(adv: torch.Tensor, mask: torch.Tensor, doc_ids: t
     m = mask.reshape(-1).to(torch.float32).contiguous()
     if m.numel() != x.numel() or doc_ids.numel() != x.numel():
         raise ValueError(f"adv has {x.numel()} tokens but mask and doc_ids have {m.numel()} and {doc_ids.numel()}")
-    off = checked_segment_offsets(doc_ids, n_docs + 1)
+    try:
+        off = checked_segment_offsets(doc_ids, n_docs + 1)
+    except UnsortedDocIdsError:
+        perm, sorted_ids = doc_order(doc_ids, n_docs + 1)
+        x, m = x.index_select(0, perm), m.index_select(0, perm)
+        off = checked_segment_offsets(sorted_ids, n_docs + 1)
     rc = _lib.load().meshy_per_sequence_mean(x.data_ptr(), m.data_ptr(), off.data_ptr(), n_docs, out.data_ptr(),
                                              _lib.stream_of(adv.device))
     _lib.check(rc, "meshy_per_sequence_mean")

@@ -57,6 +57,12 @@ class DocIdRangeError(ValueError):
     reference's ``index_add_`` raises there)."""
 
 
+class UnsortedDocIdsError(ValueError):
+    """doc_ids that decrease somewhere over the flattened micro-batch.  The
+    losses and the per-sequence mean then run on the tokens in document order
+    (``doc_order``); the offsets-based kernels alone refuse them."""
+
+
 # Segment offsets of recently seen doc_ids tensors whose order was checked,
 # or the ValueError a rejected tensor raised.  Entries hold a weak reference to
 # their tensor: a hit needs the same live object (its id and data pointer
@@ -103,8 +109,84 @@ def segment_offsets(doc_ids: torch.Tensor, n_slots: int, check_sorted: bool = Fa
         if bad & 2:
             raise DocIdRangeError(f"doc_ids must lie in [0, {n_slots - 1}] (the document slots and the padding slot)")
         if bad & 1:
-            raise ValueError("doc_ids must be non-decreasing over the flattened micro-batch")
+            raise UnsortedDocIdsError("doc_ids must be non-decreasing over the flattened micro-batch")
     return off
+
+
+def doc_order(doc_ids: torch.Tensor, n_slots: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """``(perm, sorted_ids)``: the stable order of the flattened ``doc_ids``'
+    tokens by document (``perm[k]`` is the k-th token's position, equal ids
+    keep their order) and the ids in that order, from ``meshy_doc_order``.
+    The ids must lie in ``[0, n_slots)``."""
+    ids = doc_ids.reshape(-1).to(torch.int64).contiguous()
+    n = ids.numel()
+    perm = torch.empty(n, dtype=torch.int64, device=ids.device)
+    sorted_ids = torch.empty_like(perm)
+    if n == 0:
+        return perm, sorted_ids
+    lib = _lib.load()
+    with torch.cuda.device(ids.device):
+        ws_bytes = int(lib.meshy_doc_order_workspace_size(n, n_slots))
+        ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=ids.device)
+        rc = lib.meshy_doc_order(ids.data_ptr(), n, n_slots, sorted_ids.data_ptr(), perm.data_ptr(), ws.data_ptr(),
+                                 ws_bytes, _lib.stream_of(ids.device))
+    _lib.check(rc, "meshy_doc_order")
+    return perm, sorted_ids
+
+
+class DocOrdered:
+    """A micro-batch's tokens in document order: the per-token tensors named
+    in ``token_fields`` gathered through ``perm`` into ``[1, T, ...]`` tensors,
+    ``doc_ids`` sorted, every other attribute the batch's own.  The losses run
+    on it as on a batch whose ids never decrease; per-token inputs passed
+    beside the batch go through ``gather``, which keeps the autograd graph, so
+    gradients land back on the original positions."""
+
+    def __init__(self, mb: Any, token_fields: tuple[str, ...]) -> None:
+        n_slots = int(mb.n_docs) + 1
+        self.perm, sorted_ids = doc_order(mb.doc_ids, n_slots)
+        self._mb = mb
+        self._cache: dict[tuple, torch.Tensor] = {}
+        self.doc_ids = sorted_ids.reshape(1, -1)
+        for name in token_fields:
+            t = getattr(mb, name, None)
+            object.__setattr__(self, name, None if t is None else self.gather(t))
+
+    def gather(self, t: torch.Tensor) -> torch.Tensor:
+        """``t``'s tokens in document order: ``[1, T]`` for one value per token,
+        ``[1, T, K]`` for K (the leading dimensions of ``t`` hold the T tokens)."""
+        T = self.perm.numel()
+        if t.numel() == T:
+            return t.reshape(T).index_select(0, self.perm).reshape(1, T)
+        if T == 0 or t.numel() % T:
+            raise ValueError(f"a per-token tensor of {t.numel()} elements for {T} tokens")
+        return t.reshape(T, -1).index_select(0, self.perm).reshape(1, T, -1)
+
+    def gather_cached(self, t: torch.Tensor | None) -> torch.Tensor | None:
+        """``gather`` of a tensor that needs no gradient, kept while it is unchanged."""
+        if t is None:
+            return None
+        key = tensor_key(t)
+        hit = self._cache.get(key)
+        if hit is None:
+            hit = self.gather(t.detach())
+            self._cache.clear()
+            self._cache[key] = hit
+        return hit
+
+    def __getattr__(self, name: str) -> Any:
+        # The library's own caches (offsets, inputs) belong to each object.
+        if name.startswith("_meshy"):
+            raise AttributeError(name)
+        return getattr(self._mb, name)
+
+
+def doc_ordered(mb: Any, token_fields: tuple[str, ...]) -> DocOrdered:
+    """The batch's ``DocOrdered`` copy, kept on the batch while its ids and
+    the gathered fields are unchanged (later epochs over one micro)."""
+    refs = (mb.doc_ids, *[getattr(mb, f, None) for f in token_fields])
+    key = (tuple(tensor_key(t) for t in refs), int(mb.n_docs), token_fields)
+    return batch_cached(mb, "_meshy_doc_ordered", key, refs, lambda: DocOrdered(mb, token_fields))
 
 
 class _Inputs:
@@ -204,7 +286,15 @@ def ppo_clip_loss(
         raise NotImplementedError(
             "context-parallel PPO loss needs the per-document all-reduce between the two "
             "kernel phases; this library drives one GPU")
-    inputs = _cached_inputs(self, new_lp, old_lp, mb, mini, entropy)
+    try:
+        inputs = _cached_inputs(self, new_lp, old_lp, mb, mini, entropy)
+    except UnsortedDocIdsError:
+        # Ids that decrease: the same loss over the tokens in document order
+        # (new_lp's gather carries the gradient back to its positions).
+        per_token_adv = mb.advantages is not None and mb.advantages.dim() != 1
+        od = doc_ordered(mb, ("mask", "rollout_logprobs") + (("advantages",) if per_token_adv else ()))
+        return ppo_clip_loss(self, od.gather(new_lp), od.gather_cached(old_lp), od, mini,
+                             None if entropy is None else od.gather(entropy))
     # The kernels read new_lp as one flat fp32 array; a contiguous fp32 tensor
     # of any shape is passed as it is, so that no view node sits between the
     # loss's node and new_lp's (each autograd node costs host time).
@@ -257,5 +347,6 @@ def reduce_mini_metrics(self: Any, sums: dict[str, torch.Tensor]) -> dict[str, f
     return out
 
 
-__all__ = ["DocIdRangeError", "batch_segment_offsets", "checked_segment_offsets", "ppo_clip_loss", "reduce_mini_metrics",
+__all__ = ["DocIdRangeError", "DocOrdered", "UnsortedDocIdsError", "batch_segment_offsets", "checked_segment_offsets",
+           "doc_order", "doc_ordered", "ppo_clip_loss", "reduce_mini_metrics",
            "segment_offsets"]

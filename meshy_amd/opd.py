@@ -25,7 +25,7 @@ import torch.distributed as dist
 
 from . import _lib
 from .batch import TEACHER_FIELDS, Batch, launch_pack, stage_micro_batches
-from .loss import batch_cached, batch_segment_offsets, tensor_key
+from .loss import UnsortedDocIdsError, batch_cached, batch_segment_offsets, doc_ordered, tensor_key
 from .plan import Layout, MicroPlan
 from .topk import gather_logprobs
 
@@ -173,7 +173,13 @@ def distill_from_gathered(self: Any, gathered: torch.Tensor, mb: Any, mini: Any)
         student = student.float()
     if not student.is_contiguous():
         student = student.contiguous()
-    inputs = _cached_inputs(self, mb, mini, k, student, student.numel() // (k + 1))
+    try:
+        inputs = _cached_inputs(self, mb, mini, k, student, student.numel() // (k + 1))
+    except UnsortedDocIdsError:
+        # Ids that decrease: the same loss over the tokens in document order
+        # (the gather's copy carries the gradient back to its positions).
+        od = doc_ordered(mb, ("mask", "rollout_logprobs", "teacher_topk_logprobs"))
+        return distill_from_gathered(self, od.gather(gathered), od, mini)
     # One native call: the forward kernels, the loss (carrying a C++ backward
     # node when the student requires grad) and every sum as a 0-dim view.
     loss, parts = _lib.autograd().distill_loss(student, inputs.native)

@@ -93,6 +93,11 @@ def _call(name, *args):
     ("meshy_grpo_advantage_host", (FAKE, 8, None, 2, FAKE), ENULL, "NULL"),
     ("meshy_zero_variance_groups_host", (FAKE, 8, None, 2, 1e-8, FAKE), ENULL, "NULL"),
     ("meshy_segment_offsets", (FAKE, 10, 0, FAKE, None, None), EINVAL, "bad sizes"),
+    ("meshy_doc_order", (FAKE, -1, 4, FAKE, FAKE, FAKE, 1 << 20, None), EINVAL, "bad sizes"),
+    ("meshy_doc_order", (FAKE, 10, 0, FAKE, FAKE, FAKE, 1 << 20, None), EINVAL, "bad sizes"),
+    ("meshy_doc_order", (FAKE, 1 << 31, 4, FAKE, FAKE, FAKE, 1 << 20, None), EINVAL, "too many tokens"),
+    ("meshy_doc_order", (None, 10, 4, FAKE, FAKE, FAKE, 1 << 20, None), ENULL, "required"),
+    ("meshy_doc_order", (FAKE, 10, 4, FAKE, None, FAKE, 1 << 20, None), ENULL, "required"),
     ("meshy_stream_read", (FAKE, 4, 17, FAKE, None), EINVAL, "bad shape"),
     ("meshy_stream_read", (FAKE + 4, 4, 32, FAKE, None), EALIGN, "misaligned"),
 ])

@@ -57,13 +57,23 @@ def test_per_sequence_mean_packed_with_padding_slot(dev):
     assert (out.cpu() - ref).abs().max().item() <= 1e-5
 
 
-def test_per_sequence_mean_rejects_doc_ids_out_of_order(dev):
+def test_per_sequence_mean_takes_doc_ids_in_any_order(dev):
+    """Ids in any order (the reference sums with index_add_): the mean of each
+    document's masked advantages, against the oracle."""
     from meshy_amd import critic
 
-    ids = torch.tensor([[0, 0, 2, 1, 1]], device=dev)
-    ones = torch.ones(1, 5, device=dev)
-    with pytest.raises(ValueError, match="non-decreasing"):
-        critic.advantages_to_per_sequence(ones, ones, ids, 3)
+    ids = torch.tensor([[0, 0, 2, 1, 1]])
+    adv = torch.tensor([[1.0, 2.0, 3.0, 4.0, 5.0]])
+    mask = torch.tensor([[1.0, 1.0, 1.0, 0.0, 1.0]])
+    out = critic.advantages_to_per_sequence(adv.to(dev), mask.to(dev), ids.to(dev), 3)
+    assert torch.equal(out.cpu(), torch.tensor([1.5, 5.0, 3.0]))
+    g = torch.Generator().manual_seed(2)
+    ids = torch.randint(0, 51, (3, 4000), generator=g)
+    adv = torch.randn(3, 4000, generator=g)
+    mask = (torch.rand(3, 4000, generator=g) > 0.3).float()
+    out = critic.advantages_to_per_sequence(adv.to(dev), mask.to(dev), ids.to(dev), 50)
+    ref = ocritic.advantages_to_per_sequence(adv, mask, ids, 50)
+    assert (out.cpu() - ref).abs().max().item() <= 1e-5
 
 
 @pytest.mark.parametrize("bf16", [False, True])

@@ -399,6 +399,45 @@ def test_distill_from_gathered_matches_oracle(dev, per_token, clamps, rollout):
         assert m[key] == pytest.approx(rm[key], abs=TOL), key
 
 
+@pytest.mark.parametrize("per_token", [True, False])
+def test_distill_doc_ids_in_any_order(dev, per_token):
+    """The tokens of a packed micro shuffled (so the document ids decrease):
+    the loss, its sums and the gradient match the oracle's index_add_ over the
+    shuffled order, as the reference accepts any order."""
+    from types import SimpleNamespace as NS
+
+    from meshy_amd import opd
+    from meshy_amd.plan import MicroPlan, MiniPlan
+
+    K = 8
+    samples = [_opd_sample(L, K, 40 + i) for i, L in enumerate([300, 41, 700, 129])]
+    micro = MicroPlan((0, 1, 2, 3), 1280, (300, 41, 700, 129))
+    mb = opd.build_topk_micro_batches(samples, [micro], layout="packed", device=dev, need_rollout_lp=True)[0]
+    S = micro.seq_len
+    g = torch.Generator().manual_seed(9)
+    order = torch.randperm(S, generator=g).to(dev)
+    sh = NS(teacher_topk_logprobs=mb.teacher_topk_logprobs[:, order].contiguous(),
+            mask=mb.mask[:, order].contiguous(), rollout_logprobs=mb.rollout_logprobs[:, order].contiguous(),
+            doc_ids=mb.doc_ids[:, order].contiguous(), n_docs=mb.n_docs)
+    gathered = torch.log_softmax(torch.randn(1, S, K + 1, generator=g) * 4, -1)
+    mini = MiniPlan((micro,), 5, int(mb.mask.sum().item()), (0,))
+    stub = _stub(per_token)
+    gd = gathered.to(dev).requires_grad_(True)
+    loss, sums = opd.distill_from_gathered(stub, gd, sh, mini)
+    gr = gathered.clone().requires_grad_(True)
+    rl, rs = oopd.distill_loss(gr, sh.teacher_topk_logprobs.cpu(), sh.mask.cpu(), sh.doc_ids.cpu(), sh.n_docs,
+                               rollout_lp=sh.rollout_logprobs.cpu(), n_docs_global=mini.n_docs_global,
+                               n_tokens_global=mini.n_tokens_global, per_token_loss=per_token,
+                               log_prob_min_clamp=-10.0, loss_max_clamp=10.0)
+    assert abs(float(loss.detach()) - float(rl.detach())) <= TOL
+    for key in rs:
+        want = float(rs[key])
+        assert abs(float(sums[key]) - want) <= TOL + 1e-5 * abs(want), key
+    loss.backward()
+    rl.backward()
+    assert (gd.grad.cpu() - gr.grad).abs().max().item() <= 1e-6
+
+
 def test_distill_inputs_cache_follows_edits(dev):
     """A second loss over one micro-batch reuses its flattened inputs; an
     in-place edit of the Teacher's log-probs or the mask, other clamps or a new

@@ -424,26 +424,86 @@ def test_segment_offsets_detect_unsorted(dev):
         segment_offsets(ids.to(dev), 100, check_sorted=True)
 
 
-def test_loss_rejects_doc_ids_out_of_order(dev):
-    """A batch not built by the pack kernels has its doc_ids order checked once
-    (the offsets the kernels take assume it); decreasing ids raise ValueError,
-    again on the next call, and a fix in place is accepted."""
+@pytest.mark.parametrize("n,n_slots", [(1, 1), (7, 3), (1000, 2), (65536, 1024), (1_000_003, 1000), (300_000, 70_001)])
+def test_doc_order_is_the_stable_sort(dev, n, n_slots):
+    """meshy_doc_order's permutation is numpy's stable argsort of the ids
+    (ties keep their positions) and its ids are the sorted ids, over slot
+    counts on both sides of a power of two."""
+    from meshy_amd.loss import doc_order
+
+    rng = np.random.default_rng(n + n_slots)
+    ids = rng.integers(0, n_slots, n)
+    perm, sorted_ids = doc_order(torch.from_numpy(ids).to(dev), n_slots)
+    want = np.argsort(ids, kind="stable")
+    assert np.array_equal(perm.cpu().numpy(), want)
+    assert np.array_equal(sorted_ids.cpu().numpy(), ids[want])
+
+
+def test_loss_takes_doc_ids_out_of_order(dev):
+    """doc_ids that decrease (a batch not built by the pack kernels) are
+    accepted, as the reference's index_add_ accepts them: the loss runs on the
+    tokens in document order and matches the oracle, call after call, and
+    after an in-place edit of the ids."""
+    g = torch.Generator().manual_seed(4)
+    doc_ids = torch.tensor([[0, 0, 1, 1, 0, 1, 1, 1]])
+    mask = torch.ones(1, 8)
+    mask[0, -1] = 0
+    old = -torch.rand(1, 8, generator=g) * 3
+    new = old + 0.1 * torch.randn(1, 8, generator=g)
+    adv = torch.tensor([1.0, -1.0])
+    for _ in range(2):
+        _compare(dev, new, old, mask, doc_ids, adv, 2, use_tis=True)
+    doc_ids[0, 4] = 1
+    _compare(dev, new, old, mask, doc_ids, adv, 2, use_tis=True)
+
+
+@pytest.mark.parametrize("per_token_loss", [True, False])
+@pytest.mark.parametrize("per_token_adv", [False, True])
+@pytest.mark.parametrize("icepop", [False, True])
+def test_doc_ids_in_any_order_match_oracle(dev, per_token_loss, per_token_adv, icepop):
+    """Random document ids in random order (the padding slot among them) over
+    a [3, 700] batch, with rollout log-probs, entropy and positive-LM
+    weights: loss, every sum and d loss / d new_lp against the oracle's
+    index_add_ over the same order."""
+    g = torch.Generator().manual_seed(per_token_loss * 4 + per_token_adv * 2 + icepop)
+    rows, S, n = 3, 700, 9
+    doc_ids = torch.randint(0, n + 1, (rows, S), generator=g)
+    mask = (torch.rand(rows, S, generator=g) > 0.2).float()
+    old = -torch.rand(rows, S, generator=g) * 4
+    new = old + 0.1 * torch.randn(rows, S, generator=g)
+    adv = torch.randn(rows, S, generator=g) if per_token_adv else torch.randn(n, generator=g)
+    rollout = old + 0.05 * torch.randn(rows, S, generator=g)
+    entropy = torch.rand(rows, S, generator=g)
+    pos_w = torch.rand(n, generator=g)
+    _compare(dev, new, old, mask, doc_ids, adv, n, rollout=rollout, entropy=entropy, pos_w=pos_w,
+             per_token_loss=per_token_loss, use_icepop=icepop, use_tis=not icepop, positive_lm_coef=0.1)
+
+
+def test_doc_ids_in_any_order_are_deterministic(dev):
+    """The document order is a function of the ids alone (a stable sort), so
+    repeated calls give bitwise equal losses, sums and gradients."""
+    from meshy_amd.batch import Batch
     from meshy_amd.loss import ppo_clip_loss
     from meshy_amd.plan import MiniPlan
 
-    mb = _batch(dev, rows=1, S=8)
-    mb.doc_ids = torch.tensor([[0, 0, 1, 1, 0, 1, 1, 1]], device=dev)
-    mb.advantages = torch.tensor([1.0, -1.0], device=dev)
-    mb.n_docs = 2
-    mini = MiniPlan(micros=(), n_docs_global=2, n_tokens_global=int(mb.mask.sum()), tokens_per_rank=(8,))
-    old = -torch.ones(1, 8, device=dev)
-    new = (old + 0.05).requires_grad_()
-    for _ in range(2):
-        with pytest.raises(ValueError, match="non-decreasing"):
-            ppo_clip_loss(_stub(), new, old, mb, mini)
-    mb.doc_ids[0, 4] = 1
-    loss, _ = ppo_clip_loss(_stub(), new, old, mb, mini)
-    assert torch.isfinite(loss)
+    g = torch.Generator().manual_seed(8)
+    rows, S, n = 2, 5000, 40
+    doc_ids = torch.randint(0, n, (rows, S), generator=g).to(dev)
+    mask = (torch.rand(rows, S, generator=g) > 0.1).float().to(dev)
+    old = (-torch.rand(rows, S, generator=g) * 4).to(dev)
+    z = torch.zeros(rows, S, dtype=torch.long, device=dev)
+    mb = Batch(z, z, z.int(), mask, doc_ids, torch.randn(n, generator=g).to(dev), None,
+               torch.zeros(n, device=dev), n)
+    mini = MiniPlan(micros=(), n_docs_global=n, n_tokens_global=int(mask.sum()), tokens_per_rank=())
+    outs = []
+    for stub in (_stub(calculate_per_token_loss=False), _stub(calculate_per_token_loss=False)):
+        new = (old + 0.05).requires_grad_(True)
+        loss, sums = ppo_clip_loss(stub, new, old, mb, mini)
+        loss.backward()
+        outs.append((loss.detach().clone(), {k: v.clone() for k, v in sums.items()}, new.grad.clone()))
+    (l0, s0, g0), (l1, s1, g1) = outs
+    assert torch.equal(l0, l1) and torch.equal(g0, g1)
+    assert all(torch.equal(s0[k], s1[k]) for k in s0)
 
 
 @pytest.mark.parametrize("bad", [-1, 3, 7])
