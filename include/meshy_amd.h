@@ -122,6 +122,10 @@ int meshy_host_gather_mask_u8(const float* const* srcs, const int64_t* counts, i
  * 0 when L <= 1. */
 int meshy_sample_loss_tokens(const float* mask, const int64_t* offsets, int64_t n,
                              int64_t seq_len, int64_t* lengths, int64_t* loss_tokens);
+/* The same over a mask staged as bytes (meshy_host_gather_mask_u8): a
+ * nonzero byte counts. */
+int meshy_sample_loss_tokens_u8(const uint8_t* mask, const int64_t* offsets, int64_t n,
+                                int64_t seq_len, int64_t* lengths, int64_t* loss_tokens);
 
 /* The host plan of one packing step in one call (host): what
  * TitanTrainer.plan_batch does before it builds each micro
@@ -138,7 +142,8 @@ int meshy_sample_loss_tokens(const float* mask, const int64_t* offsets, int64_t 
  * and the counts n_micro, n_docs, max_micro_elems, max_docs_per_micro.  The
  * errors are those of the two calls it makes. */
 typedef struct meshy_step_plan_args {
-    const float* mask;             /* [offsets[n]] host                       */
+    const void* mask;              /* [offsets[n]] host, fp32 (or bytes with
+                                      mask_u8)                                */
     const int64_t* offsets;        /* [n + 1]                                 */
     int64_t n;
     int64_t dp_size;
@@ -156,6 +161,8 @@ typedef struct meshy_step_plan_args {
     int64_t n_docs;                /* out                                     */
     int64_t max_micro_elems;       /* out                                     */
     int64_t max_docs_per_micro;    /* out                                     */
+    int32_t mask_u8;               /* 1: mask holds one byte per token        */
+    int32_t reserved;
 } meshy_step_plan_args;
 int meshy_step_plan(meshy_step_plan_args* args);
 
@@ -171,7 +178,8 @@ typedef struct meshy_pack_args {
     const void* tokens;            /* [total] int32 or int64                  */
     int32_t tokens_elem_bytes;     /* 4 or 8                                  */
     int32_t layout;                /* MESHY_LAYOUT_*                          */
-    const float* mask;             /* [total] mask_assistant                  */
+    const void* mask;              /* [total] mask_assistant, fp32 (or one
+                                      byte per token, 0 or 1, with mask_u8)  */
     const float* logprobs;         /* [total] rollout logprobs, nullable      */
     const float* adv_tokens;       /* [total] per-token advantages (already on
                                       the next-token grid), nullable         */
@@ -220,7 +228,7 @@ typedef struct meshy_pack_args {
     int64_t* teacher_ids_out;      /* [n_out, teacher_k]                      */
     float* teacher_lps_out;        /* [n_out, teacher_k]                      */
     int32_t teacher_ids_elem_bytes; /* 4 or 8 (0 reads as 4)                  */
-    int32_t reserved_t;
+    int32_t mask_u8;               /* 1: mask holds bytes (see mask)          */
     /* Optional int64 token offsets of each micro's n_docs + 1 document slots
        (padding slot last) over its flattened [rows, S] grid, the loss kernels'
        seg_offsets: micro k writes n_docs_k + 2 values at

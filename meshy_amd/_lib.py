@@ -91,6 +91,8 @@ class StepPlanArgs(ctypes.Structure):
         ("n_docs", c_int64),
         ("max_micro_elems", c_int64),
         ("max_docs_per_micro", c_int64),
+        ("mask_u8", c_int32),
+        ("reserved", c_int32),
     ]
 
 
@@ -129,7 +131,7 @@ class PackArgs(ctypes.Structure):
         ("teacher_ids_out", c_void_p),
         ("teacher_lps_out", c_void_p),
         ("teacher_ids_elem_bytes", c_int32),
-        ("reserved_t", c_int32),
+        ("mask_u8", c_int32),
         ("seg_offsets", c_void_p),
     ]
 
@@ -258,6 +260,7 @@ SIGNATURES = {
         [c_void_p, c_void_p, c_int64, c_int64, POINTER(PlannerCfg), POINTER(PlanOut)],
     ),
     "meshy_sample_loss_tokens": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
+    "meshy_sample_loss_tokens_u8": (c_int, [c_void_p, c_void_p, c_int64, c_int64, c_void_p, c_void_p]),
     "meshy_step_plan": (c_int, [POINTER(StepPlanArgs)]),
     "meshy_host_gather": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int]),
     "meshy_host_gather_mask_u8": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int, POINTER(c_int32)]),
@@ -357,7 +360,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 _LIB: ctypes.CDLL | None = None
 

@@ -135,7 +135,7 @@ class _Layout:
         return buf[lo:hi].view(_NP_DTYPE[dtype])
 
 
-_NP_DTYPE = {torch.int32: np.int32, torch.int64: np.int64, torch.float32: np.float32}
+_NP_DTYPE = {torch.int32: np.int32, torch.int64: np.int64, torch.float32: np.float32, torch.uint8: np.uint8}
 
 
 # Records of meshy_amd._stage.columns: one per used sample.
@@ -237,6 +237,8 @@ class PackJob:
     adv_tokens_dev: torch.Tensor | None = None
     #: Teacher Top-K width staged with the samples (0: no Teacher columns).
     teacher_k: int = 0
+    #: The staged mask holds one byte per token (0 or 1) instead of fp32.
+    mask_u8: bool = False
     #: The HIP stream handle to launch on (None: the device's current stream).
     stream: int | None = None
     #: Per micro (ids, logprobs) Teacher columns in the micro's layout, filled by
@@ -515,6 +517,7 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
     a.tokens_elem_bytes = lay.regions["tokens"][2].itemsize
     a.layout = _lib.MESHY_LAYOUT_PACKED if layout == "packed" else _lib.MESHY_LAYOUT_PADDED
     a.mask = lay.addr(base, "mask")
+    a.mask_u8 = int(job.mask_u8)
     a.logprobs = lay.addr(base, "logprobs") if job.need_rollout_lp else None
     if job.adv_tokens_dev is not None:
         a.adv_tokens = job.adv_tokens_dev.data_ptr()

@@ -34,4 +34,4 @@ int check_launch(const char* what) {
 
 extern "C" const char* meshy_last_error(void) { return meshy::g_last_error; }
 
-extern "C" int meshy_abi_version(void) { return 11; }
+extern "C" int meshy_abi_version(void) { return 12; }

@@ -164,7 +164,8 @@ __global__ __launch_bounds__(kFillThreads) void k_pack_fill(meshy_pack_args a) {
             in_id = static_cast<int64_t>(tokens[src]);
             if (p + 1 < L) {
                 lab = static_cast<int64_t>(tokens[src + 1]);
-                mk = a.mask[src + 1];
+                mk = a.mask_u8 ? static_cast<float>(static_cast<const uint8_t*>(a.mask)[src + 1])
+                               : static_cast<const float*>(a.mask)[src + 1];
                 if (a.logprobs) lp = a.logprobs[src + 1];
             }
             if (a.adv_tokens) adv = a.adv_tokens[src];

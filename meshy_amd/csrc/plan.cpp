@@ -332,24 +332,42 @@ __attribute__((target_clones("avx2", "default"))) int64_t count_positive(const f
     return c;
 }
 
-}  // namespace
+// The same over a mask of bytes (each 0 or 1, or any byte: nonzero counts).
+__attribute__((target_clones("avx2", "default"))) int64_t count_positive(const uint8_t* m, int64_t n) {
+    int32_t c = 0;
+    for (int64_t t = 0; t < n; ++t) c += static_cast<int32_t>(m[t] != 0);
+    return c;
+}
 
-extern "C" int meshy_sample_loss_tokens(const float* mask, const int64_t* offsets, int64_t n,
-                                        int64_t seq_len, int64_t* lengths, int64_t* loss_tokens) {
-    meshy::clear_error();
-    if (n < 0 || seq_len <= 0) return set_error(MESHY_EINVAL, "meshy_sample_loss_tokens: bad sizes");
+template <typename M>
+int sample_loss_tokens(const char* who, const M* mask, const int64_t* offsets, int64_t n, int64_t seq_len,
+                       int64_t* lengths, int64_t* loss_tokens) {
+    if (n < 0 || seq_len <= 0) return set_error(MESHY_EINVAL, "%s: bad sizes", who);
     if (n > 0 && (!offsets || !lengths || !loss_tokens || (!mask && offsets[n] > offsets[0])))
-        return set_error(MESHY_ENULL, "meshy_sample_loss_tokens: NULL pointer");
+        return set_error(MESHY_ENULL, "%s: NULL pointer", who);
     for (int64_t i = 0; i < n; ++i) {
         const int64_t a = offsets[i];
         const int64_t len = offsets[i + 1] - a;
-        if (len < 0) return set_error(MESHY_EINVAL, "meshy_sample_loss_tokens: offsets decrease at %lld",
-                                      static_cast<long long>(i));
+        if (len < 0) return set_error(MESHY_EINVAL, "%s: offsets decrease at %lld", who, static_cast<long long>(i));
         lengths[i] = len;
         const int64_t L = std::min(len, seq_len);
         loss_tokens[i] = L > 1 ? count_positive(mask + a + 1, L - 1) : 0;
     }
     return MESHY_OK;
+}
+
+}  // namespace
+
+extern "C" int meshy_sample_loss_tokens(const float* mask, const int64_t* offsets, int64_t n,
+                                        int64_t seq_len, int64_t* lengths, int64_t* loss_tokens) {
+    meshy::clear_error();
+    return sample_loss_tokens("meshy_sample_loss_tokens", mask, offsets, n, seq_len, lengths, loss_tokens);
+}
+
+extern "C" int meshy_sample_loss_tokens_u8(const uint8_t* mask, const int64_t* offsets, int64_t n,
+                                           int64_t seq_len, int64_t* lengths, int64_t* loss_tokens) {
+    meshy::clear_error();
+    return sample_loss_tokens("meshy_sample_loss_tokens_u8", mask, offsets, n, seq_len, lengths, loss_tokens);
 }
 
 // GRPO advantages of host rewards: per group (offsets clamped to the rewards
@@ -447,7 +465,10 @@ extern "C" int meshy_step_plan(meshy_step_plan_args* args) {
                          static_cast<long long>(a.rank), static_cast<long long>(a.dp_size));
     if (!a.micro_seq_len || !a.micro_out_off || !a.micro_doc_start || !a.doc_sample || !a.doc_len)
         return set_error(MESHY_ENULL, "meshy_step_plan: every pack table is required");
-    int rc = meshy_sample_loss_tokens(a.mask, a.offsets, a.n, a.cfg.seq_len, a.lengths, a.loss_tokens);
+    int rc = a.mask_u8 ? sample_loss_tokens("meshy_step_plan", static_cast<const uint8_t*>(a.mask), a.offsets, a.n,
+                                            a.cfg.seq_len, a.lengths, a.loss_tokens)
+                       : sample_loss_tokens("meshy_step_plan", static_cast<const float*>(a.mask), a.offsets, a.n,
+                                            a.cfg.seq_len, a.lengths, a.loss_tokens);
     if (rc) return rc;
     rc = meshy_plan_build(a.lengths, a.loss_tokens, a.n, a.dp_size, &a.cfg, &a.plan);
     if (rc) return rc;

@@ -29,15 +29,19 @@ from .plan import Plan, PlannerConfig, PlanTables, tables_to_plan
 from .wire import jagged_parts
 
 
-_NP_DTYPES = {torch.int32: np.int32, torch.int64: np.int64, torch.float32: np.float32}
+_NP_DTYPES = {torch.int32: np.int32, torch.int64: np.int64, torch.float32: np.float32, torch.uint8: np.uint8}
 
 
 class RaggedSamples:
     """One step's samples as flat pinned host arrays, in global sample order."""
 
     def __init__(self, lengths: np.ndarray, n_groups: int, need_rollout_lp: bool,
-                 token_dtype: torch.dtype = torch.int32) -> None:
+                 token_dtype: torch.dtype = torch.int32, mask_u8: bool = False) -> None:
+        """``mask_u8`` stages the mask as one byte per token (for masks of only
+        0 and 1: a quarter of the mask's copy to the device, the same values
+        in the batches); the constructors below choose it when they can."""
         n = len(lengths)
+        self.mask_u8 = bool(mask_u8)
         self.n = n
         self.lengths = np.asarray(lengths, np.int64)
         self.offsets = np.zeros(n + 1, np.int64)
@@ -48,7 +52,7 @@ class RaggedSamples:
         if token_dtype not in (torch.int32, torch.int64):
             raise ValueError("token ids are staged as int32 or int64")
         lay.add("tokens", self.total, token_dtype)
-        lay.add("mask", self.total, torch.float32)
+        lay.add("mask", self.total, torch.uint8 if self.mask_u8 else torch.float32)
         if need_rollout_lp:
             lay.add("logprobs", self.total, torch.float32)
         lay.add("s_off", n + 1, torch.int64)
@@ -90,6 +94,7 @@ class RaggedSamples:
             base = self.buf.data_ptr()
             self._counts = np.empty((2, self.n), np.int64)
             a.mask = self.lay.addr(base, "mask")
+            a.mask_u8 = int(self.mask_u8)
             a.offsets = self.lay.addr(base, "s_off")
             a.n = self.n
             a.lengths = self._counts[0].ctypes.data
@@ -133,12 +138,34 @@ class RaggedSamples:
         return v
 
     @classmethod
+    def _with_mask(cls, make, parts) -> "RaggedSamples":
+        """``make(mask_u8)`` with its mask region filled from ``parts`` (the
+        samples' masks in order): as bytes when every part is a CPU contiguous
+        fp32 tensor holding only 0 and 1 (one native pass converts and
+        checks), else as fp32."""
+        if parts and all(isinstance(p, torch.Tensor) and p.device.type == "cpu" and p.dtype == torch.float32
+                         and p.is_contiguous() for p in parts):
+            r = make(True)
+            ptrs = np.array([p.data_ptr() for p in parts], np.uint64)
+            counts = np.array([p.numel() for p in parts], np.int64)
+            binary = _lib.ctypes.c_int32(0)
+            _lib.check(_lib.load().meshy_host_gather_mask_u8(ptrs.ctypes.data, counts.ctypes.data, len(parts),
+                                                             r.view("mask").data_ptr(), 0, _lib.ctypes.byref(binary)),
+                       "meshy_host_gather_mask_u8")
+            if binary.value:
+                return r
+        r = make(False)
+        gather_into(parts, r.view("mask"))
+        return r
+
+    @classmethod
     def from_arrays(cls, tokens, mask, logprobs, offsets, rewards, group_offsets) -> "RaggedSamples":
         """From flat numpy arrays (sample i = [offsets[i], offsets[i+1]))."""
         offsets = np.asarray(offsets, np.int64)
-        r = cls(np.diff(offsets), len(group_offsets) - 1, logprobs is not None)
+        m = torch.from_numpy(np.ascontiguousarray(mask, np.float32))
+        r = cls._with_mask(lambda u8: cls(np.diff(offsets), len(group_offsets) - 1, logprobs is not None,
+                                          mask_u8=u8), [m])
         r.view("tokens").copy_(torch.from_numpy(np.ascontiguousarray(tokens, np.int32)))
-        r.view("mask").copy_(torch.from_numpy(np.ascontiguousarray(mask, np.float32)))
         if logprobs is not None:
             r.view("logprobs").copy_(torch.from_numpy(np.ascontiguousarray(logprobs, np.float32)))
         r.view("rewards")[:r.n] = torch.from_numpy(np.ascontiguousarray(rewards, np.float32))
@@ -152,9 +179,10 @@ class RaggedSamples:
         lengths = np.array([t.shape[0] if isinstance(t, torch.Tensor) else len(t) for t in toks], np.int64)
         # int64 ids (the reference's dtype) are staged as they are, others as int32.
         tok64 = all(isinstance(t, torch.Tensor) and t.dtype == torch.int64 for t in toks)
-        r = cls(lengths, len(group_offsets) - 1, need_rollout_lp, torch.int64 if tok64 else torch.int32)
+        tdt = torch.int64 if tok64 else torch.int32
+        r = cls._with_mask(lambda u8: cls(lengths, len(group_offsets) - 1, need_rollout_lp, tdt, mask_u8=u8),
+                           [s["mask_assistant"] for s in samples])
         gather_into(toks, r.view("tokens"))
-        gather_into([s["mask_assistant"] for s in samples], r.view("mask"))
         if need_rollout_lp:
             gather_into([s["logprobs"] for s in samples], r.view("logprobs"))
         r.view("rewards")[:r.n] = torch.tensor([float(s["reward"]) for s in samples], dtype=torch.float32)
@@ -167,14 +195,18 @@ class RaggedSamples:
         jagged ``tokens`` / ``mask_assistant`` / ``logprobs`` columns are copied from
         their flat ``values()`` in one pass each, ``reward`` from its ``[B, 1]`` column."""
         tok, off = jagged_parts(columns["tokens"])
-        r = cls(torch.diff(off).numpy(), len(group_offsets) - 1, need_rollout_lp)
-        r.view("tokens").copy_(tok.reshape(-1).to(torch.int32))
-        names = ["mask_assistant"] + (["logprobs"] if need_rollout_lp else [])
-        for name, region in zip(names, ["mask", "logprobs"]):
+        flats = {}
+        for name in ["mask_assistant"] + (["logprobs"] if need_rollout_lp else []):
             flat, o = jagged_parts(columns[name])
             if not torch.equal(o.cpu(), off.cpu()):
                 raise ValueError(f"column {name!r} is not as long as 'tokens' in every sample")
-            r.view(region).copy_(flat.reshape(-1).to(torch.float32))
+            flats[name] = flat.reshape(-1).to(device="cpu", dtype=torch.float32).contiguous()
+        lengths = torch.diff(off).numpy()
+        r = cls._with_mask(lambda u8: cls(lengths, len(group_offsets) - 1, need_rollout_lp, mask_u8=u8),
+                           [flats["mask_assistant"]])
+        r.view("tokens").copy_(tok.reshape(-1).to(torch.int32))
+        if need_rollout_lp:
+            r.view("logprobs").copy_(flats["logprobs"])
         r.view("rewards")[:r.n] = torch.as_tensor(columns["reward"]).reshape(-1).to(torch.float32)
         r.view("group_off").copy_(torch.as_tensor(np.asarray(group_offsets, np.int64)))
         return r
@@ -183,9 +215,10 @@ class RaggedSamples:
         """(token count, loss tokens) per sample, natively (trainer.py:577-588)."""
         lengths = np.empty(self.n, np.int64)
         loss = np.empty(self.n, np.int64)
-        rc = _lib.load().meshy_sample_loss_tokens(
-            self.view("mask").data_ptr(), self.offsets.ctypes.data, self.n, seq_len,
-            lengths.ctypes.data, loss.ctypes.data)
+        lib = _lib.load()
+        fn = lib.meshy_sample_loss_tokens_u8 if self.mask_u8 else lib.meshy_sample_loss_tokens
+        rc = fn(self.view("mask").data_ptr(), self.offsets.ctypes.data, self.n, seq_len,
+                lengths.ctypes.data, loss.ctypes.data)
         _lib.check(rc, "meshy_sample_loss_tokens")
         return lengths, loss
 
@@ -257,7 +290,7 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
         need_rollout_lp=ragged.need_rollout_lp, per_token_adv=False, n_samples=ragged.n, seq=seq,
         rows=np.ones(nm, np.int64) if packed else np.maximum(np.diff(start), 1), out_off=out_off, doc_start=start,
         max_elems=int(a.max_micro_elems), max_docs=int(a.max_docs_per_micro), adv_samples=adv,
-        broadcast_advantages=broadcast_advantages, stream=handle,
+        broadcast_advantages=broadcast_advantages, stream=handle, mask_u8=ragged.mask_u8,
     )
     batches = launch_pack(job)
     return PackResult(tables_to_plan(t) if with_plan_objects else None, t, batches, adv)

@@ -565,3 +565,35 @@ def test_one_pass_staging_equals_the_general_staging(dev, layout, tok_dtype, mon
                                        need_rollout_lp=True)
         _assert_same(mf, ref, layout)
         _assert_same(ms, ref, layout)
+
+
+@pytest.mark.parametrize("layout", ["packed", "padded"])
+def test_pack_step_byte_mask_equals_fp32_mask(dev, layout):
+    """0/1 masks staged as bytes and the same masks staged as fp32 give the
+    same batches, bit for bit; a fractional mask keeps fp32 staging and its
+    values reach the batches' masks unchanged."""
+    from meshy_amd import workloads
+    from meshy_amd.pipeline import RaggedSamples, pack_step
+    from meshy_amd.plan import PlannerConfig
+
+    batch, rewards, group_offsets = workloads.grpo_256_samples(1)
+    args = (batch.tokens, batch.mask, batch.logprobs, batch.offsets, rewards, group_offsets)
+    as_bytes = RaggedSamples.from_arrays(*args)
+    frac = batch.mask.copy()
+    frac[int(batch.offsets[3]) + 1] = 0.5  # the fractional value makes from_arrays stage fp32
+    as_fp32 = RaggedSamples.from_arrays(batch.tokens, frac, *args[2:])
+    assert as_bytes.mask_u8 and not as_fp32.mask_u8
+    budget = 8192 if layout == "packed" else 16384
+    cfg = PlannerConfig(layout=layout, mini_batch_size=256, seq_len=8192, align=64 if layout == "packed" else 1,
+                        max_tokens_per_micro=budget)
+    frac_res = pack_step(as_fp32, cfg, dev)
+    got = sum(int((mb.mask == 0.5).sum()) for mb in frac_res.batches)
+    assert got == 1
+    as_fp32.view("mask").copy_(torch.from_numpy(batch.mask))
+    a = pack_step(as_bytes, cfg, dev)
+    b = pack_step(as_fp32, cfg, dev)
+    assert len(a.batches) == len(b.batches)
+    for x, y in zip(a.batches, b.batches):
+        for k in ("input_ids", "labels", "positions", "mask", "doc_ids", "rollout_logprobs", "advantages",
+                  "lengths"):
+            assert torch.equal(getattr(x, k), getattr(y, k)), k

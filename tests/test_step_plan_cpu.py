@@ -98,3 +98,67 @@ def test_step_plan_refuses():
     assert b"rank" in lib.meshy_last_error()
     a.rank = 0
     assert lib.meshy_step_plan(ctypes.byref(a)) == -2  # no pack tables
+
+
+@pytest.mark.parametrize("seed", [0, 1])
+def test_byte_mask_counts_and_plan_equal_the_fp32_ones(seed):
+    """meshy_sample_loss_tokens_u8 over the mask as bytes gives the fp32 call's
+    counts, and meshy_step_plan gives the same plan and pack tables from
+    either staging of the mask."""
+    from meshy_amd.pipeline import RaggedSamples
+
+    rng = np.random.default_rng(seed)
+    n = 96
+    lengths = rng.integers(1, 3000, n).astype(np.int64)
+    offsets, mask = _stage(lengths, rng)
+    lib = _lib.load()
+    mb = mask.astype(np.uint8)
+    out = [np.empty((2, n), np.int64) for _ in range(2)]
+    assert lib.meshy_sample_loss_tokens(mask.ctypes.data, offsets.ctypes.data, n, 2048, out[0][0].ctypes.data,
+                                        out[0][1].ctypes.data) == 0
+    assert lib.meshy_sample_loss_tokens_u8(mb.ctypes.data, offsets.ctypes.data, n, 2048, out[1][0].ctypes.data,
+                                           out[1][1].ctypes.data) == 0
+    assert np.array_equal(out[0], out[1])
+    tokens = rng.integers(0, 151936, int(offsets[-1])).astype(np.int32)
+    lps = rng.standard_normal(int(offsets[-1])).astype(np.float32)
+    rewards = rng.random(n).astype(np.float32)
+    groups = np.arange(0, n + 1, 8, dtype=np.int64)
+    as_bytes = RaggedSamples.from_arrays(tokens, mask, lps, offsets, rewards, groups)
+    assert as_bytes.mask_u8
+    assert np.array_equal(as_bytes.view("mask").numpy(), mb)
+    frac = mask.copy()
+    frac[5] = 0.5
+    as_fp32 = RaggedSamples.from_arrays(tokens, frac, lps, offsets, rewards, groups)
+    assert not as_fp32.mask_u8
+    assert np.array_equal(as_fp32.view("mask").numpy(), frac)
+    frac[5] = mask[5]
+    as_fp32.view("mask").copy_(__import__("torch").from_numpy(frac))
+    cfg = PlannerConfig(layout="packed", mini_batch_size=32, seq_len=2048, align=64, max_tokens_per_micro=4096)
+    got = []
+    for r in (as_bytes, as_fp32):
+        assert np.array_equal(np.stack(r.sample_lengths(2048)), out[0])
+        t = PlanTables(n, 1, cfg.mini_batch_size)
+        a = r.step_plan_args(cfg, 1, 0, t)
+        assert lib.meshy_step_plan(ctypes.byref(a)) == 0
+        nm, nd = int(a.n_micro), int(a.n_docs)
+        got.append((int(a.plan.n_micro_total), r.np_view("seq")[:nm].copy(), r.np_view("doc_start")[:nm + 1].copy(),
+                    r.np_view("doc_sample")[:nd].copy(), r.np_view("doc_len")[:nd].copy(), t.local_indices.copy()))
+    for x, y in zip(*got):
+        assert np.array_equal(x, y)
+
+
+def test_columns_and_samples_pick_the_byte_mask_for_binary_masks():
+    import torch
+
+    from meshy_amd.pipeline import RaggedSamples
+
+    g = torch.Generator().manual_seed(3)
+    samples = [{"tokens": torch.randint(0, 1000, (L,), generator=g), "mask_assistant": (torch.rand(L, generator=g) > 0.5).float(),
+                "logprobs": torch.randn(L, generator=g), "reward": 1.0} for L in (5, 17, 300, 1)]
+    r = RaggedSamples.from_samples(samples, [0, 2, 4])
+    assert r.mask_u8
+    assert torch.equal(r.view("mask"), torch.cat([s["mask_assistant"] for s in samples]).to(torch.uint8))
+    samples[2]["mask_assistant"] = samples[2]["mask_assistant"].bool()  # not fp32: the fp32 staging
+    r = RaggedSamples.from_samples(samples, [0, 2, 4])
+    assert not r.mask_u8
+    assert torch.equal(r.view("mask"), torch.cat([s["mask_assistant"].float() for s in samples]))
