@@ -229,8 +229,8 @@ class PackJob:
     max_elems: int
     max_docs: int
     #: Device per-sample advantages indexed like ``doc_sample`` (overrides the
-    #: staged ``sample["advantage"]`` values).
-    adv_samples: torch.Tensor | None = None
+    #: staged ``sample["advantage"]`` values): a tensor or a device address.
+    adv_samples: torch.Tensor | int | None = None
     #: Also write ``Batch.advantage_tokens`` (per-document advantage per token).
     broadcast_advantages: bool = False
     #: Per-token advantages gathered on the device (indexed like the staged tokens).
@@ -523,8 +523,9 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
         a.adv_tokens = job.adv_tokens_dev.data_ptr()
     else:
         a.adv_tokens = lay.addr(base, "adv_tokens") if job.per_token_adv else None
-    a.adv_samples = (job.adv_samples.data_ptr() if job.adv_samples is not None
-                     else lay.addr(base, "adv_samples"))
+    src = job.adv_samples
+    a.adv_samples = (lay.addr(base, "adv_samples") if src is None
+                     else src if isinstance(src, int) else src.data_ptr())
     a.sample_offsets = lay.addr(base, "s_off")
     a.n_samples = job.n_samples
     a.n_micro = n_micro
@@ -601,14 +602,41 @@ class _PackViews:
         # weights stay in the staging buffer, where the host wrote them.
         self.obuf, self.out_lay = obuf, out_lay
         self.pos_w_src = (lay, dbuf)
-        self.out_off = job.out_off.tolist()
+        self._job = job
         self.doc_start = job.doc_start.tolist()
-        self.sizes = np.diff(job.out_off).tolist()
-        self.rows = job.rows.tolist()
-        self.seq = job.seq.tolist()
-        self.nd = np.diff(job.doc_start).tolist()
+        self.nd = [b - a for a, b in zip(self.doc_start, self.doc_start[1:])]
         self.micros = job.micros
         self._tok = self._doc = self._cu = self._seg = None
+
+    # The per-micro sizes the views read, as lists, made when a view first needs them.
+    @property
+    def out_off(self) -> list:
+        v = self.__dict__.get("_out_off")
+        if v is None:
+            v = self._out_off = self._job.out_off.tolist()
+        return v
+
+    @property
+    def sizes(self) -> list:
+        v = self.__dict__.get("_sizes")
+        if v is None:
+            o = self.out_off
+            v = self._sizes = [b - a for a, b in zip(o, o[1:])]
+        return v
+
+    @property
+    def rows(self) -> list:
+        v = self.__dict__.get("_rows")
+        if v is None:
+            v = self._rows = self._job.rows.tolist()
+        return v
+
+    @property
+    def seq(self) -> list:
+        v = self.__dict__.get("_seq")
+        if v is None:
+            v = self._seq = self._job.seq.tolist()
+        return v
 
     def _flat(self, name: str) -> torch.Tensor | None:
         """The whole-launch tensor of one output (None when not produced)."""

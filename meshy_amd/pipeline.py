@@ -228,11 +228,20 @@ class PackResult:
     flat tables the first time ``plan`` is read), the tables, one ``Batch`` per
     micro of the rank and the per-sample advantages on the device."""
 
-    def __init__(self, plan: Plan | None, tables, batches: list[Batch], advantages: torch.Tensor) -> None:
+    def __init__(self, plan: Plan | None, tables, batches: list[Batch], advantages) -> None:
         self._plan = plan
         self.tables = tables
         self.batches = batches
-        self.advantages = advantages
+        # A device tensor, or (buffer, layout, n): its view, made when first read.
+        self._adv = advantages
+
+    @property
+    def advantages(self) -> torch.Tensor:
+        adv = self._adv
+        if isinstance(adv, tuple):
+            buf, lay, n = adv
+            adv = self._adv = lay.view(buf, "adv_samples")[:n]
+        return adv
 
     @property
     def plan(self) -> Plan:
@@ -275,9 +284,9 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
     ragged.record_copy(device)
 
     base = dbuf.data_ptr()
-    adv = lay.view(dbuf, "adv_samples")[:ragged.n]
+    adv = lay.addr(base, "adv_samples")
     rc = lib.meshy_grpo_advantage(lay.addr(base, "rewards"), ragged.n, lay.addr(base, "group_off"), ragged.n_groups,
-                                  adv.data_ptr(), handle)
+                                  adv, handle)
     _lib.check(rc, "meshy_grpo_advantage")
 
     seq = ragged.np_view("seq")[:nm]
@@ -293,7 +302,7 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
         broadcast_advantages=broadcast_advantages, stream=handle, mask_u8=ragged.mask_u8,
     )
     batches = launch_pack(job)
-    return PackResult(tables_to_plan(t) if with_plan_objects else None, t, batches, adv)
+    return PackResult(tables_to_plan(t) if with_plan_objects else None, t, batches, (dbuf, lay, ragged.n))
 
 
 class _LiteMicros:

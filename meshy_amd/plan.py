@@ -140,24 +140,40 @@ class PlanTables:
         n_local = n // dp
         n_mini = -(-n_local // mini_batch_size)
         self.n, self.dp, self.n_local, self.n_mini = n, dp, n_local, n_mini
-        counts = (dp * n_local, n_mini, n_mini, n_mini, n_mini * dp, dp * n_local, dp * (n_local + 1),
-                  dp * n_local, dp * n_local)
-        offs, total = [], 0
-        for (_, _, size), c in zip(self._FIELDS, counts):
-            offs.append(total)
-            total += -(-c * size // 8) * 8
-        buf = np.zeros(max(total, 8), np.uint8)
-        self._base = buf.__array_interface__["data"][0]
-        self._offs = offs
-        d = self.__dict__
-        for (name, dtype, size), o, c in zip(self._FIELDS, offs, counts):
-            d[name] = buf[o:o + c * size].view(dtype)
+        shape = (n, dp, mini_batch_size)
+        layout = self._LAYOUTS.get(shape)
+        if layout is None:
+            counts = (dp * n_local, n_mini, n_mini, n_mini, n_mini * dp, dp * n_local, dp * (n_local + 1),
+                      dp * n_local, dp * n_local)
+            offs, total = [], 0
+            for (_, _, size), c in zip(self._FIELDS, counts):
+                offs.append(total)
+                total += -(-c * size // 8) * 8
+            layout = self._LAYOUTS[shape] = (offs, counts, max(total, 8))
+            if len(self._LAYOUTS) > 64:
+                self._LAYOUTS.pop(next(iter(self._LAYOUTS)))
+        self._offs, self._counts, total = layout
+        self._buf = np.zeros(total, np.uint8)
+        self._base = self._buf.__array_interface__["data"][0]
         self.n_micro_total = 0
 
     _FIELDS = (("local_indices", np.int32, 4), ("mini_n_micro", np.int32, 4), ("mini_n_docs_global", np.int64, 8),
                ("mini_n_tokens_global", np.int64, 8), ("mini_tokens_per_rank", np.int64, 8),
                ("micro_seq_len", np.int64, 8), ("micro_doc_start", np.int32, 4), ("doc_sample", np.int32, 4),
                ("doc_len", np.int64, 8))
+    _INDEX = {f[0]: i for i, f in enumerate(_FIELDS)}
+    # Field offsets per (n, dp, mini_batch_size): one step's shape repeats.
+    _LAYOUTS: dict = {}
+
+    def __getattr__(self, name: str):
+        # Each table is a numpy view of the buffer, made when first read.
+        i = PlanTables._INDEX.get(name)
+        if i is None:
+            raise AttributeError(name)
+        _, dtype, size = self._FIELDS[i]
+        o, c = self._offs[i], self._counts[i]
+        v = self.__dict__[name] = self._buf[o:o + c * size].view(dtype)
+        return v
 
     def c_struct(self) -> _lib.PlanOut:
         b = self._base
