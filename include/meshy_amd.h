@@ -38,6 +38,12 @@ extern "C" {
 const char* meshy_last_error(void);
 /* ABI version: bumped on any signature change. */
 int meshy_abi_version(void);
+/* An asynchronous host-to-device copy on `stream` (hipMemcpyAsync): the
+ * staging buffers' transfers, issued without a framework tensor per copy.
+ * From pinned memory it returns once queued; the caller keeps `src` intact
+ * until the copy has run.  No counterpart in the reference, which copies
+ * with torch's .to(device) (trainer.py:644-667, batch.py:126-178). */
+int meshy_copy_to_device(void* dst, const void* src, size_t bytes, hipStream_t stream);
 
 /* ------------------------------------------------------------------------
  * Token-budget planner (host).

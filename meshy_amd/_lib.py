@@ -255,6 +255,7 @@ class GaeAttachArgs(ctypes.Structure):
 SIGNATURES = {
     "meshy_last_error": (ctypes.c_char_p, []),
     "meshy_abi_version": (c_int, []),
+    "meshy_copy_to_device": (c_int, [c_void_p, c_void_p, c_size_t, c_void_p]),
     "meshy_plan_build": (
         c_int,
         [c_void_p, c_void_p, c_int64, c_int64, POINTER(PlannerCfg), POINTER(PlanOut)],
@@ -360,7 +361,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 12
+ABI_VERSION = 13
 
 _LIB: ctypes.CDLL | None = None
 

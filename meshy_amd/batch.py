@@ -13,7 +13,7 @@ reference's fields (batch.py:52-74) so the forward and the loss read it as is.
 from __future__ import annotations
 
 import weakref
-from dataclasses import dataclass
+from dataclasses import MISSING, dataclass, fields
 from typing import Any, NamedTuple, Sequence
 
 import numpy as np
@@ -239,11 +239,24 @@ class PackJob:
     teacher_k: int = 0
     #: The staged mask holds one byte per token (0 or 1) instead of fp32.
     mask_u8: bool = False
+
+    @classmethod
+    def fast(cls, **fields) -> "PackJob":
+        """A job built without the dataclass constructor (the per-step pack
+        builds one per call): the defaults, then ``fields``."""
+        job = object.__new__(cls)
+        d = job.__dict__
+        d.update(_PACK_JOB_DEFAULTS)
+        d.update(fields)
+        return job
     #: The HIP stream handle to launch on (None: the device's current stream).
     stream: int | None = None
     #: Per micro (ids, logprobs) Teacher columns in the micro's layout, filled by
     #: ``launch_pack`` when ``teacher_k`` > 0.
     teacher_views: list | None = None
+
+
+_PACK_JOB_DEFAULTS = {f.name: f.default for f in fields(PackJob) if f.default is not MISSING}
 
 
 def stage_micro_batches(

@@ -34,4 +34,14 @@ int check_launch(const char* what) {
 
 extern "C" const char* meshy_last_error(void) { return meshy::g_last_error; }
 
-extern "C" int meshy_abi_version(void) { return 12; }
+extern "C" int meshy_abi_version(void) { return 13; }
+
+extern "C" int meshy_copy_to_device(void* dst, const void* src, size_t bytes, hipStream_t stream) {
+    meshy::clear_error();
+    if (bytes == 0) return MESHY_OK;
+    if (!dst || !src) return meshy::set_error(MESHY_ENULL, "meshy_copy_to_device: NULL pointer");
+    const hipError_t e = hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, stream);
+    if (e != hipSuccess)
+        return meshy::set_error(static_cast<int>(e), "meshy_copy_to_device: %s", hipGetErrorString(e));
+    return MESHY_OK;
+}

@@ -77,6 +77,7 @@ class RaggedSamples:
         self._np: dict[str, np.ndarray] = {}
         self.copied = None  # event of the last copy of the plan tables out of buf
         self._step_args = None  # meshy_step_plan's struct over this buffer
+        self._cfg_key = None  # the settings last written into it
         self._stream = None  # (raw handle, torch Stream) of the last copy's stream
         self.view("s_off").copy_(torch.from_numpy(self.offsets))
         self.view("pos_w").zero_()
@@ -103,14 +104,20 @@ class RaggedSamples:
                                   ("micro_doc_start", "doc_start"), ("doc_sample", "doc_sample"),
                                   ("doc_len", "doc_len")):
                 setattr(a, field, self.lay.addr(base, region))
-        a.dp_size, a.rank = dp_size, rank
-        c = a.cfg
-        c.layout = _lib.MESHY_LAYOUT_PACKED if cfg.layout == "packed" else _lib.MESHY_LAYOUT_PADDED
-        c.mini_batch_size = cfg.mini_batch_size
-        c.seq_len = cfg.seq_len
-        c.align = cfg.align
-        c.max_tokens_per_micro = cfg.max_tokens_per_micro or 0
-        c.micro_batch_size = cfg.micro_batch_size or 0
+        # The planner settings are written when they change (a step's config
+        # repeats from step to step).
+        key = (dp_size, rank, cfg.layout, cfg.mini_batch_size, cfg.seq_len, cfg.align, cfg.max_tokens_per_micro,
+               cfg.micro_batch_size)
+        if key != self._cfg_key:
+            self._cfg_key = key
+            a.dp_size, a.rank = dp_size, rank
+            c = a.cfg
+            c.layout = _lib.MESHY_LAYOUT_PACKED if cfg.layout == "packed" else _lib.MESHY_LAYOUT_PADDED
+            c.mini_batch_size = cfg.mini_batch_size
+            c.seq_len = cfg.seq_len
+            c.align = cfg.align
+            c.max_tokens_per_micro = cfg.max_tokens_per_micro or 0
+            c.micro_batch_size = cfg.micro_batch_size or 0
         a.plan = tables.c_struct()
         return a
 
@@ -263,9 +270,14 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
     device = torch.device(device)
     handle = _lib.stream_of(device)
     lay = ragged.lay
+    lib = _lib.load()
     dbuf = torch.empty(lay.size, dtype=torch.uint8, device=device)
+    base = dbuf.data_ptr()
+    hbase = ragged.buf.data_ptr()
     cut = ragged.tables_at
-    dbuf[:cut].copy_(ragged.buf[:cut], non_blocking=True)
+    # Raw asynchronous copies from the pinned buffer, on the device's current
+    # stream; the buffer outlives them (ragged.copied marks the second).
+    _lib.check(lib.meshy_copy_to_device(base, hbase, cut, handle), "meshy_copy_to_device")
     if ragged.copied is not None:
         ragged.copied.synchronize()  # the tables below reuse the pinned buffer the last copy read
     if dp_size <= 0 or ragged.n % dp_size != 0:
@@ -275,15 +287,13 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
         )
     t = PlanTables(ragged.n, dp_size, cfg.mini_batch_size)
     a = ragged.step_plan_args(cfg, dp_size, rank, t)
-    lib = _lib.load()
     _lib.check(lib.meshy_step_plan(_lib.ctypes.byref(a)), "meshy_step_plan")
     t.n_micro_total = int(a.plan.n_micro_total)
     nm, nd_total = int(a.n_micro), int(a.n_docs)
 
-    dbuf[cut:].copy_(ragged.buf[cut:], non_blocking=True)
+    _lib.check(lib.meshy_copy_to_device(base + cut, hbase + cut, lay.size - cut, handle), "meshy_copy_to_device")
     ragged.record_copy(device)
 
-    base = dbuf.data_ptr()
     adv = lay.addr(base, "adv_samples")
     rc = lib.meshy_grpo_advantage(lay.addr(base, "rewards"), ragged.n, lay.addr(base, "group_off"), ragged.n_groups,
                                   adv, handle)
@@ -293,8 +303,8 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
     start = ragged.np_view("doc_start")[:nm + 1]
     out_off = ragged.np_view("out_off")[:nm + 1]
     packed = cfg.layout == "packed"
-    job = PackJob(
-        micros=_LiteMicros(seq.tolist(), start.tolist(), ragged.np_view("doc_len")[:nd_total].tolist()),
+    job = PackJob.fast(
+        micros=_LiteMicros(seq, start, ragged.np_view("doc_len")[:nd_total]),
         layout=cfg.layout, device=device, dbuf=dbuf, lay=lay,
         need_rollout_lp=ragged.need_rollout_lp, per_token_adv=False, n_samples=ragged.n, seq=seq,
         rows=np.ones(nm, np.int64) if packed else np.maximum(np.diff(start), 1), out_off=out_off, doc_start=start,
@@ -307,30 +317,36 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
 
 class _LiteMicros:
     """The micros of a step as ``launch_pack`` reads them, each made on first
-    use from the host lists of the plan (no dataclass per micro)."""
+    use from the plan's tables (numpy views, read as lists the first time a
+    micro is needed; no dataclass per micro)."""
 
-    __slots__ = ("seq", "start", "dlen", "_made")
+    __slots__ = ("_arrays", "_lists", "_n", "_made")
 
-    def __init__(self, seq: list, start: list, dlen: list) -> None:
-        self.seq, self.start, self.dlen = seq, start, dlen
+    def __init__(self, seq, start, dlen) -> None:
+        self._arrays = (seq, start, dlen)
+        self._lists = None
+        self._n = len(seq)
         self._made: dict = {}
 
     def __len__(self) -> int:
-        return len(self.seq)
+        return self._n
 
     def __getitem__(self, k: int) -> "_LiteMicro":
         m = self._made.get(k)
         if m is None:
-            if not -len(self.seq) <= k < len(self.seq):
+            if not -self._n <= k < self._n:
                 raise IndexError(k)
-            k %= len(self.seq)
-            a, b = self.start[k], self.start[k + 1]
-            dl = tuple(self.dlen[a:b])
-            m = self._made[k] = _LiteMicro(self.seq[k], b - a, sum(dl), dl)
+            k %= self._n
+            if self._lists is None:
+                self._lists = tuple(x.tolist() for x in self._arrays)
+            seq, start, dlen = self._lists
+            a, b = start[k], start[k + 1]
+            dl = tuple(dlen[a:b])
+            m = self._made[k] = _LiteMicro(seq[k], b - a, sum(dl), dl)
         return m
 
     def __iter__(self):
-        return (self[k] for k in range(len(self.seq)))
+        return (self[k] for k in range(self._n))
 
 
 class _LiteMicro:
