@@ -68,7 +68,8 @@ class RaggedSamples:
         lay.add("doc_len", max(n, 1), torch.int64)
         lay.add("doc_start", n + 1, torch.int32)
         lay.add("doc_sample", max(n, 1), torch.int32)
-        lay.add("adv_samples", max(n, 1), torch.float32)  # written on the device
+        self.adv_at = lay.size  # the second copy ends here
+        lay.add("adv_samples", max(n, 1), torch.float32)  # written on the device, last
         self.lay = lay
         self.n_groups = n_groups
         # Pinned when a device is present, so the one copy to it is a DMA.
@@ -261,8 +262,9 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
               with_plan_objects: bool = False, broadcast_advantages: bool = True) -> PackResult:
     """Plan, copy, normalise rewards and build every micro of ``rank``.
 
-    The samples' part of the staging buffer is copied to the device first, so
-    the transfer runs while the host plans.  One native call
+    The samples' part of the staging buffer is copied to the device first and
+    the GRPO kernel queued behind it, so both run while the host plans.  One
+    native call
     (``meshy_step_plan``) counts the loss tokens, plans and writes this rank's
     pack tables into the staging buffer; they follow in a second, small copy.
     The Plan dataclasses are built when ``PackResult.plan`` is first read
@@ -277,27 +279,29 @@ def pack_step(ragged: RaggedSamples, cfg: PlannerConfig, device, *, dp_size: int
     cut = ragged.tables_at
     # Raw asynchronous copies from the pinned buffer, on the device's current
     # stream; the buffer outlives them (ragged.copied marks the second).
-    _lib.check(lib.meshy_copy_to_device(base, hbase, cut, handle), "meshy_copy_to_device")
-    if ragged.copied is not None:
-        ragged.copied.synchronize()  # the tables below reuse the pinned buffer the last copy read
     if dp_size <= 0 or ragged.n % dp_size != 0:
         raise ValueError(
             f"batch size {ragged.n} is not divisible by DP size {dp_size}; adjust "
             "rollout.batch_size * group_size to a multiple of dp_replicate * dp_shard"
         )
+    _lib.check(lib.meshy_copy_to_device(base, hbase, cut, handle), "meshy_copy_to_device")
+    # GRPO reads only the rewards and group offsets of the first copy: it runs
+    # while the host plans.  Its output region lies past the plan tables, so
+    # the second copy stops short of it.
+    adv = lay.addr(base, "adv_samples")
+    rc = lib.meshy_grpo_advantage(lay.addr(base, "rewards"), ragged.n, lay.addr(base, "group_off"), ragged.n_groups,
+                                  adv, handle)
+    _lib.check(rc, "meshy_grpo_advantage")
+    if ragged.copied is not None:
+        ragged.copied.synchronize()  # the tables below reuse the pinned buffer the last copy read
     t = PlanTables(ragged.n, dp_size, cfg.mini_batch_size)
     a = ragged.step_plan_args(cfg, dp_size, rank, t)
     _lib.check(lib.meshy_step_plan(_lib.ctypes.byref(a)), "meshy_step_plan")
     t.n_micro_total = int(a.plan.n_micro_total)
     nm, nd_total = int(a.n_micro), int(a.n_docs)
 
-    _lib.check(lib.meshy_copy_to_device(base + cut, hbase + cut, lay.size - cut, handle), "meshy_copy_to_device")
+    _lib.check(lib.meshy_copy_to_device(base + cut, hbase + cut, ragged.adv_at - cut, handle), "meshy_copy_to_device")
     ragged.record_copy(device)
-
-    adv = lay.addr(base, "adv_samples")
-    rc = lib.meshy_grpo_advantage(lay.addr(base, "rewards"), ragged.n, lay.addr(base, "group_off"), ragged.n_groups,
-                                  adv, handle)
-    _lib.check(rc, "meshy_grpo_advantage")
 
     seq = ragged.np_view("seq")[:nm]
     start = ragged.np_view("doc_start")[:nm + 1]
