@@ -448,9 +448,12 @@ def _stage_common(samples, micros: tuple, layout: str, device: torch.device, nee
                    for i, (name, dtype) in enumerate(_COMMON_REGIONS) if bounds[2 * i] >= 0}
     handle = _lib.stream_of(device)
     dbuf = torch.empty(size, dtype=torch.uint8, device=device)
-    dbuf.copy_(host[:size], non_blocking=True)
+    # A raw asynchronous copy: the pinned buffer is reused only after the
+    # event stage.mark records has passed.
+    _lib.check(_lib.load().meshy_copy_to_device(dbuf.data_ptr(), host.data_ptr(), size, handle),
+               "meshy_copy_to_device")
     stage.mark(device, handle)
-    return PackJob(
+    return PackJob.fast(
         micros=micros, layout=layout, device=device, dbuf=dbuf, lay=lay, need_rollout_lp=need_rollout_lp,
         per_token_adv=False, n_samples=n_s, seq=np.frombuffer(seq_b, np.int64),
         rows=np.frombuffer(rows_b, np.int64), out_off=np.frombuffer(out_off_b, np.int64),
