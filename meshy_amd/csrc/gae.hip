@@ -86,13 +86,13 @@ __device__ __forceinline__ float apply_map(Aff f, float x) {
     return fmaf(f.p, x, f.q);
 }
 
-// Set (atomic max) by the chunks pass to the call's epoch when some chunk holds
-// a non-finite term (a NaN or infinite advantage or return term at a valid
-// position).  The apply pass then composes with hardness and folds its carry
-// up to the row's end instead of stopping at the first cut, which a non-finite
-// value crosses in the reference.  Epochs grow per call, so no clearing is
-// needed and calls on other streams can only send a call down the slower,
-// exact path.
+// Set (atomic max) by k_gae_scan to the call's epoch when some chunk holds a
+// non-finite term (a NaN or infinite advantage or return term at a valid
+// position) or a wait for a neighbour's map was given up.  k_gae_fix then
+// redoes the call, composing with hardness and folding each carry up to the
+// row's end instead of stopping at the first cut, which a non-finite value
+// crosses in the reference.  Epochs grow per call, so no clearing is needed
+// and calls on other streams can only send a call down the slower, exact path.
 __device__ unsigned long long g_gae_nonfinite_epoch = 0;
 
 struct Pair {
