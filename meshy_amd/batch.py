@@ -784,12 +784,21 @@ class PackedBatch(Batch):
     (trainer.py:557-571).  Once made, fields are plain attributes."""
 
 
-for _name, _group in (("input_ids", "tokens"), ("labels", "tokens"), ("positions", "tokens"), ("mask", "tokens"),
-                      ("doc_ids", "tokens"), ("rollout_logprobs", "tokens"), ("advantage_tokens", "tokens"),
-                      ("advantages", "doc_fields"), ("lengths", "doc_fields"),
-                      ("positive_lm_weights", "doc_fields"), ("attention_masks", "attention")):
-    setattr(PackedBatch, _name, _Lazy(_name, _group))
-del _name, _group
+# Each lazy field and the view group that makes it.
+_LAZY_FIELDS = (("input_ids", "tokens"), ("labels", "tokens"), ("positions", "tokens"), ("mask", "tokens"),
+                ("doc_ids", "tokens"), ("rollout_logprobs", "tokens"), ("advantage_tokens", "tokens"),
+                ("advantages", "doc_fields"), ("lengths", "doc_fields"),
+                ("positive_lm_weights", "doc_fields"), ("attention_masks", "attention"))
+
+
+def make_lazy(cls: type) -> type:
+    """Gives ``cls`` (a Batch subclass) the lazy pack-view fields of PackedBatch."""
+    for name, group in _LAZY_FIELDS:
+        setattr(cls, name, _Lazy(name, group))
+    return cls
+
+
+make_lazy(PackedBatch)
 
 
 def build_micro_batches(

@@ -17,19 +17,18 @@ the distillation loss with its metrics.
 
 from __future__ import annotations
 
-from dataclasses import dataclass, fields
+from dataclasses import dataclass
 from typing import Any, Sequence
 
 import torch
 import torch.distributed as dist
 
 from . import _lib
-from .batch import TEACHER_FIELDS, Batch, launch_pack, stage_micro_batches
+from .batch import TEACHER_FIELDS, Batch, launch_pack, make_lazy, stage_micro_batches
 from .loss import UnsortedDocIdsError, batch_cached, batch_segment_offsets, doc_ordered, tensor_key
 from .plan import Layout, MicroPlan
 from .topk import gather_logprobs
 
-_BATCH_FIELDS = tuple(f.name for f in fields(Batch))
 
 OPD_TEACHER_FIELDS = list(TEACHER_FIELDS)
 
@@ -51,6 +50,15 @@ class TopKBatch(Batch):
     teacher_topk_logprobs: torch.Tensor | None = None  # [rows, S_local, K] float
 
 
+class PackedTopKBatch(TopKBatch):
+    """A :class:`TopKBatch` over one micro of a pack launch: the Teacher
+    columns are set, and the :class:`Batch` fields are views of the launch's
+    outputs made on first read, as :class:`~meshy_amd.batch.PackedBatch`'s."""
+
+
+make_lazy(PackedTopKBatch)
+
+
 def build_topk_micro_batches(
     samples: Sequence[Any],
     micros: Sequence[MicroPlan],
@@ -67,6 +75,7 @@ def build_topk_micro_batches(
                               teacher=any(m.sample_idx for m in micros))
     batches = launch_pack(job, sharder)
     out = []
+    new = object.__new__
     for k, mb in enumerate(batches):
         if job.teacher_views is not None:
             ids, lps = job.teacher_views[k]
@@ -75,11 +84,10 @@ def build_topk_micro_batches(
             shape = (m.n_rows, m.seq_len, 1) if layout == "padded" else (1, m.seq_len, 1)
             ids = torch.zeros(shape, dtype=torch.int64, device=job.device)
             lps = torch.zeros(shape, dtype=torch.float32, device=job.device)
-        kw = {f: getattr(mb, f) for f in _BATCH_FIELDS}
-        tb = TopKBatch(**kw, teacher_topk_ids=ids, teacher_topk_logprobs=lps)
-        src = getattr(mb, "_meshy_seg_src", None)  # the pack's document offsets (same doc_ids)
-        if src is not None:
-            tb._meshy_seg_src = src
+        # The same lazy views as the pack's batch (its micro of the launch's
+        # outputs), plus the Teacher columns.
+        tb = new(PackedTopKBatch)
+        tb.__dict__ = {**mb.__dict__, "teacher_topk_ids": ids, "teacher_topk_logprobs": lps}
         out.append(tb)
     return out
 
@@ -228,6 +236,7 @@ def reduce_distill_metrics(self: Any, sums: dict[str, torch.Tensor]) -> dict[str
 
 __all__ = [
     "OPD_TEACHER_FIELDS",
+    "PackedTopKBatch",
     "TopKBatch",
     "build_topk_micro_batches",
     "distill_from_gathered",
