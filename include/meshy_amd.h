@@ -120,6 +120,13 @@ int meshy_host_gather(const void* const* srcs, const int64_t* nbytes, int64_t n,
  * the bytes the critic path copies to the device (trainer.py:644-667). */
 int meshy_host_gather_mask_u8(const float* const* srcs, const int64_t* counts, int64_t n, uint8_t* dst,
                               int max_threads, int32_t* binary);
+/* The same for int64 columns narrowed to int32 (host): counts[i] int64s of
+ * srcs[i] land in dst as int32, and *fits is set to 1 when every value fits
+ * in int32, else to 0 (dst then is not the column: stage the int64s).  The
+ * OPD Teacher's top-k ids are vocabulary indices (opd.py:58-89), so this
+ * halves the bytes their staging copies to the device. */
+int meshy_host_gather_i32(const int64_t* const* srcs, const int64_t* counts, int64_t n, int32_t* dst,
+                          int max_threads, int32_t* fits);
 
 /* Per-sample planner inputs from a flat host mask (host).
  * Replaces TitanTrainer._sample_lengths (meshy/backend/titan/trainer.py:577-588):

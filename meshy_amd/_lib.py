@@ -265,6 +265,7 @@ SIGNATURES = {
     "meshy_step_plan": (c_int, [POINTER(StepPlanArgs)]),
     "meshy_host_gather": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int]),
     "meshy_host_gather_mask_u8": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int, POINTER(c_int32)]),
+    "meshy_host_gather_i32": (c_int, [c_void_p, c_void_p, c_int64, c_void_p, c_int, POINTER(c_int32)]),
     "meshy_pack_micro_batches": (c_int, [POINTER(PackArgs), c_void_p]),
     "meshy_grpo_advantage": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_void_p, c_void_p]),
     "meshy_zero_variance_groups": (c_int, [c_void_p, c_int64, c_void_p, c_int64, c_double, c_void_p, c_void_p]),
@@ -361,7 +362,7 @@ SIGNATURES = {
     ),
 }
 
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 _LIB: ctypes.CDLL | None = None
 

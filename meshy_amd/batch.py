@@ -281,10 +281,9 @@ def stage_micro_batches(
         raise ValueError("meshy_amd builds micro-batches on a HIP device; pass a cuda device")
 
     micros = tuple(micros)
-    if not teacher:
-        job = _stage_common(samples, micros, layout, device, need_rollout_lp)
-        if job is not None:
-            return job
+    job = _stage_common(samples, micros, layout, device, need_rollout_lp, teacher)
+    if job is not None:
+        return job
 
     # Samples used by these micros, remapped to a compact list in order of
     # first use, with the longest prefix any micro reads of each, and the
@@ -316,8 +315,6 @@ def stage_micro_batches(
     s_off = np.zeros(n_s + 1, np.int64)
     np.cumsum(need_len, out=s_off[1:])
     total = int(s_off[-1])
-    teacher_k, teacher_ids64, teacher_recs = (_teacher_width(samples, used, used_b, need_len) if teacher
-                                              else (0, False, (None, None)))
 
     # Plan tables.
     n_micro = len(micros)
@@ -367,24 +364,17 @@ def stage_micro_batches(
     lay.add("doc_start", n_micro + 1, torch.int32)
     lay.add("doc_sample", max(n_docs_total, 1), torch.int32)
     lay.add("pos_w", max(n_docs_total, 1), torch.float32)
-    if teacher_k:
-        # int64 ids (the Teacher's dtype) are staged as they are.
-        lay.add("teacher_ids", total * teacher_k, torch.int64 if teacher_ids64 else torch.int32)
-        lay.add("teacher_lps", total * teacher_k, torch.float32)
+    base_size = lay.size
+    tea = _TeacherStaging(samples, used, used_b, need_len, lay) if teacher and n_s else None
 
     stage = _STAGING.setdefault(device.index or 0, _Staging())
-    host = stage.get(lay.size)
+    host = stage.get(tea.reserve if tea else lay.size)
     if n_s:
         # the first need_len[i] positions of each sample's columns
         _gather_column(samples, used, used_b, need_len, "tokens", lay.view(host, "tokens"), recs=tok_recs)
         _gather_column(samples, used, used_b, need_len, "mask_assistant", lay.view(host, "mask"))
         if need_rollout_lp:
             _gather_column(samples, used, used_b, need_len, "logprobs", lay.view(host, "logprobs"))
-        if teacher_k:
-            _gather_column(samples, used, used_b, need_len, TEACHER_FIELDS[0], lay.view(host, "teacher_ids"),
-                           row=teacher_k, recs=teacher_recs[0])
-            _gather_column(samples, used, used_b, need_len, TEACHER_FIELDS[1], lay.view(host, "teacher_lps"),
-                           row=teacher_k, recs=teacher_recs[1])
         if per_token_adv and adv_dev is None:
             parts = []
             for i, L in zip(used.tolist(), need_len.tolist()):
@@ -405,14 +395,17 @@ def stage_micro_batches(
         lay.np_view(hnp, "pos_w")[:n_docs_total] = pos_w
 
     handle = _lib.stream_of(device)
-    dbuf = torch.empty(lay.size, dtype=torch.uint8, device=device)
-    dbuf.copy_(host[:lay.size], non_blocking=True)
+    dbuf = torch.empty(tea.reserve if tea else lay.size, dtype=torch.uint8, device=device)
+    _copy_to_device(dbuf, host, 0, base_size, handle)
+    if tea:
+        tea.stage(lay, host, dbuf, handle)
     stage.mark(device, handle)
     return PackJob(
         micros=tuple(micros), layout=layout, device=device, dbuf=dbuf, lay=lay,
         need_rollout_lp=need_rollout_lp, per_token_adv=per_token_adv, n_samples=n_s, seq=seq, rows=rows,
         out_off=out_off, doc_start=doc_start, max_elems=int(elems.max()) if n_micro else 0,
-        max_docs=int(n_docs.max()) if n_micro else 0, adv_tokens_dev=adv_dev, teacher_k=teacher_k, stream=handle,
+        max_docs=int(n_docs.max()) if n_micro else 0, adv_tokens_dev=adv_dev, teacher_k=tea.k if tea else 0,
+        stream=handle,
     )
 
 
@@ -424,11 +417,13 @@ _COMMON_REGIONS = (("tokens", None), ("mask", torch.float32), ("logprobs", torch
                    ("doc_sample", torch.int32), ("pos_w", torch.float32))
 
 
-def _stage_common(samples, micros: tuple, layout: str, device: torch.device, need_rollout_lp: bool) -> PackJob | None:
+def _stage_common(samples, micros: tuple, layout: str, device: torch.device, need_rollout_lp: bool,
+                  teacher: bool = False) -> PackJob | None:
     """``stage_micro_batches`` in one native pass when every used sample's
     tokens (all int64 or all int32), mask and log-probs are CPU contiguous
     tensors and none has per-token advantages; None otherwise (nothing
-    staged), and the general path runs."""
+    staged), and the general path runs.  Teacher columns follow in chunks
+    (_TeacherStaging)."""
     stage = _STAGING.setdefault(device.index or 0, _Staging())
     host = stage.get(0)  # waits for the buffer's previous copy
     st = _lib.stage()
@@ -439,26 +434,102 @@ def _stage_common(samples, micros: tuple, layout: str, device: torch.device, nee
         res = st.stage_micros(samples, micros, packed, need_rollout_lp, host.data_ptr(), host.numel(), _gather_fn())
     if res is None:
         return None
-    size, bounds_b, n_s, _total, tok64, _nd, max_elems, max_docs, seq_b, rows_b, out_off_b, doc_start_b = res
+    (size, bounds_b, n_s, _total, tok64, _nd, max_elems, max_docs, seq_b, rows_b, out_off_b, doc_start_b,
+     used_b, need_b) = res
     bounds = np.frombuffer(bounds_b, np.int64).tolist()
     lay = _Layout()
     lay.size = size
     tok_dtype = torch.int64 if tok64 else torch.int32
     lay.regions = {name: (bounds[2 * i], bounds[2 * i + 1], dtype or tok_dtype)
                    for i, (name, dtype) in enumerate(_COMMON_REGIONS) if bounds[2 * i] >= 0}
+    tea = None
+    if teacher and n_s:
+        tea = _TeacherStaging(samples, np.frombuffer(used_b, np.int64), used_b, np.frombuffer(need_b, np.int64), lay)
+        if host.numel() < tea.reserve:  # room for the Teacher columns: grow the buffer and stage again
+            host = stage.get(tea.reserve)
+            res = st.stage_micros(samples, micros, packed, need_rollout_lp, host.data_ptr(), host.numel(),
+                                  _gather_fn())
+            if res is None or isinstance(res, int) or res[0] != size:
+                raise RuntimeError("stage_micros: the staging changed between two calls on the same samples")
     handle = _lib.stream_of(device)
-    dbuf = torch.empty(size, dtype=torch.uint8, device=device)
-    # A raw asynchronous copy: the pinned buffer is reused only after the
+    dbuf = torch.empty(tea.reserve if tea else size, dtype=torch.uint8, device=device)
+    # Raw asynchronous copies: the pinned buffer is reused only after the
     # event stage.mark records has passed.
-    _lib.check(_lib.load().meshy_copy_to_device(dbuf.data_ptr(), host.data_ptr(), size, handle),
-               "meshy_copy_to_device")
+    _copy_to_device(dbuf, host, 0, size, handle)
+    if tea:
+        tea.stage(lay, host, dbuf, handle)
     stage.mark(device, handle)
     return PackJob.fast(
         micros=micros, layout=layout, device=device, dbuf=dbuf, lay=lay, need_rollout_lp=need_rollout_lp,
         per_token_adv=False, n_samples=n_s, seq=np.frombuffer(seq_b, np.int64),
         rows=np.frombuffer(rows_b, np.int64), out_off=np.frombuffer(out_off_b, np.int64),
-        doc_start=np.frombuffer(doc_start_b, np.int32), max_elems=max_elems, max_docs=max_docs, stream=handle,
+        doc_start=np.frombuffer(doc_start_b, np.int32), max_elems=max_elems, max_docs=max_docs,
+        teacher_k=tea.k if tea else 0, stream=handle,
     )
+
+
+def _copy_to_device(dbuf: torch.Tensor, host: torch.Tensor, lo: int, hi: int, handle: int) -> None:
+    """Bytes [lo, hi) of the pinned buffer to the same offsets of ``dbuf``,
+    asynchronously on the stream whose raw handle is ``handle``."""
+    if hi > lo:
+        _lib.check(_lib.load().meshy_copy_to_device(dbuf.data_ptr() + lo, host.data_ptr() + lo, hi - lo, handle),
+                   "meshy_copy_to_device")
+
+
+class _TeacherStaging:
+    """The OPD Teacher columns (``teacher_topk_logprobs``, then
+    ``teacher_topk_ids``, ``[L, K]`` each) as the last two staging regions.
+
+    They are most of the bytes a distillation step stages.  Each is copied as
+    soon as it is gathered, so the copy of the regions before it runs while it
+    is gathered (a queued host-to-device copy holds the host's next one until
+    it has run, so a few large copies overlap the gathers better than many
+    small ones).  int64 ids in CPU tensors (the Teacher's dtype) are narrowed
+    to int32 as they are gathered, which checks that each fits and halves
+    their bytes; the ids' region has room for int64s and holds them when one
+    does not fit."""
+
+    def __init__(self, samples, used: np.ndarray, used_b: bytes, need_len: np.ndarray, lay: _Layout) -> None:
+        self.samples, self.used, self.used_b, self.need = samples, used, used_b, need_len
+        self.k, ids64, self.recs = _teacher_width(samples, used, used_b, need_len)
+        self.total = total = int(need_len.sum())
+        self.narrow = bool(self.k and ids64 and self.recs[0] is not None
+                           and (self.recs[0]["flags"] == _CPU_CONTIGUOUS_TENSOR).all())
+        self.reserve = lay.size
+        if not self.k:
+            return
+        lay.add("teacher_lps", total * self.k, torch.float32)
+        lay.add("teacher_ids", total * self.k, torch.int64 if ids64 and not self.narrow else torch.int32)
+        self.reserve = lay.size + (total * self.k * 4 + 256 if self.narrow else 0)
+
+    def stage(self, lay: _Layout, host: torch.Tensor, dbuf: torch.Tensor, handle: int) -> None:
+        """Gather into ``host`` and copy to ``dbuf`` on the stream ``handle``."""
+        if not self.k:
+            return
+        k = self.k
+        _gather_column(self.samples, self.used, self.used_b, self.need, TEACHER_FIELDS[1],
+                       lay.view(host, "teacher_lps"), row=k, recs=self.recs[1])
+        ids_lo = lay.regions["teacher_ids"][0]
+        _copy_to_device(dbuf, host, lay.regions["teacher_lps"][0], ids_lo, handle)
+        if not (self.narrow and _gather_ids_i32(self.recs[0], self.need * k, lay.view(host, "teacher_ids"))):
+            if self.narrow:  # an id outside int32: the region holds the int64s
+                lay.size = lay.regions.pop("teacher_ids")[0]
+                lay.add("teacher_ids", self.total * k, torch.int64)
+            _gather_column(self.samples, self.used, self.used_b, self.need, TEACHER_FIELDS[0],
+                           lay.view(host, "teacher_ids"), row=k, recs=self.recs[0])
+        _copy_to_device(dbuf, host, ids_lo, lay.size, handle)
+
+
+def _gather_ids_i32(recs: np.ndarray, counts: np.ndarray, out: torch.Tensor) -> bool:
+    """The first ``counts[j]`` int64s of each column ``recs`` describes, as
+    int32 into ``out``; False (``out`` then undefined) when a value does not
+    fit."""
+    fits = _lib.ctypes.c_int32(0)
+    ptrs = np.ascontiguousarray(recs["ptr"])
+    counts = np.ascontiguousarray(counts, np.int64)
+    _lib.check(_lib.load().meshy_host_gather_i32(ptrs.ctypes.data, counts.ctypes.data, len(recs), out.data_ptr(), 0,
+                                                 _lib.ctypes.byref(fits)), "meshy_host_gather_i32")
+    return bool(fits.value)
 
 
 def _teacher_width(samples, used, used_b, need_len) -> tuple[int, bool, tuple]:

@@ -34,7 +34,7 @@ int check_launch(const char* what) {
 
 extern "C" const char* meshy_last_error(void) { return meshy::g_last_error; }
 
-extern "C" int meshy_abi_version(void) { return 13; }
+extern "C" int meshy_abi_version(void) { return 14; }
 
 extern "C" int meshy_copy_to_device(void* dst, const void* src, size_t bytes, hipStream_t stream) {
     meshy::clear_error();

@@ -37,9 +37,22 @@ struct Job {
     char* dst = nullptr;
     int64_t total = 0;
     int workers = 0;
-    bool to_u8 = false;
+    bool to_u8 = false;   // fp32 pieces -> one byte each (nbytes[i] counts floats)
+    bool to_i32 = false;  // int64 pieces -> int32 each (nbytes[i] counts int64s)
     mutable std::atomic<bool> nonbinary{false};  // a float other than +0.0 and 1.0 was seen
+    mutable std::atomic<bool> overflow{false};   // an int64 outside int32 was seen
 };
+
+// int64 to int32; false when some value does not fit.
+bool narrow_to_i32(const int64_t* src, int64_t count, int32_t* dst) {
+    uint64_t bad = 0;
+    for (int64_t k = 0; k < count; ++k) {
+        const int64_t v = src[k];
+        bad |= static_cast<uint64_t>(v != static_cast<int64_t>(static_cast<int32_t>(v)));
+        dst[k] = static_cast<int32_t>(v);
+    }
+    return bad == 0;
+}
 
 // Floats to bytes; false when some float is not exactly +0.0 or 1.0.
 bool mask_to_u8(const float* src, int64_t count, uint8_t* dst) {
@@ -60,7 +73,7 @@ void copy_share(const Job& j, int w) {
     if (lo >= hi) return;
     // First piece overlapping [lo, hi).
     int64_t i = std::upper_bound(j.start, j.start + j.n + 1, lo) - j.start - 1;
-    bool binary = true;
+    bool binary = true, fits = true;
     for (; i < j.n && j.start[i] < hi; ++i) {
         const int64_t a = std::max(lo, j.start[i]);
         const int64_t b = std::min(hi, j.start[i] + j.nbytes[i]);
@@ -68,10 +81,14 @@ void copy_share(const Job& j, int w) {
         if (j.to_u8)
             binary &= mask_to_u8(static_cast<const float*>(j.srcs[i]) + (a - j.start[i]), b - a,
                                  reinterpret_cast<uint8_t*>(j.dst) + a);
+        else if (j.to_i32)
+            fits &= narrow_to_i32(static_cast<const int64_t*>(j.srcs[i]) + (a - j.start[i]), b - a,
+                                  reinterpret_cast<int32_t*>(j.dst) + a);
         else
             std::memcpy(j.dst + a, static_cast<const char*>(j.srcs[i]) + (a - j.start[i]), b - a);
     }
     if (!binary) j.nonbinary.store(true, std::memory_order_relaxed);
+    if (!fits) j.overflow.store(true, std::memory_order_relaxed);
 }
 
 // Workers sleep on a condition variable between jobs; the calling thread takes
@@ -153,9 +170,12 @@ namespace {
 // Both gathers: sizes checked, then the job split over the pool.  `unit` is
 // the bytes read per output byte (1 for a copy, 4 for fp32 -> byte), which
 // sets how many workers the job is worth.
+// mode: 0 copies bytes, 1 converts fp32 masks to bytes, 2 narrows int64 to
+// int32 (sizes then count elements).  `ok` reports the conversion's check.
 int run_gather(const char* who, const void* const* srcs, const int64_t* sizes, int64_t n, void* dst,
-               int max_threads, bool to_u8, bool& binary) {
-    binary = true;
+               int max_threads, int mode, bool& ok) {
+    const bool to_u8 = mode == 1;
+    ok = true;
     if (n < 0) return set_error(MESHY_EINVAL, "%s: negative count", who);
     if (n == 0) return MESHY_OK;
     if (!srcs || !sizes || !dst) return set_error(MESHY_ENULL, "%s: NULL pointer", who);
@@ -176,8 +196,9 @@ int run_gather(const char* who, const void* const* srcs, const int64_t* sizes, i
     job.dst = static_cast<char*>(dst);
     job.total = start[n];
     job.to_u8 = to_u8;
+    job.to_i32 = mode == 2;
     Pool& pool = Pool::get();
-    const int64_t want = std::max<int64_t>(1, job.total * (to_u8 ? 4 : 1) / kBytesPerWorker);
+    const int64_t want = std::max<int64_t>(1, job.total * (mode == 0 ? 1 : mode == 1 ? 4 : 8) / kBytesPerWorker);
     const int cap = max_threads > 0 ? std::min(max_threads, pool.size()) : pool.size();
     job.workers = static_cast<int>(std::min<int64_t>(want, cap));
     if (job.workers <= 1) {
@@ -186,7 +207,7 @@ int run_gather(const char* who, const void* const* srcs, const int64_t* sizes, i
     } else {
         pool.run(job);
     }
-    binary = !job.nonbinary.load(std::memory_order_relaxed);
+    ok = !job.nonbinary.load(std::memory_order_relaxed) && !job.overflow.load(std::memory_order_relaxed);
     return MESHY_OK;
 }
 
@@ -196,8 +217,8 @@ int run_gather(const char* who, const void* const* srcs, const int64_t* sizes, i
 extern "C" int meshy_host_gather(const void* const* srcs, const int64_t* nbytes, int64_t n, void* dst,
                                  int max_threads) {
     meshy::clear_error();
-    bool binary;
-    return meshy::run_gather("meshy_host_gather", srcs, nbytes, n, dst, max_threads, false, binary);
+    bool ok;
+    return meshy::run_gather("meshy_host_gather", srcs, nbytes, n, dst, max_threads, 0, ok);
 }
 
 extern "C" int meshy_host_gather_mask_u8(const float* const* srcs, const int64_t* counts, int64_t n, uint8_t* dst,
@@ -206,7 +227,18 @@ extern "C" int meshy_host_gather_mask_u8(const float* const* srcs, const int64_t
     if (!binary) return meshy::set_error(MESHY_ENULL, "meshy_host_gather_mask_u8: binary is NULL");
     bool ok;
     const int rc = meshy::run_gather("meshy_host_gather_mask_u8", reinterpret_cast<const void* const*>(srcs), counts,
-                                     n, dst, max_threads, true, ok);
+                                     n, dst, max_threads, 1, ok);
     *binary = rc == MESHY_OK && ok ? 1 : 0;
+    return rc;
+}
+
+extern "C" int meshy_host_gather_i32(const int64_t* const* srcs, const int64_t* counts, int64_t n, int32_t* dst,
+                                     int max_threads, int32_t* fits) {
+    meshy::clear_error();
+    if (!fits) return meshy::set_error(MESHY_ENULL, "meshy_host_gather_i32: fits is NULL");
+    bool ok;
+    const int rc = meshy::run_gather("meshy_host_gather_i32", reinterpret_cast<const void* const*>(srcs), counts, n,
+                                     dst, max_threads, 2, ok);
+    *fits = rc == MESHY_OK && ok ? 1 : 0;
     return rc;
 }

@@ -44,9 +44,11 @@
 //       seq_len (the Python path handles and reports it), the byte size
 //       needed when capacity is smaller (nothing written), else
 //       (size, bounds, n_used, total, tokens_int64, n_docs_total, max_elems,
-//       max_docs, seq, rows, out_off, doc_start) with bounds the regions'
-//       [start, end) byte offsets in that order as int64 pairs (-1 for an
-//       absent region) and the four tables as bytes.
+//       max_docs, seq, rows, out_off, doc_start, used, need) with bounds the
+//       regions' [start, end) byte offsets in that order as int64 pairs (-1
+//       for an absent region), the four tables as bytes, and the compact
+//       sample map with each used sample's prefix length as plan_tables
+//       gives them.
 #include <Python.h>
 
 #include <torch/csrc/autograd/python_variable.h>
@@ -637,10 +639,11 @@ PyObject* stage_micros(PyObject*, PyObject* args) {
         off_v[2 * r] = offs[r];
         off_v[2 * r + 1] = offs[r] + sizes[r];
     }
-    return Py_BuildValue("(LNLLiLLLNNNN)", static_cast<long long>(size), to_bytes(off_v), static_cast<long long>(n_s),
-                         static_cast<long long>(total), tok64, static_cast<long long>(nd_total),
-                         static_cast<long long>(max_elems), static_cast<long long>(max_docs), to_bytes(seq),
-                         to_bytes(rows), to_bytes(out_off), to_bytes(doc_start));
+    return Py_BuildValue("(LNLLiLLLNNNNNN)", static_cast<long long>(size), to_bytes(off_v),
+                         static_cast<long long>(n_s), static_cast<long long>(total), tok64,
+                         static_cast<long long>(nd_total), static_cast<long long>(max_elems),
+                         static_cast<long long>(max_docs), to_bytes(seq), to_bytes(rows), to_bytes(out_off),
+                         to_bytes(doc_start), to_bytes(used), to_bytes(need));
 }
 
 PyMethodDef kMethods[] = {

@@ -170,3 +170,52 @@ def test_mask_u8_gather_errors():
     binary.value = -1
     assert lib.meshy_host_gather_mask_u8(None, None, 0, None, 0, ctypes.byref(binary)) == 0
     assert binary.value == 1
+
+
+def _ids_i32(parts, threads=0):
+    lib = _lib.load()
+    ptrs = (ctypes.c_void_p * max(1, len(parts)))(*[p.data_ptr() for p in parts])
+    counts = (ctypes.c_int64 * max(1, len(parts)))(*[p.numel() for p in parts])
+    out = torch.full((sum(p.numel() for p in parts),), 7, dtype=torch.int32)
+    fits = ctypes.c_int32(-1)
+    rc = lib.meshy_host_gather_i32(ptrs, counts, len(parts), out.data_ptr(), threads, ctypes.byref(fits))
+    return rc, fits.value, out
+
+
+@pytest.mark.parametrize("n,hi", [(1, 10), (9, 3), (300, 5000), (64, 300_000)])
+def test_i32_gather_of_ids_that_fit(n, hi):
+    """int64 ids within int32 (both ends included) come out as the same values,
+    on every thread count."""
+    g = torch.Generator().manual_seed(n)
+    parts = [torch.randint(-(2**31), 2**31, (int(s),), generator=g) for s in torch.randint(0, hi, (n,), generator=g)]
+    parts[0][:2] = torch.tensor([2**31 - 1, -(2**31)])[: parts[0].numel()]
+    ref = torch.cat(parts).to(torch.int32)
+    for threads in (1, 3, 0):
+        rc, fits, out = _ids_i32(parts, threads)
+        assert (rc, fits) == (0, 1)
+        assert torch.equal(out, ref)
+
+
+@pytest.mark.parametrize("bad", [2**31, -(2**31) - 1, 2**32, 2**32 + 5, -(2**63), 2**63 - 1])
+def test_i32_gather_reports_values_outside_int32(bad):
+    """A value that int32 cannot hold clears `fits` wherever it lies, also one
+    whose low 32 bits are a valid id (2**32 + 5)."""
+    big = torch.arange(400_000, dtype=torch.int64)
+    for where in (0, 123_457, 399_999):
+        m = big.clone()
+        m[where] = bad
+        rc, fits, _ = _ids_i32([torch.zeros(5, dtype=torch.int64), m, torch.ones(3, dtype=torch.int64)])
+        assert (rc, fits) == (0, 0)
+
+
+def test_i32_gather_errors():
+    lib = _lib.load()
+    fits = ctypes.c_int32(-1)
+    counts = (ctypes.c_int64 * 1)(-1)
+    ptrs = (ctypes.c_void_p * 1)(0x1000)
+    assert lib.meshy_host_gather_i32(ptrs, counts, 1, 0x1000, 0, ctypes.byref(fits)) == -1
+    assert fits.value == 0
+    assert lib.meshy_host_gather_i32(ptrs, counts, 1, 0x1000, 0, None) == -2
+    fits.value = -1
+    assert lib.meshy_host_gather_i32(None, None, 0, None, 0, ctypes.byref(fits)) == 0
+    assert fits.value == 1

@@ -60,12 +60,14 @@ def test_regions_hold_the_columns_and_tables(tok_dtype, packed, need_lp):
     micros = _micros(lengths)
     res, buf = _stage(samples, micros, packed, need_lp)
     assert res is not None and not isinstance(res, int)
-    size, bounds_b, n_s, total, tok64, nd, max_elems, max_docs, seq_b, rows_b, out_off_b, doc_start_b = res
+    (size, bounds_b, n_s, total, tok64, nd, max_elems, max_docs, seq_b, rows_b, out_off_b, doc_start_b,
+     used_r, need_r) = res
     bounds = np.frombuffer(bounds_b, np.int64).reshape(-1, 2)
     assert len(bounds) == len(_COMMON_REGIONS)
     assert tok64 == (tok_dtype == torch.int64)
 
     used_b, need_b, ds_b, dl_b, seq_t, nd_b, _ = _lib.stage().plan_tables(micros, len(samples))
+    assert (used_r, need_r) == (used_b, need_b)
     used = np.frombuffer(used_b, np.int64)
     need = np.frombuffer(need_b, np.int64)
     assert n_s == len(used) and total == int(need.sum())
