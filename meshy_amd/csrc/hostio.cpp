@@ -167,11 +167,10 @@ class Pool {
 namespace meshy {
 namespace {
 
-// Both gathers: sizes checked, then the job split over the pool.  `unit` is
-// the bytes read per output byte (1 for a copy, 4 for fp32 -> byte), which
-// sets how many workers the job is worth.
-// mode: 0 copies bytes, 1 converts fp32 masks to bytes, 2 narrows int64 to
-// int32 (sizes then count elements).  `ok` reports the conversion's check.
+// Every gather: sizes checked, then the job split over the pool.  mode 0
+// copies bytes, 1 converts fp32 masks to bytes, 2 narrows int64 to int32
+// (sizes then count elements); the bytes read per unit of size (1, 4, 8) set
+// how many workers the job is worth.  `ok` reports the conversion's check.
 int run_gather(const char* who, const void* const* srcs, const int64_t* sizes, int64_t n, void* dst,
                int max_threads, int mode, bool& ok) {
     const bool to_u8 = mode == 1;
