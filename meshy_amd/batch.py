@@ -117,7 +117,7 @@ class _Layout:
         self.regions: dict[str, tuple[int, int, torch.dtype]] = {}
 
     def add(self, name: str, n: int, dtype: torch.dtype) -> None:
-        nbytes = n * dtype.itemsize
+        nbytes = n * (_ITEMSIZE.get(dtype) or dtype.itemsize)
         self.regions[name] = (self.size, self.size + nbytes, dtype)
         self.size += (nbytes + 255) // 256 * 256
 
@@ -136,6 +136,9 @@ class _Layout:
 
 
 _NP_DTYPE = {torch.int32: np.int32, torch.int64: np.int64, torch.float32: np.float32, torch.uint8: np.uint8}
+# dtype.itemsize is a property call; a dict lookup is a tenth of it.
+_ITEMSIZE = {d: d.itemsize for d in (torch.uint8, torch.int8, torch.int16, torch.int32, torch.int64, torch.float16,
+                                      torch.bfloat16, torch.float32, torch.float64, torch.bool)}
 
 
 # Records of meshy_amd._stage.columns: one per used sample.
@@ -567,6 +570,38 @@ def _teacher_width(samples, used, used_b, need_len) -> tuple[int, bool, tuple]:
     return k, bool((ids["dtype"] == _SCALAR_TYPE[torch.int64]).all()), recs
 
 
+_OUT_LAYOUTS: dict[tuple, _Layout] = {}
+
+
+def _out_layout(n_out: int, n_docs_total: int, n_micro: int, rollout_lp: bool, adv_tok: bool,
+                teacher_k: int) -> _Layout:
+    """The pack's output regions for these sizes (read-only, cached: the same
+    sizes recur from step to step)."""
+    key = (n_out, n_docs_total, n_micro, rollout_lp, adv_tok, teacher_k)
+    out_lay = _OUT_LAYOUTS.get(key)
+    if out_lay is not None:
+        return out_lay
+    out_lay = _Layout()
+    for name, dtype in (("input_ids", torch.int64), ("labels", torch.int64), ("positions", torch.int32),
+                        ("mask", torch.float32), ("doc_ids", torch.int64)):
+        out_lay.add(name, n_out, dtype)
+    if rollout_lp:
+        out_lay.add("rollout_lp", n_out, torch.float32)
+    if adv_tok:
+        out_lay.add("adv_tok", n_out, torch.float32)
+    out_lay.add("adv_doc", max(n_docs_total, 1), torch.float32)
+    out_lay.add("lengths", max(n_docs_total, 1), torch.int32)
+    out_lay.add("cu", n_docs_total + 2 * n_micro, torch.int32)
+    out_lay.add("seg", n_docs_total + 2 * n_micro, torch.int64)
+    if teacher_k:
+        out_lay.add("teacher_ids", n_out * teacher_k, torch.int64)
+        out_lay.add("teacher_lps", n_out * teacher_k, torch.float32)
+    if len(_OUT_LAYOUTS) >= 4096:
+        _OUT_LAYOUTS.clear()
+    _OUT_LAYOUTS[key] = out_lay
+    return out_lay
+
+
 def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
     """Run the pack kernels over a staged job and return one ``Batch`` per micro."""
     lib = _lib.load()
@@ -577,70 +612,60 @@ def launch_pack(job: PackJob, sharder=None) -> list[Batch]:
     # Every output lives in one device allocation; the kernel gets addresses
     # inside it, and the typed tensors are views made when a micro first needs
     # them (_PackViews).
-    out_lay = _Layout()
-    for name, dtype in (("input_ids", torch.int64), ("labels", torch.int64), ("positions", torch.int32),
-                        ("mask", torch.float32), ("doc_ids", torch.int64)):
-        out_lay.add(name, n_out, dtype)
-    if job.need_rollout_lp:
-        out_lay.add("rollout_lp", n_out, torch.float32)
-    if job.per_token_adv or job.broadcast_advantages:
-        out_lay.add("adv_tok", n_out, torch.float32)
-    out_lay.add("adv_doc", max(n_docs_total, 1), torch.float32)
-    out_lay.add("lengths", max(n_docs_total, 1), torch.int32)
-    out_lay.add("cu", n_docs_total + 2 * n_micro, torch.int32)
-    out_lay.add("seg", n_docs_total + 2 * n_micro, torch.int64)
-    if job.teacher_k:
-        out_lay.add("teacher_ids", n_out * job.teacher_k, torch.int64)
-        out_lay.add("teacher_lps", n_out * job.teacher_k, torch.float32)
+    adv_tok = bool(job.per_token_adv or job.broadcast_advantages)
+    out_lay = _out_layout(n_out, n_docs_total, n_micro, bool(job.need_rollout_lp), adv_tok, job.teacher_k)
     obuf = torch.empty(max(out_lay.size, 1), dtype=torch.uint8, device=device)
     obase = obuf.data_ptr()
-
-    def out_addr(name: str) -> int | None:
-        return out_lay.addr(obase, name) if name in out_lay.regions else None
+    o = out_lay.regions
 
     a = _lib.PackArgs()
     base = dbuf.data_ptr()
-    a.tokens = lay.addr(base, "tokens")
-    a.tokens_elem_bytes = lay.regions["tokens"][2].itemsize
+    r = lay.regions
+    tok = r["tokens"]
+    a.tokens = base + tok[0]
+    a.tokens_elem_bytes = _ITEMSIZE[tok[2]]
     a.layout = _lib.MESHY_LAYOUT_PACKED if layout == "packed" else _lib.MESHY_LAYOUT_PADDED
-    a.mask = lay.addr(base, "mask")
+    a.mask = base + r["mask"][0]
     a.mask_u8 = int(job.mask_u8)
-    a.logprobs = lay.addr(base, "logprobs") if job.need_rollout_lp else None
+    if job.need_rollout_lp:
+        a.logprobs = base + r["logprobs"][0]
     if job.adv_tokens_dev is not None:
         a.adv_tokens = job.adv_tokens_dev.data_ptr()
-    else:
-        a.adv_tokens = lay.addr(base, "adv_tokens") if job.per_token_adv else None
+    elif job.per_token_adv:
+        a.adv_tokens = base + r["adv_tokens"][0]
     src = job.adv_samples
-    a.adv_samples = (lay.addr(base, "adv_samples") if src is None
+    a.adv_samples = (base + r["adv_samples"][0] if src is None
                      else src if isinstance(src, int) else src.data_ptr())
-    a.sample_offsets = lay.addr(base, "s_off")
+    a.sample_offsets = base + r["s_off"][0]
     a.n_samples = job.n_samples
     a.n_micro = n_micro
-    a.micro_seq_len = lay.addr(base, "seq")
-    a.micro_out_off = lay.addr(base, "out_off")
-    a.micro_doc_start = lay.addr(base, "doc_start")
-    a.doc_sample = lay.addr(base, "doc_sample")
-    a.doc_len = lay.addr(base, "doc_len")
+    a.micro_seq_len = base + r["seq"][0]
+    a.micro_out_off = base + r["out_off"][0]
+    a.micro_doc_start = base + r["doc_start"][0]
+    a.doc_sample = base + r["doc_sample"][0]
+    a.doc_len = base + r["doc_len"][0]
     a.max_micro_elems = job.max_elems
     a.max_docs_per_micro = job.max_docs
-    a.input_ids = out_addr("input_ids")
-    a.labels = out_addr("labels")
-    a.positions = out_addr("positions")
-    a.mask_out = out_addr("mask")
-    a.doc_ids = out_addr("doc_ids")
-    a.rollout_lp = out_addr("rollout_lp")
-    a.adv_tok = out_addr("adv_tok")
-    a.adv_doc = out_addr("adv_doc")
-    a.doc_len_out = out_addr("lengths")
-    a.cu_seqlens = out_addr("cu")
-    a.seg_offsets = out_addr("seg")
+    a.input_ids = obase + o["input_ids"][0]
+    a.labels = obase + o["labels"][0]
+    a.positions = obase + o["positions"][0]
+    a.mask_out = obase + o["mask"][0]
+    a.doc_ids = obase + o["doc_ids"][0]
+    if job.need_rollout_lp:
+        a.rollout_lp = obase + o["rollout_lp"][0]
+    if adv_tok:
+        a.adv_tok = obase + o["adv_tok"][0]
+    a.adv_doc = obase + o["adv_doc"][0]
+    a.doc_len_out = obase + o["lengths"][0]
+    a.cu_seqlens = obase + o["cu"][0]
+    a.seg_offsets = obase + o["seg"][0]
     if job.teacher_k:
         a.teacher_k = job.teacher_k
-        a.teacher_ids = lay.addr(base, "teacher_ids")
-        a.teacher_ids_elem_bytes = lay.regions["teacher_ids"][2].itemsize
-        a.teacher_lps = lay.addr(base, "teacher_lps")
-        a.teacher_ids_out = out_addr("teacher_ids")
-        a.teacher_lps_out = out_addr("teacher_lps")
+        a.teacher_ids = base + r["teacher_ids"][0]
+        a.teacher_ids_elem_bytes = _ITEMSIZE[r["teacher_ids"][2]]
+        a.teacher_lps = base + r["teacher_lps"][0]
+        a.teacher_ids_out = obase + o["teacher_ids"][0]
+        a.teacher_lps_out = obase + o["teacher_lps"][0]
     rc = lib.meshy_pack_micro_batches(_lib.ctypes.byref(a),
                                       job.stream if job.stream is not None else _lib.stream_of(device))
     _lib.check(rc, "meshy_pack_micro_batches")
