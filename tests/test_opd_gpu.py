@@ -316,23 +316,29 @@ def _opd_sample(L, K, seed, V=1000):
     }
 
 
-@pytest.mark.parametrize("ids", ["int64", "int32", "int64_wide", "int64_strided"])
+@pytest.mark.parametrize("ids", ["int64", "int32", "int64_wide", "int64_strided", "int64_general",
+                                 "int64_wide_general"])
 @pytest.mark.parametrize("layout", ["padded", "packed"])
 def test_teacher_layout_matches_oracle(dev, layout, ids):
     """Teacher ids as int64 (the Teacher's dtype, staged as int32), as int32, as
     int64 with one value int32 cannot hold (staged as int64 after the
-    narrowing's check fails), and as strided int64 views."""
+    narrowing's check fails) and as strided int64 views; the "general" cases
+    carry per-token advantages, which take the other columns through the
+    Python staging instead of the one-pass native one."""
     from meshy_amd import opd
+    from meshy_amd.batch import ADVANTAGE_TOKENS
     from meshy_amd.plan import MicroPlan
 
     K = 8
     samples = [_opd_sample(L, K, i) for i, L in enumerate([37, 64, 5, 120, 90])]
-    for s in samples:
+    for i, s in enumerate(samples):
         if ids == "int32":
             s["teacher_topk_ids"] = s["teacher_topk_ids"].to(torch.int32)
         elif ids == "int64_strided":
             s["teacher_topk_ids"] = torch.cat([s["teacher_topk_ids"], -s["teacher_topk_ids"]], 1)[:, :K]
-    if ids == "int64_wide":
+        if ids.endswith("_general"):
+            s[ADVANTAGE_TOKENS] = torch.linspace(-1, 1, s["tokens"].numel()) + i
+    if ids.startswith("int64_wide"):
         samples[4]["teacher_topk_ids"][7, 3] = 2**33 + 11  # within sample 4's first 60 positions
     micros = [MicroPlan((1, 0, 2), 128 if layout == "packed" else 64, (64, 37, 5)),
               MicroPlan((3, 4), 256 if layout == "packed" else 120, (120, 60)),  # sample 4 truncated
