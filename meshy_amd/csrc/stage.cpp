@@ -32,11 +32,15 @@
 //       sample's column at dst (through the library's threaded gather), or
 //       False, copying nothing, when some column is not a CPU contiguous
 //       tensor of that dtype and row width.
-//   stage_micros(samples, micros, packed, need_rollout_lp, dst, capacity, gather_fn)
+//   stage_micros(samples, micros, packed, need_rollout_lp, dst, capacity, gather_fn
+//                [, gather_i32_fn, narrow_min_tokens])
 //       The whole staging of build_micro_batches in one pass, for the common
 //       case: every used sample's tokens (all int64 or all int32), fp32 mask
 //       and (with need_rollout_lp) fp32 log-probs are CPU contiguous tensors
-//       long enough for the micros.  Lays the regions out as the Python
+//       long enough for the micros.  With gather_i32_fn (the library's
+//       meshy_host_gather_i32) int64 tokens are staged as int32 when the
+//       staging holds at least narrow_min_tokens tokens, which checks each;
+//       a token outside int32 returns None.  Lays the regions out as the Python
 //       staging does (256-byte aligned: tokens, mask, [logprobs],
 //       adv_samples, s_off, seq, out_off, doc_len, doc_start, doc_sample,
 //       pos_w), gathers the columns and writes every table at dst.  Returns
@@ -307,6 +311,8 @@ PyObject* scalars(PyObject*, PyObject* args) {
 // The library's meshy_host_gather (passed in by address, so this module needs
 // no link to it).
 typedef int (*GatherFn)(const void* const*, const int64_t*, int64_t, void*, int);
+// The library's meshy_host_gather_i32.
+typedef int (*GatherI32Fn)(const int64_t* const*, const int64_t*, int64_t, int32_t*, int, int32_t*);
 
 // gather(samples, used, need, key, dst, dtype, elem_size, row, gather_fn)
 //   Copies the first need[j] rows (row elements of elem_size bytes) of
@@ -461,8 +467,10 @@ int64_t align256(int64_t x) { return (x + 255) / 256 * 256; }
 PyObject* stage_micros(PyObject*, PyObject* args) {
     PyObject *samples, *micros;
     int packed, need_lp;
-    unsigned long long dst, capacity, fn;
-    if (!PyArg_ParseTuple(args, "OOppKKK", &samples, &micros, &packed, &need_lp, &dst, &capacity, &fn))
+    unsigned long long dst, capacity, fn, fn_i32 = 0;
+    long long narrow_min = 0;
+    if (!PyArg_ParseTuple(args, "OOppKKK|KL", &samples, &micros, &packed, &need_lp, &dst, &capacity, &fn, &fn_i32,
+                          &narrow_min))
         return nullptr;
     PyObject* seq_samples = PySequence_Fast(samples, "samples must be a sequence");
     if (!seq_samples) return nullptr;
@@ -567,6 +575,8 @@ PyObject* stage_micros(PyObject*, PyObject* args) {
     // The layout (the Python staging's region order).
     int64_t total = 0;
     for (int64_t L : need) total += L;
+    const bool narrow = tok64 == 1 && fn_i32 != 0 && total >= narrow_min;
+    if (narrow) tok64 = 0;  // staged as int32
     const int64_t tok_sz = tok64 ? 8 : 4;
     const int64_t sizes[11] = {total * tok_sz,
                                total * 4,
@@ -600,9 +610,23 @@ PyObject* stage_micros(PyObject*, PyObject* args) {
         if (rc != 0) PyErr_Format(PyExc_RuntimeError, "meshy_host_gather failed (%d)", rc);
         return rc == 0;
     };
-    if (!gather_col(tok_p, tok_sz, offs[0]) || !gather_col(mask_p, 4, offs[1]) ||
-        (need_lp && !gather_col(lp_p, 4, offs[2])))
+    if (narrow) {
+        for (int64_t j = 0; j < n_s; ++j) nbytes[j] = need[j];  // elements
+        int32_t fits = 1;
+        if (total > 0) {
+            const int rc = reinterpret_cast<GatherI32Fn>(fn_i32)(reinterpret_cast<const int64_t* const*>(tok_p.data()),
+                                                                 nbytes.data(), n_s,
+                                                                 reinterpret_cast<int32_t*>(base + offs[0]), 0, &fits);
+            if (rc != 0) {
+                PyErr_Format(PyExc_RuntimeError, "meshy_host_gather_i32 failed (%d)", rc);
+                return nullptr;
+            }
+        }
+        if (!fits) Py_RETURN_NONE;  // a token outside int32: the Python staging keeps the int64s
+    } else if (!gather_col(tok_p, tok_sz, offs[0])) {
         return nullptr;
+    }
+    if (!gather_col(mask_p, 4, offs[1]) || (need_lp && !gather_col(lp_p, 4, offs[2]))) return nullptr;
     // The tables.
     float* adv_s = reinterpret_cast<float*>(base + offs[3]);
     for (int64_t j = 0; j < n_s; ++j) adv_s[j] = static_cast<float>(adv[j]);

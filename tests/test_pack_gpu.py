@@ -524,13 +524,18 @@ def test_micros_of_only_empty_samples(dev, layout):
         _assert_same(mb, ref, layout)
 
 
+@pytest.mark.parametrize("narrow", [False, True])
 @pytest.mark.parametrize("layout", ["packed", "padded"])
 @pytest.mark.parametrize("tok_dtype", [torch.int64, torch.int32])
-def test_one_pass_staging_equals_the_general_staging(dev, layout, tok_dtype, monkeypatch):
+def test_one_pass_staging_equals_the_general_staging(dev, layout, tok_dtype, narrow, monkeypatch):
     """The native one-pass staging stages the same bytes, and the pack makes the
-    same batches, as the general staging on the same samples and micros."""
+    same batches, as the general staging on the same samples and micros; int64
+    tokens of a staging at or above the narrowing's token count it stages as
+    int32 (the general staging keeps them int64), the same values."""
     from meshy_amd import batch as B
     from meshy_amd.plan import MicroPlan
+
+    monkeypatch.setattr(B, "_NARROW_MIN_TOKENS", 0 if narrow else 1 << 62)
 
     lengths = [11, 40, 3, 64, 25, 1, 70, 18]
     samples = []
@@ -551,11 +556,17 @@ def test_one_pass_staging_equals_the_general_staging(dev, layout, tok_dtype, mon
     slow_mbs = B.launch_pack(slow, _NoCp())
     torch.cuda.synchronize()
 
-    assert fast.lay.size == slow.lay.size and fast.lay.regions.keys() == slow.lay.regions.keys()
+    assert fast.lay.regions.keys() == slow.lay.regions.keys()
+    assert fast.lay.regions["tokens"][2] == (torch.int32 if narrow else tok_dtype)
+    assert slow.lay.regions["tokens"][2] == tok_dtype
     fbuf, sbuf = fast.dbuf.cpu(), slow.dbuf.cpu()
     for name, (lo, hi, dtype) in slow.lay.regions.items():
-        assert fast.lay.regions[name] == (lo, hi, dtype), name
-        assert torch.equal(fbuf[lo:hi], sbuf[lo:hi]), name
+        flo, fhi, fdtype = fast.lay.regions[name]
+        if name == "tokens":
+            assert torch.equal(fbuf[flo:fhi].view(fdtype).long(), sbuf[lo:hi].view(dtype).long())
+            continue
+        assert fdtype == dtype and fhi - flo == hi - lo, name
+        assert torch.equal(fbuf[flo:fhi], sbuf[lo:hi]), name
     for k in ("seq", "rows", "out_off", "doc_start"):
         a, b = getattr(fast, k), getattr(slow, k)
         assert a.dtype == b.dtype and np.array_equal(a, b), k

@@ -219,3 +219,47 @@ def test_no_samples_stage_empty_int64_tokens():
     assert (n_s, total, tok64) == (0, 0, 1)
     bounds = np.frombuffer(bounds_b, np.int64).reshape(-1, 2)
     assert tuple(bounds[0]) == (0, 0)
+
+
+@pytest.mark.parametrize("packed", [True, False])
+def test_int64_tokens_narrowed_to_int32(packed):
+    """With the narrowing gather, int64 tokens land as int32 (the same values)
+    and every other region is byte-equal to the staging without it."""
+    from meshy_amd.batch import _gather_i32_fn
+
+    lengths = [5, 17, 40, 1, 64, 70, 9, 3]
+    samples = _samples(lengths, 4)
+    samples[2]["tokens"][3] = 2**31 - 1  # the largest id that fits
+    samples[5]["tokens"][0] = -(2**31)
+    micros = _micros(lengths)
+    wide, wbuf = _stage(samples, micros, packed, True)
+    buf = np.zeros(1 << 20, np.uint8)
+    res = _lib.stage().stage_micros(samples, micros, packed, True, buf.ctypes.data, buf.size, _gather_fn(),
+                                    _gather_i32_fn())
+    assert res is not None and not isinstance(res, int)
+    assert res[4] == 0 and wide[4] == 1  # tokens staged as int32 / int64
+    nb = np.frombuffer(res[1], np.int64).reshape(-1, 2)
+    wb = np.frombuffer(wide[1], np.int64).reshape(-1, 2)
+    lo, hi = nb[0]
+    wlo, whi = wb[0]
+    np.testing.assert_array_equal(buf[lo:hi].view(np.int32), wbuf[wlo:whi].view(np.int64).astype(np.int32))
+    assert (hi - lo) * 2 == whi - wlo
+    for r in range(1, len(_COMMON_REGIONS)):
+        (a, b), (c, d) = nb[r], wb[r]
+        assert (a < 0) == (c < 0)
+        if a >= 0:
+            np.testing.assert_array_equal(buf[a:b], wbuf[c:d])
+    assert res[2:4] == wide[2:4] and res[5:] == wide[5:]
+
+
+@pytest.mark.parametrize("bad", [2**31, -(2**31) - 1, 2**32 + 7])
+def test_token_outside_int32_is_left_to_the_general_staging(bad):
+    from meshy_amd.batch import _gather_i32_fn
+
+    lengths = [5, 17, 40]
+    samples = _samples(lengths, 5)
+    samples[1]["tokens"][16] = bad
+    buf = np.zeros(1 << 20, np.uint8)
+    res = _lib.stage().stage_micros(samples, _micros(lengths), True, True, buf.ctypes.data, buf.size, _gather_fn(),
+                                    _gather_i32_fn())
+    assert res is None
