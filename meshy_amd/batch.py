@@ -260,6 +260,9 @@ class PackJob:
     teacher_k: int = 0
     #: The staged mask holds one byte per token (0 or 1) instead of fp32.
     mask_u8: bool = False
+    #: Per micro, whether its advantages are per token (None: every micro
+    #: with documents, when per_token_adv).
+    per_token_micros: tuple | None = None
 
     @classmethod
     def fast(cls, **fields) -> "PackJob":
@@ -332,7 +335,12 @@ def stage_micro_batches(
         j = int(short[0])
         raise ValueError(f"sample {int(used[j])} has {int(n_tk[j])} tokens, micro wants {int(need_len[j])}")
     tok64 = bool(tok_tensor.all() and (tok_recs["dtype"] == _SCALAR_TYPE[torch.int64]).all())
-    per_token_adv = any(ADVANTAGE_TOKENS in samples[m.sample_idx[0]] for m in micros if m.sample_idx)
+    # Per-token advantages are a micro's when its first sample carries them
+    # (batch.py:110): a micro without documents, or whose first sample has
+    # none, keeps per-document advantages.
+    per_token_micros = tuple(bool(m.sample_idx) and ADVANTAGE_TOKENS in samples[m.sample_idx[0]] for m in micros)
+    per_token_adv = any(per_token_micros)
+    adv_cols = _advantage_tokens(samples, micros, per_token_micros, used) if per_token_adv else None
     s_off = np.zeros(n_s + 1, np.int64)
     np.cumsum(need_len, out=s_off[1:])
     total = int(s_off[-1])
@@ -361,14 +369,8 @@ def stage_micro_batches(
     # Per-token advantages already on the device (attach_gae_advantages leaves
     # them there) are gathered on the device; host ones travel with the rest.
     adv_dev = None
-    if per_token_adv and n_s and all(samples[int(i)][ADVANTAGE_TOKENS].is_cuda for i in used):
-        parts = []
-        for i, L in zip(used.tolist(), need_len.tolist()):
-            a = samples[i][ADVANTAGE_TOKENS][:L].to(device=device, dtype=torch.float32)
-            if a.numel() < L:
-                a = torch.cat([a, a.new_zeros(L - a.numel())])
-            parts.append(a)
-        adv_dev = torch.cat(parts)
+    if per_token_adv and n_s and all(c is None or c.is_cuda for c in adv_cols):
+        adv_dev = torch.cat(_advantage_parts(adv_cols, need_len, device))
 
     lay = _Layout()
     lay.add("tokens", total, tok_dtype)
@@ -397,12 +399,7 @@ def stage_micro_batches(
         if need_rollout_lp:
             _gather_column(samples, used, used_b, need_len, "logprobs", lay.view(host, "logprobs"))
         if per_token_adv and adv_dev is None:
-            parts = []
-            for i, L in zip(used.tolist(), need_len.tolist()):
-                a = samples[i][ADVANTAGE_TOKENS][:L].to(device="cpu", dtype=torch.float32)
-                if a.numel() < L:
-                    a = torch.cat([a, a.new_zeros(L - a.numel())])
-                parts.append(a)
+            parts = _advantage_parts(adv_cols, need_len, torch.device("cpu"))
             gather_into(parts, lay.view(host, "adv_tokens"))
     hnp = stage.np
     lay.np_view(hnp, "adv_samples")[:n_s] = adv_samples
@@ -423,11 +420,42 @@ def stage_micro_batches(
     stage.mark(device, handle)
     return PackJob(
         micros=tuple(micros), layout=layout, device=device, dbuf=dbuf, lay=lay,
-        need_rollout_lp=need_rollout_lp, per_token_adv=per_token_adv, n_samples=n_s, seq=seq, rows=rows,
+        need_rollout_lp=need_rollout_lp, per_token_adv=per_token_adv, per_token_micros=per_token_micros,
+        n_samples=n_s, seq=seq, rows=rows,
         out_off=out_off, doc_start=doc_start, max_elems=int(elems.max()) if n_micro else 0,
         max_docs=int(n_docs.max()) if n_micro else 0, adv_tokens_dev=adv_dev, teacher_k=tea.k if tea else 0,
         stream=handle,
     )
+
+
+def _advantage_tokens(samples, micros, per_token_micros, used: np.ndarray) -> list:
+    """The per-token advantage column of each used sample: required of the
+    samples of micros with per-token advantages (a missing one raises, as
+    batch.py:110-116 does), None for other samples that have none."""
+    need = {i for m, f in zip(micros, per_token_micros) if f for i in m.sample_idx}
+    cols = []
+    for i in used.tolist():
+        s = samples[i]
+        if i in need or ADVANTAGE_TOKENS in s:
+            cols.append(s[ADVANTAGE_TOKENS])
+        else:
+            cols.append(None)
+    return cols
+
+
+def _advantage_parts(cols: list, need_len: np.ndarray, device: torch.device) -> list:
+    """The first need_len[j] advantages of each column as fp32 on ``device``,
+    zero-padded (zeros for a sample without the column)."""
+    parts = []
+    for c, L in zip(cols, need_len.tolist()):
+        if c is None:
+            parts.append(torch.zeros(L, dtype=torch.float32, device=device))
+            continue
+        a = c[:L].to(device=device, dtype=torch.float32)
+        if a.numel() < L:
+            a = torch.cat([a, a.new_zeros(L - a.numel())])
+        parts.append(a)
+    return parts
 
 
 # Staging regions in the order stage_micro_batches lays them out without
@@ -731,6 +759,12 @@ class _PackViews:
         self.packed = job.layout == "packed"
         self.sharder = sharder
         self.per_token_adv = job.per_token_adv
+        # Which micros take per-token advantages (batch.py:110): those with
+        # documents whose first sample carries them.
+        self.tok_adv = None
+        if job.per_token_adv:
+            self.tok_adv = (job.per_token_micros if job.per_token_micros is not None
+                            else tuple(bool(m.sample_idx) for m in job.micros))
         self.broadcast_only = job.broadcast_advantages and not job.per_token_adv
         # The launch's one output buffer and its layout; the positive-LM
         # weights stay in the staging buffer, where the host wrote them.
@@ -818,7 +852,7 @@ class _PackViews:
             sdi = di
         made = dict(input_ids=ii, labels=lb, positions=ps, mask=mk, doc_ids=sdi, rollout_logprobs=rl,
                     advantage_tokens=at if self.broadcast_only else None)
-        if self.per_token_adv:
+        if self.tok_adv is not None and self.tok_adv[k]:
             made["advantages"] = at
         _keep_set_fields(f, made)
         if sdi is di:  # not replaced by a context-parallel shard
@@ -835,7 +869,7 @@ class _PackViews:
             self._doc = [torch.split(t[:n], self.nd) for t in docs]
         adv, lengths, pos_w = (c[mb._k] for c in self._doc)
         made = {"lengths": lengths, "positive_lm_weights": pos_w}
-        if not self.per_token_adv:
+        if self.tok_adv is None or not self.tok_adv[mb._k]:
             made["advantages"] = adv
         _keep_set_fields(f, made)
 

@@ -608,3 +608,87 @@ def test_pack_step_byte_mask_equals_fp32_mask(dev, layout):
         for k in ("input_ids", "labels", "positions", "mask", "doc_ids", "rollout_logprobs", "advantages",
                   "lengths"):
             assert torch.equal(getattr(x, k), getattr(y, k)), k
+
+
+def _random_micros(lengths, rng, layout):
+    """Micros over the samples in a random order: packed ones hold up to
+    seq_len tokens, padded ones up to 4 documents; documents longer than
+    seq_len are cut; a filler micro last."""
+    from meshy_amd.plan import MicroPlan
+
+    seq = int(rng.choice([16, 64, 128, 512]))
+    micros, cur, lens, used = [], [], [], 0
+    for i in rng.permutation(len(lengths)).tolist():
+        take = min(int(lengths[i]), seq)
+        full = (used + take > seq) if layout == "packed" else len(cur) == 4
+        if full and cur:
+            micros.append(MicroPlan(tuple(cur), seq, tuple(lens)))
+            cur, lens, used = [], [], 0
+        cur.append(i)
+        lens.append(take)
+        used += take
+    if cur:
+        micros.append(MicroPlan(tuple(cur), seq, tuple(lens)))
+    micros.append(MicroPlan((), seq, ()))
+    return micros
+
+
+@pytest.mark.parametrize("seed", range(12))
+def test_random_batches_match_oracle(dev, seed, monkeypatch):
+    """Random sample sets (empty and one-token samples among them) in random
+    micros, both layouts, through the one-pass staging (int64 tokens narrowed
+    to int32 or not, int32 tokens) or, with per-token advantages, the general
+    staging: every micro equals the oracle's."""
+    from meshy_amd import batch as B
+
+    rng = np.random.default_rng(seed)
+    n = int(rng.integers(1, 40))
+    lengths = rng.integers(0, 300, n)
+    lengths[rng.random(n) < 0.15] = 1
+    lengths[rng.random(n) < 0.1] = 0
+    samples = []
+    for i, L in enumerate(lengths.tolist()):
+        s = _sample(L, prompt=min(L, int(rng.integers(0, 5))), adv=float(rng.normal()), seed=100 * seed + i)
+        s["reward"] = float(rng.random())
+        s["positive_lm_weight"] = float(rng.random())
+        if seed % 4 == 1:
+            s["tokens"] = s["tokens"].to(torch.int32)
+        if seed % 3 == 2:
+            s[B.ADVANTAGE_TOKENS] = torch.randn(L)
+        samples.append(s)
+    monkeypatch.setattr(B, "_NARROW_MIN_TOKENS", 0 if seed % 2 else 1 << 62)
+    for layout in ("packed", "padded"):
+        micros = _random_micros(lengths, rng, layout)
+        mbs = B.build_micro_batches(samples, micros, layout=layout, device=dev, sharder=_NoCp(),
+                                    need_rollout_lp=bool(seed % 5))
+        for mb, m in zip(mbs, micros):
+            ref = obatch.build_micro_batch(samples, m.sample_idx, m.seq_len, m.doc_lens, layout=layout,
+                                           need_rollout_lp=bool(seed % 5))
+            _assert_same(mb, ref, layout)
+
+
+@pytest.mark.parametrize("layout", ["packed", "padded"])
+def test_per_token_advantages_are_decided_per_micro(dev, layout):
+    """A micro takes per-token advantages when its first sample carries them
+    (batch.py:110): here samples 0-3 do and 4-7 do not, and a micro led by
+    sample 6 keeps per-document advantages although sample 2 in it has
+    per-token ones; the filler micro's advantages are an empty per-document
+    tensor."""
+    from meshy_amd import batch as B
+    from meshy_amd.plan import MicroPlan
+
+    samples = []
+    for i, L in enumerate([12, 30, 7, 20, 9, 25, 14, 3]):
+        s = _sample(L, prompt=2, adv=0.25 * i - 1.0, seed=40 + i)
+        if i < 4:
+            s[B.ADVANTAGE_TOKENS] = torch.linspace(-1.0, 1.0, L) * (i + 1)
+        samples.append(s)
+    micros = [MicroPlan((0, 1), 64, (12, 30)), MicroPlan((4, 5), 64, (9, 25)), MicroPlan((6, 2, 3), 64, (14, 7, 20)),
+              MicroPlan((7,), 64, (3,)), MicroPlan((), 64, ())]
+    mbs = B.build_micro_batches(samples, micros, layout=layout, device=dev, sharder=_NoCp(), need_rollout_lp=True)
+    for mb, m in zip(mbs, micros):
+        ref = obatch.build_micro_batch(samples, m.sample_idx, m.seq_len, m.doc_lens, layout=layout,
+                                       need_rollout_lp=True)
+        _assert_same(mb, ref, layout)
+    assert mbs[0].advantages.dim() == 2 and mbs[2].advantages.dim() == 1
+    assert mbs[-1].advantages.shape == (0,)
