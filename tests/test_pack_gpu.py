@@ -692,3 +692,61 @@ def test_per_token_advantages_are_decided_per_micro(dev, layout):
         _assert_same(mb, ref, layout)
     assert mbs[0].advantages.dim() == 2 and mbs[2].advantages.dim() == 1
     assert mbs[-1].advantages.shape == (0,)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_pack_steps_match_oracle(dev, seed):
+    """pack_step over random batches (groups of 4, lengths from 0 up, 0/1 or
+    fractional masks, random planner settings in both layouts) against the
+    oracle's plan, GRPO advantages and micro-batches."""
+    from meshy_amd.pipeline import RaggedSamples, pack_step
+    from meshy_amd.plan import PlannerConfig
+    from oracle import plan as oplan
+
+    rng = np.random.default_rng(1000 + seed)
+    G = 4
+    n = G * int(rng.integers(1, 12))
+    lengths = rng.integers(0, 400, n)
+    lengths[rng.random(n) < 0.1] = 1
+    offsets = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
+    total = int(offsets[-1])
+    tokens = rng.integers(0, 150000, total)
+    mask = (rng.random(total) < 0.7).astype(np.float32)
+    if seed % 4 == 3:
+        mask[rng.random(total) < 0.05] = 0.5  # not 0/1: staged as fp32
+    logprobs = rng.normal(size=total).astype(np.float32)
+    rewards = rng.integers(0, 2, n).astype(np.float32) if seed % 2 else rng.random(n).astype(np.float32)
+    group_offsets = np.arange(0, n + 1, G, dtype=np.int64)
+    layout = "packed" if seed % 2 == 0 else "padded"
+    seq_len = int(rng.choice([256, 512, 1024]))
+    align = int(rng.choice([1, 64, 256]))
+    mini = int(rng.choice([d for d in range(1, n + 1) if n % d == 0]))
+    kw = dict(layout=layout, mini_batch_size=mini, seq_len=seq_len, align=align,
+              max_tokens_per_micro=seq_len if layout == "packed" or seed % 3 else None,
+              micro_batch_size=None if layout == "packed" and seed % 3 else int(rng.integers(1, 5)))
+    cfg = PlannerConfig(**kw)
+    ragged = RaggedSamples.from_arrays(tokens, mask, logprobs, offsets, rewards, group_offsets)
+    res = pack_step(ragged, cfg, dev)
+
+    samples = [{"tokens": torch.from_numpy(tokens[a:b]), "mask_assistant": torch.from_numpy(mask[a:b]),
+                "logprobs": torch.from_numpy(logprobs[a:b]), "reward": float(rewards[i])}
+               for i, (a, b) in enumerate(zip(offsets[:-1], offsets[1:]))]
+    lens, loss = oplan.sample_lengths(samples, seq_len)
+    local, per_rank = oplan.build_plan(lens, loss, 1, **kw)
+    ref_adv = ogrpo.grpo_batched(torch.from_numpy(rewards), torch.from_numpy(group_offsets))
+    assert (res.advantages.cpu() - ref_adv).abs().max().item() <= 1e-5
+    assert tuple(res.plan.local_indices[0]) == tuple(local[0])
+    for s, a in zip(samples, ref_adv):
+        s["advantage"] = a
+    local_samples = [samples[i] for i in local[0]]
+    micros = [m for mini_plan in per_rank[0] for m in mini_plan[0]]
+    assert len(res.batches) == len(micros)
+    for mb, (idx, s_len, doc_lens) in zip(res.batches, micros):
+        ref = obatch.build_micro_batch(local_samples, idx, s_len, doc_lens, layout=layout, need_rollout_lp=True)
+        for k in ("input_ids", "labels", "positions", "mask", "doc_ids"):
+            assert torch.equal(getattr(mb, k).cpu(), ref[k]), k
+        assert torch.equal(mb.rollout_logprobs.cpu(), ref["rollout_logprobs"])
+        assert torch.equal(mb.lengths.cpu(), ref["lengths"])
+        if layout == "packed":
+            assert torch.equal(mb.attention_masks.cu_seq_q.cpu(), ref["cu_seqlens"])
+        assert (mb.advantages.cpu() - ref["advantages"]).abs().max().item() <= 1e-5
