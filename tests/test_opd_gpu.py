@@ -7,6 +7,7 @@ sums), bf16 gradients within their rounding (4e-3 x |g|), fp32 gradients 1e-6.
 
 from types import SimpleNamespace as NS
 
+import numpy as np
 import pytest
 import torch
 
@@ -606,3 +607,38 @@ def test_gather_random_sweep(dev, seed):
     ref = otopk.gather_logprobs(z, ids.clamp(min=0))
     ref = torch.where(drop, torch.zeros_like(ref), ref)  # -100: 0, like cross_entropy's ignore_index
     assert (out - ref).abs().max().item() <= TOL
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_teacher_layouts_match_oracle(dev, seed):
+    """Random samples (empty and one-token ones among them) with Teacher columns
+    of width 1, 3 or 8 in random micros, both layouts: the Teacher tensors
+    equal the oracle's layout."""
+    from meshy_amd import opd
+    from meshy_amd.plan import MicroPlan
+
+    rng = np.random.default_rng(500 + seed)
+    K = int(rng.choice([1, 3, 8]))
+    n = int(rng.integers(1, 24))
+    lengths = rng.integers(0, 200, n)
+    lengths[rng.random(n) < 0.15] = 1
+    samples = [_opd_sample(int(L), K, 10 * seed + i, V=151936) for i, L in enumerate(lengths)]
+    for layout in ("packed", "padded"):
+        seq = int(rng.choice([32, 128, 256]))
+        micros, cur, lens, used = [], [], [], 0
+        for i in rng.permutation(n).tolist():
+            take = min(int(lengths[i]), seq)
+            if ((used + take > seq) if layout == "packed" else len(cur) == 3) and cur:
+                micros.append(MicroPlan(tuple(cur), seq, tuple(lens)))
+                cur, lens, used = [], [], 0
+            cur.append(i)
+            lens.append(take)
+            used += take
+        if cur:
+            micros.append(MicroPlan(tuple(cur), seq, tuple(lens)))
+        micros.append(MicroPlan((), seq, ()))
+        mbs = opd.build_topk_micro_batches(samples, micros, layout=layout, device=dev, need_rollout_lp=True)
+        for mb, m in zip(mbs, micros):
+            rids, rlps = oopd.layout_teacher_topk(samples, m.sample_idx, m.seq_len, m.doc_lens, layout=layout)
+            assert torch.equal(mb.teacher_topk_ids.cpu(), rids)
+            assert torch.equal(mb.teacher_topk_logprobs.cpu(), rlps)
