@@ -736,3 +736,43 @@ def test_negative_gamma_is_refused(dev):
     z = torch.zeros(1, 8, device=dev)
     with pytest.raises(ValueError, match="gamma"):
         compute_returns(z, z + 1, torch.zeros(1, 8, dtype=torch.long, device=dev), gamma=-0.5)
+
+
+@pytest.mark.parametrize("seed", range(10))
+def test_random_attach_matches_oracle(dev, seed):
+    """Random critic batches (one-token samples, masks with holes, samples
+    longer than seq_len, fp32 or bf16 values, float rewards) and random
+    gamma, lambda and alpha: the attached advantages and the metrics equal
+    the oracle's."""
+    from types import SimpleNamespace as NS
+
+    from meshy_amd.batch import ADVANTAGE_TOKENS
+    from meshy_amd.gae import attach_gae_advantages
+
+    rng = np.random.default_rng(2000 + seed)
+    bf16 = bool(seed % 2)
+    samples = []
+    for j in range(int(rng.integers(1, 60))):
+        L = 1 if rng.random() < 0.1 else int(rng.integers(2, 900))
+        mask = (rng.random(L) < 0.8).astype(np.float32)
+        mask[: int(rng.integers(0, max(1, L // 3)))] = 0.0
+        v = torch.from_numpy(rng.normal(size=L).astype(np.float32))
+        samples.append({"tokens": torch.arange(L), "mask_assistant": torch.from_numpy(mask),
+                        "values": v.to(torch.bfloat16) if bf16 else v,
+                        "reward": torch.tensor(float(rng.normal()))})
+    seq_len = int(rng.choice([64, 512, 10 ** 6]))
+    gamma = float(rng.choice([1.0, 0.99, 0.9]))
+    lam = None if seed % 3 == 0 else float(rng.choice([0.0, 0.9, 0.95, 1.0]))
+    alpha = float(rng.uniform(0.2, 2.0))
+    ref_adv, ref_m = ogae.attach_gae_advantages(
+        [{k: (v.float() if k == "values" else v) for k, v in s.items()} for s in samples],
+        seq_len=seq_len, gamma=gamma, alpha=alpha, gae_lambda=lam)
+    trainer = NS(seq_len=seq_len, gae_gamma=gamma, gae_alpha=alpha, gae_lambda=lam, device=dev)
+    metrics = attach_gae_advantages(trainer, samples)
+    for s, r in zip(samples, ref_adv):
+        got = s[ADVANTAGE_TOKENS]
+        assert got.is_cuda and got.shape == r.shape
+        assert (got.cpu() - r).abs().max().item() <= TOL
+    assert set(metrics) == set(ref_m)
+    for k in ref_m:
+        assert abs(metrics[k] - ref_m[k]) <= TOL * max(1.0, abs(ref_m[k])), k
