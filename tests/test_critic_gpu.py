@@ -465,3 +465,24 @@ def test_pack_from_wire_columns_equals_pack_from_samples(dev, layout):
     for x, y in zip(a.batches, b.batches):
         for f in ("input_ids", "labels", "positions", "mask", "doc_ids", "rollout_logprobs", "advantages"):
             assert torch.equal(getattr(x, f), getattr(y, f)), f
+
+
+@pytest.mark.parametrize("seed", range(8))
+def test_random_rollout_metrics_match_oracle(dev, seed):
+    """Random rollout batches (1 to 80 samples, with or without the stamps,
+    a sample whose log-probs are shorter than its mask, one without a mask,
+    random seq_len and versions) against the oracle's metrics."""
+    from meshy_amd.rollout_metrics import rollout_metrics
+
+    rng = np.random.default_rng(3000 + seed)
+    n = int(rng.integers(1, 80))
+    samples = _rollout_samples(n, seed=seed + 17, stamps=bool(seed % 2))
+    if n > 3 and seed % 3 == 0:
+        samples[1]["logprobs"] = samples[1]["logprobs"][: max(1, samples[1]["logprobs"].numel() // 2)]
+    if n > 4 and seed % 4 == 1:
+        del samples[2]["mask_assistant"]
+    seq_len = int(rng.choice([64, 1000, 2048, 100000]))
+    version = int(rng.integers(3, 9))
+    m, hist = rollout_metrics(samples, seq_len=seq_len, current_version=version)
+    rm, rh = orm.rollout_metrics(samples, seq_len=seq_len, current_version=version)
+    _compare(m, hist, rm, rh)
