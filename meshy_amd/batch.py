@@ -12,7 +12,6 @@ reference's fields (batch.py:52-74) so the forward and the loss read it as is.
 
 from __future__ import annotations
 
-import weakref
 from dataclasses import MISSING, dataclass, fields
 from typing import Any, NamedTuple, Sequence
 
@@ -769,6 +768,9 @@ class _PackViews:
         # The launch's one output buffer and its layout; the positive-LM
         # weights stay in the staging buffer, where the host wrote them.
         self.obuf, self.out_lay = obuf, out_lay
+        # Every view shares obuf's version counter: its value now, against
+        # which a later in-place change of any output is seen.
+        self.version0 = obuf._version
         self.pos_w_src = (lay, dbuf)
         self._job = job
         self.doc_start = job.doc_start.tolist()
@@ -818,6 +820,15 @@ class _PackViews:
             self._seg = self._flat("seg")
         return self._seg
 
+    def seg_offsets(self, k: int, ids: torch.Tensor, n_docs: int) -> torch.Tensor | None:
+        """The segment offsets the pack wrote for micro k (n_docs + 2 of
+        them) when ``ids`` is still that micro's unchanged doc_ids view."""
+        nd = self.nd[k]
+        if n_docs != nd or ids._version != self.version0:
+            return None
+        d0 = self.doc_start[k] + 2 * k
+        return self.seg[d0:d0 + nd + 2]
+
     # Each group's views are made for every micro at once, the first time any
     # micro needs them: one torch.split per tensor (a third of a microsecond
     # per view) instead of a slice and a view per micro and field.
@@ -850,15 +861,20 @@ class _PackViews:
             at = rest.pop(0) if at is not None else None
         else:
             sdi = di
-        made = dict(input_ids=ii, labels=lb, positions=ps, mask=mk, doc_ids=sdi, rollout_logprobs=rl,
-                    advantage_tokens=at if self.broadcast_only else None)
+        setd = f.setdefault  # a field the caller set before its first read stays
+        setd("input_ids", ii)
+        setd("labels", lb)
+        setd("positions", ps)
+        setd("mask", mk)
+        setd("doc_ids", sdi)
+        setd("rollout_logprobs", rl)
+        setd("advantage_tokens", at if self.broadcast_only else None)
         if self.tok_adv is not None and self.tok_adv[k]:
-            made["advantages"] = at
-        _keep_set_fields(f, made)
+            setd("advantages", at)
         if sdi is di:  # not replaced by a context-parallel shard
-            d0 = self.doc_start[k]
-            mb.__dict__["_meshy_seg_src"] = ((id(di), di._version, di.data_ptr(), self.nd[k]), self.seg, d0 + 2 * k,
-                                             weakref.ref(di))
+            # The offsets the pack wrote for this micro (seg_offsets below),
+            # valid while this doc_ids tensor is the batch's and unchanged.
+            f["_meshy_seg_src"] = (self, k, di)
 
     def doc_fields(self, mb: "PackedBatch", f: dict) -> None:
         """Per-document advantages, lengths and positive-LM weights of micro mb._k."""

@@ -40,10 +40,9 @@ def batch_segment_offsets(mb: Any) -> torch.Tensor:
     if hit is not None and hit[0] == key and hit[2]() is ids:
         return hit[1]
     src = getattr(mb, "_meshy_seg_src", None)
-    if src is not None and src[0] == key and src[3]() is ids:
-        # Written by the pack kernel next to doc_ids: no pass over the ids.
-        off = src[1][src[2]:src[2] + key[3] + 2]
-    else:
+    # Written by the pack kernel next to doc_ids: no pass over the ids.
+    off = src[0].seg_offsets(src[1], ids, key[3]) if src is not None and src[2] is ids else None
+    if off is None:
         off = checked_segment_offsets(ids, int(mb.n_docs) + 1)
     try:
         object.__setattr__(mb, "_meshy_seg_offsets", (key, off, weakref.ref(ids)))

@@ -201,7 +201,7 @@ def test_pack_writes_the_segment_offsets_of_every_micro(dev, layout):
         got = batch_segment_offsets(mb)
         assert got.dtype == torch.int64 and torch.equal(got.cpu(), want), (mb.n_docs, got, want)
         # a view of the offsets the pack wrote, not a recomputation
-        seg = getattr(mb, "_meshy_seg_src")[1]
+        seg = getattr(mb, "_meshy_seg_src")[0].seg
         assert seg.data_ptr() <= got.data_ptr() < seg.data_ptr() + seg.numel() * seg.element_size()
 
 
