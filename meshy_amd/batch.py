@@ -883,11 +883,13 @@ class _PackViews:
             lay, dbuf = self.pos_w_src
             docs = (self._flat("adv_doc"), self._flat("lengths"), lay.view(dbuf, "pos_w"))
             self._doc = [torch.split(t[:n], self.nd) for t in docs]
-        adv, lengths, pos_w = (c[mb._k] for c in self._doc)
-        made = {"lengths": lengths, "positive_lm_weights": pos_w}
-        if self.tok_adv is None or not self.tok_adv[mb._k]:
-            made["advantages"] = adv
-        _keep_set_fields(f, made)
+        k = mb._k
+        adv, lengths, pos_w = self._doc
+        setd = f.setdefault  # a field the caller set before its first read stays
+        setd("lengths", lengths[k])
+        setd("positive_lm_weights", pos_w[k])
+        if self.tok_adv is None or not self.tok_adv[k]:
+            setd("advantages", adv[k])
 
     def attention(self, mb: "PackedBatch", f: dict) -> None:
         """cu_seqlens (n_docs + 1 slots, + 1 with a padding document) and the
@@ -909,13 +911,6 @@ class _PackViews:
         max_len = max(max(m.doc_lens, default=0), pad if pad > 0 else 0)
         f.setdefault("attention_masks",
                      VarlenMetadata(cu_seq_q=cu, cu_seq_k=cu, max_q=int(max_len), max_k=int(max_len)))
-
-
-def _keep_set_fields(f: dict, made: dict) -> None:
-    """Adds the made views to a batch's attributes, keeping any field the
-    caller set before its first read."""
-    for k, v in made.items():
-        f.setdefault(k, v)
 
 
 class _Lazy:
