@@ -581,6 +581,20 @@ def bench_pack(runs, no_cpu):
                                                                need_rollout_lp=True)),
         runs, warmup=2, before=lambda: held.pop("b", None)), 1)
     held.clear()
+    # The OPD student builds each micro as it reaches it too (opd.py:141-148).
+    per_micro = []
+    for rep in range(max(3, runs // 20) + 2):
+        for m in micros:
+            torch.cuda.synchronize()
+            t0 = time.perf_counter()
+            mb = build_topk_micro_batches(local_t, [m], layout="packed", device=dev, need_rollout_lp=True)
+            torch.cuda.synchronize()
+            if rep >= 2:  # the first two passes warm up
+                per_micro.append(time.perf_counter() - t0)
+            del mb
+    out["build_topk_micro_batch_per_micro_us"] = {"median": round(float(np.median(per_micro)) * 1e6, 1),
+                                                  "mean": round(float(np.mean(per_micro)) * 1e6, 1),
+                                                  "micros": len(micros), "calls": len(per_micro)}
     if not no_cpu:
         from oracle import batch as obatch
         from oracle import grpo as ogrpo
