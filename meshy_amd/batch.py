@@ -528,6 +528,12 @@ def _copy_to_device(dbuf: torch.Tensor, host: torch.Tensor, lo: int, hi: int, ha
                    "meshy_copy_to_device")
 
 
+# Narrowing Teacher ids pays from about this many: at 262144 int64s it took
+# as long on the host as copying them and saved a 1 MB copy to the device; at
+# 65536 (one micro of ~8 k tokens, K = 8) it took 35 us against a 20 us copy.
+_NARROW_MIN_TEACHER_IDS = 262144
+
+
 class _TeacherStaging:
     """The OPD Teacher columns (``teacher_topk_logprobs``, then
     ``teacher_topk_ids``, ``[L, K]`` each) as the last two staging regions.
@@ -536,17 +542,17 @@ class _TeacherStaging:
     soon as it is gathered, so the copy of the regions before it runs while it
     is gathered (a queued host-to-device copy holds the host's next one until
     it has run, so a few large copies overlap the gathers better than many
-    small ones).  int64 ids in CPU tensors (the Teacher's dtype) are narrowed
-    to int32 as they are gathered, which checks that each fits and halves
-    their bytes; the ids' region has room for int64s and holds them when one
-    does not fit."""
+    small ones).  int64 ids in CPU tensors (the Teacher's dtype), when there
+    are enough of them, are narrowed to int32 as they are gathered, which
+    checks that each fits and halves their bytes; the ids' region has room
+    for int64s and holds them when one does not fit."""
 
     def __init__(self, samples, used: np.ndarray, used_b: bytes, need_len: np.ndarray, lay: _Layout) -> None:
         self.samples, self.used, self.used_b, self.need = samples, used, used_b, need_len
         self.k, ids64, self.recs = _teacher_width(samples, used, used_b, need_len)
         self.total = total = int(need_len.sum())
-        self.narrow = bool(self.k and ids64 and self.recs[0] is not None
-                           and (self.recs[0]["flags"] == _CPU_CONTIGUOUS_TENSOR).all())
+        self.narrow = bool(self.k and ids64 and total * self.k >= _NARROW_MIN_TEACHER_IDS
+                           and self.recs[0] is not None and (self.recs[0]["flags"] == _CPU_CONTIGUOUS_TENSOR).all())
         self.reserve = lay.size
         if not self.k:
             return

@@ -320,16 +320,18 @@ def _opd_sample(L, K, seed, V=1000):
 @pytest.mark.parametrize("ids", ["int64", "int32", "int64_wide", "int64_strided", "int64_general",
                                  "int64_wide_general"])
 @pytest.mark.parametrize("layout", ["padded", "packed"])
-def test_teacher_layout_matches_oracle(dev, layout, ids):
+def test_teacher_layout_matches_oracle(dev, layout, ids, monkeypatch):
     """Teacher ids as int64 (the Teacher's dtype, staged as int32), as int32, as
     int64 with one value int32 cannot hold (staged as int64 after the
     narrowing's check fails) and as strided int64 views; the "general" cases
     carry per-token advantages, which take the other columns through the
     Python staging instead of the one-pass native one."""
+    from meshy_amd import batch as B
     from meshy_amd import opd
     from meshy_amd.batch import ADVANTAGE_TOKENS
     from meshy_amd.plan import MicroPlan
 
+    monkeypatch.setattr(B, "_NARROW_MIN_TEACHER_IDS", 0)  # narrow these few ids too
     K = 8
     samples = [_opd_sample(L, K, i) for i, L in enumerate([37, 64, 5, 120, 90])]
     for i, s in enumerate(samples):
